@@ -1,0 +1,159 @@
+/*
+ * rnn.h -- C ABI of the MI355X (gfx950) GEMM core of rustnn.
+ *
+ * Drop-in boundary for the reference's L2 kernels (lsiddd/rustnn, Rust): each
+ * entry point names the reference function it replaces (file:line).  A thin
+ * Rust FFI crate (extern "C" + #[link(name = "rnn")]) keeps the reference call
+ * sites in conv.rs / attn.rs / linear.rs / nn.rs unchanged; the binding is
+ * shown in INTEGRATION.md.
+ *
+ * Conventions
+ *  - Every float pointer is a DEVICE pointer (hipMalloc / torch CUDA tensor)
+ *    holding IEEE binary32, row-major, tightly packed unless a stride says
+ *    otherwise.  Shapes are element counts.
+ *  - Work is enqueued on the context's stream; calls return once the work is
+ *    enqueued (use rnn_ctx_synchronize to wait).  The library keeps no pointer
+ *    after a call returns.
+ *  - Return value: RNN_OK (0) or a negative RNN_E_* code.  rnn_ctx_last_error
+ *    gives the message.  The reference aborts on a bad shape (slice bounds
+ *    panic, panic=abort); the Rust shim maps a non-zero status to panic!.
+ *  - Results are deterministic: every reduction (split-K, dW over images,
+ *    attention dtau/drel over images) runs in a fixed order.
+ *  - One stream per context; a context may be used from several host threads
+ *    (calls are serialised by a per-context lock).
+ */
+#ifndef RNN_H
+#define RNN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    RNN_OK = 0,
+    RNN_E_INVALID = -1,     /* bad shape / argument */
+    RNN_E_NULL = -2,        /* required pointer is NULL */
+    RNN_E_HIP = -3,         /* HIP runtime error (message has hipGetErrorString) */
+    RNN_E_NOMEM = -4,       /* device workspace allocation failed */
+    RNN_E_UNSUPPORTED = -5, /* shape outside what the kernels implement */
+};
+
+typedef struct rnn_ctx rnn_ctx;
+
+/* ------------------------------------------------------------- context */
+/* Replaces the process-wide rayon pool + thread-local scratch
+ * (main.rs:41-48, gemm.rs:411-420): one device, one stream, one workspace. */
+int rnn_ctx_create(int device, rnn_ctx **out);
+int rnn_ctx_destroy(rnn_ctx *ctx);
+/* Use `stream` (a hipStream_t; NULL = the null stream) for later calls. */
+int rnn_ctx_set_stream(rnn_ctx *ctx, void *stream);
+void *rnn_ctx_stream(rnn_ctx *ctx);
+int rnn_ctx_synchronize(rnn_ctx *ctx);
+const char *rnn_ctx_last_error(rnn_ctx *ctx);
+const char *rnn_status_string(int status);
+/* Bytes of device workspace currently held by the context. */
+size_t rnn_ctx_workspace_bytes(rnn_ctx *ctx);
+
+/* ------------------------------------------------------------ gemm.rs */
+/* matmul (gemm.rs:434-493): C[m x n] = op(A) op(B) (+ C if acc).
+ * at=0: A is [m x k]; at=1: A is [k x m].  bt=0: B is [k x n]; bt=1: B is
+ * [n x k].  m == 0 or n == 0: no-op.  k == 0: C = 0 unless acc. */
+int rnn_matmul(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, int at, const float *b,
+               int bt, float *c, int acc);
+
+/* gemm_small (gemm.rs:500-545), batched: `count` independent problems,
+ * problem i uses a + i*stride_a, b + i*stride_b, c + i*stride_c.  Replaces the
+ * per-(image, head) sequential calls made from rayon workers with one launch.
+ * k == 0 leaves C untouched (gemm_small quirk). */
+int rnn_gemm_small_batched(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k,
+                           const float *a, size_t stride_a, int at, const float *b,
+                           size_t stride_b, int bt, float *c, size_t stride_c, int acc);
+
+/* matmul_dw (gemm.rs:555-598): C[m x n] += A^T B with A [k x m], B [k x n]
+ * (dense weight gradient, K = rows). */
+int rnn_matmul_dw(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, const float *b,
+                  float *c);
+
+/* ------------------------------------------------------------ conv.rs */
+/* ConvSpec (conv.rs:9-20); oh/ow follow Conv2d::out_dim (nn.rs:147-150):
+ * oh = (h + 2*pad - k)/stride + 1.  W is [cout][cin][k][k] (RowMap order,
+ * conv.rs:39-66); x, y, dx, dy are NCHW. */
+typedef struct {
+    uint32_t cin, cout, k, stride, pad, h, w, oh, ow;
+} rnn_conv_spec;
+
+/* Fills oh/ow.  Returns RNN_E_INVALID for k > h + 2*pad, stride 0, ... */
+int rnn_conv_spec_init(rnn_conv_spec *sp, uint32_t cin, uint32_t cout, uint32_t k,
+                       uint32_t stride, uint32_t pad, uint32_t h, uint32_t w);
+
+/* Conv2d::forward (nn.rs:166-185) -> conv::forward_image (conv.rs:168-203):
+ * y[n][cout][oh][ow] = conv(x) (overwritten). */
+int rnn_conv2d_forward(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
+                       const float *w, float *y);
+/* Conv2d::backward_w (nn.rs:193-227) -> conv::dw_image (conv.rs:277-322):
+ * dw[cout][cin*k*k] += sum over images of dY im2col(X)^T. */
+int rnn_conv2d_backward_w(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                          const float *x, float *dw);
+/* dX half of Conv2d::backward (nn.rs:230-250) -> conv::dx_image
+ * (conv.rs:205-246): dx[n][cin][h][w] = col2im(W^T dY) (overwritten). */
+int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                          const float *w, float *dx);
+
+/* ------------------------------------------------------------ attn.rs */
+/* Core (attn.rs:74-84) plus the stride/offset arguments of Core::forward /
+ * Core::backward (attn.rs:148-160, 226-242).  Rows of head hd are read at
+ * base + r*qstride + qoff + hd*dh (queries) and base + r*kvstride + koff/voff
+ * + hd*dh (keys / values).  relidx is a HOST pointer to tq*tk entries
+ * (rnn_rel_index); the library uploads it. */
+typedef struct {
+    uint32_t h, dh, tq, tk;
+    size_t qstride, qoff, kvstride, koff, voff;
+    uint32_t nrel;
+    const uint32_t *relidx;
+    int mask_diag;
+} rnn_attn_desc;
+
+/* rel_index (attn.rs:53-72): host-side table of th*tw*mh*mw entries;
+ * *nrel receives the bias-table length per head. */
+int rnn_rel_index(uint32_t th, uint32_t tw, uint32_t mh, uint32_t mw, uint32_t *idx,
+                  uint32_t *nrel);
+
+/* Core::forward (attn.rs:148-223): p[n][h][tq][tk] = softmax(tau*QK^T + rel,
+ * diagonal masked when mask_diag), o[n][tq][h*dh] = P V. */
+int rnn_attn_forward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
+                     const float *kv, const float *tau, const float *rel, float *p, float *o);
+/* Core::backward (attn.rs:226-343): dq, dkv, dtau, drel ACCUMULATE (+=).
+ * dq and dkv may alias (disjoint columns, as in SelfAttn, attn.rs:418-438). */
+int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
+                      const float *kv, const float *tau, const float *p, const float *dout,
+                      float *dq, float *dkv, float *dtau, float *drel);
+
+/* ---------------------------------------------------------- linear.rs */
+/* Linear::forward (linear.rs:44-63): y[rows x fout] = x W^T + b (b may be NULL). */
+int rnn_linear_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
+                       const float *w, const float *b, float *y);
+/* Linear::backward (linear.rs:66-96): dw += dy^T x; db += colsum(dy) (db may
+ * be NULL); dx = dy W (overwritten). */
+int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
+                        const float *x, const float *w, float *dw, float *db, float *dx);
+
+/* ------------------------------------------ debug exports (bit-exact tests) */
+/* im2col of ONE image through the same staging index math the conv kernels
+ * use: col[cin*k*k][oh*ow] (gather_span, conv.rs:68-120). */
+int rnn_dbg_im2col(rnn_ctx *ctx, const rnn_conv_spec *sp, const float *x_img, float *col);
+/* PackedA::pack / pack_t (gemm.rs:54-113) into out[nb*256*mpad] (positions the
+ * reference never writes are left untouched). */
+int rnn_dbg_pack_a(rnn_ctx *ctx, const float *a, size_t m, size_t k, int transposed, float *out);
+/* PackedB::pack / pack_t (gemm.rs:340-400) into out[nb*256*npad]. */
+int rnn_dbg_pack_b(rnn_ctx *ctx, const float *b, size_t n, size_t k, int transposed, float *out);
+/* rel_index computed on the device into idx (device, th*tw*mh*mw u32). */
+int rnn_dbg_rel_index(rnn_ctx *ctx, uint32_t th, uint32_t tw, uint32_t mh, uint32_t mw,
+                      uint32_t *idx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

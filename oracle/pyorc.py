@@ -1,0 +1,326 @@
+"""numpy front end of the CPU oracle (liborc.so).
+
+TEST INFRASTRUCTURE ONLY: a restatement of the reference's CPU algorithm
+(lsiddd/rustnn) used to check the HIP product path and to time the
+reference-style CPU baseline.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+``bench.py``'s cpu_baseline leg may import this module; nothing under
+``rustnn_amd/`` does.
+
+Each wrapper names the reference function (file:line) the C code restates.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liborc.so")
+
+MR, NR, KC = 6, 16, 256  # gemm.rs:11-13
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
+_sz = C.c_size_t
+
+
+def build(force: bool = False) -> str:
+    """Compile liborc.so with the committed Makefile."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-C", HERE, "-B" if force else "all"], check=True,
+                       stdout=subprocess.DEVNULL)
+    return LIB_PATH
+
+
+class ConvSpec(C.Structure):
+    """ConvSpec (conv.rs:9-20) with oh/ow as Conv2d::out_dim (nn.rs:147-150)."""
+    _fields_ = [(n, C.c_uint32) for n in
+                ("cin", "cout", "k", "stride", "pad", "h", "w", "oh", "ow")]
+
+    @classmethod
+    def make(cls, cin, cout, k, stride, pad, h, w):
+        return cls(cin, cout, k, stride, pad, h, w,
+                   (h + 2 * pad - k) // stride + 1, (w + 2 * pad - k) // stride + 1)
+
+    @property
+    def ckk(self):
+        return self.cin * self.k * self.k
+
+    @property
+    def hw(self):
+        return self.oh * self.ow
+
+
+class AttnDesc(C.Structure):
+    """Core (attn.rs:74-84) plus the stride/offset arguments of forward/backward."""
+    _fields_ = [("h", _sz), ("dh", _sz), ("tq", _sz), ("tk", _sz),
+                ("qstride", _sz), ("qoff", _sz), ("kvstride", _sz), ("koff", _sz),
+                ("voff", _sz), ("nrel", _sz), ("relidx", C.POINTER(C.c_uint32)),
+                ("mask_diag", C.c_int)]
+
+
+class RngState(C.Structure):
+    _fields_ = [("s", C.c_uint64 * 4)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        build()
+        L = C.CDLL(LIB_PATH)
+        P = C.POINTER
+        L.orc_rng_new.argtypes = [P(RngState), C.c_uint64]
+        L.orc_rng_next_u64.argtypes = [P(RngState)]
+        L.orc_rng_next_u64.restype = C.c_uint64
+        L.orc_rng_below.argtypes = [P(RngState), _sz]
+        L.orc_rng_below.restype = _sz
+        L.orc_rng_uniform.argtypes = [P(RngState)]
+        L.orc_rng_uniform.restype = C.c_float
+        L.orc_rng_normal.argtypes = [P(RngState)]
+        L.orc_rng_normal.restype = C.c_float
+        L.orc_rand_vec.argtypes = [P(RngState), _f32p, _sz]
+        L.orc_rand_uniform_vec.argtypes = [P(RngState), _f32p, _sz]
+        L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_set_threads.restype = C.c_int
+        L.orc_get_threads.restype = C.c_int
+        L.orc_set_simd.argtypes = [C.c_int]
+        L.orc_set_simd.restype = C.c_int
+        L.orc_packed_a_len.argtypes = [_sz, _sz]
+        L.orc_packed_a_len.restype = _sz
+        L.orc_packed_b_len.argtypes = [_sz, _sz]
+        L.orc_packed_b_len.restype = _sz
+        L.orc_pack_a.argtypes = [_f32p, _sz, _sz, C.c_int, _f32p]
+        L.orc_pack_b.argtypes = [_f32p, _sz, _sz, C.c_int, _f32p]
+        L.orc_transpose_to_panel.argtypes = [_f32p, _sz, _sz, _f32p]
+        L.orc_micro_kernel.argtypes = [_sz, _f32p, _f32p, _f32p, _sz, _sz, _sz, C.c_int]
+        L.orc_matmul.argtypes = [_sz, _sz, _sz, _f32p, C.c_int, _f32p, C.c_int, _f32p, C.c_int]
+        L.orc_gemm_small.argtypes = L.orc_matmul.argtypes
+        L.orc_matmul_dw.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p]
+        L.orc_fold_leaves.argtypes = [_sz, C.c_int, P(_sz), P(_sz), _sz]
+        L.orc_fold_leaves.restype = _sz
+        sp = P(ConvSpec)
+        L.orc_rowmap.argtypes = [sp, _u32p]
+        L.orc_im2col.argtypes = [sp, _f32p, _f32p]
+        L.orc_conv_forward_image.argtypes = [sp, _f32p, _f32p, _f32p]
+        L.orc_conv_dx_image.argtypes = [sp, _f32p, _f32p, _f32p]
+        L.orc_conv_dw_image.argtypes = [sp, _f32p, _f32p, _f32p]
+        L.orc_conv2d_forward.argtypes = [sp, _sz, _f32p, _f32p, _f32p]
+        L.orc_conv2d_backward_w.argtypes = [sp, _sz, _f32p, _f32p, _f32p]
+        L.orc_conv2d_backward_x.argtypes = [sp, _sz, _f32p, _f32p, _f32p]
+        L.orc_rel_index.argtypes = [_sz, _sz, _sz, _sz, _u32p]
+        L.orc_rel_index.restype = _sz
+        ad = P(AttnDesc)
+        L.orc_attn_forward.argtypes = [ad, _sz, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]
+        L.orc_attn_backward.argtypes = [ad, _sz, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                        _f32p, _f32p, _f32p, _f32p]
+        L.orc_linear_forward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, C.c_void_p, _f32p]
+        L.orc_linear_backward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p,
+                                          C.c_void_p, _f32p]
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ---------------------------------------------------------------- rng.rs
+class Rng:
+    """Rng (rng.rs:3-66): xoshiro256++ seeded by splitmix64."""
+
+    def __init__(self, seed: int):
+        self.st = RngState()
+        lib().orc_rng_new(C.byref(self.st), C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF))
+
+    def next_u64(self) -> int:
+        return int(lib().orc_rng_next_u64(C.byref(self.st)))
+
+    def below(self, n: int) -> int:
+        return int(lib().orc_rng_below(C.byref(self.st), n))
+
+    def uniform(self) -> float:
+        return float(lib().orc_rng_uniform(C.byref(self.st)))
+
+    def normal(self) -> float:
+        return float(lib().orc_rng_normal(C.byref(self.st)))
+
+    def rand_vec(self, n: int) -> np.ndarray:
+        """rand_vec (rng.rs:70-72)."""
+        out = np.empty(n, np.float32)
+        if n:
+            lib().orc_rand_vec(C.byref(self.st), out, n)
+        return out
+
+    def uniform_vec(self, n: int) -> np.ndarray:
+        out = np.empty(n, np.float32)
+        if n:
+            lib().orc_rand_uniform_vec(C.byref(self.st), out, n)
+        return out
+
+
+class threads:
+    """Context manager: number of OpenMP workers of the parallel drivers."""
+
+    def __init__(self, n: int):
+        self.n = n
+
+    def __enter__(self):
+        self.old = lib().orc_set_threads(self.n)
+        return self
+
+    def __exit__(self, *a):
+        lib().orc_set_threads(self.old)
+
+
+def set_simd(on: bool) -> bool:
+    return bool(lib().orc_set_simd(1 if on else 0))
+
+
+# ---------------------------------------------------------------- gemm.rs
+def pack_a(a, m, k, transposed=False):
+    """PackedA::pack / pack_t (gemm.rs:54-113); zero where never written."""
+    out = np.zeros(lib().orc_packed_a_len(m, k), np.float32)
+    if out.size:
+        lib().orc_pack_a(_f(a).ravel(), m, k, int(transposed), out)
+    return out
+
+
+def pack_b(b, n, k, transposed=False):
+    """PackedB::pack / pack_t (gemm.rs:340-400); zero where never written."""
+    out = np.zeros(lib().orc_packed_b_len(n, k), np.float32)
+    if out.size:
+        lib().orc_pack_b(_f(b).ravel(), n, k, int(transposed), out)
+    return out
+
+
+def transpose_to_panel(src, lds, kc):
+    out = np.zeros(kc * NR, np.float32)
+    lib().orc_transpose_to_panel(_f(src).ravel(), lds, kc, out)
+    return out
+
+
+def matmul(m, n, k, a, at, b, bt, c=None, acc=False):
+    """matmul (gemm.rs:434-493).  Returns C [m*n] (flat)."""
+    c = np.zeros(m * n, np.float32) if c is None else _f(c).ravel().copy()
+    if m and n:
+        lib().orc_matmul(m, n, k, _f(a).ravel() if a.size else np.zeros(1, np.float32), int(at),
+                         _f(b).ravel() if b.size else np.zeros(1, np.float32), int(bt), c, int(acc))
+    return c
+
+
+def gemm_small(m, n, k, a, at, b, bt, c=None, acc=False):
+    """gemm_small (gemm.rs:500-545): k == 0 leaves C untouched."""
+    c = np.zeros(m * n, np.float32) if c is None else _f(c).ravel().copy()
+    one = np.zeros(1, np.float32)
+    lib().orc_gemm_small(m, n, k, _f(a).ravel() if a.size else one, int(at),
+                         _f(b).ravel() if b.size else one, int(bt),
+                         c if c.size else one, int(acc))
+    return c
+
+
+def matmul_dw(m, n, k, a, b, c):
+    """matmul_dw (gemm.rs:555-598): returns C + A^T B."""
+    c = _f(c).ravel().copy()
+    one = np.zeros(1, np.float32)
+    lib().orc_matmul_dw(m, n, k, _f(a).ravel() if a.size else one,
+                        _f(b).ravel() if b.size else one, c if c.size else one)
+    return c
+
+
+def fold_leaves(length, nthreads):
+    lo = (_sz * 256)()
+    hi = (_sz * 256)()
+    nl = lib().orc_fold_leaves(length, nthreads, lo, hi, 256)
+    return [(lo[i], hi[i]) for i in range(nl)]
+
+
+# ---------------------------------------------------------------- conv.rs
+def rowmap(sp: ConvSpec):
+    out = np.zeros(3 * sp.ckk, np.uint32)
+    lib().orc_rowmap(C.byref(sp), out)
+    return out.reshape(-1, 3)
+
+
+def im2col(sp: ConvSpec, x_img):
+    col = np.zeros(sp.ckk * sp.hw, np.float32)
+    lib().orc_im2col(C.byref(sp), _f(x_img).ravel(), col)
+    return col.reshape(sp.ckk, sp.hw)
+
+
+def conv2d_forward(sp: ConvSpec, n, x, w):
+    """Conv2d::forward (nn.rs:166-185) -> y [n, cout, oh, ow]."""
+    y = np.empty(n * sp.cout * sp.hw, np.float32)
+    lib().orc_conv2d_forward(C.byref(sp), n, _f(x).ravel(), _f(w).ravel(), y)
+    return y.reshape(n, sp.cout, sp.oh, sp.ow)
+
+
+def conv2d_backward_w(sp: ConvSpec, n, dy, x, dw=None):
+    """Conv2d::backward_w (nn.rs:193-227): returns dw + sum_i dW_i."""
+    dw = np.zeros(sp.cout * sp.ckk, np.float32) if dw is None else _f(dw).ravel().copy()
+    lib().orc_conv2d_backward_w(C.byref(sp), n, _f(dy).ravel(), _f(x).ravel(), dw)
+    return dw.reshape(sp.cout, sp.ckk)
+
+
+def conv2d_backward_x(sp: ConvSpec, n, dy, w):
+    """dX half of Conv2d::backward (nn.rs:230-250) -> dx [n, cin, h, w]."""
+    dx = np.empty(n * sp.cin * sp.h * sp.w, np.float32)
+    lib().orc_conv2d_backward_x(C.byref(sp), n, _f(dy).ravel(), _f(w).ravel(), dx)
+    return dx.reshape(n, sp.cin, sp.h, sp.w)
+
+
+# ---------------------------------------------------------------- attn.rs
+def rel_index(th, tw, mh, mw):
+    """rel_index (attn.rs:53-72) -> (idx [th*tw*mh*mw] u32, nrel)."""
+    idx = np.zeros(th * tw * mh * mw, np.uint32)
+    nrel = lib().orc_rel_index(th, tw, mh, mw, idx)
+    return idx, int(nrel)
+
+
+def attn_desc(h, dh, tq, tk, qstride, qoff, kvstride, koff, voff, relidx, nrel, mask_diag):
+    relidx = np.ascontiguousarray(relidx, np.uint32)
+    d = AttnDesc(h, dh, tq, tk, qstride, qoff, kvstride, koff, voff, nrel,
+                 relidx.ctypes.data_as(C.POINTER(C.c_uint32)), int(mask_diag))
+    d._keep = relidx
+    return d
+
+
+def attn_forward(d: AttnDesc, n, q, kv, tau, rel):
+    """Core::forward (attn.rs:148-223) -> (p [n,h,tq,tk], o [n,tq,h*dh])."""
+    p = np.empty(n * d.h * d.tq * d.tk, np.float32)
+    o = np.empty(n * d.tq * d.h * d.dh, np.float32)
+    lib().orc_attn_forward(C.byref(d), n, _f(q).ravel(), _f(kv).ravel(), _f(tau).ravel(),
+                           _f(rel).ravel(), p, o)
+    return p, o
+
+
+def attn_backward(d: AttnDesc, n, q, kv, tau, p, dout, dq, dkv, dtau, drel):
+    """Core::backward (attn.rs:226-343): returns updated (dq, dkv, dtau, drel)."""
+    dq, dkv = _f(dq).ravel().copy(), _f(dkv).ravel().copy()
+    dtau, drel = _f(dtau).ravel().copy(), _f(drel).ravel().copy()
+    lib().orc_attn_backward(C.byref(d), n, _f(q).ravel(), _f(kv).ravel(), _f(tau).ravel(),
+                            _f(p).ravel(), _f(dout).ravel(), dq, dkv, dtau, drel)
+    return dq, dkv, dtau, drel
+
+
+# ---------------------------------------------------------------- linear.rs
+def linear_forward(rows, fin, fout, x, w, b=None):
+    y = np.empty(rows * fout, np.float32)
+    bb = _f(b).ravel() if b is not None else None
+    lib().orc_linear_forward(rows, fin, fout, _f(x).ravel(), _f(w).ravel(),
+                             bb.ctypes.data if bb is not None else None, y)
+    return y
+
+
+def linear_backward(rows, fin, fout, dy, x, w, dw, db=None):
+    """Returns (dw', db', dx)."""
+    dw = _f(dw).ravel().copy()
+    db = _f(db).ravel().copy() if db is not None else None
+    dx = np.empty(rows * fin, np.float32)
+    lib().orc_linear_backward(rows, fin, fout, _f(dy).ravel(), _f(x).ravel(), _f(w).ravel(), dw,
+                              db.ctypes.data if db is not None else None, dx)
+    return dw, db, dx

@@ -1,0 +1,452 @@
+"""rustnn_amd -- MI355X (gfx950) GEMM core of rustnn behind a C ABI.
+
+The product is ``librnn.so`` (HIP kernels + C ABI, ``include/rnn.h``).  This
+module binds it with ctypes for Python callers (tests, bench) and mirrors the
+reference's host interface for the hot path:
+
+* ``matmul`` / ``gemm_small_batched`` / ``matmul_dw``  -- gemm.rs:434, 500, 555
+* ``Conv2d`` (forward / backward_w / backward)          -- nn.rs:115-250
+* ``Linear`` (forward / backward)                       -- linear.rs:14-104
+* ``Core`` (forward / backward), ``rel_index``          -- attn.rs:21-343
+
+Device memory and streams come from PyTorch (plumbing only): every array
+argument is a float32 CUDA tensor, passed to the library as a raw device
+pointer.  There is no CPU fallback: without a built ``librnn.so`` or without a
+GPU every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+import threading
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librnn.so")
+HEADER = os.path.join(HERE, "..", "include", "rnn.h")
+
+RNN_OK, RNN_E_INVALID, RNN_E_NULL, RNN_E_HIP, RNN_E_NOMEM, RNN_E_UNSUPPORTED = 0, -1, -2, -3, -4, -5
+
+_sz = C.c_size_t
+_vp = C.c_void_p
+_i = C.c_int
+_u32 = C.c_uint32
+
+
+class RnnError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"rnn status {status}: {msg}")
+        self.status = status
+
+
+class ConvSpec(C.Structure):
+    """rnn_conv_spec = ConvSpec (conv.rs:9-20)."""
+    _fields_ = [(n, _u32) for n in ("cin", "cout", "k", "stride", "pad", "h", "w", "oh", "ow")]
+
+    @classmethod
+    def make(cls, cin, cout, k, stride, pad, h, w):
+        sp = cls()
+        rc = lib().rnn_conv_spec_init(C.byref(sp), cin, cout, k, stride, pad, h, w)
+        if rc:
+            raise ValueError(f"invalid conv spec cin={cin} cout={cout} k={k} s={stride} "
+                             f"p={pad} {h}x{w}")
+        return sp
+
+    @property
+    def ckk(self):
+        return self.cin * self.k * self.k
+
+    @property
+    def hw(self):
+        return self.oh * self.ow
+
+
+class AttnDesc(C.Structure):
+    """rnn_attn_desc = Core (attn.rs:74-84) + forward/backward strides."""
+    _fields_ = [("h", _u32), ("dh", _u32), ("tq", _u32), ("tk", _u32),
+                ("qstride", _sz), ("qoff", _sz), ("kvstride", _sz), ("koff", _sz),
+                ("voff", _sz), ("nrel", _u32), ("relidx", C.POINTER(_u32)), ("mask_diag", _i)]
+
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def lib():
+    """Loads librnn.so.  Raises if it has not been built (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m rustnn_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        P = C.POINTER
+        sigs = {
+            "rnn_ctx_create": (_i, [_i, P(_vp)]),
+            "rnn_ctx_destroy": (_i, [_vp]),
+            "rnn_ctx_set_stream": (_i, [_vp, _vp]),
+            "rnn_ctx_stream": (_vp, [_vp]),
+            "rnn_ctx_synchronize": (_i, [_vp]),
+            "rnn_ctx_last_error": (C.c_char_p, [_vp]),
+            "rnn_status_string": (C.c_char_p, [_i]),
+            "rnn_ctx_workspace_bytes": (_sz, [_vp]),
+            "rnn_matmul": (_i, [_vp, _sz, _sz, _sz, _vp, _i, _vp, _i, _vp, _i]),
+            "rnn_gemm_small_batched": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _i, _vp, _sz, _i,
+                                            _vp, _sz, _i]),
+            "rnn_matmul_dw": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp]),
+            "rnn_conv_spec_init": (_i, [P(ConvSpec), _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
+            "rnn_conv2d_forward": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
+            "rnn_conv2d_backward_w": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
+            "rnn_conv2d_backward_x": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
+            "rnn_rel_index": (_i, [_u32, _u32, _u32, _u32, P(_u32), P(_u32)]),
+            "rnn_attn_forward": (_i, [_vp, P(AttnDesc), _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_attn_backward": (_i, [_vp, P(AttnDesc), _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                       _vp, _vp]),
+            "rnn_linear_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "rnn_linear_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_dbg_im2col": (_i, [_vp, P(ConvSpec), _vp, _vp]),
+            "rnn_dbg_pack_a": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
+            "rnn_dbg_pack_b": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
+            "rnn_dbg_rel_index": (_i, [_vp, _u32, _u32, _u32, _u32, _vp]),
+        }
+        for name, (res, args) in sigs.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+        return _lib
+
+
+def declared_symbols(header: str = HEADER):
+    """Names of the functions include/rnn.h declares."""
+    import re
+    txt = open(header).read()
+    return sorted(set(re.findall(r"^\s*(?:int|void \*|const char \*|size_t)\s+(rnn_\w+)\s*\(",
+                                 txt, re.M)))
+
+
+# ------------------------------------------------------------------ context
+class Context:
+    """One device, one stream, one growing workspace (rnn_ctx)."""
+
+    def __init__(self, device: int = 0, stream=None):
+        import torch
+        if not torch.cuda.is_available():
+            raise RuntimeError("rustnn_amd needs a ROCm GPU (torch.cuda.is_available() is False)")
+        self.device = device
+        h = _vp()
+        rc = lib().rnn_ctx_create(device, C.byref(h))
+        if rc:
+            raise RnnError(rc, lib().rnn_status_string(rc).decode())
+        self.h = h
+        if stream is None:
+            with torch.cuda.device(device):
+                stream = torch.cuda.current_stream()
+        self.set_stream(stream)
+
+    def set_stream(self, stream):
+        ptr = stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream or 0)
+        self.check(lib().rnn_ctx_set_stream(self.h, _vp(ptr)))
+
+    def stream_ptr(self) -> int:
+        return lib().rnn_ctx_stream(self.h) or 0
+
+    def check(self, rc: int):
+        if rc != RNN_OK:
+            raise RnnError(rc, lib().rnn_ctx_last_error(self.h).decode() or
+                           lib().rnn_status_string(rc).decode())
+
+    def synchronize(self):
+        self.check(lib().rnn_ctx_synchronize(self.h))
+
+    def workspace_bytes(self) -> int:
+        return int(lib().rnn_ctx_workspace_bytes(self.h))
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().rnn_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_ctx = {}
+
+
+def default_ctx(device: int = 0) -> Context:
+    c = _ctx.get(device)
+    if c is None:
+        c = _ctx[device] = Context(device)
+    return c
+
+
+def _ptr(t, need: int, name: str):
+    """Device pointer of a float32/uint32 CUDA tensor holding >= need elements."""
+    if t is None:
+        return None
+    import torch
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a CUDA tensor")
+    if t.dtype not in (torch.float32, torch.uint32, torch.int32):
+        raise TypeError(f"{name} must be float32 (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.numel() < need:
+        raise ValueError(f"{name} has {t.numel()} elements, needs {need}")
+    return _vp(t.data_ptr()) if t.numel() else None
+
+
+def _new(n, like=None, device=0):
+    import torch
+    dev = like.device if like is not None else torch.device("cuda", device)
+    return torch.empty(n, dtype=torch.float32, device=dev)
+
+
+# ------------------------------------------------------------------ gemm.rs
+def matmul(m, n, k, a, at, b, bt, c, acc=False, ctx=None):
+    """matmul (gemm.rs:434-493): c[m*n] = op(a) op(b) (+ c)."""
+    ctx = ctx or default_ctx()
+    if m == 0 or n == 0:
+        return c
+    ctx.check(lib().rnn_matmul(ctx.h, m, n, k, _ptr(a, m * k, "a"), int(at),
+                               _ptr(b, k * n, "b"), int(bt), _ptr(c, m * n, "c"), int(acc)))
+    return c
+
+
+def gemm_small_batched(count, m, n, k, a, stride_a, at, b, stride_b, bt, c, stride_c, acc=False,
+                       ctx=None):
+    """gemm_small (gemm.rs:500-545) over `count` strided problems in one launch."""
+    ctx = ctx or default_ctx()
+    if count == 0 or m == 0 or n == 0 or k == 0:
+        return c
+    need = lambda s, e: (count - 1) * s + e
+    ctx.check(lib().rnn_gemm_small_batched(
+        ctx.h, count, m, n, k, _ptr(a, need(stride_a, m * k), "a"), stride_a, int(at),
+        _ptr(b, need(stride_b, k * n), "b"), stride_b, int(bt),
+        _ptr(c, need(stride_c, m * n), "c"), stride_c, int(acc)))
+    return c
+
+
+def matmul_dw(m, n, k, a, b, c, ctx=None):
+    """matmul_dw (gemm.rs:555-598): c[m*n] += a^T b with a [k x m], b [k x n]."""
+    ctx = ctx or default_ctx()
+    if m == 0 or n == 0 or k == 0:
+        return c
+    ctx.check(lib().rnn_matmul_dw(ctx.h, m, n, k, _ptr(a, k * m, "a"), _ptr(b, k * n, "b"),
+                                  _ptr(c, m * n, "c")))
+    return c
+
+
+# ------------------------------------------------------------------ conv.rs
+def conv2d_forward(sp: ConvSpec, n, x, w, y=None, ctx=None):
+    ctx = ctx or default_ctx()
+    y = _new(n * sp.cout * sp.hw, x) if y is None else y
+    ctx.check(lib().rnn_conv2d_forward(ctx.h, C.byref(sp), n, _ptr(x, n * sp.cin * sp.h * sp.w, "x"),
+                                       _ptr(w, sp.cout * sp.ckk, "w"),
+                                       _ptr(y, n * sp.cout * sp.hw, "y")))
+    return y
+
+
+def conv2d_backward_w(sp: ConvSpec, n, dy, x, dw, ctx=None):
+    ctx = ctx or default_ctx()
+    ctx.check(lib().rnn_conv2d_backward_w(ctx.h, C.byref(sp), n,
+                                          _ptr(dy, n * sp.cout * sp.hw, "dy"),
+                                          _ptr(x, n * sp.cin * sp.h * sp.w, "x"),
+                                          _ptr(dw, sp.cout * sp.ckk, "dw")))
+    return dw
+
+
+def conv2d_backward_x(sp: ConvSpec, n, dy, w, dx=None, ctx=None):
+    ctx = ctx or default_ctx()
+    dx = _new(n * sp.cin * sp.h * sp.w, dy) if dx is None else dx
+    ctx.check(lib().rnn_conv2d_backward_x(ctx.h, C.byref(sp), n,
+                                          _ptr(dy, n * sp.cout * sp.hw, "dy"),
+                                          _ptr(w, sp.cout * sp.ckk, "w"),
+                                          _ptr(dx, n * sp.cin * sp.h * sp.w, "dx")))
+    return dx
+
+
+class Conv2d:
+    """Conv2d (nn.rs:115-250) on the device: w is [cout, cin*k*k] (RowMap order),
+    Kaiming-initialised as nn.rs:95-100 when an Rng-compatible generator is
+    given.  forward caches x for the backward (nn.rs:181-183)."""
+
+    def __init__(self, cin, cout, k, stride, pad, w=None, device=0, ctx=None):
+        import torch
+        self.cin, self.cout, self.k, self.stride, self.pad = cin, cout, k, stride, pad
+        self.ctx = ctx or default_ctx(device)
+        fan_in = cin * k * k
+        if w is None:
+            w = torch.randn(cout * fan_in, device=f"cuda:{device}") * math.sqrt(2.0 / fan_in)
+        self.w = w.contiguous()
+        self.g = torch.zeros_like(self.w)
+        self.x = None
+        self.xshape = None
+
+    def spec(self, h, w):
+        """Conv2d::spec (nn.rs:152-164)."""
+        return ConvSpec.make(self.cin, self.cout, self.k, self.stride, self.pad, h, w)
+
+    def forward(self, x, n, h, w, train=True):
+        sp = self.spec(h, w)
+        y = conv2d_forward(sp, n, x, self.w, ctx=self.ctx)
+        if train:
+            self.x, self.xshape = x, (n, h, w)
+        return y
+
+    def backward_w(self, dy):
+        n, h, w = self.xshape
+        conv2d_backward_w(self.spec(h, w), n, dy, self.x, self.g, ctx=self.ctx)
+
+    def backward(self, dy):
+        """Returns dX and accumulates dW (nn.rs:230-250)."""
+        self.backward_w(dy)
+        n, h, w = self.xshape
+        return conv2d_backward_x(self.spec(h, w), n, dy, self.w, ctx=self.ctx)
+
+
+# ------------------------------------------------------------------ attn.rs
+def rel_index(th, tw, mh, mw):
+    """rel_index (attn.rs:53-72) -> (np.uint32 [th*tw*mh*mw], nrel)."""
+    idx = np.zeros(th * tw * mh * mw, np.uint32)
+    nrel = _u32()
+    rc = lib().rnn_rel_index(th, tw, mh, mw, idx.ctypes.data_as(C.POINTER(_u32)), C.byref(nrel))
+    if rc:
+        raise ValueError("rel_index: invalid grid")
+    return idx, int(nrel.value)
+
+
+class Core:
+    """Core (attn.rs:74-343): per (image, head) attention with LSA temperature,
+    2-D relative bias and optional diagonal mask."""
+
+    def __init__(self, h, dh, tq, tk, relidx, nrel, mask_diag, ctx=None):
+        self.h, self.dh, self.tq, self.tk = h, dh, tq, tk
+        self.relidx = np.ascontiguousarray(relidx, np.uint32)
+        self.nrel, self.mask_diag = nrel, bool(mask_diag)
+        self.ctx = ctx or default_ctx()
+
+    def desc(self, qstride, qoff, kvstride, koff, voff):
+        d = AttnDesc(self.h, self.dh, self.tq, self.tk, qstride, qoff, kvstride, koff, voff,
+                     self.nrel, self.relidx.ctypes.data_as(C.POINTER(_u32)), int(self.mask_diag))
+        d._keep = self.relidx
+        return d
+
+    def forward(self, n, q, qstride, qoff, kv, kvstride, koff, voff, tau, rel, p=None, o=None):
+        """Core::forward (attn.rs:148-223) -> (p [n,h,tq,tk], o [n,tq,h*dh])."""
+        d = self.desc(qstride, qoff, kvstride, koff, voff)
+        p = _new(n * self.h * self.tq * self.tk, q) if p is None else p
+        o = _new(n * self.tq * self.h * self.dh, q) if o is None else o
+        nq = (n * self.tq - 1) * qstride + qoff + self.h * self.dh if n else 0
+        nkv = (n * self.tk - 1) * kvstride + max(koff, voff) + self.h * self.dh if n else 0
+        self.ctx.check(lib().rnn_attn_forward(
+            self.ctx.h, C.byref(d), n, _ptr(q, nq, "q"), _ptr(kv, nkv, "kv"),
+            _ptr(tau, self.h, "tau"), _ptr(rel, self.h * self.nrel, "rel"),
+            _ptr(p, n * self.h * self.tq * self.tk, "p"), _ptr(o, n * self.tq * self.h * self.dh, "o")))
+        return p, o
+
+    def backward(self, n, q, qstride, qoff, kv, kvstride, koff, voff, tau, p, dout, dq, dkv, dtau,
+                 drel):
+        """Core::backward (attn.rs:226-343): accumulates into dq, dkv, dtau, drel."""
+        d = self.desc(qstride, qoff, kvstride, koff, voff)
+        nq = (n * self.tq - 1) * qstride + qoff + self.h * self.dh if n else 0
+        nkv = (n * self.tk - 1) * kvstride + max(koff, voff) + self.h * self.dh if n else 0
+        self.ctx.check(lib().rnn_attn_backward(
+            self.ctx.h, C.byref(d), n, _ptr(q, nq, "q"), _ptr(kv, nkv, "kv"),
+            _ptr(tau, self.h, "tau"), _ptr(p, n * self.h * self.tq * self.tk, "p"),
+            _ptr(dout, n * self.tq * self.h * self.dh, "dout"), _ptr(dq, nq, "dq"),
+            _ptr(dkv, nkv, "dkv"), _ptr(dtau, self.h, "dtau"),
+            _ptr(drel, self.h * self.nrel, "drel")))
+
+
+# ------------------------------------------------------------------ linear.rs
+def linear_forward(rows, fin, fout, x, w, b=None, y=None, ctx=None):
+    ctx = ctx or default_ctx()
+    y = _new(rows * fout, x) if y is None else y
+    ctx.check(lib().rnn_linear_forward(ctx.h, rows, fin, fout, _ptr(x, rows * fin, "x"),
+                                       _ptr(w, fout * fin, "w"), _ptr(b, fout, "b"),
+                                       _ptr(y, rows * fout, "y")))
+    return y
+
+
+def linear_backward(rows, fin, fout, dy, x, w, dw, db=None, dx=None, ctx=None):
+    ctx = ctx or default_ctx()
+    dx = _new(rows * fin, dy) if dx is None else dx
+    ctx.check(lib().rnn_linear_backward(ctx.h, rows, fin, fout, _ptr(dy, rows * fout, "dy"),
+                                        _ptr(x, rows * fin, "x"), _ptr(w, fout * fin, "w"),
+                                        _ptr(dw, fout * fin, "dw"), _ptr(db, fout, "db"),
+                                        _ptr(dx, rows * fin, "dx")))
+    return dx
+
+
+class Linear:
+    """Linear (linear.rs:14-104): w [fout, fin], optional bias; forward caches x."""
+
+    def __init__(self, fin, fout, bias=True, w=None, b=None, device=0, ctx=None):
+        import torch
+        self.fin, self.fout = fin, fout
+        self.ctx = ctx or default_ctx(device)
+        dev = f"cuda:{device}"
+        self.w = (w if w is not None else torch.randn(fout * fin, device=dev) * 0.02).contiguous()
+        self.b = (b if b is not None else torch.zeros(fout, device=dev)) if bias else None
+        self.gw = torch.zeros_like(self.w)
+        self.gb = torch.zeros_like(self.b) if bias else None
+        self.x, self.rows = None, 0
+
+    def forward(self, x, rows, train=True):
+        y = linear_forward(rows, self.fin, self.fout, x, self.w, self.b, ctx=self.ctx)
+        if train:
+            self.x, self.rows = x, rows
+        return y
+
+    def backward(self, dy):
+        return linear_backward(self.rows, self.fin, self.fout, dy, self.x, self.w, self.gw, self.gb,
+                               ctx=self.ctx)
+
+
+# ------------------------------------------------------------------ debug exports
+def dbg_im2col(sp: ConvSpec, x_img, ctx=None):
+    ctx = ctx or default_ctx()
+    col = _new(sp.ckk * sp.hw, x_img)
+    ctx.check(lib().rnn_dbg_im2col(ctx.h, C.byref(sp), _ptr(x_img, sp.cin * sp.h * sp.w, "x"),
+                                   _ptr(col, sp.ckk * sp.hw, "col")))
+    return col
+
+
+def packed_len(rows, k, r):
+    return ((k + 255) // 256) * 256 * ((rows + r - 1) // r) * r
+
+
+def dbg_pack_a(a, m, k, transposed=False, ctx=None):
+    import torch
+    ctx = ctx or default_ctx()
+    out = torch.zeros(packed_len(m, k, 6), dtype=torch.float32, device=a.device)
+    ctx.check(lib().rnn_dbg_pack_a(ctx.h, _ptr(a, m * k, "a"), m, k, int(transposed),
+                                   _ptr(out, out.numel(), "out")))
+    return out
+
+
+def dbg_pack_b(b, n, k, transposed=False, ctx=None):
+    import torch
+    ctx = ctx or default_ctx()
+    out = torch.zeros(packed_len(n, k, 16), dtype=torch.float32, device=b.device)
+    ctx.check(lib().rnn_dbg_pack_b(ctx.h, _ptr(b, n * k, "b"), n, k, int(transposed),
+                                   _ptr(out, out.numel(), "out")))
+    return out
+
+
+def dbg_rel_index(th, tw, mh, mw, ctx=None):
+    import torch
+    ctx = ctx or default_ctx()
+    out = torch.zeros(th * tw * mh * mw, dtype=torch.int32, device="cuda")
+    ctx.check(lib().rnn_dbg_rel_index(ctx.h, th, tw, mh, mw, _ptr(out, out.numel(), "idx")))
+    return out

@@ -1,0 +1,444 @@
+// Dense fp32 GEMM on gfx950 MFMA: matmul / gemm_small (batched) / matmul_dw
+// (split-K) / Linear, plus the PackedA / PackedB debug exports.
+//
+// Reference: gemm.rs (6x16 AVX2 micro-kernel over KC=256 packed panels,
+// parallel over 6-row C panels), linear.rs.  Here one workgroup owns a
+// BM x BN tile of C; its 4 waves each own a (BM/2) x (BN/2) sub-tile made of
+// 32x32 v_mfma_f32_32x32x2f32 accumulators.  A and B are staged through LDS
+// "k-contiguous" (row = m or n, 16 k values + 4 pad floats) so each lane
+// fetches the operands of 4 MFMA steps with one ds_read_b128; the k order
+// inside a 16-wide block is permuted identically for A and B
+// (step s of group g, lane half h  <->  k = 8g + 4h + s).
+#include "rnn_internal.h"
+
+namespace {
+
+constexpr int BK = 16;
+constexpr int LDK = BK + 4;  // padded row: conflict-free b128 reads/writes
+
+struct GemmArgs {
+    const float *a, *b;
+    float *c;
+    const float *bias;     // per output column, may be null
+    long long stride_a, stride_b, stride_c;  // per z
+    int M, N;
+    int kchunk, ktotal;    // problem z covers k = min(kchunk, ktotal - z*kchunk)
+    int lda, ldb, ldc;
+    int acc;               // C += result
+};
+
+// 4 consecutive elements starting at p[0], p[step], ... with bounds
+// (count valid), zero elsewhere.
+__device__ __forceinline__ float4 load4(const float *p, long long step, int valid, bool vec) {
+    float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (vec && step == 1 && valid >= 4) return *reinterpret_cast<const float4 *>(p);
+    if (valid > 0) r.x = p[0];
+    if (valid > 1) r.y = p[step];
+    if (valid > 2) r.z = p[2 * step];
+    if (valid > 3) r.w = p[3 * step];
+    return r;
+}
+
+// Loads the BMxBK slab of an operand as k-quads.  TRANS=false: operand stored
+// [rows][k] (row-major, ld = row length); TRANS=true: stored [k][rows].
+template <int BM, bool TRANS, bool VEC>
+struct Slab {
+    static constexpr int Q = BM * 4 / 256;  // quads per thread
+    float4 r[Q];
+    __device__ __forceinline__ void load(const float *base, int ld, int row0, int rows, int k0,
+                                         int kz, int tid) {
+#pragma unroll
+        for (int j = 0; j < Q; j++) {
+            int idx = tid + 256 * j;
+            int m, kq;
+            if (!TRANS) {
+                kq = idx & 3;
+                m = idx >> 2;
+            } else {
+                m = idx % BM;
+                kq = idx / BM;
+            }
+            int row = row0 + m, k = k0 + 4 * kq;
+            int valid = (row < rows) ? min(4, kz - k) : 0;
+            if (!TRANS)
+                r[j] = load4(base + (long long)row * ld + k, 1, valid, VEC);
+            else
+                r[j] = load4(base + (long long)k * ld + row, ld, valid, false);
+        }
+    }
+    __device__ __forceinline__ void store(float *lds, int tid) const {
+#pragma unroll
+        for (int j = 0; j < Q; j++) {
+            int idx = tid + 256 * j;
+            int m, kq;
+            if (!TRANS) {
+                kq = idx & 3;
+                m = idx >> 2;
+            } else {
+                m = idx % BM;
+                kq = idx / BM;
+            }
+            *reinterpret_cast<float4 *>(lds + m * LDK + 4 * kq) = r[j];
+        }
+    }
+};
+
+template <int BM, int BN, bool AT, bool BT, bool VEC>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+    __shared__ float As[2][BM * LDK];
+    __shared__ float Bs[2][BN * LDK];
+    constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const long long z = blockIdx.z;
+    const float *A = g.a + z * g.stride_a;
+    const float *B = g.b + z * g.stride_b;
+    float *Cp = g.c + z * g.stride_c;
+    const int kz = min(g.kchunk, g.ktotal - (int)z * g.kchunk);
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+
+    Slab<BM, AT, VEC> sa;
+    Slab<BN, !BT, VEC> sb;  // B^T stored [n][k] is the "rows = n" layout
+    const int nk = (kz + BK - 1) / BK;
+    if (nk > 0) {
+        sa.load(A, g.lda, m0, g.M, 0, kz, tid);
+        sb.load(B, g.ldb, n0, g.N, 0, kz, tid);
+        sa.store(As[0], tid);
+        sb.store(Bs[0], tid);
+    }
+    __syncthreads();
+    const int lr = lane & 31, lh = lane >> 5;
+    for (int it = 0; it < nk; it++) {
+        const int buf = it & 1;
+        if (it + 1 < nk) {
+            sa.load(A, g.lda, m0, g.M, (it + 1) * BK, kz, tid);
+            sb.load(B, g.ldb, n0, g.N, (it + 1) * BK, kz, tid);
+        }
+#pragma unroll
+        for (int gk = 0; gk < 2; gk++) {
+            float4 af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                af[i] = *reinterpret_cast<const float4 *>(
+                    &As[buf][(wm * WTM + i * 32 + lr) * LDK + 8 * gk + 4 * lh]);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                bf[j] = *reinterpret_cast<const float4 *>(
+                    &Bs[buf][(wn * WTN + j * 32 + lr) * LDK + 8 * gk + 4 * lh]);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+        if (it + 1 < nk) {
+            sa.store(As[buf ^ 1], tid);
+            sb.store(Bs[buf ^ 1], tid);
+        }
+        __syncthreads();
+    }
+    // 32x32 accumulator layout: column lane%32, row 8*(v/4) + 4*(lane/32) + v%4.
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                int row = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                int col = n0 + wn * WTN + j * 32 + lr;
+                if (row < g.M && col < g.N) {
+                    float val = acc[i][j][v];
+                    if (g.bias) val += g.bias[col];
+                    float *cp = Cp + (long long)row * g.ldc + col;
+                    if (g.acc) val = *cp + val;
+                    *cp = val;
+                }
+            }
+}
+
+__global__ void fill_kernel(float *p, long long n, float v) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long st = (long long)gridDim.x * blockDim.x;
+    for (; i < n; i += st) p[i] = v;
+}
+
+// out[e] (+)= sum_z part[z*len + e], z in order (deterministic split-K reduce).
+__global__ void splitk_reduce_kernel(const float *part, int nz, long long len, float *out,
+                                     int accumulate) {
+    long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= len) return;
+    float s = part[e];
+    for (int zz = 1; zz < nz; zz++) s += part[(long long)zz * len + e];
+    out[e] = accumulate ? out[e] + s : s;
+}
+
+// Column sums, stage 1: part[rb][c] = sum of rows [rb*rpb, ...) of column c.
+__global__ void colsum_partial_kernel(const float *x, long long rows, int cols, long long rpb,
+                                      float *part) {
+    int c = blockIdx.x * blockDim.x + threadIdx.x;
+    long long rb = blockIdx.y;
+    if (c >= cols) return;
+    long long r0 = rb * rpb, r1 = min(rows, r0 + rpb);
+    float s = 0.f;
+    for (long long r = r0; r < r1; r++) s += x[r * cols + c];
+    part[rb * cols + c] = s;
+}
+
+// PackedA::pack / pack_t layout (gemm.rs:54-113): element e of block q =
+// panel i, position p*MR + r -> A[i*MR + r][q*KC + p].
+__global__ void pack_a_kernel(const float *a, long long m, long long k, int transposed, float *out,
+                              long long mpad, long long total) {
+    const int MR = 6, KC = 256;
+    long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= total) return;
+    long long q = e / (KC * mpad), rem = e % (KC * mpad);
+    long long kc = min((long long)KC, k - q * KC);
+    if (rem >= kc * mpad) return;  // never written by the reference
+    long long i = rem / (kc * MR), w = rem % (kc * MR), p = w / MR, r = w % MR;
+    long long row = i * MR + r, col = q * KC + p;
+    float v = 0.f;
+    if (row < m) v = transposed ? a[col * m + row] : a[row * k + col];
+    out[e] = v;
+}
+
+// PackedB::pack / pack_t layout (gemm.rs:340-400): panel j, position p*NR + t
+// -> B[q*KC + p][j*NR + t].
+__global__ void pack_b_kernel(const float *b, long long n, long long k, int transposed, float *out,
+                              long long npad, long long total) {
+    const int NR = 16, KC = 256;
+    long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= total) return;
+    long long q = e / (KC * npad), rem = e % (KC * npad);
+    long long kc = min((long long)KC, k - q * KC);
+    if (rem >= kc * npad) return;
+    long long j = rem / (kc * NR), w = rem % (kc * NR), p = w / NR, t = w % NR;
+    long long col = j * NR + t, row = q * KC + p;
+    float v = 0.f;
+    if (col < n) v = transposed ? b[col * k + row] : b[row * n + col];
+    out[e] = v;
+}
+
+template <int BM, int BN, bool AT, bool BT>
+int launch_t(rnn_ctx *ctx, const GemmArgs &g, int count, bool vec) {
+    dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM, count);
+    if (vec)
+        hipLaunchKernelGGL((gemm_kernel<BM, BN, AT, BT, true>), grid, dim3(256), 0, ctx->stream, g);
+    else
+        hipLaunchKernelGGL((gemm_kernel<BM, BN, AT, BT, false>), grid, dim3(256), 0, ctx->stream, g);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+template <int BM, int BN>
+int launch_bm(rnn_ctx *ctx, const GemmArgs &g, int count, bool at, bool bt, bool vec) {
+    if (!at && !bt) return launch_t<BM, BN, false, false>(ctx, g, count, vec);
+    if (!at && bt) return launch_t<BM, BN, false, true>(ctx, g, count, vec);
+    if (at && !bt) return launch_t<BM, BN, true, false>(ctx, g, count, vec);
+    return launch_t<BM, BN, true, true>(ctx, g, count, vec);
+}
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+// Enqueues `count` GEMMs C_z = op(A_z) op(B_z) (+C_z) (+bias) with problem z
+// covering k = min(kchunk, ktotal - z*kchunk) (kchunk = k for plain batches).
+static int gemm_enqueue(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t kchunk,
+                        size_t ktotal, const float *a, size_t stride_a, int lda, int at,
+                        const float *b, size_t stride_b, int ldb, int bt, float *c,
+                        size_t stride_c, int ldc, int acc, const float *bias) {
+    if (m > INT32_MAX || n > INT32_MAX || ktotal > INT32_MAX || count > 65535)
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "gemm: dimension beyond 32-bit tile indexing");
+    GemmArgs g;
+    g.a = a;
+    g.b = b;
+    g.c = c;
+    g.bias = bias;
+    g.stride_a = (long long)stride_a;
+    g.stride_b = (long long)stride_b;
+    g.stride_c = (long long)stride_c;
+    g.M = (int)m;
+    g.N = (int)n;
+    g.kchunk = (int)kchunk;
+    g.ktotal = (int)ktotal;
+    g.lda = lda;
+    g.ldb = ldb;
+    g.ldc = ldc;
+    g.acc = acc;
+    // float4 loads along k need 16-byte aligned rows of the k-contiguous operands.
+    bool vec = true;
+    if (!at) vec = vec && aligned16(a) && (lda % 4 == 0) && (stride_a % 4 == 0);
+    if (bt) vec = vec && aligned16(b) && (ldb % 4 == 0) && (stride_b % 4 == 0);
+    size_t tiles128 = rnn_div_up(m, 128) * rnn_div_up(n, 128) * count;
+    if (m >= 128 && n >= 128 && tiles128 >= (size_t)ctx->num_cus)
+        return launch_bm<128, 128>(ctx, g, (int)count, at, bt, vec);
+    return launch_bm<64, 64>(ctx, g, (int)count, at, bt, vec);
+}
+
+int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
+                    size_t stride_a, int at, const float *b, size_t stride_b, int bt, float *c,
+                    size_t stride_c, int acc, const float *bias) {
+    int lda = at ? (int)m : (int)k, ldb = bt ? (int)k : (int)n;
+    return gemm_enqueue(ctx, count, m, n, k, k * count, a, stride_a, lda, at, b, stride_b, ldb, bt,
+                        c, stride_c, (int)n, acc, bias);
+}
+
+static int fill(rnn_ctx *ctx, float *p, size_t len, float v) {
+    if (!len) return RNN_OK;
+    int blocks = (int)std::min<size_t>(rnn_div_up(len, 256), 4096);
+    hipLaunchKernelGGL(fill_kernel, dim3(blocks), dim3(256), 0, ctx->stream, p, (long long)len, v);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, float *out) {
+    // out[c] += sum_r x[r][c], two fixed-order stages.
+    size_t rpb = 256;
+    size_t nrb = rnn_div_up(rows, rpb);
+    if (nrb > 65535) {
+        rpb = rnn_div_up(rows, 65535);
+        nrb = rnn_div_up(rows, rpb);
+    }
+    float *part = (float *)rnn_workspace(ctx, nrb * cols * sizeof(float));
+    if (!part) return RNN_E_NOMEM;
+    hipLaunchKernelGGL(colsum_partial_kernel, dim3(rnn_div_up(cols, 256), nrb), dim3(256), 0,
+                       ctx->stream, x, (long long)rows, (int)cols, (long long)rpb, part);
+    RNN_LAUNCHED(ctx);
+    // stage 2: out[c] += sum over row blocks in order (columns are the "elements")
+    // part is [nrb][cols]: reduce along z = row block.
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rnn_div_up(cols, 256)), dim3(256), 0,
+                       ctx->stream, part, (int)nrb, (long long)cols, out, 1);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+extern "C" {
+
+int rnn_matmul(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, int at, const float *b,
+               int bt, float *c, int acc) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (m == 0 || n == 0) return RNN_OK;  // gemm.rs:446-448
+    if (!c) return rnn_fail(ctx, RNN_E_NULL, "matmul: c is null");
+    if (k == 0) return acc ? RNN_OK : fill(ctx, c, m * n, 0.f);  // gemm.rs:449-454
+    if (!a || !b) return rnn_fail(ctx, RNN_E_NULL, "matmul: a or b is null");
+    return rnn_gemm_launch(ctx, 1, m, n, k, a, 0, at, b, 0, bt, c, 0, acc, nullptr);
+}
+
+int rnn_gemm_small_batched(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k,
+                           const float *a, size_t stride_a, int at, const float *b,
+                           size_t stride_b, int bt, float *c, size_t stride_c, int acc) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (count == 0 || m == 0 || n == 0 || k == 0) return RNN_OK;  // k == 0: C untouched
+    if (!a || !b || !c) return rnn_fail(ctx, RNN_E_NULL, "gemm_small: null operand");
+    for (size_t z0 = 0; z0 < count; z0 += 65535) {
+        size_t cnt = std::min<size_t>(65535, count - z0);
+        int rc = rnn_gemm_launch(ctx, cnt, m, n, k, a + z0 * stride_a, stride_a, at,
+                                 b + z0 * stride_b, stride_b, bt, c + z0 * stride_c, stride_c,
+                                 acc, nullptr);
+        if (rc) return rc;
+    }
+    return RNN_OK;
+}
+
+int rnn_matmul_dw(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, const float *b,
+                  float *c) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (m == 0 || n == 0 || k == 0) return RNN_OK;  // gemm.rs:556-558
+    if (!a || !b || !c) return rnn_fail(ctx, RNN_E_NULL, "matmul_dw: null operand");
+    // Split K into z chunks (multiples of 16) so that tiles x chunks fills
+    // the chip, then add the chunk partials into C in a fixed order.
+    size_t tiles = rnn_div_up(m, 64) * rnn_div_up(n, 64);
+    size_t want = rnn_div_up(2 * (size_t)ctx->num_cus, tiles);
+    size_t maxz = std::max<size_t>(1, k / 256);
+    size_t nz = std::min(want, maxz);
+    nz = std::min<size_t>(nz, 64);
+    if (nz <= 1) {
+        int lda = (int)m, ldb = (int)n;
+        return gemm_enqueue(ctx, 1, m, n, k, k, a, 0, lda, 1, b, 0, ldb, 0, c, 0, (int)n, 1, nullptr);
+    }
+    size_t kchunk = rnn_round_up(rnn_div_up(k, nz), 16);
+    nz = rnn_div_up(k, kchunk);
+    float *part = (float *)rnn_workspace(ctx, nz * m * n * sizeof(float));
+    if (!part) return RNN_E_NOMEM;
+    int rc = gemm_enqueue(ctx, nz, m, n, kchunk, k, a, kchunk * m, (int)m, 1, b, kchunk * n, (int)n,
+                          0, part, m * n, (int)n, 0, nullptr);
+    if (rc) return rc;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rnn_div_up(m * n, 256)), dim3(256), 0,
+                       ctx->stream, part, (int)nz, (long long)(m * n), c, 1);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_linear_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
+                       const float *w, const float *b, float *y) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || fout == 0) return RNN_OK;
+    if (!x || !w || !y) return rnn_fail(ctx, RNN_E_NULL, "linear_forward: null operand");
+    if (fin == 0) {
+        int rc = fill(ctx, y, rows * fout, 0.f);
+        if (rc || !b) return rc;
+        return rnn_gemm_launch(ctx, 1, rows, fout, 0, x, 0, 0, w, 0, 1, y, 0, 1, b);
+    }
+    // y = x W^T (+ b fused in the epilogue)
+    return rnn_gemm_launch(ctx, 1, rows, fout, fin, x, 0, 0, w, 0, 1, y, 0, 0, b);
+}
+
+int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
+                        const float *x, const float *w, float *dw, float *db, float *dx) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (!dy || !x || !w || !dw || !dx)
+        return rnn_fail(ctx, RNN_E_NULL, "linear_backward: null operand");
+    // dW[fout, fin] += dY^T X (linear.rs:69)
+    int rc = rnn_matmul_dw(ctx, fout, fin, rows, dy, x, dw);
+    if (rc) return rc;
+    if (db && rows && fout) {
+        rc = rnn_colsum_launch(ctx, rows, fout, dy, db);  // linear.rs:70-89
+        if (rc) return rc;
+    }
+    // dX[rows, fin] = dY W (linear.rs:91-94)
+    return rnn_matmul(ctx, rows, fin, fout, dy, 0, w, 0, dx, 0);
+}
+
+int rnn_dbg_pack_a(rnn_ctx *ctx, const float *a, size_t m, size_t k, int transposed, float *out) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (m == 0 || k == 0) return RNN_OK;
+    if (!a || !out) return RNN_E_NULL;
+    size_t mpad = rnn_div_up(m, 6) * 6, total = rnn_div_up(k, 256) * 256 * mpad;
+    hipLaunchKernelGGL(pack_a_kernel, dim3(rnn_div_up(total, 256)), dim3(256), 0, ctx->stream, a,
+                       (long long)m, (long long)k, transposed, out, (long long)mpad,
+                       (long long)total);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_dbg_pack_b(rnn_ctx *ctx, const float *b, size_t n, size_t k, int transposed, float *out) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || k == 0) return RNN_OK;
+    if (!b || !out) return RNN_E_NULL;
+    size_t npad = rnn_div_up(n, 16) * 16, total = rnn_div_up(k, 256) * 256 * npad;
+    hipLaunchKernelGGL(pack_b_kernel, dim3(rnn_div_up(total, 256)), dim3(256), 0, ctx->stream, b,
+                       (long long)n, (long long)k, transposed, out, (long long)npad,
+                       (long long)total);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+}  // extern "C"

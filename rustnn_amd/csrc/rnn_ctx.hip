@@ -1,0 +1,167 @@
+// Context, stream, workspace and error reporting of librnn.so.
+//
+// Replaces the reference's process-wide rayon pool (main.rs:41-48) and the
+// thread-local / per-task packing scratch (gemm.rs:411-420, nn.rs:178,
+// attn.rs:170) with one device context: a stream and a device workspace that
+// only grows, so steady-state calls never allocate.
+#include "rnn_internal.h"
+
+#include <cstring>
+
+int rnn_fail(rnn_ctx *ctx, int code, const char *fmt, ...) {
+    if (ctx) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(ctx->err, sizeof(ctx->err), fmt, ap);
+        va_end(ap);
+    }
+    return code;
+}
+
+void *rnn_workspace(rnn_ctx *ctx, size_t bytes) {
+    bytes = rnn_round_up(bytes ? bytes : 256, 256);
+    if (bytes <= ctx->ws_bytes) return ctx->ws;
+    if (ctx->ws) {
+        // Earlier kernels on this stream may still read the old block.
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            rnn_fail(ctx, RNN_E_HIP, "hipStreamSynchronize: %s", hipGetErrorString(e));
+            return nullptr;
+        }
+        (void)hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+    }
+    size_t want = bytes + bytes / 4;  // headroom against creeping regrowth
+    hipError_t e = hipMalloc(&ctx->ws, want);
+    if (e != hipSuccess) {
+        ctx->ws = nullptr;
+        rnn_fail(ctx, RNN_E_NOMEM, "workspace hipMalloc(%zu): %s", want, hipGetErrorString(e));
+        return nullptr;
+    }
+    ctx->ws_bytes = want;
+    return ctx->ws;
+}
+
+extern "C" {
+
+const char *rnn_status_string(int s) {
+    switch (s) {
+        case RNN_OK: return "ok";
+        case RNN_E_INVALID: return "invalid argument";
+        case RNN_E_NULL: return "null pointer";
+        case RNN_E_HIP: return "HIP runtime error";
+        case RNN_E_NOMEM: return "out of device memory";
+        case RNN_E_UNSUPPORTED: return "unsupported shape";
+        default: return "unknown status";
+    }
+}
+
+int rnn_ctx_create(int device, rnn_ctx **out) {
+    if (!out) return RNN_E_NULL;
+    *out = nullptr;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) return RNN_E_HIP;
+    if (device < 0 || device >= ndev) return RNN_E_INVALID;
+    if (hipSetDevice(device) != hipSuccess) return RNN_E_HIP;
+    rnn_ctx *c = new rnn_ctx();
+    c->device = device;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) c->num_cus = prop.multiProcessorCount;
+    // A stream of default priority (non-blocking w.r.t. the null stream).
+    if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return RNN_E_HIP;
+    }
+    c->own_stream = true;
+    *out = c;
+    return RNN_OK;
+}
+
+int rnn_ctx_destroy(rnn_ctx *ctx) {
+    if (!ctx) return RNN_E_NULL;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->rel_dev) (void)hipFree(ctx->rel_dev);
+    if (ctx->rel_pinned) (void)hipHostFree(ctx->rel_pinned);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return RNN_OK;
+}
+
+int rnn_ctx_set_stream(rnn_ctx *ctx, void *stream) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (ctx->stream == (hipStream_t)stream) return RNN_OK;
+    // Work queued on the old stream may still use the workspace.
+    RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+    ctx->stream = (hipStream_t)stream;
+    ctx->own_stream = false;
+    return RNN_OK;
+}
+
+void *rnn_ctx_stream(rnn_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int rnn_ctx_synchronize(rnn_ctx *ctx) {
+    if (!ctx) return RNN_E_NULL;
+    RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return RNN_OK;
+}
+
+const char *rnn_ctx_last_error(rnn_ctx *ctx) { return ctx ? ctx->err : "null context"; }
+
+size_t rnn_ctx_workspace_bytes(rnn_ctx *ctx) { return ctx ? ctx->ws_bytes : 0; }
+
+int rnn_conv_spec_init(rnn_conv_spec *sp, uint32_t cin, uint32_t cout, uint32_t k,
+                       uint32_t stride, uint32_t pad, uint32_t h, uint32_t w) {
+    if (!sp) return RNN_E_NULL;
+    if (cin == 0 || cout == 0 || k == 0 || stride == 0 || h == 0 || w == 0) return RNN_E_INVALID;
+    if (k > h + 2 * pad || k > w + 2 * pad) return RNN_E_INVALID;
+    sp->cin = cin;
+    sp->cout = cout;
+    sp->k = k;
+    sp->stride = stride;
+    sp->pad = pad;
+    sp->h = h;
+    sp->w = w;
+    sp->oh = (h + 2 * pad - k) / stride + 1;  // Conv2d::out_dim (nn.rs:147-150)
+    sp->ow = (w + 2 * pad - k) / stride + 1;
+    return RNN_OK;
+}
+
+// rel_index (attn.rs:53-72) with RelGeom (attn.rs:21-46): equal grids give
+// offsets in [-(th-1), th-1]; a memory grid of twice the resolution measures
+// the offset in half tokens, 2*q - m.
+int rnn_rel_index(uint32_t th, uint32_t tw, uint32_t mh, uint32_t mw, uint32_t *idx,
+                  uint32_t *nrel) {
+    if (!idx || !nrel) return RNN_E_NULL;
+    if (th == 0 || tw == 0 || mh == 0 || mw == 0) return RNN_E_INVALID;
+    int64_t sy, sx, scale, oy, ox;
+    if (mh == th) {
+        sy = 2 * (int64_t)th - 1;
+        sx = 2 * (int64_t)tw - 1;
+        scale = 1;
+        oy = (int64_t)th - 1;
+        ox = (int64_t)tw - 1;
+    } else {
+        sy = 2 * ((int64_t)th - 1) + mh;
+        sx = 2 * ((int64_t)tw - 1) + mw;
+        scale = 2;
+        oy = (int64_t)mh - 1;
+        ox = (int64_t)mw - 1;
+    }
+    size_t z = 0;
+    for (int64_t qy = 0; qy < th; qy++)
+        for (int64_t qx = 0; qx < tw; qx++)
+            for (int64_t my = 0; my < mh; my++)
+                for (int64_t mx = 0; mx < mw; mx++) {
+                    int64_t dy = scale * qy - my + oy, dx = scale * qx - mx + ox;
+                    idx[z++] = (uint32_t)(dy * sx + dx);
+                }
+    *nrel = (uint32_t)(sy * sx);
+    return RNN_OK;
+}
+
+}  // extern "C"

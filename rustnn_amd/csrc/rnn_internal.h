@@ -1,0 +1,82 @@
+// Internal declarations shared by the HIP sources of librnn.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <mutex>
+#include <vector>
+
+#include "../../include/rnn.h"
+
+struct rnn_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    int num_cus = 256;
+    // Growing device workspace (split-K partials, packed weights, attention
+    // reductions).  Reallocated only when a call needs more; the stream is
+    // synchronised first so no in-flight kernel still reads the old block.
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+    // Attention relative-index tables (forward index + inverse CSR), uploaded
+    // once per distinct table.
+    std::vector<uint32_t> rel_host;  // last uploaded relidx (host copy)
+    uint32_t *rel_dev = nullptr;     // [tq*tk] relidx, then CSR rowptr[nrel+1], then pos[tq*tk]
+    size_t rel_cap = 0;              // u32 capacity of rel_dev
+    uint32_t *rel_pinned = nullptr;  // staging for the async upload
+    size_t rel_pinned_cap = 0;
+    uint32_t rel_nrel = 0;
+    std::recursive_mutex mu;
+    char err[512] = {0};
+};
+
+// Records a message and returns `code`.
+int rnn_fail(rnn_ctx *ctx, int code, const char *fmt, ...);
+
+#define RNN_HIP(ctx, expr)                                                              \
+    do {                                                                                \
+        hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return rnn_fail((ctx), RNN_E_HIP, "%s failed: %s (%s:%d)", #expr,           \
+                            hipGetErrorString(e_), __FILE__, __LINE__);                 \
+    } while (0)
+
+// Checks the launch status of the kernel just enqueued.
+#define RNN_LAUNCHED(ctx)                                                               \
+    do {                                                                                \
+        hipError_t e_ = hipGetLastError();                                              \
+        if (e_ != hipSuccess)                                                           \
+            return rnn_fail((ctx), RNN_E_HIP, "kernel launch failed: %s (%s:%d)",       \
+                            hipGetErrorString(e_), __FILE__, __LINE__);                 \
+    } while (0)
+
+// Returns a device workspace of at least `bytes` (256-byte aligned), or
+// nullptr after recording RNN_E_NOMEM / RNN_E_HIP in ctx.
+void *rnn_workspace(rnn_ctx *ctx, size_t bytes);
+
+// Bump allocator over one workspace block.
+struct WsCarve {
+    size_t off = 0;
+    size_t take(size_t bytes) {
+        size_t o = off;
+        off += (bytes + 255) & ~size_t(255);
+        return o;
+    }
+};
+
+static inline size_t rnn_div_up(size_t a, size_t b) { return (a + b - 1) / b; }
+static inline size_t rnn_round_up(size_t a, size_t b) { return rnn_div_up(a, b) * b; }
+
+// fp32 MFMA operand / accumulator vectors.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Entry points implemented in the kernel sources, called from the C ABI.
+int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
+                    size_t stride_a, int at, const float *b, size_t stride_b, int bt, float *c,
+                    size_t stride_c, int acc, const float *bias);
+int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, float *out);

@@ -1,0 +1,116 @@
+"""GPU parity: implicit-GEMM convolution (conv.rs forward_image / dx_image /
+dw_image through the Conv2d batch drivers, nn.rs:166-250) against the CPU
+oracle on identical seeded inputs, at the BASELINE config shapes and at the
+reference's gradcheck shapes (check.rs:505-509)."""
+import zlib
+
+import numpy as np
+import pytest
+
+from conftest import TOL, rel_frob, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+# (name, n, cin, cout, k, stride, pad, h)
+SHAPES = [
+    ("cfg0_3x3s1_32to32_32", 128, 32, 32, 3, 1, 1, 32),
+    ("cfg1_3x3s2_32to64_32", 128, 32, 64, 3, 2, 1, 32),
+    ("cfg1_3x3s1_64to64_16", 128, 64, 64, 3, 1, 1, 16),
+    ("cfg1_3x3s2_64to128_16", 128, 64, 128, 3, 2, 1, 16),
+    ("cfg1_3x3s1_128to128_8", 128, 128, 128, 3, 1, 1, 8),
+    ("cfg1_1x1s2_32to64_32", 128, 32, 64, 1, 2, 0, 32),
+    ("cfg1_1x1s2_64to128_16", 128, 64, 128, 1, 2, 0, 16),
+    ("stem_3x3s1_3to32_32", 16, 3, 32, 3, 1, 1, 32),
+    ("gc_3x3s1_3to4_6", 2, 3, 4, 3, 1, 1, 6),
+    ("gc_1x1s2_4to6_8", 2, 4, 6, 1, 2, 0, 8),
+    ("gc_3x3s2_4to5_7", 2, 4, 5, 3, 2, 1, 7),
+    ("odd_3x3s1_5to40_9", 3, 5, 40, 3, 1, 1, 9),
+    ("odd_3x3s2_34to33_11", 5, 34, 33, 3, 2, 1, 11),
+]
+
+
+def inputs(orc, sp, n, seed=7):
+    """BASELINE config 0 draw order: x ~ N(0,1), W Kaiming-normal, dY ~ N(0,1)."""
+    rng = orc.Rng(seed)
+    x = rng.rand_vec(n * sp.cin * sp.h * sp.w)
+    w = rng.rand_vec(sp.cout * sp.ckk) * np.float32(np.sqrt(2.0 / sp.ckk))
+    dy = rng.rand_vec(n * sp.cout * sp.hw)
+    return x, w, dy
+
+
+@pytest.mark.parametrize("name,n,cin,cout,k,s,p,h", SHAPES, ids=[s[0] for s in SHAPES])
+def test_conv_parity(rnn, orc, name, n, cin, cout, k, s, p, h):
+    sp = orc.ConvSpec.make(cin, cout, k, s, p, h, h)
+    gsp = rnn.ConvSpec.make(cin, cout, k, s, p, h, h)
+    x, w, dy = inputs(orc, sp, n)
+    dw0 = np.linspace(-1, 1, sp.cout * sp.ckk).astype(np.float32)
+    with orc.threads(8):
+        y_want = orc.conv2d_forward(sp, n, x, w)
+        dx_want = orc.conv2d_backward_x(sp, n, dy, w)
+        dw_want = orc.conv2d_backward_w(sp, n, dy, x, dw0).ravel()
+    X, W, DY = to_dev(x), to_dev(w), to_dev(dy)
+    y = rnn.conv2d_forward(gsp, n, X, W)
+    dx = rnn.conv2d_backward_x(gsp, n, DY, W)
+    dw = to_dev(dw0.copy())
+    rnn.conv2d_backward_w(gsp, n, DY, X, dw)
+    assert rel_frob(to_host(y), y_want) < TOL, "forward"
+    assert rel_frob(to_host(dx), dx_want) < TOL, "dx"
+    assert rel_frob(to_host(dw) - dw0, dw_want - dw0) < TOL, "dw"
+
+
+@pytest.mark.parametrize("name,n,cin,cout,k,s,p,h", SHAPES, ids=[s[0] for s in SHAPES])
+def test_conv_integer_bit_exact(rnn, orc, name, n, cin, cout, k, s, p, h):
+    """Integer-valued fp32 inputs make every sum exact, so any summation order
+    must reproduce the oracle bit for bit."""
+    sp = orc.ConvSpec.make(cin, cout, k, s, p, h, h)
+    gsp = rnn.ConvSpec.make(cin, cout, k, s, p, h, h)
+    r = np.random.default_rng(zlib.crc32(name.encode()))
+    x = r.integers(-2, 3, n * cin * h * h).astype(np.float32)
+    w = r.integers(-2, 3, sp.cout * sp.ckk).astype(np.float32)
+    dy = r.integers(-2, 3, n * sp.cout * sp.hw).astype(np.float32)
+    with orc.threads(8):
+        y_want = orc.conv2d_forward(sp, n, x, w)
+        dx_want = orc.conv2d_backward_x(sp, n, dy, w)
+        dw_want = orc.conv2d_backward_w(sp, n, dy, x)
+    X, W, DY = to_dev(x), to_dev(w), to_dev(dy)
+    assert np.array_equal(to_host(rnn.conv2d_forward(gsp, n, X, W)).ravel(), y_want.ravel())
+    assert np.array_equal(to_host(rnn.conv2d_backward_x(gsp, n, DY, W)).ravel(), dx_want.ravel())
+    dw = to_dev(np.zeros(sp.cout * sp.ckk, np.float32))
+    rnn.conv2d_backward_w(gsp, n, DY, X, dw)
+    assert np.array_equal(to_host(dw), dw_want.ravel())
+
+
+def test_conv_deterministic(rnn, orc):
+    sp = rnn.ConvSpec.make(32, 32, 3, 1, 1, 32, 32)
+    x, w, dy = inputs(orc, sp, 128, seed=99)
+    X, W, DY = to_dev(x), to_dev(w), to_dev(dy)
+    outs = []
+    for _ in range(2):
+        dw = to_dev(np.zeros(sp.cout * sp.ckk, np.float32))
+        rnn.conv2d_backward_w(sp, 128, DY, X, dw)
+        outs.append((to_host(rnn.conv2d_forward(sp, 128, X, W)),
+                     to_host(rnn.conv2d_backward_x(sp, 128, DY, W)), to_host(dw)))
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("cin,cout,k,s,p,h", [(3, 4, 3, 1, 1, 6), (4, 6, 1, 2, 0, 8),
+                                              (4, 5, 3, 2, 1, 7), (32, 32, 3, 1, 1, 32)])
+def test_im2col_bit_exact(rnn, orc, cin, cout, k, s, p, h):
+    sp = orc.ConvSpec.make(cin, cout, k, s, p, h, h)
+    gsp = rnn.ConvSpec.make(cin, cout, k, s, p, h, h)
+    x = orc.Rng(5).rand_vec(cin * h * h)
+    got = to_host(rnn.dbg_im2col(gsp, to_dev(x))).reshape(sp.ckk, sp.hw)
+    assert np.array_equal(got, orc.im2col(sp, x))
+
+
+def test_conv_bad_spec_raises(rnn):
+    sp = rnn.ConvSpec.make(4, 4, 3, 1, 1, 8, 8)
+    bad = rnn.ConvSpec()
+    for f in ("cin", "cout", "k", "stride", "pad", "h", "w", "oh", "ow"):
+        setattr(bad, f, getattr(sp, f))
+    bad.oh = 9  # does not match Conv2d::out_dim
+    x = to_dev(np.zeros(4 * 64, np.float32))
+    w = to_dev(np.zeros(4 * 36, np.float32))
+    with pytest.raises(rnn.RnnError):
+        rnn.conv2d_forward(bad, 1, x, w, y=to_dev(np.zeros(4 * 81, np.float32)))

@@ -1,0 +1,168 @@
+"""GPU parity: dense GEMM drivers (gemm.rs matmul / gemm_small / matmul_dw),
+the Linear layer (linear.rs) and the PackedA/PackedB layouts, through the C ABI,
+against the CPU oracle (restated reference) on identical seeded inputs."""
+import numpy as np
+import pytest
+
+from conftest import TOL, rel_frob, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+# check.rs:147 gemmcheck shapes: partial 6x16 tiles and a K>256 block split
+GEMMCHECK = [(23, 37, 19), (64, 48, 96), (7, 16, 259)]
+
+
+def naive64(m, n, k, a, at, b, bt):
+    A = a.reshape(k, m).T if at else a.reshape(m, k)
+    B = b.reshape(n, k).T if bt else b.reshape(k, n)
+    return (A.astype(np.float64) @ B.astype(np.float64)).ravel()
+
+
+@pytest.mark.parametrize("m,n,k", GEMMCHECK)
+@pytest.mark.parametrize("at", [False, True])
+@pytest.mark.parametrize("bt", [False, True])
+def test_matmul_gemmcheck(rnn, orc, m, n, k, at, bt):
+    rng = orc.Rng(1234 ^ 0x1234)
+    a, b = rng.rand_vec(m * k), rng.rand_vec(k * n)
+    want = orc.matmul(m, n, k, a, at, b, bt)
+    c = to_dev(np.zeros(m * n, np.float32))
+    rnn.matmul(m, n, k, to_dev(a), at, to_dev(b), bt, c)
+    got = to_host(c)
+    assert rel_frob(got, want) < TOL
+    assert rel_frob(got, naive64(m, n, k, a, at, b, bt)) < TOL
+    # check.rs max_rel metric, tolerance 5e-3
+    assert np.abs(got - want).max() / max(np.abs(want).max(), 1e-6) < 5e-3
+
+
+@pytest.mark.parametrize("at,bt", [(False, False), (False, True), (True, False), (True, True)])
+def test_matmul_integer_bit_exact(rnn, orc, at, bt):
+    m, n, k = 133, 97, 300
+    r = np.random.default_rng(5)
+    a = r.integers(-3, 4, m * k).astype(np.float32)
+    b = r.integers(-3, 4, k * n).astype(np.float32)
+    c0 = r.integers(-3, 4, m * n).astype(np.float32)
+    for acc in (False, True):
+        want = orc.matmul(m, n, k, a, at, b, bt, c0, acc)
+        c = to_dev(c0.copy())
+        rnn.matmul(m, n, k, to_dev(a), at, to_dev(b), bt, c, acc)
+        assert np.array_equal(to_host(c), want)
+
+
+def test_matmul_edge_cases(rnn, orc):
+    c0 = np.full(12, 7.0, np.float32)
+    # k == 0: C zeroed unless acc (gemm.rs:449-454)
+    c = to_dev(c0.copy())
+    rnn.matmul(3, 4, 0, to_dev(np.zeros(1, np.float32)), False, to_dev(np.zeros(1, np.float32)),
+               False, c, False)
+    assert np.array_equal(to_host(c), np.zeros(12, np.float32))
+    c = to_dev(c0.copy())
+    rnn.matmul(3, 4, 0, to_dev(np.zeros(1, np.float32)), False, to_dev(np.zeros(1, np.float32)),
+               False, c, True)
+    assert np.array_equal(to_host(c), c0)
+    # m == 0 / n == 0: untouched
+    c = to_dev(c0.copy())
+    rnn.matmul(0, 4, 3, to_dev(np.ones(12, np.float32)), False, to_dev(np.ones(12, np.float32)),
+               False, c, False)
+    assert np.array_equal(to_host(c), c0)
+
+
+@pytest.mark.parametrize("m,n,k,at,bt", [
+    (16384, 768, 256, False, True),    # bench.rs:18 S3 qkv fwd
+    (16384, 256, 768, False, False),   # bench.rs:20 S3 qkv dX
+    (768, 256, 16384, True, False),    # bench.rs:21 S3 qkv dW (matmul with at)
+    (4096, 384, 1024, False, True),    # bench.rs:23 merge fwd
+])
+def test_matmul_gemmbench_shapes(rnn, orc, m, n, k, at, bt):
+    rng = orc.Rng(7)
+    a, b = rng.rand_vec(m * k), rng.rand_vec(k * n)
+    with orc.threads(8):
+        want = orc.matmul(m, n, k, a, at, b, bt)
+    c = to_dev(np.zeros(m * n, np.float32))
+    rnn.matmul(m, n, k, to_dev(a), at, to_dev(b), bt, c)
+    assert rel_frob(to_host(c), want) < TOL
+
+
+def test_gemm_small_batched_attention_shapes(rnn, orc):
+    # 512 (image, head) problems: QK^T (bt), PV, P^T dO (at)
+    cnt = 512
+    rng = orc.Rng(11)
+    for (m, n, k, at, bt) in [(64, 64, 32, False, True), (64, 32, 64, False, False),
+                              (64, 32, 64, True, False), (9, 9, 4, False, True)]:
+        a = rng.rand_vec(cnt * m * k)
+        b = rng.rand_vec(cnt * k * n)
+        c = to_dev(np.zeros(cnt * m * n, np.float32))
+        rnn.gemm_small_batched(cnt, m, n, k, to_dev(a), m * k, at, to_dev(b), k * n, bt, c, m * n)
+        got = to_host(c).reshape(cnt, m * n)
+        for i in (0, 1, 255, cnt - 1):
+            want = orc.gemm_small(m, n, k, a[i * m * k:(i + 1) * m * k], at,
+                                  b[i * k * n:(i + 1) * k * n], bt)
+            assert rel_frob(got[i], want) < TOL
+
+
+def test_gemm_small_k0_leaves_c(rnn, orc):
+    c0 = np.arange(8, dtype=np.float32)
+    c = to_dev(c0.copy())
+    one = to_dev(np.ones(8, np.float32))
+    rnn.gemm_small_batched(2, 2, 2, 0, one, 0, False, one, 0, False, c, 4)
+    assert np.array_equal(to_host(c), c0)
+    assert np.array_equal(orc.gemm_small(2, 2, 0, np.zeros(0, np.float32), False,
+                                         np.zeros(0, np.float32), False, c0[:4]), c0[:4])
+
+
+@pytest.mark.parametrize("m,n,k", [(768, 256, 8192), (5, 6, 3), (64, 700, 1000), (300, 40, 257)])
+def test_matmul_dw(rnn, orc, m, n, k):
+    rng = orc.Rng(3)
+    a, b, c0 = rng.rand_vec(k * m), rng.rand_vec(k * n), rng.rand_vec(m * n)
+    with orc.threads(8):
+        want = orc.matmul_dw(m, n, k, a, b, c0)
+    c = to_dev(c0.copy())
+    rnn.matmul_dw(m, n, k, to_dev(a), to_dev(b), c)
+    got = to_host(c)
+    assert rel_frob(got, want) < TOL
+    # deterministic: same inputs, same bits
+    c2 = to_dev(c0.copy())
+    rnn.matmul_dw(m, n, k, to_dev(a), to_dev(b), c2)
+    assert np.array_equal(to_host(c2), got)
+
+
+def test_matmul_dw_integer_exact(rnn, orc):
+    m, n, k = 40, 72, 5000
+    r = np.random.default_rng(9)
+    a = r.integers(-2, 3, k * m).astype(np.float32)
+    b = r.integers(-2, 3, k * n).astype(np.float32)
+    c0 = r.integers(-2, 3, m * n).astype(np.float32)
+    want = orc.matmul_dw(m, n, k, a, b, c0)
+    c = to_dev(c0.copy())
+    rnn.matmul_dw(m, n, k, to_dev(a), to_dev(b), c)
+    assert np.array_equal(to_host(c), want)
+
+
+@pytest.mark.parametrize("rows,fin,fout,bias", [(8192, 256, 768, True), (27, 8, 24, True),
+                                                 (64, 384, 1024, False)])
+def test_linear(rnn, orc, rows, fin, fout, bias):
+    rng = orc.Rng(21)
+    x, w = rng.rand_vec(rows * fin), rng.rand_vec(fout * fin) * np.float32(0.02)
+    b = rng.rand_vec(fout) if bias else None
+    dy = rng.rand_vec(rows * fout)
+    dw0, db0 = rng.rand_vec(fout * fin), (rng.rand_vec(fout) if bias else None)
+    with orc.threads(8):
+        y_want = orc.linear_forward(rows, fin, fout, x, w, b)
+        dw_want, db_want, dx_want = orc.linear_backward(rows, fin, fout, dy, x, w, dw0, db0)
+    y = rnn.linear_forward(rows, fin, fout, to_dev(x), to_dev(w), to_dev(b) if bias else None)
+    assert rel_frob(to_host(y), y_want) < TOL
+    dw = to_dev(dw0.copy())
+    db = to_dev(db0.copy()) if bias else None
+    dx = rnn.linear_backward(rows, fin, fout, to_dev(dy), to_dev(x), to_dev(w), dw, db)
+    assert rel_frob(to_host(dw), dw_want) < TOL
+    assert rel_frob(to_host(dx), dx_want) < TOL
+    if bias:
+        assert rel_frob(to_host(db), db_want) < TOL
+
+
+@pytest.mark.parametrize("m,k", [(32, 288), (288, 32), (7, 259), (1, 1), (13, 600)])
+@pytest.mark.parametrize("tr", [False, True])
+def test_pack_bit_exact(rnn, orc, m, k, tr):
+    rng = orc.Rng(m * 1000 + k)
+    a = rng.rand_vec(m * k)
+    assert np.array_equal(to_host(rnn.dbg_pack_a(to_dev(a), m, k, tr)), orc.pack_a(a, m, k, tr))
+    assert np.array_equal(to_host(rnn.dbg_pack_b(to_dev(a), m, k, tr)), orc.pack_b(a, m, k, tr))
