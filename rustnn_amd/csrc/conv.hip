@@ -30,8 +30,10 @@ constexpr int MAXT = 9;
 
 struct TileArgs {
     const float *src;  // [N][CS][HS][WS]
-    const float *wf;   // fragment-ordered weights [mblk][chunk][cp][tap][64]
+    const float *w;    // weights; element (m, ch, tap t) at w[m*sm + ch*sc + wtap[t]]
     float *dst;        // [N][CD][HD][WD]
+    int sm, sc;        // weight strides of output row m and source channel ch
+    int ch_inner;      // staging order: 1 = channel before row (sc < sm)
     int N, CS, HS, WS;
     int CD, HD, WD;
     int GA, GB;
@@ -40,6 +42,7 @@ struct TileArgs {
     int TR, IMGS, TIH, TIW, TIWP, HALF, deint;
     int CH, nchunks, nmblk, tiles_a;
     int tapoff[MAXT];
+    int wtap[MAXT];
 };
 
 // LDS column of tile column tx (de-interleaved by parity when IS == 2 so a
@@ -105,17 +108,32 @@ __global__ __launch_bounds__(256) void conv_tile_kernel(TileArgs g) {
 #pragma unroll
             for (int v = 0; v < 16; v++) acc[mb][j][v] = 0.f;
 
-    const int wchunk = CP * NTAPS * 64;  // floats per (mblk, chunk)
+    const int wchunk = CP * NTAPS * 64;  // floats per m-block of a chunk
     for (int chunk = 0; chunk < g.nchunks; chunk++) {
         __syncthreads();
         load_src_tile(g, xs, n0, a0, chunk * g.CH, tid, nthreads);
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-            int mblk = min(mb0 + mb, g.nmblk - 1);
-            const float4 *src =
-                reinterpret_cast<const float4 *>(g.wf + ((long long)mblk * g.nchunks + chunk) * wchunk);
-            float4 *dstw = reinterpret_cast<float4 *>(ws + mb * wchunk);
-            for (int i = tid; i < wchunk / 4; i += nthreads) dstw[i] = src[i];
+        // Weight slab in MFMA fragment order: ws[mb][cp][t][lane] with lane
+        // l -> row m = (mb0+mb)*32 + l%32, channel chunk*CH + cp + (l/32)*CP.
+        // Consecutive threads walk taps, then the operand with the smaller
+        // global stride, so the gather from w stays coalesced.
+        for (int idx = tid; idx < MB * 32 * g.CH * NTAPS; idx += nthreads) {
+            const int t = idx % NTAPS;
+            int r = idx / NTAPS, chl, ml;
+            if (g.ch_inner) {
+                chl = r % g.CH;
+                r /= g.CH;
+                ml = r % 32;
+            } else {
+                ml = r % 32;
+                r /= 32;
+                chl = r % g.CH;
+            }
+            const int mb = r / (g.ch_inner ? 32 : g.CH);
+            const int m = (mb0 + mb) * 32 + ml, ch = chunk * g.CH + chl;
+            float v = 0.f;
+            if (m < g.CD && ch < g.CS) v = g.w[(long long)m * g.sm + (long long)ch * g.sc + g.wtap[t]];
+            const int cp = chl % CP, hh = chl / CP;
+            ws[mb * wchunk + (cp * NTAPS + t) * 64 + ml + 32 * hh] = v;
         }
         __syncthreads();
         const float *wl = ws + lane;
@@ -158,40 +176,6 @@ __global__ __launch_bounds__(256) void conv_tile_kernel(TileArgs g) {
             }
         }
     }
-}
-
-// Fragment-ordered weights: wf[mblk][chunk][cp][t][lane], lane l -> row
-// m = mblk*32 + l%32 and channel ch = chunk*CH + cp + (l/32)*CH/2, tap t.
-// W element = w[m*sm + ch*sc + wtap[t]] (0 outside [0,M) x [0,C)).
-struct PrepArgs {
-    const float *w;
-    float *wf;
-    int M, C, CH, nchunks, nmblk, ntaps;
-    int sm, sc;
-    int wtap[MAXT];
-};
-
-__global__ void prep_weights_kernel(PrepArgs g) {
-    const int CP = g.CH >> 1;
-    long long total = (long long)g.nmblk * g.nchunks * CP * g.ntaps * 64;
-    long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= total) return;
-    int lane = (int)(e & 63);
-    long long r = e >> 6;
-    int t = (int)(r % g.ntaps);
-    r /= g.ntaps;
-    int cp = (int)(r % CP);
-    r /= CP;
-    int chunk = (int)(r % g.nchunks);
-    int mblk = (int)(r / g.nchunks);
-    int m = mblk * 32 + (lane & 31), ch = chunk * g.CH + cp + (lane >> 5) * CP;
-    float v = 0.f;
-    int wt = 0;
-#pragma unroll
-    for (int i = 0; i < MAXT; i++)
-        if (i == t) wt = g.wtap[i];
-    if (m < g.M && ch < g.C) v = g.w[(long long)m * g.sm + (long long)ch * g.sc + wt];
-    g.wf[e] = v;
 }
 
 // Zero-fills the class (py, px) positions of dst (dX classes with no tap).
@@ -450,8 +434,7 @@ static void set_lds_limits() {
 // row m and source channel ch: w[m*sm + ch*sc + kh*K + kw].
 static int run_tile(rnn_ctx *ctx, const float *src, int N, int CS, int HS, int WS, float *dst,
                     int CD, int HD, int WD, int GA, int GB, int OS, int py, int px, int IS,
-                    const Tap *taps, int ntaps, const float *w, int sm, int sc, int K,
-                    float *wf_ws) {
+                    const Tap *taps, int ntaps, const float *w, int sm, int sc, int K) {
     if (GA <= 0 || GB <= 0) return RNN_OK;
     if (ntaps == 0) {
         long long total = (long long)N * CD * GA * GB;
@@ -470,28 +453,13 @@ static int run_tile(rnn_ctx *ctx, const float *src, int N, int CS, int HS, int W
     Plan p;
     if (!plan_tile(CS, CD, GA, GB, IS, ntaps, dy_max - dy_min, dx_max - dx_min, p))
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: no LDS tiling for %dx%d grid", GA, GB);
-    // weights in fragment order
-    PrepArgs pa;
-    pa.w = w;
-    pa.wf = wf_ws;
-    pa.M = CD;
-    pa.C = CS;
-    pa.CH = p.CH;
-    pa.nchunks = p.nchunks;
-    pa.nmblk = p.nmblk;
-    pa.ntaps = ntaps;
-    pa.sm = sm;
-    pa.sc = sc;
-    for (int t = 0; t < MAXT; t++) pa.wtap[t] = t < ntaps ? taps[t].kh * K + taps[t].kw : 0;
-    long long wtotal = (long long)p.nmblk * p.nchunks * (p.CH / 2) * ntaps * 64;
-    hipLaunchKernelGGL(prep_weights_kernel, dim3((unsigned)rnn_div_up(wtotal, 256)), dim3(256), 0,
-                       ctx->stream, pa);
-    RNN_LAUNCHED(ctx);
-
     TileArgs a;
     a.src = src;
-    a.wf = wf_ws;
+    a.w = w;
     a.dst = dst;
+    a.sm = sm;
+    a.sc = sc;
+    a.ch_inner = sc < sm ? 1 : 0;
     a.N = N;
     a.CS = CS;
     a.HS = HS;
@@ -520,6 +488,7 @@ static int run_tile(rnn_ctx *ctx, const float *src, int N, int CS, int HS, int W
     a.tiles_a = (GA + p.TR - 1) / p.TR;
     for (int t = 0; t < MAXT; t++) {
         a.tapoff[t] = 0;
+        a.wtap[t] = t < ntaps ? taps[t].kh * K + taps[t].kw : 0;
         if (t < ntaps) {
             int dyp = taps[t].dy - dy_min, dxp = taps[t].dx - dx_min;
             a.tapoff[t] = dyp * p.TIWP + (p.deint ? (dxp & 1) * p.HALF + (dxp >> 1) : dxp);
@@ -532,12 +501,6 @@ static int run_tile(rnn_ctx *ctx, const float *src, int N, int CS, int HS, int W
         case 9: return launch_tile_t<9>(ctx, a, p);
         default: return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: %d taps per class", ntaps);
     }
-}
-
-static size_t wf_floats(int M, int C, int ntaps) {
-    int CH = std::min(32, (C + 1) & ~1);
-    size_t nchunks = (C + CH - 1) / CH, nmblk = (M + 31) / 32;
-    return nmblk * nchunks * (CH / 2) * ntaps * 64;
 }
 
 static int check_spec(rnn_ctx *ctx, const rnn_conv_spec *sp) {
@@ -569,11 +532,9 @@ int rnn_conv2d_forward(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const fl
     for (int kh = 0; kh < K; kh++)
         for (int kw = 0; kw < K; kw++)
             taps[kh * K + kw] = {kh, kw, kh - (int)sp->pad, kw - (int)sp->pad};
-    float *wf = (float *)rnn_workspace(ctx, wf_floats(sp->cout, sp->cin, KK) * sizeof(float));
-    if (!wf) return RNN_E_NOMEM;
     // A = W[cout][cin][kh][kw]: m = cout (stride cin*KK), ch = cin (stride KK)
     return run_tile(ctx, x, (int)n, sp->cin, sp->h, sp->w, y, sp->cout, sp->oh, sp->ow, sp->oh,
-                    sp->ow, 1, 0, 0, sp->stride, taps, KK, w, sp->cin * KK, KK, K, wf);
+                    sp->ow, 1, 0, 0, sp->stride, taps, KK, w, sp->cin * KK, KK, K);
 }
 
 int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
@@ -586,8 +547,6 @@ int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
     if (!dy || !w || !dx) return rnn_fail(ctx, RNN_E_NULL, "conv2d_backward_x: null operand");
     set_lds_limits();
     const int K = sp->k, S = sp->stride, P = sp->pad, KK = K * K;
-    float *wf = (float *)rnn_workspace(ctx, wf_floats(sp->cin, sp->cout, KK) * sizeof(float));
-    if (!wf) return RNN_E_NOMEM;
     for (int py = 0; py < S; py++)
         for (int px = 0; px < S; px++) {
             // dX[iy][ix] with iy = a*S + py gathers dY[a + (py + P - kh)/S] over
@@ -606,7 +565,7 @@ int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
             int GA = ((int)sp->h - py + S - 1) / S, GB = ((int)sp->w - px + S - 1) / S;
             // A = W^T: m = cin (stride KK), ch = cout (stride cin*KK)
             rc = run_tile(ctx, dy, (int)n, sp->cout, sp->oh, sp->ow, dx, sp->cin, sp->h, sp->w, GA,
-                          GB, S, py, px, 1, taps, nt, w, KK, sp->cin * KK, K, wf);
+                          GB, S, py, px, 1, taps, nt, w, KK, sp->cin * KK, K);
             if (rc) return rc;
         }
     return RNN_OK;
