@@ -57,6 +57,16 @@ const char *rnn_status_string(int status);
 /* Bytes of device workspace currently held by the context. */
 size_t rnn_ctx_workspace_bytes(rnn_ctx *ctx);
 
+/* Device memory for callers that hold host slices (the Rust shim keeps the
+ * reference's Vec<f32> tensors and mirrors them on the device).  No reference
+ * counterpart: the reference computes on host memory only. */
+int rnn_dev_alloc(rnn_ctx *ctx, size_t bytes, void **out);
+int rnn_dev_free(rnn_ctx *ctx, void *p);
+/* Host -> device, ordered on the context stream; returns after the copy. */
+int rnn_copy_to_device(rnn_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes);
+/* Device -> host after all work queued on the context stream. */
+int rnn_copy_to_host(rnn_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes);
+
 /* ------------------------------------------------------------ gemm.rs */
 /* matmul (gemm.rs:434-493): C[m x n] = op(A) op(B) (+ C if acc).
  * at=0: A is [m x k]; at=1: A is [k x m].  bt=0: B is [k x n]; bt=1: B is

@@ -95,6 +95,10 @@ def lib():
             "rnn_ctx_last_error": (C.c_char_p, [_vp]),
             "rnn_status_string": (C.c_char_p, [_i]),
             "rnn_ctx_workspace_bytes": (_sz, [_vp]),
+            "rnn_dev_alloc": (_i, [_vp, _sz, P(_vp)]),
+            "rnn_dev_free": (_i, [_vp, _vp]),
+            "rnn_copy_to_device": (_i, [_vp, _vp, _vp, _sz]),
+            "rnn_copy_to_host": (_i, [_vp, _vp, _vp, _sz]),
             "rnn_matmul": (_i, [_vp, _sz, _sz, _sz, _vp, _i, _vp, _i, _vp, _i]),
             "rnn_gemm_small_batched": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _i, _vp, _sz, _i,
                                             _vp, _sz, _i]),

@@ -13,7 +13,10 @@
 // N = output pixels (32 per group), K = (channel pair, tap).  Lane half h of a
 // K step carries channel cp + h*CH/2 so both halves read the same tap offset.
 //
-// Forward and dX share conv_tile_kernel.  A launch computes an output "class
+// This file holds the C entry points, the generic per-class tile kernel used
+// for (k, stride, pad) combinations without a specialisation in
+// conv_fast.hip, and the im2col debug export.  Forward and dX share
+// conv_tile_kernel.  A launch computes an output "class
 // grid" (a, b) -> dst(a*OS + py, b*OS + px) from source positions
 // (a*IS + dy_t, b*IS + dx_t) over its tap list t:
 //   forward:          one class, IS = stride, OS = 1, taps (kh-pad, kw-pad)
@@ -191,134 +194,6 @@ __global__ void zero_class_kernel(float *dst, int N, int CD, int HD, int WD, int
     dst[nc * HD * WD + (long long)(a * OS + py) * WD + (b * OS + px)] = 0.f;
 }
 
-// ------------------------------------------------------------------ dW
-// dW[co][ci][kh][kw] += sum over (n, oy, ox) of dY[n][co][oy][ox] *
-// X[n][ci][oy*S + kh - pad][ox*S + kw - pad].  GEMM M = co (32 per block),
-// N = ci (32 per block) for each tap, K = output pixels.  A workgroup owns
-// (co block, ci block) and a strided set of pixel tiles; each wave takes whole
-// tile rows and keeps one 32x32 accumulator per tap; K step = pixel pair
-// (2q, 2q+1) of a row, lane half h carrying pixel 2q+h.  The waves are summed
-// in LDS in wave order and the workgroup writes one partial slab; partial
-// slabs are added in slab order by splitk_sum_kernel.
-struct DwArgs {
-    const float *dy;  // [N][CO][OH][OW]
-    const float *x;   // [N][CI][H][W]
-    float *part;      // [nz][CO][CI*KK]
-    int N, CO, CI, H, W, OH, OW, K, IS, pad;
-    int TR, IMGS, GBP, TIH, TIW, TIWP, HALF, deint;
-    int tiles_a, ntiles, nz;
-    int DYS;  // dY tile row stride (pixels of a channel, padded)
-    int tapoff[MAXT];
-};
-
-template <int NTAPS>
-__global__ __launch_bounds__(256) void conv_dw_kernel(DwArgs g) {
-    extern __shared__ float smem[];
-    const int nthreads = blockDim.x, nw = nthreads >> 6;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, l32 = lane & 31;
-    const int cob = blockIdx.y, cib = blockIdx.z, z = blockIdx.x;
-    const int chs = g.IMGS * g.TIH * g.TIWP, imgs = g.TIH * g.TIWP;
-    float *xs = smem;                 // [32 ci][IMGS][TIH][TIWP]
-    float *dys = smem + 32 * chs;     // [32 co][DYS]
-    const int rows = g.IMGS * g.TR;   // tile rows (image-major)
-    const int npairs = g.GBP >> 1;
-    const int ppimg = g.TR * g.GBP;   // pixels per image in the tile
-
-    f32x16 acc[NTAPS];
-#pragma unroll
-    for (int t = 0; t < NTAPS; t++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
-
-    // lane bases: A = dY[co = l32][pixel + h], B = X[ci = l32][pixel + h]
-    const int abase = l32 * g.DYS + h;
-    const int bbase = l32 * chs + h * (g.deint ? 1 : g.IS);
-
-    for (int tile = z; tile < g.ntiles; tile += g.nz) {
-        const int ta = tile % g.tiles_a, tn = tile / g.tiles_a;
-        const int a0 = ta * g.TR, n0 = tn * g.IMGS;
-        __syncthreads();
-        // X halo tile for ci block (fwd geometry: IS = stride, dy_min = dx_min = -pad)
-        {
-            const int tih = g.TIH, tiw = g.TIW, per_img = tih * tiw, per_ch = g.IMGS * per_img;
-            const int total = 32 * per_ch, y0 = a0 * g.IS - g.pad;
-            for (int idx = tid; idx < total; idx += nthreads) {
-                int ch = idx / per_ch, rem = idx - ch * per_ch;
-                int img = rem / per_img;
-                rem -= img * per_img;
-                int ty = rem / tiw, tx = rem - ty * tiw;
-                int n = n0 + img, c = cib * 32 + ch, y = y0 + ty, xx = tx - g.pad;
-                float v = 0.f;
-                if (n < g.N && c < g.CI && y >= 0 && y < g.H && xx >= 0 && xx < g.W)
-                    v = g.x[(((long long)n * g.CI + c) * g.H + y) * g.W + xx];
-                xs[ch * chs + img * imgs + ty * g.TIWP + tile_col(tx, g.deint, g.HALF)] = v;
-            }
-        }
-        // dY tile for co block: [co][img][r][c], c < GBP (zero padded)
-        {
-            const int total = 32 * g.IMGS * ppimg;
-            for (int idx = tid; idx < total; idx += nthreads) {
-                int co = idx / (g.IMGS * ppimg), p = idx - co * (g.IMGS * ppimg);
-                int img = p / ppimg, rem = p - img * ppimg;
-                int r = rem / g.GBP, c = rem - r * g.GBP;
-                int n = n0 + img, oc = cob * 32 + co, oy = a0 + r;
-                float v = 0.f;
-                if (n < g.N && oc < g.CO && oy < g.OH && c < g.OW)
-                    v = g.dy[(((long long)n * g.CO + oc) * g.OH + oy) * g.OW + c];
-                dys[co * g.DYS + p] = v;
-            }
-        }
-        __syncthreads();
-        for (int row = wave; row < rows; row += nw) {
-            const int img = row / g.TR, r = row - img * g.TR;
-            const int prow = img * ppimg + r * g.GBP;               // dY tile pixel of (r, 0)
-            const int xrow = img * imgs + r * g.IS * g.TIWP;        // X tile offset of (r, 0)
-            for (int q = 0; q < npairs; q++) {
-                const float a = dys[abase + prow + 2 * q];
-                const int xo = xrow + 2 * q * (g.deint ? 1 : g.IS);
-#pragma unroll
-                for (int t = 0; t < NTAPS; t++) {
-                    const float b = xs[bbase + xo + g.tapoff[t]];
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[t], 0, 0, 0);
-                }
-            }
-        }
-    }
-    // Sum the waves' accumulators in wave order through LDS, then write the
-    // 32 x (32*KK) partial slab of this workgroup.
-    __syncthreads();
-    float *red = smem;  // NTAPS*1024 floats, reuses the tile area
-    for (int w = 0; w < nw; w++) {
-        if (wave == w) {
-#pragma unroll
-            for (int t = 0; t < NTAPS; t++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    int i = 8 * (v >> 2) + 4 * h + (v & 3);  // co
-                    int e = t * 1024 + i * 32 + l32;          // l32 = ci
-                    red[e] = (w == 0) ? acc[t][v] : red[e] + acc[t][v];
-                }
-        }
-        __syncthreads();
-    }
-    const int KK = g.K * g.K, ckk = g.CI * KK;
-    float *slab = g.part + (long long)z * g.CO * ckk;
-    for (int e = tid; e < NTAPS * 1024; e += nthreads) {
-        int t = e >> 10, i = (e >> 5) & 31, c = e & 31;
-        int co = cob * 32 + i, ci = cib * 32 + c;
-        if (co < g.CO && ci < g.CI) slab[(long long)co * ckk + ci * KK + t] = red[e];
-    }
-}
-
-// out[e] += sum_z part[z*len + e] in z order.
-__global__ void splitk_sum_kernel(const float *part, int nz, long long len, float *out) {
-    long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= len) return;
-    float s = part[e];
-    for (int zz = 1; zz < nz; zz++) s += part[(long long)zz * len + e];
-    out[e] += s;
-}
-
 __global__ void im2col_kernel(const float *x, float *col, int CI, int H, int W, int K, int S,
                               int pad, int OH, int OW) {
     long long total = (long long)CI * K * K * OH * OW;
@@ -423,7 +298,6 @@ static void set_lds_limits() {
         (const void *)conv_tile_kernel<2, 1, 1>, (const void *)conv_tile_kernel<2, 2, 1>,
         (const void *)conv_tile_kernel<4, 1, 1>, (const void *)conv_tile_kernel<4, 2, 1>,
         (const void *)conv_tile_kernel<9, 1, 1>, (const void *)conv_tile_kernel<9, 2, 1>,
-        (const void *)conv_dw_kernel<1>,         (const void *)conv_dw_kernel<9>,
     };
     for (const void *k : ks)
         (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_FULL);
@@ -526,6 +400,8 @@ int rnn_conv2d_forward(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const fl
     if (rc) return rc;
     if (n == 0) return RNN_OK;
     if (!x || !w || !y) return rnn_fail(ctx, RNN_E_NULL, "conv2d_forward: null operand");
+    rc = rnn_conv_fast(ctx, 0, sp, n, x, w, y);
+    if (rc != RNN_E_UNSUPPORTED) return rc;
     set_lds_limits();
     const int K = sp->k, KK = K * K;
     Tap taps[MAXT];
@@ -545,6 +421,8 @@ int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
     if (rc) return rc;
     if (n == 0) return RNN_OK;
     if (!dy || !w || !dx) return rnn_fail(ctx, RNN_E_NULL, "conv2d_backward_x: null operand");
+    rc = rnn_conv_fast(ctx, 1, sp, n, dy, w, dx);
+    if (rc != RNN_E_UNSUPPORTED) return rc;
     set_lds_limits();
     const int K = sp->k, S = sp->stride, P = sp->pad, KK = K * K;
     for (int py = 0; py < S; py++)
@@ -579,83 +457,7 @@ int rnn_conv2d_backward_w(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
     if (rc) return rc;
     if (n == 0) return RNN_OK;
     if (!dy || !x || !dw) return rnn_fail(ctx, RNN_E_NULL, "conv2d_backward_w: null operand");
-    set_lds_limits();
-    const int K = sp->k, KK = K * K, S = sp->stride, P = sp->pad;
-    const int OH = sp->oh, OW = sp->ow;
-    DwArgs g;
-    g.dy = dy;
-    g.x = x;
-    g.N = (int)n;
-    g.CO = sp->cout;
-    g.CI = sp->cin;
-    g.H = sp->h;
-    g.W = sp->w;
-    g.OH = OH;
-    g.OW = OW;
-    g.K = K;
-    g.IS = S;
-    g.pad = P;
-    g.deint = S == 2;
-    g.GBP = (OW + 1) & ~1;
-    // tile: up to 256 output pixels, within the LDS budget
-    int tr, imgs;
-    const int target = 256;
-    if (OH * g.GBP <= target) {
-        tr = OH;
-        imgs = std::max(1, target / (OH * g.GBP));
-    } else {
-        tr = std::max(1, target / g.GBP);
-        imgs = 1;
-    }
-    size_t lds = 0;
-    for (;;) {
-        g.TR = tr;
-        g.IMGS = imgs;
-        g.TIH = (tr - 1) * S + K;
-        g.TIW = (g.GBP - 1) * S + K;
-        g.HALF = (g.TIW + 1) / 2;
-        g.TIWP = g.deint ? 2 * g.HALF : g.TIW;
-        g.DYS = imgs * tr * g.GBP + 1;
-        size_t xs = (size_t)32 * imgs * g.TIH * g.TIWP, dys = (size_t)32 * g.DYS;
-        lds = std::max((xs + dys) * 4, (size_t)KK * 1024 * 4);
-        if (lds <= LDS_HALF || (tr == 1 && imgs == 1)) break;
-        if (imgs > 1)
-            imgs /= 2;
-        else
-            tr = std::max(1, tr / 2);
-    }
-    if (lds > LDS_FULL) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: row too wide for LDS");
-    g.tiles_a = (OH + g.TR - 1) / g.TR;
-    g.ntiles = g.tiles_a * (int)((n + g.IMGS - 1) / g.IMGS);
-    const int ncb = (g.CO + 31) / 32, ncib = (g.CI + 31) / 32;
-    // about two workgroups per CU, at least two tiles per workgroup when possible
-    int nz = std::max(1, 2 * ctx->num_cus / (ncb * ncib));
-    nz = std::min(nz, std::max(1, g.ntiles / 2));
-    nz = std::min(nz, g.ntiles);
-    g.nz = nz;
-    for (int t = 0; t < MAXT; t++) {
-        g.tapoff[t] = 0;
-        if (t < KK) {
-            int dyp = t / K, dxp = t % K;  // tap offset relative to the tile origin (-pad)
-            g.tapoff[t] = dyp * g.TIWP + (g.deint ? (dxp & 1) * g.HALF + (dxp >> 1) : dxp);
-        }
-    }
-    const size_t ckk = (size_t)g.CI * KK, len = (size_t)g.CO * ckk;
-    float *part = (float *)rnn_workspace(ctx, (size_t)nz * len * sizeof(float));
-    if (!part) return RNN_E_NOMEM;
-    g.part = part;
-    dim3 grid(nz, ncb, ncib), block(256);
-    if (KK == 9)
-        hipLaunchKernelGGL(conv_dw_kernel<9>, grid, block, lds, ctx->stream, g);
-    else if (KK == 1)
-        hipLaunchKernelGGL(conv_dw_kernel<1>, grid, block, lds, ctx->stream, g);
-    else
-        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: k must be 1 or 3");
-    RNN_LAUNCHED(ctx);
-    hipLaunchKernelGGL(splitk_sum_kernel, dim3((unsigned)rnn_div_up(len, 256)), dim3(256), 0,
-                       ctx->stream, part, nz, (long long)len, dw);
-    RNN_LAUNCHED(ctx);
-    return RNN_OK;
+    return rnn_conv_dw(ctx, sp, n, dy, x, dw);
 }
 
 int rnn_dbg_im2col(rnn_ctx *ctx, const rnn_conv_spec *sp, const float *x_img, float *col) {

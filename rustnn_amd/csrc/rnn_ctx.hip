@@ -114,6 +114,48 @@ const char *rnn_ctx_last_error(rnn_ctx *ctx) { return ctx ? ctx->err : "null con
 
 size_t rnn_ctx_workspace_bytes(rnn_ctx *ctx) { return ctx ? ctx->ws_bytes : 0; }
 
+int rnn_dev_alloc(rnn_ctx *ctx, size_t bytes, void **out) {
+    if (!ctx || !out) return RNN_E_NULL;
+    *out = nullptr;
+    if (bytes == 0) return RNN_OK;
+    RNN_HIP(ctx, hipSetDevice(ctx->device));
+    hipError_t e = hipMalloc(out, bytes);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return rnn_fail(ctx, RNN_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    }
+    return RNN_OK;
+}
+
+int rnn_dev_free(rnn_ctx *ctx, void *p) {
+    if (!ctx) return RNN_E_NULL;
+    if (!p) return RNN_OK;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));  // queued kernels may still use p
+    RNN_HIP(ctx, hipFree(p));
+    return RNN_OK;
+}
+
+int rnn_copy_to_device(rnn_ctx *ctx, void *dst_dev, const void *src_host, size_t bytes) {
+    if (!ctx) return RNN_E_NULL;
+    if (bytes == 0) return RNN_OK;
+    if (!dst_dev || !src_host) return rnn_fail(ctx, RNN_E_NULL, "copy_to_device: null pointer");
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    RNN_HIP(ctx, hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, ctx->stream));
+    RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return RNN_OK;
+}
+
+int rnn_copy_to_host(rnn_ctx *ctx, void *dst_host, const void *src_dev, size_t bytes) {
+    if (!ctx) return RNN_E_NULL;
+    if (bytes == 0) return RNN_OK;
+    if (!dst_host || !src_dev) return rnn_fail(ctx, RNN_E_NULL, "copy_to_host: null pointer");
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    RNN_HIP(ctx, hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return RNN_OK;
+}
+
 int rnn_conv_spec_init(rnn_conv_spec *sp, uint32_t cin, uint32_t cout, uint32_t k,
                        uint32_t stride, uint32_t pad, uint32_t h, uint32_t w) {
     if (!sp) return RNN_E_NULL;

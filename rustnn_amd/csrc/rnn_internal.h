@@ -80,3 +80,10 @@ int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, co
                     size_t stride_a, int at, const float *b, size_t stride_b, int bt, float *c,
                     size_t stride_c, int acc, const float *bias);
 int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, float *out);
+// Specialised forward (dx = 0) / dX (dx = 1) convolution; RNN_E_UNSUPPORTED
+// when (k, stride, pad) has no specialisation.
+int rnn_conv_fast(rnn_ctx *ctx, int dx, const rnn_conv_spec *sp, size_t n, const float *src,
+                  const float *w, float *dst);
+// dW += over the batch (k = 1 or 3).
+int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
+                float *dw);
