@@ -76,7 +76,7 @@ __device__ __forceinline__ void load_rows(float *dst, int ld, const float *src, 
 
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs g) {
     extern __shared__ float smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthreads = blockDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(), nthreads = blockDim.x;
     const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
     const int DS = g.DHP + 1, PS = g.TK + 1;
     float *Qs = smem, *Ks = Qs + g.TQ * DS, *Vs = Ks + g.TK * DS, *Ps = Vs + g.TK * DS;
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs g) {
 
 __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs g) {
     extern __shared__ float smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nthreads = blockDim.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(), nthreads = blockDim.x;
     const int nwaves = nthreads >> 6;
     const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
     const int DS = g.DHP + 1, PS = g.TK + 1;

@@ -78,7 +78,7 @@ __device__ __forceinline__ void load_src_tile(const TileArgs &g, float *xs, int 
 template <int NTAPS, int NPW, int MB>
 __global__ __launch_bounds__(256) void conv_tile_kernel(TileArgs g) {
     extern __shared__ float smem[];
-    const int nthreads = blockDim.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nthreads = blockDim.x, tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int tile = blockIdx.x;
     const int ta = tile % g.tiles_a, tn = tile / g.tiles_a;
     const int a0 = ta * g.TR, n0 = tn * g.IMGS;

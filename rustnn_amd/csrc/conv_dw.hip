@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256, 2) void conv_dw_kernel(DwArgs g) {
     constexpr int KK = K * K;
     extern __shared__ float smem[];
     const int nthreads = blockDim.x, nw = nthreads >> 6;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, l32 = lane & 31;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(), h = lane >> 5, l32 = lane & 31;
     const int z = blockIdx.x, cob = blockIdx.y, cib = blockIdx.z;
     const int rows = g.xg.IMGS * g.TR;
     const int npairs = g.GBP >> 1;

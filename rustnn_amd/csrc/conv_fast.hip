@@ -1,17 +1,25 @@
 // Specialised implicit-GEMM forward / dX convolution for the (k, stride, pad)
 // pairs rustnn uses: 3x3/s1/p1, 3x3/s2/p1, 1x1/s2/p0 (and 1x1/s1/p0).
 //
-// One launch per call.  A workgroup owns a tile of output positions (TR rows
-// of IMGS images, full width) for MB blocks of 32 output channels.  Per chunk
-// of CH source channels it stages
-//   * the zero-padded source window in LDS (x for forward, dY for dX), and
-//   * the weight slab in MFMA fragment order ws[mb][cp][tap][lane],
-// then runs v_mfma_f32_32x32x2f32 over K = (channel pair, tap): lane half h
-// carries channel cp + h*CH/2, so one per-tap LDS offset serves the whole
-// wave.  For dX with stride s the workgroup computes all s*s parity classes
-// of its block positions from the same dY window, each tap feeding exactly
-// one class accumulator (gather-form col2im: no atomics, each dX element
-// written once).
+// Persistent workgroups walk a list of work items -- (tile of output
+// positions, group of MB blocks of 32 output channels) -- and, per item, the
+// source channels in chunks of CH.  Each (item, chunk) stage is staged into
+// one of two LDS buffers by DMA (buffer_load ... lds, no registers) while the
+// previous stage is computed:
+//   * the zero-padded source window (x for forward, dY for dX), stored
+//     [channel quad][position][4]: the 4 channels of a quad are adjacent, so
+//     one ds_read_b128 gives a lane the B operand of 4 MFMA k-steps;
+//   * the weight slab, gathered straight from W into MFMA fragment order
+//     [mb][quad][tap][lane][4] (one ds_read_b128 per 4 k-steps for A).
+// MFMA mapping (v_mfma_f32_32x32x2f32): M = output channels, N = output
+// positions (32 per group), K = (channel, tap) with lane half h carrying
+// channel h*CH/2 + 4q + i, so one per-tap offset serves all 64 lanes.  The
+// operands of the next (quad, tap) step are read while the MFMAs of the
+// current one run.
+//
+// For dX with stride s the workgroup computes all s*s parity classes of its
+// block positions from the same dY window, each tap feeding exactly one class
+// accumulator (gather-form col2im: no atomics, every dX element written once).
 //
 // Reference: conv.rs forward_image (168-203), dx_image (205-246) and the
 // Conv2d batch drivers (nn.rs:166-250).
@@ -23,97 +31,250 @@
 
 namespace {
 
+constexpr int FAST_NW = 4;  // waves per workgroup
+
+// Window DMA rows of 16 positions that one wave stages per channel quad:
+// row u of wave w covers window positions (w + 4u)*16 .. +16.  Row u is issued
+// at tap u % KK of a step, so its per-lane source offsets sit in a register
+// table indexed at compile time.
+template <int KK>
+struct WinRows {
+    static constexpr int MAX = KK == 1 ? 4 : KK;
+};
+
 struct FastArgs {
     const float *src;  // [N][CS][HS][WS]
     const float *w;    // [cout][cin][k][k]
-    const float *wf;   // weights in fragment order [mblk][chunk][cp][tap][64]
     float *dst;        // [N][CD][HD][WD]
-    int xregion;       // LDS words of the source window region (64-word rows)
     int N, CS, HS, WS;
     int CD, HD, WD;
     int GA, GB;        // output block grid per image
     int TR, tiles_a, ntiles, ngroups;
-    int stage;         // LDS words of one stage buffer (window + MB weight slabs)
-    int CH, nchunks;
+    int CH, nchunks;   // source channels per stage (multiple of 8)
     int sm, sc;        // weight strides of output row m and source channel ch
-    int dymin, dxmin;  // smallest tap offsets (tile origin)
-    int lrow, lcol;    // LDS rows / columns per output row / column step
-    TileGeo geo;
-    int tapoff[9];
+    int wbytes;        // bytes of W
+    int dymin, dxmin;  // smallest tap offsets (window origin)
+    int lrow, lcol;    // window rows / columns per output row / column step
+    int plane;         // window positions per channel quad (multiple of 64)
+    int ppw;           // plane / 64: window rows per quad and wave
+    int xwords;        // LDS words of the window: CH * plane
+    int stage;         // LDS words of one stage: window, weight slabs, 64-word sink
+    TileGeo geo;       // window geometry in positions (chs unused)
+    int tapoff[9];     // window-position offset of each tap
 };
 
-// Weights in MFMA fragment order: wf[mblk][chunk][cp][tap][lane], lane l ->
-// row m = mblk*32 + l%32, channel ch = chunk*CH + cp + (l/32)*CH/2; element
-// w[m*sm + ch*sc + tap], 0 outside [0, M) x [0, C).  One small kernel per call;
-// every workgroup then stages its slab with one contiguous DMA.
-__global__ void prep_fragments_kernel(const float *__restrict__ w, float *__restrict__ wf, int M,
-                                      int C, int CH, int nchunks, int nmblk, int KK, int sm,
-                                      int sc) {
-    const int CP = CH >> 1;
-    const long long total = (long long)nmblk * nchunks * CP * KK * 64;
-    const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= total) return;
-    const int lane = (int)(e & 63);
-    long long r = e >> 6;
-    const int t = (int)(r % KK);
-    r /= KK;
-    const int cp = (int)(r % CP);
-    r /= CP;
-    const int chunk = (int)(r % nchunks), mblk = (int)(r / nchunks);
-    const int m = mblk * 32 + (lane & 31), ch = chunk * CH + cp + (lane >> 5) * CP;
-    float v = 0.f;
-    if (m < M && ch < C) v = w[(long long)m * sm + (long long)ch * sc + t];
-    wf[e] = v;
+// Wave-uniform description of the stage being staged by DMA.
+struct StageDMA {
+    __amdgpu_buffer_rsrc_t rs;  // source images n0 .. n0 + IMGS
+    float *buf;                 // stage buffer
+    float *sink;                // 64 words no compute reads (rows without data)
+    int valid;                  // 0: no stage; every row goes to the sink
+    int c0, grp;                // first source channel, output-channel group
+    int ebase;                  // element offset of window row 0 in image n0 (may be < 0)
+    int ylo, yhi;               // window rows inside the source image
+    int nimg;                   // images of the tile inside the batch
+    int mlim;                   // output rows of the group inside [0, CD)
+};
+
+template <int K, int S, int P, bool DX, int MB>
+__device__ __forceinline__ StageDMA stage_dma(const FastArgs &g, int item, int chunk,
+                                              float *buf) {
+    using T = ConvTaps<K, S, P, DX>;
+    StageDMA d;
+    d.valid = item >= 0;
+    if (!d.valid) {
+        item = 0;
+        chunk = 0;
+    }
+    const int tile = item % g.ntiles;
+    d.grp = item / g.ntiles;
+    const int n0 = (tile / g.tiles_a) * g.geo.IMGS;
+    const int y0 = (tile % g.tiles_a) * g.TR * T::IS + g.dymin;
+    const int rowstep = g.geo.rowstep;
+    const long long img_elems = (long long)g.CS * g.HS * g.WS;
+    d.rs = make_rsrc(g.src + (long long)n0 * img_elems,
+                     (uint32_t)(min(g.N - n0, g.geo.IMGS) * img_elems * 4));
+    d.buf = buf;
+    d.sink = buf + g.stage - 64;
+    d.c0 = chunk * g.CH;
+    d.ebase = y0 * g.WS;
+    d.ylo = y0 >= 0 ? 0 : (-y0 + rowstep - 1) / rowstep;
+    d.yhi = min(g.geo.TIH, (g.HS - y0 + rowstep - 1) / rowstep);
+    if (d.yhi < d.ylo) d.yhi = d.ylo;
+    d.nimg = d.valid ? min(g.N - n0, g.geo.IMGS) : 0;
+    d.mlim = d.valid ? g.CD - d.grp * MB * 32 : 0;
+    return d;
+}
+
+// Per-lane constants of the DMA rows (computed once per workgroup).
+template <int KK>
+struct LaneDMA {
+    int toff[WinRows<KK>::MAX];   // window row u: element offset in the tile, channel lane&3
+    int tmeta[WinRows<KK>::MAX];  // window row ty | img << 8 (ty = 255: no source element)
+    int wl;                       // weight row: (lane/4)*sm + (lane%4)*sc
+};
+
+template <int KK>
+__device__ __forceinline__ void lane_dma_init(const FastArgs &g, LaneDMA<KK> &L, int wave,
+                                              int lane) {
+    const TileGeo &t = g.geo;
+    const int i = lane & 3;
+#pragma unroll
+    for (int u = 0; u < WinRows<KK>::MAX; u++) {
+        const int pos = (wave + FAST_NW * u) * 16 + (lane >> 2);
+        const int img = pos / t.imgs, rem = pos - img * t.imgs;
+        const int ty = rem / t.TIWP, col = rem - ty * t.TIWP;
+        const int tx = t.deint ? (col < t.HALF ? 2 * col : 2 * (col - t.HALF) + 1) : col;
+        const int x = g.dxmin + tx * t.colstep;
+        const bool ok = u < g.ppw && img < t.IMGS && ty < t.TIH && tx < t.TIW && x >= 0 &&
+                        x < g.WS;
+        L.toff[u] = ((img * g.CS + i) * g.HS + ty * t.rowstep) * g.WS + x;
+        L.tmeta[u] = ok ? (ty | (img << 8)) : 255;
+    }
+    L.wl = (lane >> 2) * g.sm + i * g.sc;
+}
+
+// Issues the DMA rows assigned to step (q, t) of stage d: the weight rows
+// (mb, q, t) of this wave and the window rows u = t, t + KK, ... of quads q
+// and CQ + q.  Rows beyond the stage go to the sink with every lane out of
+// range (no memory traffic), which keeps the step free of branches.
+template <int KK, int MB, int TT>
+__device__ __forceinline__ void issue_step(const FastArgs &g, const StageDMA &d,
+                                           const LaneDMA<KK> &L, __amdgpu_buffer_rsrc_t rs_w,
+                                           int q, int wave, int lane) {
+    const int CP = g.CH >> 1, cq = g.CH >> 3;
+    // weights: slab (mb, q, TT), 64-word row `wave`: lane l = wave*16 + lane/4
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const int mrel = mb * 32 + (wave & 1) * 16;
+        const int cbase = d.c0 + (wave >> 1) * CP + 4 * q;
+        const bool ok = (lane >> 2) < d.mlim - mrel && (lane & 3) < g.CS - cbase;
+        const int e = L.wl + (d.grp * MB * 32 + mrel) * g.sm + cbase * g.sc + TT;
+        const uint32_t off = ok ? (uint32_t)e * 4u : DMA_OOB;
+        float *dst = d.valid ? d.buf + g.xwords + ((mb * cq + q) * KK + TT) * 256 + wave * 64
+                             : d.sink;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, (lds_ptr_t)dst, 4, off, 0, 0, 0);
+    }
+    // window rows
+    static_for<0, (WinRows<KK>::MAX - TT + KK - 1) / KK>([&](auto jc) {
+        constexpr int u = TT + KK * decltype(jc)::value;
+        const int ty = L.tmeta[u] & 255, img = L.tmeta[u] >> 8;
+        const bool rowok = (unsigned)(ty - d.ylo) < (unsigned)(d.yhi - d.ylo) && img < d.nimg;
+        const bool live = d.valid && u < g.ppw;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const int hq = hh * cq + q;
+            const int cb = d.c0 + 4 * hq;
+            const bool ok = rowok && (lane & 3) < g.CS - cb;
+            const int e = L.toff[u] + cb * (g.HS * g.WS) + d.ebase;
+            const uint32_t off = ok ? (uint32_t)e * 4u : DMA_OOB;
+            float *dst = live ? d.buf + (hq * g.plane + (wave + FAST_NW * u) * 16) * 4 : d.sink;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rs, (lds_ptr_t)dst, 4, off, 0, 0, 0);
+        }
+    });
+}
+
+// One stage of the GEMM: (quad q, tap t) steps over the window `xs` and the
+// weight slabs of the current buffer; step (q, t) also issues its share of
+// the next stage's DMA into `nxt`, so that the address arithmetic and memory
+// traffic run under the MFMAs.  `xs` and `nxt` are distinct buffers: the
+// __restrict__ qualifiers give the compiler the alias scopes it needs to not
+// wait for the DMA before the LDS reads.
+template <int K, int S, int P, bool DX, int NPW, int MB, int NACC>
+__device__ __forceinline__ void run_stage(
+    const FastArgs &g, const float *__restrict__ xs, float *__restrict__ nxt, int nitem,
+    int nchunk, const LaneDMA<ConvTaps<K, S, P, DX>::KK> &L, const int (&vb)[NPW],
+    f32x16 (&acc)[ConvTaps<K, S, P, DX>::NCLS][MB][NPW][NACC], int wave, int lane,
+    __amdgpu_buffer_rsrc_t rs_w) {
+    using T = ConvTaps<K, S, P, DX>;
+    constexpr int KK = T::KK;
+    const int CQ = g.CH >> 3;
+    const int wslab = CQ * KK * 256;
+    const float *ws = xs + g.xwords + lane * 4;
+    const StageDMA d = stage_dma<K, S, P, DX, MB>(g, nitem, nchunk, nxt);
+
+    auto fetch = [&](int q, int t, float4 *fa, float4 *fb) {
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+            fa[mb] = *reinterpret_cast<const float4 *>(ws + mb * wslab + (q * KK + t) * 256);
+        const float *xq = xs + (q * g.plane + g.tapoff[t]) * 4;
+#pragma unroll
+        for (int j = 0; j < NPW; j++) fb[j] = *reinterpret_cast<const float4 *>(xq + vb[j]);
+    };
+    float4 ca[MB], cb[NPW];
+    fetch(0, 0, ca, cb);
+    for (int q = 0; q < CQ; q++) {
+        static_for<0, KK>([&](auto tc) {
+            constexpr int t = decltype(tc)::value;
+            constexpr int c = T::cls(t);
+            float4 na[MB], nb[NPW];
+            if (t + 1 < KK)
+                fetch(q, t + 1 < KK ? t + 1 : 0, na, nb);
+            else if (q + 1 < CQ)
+                fetch(q + 1, 0, na, nb);
+            issue_step<KK, MB, t>(g, d, L, rs_w, q, wave, lane);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+                    for (int j = 0; j < NPW; j++)
+                        acc[c][mb][j][i % NACC] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            ca[mb][i], cb[j][i], acc[c][mb][j][i % NACC], 0, 0, 0);
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++) ca[mb] = na[mb];
+#pragma unroll
+            for (int j = 0; j < NPW; j++) cb[j] = nb[j];
+        });
+    }
+}
+
+// Stage 0 of the first work item, issued in full before any compute.
+template <int K, int S, int P, bool DX, int MB>
+__device__ __forceinline__ void issue_prologue(const FastArgs &g, float *__restrict__ buf,
+                                               int item, const LaneDMA<ConvTaps<K, S, P, DX>::KK> &L,
+                                               __amdgpu_buffer_rsrc_t rs_w, int wave, int lane) {
+    constexpr int KK = ConvTaps<K, S, P, DX>::KK;
+    const StageDMA d = stage_dma<K, S, P, DX, MB>(g, item, 0, buf);
+    for (int q = 0; q < (g.CH >> 3); q++)
+        static_for<0, KK>([&](auto tc) {
+            issue_step<KK, MB, decltype(tc)::value>(g, d, L, rs_w, q, wave, lane);
+        });
 }
 
 template <int K, int S, int P, bool DX, int NPW, int MB>
 __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
     using T = ConvTaps<K, S, P, DX>;
-    constexpr int KK = T::KK, NCLS = T::NCLS;
+    constexpr int NCLS = T::NCLS;
+    // A wave with a single output block alternates two accumulators so that
+    // consecutive MFMAs do not depend on each other.
+    constexpr int NACC = NCLS * NPW * MB == 1 ? 2 : 1;
     extern __shared__ float smem[];
-    const int nthreads = blockDim.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nw = nthreads >> 6, h = lane >> 5, l32 = lane & 31;
-    const int CP = g.CH >> 1, chs = g.geo.chs;
-    const int wchunk = CP * KK * 64;
-    const int nmblk = (g.CD + 31) / 32;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int h = lane >> 5, l32 = lane & 31;
+    const int CQ = g.CH >> 3;
     const int tpix = g.TR * g.GB, npix = g.geo.IMGS * tpix;
     const int nitems = g.ntiles * g.ngroups;
-    const long long img_elems = (long long)g.CS * g.HS * g.WS;
-    const __amdgpu_buffer_rsrc_t rs_w =
-        make_rsrc(g.wf, (uint32_t)((long long)nmblk * g.nchunks * wchunk * 4));
+    if ((int)blockIdx.x >= nitems) return;
+    const __amdgpu_buffer_rsrc_t rs_w = make_rsrc(g.w, (uint32_t)g.wbytes);
 
-    // Per-lane LDS base of each position group (channel half h included);
-    // tile-relative, so the same for every work item.
+    LaneDMA<T::KK> L;
+    lane_dma_init<T::KK>(g, L, wave, lane);
+
+    // LDS word offset of this lane's channel half and window position for
+    // each 32-position group (tile-relative: the same for every work item).
     int vb[NPW];
 #pragma unroll
     for (int j = 0; j < NPW; j++) {
         int p = (wave * NPW + j) * 32 + l32;
         if (p >= npix) p = 0;
         const int img = p / tpix, rem = p - img * tpix, r = rem / g.GB, c = rem - r * g.GB;
-        vb[j] = h * CP * chs + img * g.geo.imgs + r * g.lrow * g.geo.TIWP + c * g.lcol;
+        vb[j] = (h * CQ * g.plane + img * g.geo.imgs + r * g.lrow * g.geo.TIWP + c * g.lcol) * 4;
     }
 
-    // Stage = (work item, channel chunk); a work item = (tile, group of MB
-    // output-channel blocks).  Stage data lives in one of two LDS buffers.
-    auto issue = [&](int item, int chunk, float *buf) {
-        const int tile = item % g.ntiles, grp = item / g.ntiles;
-        const int ta = tile % g.tiles_a, tn = tile / g.tiles_a;
-        const int a0 = ta * g.TR, n0 = tn * g.geo.IMGS;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(
-            g.src + (long long)n0 * img_elems, (uint32_t)(min(g.N - n0, g.geo.IMGS) * img_elems * 4));
-        dma_tile(rs, g.N, g.CS, g.HS, g.WS, n0, chunk * g.CH, g.CH, a0 * T::IS + g.dymin, g.dxmin,
-                 g.geo, buf, wave, nw, lane);
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++) {
-            const int mblk = min(grp * MB + mb, nmblk - 1);
-            dma_copy(rs_w, (uint32_t)(((long long)mblk * g.nchunks + chunk) * wchunk * 4),
-                     buf + g.xregion + mb * wchunk, wchunk, wave, nw, lane);
-        }
-    };
-
-    f32x16 acc[NCLS][MB][NPW];
+    issue_prologue<K, S, P, DX, MB>(g, smem, blockIdx.x, L, rs_w, wave, lane);
+    f32x16 acc[NCLS][MB][NPW][NACC];
     int s = 0;
-    if ((int)blockIdx.x < nitems) issue(blockIdx.x, 0, smem);
     for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
 #pragma unroll
         for (int c = 0; c < NCLS; c++)
@@ -122,53 +283,23 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
 #pragma unroll
                 for (int j = 0; j < NPW; j++)
 #pragma unroll
-                    for (int v = 0; v < 16; v++) acc[c][mb][j][v] = 0.f;
+                    for (int a = 0; a < NACC; a++)
+#pragma unroll
+                        for (int v = 0; v < 16; v++) acc[c][mb][j][a][v] = 0.f;
         for (int chunk = 0; chunk < g.nchunks; chunk++, s++) {
             // Stage s has landed and every wave is done with stage s-1, whose
-            // buffer now receives stage s+1 while stage s is computed.
+            // buffer receives stage s+1 while stage s is computed.
             dma_wait_barrier();
-            float *cur = smem + (s & 1) * g.stage;
-            if (chunk + 1 < g.nchunks)
-                issue(item, chunk + 1, smem + ((s + 1) & 1) * g.stage);
-            else if (item + (int)gridDim.x < nitems)
-                issue(item + gridDim.x, 0, smem + ((s + 1) & 1) * g.stage);
-            const float *xs = cur, *ws = cur + g.xregion;
-            // Operands of channel pair cp+1 are fetched from LDS while the
-            // MFMAs of cp run (register double buffer), so no MFMA waits on a
-            // just-issued LDS read.
-            float av[2][KK][MB], bv[2][KK][NPW];
-            auto fetch = [&](int cp, int slot) {
-                const float *xc = xs + cp * chs;
-                const float *wl = ws + cp * KK * 64 + lane;
-                static_for<0, KK>([&](auto tc) {
-                    constexpr int t = decltype(tc)::value;
-#pragma unroll
-                    for (int mb = 0; mb < MB; mb++) av[slot][t][mb] = wl[mb * wchunk + t * 64];
-#pragma unroll
-                    for (int j = 0; j < NPW; j++) bv[slot][t][j] = xc[vb[j] + g.tapoff[t]];
-                });
-            };
-            auto mma = [&](int slot) {
-                static_for<0, KK>([&](auto tc) {
-                    constexpr int t = decltype(tc)::value;
-                    constexpr int c = T::cls(t);
-#pragma unroll
-                    for (int mb = 0; mb < MB; mb++)
-#pragma unroll
-                        for (int j = 0; j < NPW; j++)
-                            acc[c][mb][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                                av[slot][t][mb], bv[slot][t][j], acc[c][mb][j], 0, 0, 0);
-                });
-            };
-            fetch(0, 0);
-            int cp = 0;
-            for (; cp + 2 <= CP; cp += 2) {
-                fetch(cp + 1, 1);
-                mma(0);
-                if (cp + 2 < CP) fetch(cp + 2, 0);
-                mma(1);
+            int nitem = -1, nchunk = 0;
+            if (chunk + 1 < g.nchunks) {
+                nitem = item;
+                nchunk = chunk + 1;
+            } else if (item + (int)gridDim.x < nitems) {
+                nitem = item + gridDim.x;
             }
-            if (cp < CP) mma(0);
+            run_stage<K, S, P, DX, NPW, MB, NACC>(g, smem + (s & 1) * g.stage,
+                                                  smem + ((s + 1) & 1) * g.stage, nitem, nchunk,
+                                                  L, vb, acc, wave, lane, rs_w);
         }
         // acc row 8*(v/4) + 4*h + v%4 = output channel in the block, column = position.
         const int tile = item % g.ntiles, grp = item / g.ntiles;
@@ -188,15 +319,20 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
                 const long long cst = (long long)g.HD * g.WD;
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++) {
+                    f32x16 v16 = acc[c][mb][j][0];
+                    if constexpr (NACC == 2) v16 += acc[c][mb][j][1];
 #pragma unroll
                     for (int v = 0; v < 16; v++) {
                         const int m = (grp * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                        if (m < g.CD) dp[m * cst] = acc[c][mb][j][v];
+                        if (m < g.CD) dp[m * cst] = v16[v];
                     }
                 }
             }
         }
     }
+    // The last stage sent its (empty) DMA rows to the sink: let them land
+    // before the workgroup's LDS is released.
+    __builtin_amdgcn_s_waitcnt(0);
 }
 
 struct FastPlan {
@@ -205,9 +341,10 @@ struct FastPlan {
     size_t lds;
 };
 
-// LDS bytes of a plan and the tile geometry it implies.
+// Window geometry of a plan; returns the LDS bytes (two stage buffers), or
+// 0 when the window does not fit the per-wave DMA row tables.
 template <int K, int S, int P, bool DX>
-static size_t plan_geometry(const FastPlan &p, int GB, int CS, FastArgs &a) {
+static size_t plan_geometry(const FastPlan &p, int GB, FastArgs &a) {
     using T = ConvTaps<K, S, P, DX>;
     int dymin = 1 << 20, dymax = -(1 << 20), dxmin = 1 << 20, dxmax = -(1 << 20);
     for (int t = 0; t < T::KK; t++) {
@@ -230,86 +367,90 @@ static size_t plan_geometry(const FastPlan &p, int GB, int CS, FastArgs &a) {
     t.TIWP = t.deint ? 2 * t.HALF : t.TIW;
     a.lcol = t.deint ? 1 : IS / step;
     t.imgs = t.TIH * t.TIWP;
-    t.chs = p.IMGS * t.imgs;
+    t.chs = 0;
     tilegeo_finish(t);
+    a.plane = (p.IMGS * t.imgs + 16 * FAST_NW - 1) / (16 * FAST_NW) * (16 * FAST_NW);
+    a.ppw = a.plane / (16 * FAST_NW);
+    if (a.ppw > WinRows<T::KK>::MAX || t.TIH > 254 || p.IMGS > 255) return 0;
     a.dymin = dymin;
     a.dxmin = dxmin;
     for (int i = 0; i < 9; i++) {
         a.tapoff[i] = 0;
         if (i < T::KK) {
-            int dyp = T::dy(i) - dymin, dxp = T::dx(i) - dxmin;
+            const int dyp = T::dy(i) - dymin, dxp = T::dx(i) - dxmin;
             a.tapoff[i] = dyp * t.TIWP + (t.deint ? (dxp & 1) * t.HALF + (dxp >> 1) : dxp);
         }
     }
-    size_t xsf = dma_region((size_t)p.CH * t.chs);
-    size_t wsf = (size_t)p.MB * (p.CH / 2) * T::KK * 64;
-    a.xregion = (int)xsf;
-    a.stage = (int)(xsf + wsf);
-    (void)CS;
-    return 2 * (xsf + wsf) * 4;  // double-buffered stages
+    a.xwords = p.CH * a.plane;
+    a.stage = a.xwords + p.MB * p.CH * T::KK * 32 + 64;
+    return (size_t)2 * a.stage * 4;
+}
+
+template <int K, int S, int P, bool DX>
+static bool plan_ok(FastPlan &p, int CS, int GA, int GB, FastArgs &a) {
+    using T = ConvTaps<K, S, P, DX>;
+    const int CSe = std::max(8, (CS + 7) & ~7);
+    p.CH = std::min(p.CH, std::min(32, CSe));
+    p.TR = std::min(p.TR, GA);
+    if (p.TR <= 0 || p.IMGS <= 0 || p.CH < 8 || p.CH % 8) return false;
+    const bool shape_ok = T::NCLS == 1 ? ((p.NPW == 2 && p.MB == 1) || (p.NPW == 1 && p.MB == 1) ||
+                                          (p.NPW == 1 && p.MB == 2))
+                                       : (p.NPW == 1 && p.MB == 1);
+    if (!shape_ok || p.IMGS * p.TR * GB > FAST_NW * p.NPW * 32) return false;
+    p.lds = plan_geometry<K, S, P, DX>(p, GB, a);
+    return p.lds > 0 && p.lds <= 160 * 1024;
 }
 
 // Tile choice: RNN_CONV_PLAN="TR,IMGS,CH,NPW,MB[,WPC]" overrides (tuning
-// sweeps); otherwise up to 256 positions per workgroup, whole images first,
-// within 80 KB of LDS (two workgroups per CU) when possible.
+// sweeps); otherwise the largest tile of up to 128*NPW positions (whole
+// images first) and the widest channel chunk that leave room for two
+// workgroups per CU, else one.
 template <int K, int S, int P, bool DX>
 static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs &a) {
-    const int CSe = (CS + 1) & ~1;
+    using T = ConvTaps<K, S, P, DX>;
     if (const char *env = getenv("RNN_CONV_PLAN")) {
         FastPlan p{};
         if (sscanf(env, "%d,%d,%d,%d,%d,%d", &p.TR, &p.IMGS, &p.CH, &p.NPW, &p.MB, &p.wpc) >= 5 &&
-            p.TR > 0 &&
-            p.IMGS > 0 && p.CH >= 2 && p.CH % 2 == 0 && (p.NPW == 1 || p.NPW == 2) &&
-            (p.MB == 1 || p.MB == 2)) {
-            p.CH = std::min(p.CH, CSe);
-            p.TR = std::min(p.TR, GA);
-            p.lds = plan_geometry<K, S, P, DX>(p, GB, CS, a);
-            if (p.lds <= 160 * 1024 && p.IMGS * p.TR * GB <= 4 * p.NPW * 32) {
-                best = p;
-                return true;
-            }
+            plan_ok<K, S, P, DX>(p, CS, GA, GB, a)) {
+            best = p;
+            return true;
         }
     }
     if (GB > 256) return false;
-    const int mbs[2] = {1, 2};
     for (size_t budget : {(size_t)80 * 1024, (size_t)160 * 1024}) {
         for (int npw : {2, 1}) {
-            for (int mb : mbs) {
-                if (mb == 2 && CD <= 32) continue;
-                // stride-2 dX keeps 4 class accumulators per (mb, group)
-                if (ConvTaps<K, S, P, DX>::NCLS * npw * mb > 4) continue;
-                const int target = 4 * npw * 32;
-                for (int ch : {32, 16, 8, 4, 2}) {
-                    if (ch > CSe && ch != std::min(32, CSe)) continue;
-                    FastPlan p{};
-                    p.CH = std::min(ch, CSe);
-                    p.NPW = npw;
-                    p.MB = mb;
-                    if (GA * GB <= target) {
-                        p.TR = GA;
-                        p.IMGS = std::max(1, target / (GA * GB));
-                    } else {
-                        p.TR = std::max(1, std::min(GA, target / GB));
-                        p.IMGS = 1;
+            if (T::NCLS > 1 && npw > 1) continue;
+            const int mb = 1;
+            for (int ch : {32, 16, 8}) {
+                FastPlan p{};
+                p.CH = ch;
+                p.NPW = npw;
+                p.MB = mb;
+                const int target = FAST_NW * npw * 32;
+                if (GA * GB <= target) {
+                    p.TR = GA;
+                    p.IMGS = std::max(1, target / (GA * GB));
+                } else {
+                    p.TR = std::max(1, std::min(GA, target / GB));
+                    p.IMGS = 1;
+                }
+                for (;;) {
+                    FastPlan q = p;
+                    if (plan_ok<K, S, P, DX>(q, CS, GA, GB, a) && q.lds <= budget) {
+                        best = q;
+                        return true;
                     }
-                    for (;;) {
-                        p.lds = plan_geometry<K, S, P, DX>(p, GB, CS, a);
-                        if (p.lds <= budget) {
-                            best = p;
-                            plan_geometry<K, S, P, DX>(p, GB, CS, a);
-                            return true;
-                        }
-                        if (p.IMGS > 1)
-                            p.IMGS /= 2;
-                        else if (p.TR > 1)
-                            p.TR = (p.TR + 1) / 2;
-                        else
-                            break;
-                    }
+                    if (p.IMGS > 1)
+                        p.IMGS /= 2;
+                    else if (p.TR > 1)
+                        p.TR = (p.TR + 1) / 2;
+                    else
+                        break;
                 }
             }
         }
     }
+    (void)CD;
     return false;
 }
 
@@ -327,9 +468,10 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
     if (!attr) {
         attr = true;
         set_attr<K, S, P, DX, 1, 1>();
-        set_attr<K, S, P, DX, 2, 1>();
-        set_attr<K, S, P, DX, 1, 2>();
-        set_attr<K, S, P, DX, 2, 2>();
+        if constexpr (T::NCLS == 1) {
+            set_attr<K, S, P, DX, 2, 1>();
+            set_attr<K, S, P, DX, 1, 2>();
+        }
     }
     FastArgs a;
     std::memset(&a, 0, sizeof(a));
@@ -361,25 +503,17 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
         a.sm = T::KK;  // W^T: m = cin, ch = cout
         a.sc = cin * T::KK;
     }
+    const long long wbytes = (long long)cout * cin * T::KK * 4;
     FastPlan p;
     if (!choose_plan<K, S, P, DX>(a.CS, a.CD, a.GA, a.GB, p, a))
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: no LDS tiling for a %dx%d grid", a.GA, a.GB);
+    if ((long long)p.IMGS * a.CS * a.HS * a.WS * 4 >= 0x7FFFFFF0ll || wbytes >= 0x7FFFFFF0ll)
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: tile source or weights beyond 2 GiB");
+    a.wbytes = (int)wbytes;
     a.TR = p.TR;
     a.tiles_a = (a.GA + p.TR - 1) / p.TR;
     a.CH = p.CH;
     a.nchunks = (a.CS + p.CH - 1) / p.CH;
-    const int nmblk_all = (a.CD + 31) / 32;
-    const size_t wf_len = (size_t)nmblk_all * a.nchunks * (p.CH / 2) * T::KK * 64;
-    if ((long long)p.IMGS * a.CS * a.HS * a.WS * 4 >= 0x7FFFFFF0ll || wf_len * 4 >= (1ull << 31))
-        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: tile source or weights beyond 2 GiB");
-    float *wf = (float *)rnn_workspace(ctx, wf_len * sizeof(float));
-    if (!wf) return RNN_E_NOMEM;
-    a.wf = wf;
-    hipLaunchKernelGGL(prep_fragments_kernel, dim3((unsigned)rnn_div_up(wf_len, 256)), dim3(256), 0,
-                       ctx->stream, w, wf, a.CD, a.CS, p.CH, a.nchunks, nmblk_all, T::KK, a.sm,
-                       a.sc);
-    RNN_LAUNCHED(ctx);
-    const int nw = std::max(1, std::min(4, (p.IMGS * p.TR * a.GB + 32 * p.NPW - 1) / (32 * p.NPW)));
     const int nmblk = (a.CD + 31) / 32;
     a.ntiles = a.tiles_a * ((n + p.IMGS - 1) / p.IMGS);
     a.ngroups = (nmblk + p.MB - 1) / p.MB;
@@ -388,19 +522,21 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
     // Persistent grid: as many workgroups as fit on the chip at once.
     auto run = [&](auto kern) -> int {
         int occ = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 64 * nw, p.lds) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 64 * FAST_NW, p.lds) !=
+                hipSuccess ||
             occ < 1)
             occ = 1;
         if (p.wpc > 0) occ = std::min(occ, p.wpc);
         const long long grid = std::min<long long>(nitems, (long long)ctx->num_cus * occ);
-        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * nw), p.lds, ctx->stream, a);
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * FAST_NW), p.lds, ctx->stream, a);
         RNN_LAUNCHED(ctx);
         return RNN_OK;
     };
-    if (p.NPW == 2 && p.MB == 1) return run(conv_fast_kernel<K, S, P, DX, 2, 1>);
-    if (p.NPW == 1 && p.MB == 1) return run(conv_fast_kernel<K, S, P, DX, 1, 1>);
-    if (p.NPW == 2 && p.MB == 2) return run(conv_fast_kernel<K, S, P, DX, 2, 2>);
-    return run(conv_fast_kernel<K, S, P, DX, 1, 2>);
+    if constexpr (T::NCLS == 1) {
+        if (p.NPW == 2) return run(conv_fast_kernel<K, S, P, DX, 2, 1>);
+        if (p.MB == 2) return run(conv_fast_kernel<K, S, P, DX, 1, 2>);
+    }
+    return run(conv_fast_kernel<K, S, P, DX, 1, 1>);
 }
 
 }  // namespace

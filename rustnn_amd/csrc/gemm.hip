@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     __shared__ float As[2][BM * LDK];
     __shared__ float Bs[2][BN * LDK];
     constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int wm = wave >> 1, wn = wave & 1;
     const long long z = blockIdx.z;
     const float *A = g.a + z * g.stride_a;

@@ -75,6 +75,12 @@ static inline size_t rnn_round_up(size_t a, size_t b) { return rnn_div_up(a, b) 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// Index of the calling wave in its workgroup, as a wave-uniform (scalar)
+// value: loops and branches on it stay scalar instead of exec-masked.
+__device__ __forceinline__ int wave_index() {
+    return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
 // Entry points implemented in the kernel sources, called from the C ABI.
 int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
                     size_t stride_a, int at, const float *b, size_t stride_b, int bt, float *c,
