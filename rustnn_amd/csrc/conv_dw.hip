@@ -4,17 +4,27 @@
 //                       X[n][ci][oy*s + kh - pad][ox*s + kw - pad]
 //
 // Reference: conv.rs dw_image (277-322) folded per image and reduced over
-// rayon workers in Conv2d::backward_w (nn.rs:193-227).  Here GEMM M = co
-// (32 per block), N = ci (32 per block) for each tap, K = output pixels.  A
-// workgroup owns a (co block, ci block) pair and a strided set of pixel tiles
-// (TR output rows of IMGS images).  Per tile it stages the X halo window and
-// the dY window in LDS with odd channel strides (lanes index channels, so an
-// odd stride keeps every 32-lane b32 read conflict-free), then each wave takes
-// whole tile rows: one K step = pixel pair (2q, 2q+1) of a row, lane half h
-// carrying pixel 2q+h, one 32x32 accumulator per tap.  The waves' sums are
-// added in LDS in wave order and the workgroup writes one partial slab; slabs
-// are added in slab order by a two-level reduction (no atomics: the result is
-// bit-reproducible).
+// rayon workers in Conv2d::backward_w (nn.rs:193-227).  GEMM M = co (32 per
+// block), N = ci (32 per block) for each tap, K = output pixels.
+//
+// A workgroup owns a (co block, ci block) pair and walks a strided set of
+// pixel tiles (TR output rows of IMGS images, full width).  Each tile is
+// staged by DMA into one of two LDS buffers while the previous one is
+// computed:
+//   * the dY window [co][img][r][OWP] and the X halo window [ci][img][ty][TIWP]
+//     (stride 2: even columns then odd columns), one LDS channel every 64m+4
+//     words so that the 32 lanes of a b128 read hit distinct banks while no
+//     64-word DMA row straddles two channels;
+//   * per-lane DMA source offsets come from small register tables built once
+//     per workgroup, so a DMA row costs a few integer ops.
+// Compute: a wave takes 8-pixel groups of a tile row; lane half h reads the 4
+// pixels 4h..4h+3 of the group with one ds_read_b128 for dY and, per kernel
+// row kh, the 6 (or 5 + 4) X values those pixels touch, so the three kw taps
+// are register offsets into the same read.  MFMA k-step i takes pixels i and
+// 4 + i; the 9 tap accumulators are independent chains.  The waves' sums are
+// added through LDS in wave order and the workgroup writes one partial slab;
+// slabs are added in slab order by a two-level reduction (no atomics: the
+// result is bit-reproducible).
 #include "conv_common.h"
 
 #include <algorithm>
@@ -23,205 +33,479 @@
 
 namespace {
 
+constexpr int DW_NW = 8;  // waves per workgroup (one workgroup per CU, two waves per SIMD)
+
 struct DwArgs {
     const float *dy;  // [N][CO][OH][OW]
     const float *x;   // [N][CI][H][W]
     float *part;      // [nz][CO][CI*KK]
     int N, CO, CI, H, W, OH, OW;
-    int IS, pad;
-    int TR, GBP, tiles_a, ntiles, nz;
-    int xlrow, xlcol;  // X-window rows / columns per output row / column step
-    int xregion;       // LDS words of the X window region (64-word rows)
-    int stage;         // LDS words of one stage buffer (X window + dY window)
-    TileGeo xg, dg;    // X window [32 ci][IMGS][TIH][TIWP]; dY window [32 co][IMGS][TR][GBP]
-    int tapoff[9];
+    int S, pad;
+    int TR, IMGS, OWP;       // tile: TR output rows of IMGS images, rows padded to OWP
+    int tiles_a, ntiles, nz;
+    int TIH, TIWP, HE;       // X window rows, row length, even-column part (stride-2 3x3)
+    int xrow, xstep;         // X window rows per output row; source rows per window row
+    int ximg, dimg;          // window positions per image (X, dY)
+    int mx, md;              // 64-word DMA rows per channel (X, dY)
+    int chsx, chsd;          // LDS channel strides: 64*m + 4
+    int xwords;              // LDS words of the X region (32 * chsx)
+    int stage;               // LDS words of one stage: X, dY, 64-word sink
+    int ngroups;             // 8-pixel groups per tile
+    int gpr;                 // groups per tile row (OWP / 8)
+    int hw, ohw, cihw, cohw; // H*W, OH*OW, CI*H*W, CO*OH*OW
+    FastDiv fd_gpr, fd_tr, fd_ximg, fd_tiwp, fd_dimg, fd_owp;
+    int nbuf;                // stage buffers (1 or 2)
 };
 
-template <int K>
-__global__ __launch_bounds__(256, 2) void conv_dw_kernel(DwArgs g) {
-    constexpr int KK = K * K;
-    extern __shared__ float smem[];
-    const int nthreads = blockDim.x, nw = nthreads >> 6;
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(), h = lane >> 5, l32 = lane & 31;
-    const int z = blockIdx.x, cob = blockIdx.y, cib = blockIdx.z;
-    const int rows = g.xg.IMGS * g.TR;
-    const int npairs = g.GBP >> 1;
-    const long long ximg = (long long)g.CI * g.H * g.W, dyimg = (long long)g.CO * g.OH * g.OW;
+// Per-lane DMA table entry: (element offset in the image plane, 16 bits) |
+// window row << 16 | image << 24; window row 255 marks a position without
+// source data (padding or outside the image columns).
+constexpr int DW_NOROW = 255 << 16;
 
-    f32x16 acc[KK];
+template <int MT>
+struct DwLane {
+    int tx[MT];  // X window rows
+    int td[MT];  // dY window rows
+};
+
+template <int K, int S, int MT>
+__device__ __forceinline__ void dw_lane_init(const DwArgs &g, DwLane<MT> &L, int lane) {
 #pragma unroll
-    for (int t = 0; t < KK; t++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
-
-    const int abase = l32 * g.dg.chs + h;
-    const int bbase = l32 * g.xg.chs + h * g.xlcol;
-
-    // Stage = one pixel tile (X window + dY window) in one of two LDS buffers;
-    // the next tile is staged while the current one is computed.
-    auto issue = [&](int tile, float *buf) {
-        const int ta = tile % g.tiles_a, tn = tile / g.tiles_a;
-        const int a0 = ta * g.TR, n0 = tn * g.xg.IMGS;
-        const int nimg = min(g.N - n0, g.xg.IMGS);
-        const __amdgpu_buffer_rsrc_t rs_x =
-            make_rsrc(g.x + (long long)n0 * ximg, (uint32_t)(nimg * ximg * 4));
-        const __amdgpu_buffer_rsrc_t rs_dy =
-            make_rsrc(g.dy + (long long)n0 * dyimg, (uint32_t)(nimg * dyimg * 4));
-        dma_tile(rs_x, g.N, g.CI, g.H, g.W, n0, cib * 32, 32, a0 * g.IS - g.pad, -g.pad, g.xg, buf,
-                 wave, nw, lane);
-        dma_tile(rs_dy, g.N, g.CO, g.OH, g.OW, n0, cob * 32, 32, a0, 0, g.dg, buf + g.xregion,
-                 wave, nw, lane);
-    };
-
-    int s = 0;
-    if (z < g.ntiles) issue(z, smem);
-    for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
-        dma_wait_barrier();
-        const float *xs = smem + (s & 1) * g.stage;
-        const float *dys = xs + g.xregion;
-        if (tile + g.nz < g.ntiles) issue(tile + g.nz, smem + ((s + 1) & 1) * g.stage);
-        for (int row = wave; row < rows; row += nw) {
-            const int img = row / g.TR, r = row - img * g.TR;
-            const float *arow = dys + abase + img * g.dg.imgs + r * g.GBP;
-            const float *xrow = xs + bbase + img * g.xg.imgs + r * g.xlrow * g.xg.TIWP;
-            // operands of pixel pair q+1 are fetched while pair q's MFMAs run
-            float av[2], bv[2][KK];
-            auto fetch = [&](int q, int slot) {
-                av[slot] = arow[2 * q];
-                const float *xb = xrow + 2 * q * g.xlcol;
-                static_for<0, KK>([&](auto tc) {
-                    constexpr int t = decltype(tc)::value;
-                    bv[slot][t] = xb[g.tapoff[t]];
-                });
-            };
-            auto mma = [&](int slot) {
-                static_for<0, KK>([&](auto tc) {
-                    constexpr int t = decltype(tc)::value;
-                    acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[slot], bv[slot][t], acc[t], 0,
-                                                                  0, 0);
-                });
-            };
-            fetch(0, 0);
-            int q = 0;
-            for (; q + 2 <= npairs; q += 2) {
-                fetch(q + 1, 1);
-                mma(0);
-                if (q + 2 < npairs) fetch(q + 2, 0);
-                mma(1);
-            }
-            if (q < npairs) mma(0);
+    for (int j = 0; j < MT; j++) {
+        // X window position p = 64j + lane of a channel plane
+        {
+            const int p = 64 * j + lane;
+            const int img = (int)fdiv((uint32_t)p, g.fd_ximg), rem = p - img * g.ximg;
+            const int ty = (int)fdiv((uint32_t)rem, g.fd_tiwp), wc = rem - ty * g.TIWP;
+            int x;
+            if (K == 1)
+                x = wc * S - g.pad;
+            else if (S == 1)
+                x = wc - g.pad;
+            else
+                x = wc < g.HE ? 2 * wc - g.pad : 2 * (wc - g.HE) + 1 - g.pad;
+            const bool ok = j < g.mx && img < g.IMGS && x >= 0 && x < g.W;
+            L.tx[j] = ok ? ((ty * g.xstep * g.W + x) | (ty << 16) | (img << 24)) : DW_NOROW;
         }
-    }
-    // Sum the waves in wave order through LDS, then write the slab.
-    dma_wait_barrier();
-    float *red = smem;  // KK*1024 floats
-    for (int w = 0; w < nw; w++) {
-        if (wave == w) {
-#pragma unroll
-            for (int t = 0; t < KK; t++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    const int i = 8 * (v >> 2) + 4 * h + (v & 3);  // co
-                    const int e = t * 1024 + i * 32 + l32;          // l32 = ci
-                    red[e] = (w == 0) ? acc[t][v] : red[e] + acc[t][v];
-                }
+        // dY window position
+        {
+            const int p = 64 * j + lane;
+            const int img = (int)fdiv((uint32_t)p, g.fd_dimg), rem = p - img * g.dimg;
+            const int r = (int)fdiv((uint32_t)rem, g.fd_owp), col = rem - r * g.OWP;
+            const bool ok = j < g.md && img < g.IMGS && col < g.OW;
+            L.td[j] = ok ? ((r * g.OW + col) | (r << 16) | (img << 24)) : DW_NOROW;
         }
-        __syncthreads();
-    }
-    const int ckk = g.CI * KK;
-    float *slab = g.part + (long long)z * g.CO * ckk;
-    for (int e = tid; e < KK * 1024; e += nthreads) {
-        const int t = e >> 10, i = (e >> 5) & 31, c = e & 31;
-        const int co = cob * 32 + i, ci = cib * 32 + c;
-        if (co < g.CO && ci < g.CI) slab[(long long)co * ckk + ci * KK + t] = red[e];
     }
 }
 
-// tmp[gz][e] = sum of slabs [gz*G, min(nz, gz*G + G)) in slab order.
+// Wave-uniform description of the tile being staged plus, per lane, the
+// byte offset of each DMA row's element for the block's first channel (or
+// DMA_OOB when the position has no source data).  A channel adds c*H*W*4;
+// min() with DMA_OOB keeps out-of-range positions out of range.
+template <int MT>
+struct DwStage {
+    __amdgpu_buffer_rsrc_t rx, rd;  // X / dY images n0 .. n0 + IMGS
+    float *buf, *sink;
+    int valid;
+    uint32_t xo[MT], dof[MT];
+};
+
+template <int MT>
+__device__ __forceinline__ DwStage<MT> dw_stage(const DwArgs &g, const DwLane<MT> &L, int tile,
+                                                int cob, int cib, float *buf) {
+    DwStage<MT> d;
+    d.valid = tile < g.ntiles;
+    if (!d.valid) tile = 0;
+    const int n0 = (tile / g.tiles_a) * g.IMGS, a0 = (tile % g.tiles_a) * g.TR;
+    const int nimg0 = min(g.N - n0, g.IMGS);
+    d.rx = make_rsrc(g.x + (long long)n0 * g.cihw, (uint32_t)(nimg0 * (long long)g.cihw * 4));
+    d.rd = make_rsrc(g.dy + (long long)n0 * g.cohw, (uint32_t)(nimg0 * (long long)g.cohw * 4));
+    d.buf = buf;
+    d.sink = buf + g.stage - 64;
+    const int y0 = a0 * g.S - g.pad;
+    int ylo = y0 >= 0 ? 0 : (-y0 + g.xstep - 1) / g.xstep;
+    int yhi = min(g.TIH, (g.H - y0 + g.xstep - 1) / g.xstep);
+    if (yhi < ylo) yhi = ylo;
+    const int rhi = min(g.TR, g.OH - a0);
+    const int nimg = d.valid ? nimg0 : 0;
+    const int xb = cib * 32 * g.hw + y0 * g.W, db = cob * 32 * g.ohw + a0 * g.OW;
+#pragma unroll
+    for (int j = 0; j < MT; j++) {
+        {
+            const int e = L.tx[j];
+            const int ty = (e >> 16) & 255, img = e >> 24;
+            const bool ok = (unsigned)(ty - ylo) < (unsigned)(yhi - ylo) && img < nimg;
+            d.xo[j] = ok ? (uint32_t)(img * g.cihw + xb + (e & 0xFFFF)) * 4u : DMA_OOB;
+        }
+        {
+            const int e = L.td[j];
+            const int r = (e >> 16) & 255, img = e >> 24;
+            const bool ok = r < rhi && img < nimg;
+            d.dof[j] = ok ? (uint32_t)(img * g.cohw + db + (e & 0xFFFF)) * 4u : DMA_OOB;
+        }
+    }
+    return d;
+}
+
+// DMA of all rows of block channel c (X and dY) of stage d.
+template <int MT>
+__device__ __forceinline__ void dw_issue_channel(const DwArgs &g, const DwStage<MT> &d, int c,
+                                                 int cob, int cib, float *__restrict__ buf) {
+    if (!d.valid) return;
+    const uint32_t cx = cib * 32 + c < g.CI ? (uint32_t)(c * g.hw) * 4u : DMA_OOB;
+    const uint32_t cd = cob * 32 + c < g.CO ? (uint32_t)(c * g.ohw) * 4u : DMA_OOB;
+#pragma unroll
+    for (int j = 0; j < MT; j++) {
+        if (j < g.mx)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rx, (lds_ptr_t)(buf + c * g.chsx + 64 * j), 4,
+                                                     min(d.xo[j] + cx, DMA_OOB), 0, 0, 0);
+        if (j < g.md)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                d.rd, (lds_ptr_t)(buf + g.xwords + c * g.chsd + 64 * j), 4,
+                min(d.dof[j] + cd, DMA_OOB), 0, 0, 0);
+    }
+}
+
+// Operands of one 8-pixel group.
+template <int K, int S>
+struct DwOps {
+    float4 a;                                   // dY: pixels 4h .. 4h+3
+    float4 x0[K];                               // X: 4 values from 4h (even part for S = 2)
+    float2 x1[K];                               // X: the 2 values after them
+    float4 xo[(K == 3 && S == 2) ? K : 1];      // X odd columns (stride-2 3x3)
+};
+
+template <int K, int S>
+__device__ __forceinline__ void dw_fetch(const DwArgs &g, const float *__restrict__ xs,
+                                         const float *__restrict__ ds, int grp, int lane,
+                                         DwOps<K, S> &o) {
+    const int h = lane >> 5, l32 = lane & 31;
+    // group -> (tile row rr = img*TR + r, column group cq); the dY window is
+    // dense in groups, so its offset is 8*grp
+    const int rr = (int)fdiv((uint32_t)grp, g.fd_gpr), cq = grp - rr * g.gpr;
+    const int img = (int)fdiv((uint32_t)rr, g.fd_tr), r = rr - img * g.TR;
+    o.a = *reinterpret_cast<const float4 *>(ds + l32 * g.chsd + 8 * grp + 4 * h);
+    const float *xr =
+        xs + l32 * g.chsx + img * g.ximg + r * g.xrow * g.TIWP + 8 * cq + 4 * h;
+#pragma unroll
+    for (int kh = 0; kh < K; kh++) {
+        o.x0[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP);
+        if constexpr (K == 3) {
+            // 2 more values: b64 read of the next 4-aligned group
+            o.x1[kh] = *reinterpret_cast<const float2 *>(xr + kh * g.TIWP + 4);
+        }
+        if constexpr (K == 3 && S == 2)
+            o.xo[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP + g.HE);
+    }
+}
+
+// B value of tap (kh, kw) for k-step i.
+template <int K, int S>
+__device__ __forceinline__ float dw_bval(const DwOps<K, S> &o, int kh, int kw, int i) {
+    if constexpr (K == 1) {
+        return o.x0[0][i];
+    } else if constexpr (S == 1) {
+        const int v = kw + i;  // compile-time after unrolling
+        return v < 4 ? o.x0[kh][v] : (v == 4 ? o.x1[kh].x : o.x1[kh].y);
+    } else {
+        if (kw == 1) return o.xo[kh][i];
+        const int v = i + (kw >> 1);
+        return v < 4 ? o.x0[kh][v] : o.x1[kh].x;
+    }
+}
+
+// DMA of a whole tile: every channel of this wave.
+template <int MT>
+__device__ __forceinline__ void dw_issue_tile(const DwArgs &g, const DwLane<MT> &L, int tile,
+                                              int cob, int cib, float *__restrict__ buf,
+                                              int wave) {
+    const DwStage<MT> d = dw_stage<MT>(g, L, tile, cob, cib, buf);
+    for (int k = 0; k < 32 / DW_NW; k++)
+        dw_issue_channel<MT>(g, d, wave + DW_NW * k, cob, cib, buf);
+}
+
+// MFMAs of one 8-pixel group: k-step i takes pixels i and 4 + i.
+template <int K, int S>
+__device__ __forceinline__ void dw_mma(const DwOps<K, S> &o, f32x16 (&acc)[K == 1 ? 4 : K * K]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if constexpr (K == 1) {
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i], dw_bval<K, S>(o, 0, 0, i),
+                                                          acc[i], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int t = 0; t < K * K; t++)
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                    o.a[i], dw_bval<K, S>(o, t / K, t % K, i), acc[t], 0, 0, 0);
+        }
+    }
+}
+
+// Scheduling hint for one step: the LDS reads of the next group go out
+// among the first MFMAs of this one, so their latency hides under the rest.
+template <int K, int S>
+__device__ __forceinline__ void dw_step_schedule() {
+    constexpr int NMF = K == 1 ? 4 : 4 * K * K;
+    constexpr int NRD = 1 + (K == 1 ? 1 : K * (S == 2 ? 3 : 2));
+    static_for<0, NRD>([&](auto) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+    });
+    __builtin_amdgcn_sched_group_barrier(0x008, NMF - NRD, 0);
+}
+
+// The GEMM steps of one staged tile: 8-pixel groups wave, wave + NW, ...;
+// two operand sets alternate so that the reads of group n+1 overlap the
+// MFMAs of group n.  Reads past the tile's last group are clamped to group
+// `wave` (in range; their values are not used).  When `dma` is set, the
+// channels of the next tile that this wave stages are issued a few per step,
+// after the step's MFMAs, so that the other wave of the SIMD computes while
+// this one waits on the address unit.
+template <int K, int S, int MT>
+__device__ __forceinline__ void dw_compute(const DwArgs &g, const float *__restrict__ cur,
+                                           float *__restrict__ nxt, const DwStage<MT> &dma,
+                                           bool do_dma, int cob, int cib, int wave, int lane,
+                                           f32x16 (&acc)[K == 1 ? 4 : K * K]) {
+    constexpr int NCH = 32 / DW_NW;  // channels each wave stages
+    const float *xs = cur, *ds = cur + g.xwords;
+    const int nsteps = (g.ngroups - wave + DW_NW - 1) / DW_NW;
+    auto grp = [&](int s) {
+        const int gi = wave + DW_NW * s;
+        return gi < g.ngroups ? gi : min(wave, g.ngroups - 1);
+    };
+    int issued = 0;
+    auto dma_upto = [&](int s) {  // channels due once step s is done
+        if (!do_dma) return;
+        const int due = nsteps > 0 ? min(NCH, ((s + 1) * NCH + nsteps - 1) / nsteps) : NCH;
+        for (; issued < due; issued++)
+            dw_issue_channel<MT>(g, dma, wave + DW_NW * issued, cob, cib, nxt);
+    };
+    DwOps<K, S> oa, ob;
+    dw_fetch<K, S>(g, xs, ds, grp(0), lane, oa);
+#pragma unroll 1
+    for (int s = 0; s < nsteps; s += 2) {
+        dw_fetch<K, S>(g, xs, ds, grp(s + 1), lane, ob);
+        dw_mma<K, S>(oa, acc);
+        dw_step_schedule<K, S>();
+        dma_upto(s);
+        if (s + 1 >= nsteps) break;
+        dw_fetch<K, S>(g, xs, ds, grp(s + 2), lane, oa);
+        dw_mma<K, S>(ob, acc);
+        dw_step_schedule<K, S>();
+        dma_upto(s + 1);
+    }
+    dma_upto(nsteps);
+}
+
+// Double-buffered stage: the tile in `cur` is computed while the next tile
+// is staged into `nxt`.  The buffers are distinct; the __restrict__
+// qualifiers give the compiler the alias scopes it needs to not wait for the
+// DMA before the LDS reads.
+template <int K, int S, int MT>
+__device__ __forceinline__ void dw_stage2(const DwArgs &g, const float *__restrict__ cur,
+                                          float *__restrict__ nxt, int next_tile,
+                                          const DwLane<MT> &L, int cob, int cib, int wave,
+                                          int lane, f32x16 (&acc)[K == 1 ? 4 : K * K]) {
+    const DwStage<MT> d = dw_stage<MT>(g, L, next_tile, cob, cib, nxt);
+    dw_compute<K, S, MT>(g, cur, nxt, d, true, cob, cib, wave, lane, acc);
+}
+
+// Accumulator v of tap t of this lane lives at slab-order slot
+// ((8*(v/4) + 4*h + v%4)*32 + l32)*KK + t = (lbase + 32*(8*(v/4) + v%4))*KK + t.
+template <int KK>
+__device__ __forceinline__ void dw_red_store(float *dst, int lbase, const f32x16 *acc) {
+#pragma unroll
+    for (int t = 0; t < KK; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+            dst[(lbase + 32 * (8 * (v >> 2) + (v & 3))) * KK + t] = acc[t][v];
+}
+
+template <int KK>
+__device__ __forceinline__ void dw_red_add(const float *src, int lbase, f32x16 *acc) {
+#pragma unroll
+    for (int t = 0; t < KK; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+            acc[t][v] += src[(lbase + 32 * (8 * (v >> 2) + (v & 3))) * KK + t];
+}
+
+template <int K, int S, int MT, int NB>
+__global__ __launch_bounds__(64 * DW_NW) void conv_dw_kernel(DwArgs g) {
+    constexpr int KK = K * K, NA = K == 1 ? 4 : KK;
+    extern __shared__ float smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+    const int h = lane >> 5, l32 = lane & 31;
+    const int z = blockIdx.x, cob = blockIdx.y, cib = blockIdx.z;
+
+    DwLane<MT> L;
+    dw_lane_init<K, S, MT>(g, L, lane);
+
+    f32x16 acc[NA];
+#pragma unroll
+    for (int t = 0; t < NA; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
+
+    // Tiles z, z + nz, ...  With two stage buffers the next tile is staged
+    // while this one is computed; with one (larger tiles), the other
+    // workgroups on the CU compute while this one stages.
+    dw_issue_tile<MT>(g, L, z, cob, cib, smem, wave);
+    int s = 0;
+    for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
+        dma_wait_barrier();
+        if constexpr (NB == 2) {
+            dw_stage2<K, S, MT>(g, smem + (s & 1) * g.stage, smem + ((s + 1) & 1) * g.stage,
+                                tile + g.nz, L, cob, cib, wave, lane, acc);
+        } else {
+            DwStage<MT> none;
+            none.valid = 0;
+            dw_compute<K, S, MT>(g, smem, smem, none, false, cob, cib, wave, lane, acc);
+            __syncthreads();
+            if (tile + g.nz < g.ntiles) dw_issue_tile<MT>(g, L, tile + g.nz, cob, cib, smem, wave);
+        }
+    }
+    if constexpr (K == 1) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[0][v] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
+    }
+    // Sum the eight waves' accumulators in a fixed order, ((w0 + w4) + (w1 +
+    // w5)) + ((w2 + w6) + (w3 + w7)), through four LDS slices in slab order
+    // [co][ci][tap] (bit-reproducible), then write contiguous slab rows.
+    dma_wait_barrier();
+    float *red = smem;  // 4 slices of [32][32][KK]
+    const int SL = KK * 1024;
+    const int lbase = 4 * h * 32 + l32;  // slot of (v = 0, t = 0) for this lane
+    if (wave >= 4) dw_red_store<KK>(red + (wave - 4) * SL, lbase, acc);
+    __syncthreads();
+    if (wave < 4) {
+        dw_red_add<KK>(red + wave * SL, lbase, acc);
+    }
+    __syncthreads();
+    if (wave < 4) dw_red_store<KK>(red + wave * SL, lbase, acc);
+    __syncthreads();
+    const int ckk = g.CI * KK, rowlen = 32 * KK;
+    float *slab = g.part + (long long)z * g.CO * ckk + cib * 32 * KK;
+    const int rlim = min(32, g.CI - cib * 32) * KK;
+    for (int e = tid; e < SL; e += DW_NW * 64) {
+        const int co = e / rowlen, rem = e - co * rowlen;
+        const float v = (red[e] + red[SL + e]) + (red[2 * SL + e] + red[3 * SL + e]);
+        if (cob * 32 + co < g.CO && rem < rlim) slab[(long long)(cob * 32 + co) * ckk + rem] = v;
+    }
+}
+
+// tmp[gz][e] = sum of slabs [gz*G, min(nz, gz*G + G)) in slab order; all
+// loads of a thread are issued before the in-order sum (G <= DW_G).
+constexpr int DW_G = 16;
 __global__ void slab_sum_kernel(const float *part, int nz, int G, long long len, float *tmp) {
     const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const int gz = blockIdx.y;
     if (e >= len) return;
-    const int z0 = gz * G, z1 = min(nz, z0 + G);
-    float s = part[(long long)z0 * len + e];
-    for (int z = z0 + 1; z < z1; z++) s += part[(long long)z * len + e];
+    const int z0 = gz * G, n = min(nz, z0 + G) - z0;
+    float v[DW_G];
+#pragma unroll
+    for (int i = 0; i < DW_G; i++) v[i] = i < n ? part[(long long)(z0 + i) * len + e] : 0.f;
+    float s = v[0];
+#pragma unroll
+    for (int i = 1; i < DW_G; i++)
+        if (i < n) s += v[i];
     tmp[(long long)gz * len + e] = s;
 }
 
-// out[e] += sum_g tmp[g][e] in order.
+// out[e] += sum_g tmp[g][e] in order (ng <= DW_G).
 __global__ void slab_final_kernel(const float *tmp, int ng, long long len, float *out) {
     const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= len) return;
-    float s = tmp[e];
-    for (int gz = 1; gz < ng; gz++) s += tmp[(long long)gz * len + e];
+    float v[DW_G];
+#pragma unroll
+    for (int i = 0; i < DW_G; i++) v[i] = i < ng ? tmp[(long long)i * len + e] : 0.f;
+    float s = v[0];
+#pragma unroll
+    for (int i = 1; i < DW_G; i++)
+        if (i < ng) s += v[i];
     out[e] += s;
 }
 
-template <int K>
-void dw_attr() {
-    (void)hipFuncSetAttribute((const void *)conv_dw_kernel<K>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-}
+constexpr int DW_MT[3] = {2, 4, 8};
 
-// Geometry for (TR, IMGS); returns LDS bytes.
-size_t dw_geometry(DwArgs &g, int K, int TR, int IMGS) {
-    const int S = g.IS;
-    const int step = (K == 1) ? S : 1;
+// Geometry of a (TR, IMGS) tile; returns LDS bytes, 0 if the tile does not
+// fit the kernel's tables and formats.
+size_t dw_geometry(DwArgs &g, int K, int TR, int IMGS, int nbuf) {
+    g.nbuf = nbuf;
+    const int S = g.S;
     g.TR = TR;
-    TileGeo &x = g.xg;
-    x.IMGS = IMGS;
-    x.rowstep = step;
-    x.colstep = step;
-    g.xlrow = S / step;
-    x.TIH = (TR - 1) * g.xlrow + K;
-    x.TIW = (g.GBP - 1) * (S / step) + K;
-    x.deint = (S / step) == 2;
-    x.HALF = (x.TIW + 1) / 2;
-    x.TIWP = x.deint ? 2 * x.HALF : x.TIW;
-    g.xlcol = x.deint ? 1 : S / step;
-    x.imgs = x.TIH * x.TIWP;
-    x.chs = IMGS * x.imgs;
-    x.chs += (x.chs & 1) ? 0 : 1;
-    tilegeo_finish(x);
-    TileGeo &d = g.dg;
-    d.IMGS = IMGS;
-    d.rowstep = 1;
-    d.colstep = 1;
-    d.TIH = TR;
-    d.TIW = g.GBP;
-    d.deint = 0;
-    d.HALF = 0;
-    d.TIWP = g.GBP;
-    d.imgs = TR * g.GBP;
-    d.chs = IMGS * d.imgs;
-    d.chs += (d.chs & 1) ? 0 : 1;
-    tilegeo_finish(d);
-    for (int t = 0; t < 9; t++) {
-        g.tapoff[t] = 0;
-        if (t < K * K) {
-            const int kh = t / K, kw = t % K;
-            g.tapoff[t] = kh * x.TIWP + (x.deint ? (kw & 1) * x.HALF + (kw >> 1) : kw);
+    g.IMGS = IMGS;
+    g.gpr = g.OWP / 8;
+    g.ngroups = IMGS * TR * g.gpr;
+    if (K == 1) {
+        g.xrow = 1;
+        g.xstep = S;
+        g.TIH = TR;
+        g.TIWP = g.OWP;
+        g.HE = 0;
+    } else {
+        g.xrow = S;
+        g.xstep = 1;
+        g.TIH = (TR - 1) * S + K;
+        if (S == 1) {
+            g.TIWP = g.OWP + 4;
+            g.HE = 0;
+        } else {
+            g.HE = g.OWP + 4;
+            g.TIWP = g.HE + g.OWP;
         }
     }
-    const size_t xsf = dma_region((size_t)32 * x.chs), dsf = dma_region((size_t)32 * d.chs);
-    g.xregion = (int)xsf;
-    g.stage = (int)(xsf + dsf);
-    return std::max(2 * (xsf + dsf) * 4, (size_t)K * K * 1024 * 4);  // double-buffered
+    g.fd_gpr = make_fastdiv(g.gpr);
+    g.fd_tr = make_fastdiv(TR);
+    g.ximg = g.TIH * g.TIWP;
+    g.dimg = TR * g.OWP;
+    g.fd_ximg = make_fastdiv(g.ximg);
+    g.fd_tiwp = make_fastdiv(g.TIWP);
+    g.fd_dimg = make_fastdiv(g.dimg);
+    g.fd_owp = make_fastdiv(g.OWP);
+    g.mx = (IMGS * g.ximg + 63) / 64;
+    g.md = (IMGS * g.dimg + 63) / 64;
+    if (std::max(g.mx, g.md) > DW_MT[2] || g.TIH > 254 || IMGS > 127) return 0;
+    if ((long long)g.TIH * g.xstep * g.W > 0xFFFF || (long long)TR * g.OW > 0xFFFF) return 0;
+    g.chsx = 64 * g.mx + 4;
+    g.chsd = 64 * g.md + 4;
+    g.xwords = 32 * g.chsx;
+    g.stage = g.xwords + 32 * g.chsd + 64;
+    return std::max((size_t)nbuf * g.stage * 4, (size_t)4 * K * K * 1024 * 4);
+}
+
+template <int K, int S, int MT, int NB>
+const void *dw_kernel_ptr() {
+    static bool attr = false;
+    const void *k = (const void *)conv_dw_kernel<K, S, MT, NB>;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    }
+    return k;
+}
+
+template <int K, int S, int NB>
+const void *dw_pick_mt(int mt) {
+    if (mt <= DW_MT[0]) return dw_kernel_ptr<K, S, DW_MT[0], NB>();
+    if (mt <= DW_MT[1]) return dw_kernel_ptr<K, S, DW_MT[1], NB>();
+    return dw_kernel_ptr<K, S, DW_MT[2], NB>();
+}
+
+template <int K, int S>
+const void *dw_pick(int mt, int nb) {
+    return nb == 2 ? dw_pick_mt<K, S, 2>(mt) : dw_pick_mt<K, S, 1>(mt);
 }
 
 }  // namespace
 
-// dW += sum over images (see above).  k must be 1 or 3.
+// dW += sum over images (see above).  k must be 1 or 3, stride 1 or 2.
 int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
                 float *dw) {
     const int K = sp->k;
     if (K != 1 && K != 3) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: k must be 1 or 3");
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
-        dw_attr<1>();
-        dw_attr<3>();
-    }
+    if (sp->stride != 1 && sp->stride != 2)
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: stride must be 1 or 2");
     DwArgs g;
     std::memset(&g, 0, sizeof(g));
     g.dy = dy;
@@ -233,78 +517,86 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
     g.W = sp->w;
     g.OH = sp->oh;
     g.OW = sp->ow;
-    g.IS = sp->stride;
+    g.S = sp->stride;
     g.pad = sp->pad;
-    g.GBP = (sp->ow + 1) & ~1;
-    if (g.GBP > 512) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: output row too wide");
-    int TR = 0, IMGS = 0, NZ = 0;
-    if (const char *env = getenv("RNN_DW_PLAN"))
-        if (sscanf(env, "%d,%d,%d", &TR, &IMGS, &NZ) != 3) TR = IMGS = NZ = 0;
+    g.OWP = (sp->ow + 7) & ~7;
+    g.hw = g.H * g.W;
+    g.ohw = g.OH * g.OW;
+    if ((long long)g.CI * g.hw >= (1ll << 24) || (long long)g.CO * g.ohw >= (1ll << 24))
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: image planes beyond 2^24 elements");
+    g.cihw = g.CI * g.hw;
+    g.cohw = g.CO * g.ohw;
+    // Plan: RNN_DW_PLAN="TR,IMGS,NZ[,NBUF]" overrides (tuning sweeps).
+    // Otherwise the tile (TR rows of IMGS images) with the most useful
+    // 8-pixel groups -- groups times the fraction of tile rows inside the
+    // image -- whose two stage buffers fit in LDS (one workgroup per CU, so
+    // staging must overlap compute); a single buffer only when two do not fit.
+    int TR = 0, IMGS = 0, NZ = 0, NB = 0;
     size_t lds = 0;
-    if (TR > 0 && IMGS > 0) {
-        TR = std::min(TR, g.OH);
-        lds = dw_geometry(g, K, TR, IMGS);
-        if (lds > 160 * 1024) TR = 0;
+    if (const char *env = getenv("RNN_DW_PLAN")) {
+        if (sscanf(env, "%d,%d,%d,%d", &TR, &IMGS, &NZ, &NB) < 3) TR = IMGS = NZ = 0;
+        if (NB != 1) NB = 2;
+        if (TR > 0 && IMGS > 0) {
+            TR = std::min(TR, g.OH);
+            lds = dw_geometry(g, K, TR, IMGS, NB);
+            if (lds == 0 || lds > 160 * 1024) TR = 0;
+        }
     }
     if (TR <= 0 || IMGS <= 0) {
-        const int target = 256;
-        if (g.OH * g.GBP <= target) {
-            TR = g.OH;
-            IMGS = std::max(1, target / (g.OH * g.GBP));
-        } else {
-            TR = std::max(1, target / g.GBP);
-            IMGS = 1;
-        }
-        const int TR0 = TR, IMGS0 = IMGS;
         bool ok = false;
-        for (size_t budget : {(size_t)80 * 1024, (size_t)160 * 1024}) {
-            TR = TR0;
-            IMGS = IMGS0;
-            for (;;) {
-                lds = dw_geometry(g, K, TR, IMGS);
-                if (lds <= budget) {
-                    ok = true;
-                    break;
+        for (int nb : {2, 1}) {
+            double best = 0;
+            for (int tr = 1; tr <= g.OH; tr++)
+                for (int im = 1; im <= (tr == g.OH ? 16 : 1); im *= 2) {
+                    const size_t l = dw_geometry(g, K, tr, im, nb);
+                    if (l == 0 || l > 160 * 1024) continue;
+                    const int ta = (g.OH + tr - 1) / tr;
+                    const double score = g.ngroups * (double)g.OH / (ta * tr);
+                    if (score > best) {
+                        best = score;
+                        TR = tr;
+                        IMGS = im;
+                        NB = nb;
+                    }
                 }
-                if (IMGS > 1)
-                    IMGS /= 2;
-                else if (TR > 1)
-                    TR = (TR + 1) / 2;
-                else
-                    break;
+            if (best > 0) {
+                lds = dw_geometry(g, K, TR, IMGS, NB);
+                ok = true;
+                break;
             }
-            if (ok) break;
         }
         if (!ok) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: tile exceeds LDS");
     }
-    if ((long long)IMGS * std::max((long long)g.CI * g.H * g.W, (long long)g.CO * g.OH * g.OW) * 4 >=
-        0x7FFFFFF0ll)
+    if ((long long)IMGS * std::max(g.cihw, g.cohw) * 4 >= 0x7FFFFFF0ll)
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: tile source beyond 2 GiB");
     g.tiles_a = (g.OH + g.TR - 1) / g.TR;
     g.ntiles = g.tiles_a * (int)((n + IMGS - 1) / IMGS);
     const int ncb = (g.CO + 31) / 32, ncib = (g.CI + 31) / 32;
+    const int mt = std::max(g.mx, g.md);
+    const void *kern = nullptr;
+    if (K == 3)
+        kern = g.S == 1 ? dw_pick<3, 1>(mt, g.nbuf) : dw_pick<3, 2>(mt, g.nbuf);
+    else
+        kern = g.S == 1 ? dw_pick<1, 1>(mt, g.nbuf) : dw_pick<1, 2>(mt, g.nbuf);
     if (NZ <= 0) {
         // persistent: as many workgroups as fit on the chip at once
         int occ = 0;
-        const void *kern = K == 3 ? (const void *)conv_dw_kernel<3> : (const void *)conv_dw_kernel<1>;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 256, lds) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 64 * DW_NW, lds) !=
+                hipSuccess ||
             occ < 1)
             occ = 1;
         NZ = std::max(1, occ * ctx->num_cus / (ncb * ncib));
     }
-    NZ = std::min(NZ, g.ntiles);
+    NZ = std::min(std::min(NZ, g.ntiles), DW_G * DW_G);  // two reduction levels of <= DW_G
     g.nz = NZ;
     const size_t ckk = (size_t)g.CI * K * K, len = (size_t)g.CO * ckk;
-    const int G = 16, ng = (NZ + G - 1) / G;
+    const int G = DW_G, ng = (NZ + G - 1) / G;
     float *ws = (float *)rnn_workspace(ctx, ((size_t)NZ + (ng > 1 ? ng : 0)) * len * sizeof(float));
     if (!ws) return RNN_E_NOMEM;
     g.part = ws;
-    dim3 grid(NZ, ncb, ncib), block(256);
-    if (K == 3)
-        hipLaunchKernelGGL(conv_dw_kernel<3>, grid, block, lds, ctx->stream, g);
-    else
-        hipLaunchKernelGGL(conv_dw_kernel<1>, grid, block, lds, ctx->stream, g);
-    RNN_LAUNCHED(ctx);
+    dim3 grid(NZ, ncb, ncib), block(64 * DW_NW);
+    void *args[] = {&g};
+    RNN_HIP(ctx, hipLaunchKernel(kern, grid, block, args, lds, ctx->stream));
     const unsigned eb = (unsigned)rnn_div_up(len, 256);
     if (ng > 1) {
         float *tmp = ws + (size_t)NZ * len;

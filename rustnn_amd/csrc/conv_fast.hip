@@ -401,10 +401,14 @@ static bool plan_ok(FastPlan &p, int CS, int GA, int GB, FastArgs &a) {
     return p.lds > 0 && p.lds <= 160 * 1024;
 }
 
-// Tile choice: RNN_CONV_PLAN="TR,IMGS,CH,NPW,MB[,WPC]" overrides (tuning
-// sweeps); otherwise the largest tile of up to 128*NPW positions (whole
-// images first) and the widest channel chunk that leave room for two
-// workgroups per CU, else one.
+// Tile choice.  RNN_CONV_PLAN="TR,IMGS,CH,NPW,MB[,WPC]" overrides (tuning
+// sweeps).  Otherwise rules fitted to measured sweeps on MI355X: channel
+// chunks of a quarter of the source channels (8..32; 32 for 1x1); stride-1 3x3 takes 256
+// positions in two 32-position groups per wave when an image has 256 or more
+// positions, else 128 positions (whole images); strided forward takes 64
+// positions and two output-channel blocks; strided dX and 1x1 take 64 or 128
+// positions in one group per wave.  A plan that does not fit falls back to
+// shrinking the tile.
 template <int K, int S, int P, bool DX>
 static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs &a) {
     using T = ConvTaps<K, S, P, DX>;
@@ -417,41 +421,49 @@ static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs
         }
     }
     if (GB > 256) return false;
-    for (size_t budget : {(size_t)80 * 1024, (size_t)160 * 1024}) {
-        for (int npw : {2, 1}) {
-            if (T::NCLS > 1 && npw > 1) continue;
-            const int mb = 1;
-            for (int ch : {32, 16, 8}) {
-                FastPlan p{};
-                p.CH = ch;
-                p.NPW = npw;
-                p.MB = mb;
-                const int target = FAST_NW * npw * 32;
-                if (GA * GB <= target) {
-                    p.TR = GA;
-                    p.IMGS = std::max(1, target / (GA * GB));
-                } else {
-                    p.TR = std::max(1, std::min(GA, target / GB));
-                    p.IMGS = 1;
-                }
-                for (;;) {
-                    FastPlan q = p;
-                    if (plan_ok<K, S, P, DX>(q, CS, GA, GB, a) && q.lds <= budget) {
-                        best = q;
-                        return true;
-                    }
-                    if (p.IMGS > 1)
-                        p.IMGS /= 2;
-                    else if (p.TR > 1)
-                        p.TR = (p.TR + 1) / 2;
-                    else
-                        break;
-                }
-            }
+    const int ch = T::KK == 1 ? 32 : std::max(8, std::min(32, (CS / 4 + 7) & ~7));
+    FastPlan r{};
+    r.CH = ch;
+    r.NPW = 1;
+    r.MB = 1;
+    int npos = 128;
+    if (T::KK == 9 && T::NCLS == 1 && T::IS == 1) {
+        if (GA * GB >= 256) {
+            r.NPW = 2;
+            npos = 256;
         }
+    } else if (T::KK == 9 && T::IS == 2) {
+        npos = 64;
+        if (CD > 32) r.MB = 2;
+    } else if (T::NCLS > 1) {
+        npos = GA * GB >= 128 ? 128 : 64;
+    } else if (T::KK == 1) {
+        npos = DX ? 64 : 128;
     }
-    (void)CD;
-    return false;
+    if (GA * GB <= npos) {
+        r.TR = GA;
+        r.IMGS = std::max(1, npos / (GA * GB));
+    } else {
+        r.TR = std::max(1, npos / GB);
+        r.IMGS = 1;
+    }
+    for (;;) {
+        FastPlan q = r;
+        if (plan_ok<K, S, P, DX>(q, CS, GA, GB, a)) {
+            best = q;
+            return true;
+        }
+        if (r.IMGS > 1)
+            r.IMGS /= 2;
+        else if (r.TR > 1)
+            r.TR = (r.TR + 1) / 2;
+        else if (r.CH > 8)
+            r.CH /= 2;
+        else if (r.MB > 1)
+            r.MB = 1;
+        else
+            return false;
+    }
 }
 
 template <int K, int S, int P, bool DX, int NPW, int MB>
