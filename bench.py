@@ -40,6 +40,15 @@ SWEEP = [  # name, cin, cout, k, stride, pad, h  (BASELINE config 1)
     ("1x1s2_64to128_16", 64, 128, 1, 2, 0, 16),
 ]
 PASSES = ("fwd", "dx", "dw")
+PEAK_HBM_GBS = 8000.0
+GEMMBENCH = [  # bench.rs:17-24 (--gemmbench): m, n, k, at, bt
+    (16384, 768, 256, False, True, "S3 qkv fwd"),
+    (16384, 704, 256, False, True, "S3 swiglu wg"),
+    (16384, 256, 768, False, False, "S3 qkv dX"),
+    (768, 256, 16384, True, False, "S3 qkv dW"),
+    (16384, 256, 352, False, True, "S3 swiglu wd fwd"),
+    (4096, 384, 1024, False, True, "merge fwd"),
+]
 
 
 def pass_flops(cin, cout, k, s, p, h, n=N):
@@ -47,25 +56,22 @@ def pass_flops(cin, cout, k, s, p, h, n=N):
     return 2.0 * cout * cin * k * k * oh * oh * n
 
 
-def traffic_from_profiles(kernel_tag):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary
-    (profiles/<tag>_pmc.txt), or None when it has not been measured."""
-    path = os.path.join(ROOT, "profiles", f"{kernel_tag}_pmc.txt")
+def traffic_from_profiles(op):
+    """HBM bytes per launch of `op` (e.g. "3x3s1_32to32_32:dw") from the committed
+    rocprofv3 --pmc summary profiles/conv_sweep_hbm_traffic.md: FETCH_SIZE +
+    WRITE_SIZE summed over the op's kernels, scaled by the copy-kernel factor
+    recorded there.  None when the op has not been measured."""
+    path = os.path.join(ROOT, "profiles", "conv_sweep_hbm_traffic.md")
     if not os.path.exists(path):
         return None
-    vals = {}
     for ln in open(path):
-        if ":" in ln and not ln.lstrip().startswith("#"):
-            k, v = ln.split(":", 1)
+        cells = [c.strip().strip("`") for c in ln.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == op:
             try:
-                vals[k.strip()] = float(v.split()[0])
-            except (ValueError, IndexError):
-                pass
-    try:
-        return (vals["FETCH_SIZE_KiB_per_dispatch"] + vals["WRITE_SIZE_KiB_per_dispatch"]) * 1024 * \
-            vals.get("copy_kernel_scale", 1.0)
-    except KeyError:
-        return None
+                return float(cells[4]) * 1024
+            except ValueError:
+                return None
+    return None
 
 
 def cpu_baseline(budget_s=12.0):
@@ -109,6 +115,77 @@ def cpu_baseline(budget_s=12.0):
                       f"{reps} reps in {el:.1f}s; oracle/ AVX2 restatement, OpenMP {threads} threads"}
 
 
+def time_gpu(fn, reps):
+    """Average ms of `fn` over `reps` back-to-back calls (HIP events on the
+    current stream, which is the library's stream)."""
+    import torch
+    fn()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def bench_attention(R, ctx, reps):
+    """128 images x 4 heads, T=64 (8x8), dh=32, SelfAttn
+    buffer [128, 64, 384] (q/k/v at 0/128/256), tau=1, rel=0, no mask; Q, K, V
+    ~N(0,1)/sqrt(32), dO ~N(0,1).  HBM-bound: algorithmic bytes (each tensor
+    once) fwd Q,K,V,O + P, bwd Q,K,V,dO,P in + dQ,dK,dV out."""
+    import torch
+    n, h, dh, t = 128, 4, 32, 64
+    c = h * dh
+    g = torch.Generator(device="cuda").manual_seed(7)
+    qkv = torch.randn(n * t * 3 * c, device="cuda", generator=g) / dh ** 0.5
+    dout = torch.randn(n * t * c, device="cuda", generator=g)
+    relidx, nrel = R.rel_index(8, 8, 8, 8)
+    tau = torch.ones(h, device="cuda")
+    rel = torch.zeros(h * nrel, device="cuda")
+    core = R.Core(h, dh, t, t, relidx, nrel, False, ctx=ctx)
+    p = torch.empty(n * h * t * t, device="cuda")
+    o = torch.empty(n * t * c, device="cuda")
+    dqkv = torch.zeros_like(qkv)
+    dtau = torch.zeros(h, device="cuda")
+    drel = torch.zeros(h * nrel, device="cuda")
+    fwd = lambda: core.forward(n, qkv, 3 * c, 0, qkv, 3 * c, c, 2 * c, tau, rel, p, o)
+    bwd = lambda: core.backward(n, qkv, 3 * c, 0, qkv, 3 * c, c, 2 * c, tau, p, dout, dqkv, dqkv,
+                                dtau, drel)
+    fwd()
+    tf, tb = time_gpu(fwd, reps), time_gpu(bwd, reps)
+    mb = n * h * t * dh * 4  # one [n, h, t, dh] tensor, bytes
+    pb = n * h * t * t * 4
+    fwd_bytes, bwd_bytes = 4 * mb + pb, 7 * mb + pb
+    fwd_flop = 2 * 2.0 * n * h * t * t * dh
+    bwd_flop = 4 * 2.0 * n * h * t * t * dh
+    res = {}
+    for name, ms, by, fl in (("fwd", tf, fwd_bytes, fwd_flop), ("bwd", tb, bwd_bytes, bwd_flop)):
+        gbs = by / (ms * 1e-3) / 1e9
+        res[name] = {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
+                     "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+                     "TFLOP_s": round(fl / (ms * 1e-3) / 1e12, 3)}
+    res["workload"] = "config2: 512 (image, head) problems, T=64, dh=32, fwd + bwd"
+    return res
+
+
+def bench_gemm(R, ctx, reps):
+    """The reference's --gemmbench shapes (bench.rs:17-24) through rnn_matmul."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(7)
+    out = []
+    for m, n, k, at, bt, tag in GEMMBENCH:
+        a = torch.randn(m * k, device="cuda", generator=g)
+        b = torch.randn(k * n, device="cuda", generator=g)
+        cc = torch.empty(m * n, device="cuda")
+        ms = time_gpu(lambda: R.matmul(m, n, k, a, at, b, bt, cc, False, ctx=ctx), reps)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        out.append({"shape": f"{m}x{n}x{k}", "at": at, "bt": bt, "tag": tag,
+                    "us": round(ms * 1e3, 2), "TFLOP_s": round(tf, 2),
+                    "frac": round(tf / PEAK_FP32_MFMA_TFLOPS, 4)})
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -117,6 +194,9 @@ def main():
     ap.add_argument("--op-reps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--ops-only", type=int, default=0, metavar="REPS",
+                    help="no timing: run a 256 MiB copy, then each sweep op REPS times in sweep "
+                         "order (the workload of the rocprofv3 --pmc passes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -154,6 +234,20 @@ def main():
             for ps in PASSES:
                 run_op(L, ps)
 
+    if args.ops_only:
+        # calibration copy of known size first, then the ops in sweep order
+        src = torch.empty(64 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        for L in layers:
+            for ps in PASSES:
+                for _ in range(args.ops_only):
+                    run_op(L, ps)
+        torch.cuda.synchronize()
+        print(json.dumps({"ops_only": [f"{L['name']}:{ps}" for L in layers for ps in PASSES],
+                          "reps": args.ops_only, "copy_bytes": 2 * src.numel() * 4}))
+        return
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -189,10 +283,12 @@ def main():
     dom = max(per_op, key=lambda r: r["ms"])
     dom_layer = next(L for L in layers if dom["op"].startswith(L["name"] + ":"))
     achieved = dom_layer["flops"] / (dom["ms"] * 1e-3) / 1e12
-    tag = dom["op"].replace(":", "_")
     roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-            "traffic": traffic_from_profiles(tag), "kernel": dom["op"]}
+            "traffic": traffic_from_profiles(dom["op"]), "kernel": dom["op"]}
+
+    attention = bench_attention(R, ctx, args.op_reps)
+    gemms = bench_gemm(R, ctx, args.op_reps)
 
     cpu = None
     if not args.no_cpu:
@@ -209,6 +305,7 @@ def main():
                    "conv_sweep_frac_of_fp32_mfma_peak": round(value / PEAK_FP32_MFMA_TFLOPS, 4),
                    "wall_s_timed": round(wall, 3)},
         "roofline": roof, "cpu_baseline": cpu, "per_op": per_op,
+        "config2_attention": attention, "gemmbench": gemms,
     }
     print(json.dumps(out))
 
