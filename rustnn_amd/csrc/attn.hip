@@ -291,20 +291,48 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs g) {
 }
 
 // dtau[h] += sum_img part[img][h]; drel[h*nrel + r] += sum_img part[img][h][r]
-// (image order, attn.rs:333-342).
-__global__ void attn_reduce_kernel(const float *dtau_part, const float *drel_part, int n, int h,
-                                   int nrel, float *dtau, float *drel) {
-    int e = blockIdx.x * blockDim.x + threadIdx.x;
-    int per = h * nrel;
-    if (e < per) {
-        float s = drel_part[e];
-        for (int i = 1; i < n; i++) s += drel_part[(long long)i * per + e];
-        drel[e] += s;
-    } else if (e < per + h) {
-        int hh = e - per;
-        float s = dtau_part[hh];
-        for (int i = 1; i < n; i++) s += dtau_part[(long long)i * h + hh];
-        dtau[hh] += s;
+// (image order, attn.rs:333-342).  A block takes 32 elements; thread (j, e)
+// sums images [j*G, j*G + G) of element e with the loads issued ahead of the
+// in-order adds, then the 8 partials are added in j order (fixed order:
+// bit-reproducible).
+constexpr int ATTN_RED_PARTS = 8;
+__global__ __launch_bounds__(256) void attn_reduce_kernel(const float *dtau_part,
+                                                          const float *drel_part, int n, int h,
+                                                          int nrel, float *dtau, float *drel) {
+    __shared__ float part[ATTN_RED_PARTS][32];
+    const int el = threadIdx.x & 31, j = threadIdx.x >> 5;
+    const int e = blockIdx.x * 32 + el;
+    const int per = h * nrel;
+    const bool is_rel = e < per, live = e < per + h;
+    const float *src = is_rel ? drel_part + e : dtau_part + (e - per);
+    const long long stride = is_rel ? per : h;
+    const int G = (n + ATTN_RED_PARTS - 1) / ATTN_RED_PARTS;
+    const int i0 = j * G, i1 = min(n, i0 + G);
+    float s = 0.f;
+    if (live) {
+        for (int b = i0; b < i1; b += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = b + u < i1 ? src[(long long)(b + u) * stride] : 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (b + u < i1) s = (b + u == i0) ? v[u] : s + v[u];
+        }
+    }
+    part[j][el] = s;
+    __syncthreads();
+    if (j == 0 && live) {
+        float t = 0.f;
+        bool first = true;
+        for (int q = 0; q < ATTN_RED_PARTS; q++) {
+            if (q * G >= n) break;
+            t = first ? part[q][el] : t + part[q][el];
+            first = false;
+        }
+        if (is_rel)
+            drel[e] += t;
+        else
+            dtau[e - per] += t;
     }
 }
 
@@ -482,7 +510,7 @@ int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const floa
     hipLaunchKernelGGL(attn_bwd_kernel, dim3((unsigned)(n * d->h)), dim3(256), lds, ctx->stream, g);
     RNN_LAUNCHED(ctx);
     int tot = (int)(d->h * d->nrel + d->h);
-    hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rnn_div_up(tot, 256)), dim3(256), 0,
+    hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rnn_div_up(tot, 32)), dim3(256), 0,
                        ctx->stream, (const float *)g.dtau_part, (const float *)g.drel_part, (int)n,
                        (int)d->h, (int)d->nrel, dtau, drel);
     RNN_LAUNCHED(ctx);

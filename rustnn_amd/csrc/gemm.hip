@@ -173,13 +173,21 @@ __global__ void fill_kernel(float *p, long long n, float v) {
     for (; i < n; i += st) p[i] = v;
 }
 
-// out[e] (+)= sum_z part[z*len + e], z in order (deterministic split-K reduce).
+// out[e] (+)= sum_z part[z*len + e], z in order (deterministic split-K
+// reduce).  Loads go out 8 at a time ahead of the in-order adds.
 __global__ void splitk_reduce_kernel(const float *part, int nz, long long len, float *out,
                                      int accumulate) {
     long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= len) return;
-    float s = part[e];
-    for (int zz = 1; zz < nz; zz++) s += part[(long long)zz * len + e];
+    float s = 0.f;
+    for (int z0 = 0; z0 < nz; z0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = z0 + i < nz ? part[(long long)(z0 + i) * len + e] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (z0 + i < nz) s = (z0 + i == 0) ? v[i] : s + v[i];
+    }
     out[e] = accumulate ? out[e] + s : s;
 }
 
@@ -323,6 +331,32 @@ int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, fl
     return RNN_OK;
 }
 
+// C = op(A) op(B) (+ C) with K split into nz chunks (multiples of 16) when
+// the C tiles alone cannot fill the chip; the chunk partials are added into C
+// in chunk order (deterministic).  Returns -1 when splitting does not pay.
+static int gemm_splitk(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, int at,
+                       const float *b, int bt, float *c, int acc) {
+    const size_t tiles = rnn_div_up(m, 64) * rnn_div_up(n, 64);
+    if (tiles >= (size_t)ctx->num_cus || k < 1024) return -1;
+    size_t nz = std::min(rnn_div_up(2 * (size_t)ctx->num_cus, tiles), k / 256);
+    nz = std::min<size_t>(nz, 64);
+    if (nz <= 1) return -1;
+    const size_t kchunk = rnn_round_up(rnn_div_up(k, nz), 16);
+    nz = rnn_div_up(k, kchunk);
+    float *part = (float *)rnn_workspace(ctx, nz * m * n * sizeof(float));
+    if (!part) return RNN_E_NOMEM;
+    // chunk z of A: rows z*kchunk of [k x m] (at) or columns z*kchunk of [m x k]
+    const size_t sa = at ? kchunk * m : kchunk, sb = bt ? kchunk : kchunk * n;
+    const int lda = at ? (int)m : (int)k, ldb = bt ? (int)k : (int)n;
+    int rc = gemm_enqueue(ctx, nz, m, n, kchunk, k, a, sa, lda, at, b, sb, ldb, bt, part, m * n,
+                          (int)n, 0, nullptr);
+    if (rc) return rc;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rnn_div_up(m * n, 256)), dim3(256), 0,
+                       ctx->stream, part, (int)nz, (long long)(m * n), c, acc);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
 extern "C" {
 
 int rnn_matmul(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, int at, const float *b,
@@ -333,6 +367,8 @@ int rnn_matmul(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, int a
     if (!c) return rnn_fail(ctx, RNN_E_NULL, "matmul: c is null");
     if (k == 0) return acc ? RNN_OK : fill(ctx, c, m * n, 0.f);  // gemm.rs:449-454
     if (!a || !b) return rnn_fail(ctx, RNN_E_NULL, "matmul: a or b is null");
+    const int rc = gemm_splitk(ctx, m, n, k, a, at, b, bt, c, acc);
+    if (rc != -1) return rc;
     return rnn_gemm_launch(ctx, 1, m, n, k, a, 0, at, b, 0, bt, c, 0, acc, nullptr);
 }
 
@@ -359,28 +395,12 @@ int rnn_matmul_dw(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, co
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     if (m == 0 || n == 0 || k == 0) return RNN_OK;  // gemm.rs:556-558
     if (!a || !b || !c) return rnn_fail(ctx, RNN_E_NULL, "matmul_dw: null operand");
-    // Split K into z chunks (multiples of 16) so that tiles x chunks fills
-    // the chip, then add the chunk partials into C in a fixed order.
-    size_t tiles = rnn_div_up(m, 64) * rnn_div_up(n, 64);
-    size_t want = rnn_div_up(2 * (size_t)ctx->num_cus, tiles);
-    size_t maxz = std::max<size_t>(1, k / 256);
-    size_t nz = std::min(want, maxz);
-    nz = std::min<size_t>(nz, 64);
-    if (nz <= 1) {
-        int lda = (int)m, ldb = (int)n;
-        return gemm_enqueue(ctx, 1, m, n, k, k, a, 0, lda, 1, b, 0, ldb, 0, c, 0, (int)n, 1, nullptr);
-    }
-    size_t kchunk = rnn_round_up(rnn_div_up(k, nz), 16);
-    nz = rnn_div_up(k, kchunk);
-    float *part = (float *)rnn_workspace(ctx, nz * m * n * sizeof(float));
-    if (!part) return RNN_E_NOMEM;
-    int rc = gemm_enqueue(ctx, nz, m, n, kchunk, k, a, kchunk * m, (int)m, 1, b, kchunk * n, (int)n,
-                          0, part, m * n, (int)n, 0, nullptr);
-    if (rc) return rc;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rnn_div_up(m * n, 256)), dim3(256), 0,
-                       ctx->stream, part, (int)nz, (long long)(m * n), c, 1);
-    RNN_LAUNCHED(ctx);
-    return RNN_OK;
+    // C += A^T B: split K when the C tiles cannot fill the chip (chunk
+    // partials added into C in chunk order), else one accumulating GEMM.
+    const int rc = gemm_splitk(ctx, m, n, k, a, 1, b, 0, c, 1);
+    if (rc != -1) return rc;
+    return gemm_enqueue(ctx, 1, m, n, k, k, a, 0, (int)m, 1, b, 0, (int)n, 0, c, 0, (int)n, 1,
+                        nullptr);
 }
 
 int rnn_linear_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
