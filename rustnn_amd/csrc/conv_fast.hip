@@ -61,6 +61,7 @@ struct FastArgs {
     int stage;         // LDS words of one stage: window, weight slabs, 64-word sink
     TileGeo geo;       // window geometry in positions (chs unused)
     int tapoff[9];     // window-position offset of each tap
+    uint32_t m_imgs, m_tiwp;  // FastDiv multipliers of geo.imgs and geo.TIWP
 };
 
 // Wave-uniform description of the stage being staged by DMA.
@@ -122,8 +123,11 @@ __device__ __forceinline__ void lane_dma_init(const FastArgs &g, LaneDMA<KK> &L,
 #pragma unroll
     for (int u = 0; u < WinRows<KK>::MAX; u++) {
         const int pos = (wave + FAST_NW * u) * 16 + (lane >> 2);
-        const int img = pos / t.imgs, rem = pos - img * t.imgs;
-        const int ty = rem / t.TIWP, col = rem - ty * t.TIWP;
+        const uint32_t mi = g.m_imgs, mt = g.m_tiwp;  // FastDiv magic multipliers
+        const int img = (int)(mi ? __umulhi((uint32_t)pos, mi) : (uint32_t)pos);
+        const int rem = pos - img * t.imgs;
+        const int ty = (int)(mt ? __umulhi((uint32_t)rem, mt) : (uint32_t)rem);
+        const int col = rem - ty * t.TIWP;
         const int tx = t.deint ? (col < t.HALF ? 2 * col : 2 * (col - t.HALF) + 1) : col;
         const int x = g.dxmin + tx * t.colstep;
         const bool ok = u < g.ppw && img < t.IMGS && ty < t.TIH && tx < t.TIW && x >= 0 &&
@@ -311,20 +315,51 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
             const int img = p / tpix, rem = p - img * tpix, r = rem / g.GB, cb = rem - r * g.GB;
             const int n = n0 + img, a = a0 + r;
             if (n >= g.N || a >= g.GA) continue;
+            const long long cst = (long long)g.HD * g.WD;
+            if constexpr (NCLS == 4) {
+                // stride-2 dX: the two column classes of a row are adjacent in
+                // dX, so one 8-byte store writes both (each line written once)
 #pragma unroll
-            for (int c = 0; c < NCLS; c++) {
-                const int y = a * T::OS + (DX ? c / S : 0), x = cb * T::OS + (DX ? c % S : 0);
-                if (y >= g.HD || x >= g.WD) continue;
-                float *dp = g.dst + ((long long)n * g.CD * g.HD + y) * g.WD + x;
-                const long long cst = (long long)g.HD * g.WD;
+                for (int py = 0; py < 2; py++) {
+                    const int y = 2 * a + py, x = 2 * cb;
+                    if (y >= g.HD || x >= g.WD) continue;
+                    float *dp = g.dst + ((long long)n * g.CD * g.HD + y) * g.WD + x;
+                    const bool pair = (g.WD & 1) == 0;  // x + 1 < WD and 8-byte aligned
 #pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-                    f32x16 v16 = acc[c][mb][j][0];
-                    if constexpr (NACC == 2) v16 += acc[c][mb][j][1];
+                    for (int mb = 0; mb < MB; mb++) {
+                        f32x16 v0 = acc[2 * py][mb][j][0], v1 = acc[2 * py + 1][mb][j][0];
+                        if constexpr (NACC == 2) {
+                            v0 += acc[2 * py][mb][j][1];
+                            v1 += acc[2 * py + 1][mb][j][1];
+                        }
 #pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const int m = (grp * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                        if (m < g.CD) dp[m * cst] = v16[v];
+                        for (int v = 0; v < 16; v++) {
+                            const int m = (grp * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                            if (m >= g.CD) continue;
+                            if (pair) {
+                                *reinterpret_cast<float2 *>(dp + m * cst) = float2{v0[v], v1[v]};
+                            } else {
+                                dp[m * cst] = v0[v];
+                                if (x + 1 < g.WD) dp[m * cst + 1] = v1[v];
+                            }
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int c = 0; c < NCLS; c++) {
+                    const int y = a * T::OS + (DX ? c / S : 0), x = cb * T::OS + (DX ? c % S : 0);
+                    if (y >= g.HD || x >= g.WD) continue;
+                    float *dp = g.dst + ((long long)n * g.CD * g.HD + y) * g.WD + x;
+#pragma unroll
+                    for (int mb = 0; mb < MB; mb++) {
+                        f32x16 v16 = acc[c][mb][j][0];
+                        if constexpr (NACC == 2) v16 += acc[c][mb][j][1];
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const int m = (grp * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                            if (m < g.CD) dp[m * cst] = v16[v];
+                        }
                     }
                 }
             }
@@ -381,6 +416,8 @@ static size_t plan_geometry(const FastPlan &p, int GB, FastArgs &a) {
             a.tapoff[i] = dyp * t.TIWP + (t.deint ? (dxp & 1) * t.HALF + (dxp >> 1) : dxp);
         }
     }
+    a.m_imgs = t.fd_imgstr.m;
+    a.m_tiwp = t.fd_tiwp.m;
     a.xwords = p.CH * a.plane;
     a.stage = a.xwords + p.MB * p.CH * T::KK * 32 + 64;
     return (size_t)2 * a.stage * 4;
