@@ -77,7 +77,7 @@ struct StageDMA {
     int mlim;                   // output rows of the group inside [0, CD)
 };
 
-template <int K, int S, int P, bool DX, int MB>
+template <int K, int S, int P, bool DX, int SL>
 __device__ __forceinline__ StageDMA stage_dma(const FastArgs &g, int item, int chunk,
                                               float *buf) {
     using T = ConvTaps<K, S, P, DX>;
@@ -103,7 +103,7 @@ __device__ __forceinline__ StageDMA stage_dma(const FastArgs &g, int item, int c
     d.yhi = min(g.geo.TIH, (g.HS - y0 + rowstep - 1) / rowstep);
     if (d.yhi < d.ylo) d.yhi = d.ylo;
     d.nimg = d.valid ? min(g.N - n0, g.geo.IMGS) : 0;
-    d.mlim = d.valid ? g.CD - d.grp * MB * 32 : 0;
+    d.mlim = d.valid ? g.CD - d.grp * SL * 32 : 0;
     return d;
 }
 
@@ -142,18 +142,18 @@ __device__ __forceinline__ void lane_dma_init(const FastArgs &g, LaneDMA<KK> &L,
 // (mb, q, t) of this wave and the window rows u = t, t + KK, ... of quads q
 // and CQ + q.  Rows beyond the stage go to the sink with every lane out of
 // range (no memory traffic), which keeps the step free of branches.
-template <int KK, int MB, int TT>
+template <int KK, int SL, int TT>
 __device__ __forceinline__ void issue_step(const FastArgs &g, const StageDMA &d,
                                            const LaneDMA<KK> &L, __amdgpu_buffer_rsrc_t rs_w,
                                            int q, int wave, int lane) {
     const int CP = g.CH >> 1, cq = g.CH >> 3;
     // weights: slab (mb, q, TT), 64-word row `wave`: lane l = wave*16 + lane/4
 #pragma unroll
-    for (int mb = 0; mb < MB; mb++) {
+    for (int mb = 0; mb < SL; mb++) {
         const int mrel = mb * 32 + (wave & 1) * 16;
         const int cbase = d.c0 + (wave >> 1) * CP + 4 * q;
         const bool ok = (lane >> 2) < d.mlim - mrel && (lane & 3) < g.CS - cbase;
-        const int e = L.wl + (d.grp * MB * 32 + mrel) * g.sm + cbase * g.sc + TT;
+        const int e = L.wl + (d.grp * SL * 32 + mrel) * g.sm + cbase * g.sc + TT;
         const uint32_t off = ok ? (uint32_t)e * 4u : DMA_OOB;
         float *dst = d.valid ? d.buf + g.xwords + ((mb * cq + q) * KK + TT) * 256 + wave * 64
                              : d.sink;
@@ -184,7 +184,7 @@ __device__ __forceinline__ void issue_step(const FastArgs &g, const StageDMA &d,
 // traffic run under the MFMAs.  `xs` and `nxt` are distinct buffers: the
 // __restrict__ qualifiers give the compiler the alias scopes it needs to not
 // wait for the DMA before the LDS reads.
-template <int K, int S, int P, bool DX, int NPW, int MB, int NACC>
+template <int K, int S, int P, bool DX, int NPW, int MB, int WM, int NACC>
 __device__ __forceinline__ void run_stage(
     const FastArgs &g, const float *__restrict__ xs, float *__restrict__ nxt, int nitem,
     int nchunk, const LaneDMA<ConvTaps<K, S, P, DX>::KK> &L, const int (&vb)[NPW],
@@ -195,12 +195,14 @@ __device__ __forceinline__ void run_stage(
     const int CQ = g.CH >> 3;
     const int wslab = CQ * KK * 256;
     const float *ws = xs + g.xwords + lane * 4;
-    const StageDMA d = stage_dma<K, S, P, DX, MB>(g, nitem, nchunk, nxt);
+    constexpr int WP = FAST_NW / WM;  // waves along positions
+    const float *wsw = ws + (wave / WP) * MB * wslab;  // this wave's m-blocks
+    const StageDMA d = stage_dma<K, S, P, DX, WM * MB>(g, nitem, nchunk, nxt);
 
     auto fetch = [&](int q, int t, float4 *fa, float4 *fb) {
 #pragma unroll
         for (int mb = 0; mb < MB; mb++)
-            fa[mb] = *reinterpret_cast<const float4 *>(ws + mb * wslab + (q * KK + t) * 256);
+            fa[mb] = *reinterpret_cast<const float4 *>(wsw + mb * wslab + (q * KK + t) * 256);
         const float *xq = xs + (q * g.plane + g.tapoff[t]) * 4;
 #pragma unroll
         for (int j = 0; j < NPW; j++) fb[j] = *reinterpret_cast<const float4 *>(xq + vb[j]);
@@ -216,7 +218,7 @@ __device__ __forceinline__ void run_stage(
                 fetch(q, t + 1 < KK ? t + 1 : 0, na, nb);
             else if (q + 1 < CQ)
                 fetch(q + 1, 0, na, nb);
-            issue_step<KK, MB, t>(g, d, L, rs_w, q, wave, lane);
+            issue_step<KK, WM * MB, t>(g, d, L, rs_w, q, wave, lane);
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -234,25 +236,28 @@ __device__ __forceinline__ void run_stage(
 }
 
 // Stage 0 of the first work item, issued in full before any compute.
-template <int K, int S, int P, bool DX, int MB>
+template <int K, int S, int P, bool DX, int SL>
 __device__ __forceinline__ void issue_prologue(const FastArgs &g, float *__restrict__ buf,
                                                int item, const LaneDMA<ConvTaps<K, S, P, DX>::KK> &L,
                                                __amdgpu_buffer_rsrc_t rs_w, int wave, int lane) {
     constexpr int KK = ConvTaps<K, S, P, DX>::KK;
-    const StageDMA d = stage_dma<K, S, P, DX, MB>(g, item, 0, buf);
+    const StageDMA d = stage_dma<K, S, P, DX, SL>(g, item, 0, buf);
     for (int q = 0; q < (g.CH >> 3); q++)
         static_for<0, KK>([&](auto tc) {
-            issue_step<KK, MB, decltype(tc)::value>(g, d, L, rs_w, q, wave, lane);
+            issue_step<KK, SL, decltype(tc)::value>(g, d, L, rs_w, q, wave, lane);
         });
 }
 
-template <int K, int S, int P, bool DX, int NPW, int MB>
+// Waves: WP = 4 / WM along positions (NPW groups of 32 each) times WM along
+// output channels (MB blocks of 32 each).
+template <int K, int S, int P, bool DX, int NPW, int MB, int WM>
 __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
     using T = ConvTaps<K, S, P, DX>;
     constexpr int NCLS = T::NCLS;
     // A wave with a single output block alternates two accumulators so that
     // consecutive MFMAs do not depend on each other.
     constexpr int NACC = NCLS * NPW * MB == 1 ? 2 : 1;
+    constexpr int WP = FAST_NW / WM, SL = WM * MB;
     extern __shared__ float smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int h = lane >> 5, l32 = lane & 31;
@@ -270,13 +275,13 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
     int vb[NPW];
 #pragma unroll
     for (int j = 0; j < NPW; j++) {
-        int p = (wave * NPW + j) * 32 + l32;
+        int p = ((wave % WP) * NPW + j) * 32 + l32;
         if (p >= npix) p = 0;
         const int img = p / tpix, rem = p - img * tpix, r = rem / g.GB, c = rem - r * g.GB;
         vb[j] = (h * CQ * g.plane + img * g.geo.imgs + r * g.lrow * g.geo.TIWP + c * g.lcol) * 4;
     }
 
-    issue_prologue<K, S, P, DX, MB>(g, smem, blockIdx.x, L, rs_w, wave, lane);
+    issue_prologue<K, S, P, DX, SL>(g, smem, blockIdx.x, L, rs_w, wave, lane);
     f32x16 acc[NCLS][MB][NPW][NACC];
     int s = 0;
     for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
             } else if (item + (int)gridDim.x < nitems) {
                 nitem = item + gridDim.x;
             }
-            run_stage<K, S, P, DX, NPW, MB, NACC>(g, smem + (s & 1) * g.stage,
+            run_stage<K, S, P, DX, NPW, MB, WM, NACC>(g, smem + (s & 1) * g.stage,
                                                   smem + ((s + 1) & 1) * g.stage, nitem, nchunk,
                                                   L, vb, acc, wave, lane, rs_w);
         }
@@ -310,7 +315,7 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
         const int a0 = (tile % g.tiles_a) * g.TR, n0 = (tile / g.tiles_a) * g.geo.IMGS;
 #pragma unroll
         for (int j = 0; j < NPW; j++) {
-            const int p = (wave * NPW + j) * 32 + l32;
+            const int p = ((wave % WP) * NPW + j) * 32 + l32;
             if (p >= npix) continue;
             const int img = p / tpix, rem = p - img * tpix, r = rem / g.GB, cb = rem - r * g.GB;
             const int n = n0 + img, a = a0 + r;
@@ -334,7 +339,7 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
                         }
 #pragma unroll
                         for (int v = 0; v < 16; v++) {
-                            const int m = (grp * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                            const int m = (grp * SL + (wave / WP) * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
                             if (m >= g.CD) continue;
                             if (pair) {
                                 *reinterpret_cast<float2 *>(dp + m * cst) = float2{v0[v], v1[v]};
@@ -357,7 +362,7 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
                         if constexpr (NACC == 2) v16 += acc[c][mb][j][1];
 #pragma unroll
                         for (int v = 0; v < 16; v++) {
-                            const int m = (grp * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                            const int m = (grp * SL + (wave / WP) * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
                             if (m < g.CD) dp[m * cst] = v16[v];
                         }
                     }
@@ -371,7 +376,7 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
 }
 
 struct FastPlan {
-    int TR, IMGS, CH, NPW, MB;
+    int TR, IMGS, CH, NPW, MB, WM;
     int wpc;  // cap on resident workgroups per CU (0 = occupancy limit)
     size_t lds;
 };
@@ -419,7 +424,7 @@ static size_t plan_geometry(const FastPlan &p, int GB, FastArgs &a) {
     a.m_imgs = t.fd_imgstr.m;
     a.m_tiwp = t.fd_tiwp.m;
     a.xwords = p.CH * a.plane;
-    a.stage = a.xwords + p.MB * p.CH * T::KK * 32 + 64;
+    a.stage = a.xwords + p.WM * p.MB * p.CH * T::KK * 32 + 64;
     return (size_t)2 * a.stage * 4;
 }
 
@@ -430,29 +435,31 @@ static bool plan_ok(FastPlan &p, int CS, int GA, int GB, FastArgs &a) {
     p.CH = std::min(p.CH, std::min(32, CSe));
     p.TR = std::min(p.TR, GA);
     if (p.TR <= 0 || p.IMGS <= 0 || p.CH < 8 || p.CH % 8) return false;
-    const bool shape_ok = T::NCLS == 1 ? ((p.NPW == 2 && p.MB == 1) || (p.NPW == 1 && p.MB == 1) ||
-                                          (p.NPW == 1 && p.MB == 2))
-                                       : (p.NPW == 1 && p.MB == 1);
-    if (!shape_ok || p.IMGS * p.TR * GB > FAST_NW * p.NPW * 32) return false;
+    if (p.WM <= 0) p.WM = 1;
+    const int nwm = p.NPW * 100 + p.MB * 10 + p.WM;
+    const bool shape_ok = T::NCLS == 1 ? (nwm == 211 || nwm == 111 || nwm == 121 || nwm == 112)
+                                       : (nwm == 111 || nwm == 112);
+    if (!shape_ok || p.IMGS * p.TR * GB > (FAST_NW / p.WM) * p.NPW * 32) return false;
     p.lds = plan_geometry<K, S, P, DX>(p, GB, a);
     return p.lds > 0 && p.lds <= 160 * 1024;
 }
 
-// Tile choice.  RNN_CONV_PLAN="TR,IMGS,CH,NPW,MB[,WPC]" overrides (tuning
-// sweeps).  Otherwise rules fitted to measured sweeps on MI355X: channel
-// chunks of a quarter of the source channels (8..32; 32 for 1x1); stride-1 3x3 takes 256
-// positions in two 32-position groups per wave when an image has 256 or more
-// positions, else 128 positions (whole images); strided forward takes 64
-// positions and two output-channel blocks; strided dX and 1x1 take 64 or 128
-// positions in one group per wave.  A plan that does not fit falls back to
-// shrinking the tile.
+// Tile choice.  RNN_CONV_PLAN="TR,IMGS,CH,NPW,MB[,WM[,WPC]]" overrides
+// (tuning sweeps).  Otherwise rules fitted to measured sweeps on MI355X:
+// channel chunks of a quarter of the source channels (8..32; 32 for 1x1);
+// stride-1 3x3 and 1x1 forward take 256 positions in two 32-position groups
+// per wave when an image has 256 or more positions, else 128 positions (whole
+// images); strided 3x3 forward takes 64 positions with the waves split two
+// ways along output channels, so every wave has a 32x32 block.  A plan that
+// does not fit falls back to shrinking the tile.
 template <int K, int S, int P, bool DX>
 static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs &a) {
     using T = ConvTaps<K, S, P, DX>;
     if (const char *env = getenv("RNN_CONV_PLAN")) {
         FastPlan p{};
-        if (sscanf(env, "%d,%d,%d,%d,%d,%d", &p.TR, &p.IMGS, &p.CH, &p.NPW, &p.MB, &p.wpc) >= 5 &&
-            plan_ok<K, S, P, DX>(p, CS, GA, GB, a)) {
+        const int got = sscanf(env, "%d,%d,%d,%d,%d,%d,%d", &p.TR, &p.IMGS, &p.CH, &p.NPW, &p.MB,
+                               &p.WM, &p.wpc);
+        if (got >= 5 && plan_ok<K, S, P, DX>(p, CS, GA, GB, a)) {
             best = p;
             return true;
         }
@@ -463,6 +470,7 @@ static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs
     r.CH = ch;
     r.NPW = 1;
     r.MB = 1;
+    r.WM = 1;
     int npos = 128;
     if (T::KK == 9 && T::NCLS == 1 && T::IS == 1) {
         if (GA * GB >= 256) {
@@ -471,11 +479,10 @@ static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs
         }
     } else if (T::KK == 9 && T::IS == 2) {
         npos = 64;
-        if (CD > 32) r.MB = 2;
-    } else if (T::NCLS > 1) {
-        npos = GA * GB >= 128 ? 128 : 64;
-    } else if (T::KK == 1) {
-        npos = DX ? 64 : 128;
+        if (CD > 32) r.WM = 2;
+    } else if (T::KK == 1 && T::NCLS == 1 && GA * GB >= 256) {
+        r.NPW = 2;
+        npos = 256;
     }
     if (GA * GB <= npos) {
         r.TR = GA;
@@ -496,16 +503,16 @@ static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs
             r.TR = (r.TR + 1) / 2;
         else if (r.CH > 8)
             r.CH /= 2;
-        else if (r.MB > 1)
-            r.MB = 1;
+        else if (r.WM > 1)
+            r.WM = 1;
         else
             return false;
     }
 }
 
-template <int K, int S, int P, bool DX, int NPW, int MB>
+template <int K, int S, int P, bool DX, int NPW, int MB, int WM>
 static void set_attr() {
-    (void)hipFuncSetAttribute((const void *)conv_fast_kernel<K, S, P, DX, NPW, MB>,
+    (void)hipFuncSetAttribute((const void *)conv_fast_kernel<K, S, P, DX, NPW, MB, WM>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
 }
 
@@ -516,10 +523,11 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
     static bool attr = false;
     if (!attr) {
         attr = true;
-        set_attr<K, S, P, DX, 1, 1>();
+        set_attr<K, S, P, DX, 1, 1, 1>();
+        set_attr<K, S, P, DX, 1, 1, 2>();
         if constexpr (T::NCLS == 1) {
-            set_attr<K, S, P, DX, 2, 1>();
-            set_attr<K, S, P, DX, 1, 2>();
+            set_attr<K, S, P, DX, 2, 1, 1>();
+            set_attr<K, S, P, DX, 1, 2, 1>();
         }
     }
     FastArgs a;
@@ -565,7 +573,7 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
     a.nchunks = (a.CS + p.CH - 1) / p.CH;
     const int nmblk = (a.CD + 31) / 32;
     a.ntiles = a.tiles_a * ((n + p.IMGS - 1) / p.IMGS);
-    a.ngroups = (nmblk + p.MB - 1) / p.MB;
+    a.ngroups = (nmblk + p.MB * p.WM - 1) / (p.MB * p.WM);
     const long long nitems = (long long)a.ntiles * a.ngroups;
     if (nitems > 0x7fffffffll) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: too many tiles");
     // Persistent grid: as many workgroups as fit on the chip at once.
@@ -582,10 +590,11 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
         return RNN_OK;
     };
     if constexpr (T::NCLS == 1) {
-        if (p.NPW == 2) return run(conv_fast_kernel<K, S, P, DX, 2, 1>);
-        if (p.MB == 2) return run(conv_fast_kernel<K, S, P, DX, 1, 2>);
+        if (p.NPW == 2) return run(conv_fast_kernel<K, S, P, DX, 2, 1, 1>);
+        if (p.MB == 2) return run(conv_fast_kernel<K, S, P, DX, 1, 2, 1>);
     }
-    return run(conv_fast_kernel<K, S, P, DX, 1, 1>);
+    if (p.WM == 2) return run(conv_fast_kernel<K, S, P, DX, 1, 1, 2>);
+    return run(conv_fast_kernel<K, S, P, DX, 1, 1, 1>);
 }
 
 }  // namespace
