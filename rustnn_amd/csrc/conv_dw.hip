@@ -394,36 +394,36 @@ __global__ __launch_bounds__(64 * DW_NW) void conv_dw_kernel(DwArgs g) {
     }
 }
 
-// tmp[gz][e] = sum of slabs [gz*G, min(nz, gz*G + G)) in slab order; all
-// loads of a thread are issued before the in-order sum (G <= DW_G).
-constexpr int DW_G = 16;
-__global__ void slab_sum_kernel(const float *part, int nz, int G, long long len, float *tmp) {
-    const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const int gz = blockIdx.y;
-    if (e >= len) return;
-    const int z0 = gz * G, n = min(nz, z0 + G) - z0;
-    float v[DW_G];
+// out[e] += sum over slabs z of part[z][e], in slab order, in one launch: a
+// block takes 32 elements; thread (j, e) sums slabs [j*G, j*G + G) with its
+// loads issued ahead of the in-order adds, then the 8 partials are added in
+// j order (a fixed order: bit-reproducible).
+constexpr int DW_RED_PARTS = 8;
+__global__ __launch_bounds__(256) void slab_reduce_kernel(const float *part, int nz, long long len,
+                                                          float *out) {
+    __shared__ float red[DW_RED_PARTS][32];
+    const int el = threadIdx.x & 31, j = threadIdx.x >> 5;
+    const long long e = (long long)blockIdx.x * 32 + el;
+    const int G = (nz + DW_RED_PARTS - 1) / DW_RED_PARTS;
+    const int z0 = j * G, z1 = min(nz, z0 + G);
+    float s = 0.f;
+    if (e < len) {
+        for (int b = z0; b < z1; b += 16) {
+            float v[16];
 #pragma unroll
-    for (int i = 0; i < DW_G; i++) v[i] = i < n ? part[(long long)(z0 + i) * len + e] : 0.f;
-    float s = v[0];
+            for (int u = 0; u < 16; u++) v[u] = b + u < z1 ? part[(long long)(b + u) * len + e] : 0.f;
 #pragma unroll
-    for (int i = 1; i < DW_G; i++)
-        if (i < n) s += v[i];
-    tmp[(long long)gz * len + e] = s;
-}
-
-// out[e] += sum_g tmp[g][e] in order (ng <= DW_G).
-__global__ void slab_final_kernel(const float *tmp, int ng, long long len, float *out) {
-    const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= len) return;
-    float v[DW_G];
-#pragma unroll
-    for (int i = 0; i < DW_G; i++) v[i] = i < ng ? tmp[(long long)i * len + e] : 0.f;
-    float s = v[0];
-#pragma unroll
-    for (int i = 1; i < DW_G; i++)
-        if (i < ng) s += v[i];
-    out[e] += s;
+            for (int u = 0; u < 16; u++)
+                if (b + u < z1) s = (b + u == z0) ? v[u] : s + v[u];
+        }
+    }
+    red[j][el] = s;
+    __syncthreads();
+    if (j == 0 && e < len) {
+        float t = red[0][el];
+        for (int q = 1; q < DW_RED_PARTS && q * G < nz; q++) t += red[q][el];
+        out[e] += t;
+    }
 }
 
 constexpr int DW_MT[3] = {2, 4, 8};
@@ -530,7 +530,9 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
     // Otherwise the tile (TR rows of IMGS images) with the most useful
     // 8-pixel groups -- groups times the fraction of tile rows inside the
     // image -- whose two stage buffers fit in LDS (one workgroup per CU, so
-    // staging must overlap compute); a single buffer only when two do not fit.
+    // staging must overlap compute) with at most 4 DMA rows per channel (the
+    // 8-row lane tables cost registers); larger tables, then a single buffer,
+    // only when nothing smaller fits.
     int TR = 0, IMGS = 0, NZ = 0, NB = 0;
     size_t lds = 0;
     if (const char *env = getenv("RNN_DW_PLAN")) {
@@ -544,12 +546,15 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
     }
     if (TR <= 0 || IMGS <= 0) {
         bool ok = false;
-        for (int nb : {2, 1}) {
+        for (int pass = 0; pass < 4 && !ok; pass++) {
+            // passes: two buffers with <= 4 DMA rows per channel (small lane
+            // tables, no register spills), two buffers, one buffer, one buffer
+            const int nb = pass < 2 ? 2 : 1, mtmax = (pass & 1) ? DW_MT[2] : DW_MT[1];
             double best = 0;
             for (int tr = 1; tr <= g.OH; tr++)
                 for (int im = 1; im <= (tr == g.OH ? 16 : 1); im *= 2) {
                     const size_t l = dw_geometry(g, K, tr, im, nb);
-                    if (l == 0 || l > 160 * 1024) continue;
+                    if (l == 0 || l > 160 * 1024 || std::max(g.mx, g.md) > mtmax) continue;
                     const int ta = (g.OH + tr - 1) / tr;
                     const double score = g.ngroups * (double)g.OH / (ta * tr);
                     if (score > best) {
@@ -587,28 +592,17 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
             occ = 1;
         NZ = std::max(1, occ * ctx->num_cus / (ncb * ncib));
     }
-    NZ = std::min(std::min(NZ, g.ntiles), DW_G * DW_G);  // two reduction levels of <= DW_G
+    NZ = std::min(NZ, g.ntiles);
     g.nz = NZ;
     const size_t ckk = (size_t)g.CI * K * K, len = (size_t)g.CO * ckk;
-    const int G = DW_G, ng = (NZ + G - 1) / G;
-    float *ws = (float *)rnn_workspace(ctx, ((size_t)NZ + (ng > 1 ? ng : 0)) * len * sizeof(float));
+    float *ws = (float *)rnn_workspace(ctx, (size_t)NZ * len * sizeof(float));
     if (!ws) return RNN_E_NOMEM;
     g.part = ws;
     dim3 grid(NZ, ncb, ncib), block(64 * DW_NW);
     void *args[] = {&g};
     RNN_HIP(ctx, hipLaunchKernel(kern, grid, block, args, lds, ctx->stream));
-    const unsigned eb = (unsigned)rnn_div_up(len, 256);
-    if (ng > 1) {
-        float *tmp = ws + (size_t)NZ * len;
-        hipLaunchKernelGGL(slab_sum_kernel, dim3(eb, ng), dim3(256), 0, ctx->stream, ws, NZ, G,
-                           (long long)len, tmp);
-        RNN_LAUNCHED(ctx);
-        hipLaunchKernelGGL(slab_final_kernel, dim3(eb), dim3(256), 0, ctx->stream, tmp, ng,
-                           (long long)len, dw);
-    } else {
-        hipLaunchKernelGGL(slab_final_kernel, dim3(eb), dim3(256), 0, ctx->stream, ws, NZ,
-                           (long long)len, dw);
-    }
+    hipLaunchKernelGGL(slab_reduce_kernel, dim3((unsigned)rnn_div_up(len, 32)), dim3(256), 0,
+                       ctx->stream, ws, NZ, (long long)len, dw);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
