@@ -21,9 +21,9 @@
 // pixels 4h..4h+3 of the group with one ds_read_b128 for dY and, per kernel
 // row kh, the 6 (or 5 + 4) X values those pixels touch, so the three kw taps
 // are register offsets into the same read.  MFMA k-step i takes pixels i and
-// 4 + i; the 9 tap accumulators are independent chains.  The waves' sums are
-// added through LDS in wave order and the workgroup writes one partial slab;
-// slabs are added in slab order by a two-level reduction (no atomics: the
+// 4 + i; the 9 tap accumulators are independent chains.  The 8 waves' sums are
+// added through LDS in a fixed pairwise order and the workgroup writes one partial slab;
+// slabs are added in slab order by one reduction launch (no atomics: the
 // result is bit-reproducible).
 #include "conv_common.h"
 
