@@ -150,6 +150,110 @@ int rnn_linear_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const
 int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
                         const float *x, const float *w, float *dw, float *db, float *dx);
 
+/* -------------------------------------------------------------- nn.rs */
+/* The ResNet layers around the convs.  Elementwise formulas round exactly as
+ * the reference's (no FMA contraction); per-channel sums are f64 in a fixed
+ * order.  x, y, dy, dx are NCHW [n][c][hw]; per-channel arrays hold c floats. */
+
+/* BatchNorm2d::forward / forward_relu in train mode (nn.rs:253-348): batch
+ * statistics (f64 sums), y = [relu](gamma*(x - mean)*invstd + beta), running
+ * mean / unbiased running variance updated with `momentum` (0.1 in rustnn).
+ * mean and invstd are written for rnn_bn_backward.  y may alias x; the
+ * reference keeps xhat for the backward, this API keeps x instead (a caller
+ * that normalises in place must keep a copy of x).  running_mean and
+ * running_var may both be NULL (statistics only, no running update). */
+int rnn_bn_forward_train(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, float *y,
+                         const float *gamma, const float *beta, float *running_mean,
+                         float *running_var, float *mean, float *invstd, float momentum, float eps,
+                         int relu);
+/* BatchNorm2d forward in eval mode (run_eval, nn.rs:350-365). */
+int rnn_bn_forward_eval(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, float *y,
+                        const float *gamma, const float *beta, const float *running_mean,
+                        const float *running_var, float eps, int relu);
+/* BatchNorm2d::backward (nn.rs:379-425): dx overwritten, dgamma / dbeta
+ * ACCUMULATE.  x, mean, invstd as passed to / written by the train forward.
+ * relu_out (may be NULL): apply relu_back_ (nn.rs:432-439) to dy first, i.e.
+ * use 0 where relu_out <= 0 (dy itself is not modified). */
+int rnn_bn_backward(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
+                    const float *relu_out, const float *x, const float *mean, const float *invstd,
+                    const float *gamma, float *dx, float *dgamma, float *dbeta);
+/* relu_back_ (nn.rs:432-439): d = 0 where y <= 0. */
+int rnn_relu_back(rnn_ctx *ctx, size_t len, float *d, const float *y);
+/* add_ (nn.rs:441-443): a += b. */
+int rnn_add(rnn_ctx *ctx, size_t len, float *a, const float *b);
+/* add_relu_ (nn.rs:446-450): a = max(a + b, 0). */
+int rnn_add_relu(rnn_ctx *ctx, size_t len, float *a, const float *b);
+/* gap_forward (nn.rs:455-463): y[n][c] = plane sum (pixel order) / hw. */
+int rnn_gap_forward(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, float *y);
+/* gap_backward (nn.rs:465-473): dx[n][c][p] = dy[n][c] / hw. */
+int rnn_gap_backward(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy, float *dx);
+/* nn.rs Linear (the ResNet classifier, nn.rs:475-564), bit-identical to the
+ * reference's scalar loops.  forward: y[i][o] = b[o] + sum_j w[o][j] x[i][j].
+ * backward: dw, db ACCUMULATE over rows in order; dx (may be NULL) is
+ * overwritten. */
+int rnn_fc_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
+                   const float *w, const float *b, float *y);
+int rnn_fc_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
+                    const float *x, const float *w, float *dw, float *db, float *dx);
+/* softmax_ce (nn.rs:566-637): dlogits = (softmax - smoothed target) / rows;
+ * *loss (device, may be NULL) = mean loss; *correct (device u32, may be NULL)
+ * = rows whose first maximal logit is the label.  labels: device u32[rows].
+ * rows <= 8192. */
+int rnn_softmax_ce(rnn_ctx *ctx, size_t rows, size_t nclass, const float *logits,
+                   const uint32_t *labels, float smooth, float *dlogits, float *loss,
+                   uint32_t *correct);
+/* Param::step (nn.rs:102-110): Nesterov SGD, g zeroed.  Pass wd = 0 for the
+ * parameters the reference does not decay (BN gamma / beta, biases). */
+int rnn_sgd_step(rnn_ctx *ctx, size_t len, float *v, float *g, float *m, float lr, float momentum,
+                 float wd);
+
+/* ----------------------------------------------------------- model.rs */
+/* Device-resident CIFAR ResNet (ResNet::new, model.rs:113-135): depth_n
+ * blocks per stage (6n+2 layers), widths width/2w/4w, nclass outputs, Kaiming
+ * initialisation from rng.rs seeded with `seed` (bit-identical to the
+ * reference's).  Parameters, gradients, momenta, running statistics and the
+ * activations of the last train forward live on the device. */
+typedef struct rnn_resnet rnn_resnet;
+int rnn_resnet_create(rnn_ctx *ctx, size_t depth_n, size_t width, size_t nclass, uint64_t seed,
+                      rnn_resnet **out);
+int rnn_resnet_destroy(rnn_resnet *net);
+/* Total floats of all parameters / BN running buffers; number of parameter
+ * tensors and the length (and weight-decay flag) of tensor i, in the
+ * reference's for_each_param order (model.rs:164-175). */
+size_t rnn_resnet_num_params(const rnn_resnet *net);
+size_t rnn_resnet_num_buffers(const rnn_resnet *net);
+size_t rnn_resnet_num_tensors(const rnn_resnet *net);
+int rnn_resnet_tensor_len(const rnn_resnet *net, size_t i, size_t *len, int *decay);
+/* Device copies of the state in for_each_param order (which 0 = values,
+ * 1 = gradients, 2 = momenta) or for_each_buffer order (which 3 = BN running
+ * mean / var): exactly one of dst (read out) and src (write in) is set. */
+int rnn_resnet_copy(rnn_resnet *net, int which, float *dst, const float *src);
+/* ResNet::forward (model.rs:138-150): x [n][3][h][w] -> logits [n][nclass].
+ * train = 1 uses batch statistics, updates the running ones and keeps the
+ * activations for rnn_resnet_backward. */
+int rnn_resnet_forward(rnn_resnet *net, size_t n, size_t h, size_t w, const float *x, int train,
+                       float *logits);
+/* ResNet::backward (model.rs:152-162): gradients ACCUMULATE into the
+ * parameters' g after the last train forward. */
+int rnn_resnet_backward(rnn_resnet *net, const float *dlogits);
+/* ResNet::step (model.rs:205-207): Param::step on every parameter. */
+int rnn_resnet_step(rnn_resnet *net, float lr, float momentum, float wd);
+/* One train step (train.rs:686-699): forward(train), softmax_ce with label
+ * smoothing, backward, step.  labels: device u32[n].  loss / correct (device,
+ * may be NULL) receive the mean loss and the hit count.  Replayed from a
+ * hipGraph from the second call on for a given (n, h, w). */
+int rnn_resnet_train_step(rnn_resnet *net, size_t n, size_t h, size_t w, const float *x,
+                          const uint32_t *labels, float smooth, float lr, float momentum, float wd,
+                          float *loss, uint32_t *correct);
+/* Logits of the last forward (device [n][nclass]). */
+int rnn_resnet_logits(rnn_resnet *net, float *logits);
+/* Train-step graph: enable / disable (drops a recorded graph); state 1 when a
+ * graph is recorded, 0 otherwise, with *why the reason recording failed. */
+int rnn_resnet_set_graph(rnn_resnet *net, int on);
+int rnn_resnet_graph_state(const rnn_resnet *net, const char **why);
+/* ResNet::flops (model.rs:179-198): forward FLOP per image at h x w. */
+uint64_t rnn_resnet_flops(const rnn_resnet *net, size_t h, size_t w);
+
 /* ------------------------------------------ debug exports (bit-exact tests) */
 /* im2col of ONE image through the same staging index math the conv kernels
  * use: col[cin*k*k][oh*ow] (gather_span, conv.rs:68-120). */

@@ -148,6 +148,37 @@ void orc_linear_forward(size_t rows, size_t fin, size_t fout, const float *x, co
 void orc_linear_backward(size_t rows, size_t fin, size_t fout, const float *dy, const float *x,
                          const float *w, float *dw, float *db, float *dx);
 
+/* ------------------------------------------------------------------- nn.rs */
+/* BatchNorm2d train forward (nn.rs:297-348), in place on y [n][c][hw]; writes
+ * xhat, mean_out (may be NULL) and invstd; updates rm / rv. */
+void orc_bn_train_forward(size_t n, size_t c, size_t hw, float *y, const float *gamma,
+                          const float *beta, float *rm, float *rv, float *xhat, float *mean_out,
+                          float *invstd, float mom, float eps, int relu);
+/* BatchNorm2d eval forward (nn.rs:350-365), in place. */
+void orc_bn_eval_forward(size_t n, size_t c, size_t hw, float *y, const float *gamma,
+                         const float *beta, const float *rm, const float *rv, float eps, int relu);
+/* BatchNorm2d::backward (nn.rs:379-425): dx overwritten; dgamma, dbeta +=. */
+void orc_bn_backward(size_t n, size_t c, size_t hw, const float *dy, const float *xhat,
+                     const float *gamma, const float *invstd, float *dx, float *dgamma,
+                     float *dbeta);
+/* relu_back_, add_, add_relu_ (nn.rs:430-450). */
+void orc_relu_back(size_t len, float *d, const float *y);
+void orc_add(size_t len, float *a, const float *b);
+void orc_add_relu(size_t len, float *a, const float *b);
+/* gap_forward / gap_backward (nn.rs:452-473); nc = n*c planes of hw. */
+void orc_gap_forward(size_t nc, size_t hw, const float *x, float *y);
+void orc_gap_backward(size_t nc, size_t hw, const float *dy, float *dx);
+/* nn.rs Linear (the ResNet classifier, nn.rs:475-564). */
+void orc_fc_forward(size_t rows, size_t fin, size_t fout, const float *x, const float *w,
+                    const float *b, float *y);
+void orc_fc_backward(size_t rows, size_t fin, size_t fout, const float *dy, const float *x,
+                     const float *w, float *dw, float *db, float *dx);
+/* softmax_ce (nn.rs:566-637): returns the mean loss. */
+float orc_softmax_ce(size_t rows, size_t nclass, const float *logits, const uint32_t *labels,
+                     float smooth, float *dlogits, size_t *correct);
+/* Param::step (nn.rs:102-110). */
+void orc_sgd_step(size_t len, float *v, float *g, float *m, float lr, float mom, float wd);
+
 #ifdef __cplusplus
 }
 #endif

@@ -121,6 +121,23 @@ def lib():
         L.orc_linear_forward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, C.c_void_p, _f32p]
         L.orc_linear_backward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p,
                                           C.c_void_p, _f32p]
+        L.orc_bn_train_forward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                           _f32p, C.c_void_p, _f32p, C.c_float, C.c_float,
+                                           C.c_int]
+        L.orc_bn_eval_forward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                          C.c_float, C.c_int]
+        L.orc_bn_backward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                      _f32p]
+        L.orc_relu_back.argtypes = [_sz, _f32p, _f32p]
+        L.orc_add.argtypes = [_sz, _f32p, _f32p]
+        L.orc_add_relu.argtypes = [_sz, _f32p, _f32p]
+        L.orc_gap_forward.argtypes = [_sz, _sz, _f32p, _f32p]
+        L.orc_gap_backward.argtypes = [_sz, _sz, _f32p, _f32p]
+        L.orc_fc_forward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p]
+        L.orc_fc_backward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]
+        L.orc_softmax_ce.argtypes = [_sz, _sz, _f32p, _u32p, C.c_float, _f32p, P(_sz)]
+        L.orc_softmax_ce.restype = C.c_float
+        L.orc_sgd_step.argtypes = [_sz, _f32p, _f32p, _f32p, C.c_float, C.c_float, C.c_float]
         _lib = L
     return _lib
 
@@ -324,3 +341,117 @@ def linear_backward(rows, fin, fout, dy, x, w, dw, db=None):
     lib().orc_linear_backward(rows, fin, fout, _f(dy).ravel(), _f(x).ravel(), _f(w).ravel(), dw,
                               db.ctypes.data if db is not None else None, dx)
     return dw, db, dx
+
+
+# ---------------------------------------------------------------- nn.rs
+# These wrappers work in place on C-contiguous float32 arrays, like the
+# reference's &mut Tensor functions.
+def _chk(*arrs):
+    for a in arrs:
+        assert a.dtype == np.float32 and a.flags.c_contiguous, "float32 C-contiguous array required"
+
+
+def bn_train_forward(y, gamma, beta, rm, rv, mom=0.1, eps=1e-5, relu=False):
+    """BatchNorm2d run_train (nn.rs:297-348) on y [n, c, h, w] in place.
+    Returns (xhat, mean, invstd); rm / rv are updated in place."""
+    _chk(y, gamma, beta, rm, rv)
+    n, c = y.shape[0], y.shape[1]
+    hw = y.size // max(n * c, 1)
+    xhat = np.empty_like(y)
+    mean = np.empty(c, np.float32)
+    invstd = np.empty(c, np.float32)
+    lib().orc_bn_train_forward(n, c, hw, y.reshape(-1), gamma, beta, rm, rv, xhat.reshape(-1),
+                               mean.ctypes.data, invstd, mom, eps, int(relu))
+    return xhat, mean, invstd
+
+
+def bn_eval_forward(y, gamma, beta, rm, rv, eps=1e-5, relu=False):
+    """BatchNorm2d run_eval (nn.rs:350-365) on y in place."""
+    _chk(y, gamma, beta, rm, rv)
+    n, c = y.shape[0], y.shape[1]
+    lib().orc_bn_eval_forward(n, c, y.size // max(n * c, 1), y.reshape(-1), gamma, beta, rm, rv,
+                              eps, int(relu))
+
+
+def bn_backward(dy, xhat, gamma, invstd, dgamma, dbeta):
+    """BatchNorm2d::backward (nn.rs:379-425): returns dx; dgamma / dbeta +=."""
+    _chk(dy, xhat, gamma, invstd, dgamma, dbeta)
+    n, c = dy.shape[0], dy.shape[1]
+    dx = np.empty_like(dy)
+    lib().orc_bn_backward(n, c, dy.size // max(n * c, 1), dy.reshape(-1), xhat.reshape(-1),
+                          gamma, invstd, dx.reshape(-1), dgamma, dbeta)
+    return dx
+
+
+def relu_back(d, y):
+    _chk(d, y)
+    lib().orc_relu_back(d.size, d.reshape(-1), y.reshape(-1))
+
+
+def add_(a, b):
+    _chk(a, b)
+    lib().orc_add(a.size, a.reshape(-1), b.reshape(-1))
+
+
+def add_relu(a, b):
+    _chk(a, b)
+    lib().orc_add_relu(a.size, a.reshape(-1), b.reshape(-1))
+
+
+def gap_forward(x):
+    """gap_forward (nn.rs:455-463): [n, c, h, w] -> [n, c]."""
+    _chk(x)
+    n, c = x.shape[0], x.shape[1]
+    y = np.empty((n, c), np.float32)
+    lib().orc_gap_forward(n * c, x.size // max(n * c, 1), x.reshape(-1), y.reshape(-1))
+    return y
+
+
+def gap_backward(dy, h, w):
+    _chk(dy)
+    n, c = dy.shape[0], dy.shape[1]
+    dx = np.empty((n, c, h, w), np.float32)
+    lib().orc_gap_backward(n * c, h * w, dy.reshape(-1), dx.reshape(-1))
+    return dx
+
+
+def fc_forward(x, w, b, fout):
+    """nn.rs Linear::forward (nn.rs:500-517): x [rows, fin] -> [rows, fout]."""
+    x = _f(x)
+    rows = x.shape[0]
+    fin = x.size // rows
+    y = np.empty((rows, fout), np.float32)
+    lib().orc_fc_forward(rows, fin, fout, x.reshape(-1), _f(w).ravel(), _f(b).ravel(),
+                         y.reshape(-1))
+    return y
+
+
+def fc_backward(dy, x, w, dw, db):
+    """nn.rs Linear::backward (nn.rs:519-564): dw / db += in place; returns dx."""
+    _chk(dw, db)
+    dy, x = _f(dy), _f(x)
+    rows, fout = dy.shape[0], dy.size // dy.shape[0]
+    fin = x.size // rows
+    dx = np.empty((rows, fin), np.float32)
+    lib().orc_fc_backward(rows, fin, fout, dy.reshape(-1), x.reshape(-1), _f(w).ravel(), dw, db,
+                          dx.reshape(-1))
+    return dx
+
+
+def softmax_ce(logits, labels, smooth):
+    """softmax_ce (nn.rs:620-637) -> (mean loss, correct, dlogits)."""
+    logits = _f(logits)
+    rows = logits.shape[0]
+    nclass = logits.size // rows
+    d = np.empty((rows, nclass), np.float32)
+    corr = _sz(0)
+    loss = lib().orc_softmax_ce(rows, nclass, logits.reshape(-1),
+                                np.ascontiguousarray(labels, np.uint32), smooth, d.reshape(-1),
+                                C.byref(corr))
+    return float(np.float32(loss)), int(corr.value), d
+
+
+def sgd_step(v, g, m, lr, mom, wd):
+    """Param::step (nn.rs:102-110) in place."""
+    _chk(v, g, m)
+    lib().orc_sgd_step(v.size, v, g, m, lr, mom, wd)

@@ -8,6 +8,9 @@ reference's host interface for the hot path:
 * ``Conv2d`` (forward / backward_w / backward)          -- nn.rs:115-250
 * ``Linear`` (forward / backward)                       -- linear.rs:14-104
 * ``Core`` (forward / backward), ``rel_index``          -- attn.rs:21-343
+* ``rustnn_amd.nn``: BatchNorm2d, the classifier Linear, gap, softmax_ce,
+  Param::step                                           -- nn.rs:37-637
+* ``rustnn_amd.model.ResNet``: the device-resident train step -- model.rs
 
 Device memory and streams come from PyTorch (plumbing only): every array
 argument is a float32 CUDA tensor, passed to the library as a raw device
@@ -117,6 +120,37 @@ def lib():
             "rnn_dbg_pack_a": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
             "rnn_dbg_pack_b": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
             "rnn_dbg_rel_index": (_i, [_vp, _u32, _u32, _u32, _u32, _vp]),
+            "rnn_bn_forward_train": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                          _vp, C.c_float, C.c_float, _i]),
+            "rnn_bn_forward_eval": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
+                                         C.c_float, _i]),
+            "rnn_bn_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                     _vp]),
+            "rnn_relu_back": (_i, [_vp, _sz, _vp, _vp]),
+            "rnn_add": (_i, [_vp, _sz, _vp, _vp]),
+            "rnn_add_relu": (_i, [_vp, _sz, _vp, _vp]),
+            "rnn_gap_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
+            "rnn_gap_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
+            "rnn_fc_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "rnn_fc_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_softmax_ce": (_i, [_vp, _sz, _sz, _vp, _vp, C.c_float, _vp, _vp, _vp]),
+            "rnn_sgd_step": (_i, [_vp, _sz, _vp, _vp, _vp, C.c_float, C.c_float, C.c_float]),
+            "rnn_resnet_create": (_i, [_vp, _sz, _sz, _sz, C.c_uint64, P(_vp)]),
+            "rnn_resnet_destroy": (_i, [_vp]),
+            "rnn_resnet_num_params": (_sz, [_vp]),
+            "rnn_resnet_num_buffers": (_sz, [_vp]),
+            "rnn_resnet_num_tensors": (_sz, [_vp]),
+            "rnn_resnet_tensor_len": (_i, [_vp, _sz, P(_sz), P(_i)]),
+            "rnn_resnet_copy": (_i, [_vp, _i, _vp, _vp]),
+            "rnn_resnet_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _i, _vp]),
+            "rnn_resnet_backward": (_i, [_vp, _vp]),
+            "rnn_resnet_step": (_i, [_vp, C.c_float, C.c_float, C.c_float]),
+            "rnn_resnet_train_step": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, C.c_float, C.c_float,
+                                           C.c_float, C.c_float, _vp, _vp]),
+            "rnn_resnet_logits": (_i, [_vp, _vp]),
+            "rnn_resnet_set_graph": (_i, [_vp, _i]),
+            "rnn_resnet_graph_state": (_i, [_vp, P(C.c_char_p)]),
+            "rnn_resnet_flops": (C.c_uint64, [_vp, _sz, _sz]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -130,7 +164,7 @@ def declared_symbols(header: str = HEADER):
     """Names of the functions include/rnn.h declares."""
     import re
     txt = open(header).read()
-    return sorted(set(re.findall(r"^\s*(?:int|void \*|const char \*|size_t)\s+(rnn_\w+)\s*\(",
+    return sorted(set(re.findall(r"^\s*(?:int|void \*|const char \*|size_t|uint64_t)\s+(rnn_\w+)\s*\(",
                                  txt, re.M)))
 
 

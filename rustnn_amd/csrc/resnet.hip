@@ -1,0 +1,727 @@
+// Device-resident CIFAR ResNet train step (model.rs, nn.rs) on one MI355X.
+//
+// Reference: ResNet / BasicBlock (model.rs:10-209) over Conv2d, BatchNorm2d,
+// gap, the classifier Linear, softmax_ce and Param::step (nn.rs), driven as in
+// train.rs:686-699 / bench.rs:128-140: forward, softmax-CE, backward, SGD.
+//
+// Everything stays in HBM for the whole step: parameters, gradients and
+// momenta in three flat arrays (weight-decayed parameters first, so the SGD
+// step is one launch), BN running statistics in one array, and every
+// activation the backward needs, planned once per input shape.  No tensor is
+// copied between layers: BN writes its output next to its input (the input is
+// kept so the backward recomputes xhat bit for bit instead of storing it), the
+// second BN of a block, the shortcut (identity or 1x1 conv + BN), the residual
+// add and the ReLU are one kernel, and each ReLU's backward is folded into the
+// BN backward / residual add that consume its gradient.
+//
+// rnn_resnet_train_step records the step into a hipGraph the second time it
+// is called for a shape and replays it from then on (RNN_GRAPH=0 disables
+// this).  Step scalars (lr, momentum, wd, label smoothing) live in device
+// memory written by a one-thread kernel before each replay; inputs are copied
+// into the network's own buffers, so the graph never sees caller pointers.
+#include "rnn_internal.h"
+
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+namespace {
+
+// rng.rs (Rng::new, next_u64, uniform, normal): splitmix64-seeded
+// xoshiro256++ and Box-Muller on 24-bit uniforms, used for the Kaiming
+// initialisation of ResNet::new.
+struct HostRng {
+    uint64_t s[4];
+    explicit HostRng(uint64_t seed) {
+        uint64_t z = seed + 0x9E3779B97F4A7C15ull;
+        for (auto &w : s) {
+            z += 0x9E3779B97F4A7C15ull;
+            uint64_t x = z;
+            x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+            x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+            w = x ^ (x >> 31);
+        }
+    }
+    static uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+    uint64_t next() {
+        const uint64_t r = rotl(s[0] + s[3], 23) + s[0];
+        const uint64_t t = s[1] << 17;
+        s[2] ^= s[0];
+        s[3] ^= s[1];
+        s[1] ^= s[2];
+        s[0] ^= s[3];
+        s[2] ^= t;
+        s[3] = rotl(s[3], 45);
+        return r;
+    }
+    float uniform() { return (float)(next() >> 40) * (1.0f / 16777216.0f); }
+    float normal() {
+        float u1 = uniform();
+        if (!(u1 > 1e-7f)) u1 = 1e-7f;
+        const float u2 = uniform();
+        return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
+    }
+};
+
+struct ParamSlot {
+    size_t off = 0, len = 0;
+    bool decay = false;
+};
+
+struct NetConv {
+    uint32_t cin = 0, cout = 0, k = 0, stride = 1, pad = 0;
+    int w = -1;  // parameter index
+    rnn_conv_spec spec(uint32_t h, uint32_t w_) const {
+        rnn_conv_spec sp;
+        rnn_conv_spec_init(&sp, cin, cout, k, stride, pad, h, w_);
+        return sp;
+    }
+};
+
+struct NetBn {
+    uint32_t c = 0;
+    int g = -1, b = -1;  // parameter indices
+    size_t buf = 0;      // rm at buf, rv at buf + c in the buffer array
+    float *coef = nullptr;  // device [4c]: mean, invstd (train) | sc, sh (eval)
+};
+
+struct NetBlock {
+    NetConv c1, c2, cd;
+    NetBn b1, b2, bd;
+    bool down = false;
+    uint32_t hin = 0, win = 0, hout = 0, wout = 0;
+    float *in = nullptr;  // block input (previous output), not owned
+    float *y1 = nullptr, *h = nullptr, *y2 = nullptr, *ys = nullptr, *out = nullptr;
+};
+
+}  // namespace
+
+struct rnn_resnet {
+    rnn_ctx *ctx = nullptr;
+    uint32_t depth = 0, width = 0, nclass = 0;
+    NetConv stem;
+    NetBn stem_bn;
+    std::vector<NetBlock> blocks;
+    uint32_t fc_w = 0, fc_b = 0, fin = 0;  // parameter indices, classifier width
+    std::vector<ParamSlot> params;         // for_each_param order
+    size_t np = 0, ndecay = 0, nbuf = 0;
+    float *pv = nullptr, *pg = nullptr, *pm = nullptr, *bufs = nullptr, *coefs = nullptr;
+    // Activation plan for (n, h, w).
+    size_t n = 0, H = 0, W = 0;
+    void *arena = nullptr;
+    float *x = nullptr, *y0 = nullptr, *s0 = nullptr, *pooled = nullptr, *logits = nullptr;
+    float *dlogits = nullptr, *dpool = nullptr, *d0 = nullptr, *d1 = nullptr, *t1 = nullptr,
+          *t2 = nullptr, *scal = nullptr, *loss = nullptr, *dgdb = nullptr;
+    uint32_t *labels = nullptr, *correct = nullptr;
+    double *part = nullptr;
+    size_t fh = 0, fw = 0;  // feature map at the pooling layer
+    bool fwd_train = false;  // last forward saved the backward's activations
+    // Graph of the train step for the current plan.
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t gexec = nullptr;
+    hipStream_t rec_stream = nullptr;  // default priority, used only to record
+    int step_calls = 0;
+    bool use_graph = true;
+    char graph_err[160] = {0};
+};
+
+namespace {
+
+float *pv_of(rnn_resnet *r, int p) { return r->pv + r->params[p].off; }
+float *pg_of(rnn_resnet *r, int p) { return r->pg + r->params[p].off; }
+
+void drop_graph(rnn_resnet *r) {
+    if (r->gexec) (void)hipGraphExecDestroy(r->gexec);
+    if (r->graph) (void)hipGraphDestroy(r->graph);
+    r->gexec = nullptr;
+    r->graph = nullptr;
+    r->step_calls = 0;
+}
+
+int add_param(rnn_resnet *r, size_t len, bool decay) {
+    ParamSlot s;
+    s.len = len;
+    s.decay = decay;
+    r->params.push_back(s);
+    return (int)r->params.size() - 1;
+}
+
+NetConv make_conv(uint32_t cin, uint32_t cout, uint32_t k, uint32_t stride, uint32_t pad) {
+    NetConv c;
+    c.cin = cin;
+    c.cout = cout;
+    c.k = k;
+    c.stride = stride;
+    c.pad = pad;
+    return c;
+}
+
+// Plans the activations for (n, h, w) in one device block.
+int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
+    rnn_ctx *ctx = r->ctx;
+    if (r->arena && r->n == n && r->H == H && r->W == W) return RNN_OK;
+    drop_graph(r);
+    if (r->arena) {
+        RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        RNN_HIP(ctx, hipFree(r->arena));
+        r->arena = nullptr;
+    }
+    WsCarve cv;
+    std::vector<std::pair<float **, size_t>> f32;
+    const size_t w0 = r->width;
+    size_t maxact = n * w0 * H * W, maxc = w0, maxpart = rnn_bn_scratch_doubles(n, w0);
+    f32.push_back({&r->x, n * 3 * H * W});
+    f32.push_back({&r->y0, n * w0 * H * W});
+    f32.push_back({&r->s0, n * w0 * H * W});
+    size_t h = H, w = W;
+    for (auto &b : r->blocks) {
+        b.hin = (uint32_t)h;
+        b.win = (uint32_t)w;
+        rnn_conv_spec sp = b.c1.spec((uint32_t)h, (uint32_t)w);
+        b.hout = sp.oh;
+        b.wout = sp.ow;
+        const size_t a = n * b.c1.cout * sp.oh * sp.ow;
+        f32.push_back({&b.y1, a});
+        f32.push_back({&b.h, a});
+        f32.push_back({&b.y2, a});
+        if (b.down) f32.push_back({&b.ys, a});
+        f32.push_back({&b.out, a});
+        maxact = std::max(maxact, a);
+        maxc = std::max<size_t>(maxc, b.c1.cout);
+        maxpart = std::max(maxpart, rnn_bn_scratch_doubles(n, b.c1.cout));
+        h = sp.oh;
+        w = sp.ow;
+    }
+    r->fh = h;
+    r->fw = w;
+    f32.push_back({&r->pooled, n * r->fin});
+    f32.push_back({&r->dpool, n * r->fin});
+    f32.push_back({&r->logits, n * r->nclass});
+    f32.push_back({&r->dlogits, n * r->nclass});
+    f32.push_back({&r->d0, maxact});
+    f32.push_back({&r->d1, maxact});
+    f32.push_back({&r->t1, maxact});
+    f32.push_back({&r->t2, maxact});
+    f32.push_back({&r->scal, 4});
+    f32.push_back({&r->loss, 1});
+    f32.push_back({&r->dgdb, 2 * maxc});
+    std::vector<size_t> offs;
+    for (auto &e : f32) offs.push_back(cv.take(e.second * sizeof(float)));
+    const size_t o_part = cv.take(maxpart * sizeof(double));
+    const size_t o_lab = cv.take(n * sizeof(uint32_t));
+    const size_t o_cor = cv.take(sizeof(uint32_t));
+    void *mem = nullptr;
+    hipError_t e = hipMalloc(&mem, cv.off);
+    if (e != hipSuccess)
+        return rnn_fail(ctx, RNN_E_NOMEM, "resnet activations hipMalloc(%zu): %s", cv.off,
+                        hipGetErrorString(e));
+    r->arena = mem;
+    char *base = (char *)mem;
+    for (size_t i = 0; i < f32.size(); i++) *f32[i].first = (float *)(base + offs[i]);
+    r->part = (double *)(base + o_part);
+    r->labels = (uint32_t *)(base + o_lab);
+    r->correct = (uint32_t *)(base + o_cor);
+    float *prev = r->s0;
+    for (auto &b : r->blocks) {
+        b.in = prev;
+        prev = b.out;
+    }
+    r->n = n;
+    r->H = H;
+    r->W = W;
+    r->fwd_train = false;
+    return RNN_OK;
+}
+
+RnnBnCoef train_coef(rnn_resnet *r, const NetBn &bn) {
+    return RnnBnCoef{false, bn.coef, bn.coef + bn.c, pv_of(r, bn.g), pv_of(r, bn.b)};
+}
+
+RnnBnCoef eval_coef(const NetBn &bn) {
+    return RnnBnCoef{true, bn.coef + 2 * bn.c, bn.coef + 3 * bn.c, nullptr, nullptr};
+}
+
+// Batch statistics (train) or the running-statistics scale / shift (eval).
+int bn_prepare(rnn_resnet *r, const NetBn &bn, const float *y, size_t hw, bool train) {
+    float *rm = r->bufs + bn.buf, *rv = rm + bn.c;
+    if (train)
+        return rnn_bn_stats_launch(r->ctx, r->n, bn.c, hw, y, r->part, bn.coef, bn.coef + bn.c,
+                                   rm, rv, 0.1f, 1e-5f);
+    return rnn_bn_eval_prep_launch(r->ctx, bn.c, pv_of(r, bn.g), pv_of(r, bn.b), rm, rv, 1e-5f,
+                                   bn.coef + 2 * bn.c, bn.coef + 3 * bn.c);
+}
+
+RnnBnCoef coef(rnn_resnet *r, const NetBn &bn, bool train) {
+    return train ? train_coef(r, bn) : eval_coef(bn);
+}
+
+#define TRY(expr)                 \
+    do {                          \
+        int st_ = (expr);         \
+        if (st_ != RNN_OK) return st_; \
+    } while (0)
+
+// ResNet::forward (model.rs:138-150) with BasicBlock::forward (model.rs:39-57).
+int forward(rnn_resnet *r, bool train) {
+    rnn_ctx *ctx = r->ctx;
+    const size_t n = r->n;
+    rnn_conv_spec sp = r->stem.spec((uint32_t)r->H, (uint32_t)r->W);
+    TRY(rnn_conv2d_forward(ctx, &sp, n, r->x, pv_of(r, r->stem.w), r->y0));
+    TRY(bn_prepare(r, r->stem_bn, r->y0, sp.oh * sp.ow, train));
+    RnnBnCoef c0 = coef(r, r->stem_bn, train);
+    TRY(rnn_bn_apply_launch(ctx, n, r->stem_bn.c, sp.oh * sp.ow, r->y0, c0, 1, 0, nullptr, c0,
+                            r->s0));
+    for (auto &b : r->blocks) {
+        const size_t hw = (size_t)b.hout * b.wout;
+        rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
+        TRY(rnn_conv2d_forward(ctx, &s1, n, b.in, pv_of(r, b.c1.w), b.y1));
+        TRY(bn_prepare(r, b.b1, b.y1, hw, train));
+        RnnBnCoef k1 = coef(r, b.b1, train);
+        TRY(rnn_bn_apply_launch(ctx, n, b.b1.c, hw, b.y1, k1, 1, 0, nullptr, k1, b.h));
+        rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
+        TRY(rnn_conv2d_forward(ctx, &s2, n, b.h, pv_of(r, b.c2.w), b.y2));
+        TRY(bn_prepare(r, b.b2, b.y2, hw, train));
+        RnnBnCoef k2 = coef(r, b.b2, train);
+        if (b.down) {
+            rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
+            TRY(rnn_conv2d_forward(ctx, &sd, n, b.in, pv_of(r, b.cd.w), b.ys));
+            TRY(bn_prepare(r, b.bd, b.ys, hw, train));
+            RnnBnCoef kd = coef(r, b.bd, train);
+            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, k2, 1, 2, b.ys, kd, b.out));
+        } else {
+            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, k2, 1, 1, b.in, k2, b.out));
+        }
+    }
+    const float *feat = r->blocks.empty() ? r->s0 : r->blocks.back().out;
+    TRY(rnn_gap_forward_launch(ctx, n * r->fin, r->fh * r->fw, feat, r->pooled));
+    TRY(rnn_fc_forward_launch(ctx, n, r->fin, r->nclass, r->pooled, pv_of(r, r->fc_w),
+                              pv_of(r, r->fc_b), r->logits));
+    r->fwd_train = train;
+    return RNN_OK;
+}
+
+// ResNet::backward (model.rs:152-162) with BasicBlock::backward
+// (model.rs:59-77).  Gradients accumulate into pg (Param::g).
+int backward(rnn_resnet *r, const float *dlogits) {
+    rnn_ctx *ctx = r->ctx;
+    const size_t n = r->n;
+    TRY(rnn_fc_backward_launch(ctx, n, r->fin, r->nclass, dlogits, r->pooled, pv_of(r, r->fc_w),
+                               pg_of(r, r->fc_w), pg_of(r, r->fc_b), r->dpool));
+    TRY(rnn_gap_backward_launch(ctx, n * r->fin, r->fh * r->fw, r->dpool, r->d0));
+    float *d = r->d0, *other = r->d1;
+    for (size_t i = r->blocks.size(); i-- > 0;) {
+        NetBlock &b = r->blocks[i];
+        const size_t hw = (size_t)b.hout * b.wout;
+        // relu_back_(d, out) is folded into the consumers of d below.
+        TRY(rnn_bn_backward_launch(ctx, n, b.b2.c, hw, d, b.out, b.y2, b.b2.coef,
+                                   b.b2.coef + b.b2.c, pv_of(r, b.b2.g), r->t1, pg_of(r, b.b2.g),
+                                   pg_of(r, b.b2.b), r->part, r->dgdb));
+        rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
+        TRY(rnn_conv2d_backward_w(ctx, &s2, n, r->t1, b.h, pg_of(r, b.c2.w)));
+        TRY(rnn_conv2d_backward_x(ctx, &s2, n, r->t1, pv_of(r, b.c2.w), r->t2));
+        TRY(rnn_bn_backward_launch(ctx, n, b.b1.c, hw, r->t2, b.h, b.y1, b.b1.coef,
+                                   b.b1.coef + b.b1.c, pv_of(r, b.b1.g), r->t1, pg_of(r, b.b1.g),
+                                   pg_of(r, b.b1.b), r->part, r->dgdb));
+        rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
+        TRY(rnn_conv2d_backward_w(ctx, &s1, n, r->t1, b.in, pg_of(r, b.c1.w)));
+        TRY(rnn_conv2d_backward_x(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), other));
+        const size_t in_len = n * (size_t)b.c1.cin * b.hin * b.win;
+        if (b.down) {
+            TRY(rnn_bn_backward_launch(ctx, n, b.bd.c, hw, d, b.out, b.ys, b.bd.coef,
+                                       b.bd.coef + b.bd.c, pv_of(r, b.bd.g), r->t1,
+                                       pg_of(r, b.bd.g), pg_of(r, b.bd.b), r->part, r->dgdb));
+            rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
+            TRY(rnn_conv2d_backward_w(ctx, &sd, n, r->t1, b.in, pg_of(r, b.cd.w)));
+            TRY(rnn_conv2d_backward_x(ctx, &sd, n, r->t1, pv_of(r, b.cd.w), r->t2));
+            TRY(rnn_add_launch(ctx, in_len, other, r->t2, nullptr));
+        } else {
+            TRY(rnn_add_launch(ctx, in_len, other, d, b.out));
+        }
+        std::swap(d, other);
+    }
+    rnn_conv_spec sp = r->stem.spec((uint32_t)r->H, (uint32_t)r->W);
+    TRY(rnn_bn_backward_launch(ctx, n, r->stem_bn.c, sp.oh * sp.ow, d, r->s0, r->y0,
+                               r->stem_bn.coef, r->stem_bn.coef + r->stem_bn.c,
+                               pv_of(r, r->stem_bn.g), r->t1, pg_of(r, r->stem_bn.g),
+                               pg_of(r, r->stem_bn.b), r->part, r->dgdb));
+    // The stem's dX would be the image gradient: discarded (model.rs:161).
+    TRY(rnn_conv2d_backward_w(ctx, &sp, n, r->t1, r->x, pg_of(r, r->stem.w)));
+    return RNN_OK;
+}
+
+int sgd(rnn_resnet *r, const float *scal, float lr, float mom, float wd) {
+    return rnn_sgd_launch(r->ctx, r->np, r->ndecay, r->pv, r->pg, r->pm, lr, mom, wd, scal);
+}
+
+// One train step on the inputs already in r->x / r->labels, scalars in
+// r->scal: forward, softmax-CE, backward, SGD (train.rs:686-699).
+int step_body(rnn_resnet *r) {
+    TRY(forward(r, true));
+    TRY(rnn_softmax_ce_launch(r->ctx, r->n, r->nclass, r->logits, r->labels, 0.0f, r->scal,
+                              r->dlogits, r->loss, r->correct));
+    TRY(backward(r, r->dlogits));
+    return sgd(r, r->scal, 0.f, 0.f, 0.f);
+}
+
+// Runs one step: eagerly, or through the recorded graph (recording it on the
+// second call of a plan).  If recording fails nothing of the step has run: the
+// reason is kept, the network stays eager and the step runs now.
+int run_step(rnn_resnet *r) {
+    rnn_ctx *ctx = r->ctx;
+    if (!r->use_graph || r->step_calls == 0) return step_body(r);
+    if (!r->gexec) {
+        // Recording needs a stream of its own (the caller's may be the null
+        // stream, which cannot record).  Recording runs nothing, so no
+        // ordering with the caller's stream is needed here; the replay is
+        // launched on the caller's stream below.
+        if (!r->rec_stream)
+            RNN_HIP(ctx, hipStreamCreateWithFlags(&r->rec_stream, hipStreamNonBlocking));
+        hipStream_t caller = ctx->stream;
+        ctx->stream = r->rec_stream;
+        hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal);
+        int st = RNN_E_HIP;
+        hipGraph_t g = nullptr;
+        if (e == hipSuccess) {
+            st = step_body(r);
+            e = hipStreamEndCapture(ctx->stream, &g);
+        }
+        ctx->stream = caller;
+        if (st == RNN_OK && e == hipSuccess && g) {
+            r->graph = g;
+            e = hipGraphInstantiate(&r->gexec, g, nullptr, nullptr, 0);
+        } else if (g) {
+            (void)hipGraphDestroy(g);
+        }
+        if (st != RNN_OK || e != hipSuccess || !r->gexec) {
+            const int calls = r->step_calls;
+            drop_graph(r);
+            r->step_calls = calls;
+            snprintf(r->graph_err, sizeof(r->graph_err), "capture: status %d, %s", st,
+                     hipGetErrorString(e));
+            (void)hipGetLastError();
+            r->use_graph = false;
+            return step_body(r);
+        }
+    }
+    RNN_HIP(ctx, hipGraphLaunch(r->gexec, ctx->stream));
+    return RNN_OK;
+}
+
+bool shape_ok(rnn_resnet *r, size_t n, size_t h, size_t w) {
+    return n > 0 && h >= 4 && w >= 4 && n <= 8192 && n * r->width * h * w < (1ull << 32);
+}
+
+}  // namespace
+
+extern "C" {
+
+int rnn_resnet_create(rnn_ctx *ctx, size_t depth_n, size_t width, size_t nclass, uint64_t seed,
+                      rnn_resnet **out) {
+    if (!ctx || !out) return RNN_E_NULL;
+    *out = nullptr;
+    if (depth_n == 0 || width == 0 || nclass == 0 || width > 4096 || nclass > 65536 ||
+        depth_n > 1024)
+        return rnn_fail(ctx, RNN_E_INVALID, "resnet_create: depth %zu width %zu nclass %zu",
+                        depth_n, width, nclass);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    rnn_resnet *r = new rnn_resnet();
+    r->ctx = ctx;
+    r->depth = (uint32_t)depth_n;
+    r->width = (uint32_t)width;
+    r->nclass = (uint32_t)nclass;
+    const char *g = getenv("RNN_GRAPH");
+    r->use_graph = !(g && g[0] == '0');
+    // ResNet::new (model.rs:113-135): blocks first (their convs draw from the
+    // Rng in c1, c2, shortcut order), then the stem conv, then the classifier.
+    const uint32_t widths[3] = {(uint32_t)width, (uint32_t)width * 2, (uint32_t)width * 4};
+    uint32_t cin = (uint32_t)width;
+    size_t nbuf = 0;
+    auto make_bn = [&](uint32_t c) {
+        NetBn bn;
+        bn.c = c;
+        bn.buf = nbuf;
+        nbuf += 2 * c;
+        return bn;
+    };
+    // Visit order (for_each_param, model.rs:164-175 / 79-91): stem w, stem BN
+    // g, b; per block c1 w, b1 g, b, c2 w, b2 g, b, [shortcut w, g, b]; fc w, b.
+    r->stem = make_conv(3, (uint32_t)width, 3, 1, 1);
+    r->stem.w = add_param(r, (size_t)width * 27, true);
+    r->stem_bn = make_bn((uint32_t)width);
+    r->stem_bn.g = add_param(r, width, false);
+    r->stem_bn.b = add_param(r, width, false);
+    for (int s = 0; s < 3; s++)
+        for (size_t bi = 0; bi < depth_n; bi++) {
+            const uint32_t co = widths[s];
+            const uint32_t stride = (s > 0 && bi == 0) ? 2 : 1;
+            NetBlock b;
+            b.c1 = make_conv(cin, co, 3, stride, 1);
+            b.c1.w = add_param(r, (size_t)co * cin * 9, true);
+            b.b1 = make_bn(co);
+            b.b1.g = add_param(r, co, false);
+            b.b1.b = add_param(r, co, false);
+            b.c2 = make_conv(co, co, 3, 1, 1);
+            b.c2.w = add_param(r, (size_t)co * co * 9, true);
+            b.b2 = make_bn(co);
+            b.b2.g = add_param(r, co, false);
+            b.b2.b = add_param(r, co, false);
+            b.down = stride != 1 || cin != co;
+            if (b.down) {
+                b.cd = make_conv(cin, co, 1, stride, 0);
+                b.cd.w = add_param(r, (size_t)co * cin, true);
+                b.bd = make_bn(co);
+                b.bd.g = add_param(r, co, false);
+                b.bd.b = add_param(r, co, false);
+            }
+            r->blocks.push_back(b);
+            cin = co;
+        }
+    r->fin = cin;
+    r->fc_w = add_param(r, (size_t)cin * nclass, true);
+    r->fc_b = add_param(r, nclass, false);
+    r->nbuf = nbuf;
+    // Flat layout: weight-decayed parameters first, each group in visit order.
+    size_t off = 0;
+    for (int pass = 0; pass < 2; pass++)
+        for (auto &p : r->params)
+            if (p.decay == (pass == 0)) {
+                p.off = off;
+                off += p.len;
+                if (pass == 0) r->ndecay = off;
+            }
+    r->np = off;
+    // Host values: Kaiming draws in creation order, BN gamma 1 (0 for the
+    // second BN of a block, model.rs:22-23), beta 0, classifier * 0.5.
+    std::vector<float> hv(r->np, 0.0f), hb(r->nbuf, 0.0f);
+    HostRng rng(seed);
+    auto kaiming = [&](int p, size_t fan_in) {
+        const float sc = sqrtf(2.0f / (float)fan_in);
+        float *v = hv.data() + r->params[p].off;
+        for (size_t i = 0; i < r->params[p].len; i++) v[i] = rng.normal() * sc;
+    };
+    auto bn_init = [&](const NetBn &bn, float gamma) {
+        float *gv = hv.data() + r->params[bn.g].off;
+        for (uint32_t i = 0; i < bn.c; i++) gv[i] = gamma;
+        for (uint32_t i = 0; i < bn.c; i++) hb[bn.buf + bn.c + i] = 1.0f;  // running var
+    };
+    for (auto &b : r->blocks) {
+        kaiming(b.c1.w, (size_t)b.c1.cin * 9);
+        kaiming(b.c2.w, (size_t)b.c2.cin * 9);
+        if (b.down) kaiming(b.cd.w, b.cd.cin);
+        bn_init(b.b1, 1.0f);
+        bn_init(b.b2, 0.0f);
+        if (b.down) bn_init(b.bd, 1.0f);
+    }
+    kaiming(r->stem.w, 27);
+    bn_init(r->stem_bn, 1.0f);
+    kaiming(r->fc_w, cin);
+    {
+        float *v = hv.data() + r->params[r->fc_w].off;
+        for (size_t i = 0; i < r->params[r->fc_w].len; i++) v[i] = v[i] * 0.5f;
+    }
+    // Device state: v, g, m, buffers, BN coefficients.
+    size_t ncoef = 4 * (size_t)r->stem_bn.c;
+    for (auto &b : r->blocks) ncoef += 4 * (size_t)(b.b1.c + b.b2.c + (b.down ? b.bd.c : 0));
+    const size_t bytes = (3 * r->np + r->nbuf + ncoef) * sizeof(float);
+    void *mem = nullptr;
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipMalloc(&mem, bytes);
+    if (e != hipSuccess) {
+        delete r;
+        return rnn_fail(ctx, RNN_E_NOMEM, "resnet_create hipMalloc(%zu): %s", bytes,
+                        hipGetErrorString(e));
+    }
+    r->pv = (float *)mem;
+    r->pg = r->pv + r->np;
+    r->pm = r->pg + r->np;
+    r->bufs = r->pm + r->np;
+    r->coefs = r->bufs + r->nbuf;
+    float *cp = r->coefs;
+    auto give = [&](NetBn &bn) {
+        bn.coef = cp;
+        cp += 4 * (size_t)bn.c;
+    };
+    give(r->stem_bn);
+    for (auto &b : r->blocks) {
+        give(b.b1);
+        give(b.b2);
+        if (b.down) give(b.bd);
+    }
+    e = hipMemcpy(r->pv, hv.data(), r->np * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(r->pg, 0, 2 * r->np * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMemcpy(r->bufs, hb.data(), r->nbuf * sizeof(float), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(r->coefs, 0, ncoef * sizeof(float));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(mem);
+        delete r;
+        return rnn_fail(ctx, RNN_E_HIP, "resnet_create upload: %s", hipGetErrorString(e));
+    }
+    *out = r;
+    return RNN_OK;
+}
+
+int rnn_resnet_destroy(rnn_resnet *r) {
+    if (!r) return RNN_E_NULL;
+    rnn_ctx *ctx = r->ctx;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    (void)hipStreamSynchronize(ctx->stream);
+    drop_graph(r);
+    if (r->rec_stream) (void)hipStreamDestroy(r->rec_stream);
+    if (r->arena) (void)hipFree(r->arena);
+    if (r->pv) (void)hipFree(r->pv);
+    delete r;
+    return RNN_OK;
+}
+
+size_t rnn_resnet_num_params(const rnn_resnet *r) { return r ? r->np : 0; }
+size_t rnn_resnet_num_buffers(const rnn_resnet *r) { return r ? r->nbuf : 0; }
+size_t rnn_resnet_num_tensors(const rnn_resnet *r) { return r ? r->params.size() : 0; }
+
+int rnn_resnet_tensor_len(const rnn_resnet *r, size_t i, size_t *len, int *decay) {
+    if (!r || !len) return RNN_E_NULL;
+    if (i >= r->params.size()) return rnn_fail(r->ctx, RNN_E_INVALID, "tensor %zu out of range", i);
+    *len = r->params[i].len;
+    if (decay) *decay = r->params[i].decay ? 1 : 0;
+    return RNN_OK;
+}
+
+int rnn_resnet_copy(rnn_resnet *r, int which, float *dst, const float *src) {
+    if (!r) return RNN_E_NULL;
+    rnn_ctx *ctx = r->ctx;
+    if ((dst == nullptr) == (src == nullptr))
+        return rnn_fail(ctx, RNN_E_INVALID, "resnet_copy: exactly one of dst / src");
+    if (which < 0 || which > 3) return rnn_fail(ctx, RNN_E_INVALID, "resnet_copy: which %d", which);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (which == 3) {
+        const size_t bytes = r->nbuf * sizeof(float);
+        if (dst)
+            RNN_HIP(ctx, hipMemcpyAsync(dst, r->bufs, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+        else
+            RNN_HIP(ctx, hipMemcpyAsync(r->bufs, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+        return RNN_OK;
+    }
+    float *base = which == 0 ? r->pv : which == 1 ? r->pg : r->pm;
+    size_t pos = 0;  // position in for_each_param order
+    for (auto &p : r->params) {
+        if (dst)
+            RNN_HIP(ctx, hipMemcpyAsync(dst + pos, base + p.off, p.len * sizeof(float),
+                                        hipMemcpyDeviceToDevice, ctx->stream));
+        else
+            RNN_HIP(ctx, hipMemcpyAsync(base + p.off, src + pos, p.len * sizeof(float),
+                                        hipMemcpyDeviceToDevice, ctx->stream));
+        pos += p.len;
+    }
+    return RNN_OK;
+}
+
+int rnn_resnet_forward(rnn_resnet *r, size_t n, size_t h, size_t w, const float *x, int train,
+                       float *logits) {
+    if (!r) return RNN_E_NULL;
+    rnn_ctx *ctx = r->ctx;
+    if (!x || !logits) return rnn_fail(ctx, RNN_E_NULL, "resnet_forward: null pointer");
+    if (!shape_ok(r, n, h, w))
+        return rnn_fail(ctx, RNN_E_INVALID, "resnet_forward: n %zu h %zu w %zu", n, h, w);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    TRY(plan(r, n, h, w));
+    RNN_HIP(ctx, hipMemcpyAsync(r->x, x, n * 3 * h * w * sizeof(float), hipMemcpyDeviceToDevice,
+                                ctx->stream));
+    TRY(forward(r, train != 0));
+    RNN_HIP(ctx, hipMemcpyAsync(logits, r->logits, n * r->nclass * sizeof(float),
+                                hipMemcpyDeviceToDevice, ctx->stream));
+    return RNN_OK;
+}
+
+int rnn_resnet_backward(rnn_resnet *r, const float *dlogits) {
+    if (!r) return RNN_E_NULL;
+    rnn_ctx *ctx = r->ctx;
+    if (!dlogits) return rnn_fail(ctx, RNN_E_NULL, "resnet_backward: null pointer");
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (!r->arena || !r->fwd_train)
+        return rnn_fail(ctx, RNN_E_INVALID, "resnet_backward: no train-mode forward to differentiate");
+    RNN_HIP(ctx, hipMemcpyAsync(r->dlogits, dlogits, r->n * r->nclass * sizeof(float),
+                                hipMemcpyDeviceToDevice, ctx->stream));
+    return backward(r, r->dlogits);
+}
+
+int rnn_resnet_step(rnn_resnet *r, float lr, float momentum, float wd) {
+    if (!r) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(r->ctx->mu);
+    return sgd(r, nullptr, lr, momentum, wd);
+}
+
+int rnn_resnet_train_step(rnn_resnet *r, size_t n, size_t h, size_t w, const float *x,
+                          const uint32_t *labels, float smooth, float lr, float momentum, float wd,
+                          float *loss, uint32_t *correct) {
+    if (!r) return RNN_E_NULL;
+    rnn_ctx *ctx = r->ctx;
+    if (!x || !labels) return rnn_fail(ctx, RNN_E_NULL, "resnet_train_step: null pointer");
+    if (!shape_ok(r, n, h, w))
+        return rnn_fail(ctx, RNN_E_INVALID, "resnet_train_step: n %zu h %zu w %zu", n, h, w);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    TRY(plan(r, n, h, w));
+    RNN_HIP(ctx, hipMemcpyAsync(r->x, x, n * 3 * h * w * sizeof(float), hipMemcpyDeviceToDevice,
+                                ctx->stream));
+    RNN_HIP(ctx, hipMemcpyAsync(r->labels, labels, n * sizeof(uint32_t), hipMemcpyDeviceToDevice,
+                                ctx->stream));
+    TRY(rnn_set_scalars_launch(ctx, r->scal, lr, momentum, wd, smooth));
+    // The first call of a plan runs eagerly (it also sizes the shared
+    // workspace); the second records the graph; later calls replay it.
+    TRY(run_step(r));
+    r->step_calls++;
+    r->fwd_train = true;
+    if (loss)
+        RNN_HIP(ctx, hipMemcpyAsync(loss, r->loss, sizeof(float), hipMemcpyDeviceToDevice,
+                                    ctx->stream));
+    if (correct)
+        RNN_HIP(ctx, hipMemcpyAsync(correct, r->correct, sizeof(uint32_t),
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+    return RNN_OK;
+}
+
+int rnn_resnet_set_graph(rnn_resnet *r, int on) {
+    if (!r) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(r->ctx->mu);
+    RNN_HIP(r->ctx, hipStreamSynchronize(r->ctx->stream));
+    drop_graph(r);
+    r->use_graph = on != 0;
+    r->graph_err[0] = 0;
+    return RNN_OK;
+}
+
+int rnn_resnet_graph_state(const rnn_resnet *r, const char **why) {
+    if (!r) return RNN_E_NULL;
+    if (why) *why = r->graph_err;
+    return r->gexec ? 1 : 0;
+}
+
+int rnn_resnet_logits(rnn_resnet *r, float *logits) {
+    if (!r || !logits) return RNN_E_NULL;
+    rnn_ctx *ctx = r->ctx;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (!r->arena) return rnn_fail(ctx, RNN_E_INVALID, "resnet_logits: no forward yet");
+    RNN_HIP(ctx, hipMemcpyAsync(logits, r->logits, r->n * r->nclass * sizeof(float),
+                                hipMemcpyDeviceToDevice, ctx->stream));
+    return RNN_OK;
+}
+
+uint64_t rnn_resnet_flops(const rnn_resnet *r, size_t h, size_t w) {
+    // ResNet::flops (model.rs:179-198): forward FLOP per image.
+    if (!r) return 0;
+    uint64_t f = 2ull * 3 * 9 * r->stem.cout * h * w;
+    size_t hh = h, ww = w, c = r->stem.cout;
+    for (auto &b : r->blocks) {
+        const size_t oh = hh / b.c1.stride, ow = ww / b.c1.stride;
+        f += 2ull * b.c1.cin * 9 * b.c1.cout * oh * ow;
+        f += 2ull * b.c2.cin * 9 * b.c2.cout * oh * ow;
+        if (b.down) f += 2ull * b.cd.cin * b.cd.cout * oh * ow;
+        hh = oh;
+        ww = ow;
+        c = b.c2.cout;
+    }
+    return f + 2ull * c * r->nclass;
+}
+
+}  // extern "C"

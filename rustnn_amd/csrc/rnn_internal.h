@@ -93,3 +93,46 @@ int rnn_conv_fast(rnn_ctx *ctx, int dx, const rnn_conv_spec *sp, size_t n, const
 // dW += over the batch (k = 1 or 3).
 int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
                 float *dw);
+
+// ResNet layer launchers (nn.hip).  Per-channel BN coefficients: train mode
+// uses (mean, invstd, gamma, beta); eval mode (eval = true) uses the
+// precomputed scale / shift in the mean / invstd slots.
+struct RnnBnCoef {
+    bool eval;
+    const float *mean, *invstd, *gamma, *beta;
+};
+// f64 elements of BN partial-sum scratch for n images of c channels.
+size_t rnn_bn_scratch_doubles(size_t n, size_t c);
+// Batch statistics: mean / invstd, and running mean / var when rm is set.
+int rnn_bn_stats_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, double *part,
+                        float *mean, float *invstd, float *rm, float *rv, float mom, float eps);
+// out = [relu](bn(x) [+ skip | + sbn(skip)]); skip_mode 0 / 1 / 2 (2 and 1
+// imply relu).
+int rnn_bn_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x,
+                        const RnnBnCoef &bn, int relu, int skip_mode, const float *skip,
+                        const RnnBnCoef &sbn, float *out);
+int rnn_bn_eval_prep_launch(rnn_ctx *ctx, size_t c, const float *gamma, const float *beta,
+                            const float *rm, const float *rv, float eps, float *sc, float *sh);
+// BN backward with relu_back by `mask` folded in (mask may be null); dgamma /
+// dbeta accumulate (may be null); dgdb[2c] is scratch.
+int rnn_bn_backward_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
+                           const float *mask, const float *x, const float *mean,
+                           const float *invstd, const float *gamma, float *dx, float *dgamma,
+                           float *dbeta, double *part, float *dgdb);
+// a += [mask] b.
+int rnn_add_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *mask);
+int rnn_gap_forward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *x, float *y);
+int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx);
+int rnn_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
+                          const float *w, const float *b, float *y);
+int rnn_fc_backward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
+                           const float *x, const float *w, float *dw, float *db, float *dx);
+// scal (device, may be null) overrides smooth with scal[3].
+int rnn_softmax_ce_launch(rnn_ctx *ctx, size_t rows, size_t nclass, const float *logits,
+                          const uint32_t *labels, float smooth, const float *scal, float *dl,
+                          float *loss, uint32_t *correct);
+// Nesterov SGD over [0, len), weight decay on [0, ndecay); scal (device, may
+// be null) overrides (lr, mom, wd) with scal[0..3].
+int rnn_sgd_launch(rnn_ctx *ctx, size_t len, size_t ndecay, float *v, float *g, float *m, float lr,
+                   float mom, float wd, const float *scal);
+int rnn_set_scalars_launch(rnn_ctx *ctx, float *scal, float a, float b, float c, float d);

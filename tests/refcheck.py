@@ -1,11 +1,17 @@
 """Restatement of the reference's gradient-check harness (check.rs), run
-against a pluggable conv / attention backend (the CPU oracle or the HIP path).
+against a pluggable backend (the CPU oracle or the HIP path).
 
 * dircheck (check.rs:16-40): central difference along a random direction v
   drawn from the same Rng, relative error |num - ana| / (|num| + |ana| + 1e-6).
 * conv_layercheck (check.rs:503-546): the three conv layer shapes at seed 1234
   in the reference's exact Rng draw order (Kaiming W, x, r, then one direction
   per dircheck), tolerance 5e-3, eps = GC_EPS or 3e-4 (check.rs:55-60).
+* nn_layercheck (check.rs:548-670): batchnorm dx / dgamma / dbeta, linear dx /
+  dw, the two BasicBlock shapes (dx, dparams) and softmax_ce dlogits, drawing
+  from the same Rng after the conv shapes.
+* resnet_gradcheck (check.rs:727-775): ResNet(1, 4, 10, seed), parameters
+  perturbed by 0.3*normal, batch 8 at 16x16, smooth 0, one dircheck over every
+  parameter.
 """
 import os
 
@@ -107,3 +113,379 @@ def conv_layercheck(rng_cls, backend):
         e = dircheck(w, dw, eps, rng, lambda c: dot32(backend.forward(sp, 2, x, c), r))
         out.append((f"{tag} dw", e))
     return out
+
+
+# ------------------------------------------------------------- nn.rs layers
+def _skip_conv_draws(rng):
+    """Advances the Rng past conv_layercheck's draws (W, x, r, two directions)."""
+    for cin, cout, k, s, p, hh, _ in CONV_SHAPES:
+        oh = (hh + 2 * p - k) // s + 1
+        ckk = cin * k * k
+        rng.rand_vec(cout * ckk)
+        rng.rand_vec(2 * cin * hh * hh)
+        rng.rand_vec(2 * cout * oh * oh)
+        rng.rand_vec(2 * cin * hh * hh)
+        rng.rand_vec(cout * ckk)
+
+
+def nn_layercheck(orc, be):
+    """check.rs:548-670 on backend `be`; returns [(tag, err)]."""
+    rng = orc.Rng(SEED)
+    eps = gc_eps()
+    _skip_conv_draws(rng)
+    out = []
+    # batchnorm (check.rs:548-598)
+    c = 4
+    g = (np.float32(0.5) + rng.uniform_vec(c)).astype(np.float32)
+    b = rng.rand_vec(c)
+    x = (rng.rand_vec(3 * c * 25) * np.float32(2.0) + np.float32(1.0)).reshape(3, c, 5, 5)
+    bn = be.bn(c, g, b)
+    y0 = bn.forward(x)
+    r = rng.rand_vec(y0.size)
+    dx = bn.backward(r.reshape(x.shape))
+    dg, db = bn.grads()
+    out.append(("batchnorm dx", dircheck(x.ravel(), dx, eps, rng,
+                                         lambda cc: dot32(bn.forward(cc.reshape(x.shape)), r))))
+    out.append(("batchnorm dgamma", dircheck(g, dg, eps, rng,
+                                             lambda cc: dot32(bn.with_gamma(cc, x), r))))
+    out.append(("batchnorm dbeta", dircheck(b, db, eps, rng,
+                                            lambda cc: dot32(bn.with_beta(cc, x), r))))
+    # linear (check.rs:600-624)
+    lin = be.linear(6, 5, rng)
+    lin.set_bias(rng.rand_vec(5))
+    x = rng.rand_vec(3 * 6).reshape(3, 6)
+    y0 = lin.forward(x)
+    r = rng.rand_vec(y0.size)
+    dx = lin.backward(r.reshape(y0.shape))
+    dw = lin.dw()
+    out.append(("linear dx", dircheck(x.ravel(), dx, eps, rng,
+                                      lambda cc: dot32(lin.forward(cc.reshape(x.shape)), r))))
+    w0 = lin.weight()
+    out.append(("linear dw", dircheck(w0, dw, eps, rng, lambda cc: dot32(lin.with_weight(cc, x),
+                                                                         r))))
+    # BasicBlock (check.rs:625-657)
+    for cin, cout, stride, tag in ((4, 4, 1, "block id/s1"), (4, 8, 2, "block down/s2")):
+        blk = be.block(cin, cout, stride, rng)
+        base = blk.params()
+        base = (base + np.float32(0.3) * rng.rand_vec(base.size)).astype(np.float32)
+        blk.set_params(base)
+        x = rng.rand_vec(2 * cin * 64).reshape(2, cin, 8, 8)
+        y0 = blk.forward(x)
+        r = rng.rand_vec(y0.size)
+        dx = blk.backward(r.reshape(y0.shape))
+        out.append((f"{tag} dx", dircheck(x.ravel(), dx, eps, rng,
+                                          lambda cc: dot32(blk.forward(cc.reshape(x.shape)), r))))
+        grad = blk.grads()
+
+        def lossp(cc):
+            blk.set_params(cc)
+            return dot32(blk.forward(x), r)
+        out.append((f"{tag} dparams", dircheck(base, grad, eps, rng, lossp)))
+        blk.set_params(base)
+    # softmax_ce (check.rs:659-670)
+    n, nc = 4, 7
+    z = rng.rand_vec(n * nc).reshape(n, nc)
+    labels = np.array([rng.below(nc) for _ in range(n)], np.uint32)
+    _, d = be.softmax_ce(z, labels, 0.1)
+    out.append(("softmax_ce dlogits", dircheck(z.ravel(), d, eps, rng,
+                                               lambda cc: be.softmax_ce(cc.reshape(n, nc), labels,
+                                                                        0.1)[0])))
+    return out
+
+
+def resnet_gradcheck(orc, be, seed=SEED):
+    """check.rs:727-775 on backend `be` (a ResNet factory); returns the error."""
+    NC, BS = 10, 8
+    eps = gc_eps()
+    net = be.resnet(1, 4, NC, seed)
+    rng = orc.Rng(seed ^ 0x5EED)
+    base = net.params()
+    base = (base + np.float32(0.3) * rng.rand_vec(base.size)).astype(np.float32)
+    net.set_params(base)
+    x = rng.rand_vec(BS * 3 * 16 * 16).reshape(BS, 3, 16, 16)
+    labels = np.array([rng.below(NC) for _ in range(BS)], np.uint32)
+    logits = net.forward(x)
+    _, dl = be.softmax_ce(logits, labels, 0.0)
+    net.backward(dl.reshape(BS, NC))
+    grad = net.grads()
+
+    def lossf(cc):
+        net.set_params(cc)
+        return be.softmax_ce(net.forward(x), labels, 0.0)[0]
+    return dircheck(base, grad, eps, rng, lossf)
+
+
+class _OracleBn:
+    def __init__(self, M, c, g, b):
+        self.bn = M.BatchNorm2d(c)
+        self.bn.g.v[:] = g
+        self.bn.b.v[:] = b
+
+    def forward(self, x):
+        return self.bn.forward(np.ascontiguousarray(x, np.float32), True)
+
+    def backward(self, dy):
+        return self.bn.backward(np.ascontiguousarray(dy, np.float32)).ravel()
+
+    def grads(self):
+        return self.bn.g.g.copy(), self.bn.b.g.copy()
+
+    def with_gamma(self, g, x):
+        old = self.bn.g.v.copy()
+        self.bn.g.v[:] = g
+        y = self.forward(x)
+        self.bn.g.v[:] = old
+        return y
+
+    def with_beta(self, b, x):
+        old = self.bn.b.v.copy()
+        self.bn.b.v[:] = b
+        y = self.forward(x)
+        self.bn.b.v[:] = old
+        return y
+
+
+class _OracleLinear:
+    def __init__(self, M, fin, fout, rng):
+        self.l = M.Linear(fin, fout, rng)
+
+    def set_bias(self, b):
+        self.l.b.v[:] = b
+
+    def forward(self, x):
+        return self.l.forward(x, True)
+
+    def backward(self, dy):
+        return self.l.backward(dy).ravel()
+
+    def dw(self):
+        return self.l.w.g.copy()
+
+    def weight(self):
+        return self.l.w.v.copy()
+
+    def with_weight(self, w, x):
+        old = self.l.w.v.copy()
+        self.l.w.v[:] = w
+        y = self.l.forward(x, False)
+        self.l.w.v[:] = old
+        return y
+
+
+class _OracleBlock:
+    def __init__(self, M, cin, cout, stride, rng):
+        self.b = M.BasicBlock(cin, cout, stride, rng)
+
+    def params(self):
+        return np.concatenate([p.v for p in self.b.params()])
+
+    def grads(self):
+        return np.concatenate([p.g for p in self.b.params()])
+
+    def set_params(self, flat):
+        off = 0
+        for p in self.b.params():
+            p.v[:] = flat[off:off + p.v.size]
+            off += p.v.size
+
+    def forward(self, x):
+        return self.b.forward(np.ascontiguousarray(x, np.float32), True)
+
+    def backward(self, dy):
+        return self.b.backward(dy).ravel()
+
+
+class _OracleNet:
+    def __init__(self, M, depth, width, nc, seed):
+        self.n = M.ResNet(depth, width, nc, seed)
+
+    def params(self):
+        return np.concatenate([p.v for p in self.n.params()])
+
+    def grads(self):
+        return np.concatenate([p.g for p in self.n.params()])
+
+    def set_params(self, flat):
+        off = 0
+        for p in self.n.params():
+            p.v[:] = flat[off:off + p.v.size]
+            off += p.v.size
+
+    def forward(self, x):
+        return self.n.forward(x, True)
+
+    def backward(self, dl):
+        self.n.backward(dl)
+
+
+class OracleNN:
+    """Layer factory on the CPU oracle (oracle/pymodel.py)."""
+
+    def __init__(self, orc, pymodel):
+        self.o, self.M = orc, pymodel
+
+    def bn(self, c, g, b):
+        return _OracleBn(self.M, c, g, b)
+
+    def linear(self, fin, fout, rng):
+        return _OracleLinear(self.M, fin, fout, rng)
+
+    def block(self, cin, cout, stride, rng):
+        return _OracleBlock(self.M, cin, cout, stride, rng)
+
+    def softmax_ce(self, z, labels, smooth):
+        loss, _, d = self.o.softmax_ce(z, labels, smooth)
+        return loss, d.ravel()
+
+
+class OracleResNet(OracleNN):
+    def __init__(self, pymodel):
+        from oracle import pyorc
+        super().__init__(pyorc, pymodel)
+
+    def resnet(self, depth, width, nc, seed):
+        return _OracleNet(self.M, depth, width, nc, seed)
+
+
+# ---------------------------------------------------------------- GPU side
+def _dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+
+
+def _host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+class _GpuBn:
+    def __init__(self, rnn, c, g, b):
+        from rustnn_amd.nn import BatchNorm2d
+        self.bn = BatchNorm2d(c)
+        self.bn.g.v.copy_(_dev(g))
+        self.bn.b.v.copy_(_dev(b))
+
+    def forward(self, x):
+        return _host(self.bn.forward(_dev(x), True))
+
+    def backward(self, dy):
+        return _host(self.bn.backward(_dev(dy))).ravel()
+
+    def grads(self):
+        return _host(self.bn.g.g).copy(), _host(self.bn.b.g).copy()
+
+    def with_gamma(self, g, x):
+        old = self.bn.g.v.clone()
+        self.bn.g.v.copy_(_dev(g))
+        y = self.forward(x)
+        self.bn.g.v.copy_(old)
+        return y
+
+    def with_beta(self, b, x):
+        old = self.bn.b.v.clone()
+        self.bn.b.v.copy_(_dev(b))
+        y = self.forward(x)
+        self.bn.b.v.copy_(old)
+        return y
+
+
+class _GpuLinear:
+    def __init__(self, M, fin, fout, rng):
+        from rustnn_amd.nn import Linear
+        ref = M.Linear(fin, fout, rng)  # the reference's Kaiming draws
+        self.l = Linear(fin, fout, _dev(ref.w.v))
+
+    def set_bias(self, b):
+        self.l.b.v.copy_(_dev(b))
+
+    def forward(self, x):
+        return _host(self.l.forward(_dev(x), True))
+
+    def backward(self, dy):
+        return _host(self.l.backward(_dev(dy))).ravel()
+
+    def dw(self):
+        return _host(self.l.w.g).copy()
+
+    def weight(self):
+        return _host(self.l.w.v).copy()
+
+    def with_weight(self, w, x):
+        old = self.l.w.v.clone()
+        self.l.w.v.copy_(_dev(w))
+        y = _host(self.l.forward(_dev(x), False))
+        self.l.w.v.copy_(old)
+        return y
+
+
+class _GpuBlock:
+    def __init__(self, M, cin, cout, stride, rng):
+        from rustnn_amd.model import BasicBlock
+        ref = M.BasicBlock(cin, cout, stride, rng)  # the reference's draws
+        wd = _dev(ref.down[0].w.v) if ref.down is not None else None
+        self.b = BasicBlock(cin, cout, stride, _dev(ref.c1.w.v), _dev(ref.c2.w.v), wd)
+
+    def params(self):
+        return np.concatenate([_host(v).ravel() for v, _ in self.b.params()])
+
+    def grads(self):
+        return np.concatenate([_host(g).ravel() for _, g in self.b.params()])
+
+    def set_params(self, flat):
+        off = 0
+        for v, _ in self.b.params():
+            v.copy_(_dev(flat[off:off + v.numel()]))
+            off += v.numel()
+
+    def forward(self, x):
+        return _host(self.b.forward(_dev(x), True))
+
+    def backward(self, dy):
+        return _host(self.b.backward(_dev(dy))).ravel()
+
+
+class _GpuNet:
+    def __init__(self, depth, width, nc, seed):
+        from rustnn_amd.model import ResNet
+        self.n = ResNet(depth, width, nc, seed)
+
+    def params(self):
+        return _host(self.n.params())
+
+    def grads(self):
+        return _host(self.n.grads())
+
+    def set_params(self, flat):
+        self.n.set_params(_dev(flat))
+
+    def forward(self, x):
+        return _host(self.n.forward(_dev(x), True))
+
+    def backward(self, dl):
+        self.n.backward(_dev(dl))
+
+
+class GpuNN:
+    """Layer / network factory on the HIP path (C ABI through rustnn_amd)."""
+
+    def __init__(self, pymodel):
+        self.M = pymodel
+
+    def bn(self, c, g, b):
+        return _GpuBn(None, c, g, b)
+
+    def linear(self, fin, fout, rng):
+        return _GpuLinear(self.M, fin, fout, rng)
+
+    def block(self, cin, cout, stride, rng):
+        return _GpuBlock(self.M, cin, cout, stride, rng)
+
+    def softmax_ce(self, z, labels, smooth):
+        import torch
+        from rustnn_amd.nn import softmax_ce
+        loss, _, d = softmax_ce(_dev(z), torch.from_numpy(labels.astype(np.int32)).cuda(), smooth)
+        return float(_host(loss)[0]), _host(d).ravel()
+
+    def resnet(self, depth, width, nc, seed):
+        return _GpuNet(depth, width, nc, seed)

@@ -1,0 +1,187 @@
+"""GPU parity: the device-resident ResNet train step (model.rs, nn.rs,
+train.rs:686-699) through the C ABI (rnn_resnet_*) against the CPU oracle's
+ResNet (oracle/pymodel.py) on identical seeded inputs.
+
+* initialisation: ResNet::new's Kaiming draws and BN / classifier init,
+  bit-exact, in for_each_param / for_each_buffer order;
+* one train step at BASELINE config 3 (ResNet-20 W32, batch 128, 32x32,
+  smooth 0.1, SGD 0.2 / 0.9 / 5e-4): logits, loss, gradients, updated
+  parameters, momenta and running statistics;
+* the reference's full-network gradcheck (check.rs:727-775) through the GPU;
+* the recorded hipGraph replays bit-identically to eager execution, with eager
+  work and synchronisation between the replays."""
+import numpy as np
+import pytest
+
+from conftest import rel_frob, to_dev, to_host
+
+import refcheck
+
+pytestmark = pytest.mark.gpu
+
+# Tolerances of the whole-network comparison (relative Frobenius): 1e-5 for
+# the logits and the whole gradient vector (measured on MI355X: 2.3e-7 and
+# 2.0e-6).  Single small tensors (a BN beta of 32 values whose gradient sums
+# cancel) get 1e-4: the convolutions sum in a different order than the
+# reference and BatchNorm's backward divides by the per-channel deviation.
+TOL_FWD = 1e-5
+TOL_GRAD = 1e-5
+TOL_TENSOR = 1e-4
+
+
+def _cfg3_inputs(orc, n, seed=2026):
+    """Config 3: images uniform in [0, 1] normalised per channel with the
+    reference's MEAN / STD (data.rs:13-14, 96-98); labels uniform in 0..99."""
+    rng = orc.Rng(seed)
+    u = rng.uniform_vec(n * 3 * 32 * 32).reshape(n, 3, 32, 32)
+    mean = np.array([0.5071, 0.4865, 0.4409], np.float32)[None, :, None, None]
+    std = np.array([0.2673, 0.2564, 0.2762], np.float32)[None, :, None, None]
+    x = ((u - mean) / std).astype(np.float32)
+    labels = np.array([rng.below(100) for _ in range(n)], np.uint32)
+    return x, labels
+
+
+def _oracle_flat(net, attr):
+    return np.concatenate([getattr(p, attr).ravel() for p in net.params()])
+
+
+def test_init_bit_exact(rnn, orc):
+    from oracle import pymodel
+    from rustnn_amd.model import ResNet
+    for depth, width, nc, seed in ((3, 32, 100, 0), (1, 4, 10, 1234)):
+        want = pymodel.ResNet(depth, width, nc, seed)
+        got = ResNet(depth, width, nc, seed)
+        lens = got.tensor_lens()
+        assert [n for n, _ in lens] == [p.v.size for p in want.params()]
+        assert [d for _, d in lens] == [p.decay for p in want.params()]
+        assert np.array_equal(to_host(got.params()), _oracle_flat(want, "v"))
+        assert np.array_equal(to_host(got.buffers()), np.concatenate(want.buffers()))
+        assert not to_host(got.grads()).any() and not to_host(got.momenta()).any()
+        assert got.flops(32, 32) == want.flops(32, 32)
+        got.close()
+
+
+def test_train_step_config3(rnn, orc):
+    """One BASELINE config-3 step on the device vs the oracle."""
+    import torch
+    from oracle import pymodel
+    from rustnn_amd.model import ResNet
+    n = 128
+    x, labels = _cfg3_inputs(orc, n)
+    want = pymodel.ResNet(3, 32, 100, 7)
+    got = ResNet(3, 32, 100, 7)
+    with orc.threads(16):
+        lg_w = want.forward(x, True)
+        loss_w, corr_w, dl_w = orc.softmax_ce(lg_w, labels, 0.1)
+        want.backward(dl_w)
+    X = to_dev(x)
+    L = torch.from_numpy(labels.astype(np.int32)).cuda()
+    lg = got.forward(X, True)
+    from rustnn_amd.nn import softmax_ce
+    loss, corr, dl = softmax_ce(lg, L, 0.1)
+    got.backward(dl)
+    print("logits err", rel_frob(to_host(lg), lg_w), "grad err",
+          rel_frob(to_host(got.grads()), _oracle_flat(want, "g")))
+    assert rel_frob(to_host(lg), lg_w) < TOL_FWD
+    assert abs(float(to_host(loss)[0]) - loss_w) < 1e-5 * abs(loss_w)
+    assert int(to_host(corr)[0]) == corr_w
+    g_got, g_want = to_host(got.grads()), _oracle_flat(want, "g")
+    off = 0
+    for i, p in enumerate(want.params()):
+        e = rel_frob(g_got[off:off + p.v.size], p.g)
+        assert e < TOL_TENSOR, (i, p.v.size, e)
+        off += p.v.size
+    assert rel_frob(g_got, g_want) < TOL_GRAD
+    assert rel_frob(to_host(got.buffers()), np.concatenate(want.buffers())) < 1e-6
+    # the SGD step on those gradients
+    with orc.threads(16):
+        want.step(0.2, 0.9, 5e-4)
+    got.step(0.2, 0.9, 5e-4)
+    assert rel_frob(to_host(got.params()), _oracle_flat(want, "v")) < 1e-6
+    assert rel_frob(to_host(got.momenta()), _oracle_flat(want, "m")) < TOL_GRAD
+    assert not to_host(got.grads()).any()
+    got.close()
+
+
+def test_fused_train_step_matches_layer_calls(rnn, orc):
+    """rnn_resnet_train_step (eager, then graph) == forward + softmax_ce +
+    backward + step called one by one, bit for bit."""
+    import torch
+    from rustnn_amd.model import ResNet
+    from rustnn_amd.nn import softmax_ce
+    n = 32
+    a, b = ResNet(3, 32, 100, 11), ResNet(3, 32, 100, 11)
+    loss = torch.zeros(1, device="cuda")
+    corr = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for step in range(4):
+        x, labels = _cfg3_inputs(orc, n, seed=50 + step)
+        X = to_dev(x)
+        L = torch.from_numpy(labels.astype(np.int32)).cuda()
+        a.train_step(X, L, 0.1, 0.2, 0.9, 5e-4, loss, corr)
+        lg = b.forward(X, True)
+        lb, cb, dl = softmax_ce(lg, L, 0.1)
+        b.backward(dl)
+        b.step(0.2, 0.9, 5e-4)
+        assert float(to_host(loss)[0]) == float(to_host(lb)[0]), step
+        assert int(to_host(corr)[0]) == int(to_host(cb)[0]), step
+        assert np.array_equal(to_host(a.params()), to_host(b.params())), step
+        assert np.array_equal(to_host(a.momenta()), to_host(b.momenta())), step
+        assert np.array_equal(to_host(a.buffers()), to_host(b.buffers())), step
+    active, why = a.graph_state()
+    assert active, why
+    a.close()
+    b.close()
+
+
+def test_graph_replays_match_eager(rnn, orc):
+    """Graph replays with eager work and synchronisation in between, each
+    checked against an eager network stepping on the same inputs."""
+    import torch
+    from rustnn_amd.model import ResNet
+    n = 64
+    g, e = ResNet(3, 32, 100, 3), ResNet(3, 32, 100, 3)
+    e.set_graph(False)
+    for step in range(5):
+        x, labels = _cfg3_inputs(orc, n, seed=80 + step)
+        X = to_dev(x)
+        L = torch.from_numpy(labels.astype(np.int32)).cuda()
+        g.train_step(X, L, 0.1, 0.2, 0.9, 5e-4)
+        junk = torch.randn(1 << 20, device="cuda")  # unrelated eager work
+        junk.mul_(2.0).sum().item()
+        e.train_step(X, L, 0.1, 0.2, 0.9, 5e-4)
+        torch.cuda.synchronize()
+        assert np.array_equal(to_host(g.params()), to_host(e.params())), step
+        assert np.array_equal(to_host(g.buffers()), to_host(e.buffers())), step
+    assert g.graph_state()[0] and not e.graph_state()[0]
+    g.close()
+    e.close()
+
+
+def test_resnet_gradcheck_gpu(rnn, orc):
+    """check.rs:727-775 through the device ResNet (tolerance 5e-3)."""
+    from oracle import pymodel
+    err = refcheck.resnet_gradcheck(orc, refcheck.GpuNN(pymodel))
+    assert err < refcheck.TOL, err
+
+
+def test_gradcheck_net_matches_oracle(rnn, orc):
+    """The gradcheck network (ResNet(1, 4, 10), batch 8 at 16x16) step by
+    step against the oracle: logits, gradients, updated parameters."""
+    import torch
+    from oracle import pymodel
+    from rustnn_amd.model import ResNet
+    from rustnn_amd.nn import softmax_ce
+    want, got = pymodel.ResNet(1, 4, 10, 1234), ResNet(1, 4, 10, 1234)
+    rng = orc.Rng(99)
+    for step in range(3):
+        x = rng.rand_vec(8 * 3 * 16 * 16).reshape(8, 3, 16, 16)
+        labels = np.array([rng.below(10) for _ in range(8)], np.uint32)
+        lw, _, _ = want.train_step(x, labels, 0.1, 0.2, 0.9, 5e-4)
+        lg = got.forward(to_dev(x), True)
+        loss, _, dl = softmax_ce(lg, torch.from_numpy(labels.astype(np.int32)).cuda(), 0.1)
+        got.backward(dl)
+        got.step(0.2, 0.9, 5e-4)
+        assert abs(float(to_host(loss)[0]) - lw) < 1e-5 * abs(lw), step
+        assert rel_frob(to_host(got.params()), _oracle_flat(want, "v")) < 1e-5, step
+        assert rel_frob(to_host(got.buffers()), np.concatenate(want.buffers())) < 1e-5, step
+    got.close()
