@@ -2,19 +2,29 @@
 """Benchmark of the MI355X GEMM core of rustnn (one GPU).
 
 Metric: "ResNet-20 W32 train images/s; implicit-GEMM conv
-TFLOP/s and % fp32 MFMA peak".  Until the device-resident ResNet-20 step
-exists, the step timed here is BASELINE config 1: the ResNet stage sweep of
-fp32 convolutions at batch 128 -- 3x3 32->32 @32x32 s1, 32->64 @32x32 s2,
-64->64 @16x16, 64->128 @16x16 s2, 128->128 @8x8, and the 1x1 s2 projections
-32->64 @32x32 and 64->128 @16x16 -- each forward + dX + dW.  `value` is the
-whole step's algorithmic conv TFLOP/s (2*cout*cin*k*k*oh*ow*N per pass) with
-every operand resident in HBM.
+TFLOP/s and % fp32 MFMA peak".
 
-Also reported: `roofline` for the dominant kernel (HIP events on the library's
-stream around that op, algorithmic FLOP / average duration vs the 157.3 TFLOP/s
-fp32 MFMA peak) and `cpu_baseline`: the restated reference CPU path (oracle/,
-AVX2 micro-kernel, per-image OpenMP parallelism) on a bounded sample of the
-same sweep, timed on this host's cores.
+Headline (`value`, images/s): BASELINE config 3, the full ResNet-20 (W=32)
+train step at batch 128 on 32x32 synthetic images -- forward, softmax
+cross-entropy (smoothing 0.1), backward and the Nesterov SGD step (lr 0.2,
+momentum 0.9, wd 5e-4) -- through the device-resident runtime (rnn_resnet_*,
+replayed from a hipGraph), every operand resident in HBM.  One "step" is one
+train step on one batch; `value` = steps * 128 / timed seconds.
+
+Also reported:
+  * `roofline`: the kernel with the largest share of the ResNet step, timed
+    on its own with HIP events on the library's stream: its algorithmic FLOP
+    per launch / average launch duration vs the 157.3 TFLOP/s fp32 MFMA peak;
+    `traffic` from the committed rocprofv3 --pmc summary;
+  * `cpu_baseline`: the restated reference CPU path (oracle/, AVX2 micro-kernel,
+    OpenMP) running the same ResNet-20 train step on this host's cores for a
+    bounded number of steps;
+  * `config1_conv_sweep`: BASELINE config 1, the ResNet stage sweep of fp32
+    convolutions at batch 128 (3x3 32->32 @32 s1, 32->64 @32 s2, 64->64 @16,
+    64->128 @16 s2, 128->128 @8, and the 1x1 s2 projections) each forward + dX
+    + dW: algorithmic conv TFLOP/s of the sweep, per-op durations, and the
+    oracle's rate on a sample of it;
+  * `config2_attention` and `gemmbench` (bench.rs:17-24 shapes).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 """
@@ -186,6 +196,97 @@ def bench_gemm(R, ctx, reps):
     return out
 
 
+RESNET = dict(depth_n=3, width=32, nclass=100, batch=128, hw=32, smooth=0.1, lr=0.2, mom=0.9,
+              wd=5e-4, seed=7)
+# Each conv op of the ResNet-20 step with its multiplicity (config-1 sweep
+# names; the stem 3->32 conv runs forward + dW only).
+RESNET_OPS = {"3x3s1_32to32_32": 6, "3x3s2_32to64_32": 1, "3x3s1_64to64_16": 5,
+              "3x3s2_64to128_16": 1, "3x3s1_128to128_8": 5, "1x1s2_32to64_32": 1,
+              "1x1s2_64to128_16": 1}
+CIFAR_MEAN = (0.5071, 0.4865, 0.4409)  # data.rs:13-14
+CIFAR_STD = (0.2673, 0.2564, 0.2762)
+
+
+def resnet_inputs_gpu(n, seed):
+    """Config 3 inputs: images uniform in [0, 1] normalised per channel
+    (data.rs:96-98), labels uniform over 100 classes; drawn on the device."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    u = torch.rand(n, 3, 32, 32, device="cuda", generator=g)
+    mean = torch.tensor(CIFAR_MEAN, device="cuda").view(1, 3, 1, 1)
+    std = torch.tensor(CIFAR_STD, device="cuda").view(1, 3, 1, 1)
+    x = ((u - mean) / std).contiguous()
+    labels = torch.randint(0, 100, (n,), device="cuda", generator=g, dtype=torch.int32)
+    return x, labels
+
+
+def cpu_baseline_resnet(budget_s=12.0):
+    """The oracle's ResNet-20 train step (restated reference CPU path: AVX2
+    micro-kernel convs, f64 BN statistics, OpenMP over images / channels) on
+    config-3 batches of 128, one untimed warm-up step, then steps until the
+    budget is used.  Returns images/s."""
+    import numpy as np
+    from oracle import pyorc as O
+    from oracle import pymodel as M
+    O.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads = max(1, min(threads, 16, os.cpu_count() or 1))
+    c = RESNET
+    rng = O.Rng(2026)
+    n = c["batch"]
+    u = rng.uniform_vec(n * 3 * 32 * 32).reshape(n, 3, 32, 32)
+    x = ((u - np.array(CIFAR_MEAN, np.float32)[None, :, None, None]) /
+         np.array(CIFAR_STD, np.float32)[None, :, None, None]).astype(np.float32)
+    labels = np.array([rng.below(100) for _ in range(n)], np.uint32)
+    net = M.ResNet(c["depth_n"], c["width"], c["nclass"], c["seed"])
+    with O.threads(threads):
+        net.train_step(x, labels, c["smooth"], c["lr"], c["mom"], c["wd"])  # warm-up
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            net.train_step(x, labels, c["smooth"], c["lr"], c["mom"], c["wd"])
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s or el / steps * (steps + 1) > 2.5 * budget_s:
+                break
+    return {"value": round(steps * n / el, 2), "unit": "images/s", "cores": threads,
+            "kind": "port",
+            "sample": f"config-3 ResNet-20 W32 train step (fwd + softmax-CE + bwd + SGD) at batch "
+                      f"{n}, {steps} steps in {el:.1f}s after 1 warm-up step; oracle/ AVX2 "
+                      f"restatement, OpenMP {threads} threads"}
+
+
+def bench_resnet(R, ctx, steps, warmup):
+    """Config 3: the ResNet-20 train step through rnn_resnet_train_step."""
+    import torch
+    from rustnn_amd.model import ResNet
+    c = RESNET
+    net = ResNet(c["depth_n"], c["width"], c["nclass"], c["seed"], ctx=ctx)
+    x, labels = resnet_inputs_gpu(c["batch"], 2026)
+    loss = torch.zeros(1, device="cuda")
+    corr = torch.zeros(1, dtype=torch.int32, device="cuda")
+    step = lambda: net.train_step(x, labels, c["smooth"], c["lr"], c["mom"], c["wd"], loss, corr)
+    for _ in range(max(warmup, 2)):  # the second call records the graph
+        step()
+    torch.cuda.synchronize()
+    assert ctx.stream_ptr() == torch.cuda.current_stream().cuda_stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    graph, why = net.graph_state()
+    flop_img = 3 * net.flops(32, 32)  # bench.rs:142: train = 3 x forward
+    out = {"ms": ms, "images_s": c["batch"] / (ms * 1e-3), "wall": wall, "graph": graph,
+           "graph_note": why, "flop_per_image": flop_img,
+           "loss": float(loss.item()), "params": net.num_params()}
+    net.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -197,6 +298,9 @@ def main():
     ap.add_argument("--ops-only", type=int, default=0, metavar="REPS",
                     help="no timing: run a 256 MiB copy, then each sweep op REPS times in sweep "
                          "order (the workload of the rocprofv3 --pmc passes)")
+    ap.add_argument("--resnet-only", type=int, default=0, metavar="STEPS",
+                    help="no timing: STEPS ResNet-20 train steps (the workload of the "
+                         "rocprofv3 kernel trace of the step)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -208,6 +312,12 @@ def main():
 
     torch.cuda.set_device(0)
     ctx = R.default_ctx(0)
+
+    if args.resnet_only:
+        r = bench_resnet(R, ctx, args.resnet_only, 2)
+        print(json.dumps({"resnet_only": args.resnet_only, "ms": r["ms"]}))
+        return
+
     g = torch.Generator(device="cuda").manual_seed(7)
     layers = []
     for name, cin, cout, k, s, p, h in SWEEP:
@@ -229,7 +339,7 @@ def main():
         else:
             R.conv2d_backward_w(L["sp"], N, L["dy"], L["x"], L["dw"], ctx=ctx)
 
-    def step():
+    def sweep_step():
         for L in layers:
             for ps in PASSES:
                 run_op(L, ps)
@@ -248,24 +358,24 @@ def main():
                           "reps": args.ops_only, "copy_bytes": 2 * src.numel() * 4}))
         return
 
+    # ---- headline: config 3, the ResNet-20 train step
+    rn = bench_resnet(R, ctx, args.steps, args.warmup)
+
+    # ---- config 1: the conv sweep
     for _ in range(args.warmup):
-        step()
+        sweep_step()
     torch.cuda.synchronize()
-    # events are recorded on the current stream, which is the library's stream
-    assert ctx.stream_ptr() == torch.cuda.current_stream().cuda_stream
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
     e0.record()
     for _ in range(args.steps):
-        step()
+        sweep_step()
     e1.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / args.steps
-    step_flops = sum(3 * L["flops"] for L in layers)
-    value = step_flops / (ms * 1e-3) / 1e12
+    sweep_ms = e0.elapsed_time(e1) / args.steps
+    sweep_flops = sum(3 * L["flops"] for L in layers)
+    sweep_tf = sweep_flops / (sweep_ms * 1e-3) / 1e12
 
-    # per-op durations (HIP events around each op, op-reps back-to-back)
+    # per-op durations (HIP events on the library's stream, op-reps back-to-back)
     per_op = []
     for L in layers:
         for ps in PASSES:
@@ -277,34 +387,58 @@ def main():
             b.record()
             torch.cuda.synchronize()
             t = a.elapsed_time(b) / args.op_reps
-            per_op.append(dict(op=f"{L['name']}:{ps}", ms=round(t, 5),
-                               tflops=round(L["flops"] / (t * 1e-3) / 1e12, 2),
-                               frac=round(L["flops"] / (t * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)))
-    dom = max(per_op, key=lambda r: r["ms"])
-    dom_layer = next(L for L in layers if dom["op"].startswith(L["name"] + ":"))
-    achieved = dom_layer["flops"] / (dom["ms"] * 1e-3) / 1e12
-    roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-            "traffic": traffic_from_profiles(dom["op"]), "kernel": dom["op"]}
+            tf = L["flops"] / (t * 1e-3) / 1e12
+            per_op.append(dict(op=f"{L['name']}:{ps}", ms=round(t, 5), tflops=round(tf, 2),
+                               frac=round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
+                               in_resnet_step=RESNET_OPS[L["name"]]))
+
+    def roofline(op_row, flops):
+        achieved = flops / (op_row["ms"] * 1e-3) / 1e12
+        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                "traffic": traffic_from_profiles(op_row["op"]), "kernel": op_row["op"],
+                "flop_per_launch": flops, "avg_launch_ms": op_row["ms"]}
+
+    lay = {L["name"]: L for L in layers}
+    # dominant op of the ResNet step: largest multiplicity x duration
+    dom = max(per_op, key=lambda r: r["ms"] * r["in_resnet_step"])
+    roof = roofline(dom, lay[dom["op"].split(":")[0]]["flops"])
+    roof["share_of_resnet_step"] = round(dom["ms"] * dom["in_resnet_step"] / rn["ms"], 4)
+    sdom = max(per_op, key=lambda r: r["ms"])
+    sweep_roof = roofline(sdom, lay[sdom["op"].split(":")[0]]["flops"])
 
     attention = bench_attention(R, ctx, args.op_reps)
     gemms = bench_gemm(R, ctx, args.op_reps)
 
-    cpu = None
+    cpu = sweep_cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(args.cpu_budget)
+        cpu = cpu_baseline_resnet(args.cpu_budget)
+        sweep_cpu = cpu_baseline(args.cpu_budget / 2)
 
+    c = RESNET
+    model_tf = rn["flop_per_image"] * rn["images_s"] / 1e12
     out = {
-        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "metric": METRIC, "value": round(rn["images_s"], 1), "unit": "images/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": max(args.warmup, 2), "ms_per_step": round(rn["ms"], 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
-        "data": "synthetic (x, dY ~ N(0,1); W Kaiming-normal; seeded on device)",
-        "config": {"workload": "config1 ResNet stage conv sweep, batch 128, fwd+dX+dW "
-                               "(5 3x3 shapes + 2 1x1 s2 projections)",
-                   "batch": N, "flop_per_step": step_flops,
-                   "conv_sweep_frac_of_fp32_mfma_peak": round(value / PEAK_FP32_MFMA_TFLOPS, 4),
-                   "wall_s_timed": round(wall, 3)},
-        "roofline": roof, "cpu_baseline": cpu, "per_op": per_op,
+        "data": "synthetic (images uniform [0,1] normalised with the CIFAR-100 mean/std, "
+                "labels uniform over 100; random Kaiming init; drawn on the device)",
+        "config": {"workload": "config3 ResNet-20 W32 train step: forward + softmax-CE "
+                               "(smooth 0.1) + backward + Nesterov SGD (lr 0.2, mom 0.9, "
+                               "wd 5e-4), batch 128, 32x32x3",
+                   "batch": c["batch"], "depth": 6 * c["depth_n"] + 2, "width": c["width"],
+                   "classes": c["nclass"], "params": rn["params"],
+                   "flop_per_image": rn["flop_per_image"],
+                   "model_tflops": round(model_tf, 3),
+                   "model_frac_of_fp32_mfma_peak": round(model_tf / PEAK_FP32_MFMA_TFLOPS, 4),
+                   "hip_graph": rn["graph"], "wall_s_timed": round(rn["wall"], 3)},
+        "roofline": roof, "cpu_baseline": cpu,
+        "vs_cpu_baseline": round(rn["images_s"] / cpu["value"], 1) if cpu else None,
+        "config1_conv_sweep": {
+            "value": round(sweep_tf, 3), "unit": "TFLOP/s", "ms_per_step": round(sweep_ms, 4),
+            "frac_of_fp32_mfma_peak": round(sweep_tf / PEAK_FP32_MFMA_TFLOPS, 4),
+            "flop_per_step": sweep_flops, "roofline": sweep_roof, "cpu_baseline": sweep_cpu,
+            "per_op": per_op},
         "config2_attention": attention, "gemmbench": gemms,
     }
     print(json.dumps(out))

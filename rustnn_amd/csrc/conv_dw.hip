@@ -500,8 +500,18 @@ const void *dw_pick(int mt, int nb) {
 }  // namespace
 
 // dW += sum over images (see above).  k must be 1 or 3, stride 1 or 2.
-int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
-                float *dw) {
+// Plan of one dW launch: kernel arguments (slab pointer unset), kernel, LDS
+// bytes and the grid (NZ slabs x output-channel blocks x input-channel blocks).
+struct DwLaunch {
+    DwArgs g;
+    const void *kern;
+    size_t lds;
+    dim3 grid;
+    size_t len;  // floats of one slab: cout * cin * k * k
+};
+
+static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                   const float *x, DwLaunch &L) {
     const int K = sp->k;
     if (K != 1 && K != 3) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: k must be 1 or 3");
     if (sp->stride != 1 && sp->stride != 2)
@@ -594,15 +604,45 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
     }
     NZ = std::min(NZ, g.ntiles);
     g.nz = NZ;
-    const size_t ckk = (size_t)g.CI * K * K, len = (size_t)g.CO * ckk;
-    float *ws = (float *)rnn_workspace(ctx, (size_t)NZ * len * sizeof(float));
+    L.g = g;
+    L.kern = kern;
+    L.lds = lds;
+    L.grid = dim3(NZ, ncb, ncib);
+    L.len = (size_t)g.CO * g.CI * K * K;
+    return RNN_OK;
+}
+
+size_t rnn_conv_dw_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n) {
+    DwLaunch L;
+    if (dw_plan(ctx, sp, n, nullptr, nullptr, L) != RNN_OK) return 0;
+    return (size_t)L.g.nz * L.len;
+}
+
+int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                      const float *x, float *slabs, int *nz) {
+    DwLaunch L;
+    int rc = dw_plan(ctx, sp, n, dy, x, L);
+    if (rc) return rc;
+    L.g.part = slabs;
+    void *args[] = {&L.g};
+    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(64 * DW_NW), args, L.lds, ctx->stream));
+    if (nz) *nz = L.g.nz;
+    return RNN_OK;
+}
+
+// dW += over the batch (k = 1 or 3): slabs in the workspace, then one reduce.
+int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
+                float *dw) {
+    DwLaunch L;
+    int rc = dw_plan(ctx, sp, n, dy, x, L);
+    if (rc) return rc;
+    float *ws = (float *)rnn_workspace(ctx, (size_t)L.g.nz * L.len * sizeof(float));
     if (!ws) return RNN_E_NOMEM;
-    g.part = ws;
-    dim3 grid(NZ, ncb, ncib), block(64 * DW_NW);
-    void *args[] = {&g};
-    RNN_HIP(ctx, hipLaunchKernel(kern, grid, block, args, lds, ctx->stream));
-    hipLaunchKernelGGL(slab_reduce_kernel, dim3((unsigned)rnn_div_up(len, 32)), dim3(256), 0,
-                       ctx->stream, ws, NZ, (long long)len, dw);
+    L.g.part = ws;
+    void *args[] = {&L.g};
+    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(64 * DW_NW), args, L.lds, ctx->stream));
+    hipLaunchKernelGGL(slab_reduce_kernel, dim3((unsigned)rnn_div_up(L.len, 32)), dim3(256), 0,
+                       ctx->stream, ws, L.g.nz, (long long)L.len, dw);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

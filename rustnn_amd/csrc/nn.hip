@@ -112,89 +112,110 @@ __global__ __launch_bounds__(RED_THREADS) void bn_stats_part_kernel(
     }
 }
 
-// batch_stats + the per-channel part of run_train (nn.rs:272-320): mean, var
-// (f64, clamped at 0), invstd = 1/sqrt(var + eps), running mean / unbiased
-// running variance.
-__global__ void bn_stats_final_kernel(const double *__restrict__ part, int P, int C, float m,
-                                      float mom, float eps, float *mean, float *invstd, float *rm,
-                                      float *rv) {
-    const int ci = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ci >= C) return;
-    double s = 0.0, s2 = 0.0;
-    for (int p = 0; p < P; p++) {
-        s += part[((size_t)ci * P + p) * 2 + 0];
-        s2 += part[((size_t)ci * P + p) * 2 + 1];
-    }
-    const double mu = s / (double)m;
-    const double va = s2 / (double)m - mu * mu;
-    const float meanf = (float)mu, varf = (float)(va > 0.0 ? va : 0.0);
-    const float is = 1.0f / sqrtf(varf + eps);
-    mean[ci] = meanf;
-    invstd[ci] = is;
-    if (rm) {
-        rm[ci] = (1.0f - mom) * rm[ci] + mom * meanf;
-        const float den = fmaxf(m - 1.0f, 1.0f);
-        const float unb = varf * m / den;
-        rv[ci] = (1.0f - mom) * rv[ci] + mom * unb;
-    }
-}
-
-// run_eval (nn.rs:350-365): per-channel scale and shift.
-__global__ void bn_eval_prep_kernel(const float *__restrict__ gamma, const float *__restrict__ beta,
-                                    const float *__restrict__ rm, const float *__restrict__ rv,
-                                    float eps, int C, float *sc, float *sh) {
-    const int ci = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ci >= C) return;
-    const float is = 1.0f / sqrtf(rv[ci] + eps);
-    sc[ci] = gamma[ci] * is;
-    sh[ci] = beta[ci] - gamma[ci] * is * rm[ci];
-}
-
-// Per-channel normalisation of one element.  Train (run_train, nn.rs:336-342):
-// g * ((x - mean) * invstd) + b.  Eval (run_eval): sc * x + sh, with sc / sh
-// passed in the mean / invstd slots.
+// Channel coefficients, computed by every thread of a block (uniform loads).
+// Train: mean and invstd from the partial sums added in range order -- the
+// same values in every block of the channel (batch_stats + run_train,
+// nn.rs:272-320: f64 mean and variance clamped at 0, invstd =
+// 1/sqrt(var + eps)); thread 0 of the channel's first block also stores them
+// and updates the running mean / unbiased running variance.  Eval: the scale
+// and shift of run_eval (nn.rs:350-365).
 template <bool EVAL>
-struct BnCoef {
-    const float *a, *b, *g, *be;
-    __device__ __forceinline__ float apply(int ci, float x) const {
+__device__ __forceinline__ void bn_channel(const RnnBn &s, int ci, bool first, float &a,
+                                           float &b) {
+    if constexpr (EVAL) {
+        const float is = 1.0f / sqrtf(s.rv[ci] + s.eps);
+        a = s.gamma[ci] * is;
+        b = s.beta[ci] - s.gamma[ci] * is * s.rm[ci];
+    } else {
+        double sx = 0.0, sx2 = 0.0;
+        for (int p = 0; p < s.P; p++) {
+            sx += s.part[((size_t)ci * s.P + p) * 2 + 0];
+            sx2 += s.part[((size_t)ci * s.P + p) * 2 + 1];
+        }
+        const double mu = sx / (double)s.m;
+        const double va = sx2 / (double)s.m - mu * mu;
+        const float meanf = (float)mu, varf = (float)(va > 0.0 ? va : 0.0);
+        const float is = 1.0f / sqrtf(varf + s.eps);
+        a = meanf;
+        b = is;
+        if (first && threadIdx.x == 0) {
+            s.mean[ci] = meanf;
+            s.invstd[ci] = is;
+            if (s.rm) {
+                s.rm[ci] = (1.0f - s.mom) * s.rm[ci] + s.mom * meanf;
+                const float den = fmaxf(s.m - 1.0f, 1.0f);
+                const float unb = varf * s.m / den;
+                s.rv[ci] = (1.0f - s.mom) * s.rv[ci] + s.mom * unb;
+            }
+        }
+    }
+}
+
+// Normalisation of one element with the channel coefficients (a, b): train
+// (run_train, nn.rs:336-342) g * ((x - mean) * invstd) + beta; eval
+// (run_eval) sc * x + sh.
+template <bool EVAL>
+struct BnFn {
+    float a, b, g, be;
+    __device__ __forceinline__ float operator()(float x) const {
         if constexpr (EVAL) {
-            return a[ci] * x + b[ci];
+            return a * x + b;
         } else {
-            const float h = (x - a[ci]) * b[ci];
-            return g[ci] * h + be[ci];
+            const float h = (x - a) * b;
+            return g * h + be;
         }
     }
 };
 
-// out = [relu]( bn(x) [+ skip | + bn'(skip)] ), elementwise over [n][C][hw].
-// SKIP 0: none; 1: add the tensor `skip` (identity shortcut); 2: add
-// bn'(skip) (projection shortcut).  The residual add and the ReLU follow
-// add_relu_ (nn.rs:446-450): max(y + s, 0).
+template <bool EVAL>
+__device__ __forceinline__ BnFn<EVAL> bn_fn(const RnnBn &s, int ci, bool first) {
+    BnFn<EVAL> f;
+    bn_channel<EVAL>(s, ci, first, f.a, f.b);
+    f.g = EVAL ? 0.0f : s.gamma[ci];
+    f.be = EVAL ? 0.0f : s.beta[ci];
+    return f;
+}
+
+// out = [relu]( bn(x) [+ skip | + bn'(skip)] ) over channel blockIdx.x of
+// images [p*G, p*G + G), p = blockIdx.y.  SKIP 0: none; 1: add the tensor
+// `skip` (identity shortcut); 2: add bn'(skip) (projection shortcut).  The
+// residual add and the ReLU follow add_relu_ (nn.rs:446-450): max(y + s, 0).
 template <bool EVAL, bool RELU, int SKIP>
-__global__ __launch_bounds__(EW_THREADS) void bn_apply_kernel(
-    const float *x, BnCoef<EVAL> bn, const float *skip, BnCoef<EVAL> sbn, float *out,
-    size_t total4, FastDiv fd_hw4, FastDiv fd_c) {
-    for (size_t q = (size_t)blockIdx.x * EW_THREADS + threadIdx.x; q < total4;
-         q += (size_t)gridDim.x * EW_THREADS) {
-        const uint32_t plane = div_by((uint32_t)q, fd_hw4);
-        const int ci = (int)(plane - div_by(plane, fd_c) * fd_c.d);
-        float4 v = reinterpret_cast<const float4 *>(x)[q];
-        float r[4] = {bn.apply(ci, v.x), bn.apply(ci, v.y), bn.apply(ci, v.z), bn.apply(ci, v.w)};
-        if constexpr (SKIP != 0) {
-            const float4 s = reinterpret_cast<const float4 *>(skip)[q];
-            float t[4] = {s.x, s.y, s.z, s.w};
-            if constexpr (SKIP == 2) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) t[j] = sbn.apply(ci, t[j]);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) r[j] = r[j] + t[j];
+__global__ __launch_bounds__(EW_THREADS) void bn_apply_kernel(const float *x, RnnBn bn,
+                                                              const float *skip, RnnBn sbn,
+                                                              float *out, int n, int C, int hw,
+                                                              int G, FastDiv fd_hw4, int vec) {
+    const int ci = blockIdx.x, p = blockIdx.y;
+    const bool first = p == 0;
+    const BnFn<EVAL> f = bn_fn<EVAL>(bn, ci, first);
+    BnFn<EVAL> fs{};
+    if constexpr (SKIP == 2) fs = bn_fn<EVAL>(sbn, ci, first);
+    const int i0 = p * G, i1 = min(n, i0 + G);
+    auto one = [&](float v, float sv) {
+        float r = f(v);
+        if constexpr (SKIP == 1) r = r + sv;
+        if constexpr (SKIP == 2) r = r + fs(sv);
+        if constexpr (RELU) r = r > 0.0f ? r : 0.0f;
+        return r;
+    };
+    if (vec) {
+        const int hw4 = hw >> 2, tot = (i1 - i0) * hw4;
+        for (int e = threadIdx.x; e < tot; e += EW_THREADS) {
+            const int img = (int)div_by((uint32_t)e, fd_hw4), r = e - img * hw4;
+            const size_t q = ((size_t)(i0 + img) * C + ci) * hw4 + r;
+            const float4 v = reinterpret_cast<const float4 *>(x)[q];
+            float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (SKIP != 0) sv = reinterpret_cast<const float4 *>(skip)[q];
+            reinterpret_cast<float4 *>(out)[q] =
+                make_float4(one(v.x, sv.x), one(v.y, sv.y), one(v.z, sv.z), one(v.w, sv.w));
         }
-        if constexpr (RELU) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) r[j] = r[j] > 0.0f ? r[j] : 0.0f;
+    } else {
+        const int tot = (i1 - i0) * hw;
+        for (int e = threadIdx.x; e < tot; e += EW_THREADS) {
+            const int img = e / hw, r = e - img * hw;
+            const size_t i = ((size_t)(i0 + img) * C + ci) * hw + r;
+            out[i] = one(x[i], SKIP != 0 ? skip[i] : 0.0f);
         }
-        reinterpret_cast<float4 *>(out)[q] = make_float4(r[0], r[1], r[2], r[3]);
     }
 }
 
@@ -256,88 +277,56 @@ __global__ __launch_bounds__(RED_THREADS) void bn_bwd_part_kernel(
     }
 }
 
-// dgamma / dbeta of BatchNorm2d::backward: g.g += dgamma, b.g += dbeta
-// (nn.rs:423-424); the values are kept in dgdb[2*C] for the dx pass.
-__global__ void bn_bwd_final_kernel(const double *__restrict__ part, int P, int C, float *dgamma,
-                                    float *dbeta, float *dgdb) {
-    const int ci = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ci >= C) return;
-    double a = 0.0, b = 0.0;
-    for (int p = 0; p < P; p++) {
-        a += part[((size_t)ci * P + p) * 2 + 0];
-        b += part[((size_t)ci * P + p) * 2 + 1];
-    }
-    const float dg = (float)a, db = (float)b;
-    dgdb[ci] = dg;
-    dgdb[C + ci] = db;
-    if (dgamma) dgamma[ci] += dg;
-    if (dbeta) dbeta[ci] += db;
-}
-
-// dx = s * (m*dy - dbeta - xhat*dgamma), s = gamma*invstd/m (nn.rs:406-421).
+// dx = s * (m*dy - dbeta - xhat*dgamma), s = gamma*invstd/m (nn.rs:406-421),
+// over channel blockIdx.x of images [p*G, p*G + G).  dgamma / dbeta are the
+// partial sums added in range order (the same in every block); thread 0 of
+// the channel's first block adds them into g.g / b.g (nn.rs:423-424).
 template <bool MASK>
 __global__ __launch_bounds__(EW_THREADS) void bn_bwd_apply_kernel(
     const float *__restrict__ d, const float *__restrict__ mask, const float *__restrict__ x,
-    const float *__restrict__ mean, const float *__restrict__ invstd,
-    const float *__restrict__ gamma, const float *__restrict__ dgdb, float m, float *dx,
-    size_t total4, FastDiv fd_hw4, FastDiv fd_c) {
-    const int C = (int)fd_c.d;
-    for (size_t q = (size_t)blockIdx.x * EW_THREADS + threadIdx.x; q < total4;
-         q += (size_t)gridDim.x * EW_THREADS) {
-        const uint32_t plane = div_by((uint32_t)q, fd_hw4);
-        const int ci = (int)(plane - div_by(plane, fd_c) * fd_c.d);
-        const float mu = mean[ci], is = invstd[ci];
-        const float s = gamma[ci] * is / m;
-        const float dg = dgdb[ci], db = dgdb[C + ci];
-        const float4 dv = reinterpret_cast<const float4 *>(d)[q];
-        const float4 xv = reinterpret_cast<const float4 *>(x)[q];
-        float4 mv = make_float4(1.f, 1.f, 1.f, 1.f);
-        if constexpr (MASK) mv = reinterpret_cast<const float4 *>(mask)[q];
-        const float dd[4] = {dv.x, dv.y, dv.z, dv.w}, xx[4] = {xv.x, xv.y, xv.z, xv.w};
-        const float mm[4] = {mv.x, mv.y, mv.z, mv.w};
-        float r[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float g = (MASK && mm[j] <= 0.0f) ? 0.0f : dd[j];
-            const float xh = (xx[j] - mu) * is;
-            r[j] = s * (m * g - db - xh * dg);
+    RnnBn bn, const double *__restrict__ part, float *dx, int n, int C, int hw, int G,
+    FastDiv fd_hw4, int vec) {
+    const int ci = blockIdx.x, p = blockIdx.y, P = gridDim.y;
+    double sa = 0.0, sb = 0.0;
+    for (int k = 0; k < P; k++) {
+        sa += part[((size_t)ci * P + k) * 2 + 0];
+        sb += part[((size_t)ci * P + k) * 2 + 1];
+    }
+    const float dg = (float)sa, db = (float)sb;
+    if (p == 0 && threadIdx.x == 0) {
+        if (bn.dgamma) bn.dgamma[ci] += dg;
+        if (bn.dbeta) bn.dbeta[ci] += db;
+    }
+    const float mu = bn.mean[ci], is = bn.invstd[ci], m = bn.m;
+    const float s = bn.gamma[ci] * is / m;
+    auto one = [&](float g, float xv) {
+        const float xh = (xv - mu) * is;
+        return s * (m * g - db - xh * dg);
+    };
+    const int i0 = p * G, i1 = min(n, i0 + G);
+    if (vec) {
+        const int hw4 = hw >> 2, tot = (i1 - i0) * hw4;
+        for (int e = threadIdx.x; e < tot; e += EW_THREADS) {
+            const int img = (int)div_by((uint32_t)e, fd_hw4), r = e - img * hw4;
+            const size_t q = ((size_t)(i0 + img) * C + ci) * hw4 + r;
+            const float4 dv = reinterpret_cast<const float4 *>(d)[q];
+            const float4 xv = reinterpret_cast<const float4 *>(x)[q];
+            float4 mv = make_float4(1.f, 1.f, 1.f, 1.f);
+            if constexpr (MASK) mv = reinterpret_cast<const float4 *>(mask)[q];
+            const float g0 = (MASK && mv.x <= 0.0f) ? 0.0f : dv.x;
+            const float g1 = (MASK && mv.y <= 0.0f) ? 0.0f : dv.y;
+            const float g2 = (MASK && mv.z <= 0.0f) ? 0.0f : dv.z;
+            const float g3 = (MASK && mv.w <= 0.0f) ? 0.0f : dv.w;
+            reinterpret_cast<float4 *>(dx)[q] =
+                make_float4(one(g0, xv.x), one(g1, xv.y), one(g2, xv.z), one(g3, xv.w));
         }
-        reinterpret_cast<float4 *>(dx)[q] = make_float4(r[0], r[1], r[2], r[3]);
-    }
-}
-
-// Scalar-tail variants of the elementwise kernels (hw not a multiple of 4).
-template <bool MASK>
-__global__ void bn_bwd_apply_scalar_kernel(const float *__restrict__ d,
-                                           const float *__restrict__ mask,
-                                           const float *__restrict__ x,
-                                           const float *__restrict__ mean,
-                                           const float *__restrict__ invstd,
-                                           const float *__restrict__ gamma,
-                                           const float *__restrict__ dgdb, float m, float *dx,
-                                           size_t total, int hw, int C) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const int ci = (int)((i / hw) % C);
-        const float mu = mean[ci], is = invstd[ci];
-        const float s = gamma[ci] * is / m;
-        const float g = masked<MASK>(d[i], mask, i);
-        const float xh = (x[i] - mu) * is;
-        dx[i] = s * (m * g - dgdb[C + ci] - xh * dgdb[ci]);
-    }
-}
-
-template <bool EVAL, bool RELU, int SKIP>
-__global__ void bn_apply_scalar_kernel(const float *x, BnCoef<EVAL> bn, const float *skip,
-                                       BnCoef<EVAL> sbn, float *out, size_t total, int hw, int C) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const int ci = (int)((i / hw) % C);
-        float r = bn.apply(ci, x[i]);
-        if constexpr (SKIP == 1) r = r + skip[i];
-        if constexpr (SKIP == 2) r = r + sbn.apply(ci, skip[i]);
-        if constexpr (RELU) r = r > 0.0f ? r : 0.0f;
-        out[i] = r;
+    } else {
+        const int tot = (i1 - i0) * hw;
+        for (int e = threadIdx.x; e < tot; e += EW_THREADS) {
+            const int img = e / hw, r = e - img * hw;
+            const size_t i = ((size_t)(i0 + img) * C + ci) * hw + r;
+            dx[i] = one(masked<MASK>(d[i], mask, i), x[i]);
+        }
     }
 }
 
@@ -360,6 +349,38 @@ __global__ __launch_bounds__(EW_THREADS) void add_kernel(float *a, const float *
             reinterpret_cast<float4 *>(a)[i] = av;
         } else {
             for (size_t j = 4 * i; j < total; j++) a[j] = a[j] + masked<MASK>(b[j], mask, j);
+        }
+    }
+}
+
+// a = a + b, then 0 where mask <= 0 (add_ then relu_back_, nn.rs:432-443).
+template <bool ADD, bool MASK>
+__global__ __launch_bounds__(EW_THREADS) void add_mask_kernel(float *a,
+                                                              const float *__restrict__ b,
+                                                              const float *__restrict__ mask,
+                                                              size_t total, int vec) {
+    for (size_t i = (size_t)blockIdx.x * EW_THREADS + threadIdx.x; 4 * i < total;
+         i += (size_t)gridDim.x * EW_THREADS) {
+        if (vec && 4 * i + 4 <= total) {
+            float4 av = reinterpret_cast<float4 *>(a)[i];
+            float4 bv = make_float4(0.f, 0.f, 0.f, 0.f), mv = make_float4(1.f, 1.f, 1.f, 1.f);
+            if constexpr (ADD) bv = reinterpret_cast<const float4 *>(b)[i];
+            if constexpr (MASK) mv = reinterpret_cast<const float4 *>(mask)[i];
+            float r[4] = {av.x, av.y, av.z, av.w};
+            const float bb[4] = {bv.x, bv.y, bv.z, bv.w}, mm[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if constexpr (ADD) r[j] = r[j] + bb[j];
+                if constexpr (MASK) r[j] = mm[j] <= 0.0f ? 0.0f : r[j];
+            }
+            reinterpret_cast<float4 *>(a)[i] = make_float4(r[0], r[1], r[2], r[3]);
+        } else {
+            for (size_t j = 4 * i; j < total && j < 4 * i + 4; j++) {
+                float r = a[j];
+                if constexpr (ADD) r = r + b[j];
+                if constexpr (MASK) r = mask[j] <= 0.0f ? 0.0f : r;
+                a[j] = r;
+            }
         }
     }
 }
@@ -401,14 +422,19 @@ __global__ void gap_fwd_kernel(const float *__restrict__ x, int hw, size_t nc, i
 }
 
 // gap_backward (nn.rs:465-473).
-__global__ void gap_bwd_kernel(const float *__restrict__ dy, int hw, size_t total, float *dx) {
+__global__ void gap_bwd_kernel(const float *__restrict__ dy, int hw, size_t total,
+                               const float *__restrict__ mask, float *dx) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x)
-        dx[i] = dy[i / hw] / (float)hw;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const float v = dy[i / hw] / (float)hw;
+        dx[i] = (mask && mask[i] <= 0.0f) ? 0.0f : v;
+    }
 }
 
 // nn.rs Linear::forward (nn.rs:500-517): y[i][o] = b[o] + w[o][0]*x[i][0] +
-// ... in j order, one thread per output (bit-identical to the reference).
+// ... in j order, one thread per output (bit-identical to the reference);
+// VEC reads the rows as float4 (the adds stay in j order).
+template <bool VEC>
 __global__ void fc_fwd_kernel(const float *__restrict__ x, const float *__restrict__ w,
                               const float *__restrict__ b, int rows, int fin, int fout, float *y) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
@@ -416,99 +442,181 @@ __global__ void fc_fwd_kernel(const float *__restrict__ x, const float *__restri
     const int i = t / fout, o = t - i * fout;
     const float *wr = w + (size_t)o * fin, *xr = x + (size_t)i * fin;
     float s = b[o];
-    for (int j = 0; j < fin; j++) s = s + wr[j] * xr[j];
+    if constexpr (VEC) {
+        for (int j = 0; j < fin; j += 4) {
+            const float4 wv = *reinterpret_cast<const float4 *>(wr + j);
+            const float4 xv = *reinterpret_cast<const float4 *>(xr + j);
+            s = s + wv.x * xv.x;
+            s = s + wv.y * xv.y;
+            s = s + wv.z * xv.z;
+            s = s + wv.w * xv.w;
+        }
+    } else {
+        for (int j = 0; j < fin; j++) s = s + wr[j] * xr[j];
+    }
     y[t] = s;
 }
 
 // Linear::backward_w (nn.rs:521-537): w.g[o][j] += dy[i][o]*x[i][j] in row
-// order, zero gradients skipped; thread (o, j).  Threads with j == fin do the
-// bias: b.g[o] += dy[i][o].
-__global__ void fc_bwd_w_kernel(const float *__restrict__ dy, const float *__restrict__ x, int rows,
-                                int fin, int fout, float *dw, float *db) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    const int fin1 = fin + 1;
-    if (t >= fout * fin1) return;
-    const int o = t / fin1, j = t - o * fin1;
-    if (j == fin) {
-        float acc = db[o];
-        for (int i = 0; i < rows; i++) {
-            const float g = dy[(size_t)i * fout + o];
-            if (g != 0.0f) acc = acc + g;
+// order, zero gradients skipped.  Block o; thread j (coalesced over x rows);
+// thread j == fin adds the bias: b.g[o] += dy[i][o].
+__global__ __launch_bounds__(256) void fc_bwd_w_kernel(const float *__restrict__ dy,
+                                                       const float *__restrict__ x, int rows,
+                                                       int fin, int fout, float *dw, float *db) {
+    constexpr int U = 8;  // loads of U rows go out before their in-order adds
+    const int o = blockIdx.x;
+    for (int j = threadIdx.x; j <= fin; j += blockDim.x) {
+        const bool bias = j == fin;
+        float acc = bias ? db[o] : dw[(size_t)o * fin + j];
+        int i = 0;
+        for (; i + U <= rows; i += U) {
+            float g[U], xv[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                g[u] = dy[(size_t)(i + u) * fout + o];
+                xv[u] = bias ? 1.0f : x[(size_t)(i + u) * fin + j];
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (g[u] != 0.0f) acc = bias ? acc + g[u] : acc + g[u] * xv[u];
         }
-        db[o] = acc;
-        return;
+        for (; i < rows; i++) {
+            const float g = dy[(size_t)i * fout + o];
+            if (g != 0.0f) acc = bias ? acc + g : acc + g * x[(size_t)i * fin + j];
+        }
+        if (bias)
+            db[o] = acc;
+        else
+            dw[(size_t)o * fin + j] = acc;
     }
-    float acc = dw[(size_t)o * fin + j];
-    for (int i = 0; i < rows; i++) {
-        const float g = dy[(size_t)i * fout + o];
-        if (g != 0.0f) acc = acc + g * x[(size_t)i * fin + j];
-    }
-    dw[(size_t)o * fin + j] = acc;
 }
 
 // Linear::backward_x (nn.rs:539-556): dx[i][j] = sum over o (in order, zero
-// gradients skipped) of dy[i][o]*w[o][j], from 0.
-__global__ void fc_bwd_x_kernel(const float *__restrict__ dy, const float *__restrict__ w, int rows,
-                                int fin, int fout, float *dx) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= rows * fin) return;
-    const int i = t / fin, j = t - i * fin;
-    float acc = 0.0f;
-    for (int o = 0; o < fout; o++) {
-        const float g = dy[(size_t)i * fout + o];
-        if (g != 0.0f) acc = acc + g * w[(size_t)o * fin + j];
+// gradients skipped) of dy[i][o]*w[o][j], from 0.  Block i; thread j.
+__global__ __launch_bounds__(256) void fc_bwd_x_kernel(const float *__restrict__ dy,
+                                                       const float *__restrict__ w, int rows,
+                                                       int fin, int fout, float *dx) {
+    constexpr int U = 8;
+    const int i = blockIdx.x;
+    for (int j = threadIdx.x; j < fin; j += blockDim.x) {
+        float acc = 0.0f;
+        int o = 0;
+        for (; o + U <= fout; o += U) {
+            float g[U], wv[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                g[u] = dy[(size_t)i * fout + o + u];
+                wv[u] = w[(size_t)(o + u) * fin + j];
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (g[u] != 0.0f) acc = acc + g[u] * wv[u];
+        }
+        for (; o < fout; o++) {
+            const float g = dy[(size_t)i * fout + o];
+            if (g != 0.0f) acc = acc + g * w[(size_t)o * fin + j];
+        }
+        dx[(size_t)i * fin + j] = acc;
     }
-    dx[t] = acc;
 }
 
-// softmax_ce (nn.rs:566-637).  Thread r handles rows r, r + blockDim, ...;
-// thread 0 then adds the row losses and hits in row order.  `smooth` comes
+// Max and its first index over a wave (ties keep the lower index, as the
+// reference's strict > scan does).
+__device__ __forceinline__ void wave_argmax(float &m, int &idx) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float m2 = __shfl_xor(m, o, 64);
+        const int i2 = __shfl_xor(idx, o, 64);
+        if (m2 > m || (m2 == m && i2 < idx)) {
+            m = m2;
+            idx = i2;
+        }
+    }
+}
+
+__device__ __forceinline__ float wave_sumf(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// softmax_ce (nn.rs:566-637).  One wave per row (rows wave, wave + NW, ...):
+// max / first argmax, sum of exp(z - max), lse, the smoothed loss and the
+// gradient (softmax - target) / rows; the wave sums run in a tree order.
+// Thread 0 then adds the row losses and hits in row order.  `smooth` comes
 // from device memory when `scal` is set (scal[3]), else from the argument.
-__global__ void softmax_ce_kernel(const float *__restrict__ logits,
-                                  const uint32_t *__restrict__ labels, int rows, int nclass,
-                                  float smooth_arg, const float *scal, float *dl, float *loss_out,
-                                  uint32_t *correct_out) {
+template <int ZR>
+__global__ __launch_bounds__(1024) void softmax_ce_kernel(
+    const float *__restrict__ logits, const uint32_t *__restrict__ labels, int rows, int nclass,
+    float smooth_arg, const float *scal, float *dl, float *loss_out, uint32_t *correct_out) {
     extern __shared__ float row_loss[];  // [rows] losses, then [rows] hits
     const float smooth = scal ? scal[3] : smooth_arg;
     const float inv = 1.0f / (float)rows;
-    for (int r = threadIdx.x; r < rows; r += blockDim.x) {
+    const float on = 1.0f - smooth, off = smooth / (float)nclass;
+    const int wave = wave_index(), lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    for (int r = wave; r < rows; r += nw) {
         const float *z = logits + (size_t)r * nclass;
         float *d = dl + (size_t)r * nclass;
         const uint32_t yl = labels[r];
+        // the row, ZR values per lane (class lane + 64*k), loaded once
+        float zv[ZR];
+#pragma unroll
+        for (int k = 0; k < ZR; k++) {
+            const int j = lane + 64 * k;
+            zv[k] = j < nclass ? z[j] : -INFINITY;
+        }
         if (yl >= (uint32_t)nclass) {  // the reference panics on such a label
-            for (int j = 0; j < nclass; j++) d[j] = NAN;
-            row_loss[r] = NAN;
-            row_loss[rows + r] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < ZR; k++)
+                if (lane + 64 * k < nclass) d[lane + 64 * k] = NAN;
+            if (lane == 0) {
+                row_loss[r] = NAN;
+                row_loss[rows + r] = 0.0f;
+            }
             continue;
         }
         const int y = (int)yl;
         float mx = -INFINITY;
-        int arg = 0;
-        for (int j = 0; j < nclass; j++)
-            if (z[j] > mx) {
-                mx = z[j];
-                arg = j;
+        int arg = 0x7fffffff;
+#pragma unroll
+        for (int k = 0; k < ZR; k++)
+            if (zv[k] > mx) {
+                mx = zv[k];
+                arg = lane + 64 * k;
             }
-        float sum = 0.0f;
-        for (int j = 0; j < nclass; j++) {
-            const float e = expf(z[j] - mx);
-            d[j] = e;
-            sum = sum + e;
+        wave_argmax(mx, arg);
+        float e[ZR], sum = 0.0f, zs = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ZR; k++) {
+            const bool in = lane + 64 * k < nclass;
+            e[k] = in ? expf(zv[k] - mx) : 0.0f;
+            sum += e[k];
+            zs += in ? zv[k] : 0.0f;
         }
+        sum = wave_sumf(sum);
+        zs = wave_sumf(zs);
         const float lse = mx + logf(sum);
-        const float on = 1.0f - smooth, off = smooth / (float)nclass;
-        float l = on * (lse - z[y]);
-        if (smooth > 0.0f) {
-            float s = 0.0f;
-            for (int j = 0; j < nclass; j++) s = s + (lse - z[j]);
-            l = l + off * s;
+#pragma unroll
+        for (int k = 0; k < ZR; k++) {
+            const int j = lane + 64 * k;
+            if (j < nclass) {
+                const float t = j == y ? on + off : off;
+                d[j] = (e[k] / sum - t) * inv;
+            }
         }
-        for (int j = 0; j < nclass; j++) {
-            const float t = j == y ? on + off : off;
-            d[j] = (d[j] / sum - t) * inv;
+        // z[y] from the lane that holds it
+        float zy = 0.0f;
+#pragma unroll
+        for (int k = 0; k < ZR; k++)
+            if (lane + 64 * k == y) zy = zv[k];
+        zy = wave_sumf(zy);
+        if (lane == 0) {
+            float l = on * (lse - zy);
+            // sum_j (lse - z_j) = nclass*lse - sum_j z_j
+            if (smooth > 0.0f) l = l + off * ((float)nclass * lse - zs);
+            row_loss[r] = l;
+            row_loss[rows + r] = arg == y ? 1.0f : 0.0f;
         }
-        row_loss[r] = l;
-        row_loss[rows + r] = arg == y ? 1.0f : 0.0f;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -542,6 +650,68 @@ __global__ __launch_bounds__(EW_THREADS) void sgd_kernel(float *v, float *g, flo
     }
 }
 
+// Gradient finalisation over a flat parameter layout: block b belongs to the
+// segment with the last blk0 <= b and takes its 32 elements [32*(b - blk0),
+// +32).  Slab sums follow the dW reduction exactly (8 thread groups each sum
+// a contiguous run of slabs with 16 loads in flight, then the 8 partials in
+// order), so g ends as it would after a separate reduce; the SGD step is
+// Param::step (nn.rs:102-110) on that g.
+__global__ __launch_bounds__(256) void grad_finalize_kernel(const GradSeg *__restrict__ segs,
+                                                            int nseg, float *v, float *g,
+                                                            float *m, const float *scal,
+                                                            int do_sgd) {
+    constexpr int PARTS = 8;
+    __shared__ float red[PARTS][32];
+    int lo = 0, hi = nseg - 1;
+    while (lo < hi) {  // last segment with blk0 <= blockIdx.x
+        const int mid = (lo + hi + 1) >> 1;
+        if (segs[mid].blk0 <= (long long)blockIdx.x)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const GradSeg sg = segs[lo];
+    const int el = threadIdx.x & 31, j = threadIdx.x >> 5;
+    const long long e = ((long long)blockIdx.x - sg.blk0) * 32 + el;
+    const bool in = e < sg.len;
+    if (sg.nz > 0) {
+        const int G = (sg.nz + PARTS - 1) / PARTS;
+        const int z0 = j * G, z1 = min(sg.nz, z0 + G);
+        float s = 0.f;
+        if (in) {
+            for (int b = z0; b < z1; b += 16) {
+                float t[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    t[u] = b + u < z1 ? sg.slabs[(long long)(b + u) * sg.len + e] : 0.f;
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if (b + u < z1) s = (b + u == z0) ? t[u] : s + t[u];
+            }
+        }
+        red[j][el] = s;
+    }
+    __syncthreads();
+    if (j != 0 || !in) return;
+    const long long i = sg.off + e;
+    float gi = g[i];
+    if (sg.nz > 0) {
+        float t = red[0][el];
+        for (int q = 1; q < PARTS && q * ((sg.nz + PARTS - 1) / PARTS) < sg.nz; q++) t += red[q][el];
+        gi += t;
+    }
+    if (!do_sgd) {
+        g[i] = gi;
+        return;
+    }
+    const float lr = scal[0], mom = scal[1], wd = sg.decay ? scal[2] : 0.0f;
+    const float gg = gi + wd * v[i];
+    const float mi = mom * m[i] + gg;
+    m[i] = mi;
+    v[i] = v[i] - lr * (gg + mom * mi);
+    g[i] = 0.0f;
+}
+
 __global__ void set_scalars_kernel(float *scal, float a, float b, float c, float d) {
     scal[0] = a;
     scal[1] = b;
@@ -573,106 +743,88 @@ size_t rnn_bn_scratch_doubles(size_t n, size_t c) {
     return 2 * c * (size_t)s.P;
 }
 
-int rnn_bn_stats_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, double *part,
-                        float *mean, float *invstd, float *rm, float *rv, float mom, float eps) {
+int rnn_bn_stats_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x,
+                        double *part) {
     ChanSplit s = chan_split(n, c);
     bn_stats_part_kernel<<<dim3((unsigned)c, (unsigned)s.P), RED_THREADS, 0, ctx->stream>>>(
         x, (int)n, (int)c, (int)hw, aligned16(x), s.G, divider(hw / 4, (size_t)s.G * (hw / 4)),
         part);
     RNN_LAUNCHED(ctx);
-    bn_stats_final_kernel<<<(unsigned)rnn_div_up(c, 64), 64, 0, ctx->stream>>>(
-        part, s.P, (int)c, (float)(n * hw), mom, eps, mean, invstd, rm, rv);
-    RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
 
 template <bool EVAL, bool RELU, int SKIP>
-static int bn_apply_t(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x,
-                      BnCoef<EVAL> bn, const float *skip, BnCoef<EVAL> sbn, float *out) {
-    const size_t total = n * c * hw;
-    if (total == 0) return RNN_OK;
-    if ((hw & 3) == 0 && total / 4 < (1ull << 31) && aligned16(x) && aligned16(out) &&
-        (SKIP == 0 || aligned16(skip))) {
-        const size_t t4 = total / 4;
-        bn_apply_kernel<EVAL, RELU, SKIP><<<ew_grid(ctx, t4), EW_THREADS, 0, ctx->stream>>>(
-            x, bn, skip, sbn, out, t4, divider(hw / 4, t4), divider(c, n * c));
+static void bn_apply_t(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x,
+                       const RnnBn &bn, const float *skip, const RnnBn &sbn, float *out) {
+    ChanSplit s = chan_split(n, c);
+    const int vec = (hw & 3) == 0 && aligned16(x) && aligned16(out) &&
+                    (SKIP == 0 || aligned16(skip));
+    bn_apply_kernel<EVAL, RELU, SKIP><<<dim3((unsigned)c, (unsigned)s.P), EW_THREADS, 0,
+                                        ctx->stream>>>(
+        x, bn, skip, sbn, out, (int)n, (int)c, (int)hw, s.G,
+        divider(hw / 4, (size_t)s.G * (hw / 4)), vec);
+}
+
+int rnn_bn_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, RnnBn bn,
+                        bool eval, int relu, int skip_mode, const float *skip, const RnnBn *sbn,
+                        float *out) {
+    if (n * c * hw == 0) return RNN_OK;
+    ChanSplit s = chan_split(n, c);
+    bn.P = s.P;
+    bn.m = (float)(n * hw);
+    RnnBn sb = sbn ? *sbn : bn;
+    sb.P = s.P;
+    sb.m = bn.m;
+    if (eval) {
+        if (skip_mode == 0) {
+            if (relu)
+                bn_apply_t<true, true, 0>(ctx, n, c, hw, x, bn, skip, sb, out);
+            else
+                bn_apply_t<true, false, 0>(ctx, n, c, hw, x, bn, skip, sb, out);
+        } else if (skip_mode == 1) {
+            bn_apply_t<true, true, 1>(ctx, n, c, hw, x, bn, skip, sb, out);
+        } else {
+            bn_apply_t<true, true, 2>(ctx, n, c, hw, x, bn, skip, sb, out);
+        }
     } else {
-        bn_apply_scalar_kernel<EVAL, RELU, SKIP><<<ew_grid(ctx, total), EW_THREADS, 0,
-                                                   ctx->stream>>>(x, bn, skip, sbn, out, total,
-                                                                  (int)hw, (int)c);
+        if (skip_mode == 0) {
+            if (relu)
+                bn_apply_t<false, true, 0>(ctx, n, c, hw, x, bn, skip, sb, out);
+            else
+                bn_apply_t<false, false, 0>(ctx, n, c, hw, x, bn, skip, sb, out);
+        } else if (skip_mode == 1) {
+            bn_apply_t<false, true, 1>(ctx, n, c, hw, x, bn, skip, sb, out);
+        } else {
+            bn_apply_t<false, true, 2>(ctx, n, c, hw, x, bn, skip, sb, out);
+        }
     }
-    RNN_LAUNCHED(ctx);
-    return RNN_OK;
-}
-
-int rnn_bn_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x,
-                        const RnnBnCoef &bn, int relu, int skip_mode, const float *skip,
-                        const RnnBnCoef &sbn, float *out) {
-    if (bn.eval) {
-        BnCoef<true> a{bn.mean, bn.invstd, bn.gamma, bn.beta};
-        BnCoef<true> b{sbn.mean, sbn.invstd, sbn.gamma, sbn.beta};
-        if (skip_mode == 0)
-            return relu ? bn_apply_t<true, true, 0>(ctx, n, c, hw, x, a, skip, b, out)
-                        : bn_apply_t<true, false, 0>(ctx, n, c, hw, x, a, skip, b, out);
-        if (skip_mode == 1) return bn_apply_t<true, true, 1>(ctx, n, c, hw, x, a, skip, b, out);
-        return bn_apply_t<true, true, 2>(ctx, n, c, hw, x, a, skip, b, out);
-    }
-    BnCoef<false> a{bn.mean, bn.invstd, bn.gamma, bn.beta};
-    BnCoef<false> b{sbn.mean, sbn.invstd, sbn.gamma, sbn.beta};
-    if (skip_mode == 0)
-        return relu ? bn_apply_t<false, true, 0>(ctx, n, c, hw, x, a, skip, b, out)
-                    : bn_apply_t<false, false, 0>(ctx, n, c, hw, x, a, skip, b, out);
-    if (skip_mode == 1) return bn_apply_t<false, true, 1>(ctx, n, c, hw, x, a, skip, b, out);
-    return bn_apply_t<false, true, 2>(ctx, n, c, hw, x, a, skip, b, out);
-}
-
-int rnn_bn_eval_prep_launch(rnn_ctx *ctx, size_t c, const float *gamma, const float *beta,
-                            const float *rm, const float *rv, float eps, float *sc, float *sh) {
-    bn_eval_prep_kernel<<<(unsigned)rnn_div_up(c, 64), 64, 0, ctx->stream>>>(gamma, beta, rm, rv,
-                                                                             eps, (int)c, sc, sh);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
 
 int rnn_bn_backward_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
-                           const float *mask, const float *x, const float *mean,
-                           const float *invstd, const float *gamma, float *dx, float *dgamma,
-                           float *dbeta, double *part, float *dgdb) {
+                           const float *mask, const float *x, RnnBn bn, double *part, float *dx) {
+    if (n * c * hw == 0) return RNN_OK;
     ChanSplit s = chan_split(n, c);
+    bn.P = s.P;
+    bn.m = (float)(n * hw);
     const FastDiv fd_hw4 = divider(hw / 4, (size_t)s.G * (hw / 4));
     const dim3 grid((unsigned)c, (unsigned)s.P);
-    const int vec = aligned16(dy) && aligned16(x) && (!mask || aligned16(mask));
+    const int vec = (hw & 3) == 0 && aligned16(dy) && aligned16(x) && (!mask || aligned16(mask));
     if (mask)
         bn_bwd_part_kernel<true><<<grid, RED_THREADS, 0, ctx->stream>>>(
-            dy, mask, x, mean, invstd, (int)n, (int)c, (int)hw, vec, s.G, fd_hw4, part);
+            dy, mask, x, bn.mean, bn.invstd, (int)n, (int)c, (int)hw, vec, s.G, fd_hw4, part);
     else
         bn_bwd_part_kernel<false><<<grid, RED_THREADS, 0, ctx->stream>>>(
-            dy, mask, x, mean, invstd, (int)n, (int)c, (int)hw, vec, s.G, fd_hw4, part);
+            dy, mask, x, bn.mean, bn.invstd, (int)n, (int)c, (int)hw, vec, s.G, fd_hw4, part);
     RNN_LAUNCHED(ctx);
-    bn_bwd_final_kernel<<<(unsigned)rnn_div_up(c, 64), 64, 0, ctx->stream>>>(part, s.P, (int)c,
-                                                                             dgamma, dbeta, dgdb);
-    RNN_LAUNCHED(ctx);
-    const size_t total = n * c * hw;
-    const float m = (float)(n * hw);
-    if ((hw & 3) == 0 && total / 4 < (1ull << 31) && aligned16(dy) && aligned16(x) &&
-        aligned16(dx) && (!mask || aligned16(mask))) {
-        const size_t t4 = total / 4;
-        const FastDiv fq = divider(hw / 4, t4), fc = divider(c, n * c);
-        if (mask)
-            bn_bwd_apply_kernel<true><<<ew_grid(ctx, t4), EW_THREADS, 0, ctx->stream>>>(
-                dy, mask, x, mean, invstd, gamma, dgdb, m, dx, t4, fq, fc);
-        else
-            bn_bwd_apply_kernel<false><<<ew_grid(ctx, t4), EW_THREADS, 0, ctx->stream>>>(
-                dy, mask, x, mean, invstd, gamma, dgdb, m, dx, t4, fq, fc);
-    } else {
-        if (mask)
-            bn_bwd_apply_scalar_kernel<true><<<ew_grid(ctx, total), EW_THREADS, 0, ctx->stream>>>(
-                dy, mask, x, mean, invstd, gamma, dgdb, m, dx, total, (int)hw, (int)c);
-        else
-            bn_bwd_apply_scalar_kernel<false><<<ew_grid(ctx, total), EW_THREADS, 0,
-                                                ctx->stream>>>(dy, mask, x, mean, invstd, gamma,
-                                                               dgdb, m, dx, total, (int)hw, (int)c);
-    }
+    const int vec2 = vec && aligned16(dx);
+    if (mask)
+        bn_bwd_apply_kernel<true><<<grid, EW_THREADS, 0, ctx->stream>>>(
+            dy, mask, x, bn, part, dx, (int)n, (int)c, (int)hw, s.G, fd_hw4, vec2);
+    else
+        bn_bwd_apply_kernel<false><<<grid, EW_THREADS, 0, ctx->stream>>>(
+            dy, mask, x, bn, part, dx, (int)n, (int)c, (int)hw, s.G, fd_hw4, vec2);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -691,6 +843,28 @@ int rnn_add_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const flo
     return RNN_OK;
 }
 
+int rnn_add_mask_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *mask) {
+    if (len == 0 || (!b && !mask)) return RNN_OK;
+    const size_t items = rnn_div_up(len, 4);
+    const int vec = aligned16(a) && (!b || aligned16(b)) && (!mask || aligned16(mask));
+    const unsigned gr = ew_grid(ctx, items);
+    if (b && mask)
+        add_mask_kernel<true, true><<<gr, EW_THREADS, 0, ctx->stream>>>(a, b, mask, len, vec);
+    else if (b)
+        add_mask_kernel<true, false><<<gr, EW_THREADS, 0, ctx->stream>>>(a, b, mask, len, vec);
+    else
+        add_mask_kernel<false, true><<<gr, EW_THREADS, 0, ctx->stream>>>(a, b, mask, len, vec);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_relu_back_launch(rnn_ctx *ctx, size_t len, float *d, const float *y) {
+    if (len == 0) return RNN_OK;
+    relu_back_kernel<<<ew_grid(ctx, len), EW_THREADS, 0, ctx->stream>>>(d, y, len);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
 int rnn_gap_forward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *x, float *y) {
     if (nc == 0) return RNN_OK;
     const int vec = (hw & 3) == 0 && aligned16(x);
@@ -699,10 +873,11 @@ int rnn_gap_forward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *x, f
     return RNN_OK;
 }
 
-int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx) {
+int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx,
+                            const float *mask) {
     if (nc * hw == 0) return RNN_OK;
     gap_bwd_kernel<<<ew_grid(ctx, nc * hw), EW_THREADS, 0, ctx->stream>>>(dy, (int)hw, nc * hw,
-                                                                         dx);
+                                                                         mask, dx);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -711,23 +886,27 @@ int rnn_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, co
                           const float *w, const float *b, float *y) {
     const size_t t = rows * fout;
     if (t == 0) return RNN_OK;
-    fc_fwd_kernel<<<(unsigned)rnn_div_up(t, 128), 128, 0, ctx->stream>>>(x, w, b, (int)rows,
-                                                                        (int)fin, (int)fout, y);
+    if ((fin & 3) == 0 && aligned16(x) && aligned16(w))
+        fc_fwd_kernel<true><<<(unsigned)rnn_div_up(t, 128), 128, 0, ctx->stream>>>(
+            x, w, b, (int)rows, (int)fin, (int)fout, y);
+    else
+        fc_fwd_kernel<false><<<(unsigned)rnn_div_up(t, 128), 128, 0, ctx->stream>>>(
+            x, w, b, (int)rows, (int)fin, (int)fout, y);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
 
 int rnn_fc_backward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
                            const float *x, const float *w, float *dw, float *db, float *dx) {
-    const size_t tw = fout * (fin + 1), tx = rows * fin;
-    if (tw) {
-        fc_bwd_w_kernel<<<(unsigned)rnn_div_up(tw, 128), 128, 0, ctx->stream>>>(
-            dy, x, (int)rows, (int)fin, (int)fout, dw, db);
+    const unsigned tb = (unsigned)std::min<size_t>(256, rnn_round_up(fin + 1, 64));
+    if (fout) {
+        fc_bwd_w_kernel<<<(unsigned)fout, tb, 0, ctx->stream>>>(dy, x, (int)rows, (int)fin,
+                                                                (int)fout, dw, db);
         RNN_LAUNCHED(ctx);
     }
-    if (tx && dx) {
-        fc_bwd_x_kernel<<<(unsigned)rnn_div_up(tx, 128), 128, 0, ctx->stream>>>(
-            dy, w, (int)rows, (int)fin, (int)fout, dx);
+    if (rows && fin && dx) {
+        fc_bwd_x_kernel<<<(unsigned)rows, tb, 0, ctx->stream>>>(dy, w, (int)rows, (int)fin,
+                                                                (int)fout, dx);
         RNN_LAUNCHED(ctx);
     }
     return RNN_OK;
@@ -737,9 +916,22 @@ int rnn_softmax_ce_launch(rnn_ctx *ctx, size_t rows, size_t nclass, const float 
                           const uint32_t *labels, float smooth, const float *scal, float *dl,
                           float *loss, uint32_t *correct) {
     if (rows == 0) return RNN_OK;
-    const unsigned threads = (unsigned)std::min<size_t>(rnn_round_up(rows, 64), 1024);
-    softmax_ce_kernel<<<1, threads, 2 * rows * sizeof(float), ctx->stream>>>(
-        logits, labels, (int)rows, (int)nclass, smooth, scal, dl, loss, correct);
+    const unsigned threads = (unsigned)std::min<size_t>(64 * rows, 1024);
+    const size_t lds = 2 * rows * sizeof(float);
+    auto go = [&](auto kern) {
+        kern<<<1, threads, lds, ctx->stream>>>(logits, labels, (int)rows, (int)nclass, smooth, scal,
+                                               dl, loss, correct);
+    };
+    if (nclass <= 64)
+        go(softmax_ce_kernel<1>);
+    else if (nclass <= 128)
+        go(softmax_ce_kernel<2>);
+    else if (nclass <= 256)
+        go(softmax_ce_kernel<4>);
+    else if (nclass <= 1024)
+        go(softmax_ce_kernel<16>);
+    else
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "softmax_ce: nclass %zu > 1024", nclass);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -749,6 +941,15 @@ int rnn_sgd_launch(rnn_ctx *ctx, size_t len, size_t ndecay, float *v, float *g, 
     if (len == 0) return RNN_OK;
     sgd_kernel<<<ew_grid(ctx, len), EW_THREADS, 0, ctx->stream>>>(v, g, m, len, ndecay, lr, mom,
                                                                   wd, scal);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_grad_finalize_launch(rnn_ctx *ctx, const GradSeg *segs, int nseg, long long nblocks,
+                             float *v, float *g, float *m, const float *scal, int do_sgd) {
+    if (nblocks <= 0) return RNN_OK;
+    grad_finalize_kernel<<<(unsigned)nblocks, 256, 0, ctx->stream>>>(segs, nseg, v, g, m, scal,
+                                                                     do_sgd);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -763,21 +964,9 @@ int rnn_set_scalars_launch(rnn_ctx *ctx, float *scal, float a, float b, float c,
 
 namespace {
 
-// Carves BN scratch (partials + dgamma/dbeta values) out of the workspace.
-struct BnScratch {
-    double *part;
-    float *f;
-};
-
-bool bn_scratch(rnn_ctx *ctx, size_t n, size_t c, BnScratch &s) {
-    WsCarve cv;
-    size_t o1 = cv.take(rnn_bn_scratch_doubles(n, c) * sizeof(double));
-    size_t o2 = cv.take(2 * c * sizeof(float));
-    char *ws = (char *)rnn_workspace(ctx, cv.off);
-    if (!ws) return false;
-    s.part = (double *)(ws + o1);
-    s.f = (float *)(ws + o2);
-    return true;
+// BN partial sums in the workspace.
+double *bn_scratch(rnn_ctx *ctx, size_t n, size_t c) {
+    return (double *)rnn_workspace(ctx, rnn_bn_scratch_doubles(n, c) * sizeof(double));
 }
 
 bool dims_ok(size_t n, size_t c, size_t hw) {
@@ -800,13 +989,21 @@ int rnn_bn_forward_train(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const floa
         return rnn_fail(ctx, RNN_E_NULL, "bn_forward_train: running mean/var must both be set");
     if (!dims_ok(n, c, hw)) return rnn_fail(ctx, RNN_E_INVALID, "bn_forward_train: too large");
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
-    BnScratch s;
-    if (!bn_scratch(ctx, n, c, s)) return RNN_E_NOMEM;
-    int st = rnn_bn_stats_launch(ctx, n, c, hw, x, s.part, mean, invstd, running_mean,
-                                 running_var, momentum, eps);
+    double *part = bn_scratch(ctx, n, c);
+    if (!part) return RNN_E_NOMEM;
+    int st = rnn_bn_stats_launch(ctx, n, c, hw, x, part);
     if (st) return st;
-    RnnBnCoef bn{false, mean, invstd, gamma, beta};
-    return rnn_bn_apply_launch(ctx, n, c, hw, x, bn, relu, 0, nullptr, bn, y);
+    RnnBn bn;
+    bn.part = part;
+    bn.mom = momentum;
+    bn.eps = eps;
+    bn.mean = mean;
+    bn.invstd = invstd;
+    bn.rm = running_mean;
+    bn.rv = running_var;
+    bn.gamma = gamma;
+    bn.beta = beta;
+    return rnn_bn_apply_launch(ctx, n, c, hw, x, bn, false, relu, 0, nullptr, nullptr, y);
 }
 
 int rnn_bn_forward_eval(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, float *y,
@@ -818,13 +1015,13 @@ int rnn_bn_forward_eval(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float
         return rnn_fail(ctx, RNN_E_NULL, "bn_forward_eval: null pointer");
     if (!dims_ok(n, c, hw)) return rnn_fail(ctx, RNN_E_INVALID, "bn_forward_eval: too large");
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
-    BnScratch s;
-    if (!bn_scratch(ctx, n, c, s)) return RNN_E_NOMEM;
-    float *sc = s.f, *sh = s.f + c;
-    int st = rnn_bn_eval_prep_launch(ctx, c, gamma, beta, running_mean, running_var, eps, sc, sh);
-    if (st) return st;
-    RnnBnCoef bn{true, sc, sh, nullptr, nullptr};
-    return rnn_bn_apply_launch(ctx, n, c, hw, x, bn, relu, 0, nullptr, bn, y);
+    RnnBn bn;
+    bn.eps = eps;
+    bn.rm = const_cast<float *>(running_mean);  // read only in eval mode
+    bn.rv = const_cast<float *>(running_var);
+    bn.gamma = gamma;
+    bn.beta = beta;
+    return rnn_bn_apply_launch(ctx, n, c, hw, x, bn, true, relu, 0, nullptr, nullptr, y);
 }
 
 int rnn_bn_backward(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
@@ -836,10 +1033,15 @@ int rnn_bn_backward(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy
         return rnn_fail(ctx, RNN_E_NULL, "bn_backward: null pointer");
     if (!dims_ok(n, c, hw)) return rnn_fail(ctx, RNN_E_INVALID, "bn_backward: too large");
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
-    BnScratch s;
-    if (!bn_scratch(ctx, n, c, s)) return RNN_E_NOMEM;
-    return rnn_bn_backward_launch(ctx, n, c, hw, dy, relu_out, x, mean, invstd, gamma, dx, dgamma,
-                                  dbeta, s.part, s.f);
+    double *part = bn_scratch(ctx, n, c);
+    if (!part) return RNN_E_NOMEM;
+    RnnBn bn;
+    bn.mean = const_cast<float *>(mean);
+    bn.invstd = const_cast<float *>(invstd);
+    bn.gamma = gamma;
+    bn.dgamma = dgamma;
+    bn.dbeta = dbeta;
+    return rnn_bn_backward_launch(ctx, n, c, hw, dy, relu_out, x, bn, part, dx);
 }
 
 int rnn_relu_back(rnn_ctx *ctx, size_t len, float *d, const float *y) {
@@ -847,9 +1049,7 @@ int rnn_relu_back(rnn_ctx *ctx, size_t len, float *d, const float *y) {
     if (len == 0) return RNN_OK;
     if (!d || !y) return rnn_fail(ctx, RNN_E_NULL, "relu_back: null pointer");
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
-    relu_back_kernel<<<ew_grid(ctx, len), EW_THREADS, 0, ctx->stream>>>(d, y, len);
-    RNN_LAUNCHED(ctx);
-    return RNN_OK;
+    return rnn_relu_back_launch(ctx, len, d, y);
 }
 
 int rnn_add(rnn_ctx *ctx, size_t len, float *a, const float *b) {

@@ -21,6 +21,7 @@
 // into the network's own buffers, so the graph never sees caller pointers.
 #include "rnn_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -72,6 +73,10 @@ struct ParamSlot {
 struct NetConv {
     uint32_t cin = 0, cout = 0, k = 0, stride = 1, pad = 0;
     int w = -1;  // parameter index
+    // dW partial slabs of the last backward (per plan); null: dW is added
+    // straight into the gradient instead
+    float *slabs = nullptr;
+    int nz = 0;
     rnn_conv_spec spec(uint32_t h, uint32_t w_) const {
         rnn_conv_spec sp;
         rnn_conv_spec_init(&sp, cin, cout, k, stride, pad, h, w_);
@@ -83,7 +88,8 @@ struct NetBn {
     uint32_t c = 0;
     int g = -1, b = -1;  // parameter indices
     size_t buf = 0;      // rm at buf, rv at buf + c in the buffer array
-    float *coef = nullptr;  // device [4c]: mean, invstd (train) | sc, sh (eval)
+    float *coef = nullptr;   // device [2c]: batch mean, invstd of the last train forward
+    double *part = nullptr;  // device: partial sums of the batch statistics (per plan)
 };
 
 struct NetBlock {
@@ -112,7 +118,11 @@ struct rnn_resnet {
     void *arena = nullptr;
     float *x = nullptr, *y0 = nullptr, *s0 = nullptr, *pooled = nullptr, *logits = nullptr;
     float *dlogits = nullptr, *dpool = nullptr, *d0 = nullptr, *d1 = nullptr, *t1 = nullptr,
-          *t2 = nullptr, *scal = nullptr, *loss = nullptr, *dgdb = nullptr;
+          *t2 = nullptr, *t3 = nullptr, *scal = nullptr, *loss = nullptr;
+    // Gradient finalisation: one segment per parameter tensor in flat order.
+    GradSeg *segs = nullptr;
+    int nseg = 0;
+    long long nseg_blocks = 0;
     uint32_t *labels = nullptr, *correct = nullptr;
     double *part = nullptr;
     size_t fh = 0, fw = 0;  // feature map at the pooling layer
@@ -170,7 +180,7 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     WsCarve cv;
     std::vector<std::pair<float **, size_t>> f32;
     const size_t w0 = r->width;
-    size_t maxact = n * w0 * H * W, maxc = w0, maxpart = rnn_bn_scratch_doubles(n, w0);
+    size_t maxact = n * w0 * H * W, maxpart = rnn_bn_scratch_doubles(n, w0);
     f32.push_back({&r->x, n * 3 * H * W});
     f32.push_back({&r->y0, n * w0 * H * W});
     f32.push_back({&r->s0, n * w0 * H * W});
@@ -188,7 +198,6 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
         if (b.down) f32.push_back({&b.ys, a});
         f32.push_back({&b.out, a});
         maxact = std::max(maxact, a);
-        maxc = std::max<size_t>(maxc, b.c1.cout);
         maxpart = std::max(maxpart, rnn_bn_scratch_doubles(n, b.c1.cout));
         h = sp.oh;
         w = sp.ow;
@@ -203,12 +212,38 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     f32.push_back({&r->d1, maxact});
     f32.push_back({&r->t1, maxact});
     f32.push_back({&r->t2, maxact});
+    f32.push_back({&r->t3, maxact});
     f32.push_back({&r->scal, 4});
     f32.push_back({&r->loss, 1});
-    f32.push_back({&r->dgdb, 2 * maxc});
     std::vector<size_t> offs;
     for (auto &e : f32) offs.push_back(cv.take(e.second * sizeof(float)));
     const size_t o_part = cv.take(maxpart * sizeof(double));
+    std::vector<std::pair<NetBn *, size_t>> bnparts;
+    auto bnpart = [&](NetBn &bn) {
+        bnparts.push_back({&bn, cv.take(rnn_bn_scratch_doubles(n, bn.c) * sizeof(double))});
+    };
+    bnpart(r->stem_bn);
+    for (auto &b : r->blocks) {
+        bnpart(b.b1);
+        bnpart(b.b2);
+        if (b.down) bnpart(b.bd);
+    }
+    // dW slabs of every conv, and the gradient segment table.
+    std::vector<std::pair<NetConv *, size_t>> slabs;
+    auto slab = [&](NetConv &c, uint32_t h, uint32_t w) {
+        rnn_conv_spec sp = c.spec(h, w);
+        const size_t f = rnn_conv_dw_slab_floats(ctx, &sp, n);
+        const size_t len = (size_t)c.cout * c.cin * c.k * c.k;
+        c.nz = f ? (int)(f / len) : 0;
+        if (f) slabs.push_back({&c, cv.take(f * sizeof(float))});
+    };
+    slab(r->stem, (uint32_t)H, (uint32_t)W);
+    for (auto &b : r->blocks) {
+        slab(b.c1, b.hin, b.win);
+        slab(b.c2, b.hout, b.wout);
+        if (b.down) slab(b.cd, b.hin, b.win);
+    }
+    const size_t o_segs = cv.take(r->params.size() * sizeof(GradSeg));
     const size_t o_lab = cv.take(n * sizeof(uint32_t));
     const size_t o_cor = cv.take(sizeof(uint32_t));
     void *mem = nullptr;
@@ -220,6 +255,47 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     char *base = (char *)mem;
     for (size_t i = 0; i < f32.size(); i++) *f32[i].first = (float *)(base + offs[i]);
     r->part = (double *)(base + o_part);
+    for (auto &e : bnparts) e.first->part = (double *)(base + e.second);
+    r->stem.slabs = nullptr;
+    for (auto &b : r->blocks) b.c1.slabs = b.c2.slabs = b.cd.slabs = nullptr;
+    for (auto &e : slabs) e.first->slabs = (float *)(base + e.second);
+    // Segment table: parameters in flat order, conv weights with their slabs.
+    std::vector<GradSeg> segs(r->params.size());
+    std::vector<const NetConv *> conv_of(r->params.size(), nullptr);
+    conv_of[r->stem.w] = &r->stem;
+    for (auto &b : r->blocks) {
+        conv_of[b.c1.w] = &b.c1;
+        conv_of[b.c2.w] = &b.c2;
+        if (b.down) conv_of[b.cd.w] = &b.cd;
+    }
+    std::vector<int> order(r->params.size());
+    for (size_t i = 0; i < order.size(); i++) order[i] = (int)i;
+    std::sort(order.begin(), order.end(),
+              [&](int a, int b) { return r->params[a].off < r->params[b].off; });
+    long long blk = 0;
+    for (size_t k = 0; k < order.size(); k++) {
+        const ParamSlot &ps = r->params[order[k]];
+        const NetConv *c = conv_of[order[k]];
+        GradSeg g;
+        g.off = (long long)ps.off;
+        g.len = (long long)ps.len;
+        g.blk0 = blk;
+        g.slabs = c && c->slabs ? c->slabs : nullptr;
+        g.nz = g.slabs ? c->nz : 0;
+        g.decay = ps.decay ? 1 : 0;
+        segs[k] = g;
+        blk += (long long)rnn_div_up(ps.len, 32);
+    }
+    r->segs = (GradSeg *)(base + o_segs);
+    r->nseg = (int)segs.size();
+    r->nseg_blocks = blk;
+    hipError_t ce = hipMemcpy(r->segs, segs.data(), segs.size() * sizeof(GradSeg),
+                              hipMemcpyHostToDevice);
+    if (ce != hipSuccess) {
+        (void)hipFree(r->arena);
+        r->arena = nullptr;
+        return rnn_fail(ctx, RNN_E_HIP, "resnet plan upload: %s", hipGetErrorString(ce));
+    }
     r->labels = (uint32_t *)(base + o_lab);
     r->correct = (uint32_t *)(base + o_cor);
     float *prev = r->s0;
@@ -234,26 +310,22 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     return RNN_OK;
 }
 
-RnnBnCoef train_coef(rnn_resnet *r, const NetBn &bn) {
-    return RnnBnCoef{false, bn.coef, bn.coef + bn.c, pv_of(r, bn.g), pv_of(r, bn.b)};
-}
-
-RnnBnCoef eval_coef(const NetBn &bn) {
-    return RnnBnCoef{true, bn.coef + 2 * bn.c, bn.coef + 3 * bn.c, nullptr, nullptr};
-}
-
-// Batch statistics (train) or the running-statistics scale / shift (eval).
-int bn_prepare(rnn_resnet *r, const NetBn &bn, const float *y, size_t hw, bool train) {
-    float *rm = r->bufs + bn.buf, *rv = rm + bn.c;
-    if (train)
-        return rnn_bn_stats_launch(r->ctx, r->n, bn.c, hw, y, r->part, bn.coef, bn.coef + bn.c,
-                                   rm, rv, 0.1f, 1e-5f);
-    return rnn_bn_eval_prep_launch(r->ctx, bn.c, pv_of(r, bn.g), pv_of(r, bn.b), rm, rv, 1e-5f,
-                                   bn.coef + 2 * bn.c, bn.coef + 3 * bn.c);
-}
-
-RnnBnCoef coef(rnn_resnet *r, const NetBn &bn, bool train) {
-    return train ? train_coef(r, bn) : eval_coef(bn);
+// The RnnBn view of a layer: parameters, gradients, running statistics,
+// batch statistics and partial sums.
+RnnBn bn_state(rnn_resnet *r, const NetBn &bn) {
+    RnnBn s;
+    s.part = bn.part;
+    s.mom = 0.1f;
+    s.eps = 1e-5f;
+    s.mean = bn.coef;
+    s.invstd = bn.coef + bn.c;
+    s.rm = r->bufs + bn.buf;
+    s.rv = s.rm + bn.c;
+    s.gamma = pv_of(r, bn.g);
+    s.beta = pv_of(r, bn.b);
+    s.dgamma = pg_of(r, bn.g);
+    s.dbeta = pg_of(r, bn.b);
+    return s;
 }
 
 #define TRY(expr)                 \
@@ -263,34 +335,38 @@ RnnBnCoef coef(rnn_resnet *r, const NetBn &bn, bool train) {
     } while (0)
 
 // ResNet::forward (model.rs:138-150) with BasicBlock::forward (model.rs:39-57).
+// Train mode: each BN's partial sums are taken right after its conv and
+// finalised inside the kernel that applies the BN.
 int forward(rnn_resnet *r, bool train) {
     rnn_ctx *ctx = r->ctx;
     const size_t n = r->n;
+    const bool ev = !train;
     rnn_conv_spec sp = r->stem.spec((uint32_t)r->H, (uint32_t)r->W);
+    const size_t hw0 = (size_t)sp.oh * sp.ow;
     TRY(rnn_conv2d_forward(ctx, &sp, n, r->x, pv_of(r, r->stem.w), r->y0));
-    TRY(bn_prepare(r, r->stem_bn, r->y0, sp.oh * sp.ow, train));
-    RnnBnCoef c0 = coef(r, r->stem_bn, train);
-    TRY(rnn_bn_apply_launch(ctx, n, r->stem_bn.c, sp.oh * sp.ow, r->y0, c0, 1, 0, nullptr, c0,
-                            r->s0));
+    if (train) TRY(rnn_bn_stats_launch(ctx, n, r->stem_bn.c, hw0, r->y0, r->stem_bn.part));
+    TRY(rnn_bn_apply_launch(ctx, n, r->stem_bn.c, hw0, r->y0, bn_state(r, r->stem_bn), ev, 1, 0,
+                            nullptr, nullptr, r->s0));
     for (auto &b : r->blocks) {
         const size_t hw = (size_t)b.hout * b.wout;
         rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
         TRY(rnn_conv2d_forward(ctx, &s1, n, b.in, pv_of(r, b.c1.w), b.y1));
-        TRY(bn_prepare(r, b.b1, b.y1, hw, train));
-        RnnBnCoef k1 = coef(r, b.b1, train);
-        TRY(rnn_bn_apply_launch(ctx, n, b.b1.c, hw, b.y1, k1, 1, 0, nullptr, k1, b.h));
+        if (train) TRY(rnn_bn_stats_launch(ctx, n, b.b1.c, hw, b.y1, b.b1.part));
+        TRY(rnn_bn_apply_launch(ctx, n, b.b1.c, hw, b.y1, bn_state(r, b.b1), ev, 1, 0, nullptr,
+                                nullptr, b.h));
         rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
         TRY(rnn_conv2d_forward(ctx, &s2, n, b.h, pv_of(r, b.c2.w), b.y2));
-        TRY(bn_prepare(r, b.b2, b.y2, hw, train));
-        RnnBnCoef k2 = coef(r, b.b2, train);
+        if (train) TRY(rnn_bn_stats_launch(ctx, n, b.b2.c, hw, b.y2, b.b2.part));
         if (b.down) {
             rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
             TRY(rnn_conv2d_forward(ctx, &sd, n, b.in, pv_of(r, b.cd.w), b.ys));
-            TRY(bn_prepare(r, b.bd, b.ys, hw, train));
-            RnnBnCoef kd = coef(r, b.bd, train);
-            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, k2, 1, 2, b.ys, kd, b.out));
+            if (train) TRY(rnn_bn_stats_launch(ctx, n, b.bd.c, hw, b.ys, b.bd.part));
+            const RnnBn sd_bn = bn_state(r, b.bd);
+            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, bn_state(r, b.b2), ev, 1, 2, b.ys,
+                                    &sd_bn, b.out));
         } else {
-            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, k2, 1, 1, b.in, k2, b.out));
+            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, bn_state(r, b.b2), ev, 1, 1, b.in,
+                                    nullptr, b.out));
         }
     }
     const float *feat = r->blocks.empty() ? r->s0 : r->blocks.back().out;
@@ -301,53 +377,67 @@ int forward(rnn_resnet *r, bool train) {
     return RNN_OK;
 }
 
+// dW of one conv: into its slabs (summed at the end of the backward), or
+// straight into the gradient when the shape has no slab plan.
+int conv_dw(rnn_resnet *r, const NetConv &c, const rnn_conv_spec &sp, const float *dy,
+            const float *x) {
+    if (c.slabs) return rnn_conv_dw_slabs(r->ctx, &sp, r->n, dy, x, c.slabs, nullptr);
+    return rnn_conv2d_backward_w(r->ctx, &sp, r->n, dy, x, pg_of(r, c.w));
+}
+
 // ResNet::backward (model.rs:152-162) with BasicBlock::backward
-// (model.rs:59-77).  Gradients accumulate into pg (Param::g).
-int backward(rnn_resnet *r, const float *dlogits) {
+// (model.rs:59-77).  relu_back_ of a block's output gradient is folded into
+// the kernel that produces it: the GAP backward for the last block, and for
+// the others the pass after the next block's first dX that adds the shortcut
+// term (the residual add_) and masks by that block's input, the previous
+// block's output (or the stem's ReLU output).  relu_back_ by h is folded into
+// the first BN backward that reads c2's dX.
+// The conv weight gradients are left as slabs; the finalisation adds them
+// into pg (Param::g) -- and with `sgd` also takes the Nesterov step -- in one
+// pass over all parameters.
+int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
     rnn_ctx *ctx = r->ctx;
     const size_t n = r->n;
     TRY(rnn_fc_backward_launch(ctx, n, r->fin, r->nclass, dlogits, r->pooled, pv_of(r, r->fc_w),
                                pg_of(r, r->fc_w), pg_of(r, r->fc_b), r->dpool));
-    TRY(rnn_gap_backward_launch(ctx, n * r->fin, r->fh * r->fw, r->dpool, r->d0));
+    const float *feat = r->blocks.empty() ? r->s0 : r->blocks.back().out;
+    TRY(rnn_gap_backward_launch(ctx, n * r->fin, r->fh * r->fw, r->dpool, r->d0, feat));
     float *d = r->d0, *other = r->d1;
     for (size_t i = r->blocks.size(); i-- > 0;) {
         NetBlock &b = r->blocks[i];
         const size_t hw = (size_t)b.hout * b.wout;
-        // relu_back_(d, out) is folded into the consumers of d below.
-        TRY(rnn_bn_backward_launch(ctx, n, b.b2.c, hw, d, b.out, b.y2, b.b2.coef,
-                                   b.b2.coef + b.b2.c, pv_of(r, b.b2.g), r->t1, pg_of(r, b.b2.g),
-                                   pg_of(r, b.b2.b), r->part, r->dgdb));
+        TRY(rnn_bn_backward_launch(ctx, n, b.b2.c, hw, d, nullptr, b.y2, bn_state(r, b.b2),
+                                   r->part, r->t1));
         rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
-        TRY(rnn_conv2d_backward_w(ctx, &s2, n, r->t1, b.h, pg_of(r, b.c2.w)));
+        TRY(conv_dw(r, b.c2, s2, r->t1, b.h));
         TRY(rnn_conv2d_backward_x(ctx, &s2, n, r->t1, pv_of(r, b.c2.w), r->t2));
-        TRY(rnn_bn_backward_launch(ctx, n, b.b1.c, hw, r->t2, b.h, b.y1, b.b1.coef,
-                                   b.b1.coef + b.b1.c, pv_of(r, b.b1.g), r->t1, pg_of(r, b.b1.g),
-                                   pg_of(r, b.b1.b), r->part, r->dgdb));
+        TRY(rnn_bn_backward_launch(ctx, n, b.b1.c, hw, r->t2, b.h, b.y1, bn_state(r, b.b1),
+                                   r->part, r->t1));
         rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
-        TRY(rnn_conv2d_backward_w(ctx, &s1, n, r->t1, b.in, pg_of(r, b.c1.w)));
-        TRY(rnn_conv2d_backward_x(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), other));
-        const size_t in_len = n * (size_t)b.c1.cin * b.hin * b.win;
+        TRY(conv_dw(r, b.c1, s1, r->t1, b.in));
         if (b.down) {
-            TRY(rnn_bn_backward_launch(ctx, n, b.bd.c, hw, d, b.out, b.ys, b.bd.coef,
-                                       b.bd.coef + b.bd.c, pv_of(r, b.bd.g), r->t1,
-                                       pg_of(r, b.bd.g), pg_of(r, b.bd.b), r->part, r->dgdb));
+            TRY(rnn_bn_backward_launch(ctx, n, b.bd.c, hw, d, nullptr, b.ys, bn_state(r, b.bd),
+                                       r->part, r->t2));
             rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
-            TRY(rnn_conv2d_backward_w(ctx, &sd, n, r->t1, b.in, pg_of(r, b.cd.w)));
-            TRY(rnn_conv2d_backward_x(ctx, &sd, n, r->t1, pv_of(r, b.cd.w), r->t2));
-            TRY(rnn_add_launch(ctx, in_len, other, r->t2, nullptr));
+            TRY(conv_dw(r, b.cd, sd, r->t2, b.in));
+            TRY(rnn_conv2d_backward_x(ctx, &sd, n, r->t2, pv_of(r, b.cd.w), r->t3));
+            // dx = c1 dX + shortcut dX (add_, model.rs:70-71), masked by the input
+            TRY(rnn_conv2d_backward_x_ep(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), other, r->t3,
+                                         b.in));
         } else {
-            TRY(rnn_add_launch(ctx, in_len, other, d, b.out));
+            // dx = c1 dX + d (add_, model.rs:72), masked by the input
+            TRY(rnn_conv2d_backward_x_ep(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), other, d, b.in));
         }
         std::swap(d, other);
     }
     rnn_conv_spec sp = r->stem.spec((uint32_t)r->H, (uint32_t)r->W);
-    TRY(rnn_bn_backward_launch(ctx, n, r->stem_bn.c, sp.oh * sp.ow, d, r->s0, r->y0,
-                               r->stem_bn.coef, r->stem_bn.coef + r->stem_bn.c,
-                               pv_of(r, r->stem_bn.g), r->t1, pg_of(r, r->stem_bn.g),
-                               pg_of(r, r->stem_bn.b), r->part, r->dgdb));
+    // d is already relu_back_'d by the stem output (model.rs:159)
+    TRY(rnn_bn_backward_launch(ctx, n, r->stem_bn.c, (size_t)sp.oh * sp.ow, d, nullptr, r->y0,
+                               bn_state(r, r->stem_bn), r->part, r->t1));
     // The stem's dX would be the image gradient: discarded (model.rs:161).
-    TRY(rnn_conv2d_backward_w(ctx, &sp, n, r->t1, r->x, pg_of(r, r->stem.w)));
-    return RNN_OK;
+    TRY(conv_dw(r, r->stem, sp, r->t1, r->x));
+    return rnn_grad_finalize_launch(ctx, r->segs, r->nseg, r->nseg_blocks, r->pv, r->pg, r->pm,
+                                    r->scal, sgd ? 1 : 0);
 }
 
 int sgd(rnn_resnet *r, const float *scal, float lr, float mom, float wd) {
@@ -360,8 +450,7 @@ int step_body(rnn_resnet *r) {
     TRY(forward(r, true));
     TRY(rnn_softmax_ce_launch(r->ctx, r->n, r->nclass, r->logits, r->labels, 0.0f, r->scal,
                               r->dlogits, r->loss, r->correct));
-    TRY(backward(r, r->dlogits));
-    return sgd(r, r->scal, 0.f, 0.f, 0.f);
+    return backward(r, r->dlogits, true);
 }
 
 // Runs one step: eagerly, or through the recorded graph (recording it on the
@@ -521,8 +610,8 @@ int rnn_resnet_create(rnn_ctx *ctx, size_t depth_n, size_t width, size_t nclass,
         for (size_t i = 0; i < r->params[r->fc_w].len; i++) v[i] = v[i] * 0.5f;
     }
     // Device state: v, g, m, buffers, BN coefficients.
-    size_t ncoef = 4 * (size_t)r->stem_bn.c;
-    for (auto &b : r->blocks) ncoef += 4 * (size_t)(b.b1.c + b.b2.c + (b.down ? b.bd.c : 0));
+    size_t ncoef = 2 * (size_t)r->stem_bn.c;
+    for (auto &b : r->blocks) ncoef += 2 * (size_t)(b.b1.c + b.b2.c + (b.down ? b.bd.c : 0));
     const size_t bytes = (3 * r->np + r->nbuf + ncoef) * sizeof(float);
     void *mem = nullptr;
     hipError_t e = hipSetDevice(ctx->device);
@@ -540,7 +629,7 @@ int rnn_resnet_create(rnn_ctx *ctx, size_t depth_n, size_t width, size_t nclass,
     float *cp = r->coefs;
     auto give = [&](NetBn &bn) {
         bn.coef = cp;
-        cp += 4 * (size_t)bn.c;
+        cp += 2 * (size_t)bn.c;
     };
     give(r->stem_bn);
     for (auto &b : r->blocks) {
@@ -643,7 +732,7 @@ int rnn_resnet_backward(rnn_resnet *r, const float *dlogits) {
         return rnn_fail(ctx, RNN_E_INVALID, "resnet_backward: no train-mode forward to differentiate");
     RNN_HIP(ctx, hipMemcpyAsync(r->dlogits, dlogits, r->n * r->nclass * sizeof(float),
                                 hipMemcpyDeviceToDevice, ctx->stream));
-    return backward(r, r->dlogits);
+    return backward(r, r->dlogits, false);
 }
 
 int rnn_resnet_step(rnn_resnet *r, float lr, float momentum, float wd) {

@@ -90,39 +90,56 @@ int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, fl
 // when (k, stride, pad) has no specialisation.
 int rnn_conv_fast(rnn_ctx *ctx, int dx, const rnn_conv_spec *sp, size_t n, const float *src,
                   const float *w, float *dst);
+// dX followed by an elementwise epilogue: dx = col2im(W^T dY) (+ add), then 0
+// where mask <= 0 (add, mask may be null).
+int rnn_conv2d_backward_x_ep(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                             const float *w, float *dx, const float *add, const float *mask);
 // dW += over the batch (k = 1 or 3).
 int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
                 float *dw);
+// The same dW left as *nz partial slabs of cout*cin*k*k floats in `slabs`
+// (rnn_conv_dw_slab_floats(...) floats, 0 when the shape is unsupported);
+// their slab-order sum is added by rnn_grad_finalize_launch.
+size_t rnn_conv_dw_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n);
+int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                      const float *x, float *slabs, int *nz);
 
-// ResNet layer launchers (nn.hip).  Per-channel BN coefficients: train mode
-// uses (mean, invstd, gamma, beta); eval mode (eval = true) uses the
-// precomputed scale / shift in the mean / invstd slots.
-struct RnnBnCoef {
-    bool eval;
-    const float *mean, *invstd, *gamma, *beta;
+// ResNet layer launchers (nn.hip).  One BatchNorm2d layer's device state:
+struct RnnBn {
+    const double *part = nullptr;  // train: [c][P][2] partial sums of the layer input
+    int P = 0;                     // set by the launchers
+    float m = 0.f, mom = 0.1f, eps = 1e-5f;  // m = n*hw (set by the launchers)
+    float *mean = nullptr, *invstd = nullptr;  // batch statistics (train forward writes)
+    float *rm = nullptr, *rv = nullptr;        // running statistics (train: updated if set)
+    const float *gamma = nullptr, *beta = nullptr;
+    float *dgamma = nullptr, *dbeta = nullptr;  // backward accumulators (may be null)
 };
 // f64 elements of BN partial-sum scratch for n images of c channels.
 size_t rnn_bn_scratch_doubles(size_t n, size_t c);
-// Batch statistics: mean / invstd, and running mean / var when rm is set.
-int rnn_bn_stats_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, double *part,
-                        float *mean, float *invstd, float *rm, float *rv, float mom, float eps);
-// out = [relu](bn(x) [+ skip | + sbn(skip)]); skip_mode 0 / 1 / 2 (2 and 1
-// imply relu).
-int rnn_bn_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x,
-                        const RnnBnCoef &bn, int relu, int skip_mode, const float *skip,
-                        const RnnBnCoef &sbn, float *out);
-int rnn_bn_eval_prep_launch(rnn_ctx *ctx, size_t c, const float *gamma, const float *beta,
-                            const float *rm, const float *rv, float eps, float *sc, float *sh);
-// BN backward with relu_back by `mask` folded in (mask may be null); dgamma /
-// dbeta accumulate (may be null); dgdb[2c] is scratch.
+// Partial sums (x, x^2) per (channel, image range) into part.
+int rnn_bn_stats_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, double *part);
+// out = [relu](bn(x) [+ skip | + sbn(skip)]); skip_mode 0 / 1 / 2 (1 and 2
+// imply relu).  Train mode finalises the statistics from bn.part (and
+// sbn->part) and stores mean / invstd / running statistics; eval mode reads
+// the running statistics.
+int rnn_bn_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, RnnBn bn,
+                        bool eval, int relu, int skip_mode, const float *skip, const RnnBn *sbn,
+                        float *out);
+// BN backward with relu_back by `mask` folded in (mask may be null): partial
+// sums into `part`, then dx; bn.dgamma / bn.dbeta accumulate.
 int rnn_bn_backward_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
-                           const float *mask, const float *x, const float *mean,
-                           const float *invstd, const float *gamma, float *dx, float *dgamma,
-                           float *dbeta, double *part, float *dgdb);
+                           const float *mask, const float *x, RnnBn bn, double *part, float *dx);
 // a += [mask] b.
 int rnn_add_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *mask);
+// a = (a + b), then 0 where mask <= 0 (b may be null; relu_back_ of the sum).
+int rnn_add_mask_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *mask);
+// relu_back_ (nn.rs:432-439): d = 0 where y <= 0.
+int rnn_relu_back_launch(rnn_ctx *ctx, size_t len, float *d, const float *y);
 int rnn_gap_forward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *x, float *y);
-int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx);
+// dx = dy / hw broadcast over each plane, then 0 where mask <= 0 (mask may be
+// null: relu_back_ of the pooled feature map folded in).
+int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx,
+                            const float *mask = nullptr);
 int rnn_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
                           const float *w, const float *b, float *y);
 int rnn_fc_backward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
@@ -136,3 +153,16 @@ int rnn_softmax_ce_launch(rnn_ctx *ctx, size_t rows, size_t nclass, const float 
 int rnn_sgd_launch(rnn_ctx *ctx, size_t len, size_t ndecay, float *v, float *g, float *m, float lr,
                    float mom, float wd, const float *scal);
 int rnn_set_scalars_launch(rnn_ctx *ctx, float *scal, float a, float b, float c, float d);
+
+// One parameter tensor of a flat (v, g, m) layout for rnn_grad_finalize_launch:
+// g[off, off+len) += the slab-order sum of nz slabs (nz may be 0); blk0 is the
+// segment's first block (32 elements per block, segments in order).
+struct GradSeg {
+    long long off, len, blk0;
+    const float *slabs;
+    int nz, decay;
+};
+// Over every segment: g += slab sums; with do_sgd, then Param::step with
+// (lr, mom, wd) from scal[0..3] (wd only where decay) and g zeroed.
+int rnn_grad_finalize_launch(rnn_ctx *ctx, const GradSeg *segs, int nseg, long long nblocks,
+                             float *v, float *g, float *m, const float *scal, int do_sgd);
