@@ -198,7 +198,8 @@ int rnn_fc_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const fl
 /* softmax_ce (nn.rs:566-637): dlogits = (softmax - smoothed target) / rows;
  * *loss (device, may be NULL) = mean loss; *correct (device u32, may be NULL)
  * = rows whose first maximal logit is the label.  labels: device u32[rows].
- * rows <= 8192. */
+ * rows <= 8192, nclass <= 1024.  A label >= nclass (a panic in the reference)
+ * gives NaN for that row instead of an out-of-bounds read. */
 int rnn_softmax_ce(rnn_ctx *ctx, size_t rows, size_t nclass, const float *logits,
                    const uint32_t *labels, float smooth, float *dlogits, float *loss,
                    uint32_t *correct);
