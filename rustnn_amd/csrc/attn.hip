@@ -28,15 +28,23 @@ struct AttnArgs {
     float *dtau_part, *drel_part;  // [n][h], [n][h][nrel]
     const uint32_t *relidx;        // [tq*tk]
     const uint32_t *rowptr;        // [nrel+1] inverse index (drel gather)
-    const uint32_t *pos;           // [tq*tk]
+    const uint32_t *pos;           // [tq*tk] LDS offsets (row*LS + col), by bias slot
+    const uint32_t *rperm;         // [64][2][32] relidx in lane order (see key_of)
     long long qstride, qoff, kvstride, koff, voff;
     int n, h, dh, tq, tk, nrel, mask;
-    int TQ, TK, DHP, DHK;  // padded sizes (tiles of 32; even K for MFMA)
+    int DHP;  // dh padded to 32 or 64
 };
 
-__device__ __forceinline__ float wave_max(float v) {
+// Row reductions over the 32 lanes of a wave half (the 32 columns a 32x32
+// MFMA tile spreads over lanes): xor offsets below 32 stay inside the half.
+__device__ __forceinline__ float half_max(float v) {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float half_sum(float v) {
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
 }
 __device__ __forceinline__ float wave_sum(float v) {
@@ -45,248 +53,385 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-// acc += A * B for one 32x32 tile with A(m, k) = LA[m*sam + k*sak] and
-// B(k, n) = LB[k*sbk + n*sbn], k in [0, K) with K even.  Odd row strides keep
-// every b32 LDS read conflict-free.
-__device__ __forceinline__ void tile_mma(f32x16 &acc, const float *LA, int sam, int sak,
-                                         const float *LB, int sbk, int sbn, int K, int lane) {
-    const int l32 = lane & 31, h = lane >> 5;
-    const float *pa = LA + l32 * sam + h * sak;
-    const float *pb = LB + h * sbk + l32 * sbn;
-    for (int k0 = 0; k0 < K; k0 += 2) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[k0 * sak], pb[k0 * sbk], acc, 0, 0, 0);
-    }
-}
-
 __device__ __forceinline__ void zero16(f32x16 &a) {
 #pragma unroll
     for (int v = 0; v < 16; v++) a[v] = 0.f;
 }
 
-// Loads rows [0, rows) x cols [0, cols) of a strided matrix into LDS
-// (row stride ld), zero-padding up to prow x pcol.
-__device__ __forceinline__ void load_rows(float *dst, int ld, const float *src, long long sstride,
-                                          int rows, int cols, int prow, int pcol, int tid,
-                                          int nthreads) {
-    for (int idx = tid; idx < prow * pcol; idx += nthreads) {
-        int r = idx / pcol, c = idx - r * pcol;
-        dst[r * ld + c] = (r < rows && c < cols) ? src[r * sstride + c] : 0.f;
+// MFMA operands of a product over the head dimension (S = Q K^T, dP = dO V^T):
+// step s of lane half hh takes k = hh*HALF + s, for A and B alike, so a lane
+// holds HALF consecutive columns of one row -- a contiguous half-row.
+//
+// Loads are unconditional, from clamped (in-range) addresses.  Rows past the
+// matrix need no zeroing: they only reach score entries that are masked or
+// products with a zero P.  Columns past dh are summed over, so they are
+// zeroed (VEC = false only; VEC means dh == DHP with aligned rows, read as
+// float4).  A guarded load -- or a select the compiler may turn back into one
+// -- becomes a branch of its own, and the loads can no longer be issued
+// together.
+__device__ __forceinline__ float keep(float v, bool c) {
+    return __uint_as_float(__float_as_uint(v) & (c ? 0xffffffffu : 0u));
+}
+
+template <int HALF, bool VEC>
+__device__ __forceinline__ void load_half(float (&r)[HALF], const float *base, long long stride,
+                                          int row, int nrows, int c0, int dh) {
+    const float *p = base + (long long)min(row, nrows - 1) * stride;
+    if constexpr (VEC) {
+#pragma unroll
+        for (int i = 0; i < HALF; i += 4) {
+            const float4 t = *reinterpret_cast<const float4 *>(p + c0 + i);
+            r[i] = t.x;
+            r[i + 1] = t.y;
+            r[i + 2] = t.z;
+            r[i + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < HALF; i++) r[i] = keep(p[min(c0 + i, dh - 1)], c0 + i < dh);
     }
 }
 
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs g) {
+template <int HALF>
+__device__ __forceinline__ void mma_half(f32x16 &acc, const float (&a)[HALF],
+                                         const float (&b)[HALF]) {
+#pragma unroll
+    for (int s = 0; s < HALF; s++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc, 0, 0, 0);
+}
+
+// Rows [0, 64) x cols [0, DHP) of a strided matrix into LDS (row stride XS),
+// zero past (nrows, dh); 4-float groups with float4 loads when `vec`.
+template <int DHP>
+__device__ __forceinline__ void stage_rows(float *dst, int XS, const float *src, long long stride,
+                                           int nrows, int dh, bool vec, int tid, int nthreads) {
+    constexpr int G = DHP / 4;  // 4-float groups per row (a power of two)
+    for (int idx = tid; idx < 64 * G; idx += nthreads) {
+        const int r = idx / G, c = (idx % G) * 4;
+        float t[4] = {0.f, 0.f, 0.f, 0.f};
+        if (r < nrows) {
+            const float *p = src + (long long)r * stride + c;
+            if (vec && c + 4 <= dh) {
+                const float4 v = *reinterpret_cast<const float4 *>(p);
+                t[0] = v.x;
+                t[1] = v.y;
+                t[2] = v.z;
+                t[3] = v.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++) t[i] = c + i < dh ? p[i] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[r * XS + c + i] = t[i];
+    }
+}
+
+constexpr int LS = 65;  // LDS row stride of the 64 x 64 P / dS tiles
+
+// Transposed score tiles: S^T = K Q^T with A = K (key rows) and B = Q (query
+// rows), so in the accumulator layout lane l holds query qi = 32w + l%32 and
+// register v of key tile nt holds key kj = 32nt + 8(v/4) + 4(l/32) + v%4.  A
+// query row is then split over two lanes only (l and l ^ 32): row max and
+// sum take one cross-lane step.  And those registers are, step for step, the
+// A operand of a product over keys (O = P V, dQ = dS K): MFMA step s = 16nt
+// + v pairs key kj(s, half) for both operands.
+__device__ __forceinline__ int key_of(int nt, int v, int hh) {
+    return 32 * nt + 8 * (v >> 2) + 4 * hh + (v & 3);
+}
+
+// dst[r][d] += acc[v] for the 16 rows r = r0 + 8(v/4) + 4hh + v%4 of an
+// accumulator tile (column d): the 16 old values are loaded together (clamped
+// addresses), then added and stored where in range.
+__device__ __forceinline__ void accumulate16(float *dst, long long stride, int r0, int nrows, int d,
+                                             int dh, int hh, const f32x16 &acc) {
+    float old[16];
+    const int dc = min(d, dh - 1);
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int r = min(r0 + 8 * (v >> 2) + 4 * hh + (v & 3), nrows - 1);
+        old[v] = dst[(long long)r * stride + dc];
+    }
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int r = r0 + 8 * (v >> 2) + 4 * hh + (v & 3);
+        if (r < nrows && d < dh) dst[(long long)r * stride + d] = old[v] + acc[v];
+    }
+}
+
+// Core::forward (attn.rs:148-223) for one (image, head), tq, tk <= 64,
+// dh <= DHP (32 or 64).  Two waves; wave w owns queries [32w, 32w + 32):
+//   * S^T from half-row operands (K, Q straight from HBM into registers);
+//   * x = tau*S + rel[relidx] (the head's bias slots and the index table
+//     staged in LDS), diagonal -> -inf when masked, -inf outside (tq, tk);
+//   * softmax per query: exp(x - max) (-inf -> 0), times 1/sum (attn.rs:
+//     199-210), max and sum in-lane plus one exchange with lane ^ 32;
+//   * O = P V with P from the registers and V rows from HBM.
+template <int DHP, bool VEC>
+__global__ __launch_bounds__(128) void attn_fwd_kernel(AttnArgs g) {
+    constexpr int HALF = DHP / 2, NDT = DHP / 32;
     extern __shared__ float smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(), nthreads = blockDim.x;
+    float *Pw = smem + wave_index() * 32 * LS;  // [32][LS] P rows of this wave
+    uint32_t *rp = reinterpret_cast<uint32_t *>(smem + 64 * LS);  // [64][2][32] lane-order relidx
+    float *rels = smem + 64 * LS + 4096;        // [nrel] bias slots of the head
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_index();
+    const int l32 = lane & 31, hh = lane >> 5;
     const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
-    const int DS = g.DHP + 1, PS = g.TK + 1;
-    float *Qs = smem, *Ks = Qs + g.TQ * DS, *Vs = Ks + g.TK * DS, *Ps = Vs + g.TK * DS;
+    const int tq = g.tq, tk = g.tk, dh = g.dh;
+    const float *qb = g.q + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
+    const float *kb = g.kv + (long long)img * tk * g.kvstride + g.koff + (long long)hd * dh;
+    const float *vb = g.kv + (long long)img * tk * g.kvstride + g.voff + (long long)hd * dh;
+    const int qi = 32 * w + l32;
 
-    const float *qsrc = g.q + (long long)img * g.tq * g.qstride + g.qoff + (long long)hd * g.dh;
-    const float *ksrc = g.kv + (long long)img * g.tk * g.kvstride + g.koff + (long long)hd * g.dh;
-    const float *vsrc = g.kv + (long long)img * g.tk * g.kvstride + g.voff + (long long)hd * g.dh;
-    load_rows(Qs, DS, qsrc, g.qstride, g.tq, g.dh, g.TQ, g.DHP, tid, nthreads);
-    load_rows(Ks, DS, ksrc, g.kvstride, g.tk, g.dh, g.TK, g.DHP, tid, nthreads);
-    load_rows(Vs, DS, vsrc, g.kvstride, g.tk, g.dh, g.TK, g.DHP, tid, nthreads);
+    // Operands of S^T first (the load counter is in order: what is needed
+    // first is issued first), then the tables, then V.
+    float qb_[HALF], ka[2][HALF];
+    load_half<HALF, VEC>(qb_, qb, g.qstride, qi, tq, hh * HALF, dh);
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
+        load_half<HALF, VEC>(ka[nt], kb, g.kvstride, 32 * nt + l32, tk, hh * HALF, dh);
+    {  // relidx in lane order: 16 KB, coalesced 16-byte loads
+        const uint4 *src = reinterpret_cast<const uint4 *>(g.rperm);
+        uint4 t4[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) t4[i] = src[tid + 128 * i];
+#pragma unroll
+        for (int i = 0; i < 8; i++) reinterpret_cast<uint4 *>(rp)[tid + 128 * i] = t4[i];
+    }
+    for (int e = tid; e < g.nrel; e += blockDim.x) rels[e] = g.rel[(long long)hd * g.nrel + e];
+    f32x16 st[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++) {
+        zero16(st[nt]);
+        mma_half<HALF>(st[nt], ka[nt], qb_);
+    }
+    // V rows as the B operand of O = P V (step s = 16nt + v).
+    float vv[NDT][32];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int s2 = 0; s2 < 32; s2++) {
+            const int kj = key_of(s2 >> 4, s2 & 15, hh), d = 32 * dt + l32;
+            // rows past tk meet P = 0; columns past dh are not stored
+            vv[dt][s2] = vb[(long long)min(kj, tk - 1) * g.kvstride + min(d, dh - 1)];
+        }
     __syncthreads();
-
     const float t = g.tau[hd];
-    const float *rb = g.rel + (long long)hd * g.nrel;
-    const int l32 = lane & 31, lh = lane >> 5;
-    // S = Q K^T, epilogue x = tau*S + rel[idx], diagonal -> -inf (attn.rs:187-198)
-    const int stm = g.TQ / 32, stn = g.TK / 32;
-    if (wave < stm * stn) {
-        const int mt = wave / stn, nt = wave % stn;
-        f32x16 acc;
-        zero16(acc);
-        tile_mma(acc, Qs + mt * 32 * DS, DS, 1, Ks + nt * 32 * DS, 1, DS, g.DHK, lane);
+    float x[2][16];
+    // bias reads first, all of them (the table holds valid slots everywhere)
+    {
+        const uint4 *mine = reinterpret_cast<const uint4 *>(rp + (qi * 2 + hh) * 32);
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            int qi = mt * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), kj = nt * 32 + l32;
-            float x = -INFINITY;
-            if (qi < g.tq && kj < g.tk) {
-                x = t * acc[v] + rb[g.relidx[qi * g.tk + kj]];
-                if (g.mask && kj == qi) x = -INFINITY;
-            }
-            Ps[qi * PS + kj] = x;
+        for (int i = 0; i < 8; i++) {
+            const uint4 r4 = mine[i];
+            x[i >> 2][(i & 3) * 4 + 0] = rels[r4.x];
+            x[i >> 2][(i & 3) * 4 + 1] = rels[r4.y];
+            x[i >> 2][(i & 3) * 4 + 2] = rels[r4.z];
+            x[i >> 2][(i & 3) * 4 + 3] = rels[r4.w];
         }
     }
-    __syncthreads();
-    // Row softmax: exp(x - max) (-inf -> 0), sum, times 1/sum (attn.rs:199-210).
-    float *pg = g.pout + ((long long)img * g.h + hd) * g.tq * g.tk;
-    for (int qi = wave; qi < g.TQ; qi += nthreads >> 6) {
-        float *row = Ps + qi * PS;
-        if (qi >= g.tq) {
-            for (int kj = lane; kj < g.TK; kj += 64) row[kj] = 0.f;
-            continue;
-        }
-        float x0 = lane < g.tk ? row[lane] : -INFINITY;
-        float mx = wave_max(x0);
-        float e0 = (x0 == -INFINITY) ? 0.f : expf(x0 - mx);
-        float sum = wave_sum(e0);
-        float inv = 1.0f / sum;
-        float p0 = e0 * inv;
-        if (lane < g.TK) row[lane] = lane < g.tk ? p0 : 0.f;
-        if (lane < g.tk) pg[(long long)qi * g.tk + lane] = p0;
-    }
-    __syncthreads();
-    // O = P V (attn.rs:213-220), written at column hd*dh of o[n][tq][h*dh].
-    const int otm = g.TQ / 32, otn = g.DHP / 32;
-    if (wave < otm * otn) {
-        const int mt = wave / otn, nt = wave % otn;
-        f32x16 acc;
-        zero16(acc);
-        tile_mma(acc, Ps + mt * 32 * PS, PS, 1, Vs + nt * 32, DS, 1, g.TK, lane);
-        const int c = g.h * g.dh;
-        float *od = g.o + (long long)img * g.tq * c + (long long)hd * g.dh;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
-            int qi = mt * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), d = nt * 32 + l32;
-            if (qi < g.tq && d < g.dh) od[(long long)qi * c + d] = acc[v];
+            const int kj = key_of(nt, v, hh);
+            const bool live = qi < tq && kj < tk && !(g.mask && kj == qi);
+            const float xv = t * st[nt][v] + x[nt][v];
+            x[nt][v] = __uint_as_float(live ? __float_as_uint(xv) : 0xff800000u);  // -inf
+            mx = fmaxf(mx, x[nt][v]);
+        }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float e = x[nt][v] == -INFINITY ? 0.f : __expf(x[nt][v] - mx);
+            x[nt][v] = e;
+            sum += e;
+        }
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float p = qi < tq ? x[nt][v] * inv : 0.f;
+            x[nt][v] = p;
+            Pw[l32 * LS + key_of(nt, v, hh)] = p;
+        }
+    // P rows to HBM through LDS: one coalesced row per store instruction.
+    float *pg = g.pout + ((long long)img * g.h + hd) * tq * tk;
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
+    __builtin_amdgcn_wave_barrier();
+    const int rows = min(32, tq - 32 * w);
+    if (lane < tk) {
+        float pr[32];
+#pragma unroll
+        for (int r = 0; r < 32; r++) pr[r] = Pw[r * LS + lane];
+#pragma unroll
+        for (int r = 0; r < 32; r++)
+            if (r < rows) pg[(long long)(32 * w + r) * tk + lane] = pr[r];
+    }
+    const int c = g.h * dh;
+    float *od = g.o + (long long)img * tq * c + (long long)hd * dh;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) {
+        f32x16 acc;
+        zero16(acc);
+#pragma unroll
+        for (int s2 = 0; s2 < 32; s2++)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x[s2 >> 4][s2 & 15], vv[dt][s2], acc, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int q = 32 * w + 8 * (v >> 2) + 4 * hh + (v & 3), d = 32 * dt + l32;
+            if (q < tq && d < dh) od[(long long)q * c + d] = acc[v];
         }
     }
 }
 
-__global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs g) {
+// Core::backward (attn.rs:226-343) for one (image, head), same limits and
+// waves.  Phase 1 in registers, lane = query (as the forward): dP^T = V dO^T,
+// the recomputed raw S^T = K Q^T, P from HBM, the row dot <dP, P> (in-lane
+// plus one exchange), dS = P o (dP - dot), the dtau partial sum(dS o S).
+// dQ = tau*dS K takes dS straight from the registers and K rows from HBM.
+// P and dS go to LDS for the drel partial (inverse index, ascending
+// positions) and for dK = tau*dS^T Q and dV = P^T dO (key rows, Q and dO rows
+// from HBM).  dQ, dK, dV accumulate into HBM.
+template <int DHP, bool VEC>
+__global__ __launch_bounds__(128) void attn_bwd_kernel(AttnArgs g) {
+    constexpr int HALF = DHP / 2, NDT = DHP / 32;
     extern __shared__ float smem[];
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index(), nthreads = blockDim.x;
-    const int nwaves = nthreads >> 6;
+    float *Pl = smem, *Sl = Pl + 64 * LS, *red = Sl + 64 * LS;
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_index(), nthreads = blockDim.x;
+    const int l32 = lane & 31, hh = lane >> 5;
     const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
-    const int DS = g.DHP + 1, PS = g.TK + 1;
-    float *Qs = smem, *Ks = Qs + g.TQ * DS, *Vs = Ks + g.TK * DS, *Os = Vs + g.TK * DS;
-    float *Ps = Os + g.TQ * DS, *Ss = Ps + g.TQ * PS, *red = Ss + g.TQ * PS;
-    const int l32 = lane & 31, lh = lane >> 5;
-    const int c = g.h * g.dh;
+    const int tq = g.tq, tk = g.tk, dh = g.dh, c = g.h * dh;
+    const float *qb = g.q + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
+    const float *kb = g.kv + (long long)img * tk * g.kvstride + g.koff + (long long)hd * dh;
+    const float *vb = g.kv + (long long)img * tk * g.kvstride + g.voff + (long long)hd * dh;
+    const float *ob = g.dout + (long long)img * tq * c + (long long)hd * dh;
+    const float *pb = g.p + ((long long)img * g.h + hd) * tq * tk;
+    const int qi = 32 * w + l32;
 
-    const float *qsrc = g.q + (long long)img * g.tq * g.qstride + g.qoff + (long long)hd * g.dh;
-    const float *ksrc = g.kv + (long long)img * g.tk * g.kvstride + g.koff + (long long)hd * g.dh;
-    const float *vsrc = g.kv + (long long)img * g.tk * g.kvstride + g.voff + (long long)hd * g.dh;
-    const float *dosrc = g.dout + (long long)img * g.tq * c + (long long)hd * g.dh;
-    const float *psrc = g.p + ((long long)img * g.h + hd) * g.tq * g.tk;
-    load_rows(Qs, DS, qsrc, g.qstride, g.tq, g.dh, g.TQ, g.DHP, tid, nthreads);
-    load_rows(Ks, DS, ksrc, g.kvstride, g.tk, g.dh, g.TK, g.DHP, tid, nthreads);
-    load_rows(Vs, DS, vsrc, g.kvstride, g.tk, g.dh, g.TK, g.DHP, tid, nthreads);
-    load_rows(Os, DS, dosrc, c, g.tq, g.dh, g.TQ, g.DHP, tid, nthreads);
-    load_rows(Ps, PS, psrc, g.tk, g.tq, g.tk, g.TQ, g.TK, tid, nthreads);
-    __syncthreads();
-
-    float *dqi = g.dq + (long long)img * g.tq * g.qstride + g.qoff + (long long)hd * g.dh;
-    float *dki = g.dkv + (long long)img * g.tk * g.kvstride + g.koff + (long long)hd * g.dh;
-    float *dvi = g.dkv + (long long)img * g.tk * g.kvstride + g.voff + (long long)hd * g.dh;
-
-    // dV = P^T dO -> dkv at voff (attn.rs:270-274)
-    {
-        const int tm = g.TK / 32, tn = g.DHP / 32;
-        if (wave < tm * tn) {
-            const int mt = wave / tn, nt = wave % tn;
-            f32x16 acc;
-            zero16(acc);
-            tile_mma(acc, Ps + mt * 32, 1, PS, Os + nt * 32, DS, 1, g.TQ, lane);
+    // P of this wave's rows into LDS with coalesced row loads (0 outside).
+#pragma unroll 8
+    for (int r = 0; r < 32; r++) {
+        const int q = 32 * w + r;
+        const float t0 = pb[(long long)min(q, tq - 1) * tk + min(lane, tk - 1)];
+        Pl[q * LS + lane] = keep(t0, q < tq && lane < tk);
+    }
+    float qv[HALF], ov[HALF];
+    load_half<HALF, VEC>(qv, qb, g.qstride, qi, tq, hh * HALF, dh);
+    load_half<HALF, VEC>(ov, ob, c, qi, tq, hh * HALF, dh);
+    f32x16 dp[2], sr[2];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                int kj = mt * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), d = nt * 32 + l32;
-                if (kj < g.tk && d < g.dh) dvi[(long long)kj * g.kvstride + d] += acc[v];
-            }
-        }
+    for (int nt = 0; nt < 2; nt++) {
+        float ka[HALF], va[HALF];
+        load_half<HALF, VEC>(ka, kb, g.kvstride, 32 * nt + l32, tk, hh * HALF, dh);
+        load_half<HALF, VEC>(va, vb, g.kvstride, 32 * nt + l32, tk, hh * HALF, dh);
+        zero16(dp[nt]);
+        zero16(sr[nt]);
+        mma_half<HALF>(dp[nt], va, ov);
+        mma_half<HALF>(sr[nt], ka, qv);
     }
-    // dP = dO V^T into Ss (attn.rs:276-279)
-    {
-        const int tm = g.TQ / 32, tn = g.TK / 32;
-        if (wave < tm * tn) {
-            const int mt = wave / tn, nt = wave % tn;
-            f32x16 acc;
-            zero16(acc);
-            tile_mma(acc, Os + mt * 32 * DS, DS, 1, Vs + nt * 32 * DS, 1, DS, g.DHK, lane);
+    // K rows as the B operand of dQ = dS K (step s = 16nt + v).
+    float kk[NDT][32];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                int qi = mt * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), kj = nt * 32 + l32;
-                Ss[qi * PS + kj] = acc[v];
-            }
+    for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
+        for (int s2 = 0; s2 < 32; s2++) {
+            const int kj = key_of(s2 >> 4, s2 & 15, hh), d = 32 * dt + l32;
+            // rows past tk meet dS = 0; columns past dh are not stored
+            kk[dt][s2] = kb[(long long)min(kj, tk - 1) * g.kvstride + min(d, dh - 1)];
         }
+    // P in the accumulator layout, from this wave's LDS rows.
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+    float pv[2][16];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) pv[nt][v] = Pl[qi * LS + key_of(nt, v, hh)];
+    // dS = P o (dP - <dP, P>) (attn.rs:280-290); dtau partial (attn.rs:292-308)
+    float dot = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) dot += dp[nt][v] * pv[nt][v];
+    dot += __shfl_xor(dot, 32, 64);
+    float tpart = 0.f;
+    const float t = g.tau[hd];
+    float ds[2][16];
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int kj = key_of(nt, v, hh);
+            const float d0 = pv[nt][v] * (dp[nt][v] - dot);  // 0 outside (tq, tk): P is 0
+            tpart += d0 * sr[nt][v];
+            Sl[qi * LS + kj] = d0;
+            ds[nt][v] = d0 * t;  // attn.rs:316: dS *= tau
+        }
+    tpart = wave_sum(tpart);
+    if (lane == 0) red[w] = tpart;
+    // dQ = tau*dS K (attn.rs:319-323): queries of this lane, from registers
+    float *dqi = g.dq + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) {
+        f32x16 acc;
+        zero16(acc);
+#pragma unroll
+        for (int s2 = 0; s2 < 32; s2++)
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s2 >> 4][s2 & 15], kk[dt][s2], acc, 0, 0, 0);
+        accumulate16(dqi, g.qstride, 32 * w, tq, 32 * dt + l32, dh, hh, acc);
     }
     __syncthreads();
-    // dS = P o (dP - <dP, P>) per row (attn.rs:280-290)
-    for (int qi = wave; qi < g.TQ; qi += nwaves) {
-        float *sr = Ss + qi * PS;
-        const float *pr = Ps + qi * PS;
-        if (qi >= g.tq) {
-            for (int kj = lane; kj < g.TK; kj += 64) sr[kj] = 0.f;
-            continue;
-        }
-        float dp = lane < g.tk ? sr[lane] : 0.f, pp = lane < g.tk ? pr[lane] : 0.f;
-        float dot = wave_sum(dp * pp);
-        if (lane < g.TK) sr[lane] = lane < g.tk ? pp * (dp - dot) : 0.f;
-    }
-    __syncthreads();
-    // dtau partial: sum of dS o raw QK^T (attn.rs:292-308)
-    {
-        const int tm = g.TQ / 32, tn = g.TK / 32;
-        float part = 0.f;
-        if (wave < tm * tn) {
-            const int mt = wave / tn, nt = wave % tn;
-            f32x16 acc;
-            zero16(acc);
-            tile_mma(acc, Qs + mt * 32 * DS, DS, 1, Ks + nt * 32 * DS, 1, DS, g.DHK, lane);
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                int qi = mt * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), kj = nt * 32 + l32;
-                part += Ss[qi * PS + kj] * acc[v];  // padded entries of dS are 0
-            }
-        }
-        part = wave_sum(part);
-        if (lane == 0) red[wave] = part;
-    }
     // drel partial: gather by inverse index in ascending position (attn.rs:309-315)
     float *drp = g.drel_part + ((long long)img * g.h + hd) * g.nrel;
     for (int r = tid; r < g.nrel; r += nthreads) {
-        float s = 0.f;
-        for (uint32_t e = g.rowptr[r]; e < g.rowptr[r + 1]; e++) {
-            uint32_t ps = g.pos[e];
-            s += Ss[(ps / g.tk) * PS + ps % g.tk];
-        }
-        drp[r] = s;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float s = 0.f;
-        for (int w = 0; w < nwaves; w++) s += red[w];
-        g.dtau_part[(long long)img * g.h + hd] = s;
-    }
-    // dS *= tau (attn.rs:316)
-    const float t = g.tau[hd];
-    for (int idx = tid; idx < g.TQ * g.TK; idx += nthreads) {
-        int qi = idx / g.TK, kj = idx - qi * g.TK;
-        Ss[qi * PS + kj] *= t;
-    }
-    __syncthreads();
-    // dQ = dS K -> dq at qoff (attn.rs:319-323)
-    {
-        const int tm = g.TQ / 32, tn = g.DHP / 32;
-        if (wave < tm * tn) {
-            const int mt = wave / tn, nt = wave % tn;
-            f32x16 acc;
-            zero16(acc);
-            tile_mma(acc, Ss + mt * 32 * PS, PS, 1, Ks + nt * 32, DS, 1, g.TK, lane);
+        float sacc = 0.f;
+        const uint32_t e0 = g.rowptr[r], e1 = g.rowptr[r + 1];
+        for (uint32_t e = e0; e < e1; e += 8) {
+            uint32_t off[8];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                int qi = mt * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), d = nt * 32 + l32;
-                if (qi < g.tq && d < g.dh) dqi[(long long)qi * g.qstride + d] += acc[v];
+            for (int u = 0; u < 8; u++) off[u] = e + u < e1 ? g.pos[e + u] : 0u;
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (e + u < e1) sacc += Sl[off[u]];
+        }
+        drp[r] = sacc;
+    }
+    if (tid == 0) g.dtau_part[(long long)img * g.h + hd] = red[0] + red[1];
+    // dK = tau*dS^T Q and dV = P^T dO (attn.rs:270-274, 324-327): key rows
+    // [32w, 32w + 32), A from LDS (transposed reads), Q / dO rows from HBM.
+    float *dki = g.dkv + (long long)img * tk * g.kvstride + g.koff + (long long)hd * dh;
+    float *dvi = g.dkv + (long long)img * tk * g.kvstride + g.voff + (long long)hd * dh;
+    const int kr = 32 * w + l32;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) {
+        f32x16 ak, av;
+        zero16(ak);
+        zero16(av);
+        for (int s0 = 0; s0 < 32; s0 += 16) {
+            float qv2[16], ov2[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const int q = key_of((s0 + u) >> 4, (s0 + u) & 15, hh), d = 32 * dt + l32;
+                // rows past tq meet dS = P = 0; columns past dh are not stored
+                const int qc = min(q, tq - 1), dc = min(d, dh - 1);
+                qv2[u] = qb[(long long)qc * g.qstride + dc];
+                ov2[u] = ob[(long long)qc * c + dc];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const int q = key_of((s0 + u) >> 4, (s0 + u) & 15, hh);
+                ak = __builtin_amdgcn_mfma_f32_32x32x2f32(t * Sl[q * LS + kr], qv2[u], ak, 0, 0, 0);
+                av = __builtin_amdgcn_mfma_f32_32x32x2f32(Pl[q * LS + kr], ov2[u], av, 0, 0, 0);
             }
         }
-    }
-    // dK = dS^T Q -> dkv at koff (attn.rs:324-327)
-    {
-        const int tm = g.TK / 32, tn = g.DHP / 32;
-        if (wave < tm * tn) {
-            const int mt = wave / tn, nt = wave % tn;
-            f32x16 acc;
-            zero16(acc);
-            tile_mma(acc, Ss + mt * 32, 1, PS, Qs + nt * 32, DS, 1, g.TQ, lane);
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                int kj = mt * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), d = nt * 32 + l32;
-                if (kj < g.tk && d < g.dh) dki[(long long)kj * g.kvstride + d] += acc[v];
-            }
-        }
+        accumulate16(dki, g.kvstride, 32 * w, tk, 32 * dt + l32, dh, hh, ak);
+        accumulate16(dvi, g.kvstride, 32 * w, tk, 32 * dt + l32, dh, hh, av);
     }
 }
 
@@ -370,19 +515,30 @@ int check_desc(rnn_ctx *ctx, const rnn_attn_desc *d) {
         return rnn_fail(ctx, RNN_E_UNSUPPORTED,
                         "attn: tq=%u tk=%u dh=%u beyond the LDS-resident kernel (64/64/64)", d->tq,
                         d->tk, d->dh);
-    for (size_t i = 0; i < (size_t)d->tq * d->tk; i++)
+    // The table last uploaded was validated already.
+    const size_t cnt = (size_t)d->tq * d->tk;
+    if (ctx->rel_dev && ctx->rel_nrel == d->nrel && ctx->rel_host.size() == cnt &&
+        std::memcmp(ctx->rel_host.data(), d->relidx, cnt * 4) == 0)
+        return RNN_OK;
+    for (size_t i = 0; i < cnt; i++)
         if (d->relidx[i] >= d->nrel) return rnn_fail(ctx, RNN_E_INVALID, "attn: relidx >= nrel");
     return RNN_OK;
 }
 
-// Uploads relidx and its inverse index (CSR over bias slots) when the table
-// differs from the last one.
+// The lane-order table's place in the uploaded block: after relidx, rowptr
+// and pos, rounded up to 16 bytes.
+uint32_t *rperm_of(uint32_t *base, size_t cnt, size_t nrel) {
+    return base + rnn_round_up(cnt + (nrel + 1) + cnt, 4);
+}
+
+// Uploads relidx, its inverse index (CSR over bias slots) and the lane-order
+// table when the table differs from the last one.
 int upload_rel(rnn_ctx *ctx, const rnn_attn_desc *d) {
     size_t cnt = (size_t)d->tq * d->tk;
     if (ctx->rel_dev && ctx->rel_nrel == d->nrel && ctx->rel_host.size() == cnt &&
-        std::memcmp(ctx->rel_host.data(), d->relidx, cnt * 4) == 0)
+        ctx->rel_tk == d->tk && std::memcmp(ctx->rel_host.data(), d->relidx, cnt * 4) == 0)
         return RNN_OK;
-    size_t need = cnt + (d->nrel + 1) + cnt;
+    size_t need = cnt + (d->nrel + 1) + cnt + 4096 + 4;  // + lane-order table (16-byte aligned)
     // The previous upload (and kernels reading it) must be done before reuse.
     RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (need > ctx->rel_cap) {
@@ -404,10 +560,25 @@ int upload_rel(rnn_ctx *ctx, const rnn_attn_desc *d) {
     for (size_t i = 0; i < cnt; i++) count[d->relidx[i] + 1]++;
     for (uint32_t r = 0; r < d->nrel; r++) count[r + 1] += count[r];
     for (uint32_t r = 0; r <= d->nrel; r++) rowptr[r] = count[r];
-    for (size_t i = 0; i < cnt; i++) pos[count[d->relidx[i]]++] = (uint32_t)i;
+    // positions as offsets into the kernels' LDS [tq][LS] score tiles
+    for (size_t i = 0; i < cnt; i++)
+        pos[count[d->relidx[i]]++] = (uint32_t)((i / d->tk) * LS + i % d->tk);
+    // relidx in the forward's lane order: entry (qi*2 + half)*32 + 16nt + v is
+    // the slot of query qi, key key_of(nt, v, half); clamped into the table,
+    // so every entry is a valid slot.
+    uint32_t *rperm = rperm_of(h, cnt, d->nrel);
+    for (int q = 0; q < 64; q++)
+        for (int hf = 0; hf < 2; hf++)
+            for (int nt = 0; nt < 2; nt++)
+                for (int v = 0; v < 16; v++) {
+                    const int kj = 32 * nt + 8 * (v >> 2) + 4 * hf + (v & 3);
+                    const int qc = std::min(q, (int)d->tq - 1), kc = std::min(kj, (int)d->tk - 1);
+                    rperm[(q * 2 + hf) * 32 + 16 * nt + v] = d->relidx[(size_t)qc * d->tk + kc];
+                }
     RNN_HIP(ctx, hipMemcpyAsync(ctx->rel_dev, h, need * 4, hipMemcpyHostToDevice, ctx->stream));
     ctx->rel_host.assign(d->relidx, d->relidx + cnt);
     ctx->rel_nrel = d->nrel;
+    ctx->rel_tk = d->tk;
     return RNN_OK;
 }
 
@@ -425,24 +596,41 @@ void fill_args(AttnArgs &g, rnn_ctx *ctx, const rnn_attn_desc *d, size_t n) {
     g.tk = d->tk;
     g.nrel = d->nrel;
     g.mask = d->mask_diag ? 1 : 0;
-    g.TQ = (int)rnn_round_up(d->tq, 32);
-    g.TK = (int)rnn_round_up(d->tk, 32);
-    g.DHP = (int)rnn_round_up(d->dh, 32);
-    g.DHK = (int)rnn_round_up(d->dh, 2);
+    g.DHP = d->dh <= 32 ? 32 : 64;
     size_t cnt = (size_t)d->tq * d->tk;
     g.relidx = ctx->rel_dev;
     g.rowptr = ctx->rel_dev + cnt;
     g.pos = ctx->rel_dev + cnt + d->nrel + 1;
+    g.rperm = rperm_of(ctx->rel_dev, cnt, d->nrel);
 }
+
+inline bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// float4 row loads need 16-byte aligned row starts for every image and head.
+// VEC kernels: dh == DHP (no column padding) and float4-aligned rows.
+bool use_vec(const AttnArgs &g) {
+    return g.dh == g.DHP && g.qstride % 4 == 0 && g.qoff % 4 == 0 && al16(g.q) &&
+           g.kvstride % 4 == 0 && g.koff % 4 == 0 && g.voff % 4 == 0 && al16(g.kv) &&
+           (g.dout == nullptr || al16(g.dout));
+}
+
+size_t bwd_lds() { return ((size_t)2 * 64 * LS + 2) * 4; }
+size_t fwd_lds(size_t nrel) { return ((size_t)64 * LS + 4096 + nrel) * 4; }
 
 bool lds_attr_done = false;
 void set_lds_limits() {
     if (lds_attr_done) return;
     lds_attr_done = true;
-    (void)hipFuncSetAttribute((const void *)attn_fwd_kernel,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    (void)hipFuncSetAttribute((const void *)attn_bwd_kernel,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    const void *ks[] = {(const void *)attn_bwd_kernel<32, false>,
+                        (const void *)attn_bwd_kernel<32, true>,
+                        (const void *)attn_bwd_kernel<64, false>,
+                        (const void *)attn_bwd_kernel<64, true>,
+                        (const void *)attn_fwd_kernel<32, false>,
+                        (const void *)attn_fwd_kernel<32, true>,
+                        (const void *)attn_fwd_kernel<64, false>,
+                        (const void *)attn_fwd_kernel<64, true>};
+    for (const void *k : ks)
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
 }
 
 }  // namespace
@@ -470,9 +658,16 @@ int rnn_attn_forward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float
     g.rel = rel;
     g.pout = p;
     g.o = o;
-    size_t lds = ((size_t)g.TQ * (g.DHP + 1) + 2 * (size_t)g.TK * (g.DHP + 1) +
-                  (size_t)g.TQ * (g.TK + 1)) * 4;
-    hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)(n * d->h)), dim3(256), lds, ctx->stream, g);
+    const dim3 grid((unsigned)(n * d->h));
+    const size_t lds = fwd_lds(d->nrel);
+    if (lds > 160 * 1024)
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: nrel %u bias slots exceed LDS", d->nrel);
+    const bool vec = use_vec(g);
+    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(128), lds, ctx->stream, g); };
+    if (g.DHP == 32)
+        vec ? go(attn_fwd_kernel<32, true>) : go(attn_fwd_kernel<32, false>);
+    else
+        vec ? go(attn_fwd_kernel<64, true>) : go(attn_fwd_kernel<64, false>);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -505,9 +700,15 @@ int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const floa
     g.dkv = dkv;
     g.dtau_part = ws;
     g.drel_part = ws + n * d->h;
-    size_t lds = ((size_t)2 * g.TQ * (g.DHP + 1) + 2 * (size_t)g.TK * (g.DHP + 1) +
-                  2 * (size_t)g.TQ * (g.TK + 1) + 8) * 4;
-    hipLaunchKernelGGL(attn_bwd_kernel, dim3((unsigned)(n * d->h)), dim3(256), lds, ctx->stream, g);
+    const dim3 grid((unsigned)(n * d->h));
+    const bool vec = use_vec(g);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, dim3(128), bwd_lds(), ctx->stream, g);
+    };
+    if (g.DHP == 32)
+        vec ? go(attn_bwd_kernel<32, true>) : go(attn_bwd_kernel<32, false>);
+    else
+        vec ? go(attn_bwd_kernel<64, true>) : go(attn_bwd_kernel<64, false>);
     RNN_LAUNCHED(ctx);
     int tot = (int)(d->h * d->nrel + d->h);
     hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rnn_div_up(tot, 32)), dim3(256), 0,

@@ -30,6 +30,7 @@ struct rnn_ctx {
     uint32_t *rel_pinned = nullptr;  // staging for the async upload
     size_t rel_pinned_cap = 0;
     uint32_t rel_nrel = 0;
+    uint32_t rel_tk = 0;
     std::recursive_mutex mu;
     char err[512] = {0};
 };
