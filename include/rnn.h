@@ -242,10 +242,19 @@ int rnn_resnet_step(rnn_resnet *net, float lr, float momentum, float wd);
 /* One train step (train.rs:686-699): forward(train), softmax_ce with label
  * smoothing, backward, step.  labels: device u32[n].  loss / correct (device,
  * may be NULL) receive the mean loss and the hit count.  Replayed from a
- * hipGraph from the second call on for a given (n, h, w). */
+ * hipGraph from the second call on for a given (n, h, w).  x and labels both
+ * NULL: the batch is the one already in the network's input slots
+ * (rnn_resnet_inputs), nothing is copied. */
 int rnn_resnet_train_step(rnn_resnet *net, size_t n, size_t h, size_t w, const float *x,
                           const uint32_t *labels, float smooth, float lr, float momentum, float wd,
                           float *loss, uint32_t *correct);
+/* The network's own input slots for batches of n x 3 x h x w (planning that
+ * shape): device x[n][3][h][w] and labels u32[n] that a loader may fill in
+ * place before rnn_resnet_train_step(x = labels = NULL) -- the batch
+ * assembly of train.rs:670-684 writing straight to where the step reads.
+ * Valid until the shape changes or the network is destroyed. */
+int rnn_resnet_inputs(rnn_resnet *net, size_t n, size_t h, size_t w, float **x,
+                      uint32_t **labels);
 /* Logits of the last forward (device [n][nclass]). */
 int rnn_resnet_logits(rnn_resnet *net, float *logits);
 /* Train-step graph: enable / disable (drops a recorded graph); state 1 when a

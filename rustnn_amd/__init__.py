@@ -147,6 +147,7 @@ def lib():
             "rnn_resnet_step": (_i, [_vp, C.c_float, C.c_float, C.c_float]),
             "rnn_resnet_train_step": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, C.c_float, C.c_float,
                                            C.c_float, C.c_float, _vp, _vp]),
+            "rnn_resnet_inputs": (_i, [_vp, _sz, _sz, _sz, P(_vp), P(_vp)]),
             "rnn_resnet_logits": (_i, [_vp, _vp]),
             "rnn_resnet_set_graph": (_i, [_vp, _i]),
             "rnn_resnet_graph_state": (_i, [_vp, P(C.c_char_p)]),

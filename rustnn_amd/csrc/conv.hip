@@ -390,18 +390,6 @@ static int check_spec(rnn_ctx *ctx, const rnn_conv_spec *sp) {
 
 }  // namespace
 
-// dX then an elementwise epilogue: dx = col2im(W^T dY) + add, then 0 where
-// mask <= 0.  BasicBlock::backward (model.rs:59-77) uses it for the block
-// input gradient: the residual add_ and the relu_back_ by the block input (a
-// ReLU output) that the previous block applies first, in one pass.
-int rnn_conv2d_backward_x_ep(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
-                             const float *w, float *dx, const float *add, const float *mask) {
-    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
-    int rc = rnn_conv2d_backward_x(ctx, sp, n, dy, w, dx);
-    if (rc || n == 0 || (!add && !mask)) return rc;
-    return rnn_add_mask_launch(ctx, n * sp->cin * sp->h * sp->w, dx, add, mask);
-}
-
 extern "C" {
 
 int rnn_conv2d_forward(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,

@@ -353,34 +353,92 @@ __global__ __launch_bounds__(EW_THREADS) void add_kernel(float *a, const float *
     }
 }
 
-// a = a + b, then 0 where mask <= 0 (add_ then relu_back_, nn.rs:432-443).
-template <bool ADD, bool MASK>
-__global__ __launch_bounds__(EW_THREADS) void add_mask_kernel(float *a,
-                                                              const float *__restrict__ b,
-                                                              const float *__restrict__ mask,
-                                                              size_t total, int vec) {
-    for (size_t i = (size_t)blockIdx.x * EW_THREADS + threadIdx.x; 4 * i < total;
-         i += (size_t)gridDim.x * EW_THREADS) {
-        if (vec && 4 * i + 4 <= total) {
-            float4 av = reinterpret_cast<float4 *>(a)[i];
-            float4 bv = make_float4(0.f, 0.f, 0.f, 0.f), mv = make_float4(1.f, 1.f, 1.f, 1.f);
-            if constexpr (ADD) bv = reinterpret_cast<const float4 *>(b)[i];
-            if constexpr (MASK) mv = reinterpret_cast<const float4 *>(mask)[i];
-            float r[4] = {av.x, av.y, av.z, av.w};
-            const float bb[4] = {bv.x, bv.y, bv.z, bv.w}, mm[4] = {mv.x, mv.y, mv.z, mv.w};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if constexpr (ADD) r[j] = r[j] + bb[j];
-                if constexpr (MASK) r[j] = mm[j] <= 0.0f ? 0.0f : r[j];
+// The gradient a block's backward starts from, plus the partial sums its
+// BN backwards need (BasicBlock::backward, model.rs:59-77), in one pass over
+// channel blockIdx.x of images [p*G, p*G + G):
+//   d = relu_back_(src, mask) with src = a + add (the previous block's input
+//   gradient and its shortcut term) or, for the last block, the GAP backward
+//   gsrc[n][c] / hw broadcast over the plane;
+//   part1 = (sum d*xhat1, sum d) with xhat1 = (x1 - mean1)*invstd1 for the
+//   block's second BN, part2 likewise for its shortcut BN (when x2 is set).
+// d is written over a.
+struct ResidBn {
+    const float *x, *mean, *invstd;
+    double *part;
+};
+
+__global__ __launch_bounds__(RED_THREADS) void resid_bwd_kernel(
+    float *a, const float *__restrict__ add, const float *__restrict__ mask,
+    const float *__restrict__ gsrc, ResidBn b1, ResidBn b2, int n, int C, int hw, int G,
+    FastDiv fd_hw4, int vec) {
+    const int ci = blockIdx.x, p = blockIdx.y, P = gridDim.y;
+    const int i0 = p * G, i1 = min(n, i0 + G);
+    const float mu1 = b1.mean[ci], is1 = b1.invstd[ci];
+    const float mu2 = b2.x ? b2.mean[ci] : 0.f, is2 = b2.x ? b2.invstd[ci] : 0.f;
+    double s1 = 0.0, s2 = 0.0, sd = 0.0;
+    auto one = [&](float src, float m, float x1, float x2) {
+        const float d = m <= 0.0f ? 0.0f : src;
+        sd += (double)d;
+        s1 += (double)(d * ((x1 - mu1) * is1));
+        if (b2.x) s2 += (double)(d * ((x2 - mu2) * is2));
+        return d;
+    };
+    if (vec) {
+        const int hw4 = hw >> 2, tot = (i1 - i0) * hw4;
+        for (int e = threadIdx.x; e < tot; e += RED_THREADS) {
+            const int img = (int)div_by((uint32_t)e, fd_hw4), r = e - img * hw4;
+            const size_t q = ((size_t)(i0 + img) * C + ci) * hw4 + r;
+            float4 sv;
+            if (gsrc) {
+                const float g = gsrc[(size_t)(i0 + img) * C + ci] / (float)hw;
+                sv = make_float4(g, g, g, g);
+            } else {
+                sv = reinterpret_cast<const float4 *>(a)[q];
+                if (add) {
+                    const float4 av = reinterpret_cast<const float4 *>(add)[q];
+                    sv.x = sv.x + av.x;
+                    sv.y = sv.y + av.y;
+                    sv.z = sv.z + av.z;
+                    sv.w = sv.w + av.w;
+                }
             }
-            reinterpret_cast<float4 *>(a)[i] = make_float4(r[0], r[1], r[2], r[3]);
-        } else {
-            for (size_t j = 4 * i; j < total && j < 4 * i + 4; j++) {
-                float r = a[j];
-                if constexpr (ADD) r = r + b[j];
-                if constexpr (MASK) r = mask[j] <= 0.0f ? 0.0f : r;
-                a[j] = r;
-            }
+            const float4 mv = reinterpret_cast<const float4 *>(mask)[q];
+            const float4 x1 = reinterpret_cast<const float4 *>(b1.x)[q];
+            float4 x2 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (b2.x) x2 = reinterpret_cast<const float4 *>(b2.x)[q];
+            float4 dv;  // element order fixed: the sums run x, y, z, w
+            dv.x = one(sv.x, mv.x, x1.x, x2.x);
+            dv.y = one(sv.y, mv.y, x1.y, x2.y);
+            dv.z = one(sv.z, mv.z, x1.z, x2.z);
+            dv.w = one(sv.w, mv.w, x1.w, x2.w);
+            reinterpret_cast<float4 *>(a)[q] = dv;
+        }
+    } else {
+        const int tot = (i1 - i0) * hw;
+        for (int e = threadIdx.x; e < tot; e += RED_THREADS) {
+            const int img = e / hw, r = e - img * hw;
+            const size_t i = ((size_t)(i0 + img) * C + ci) * hw + r;
+            float src;
+            if (gsrc)
+                src = gsrc[(size_t)(i0 + img) * C + ci] / (float)hw;
+            else
+                src = add ? a[i] + add[i] : a[i];
+            a[i] = one(src, mask[i], b1.x[i], b2.x ? b2.x[i] : 0.f);
+        }
+    }
+    block_sum2(s1, sd);
+    double s2t = 0.0, dummy = 0.0;
+    if (b2.x) {
+        __syncthreads();
+        s2t = s2;
+        block_sum2(s2t, dummy);
+    }
+    if (threadIdx.x == 0) {
+        b1.part[((size_t)ci * P + p) * 2 + 0] = s1;
+        b1.part[((size_t)ci * P + p) * 2 + 1] = sd;
+        if (b2.x) {
+            b2.part[((size_t)ci * P + p) * 2 + 0] = s2t;
+            b2.part[((size_t)ci * P + p) * 2 + 1] = sd;
         }
     }
 }
@@ -422,13 +480,10 @@ __global__ void gap_fwd_kernel(const float *__restrict__ x, int hw, size_t nc, i
 }
 
 // gap_backward (nn.rs:465-473).
-__global__ void gap_bwd_kernel(const float *__restrict__ dy, int hw, size_t total,
-                               const float *__restrict__ mask, float *dx) {
+__global__ void gap_bwd_kernel(const float *__restrict__ dy, int hw, size_t total, float *dx) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const float v = dy[i / hw] / (float)hw;
-        dx[i] = (mask && mask[i] <= 0.0f) ? 0.0f : v;
-    }
+         i += (size_t)gridDim.x * blockDim.x)
+        dx[i] = dy[i / hw] / (float)hw;
 }
 
 // nn.rs Linear::forward (nn.rs:500-517): y[i][o] = b[o] + w[o][0]*x[i][0] +
@@ -802,12 +857,31 @@ int rnn_bn_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float
     return RNN_OK;
 }
 
-int rnn_bn_backward_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
-                           const float *mask, const float *x, RnnBn bn, double *part, float *dx) {
+int rnn_bn_backward_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
+                                 const float *mask, const float *x, RnnBn bn,
+                                 const double *part, float *dx) {
     if (n * c * hw == 0) return RNN_OK;
     ChanSplit s = chan_split(n, c);
     bn.P = s.P;
     bn.m = (float)(n * hw);
+    const FastDiv fd_hw4 = divider(hw / 4, (size_t)s.G * (hw / 4));
+    const dim3 grid((unsigned)c, (unsigned)s.P);
+    const int vec = (hw & 3) == 0 && aligned16(dy) && aligned16(x) && aligned16(dx) &&
+                    (!mask || aligned16(mask));
+    if (mask)
+        bn_bwd_apply_kernel<true><<<grid, EW_THREADS, 0, ctx->stream>>>(
+            dy, mask, x, bn, part, dx, (int)n, (int)c, (int)hw, s.G, fd_hw4, vec);
+    else
+        bn_bwd_apply_kernel<false><<<grid, EW_THREADS, 0, ctx->stream>>>(
+            dy, mask, x, bn, part, dx, (int)n, (int)c, (int)hw, s.G, fd_hw4, vec);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_bn_backward_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
+                           const float *mask, const float *x, RnnBn bn, double *part, float *dx) {
+    if (n * c * hw == 0) return RNN_OK;
+    ChanSplit s = chan_split(n, c);
     const FastDiv fd_hw4 = divider(hw / 4, (size_t)s.G * (hw / 4));
     const dim3 grid((unsigned)c, (unsigned)s.P);
     const int vec = (hw & 3) == 0 && aligned16(dy) && aligned16(x) && (!mask || aligned16(mask));
@@ -818,13 +892,22 @@ int rnn_bn_backward_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const fl
         bn_bwd_part_kernel<false><<<grid, RED_THREADS, 0, ctx->stream>>>(
             dy, mask, x, bn.mean, bn.invstd, (int)n, (int)c, (int)hw, vec, s.G, fd_hw4, part);
     RNN_LAUNCHED(ctx);
-    const int vec2 = vec && aligned16(dx);
-    if (mask)
-        bn_bwd_apply_kernel<true><<<grid, EW_THREADS, 0, ctx->stream>>>(
-            dy, mask, x, bn, part, dx, (int)n, (int)c, (int)hw, s.G, fd_hw4, vec2);
-    else
-        bn_bwd_apply_kernel<false><<<grid, EW_THREADS, 0, ctx->stream>>>(
-            dy, mask, x, bn, part, dx, (int)n, (int)c, (int)hw, s.G, fd_hw4, vec2);
+    return rnn_bn_backward_apply_launch(ctx, n, c, hw, dy, mask, x, bn, part, dx);
+}
+
+int rnn_resid_bwd_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, float *a, const float *add,
+                         const float *mask, const float *gsrc, const RnnBn &bn1, const float *x1,
+                         double *part1, const RnnBn *bn2, const float *x2, double *part2) {
+    if (n * c * hw == 0) return RNN_OK;
+    ChanSplit s = chan_split(n, c);
+    ResidBn b1{x1, bn1.mean, bn1.invstd, part1};
+    ResidBn b2{bn2 ? x2 : nullptr, bn2 ? bn2->mean : nullptr, bn2 ? bn2->invstd : nullptr,
+               bn2 ? part2 : nullptr};
+    const int vec = (hw & 3) == 0 && aligned16(a) && (!add || aligned16(add)) &&
+                    aligned16(mask) && aligned16(x1) && (!b2.x || aligned16(b2.x));
+    resid_bwd_kernel<<<dim3((unsigned)c, (unsigned)s.P), RED_THREADS, 0, ctx->stream>>>(
+        a, add, mask, gsrc, b1, b2, (int)n, (int)c, (int)hw, s.G,
+        divider(hw / 4, (size_t)s.G * (hw / 4)), vec);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -839,21 +922,6 @@ int rnn_add_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const flo
     else
         add_kernel<false><<<ew_grid(ctx, items), EW_THREADS, 0, ctx->stream>>>(a, b, mask, len,
                                                                                 vec);
-    RNN_LAUNCHED(ctx);
-    return RNN_OK;
-}
-
-int rnn_add_mask_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *mask) {
-    if (len == 0 || (!b && !mask)) return RNN_OK;
-    const size_t items = rnn_div_up(len, 4);
-    const int vec = aligned16(a) && (!b || aligned16(b)) && (!mask || aligned16(mask));
-    const unsigned gr = ew_grid(ctx, items);
-    if (b && mask)
-        add_mask_kernel<true, true><<<gr, EW_THREADS, 0, ctx->stream>>>(a, b, mask, len, vec);
-    else if (b)
-        add_mask_kernel<true, false><<<gr, EW_THREADS, 0, ctx->stream>>>(a, b, mask, len, vec);
-    else
-        add_mask_kernel<false, true><<<gr, EW_THREADS, 0, ctx->stream>>>(a, b, mask, len, vec);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -873,11 +941,10 @@ int rnn_gap_forward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *x, f
     return RNN_OK;
 }
 
-int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx,
-                            const float *mask) {
+int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx) {
     if (nc * hw == 0) return RNN_OK;
     gap_bwd_kernel<<<ew_grid(ctx, nc * hw), EW_THREADS, 0, ctx->stream>>>(dy, (int)hw, nc * hw,
-                                                                         mask, dx);
+                                                                         dx);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

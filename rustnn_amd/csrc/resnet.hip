@@ -18,7 +18,8 @@
 // is called for a shape and replays it from then on (RNN_GRAPH=0 disables
 // this).  Step scalars (lr, momentum, wd, label smoothing) live in device
 // memory written by a one-thread kernel before each replay; inputs are copied
-// into the network's own buffers, so the graph never sees caller pointers.
+// into the network's own input slots (or written there by the caller through
+// rnn_resnet_inputs), so the graph never sees caller pointers.
 #include "rnn_internal.h"
 
 #include <algorithm>
@@ -385,29 +386,57 @@ int conv_dw(rnn_resnet *r, const NetConv &c, const rnn_conv_spec &sp, const floa
     return rnn_conv2d_backward_w(r->ctx, &sp, r->n, dy, x, pg_of(r, c.w));
 }
 
+// The starting gradient of the BN layers that consume activation `a` of the
+// backward: the second BN of the block before block i, plus its shortcut BN
+// (i == 0: the stem BN).  resid_bwd computes their partial sums in the pass
+// that produces that gradient.
+struct ResidTarget {
+    const NetBn *b1, *b2;
+    const float *x1, *x2;
+};
+
+ResidTarget resid_target(rnn_resnet *r, size_t i) {
+    if (i == 0) return {&r->stem_bn, nullptr, r->y0, nullptr};
+    const NetBlock &p = r->blocks[i - 1];
+    return {&p.b2, p.down ? &p.bd : nullptr, p.y2, p.down ? p.ys : nullptr};
+}
+
+int resid(rnn_resnet *r, size_t i, size_t c, size_t hw, float *a, const float *add,
+          const float *mask, const float *gsrc) {
+    const ResidTarget t = resid_target(r, i);
+    const RnnBn s1 = bn_state(r, *t.b1);
+    RnnBn s2;
+    if (t.b2) s2 = bn_state(r, *t.b2);
+    return rnn_resid_bwd_launch(r->ctx, r->n, c, hw, a, add, mask, gsrc, s1, t.x1, t.b1->part,
+                                t.b2 ? &s2 : nullptr, t.x2, t.b2 ? t.b2->part : nullptr);
+}
+
 // ResNet::backward (model.rs:152-162) with BasicBlock::backward
-// (model.rs:59-77).  relu_back_ of a block's output gradient is folded into
-// the kernel that produces it: the GAP backward for the last block, and for
-// the others the pass after the next block's first dX that adds the shortcut
-// term (the residual add_) and masks by that block's input, the previous
-// block's output (or the stem's ReLU output).  relu_back_ by h is folded into
-// the first BN backward that reads c2's dX.
+// (model.rs:59-77).  A block's starting gradient d = relu_back_(.., out) is
+// produced by one pass that also takes the partial sums of the BN backwards
+// reading d (the block's second BN and its shortcut BN): for the last block
+// the GAP backward, for the others the pass after the next block's first dX
+// that adds the shortcut term (the residual add_) and masks by that block's
+// input -- the previous block's output, or the stem's ReLU output, whose BN
+// is then the one summed.  Those BN backwards then only apply dx.
+// relu_back_ by h is folded into the first BN backward that reads c2's dX.
 // The conv weight gradients are left as slabs; the finalisation adds them
 // into pg (Param::g) -- and with `sgd` also takes the Nesterov step -- in one
 // pass over all parameters.
 int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
     rnn_ctx *ctx = r->ctx;
-    const size_t n = r->n;
+    const size_t n = r->n, nb = r->blocks.size();
     TRY(rnn_fc_backward_launch(ctx, n, r->fin, r->nclass, dlogits, r->pooled, pv_of(r, r->fc_w),
                                pg_of(r, r->fc_w), pg_of(r, r->fc_b), r->dpool));
-    const float *feat = r->blocks.empty() ? r->s0 : r->blocks.back().out;
-    TRY(rnn_gap_backward_launch(ctx, n * r->fin, r->fh * r->fw, r->dpool, r->d0, feat));
+    const float *feat = nb == 0 ? r->s0 : r->blocks.back().out;
+    // GAP backward (nn.rs:465-473) masked by the last ReLU output
+    TRY(resid(r, nb, r->fin, r->fh * r->fw, r->d0, nullptr, feat, r->dpool));
     float *d = r->d0, *other = r->d1;
-    for (size_t i = r->blocks.size(); i-- > 0;) {
+    for (size_t i = nb; i-- > 0;) {
         NetBlock &b = r->blocks[i];
         const size_t hw = (size_t)b.hout * b.wout;
-        TRY(rnn_bn_backward_launch(ctx, n, b.b2.c, hw, d, nullptr, b.y2, bn_state(r, b.b2),
-                                   r->part, r->t1));
+        TRY(rnn_bn_backward_apply_launch(ctx, n, b.b2.c, hw, d, nullptr, b.y2,
+                                         bn_state(r, b.b2), b.b2.part, r->t1));
         rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
         TRY(conv_dw(r, b.c2, s2, r->t1, b.h));
         TRY(rnn_conv2d_backward_x(ctx, &s2, n, r->t1, pv_of(r, b.c2.w), r->t2));
@@ -415,25 +444,23 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
                                    r->part, r->t1));
         rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
         TRY(conv_dw(r, b.c1, s1, r->t1, b.in));
+        TRY(rnn_conv2d_backward_x(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), other));
+        const float *add = d;  // dx = c1 dX + d (add_, model.rs:72)
         if (b.down) {
-            TRY(rnn_bn_backward_launch(ctx, n, b.bd.c, hw, d, nullptr, b.ys, bn_state(r, b.bd),
-                                       r->part, r->t2));
+            TRY(rnn_bn_backward_apply_launch(ctx, n, b.bd.c, hw, d, nullptr, b.ys,
+                                             bn_state(r, b.bd), b.bd.part, r->t2));
             rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
             TRY(conv_dw(r, b.cd, sd, r->t2, b.in));
             TRY(rnn_conv2d_backward_x(ctx, &sd, n, r->t2, pv_of(r, b.cd.w), r->t3));
-            // dx = c1 dX + shortcut dX (add_, model.rs:70-71), masked by the input
-            TRY(rnn_conv2d_backward_x_ep(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), other, r->t3,
-                                         b.in));
-        } else {
-            // dx = c1 dX + d (add_, model.rs:72), masked by the input
-            TRY(rnn_conv2d_backward_x_ep(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), other, d, b.in));
+            add = r->t3;  // dx = c1 dX + shortcut dX (add_, model.rs:70-71)
         }
+        TRY(resid(r, i, b.c1.cin, (size_t)b.hin * b.win, other, add, b.in, nullptr));
         std::swap(d, other);
     }
     rnn_conv_spec sp = r->stem.spec((uint32_t)r->H, (uint32_t)r->W);
     // d is already relu_back_'d by the stem output (model.rs:159)
-    TRY(rnn_bn_backward_launch(ctx, n, r->stem_bn.c, (size_t)sp.oh * sp.ow, d, nullptr, r->y0,
-                               bn_state(r, r->stem_bn), r->part, r->t1));
+    TRY(rnn_bn_backward_apply_launch(ctx, n, r->stem_bn.c, (size_t)sp.oh * sp.ow, d, nullptr,
+                                     r->y0, bn_state(r, r->stem_bn), r->stem_bn.part, r->t1));
     // The stem's dX would be the image gradient: discarded (model.rs:161).
     TRY(conv_dw(r, r->stem, sp, r->t1, r->x));
     return rnn_grad_finalize_launch(ctx, r->segs, r->nseg, r->nseg_blocks, r->pv, r->pg, r->pm,
@@ -746,15 +773,23 @@ int rnn_resnet_train_step(rnn_resnet *r, size_t n, size_t h, size_t w, const flo
                           float *loss, uint32_t *correct) {
     if (!r) return RNN_E_NULL;
     rnn_ctx *ctx = r->ctx;
-    if (!x || !labels) return rnn_fail(ctx, RNN_E_NULL, "resnet_train_step: null pointer");
+    if (!x != !labels)
+        return rnn_fail(ctx, RNN_E_NULL, "resnet_train_step: x and labels must both be set "
+                                         "or both be NULL");
     if (!shape_ok(r, n, h, w))
         return rnn_fail(ctx, RNN_E_INVALID, "resnet_train_step: n %zu h %zu w %zu", n, h, w);
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
-    TRY(plan(r, n, h, w));
-    RNN_HIP(ctx, hipMemcpyAsync(r->x, x, n * 3 * h * w * sizeof(float), hipMemcpyDeviceToDevice,
-                                ctx->stream));
-    RNN_HIP(ctx, hipMemcpyAsync(r->labels, labels, n * sizeof(uint32_t), hipMemcpyDeviceToDevice,
-                                ctx->stream));
+    if (!x) {
+        if (!r->arena || r->n != n || r->H != h || r->W != w)
+            return rnn_fail(ctx, RNN_E_INVALID,
+                            "resnet_train_step: no input slots of this shape (rnn_resnet_inputs)");
+    } else {
+        TRY(plan(r, n, h, w));
+        RNN_HIP(ctx, hipMemcpyAsync(r->x, x, n * 3 * h * w * sizeof(float),
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+        RNN_HIP(ctx, hipMemcpyAsync(r->labels, labels, n * sizeof(uint32_t),
+                                    hipMemcpyDeviceToDevice, ctx->stream));
+    }
     TRY(rnn_set_scalars_launch(ctx, r->scal, lr, momentum, wd, smooth));
     // The first call of a plan runs eagerly (it also sizes the shared
     // workspace); the second records the graph; later calls replay it.
@@ -767,6 +802,20 @@ int rnn_resnet_train_step(rnn_resnet *r, size_t n, size_t h, size_t w, const flo
     if (correct)
         RNN_HIP(ctx, hipMemcpyAsync(correct, r->correct, sizeof(uint32_t),
                                     hipMemcpyDeviceToDevice, ctx->stream));
+    return RNN_OK;
+}
+
+int rnn_resnet_inputs(rnn_resnet *r, size_t n, size_t h, size_t w, float **x,
+                      uint32_t **labels) {
+    if (!r) return RNN_E_NULL;
+    rnn_ctx *ctx = r->ctx;
+    if (!x || !labels) return rnn_fail(ctx, RNN_E_NULL, "resnet_inputs: null pointer");
+    if (!shape_ok(r, n, h, w))
+        return rnn_fail(ctx, RNN_E_INVALID, "resnet_inputs: n %zu h %zu w %zu", n, h, w);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    TRY(plan(r, n, h, w));
+    *x = r->x;
+    *labels = r->labels;
     return RNN_OK;
 }
 

@@ -91,10 +91,6 @@ int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, fl
 // when (k, stride, pad) has no specialisation.
 int rnn_conv_fast(rnn_ctx *ctx, int dx, const rnn_conv_spec *sp, size_t n, const float *src,
                   const float *w, float *dst);
-// dX followed by an elementwise epilogue: dx = col2im(W^T dY) (+ add), then 0
-// where mask <= 0 (add, mask may be null).
-int rnn_conv2d_backward_x_ep(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
-                             const float *w, float *dx, const float *add, const float *mask);
 // dW += over the batch (k = 1 or 3).
 int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
                 float *dw);
@@ -130,17 +126,23 @@ int rnn_bn_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float
 // sums into `part`, then dx; bn.dgamma / bn.dbeta accumulate.
 int rnn_bn_backward_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
                            const float *mask, const float *x, RnnBn bn, double *part, float *dx);
+// The dx pass alone, from partial sums already in `part`.
+int rnn_bn_backward_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy,
+                                 const float *mask, const float *x, RnnBn bn,
+                                 const double *part, float *dx);
+// A block's starting gradient d = relu_back_(a + add, mask) (or, with gsrc,
+// of the GAP backward gsrc / hw), written over a, plus the BN-backward partial
+// sums of bn1 (input x1) and optionally bn2 (input x2) over d.
+int rnn_resid_bwd_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, float *a, const float *add,
+                         const float *mask, const float *gsrc, const RnnBn &bn1, const float *x1,
+                         double *part1, const RnnBn *bn2, const float *x2, double *part2);
 // a += [mask] b.
 int rnn_add_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *mask);
-// a = (a + b), then 0 where mask <= 0 (b may be null; relu_back_ of the sum).
-int rnn_add_mask_launch(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *mask);
 // relu_back_ (nn.rs:432-439): d = 0 where y <= 0.
 int rnn_relu_back_launch(rnn_ctx *ctx, size_t len, float *d, const float *y);
 int rnn_gap_forward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *x, float *y);
-// dx = dy / hw broadcast over each plane, then 0 where mask <= 0 (mask may be
-// null: relu_back_ of the pooled feature map folded in).
-int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx,
-                            const float *mask = nullptr);
+// dx = dy / hw broadcast over each plane.
+int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx);
 int rnn_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
                           const float *w, const float *b, float *y);
 int rnn_fc_backward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,

@@ -14,6 +14,15 @@ import ctypes as C
 from . import RnnError, _ptr, _sz, _i, _vp, default_ctx, lib
 
 
+class _DevArray:
+    """Device memory owned by the library, exposed to torch.as_tensor through
+    the CUDA array interface (no copy)."""
+
+    def __init__(self, ptr, shape, typestr):
+        self.__cuda_array_interface__ = {"shape": shape, "typestr": typestr, "data": (ptr, False),
+                                         "strides": None, "version": 2}
+
+
 class ResNet:
     """ResNet::new(depth_n, width, nclass, seed) (model.rs:113-135)."""
 
@@ -96,12 +105,30 @@ class ResNet:
 
     def train_step(self, x, labels, smooth, lr, mom, wd, loss=None, correct=None):
         """forward + softmax_ce + backward + step (train.rs:686-699).  loss /
-        correct: optional CUDA tensors ([1] float32 / [1] int32)."""
-        n, _, h, w = x.shape
+        correct: optional CUDA tensors ([1] float32 / [1] int32).  x and
+        labels None: the batch already written into ``inputs()``."""
+        if x is None and labels is None:
+            n, h, w = self._in_shape
+            xp = lp = None
+        else:
+            n, _, h, w = x.shape
+            xp, lp = _ptr(x, n * 3 * h * w, "x"), _ptr(labels, n, "labels")
         self.ctx.check(lib().rnn_resnet_train_step(
-            self.h, n, h, w, _ptr(x, n * 3 * h * w, "x"), _ptr(labels, n, "labels"),
-            float(smooth), float(lr), float(mom), float(wd), _ptr(loss, 1, "loss"),
-            _ptr(correct, 1, "correct")))
+            self.h, n, h, w, xp, lp, float(smooth), float(lr), float(mom), float(wd),
+            _ptr(loss, 1, "loss"), _ptr(correct, 1, "correct")))
+
+    def inputs(self, n, h, w):
+        """The network's input slots for n x 3 x h x w batches as CUDA tensors
+        (x float32 [n, 3, h, w], labels int32 [n]) over device memory the
+        network owns: fill them in place, then ``train_step(None, None, ...)``.
+        Valid until the shape changes or the network is closed."""
+        import torch
+        xp, lp = _vp(), _vp()
+        self.ctx.check(lib().rnn_resnet_inputs(self.h, n, h, w, C.byref(xp), C.byref(lp)))
+        self._in_shape = (n, h, w)
+        dev = torch.device("cuda", self.device)
+        return (torch.as_tensor(_DevArray(xp.value, (n, 3, h, w), "<f4"), device=dev),
+                torch.as_tensor(_DevArray(lp.value, (n,), "<i4"), device=dev))
 
     def set_graph(self, on):
         self.ctx.check(lib().rnn_resnet_set_graph(self.h, int(bool(on))))

@@ -133,6 +133,33 @@ def test_fused_train_step_matches_layer_calls(rnn, orc):
     b.close()
 
 
+def test_train_step_from_input_slots(rnn, orc):
+    """rnn_resnet_inputs: batches written in place into the network's input
+    slots and stepped with x = labels = NULL == the same batches passed by
+    pointer, bit for bit, through eager, recording and replay calls."""
+    import torch
+    from rustnn_amd.model import ResNet
+    n = 32
+    a, b = ResNet(3, 32, 100, 5), ResNet(3, 32, 100, 5)
+    xs, ls = a.inputs(n, 32, 32)
+    assert tuple(xs.shape) == (n, 3, 32, 32) and tuple(ls.shape) == (n,)
+    la, lb = torch.zeros(1, device="cuda"), torch.zeros(1, device="cuda")
+    for step in range(4):
+        x, labels = _cfg3_inputs(orc, n, seed=120 + step)
+        X = to_dev(x)
+        L = torch.from_numpy(labels.astype(np.int32)).cuda()
+        xs.copy_(X)
+        ls.copy_(L)
+        a.train_step(None, None, 0.1, 0.2, 0.9, 5e-4, la)
+        b.train_step(X, L, 0.1, 0.2, 0.9, 5e-4, lb)
+        assert float(to_host(la)[0]) == float(to_host(lb)[0]), step
+        assert np.array_equal(to_host(a.params()), to_host(b.params())), step
+        assert np.array_equal(to_host(a.buffers()), to_host(b.buffers())), step
+    assert a.graph_state()[0]
+    a.close()
+    b.close()
+
+
 def test_graph_replays_match_eager(rnn, orc):
     """Graph replays with eager work and synchronisation in between, each
     checked against an eager network stepping on the same inputs."""
