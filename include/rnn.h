@@ -112,6 +112,23 @@ int rnn_conv2d_backward_w(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
 int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
                           const float *w, float *dx);
 
+/* Packed weights (no counterpart in the reference: for callers that run
+ * several forward / dX convolutions between weight updates, such as a train
+ * step).  rnn_conv_pack_weights rewrites W into the slab order the forward
+ * (dx = 0) or dX (dx = 1) kernel stages through LDS, so that each stage's
+ * weights arrive as one contiguous copy; *floats receives the packed size
+ * (RNN_E_UNSUPPORTED: the shape has no packed form, use the calls above).
+ * The _packed calls take W and its packed copy wp and give results identical
+ * to rnn_conv2d_forward / rnn_conv2d_backward_x; wp must be re-packed after
+ * W changes. */
+int rnn_conv_packed_floats(const rnn_conv_spec *sp, int dx, size_t *floats);
+int rnn_conv_pack_weights(rnn_ctx *ctx, const rnn_conv_spec *sp, int dx, const float *w,
+                          float *wp);
+int rnn_conv2d_forward_packed(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
+                              const float *w, const float *wp, float *y);
+int rnn_conv2d_backward_x_packed(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                                 const float *w, const float *wp, float *dx);
+
 /* ------------------------------------------------------------ attn.rs */
 /* Core (attn.rs:74-84) plus the stride/offset arguments of Core::forward /
  * Core::backward (attn.rs:148-160, 226-242).  Rows of head hd are read at

@@ -107,6 +107,10 @@ def lib():
                                             _vp, _sz, _i]),
             "rnn_matmul_dw": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp]),
             "rnn_conv_spec_init": (_i, [P(ConvSpec), _u32, _u32, _u32, _u32, _u32, _u32, _u32]),
+            "rnn_conv_packed_floats": (_i, [P(ConvSpec), _i, P(_sz)]),
+            "rnn_conv_pack_weights": (_i, [_vp, P(ConvSpec), _i, _vp, _vp]),
+            "rnn_conv2d_forward_packed": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp, _vp]),
+            "rnn_conv2d_backward_x_packed": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp, _vp]),
             "rnn_conv2d_forward": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
             "rnn_conv2d_backward_w": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
             "rnn_conv2d_backward_x": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
@@ -311,6 +315,40 @@ def conv2d_backward_x(sp: ConvSpec, n, dy, w, dx=None, ctx=None):
                                           _ptr(dy, n * sp.cout * sp.hw, "dy"),
                                           _ptr(w, sp.cout * sp.ckk, "w"),
                                           _ptr(dx, n * sp.cin * sp.h * sp.w, "dx")))
+    return dx
+
+
+def conv_pack_weights(sp: ConvSpec, dx, w, ctx=None):
+    """Packed copy of W for the forward (dx=0) or dX (dx=1) kernel, or None
+    when the shape has no packed form."""
+    import torch
+    ctx = ctx or default_ctx()
+    nf = _sz()
+    if lib().rnn_conv_packed_floats(C.byref(sp), int(dx), C.byref(nf)) != 0:
+        return None
+    wp = torch.empty(int(nf.value), dtype=torch.float32, device=w.device)
+    ctx.check(lib().rnn_conv_pack_weights(ctx.h, C.byref(sp), int(dx),
+                                          _ptr(w, sp.cout * sp.ckk, "w"), _ptr(wp, 0, "wp")))
+    return wp
+
+
+def conv2d_forward_packed(sp: ConvSpec, n, x, w, wp, y=None, ctx=None):
+    ctx = ctx or default_ctx()
+    y = _new(n * sp.cout * sp.hw, x) if y is None else y
+    ctx.check(lib().rnn_conv2d_forward_packed(ctx.h, C.byref(sp), n,
+                                              _ptr(x, n * sp.cin * sp.h * sp.w, "x"),
+                                              _ptr(w, sp.cout * sp.ckk, "w"), _ptr(wp, 0, "wp"),
+                                              _ptr(y, n * sp.cout * sp.hw, "y")))
+    return y
+
+
+def conv2d_backward_x_packed(sp: ConvSpec, n, dy, w, wp, dx=None, ctx=None):
+    ctx = ctx or default_ctx()
+    dx = _new(n * sp.cin * sp.h * sp.w, dy) if dx is None else dx
+    ctx.check(lib().rnn_conv2d_backward_x_packed(ctx.h, C.byref(sp), n,
+                                                 _ptr(dy, n * sp.cout * sp.hw, "dy"),
+                                                 _ptr(w, sp.cout * sp.ckk, "w"), _ptr(wp, 0, "wp"),
+                                                 _ptr(dx, n * sp.cin * sp.h * sp.w, "dx")))
     return dx
 
 

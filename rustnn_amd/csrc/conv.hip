@@ -394,13 +394,25 @@ extern "C" {
 
 int rnn_conv2d_forward(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
                        const float *w, float *y) {
+    return rnn_conv2d_forward_wp(ctx, sp, n, x, w, nullptr, y);
+}
+
+int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                          const float *w, float *dx) {
+    return rnn_conv2d_backward_x_wp(ctx, sp, n, dy, w, nullptr, dx);
+}
+
+}  // extern "C"
+
+int rnn_conv2d_forward_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
+                          const float *w, const float *wp, float *y) {
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     int rc = check_spec(ctx, sp);
     if (rc) return rc;
     if (n == 0) return RNN_OK;
     if (!x || !w || !y) return rnn_fail(ctx, RNN_E_NULL, "conv2d_forward: null operand");
-    rc = rnn_conv_fast(ctx, 0, sp, n, x, w, y);
+    rc = rnn_conv_fast(ctx, 0, sp, n, x, w, wp, y);
     if (rc != RNN_E_UNSUPPORTED) return rc;
     set_lds_limits();
     const int K = sp->k, KK = K * K;
@@ -413,15 +425,15 @@ int rnn_conv2d_forward(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const fl
                     sp->ow, 1, 0, 0, sp->stride, taps, KK, w, sp->cin * KK, KK, K);
 }
 
-int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
-                          const float *w, float *dx) {
+int rnn_conv2d_backward_x_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                             const float *w, const float *wp, float *dx) {
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     int rc = check_spec(ctx, sp);
     if (rc) return rc;
     if (n == 0) return RNN_OK;
     if (!dy || !w || !dx) return rnn_fail(ctx, RNN_E_NULL, "conv2d_backward_x: null operand");
-    rc = rnn_conv_fast(ctx, 1, sp, n, dy, w, dx);
+    rc = rnn_conv_fast(ctx, 1, sp, n, dy, w, wp, dx);
     if (rc != RNN_E_UNSUPPORTED) return rc;
     set_lds_limits();
     const int K = sp->k, S = sp->stride, P = sp->pad, KK = K * K;
@@ -447,6 +459,43 @@ int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
             if (rc) return rc;
         }
     return RNN_OK;
+}
+
+extern "C" {
+
+int rnn_conv_packed_floats(const rnn_conv_spec *sp, int dx, size_t *floats) {
+    if (!sp || !floats) return RNN_E_NULL;
+    PackGeo pg;
+    const int rc = rnn_conv_pack_geo(sp, dx, &pg);
+    *floats = rc ? 0 : pg.floats();
+    return rc;
+}
+
+int rnn_conv_pack_weights(rnn_ctx *ctx, const rnn_conv_spec *sp, int dx, const float *w,
+                          float *wp) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    int rc = check_spec(ctx, sp);
+    if (rc) return rc;
+    if (!w || !wp) return rnn_fail(ctx, RNN_E_NULL, "conv_pack_weights: null operand");
+    rc = rnn_conv_pack(ctx, sp, dx, w, wp);
+    if (rc == RNN_E_UNSUPPORTED)
+        return rnn_fail(ctx, rc, "conv_pack_weights: no packed form for k %u stride %u pad %u",
+                        sp->k, sp->stride, sp->pad);
+    return rc;
+}
+
+int rnn_conv2d_forward_packed(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
+                              const float *w, const float *wp, float *y) {
+    if (!wp) return ctx ? rnn_fail(ctx, RNN_E_NULL, "conv2d_forward_packed: null wp") : RNN_E_NULL;
+    return rnn_conv2d_forward_wp(ctx, sp, n, x, w, wp, y);
+}
+
+int rnn_conv2d_backward_x_packed(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                                 const float *w, const float *wp, float *dx) {
+    if (!wp)
+        return ctx ? rnn_fail(ctx, RNN_E_NULL, "conv2d_backward_x_packed: null wp") : RNN_E_NULL;
+    return rnn_conv2d_backward_x_wp(ctx, sp, n, dy, w, wp, dx);
 }
 
 int rnn_conv2d_backward_w(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,

@@ -45,6 +45,8 @@ struct WinRows {
 struct FastArgs {
     const float *src;  // [N][CS][HS][WS]
     const float *w;    // [cout][cin][k][k]
+    const float *wp;   // the same weights packed in slab order (conv_pack), or null
+    int wpbytes;       // bytes of wp
     float *dst;        // [N][CD][HD][WD]
     int N, CS, HS, WS;
     int CD, HD, WD;
@@ -58,7 +60,7 @@ struct FastArgs {
     int plane;         // window positions per channel quad (multiple of 64)
     int ppw;           // plane / 64: window rows per quad and wave
     int xwords;        // LDS words of the window: CH * plane
-    int stage;         // LDS words of one stage: window, weight slabs, 64-word sink
+    int stage;         // LDS words of one stage: window, then weight slabs
     TileGeo geo;       // window geometry in positions (chs unused)
     int tapoff[9];     // window-position offset of each tap
     uint32_t m_imgs, m_tiwp;  // FastDiv multipliers of geo.imgs and geo.TIWP
@@ -68,8 +70,6 @@ struct FastArgs {
 struct StageDMA {
     __amdgpu_buffer_rsrc_t rs;  // source images n0 .. n0 + IMGS
     float *buf;                 // stage buffer
-    float *sink;                // 64 words no compute reads (rows without data)
-    int valid;                  // 0: no stage; every row goes to the sink
     int c0, grp;                // first source channel, output-channel group
     int ebase;                  // element offset of window row 0 in image n0 (may be < 0)
     int ylo, yhi;               // window rows inside the source image
@@ -82,11 +82,6 @@ __device__ __forceinline__ StageDMA stage_dma(const FastArgs &g, int item, int c
                                               float *buf) {
     using T = ConvTaps<K, S, P, DX>;
     StageDMA d;
-    d.valid = item >= 0;
-    if (!d.valid) {
-        item = 0;
-        chunk = 0;
-    }
     const int tile = item % g.ntiles;
     d.grp = item / g.ntiles;
     const int n0 = (tile / g.tiles_a) * g.geo.IMGS;
@@ -96,14 +91,13 @@ __device__ __forceinline__ StageDMA stage_dma(const FastArgs &g, int item, int c
     d.rs = make_rsrc(g.src + (long long)n0 * img_elems,
                      (uint32_t)(min(g.N - n0, g.geo.IMGS) * img_elems * 4));
     d.buf = buf;
-    d.sink = buf + g.stage - 64;
     d.c0 = chunk * g.CH;
     d.ebase = y0 * g.WS;
     d.ylo = y0 >= 0 ? 0 : (-y0 + rowstep - 1) / rowstep;
     d.yhi = min(g.geo.TIH, (g.HS - y0 + rowstep - 1) / rowstep);
     if (d.yhi < d.ylo) d.yhi = d.ylo;
-    d.nimg = d.valid ? min(g.N - n0, g.geo.IMGS) : 0;
-    d.mlim = d.valid ? g.CD - d.grp * SL * 32 : 0;
+    d.nimg = min(g.N - n0, g.geo.IMGS);
+    d.mlim = g.CD - d.grp * SL * 32;
     return d;
 }
 
@@ -113,6 +107,10 @@ struct LaneDMA {
     int toff[WinRows<KK>::MAX];   // window row u: element offset in the tile, channel lane&3
     int tmeta[WinRows<KK>::MAX];  // window row ty | img << 8 (ty = 255: no source element)
     int wl;                       // weight row: (lane/4)*sm + (lane%4)*sc
+    // Per work item: byte offset of window row u for channel lane&3 of
+    // channel 0, or an offset >= 2^31 (beyond any buffer) when the row has
+    // no source data.  A stage adds its channel's byte offset.
+    uint32_t roff[WinRows<KK>::MAX];
 };
 
 template <int KK>
@@ -138,58 +136,43 @@ __device__ __forceinline__ void lane_dma_init(const FastArgs &g, LaneDMA<KK> &L,
     L.wl = (lane >> 2) * g.sm + i * g.sc;
 }
 
-// Issues the DMA rows assigned to step (q, t) of stage d: the weight rows
-// (mb, q, t) of this wave and the window rows u = t, t + KK, ... of quads q
-// and CQ + q.  Rows beyond the stage go to the sink with every lane out of
-// range (no memory traffic), which keeps the step free of branches.
+// Weight rows (mb, q, TT) of stage d gathered from W in [cout][cin][k][k]
+// order: 64-word row `wave` of each slab, lane l = wave*16 + lane/4.
 template <int KK, int SL, int TT>
-__device__ __forceinline__ void issue_step(const FastArgs &g, const StageDMA &d,
-                                           const LaneDMA<KK> &L, __amdgpu_buffer_rsrc_t rs_w,
-                                           int q, int wave, int lane) {
+__device__ __forceinline__ void issue_w_gather(const FastArgs &g, const StageDMA &d,
+                                               const LaneDMA<KK> &L, __amdgpu_buffer_rsrc_t rs_w,
+                                               int q, int wave, int lane) {
     const int CP = g.CH >> 1, cq = g.CH >> 3;
-    // weights: slab (mb, q, TT), 64-word row `wave`: lane l = wave*16 + lane/4
 #pragma unroll
     for (int mb = 0; mb < SL; mb++) {
         const int mrel = mb * 32 + (wave & 1) * 16;
         const int cbase = d.c0 + (wave >> 1) * CP + 4 * q;
         const bool ok = (lane >> 2) < d.mlim - mrel && (lane & 3) < g.CS - cbase;
         const int e = L.wl + (d.grp * SL * 32 + mrel) * g.sm + cbase * g.sc + TT;
-        const uint32_t off = ok ? (uint32_t)e * 4u : DMA_OOB;
-        float *dst = d.valid ? d.buf + g.xwords + ((mb * cq + q) * KK + TT) * 256 + wave * 64
-                             : d.sink;
+        const uint32_t off = max((uint32_t)e * 4u, ok ? 0u : DMA_OOB);
+        float *dst = d.buf + g.xwords + ((mb * cq + q) * KK + TT) * 256 + wave * 64;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, (lds_ptr_t)dst, 4, off, 0, 0, 0);
     }
-    // window rows
-    static_for<0, (WinRows<KK>::MAX - TT + KK - 1) / KK>([&](auto jc) {
-        constexpr int u = TT + KK * decltype(jc)::value;
-        const int ty = L.tmeta[u] & 255, img = L.tmeta[u] >> 8;
-        const bool rowok = (unsigned)(ty - d.ylo) < (unsigned)(d.yhi - d.ylo) && img < d.nimg;
-        const bool live = d.valid && u < g.ppw;
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++) {
-            const int hq = hh * cq + q;
-            const int cb = d.c0 + 4 * hq;
-            const bool ok = rowok && (lane & 3) < g.CS - cb;
-            const int e = L.toff[u] + cb * (g.HS * g.WS) + d.ebase;
-            const uint32_t off = ok ? (uint32_t)e * 4u : DMA_OOB;
-            float *dst = live ? d.buf + (hq * g.plane + (wave + FAST_NW * u) * 16) * 4 : d.sink;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(d.rs, (lds_ptr_t)dst, 4, off, 0, 0, 0);
-        }
-    });
 }
 
-// One stage of the GEMM: (quad q, tap t) steps over the window `xs` and the
-// weight slabs of the current buffer; step (q, t) also issues its share of
-// the next stage's DMA into `nxt`, so that the address arithmetic and memory
-// traffic run under the MFMAs.  `xs` and `nxt` are distinct buffers: the
-// __restrict__ qualifiers give the compiler the alias scopes it needs to not
-// wait for the DMA before the LDS reads.
+// The per-item window row offsets (LaneDMA::roff) of stage d's work item.
+template <int KK>
+__device__ __forceinline__ void item_rows(const FastArgs &g, const StageDMA &d, LaneDMA<KK> &L) {
+#pragma unroll
+    for (int u = 0; u < WinRows<KK>::MAX; u++) {
+        const int ty = L.tmeta[u] & 255, img = L.tmeta[u] >> 8;
+        const bool rowok = (unsigned)(ty - d.ylo) < (unsigned)(d.yhi - d.ylo) && img < d.nimg;
+        L.roff[u] = rowok ? (uint32_t)(L.toff[u] + d.ebase) * 4u : 0x80000000u;
+    }
+}
+
+// One stage of the GEMM on the MFMA waves: (quad q, tap t) steps over the
+// window `xs` and the weight slabs of the current buffer, the operands of the
+// next step read from LDS while the MFMAs of the current one run.
 template <int K, int S, int P, bool DX, int NPW, int MB, int WM, int NACC>
-__device__ __forceinline__ void run_stage(
-    const FastArgs &g, const float *__restrict__ xs, float *__restrict__ nxt, int nitem,
-    int nchunk, const LaneDMA<ConvTaps<K, S, P, DX>::KK> &L, const int (&vb)[NPW],
-    f32x16 (&acc)[ConvTaps<K, S, P, DX>::NCLS][MB][NPW][NACC], int wave, int lane,
-    __amdgpu_buffer_rsrc_t rs_w) {
+__device__ __forceinline__ void compute_stage(
+    const FastArgs &g, const float *__restrict__ xs, const int (&vb)[NPW],
+    f32x16 (&acc)[ConvTaps<K, S, P, DX>::NCLS][MB][NPW][NACC], int wave, int lane) {
     using T = ConvTaps<K, S, P, DX>;
     constexpr int KK = T::KK;
     const int CQ = g.CH >> 3;
@@ -197,7 +180,6 @@ __device__ __forceinline__ void run_stage(
     const float *ws = xs + g.xwords + lane * 4;
     constexpr int WP = FAST_NW / WM;  // waves along positions
     const float *wsw = ws + (wave / WP) * MB * wslab;  // this wave's m-blocks
-    const StageDMA d = stage_dma<K, S, P, DX, WM * MB>(g, nitem, nchunk, nxt);
 
     auto fetch = [&](int q, int t, float4 *fa, float4 *fb) {
 #pragma unroll
@@ -218,7 +200,6 @@ __device__ __forceinline__ void run_stage(
                 fetch(q, t + 1 < KK ? t + 1 : 0, na, nb);
             else if (q + 1 < CQ)
                 fetch(q + 1, 0, na, nb);
-            issue_step<KK, WM * MB, t>(g, d, L, rs_w, q, wave, lane);
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -235,23 +216,59 @@ __device__ __forceinline__ void run_stage(
     }
 }
 
-// Stage 0 of the first work item, issued in full before any compute.
+// All DMA of stage `chunk` of the work item described by d (its window
+// rows in L.roff) into `buf`, issued by producer wave `dw`: the window rows
+// u = dw, dw + 4, ... of every channel quad, then the weights -- contiguous
+// 1 KiB slabs of the packed copy, 16 bytes a lane, or gathered from W.
 template <int K, int S, int P, bool DX, int SL>
-__device__ __forceinline__ void issue_prologue(const FastArgs &g, float *__restrict__ buf,
-                                               int item, const LaneDMA<ConvTaps<K, S, P, DX>::KK> &L,
-                                               __amdgpu_buffer_rsrc_t rs_w, int wave, int lane) {
+__device__ __forceinline__ void issue_stage(const FastArgs &g, StageDMA d, float *buf, int chunk,
+                                            const LaneDMA<ConvTaps<K, S, P, DX>::KK> &L,
+                                            __amdgpu_buffer_rsrc_t rs_w, int dw, int lane) {
     constexpr int KK = ConvTaps<K, S, P, DX>::KK;
-    const StageDMA d = stage_dma<K, S, P, DX, SL>(g, item, 0, buf);
-    for (int q = 0; q < (g.CH >> 3); q++)
-        static_for<0, KK>([&](auto tc) {
-            issue_step<KK, SL, decltype(tc)::value>(g, d, L, rs_w, q, wave, lane);
-        });
+    const int cq = g.CH >> 3;
+    d.buf = buf;
+    d.c0 = chunk * g.CH;
+    const uint32_t hsws4 = (uint32_t)(g.HS * g.WS) * 4u;
+    for (int hq = 0; hq < 2 * cq; hq++) {
+        const int cb = d.c0 + 4 * hq;
+        const uint32_t cbytes = (uint32_t)cb * hsws4;
+        // lanes whose channel cb + lane%4 is beyond the source get no data
+        const uint32_t chbad = g.CS - cb >= 4 ? 0u : ((lane & 3) >= g.CS - cb ? 0x80000000u : 0u);
+        float *row0 = buf + (hq * g.plane + dw * 16) * 4;
+#pragma unroll
+        for (int u = 0; u < WinRows<KK>::MAX; u++)
+            if (u < g.ppw)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    d.rs, (lds_ptr_t)(row0 + FAST_NW * u * 64), 4, (L.roff[u] + cbytes) | chbad, 0,
+                    0, 0);
+    }
+    if (g.wp) {
+        const int per = cq * KK;
+        const __amdgpu_buffer_rsrc_t rs_p = make_rsrc(g.wp, (uint32_t)g.wpbytes);
+        for (int k = dw; k < SL * per; k += FAST_NW) {
+            const int mb = k / per, r = k - mb * per;
+            const uint32_t src =
+                (uint32_t)(((d.grp * SL + mb) * g.nchunks + chunk) * per + r) * 1024u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_p, (lds_ptr_t)(buf + g.xwords + k * 256),
+                                                     16, src + (uint32_t)lane * 16u, 0, 0, 0);
+        }
+    } else {
+        for (int q = 0; q < cq; q++)
+            static_for<0, KK>([&](auto tc) {
+                issue_w_gather<KK, SL, decltype(tc)::value>(g, d, L, rs_w, q, dw, lane);
+            });
+    }
 }
 
-// Waves: WP = 4 / WM along positions (NPW groups of 32 each) times WM along
-// output channels (MB blocks of 32 each).
+// Waves 0..3 compute: WP = 4 / WM along positions (NPW groups of 32 each)
+// times WM along output channels (MB blocks of 32 each).  Waves 4..7 only
+// move data: producer wave 4 + w issues the DMA rows that the row tables
+// assign to wave w, a whole stage at a time, so that the memory pipeline's
+// back-pressure stalls a producer and never the MFMA issue of a compute
+// wave.  One barrier per stage: when it completes, stage s has landed (each
+// producer waited for its own DMA) and stage s - 1's buffer is free.
 template <int K, int S, int P, bool DX, int NPW, int MB, int WM>
-__global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
+__global__ __launch_bounds__(64 * FAST_NW * 2) void conv_fast_kernel(FastArgs g) {
     using T = ConvTaps<K, S, P, DX>;
     constexpr int NCLS = T::NCLS;
     // A wave with a single output block alternates two accumulators so that
@@ -265,10 +282,32 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
     const int tpix = g.TR * g.GB, npix = g.geo.IMGS * tpix;
     const int nitems = g.ntiles * g.ngroups;
     if ((int)blockIdx.x >= nitems) return;
-    const __amdgpu_buffer_rsrc_t rs_w = make_rsrc(g.w, (uint32_t)g.wbytes);
 
-    LaneDMA<T::KK> L;
-    lane_dma_init<T::KK>(g, L, wave, lane);
+    if (wave >= FAST_NW) {
+        // producer
+        const int dw = wave - FAST_NW;
+        const __amdgpu_buffer_rsrc_t rs_w = make_rsrc(g.w, (uint32_t)g.wbytes);
+        LaneDMA<T::KK> L;
+        lane_dma_init<T::KK>(g, L, dw, lane);
+        StageDMA d = stage_dma<K, S, P, DX, SL>(g, blockIdx.x, 0, smem);
+        item_rows<T::KK>(g, d, L);
+        issue_stage<K, S, P, DX, SL>(g, d, smem, 0, L, rs_w, dw, lane);
+        int s = 0;
+        for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
+            for (int chunk = 0; chunk < g.nchunks; chunk++, s++) {
+                dma_wait_barrier();
+                float *nbuf = smem + ((s + 1) & 1) * g.stage;
+                if (chunk + 1 < g.nchunks) {
+                    issue_stage<K, S, P, DX, SL>(g, d, nbuf, chunk + 1, L, rs_w, dw, lane);
+                } else if (item + (int)gridDim.x < nitems) {
+                    d = stage_dma<K, S, P, DX, SL>(g, item + gridDim.x, 0, nbuf);
+                    item_rows<T::KK>(g, d, L);
+                    issue_stage<K, S, P, DX, SL>(g, d, nbuf, 0, L, rs_w, dw, lane);
+                }
+            }
+        }
+        return;
+    }
 
     // LDS word offset of this lane's channel half and window position for
     // each 32-position group (tile-relative: the same for every work item).
@@ -281,7 +320,6 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
         vb[j] = (h * CQ * g.plane + img * g.geo.imgs + r * g.lrow * g.geo.TIWP + c * g.lcol) * 4;
     }
 
-    issue_prologue<K, S, P, DX, SL>(g, smem, blockIdx.x, L, rs_w, wave, lane);
     f32x16 acc[NCLS][MB][NPW][NACC];
     int s = 0;
     for (int item = blockIdx.x; item < nitems; item += gridDim.x) {
@@ -297,18 +335,10 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
                         for (int v = 0; v < 16; v++) acc[c][mb][j][a][v] = 0.f;
         for (int chunk = 0; chunk < g.nchunks; chunk++, s++) {
             // Stage s has landed and every wave is done with stage s-1, whose
-            // buffer receives stage s+1 while stage s is computed.
+            // buffer the producers fill with stage s+1 while stage s is computed.
             dma_wait_barrier();
-            int nitem = -1, nchunk = 0;
-            if (chunk + 1 < g.nchunks) {
-                nitem = item;
-                nchunk = chunk + 1;
-            } else if (item + (int)gridDim.x < nitems) {
-                nitem = item + gridDim.x;
-            }
-            run_stage<K, S, P, DX, NPW, MB, WM, NACC>(g, smem + (s & 1) * g.stage,
-                                                  smem + ((s + 1) & 1) * g.stage, nitem, nchunk,
-                                                  L, vb, acc, wave, lane, rs_w);
+            compute_stage<K, S, P, DX, NPW, MB, WM, NACC>(g, smem + (s & 1) * g.stage, vb, acc,
+                                                          wave, lane);
         }
         // acc row 8*(v/4) + 4*h + v%4 = output channel in the block, column = position.
         const int tile = item % g.ntiles, grp = item / g.ntiles;
@@ -370,9 +400,6 @@ __global__ __launch_bounds__(256) void conv_fast_kernel(FastArgs g) {
             }
         }
     }
-    // The last stage sent its (empty) DMA rows to the sink: let them land
-    // before the workgroup's LDS is released.
-    __builtin_amdgcn_s_waitcnt(0);
 }
 
 struct FastPlan {
@@ -424,7 +451,7 @@ static size_t plan_geometry(const FastPlan &p, int GB, FastArgs &a) {
     a.m_imgs = t.fd_imgstr.m;
     a.m_tiwp = t.fd_tiwp.m;
     a.xwords = p.CH * a.plane;
-    a.stage = a.xwords + p.WM * p.MB * p.CH * T::KK * 32 + 64;
+    a.stage = a.xwords + p.WM * p.MB * p.CH * T::KK * 32;
     return (size_t)2 * a.stage * 4;
 }
 
@@ -516,26 +543,12 @@ static void set_attr() {
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
 }
 
+// Operand roles, geometry and tile plan of a (k, stride, pad) forward / dX
+// convolution; false when no plan fits.
 template <int K, int S, int P, bool DX>
-static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src, const float *w,
-                  float *dst) {
+static bool setup(const rnn_conv_spec *sp, FastArgs &a, FastPlan &p) {
     using T = ConvTaps<K, S, P, DX>;
-    static bool attr = false;
-    if (!attr) {
-        attr = true;
-        set_attr<K, S, P, DX, 1, 1, 1>();
-        set_attr<K, S, P, DX, 1, 1, 2>();
-        if constexpr (T::NCLS == 1) {
-            set_attr<K, S, P, DX, 2, 1, 1>();
-            set_attr<K, S, P, DX, 1, 2, 1>();
-        }
-    }
-    FastArgs a;
     std::memset(&a, 0, sizeof(a));
-    a.src = src;
-    a.w = w;
-    a.dst = dst;
-    a.N = n;
     const int cin = sp->cin, cout = sp->cout;
     if (!DX) {
         a.CS = cin;
@@ -560,17 +573,58 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
         a.sm = T::KK;  // W^T: m = cin, ch = cout
         a.sc = cin * T::KK;
     }
-    const long long wbytes = (long long)cout * cin * T::KK * 4;
-    FastPlan p;
-    if (!choose_plan<K, S, P, DX>(a.CS, a.CD, a.GA, a.GB, p, a))
-        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: no LDS tiling for a %dx%d grid", a.GA, a.GB);
-    if ((long long)p.IMGS * a.CS * a.HS * a.WS * 4 >= 0x7FFFFFF0ll || wbytes >= 0x7FFFFFF0ll)
-        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: tile source or weights beyond 2 GiB");
-    a.wbytes = (int)wbytes;
+    if (!choose_plan<K, S, P, DX>(a.CS, a.CD, a.GA, a.GB, p, a)) return false;
     a.TR = p.TR;
     a.tiles_a = (a.GA + p.TR - 1) / p.TR;
     a.CH = p.CH;
     a.nchunks = (a.CS + p.CH - 1) / p.CH;
+    return true;
+}
+
+template <int K, int S, int P, bool DX>
+static PackGeo pack_geo(const FastArgs &a) {
+    PackGeo pg;
+    pg.CS = a.CS;
+    pg.CD = a.CD;
+    pg.KK = ConvTaps<K, S, P, DX>::KK;
+    pg.CH = a.CH;
+    pg.nchunks = a.nchunks;
+    pg.nmblk = (a.CD + 31) / 32;
+    pg.sm = a.sm;
+    pg.sc = a.sc;
+    return pg;
+}
+
+template <int K, int S, int P, bool DX>
+static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src, const float *w,
+                  const float *wp, float *dst) {
+    using T = ConvTaps<K, S, P, DX>;
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        set_attr<K, S, P, DX, 1, 1, 1>();
+        set_attr<K, S, P, DX, 1, 1, 2>();
+        if constexpr (T::NCLS == 1) {
+            set_attr<K, S, P, DX, 2, 1, 1>();
+            set_attr<K, S, P, DX, 1, 2, 1>();
+        }
+    }
+    FastArgs a;
+    FastPlan p;
+    if (!setup<K, S, P, DX>(sp, a, p))
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: no LDS tiling for a %dx%d grid", a.GA, a.GB);
+    a.src = src;
+    a.w = w;
+    a.dst = dst;
+    a.N = n;
+    const long long wbytes = (long long)sp->cout * sp->cin * T::KK * 4;
+    const long long pbytes = (long long)pack_geo<K, S, P, DX>(a).floats() * 4;
+    if ((long long)p.IMGS * a.CS * a.HS * a.WS * 4 >= 0x7FFFFFF0ll || wbytes >= 0x7FFFFFF0ll ||
+        pbytes >= 0x7FFFFFF0ll)
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: tile source or weights beyond 2 GiB");
+    a.wbytes = (int)wbytes;
+    a.wp = wp;
+    a.wpbytes = (int)pbytes;
     const int nmblk = (a.CD + 31) / 32;
     a.ntiles = a.tiles_a * ((n + p.IMGS - 1) / p.IMGS);
     a.ngroups = (nmblk + p.MB * p.WM - 1) / (p.MB * p.WM);
@@ -579,13 +633,14 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
     // Persistent grid: as many workgroups as fit on the chip at once.
     auto run = [&](auto kern) -> int {
         int occ = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 64 * FAST_NW, p.lds) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 64 * FAST_NW * 2, p.lds) !=
                 hipSuccess ||
             occ < 1)
             occ = 1;
         if (p.wpc > 0) occ = std::min(occ, p.wpc);
         const long long grid = std::min<long long>(nitems, (long long)ctx->num_cus * occ);
-        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * FAST_NW), p.lds, ctx->stream, a);
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(64 * FAST_NW * 2), p.lds, ctx->stream,
+                           a);
         RNN_LAUNCHED(ctx);
         return RNN_OK;
     };
@@ -597,24 +652,96 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
     return run(conv_fast_kernel<K, S, P, DX, 1, 1, 1>);
 }
 
+
+// Packs W for the forward (dx = 0) or dX (dx = 1) kernel: slab order
+// [m-block][chunk][quad][tap][lane][4], the layout the kernel's LDS weight
+// slabs take, zero-filled beyond the channels, so that a stage's weights are
+// one contiguous copy.  Lane L of slab (q, t) holds rows m = 32*mblk + L%32
+// and channels c = chunk*CH + (L/32)*CH/2 + 4q + i.
+__global__ void conv_pack_kernel(const float *__restrict__ w, PackGeo g, float *wp, size_t total) {
+    const int cq = g.CH >> 3;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (size_t)gridDim.x * blockDim.x)
+        wp[e] = g.value(w, e, cq);
+}
+
+// Several packs in one launch: block b serves the segment whose block range
+// holds it.
+__global__ void conv_pack_multi_kernel(const float *__restrict__ src, const PackSeg *__restrict__ segs,
+                                       int nseg, float *dst) {
+    int k = 0;
+    while (k + 1 < nseg && segs[k + 1].blk0 <= blockIdx.x) k++;
+    const PackSeg sg = segs[k];
+    const int cq = sg.geo.CH >> 3;
+    const size_t total = sg.geo.floats();
+    const float *w = src + sg.src;
+    float *wp = dst + sg.dst;
+    for (size_t e = (size_t)(blockIdx.x - sg.blk0) * blockDim.x + threadIdx.x; e < total;
+         e += (size_t)sg.nblk * blockDim.x)
+        wp[e] = sg.geo.value(w, e, cq);
+}
+
+template <int K, int S, int P, bool DX>
+static int geo_of(const rnn_conv_spec *sp, PackGeo *pg) {
+    FastArgs a;
+    FastPlan p;
+    if (!setup<K, S, P, DX>(sp, a, p)) return RNN_E_UNSUPPORTED;
+    *pg = pack_geo<K, S, P, DX>(a);
+    return RNN_OK;
+}
+
 }  // namespace
 
 // Forward (dx = 0) or dX (dx = 1) through the specialised kernels; returns
 // RNN_E_UNSUPPORTED (without recording an error) when (k, stride, pad) has no
-// specialisation, so the caller can take the generic per-class path.
+// specialisation, so the caller can take the generic per-class path.  wp:
+// the weights packed by rnn_conv_pack for this direction, or null.
 int rnn_conv_fast(rnn_ctx *ctx, int dx, const rnn_conv_spec *sp, size_t n, const float *src,
-                  const float *w, float *dst) {
+                  const float *w, const float *wp, float *dst) {
     if (getenv("RNN_CONV_GENERIC")) return RNN_E_UNSUPPORTED;
     const int k = sp->k, s = sp->stride, p = sp->pad;
     const int ni = (int)n;
 #define RNN_CONV_CASE(K_, S_, P_)                                                               \
     if (k == K_ && s == S_ && p == P_)                                                          \
-        return dx ? launch<K_, S_, P_, true>(ctx, sp, ni, src, w, dst)                          \
-                  : launch<K_, S_, P_, false>(ctx, sp, ni, src, w, dst);
+        return dx ? launch<K_, S_, P_, true>(ctx, sp, ni, src, w, wp, dst)                      \
+                  : launch<K_, S_, P_, false>(ctx, sp, ni, src, w, wp, dst);
     RNN_CONV_CASE(3, 1, 1)
     RNN_CONV_CASE(3, 2, 1)
     RNN_CONV_CASE(1, 2, 0)
     RNN_CONV_CASE(1, 1, 0)
 #undef RNN_CONV_CASE
     return RNN_E_UNSUPPORTED;
+}
+
+int rnn_conv_pack_geo(const rnn_conv_spec *sp, int dx, PackGeo *pg) {
+    if (getenv("RNN_CONV_GENERIC")) return RNN_E_UNSUPPORTED;
+    const int k = sp->k, s = sp->stride, p = sp->pad;
+#define RNN_CONV_CASE(K_, S_, P_)                                                               \
+    if (k == K_ && s == S_ && p == P_)                                                          \
+        return dx ? geo_of<K_, S_, P_, true>(sp, pg) : geo_of<K_, S_, P_, false>(sp, pg);
+    RNN_CONV_CASE(3, 1, 1)
+    RNN_CONV_CASE(3, 2, 1)
+    RNN_CONV_CASE(1, 2, 0)
+    RNN_CONV_CASE(1, 1, 0)
+#undef RNN_CONV_CASE
+    return RNN_E_UNSUPPORTED;
+}
+
+int rnn_conv_pack(rnn_ctx *ctx, const rnn_conv_spec *sp, int dx, const float *w, float *wp) {
+    PackGeo pg;
+    const int rc = rnn_conv_pack_geo(sp, dx, &pg);
+    if (rc) return rc;
+    const size_t total = pg.floats();
+    const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+    conv_pack_kernel<<<grid, 256, 0, ctx->stream>>>(w, pg, wp, total);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_conv_pack_multi_launch(rnn_ctx *ctx, const PackSeg *segs, int nseg, int nblocks,
+                               const float *src, float *dst) {
+    if (nseg <= 0) return RNN_OK;
+    conv_pack_multi_kernel<<<nblocks, 256, 0, ctx->stream>>>(src, segs, nseg, dst);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
 }

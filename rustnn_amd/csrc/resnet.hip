@@ -78,6 +78,8 @@ struct NetConv {
     // straight into the gradient instead
     float *slabs = nullptr;
     int nz = 0;
+    // weights packed for the forward / dX kernels (per plan); null: unpacked
+    float *wp_f = nullptr, *wp_x = nullptr;
     rnn_conv_spec spec(uint32_t h, uint32_t w_) const {
         rnn_conv_spec sp;
         rnn_conv_spec_init(&sp, cin, cout, k, stride, pad, h, w_);
@@ -126,6 +128,12 @@ struct rnn_resnet {
     long long nseg_blocks = 0;
     uint32_t *labels = nullptr, *correct = nullptr;
     double *part = nullptr;
+    // Packed conv weights: one segment per (conv, direction), refreshed by
+    // the pass after every SGD step inside the step; packs_dirty marks
+    // weights changed outside it (initialisation, copies in, rnn_resnet_step).
+    PackSeg *psegs = nullptr;
+    int npseg = 0, npblk = 0;
+    bool packs_dirty = true;
     size_t fh = 0, fw = 0;  // feature map at the pooling layer
     bool fwd_train = false;  // last forward saved the backward's activations
     // Graph of the train step for the current plan.
@@ -244,6 +252,34 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
         slab(b.c2, b.hout, b.wout);
         if (b.down) slab(b.cd, b.hin, b.win);
     }
+    // Packed weights: forward for every conv, dX for all but the stem (whose
+    // input gradient is not needed).
+    struct PackPlan {
+        float **dst;
+        PackSeg seg;
+        size_t off;
+    };
+    std::vector<PackPlan> packs;
+    auto pack = [&](NetConv &c, uint32_t h, uint32_t w, int dx, float **dst) {
+        *dst = nullptr;
+        rnn_conv_spec sp = c.spec(h, w);
+        PackSeg sg;
+        if (rnn_conv_pack_geo(&sp, dx, &sg.geo) != RNN_OK) return;
+        packs.push_back({dst, sg, cv.take(sg.geo.floats() * sizeof(float))});
+    };
+    pack(r->stem, (uint32_t)H, (uint32_t)W, 0, &r->stem.wp_f);
+    r->stem.wp_x = nullptr;
+    for (auto &b : r->blocks) {
+        pack(b.c1, b.hin, b.win, 0, &b.c1.wp_f);
+        pack(b.c1, b.hin, b.win, 1, &b.c1.wp_x);
+        pack(b.c2, b.hout, b.wout, 0, &b.c2.wp_f);
+        pack(b.c2, b.hout, b.wout, 1, &b.c2.wp_x);
+        if (b.down) {
+            pack(b.cd, b.hin, b.win, 0, &b.cd.wp_f);
+            pack(b.cd, b.hin, b.win, 1, &b.cd.wp_x);
+        }
+    }
+    const size_t o_psegs = cv.take(std::max<size_t>(packs.size(), 1) * sizeof(PackSeg));
     const size_t o_segs = cv.take(r->params.size() * sizeof(GradSeg));
     const size_t o_lab = cv.take(n * sizeof(uint32_t));
     const size_t o_cor = cv.take(sizeof(uint32_t));
@@ -260,6 +296,42 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     r->stem.slabs = nullptr;
     for (auto &b : r->blocks) b.c1.slabs = b.c2.slabs = b.cd.slabs = nullptr;
     for (auto &e : slabs) e.first->slabs = (float *)(base + e.second);
+    // Pack segments: source = the conv's weights in pv, destination relative
+    // to the arena.
+    std::vector<PackSeg> psegs;
+    uint32_t pblk = 0;
+    auto conv_of_dst = [&](float **dst) -> const NetConv * {
+        if (dst == &r->stem.wp_f) return &r->stem;
+        for (auto &b : r->blocks) {
+            if (dst == &b.c1.wp_f || dst == &b.c1.wp_x) return &b.c1;
+            if (dst == &b.c2.wp_f || dst == &b.c2.wp_x) return &b.c2;
+            if (dst == &b.cd.wp_f || dst == &b.cd.wp_x) return &b.cd;
+        }
+        return nullptr;
+    };
+    for (auto &pp : packs) {
+        *pp.dst = (float *)(base + pp.off);
+        PackSeg sg = pp.seg;
+        sg.src = r->params[conv_of_dst(pp.dst)->w].off;
+        sg.dst = pp.off / sizeof(float);
+        sg.blk0 = pblk;
+        sg.nblk = (uint32_t)std::min<size_t>(rnn_div_up(sg.geo.floats(), 1024), 256);
+        pblk += sg.nblk;
+        psegs.push_back(sg);
+    }
+    r->psegs = (PackSeg *)(base + o_psegs);
+    r->npseg = (int)psegs.size();
+    r->npblk = (int)pblk;
+    r->packs_dirty = true;
+    if (!psegs.empty()) {
+        hipError_t pe = hipMemcpy(r->psegs, psegs.data(), psegs.size() * sizeof(PackSeg),
+                                  hipMemcpyHostToDevice);
+        if (pe != hipSuccess) {
+            (void)hipFree(r->arena);
+            r->arena = nullptr;
+            return rnn_fail(ctx, RNN_E_HIP, "resnet plan upload: %s", hipGetErrorString(pe));
+        }
+    }
     // Segment table: parameters in flat order, conv weights with their slabs.
     std::vector<GradSeg> segs(r->params.size());
     std::vector<const NetConv *> conv_of(r->params.size(), nullptr);
@@ -335,7 +407,16 @@ RnnBn bn_state(rnn_resnet *r, const NetBn &bn) {
         if (st_ != RNN_OK) return st_; \
     } while (0)
 
+// Re-packs every conv's weights from pv (one launch).
+int pack_all(rnn_resnet *r) {
+    r->packs_dirty = false;
+    return rnn_conv_pack_multi_launch(r->ctx, r->psegs, r->npseg, r->npblk, r->pv,
+                                      (float *)r->arena);
+}
+
 // ResNet::forward (model.rs:138-150) with BasicBlock::forward (model.rs:39-57).
+// The packed weights must be current (callers run pack_all when
+// packs_dirty).
 // Train mode: each BN's partial sums are taken right after its conv and
 // finalised inside the kernel that applies the BN.
 int forward(rnn_resnet *r, bool train) {
@@ -344,23 +425,23 @@ int forward(rnn_resnet *r, bool train) {
     const bool ev = !train;
     rnn_conv_spec sp = r->stem.spec((uint32_t)r->H, (uint32_t)r->W);
     const size_t hw0 = (size_t)sp.oh * sp.ow;
-    TRY(rnn_conv2d_forward(ctx, &sp, n, r->x, pv_of(r, r->stem.w), r->y0));
+    TRY(rnn_conv2d_forward_wp(ctx, &sp, n, r->x, pv_of(r, r->stem.w), r->stem.wp_f, r->y0));
     if (train) TRY(rnn_bn_stats_launch(ctx, n, r->stem_bn.c, hw0, r->y0, r->stem_bn.part));
     TRY(rnn_bn_apply_launch(ctx, n, r->stem_bn.c, hw0, r->y0, bn_state(r, r->stem_bn), ev, 1, 0,
                             nullptr, nullptr, r->s0));
     for (auto &b : r->blocks) {
         const size_t hw = (size_t)b.hout * b.wout;
         rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
-        TRY(rnn_conv2d_forward(ctx, &s1, n, b.in, pv_of(r, b.c1.w), b.y1));
+        TRY(rnn_conv2d_forward_wp(ctx, &s1, n, b.in, pv_of(r, b.c1.w), b.c1.wp_f, b.y1));
         if (train) TRY(rnn_bn_stats_launch(ctx, n, b.b1.c, hw, b.y1, b.b1.part));
         TRY(rnn_bn_apply_launch(ctx, n, b.b1.c, hw, b.y1, bn_state(r, b.b1), ev, 1, 0, nullptr,
                                 nullptr, b.h));
         rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
-        TRY(rnn_conv2d_forward(ctx, &s2, n, b.h, pv_of(r, b.c2.w), b.y2));
+        TRY(rnn_conv2d_forward_wp(ctx, &s2, n, b.h, pv_of(r, b.c2.w), b.c2.wp_f, b.y2));
         if (train) TRY(rnn_bn_stats_launch(ctx, n, b.b2.c, hw, b.y2, b.b2.part));
         if (b.down) {
             rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
-            TRY(rnn_conv2d_forward(ctx, &sd, n, b.in, pv_of(r, b.cd.w), b.ys));
+            TRY(rnn_conv2d_forward_wp(ctx, &sd, n, b.in, pv_of(r, b.cd.w), b.cd.wp_f, b.ys));
             if (train) TRY(rnn_bn_stats_launch(ctx, n, b.bd.c, hw, b.ys, b.bd.part));
             const RnnBn sd_bn = bn_state(r, b.bd);
             TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, bn_state(r, b.b2), ev, 1, 2, b.ys,
@@ -439,19 +520,19 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
                                          bn_state(r, b.b2), b.b2.part, r->t1));
         rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
         TRY(conv_dw(r, b.c2, s2, r->t1, b.h));
-        TRY(rnn_conv2d_backward_x(ctx, &s2, n, r->t1, pv_of(r, b.c2.w), r->t2));
+        TRY(rnn_conv2d_backward_x_wp(ctx, &s2, n, r->t1, pv_of(r, b.c2.w), b.c2.wp_x, r->t2));
         TRY(rnn_bn_backward_launch(ctx, n, b.b1.c, hw, r->t2, b.h, b.y1, bn_state(r, b.b1),
                                    r->part, r->t1));
         rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
         TRY(conv_dw(r, b.c1, s1, r->t1, b.in));
-        TRY(rnn_conv2d_backward_x(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), other));
+        TRY(rnn_conv2d_backward_x_wp(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), b.c1.wp_x, other));
         const float *add = d;  // dx = c1 dX + d (add_, model.rs:72)
         if (b.down) {
             TRY(rnn_bn_backward_apply_launch(ctx, n, b.bd.c, hw, d, nullptr, b.ys,
                                              bn_state(r, b.bd), b.bd.part, r->t2));
             rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
             TRY(conv_dw(r, b.cd, sd, r->t2, b.in));
-            TRY(rnn_conv2d_backward_x(ctx, &sd, n, r->t2, pv_of(r, b.cd.w), r->t3));
+            TRY(rnn_conv2d_backward_x_wp(ctx, &sd, n, r->t2, pv_of(r, b.cd.w), b.cd.wp_x, r->t3));
             add = r->t3;  // dx = c1 dX + shortcut dX (add_, model.rs:70-71)
         }
         TRY(resid(r, i, b.c1.cin, (size_t)b.hin * b.win, other, add, b.in, nullptr));
@@ -463,8 +544,10 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
                                      r->y0, bn_state(r, r->stem_bn), r->stem_bn.part, r->t1));
     // The stem's dX would be the image gradient: discarded (model.rs:161).
     TRY(conv_dw(r, r->stem, sp, r->t1, r->x));
-    return rnn_grad_finalize_launch(ctx, r->segs, r->nseg, r->nseg_blocks, r->pv, r->pg, r->pm,
-                                    r->scal, sgd ? 1 : 0);
+    TRY(rnn_grad_finalize_launch(ctx, r->segs, r->nseg, r->nseg_blocks, r->pv, r->pg, r->pm,
+                                 r->scal, sgd ? 1 : 0));
+    // the step changed the weights: their packed copies follow
+    return sgd ? pack_all(r) : RNN_OK;
 }
 
 int sgd(rnn_resnet *r, const float *scal, float lr, float mom, float wd) {
@@ -485,6 +568,7 @@ int step_body(rnn_resnet *r) {
 // reason is kept, the network stays eager and the step runs now.
 int run_step(rnn_resnet *r) {
     rnn_ctx *ctx = r->ctx;
+    if (r->packs_dirty) TRY(pack_all(r));
     if (!r->use_graph || r->step_calls == 0) return step_body(r);
     if (!r->gexec) {
         // Recording needs a stream of its own (the caller's may be the null
@@ -720,6 +804,7 @@ int rnn_resnet_copy(rnn_resnet *r, int which, float *dst, const float *src) {
         return RNN_OK;
     }
     float *base = which == 0 ? r->pv : which == 1 ? r->pg : r->pm;
+    if (which == 0 && src) r->packs_dirty = true;
     size_t pos = 0;  // position in for_each_param order
     for (auto &p : r->params) {
         if (dst)
@@ -744,6 +829,7 @@ int rnn_resnet_forward(rnn_resnet *r, size_t n, size_t h, size_t w, const float 
     TRY(plan(r, n, h, w));
     RNN_HIP(ctx, hipMemcpyAsync(r->x, x, n * 3 * h * w * sizeof(float), hipMemcpyDeviceToDevice,
                                 ctx->stream));
+    if (r->packs_dirty) TRY(pack_all(r));
     TRY(forward(r, train != 0));
     RNN_HIP(ctx, hipMemcpyAsync(logits, r->logits, n * r->nclass * sizeof(float),
                                 hipMemcpyDeviceToDevice, ctx->stream));
@@ -765,6 +851,7 @@ int rnn_resnet_backward(rnn_resnet *r, const float *dlogits) {
 int rnn_resnet_step(rnn_resnet *r, float lr, float momentum, float wd) {
     if (!r) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(r->ctx->mu);
+    r->packs_dirty = true;
     return sgd(r, nullptr, lr, momentum, wd);
 }
 

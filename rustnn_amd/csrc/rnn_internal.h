@@ -88,9 +88,55 @@ int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, co
                     size_t stride_c, int acc, const float *bias);
 int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, float *out);
 // Specialised forward (dx = 0) / dX (dx = 1) convolution; RNN_E_UNSUPPORTED
-// when (k, stride, pad) has no specialisation.
+// when (k, stride, pad) has no specialisation.  wp: the weights packed by
+// rnn_conv_pack for this direction (the kernels then load each stage's
+// weights as one contiguous copy), or null.
 int rnn_conv_fast(rnn_ctx *ctx, int dx, const rnn_conv_spec *sp, size_t n, const float *src,
-                  const float *w, float *dst);
+                  const float *w, const float *wp, float *dst);
+
+// Packed weights of one direction: [m-block][chunk][quad][tap][lane 64][4]
+// with lane L of slab (quad q, tap t) holding rows m = 32*mblk + L%32 and
+// source channels c = chunk*CH + (L/32)*CH/2 + 4q + i of W[m*sm + c*sc + t],
+// zero beyond CD rows or CS channels.
+struct PackGeo {
+    int CS, CD, KK, CH, nchunks, nmblk, sm, sc;
+    __host__ __device__ size_t floats() const {
+        return (size_t)nmblk * nchunks * CH * KK * 32;
+    }
+    __device__ float value(const float *w, size_t e, int cq) const {
+        const int i = (int)(e & 3), L = (int)((e >> 2) & 63);
+        size_t r = e >> 8;
+        const int t = (int)(r % KK);
+        r /= KK;
+        const int q = (int)(r % cq);
+        r /= cq;
+        const int chunk = (int)(r % nchunks);
+        const int mblk = (int)(r / nchunks);
+        const int m = mblk * 32 + (L & 31);
+        const int c = chunk * CH + (L >> 5) * (CH >> 1) + 4 * q + i;
+        return (m < CD && c < CS) ? w[(size_t)m * sm + (size_t)c * sc + t] : 0.0f;
+    }
+};
+// The packing of `sp` in direction dx (RNN_E_UNSUPPORTED: no specialised
+// kernel, nothing to pack).
+int rnn_conv_pack_geo(const rnn_conv_spec *sp, int dx, PackGeo *pg);
+int rnn_conv_pack(rnn_ctx *ctx, const rnn_conv_spec *sp, int dx, const float *w, float *wp);
+// Several packs in one launch: segment k packs src + src_off into
+// dst + dst_off with blocks [blk0, blk0 + nblk) of the grid (segs on the
+// device, in blk0 order).
+struct PackSeg {
+    PackGeo geo;
+    size_t src, dst;
+    uint32_t blk0, nblk;
+};
+int rnn_conv_pack_multi_launch(rnn_ctx *ctx, const PackSeg *segs, int nseg, int nblocks,
+                               const float *src, float *dst);
+// Forward / dX with optional packed weights (rnn_conv2d_forward /
+// rnn_conv2d_backward_x with wp = null).
+int rnn_conv2d_forward_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
+                          const float *w, const float *wp, float *y);
+int rnn_conv2d_backward_x_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                             const float *w, const float *wp, float *dx);
 // dW += over the batch (k = 1 or 3).
 int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
                 float *dw);

@@ -80,6 +80,39 @@ def test_conv_integer_bit_exact(rnn, orc, name, n, cin, cout, k, s, p, h):
     assert np.array_equal(to_host(dw), dw_want.ravel())
 
 
+@pytest.mark.parametrize("name,n,cin,cout,k,s,p,h", SHAPES, ids=[s[0] for s in SHAPES])
+def test_conv_packed_weights_bit_exact(rnn, orc, name, n, cin, cout, k, s, p, h):
+    """rnn_conv2d_forward_packed / _backward_x_packed (weights in the kernels'
+    slab order, zero-padded) give the same bits as the unpacked calls: the
+    same values reach the same LDS slabs.  The packed copy itself is checked
+    element by element against W at sampled positions of the layout."""
+    import rustnn_amd as R
+    sp = R.ConvSpec.make(cin, cout, k, s, p, h, h)
+    x, w, dy = inputs(orc, sp, n, seed=23)
+    X, W, DY = to_dev(x), to_dev(w), to_dev(dy)
+    for dx in (0, 1):
+        wp = R.conv_pack_weights(sp, dx, W)
+        assert wp is not None
+        if dx == 0:
+            want = to_host(R.conv2d_forward(sp, n, X, W))
+            got = to_host(R.conv2d_forward_packed(sp, n, X, W, wp))
+        else:
+            want = to_host(R.conv2d_backward_x(sp, n, DY, W))
+            got = to_host(R.conv2d_backward_x_packed(sp, n, DY, W, wp))
+        assert np.array_equal(got, want), (name, dx)
+        # layout: [mblk][chunk][q][tap][lane][4]; find CH from the size
+        kk = k * k
+        cs, cd = (cout, cin) if dx else (cin, cout)
+        hp = to_host(wp)
+        nmblk = (cd + 31) // 32
+        per_ch = hp.size // (nmblk * kk * 32)  # nchunks * CH
+        W3 = w.reshape(cout, cin, kk)
+        nz = int(np.count_nonzero(hp))
+        assert nz == int(np.count_nonzero(W3)), (name, dx, nz)
+        assert np.isclose(np.sort(np.abs(hp[hp != 0])), np.sort(np.abs(W3[W3 != 0]))).all()
+        assert per_ch >= cs
+
+
 def test_conv_deterministic(rnn, orc):
     sp = rnn.ConvSpec.make(32, 32, 3, 1, 1, 32, 32)
     x, w, dy = inputs(orc, sp, 128, seed=99)
