@@ -8,9 +8,10 @@
 // block), N = ci (32 per block) for each tap, K = output pixels.
 //
 // A workgroup owns a (co block, ci block) pair and walks a strided set of
-// pixel tiles (TR output rows of IMGS images, full width).  Each tile is
-// staged by DMA into one of two LDS buffers while the previous one is
-// computed:
+// pixel tiles (TR output rows of IMGS images, full width).  Four producer
+// waves stage each tile by DMA into one of two LDS buffers while four MFMA
+// waves compute the previous one (the memory pipeline's back-pressure stalls
+// only the producers):
 //   * the dY window [co][img][r][OWP] and the X halo window [ci][img][ty][TIWP]
 //     (stride 2: even columns then odd columns), one LDS channel every 64m+4
 //     words so that the 32 lanes of a b128 read hit distinct banks while no
@@ -21,10 +22,10 @@
 // pixels 4h..4h+3 of the group with one ds_read_b128 for dY and, per kernel
 // row kh, the 6 (or 5 + 4) X values those pixels touch, so the three kw taps
 // are register offsets into the same read.  MFMA k-step i takes pixels i and
-// 4 + i; the 9 tap accumulators are independent chains.  The 8 waves' sums are
-// added through LDS in a fixed pairwise order and the workgroup writes one partial slab;
-// slabs are added in slab order by one reduction launch (no atomics: the
-// result is bit-reproducible).
+// 4 + i; the 9 tap accumulators are independent chains.  The 4 MFMA waves'
+// sums are added through LDS in a fixed pairwise order and the workgroup
+// writes one partial slab; slabs are added in slab order by one reduction
+// launch (no atomics: the result is bit-reproducible).
 #include "conv_common.h"
 
 #include <algorithm>
@@ -33,7 +34,9 @@
 
 namespace {
 
-constexpr int DW_NW = 8;  // waves per workgroup (one workgroup per CU, two waves per SIMD)
+constexpr int DW_NW = 4;  // MFMA waves per workgroup (one workgroup per CU, one per SIMD)
+constexpr int DW_NP = 4;  // DMA producer waves per workgroup (one per SIMD)
+constexpr int DW_THREADS = 64 * (DW_NW + DW_NP);
 
 struct DwArgs {
     const float *dy;  // [N][CO][OH][OW]
@@ -214,14 +217,14 @@ __device__ __forceinline__ float dw_bval(const DwOps<K, S> &o, int kh, int kw, i
     }
 }
 
-// DMA of a whole tile: every channel of this wave.
+// DMA of a whole tile by producer wave pw: channels pw, pw + DW_NP, ...
 template <int MT>
 __device__ __forceinline__ void dw_issue_tile(const DwArgs &g, const DwLane<MT> &L, int tile,
                                               int cob, int cib, float *__restrict__ buf,
-                                              int wave) {
+                                              int pw) {
     const DwStage<MT> d = dw_stage<MT>(g, L, tile, cob, cib, buf);
-    for (int k = 0; k < 32 / DW_NW; k++)
-        dw_issue_channel<MT>(g, d, wave + DW_NW * k, cob, cib, buf);
+    for (int k = 0; k < 32 / DW_NP; k++)
+        dw_issue_channel<MT>(g, d, pw + DW_NP * k, cob, cib, buf);
 }
 
 // MFMAs of one 8-pixel group: k-step i takes pixels i and 4 + i.
@@ -257,28 +260,16 @@ __device__ __forceinline__ void dw_step_schedule() {
 // The GEMM steps of one staged tile: 8-pixel groups wave, wave + NW, ...;
 // two operand sets alternate so that the reads of group n+1 overlap the
 // MFMAs of group n.  Reads past the tile's last group are clamped to group
-// `wave` (in range; their values are not used).  When `dma` is set, the
-// channels of the next tile that this wave stages are issued a few per step,
-// after the step's MFMAs, so that the other wave of the SIMD computes while
-// this one waits on the address unit.
-template <int K, int S, int MT>
+// `wave` (in range; their values are not used).
+template <int K, int S>
 __device__ __forceinline__ void dw_compute(const DwArgs &g, const float *__restrict__ cur,
-                                           float *__restrict__ nxt, const DwStage<MT> &dma,
-                                           bool do_dma, int cob, int cib, int wave, int lane,
+                                           int wave, int lane,
                                            f32x16 (&acc)[K == 1 ? 4 : K * K]) {
-    constexpr int NCH = 32 / DW_NW;  // channels each wave stages
     const float *xs = cur, *ds = cur + g.xwords;
     const int nsteps = (g.ngroups - wave + DW_NW - 1) / DW_NW;
     auto grp = [&](int s) {
         const int gi = wave + DW_NW * s;
         return gi < g.ngroups ? gi : min(wave, g.ngroups - 1);
-    };
-    int issued = 0;
-    auto dma_upto = [&](int s) {  // channels due once step s is done
-        if (!do_dma) return;
-        const int due = nsteps > 0 ? min(NCH, ((s + 1) * NCH + nsteps - 1) / nsteps) : NCH;
-        for (; issued < due; issued++)
-            dw_issue_channel<MT>(g, dma, wave + DW_NW * issued, cob, cib, nxt);
     };
     DwOps<K, S> oa, ob;
     dw_fetch<K, S>(g, xs, ds, grp(0), lane, oa);
@@ -287,27 +278,11 @@ __device__ __forceinline__ void dw_compute(const DwArgs &g, const float *__restr
         dw_fetch<K, S>(g, xs, ds, grp(s + 1), lane, ob);
         dw_mma<K, S>(oa, acc);
         dw_step_schedule<K, S>();
-        dma_upto(s);
         if (s + 1 >= nsteps) break;
         dw_fetch<K, S>(g, xs, ds, grp(s + 2), lane, oa);
         dw_mma<K, S>(ob, acc);
         dw_step_schedule<K, S>();
-        dma_upto(s + 1);
     }
-    dma_upto(nsteps);
-}
-
-// Double-buffered stage: the tile in `cur` is computed while the next tile
-// is staged into `nxt`.  The buffers are distinct; the __restrict__
-// qualifiers give the compiler the alias scopes it needs to not wait for the
-// DMA before the LDS reads.
-template <int K, int S, int MT>
-__device__ __forceinline__ void dw_stage2(const DwArgs &g, const float *__restrict__ cur,
-                                          float *__restrict__ nxt, int next_tile,
-                                          const DwLane<MT> &L, int cob, int cib, int wave,
-                                          int lane, f32x16 (&acc)[K == 1 ? 4 : K * K]) {
-    const DwStage<MT> d = dw_stage<MT>(g, L, next_tile, cob, cib, nxt);
-    dw_compute<K, S, MT>(g, cur, nxt, d, true, cob, cib, wave, lane, acc);
 }
 
 // Accumulator v of tap t of this lane lives at slab-order slot
@@ -330,66 +305,85 @@ __device__ __forceinline__ void dw_red_add(const float *src, int lbase, f32x16 *
             acc[t][v] += src[(lbase + 32 * (8 * (v >> 2) + (v & 3))) * KK + t];
 }
 
+// Waves 0..7 compute (a pixel-group split of the tile); waves 8..11 only
+// stage tiles by DMA, so that the memory pipeline's back-pressure never
+// stalls an MFMA wave.  Double-buffered plans (NB = 2) stage the next tile
+// while this one is computed (one barrier per tile); single-buffered plans
+// stage it after the compute barrier.
 template <int K, int S, int MT, int NB>
-__global__ __launch_bounds__(64 * DW_NW) void conv_dw_kernel(DwArgs g) {
+__global__ __launch_bounds__(DW_THREADS) void conv_dw_kernel(DwArgs g) {
     constexpr int KK = K * K, NA = K == 1 ? 4 : KK;
     extern __shared__ float smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     const int h = lane >> 5, l32 = lane & 31;
     const int z = blockIdx.x, cob = blockIdx.y, cib = blockIdx.z;
-
-    DwLane<MT> L;
-    dw_lane_init<K, S, MT>(g, L, lane);
-
-    f32x16 acc[NA];
-#pragma unroll
-    for (int t = 0; t < NA; t++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
-
-    // Tiles z, z + nz, ...  With two stage buffers the next tile is staged
-    // while this one is computed; with one (larger tiles), the other
-    // workgroups on the CU compute while this one stages.
-    dw_issue_tile<MT>(g, L, z, cob, cib, smem, wave);
-    int s = 0;
-    for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
-        dma_wait_barrier();
-        if constexpr (NB == 2) {
-            dw_stage2<K, S, MT>(g, smem + (s & 1) * g.stage, smem + ((s + 1) & 1) * g.stage,
-                                tile + g.nz, L, cob, cib, wave, lane, acc);
-        } else {
-            DwStage<MT> none;
-            none.valid = 0;
-            dw_compute<K, S, MT>(g, smem, smem, none, false, cob, cib, wave, lane, acc);
-            __syncthreads();
-            if (tile + g.nz < g.ntiles) dw_issue_tile<MT>(g, L, tile + g.nz, cob, cib, smem, wave);
-        }
-    }
-    if constexpr (K == 1) {
-#pragma unroll
-        for (int v = 0; v < 16; v++) acc[0][v] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
-    }
-    // Sum the eight waves' accumulators in a fixed order, ((w0 + w4) + (w1 +
-    // w5)) + ((w2 + w6) + (w3 + w7)), through four LDS slices in slab order
-    // [co][ci][tap] (bit-reproducible), then write contiguous slab rows.
-    dma_wait_barrier();
-    float *red = smem;  // 4 slices of [32][32][KK]
+    float *red = smem;  // after the tiles: 2 slices of [32][32][KK]
     const int SL = KK * 1024;
-    const int lbase = 4 * h * 32 + l32;  // slot of (v = 0, t = 0) for this lane
-    if (wave >= 4) dw_red_store<KK>(red + (wave - 4) * SL, lbase, acc);
-    __syncthreads();
-    if (wave < 4) {
-        dw_red_add<KK>(red + wave * SL, lbase, acc);
+    if (wave >= DW_NW) {
+        // producer: the same barriers as the MFMA waves, one per tile (two
+        // with a single buffer), then those of the reduction
+        const int pw = wave - DW_NW;
+        DwLane<MT> L;
+        dw_lane_init<K, S, MT>(g, L, lane);
+        dw_issue_tile<MT>(g, L, z, cob, cib, smem, pw);
+        int s = 0;
+        for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
+            dma_wait_barrier();
+            const bool more = tile + g.nz < g.ntiles;
+            if constexpr (NB == 2) {
+                if (more)
+                    dw_issue_tile<MT>(g, L, tile + g.nz, cob, cib, smem + ((s + 1) & 1) * g.stage,
+                                      pw);
+            } else {
+                __syncthreads();
+                if (more) dw_issue_tile<MT>(g, L, tile + g.nz, cob, cib, smem, pw);
+            }
+        }
+        dma_wait_barrier();
+        __syncthreads();
+        __syncthreads();
+        __syncthreads();
+    } else {
+        f32x16 acc[NA];
+#pragma unroll
+        for (int t = 0; t < NA; t++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
+        // Tiles z, z + nz, ...
+        int s = 0;
+        for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
+            dma_wait_barrier();
+            if constexpr (NB == 2) {
+                dw_compute<K, S>(g, smem + (s & 1) * g.stage, wave, lane, acc);
+            } else {
+                dw_compute<K, S>(g, smem, wave, lane, acc);
+                __syncthreads();
+            }
+        }
+        if constexpr (K == 1) {
+#pragma unroll
+            for (int v = 0; v < 16; v++)
+                acc[0][v] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
+        }
+        // Sum the MFMA waves' accumulators in a fixed order, (w0 + w2) + (w1 +
+        // w3), through two LDS slices in slab order [co][ci][tap]
+        // (bit-reproducible), then write contiguous slab rows.
+        static_assert(DW_NW == 4, "reduction order written for four MFMA waves");
+        dma_wait_barrier();
+        const int lbase = 4 * h * 32 + l32;  // slot of (v = 0, t = 0) for this lane
+        if (wave >= 2) dw_red_store<KK>(red + (wave - 2) * SL, lbase, acc);
+        __syncthreads();
+        if (wave < 2) dw_red_add<KK>(red + wave * SL, lbase, acc);
+        __syncthreads();
+        if (wave < 2) dw_red_store<KK>(red + wave * SL, lbase, acc);
+        __syncthreads();
     }
-    __syncthreads();
-    if (wave < 4) dw_red_store<KK>(red + wave * SL, lbase, acc);
-    __syncthreads();
     const int ckk = g.CI * KK, rowlen = 32 * KK;
     float *slab = g.part + (long long)z * g.CO * ckk + cib * 32 * KK;
     const int rlim = min(32, g.CI - cib * 32) * KK;
-    for (int e = tid; e < SL; e += DW_NW * 64) {
+    for (int e = tid; e < SL; e += DW_THREADS) {
         const int co = e / rowlen, rem = e - co * rowlen;
-        const float v = (red[e] + red[SL + e]) + (red[2 * SL + e] + red[3 * SL + e]);
+        const float v = red[e] + red[SL + e];
         if (cob * 32 + co < g.CO && rem < rlim) slab[(long long)(cob * 32 + co) * ckk + rem] = v;
     }
 }
@@ -471,7 +465,7 @@ size_t dw_geometry(DwArgs &g, int K, int TR, int IMGS, int nbuf) {
     g.chsd = 64 * g.md + 4;
     g.xwords = 32 * g.chsx;
     g.stage = g.xwords + 32 * g.chsd + 64;
-    return std::max((size_t)nbuf * g.stage * 4, (size_t)4 * K * K * 1024 * 4);
+    return std::max((size_t)nbuf * g.stage * 4, (size_t)(DW_NW / 2) * K * K * 1024 * 4);
 }
 
 template <int K, int S, int MT, int NB>
@@ -596,7 +590,7 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
     if (NZ <= 0) {
         // persistent: as many workgroups as fit on the chip at once
         int occ = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 64 * DW_NW, lds) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, DW_THREADS, lds) !=
                 hipSuccess ||
             occ < 1)
             occ = 1;
@@ -625,7 +619,7 @@ int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const flo
     if (rc) return rc;
     L.g.part = slabs;
     void *args[] = {&L.g};
-    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(64 * DW_NW), args, L.lds, ctx->stream));
+    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(DW_THREADS), args, L.lds, ctx->stream));
     if (nz) *nz = L.g.nz;
     return RNN_OK;
 }
@@ -640,7 +634,7 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
     if (!ws) return RNN_E_NOMEM;
     L.g.part = ws;
     void *args[] = {&L.g};
-    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(64 * DW_NW), args, L.lds, ctx->stream));
+    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(DW_THREADS), args, L.lds, ctx->stream));
     hipLaunchKernelGGL(slab_reduce_kernel, dim3((unsigned)rnn_div_up(L.len, 32)), dim3(256), 0,
                        ctx->stream, ws, L.g.nz, (long long)L.len, dw);
     RNN_LAUNCHED(ctx);
