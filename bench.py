@@ -365,21 +365,44 @@ def main():
         y = torch.empty(N * cout * sp.hw, device="cuda")
         dx = torch.empty(N * cin * h * h, device="cuda")
         dw = torch.zeros(cout * sp.ckk, device="cuda")
-        layers.append(dict(name=name, sp=sp, x=x, w=w, dy=dy, y=y, dx=dx, dw=dw,
-                           flops=pass_flops(cin, cout, k, s, p, h)))
+        # W in the slab order of the forward / dX kernels (rnn_conv_pack_weights):
+        # a train step packs each conv's weights once per update
+        wpf, wpx = R.conv_pack_weights(sp, 0, w, ctx=ctx), R.conv_pack_weights(sp, 1, w, ctx=ctx)
+        layers.append(dict(name=name, sp=sp, x=x, w=w, dy=dy, y=y, dx=dx, dw=dw, wpf=wpf,
+                           wpx=wpx, flops=pass_flops(cin, cout, k, s, p, h)))
 
-    def run_op(L, ps):
+    def run_op(L, ps, packed=True):
         if ps == "fwd":
-            R.conv2d_forward(L["sp"], N, L["x"], L["w"], L["y"], ctx=ctx)
+            if packed:
+                R.conv2d_forward_packed(L["sp"], N, L["x"], L["w"], L["wpf"], L["y"], ctx=ctx)
+            else:
+                R.conv2d_forward(L["sp"], N, L["x"], L["w"], L["y"], ctx=ctx)
         elif ps == "dx":
-            R.conv2d_backward_x(L["sp"], N, L["dy"], L["w"], L["dx"], ctx=ctx)
+            if packed:
+                R.conv2d_backward_x_packed(L["sp"], N, L["dy"], L["w"], L["wpx"], L["dx"],
+                                           ctx=ctx)
+            else:
+                R.conv2d_backward_x(L["sp"], N, L["dy"], L["w"], L["dx"], ctx=ctx)
+        elif ps == "pack":
+            R.conv_pack_weights(L["sp"], 0, L["w"], L["wpf"], ctx=ctx)
+            R.conv_pack_weights(L["sp"], 1, L["w"], L["wpx"], ctx=ctx)
         else:
             R.conv2d_backward_w(L["sp"], N, L["dy"], L["x"], L["dw"], ctx=ctx)
 
-    def sweep_step():
+    def sweep_step(packs=True, packed=True):
         for L in layers:
+            if packs:
+                run_op(L, "pack")
             for ps in PASSES:
-                run_op(L, ps)
+                run_op(L, ps, packed)
+
+    def time_sweep(**kw):
+        # eager warm-up (sizes the workspaces), then graph replays: the GPU's
+        # time for the step, without the Python launch overhead
+        for _ in range(args.warmup):
+            sweep_step(**kw)
+        torch.cuda.synchronize()
+        return time_graph(ctx, lambda: sweep_step(**kw), args.steps)
 
     if args.ops_only:
         # calibration copy of known size first, then the ops in sweep order
@@ -398,32 +421,26 @@ def main():
     # ---- headline: config 3, the ResNet-20 train step
     rn = bench_resnet(R, ctx, args.steps, args.warmup)
 
-    # ---- config 1: the conv sweep
-    for _ in range(args.warmup):
-        sweep_step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(args.steps):
-        sweep_step()
-    e1.record()
-    torch.cuda.synchronize()
-    sweep_ms = e0.elapsed_time(e1) / args.steps
+    # ---- config 1: the conv sweep.  One sweep step = per layer: pack W for
+    # the forward and dX kernels, forward, dX, dW (the weights are packed once
+    # per update, as the ResNet step does).  Also timed: the same without the
+    # packs (the conv kernels alone) and with unpacked weights.
+    sweep_ms = time_sweep()
+    sweep_ms_nopack = time_sweep(packs=False)
+    sweep_ms_unpacked = time_sweep(packs=False, packed=False)
     sweep_flops = sum(3 * L["flops"] for L in layers)
     sweep_tf = sweep_flops / (sweep_ms * 1e-3) / 1e12
 
-    # per-op durations (HIP events on the library's stream, op-reps back-to-back)
+    # per-op durations: op-reps back-to-back launches replayed from a graph
     per_op = []
     for L in layers:
-        for ps in PASSES:
+        for ps in PASSES + ("pack",):
             run_op(L, ps)
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            for _ in range(args.op_reps):
-                run_op(L, ps)
-            b.record()
-            torch.cuda.synchronize()
-            t = a.elapsed_time(b) / args.op_reps
+            t = time_graph(ctx, lambda: run_op(L, ps), args.op_reps)
+            if ps == "pack":
+                per_op.append(dict(op=f"{L['name']}:pack", ms=round(t, 5),
+                                   note="packs W for both the forward and dX kernels"))
+                continue
             tf = L["flops"] / (t * 1e-3) / 1e12
             per_op.append(dict(op=f"{L['name']}:{ps}", ms=round(t, 5), tflops=round(tf, 2),
                                frac=round(tf / PEAK_FP32_MFMA_TFLOPS, 4),
@@ -438,10 +455,11 @@ def main():
 
     lay = {L["name"]: L for L in layers}
     # dominant op of the ResNet step: largest multiplicity x duration
-    dom = max(per_op, key=lambda r: r["ms"] * r["in_resnet_step"])
+    conv_ops = [r for r in per_op if "tflops" in r]
+    dom = max(conv_ops, key=lambda r: r["ms"] * r["in_resnet_step"])
     roof = roofline(dom, lay[dom["op"].split(":")[0]]["flops"])
     roof["share_of_resnet_step"] = round(dom["ms"] * dom["in_resnet_step"] / rn["ms"], 4)
-    sdom = max(per_op, key=lambda r: r["ms"])
+    sdom = max(conv_ops, key=lambda r: r["ms"])
     sweep_roof = roofline(sdom, lay[sdom["op"].split(":")[0]]["flops"])
 
     attention = bench_attention(R, ctx, args.op_reps)
@@ -474,6 +492,10 @@ def main():
         "config1_conv_sweep": {
             "value": round(sweep_tf, 3), "unit": "TFLOP/s", "ms_per_step": round(sweep_ms, 4),
             "frac_of_fp32_mfma_peak": round(sweep_tf / PEAK_FP32_MFMA_TFLOPS, 4),
+            "step": "per layer: pack W (forward + dX forms), forward, dX, dW",
+            "tflops_without_packs": round(sweep_flops / (sweep_ms_nopack * 1e-3) / 1e12, 3),
+            "tflops_unpacked_weights": round(sweep_flops / (sweep_ms_unpacked * 1e-3) / 1e12,
+                                             3),
             "flop_per_step": sweep_flops, "roofline": sweep_roof, "cpu_baseline": sweep_cpu,
             "per_op": per_op},
         "config2_attention": attention, "gemmbench": gemms,

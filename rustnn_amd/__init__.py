@@ -318,17 +318,26 @@ def conv2d_backward_x(sp: ConvSpec, n, dy, w, dx=None, ctx=None):
     return dx
 
 
-def conv_pack_weights(sp: ConvSpec, dx, w, ctx=None):
-    """Packed copy of W for the forward (dx=0) or dX (dx=1) kernel, or None
-    when the shape has no packed form."""
-    import torch
-    ctx = ctx or default_ctx()
+def conv_packed_floats(sp: ConvSpec, dx):
+    """Size of the packed copy of W for direction dx, or None (no packed form)."""
     nf = _sz()
     if lib().rnn_conv_packed_floats(C.byref(sp), int(dx), C.byref(nf)) != 0:
         return None
-    wp = torch.empty(int(nf.value), dtype=torch.float32, device=w.device)
+    return int(nf.value)
+
+
+def conv_pack_weights(sp: ConvSpec, dx, w, wp=None, ctx=None):
+    """Packed copy of W for the forward (dx=0) or dX (dx=1) kernel (into wp
+    when given), or None when the shape has no packed form."""
+    import torch
+    ctx = ctx or default_ctx()
+    nf = conv_packed_floats(sp, dx)
+    if nf is None:
+        return None
+    if wp is None:
+        wp = torch.empty(nf, dtype=torch.float32, device=w.device)
     ctx.check(lib().rnn_conv_pack_weights(ctx.h, C.byref(sp), int(dx),
-                                          _ptr(w, sp.cout * sp.ckk, "w"), _ptr(wp, 0, "wp")))
+                                          _ptr(w, sp.cout * sp.ckk, "w"), _ptr(wp, nf, "wp")))
     return wp
 
 

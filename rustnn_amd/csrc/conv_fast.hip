@@ -658,27 +658,24 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
 // slabs take, zero-filled beyond the channels, so that a stage's weights are
 // one contiguous copy.  Lane L of slab (q, t) holds rows m = 32*mblk + L%32
 // and channels c = chunk*CH + (L/32)*CH/2 + 4q + i.
-__global__ void conv_pack_kernel(const float *__restrict__ w, PackGeo g, float *wp, size_t total) {
-    const int cq = g.CH >> 3;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-         e += (size_t)gridDim.x * blockDim.x)
-        wp[e] = g.value(w, e, cq);
+__global__ __launch_bounds__(256) void conv_pack_kernel(const float *__restrict__ w, PackGeo g,
+                                                        float *wp) {
+    for (int r = blockIdx.x; r < g.slabs(); r += gridDim.x)
+        wp[(size_t)r * 256 + threadIdx.x] = g.value(w, r, threadIdx.x);
 }
 
 // Several packs in one launch: block b serves the segment whose block range
-// holds it.
-__global__ void conv_pack_multi_kernel(const float *__restrict__ src, const PackSeg *__restrict__ segs,
-                                       int nseg, float *dst) {
+// holds it, one 256-float slab at a time.
+__global__ __launch_bounds__(256) void conv_pack_multi_kernel(const float *__restrict__ src,
+                                                              const PackSeg *__restrict__ segs,
+                                                              int nseg, float *dst) {
     int k = 0;
     while (k + 1 < nseg && segs[k + 1].blk0 <= blockIdx.x) k++;
     const PackSeg sg = segs[k];
-    const int cq = sg.geo.CH >> 3;
-    const size_t total = sg.geo.floats();
     const float *w = src + sg.src;
     float *wp = dst + sg.dst;
-    for (size_t e = (size_t)(blockIdx.x - sg.blk0) * blockDim.x + threadIdx.x; e < total;
-         e += (size_t)sg.nblk * blockDim.x)
-        wp[e] = sg.geo.value(w, e, cq);
+    for (int r = blockIdx.x - sg.blk0; r < sg.geo.slabs(); r += sg.nblk)
+        wp[(size_t)r * 256 + threadIdx.x] = sg.geo.value(w, r, threadIdx.x);
 }
 
 template <int K, int S, int P, bool DX>
@@ -731,9 +728,8 @@ int rnn_conv_pack(rnn_ctx *ctx, const rnn_conv_spec *sp, int dx, const float *w,
     PackGeo pg;
     const int rc = rnn_conv_pack_geo(sp, dx, &pg);
     if (rc) return rc;
-    const size_t total = pg.floats();
-    const unsigned grid = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
-    conv_pack_kernel<<<grid, 256, 0, ctx->stream>>>(w, pg, wp, total);
+    const unsigned grid = (unsigned)std::min(pg.slabs(), 4096);
+    conv_pack_kernel<<<grid, 256, 0, ctx->stream>>>(w, pg, wp);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

@@ -315,7 +315,7 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
         sg.src = r->params[conv_of_dst(pp.dst)->w].off;
         sg.dst = pp.off / sizeof(float);
         sg.blk0 = pblk;
-        sg.nblk = (uint32_t)std::min<size_t>(rnn_div_up(sg.geo.floats(), 1024), 256);
+        sg.nblk = (uint32_t)std::min(sg.geo.slabs(), 512);
         pblk += sg.nblk;
         psegs.push_back(sg);
     }

@@ -103,15 +103,15 @@ struct PackGeo {
     __host__ __device__ size_t floats() const {
         return (size_t)nmblk * nchunks * CH * KK * 32;
     }
-    __device__ float value(const float *w, size_t e, int cq) const {
-        const int i = (int)(e & 3), L = (int)((e >> 2) & 63);
-        size_t r = e >> 8;
-        const int t = (int)(r % KK);
-        r /= KK;
-        const int q = (int)(r % cq);
-        r /= cq;
-        const int chunk = (int)(r % nchunks);
-        const int mblk = (int)(r / nchunks);
+    // 256-float slabs: slab r = ((mblk*nchunks + chunk)*CH/8 + q)*KK + t
+    __host__ __device__ int slabs() const { return nmblk * nchunks * (CH >> 3) * KK; }
+    // word j = 4L + i of slab r
+    __device__ float value(const float *w, int r, int j) const {
+        const int cq = CH >> 3;
+        const int t = r % KK, rq = r / KK;
+        const int q = rq % cq, rc = rq / cq;
+        const int chunk = rc % nchunks, mblk = rc / nchunks;
+        const int i = j & 3, L = j >> 2;
         const int m = mblk * 32 + (L & 31);
         const int c = chunk * CH + (L >> 5) * (CH >> 1) + 4 * q + i;
         return (m < CD && c < CS) ? w[(size_t)m * sm + (size_t)c * sc + t] : 0.0f;
