@@ -338,6 +338,9 @@ def main():
     ap.add_argument("--resnet-only", type=int, default=0, metavar="STEPS",
                     help="no timing: STEPS ResNet-20 train steps (the workload of the "
                          "rocprofv3 kernel trace of the step)")
+    ap.add_argument("--attn-only", type=int, default=0, metavar="REPS",
+                    help="config 2 only: the attention forward / backward timing with REPS calls "
+                         "per graph (the workload of the rocprofv3 kernel trace of attention)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -353,6 +356,9 @@ def main():
     if args.resnet_only:
         r = bench_resnet(R, ctx, args.resnet_only, 2)
         print(json.dumps({"resnet_only": args.resnet_only, "ms": r["ms"]}))
+        return
+    if args.attn_only:
+        print(json.dumps({"attn_only": bench_attention(R, ctx, args.attn_only)}))
         return
 
     g = torch.Generator(device="cuda").manual_seed(7)

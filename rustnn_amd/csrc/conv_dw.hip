@@ -31,6 +31,8 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 
 namespace {
 
@@ -548,54 +550,66 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
             if (lds == 0 || lds > 160 * 1024) TR = 0;
         }
     }
+    const int ncb = (g.CO + 31) / 32, ncib = (g.CI + 31) / 32;
+    auto kernel_of = [&](const DwArgs &a) -> const void * {
+        const int mt = std::max(a.mx, a.md);
+        if (K == 3)
+            return a.S == 1 ? dw_pick<3, 1>(mt, a.nbuf) : dw_pick<3, 2>(mt, a.nbuf);
+        return a.S == 1 ? dw_pick<1, 1>(mt, a.nbuf) : dw_pick<1, 2>(mt, a.nbuf);
+    };
+    auto slabs_of = [&](const void *kern, size_t l, int ntiles) {
+        // occupancy per (kernel, LDS bytes), cached: the planner asks for
+        // every candidate tile on every call
+        static std::mutex mu;
+        static std::map<std::pair<const void *, size_t>, int> cache;
+        int occ = 0;
+        {
+            std::lock_guard<std::mutex> lk(mu);
+            auto it = cache.find({kern, l});
+            if (it != cache.end()) {
+                occ = it->second;
+            } else {
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, DW_THREADS, l) !=
+                        hipSuccess ||
+                    occ < 1)
+                    occ = 1;
+                cache[{kern, l}] = occ;
+            }
+        }
+        return std::min(std::max(1, occ * ctx->num_cus / (ncb * ncib)), ntiles);
+    };
     if (TR <= 0 || IMGS <= 0) {
-        bool ok = false;
-        for (int pass = 0; pass < 4 && !ok; pass++) {
-            // passes: two buffers with <= 4 DMA rows per channel (small lane
-            // tables, no register spills), two buffers, one buffer, one buffer
-            const int nb = pass < 2 ? 2 : 1, mtmax = (pass & 1) ? DW_MT[2] : DW_MT[1];
-            double best = 0;
+        // The tile with the shortest critical path: every workgroup walks
+        // ceil(ntiles / NZ) tiles of ngroups 8-pixel groups plus a fixed
+        // per-tile cost (the barrier and the restart of the operand
+        // pipeline, about two groups).  Double-buffered plans first; a
+        // single buffer only when no double-buffered tile fits.
+        double best = 0;
+        for (int nb = 2; nb >= 1 && best == 0; nb--)
             for (int tr = 1; tr <= g.OH; tr++)
                 for (int im = 1; im <= (tr == g.OH ? 16 : 1); im *= 2) {
                     const size_t l = dw_geometry(g, K, tr, im, nb);
-                    if (l == 0 || l > 160 * 1024 || std::max(g.mx, g.md) > mtmax) continue;
-                    const int ta = (g.OH + tr - 1) / tr;
-                    const double score = g.ngroups * (double)g.OH / (ta * tr);
-                    if (score > best) {
-                        best = score;
+                    if (l == 0 || l > 160 * 1024) continue;
+                    const int ntiles = ((g.OH + tr - 1) / tr) * (int)((n + im - 1) / im);
+                    const int nz = slabs_of(kernel_of(g), l, ntiles);
+                    const double cost = (double)((ntiles + nz - 1) / nz) * (g.ngroups + 2);
+                    if (best == 0 || cost < best) {
+                        best = cost;
                         TR = tr;
                         IMGS = im;
                         NB = nb;
                     }
                 }
-            if (best > 0) {
-                lds = dw_geometry(g, K, TR, IMGS, NB);
-                ok = true;
-                break;
-            }
-        }
-        if (!ok) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: tile exceeds LDS");
+        if (best == 0) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: tile exceeds LDS");
     }
+    lds = dw_geometry(g, K, TR, IMGS, NB);
     if ((long long)IMGS * std::max(g.cihw, g.cohw) * 4 >= 0x7FFFFFF0ll)
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: tile source beyond 2 GiB");
     g.tiles_a = (g.OH + g.TR - 1) / g.TR;
     g.ntiles = g.tiles_a * (int)((n + IMGS - 1) / IMGS);
-    const int ncb = (g.CO + 31) / 32, ncib = (g.CI + 31) / 32;
-    const int mt = std::max(g.mx, g.md);
-    const void *kern = nullptr;
-    if (K == 3)
-        kern = g.S == 1 ? dw_pick<3, 1>(mt, g.nbuf) : dw_pick<3, 2>(mt, g.nbuf);
-    else
-        kern = g.S == 1 ? dw_pick<1, 1>(mt, g.nbuf) : dw_pick<1, 2>(mt, g.nbuf);
-    if (NZ <= 0) {
-        // persistent: as many workgroups as fit on the chip at once
-        int occ = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, DW_THREADS, lds) !=
-                hipSuccess ||
-            occ < 1)
-            occ = 1;
-        NZ = std::max(1, occ * ctx->num_cus / (ncb * ncib));
-    }
+    const void *kern = kernel_of(g);
+    // persistent: as many workgroups as fit on the chip at once
+    if (NZ <= 0) NZ = slabs_of(kern, lds, g.ntiles);
     NZ = std::min(NZ, g.ntiles);
     g.nz = NZ;
     L.g = g;

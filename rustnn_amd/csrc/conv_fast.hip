@@ -669,9 +669,15 @@ __global__ __launch_bounds__(256) void conv_pack_kernel(const float *__restrict_
 __global__ __launch_bounds__(256) void conv_pack_multi_kernel(const float *__restrict__ src,
                                                               const PackSeg *__restrict__ segs,
                                                               int nseg, float *dst) {
-    int k = 0;
-    while (k + 1 < nseg && segs[k + 1].blk0 <= blockIdx.x) k++;
-    const PackSeg sg = segs[k];
+    int lo = 0, hi = nseg - 1;
+    while (lo < hi) {  // last segment with blk0 <= blockIdx.x
+        const int mid = (lo + hi + 1) >> 1;
+        if (segs[mid].blk0 <= blockIdx.x)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const PackSeg sg = segs[lo];
     const float *w = src + sg.src;
     float *wp = dst + sg.dst;
     for (int r = blockIdx.x - sg.blk0; r < sg.geo.slabs(); r += sg.nblk)

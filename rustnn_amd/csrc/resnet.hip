@@ -134,6 +134,9 @@ struct rnn_resnet {
     PackSeg *psegs = nullptr;
     int npseg = 0, npblk = 0;
     bool packs_dirty = true;
+    // the values last written to scal (lr, momentum, wd, smoothing)
+    float scal_host[4] = {0, 0, 0, 0};
+    bool scal_valid = false;
     size_t fh = 0, fw = 0;  // feature map at the pooling layer
     bool fwd_train = false;  // last forward saved the backward's activations
     // Graph of the train step for the current plan.
@@ -323,6 +326,7 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     r->npseg = (int)psegs.size();
     r->npblk = (int)pblk;
     r->packs_dirty = true;
+    r->scal_valid = false;
     if (!psegs.empty()) {
         hipError_t pe = hipMemcpy(r->psegs, psegs.data(), psegs.size() * sizeof(PackSeg),
                                   hipMemcpyHostToDevice);
@@ -877,7 +881,13 @@ int rnn_resnet_train_step(rnn_resnet *r, size_t n, size_t h, size_t w, const flo
         RNN_HIP(ctx, hipMemcpyAsync(r->labels, labels, n * sizeof(uint32_t),
                                     hipMemcpyDeviceToDevice, ctx->stream));
     }
-    TRY(rnn_set_scalars_launch(ctx, r->scal, lr, momentum, wd, smooth));
+    // the step scalars live in r->scal; rewrite them only when they change
+    const float sc[4] = {lr, momentum, wd, smooth};
+    if (!r->scal_valid || std::memcmp(sc, r->scal_host, sizeof(sc)) != 0) {
+        TRY(rnn_set_scalars_launch(ctx, r->scal, lr, momentum, wd, smooth));
+        std::memcpy(r->scal_host, sc, sizeof(sc));
+        r->scal_valid = true;
+    }
     // The first call of a plan runs eagerly (it also sizes the shared
     // workspace); the second records the graph; later calls replay it.
     TRY(run_step(r));
