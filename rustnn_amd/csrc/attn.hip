@@ -1,6 +1,9 @@
-// Batched small attention (attn.rs Core) on gfx950: one workgroup per
-// (image, head), all operands resident in LDS, 32x32 fp32 MFMA tiles and
-// wave-wide reductions for the row softmax.
+// Batched small attention (attn.rs Core) on gfx950: one workgroup of two
+// waves per (image, head), each wave 32 query rows; the operands live in
+// registers (contiguous half-row loads in the k order the MFMA A and B
+// layouts share), the score tiles are computed transposed (S^T = K Q^T) so
+// that a query row spans lanes l and l^32 only, and 32x32 fp32 MFMA tiles
+// do every product.
 //
 // Reference: Core::forward (attn.rs:148-223) runs per image (rayon) and per
 // head: gather Q/K/V rows, S = QK^T (gemm_small), x = tau*S + rel[idx] with the
