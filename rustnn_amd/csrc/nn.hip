@@ -21,6 +21,7 @@
 namespace {
 
 constexpr int EW_THREADS = 256;
+constexpr int BN_PF = 4;  // items a thread of the BN backward loads before the coefficients
 constexpr int RED_THREADS = 256;
 
 // ------------------------------------------------------------ reductions
@@ -287,23 +288,58 @@ __global__ __launch_bounds__(EW_THREADS) void bn_bwd_apply_kernel(
     RnnBn bn, const double *__restrict__ part, float *dx, int n, int C, int hw, int G,
     FastDiv fd_hw4, int vec) {
     const int ci = blockIdx.x, p = blockIdx.y, P = gridDim.y;
-    double sa = 0.0, sb = 0.0;
-    for (int k = 0; k < P; k++) {
-        sa += part[((size_t)ci * P + k) * 2 + 0];
-        sb += part[((size_t)ci * P + k) * 2 + 1];
-    }
-    const float dg = (float)sa, db = (float)sb;
-    if (p == 0 && threadIdx.x == 0) {
-        if (bn.dgamma) bn.dgamma[ci] += dg;
-        if (bn.dbeta) bn.dbeta[ci] += db;
-    }
-    const float mu = bn.mean[ci], is = bn.invstd[ci], m = bn.m;
-    const float s = bn.gamma[ci] * is / m;
+    const int i0 = p * G, i1 = min(n, i0 + G);
+    float dg, db, mu, is, m, s;
+    auto coefs = [&]() {
+        double sa = 0.0, sb = 0.0;
+        for (int k = 0; k < P; k++) {
+            sa += part[((size_t)ci * P + k) * 2 + 0];
+            sb += part[((size_t)ci * P + k) * 2 + 1];
+        }
+        dg = (float)sa;
+        db = (float)sb;
+        if (p == 0 && threadIdx.x == 0) {
+            if (bn.dgamma) bn.dgamma[ci] += dg;
+            if (bn.dbeta) bn.dbeta[ci] += db;
+        }
+        mu = bn.mean[ci];
+        is = bn.invstd[ci];
+        m = bn.m;
+        s = bn.gamma[ci] * is / m;
+    };
     auto one = [&](float g, float xv) {
         const float xh = (xv - mu) * is;
         return s * (m * g - db - xh * dg);
     };
-    const int i0 = p * G, i1 = min(n, i0 + G);
+    const int hw4 = hw >> 2, tot4 = (i1 - i0) * hw4;
+    if (vec && tot4 <= BN_PF * EW_THREADS) {
+        // the items' loads go out before the partial sums are read
+        float4 dv[BN_PF], xv[BN_PF], mv[BN_PF];
+        size_t q[BN_PF];
+#pragma unroll
+        for (int u = 0; u < BN_PF; u++) {
+            const int e = min((int)threadIdx.x + u * EW_THREADS, tot4 - 1);
+            const int img = (int)div_by((uint32_t)e, fd_hw4), r = e - img * hw4;
+            q[u] = ((size_t)(i0 + img) * C + ci) * hw4 + r;
+            dv[u] = reinterpret_cast<const float4 *>(d)[q[u]];
+            xv[u] = reinterpret_cast<const float4 *>(x)[q[u]];
+            mv[u] = make_float4(1.f, 1.f, 1.f, 1.f);
+            if constexpr (MASK) mv[u] = reinterpret_cast<const float4 *>(mask)[q[u]];
+        }
+        coefs();
+#pragma unroll
+        for (int u = 0; u < BN_PF; u++) {
+            if ((int)threadIdx.x + u * EW_THREADS >= tot4) continue;
+            const float g0 = (MASK && mv[u].x <= 0.0f) ? 0.0f : dv[u].x;
+            const float g1 = (MASK && mv[u].y <= 0.0f) ? 0.0f : dv[u].y;
+            const float g2 = (MASK && mv[u].z <= 0.0f) ? 0.0f : dv[u].z;
+            const float g3 = (MASK && mv[u].w <= 0.0f) ? 0.0f : dv[u].w;
+            reinterpret_cast<float4 *>(dx)[q[u]] = make_float4(
+                one(g0, xv[u].x), one(g1, xv[u].y), one(g2, xv[u].z), one(g3, xv[u].w));
+        }
+        return;
+    }
+    coefs();
     if (vec) {
         const int hw4 = hw >> 2, tot = (i1 - i0) * hw4;
         for (int e = threadIdx.x; e < tot; e += EW_THREADS) {
