@@ -225,6 +225,47 @@ int rnn_softmax_ce(rnn_ctx *ctx, size_t rows, size_t nclass, const float *logits
 int rnn_sgd_step(rnn_ctx *ctx, size_t len, float *v, float *g, float *m, float lr, float momentum,
                  float wd);
 
+/* ----------------------------------------------------------- optim.rs */
+/* Newton-Schulz orthogonalisation (newton_schulz, optim.rs:124-145), in
+ * place on `count` [rows x cols] matrices at g + i*stride: X = G (G^T when
+ * rows > cols) / (||G||_F + 1e-7), then `steps` quintic steps
+ * X = a X + (b A + c A A) X with A = X X^T (a, b, c = 3.4445, -4.7750,
+ * 2.0315), each product a batched GEMM over the matrices. */
+int rnn_newton_schulz(rnn_ctx *ctx, size_t count, size_t rows, size_t cols, size_t steps,
+                      float *g, size_t stride);
+
+/* One parameter of Optim::step_all (nn.rs Param, nn.rs:43-53): device
+ * buffers; v2 (AdamW's second moment, zero-initialised) may be NULL for a
+ * Muon matrix; rows = 0 marks a tensor that is not a matrix. */
+typedef struct {
+    float *v, *g, *m, *v2;
+    size_t len, rows, cols;
+    int decay;
+} rnn_param;
+
+/* Optim (optim.rs:147-235).  rnn_optim_create = Optim::new(muon, ns_steps)
+ * with mom 0.95, b1 0.9, b2 0.999, eps 1e-8, t 0 (rnn_optim_set changes
+ * them).  rnn_optim_step = Optim::step_all(params, lr, wd): matrices with
+ * both sides > 1 take the Muon step when muon is set (Nesterov momentum,
+ * Newton-Schulz, v -= lr (0.2 sqrt(max(rows, cols)) g + wd v)), the rest
+ * AdamW with bias corrections at t + 1; every g is zeroed; t += 1.  Same-shape
+ * matrices run Newton-Schulz together. */
+typedef struct rnn_optim rnn_optim;
+int rnn_optim_create(rnn_ctx *ctx, int muon, size_t ns_steps, rnn_optim **out);
+int rnn_optim_destroy(rnn_optim *opt);
+int rnn_optim_set(rnn_optim *opt, float mom, float b1, float b2, float eps, size_t t);
+size_t rnn_optim_t(const rnn_optim *opt);
+int rnn_optim_step(rnn_optim *opt, size_t nparam, const rnn_param *params, float lr, float wd);
+/* clip_ (optim.rs:237-251) on a flat gradient: the f64 sum of squares in a
+ * fixed order; norm = sqrt as f32; above `max` every element is scaled by
+ * max / norm.  *norm (device, may be NULL) receives the norm. */
+int rnn_clip_grad_norm(rnn_ctx *ctx, size_t len, float *g, float max, float *norm);
+/* Ema::update (optim.rs:283-287): w = d w + (1 - d) v, with d computed by
+ * the caller as min(decay, (1 + t) / (10 + t)). */
+int rnn_ema_update(rnn_ctx *ctx, size_t len, float *w, const float *v, float d);
+/* f32::powi as the reference's bias corrections compute it. */
+float rnn_powi_f32(float a, int b);
+
 /* ----------------------------------------------------------- model.rs */
 /* Device-resident CIFAR ResNet (ResNet::new, model.rs:113-135): depth_n
  * blocks per stage (6n+2 layers), widths width/2w/4w, nclass outputs, Kaiming

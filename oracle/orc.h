@@ -26,8 +26,13 @@
  *                     and the check.rs:503-546 dircheck at its shapes.
  *   attention fwd/bwd -- closed-form f64 softmax attention, finite
  *                     differences for dtau/drel, the check.rs:294-358 shapes.
+ *   optim (Muon/NS, AdamW, clip, EMA) -- float64 numpy restatements of the
+ *                     same iterations, torch's AdamW (decoupled decay, a
+ *                     different but equivalent formula), the Newton-Schulz
+ *                     spectrum property and transposition symmetry.
  *   The multi-thread reduction order of rayon (dW fold/reduce, attention
- *   dtau/drel, linear bias) is "parity unpinned": no reference test pins it.
+ *   dtau/drel, linear bias, clip_'s norm) is "parity unpinned": no reference
+ *   test pins it.
  */
 #ifndef ORC_H
 #define ORC_H
@@ -178,6 +183,16 @@ float orc_softmax_ce(size_t rows, size_t nclass, const float *logits, const uint
                      float smooth, float *dlogits, size_t *correct);
 /* Param::step (nn.rs:102-110). */
 void orc_sgd_step(size_t len, float *v, float *g, float *m, float lr, float mom, float wd);
+
+/* --------------------------------------------------------------- optim.rs */
+float orc_powi(float a, int b);
+void orc_newton_schulz(float *g, size_t rows, size_t cols, size_t steps);
+void orc_muon_step(float *v, float *g, float *m, size_t rows, size_t cols, int decay, float lr,
+                   float wd, float mom, size_t ns_steps);
+void orc_adam_step(size_t n, float *v, float *g, float *m, float *v2, int decay, float lr,
+                   float wd, float b1, float b2, float eps, size_t t);
+float orc_clip(float *g, const size_t *lens, size_t nseg, float max);
+void orc_ema_update(size_t n, float *w, const float *v, float decay, size_t t);
 
 #ifdef __cplusplus
 }

@@ -138,6 +138,16 @@ def lib():
         L.orc_softmax_ce.argtypes = [_sz, _sz, _f32p, _u32p, C.c_float, _f32p, P(_sz)]
         L.orc_softmax_ce.restype = C.c_float
         L.orc_sgd_step.argtypes = [_sz, _f32p, _f32p, _f32p, C.c_float, C.c_float, C.c_float]
+        L.orc_powi.argtypes = [C.c_float, C.c_int]
+        L.orc_powi.restype = C.c_float
+        L.orc_newton_schulz.argtypes = [_f32p, _sz, _sz, _sz]
+        L.orc_muon_step.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, C.c_int, C.c_float,
+                                    C.c_float, C.c_float, _sz]
+        L.orc_adam_step.argtypes = [_sz, _f32p, _f32p, _f32p, _f32p, C.c_int, C.c_float,
+                                    C.c_float, C.c_float, C.c_float, C.c_float, _sz]
+        L.orc_clip.argtypes = [_f32p, P(_sz), _sz, C.c_float]
+        L.orc_clip.restype = C.c_float
+        L.orc_ema_update.argtypes = [_sz, _f32p, _f32p, C.c_float, _sz]
         _lib = L
     return _lib
 
@@ -455,3 +465,42 @@ def sgd_step(v, g, m, lr, mom, wd):
     """Param::step (nn.rs:102-110) in place."""
     _chk(v, g, m)
     lib().orc_sgd_step(v.size, v, g, m, lr, mom, wd)
+
+
+# ---------------------------------------------------------------- optim.rs
+def powi(a, b):
+    """f32::powi with a run-time exponent (compiler-rt __powisf2)."""
+    return float(lib().orc_powi(a, int(b)))
+
+
+def newton_schulz(g, rows, cols, steps):
+    """newton_schulz (optim.rs:124-145); returns the orthogonalised copy."""
+    g = _f(g).ravel().copy()
+    lib().orc_newton_schulz(g, rows, cols, steps)
+    return g
+
+
+def muon_step(v, g, m, rows, cols, decay, lr, wd, mom=0.95, ns_steps=3):
+    """The Muon branch of Optim::step_all (optim.rs:182-195), in place."""
+    _chk(v, g, m)
+    lib().orc_muon_step(v, g, m, rows, cols, int(decay), lr, wd, mom, ns_steps)
+
+
+def adam_step(v, g, m, v2, decay, lr, wd, t, b1=0.9, b2=0.999, eps=1e-8):
+    """Optim::step_adam (optim.rs:207-235) at step count t, in place."""
+    _chk(v, g, m, v2)
+    lib().orc_adam_step(v.size, v, g, m, v2, int(decay), lr, wd, b1, b2, eps, t)
+
+
+def clip(g, lens, max_norm):
+    """clip_ (optim.rs:237-251) over tensors laid end to end in g (in place);
+    returns the global norm."""
+    _chk(g)
+    ls = (_sz * len(lens))(*lens)
+    return float(lib().orc_clip(g, ls, len(lens), max_norm))
+
+
+def ema_update(w, v, decay, t):
+    """Ema::update (optim.rs:270-288) after the first call, in place on w."""
+    _chk(w)
+    lib().orc_ema_update(w.size, w, _f(v).ravel(), decay, t)

@@ -152,6 +152,15 @@ def lib():
             "rnn_resnet_train_step": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, C.c_float, C.c_float,
                                            C.c_float, C.c_float, _vp, _vp]),
             "rnn_resnet_inputs": (_i, [_vp, _sz, _sz, _sz, P(_vp), P(_vp)]),
+            "rnn_newton_schulz": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _sz]),
+            "rnn_optim_create": (_i, [_vp, _i, _sz, P(_vp)]),
+            "rnn_optim_destroy": (_i, [_vp]),
+            "rnn_optim_set": (_i, [_vp, C.c_float, C.c_float, C.c_float, C.c_float, _sz]),
+            "rnn_optim_t": (_sz, [_vp]),
+            "rnn_optim_step": (_i, [_vp, _sz, _vp, C.c_float, C.c_float]),
+            "rnn_clip_grad_norm": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
+            "rnn_ema_update": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
+            "rnn_powi_f32": (C.c_float, [C.c_float, _i]),
             "rnn_resnet_logits": (_i, [_vp, _vp]),
             "rnn_resnet_set_graph": (_i, [_vp, _i]),
             "rnn_resnet_graph_state": (_i, [_vp, P(C.c_char_p)]),
@@ -169,7 +178,7 @@ def declared_symbols(header: str = HEADER):
     """Names of the functions include/rnn.h declares."""
     import re
     txt = open(header).read()
-    return sorted(set(re.findall(r"^\s*(?:int|void \*|const char \*|size_t|uint64_t)\s+(rnn_\w+)\s*\(",
+    return sorted(set(re.findall(r"^\s*(?:int|void \*|const char \*|size_t|uint64_t|float)\s+(rnn_\w+)\s*\(",
                                  txt, re.M)))
 
 
