@@ -227,6 +227,203 @@ def bench_gemm(R, ctx, reps):
     return out
 
 
+# rustvit default configuration (vit.rs:371-387, cli.rs:97-100): Muon with 3
+# Newton-Schulz steps, clip 1.0, EMA 0.9998; 100 fine / 20 coarse classes.
+VIT = dict(width=32, cmid=96, dim=256, heads=4, depth3=5, dim4=384, heads4=6, depth4=2,
+           mem_at=(1, 3), img=32, nclass=100, ncoarse=20, ns=3, clip=1.0, ema=0.9998)
+
+
+def rustvit_param_specs(R):
+    """(len, rows, cols, decay) of every parameter of the default RustViT in
+    for_each_param order (vit.rs:690-716, Block vit.rs:234-249): Linear
+    weights are [fout x fin] matrices (linear.rs:25-33) and take Muon; conv
+    kernels, norms, LayerScale, biases, tau / rel and SeqPool vectors AdamW."""
+    c = VIT
+    out = []
+    conv = lambda cin, cout, k: out.append((cout * cin * k * k, 0, 0, True))  # nn.rs:135
+    vec = lambda n, decay=False: out.append((n, 0, 0, decay))
+
+    def bn(ch):
+        vec(ch)
+        vec(ch)
+
+    def lin(fin, fout, bias=True):
+        out.append((fin * fout, fout, fin, True))
+        if bias:
+            vec(fout)
+
+    def basic(cin, cout, stride):  # model.rs:21-33
+        conv(cin, cout, 3)
+        bn(cout)
+        conv(cout, cout, 3)
+        bn(cout)
+        if stride != 1 or cin != cout:
+            conv(cin, cout, 1)
+            bn(cout)
+
+    def block(ch, h, th, mem):  # vit.rs:108-135
+        hidden = -(-(4 * ch // 3) // 16) * 16
+        nrel = R.rel_index(th, th, th, th)[1]
+        bn(ch)                                  # n1
+        lin(ch, 3 * ch)                         # attn.qkv
+        lin(ch, ch)                             # attn.proj
+        vec(h)                                  # attn.tau
+        vec(h * nrel)                           # attn.rel
+        vec(9 * ch)                             # dw.w
+        vec(ch)                                 # dw.b
+        vec(ch)                                 # gamma
+        vec(ch)                                 # ls1
+        if mem:
+            lin(ch, ch)                         # cross.wq
+            lin(ch, ch)                         # cross.proj
+            vec(h)
+            vec(h * R.rel_index(th, th, 2 * th, 2 * th)[1])
+            vec(ch)                             # lsm
+        bn(ch)                                  # n2
+        lin(ch, 2 * hidden)                     # mlp.wg
+        lin(hidden, ch)                         # mlp.wd
+        vec(ch)                                 # ls2
+
+    w, cm, d, d4 = c["width"], c["cmid"], c["dim"], c["dim4"]
+    th = c["img"] // 4
+    conv(3, w, 3)
+    bn(w)
+    basic(w, w, 1)
+    basic(w, cm, 2)
+    conv(cm, 2 * d, 1)                          # memconv
+    bn(2 * d)                                   # memln
+    conv(cm, d, 3)                              # tokconv
+    bn(d)
+    for i in range(c["depth3"]):
+        block(d, c["heads"], th, i in c["mem_at"])
+    bn(4 * d)                                   # mergeln
+    lin(4 * d, d4)                              # merge
+    for _ in range(c["depth4"]):
+        block(d4, c["heads4"], th // 2, False)
+    bn(d4)                                      # headln
+    vec(d4, True)                               # pool.p
+    lin(d4, c["ncoarse"])                       # head.coarse
+    lin(d4, c["nclass"])                        # head.resid
+    lin(cm, c["nclass"])                        # e1.fc
+    lin(cm, d4, False)                          # e1.hint
+    vec(d, True)                                # pool2.p
+    lin(d, c["nclass"])                         # e2.fc
+    lin(d, d4, False)                           # e2.hint
+    return out
+
+
+def bench_rustvit_optim(R, ctx, reps, cpu_budget):
+    """The optimiser phase of a rustvit train step (train.rs:371-379) over the
+    default model's parameters: clip_ (1.0), Optim::step_all (Muon, 3
+    Newton-Schulz steps; AdamW for the rest) and the EMA update.  Gradients are
+    N(0,1) in one flat buffer that every step refills (one copy, included).
+    Timed from graph replays of `reps` steps (the AdamW bias correction stays
+    at the captured step) and, eagerly, with the Python calls included."""
+    import numpy as np
+    import torch
+    from rustnn_amd.optim import Ema, Optim, Param, clip_
+    specs = rustvit_param_specs(R)
+    total = sum(n for n, _, _, _ in specs)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    gsrc = torch.randn(total, device="cuda", generator=g)
+    gflat = torch.empty_like(gsrc)
+    params, off = [], 0
+    for n, r, cc, dec in specs:
+        p = Param(torch.randn(n, device="cuda", generator=g) * 0.02, dec, r, cc)
+        p.g = gflat[off:off + n]
+        off += n
+        params.append(p)
+    opt = Optim(True, VIT["ns"], ctx=ctx)
+    ema = Ema(VIT["ema"], ctx=ctx)
+    norm = torch.zeros(1, device="cuda")
+    lr, wd = 1e-3, 0.05
+
+    def phase():
+        gflat.copy_(gsrc)
+        clip_(params, VIT["clip"], ctx=ctx, norm=norm)
+        opt.step_all(params, lr, wd)
+        ema.update(params)
+
+    def step_only():
+        gflat.copy_(gsrc)
+        opt.step_all(params, lr, wd)
+
+    for _ in range(3):
+        phase()
+    torch.cuda.synchronize()
+    ms_phase = time_graph(ctx, phase, reps)
+    ms_step = time_graph(ctx, step_only, reps)
+    ms_eager = time_gpu(phase, reps)
+    muon = [(n, r, cc) for n, r, cc, _ in specs if r > 0 and min(r, cc) > 1]
+    ns_flop = 0
+    for _, r, cc in muon:
+        m, n = min(r, cc), max(r, cc)
+        ns_flop += VIT["ns"] * 2.0 * (m * m * n + m * m * m + m * m * n)
+    res = {"workload": "rustvit default (d256x5-384x2, mem at blocks 1,3): clip 1.0 + "
+                       "Muon/AdamW step_all + EMA 0.9998 over every parameter",
+           "params": total, "tensors": len(specs), "muon_matrices": len(muon),
+           "muon_shapes": len({(r, cc) for _, r, cc in muon}),
+           "ms_optimizer_phase": round(ms_phase, 4), "ms_step_all": round(ms_step, 4),
+           "ms_optimizer_phase_eager": round(ms_eager, 4),
+           "ns_tflop_s": round(ns_flop / (ms_step * 1e-3) / 1e12, 3),
+           "timing": "graph replays (ms per phase); eager: back-to-back Python calls"}
+    if cpu_budget > 0:
+        res["cpu_baseline"] = cpu_rustvit_optim(specs, cpu_budget)
+        res["vs_cpu_baseline"] = round(res["cpu_baseline"]["ms"] / ms_phase, 1)
+    opt.close()
+    return res
+
+
+def cpu_rustvit_optim(specs, budget_s):
+    """The oracle's optimiser phase over the same parameter list: clip, then
+    Muon per matrix in parallel over the matrices (the reference's rayon split,
+    optim.rs:177-196), AdamW, the EMA; on host threads."""
+    import numpy as np
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import pyorc as O
+    O.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    threads = max(1, min(threads, 16, os.cpu_count() or 1))
+    rng = np.random.default_rng(3)
+    ps = [dict(v=(rng.standard_normal(n) * 0.02).astype(np.float32),
+               g0=rng.standard_normal(n).astype(np.float32), m=np.zeros(n, np.float32),
+               v2=np.zeros(n, np.float32), w=None, r=r, c=cc, d=dec) for n, r, cc, dec in specs]
+    for p in ps:
+        p["w"] = p["v"].copy()
+    lens = [p["v"].size for p in ps]
+    muon = [p for p in ps if p["r"] > 0 and min(p["r"], p["c"]) > 1]
+    adam = [p for p in ps if not (p["r"] > 0 and min(p["r"], p["c"]) > 1)]
+    gall = np.concatenate([p["g0"] for p in ps])
+    pool = ThreadPoolExecutor(threads)
+
+    def one(t):
+        g = gall.copy()
+        O.clip(g, lens, VIT["clip"])
+        off = 0
+        for p, n in zip(ps, lens):
+            p["g"] = g[off:off + n]
+            off += n
+        list(pool.map(lambda p: O.muon_step(p["v"], p["g"], p["m"], p["r"], p["c"], p["d"],
+                                            1e-3, 0.05, 0.95, VIT["ns"]), muon))
+        for p in adam:
+            O.adam_step(p["v"], p["g"], p["m"], p["v2"], p["d"], 1e-3, 0.05, t)
+        for p in ps:
+            O.ema_update(p["w"], p["v"], VIT["ema"], t + 2)
+
+    one(0)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        one(steps + 1)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or el / steps * (steps + 1) > 2.5 * budget_s:
+            break
+    pool.shutdown()
+    return {"ms": round(el / steps * 1e3, 3), "cores": threads, "kind": "port",
+            "sample": f"{steps} optimiser phases in {el:.1f}s after 1 warm-up; Muon matrices "
+                      f"over {threads} threads, the rest on one"}
+
+
 RESNET = dict(depth_n=3, width=32, nclass=100, batch=128, hw=32, smooth=0.1, lr=0.2, mom=0.9,
               wd=5e-4, seed=7)
 # Each conv op of the ResNet-20 step with its multiplicity (config-1 sweep
@@ -341,6 +538,8 @@ def main():
     ap.add_argument("--attn-only", type=int, default=0, metavar="REPS",
                     help="config 2 only: the attention forward / backward timing with REPS calls "
                          "per graph (the workload of the rocprofv3 kernel trace of attention)")
+    ap.add_argument("--optim-only", type=int, default=0, metavar="REPS",
+                    help="only the rustvit optimiser phase, REPS phases per graph")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build runs on one GPU only (single-GPU tier); "
@@ -359,6 +558,10 @@ def main():
         return
     if args.attn_only:
         print(json.dumps({"attn_only": bench_attention(R, ctx, args.attn_only)}))
+        return
+    if args.optim_only:
+        print(json.dumps({"optim_only": bench_rustvit_optim(R, ctx, args.optim_only,
+                                                            0 if args.no_cpu else 4.0)}))
         return
 
     g = torch.Generator(device="cuda").manual_seed(7)
@@ -470,6 +673,7 @@ def main():
 
     attention = bench_attention(R, ctx, args.op_reps)
     gemms = bench_gemm(R, ctx, args.op_reps)
+    vit_optim = bench_rustvit_optim(R, ctx, 5, 0 if args.no_cpu else args.cpu_budget / 4)
 
     cpu = sweep_cpu = None
     if not args.no_cpu:
@@ -504,7 +708,7 @@ def main():
                                              3),
             "flop_per_step": sweep_flops, "roofline": sweep_roof, "cpu_baseline": sweep_cpu,
             "per_op": per_op},
-        "config2_attention": attention, "gemmbench": gemms,
+        "config2_attention": attention, "gemmbench": gemms, "rustvit_optimizer": vit_optim,
     }
     print(json.dumps(out))
 

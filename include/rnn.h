@@ -260,9 +260,21 @@ int rnn_optim_step(rnn_optim *opt, size_t nparam, const rnn_param *params, float
  * fixed order; norm = sqrt as f32; above `max` every element is scaled by
  * max / norm.  *norm (device, may be NULL) receives the norm. */
 int rnn_clip_grad_norm(rnn_ctx *ctx, size_t len, float *g, float max, float *norm);
+/* clip_ (optim.rs:237-251) over the gradients of a parameter list, as the
+ * reference calls it (train.rs:372-375): one f64 sum of squares over every
+ * gradient, norm = sqrt as f32 into *norm (device, may be NULL); above `max`
+ * every gradient is scaled by max / norm.  The list's pointer table is kept on
+ * the device and uploaded again only when the list changes. */
+int rnn_clip_params(rnn_ctx *ctx, size_t nparam, const rnn_param *params, float max,
+                    float *norm);
 /* Ema::update (optim.rs:283-287): w = d w + (1 - d) v, with d computed by
  * the caller as min(decay, (1 + t) / (10 + t)). */
 int rnn_ema_update(rnn_ctx *ctx, size_t len, float *w, const float *v, float d);
+/* Ema::update over a whole parameter list (train.rs:377-379): w[i] = d w[i] +
+ * (1 - d) params[i].v, one launch for the list (pointer table cached as in
+ * rnn_clip_params). */
+int rnn_ema_update_params(rnn_ctx *ctx, size_t nparam, float *const *w, const rnn_param *params,
+                          float d);
 /* f32::powi as the reference's bias corrections compute it. */
 float rnn_powi_f32(float a, int b);
 

@@ -160,6 +160,8 @@ def lib():
             "rnn_optim_step": (_i, [_vp, _sz, _vp, C.c_float, C.c_float]),
             "rnn_clip_grad_norm": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
             "rnn_ema_update": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
+            "rnn_clip_params": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
+            "rnn_ema_update_params": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
             "rnn_powi_f32": (C.c_float, [C.c_float, _i]),
             "rnn_resnet_logits": (_i, [_vp, _vp]),
             "rnn_resnet_set_graph": (_i, [_vp, _i]),

@@ -83,88 +83,173 @@ struct Slab {
     }
 };
 
+// The MFMA main loop of one BM x BN tile of C = op(A) op(B) over kz values of
+// k, rows m0.. of op(A) and columns n0.. of op(B); leaves the tile in acc.
+template <int BM, int BN, bool AT, bool BT, bool VEC>
+struct GemmTile {
+    static constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
+    f32x16 acc[TM][TN];
+
+    __device__ __forceinline__ void run(const float *A, int lda, int M, const float *B, int ldb,
+                                        int N, int kz, int m0, int n0, float (*As)[BM * LDK],
+                                        float (*Bs)[BN * LDK]) {
+        const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
+        const int wm = wave >> 1, wn = wave & 1;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+
+        Slab<BM, AT, VEC> sa;
+        Slab<BN, !BT, VEC> sb;  // B^T stored [n][k] is the "rows = n" layout
+        const int nk = (kz + BK - 1) / BK;
+        if (nk > 0) {
+            sa.load(A, lda, m0, M, 0, kz, tid);
+            sb.load(B, ldb, n0, N, 0, kz, tid);
+            sa.store(As[0], tid);
+            sb.store(Bs[0], tid);
+        }
+        __syncthreads();
+        const int lr = lane & 31, lh = lane >> 5;
+        for (int it = 0; it < nk; it++) {
+            const int buf = it & 1;
+            if (it + 1 < nk) {
+                sa.load(A, lda, m0, M, (it + 1) * BK, kz, tid);
+                sb.load(B, ldb, n0, N, (it + 1) * BK, kz, tid);
+            }
+#pragma unroll
+            for (int gk = 0; gk < 2; gk++) {
+                float4 af[TM], bf[TN];
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    af[i] = *reinterpret_cast<const float4 *>(
+                        &As[buf][(wm * WTM + i * 32 + lr) * LDK + 8 * gk + 4 * lh]);
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    bf[j] = *reinterpret_cast<const float4 *>(
+                        &Bs[buf][(wn * WTN + j * 32 + lr) * LDK + 8 * gk + 4 * lh]);
+#pragma unroll
+                for (int s = 0; s < 4; s++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int j = 0; j < TN; j++)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
+                                                                             acc[i][j], 0, 0, 0);
+            }
+            if (it + 1 < nk) {
+                sa.store(As[buf ^ 1], tid);
+                sb.store(Bs[buf ^ 1], tid);
+            }
+            __syncthreads();
+        }
+    }
+
+    // Element v of accumulator (i, j) of this lane sits at tile row
+    // wm*WTM + 32i + 8(v/4) + 4(lane/32) + v%4, column wn*WTN + 32j + lane%32
+    // (the 32x32 MFMA accumulator layout).
+    template <typename F>
+    __device__ __forceinline__ void each(F f) const {
+        const int lane = threadIdx.x & 63, wave = wave_index();
+        const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int v = 0; v < 16; v++)
+                    f(wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), wn * WTN + j * 32 + lr,
+                      acc[i][j][v]);
+    }
+};
+
 template <int BM, int BN, bool AT, bool BT, bool VEC>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     __shared__ float As[2][BM * LDK];
     __shared__ float Bs[2][BN * LDK];
-    constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
-    const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
-    const int wm = wave >> 1, wn = wave & 1;
     const long long z = blockIdx.z;
     const float *A = g.a + z * g.stride_a;
     const float *B = g.b + z * g.stride_b;
     float *Cp = g.c + z * g.stride_c;
     const int kz = min(g.kchunk, g.ktotal - (int)z * g.kchunk);
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    GemmTile<BM, BN, AT, BT, VEC> t;
+    t.run(A, g.lda, g.M, B, g.ldb, g.N, kz, m0, n0, As, Bs);
+    t.each([&](int r, int c, float val) {
+        const int row = m0 + r, col = n0 + c;
+        if (row < g.M && col < g.N) {
+            if (g.bias) val += g.bias[col];
+            float *cp = Cp + (long long)row * g.ldc + col;
+            if (g.acc) val = *cp + val;
+            *cp = val;
+        }
+    });
+}
 
-    f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+// One 64 x 64 tile of a grouped Newton-Schulz problem with operand layout
+// (AT, BT); stores C = alpha E + beta (A op(B)) when E is set, else the
+// product, and for a symmetric problem the mirrored tile too.
+template <bool AT, bool BT, bool VEC>
+__device__ __forceinline__ void ns_tile(const NsGemmProb &p, uint32_t z, int ti, int tj,
+                                        float alpha, float beta, float (*As)[64 * LDK],
+                                        float (*Bs)[64 * LDK]) {
+#pragma clang fp contract(off)
+    const int m0 = ti * 64, n0 = tj * 64;
+    GemmTile<64, 64, AT, BT, VEC> t;
+    t.run(p.a + z * p.stride_a, p.lda, p.M, p.b + z * p.stride_b, p.ldb, p.N, p.K, m0, n0, As,
+          Bs);
+    float *Cp = p.c + z * p.stride_c;
+    const float *Ep = p.e ? p.e + z * p.stride_c : nullptr;
+    const bool mirror = p.sym && ti != tj;
+    t.each([&](int rr, int cc, float val) {
+        const int row = m0 + rr, col = n0 + cc;
+        if (row < p.M && col < p.N) {
+            const long long o = (long long)row * p.ldc + col;
+            const float v = Ep ? alpha * Ep[o] + beta * val : val;
+            Cp[o] = v;
+            if (mirror) Cp[(long long)col * p.ldc + row] = v;
+        }
+    });
+}
 
-    Slab<BM, AT, VEC> sa;
-    Slab<BN, !BT, VEC> sb;  // B^T stored [n][k] is the "rows = n" layout
-    const int nk = (kz + BK - 1) / BK;
-    if (nk > 0) {
-        sa.load(A, g.lda, m0, g.M, 0, kz, tid);
-        sb.load(B, g.ldb, n0, g.N, 0, kz, tid);
-        sa.store(As[0], tid);
-        sb.store(Bs[0], tid);
+// Grouped GEMMs of the Newton-Schulz iteration: problem p (found from the
+// block index) is a batch of cnt same-shape products; a symmetric problem
+// (C = C^T, M = N) computes the tiles on and above the diagonal only.
+template <bool VEC>
+__global__ __launch_bounds__(256) void ns_gemm_kernel(const NsGemmProb *__restrict__ probs,
+                                                      int nprob, float alpha, float beta) {
+    __shared__ float As[2][64 * LDK];
+    __shared__ float Bs[2][64 * LDK];
+    int lo = 0, hi = nprob - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (probs[mid].tile0 <= blockIdx.x)
+            lo = mid;
+        else
+            hi = mid - 1;
     }
-    __syncthreads();
-    const int lr = lane & 31, lh = lane >> 5;
-    for (int it = 0; it < nk; it++) {
-        const int buf = it & 1;
-        if (it + 1 < nk) {
-            sa.load(A, g.lda, m0, g.M, (it + 1) * BK, kz, tid);
-            sb.load(B, g.ldb, n0, g.N, (it + 1) * BK, kz, tid);
-        }
-#pragma unroll
-        for (int gk = 0; gk < 2; gk++) {
-            float4 af[TM], bf[TN];
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-                af[i] = *reinterpret_cast<const float4 *>(
-                    &As[buf][(wm * WTM + i * 32 + lr) * LDK + 8 * gk + 4 * lh]);
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-                bf[j] = *reinterpret_cast<const float4 *>(
-                    &Bs[buf][(wn * WTN + j * 32 + lr) * LDK + 8 * gk + 4 * lh]);
-#pragma unroll
-            for (int s = 0; s < 4; s++)
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s],
-                                                                         acc[i][j], 0, 0, 0);
-        }
-        if (it + 1 < nk) {
-            sa.store(As[buf ^ 1], tid);
-            sb.store(Bs[buf ^ 1], tid);
-        }
-        __syncthreads();
+    const NsGemmProb p = probs[lo];
+    const uint32_t local = blockIdx.x - p.tile0;
+    const uint32_t z = local / p.tmn;
+    uint32_t r = local - z * p.tmn;
+    int ti, tj;
+    if (p.sym) {
+        // row ti of the upper triangle holds tn - ti tiles
+        ti = 0;
+        while (r >= p.tn - (uint32_t)ti) r -= p.tn - (uint32_t)ti++;
+        tj = ti + (int)r;
+    } else {
+        ti = (int)(r / p.tn);
+        tj = (int)(r % p.tn);
     }
-    // 32x32 accumulator layout: column lane%32, row 8*(v/4) + 4*(lane/32) + v%4.
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                int row = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                int col = n0 + wn * WTN + j * 32 + lr;
-                if (row < g.M && col < g.N) {
-                    float val = acc[i][j][v];
-                    if (g.bias) val += g.bias[col];
-                    float *cp = Cp + (long long)row * g.ldc + col;
-                    if (g.acc) val = *cp + val;
-                    *cp = val;
-                }
-            }
+    if (p.lay == NS_LAY_NT)
+        ns_tile<false, true, VEC>(p, z, ti, tj, alpha, beta, As, Bs);
+    else if (p.lay == NS_LAY_TN)
+        ns_tile<true, false, VEC>(p, z, ti, tj, alpha, beta, As, Bs);
+    else
+        ns_tile<false, false, VEC>(p, z, ti, tj, alpha, beta, As, Bs);
 }
 
 __global__ void fill_kernel(float *p, long long n, float v) {
@@ -300,6 +385,21 @@ int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, co
     int lda = at ? (int)m : (int)k, ldb = bt ? (int)k : (int)n;
     return gemm_enqueue(ctx, count, m, n, k, k * count, a, stride_a, lda, at, b, stride_b, ldb, bt,
                         c, stride_c, (int)n, acc, bias);
+}
+
+int rnn_ns_gemm_launch(rnn_ctx *ctx, const NsGemmProb *probs, int nprob, size_t ntiles, int vec,
+                       float alpha, float beta) {
+    if (ntiles == 0) return RNN_OK;
+    if (ntiles > 0x7fffffffu) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "ns_gemm: too many tiles");
+    const dim3 grid((unsigned)ntiles);
+    if (vec)
+        hipLaunchKernelGGL(ns_gemm_kernel<true>, grid, dim3(256), 0, ctx->stream, probs, nprob,
+                           alpha, beta);
+    else
+        hipLaunchKernelGGL(ns_gemm_kernel<false>, grid, dim3(256), 0, ctx->stream, probs, nprob,
+                           alpha, beta);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
 }
 
 static int fill(rnn_ctx *ctx, float *p, size_t len, float v) {

@@ -33,24 +33,43 @@ constexpr float NS_C = 2.0315f;
 constexpr int OPT_THREADS = 256;
 constexpr int NS_CHUNK = 4096;  // elements of one matrix per block in the norm passes
 
-// One Muon matrix of a same-shape group.
-struct MuonMat {
-    float *v, *g, *m;
+// One matrix of a Newton-Schulz plan.  Its elementwise passes use one block
+// per NS_CHUNK elements: blocks blk0 .. blk0 + nchunk - 1 of those launches.
+struct NsMat {
+    float *v, *g, *m;  // v and m are null when only g is orthogonalised
+    float *x;          // X slot [rows x cols] in the scratch
+    const float *xf;   // the slot holding X after the last quintic step
+    double *part;      // nchunk partial sums of squares
+    uint32_t blk0, nchunk;
+    int rows, cols, decay;
+    float scale;  // 0.2 sqrt(max(rows, cols))
 };
 
-// Block sums of g'^2 after the momentum update, in element order per thread
-// then a fixed tree: matrix blockIdx.y, chunk blockIdx.x.
-__global__ __launch_bounds__(OPT_THREADS) void muon_momentum_kernel(const MuonMat *__restrict__ mats,
-                                                                    size_t len, float mom,
-                                                                    int momentum, double *part) {
+__device__ __forceinline__ int mat_of(const NsMat *__restrict__ mats, int nmat, unsigned b) {
+    int lo = 0, hi = nmat - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (mats[mid].blk0 <= b)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    return lo;
+}
+
+// Nesterov momentum (optim.rs:186-189: m = mom m + g; g += mom m) and the
+// block sums of g^2: in element order per thread, then a fixed tree.
+__global__ __launch_bounds__(OPT_THREADS) void muon_momentum_kernel(const NsMat *__restrict__ mats,
+                                                                    int nmat, float mom,
+                                                                    int momentum) {
     __shared__ double red[OPT_THREADS / 64];
-    const MuonMat mt = mats[blockIdx.y];
-    const size_t e0 = (size_t)blockIdx.x * NS_CHUNK, e1 = min(len, e0 + NS_CHUNK);
+    const NsMat mt = mats[mat_of(mats, nmat, blockIdx.x)];
+    const size_t chunk = blockIdx.x - mt.blk0, len = (size_t)mt.rows * mt.cols;
+    const size_t e0 = chunk * NS_CHUNK, e1 = min(len, e0 + NS_CHUNK);
     double s = 0.0;
     for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS) {
         float gi = mt.g[e];
         if (momentum) {
-            // Optim::step_all (optim.rs:186-189): m = mom m + g; g += mom m
             const float mi = mom * mt.m[e] + gi;
             mt.m[e] = mi;
             gi += mom * mi;
@@ -64,69 +83,40 @@ __global__ __launch_bounds__(OPT_THREADS) void muon_momentum_kernel(const MuonMa
     if (threadIdx.x == 0) {
         double t = red[0];
         for (int w = 1; w < OPT_THREADS / 64; w++) t += red[w];
-        part[(size_t)blockIdx.y * gridDim.x + blockIdx.x] = t;
+        mt.part[chunk] = t;
     }
 }
 
-// X[i] = G[i] / (||G[i]||_F + 1e-7), transposed when rows > cols
-// (load_maybe_t, optim.rs:41-53, and the normalisation, optim.rs:133-136).
-__global__ __launch_bounds__(OPT_THREADS) void ns_load_kernel(const MuonMat *__restrict__ mats,
-                                                              const double *__restrict__ part,
-                                                              int nchunk, int rows, int cols,
-                                                              int tr, float *x) {
-    const MuonMat mt = mats[blockIdx.y];
+// X = G / (||G||_F + 1e-7) (optim.rs:133-136); the partial sums are added
+// in chunk order.  X keeps G's [rows x cols] layout also when rows > cols: the
+// quintic steps then run on X^T's transpose (load_maybe_t, optim.rs:41-53, has
+// no counterpart here; see ns_layout).
+__global__ __launch_bounds__(OPT_THREADS) void ns_load_kernel(const NsMat *__restrict__ mats,
+                                                              int nmat) {
+    const NsMat mt = mats[mat_of(mats, nmat, blockIdx.x)];
     double ss = 0.0;
-    for (int k = 0; k < nchunk; k++) ss += part[(size_t)blockIdx.y * nchunk + k];
+    for (uint32_t k = 0; k < mt.nchunk; k++) ss += mt.part[k];
     const float norm = sqrtf((float)ss) + 1e-7f;
     const float inv = 1.0f / norm;
-    const size_t len = (size_t)rows * cols;
-    float *xi = x + (size_t)blockIdx.y * len;
-    const size_t e0 = (size_t)blockIdx.x * NS_CHUNK, e1 = min(len, e0 + NS_CHUNK);
-    for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS) {
-        // e indexes X; element (j, i) of X is G[i][j] when transposed
-        size_t src = e;
-        if (tr) {
-            const size_t j = e / rows, i = e - j * rows;
-            src = i * cols + j;
-        }
-        xi[e] = mt.g[src] * inv;
-    }
-}
-
-// B = b A + c AA, in place in A (optim.rs:103-106).
-__global__ void ns_combine_a_kernel(float *a, const float *__restrict__ aa, size_t len) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
-         i += (size_t)gridDim.x * blockDim.x)
-        a[i] = NS_B * a[i] + NS_C * aa[i];
-}
-
-// X = a X + T (optim.rs:118-120).
-__global__ void ns_combine_x_kernel(float *x, const float *__restrict__ t, size_t len) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
-         i += (size_t)gridDim.x * blockDim.x)
-        x[i] = NS_A * x[i] + t[i];
+    const size_t len = (size_t)mt.rows * mt.cols;
+    const size_t e0 = (size_t)(blockIdx.x - mt.blk0) * NS_CHUNK, e1 = min(len, e0 + NS_CHUNK);
+    for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS) mt.x[e] = mt.g[e] * inv;
 }
 
 // End of a Muon step (optim.rs:191-195), reading the orthogonalised matrix
-// straight from X (store_maybe_t folded in): v -= lr (scale x + wd v); g = 0.
-// With update = 0, only the store back into g (newton_schulz alone).
-__global__ void muon_finish_kernel(const MuonMat *__restrict__ mats, const float *__restrict__ x,
-                                   int rows, int cols, int tr, int update, float lr, float scale,
-                                   float wdp) {
-    const MuonMat mt = mats[blockIdx.y];
-    const size_t len = (size_t)rows * cols;
-    const float *xi = x + (size_t)blockIdx.y * len;
-    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < len;
-         e += (size_t)gridDim.x * blockDim.x) {
-        // e indexes G; its X element is (j, i) when transposed
-        size_t xs = e;
-        if (tr) {
-            const size_t i = e / cols, j = e - i * cols;
-            xs = j * rows + i;
-        }
-        const float gx = xi[xs];
+// from its final slot: v -= lr (scale x + wd v); g = 0.  With update = 0 only
+// the store into g (newton_schulz alone).
+__global__ __launch_bounds__(OPT_THREADS) void muon_finish_kernel(const NsMat *__restrict__ mats,
+                                                                  int nmat, int update, float lr,
+                                                                  float wd) {
+    const NsMat mt = mats[mat_of(mats, nmat, blockIdx.x)];
+    const size_t len = (size_t)mt.rows * mt.cols;
+    const size_t e0 = (size_t)(blockIdx.x - mt.blk0) * NS_CHUNK, e1 = min(len, e0 + NS_CHUNK);
+    const float wdp = mt.decay ? wd : 0.0f;
+    for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS) {
+        const float gx = mt.xf[e];
         if (update) {
-            mt.v[e] -= lr * (scale * gx + wdp * mt.v[e]);
+            mt.v[e] -= lr * (mt.scale * gx + wdp * mt.v[e]);
             mt.g[e] = 0.0f;
         } else {
             mt.g[e] = gx;
@@ -139,21 +129,29 @@ __global__ void muon_finish_kernel(const MuonMat *__restrict__ mats, const float
 struct AdamSeg {
     float *v, *g, *m, *v2;
     size_t len;
-    float wd;  // 0 for tensors that do not decay
+    int decay;  // 0: no weight decay for this tensor
     uint32_t blk0, nblk;
 };
 
-__global__ void adam_kernel(const AdamSeg *__restrict__ segs, int nseg, float lr, float b1,
-                            float b2, float eps, float c1, float c2) {
+// Index of the segment whose block range [blk0, blk0 + nblk) holds block b
+// (segments sorted by blk0, the first at 0).
+template <typename Seg>
+__device__ int seg_of(const Seg *__restrict__ segs, int nseg, unsigned b) {
     int lo = 0, hi = nseg - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (segs[mid].blk0 <= blockIdx.x)
+        if (segs[mid].blk0 <= b)
             lo = mid;
         else
             hi = mid - 1;
     }
-    const AdamSeg s = segs[lo];
+    return lo;
+}
+
+__global__ void adam_kernel(const AdamSeg *__restrict__ segs, int nseg, float lr, float wd,
+                            float b1, float b2, float eps, float c1, float c2) {
+    const AdamSeg s = segs[seg_of(segs, nseg, blockIdx.x)];
+    const float wdd = s.decay ? wd : 0.0f;
     for (size_t i = (size_t)(blockIdx.x - s.blk0) * blockDim.x + threadIdx.x; i < s.len;
          i += (size_t)s.nblk * blockDim.x) {
         const float g = s.g[i];
@@ -161,7 +159,7 @@ __global__ void adam_kernel(const AdamSeg *__restrict__ segs, int nseg, float lr
         const float v2 = b2 * s.v2[i] + (1.0f - b2) * g * g;
         s.m[i] = m;
         s.v2[i] = v2;
-        s.v[i] -= lr * ((m / c1) / (sqrtf(v2 / c2) + eps) + s.wd * s.v[i]);
+        s.v[i] -= lr * ((m / c1) / (sqrtf(v2 / c2) + eps) + wdd * s.v[i]);
         s.g[i] = 0.0f;
     }
 }
@@ -184,21 +182,37 @@ __global__ __launch_bounds__(OPT_THREADS) void sumsq_kernel(const float *__restr
     }
 }
 
-// ... then every block adds the partials in order, and scales its share of g
-// by max / norm when the norm is above max (the first block stores the norm).
+// ... then one block adds the partials (a fixed order: per thread a strided
+// sequence, then a fixed tree), stores the norm and the scale max / norm with
+// the flag "norm above max" (sc[0], sc[1]) ...
+__global__ __launch_bounds__(OPT_THREADS) void clip_norm_kernel(const double *__restrict__ part,
+                                                                int nparts, float max,
+                                                                float *norm_out, float *sc) {
+    __shared__ double red[OPT_THREADS / 64];
+    double s = 0.0;
+    for (int k = threadIdx.x; k < nparts; k += OPT_THREADS) s += part[k];
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = red[0];
+        for (int w = 1; w < OPT_THREADS / 64; w++) t += red[w];
+        const float norm = (float)sqrt(t);
+        if (norm_out) *norm_out = norm;
+        const bool clip = norm > max && norm > 0.0f;
+        sc[0] = clip ? max / norm : 1.0f;
+        sc[1] = clip ? 1.0f : 0.0f;
+    }
+}
+
+// ... and every block scales its share of g when the flag is set.
 __global__ __launch_bounds__(OPT_THREADS) void clip_scale_kernel(float *g, size_t len,
-                                                                 const double *__restrict__ part,
-                                                                 int nparts, float max,
-                                                                 float *norm_out) {
-    double sq = 0.0;
-    for (int k = 0; k < nparts; k++) sq += part[k];
-    const float norm = (float)sqrt(sq);
-    if (blockIdx.x == 0 && threadIdx.x == 0 && norm_out) *norm_out = norm;
-    if (!(norm > max && norm > 0.0f)) return;
-    const float sc = max / norm;
+                                                                 const float *__restrict__ sc) {
+    if (sc[1] == 0.0f) return;
+    const float f = sc[0];
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
          i += (size_t)gridDim.x * blockDim.x)
-        g[i] *= sc;
+        g[i] *= f;
 }
 
 // Ema::update (optim.rs:283-287): w = d w + (1 - d) v.
@@ -206,6 +220,75 @@ __global__ void ema_kernel(float *w, const float *__restrict__ v, size_t len, fl
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
          i += (size_t)gridDim.x * blockDim.x)
         w[i] = d * w[i] + (1.0f - d) * v[i];
+}
+
+// clip_ over a list of gradient tensors (optim.rs:237-251).  Sum pass: block b
+// sums the squares of chunk (b - sblk0) of its tensor into part[b]; scale pass:
+// block b scales its share (stride cnblk blocks) of its tensor.
+struct ClipSeg {
+    float *g;
+    size_t len;
+    uint32_t blk0, nblk;    // sum pass: one block per CLIP_CHUNK elements
+    uint32_t cblk0, cnblk;  // scale pass
+};
+constexpr size_t CLIP_CHUNK = 4096;
+
+__global__ __launch_bounds__(OPT_THREADS) void clip_sumsq_kernel(const ClipSeg *__restrict__ segs,
+                                                                 int nseg, double *part) {
+    __shared__ double red[OPT_THREADS / 64];
+    const ClipSeg sg = segs[seg_of(segs, nseg, blockIdx.x)];
+    const size_t e0 = (size_t)(blockIdx.x - sg.blk0) * CLIP_CHUNK;
+    const size_t e1 = min(sg.len, e0 + CLIP_CHUNK);
+    double s = 0.0;
+    for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS)
+        s += (double)sg.g[e] * (double)sg.g[e];
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t = red[0];
+        for (int w = 1; w < OPT_THREADS / 64; w++) t += red[w];
+        part[blockIdx.x] = t;
+    }
+}
+
+struct ClipScaleSeg {
+    uint32_t blk0;
+    int seg;
+};
+
+__global__ __launch_bounds__(OPT_THREADS) void clip_scale_segs_kernel(
+    const ClipSeg *__restrict__ segs, const ClipScaleSeg *__restrict__ sidx, int nseg,
+    const float *__restrict__ sc) {
+    if (sc[1] == 0.0f) return;
+    const float f = sc[0];
+    const ClipSeg sg = segs[sidx[seg_of(sidx, nseg, blockIdx.x)].seg];
+    for (size_t i = (size_t)(blockIdx.x - sg.cblk0) * OPT_THREADS + threadIdx.x; i < sg.len;
+         i += (size_t)sg.cnblk * OPT_THREADS)
+        sg.g[i] *= f;
+}
+
+// Stores zeros (a kernel rather than a memset node, for graph capture).
+__global__ void zero_kernel(float *p, size_t len) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0.0f;
+}
+
+// Ema::update over a list of tensors (optim.rs:283-287): w = d w + (1 - d) v.
+struct EmaSeg {
+    float *w;
+    const float *v;
+    size_t len;
+    uint32_t blk0, nblk;
+};
+
+__global__ __launch_bounds__(OPT_THREADS) void ema_segs_kernel(const EmaSeg *__restrict__ segs,
+                                                               int nseg, float d) {
+    const EmaSeg s = segs[seg_of(segs, nseg, blockIdx.x)];
+    for (size_t i = (size_t)(blockIdx.x - s.blk0) * OPT_THREADS + threadIdx.x; i < s.len;
+         i += (size_t)s.nblk * OPT_THREADS)
+        s.w[i] = d * s.w[i] + (1.0f - d) * s.v[i];
 }
 
 unsigned grid_for(size_t items, unsigned threads) {
@@ -228,15 +311,36 @@ static float powi_f32(float a, int b) {
     return recip ? 1.0f / r : r;
 }
 
+// A grouped Newton-Schulz plan: every matrix's elementwise passes in one
+// launch each, and per quintic step three grouped GEMM launches over all
+// shapes (rnn_ns_gemm_launch).  Offsets are bytes into the device table.
+struct NsPlan {
+    size_t mats = 0, nmat = 0, blocks = 0;  // NsMat table, count, elementwise blocks
+    struct Op {
+        size_t probs = 0, nprob = 0, tiles = 0;
+        int vec = 0;
+        float alpha = 0.0f, beta = 0.0f;
+    };
+    std::vector<Op> ops;  // 3 per quintic step
+};
+
 struct rnn_optim {
     rnn_ctx *ctx = nullptr;
     bool muon = true;
     size_t ns_steps = 3;
     float mom = 0.95f, b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
     size_t t = 0;
-    // device scratch: Newton-Schulz buffers, norm partials, tables
+    // device scratch: Newton-Schulz buffers and norm partials
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // The plan of the last parameter list: Muon matrices, AdamW segments and
+    // the device table holding their pointers.  Rebuilt only when the list
+    // changes, so a training loop uploads nothing after its first step.
+    std::vector<rnn_param> plan_params;
+    size_t plan_steps = 0;
+    NsPlan ns;
+    size_t adam_tab = 0, nseg = 0, adam_blocks = 0;
+    RnnDevTable table;
 };
 
 namespace {
@@ -259,58 +363,258 @@ int ensure_scratch(rnn_optim *o, size_t bytes) {
     return RNN_OK;
 }
 
-// Newton-Schulz (and, with `update`, the rest of the Muon step) for `mats`
-// same-shape matrices whose pointer table sits at the start of the scratch.
-int ns_group(rnn_optim *o, const std::vector<MuonMat> &mats, size_t rows, size_t cols,
-             size_t steps, int momentum, int update, float lr, float wdp) {
-    rnn_ctx *ctx = o->ctx;
-    const size_t cnt = mats.size();
-    const int tr = rows > cols;
-    const size_t m = tr ? cols : rows, n = tr ? rows : cols, len = rows * cols;
-    const size_t nchunk = rnn_div_up(len, NS_CHUNK);
-    WsCarve cv;
-    const size_t o_mats = cv.take(cnt * sizeof(MuonMat));
-    const size_t o_part = cv.take(cnt * nchunk * sizeof(double));
-    const size_t o_x = cv.take(cnt * m * n * sizeof(float));
-    const size_t o_t = cv.take(cnt * m * n * sizeof(float));
-    const size_t o_a = cv.take(cnt * m * m * sizeof(float));
-    const size_t o_aa = cv.take(cnt * m * m * sizeof(float));
-    int rc = ensure_scratch(o, cv.off);
-    if (rc) return rc;
-    char *base = (char *)o->scratch;
-    MuonMat *dm = (MuonMat *)(base + o_mats);
-    double *part = (double *)(base + o_part);
-    float *x = (float *)(base + o_x), *t = (float *)(base + o_t);
-    float *a = (float *)(base + o_a), *aa = (float *)(base + o_aa);
-    RNN_HIP(ctx, hipMemcpyAsync(dm, mats.data(), cnt * sizeof(MuonMat), hipMemcpyHostToDevice,
-                                ctx->stream));
-    const dim3 gchunk((unsigned)nchunk, (unsigned)cnt);
-    muon_momentum_kernel<<<gchunk, OPT_THREADS, 0, ctx->stream>>>(dm, len, o->mom, momentum, part);
-    RNN_LAUNCHED(ctx);
-    ns_load_kernel<<<gchunk, OPT_THREADS, 0, ctx->stream>>>(dm, part, (int)nchunk, (int)rows,
-                                                           (int)cols, tr, x);
-    RNN_LAUNCHED(ctx);
-    for (size_t s = 0; s < steps; s++) {
-        // A = X X^T; AA = A A; B = b A + c AA; T = B X; X = a X + T
-        rc = rnn_gemm_launch(ctx, cnt, m, m, n, x, m * n, 0, x, m * n, 1, a, m * m, 0, nullptr);
-        if (rc) return rc;
-        rc = rnn_gemm_launch(ctx, cnt, m, m, m, a, m * m, 0, a, m * m, 0, aa, m * m, 0, nullptr);
-        if (rc) return rc;
-        ns_combine_a_kernel<<<grid_for(cnt * m * m, OPT_THREADS), OPT_THREADS, 0, ctx->stream>>>(
-            a, aa, cnt * m * m);
-        RNN_LAUNCHED(ctx);
-        rc = rnn_gemm_launch(ctx, cnt, m, n, m, a, m * m, 0, x, m * n, 0, t, m * n, 0, nullptr);
-        if (rc) return rc;
-        ns_combine_x_kernel<<<grid_for(cnt * m * n, OPT_THREADS), OPT_THREADS, 0, ctx->stream>>>(
-            x, t, cnt * m * n);
-        RNN_LAUNCHED(ctx);
+// Host-side table under construction; every piece starts 256-byte aligned.
+struct TableBuf {
+    std::vector<char> b;
+    size_t put(const void *src, size_t bytes) {
+        const size_t off = rnn_round_up(b.size(), 256);
+        b.resize(off + bytes);
+        if (bytes) std::memcpy(b.data() + off, src, bytes);
+        return off;
     }
-    const float scale = 0.2f * sqrtf((float)std::max(rows, cols));
-    muon_finish_kernel<<<dim3((unsigned)std::min<size_t>(rnn_div_up(len, OPT_THREADS), 1024),
-                              (unsigned)cnt),
-                         OPT_THREADS, 0, ctx->stream>>>(dm, x, (int)rows, (int)cols, tr, update,
-                                                        lr, scale, wdp);
+};
+
+// One matrix handed to a Newton-Schulz plan.
+struct NsIn {
+    float *v, *g, *m;
+    size_t rows, cols;
+    int decay;
+};
+
+// Lays out the scratch (offsets from 0) and the tables of a plan over `mats`
+// with `steps` quintic steps; the NsMat and problem tables hold offsets from
+// the scratch base `base` (known when the plan is built: the scratch is sized
+// first).  Returns the scratch bytes needed in *need when base is null.
+void ns_layout(const std::vector<NsIn> &mats, size_t steps, char *base, TableBuf &tab,
+               NsPlan &plan, size_t *need) {
+    // same-shape matrices form a batch of each GEMM
+    std::map<std::pair<size_t, size_t>, std::vector<size_t>> shapes;
+    for (size_t i = 0; i < mats.size(); i++) shapes[{mats[i].rows, mats[i].cols}].push_back(i);
+    WsCarve cv;
+    size_t nchunk_all = 0;
+    for (const NsIn &mt : mats) nchunk_all += rnn_div_up(mt.rows * mt.cols, NS_CHUNK);
+    const size_t o_part = cv.take(nchunk_all * sizeof(double));
+    struct Grp {
+        size_t rows, cols, m, n, cnt, x, t, a, aa;
+    };
+    std::vector<Grp> grps;
+    for (auto &sh : shapes) {
+        Grp g;
+        g.rows = sh.first.first;
+        g.cols = sh.first.second;
+        g.m = std::min(g.rows, g.cols);
+        g.n = std::max(g.rows, g.cols);
+        g.cnt = sh.second.size();
+        g.x = cv.take(g.cnt * g.m * g.n * sizeof(float));
+        g.t = cv.take(g.cnt * g.m * g.n * sizeof(float));
+        g.a = cv.take(g.cnt * g.m * g.m * sizeof(float));
+        g.aa = cv.take(g.cnt * g.m * g.m * sizeof(float));
+        grps.push_back(g);
+    }
+    *need = cv.off;
+    if (!base) return;
+    auto F = [base](size_t off) { return (float *)(base + off); };
+    // the matrices, in shape order (the GEMM batches' order)
+    std::vector<NsMat> nm;
+    size_t part = 0, gi = 0;
+    uint32_t blk = 0;
+    for (auto &sh : shapes) {
+        const Grp &g = grps[gi++];
+        for (size_t k = 0; k < sh.second.size(); k++) {
+            const NsIn &in = mats[sh.second[k]];
+            NsMat e;
+            e.v = in.v;
+            e.g = in.g;
+            e.m = in.m;
+            e.x = F(g.x) + k * g.m * g.n;
+            e.xf = (steps & 1 ? F(g.t) : F(g.x)) + k * g.m * g.n;
+            e.part = (double *)(base + o_part) + part;
+            e.nchunk = (uint32_t)rnn_div_up(g.rows * g.cols, NS_CHUNK);
+            e.blk0 = blk;
+            e.rows = (int)g.rows;
+            e.cols = (int)g.cols;
+            e.decay = in.decay;
+            e.scale = 0.2f * sqrtf((float)g.n);
+            part += e.nchunk;
+            blk += e.nchunk;
+            nm.push_back(e);
+        }
+    }
+    plan.mats = tab.put(nm.data(), nm.size() * sizeof(NsMat));
+    plan.nmat = nm.size();
+    plan.blocks = blk;
+    // Every X slot keeps G's layout [rows x cols].  For a wide G (rows <= cols,
+    // X = G as in the reference) a step is A = X X^T, B = b A + c A A,
+    // X' = a X + B X.  For a tall G the reference iterates on X = G^T; here
+    // Y = X^T = G is iterated directly: A = Y^T Y, B as before, Y' = a Y + Y B
+    // (the transpose of X' = a X + B X, B being symmetric).  A and B are
+    // symmetric (each element and its mirror are the same products in the
+    // same order), so only their upper tiles are computed, A A is taken as
+    // A A^T, and B is read as B^T where that keeps k contiguous.
+    std::vector<size_t> order(grps.size());
+    for (size_t i = 0; i < order.size(); i++) order[i] = i;
+    plan.ops.clear();
+    for (size_t s = 0; s < steps; s++) {
+        for (int op = 0; op < 3; op++) {
+            // longest k first: the long tiles start early
+            std::stable_sort(order.begin(), order.end(), [&](size_t p, size_t q) {
+                return (op == 0 ? grps[p].n : grps[p].m) > (op == 0 ? grps[q].n : grps[q].m);
+            });
+            std::vector<NsGemmProb> probs;
+            uint32_t tile = 0;
+            bool vec = true;
+            for (size_t k : order) {
+                const Grp &g = grps[k];
+                const size_t m = g.m, n = g.n;
+                const bool tall = g.rows > g.cols;
+                float *xs = (s & 1) ? F(g.t) : F(g.x), *xn = (s & 1) ? F(g.x) : F(g.t);
+                NsGemmProb p{};
+                p.stride_c = (long long)(op == 2 ? m * n : m * m);
+                if (op == 0) {
+                    // A [m x m] = X X^T (X [m][n]) or Y^T Y (Y [n][m])
+                    p.a = xs;
+                    p.b = xs;
+                    p.c = F(g.a);
+                    p.stride_a = p.stride_b = (long long)(m * n);
+                    p.M = p.N = (int)m;
+                    p.K = (int)n;
+                    p.lda = p.ldb = tall ? (int)m : (int)n;
+                    p.ldc = (int)m;
+                    p.lay = tall ? NS_LAY_TN : NS_LAY_NT;
+                    p.sym = 1;
+                    if (!tall) vec = vec && n % 4 == 0;
+                } else if (op == 1) {
+                    // B = b A + c A A^T, into the AA slot
+                    p.a = p.b = F(g.a);
+                    p.c = F(g.aa);
+                    p.e = F(g.a);
+                    p.stride_a = p.stride_b = (long long)(m * m);
+                    p.M = p.N = p.K = (int)m;
+                    p.lda = p.ldb = p.ldc = (int)m;
+                    p.lay = NS_LAY_NT;
+                    p.sym = 1;
+                    vec = vec && m % 4 == 0;
+                } else if (!tall) {
+                    // X' = a X + B X: [m x m] [m x n]
+                    p.a = F(g.aa);
+                    p.b = xs;
+                    p.c = xn;
+                    p.e = xs;
+                    p.stride_a = (long long)(m * m);
+                    p.stride_b = (long long)(m * n);
+                    p.M = (int)m;
+                    p.N = (int)n;
+                    p.K = (int)m;
+                    p.lda = (int)m;
+                    p.ldb = p.ldc = (int)n;
+                    p.lay = NS_LAY_NN;
+                    vec = vec && m % 4 == 0;
+                } else {
+                    // Y' = a Y + Y B^T: [n x m] [m x m]
+                    p.a = xs;
+                    p.b = F(g.aa);
+                    p.c = xn;
+                    p.e = xs;
+                    p.stride_a = (long long)(m * n);
+                    p.stride_b = (long long)(m * m);
+                    p.M = (int)n;
+                    p.N = (int)m;
+                    p.K = (int)m;
+                    p.lda = p.ldb = p.ldc = (int)m;
+                    p.lay = NS_LAY_NT;
+                    vec = vec && m % 4 == 0;
+                }
+                p.tn = (uint32_t)rnn_div_up((size_t)p.N, 64);
+                p.tmn = p.sym ? p.tn * (p.tn + 1) / 2
+                              : (uint32_t)rnn_div_up((size_t)p.M, 64) * p.tn;
+                p.tile0 = tile;
+                tile += (uint32_t)(g.cnt * p.tmn);
+                probs.push_back(p);
+            }
+            NsPlan::Op o;
+            o.probs = tab.put(probs.data(), probs.size() * sizeof(NsGemmProb));
+            o.nprob = probs.size();
+            o.tiles = tile;
+            o.vec = vec;
+            o.alpha = op == 0 ? 0.0f : (op == 1 ? NS_B : NS_A);
+            o.beta = op == 0 ? 0.0f : (op == 1 ? NS_C : 1.0f);
+            plan.ops.push_back(o);
+        }
+    }
+}
+
+// Runs a plan whose table sits at `tab` (device): momentum (when set), the
+// normalised load, the quintic steps, then the update (or the store into g).
+int ns_run(rnn_ctx *ctx, const NsPlan &plan, const char *tab, float mom, int momentum,
+           int update, float lr, float wd) {
+    if (!plan.nmat) return RNN_OK;
+    const NsMat *mats = (const NsMat *)(tab + plan.mats);
+    const int nmat = (int)plan.nmat;
+    const dim3 grid((unsigned)plan.blocks);
+    muon_momentum_kernel<<<grid, OPT_THREADS, 0, ctx->stream>>>(mats, nmat, mom, momentum);
     RNN_LAUNCHED(ctx);
+    ns_load_kernel<<<grid, OPT_THREADS, 0, ctx->stream>>>(mats, nmat);
+    RNN_LAUNCHED(ctx);
+    for (const NsPlan::Op &op : plan.ops) {
+        const int rc = rnn_ns_gemm_launch(ctx, (const NsGemmProb *)(tab + op.probs), (int)op.nprob,
+                                          op.tiles, op.vec, op.alpha, op.beta);
+        if (rc) return rc;
+    }
+    muon_finish_kernel<<<grid, OPT_THREADS, 0, ctx->stream>>>(mats, nmat, update, lr, wd);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+bool same_param(const rnn_param &a, const rnn_param &b) {
+    return a.v == b.v && a.g == b.g && a.m == b.m && a.v2 == b.v2 && a.len == b.len &&
+           a.rows == b.rows && a.cols == b.cols && (a.decay != 0) == (b.decay != 0);
+}
+
+// Builds the plan of `params` (already validated) and uploads its table.
+int build_plan(rnn_optim *o, size_t nparam, const rnn_param *params) {
+    rnn_ctx *ctx = o->ctx;
+    // Optim::step_all (optim.rs:177-205): 2-D matrices with both sides > 1 go
+    // to Muon (when enabled), everything else to AdamW.
+    std::vector<NsIn> mats;
+    std::vector<AdamSeg> segs;
+    uint32_t blk = 0;
+    for (size_t i = 0; i < nparam; i++) {
+        const rnn_param &p = params[i];
+        if (o->muon && p.rows > 0 && std::min(p.rows, p.cols) > 1) {
+            mats.push_back({p.v, p.g, p.m, p.rows, p.cols, p.decay != 0});
+        } else if (p.len) {
+            AdamSeg sg;
+            sg.v = p.v;
+            sg.g = p.g;
+            sg.m = p.m;
+            sg.v2 = p.v2;
+            sg.len = p.len;
+            sg.decay = p.decay != 0;
+            sg.blk0 = blk;
+            sg.nblk = (uint32_t)std::min<size_t>(rnn_div_up(p.len, OPT_THREADS), 1024);
+            blk += sg.nblk;
+            segs.push_back(sg);
+        }
+    }
+    // the old plan is dropped before anything can fail half-way
+    o->plan_params.clear();
+    TableBuf tab;
+    NsPlan plan;
+    size_t need = 0;
+    ns_layout(mats, o->ns_steps, nullptr, tab, plan, &need);
+    int rc = ensure_scratch(o, need);
+    if (rc) return rc;
+    ns_layout(mats, o->ns_steps, (char *)o->scratch, tab, plan, &need);
+    const size_t adam_tab = segs.empty() ? 0 : tab.put(segs.data(), segs.size() * sizeof(AdamSeg));
+    void *dev = nullptr;
+    rc = rnn_dev_table(ctx, o->table, tab.b.data(), tab.b.size(), &dev);
+    if (rc) return rc;
+    o->ns = std::move(plan);
+    o->adam_tab = adam_tab;
+    o->nseg = segs.size();
+    o->adam_blocks = blk;
+    o->plan_params.assign(params, params + nparam);
+    o->plan_steps = o->ns_steps;
     return RNN_OK;
 }
 
@@ -332,16 +636,25 @@ int rnn_newton_schulz(rnn_ctx *ctx, size_t count, size_t rows, size_t cols, size
     if (!muon_shape_ok(rows, cols) || stride < rows * cols || count > 65535)
         return rnn_fail(ctx, RNN_E_INVALID, "newton_schulz: %zu x %zu, stride %zu, count %zu",
                         rows, cols, stride, count);
-    // a private optimiser object for the scratch
+    // a private optimiser object for the scratch and the table
     rnn_optim o;
     o.ctx = ctx;
-    std::vector<MuonMat> mats(count);
-    for (size_t i = 0; i < count; i++) mats[i] = {nullptr, g + i * stride, nullptr};
-    const int rc = ns_group(&o, mats, rows, cols, steps, 0, 0, 0.0f, 0.0f);
-    if (o.scratch) {
-        (void)hipStreamSynchronize(ctx->stream);
-        (void)hipFree(o.scratch);
+    std::vector<NsIn> mats(count);
+    for (size_t i = 0; i < count; i++) mats[i] = {nullptr, g + i * stride, nullptr, rows, cols, 0};
+    TableBuf tab;
+    NsPlan plan;
+    size_t need = 0;
+    ns_layout(mats, steps, nullptr, tab, plan, &need);
+    int rc = ensure_scratch(&o, need);
+    if (!rc) {
+        ns_layout(mats, steps, (char *)o.scratch, tab, plan, &need);
+        void *dev = nullptr;
+        rc = rnn_dev_table(ctx, o.table, tab.b.data(), tab.b.size(), &dev);
+        if (!rc) rc = ns_run(ctx, plan, (const char *)dev, 0.0f, 0, 0, 0.0f, 0.0f);
     }
+    (void)hipStreamSynchronize(ctx->stream);
+    if (o.scratch) (void)hipFree(o.scratch);
+    rnn_dev_table_free(o.table);
     return rc;
 }
 
@@ -357,10 +670,9 @@ int rnn_optim_create(rnn_ctx *ctx, int muon, size_t ns_steps, rnn_optim **out) {
 
 int rnn_optim_destroy(rnn_optim *o) {
     if (!o) return RNN_E_NULL;
-    if (o->scratch) {
-        (void)hipStreamSynchronize(o->ctx->stream);
-        (void)hipFree(o->scratch);
-    }
+    (void)hipStreamSynchronize(o->ctx->stream);
+    if (o->scratch) (void)hipFree(o->scratch);
+    rnn_dev_table_free(o->table);
     delete o;
     return RNN_OK;
 }
@@ -382,12 +694,12 @@ int rnn_optim_step(rnn_optim *o, size_t nparam, const rnn_param *params, float l
     rnn_ctx *ctx = o->ctx;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     if (nparam && !params) return rnn_fail(ctx, RNN_E_NULL, "optim_step: null params");
-    // Optim::step_all (optim.rs:177-205): 2-D matrices with both sides > 1 go
-    // to Muon (when enabled), everything else to AdamW.
-    std::map<std::pair<size_t, size_t>, std::vector<size_t>> groups;
-    std::vector<size_t> adam;
+    bool same = o->plan_params.size() == nparam && (nparam > 0 || o->table.dev);
     for (size_t i = 0; i < nparam; i++) {
         const rnn_param &p = params[i];
+        if (same && same_param(p, o->plan_params[i])) continue;
+        same = false;
+        if (p.len == 0 && p.rows == 0) continue;  // an empty tensor: nothing to update
         if (!p.v || !p.g || !p.m)
             return rnn_fail(ctx, RNN_E_NULL, "optim_step: param %zu has a null buffer", i);
         const bool is_muon = o->muon && p.rows > 0 && std::min(p.rows, p.cols) > 1;
@@ -395,58 +707,25 @@ int rnn_optim_step(rnn_optim *o, size_t nparam, const rnn_param *params, float l
             if (p.rows * p.cols != p.len || !muon_shape_ok(p.rows, p.cols))
                 return rnn_fail(ctx, RNN_E_INVALID, "optim_step: param %zu is %zu x %zu, len %zu",
                                 i, p.rows, p.cols, p.len);
-            groups[{p.rows, p.cols}].push_back(i);
-        } else {
-            if (!p.v2) return rnn_fail(ctx, RNN_E_NULL, "optim_step: param %zu has no v2", i);
-            adam.push_back(i);
+        } else if (!p.v2) {
+            return rnn_fail(ctx, RNN_E_NULL, "optim_step: param %zu has no v2", i);
         }
     }
-    for (auto &gr : groups) {
-        // matrices of one shape and one decay setting share a launch sequence
-        for (int dec = 0; dec < 2; dec++) {
-            std::vector<MuonMat> mats;
-            for (size_t i : gr.second)
-                if ((params[i].decay != 0) == (dec != 0))
-                    mats.push_back({params[i].v, params[i].g, params[i].m});
-            for (size_t c0 = 0; c0 < mats.size(); c0 += 65535) {
-                std::vector<MuonMat> part(mats.begin() + c0,
-                                          mats.begin() + std::min(mats.size(), c0 + 65535));
-                const int rc = ns_group(o, part, gr.first.first, gr.first.second, o->ns_steps, 1,
-                                        1, lr, dec ? wd : 0.0f);
-                if (rc) return rc;
-            }
-        }
+    if (o->plan_steps != o->ns_steps) same = false;
+    if (!same) {
+        const int rc = build_plan(o, nparam, params);
+        if (rc) return rc;
     }
-    if (!adam.empty()) {
-        std::vector<AdamSeg> segs;
-        uint32_t blk = 0;
-        for (size_t i : adam) {
-            const rnn_param &p = params[i];
-            if (p.len == 0) continue;
-            AdamSeg s;
-            s.v = p.v;
-            s.g = p.g;
-            s.m = p.m;
-            s.v2 = p.v2;
-            s.len = p.len;
-            s.wd = p.decay ? wd : 0.0f;
-            s.blk0 = blk;
-            s.nblk = (uint32_t)std::min<size_t>(rnn_div_up(p.len, OPT_THREADS), 1024);
-            blk += s.nblk;
-            segs.push_back(s);
-        }
-        if (!segs.empty()) {
-            int rc = ensure_scratch(o, segs.size() * sizeof(AdamSeg));
-            if (rc) return rc;
-            RNN_HIP(ctx, hipMemcpyAsync(o->scratch, segs.data(), segs.size() * sizeof(AdamSeg),
-                                        hipMemcpyHostToDevice, ctx->stream));
-            const float c1 = 1.0f - powi_f32(o->b1, (int)o->t + 1);
-            const float c2 = 1.0f - powi_f32(o->b2, (int)o->t + 1);
-            adam_kernel<<<blk, OPT_THREADS, 0, ctx->stream>>>((const AdamSeg *)o->scratch,
-                                                             (int)segs.size(), lr, o->b1, o->b2,
-                                                             o->eps, c1, c2);
-            RNN_LAUNCHED(ctx);
-        }
+    const char *tab = (const char *)o->table.dev;
+    int rc = ns_run(ctx, o->ns, tab, o->mom, 1, 1, lr, wd);
+    if (rc) return rc;
+    if (o->nseg) {
+        const float c1 = 1.0f - powi_f32(o->b1, (int)o->t + 1);
+        const float c2 = 1.0f - powi_f32(o->b2, (int)o->t + 1);
+        adam_kernel<<<(unsigned)o->adam_blocks, OPT_THREADS, 0, ctx->stream>>>(
+            (const AdamSeg *)(tab + o->adam_tab), (int)o->nseg, lr, wd, o->b1, o->b2, o->eps, c1,
+            c2);
+        RNN_LAUNCHED(ctx);
     }
     // after the step, not before: step_adam corrects the bias with t + 1
     o->t += 1;
@@ -457,14 +736,19 @@ int rnn_clip_grad_norm(rnn_ctx *ctx, size_t len, float *g, float max, float *nor
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     if (!g && len) return rnn_fail(ctx, RNN_E_NULL, "clip_grad_norm: null g");
-    const size_t chunk = 16384;
+    const size_t chunk = CLIP_CHUNK;
     const size_t nparts = std::max<size_t>(1, rnn_div_up(len, chunk));
-    double *part = (double *)rnn_workspace(ctx, nparts * sizeof(double));
-    if (!part) return rnn_fail(ctx, RNN_E_NOMEM, "clip_grad_norm: workspace");
+    WsCarve cv;
+    const size_t o_sc = cv.take(2 * sizeof(float)), o_part = cv.take(nparts * sizeof(double));
+    char *ws = (char *)rnn_workspace(ctx, cv.off);
+    if (!ws) return rnn_fail(ctx, RNN_E_NOMEM, "clip_grad_norm: workspace");
+    float *sc = (float *)(ws + o_sc);
+    double *part = (double *)(ws + o_part);
     sumsq_kernel<<<(unsigned)nparts, OPT_THREADS, 0, ctx->stream>>>(g, len, chunk, part);
     RNN_LAUNCHED(ctx);
-    clip_scale_kernel<<<grid_for(len, OPT_THREADS), OPT_THREADS, 0, ctx->stream>>>(
-        g, len, part, (int)nparts, max, norm);
+    clip_norm_kernel<<<1, OPT_THREADS, 0, ctx->stream>>>(part, (int)nparts, max, norm, sc);
+    RNN_LAUNCHED(ctx);
+    clip_scale_kernel<<<grid_for(len, OPT_THREADS), OPT_THREADS, 0, ctx->stream>>>(g, len, sc);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -475,6 +759,94 @@ int rnn_ema_update(rnn_ctx *ctx, size_t len, float *w, const float *v, float d) 
     if (len == 0) return RNN_OK;
     if (!w || !v) return rnn_fail(ctx, RNN_E_NULL, "ema_update: null pointer");
     ema_kernel<<<grid_for(len, OPT_THREADS), OPT_THREADS, 0, ctx->stream>>>(w, v, len, d);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_clip_params(rnn_ctx *ctx, size_t nparam, const rnn_param *params, float max,
+                    float *norm) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (nparam && !params) return rnn_fail(ctx, RNN_E_NULL, "clip_params: null params");
+    std::vector<ClipSeg> segs;
+    uint32_t sblk = 0, cblk = 0;
+    for (size_t i = 0; i < nparam; i++) {
+        if (params[i].len == 0) continue;
+        if (!params[i].g)
+            return rnn_fail(ctx, RNN_E_NULL, "clip_params: param %zu has a null gradient", i);
+        ClipSeg sg;
+        sg.g = params[i].g;
+        sg.len = params[i].len;
+        sg.blk0 = sblk;
+        sg.nblk = (uint32_t)rnn_div_up(sg.len, CLIP_CHUNK);
+        sg.cblk0 = cblk;
+        sg.cnblk = (uint32_t)std::min<size_t>(rnn_div_up(sg.len, OPT_THREADS), 1024);
+        sblk += sg.nblk;
+        cblk += sg.cnblk;
+        segs.push_back(sg);
+    }
+    if (segs.empty()) {
+        // no gradient at all: the norm is 0 and nothing is scaled
+        if (norm) {
+            zero_kernel<<<1, 64, 0, ctx->stream>>>(norm, 1);
+            RNN_LAUNCHED(ctx);
+        }
+        return RNN_OK;
+    }
+    std::vector<char> tab(rnn_round_up(segs.size() * sizeof(ClipSeg), 256) +
+                          segs.size() * sizeof(ClipScaleSeg));
+    std::memcpy(tab.data(), segs.data(), segs.size() * sizeof(ClipSeg));
+    ClipScaleSeg *sidx = (ClipScaleSeg *)(tab.data() + rnn_round_up(segs.size() * sizeof(ClipSeg),
+                                                                    256));
+    for (size_t k = 0; k < segs.size(); k++) sidx[k] = {segs[k].cblk0, (int)k};
+    void *dev = nullptr;
+    int rc = rnn_dev_table(ctx, ctx->tables[RNN_TABLE_CLIP], tab.data(), tab.size(), &dev);
+    if (rc) return rc;
+    WsCarve cv;
+    const size_t o_sc = cv.take(2 * sizeof(float)), o_part = cv.take(sblk * sizeof(double));
+    char *ws = (char *)rnn_workspace(ctx, cv.off);
+    if (!ws) return rnn_fail(ctx, RNN_E_NOMEM, "clip_params: workspace");
+    float *sc = (float *)(ws + o_sc);
+    double *part = (double *)(ws + o_part);
+    const ClipSeg *dsegs = (const ClipSeg *)dev;
+    const ClipScaleSeg *dsidx = (const ClipScaleSeg *)((char *)dev + ((char *)sidx - tab.data()));
+    clip_sumsq_kernel<<<sblk, OPT_THREADS, 0, ctx->stream>>>(dsegs, (int)segs.size(), part);
+    RNN_LAUNCHED(ctx);
+    clip_norm_kernel<<<1, OPT_THREADS, 0, ctx->stream>>>(part, (int)sblk, max, norm, sc);
+    RNN_LAUNCHED(ctx);
+    clip_scale_segs_kernel<<<cblk, OPT_THREADS, 0, ctx->stream>>>(dsegs, dsidx, (int)segs.size(),
+                                                                  sc);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_ema_update_params(rnn_ctx *ctx, size_t nparam, float *const *w, const rnn_param *params,
+                          float d) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (nparam && (!params || !w)) return rnn_fail(ctx, RNN_E_NULL, "ema_update_params: null list");
+    std::vector<EmaSeg> segs;
+    uint32_t blk = 0;
+    for (size_t i = 0; i < nparam; i++) {
+        if (params[i].len == 0) continue;
+        if (!w[i] || !params[i].v)
+            return rnn_fail(ctx, RNN_E_NULL, "ema_update_params: tensor %zu is null", i);
+        EmaSeg sg;
+        sg.w = w[i];
+        sg.v = params[i].v;
+        sg.len = params[i].len;
+        sg.blk0 = blk;
+        sg.nblk = (uint32_t)std::min<size_t>(rnn_div_up(sg.len, OPT_THREADS), 1024);
+        blk += sg.nblk;
+        segs.push_back(sg);
+    }
+    if (segs.empty()) return RNN_OK;
+    void *dev = nullptr;
+    int rc = rnn_dev_table(ctx, ctx->tables[RNN_TABLE_EMA], segs.data(),
+                           segs.size() * sizeof(EmaSeg), &dev);
+    if (rc) return rc;
+    ema_segs_kernel<<<blk, OPT_THREADS, 0, ctx->stream>>>((const EmaSeg *)dev, (int)segs.size(),
+                                                         d);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

@@ -43,6 +43,44 @@ void *rnn_workspace(rnn_ctx *ctx, size_t bytes) {
     return ctx->ws;
 }
 
+int rnn_dev_table(rnn_ctx *ctx, RnnDevTable &t, const void *src, size_t bytes, void **dev) {
+    if (t.dev && bytes == t.host.size() &&
+        (bytes == 0 || std::memcmp(t.host.data(), src, bytes) == 0)) {
+        *dev = t.dev;
+        return RNN_OK;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    RNN_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return rnn_fail(ctx, RNN_E_INVALID,
+                        "tensor list changed during graph capture (call once before capturing)");
+    RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    const size_t want = rnn_round_up(bytes ? bytes : 256, 256);
+    if (want > t.cap) {
+        if (t.dev) (void)hipFree(t.dev);
+        t.dev = nullptr;
+        t.cap = 0;
+        hipError_t e = hipMalloc(&t.dev, want);
+        if (e != hipSuccess) {
+            t.dev = nullptr;
+            return rnn_fail(ctx, RNN_E_NOMEM, "table hipMalloc(%zu): %s", want,
+                            hipGetErrorString(e));
+        }
+        t.cap = want;
+    }
+    if (bytes) RNN_HIP(ctx, hipMemcpy(t.dev, src, bytes, hipMemcpyHostToDevice));
+    t.host.assign((const char *)src, (const char *)src + bytes);
+    *dev = t.dev;
+    return RNN_OK;
+}
+
+void rnn_dev_table_free(RnnDevTable &t) {
+    if (t.dev) (void)hipFree(t.dev);
+    t.dev = nullptr;
+    t.cap = 0;
+    t.host.clear();
+}
+
 extern "C" {
 
 const char *rnn_status_string(int s) {
@@ -85,6 +123,7 @@ int rnn_ctx_destroy(rnn_ctx *ctx) {
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->rel_dev) (void)hipFree(ctx->rel_dev);
     if (ctx->rel_pinned) (void)hipHostFree(ctx->rel_pinned);
+    for (auto &kv : ctx->tables) rnn_dev_table_free(kv.second);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
     return RNN_OK;

@@ -7,10 +7,20 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstdio>
+#include <map>
 #include <mutex>
 #include <vector>
 
 #include "../../include/rnn.h"
+
+// A small table (pointers, lengths) kept on the device for kernels that walk a
+// list of tensors.  Uploaded again only when its bytes change, so a caller
+// that passes the same list every step issues no copy after the first.
+struct RnnDevTable {
+    std::vector<char> host;  // bytes of the last upload
+    void *dev = nullptr;
+    size_t cap = 0;
+};
 
 struct rnn_ctx {
     int device = 0;
@@ -31,6 +41,8 @@ struct rnn_ctx {
     size_t rel_pinned_cap = 0;
     uint32_t rel_nrel = 0;
     uint32_t rel_tk = 0;
+    // Tensor-list tables of the optimizer entry points (slot -> table).
+    std::map<int, RnnDevTable> tables;
     std::recursive_mutex mu;
     char err[512] = {0};
 };
@@ -59,6 +71,16 @@ int rnn_fail(rnn_ctx *ctx, int code, const char *fmt, ...);
 // nullptr after recording RNN_E_NOMEM / RNN_E_HIP in ctx.
 void *rnn_workspace(rnn_ctx *ctx, size_t bytes);
 
+// Device copy of `bytes` bytes at `src` in table `t`: a table whose bytes are
+// unchanged since its last upload is reused as it is; otherwise the stream is
+// drained (queued kernels may still read the old copy), the copy is made
+// synchronously, and the new device address returned in *dev.  An upload is
+// refused while the stream is being captured into a graph.
+int rnn_dev_table(rnn_ctx *ctx, RnnDevTable &t, const void *src, size_t bytes, void **dev);
+void rnn_dev_table_free(RnnDevTable &t);
+// Slots of rnn_ctx::tables.
+enum { RNN_TABLE_CLIP = 1, RNN_TABLE_EMA = 2 };
+
 // Bump allocator over one workspace block.
 struct WsCarve {
     size_t off = 0;
@@ -83,6 +105,33 @@ __device__ __forceinline__ int wave_index() {
 }
 
 // Entry points implemented in the kernel sources, called from the C ABI.
+// One batch of the grouped Newton-Schulz GEMMs (rnn_ns_gemm_launch): cnt
+// products C_z = op(A_z) op(B_z) of one shape, [M x K] times [K x N].  The
+// layout `lay` says how the operands are stored: NS_LAY_NT: A [M][K], B [N][K];
+// NS_LAY_TN: A [K][M], B [K][N]; NS_LAY_NN: A [M][K], B [K][N] (leading
+// dimensions lda, ldb).  C and the optional epilogue source E share ldc and
+// stride_c.  sym: C is symmetric (M = N, and E symmetric too); only tiles on
+// or above the diagonal are computed, each stored twice.  The problem's 64 x 64
+// tiles are blocks tile0 .. tile0 + cnt * tmn - 1 of the launch, tn tiles along
+// N (tmn = tn (tn + 1) / 2 when sym).
+enum { NS_LAY_NT = 0, NS_LAY_TN = 1, NS_LAY_NN = 2 };
+struct NsGemmProb {
+    const float *a, *b;
+    float *c;
+    const float *e;
+    long long stride_a, stride_b, stride_c;
+    int M, N, K, lda, ldb, ldc;
+    uint32_t tile0, tn, tmn;
+    int lay, sym;
+};
+
+// One launch over `nprob` problems (device table, sorted by tile0, the first
+// at 0) covering `ntiles` tiles: C = alpha E + beta (A op(B)) where E is set,
+// else the product.  vec: every k-contiguous operand row and batch stride is a
+// multiple of 4 floats and 16-byte aligned.
+int rnn_ns_gemm_launch(rnn_ctx *ctx, const NsGemmProb *probs, int nprob, size_t ntiles, int vec,
+                       float alpha, float beta);
+
 int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
                     size_t stride_a, int at, const float *b, size_t stride_b, int bt, float *c,
                     size_t stride_c, int acc, const float *bias);

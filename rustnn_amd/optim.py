@@ -34,6 +34,12 @@ class Param:
         self.decay = bool(decay)
         self.rows, self.cols = int(rows), int(cols)
 
+    def __setattr__(self, name, value):
+        # any change of a buffer or of the shape drops the cached C view
+        object.__setattr__(self, name, value)
+        if name != "_cs":
+            object.__setattr__(self, "_cs", None)
+
     def shaped(self, rows, cols):
         """Param::shaped (nn.rs:69-74)."""
         assert rows * cols == self.v.numel()
@@ -41,9 +47,27 @@ class Param:
         return self
 
     def _c(self):
-        n = self.v.numel()
-        return RnnParam(_ptr(self.v, n, "v"), _ptr(self.g, n, "g"), _ptr(self.m, n, "m"),
-                        _ptr(self.v2, n, "v2"), n, self.rows, self.cols, int(self.decay))
+        if self._cs is None:
+            n = self.v.numel()
+            self._cs = RnnParam(_ptr(self.v, n, "v"), _ptr(self.g, n, "g"), _ptr(self.m, n, "m"),
+                                _ptr(self.v2, n, "v2"), n, self.rows, self.cols, int(self.decay))
+        return self._cs
+
+
+class _ParamList:
+    """The C array of a parameter list, rebuilt only when one of the
+    parameters' C views changed."""
+
+    def __init__(self):
+        self.key, self.arr = None, None
+
+    def __call__(self, params):
+        cs = [p._c() for p in params]
+        key = tuple(map(id, cs))
+        if key != self.key:
+            self.arr = (RnnParam * len(cs))(*cs)
+            self.key = key
+        return self.arr
 
 
 def newton_schulz(g, rows, cols, steps, ctx=None):
@@ -67,6 +91,7 @@ class Optim:
         self.h = h
         self.muon, self.ns_steps = bool(muon), ns_steps
         self.mom, self.b1, self.b2, self.eps = 0.95, 0.9, 0.999, 1e-8
+        self._list = _ParamList()
 
     @property
     def t(self):
@@ -82,7 +107,7 @@ class Optim:
 
     def step_all(self, params, lr, wd):
         """Optim::step_all (optim.rs:177-205)."""
-        arr = (RnnParam * len(params))(*[p._c() for p in params])
+        arr = self._list(params)
         self.ctx.check(lib().rnn_optim_step(self.h, len(params), C.cast(arr, _vp), float(lr),
                                             float(wd)))
 
@@ -98,23 +123,24 @@ class Optim:
             pass
 
 
-def clip_(params, max_norm, ctx=None):
-    """clip_ (optim.rs:237-251): the global gradient norm (returned) and, above
-    ``max_norm``, every gradient scaled by max / norm.  The gradients are
-    gathered into one flat buffer for the device reduction."""
+_clip_list = _ParamList()
+
+
+def clip_(params, max_norm, ctx=None, norm=None):
+    """clip_ (optim.rs:237-251): the global gradient norm over every
+    parameter's gradient and, above ``max_norm``, every gradient scaled by
+    max / norm.  Returns the norm as a float (one device sync), or, when
+    ``norm`` (a 1-element device tensor) is given, leaves it there and
+    returns ``norm`` without synchronising."""
     import torch
     ctx = ctx or default_ctx()
-    flat = torch.cat([p.g.reshape(-1) for p in params]) if params else torch.zeros(
-        1, device="cuda")
-    norm = torch.zeros(1, dtype=torch.float32, device=flat.device)
-    ctx.check(lib().rnn_clip_grad_norm(ctx.h, flat.numel(), _ptr(flat, flat.numel(), "g"),
-                                       float(max_norm), _ptr(norm, 1, "norm")))
-    off = 0
-    for p in params:
-        n = p.g.numel()
-        p.g.copy_(flat[off:off + n].view_as(p.g))
-        off += n
-    return float(norm.item())
+    sync = norm is None
+    if norm is None:
+        norm = torch.zeros(1, dtype=torch.float32, device="cuda")
+    arr = _clip_list(params)
+    ctx.check(lib().rnn_clip_params(ctx.h, len(params), C.cast(arr, _vp), float(max_norm),
+                                    _ptr(norm, 1, "norm")))
+    return float(norm.item()) if sync else norm
 
 
 class Ema:
@@ -126,20 +152,26 @@ class Ema:
         self.w = []
         self.ready = False
         self.t = 0
+        self._list = _ParamList()
 
     def update(self, params):
-        """Ema::update (optim.rs:270-288)."""
+        """Ema::update (optim.rs:270-288): one launch over the whole list."""
         self.t += 1
         if not self.ready:
             self.w = [p.v.clone() for p in params]
+            self._wp = (C.c_void_p * len(self.w))(*[e.data_ptr() for e in self.w])
             self.ready = True
             return
+        if len(params) != len(self.w):
+            raise RnnError(-2, f"EMA with {len(self.w)} tensors for {len(params)} parameters")
+        for e, p in zip(self.w, params):
+            if e.numel() != p.v.numel():
+                raise RnnError(-2, "EMA tensor and parameter differ in length")
         t = np.float32(self.t)
         d = min(self.d, (np.float32(1.0) + t) / (np.float32(10.0) + t))
-        for e, p in zip(self.w, params):
-            n = e.numel()
-            self.ctx.check(lib().rnn_ema_update(self.ctx.h, n, _ptr(e, n, "w"), _ptr(p.v, n, "v"),
-                                                float(d)))
+        arr = self._list(params)
+        self.ctx.check(lib().rnn_ema_update_params(self.ctx.h, len(params), C.cast(self._wp, _vp),
+                                                   C.cast(arr, _vp), float(d)))
 
     def swap_in(self, params):
         """Ema::swap_in (optim.rs:290-305): the model takes the average's

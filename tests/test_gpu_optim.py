@@ -153,3 +153,146 @@ def test_ema(rnn, orc):
     assert np.array_equal(to_host(p.v), w)
     Ema.swap_out([p], old)
     assert np.array_equal(to_host(p.v), nv)
+
+
+def _oracle_step(orc, ps, want, grads, lr, wd, step):
+    for p, w, g in zip(ps, want, grads):
+        gg = g.copy()
+        if p["rows"] > 0 and min(p["rows"], p["cols"]) > 1:
+            orc.muon_step(w["v"], gg, w["m"], p["rows"], p["cols"], p["decay"], lr, wd, 0.95, 3)
+        else:
+            orc.adam_step(w["v"], gg, w["m"], w["v2"], p["decay"], lr, wd, step)
+
+
+def _check(ps, want, gp, tag):
+    for i, (p, w, q) in enumerate(zip(ps, want, gp)):
+        if p["rows"] > 0 and min(p["rows"], p["cols"]) > 1:
+            assert rel_frob(to_host(q.v), w["v"]) < TOL_NS, (tag, i)
+        else:
+            assert np.array_equal(to_host(q.v), w["v"]), (tag, i)
+
+
+def test_optim_list_changes(rnn, orc):
+    """The optimiser keeps the plan of the last parameter list: the same list
+    again reuses it, a reordered list with one more tensor (and a zero-length
+    one) rebuilds it; every step matches the oracle."""
+    from rustnn_amd.optim import Optim, Param
+    rng = np.random.default_rng(21)
+    specs = [(32 * 24, 32, 24, True), (32 * 24, 32, 24, True), (50, 0, 0, False),
+             (24 * 32, 24, 32, False), (0, 0, 0, False), (90, 0, 0, True)]
+    ps = _params(rng, specs)
+    gp = [Param(to_dev(p["v"]) if p["v"].size else to_dev(np.zeros(1, np.float32))[:0],
+                p["decay"], p["rows"], p["cols"]) for p in ps]
+    want = [dict(v=p["v"].copy(), m=np.zeros_like(p["v"]), v2=np.zeros_like(p["v"])) for p in ps]
+    opt = Optim(True, 3)
+    lr, wd = 0.02, 0.1
+    order = [[0, 1, 2, 3], [0, 1, 2, 3], [5, 3, 4, 1, 2, 0], [5, 3, 4, 1, 2, 0]]
+    for step, idx in enumerate(order):
+        sel = [ps[i] for i in idx]
+        grads = [rng.standard_normal(p["v"].size).astype(np.float32) for p in sel]
+        for i, g in zip(idx, grads):
+            if g.size:
+                gp[i].g.copy_(to_dev(g))
+        opt.step_all([gp[i] for i in idx], lr, wd)
+        _oracle_step(orc, sel, [want[i] for i in idx], grads, lr, wd, step)
+        _check(sel, [want[i] for i in idx], [gp[i] for i in idx], step)
+    opt.close()
+
+
+def test_optim_step_in_graph(rnn, orc):
+    """Optim::step_all recorded in a HIP graph after one eager step (the plan
+    and scratch exist by then) and replayed four times, with the gradients
+    written between replays: every replay matches an eager twin bit for bit."""
+    import torch
+    from rustnn_amd import default_ctx
+    from rustnn_amd.optim import Optim, Param
+    rng = np.random.default_rng(5)
+    specs = [(48 * 64, 48, 64, True), (48 * 64, 48, 64, True), (64 * 96, 64, 96, False),
+             (200, 0, 0, False), (33, 0, 0, True)]
+    ps = _params(rng, specs)
+    ea = [Param(to_dev(p["v"]), p["decay"], p["rows"], p["cols"]) for p in ps]
+    gb = [Param(to_dev(p["v"]), p["decay"], p["rows"], p["cols"]) for p in ps]
+    oa, ob = Optim(True, 3), Optim(True, 3)
+    ctx = default_ctx()
+    lr, wd = 0.01, 0.05
+
+    def grads():
+        gs = [to_dev(rng.standard_normal(p["v"].size).astype(np.float32)) for p in ps]
+        for a, b, g in zip(ea, gb, gs):
+            a.g.copy_(g)
+            b.g.copy_(g)
+
+    grads()
+    oa.step_all(ea, lr, wd)
+    ob.step_all(gb, lr, wd)  # eager first step: plan + scratch
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    ctx.set_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    try:
+        with torch.cuda.graph(graph, stream=side):
+            ob.step_all(gb, lr, wd)
+    finally:
+        ctx.set_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    # capture enqueued nothing; the twin's t advanced on the host only
+    for k in range(4):
+        grads()
+        oa.step_all(ea, lr, wd)
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(ea, gb)):
+            if specs[i][1] == 0:
+                continue  # AdamW's bias corrections are baked into the graph (t fixed)
+            assert torch.equal(a.v, b.v), (k, i)
+            assert torch.equal(a.m, b.m), (k, i)
+    oa.close()
+    ob.close()
+
+
+def test_clip_list_edges(rnn, orc):
+    """clip_ over a list with a zero-length tensor and tensors spanning
+    several reduction chunks; under the limit nothing changes; a second call
+    with another list re-uploads the table."""
+    import torch
+    from rustnn_amd.optim import Param, clip_
+    rng = np.random.default_rng(9)
+    lens = [16384 * 3 + 5, 0, 1, 20000]
+    ps = [Param(torch.zeros(n, device="cuda"), False) for n in lens]
+    g = (rng.standard_normal(sum(lens)) * 2).astype(np.float32)
+    off = 0
+    for p, n in zip(ps, lens):
+        p.g.copy_(to_dev(g[off:off + n]))
+        off += n
+    norm = clip_(ps, 1e9)
+    want = g.copy()
+    assert norm == pytest.approx(orc.clip(want, lens, 1e9), rel=1e-6)
+    assert np.array_equal(np.concatenate([to_host(p.g) for p in ps]), g)
+    sub = [ps[3], ps[0]]
+    want = np.concatenate([g[-lens[3]:], g[:lens[0]]])
+    norm_w = orc.clip(want, [lens[3], lens[0]], 3.0)
+    norm = clip_(sub, 3.0)
+    assert abs(norm - norm_w) <= 1e-6 * norm_w
+    assert rel_frob(np.concatenate([to_host(p.g) for p in sub]), want) < 1e-6
+    assert clip_([ps[1]], 1.0) == 0.0
+
+
+def test_ema_list(rnn, orc):
+    """Ema::update over several tensors in one launch, bit-exact per tensor."""
+    from rustnn_amd.optim import Ema, Param
+    rng = np.random.default_rng(13)
+    lens = [3, 70000, 1, 300]
+    vs = [rng.standard_normal(n).astype(np.float32) for n in lens]
+    ps = [Param(to_dev(v), True) for v in vs]
+    ema = Ema(0.99)
+    ema.update(ps)
+    ws = [v.copy() for v in vs]
+    for t in range(2, 20, 3):
+        for p, w in zip(ps, ws):
+            nv = rng.standard_normal(w.size).astype(np.float32)
+            p.v.copy_(to_dev(nv))
+            orc.ema_update(w, nv, 0.99, t)
+        ema.t = t - 1
+        ema.update(ps)
+        for i, (e, w) in enumerate(zip(ema.w, ws)):
+            assert np.array_equal(to_host(e), w), (t, i)
