@@ -225,6 +225,44 @@ int rnn_softmax_ce(rnn_ctx *ctx, size_t rows, size_t nclass, const float *logits
 int rnn_sgd_step(rnn_ctx *ctx, size_t len, float *v, float *g, float *m, float lr, float momentum,
                  float wd);
 
+/* ----------------------------------------------------------- norm.rs */
+/* Token tensors are [rows = n*t][c] row-major, channel fastest (tok.rs).
+ * Parameter gradients (dg, db, dl, dw, dp) accumulate (+=), as Param::g does;
+ * dx is overwritten. */
+/* LayerNorm::forward (norm.rs:38-85): per row f64 sums, mu, var = max(s2/c -
+ * mu^2, 0) as f32, invstd = 1/sqrt(var + eps); y = g (x - mu) invstd + b.
+ * Training keeps xhat [rows][c] and invstd [rows]; pass both NULL for eval. */
+int rnn_ln_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *g,
+                   const float *b, float eps, float *y, float *xhat, float *invstd);
+/* LayerNorm::backward (norm.rs:87-137). */
+int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
+                    const float *invstd, const float *g, float *dx, float *dg, float *db);
+/* LayerScale::forward / backward (norm.rs:166-212): y = x l per channel (y may
+ * be x); dl += sum dy x, dx = dy l (dx may be dy). */
+int rnn_layerscale_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *l,
+                           float *y);
+int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *x,
+                            const float *l, float *dx, float *dl);
+/* The SwiGLU gate between SwiGlu's two Linear calls (norm.rs:250-288): ab is
+ * [rows][2h] (a | b), u = a sigmoid(a) b [rows][h]; the backward writes
+ * dab [rows][2h] from du [rows][h]. */
+int rnn_swiglu_forward(rnn_ctx *ctx, size_t rows, size_t h, const float *ab, float *u);
+int rnn_swiglu_backward(rnn_ctx *ctx, size_t rows, size_t h, const float *du, const float *ab,
+                        float *dab);
+/* DwConv3 (norm.rs:296-457): depthwise 3x3, pad 1, over n images of th x tw
+ * tokens, channel-last; w [9][c] (tap-major), b [c]. */
+int rnn_dwconv3_forward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, const float *x,
+                        const float *w, const float *b, float *y);
+int rnn_dwconv3_backward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, const float *dy,
+                         const float *x, const float *w, float *dx, float *dw, float *db);
+/* SeqPool (norm.rs:459-586): w = softmax_t(x p), z = sum_t w_t x_t; z [n][c];
+ * the forward writes the softmax weights w [n][t] that the backward reads.
+ * t <= 1024. */
+int rnn_seqpool_forward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float *x,
+                        const float *p, float *z, float *w);
+int rnn_seqpool_backward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float *dz,
+                         const float *w, const float *x, const float *p, float *dx, float *dp);
+
 /* ----------------------------------------------------------- optim.rs */
 /* Newton-Schulz orthogonalisation (newton_schulz, optim.rs:124-145), in
  * place on `count` [rows x cols] matrices at g + i*stride: X = G (G^T when

@@ -194,6 +194,25 @@ void orc_adam_step(size_t n, float *v, float *g, float *m, float *v2, int decay,
 float orc_clip(float *g, const size_t *lens, size_t nseg, float max);
 void orc_ema_update(size_t n, float *w, const float *v, float decay, size_t t);
 
+/* ---------------------------------------------------------------- norm.rs */
+void orc_ln_forward(size_t rows, size_t c, const float *x, const float *g, const float *b,
+                    float eps, float *y, float *xhat, float *invstd);
+void orc_ln_backward(size_t rows, size_t c, const float *dy, const float *xhat,
+                     const float *invstd, const float *g, float *dx, float *dg, float *db);
+void orc_layerscale_forward(size_t rows, size_t c, const float *x, const float *l, float *y);
+void orc_layerscale_backward(size_t rows, size_t c, const float *dy, const float *x,
+                             const float *l, float *dx, float *dl);
+void orc_swiglu_forward(size_t rows, size_t h, const float *ab, float *u);
+void orc_swiglu_backward(size_t rows, size_t h, const float *du, const float *ab, float *dab);
+void orc_dwconv3_forward(size_t n, size_t th, size_t tw, size_t c, const float *x,
+                         const float *w, const float *b, float *y);
+void orc_dwconv3_backward(size_t n, size_t th, size_t tw, size_t c, const float *dy,
+                          const float *x, const float *w, float *dx, float *dw, float *db);
+void orc_seqpool_forward(size_t n, size_t t, size_t c, const float *x, const float *p, float *z,
+                         float *w);
+void orc_seqpool_backward(size_t n, size_t t, size_t c, const float *dz, const float *w,
+                          const float *x, const float *p, float *dx, float *dp);
+
 #ifdef __cplusplus
 }
 #endif

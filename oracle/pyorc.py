@@ -148,6 +148,19 @@ def lib():
         L.orc_clip.argtypes = [_f32p, P(_sz), _sz, C.c_float]
         L.orc_clip.restype = C.c_float
         L.orc_ema_update.argtypes = [_sz, _f32p, _f32p, C.c_float, _sz]
+        vp = C.c_void_p
+        L.orc_ln_forward.argtypes = [_sz, _sz, _f32p, _f32p, _f32p, C.c_float, _f32p, vp, vp]
+        L.orc_ln_backward.argtypes = [_sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]
+        L.orc_layerscale_forward.argtypes = [_sz, _sz, _f32p, _f32p, _f32p]
+        L.orc_layerscale_backward.argtypes = [_sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p]
+        L.orc_swiglu_forward.argtypes = [_sz, _sz, _f32p, _f32p]
+        L.orc_swiglu_backward.argtypes = [_sz, _sz, _f32p, _f32p, _f32p]
+        L.orc_dwconv3_forward.argtypes = [_sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p]
+        L.orc_dwconv3_backward.argtypes = [_sz, _sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p,
+                                           _f32p, _f32p]
+        L.orc_seqpool_forward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p]
+        L.orc_seqpool_backward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                           _f32p]
         _lib = L
     return _lib
 
@@ -504,3 +517,106 @@ def ema_update(w, v, decay, t):
     """Ema::update (optim.rs:270-288) after the first call, in place on w."""
     _chk(w)
     lib().orc_ema_update(w.size, w, _f(v).ravel(), decay, t)
+
+
+# ---------------------------------------------------------------- norm.rs
+# Token tensors [rows, c] (or [n, t, c]) as float32 arrays; new outputs are
+# returned, parameter gradients (dg, db, dl, dw, dp) are accumulated in place.
+def ln_forward(x, g, b, eps=1e-5, train=True):
+    """LayerNorm::forward (norm.rs:38-85): returns y, and xhat, invstd when
+    training."""
+    x, g, b = _f(x), _f(g), _f(b)
+    c = g.size
+    rows = x.size // c
+    y = np.empty_like(x)
+    if train:
+        xhat = np.empty_like(x)
+        invstd = np.empty(rows, np.float32)
+        lib().orc_ln_forward(rows, c, x.ravel(), g, b, eps, y.ravel(), xhat.ctypes.data,
+                             invstd.ctypes.data)
+        return y, xhat, invstd
+    lib().orc_ln_forward(rows, c, x.ravel(), g, b, eps, y.ravel(), None, None)
+    return y
+
+
+def ln_backward(dy, xhat, invstd, g, dg, db):
+    """LayerNorm::backward (norm.rs:87-137): returns dx; dg / db +=."""
+    _chk(dg, db)
+    dy, xhat = _f(dy), _f(xhat)
+    c = g.size
+    dx = np.empty_like(dy)
+    lib().orc_ln_backward(dy.size // c, c, dy.ravel(), xhat.ravel(), _f(invstd), _f(g),
+                          dx.ravel(), dg, db)
+    return dx
+
+
+def layerscale_forward(x, l):
+    x = _f(x)
+    y = np.empty_like(x)
+    lib().orc_layerscale_forward(x.size // l.size, l.size, x.ravel(), _f(l), y.ravel())
+    return y
+
+
+def layerscale_backward(dy, x, l, dl):
+    _chk(dl)
+    dy = _f(dy)
+    dx = np.empty_like(dy)
+    lib().orc_layerscale_backward(dy.size // l.size, l.size, dy.ravel(), _f(x).ravel(), _f(l),
+                                  dx.ravel(), dl)
+    return dx
+
+
+def swiglu_forward(ab, h):
+    ab = _f(ab)
+    rows = ab.size // (2 * h)
+    u = np.empty(rows * h, np.float32)
+    lib().orc_swiglu_forward(rows, h, ab.ravel(), u)
+    return u
+
+
+def swiglu_backward(du, ab, h):
+    ab = _f(ab)
+    rows = ab.size // (2 * h)
+    dab = np.empty(rows * 2 * h, np.float32)
+    lib().orc_swiglu_backward(rows, h, _f(du).ravel(), ab.ravel(), dab)
+    return dab
+
+
+def dwconv3_forward(x, w, b, n, th, tw):
+    """DwConv3::forward (norm.rs:338-375); x [n, th*tw, c], w [9, c]."""
+    x = _f(x)
+    c = b.size
+    y = np.empty_like(x)
+    lib().orc_dwconv3_forward(n, th, tw, c, x.ravel(), _f(w).ravel(), _f(b), y.ravel())
+    return y
+
+
+def dwconv3_backward(dy, x, w, n, th, tw, dw, db):
+    """DwConv3::backward (norm.rs:377-452): returns dx; dw / db +=."""
+    _chk(dw, db)
+    dy = _f(dy)
+    c = db.size
+    dx = np.empty_like(dy)
+    lib().orc_dwconv3_backward(n, th, tw, c, dy.ravel(), _f(x).ravel(), _f(w).ravel(),
+                               dx.ravel(), dw.reshape(-1), db)
+    return dx
+
+
+def seqpool_forward(x, p, n, t):
+    """SeqPool::forward (norm.rs:487-528): returns (z [n, c], w [n, t])."""
+    x = _f(x)
+    c = p.size
+    z = np.empty(n * c, np.float32)
+    w = np.empty(n * t, np.float32)
+    lib().orc_seqpool_forward(n, t, c, x.ravel(), _f(p), z, w)
+    return z, w
+
+
+def seqpool_backward(dz, w, x, p, n, t, dp):
+    """SeqPool::backward (norm.rs:530-580): returns dx; dp +=."""
+    _chk(dp)
+    c = p.size
+    dx = np.empty(n * t * c, np.float32)
+    lib().orc_seqpool_backward(n, t, c, _f(dz).ravel(), _f(w).ravel(), _f(x).ravel(), _f(p),
+                               dx, dp)
+    return dx

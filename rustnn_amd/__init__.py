@@ -161,6 +161,17 @@ def lib():
             "rnn_clip_grad_norm": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
             "rnn_ema_update": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
             "rnn_clip_params": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
+            "rnn_ln_forward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp]),
+            "rnn_ln_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_layerscale_forward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),
+            "rnn_layerscale_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_swiglu_forward": (_i, [_vp, _sz, _sz, _vp, _vp]),
+            "rnn_swiglu_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),
+            "rnn_dwconv3_forward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "rnn_dwconv3_backward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
+                                          _vp]),
+            "rnn_seqpool_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "rnn_seqpool_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_ema_update_params": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
             "rnn_powi_f32": (C.c_float, [C.c_float, _i]),
             "rnn_resnet_logits": (_i, [_vp, _vp]),

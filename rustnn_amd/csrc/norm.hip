@@ -1,0 +1,574 @@
+// norm.rs on the device: LayerNorm, LayerScale, the SwiGLU gate, the
+// channel-last depthwise 3x3 convolution and SeqPool, over token tensors
+// [n, t, c] (tok.rs: rows = n*t, channel fastest).
+//
+// Reference: LayerNorm (norm.rs:17-143) with f64 row statistics; LayerScale
+// (norm.rs:147-217); SwiGlu's gate (norm.rs:221-294; its two projections are
+// Linear calls through the GEMM core); DwConv3 (norm.rs:296-457); SeqPool
+// (norm.rs:459-586).  Each reference layer runs rayon over rows or images.
+//
+// HBM-bound work: every kernel reads its inputs once and writes its outputs
+// once, except the channel reductions (dgamma / dbeta, dlambda, the depthwise
+// dW / db, dp), which read their operands once more in a column pass:
+// column partials per row block in f64, then one fixed-order pass over the
+// blocks (deterministic, like every reduction in this library).
+//
+// Operation order.  Where the reference's per-element arithmetic is a fixed
+// sequence (the depthwise taps, SeqPool's sums over tokens, the LayerNorm
+// output, SwiGLU's products) the kernels keep it, with contraction off, so
+// those outputs round as the reference does; row sums that the reference
+// makes sequentially in f32 (LayerNorm backward's m1 / m2) are summed in f64
+// here.  exp is the device's expf.
+#include "rnn_internal.h"
+
+#include <algorithm>
+#include <cmath>
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int NT = 256;  // threads per block
+
+__device__ __forceinline__ double wave_sum(double v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ------------------------------------------------------------ LayerNorm
+// One wave per row: f64 sums of x and x^2 (norm.rs:56-62), mu, var =
+// max(s2/c - mu^2, 0) as f32, invstd = 1 / sqrt(var + eps) in f32; then
+// xhat = (x - mu) invstd and y = g xhat + b (norm.rs:63-69).
+__global__ __launch_bounds__(NT) void ln_fwd_kernel(size_t rows, int c, const float *__restrict__ x,
+                                                    const float *__restrict__ g,
+                                                    const float *__restrict__ b, float eps,
+                                                    float *__restrict__ y, float *__restrict__ xhat,
+                                                    float *__restrict__ invstd) {
+    const int lane = threadIdx.x & 63;
+    const size_t r = (size_t)blockIdx.x * (NT / 64) + wave_index();
+    if (r >= rows) return;
+    const float *xr = x + r * c;
+    double s = 0.0, s2 = 0.0;
+    for (int j = lane; j < c; j += 64) {
+        const double v = xr[j];
+        s += v;
+        s2 += v * v;
+    }
+    s = wave_sum(s);
+    s2 = wave_sum(s2);
+    const double m = (double)c;
+    const double mu = s / m;
+    const float var = (float)fmax(s2 / m - mu * mu, 0.0);
+    const float inv = 1.0f / sqrtf(var + eps);
+    const float muf = (float)mu;
+    float *yr = y + r * c;
+    float *hr = xhat ? xhat + r * c : nullptr;
+    for (int j = lane; j < c; j += 64) {
+        const float h = (xr[j] - muf) * inv;
+        if (hr) hr[j] = h;
+        yr[j] = g[j] * h + b[j];
+    }
+    if (invstd && lane == 0) invstd[r] = inv;
+}
+
+// dx per row (norm.rs:121-135): d = dy g; m1 = sum d, m2 = sum d xhat;
+// dx = invstd (d - m1/c - xhat m2/c).
+__global__ __launch_bounds__(NT) void ln_bwd_kernel(size_t rows, int c, const float *__restrict__ dy,
+                                                    const float *__restrict__ xhat,
+                                                    const float *__restrict__ invstd,
+                                                    const float *__restrict__ g,
+                                                    float *__restrict__ dx) {
+    const int lane = threadIdx.x & 63;
+    const size_t r = (size_t)blockIdx.x * (NT / 64) + wave_index();
+    if (r >= rows) return;
+    const float *dr = dy + r * c, *hr = xhat + r * c;
+    double m1 = 0.0, m2 = 0.0;
+    for (int j = lane; j < c; j += 64) {
+        const float d = dr[j] * g[j];
+        m1 += d;
+        m2 += (double)(d * hr[j]);
+    }
+    const float s1 = (float)wave_sum(m1), s2 = (float)wave_sum(m2);
+    const float inv = 1.0f / (float)c;
+    const float is = invstd[r];
+    float *xr = dx + r * c;
+    for (int j = lane; j < c; j += 64) {
+        const float d = dr[j] * g[j];
+        xr[j] = is * (d - s1 * inv - hr[j] * s2 * inv);
+    }
+}
+
+// Column partial sums over a block of rows: thread j (channel) adds
+// a[r][j] b[r][j] (when b is set) and a[r][j] over rows r of its block, in row
+// order, in f64.  part: [nblk][c] products, then [nblk][c] plain sums.
+__global__ __launch_bounds__(NT) void colsum_kernel(size_t rows, int c, size_t rpb,
+                                                    const float *__restrict__ a,
+                                                    const float *__restrict__ b, int want_a,
+                                                    double *__restrict__ part) {
+    const int j = blockIdx.x * NT + threadIdx.x;
+    if (j >= c) return;
+    const size_t r0 = (size_t)blockIdx.y * rpb, r1 = min(rows, r0 + rpb);
+    double sab = 0.0, sa = 0.0;
+    for (size_t r = r0; r < r1; r++) {
+        const float av = a[r * c + j];
+        if (b) sab += (double)(av * b[r * c + j]);
+        sa += av;
+    }
+    const size_t nblk = gridDim.y;
+    if (b) part[(size_t)blockIdx.y * c + j] = sab;
+    if (want_a) part[(b ? nblk * c : 0) + (size_t)blockIdx.y * c + j] = sa;
+}
+
+// out0[j] += sum over blocks of part[blk][j] (block order, f64), likewise
+// out1 from the second half when set.
+__global__ __launch_bounds__(NT) void colred_kernel(int nblk, size_t len,
+                                                    const double *__restrict__ part,
+                                                    float *__restrict__ out0,
+                                                    float *__restrict__ out1) {
+    const size_t j = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (j >= len) return;
+    double s = 0.0;
+    for (int k = 0; k < nblk; k++) s += part[(size_t)k * len + j];
+    out0[j] += (float)s;
+    if (out1) {
+        double t = 0.0;
+        for (int k = 0; k < nblk; k++) t += part[(size_t)(nblk + k) * len + j];
+        out1[j] += (float)t;
+    }
+}
+
+// Like colred_kernel over one column set of length len, sending columns
+// below `split` to out0 and the rest to out1 (out1[j - split]).
+__global__ __launch_bounds__(NT) void colred_split_kernel(int nblk, size_t len, size_t split,
+                                                          const double *__restrict__ part,
+                                                          float *__restrict__ out0,
+                                                          float *__restrict__ out1) {
+    const size_t j = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (j >= len) return;
+    double s = 0.0;
+    for (int k = 0; k < nblk; k++) s += part[(size_t)k * len + j];
+    if (j < split)
+        out0[j] += (float)s;
+    else
+        out1[j - split] += (float)s;
+}
+
+// ------------------------------------------------------------ LayerScale
+// y = x l (norm.rs:168-180); backward dx = dy l (norm.rs:205-211).  y may be x.
+__global__ void scale_cols_kernel(size_t len, int c, const float *x, const float *__restrict__ l,
+                                  float *y) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x)
+        y[i] = x[i] * l[i % c];
+}
+
+// ------------------------------------------------------------ SwiGLU gate
+__device__ __forceinline__ float sigmoid(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// u = a sigmoid(a) b with a = ab[r][j], b = ab[r][h + j] (norm.rs:255-262).
+__global__ void swiglu_fwd_kernel(size_t rows, int h, const float *__restrict__ ab,
+                                  float *__restrict__ u) {
+    const size_t len = rows * h;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / h, j = i - r * h;
+        const float a = ab[r * 2 * h + j];
+        u[i] = a * sigmoid(a) * ab[r * 2 * h + h + j];
+    }
+}
+
+// dab[r][j] = du b s (1 + a (1 - s)), dab[r][h + j] = du a s (norm.rs:276-287).
+__global__ void swiglu_bwd_kernel(size_t rows, int h, const float *__restrict__ du,
+                                  const float *__restrict__ ab, float *__restrict__ dab) {
+    const size_t len = rows * h;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / h, j = i - r * h;
+        const float a = ab[r * 2 * h + j], b = ab[r * 2 * h + h + j];
+        const float s = sigmoid(a);
+        const float sa = a * s;
+        const float d = du[i];
+        dab[r * 2 * h + j] = d * b * s * (1.0f + a * (1.0f - s));
+        dab[r * 2 * h + h + j] = d * sa;
+    }
+}
+
+// ------------------------------------------------------------ DwConv3
+// y = b, then the in-bounds taps in (ky, kx) order: y += w[tap] x[src]
+// (norm.rs:344-369).  One thread per output element.
+__global__ void dw3_fwd_kernel(size_t n, int th, int tw, int c, const float *__restrict__ x,
+                               const float *__restrict__ w, const float *__restrict__ b,
+                               float *__restrict__ y) {
+    const size_t len = n * th * tw * c;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int ch = (int)(i % c);
+        const size_t pos = i / c;
+        const int ox = (int)(pos % tw), oy = (int)((pos / tw) % th);
+        const size_t img = pos / ((size_t)th * tw);
+        const float *xi = x + img * th * tw * c;
+        float acc = b[ch];
+        for (int ky = 0; ky < 3; ky++) {
+            const int sy = oy + ky - 1;
+            if (sy < 0 || sy >= th) continue;
+            for (int kx = 0; kx < 3; kx++) {
+                const int sx = ox + kx - 1;
+                if (sx < 0 || sx >= tw) continue;
+                acc += w[(ky * 3 + kx) * c + ch] * xi[((size_t)sy * tw + sx) * c + ch];
+            }
+        }
+        y[i] = acc;
+    }
+}
+
+// dx[src] = sum over the outputs that read src of w[tap] dy[out], in the
+// order the reference's scatter visits them (output raster order, i.e. taps
+// 8, 7, ..., 0; norm.rs:423-450).
+__global__ void dw3_bwd_x_kernel(size_t n, int th, int tw, int c, const float *__restrict__ dy,
+                                 const float *__restrict__ w, float *__restrict__ dx) {
+    const size_t len = n * th * tw * c;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const int ch = (int)(i % c);
+        const size_t pos = i / c;
+        const int sx = (int)(pos % tw), sy = (int)((pos / tw) % th);
+        const size_t img = pos / ((size_t)th * tw);
+        const float *di = dy + img * th * tw * c;
+        float acc = 0.0f;
+        for (int ky = 2; ky >= 0; ky--) {
+            const int oy = sy - ky + 1;
+            if (oy < 0 || oy >= th) continue;
+            for (int kx = 2; kx >= 0; kx--) {
+                const int ox = sx - kx + 1;
+                if (ox < 0 || ox >= tw) continue;
+                acc += w[(ky * 3 + kx) * c + ch] * di[((size_t)oy * tw + ox) * c + ch];
+            }
+        }
+        dx[i] = acc;
+    }
+}
+
+// dW [9][c] and db [c] partials over a block of images: thread = channel,
+// f64 sums in (image, output position, tap) order (norm.rs:377-418).
+// part: [nblk][10][c] (taps 0-8, then db).
+__global__ __launch_bounds__(NT) void dw3_bwd_w_kernel(size_t n, int th, int tw, int c,
+                                                       size_t ipb, const float *__restrict__ dy,
+                                                       const float *__restrict__ x,
+                                                       double *__restrict__ part) {
+    const int ch = blockIdx.x * NT + threadIdx.x;
+    if (ch >= c) return;
+    const size_t i0 = (size_t)blockIdx.y * ipb, i1 = min(n, i0 + ipb);
+    double aw[9], ab = 0.0;
+    for (int k = 0; k < 9; k++) aw[k] = 0.0;
+    const size_t img = (size_t)th * tw * c;
+    for (size_t im = i0; im < i1; im++) {
+        const float *di = dy + im * img, *xi = x + im * img;
+        for (int oy = 0; oy < th; oy++)
+            for (int ox = 0; ox < tw; ox++) {
+                const float d = di[((size_t)oy * tw + ox) * c + ch];
+                ab += d;
+#pragma unroll
+                for (int ky = 0; ky < 3; ky++) {
+                    const int sy = oy + ky - 1;
+                    if (sy < 0 || sy >= th) continue;
+#pragma unroll
+                    for (int kx = 0; kx < 3; kx++) {
+                        const int sx = ox + kx - 1;
+                        if (sx < 0 || sx >= tw) continue;
+                        aw[ky * 3 + kx] += (double)(d * xi[((size_t)sy * tw + sx) * c + ch]);
+                    }
+                }
+            }
+    }
+    double *pb = part + (size_t)blockIdx.y * 10 * c;
+    for (int k = 0; k < 9; k++) pb[(size_t)k * c + ch] = aw[k];
+    pb[(size_t)9 * c + ch] = ab;
+}
+
+// ------------------------------------------------------------ SeqPool
+// One block per image (norm.rs:488-519): s_j = sum_k x[j][k] p[k] in k order;
+// w = softmax(s) with a sequential sum and a multiply by 1/sum;
+// z[k] = sum_j w_j x[j][k] in j order.  s, w live in LDS (t <= SP_MAXT).
+constexpr int SP_MAXT = 1024;
+
+__global__ __launch_bounds__(NT) void seqpool_fwd_kernel(int t, int c, const float *__restrict__ x,
+                                                         const float *__restrict__ p,
+                                                         float *__restrict__ z,
+                                                         float *__restrict__ wout) {
+    __shared__ float w[SP_MAXT];
+    const size_t im = blockIdx.x;
+    const float *xi = x + im * t * c;
+    for (int j = threadIdx.x; j < t; j += NT) {
+        float s = 0.0f;
+        for (int k = 0; k < c; k++) s += xi[(size_t)j * c + k] * p[k];
+        w[j] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float mx = -INFINITY;
+        for (int j = 0; j < t; j++) mx = w[j] > mx ? w[j] : mx;
+        float sum = 0.0f;
+        for (int j = 0; j < t; j++) {
+            w[j] = expf(w[j] - mx);
+            sum += w[j];
+        }
+        const float inv = 1.0f / sum;
+        for (int j = 0; j < t; j++) w[j] *= inv;
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < t; j += NT) wout[im * t + j] = w[j];
+    for (int k = threadIdx.x; k < c; k += NT) {
+        float acc = 0.0f;
+        for (int j = 0; j < t; j++) acc += w[j] * xi[(size_t)j * c + k];
+        z[im * c + k] = acc;
+    }
+}
+
+// Backward, one block per image (norm.rs:530-572): dw_j = sum_k dz_k x[j][k];
+// dot = sum_j dw_j w_j; ds_j = w_j (dw_j - dot); dx[j][k] = w_j dz_k +
+// ds_j p_k; the image's share of dp, sum_j ds_j x[j][k], into part[image][k].
+__global__ __launch_bounds__(NT) void seqpool_bwd_kernel(int t, int c, const float *__restrict__ dz,
+                                                         const float *__restrict__ wsave,
+                                                         const float *__restrict__ x,
+                                                         const float *__restrict__ p,
+                                                         float *__restrict__ dx,
+                                                         float *__restrict__ part) {
+    __shared__ float dw[SP_MAXT];
+    __shared__ float dot_s;
+    const size_t im = blockIdx.x;
+    const float *xi = x + im * t * c, *dzi = dz + im * c, *wi = wsave + im * t;
+    for (int j = threadIdx.x; j < t; j += NT) {
+        float s = 0.0f;
+        for (int k = 0; k < c; k++) s += dzi[k] * xi[(size_t)j * c + k];
+        dw[j] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float dot = 0.0f;
+        for (int j = 0; j < t; j++) dot += dw[j] * wi[j];
+        dot_s = dot;
+    }
+    __syncthreads();
+    const float dot = dot_s;
+    for (int j = threadIdx.x; j < t; j += NT) dw[j] = wi[j] * (dw[j] - dot);  // ds_j
+    __syncthreads();
+    float *dxi = dx + im * t * c;
+    for (int k = threadIdx.x; k < c; k += NT) {
+        const float dzk = dzi[k], pk = p[k];
+        float adp = 0.0f;
+        for (int j = 0; j < t; j++) {
+            const float ds = dw[j];
+            dxi[(size_t)j * c + k] = wi[j] * dzk + ds * pk;
+            adp += ds * xi[(size_t)j * c + k];
+        }
+        part[im * c + k] = adp;
+    }
+}
+
+// out[k] += sum over images of part[image][k] (image order, f64).
+__global__ void rowsum_add_kernel(size_t n, int c, const float *__restrict__ part,
+                                  float *__restrict__ out) {
+    const int k = blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= c) return;
+    double s = 0.0;
+    for (size_t i = 0; i < n; i++) s += part[i * c + k];
+    out[k] += (float)s;
+}
+
+unsigned ew_grid(size_t len) {
+    return (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(len, NT), 16384));
+}
+
+// Rows per column-partial block: enough blocks to cover the chip.
+size_t rows_per_block(size_t rows, int c) {
+    const size_t cblk = rnn_div_up((size_t)c, NT);
+    const size_t want = std::max<size_t>(1, 2048 / cblk);
+    return std::max<size_t>(16, rnn_div_up(rows, want));
+}
+
+// Column sums of a*b (b set) and of a over rows, added into outab / outa.
+int colsum_add(rnn_ctx *ctx, size_t rows, int c, const float *a, const float *b, float *outab,
+               float *outa) {
+    if (rows == 0 || c == 0) return RNN_OK;
+    const size_t rpb = rows_per_block(rows, c);
+    const size_t nblk = rnn_div_up(rows, rpb);
+    if (nblk > 65535) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "column sums: too many rows");
+    const int nout = (b ? 1 : 0) + (outa ? 1 : 0);
+    double *part = (double *)rnn_workspace(ctx, nout * nblk * c * sizeof(double));
+    if (!part) return RNN_E_NOMEM;
+    colsum_kernel<<<dim3((unsigned)rnn_div_up((size_t)c, NT), (unsigned)nblk), NT, 0,
+                    ctx->stream>>>(rows, c, rpb, a, b, outa != nullptr, part);
+    RNN_LAUNCHED(ctx);
+    colred_kernel<<<(unsigned)rnn_div_up((size_t)c, NT), NT, 0, ctx->stream>>>(
+        (int)nblk, (size_t)c, part, b ? outab : outa, b ? outa : nullptr);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+bool dims_ok(size_t rows, size_t c) { return c <= (1u << 20) && rows <= ((size_t)1 << 40); }
+
+}  // namespace
+
+extern "C" {
+
+int rnn_ln_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *g,
+                   const float *b, float eps, float *y, float *xhat, float *invstd) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!x || !g || !b || !y) return rnn_fail(ctx, RNN_E_NULL, "ln_forward: null operand");
+    if ((xhat == nullptr) != (invstd == nullptr))
+        return rnn_fail(ctx, RNN_E_INVALID, "ln_forward: xhat and invstd go together");
+    if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "ln_forward: %zu x %zu", rows, c);
+    ln_fwd_kernel<<<(unsigned)rnn_div_up(rows, NT / 64), NT, 0, ctx->stream>>>(
+        rows, (int)c, x, g, b, eps, y, xhat, invstd);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
+                    const float *invstd, const float *g, float *dx, float *dg, float *db) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!dy || !xhat || !invstd || !g || !dx || !dg || !db)
+        return rnn_fail(ctx, RNN_E_NULL, "ln_backward: null operand");
+    if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "ln_backward: %zu x %zu", rows, c);
+    // dgamma += sum dy xhat, dbeta += sum dy (norm.rs:94-119)
+    int rc = colsum_add(ctx, rows, (int)c, dy, xhat, dg, db);
+    if (rc) return rc;
+    ln_bwd_kernel<<<(unsigned)rnn_div_up(rows, NT / 64), NT, 0, ctx->stream>>>(
+        rows, (int)c, dy, xhat, invstd, g, dx);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_layerscale_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *l,
+                           float *y) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!x || !l || !y) return rnn_fail(ctx, RNN_E_NULL, "layerscale_forward: null operand");
+    if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "layerscale: %zu x %zu", rows, c);
+    scale_cols_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, (int)c, x, l, y);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *x,
+                            const float *l, float *dx, float *dl) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!dy || !x || !l || !dx || !dl)
+        return rnn_fail(ctx, RNN_E_NULL, "layerscale_backward: null operand");
+    if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "layerscale: %zu x %zu", rows, c);
+    // dl += sum dy x (norm.rs:183-204), before dx may overwrite dy
+    int rc = colsum_add(ctx, rows, (int)c, dy, x, dl, nullptr);
+    if (rc) return rc;
+    scale_cols_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, (int)c, dy, l, dx);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_swiglu_forward(rnn_ctx *ctx, size_t rows, size_t h, const float *ab, float *u) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || h == 0) return RNN_OK;
+    if (!ab || !u) return rnn_fail(ctx, RNN_E_NULL, "swiglu_forward: null operand");
+    if (!dims_ok(rows, h)) return rnn_fail(ctx, RNN_E_INVALID, "swiglu: %zu x %zu", rows, h);
+    swiglu_fwd_kernel<<<ew_grid(rows * h), NT, 0, ctx->stream>>>(rows, (int)h, ab, u);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_swiglu_backward(rnn_ctx *ctx, size_t rows, size_t h, const float *du, const float *ab,
+                        float *dab) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || h == 0) return RNN_OK;
+    if (!du || !ab || !dab) return rnn_fail(ctx, RNN_E_NULL, "swiglu_backward: null operand");
+    if (!dims_ok(rows, h)) return rnn_fail(ctx, RNN_E_INVALID, "swiglu: %zu x %zu", rows, h);
+    swiglu_bwd_kernel<<<ew_grid(rows * h), NT, 0, ctx->stream>>>(rows, (int)h, du, ab, dab);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_dwconv3_forward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, const float *x,
+                        const float *w, const float *b, float *y) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || th == 0 || tw == 0 || c == 0) return RNN_OK;
+    if (!x || !w || !b || !y) return rnn_fail(ctx, RNN_E_NULL, "dwconv3_forward: null operand");
+    if (th > 65536 || tw > 65536 || !dims_ok(n * th * tw, c))
+        return rnn_fail(ctx, RNN_E_INVALID, "dwconv3: %zu x %zu x %zu x %zu", n, th, tw, c);
+    const size_t len = n * th * tw * c;
+    dw3_fwd_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)tw, (int)c, x, w, b, y);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_dwconv3_backward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, const float *dy,
+                         const float *x, const float *w, float *dx, float *dw, float *db) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || th == 0 || tw == 0 || c == 0) return RNN_OK;
+    if (!dy || !x || !w || !dx || !dw || !db)
+        return rnn_fail(ctx, RNN_E_NULL, "dwconv3_backward: null operand");
+    if (th > 65536 || tw > 65536 || !dims_ok(n * th * tw, c))
+        return rnn_fail(ctx, RNN_E_INVALID, "dwconv3: %zu x %zu x %zu x %zu", n, th, tw, c);
+    // dW and db partials per block of images, then the block-order sum
+    const size_t cblk = rnn_div_up(c, (size_t)NT);
+    const size_t ipb = std::max<size_t>(1, rnn_div_up(n, std::max<size_t>(1, 1024 / cblk)));
+    const size_t nblk = rnn_div_up(n, ipb);
+    if (nblk > 65535) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "dwconv3: too many images");
+    double *part = (double *)rnn_workspace(ctx, nblk * 10 * c * sizeof(double));
+    if (!part) return RNN_E_NOMEM;
+    dw3_bwd_w_kernel<<<dim3((unsigned)cblk, (unsigned)nblk), NT, 0, ctx->stream>>>(
+        n, (int)th, (int)tw, (int)c, ipb, dy, x, part);
+    RNN_LAUNCHED(ctx);
+    // part is [nblk][10c]: taps 0-8 (dW's [9][c] order), then db
+    colred_split_kernel<<<(unsigned)rnn_div_up(10 * c, (size_t)NT), NT, 0, ctx->stream>>>(
+        (int)nblk, 10 * c, 9 * c, part, dw, db);
+    RNN_LAUNCHED(ctx);
+    const size_t len = n * th * tw * c;
+    dw3_bwd_x_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)tw, (int)c, dy, w, dx);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_seqpool_forward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float *x,
+                        const float *p, float *z, float *w) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || c == 0) return RNN_OK;
+    if (!x || !p || !z || !w) return rnn_fail(ctx, RNN_E_NULL, "seqpool_forward: null operand");
+    if (t == 0 || t > SP_MAXT || n > 0x7fffffff || !dims_ok(n * t, c))
+        return rnn_fail(ctx, RNN_E_INVALID, "seqpool: n %zu, t %zu (1..%d), c %zu", n, t, SP_MAXT,
+                        c);
+    seqpool_fwd_kernel<<<(unsigned)n, NT, 0, ctx->stream>>>((int)t, (int)c, x, p, z, w);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_seqpool_backward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float *dz,
+                         const float *w, const float *x, const float *p, float *dx, float *dp) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || c == 0) return RNN_OK;
+    if (!dz || !w || !x || !p || !dx || !dp)
+        return rnn_fail(ctx, RNN_E_NULL, "seqpool_backward: null operand");
+    if (t == 0 || t > SP_MAXT || n > 0x7fffffff || !dims_ok(n * t, c))
+        return rnn_fail(ctx, RNN_E_INVALID, "seqpool: n %zu, t %zu (1..%d), c %zu", n, t, SP_MAXT,
+                        c);
+    float *part = (float *)rnn_workspace(ctx, n * c * sizeof(float));
+    if (!part) return RNN_E_NOMEM;
+    seqpool_bwd_kernel<<<(unsigned)n, NT, 0, ctx->stream>>>((int)t, (int)c, dz, w, x, p, dx, part);
+    RNN_LAUNCHED(ctx);
+    rowsum_add_kernel<<<(unsigned)rnn_div_up(c, (size_t)NT), NT, 0, ctx->stream>>>(n, (int)c, part,
+                                                                                   dp);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+}  // extern "C"

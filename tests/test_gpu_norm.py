@@ -1,0 +1,215 @@
+"""GPU parity: norm.rs on the device (rustnn_amd/norm.py over norm.hip)
+against the CPU oracle (oracle/orc_norm.c) on identical seeded inputs.
+
+Bars:
+* bit-exact where the kernels keep the reference's per-element operation
+  order and no transcendental is involved: the depthwise forward and dX, the
+  LayerScale outputs;
+* LayerNorm y / xhat / invstd: relative 1e-6 (the f64 row sums are added in
+  another order, which can move mu or var by one f32 ulp), and at least 99%
+  of the elements bit-identical;
+* SwiGLU and SeqPool forward: relative 1e-6 (the device's expf);
+* every gradient (column reductions in another order, f64 here): 1e-5
+  relative Frobenius (TOL);
+* the reference's normcheck (check.rs:182-291) through the GPU path."""
+import numpy as np
+import pytest
+
+from conftest import TOL, rel_frob, to_dev, to_host
+
+import refcheck
+from test_oracle_norm import normcheck
+
+pytestmark = pytest.mark.gpu
+
+
+def _r(shape, seed, scale=1.0, shift=0.0):
+    return (np.random.default_rng(seed).standard_normal(shape) * scale + shift).astype(np.float32)
+
+
+def _dev(a):
+    import torch
+    return to_dev(np.ascontiguousarray(a, np.float32)).reshape(torch.Size(a.shape))
+
+
+@pytest.mark.parametrize("rows,c", [(4096, 256), (1024, 384), (300, 1024), (33, 7), (1, 64)])
+def test_layernorm(rnn, orc, rows, c):
+    from rustnn_amd.norm import LayerNorm
+    x = _r((rows, c), rows + c, 1.5, 0.3)
+    g, b = _r(c, 1, 0.2, 1.0), _r(c, 2)
+    dy = _r((rows, c), 3)
+    ln = LayerNorm(c)
+    ln.g.v.copy_(to_dev(g))
+    ln.b.v.copy_(to_dev(b))
+    y = to_host(ln.forward(_dev(x), True))
+    want, xh, iv = orc.ln_forward(x, g, b)
+    assert rel_frob(y, want) < 1e-6
+    assert np.mean(y.ravel() == want.ravel()) >= 0.99
+    assert rel_frob(to_host(ln.xhat), xh) < 1e-6
+    assert rel_frob(to_host(ln.invstd), iv) < 1e-6
+    ye = to_host(ln.forward(_dev(x), False))  # eval: same output, nothing kept
+    assert rel_frob(ye, want) < 1e-6
+    ln.forward(_dev(x), True)
+    dx = to_host(ln.backward(_dev(dy)))
+    dg, db = np.zeros(c, np.float32), np.zeros(c, np.float32)
+    # the oracle's backward on the device's xhat / invstd, so only the
+    # backward's own arithmetic is compared
+    wdx = orc.ln_backward(dy, to_host(ln.xhat).reshape(rows, c), to_host(ln.invstd), g, dg, db)
+    assert rel_frob(dx, wdx) < TOL
+    assert rel_frob(to_host(ln.g.g), dg) < TOL
+    assert rel_frob(to_host(ln.b.g), db) < TOL
+
+
+def test_layerscale(rnn, orc):
+    from rustnn_amd.norm import LayerScale
+    rows, c = 2048, 384
+    x, l, dy = _r((rows, c), 4), _r(c, 5, 1e-2), _r((rows, c), 6)
+    ls = LayerScale(c, 1e-4)
+    ls.l.v.copy_(to_dev(l))
+    y = to_host(ls.forward(_dev(x), True))
+    assert np.array_equal(y.reshape(rows, c), orc.layerscale_forward(x, l))
+    dl = np.zeros(c, np.float32)
+    wdx = orc.layerscale_backward(dy, x, l, dl)
+    dx = to_host(ls.backward(_dev(dy)))
+    assert np.array_equal(dx.reshape(rows, c), wdx)
+    assert rel_frob(to_host(ls.l.g), dl) < TOL
+
+
+@pytest.mark.parametrize("rows,h", [(4096, 352), (1000, 512), (7, 5)])
+def test_swiglu_gate(rnn, orc, rows, h):
+    import torch
+    from rustnn_amd import default_ctx, lib, _ptr
+    ab = _r((rows, 2 * h), rows + h, 2.0)
+    du = _r((rows, h), 7)
+    ctx = default_ctx()
+    u = torch.empty(rows * h, device="cuda")
+    dab = torch.empty(rows * 2 * h, device="cuda")
+    A, D = to_dev(ab), to_dev(du)
+    ctx.check(lib().rnn_swiglu_forward(ctx.h, rows, h, _ptr(A, ab.size, "ab"),
+                                       _ptr(u, rows * h, "u")))
+    ctx.check(lib().rnn_swiglu_backward(ctx.h, rows, h, _ptr(D, du.size, "du"),
+                                        _ptr(A, ab.size, "ab"), _ptr(dab, ab.size, "dab")))
+    assert rel_frob(to_host(u), orc.swiglu_forward(ab, h)) < 1e-6
+    assert rel_frob(to_host(dab), orc.swiglu_backward(du, ab, h)) < 1e-6
+
+
+def test_swiglu_layer(rnn, orc):
+    """SwiGlu (wg, gate, wd) at the rustvit's stage-3 shape vs the oracle."""
+    from rustnn_amd.norm import SwiGlu
+    rows, c, h = 2048, 256, 352
+    x, dy = _r((rows, c), 8), _r((rows, c), 9)
+    wg, bg = _r(2 * h * c, 10, 0.02), _r(2 * h, 11, 0.1)
+    wd, bd = _r(c * h, 12, 0.02), _r(c, 13, 0.1)
+    sw = SwiGlu(c, h, to_dev(wg), to_dev(bg), to_dev(wd), to_dev(bd))
+    y = to_host(sw.forward(_dev(x), True))
+    ab = orc.linear_forward(rows, c, 2 * h, x, wg, bg)
+    u = orc.swiglu_forward(ab, h)
+    assert rel_frob(y, orc.linear_forward(rows, h, c, u, wd, bd)) < TOL
+    dx = to_host(sw.backward(_dev(dy)))
+    dwd, dbd, du = orc.linear_backward(rows, h, c, dy, u, wd, np.zeros_like(wd), np.zeros_like(bd))
+    dab = orc.swiglu_backward(du, ab, h)
+    dwg, dbg, wdx = orc.linear_backward(rows, c, 2 * h, dab, x, wg, np.zeros_like(wg),
+                                        np.zeros_like(bg))
+    assert rel_frob(dx, wdx) < TOL
+    got = []
+    sw.for_each_param(lambda p: got.append(to_host(p.g)))
+    for g_, w_ in zip(got, (dwg, dbg, dwd, dbd)):
+        assert rel_frob(g_, w_) < TOL
+
+
+@pytest.mark.parametrize("n,th,tw,c", [(64, 8, 8, 256), (16, 4, 4, 384), (3, 5, 4, 12),
+                                       (2, 1, 7, 5)])
+def test_dwconv3(rnn, orc, n, th, tw, c):
+    from rustnn_amd.norm import DwConv3
+    x, dy = _r((n, th * tw, c), n + c), _r((n, th * tw, c), 14)
+    w, b = _r((9, c), 15, 0.1), _r(c, 16)
+    dw = DwConv3(c, th, tw, to_dev(w.ravel()), to_dev(b))
+    y = to_host(dw.forward(_dev(x), True))
+    assert np.array_equal(y.reshape(x.shape), orc.dwconv3_forward(x, w, b, n, th, tw))
+    gw, gb = np.zeros((9, c), np.float32), np.zeros(c, np.float32)
+    wdx = orc.dwconv3_backward(dy, x, w, n, th, tw, gw, gb)
+    dx = to_host(dw.backward(_dev(dy)))
+    assert np.array_equal(dx.reshape(x.shape), wdx)
+    assert rel_frob(to_host(dw.w.g), gw) < TOL
+    assert rel_frob(to_host(dw.b.g), gb) < TOL
+
+
+@pytest.mark.parametrize("n,t,c", [(256, 16, 384), (64, 64, 256), (3, 9, 8), (5, 1, 33)])
+def test_seqpool(rnn, orc, n, t, c):
+    from rustnn_amd.norm import SeqPool
+    x, p, dz = _r((n, t, c), n + t), _r(c, 17, 0.3), _r((n, c), 18)
+    sp = SeqPool(c, to_dev(p))
+    z = to_host(sp.forward(_dev(x), True))
+    wz, ww = orc.seqpool_forward(x, p, n, t)
+    assert rel_frob(z, wz) < 1e-6
+    assert rel_frob(to_host(sp.w), ww) < 1e-6
+    dp = np.zeros(c, np.float32)
+    # the oracle's backward on the device's softmax weights
+    wdx = orc.seqpool_backward(dz, to_host(sp.w), x, p, n, t, dp)
+    dx = to_host(sp.backward(_dev(dz)))
+    assert rel_frob(dx, wdx) < TOL
+    assert rel_frob(to_host(sp.p.g), dp) < TOL
+
+
+class GpuNorm:
+    """normcheck backend on the device layers (numpy in and out)."""
+
+    def ln(self, x, g, b, dy):
+        from rustnn_amd.norm import LayerNorm
+        ln = LayerNorm(g.size)
+        ln.g.v.copy_(to_dev(g))
+        ln.b.v.copy_(to_dev(b))
+        y = ln.forward(_dev(x), True)
+        dx = ln.backward(_dev(dy))
+        return to_host(y), to_host(dx), np.concatenate([to_host(ln.g.g), to_host(ln.b.g)])
+
+    def ln_y(self, x, g, b):
+        from rustnn_amd.norm import LayerNorm
+        ln = LayerNorm(g.size)
+        ln.g.v.copy_(to_dev(g))
+        ln.b.v.copy_(to_dev(b))
+        return to_host(ln.forward(_dev(x), False))
+
+    def _sw(self, wg, bg, wd, bd, h):
+        from rustnn_amd.norm import SwiGlu
+        return SwiGlu(wd.size // h, h, to_dev(wg), to_dev(bg), to_dev(wd), to_dev(bd))
+
+    def sw(self, x, wg, bg, wd, bd, h, dy):
+        sw = self._sw(wg, bg, wd, bd, h)
+        y = sw.forward(_dev(x), True)
+        dx = sw.backward(_dev(dy))
+        g = []
+        sw.for_each_param(lambda p: g.append(to_host(p.g)))
+        return to_host(y), to_host(dx), np.concatenate(g)
+
+    def sw_y(self, x, wg, bg, wd, bd, h):
+        return to_host(self._sw(wg, bg, wd, bd, h).forward(_dev(x), False))
+
+    def dw(self, x, w, b, n, th, tw, dy):
+        from rustnn_amd.norm import DwConv3
+        d = DwConv3(b.size, th, tw, to_dev(w.ravel()), to_dev(b))
+        y = d.forward(_dev(x), True)
+        dx = d.backward(_dev(dy))
+        return to_host(y), to_host(dx), np.concatenate([to_host(d.w.g), to_host(d.b.g)])
+
+    def dw_y(self, x, w, b, n, th, tw):
+        from rustnn_amd.norm import DwConv3
+        return to_host(DwConv3(b.size, th, tw, to_dev(w.ravel()), to_dev(b)).forward(_dev(x),
+                                                                                      False))
+
+    def sp(self, x, p, n, t, dz):
+        from rustnn_amd.norm import SeqPool
+        s = SeqPool(p.size, to_dev(p))
+        z = s.forward(_dev(x), True)
+        dx = s.backward(to_dev(dz))
+        return to_host(z), to_host(dx), to_host(s.p.g)
+
+    def sp_z(self, x, p, n, t):
+        from rustnn_amd.norm import SeqPool
+        return to_host(SeqPool(p.size, to_dev(p)).forward(_dev(x), False))
+
+
+def test_reference_normcheck_on_gpu(rnn, orc):
+    errs = normcheck(orc, GpuNorm())
+    bad = {k: v for k, v in errs.items() if not v < refcheck.TOL}
+    assert not bad, errs
