@@ -263,6 +263,31 @@ int rnn_seqpool_forward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float 
 int rnn_seqpool_backward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float *dz,
                          const float *w, const float *x, const float *p, float *dx, float *dp);
 
+/* ----------------------------------------------------------- loss.rs */
+/* Soft targets of a batch (targets, train.rs:121-155): tf [n][nf] = lam a +
+ * (1 - lam) b with a / b the targets of labels[i] / labels[perm[i]] --
+ * taxo_target (loss.rs:11-28, sibling share sib of eps, parent [nf] the
+ * superclass of each fine class) when taxo, else uniform_target
+ * (loss.rs:30-34); tc [n][nc] (may be NULL) the same over coarse labels with
+ * uniform smoothing.  perm NULL = identity, lam NULL = all 1. */
+int rnn_soft_targets(rnn_ctx *ctx, size_t n, size_t nf, size_t nc, const uint32_t *labels,
+                     const uint32_t *coarse, const uint32_t *perm, const float *lam,
+                     const uint32_t *parent, int taxo, float eps, float sib, float *tf,
+                     float *tc);
+/* ce_soft (loss.rs:39-83): dz [n][nclass] overwritten with scale (softmax -
+ * target) / n; *loss (device, may be NULL) the mean loss; *correct (device,
+ * may be NULL) the argmax hits against hard. */
+int rnn_ce_soft(rnn_ctx *ctx, size_t n, size_t nclass, const float *logits, const float *target,
+                const uint32_t *hard, float scale, float *dz, float *loss, uint32_t *correct);
+/* kl_distill (loss.rs:87-130): teacher detached; dz += temp (ps - pt) / n *
+ * scale; *loss = mean of temp^2 KL(pt || ps). */
+int rnn_kl_distill(rnn_ctx *ctx, size_t n, size_t nclass, const float *student,
+                   const float *teacher, float temp, float scale, float *dz, float *loss);
+/* hint_mse (loss.rs:133-151): dz += 2 (pred - target) / (n c) * scale; *loss =
+ * scale * mean squared error. */
+int rnn_hint_mse(rnn_ctx *ctx, size_t n, size_t c, const float *pred, const float *target,
+                 float scale, float *dz, float *loss);
+
 /* ----------------------------------------------------------- optim.rs */
 /* Newton-Schulz orthogonalisation (newton_schulz, optim.rs:124-145), in
  * place on `count` [rows x cols] matrices at g + i*stride: X = G (G^T when

@@ -213,6 +213,21 @@ void orc_seqpool_forward(size_t n, size_t t, size_t c, const float *x, const flo
 void orc_seqpool_backward(size_t n, size_t t, size_t c, const float *dz, const float *w,
                           const float *x, const float *p, float *dx, float *dp);
 
+/* ---------------------------------------------------------------- loss.rs */
+void orc_taxo_target(size_t y, const uint32_t *parent, size_t nf, float eps, float sib,
+                     float *out);
+void orc_uniform_target(size_t y, size_t k, float eps, float *out);
+void orc_soft_targets(size_t n, size_t nf, size_t nc, const uint32_t *labels,
+                      const uint32_t *coarse, const uint32_t *perm, const float *lam,
+                      const uint32_t *parent, int taxo, float eps, float sib, float *tf,
+                      float *tc);
+float orc_ce_soft(size_t n, size_t nc, const float *logits, const float *target,
+                  const uint32_t *hard, float scale, float *dz, size_t *correct);
+float orc_kl_distill(size_t n, size_t nc, const float *student, const float *teacher, float temp,
+                     float scale, float *dz);
+float orc_hint_mse(size_t n, size_t c, const float *pred, const float *target, float scale,
+                   float *dz);
+
 #ifdef __cplusplus
 }
 #endif

@@ -161,6 +161,16 @@ def lib():
         L.orc_seqpool_forward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p]
         L.orc_seqpool_backward.argtypes = [_sz, _sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p,
                                            _f32p]
+        L.orc_taxo_target.argtypes = [_sz, _u32p, _sz, C.c_float, C.c_float, _f32p]
+        L.orc_uniform_target.argtypes = [_sz, _sz, C.c_float, _f32p]
+        L.orc_soft_targets.argtypes = [_sz, _sz, _sz, _u32p, vp, vp, vp, vp, C.c_int, C.c_float,
+                                       C.c_float, _f32p, vp]
+        L.orc_ce_soft.argtypes = [_sz, _sz, _f32p, _f32p, _u32p, C.c_float, _f32p, P(_sz)]
+        L.orc_ce_soft.restype = C.c_float
+        L.orc_kl_distill.argtypes = [_sz, _sz, _f32p, _f32p, C.c_float, C.c_float, _f32p]
+        L.orc_kl_distill.restype = C.c_float
+        L.orc_hint_mse.argtypes = [_sz, _sz, _f32p, _f32p, C.c_float, _f32p]
+        L.orc_hint_mse.restype = C.c_float
         _lib = L
     return _lib
 
@@ -620,3 +630,70 @@ def seqpool_backward(dz, w, x, p, n, t, dp):
     lib().orc_seqpool_backward(n, t, c, _f(dz).ravel(), _f(w).ravel(), _f(x).ravel(), _f(p),
                                dx, dp)
     return dx
+
+
+# ---------------------------------------------------------------- loss.rs
+def _u32(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def _addr(a):
+    return a.ctypes.data if a is not None else None
+
+
+def taxo_target(y, parent, eps, sib):
+    parent = _u32(parent)
+    out = np.empty(parent.size, np.float32)
+    lib().orc_taxo_target(y, parent, parent.size, eps, sib, out)
+    return out
+
+
+def uniform_target(y, k, eps):
+    out = np.empty(k, np.float32)
+    lib().orc_uniform_target(y, k, eps, out)
+    return out
+
+
+def soft_targets(labels, nf, eps, parent=None, sib=0.0, coarse=None, nc=0, perm=None, lam=None):
+    """targets (train.rs:121-155): returns (tf [n, nf], tc [n, nc] or None)."""
+    labels = _u32(labels)
+    n = labels.size
+    coarse = _u32(coarse) if coarse is not None else None
+    perm = _u32(perm) if perm is not None else None
+    lam = _f(lam) if lam is not None else None
+    parent = _u32(parent) if parent is not None else None
+    tf = np.empty((n, nf), np.float32)
+    tc = np.empty((n, nc), np.float32) if coarse is not None else None
+    lib().orc_soft_targets(n, nf, nc, labels, _addr(coarse), _addr(perm), _addr(lam),
+                           _addr(parent), int(parent is not None), eps, sib, tf.reshape(-1),
+                           _addr(tc))
+    return tf, tc
+
+
+def ce_soft(logits, target, hard, scale):
+    """ce_soft (loss.rs:39-83): returns (loss, correct, dz)."""
+    logits, target = _f(logits), _f(target)
+    n, nc = logits.shape
+    dz = np.empty_like(logits)
+    cor = _sz(0)
+    loss = lib().orc_ce_soft(n, nc, logits.reshape(-1), target.reshape(-1), _u32(hard), scale,
+                             dz.reshape(-1), C.byref(cor))
+    return float(loss), cor.value, dz
+
+
+def kl_distill(student, teacher, temp, scale, dz):
+    """kl_distill (loss.rs:87-130): dz += ...; returns the loss."""
+    _chk(dz)
+    student = _f(student)
+    n, nc = student.shape
+    return float(lib().orc_kl_distill(n, nc, student.reshape(-1), _f(teacher).reshape(-1), temp,
+                                      scale, dz.reshape(-1)))
+
+
+def hint_mse(pred, target, scale, dz):
+    """hint_mse (loss.rs:133-151): dz += ...; returns the loss."""
+    _chk(dz)
+    pred = _f(pred)
+    n, c = pred.shape
+    return float(lib().orc_hint_mse(n, c, pred.reshape(-1), _f(target).reshape(-1), scale,
+                                    dz.reshape(-1)))

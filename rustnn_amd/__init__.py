@@ -161,6 +161,11 @@ def lib():
             "rnn_clip_grad_norm": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
             "rnn_ema_update": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
             "rnn_clip_params": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
+            "rnn_soft_targets": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, C.c_int,
+                                      C.c_float, C.c_float, _vp, _vp]),
+            "rnn_ce_soft": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp]),
+            "rnn_kl_distill": (_i, [_vp, _sz, _sz, _vp, _vp, C.c_float, C.c_float, _vp, _vp]),
+            "rnn_hint_mse": (_i, [_vp, _sz, _sz, _vp, _vp, C.c_float, _vp, _vp]),
             "rnn_ln_forward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp]),
             "rnn_ln_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_layerscale_forward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),

@@ -1,0 +1,289 @@
+// loss.rs on the device: the soft targets (taxonomy / uniform smoothing with
+// the mixup blend of train.rs), soft-target cross-entropy, the distillation
+// KL and the hint MSE.
+//
+// Reference: taxo_target / uniform_target (loss.rs:11-34), ce_soft
+// (loss.rs:39-83), kl_distill (loss.rs:87-130), hint_mse (loss.rs:133-151),
+// targets (train.rs:121-155).  Each runs rayon over rows.
+//
+// The rows are few (a batch) and short (100 or 20 classes, or a 384-wide
+// feature), so every row is one thread running the reference's loops in
+// their order, with contraction off: the per-row arithmetic matches the
+// reference except for the device's expf / logf.  The per-row losses go to
+// the workspace and one thread adds them in row order (ce_soft and
+// kl_distill collect and sum in order; hint_mse's rayon sum has no fixed
+// order).  Scalars land in device memory, so nothing waits on the host.
+#include "rnn_internal.h"
+
+#include <algorithm>
+#include <cmath>
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int NT = 256;
+
+// ce_soft per row: dz overwritten with scale (softmax - t) / n; part[i] = the
+// row's loss, hit[i] = argmax == hard[i] (first maximum, as `v > mx`).
+__global__ void ce_soft_kernel(size_t n, int nc, const float *__restrict__ logits,
+                               const float *__restrict__ target, const uint32_t *__restrict__ hard,
+                               float scale, float *__restrict__ dz, float *__restrict__ part,
+                               uint32_t *__restrict__ hit) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n) return;
+    const float *z = logits + i * nc, *t = target + i * nc;
+    float *d = dz + i * nc;
+    const float inv = 1.0f / (float)n;
+    float mx = -INFINITY;
+    int arg = 0;
+    for (int j = 0; j < nc; j++)
+        if (z[j] > mx) {
+            mx = z[j];
+            arg = j;
+        }
+    float sum = 0.0f;
+    for (int j = 0; j < nc; j++) {
+        const float e = expf(z[j] - mx);
+        d[j] = e;
+        sum += e;
+    }
+    const float lse = mx + logf(sum);
+    float l = 0.0f;
+    for (int j = 0; j < nc; j++) {
+        l += t[j] * (lse - z[j]);
+        d[j] = (d[j] / sum - t[j]) * inv * scale;
+    }
+    part[i] = l;
+    if (hit) hit[i] = (uint32_t)arg == hard[i] ? 1u : 0u;
+}
+
+// Softmax of z / temp as kl_distill's `soft` closure (loss.rs:104-113): the
+// maximum, then the sum of exp((z - mx) / temp), then the inverse.
+__device__ __forceinline__ void soft_stats(const float *z, int nc, float it, float *mx,
+                                           float *is) {
+    float m = -INFINITY;
+    for (int j = 0; j < nc; j++) m = fmaxf(m, z[j]);
+    float s = 0.0f;
+    for (int j = 0; j < nc; j++) s += expf((z[j] - m) * it);
+    *mx = m;
+    *is = 1.0f / s;
+}
+
+// kl_distill per row (loss.rs:114-126): dz += temp (ps - pt) / n * scale;
+// part[i] = temp^2 KL(pt || ps).  ps / pt are recomputed per class from the
+// row's max and 1/sum, which gives the values the reference stores.
+__global__ void kl_distill_kernel(size_t n, int nc, const float *__restrict__ student,
+                                  const float *__restrict__ teacher, float temp, float scale,
+                                  float *__restrict__ dz, float *__restrict__ part) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n) return;
+    const float *zs = student + i * nc, *zt = teacher + i * nc;
+    float *d = dz + i * nc;
+    const float inv = 1.0f / (float)n, it = 1.0f / temp;
+    float ms, iss, mt, ist;
+    soft_stats(zs, nc, it, &ms, &iss);
+    soft_stats(zt, nc, it, &mt, &ist);
+    float l = 0.0f;
+    for (int j = 0; j < nc; j++) {
+        const float ps = expf((zs[j] - ms) * it) * iss;
+        const float pt = expf((zt[j] - mt) * it) * ist;
+        if (pt > 1e-9f) l += pt * (logf(fmaxf(pt, 1e-9f)) - logf(fmaxf(ps, 1e-9f)));
+        d[j] += temp * (ps - pt) * inv * scale;
+    }
+    part[i] = l * temp * temp;
+}
+
+// hint_mse per row (loss.rs:139-150): dz += 2 e / (n c) * scale; part[i] =
+// sum e^2.
+__global__ void hint_mse_kernel(size_t n, int c, const float *__restrict__ pred,
+                                const float *__restrict__ target, float scale,
+                                float *__restrict__ dz, float *__restrict__ part) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n) return;
+    const float inv = 1.0f / (float)(n * c);
+    const float *p = pred + i * c, *t = target + i * c;
+    float *d = dz + i * c;
+    float s = 0.0f;
+    for (int j = 0; j < c; j++) {
+        const float e = p[j] - t[j];
+        s += e * e;
+        d[j] += 2.0f * e * inv * scale;
+    }
+    part[i] = s;
+}
+
+// out = (sum of part in row order) * mul1 * mul2; hits summed likewise.
+__global__ void rows_total_kernel(size_t n, const float *__restrict__ part, float mul1, float mul2,
+                                  float *__restrict__ out, const uint32_t *__restrict__ hit,
+                                  uint32_t *__restrict__ correct) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    float s = 0.0f;
+    uint32_t h = 0;
+    for (size_t i = 0; i < n; i++) {
+        s += part[i];
+        if (hit) h += hit[i];
+    }
+    if (out) *out = s * mul1 * mul2;
+    if (correct) *correct = h;
+}
+
+// uniform_target (loss.rs:30-34), value at class j for label y of k classes.
+__device__ __forceinline__ float uniform_at(int y, int j, int k, float eps) {
+    const float v = eps / (float)k;
+    return j == y ? v + (1.0f - eps) : v;
+}
+
+// taxo_target (loss.rs:11-28), value at class j.
+__device__ __forceinline__ float taxo_at(int y, int j, int nf, const uint32_t *parent, float eps,
+                                         float sib) {
+    const uint32_t py = parent[y];
+    int k = 0;
+    for (int c = 0; c < nf; c++) k += parent[c] == py;
+    if (j == y) return 1.0f - eps;
+    if (k > 1 && parent[j] == py) return eps * sib / (float)(k - 1);
+    return nf > k ? eps * (1.0f - sib) / (float)(nf - k) : 0.0f;
+}
+
+// targets (train.rs:121-155): tf[i][j] = lam a_j + (1 - lam) b_j with a, b the
+// fine targets of labels[i] and labels[perm[i]] (taxonomy or uniform); tc the
+// same over the coarse labels with uniform smoothing.
+__global__ void targets_kernel(size_t n, int nf, int nc, const uint32_t *__restrict__ labels,
+                               const uint32_t *__restrict__ coarse,
+                               const uint32_t *__restrict__ perm, const float *__restrict__ lam,
+                               const uint32_t *__restrict__ parent, int taxo, float eps,
+                               float sib, float *__restrict__ tf, float *__restrict__ tc) {
+    const size_t per = (size_t)nf + (tc ? nc : 0);
+    const size_t len = n * per;
+    for (size_t e = (size_t)blockIdx.x * NT + threadIdx.x; e < len;
+         e += (size_t)gridDim.x * NT) {
+        const size_t i = e / per;
+        const int j = (int)(e - i * per);
+        const size_t pi = perm ? perm[i] : i;
+        const float l = lam ? lam[i] : 1.0f;
+        // an index out of range (a panic in the reference) gives NaN targets
+        // instead of an out-of-bounds read
+        if (j < nf) {
+            float v = NAN;
+            if (pi < n) {
+                const uint32_t ya = labels[i], yb = labels[pi];
+                if (ya < (uint32_t)nf && yb < (uint32_t)nf) {
+                    const float a = taxo ? taxo_at((int)ya, j, nf, parent, eps, sib)
+                                         : uniform_at((int)ya, j, nf, eps);
+                    const float b = taxo ? taxo_at((int)yb, j, nf, parent, eps, sib)
+                                         : uniform_at((int)yb, j, nf, eps);
+                    v = l * a + (1.0f - l) * b;
+                }
+            }
+            tf[i * nf + j] = v;
+        } else {
+            const int jc = j - nf;
+            float v = NAN;
+            if (pi < n) {
+                const uint32_t ca = coarse[i], cb = coarse[pi];
+                if (ca < (uint32_t)nc && cb < (uint32_t)nc)
+                    v = l * uniform_at((int)ca, jc, nc, eps) +
+                        (1.0f - l) * uniform_at((int)cb, jc, nc, eps);
+            }
+            tc[i * nc + jc] = v;
+        }
+    }
+}
+
+bool rows_ok(rnn_ctx *ctx, size_t n, size_t c, const char *what) {
+    if (n > 0x7fffffffull || c == 0 || c > (1u << 24)) {
+        rnn_fail(ctx, RNN_E_INVALID, "%s: %zu rows of %zu", what, n, c);
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rnn_soft_targets(rnn_ctx *ctx, size_t n, size_t nf, size_t nc, const uint32_t *labels,
+                     const uint32_t *coarse, const uint32_t *perm, const float *lam,
+                     const uint32_t *parent, int taxo, float eps, float sib, float *tf,
+                     float *tc) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0) return RNN_OK;
+    if (!labels || !tf || (taxo && !parent) || (tc && !coarse))
+        return rnn_fail(ctx, RNN_E_NULL, "soft_targets: null operand");
+    if (!rows_ok(ctx, n, nf, "soft_targets") || (tc && !rows_ok(ctx, n, nc, "soft_targets")))
+        return RNN_E_INVALID;
+    const size_t len = n * (nf + (tc ? nc : 0));
+    const unsigned grid = (unsigned)std::min<size_t>(rnn_div_up(len, NT), 4096);
+    targets_kernel<<<grid, NT, 0, ctx->stream>>>(n, (int)nf, (int)nc, labels, coarse, perm, lam,
+                                                 parent, taxo, eps, sib, tf, tc);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_ce_soft(rnn_ctx *ctx, size_t n, size_t nclass, const float *logits, const float *target,
+                const uint32_t *hard, float scale, float *dz, float *loss, uint32_t *correct) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0) return RNN_OK;
+    if (!logits || !target || !dz || (correct && !hard))
+        return rnn_fail(ctx, RNN_E_NULL, "ce_soft: null operand");
+    if (!rows_ok(ctx, n, nclass, "ce_soft")) return RNN_E_INVALID;
+    WsCarve cv;
+    const size_t o_part = cv.take(n * sizeof(float)), o_hit = cv.take(n * sizeof(uint32_t));
+    char *ws = (char *)rnn_workspace(ctx, cv.off);
+    if (!ws) return RNN_E_NOMEM;
+    float *part = (float *)(ws + o_part);
+    uint32_t *hit = correct ? (uint32_t *)(ws + o_hit) : nullptr;
+    ce_soft_kernel<<<(unsigned)rnn_div_up(n, NT), NT, 0, ctx->stream>>>(
+        n, (int)nclass, logits, target, hard, scale, dz, part, hit);
+    RNN_LAUNCHED(ctx);
+    if (loss || correct) {
+        rows_total_kernel<<<1, 64, 0, ctx->stream>>>(n, part, 1.0f / (float)n, 1.0f, loss, hit,
+                                                     correct);
+        RNN_LAUNCHED(ctx);
+    }
+    return RNN_OK;
+}
+
+int rnn_kl_distill(rnn_ctx *ctx, size_t n, size_t nclass, const float *student,
+                   const float *teacher, float temp, float scale, float *dz, float *loss) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0) return RNN_OK;
+    if (!student || !teacher || !dz) return rnn_fail(ctx, RNN_E_NULL, "kl_distill: null operand");
+    if (!rows_ok(ctx, n, nclass, "kl_distill")) return RNN_E_INVALID;
+    float *part = (float *)rnn_workspace(ctx, n * sizeof(float));
+    if (!part) return RNN_E_NOMEM;
+    kl_distill_kernel<<<(unsigned)rnn_div_up(n, NT), NT, 0, ctx->stream>>>(
+        n, (int)nclass, student, teacher, temp, scale, dz, part);
+    RNN_LAUNCHED(ctx);
+    if (loss) {
+        rows_total_kernel<<<1, 64, 0, ctx->stream>>>(n, part, 1.0f / (float)n, 1.0f, loss, nullptr,
+                                                     nullptr);
+        RNN_LAUNCHED(ctx);
+    }
+    return RNN_OK;
+}
+
+int rnn_hint_mse(rnn_ctx *ctx, size_t n, size_t c, const float *pred, const float *target,
+                 float scale, float *dz, float *loss) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0) return RNN_OK;
+    if (!pred || !target || !dz) return rnn_fail(ctx, RNN_E_NULL, "hint_mse: null operand");
+    if (!rows_ok(ctx, n, c, "hint_mse")) return RNN_E_INVALID;
+    float *part = (float *)rnn_workspace(ctx, n * sizeof(float));
+    if (!part) return RNN_E_NOMEM;
+    hint_mse_kernel<<<(unsigned)rnn_div_up(n, NT), NT, 0, ctx->stream>>>(n, (int)c, pred, target,
+                                                                         scale, dz, part);
+    RNN_LAUNCHED(ctx);
+    if (loss) {
+        rows_total_kernel<<<1, 64, 0, ctx->stream>>>(n, part, 1.0f / (float)(n * c), scale, loss,
+                                                     nullptr, nullptr);
+        RNN_LAUNCHED(ctx);
+    }
+    return RNN_OK;
+}
+
+}  // extern "C"
