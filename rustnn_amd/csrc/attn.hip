@@ -509,15 +509,20 @@ __global__ void rel_index_kernel(int th, int tw, int mh, int mw, uint32_t *idx) 
     idx[e] = (uint32_t)(dy * sx + dx);
 }
 
+// tq or tk above 64: the composed path (batched GEMMs + row kernels).
+bool large_desc(const rnn_attn_desc *d) { return d->tq > MAXT || d->tk > MAXT; }
+
 int check_desc(rnn_ctx *ctx, const rnn_attn_desc *d) {
     if (!d) return rnn_fail(ctx, RNN_E_NULL, "attn: desc is null");
     if (!d->relidx) return rnn_fail(ctx, RNN_E_NULL, "attn: relidx is null");
     if (!d->h || !d->dh || !d->tq || !d->tk || !d->nrel)
         return rnn_fail(ctx, RNN_E_INVALID, "attn: zero dimension");
-    if (d->tq > MAXT || d->tk > MAXT || d->dh > MAXDH)
+    if (d->dh > MAXDH && !large_desc(d))
         return rnn_fail(ctx, RNN_E_UNSUPPORTED,
-                        "attn: tq=%u tk=%u dh=%u beyond the LDS-resident kernel (64/64/64)", d->tq,
-                        d->tk, d->dh);
+                        "attn: dh=%u beyond the register-resident kernel (64) at tq=%u tk=%u",
+                        d->dh, d->tq, d->tk);
+    if ((size_t)d->tq * d->tk > ((size_t)1 << 26) || d->tk > (1u << 20))
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: tq=%u tk=%u too large", d->tq, d->tk);
     // The table last uploaded was validated already.
     const size_t cnt = (size_t)d->tq * d->tk;
     if (ctx->rel_dev && ctx->rel_nrel == d->nrel && ctx->rel_host.size() == cnt &&
@@ -541,7 +546,9 @@ int upload_rel(rnn_ctx *ctx, const rnn_attn_desc *d) {
     if (ctx->rel_dev && ctx->rel_nrel == d->nrel && ctx->rel_host.size() == cnt &&
         ctx->rel_tk == d->tk && std::memcmp(ctx->rel_host.data(), d->relidx, cnt * 4) == 0)
         return RNN_OK;
-    size_t need = cnt + (d->nrel + 1) + cnt + 4096 + 4;  // + lane-order table (16-byte aligned)
+    const bool large = large_desc(d);
+    // + the lane-order table (16-byte aligned) of the register-resident kernels
+    size_t need = cnt + (d->nrel + 1) + cnt + (large ? 0 : 4096 + 4);
     // The previous upload (and kernels reading it) must be done before reuse.
     RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (need > ctx->rel_cap) {
@@ -563,21 +570,27 @@ int upload_rel(rnn_ctx *ctx, const rnn_attn_desc *d) {
     for (size_t i = 0; i < cnt; i++) count[d->relidx[i] + 1]++;
     for (uint32_t r = 0; r < d->nrel; r++) count[r + 1] += count[r];
     for (uint32_t r = 0; r <= d->nrel; r++) rowptr[r] = count[r];
-    // positions as offsets into the kernels' LDS [tq][LS] score tiles
+    // positions: offsets into the kernels' LDS [tq][LS] score tiles, or, on
+    // the composed path, flat offsets q*tk + k into a [tq][tk] score matrix
     for (size_t i = 0; i < cnt; i++)
-        pos[count[d->relidx[i]]++] = (uint32_t)((i / d->tk) * LS + i % d->tk);
+        pos[count[d->relidx[i]]++] =
+            large ? (uint32_t)i : (uint32_t)((i / d->tk) * LS + i % d->tk);
     // relidx in the forward's lane order: entry (qi*2 + half)*32 + 16nt + v is
     // the slot of query qi, key key_of(nt, v, half); clamped into the table,
     // so every entry is a valid slot.
-    uint32_t *rperm = rperm_of(h, cnt, d->nrel);
-    for (int q = 0; q < 64; q++)
-        for (int hf = 0; hf < 2; hf++)
-            for (int nt = 0; nt < 2; nt++)
-                for (int v = 0; v < 16; v++) {
-                    const int kj = 32 * nt + 8 * (v >> 2) + 4 * hf + (v & 3);
-                    const int qc = std::min(q, (int)d->tq - 1), kc = std::min(kj, (int)d->tk - 1);
-                    rperm[(q * 2 + hf) * 32 + 16 * nt + v] = d->relidx[(size_t)qc * d->tk + kc];
-                }
+    if (!large) {
+        uint32_t *rperm = rperm_of(h, cnt, d->nrel);
+        for (int q = 0; q < 64; q++)
+            for (int hf = 0; hf < 2; hf++)
+                for (int nt = 0; nt < 2; nt++)
+                    for (int v = 0; v < 16; v++) {
+                        const int kj = 32 * nt + 8 * (v >> 2) + 4 * hf + (v & 3);
+                        const int qc = std::min(q, (int)d->tq - 1);
+                        const int kc = std::min(kj, (int)d->tk - 1);
+                        rperm[(q * 2 + hf) * 32 + 16 * nt + v] =
+                            d->relidx[(size_t)qc * d->tk + kc];
+                    }
+    }
     RNN_HIP(ctx, hipMemcpyAsync(ctx->rel_dev, h, need * 4, hipMemcpyHostToDevice, ctx->stream));
     ctx->rel_host.assign(d->relidx, d->relidx + cnt);
     ctx->rel_nrel = d->nrel;
@@ -617,6 +630,111 @@ bool use_vec(const AttnArgs &g) {
            (g.dout == nullptr || al16(g.dout));
 }
 
+// ---------------------------------------------------------------------------
+// The composed path for tq or tk above 64 (the rustvit's cross-attention:
+// tq 64, tk 256, dh 64, nrel 900).  The reference's own structure: per head, a
+// batched GEMM over the images (strided Q/K/V through leading dimensions) for
+// S = QK^T, a row kernel for the biased, masked softmax (P kept, as the
+// backward reads it), a batched GEMM for O = PV; the backward likewise.
+
+// Softmax of the rows of P in place (attn.rs:190-212): x = tau S + rel[idx],
+// the diagonal -inf when masked; max, exp(x - max) (-inf -> 0), sum, times
+// 1/sum.  One wave per row (image, head, query).
+__global__ __launch_bounds__(256) void attn_softmax_rows_kernel(
+    float *p, const float *__restrict__ tau, const float *__restrict__ rel,
+    const uint32_t *__restrict__ relidx, long long rows, int h, int tq, int tk, int nrel,
+    int mask) {
+    const long long r = (long long)blockIdx.x * 4 + wave_index();
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const int qi = (int)(r % tq), hd = (int)((r / tq) % h);
+    float *row = p + r * tk;
+    const float t = tau[hd];
+    const float *rh = rel + (long long)hd * nrel;
+    const uint32_t *ix = relidx + (long long)qi * tk;
+    float mx = -INFINITY;
+    for (int k = lane; k < tk; k += 64) {
+        const float x = (mask && k == qi) ? -INFINITY : t * row[k] + rh[ix[k]];
+        row[k] = x;
+        mx = fmaxf(mx, x);
+    }
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+    float sum = 0.f;
+    for (int k = lane; k < tk; k += 64) {
+        const float x = row[k];
+        const float e = x == -INFINITY ? 0.f : expf(x - mx);
+        row[k] = e;
+        sum += e;
+    }
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+    const float inv = 1.0f / sum;
+    for (int k = lane; k < tk; k += 64) row[k] *= inv;
+}
+
+// Backward rows (attn.rs:280-330): s1 holds dP, s2 the recomputed raw S.
+// dS = P o (dP - <dP, P>) goes to s1 (for drel), tau dS to s2 (for dQ, dK);
+// part[row] = sum dS o S_raw (the dtau share of the row).
+__global__ __launch_bounds__(256) void attn_dsoft_rows_kernel(
+    const float *__restrict__ p, float *s1, float *s2, const float *__restrict__ tau,
+    float *__restrict__ part, long long rows, int h, int tq, int tk) {
+    const long long r = (long long)blockIdx.x * 4 + wave_index();
+    if (r >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const int hd = (int)((r / tq) % h);
+    const float *pr = p + r * tk;
+    float *dp = s1 + r * tk, *sr = s2 + r * tk;
+    float dot = 0.f;
+    for (int k = lane; k < tk; k += 64) dot += dp[k] * pr[k];
+    for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
+    const float t = tau[hd];
+    float dt = 0.f;
+    for (int k = lane; k < tk; k += 64) {
+        const float ds = pr[k] * (dp[k] - dot);
+        dt += ds * sr[k];
+        dp[k] = ds;
+        sr[k] = ds * t;
+    }
+    for (int o = 32; o >= 1; o >>= 1) dt += __shfl_xor(dt, o, 64);
+    if (lane == 0) part[r] = dt;
+}
+
+// dtau[hd] += sum over (image, query) rows of head hd of part (block hd;
+// strided per thread, then a fixed tree).
+__global__ __launch_bounds__(256) void attn_head_sum_kernel(const float *__restrict__ part,
+                                                            long long n, int h, int tq,
+                                                            float *dtau) {
+    __shared__ float red[4];
+    const int hd = blockIdx.x;
+    const long long per = n * tq;
+    float s = 0.f;
+    for (long long i = threadIdx.x; i < per; i += 256) {
+        const long long img = i / tq, q = i - img * tq;
+        s += part[(img * h + hd) * tq + q];
+    }
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) dtau[hd] += (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// drel[hd*nrel + slot] += sum over images and the positions of the slot (the
+// inverse index, ascending) of dS.  One thread per (head, slot).
+__global__ __launch_bounds__(256) void attn_drel_gather_kernel(
+    const float *__restrict__ ds, const uint32_t *__restrict__ rowptr,
+    const uint32_t *__restrict__ pos, long long n, int h, int nrel, long long cnt,
+    float *drel) {
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (long long)h * nrel) return;
+    const int hd = (int)(e / nrel), slot = (int)(e - (long long)hd * nrel);
+    const uint32_t p0 = rowptr[slot], p1 = rowptr[slot + 1];
+    float s = 0.f;
+    for (long long img = 0; img < n; img++) {
+        const float *base = ds + (img * h + hd) * cnt;
+        for (uint32_t i = p0; i < p1; i++) s += base[pos[i]];
+    }
+    drel[e] += s;
+}
+
 size_t bwd_lds() { return ((size_t)2 * 64 * LS + 2) * 4; }
 size_t fwd_lds(size_t nrel) { return ((size_t)64 * LS + 4096 + nrel) * 4; }
 
@@ -636,6 +754,88 @@ void set_lds_limits() {
         (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
 }
 
+// Core::forward on the composed path (see attn_softmax_rows_kernel).
+int attn_forward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
+                       const float *kv, const float *tau, const float *rel, float *p, float *o) {
+    const size_t tq = d->tq, tk = d->tk, dh = d->dh, h = d->h, c = h * dh;
+    for (size_t hd = 0; hd < h; hd++) {
+        int rc = rnn_gemm_launch_ld(ctx, n, tq, tk, dh, q + d->qoff + hd * dh, d->qstride,
+                                    tq * d->qstride, 0, kv + d->koff + hd * dh, d->kvstride,
+                                    tk * d->kvstride, 1, p + hd * tq * tk, tk, h * tq * tk, 0);
+        if (rc) return rc;
+    }
+    const long long rows = (long long)n * h * tq;
+    attn_softmax_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
+        p, tau, rel, ctx->rel_dev, rows, (int)h, (int)tq, (int)tk, (int)d->nrel,
+        d->mask_diag ? 1 : 0);
+    RNN_LAUNCHED(ctx);
+    for (size_t hd = 0; hd < h; hd++) {
+        int rc = rnn_gemm_launch_ld(ctx, n, tq, dh, tk, p + hd * tq * tk, tk, h * tq * tk, 0,
+                                    kv + d->voff + hd * dh, d->kvstride, tk * d->kvstride, 0,
+                                    o + hd * dh, c, tq * c, 0);
+        if (rc) return rc;
+    }
+    return RNN_OK;
+}
+
+// Core::backward on the composed path: dV = P^T dO, dP = dO V^T, the raw S
+// recomputed, the row kernel (dS, tau dS, dtau shares), dtau and drel, then
+// dQ = (tau dS) K and dK = (tau dS)^T Q; dq, dkv, dtau, drel accumulate.
+int attn_backward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
+                        const float *kv, const float *tau, const float *p, const float *dout,
+                        float *dq, float *dkv, float *dtau, float *drel) {
+    const size_t tq = d->tq, tk = d->tk, dh = d->dh, h = d->h, c = h * dh;
+    const size_t cnt = tq * tk, mat = n * h * cnt;
+    const long long rows = (long long)n * h * tq;
+    WsCarve cv;
+    const size_t o1 = cv.take(mat * 4), o2 = cv.take(mat * 4), o3 = cv.take((size_t)rows * 4);
+    char *ws = (char *)rnn_workspace(ctx, cv.off);
+    if (!ws) return RNN_E_NOMEM;
+    float *s1 = (float *)(ws + o1), *s2 = (float *)(ws + o2), *part = (float *)(ws + o3);
+    for (size_t hd = 0; hd < h; hd++) {
+        // dV += P^T dO (attn.rs:262-270)
+        int rc = rnn_gemm_launch_ld(ctx, n, tk, dh, tq, p + hd * cnt, tk, h * cnt, 1,
+                                    dout + hd * dh, c, tq * c, 0, dkv + d->voff + hd * dh,
+                                    d->kvstride, tk * d->kvstride, 1);
+        if (rc) return rc;
+        // dP = dO V^T (attn.rs:272-278)
+        rc = rnn_gemm_launch_ld(ctx, n, tq, tk, dh, dout + hd * dh, c, tq * c, 0,
+                                kv + d->voff + hd * dh, d->kvstride, tk * d->kvstride, 1,
+                                s1 + hd * cnt, tk, h * cnt, 0);
+        if (rc) return rc;
+        // the raw scores again (attn.rs:292-300)
+        rc = rnn_gemm_launch_ld(ctx, n, tq, tk, dh, q + d->qoff + hd * dh, d->qstride,
+                                tq * d->qstride, 0, kv + d->koff + hd * dh, d->kvstride,
+                                tk * d->kvstride, 1, s2 + hd * cnt, tk, h * cnt, 0);
+        if (rc) return rc;
+    }
+    attn_dsoft_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
+        p, s1, s2, tau, part, rows, (int)h, (int)tq, (int)tk);
+    RNN_LAUNCHED(ctx);
+    attn_head_sum_kernel<<<(unsigned)h, 256, 0, ctx->stream>>>(part, (long long)n, (int)h,
+                                                              (int)tq, dtau);
+    RNN_LAUNCHED(ctx);
+    attn_drel_gather_kernel<<<(unsigned)rnn_div_up(h * d->nrel, (size_t)256), 256, 0,
+                              ctx->stream>>>(s1, ctx->rel_dev + cnt, ctx->rel_dev + cnt +
+                                                                         d->nrel + 1,
+                                             (long long)n, (int)h, (int)d->nrel,
+                                             (long long)cnt, drel);
+    RNN_LAUNCHED(ctx);
+    for (size_t hd = 0; hd < h; hd++) {
+        // dQ += (tau dS) K (attn.rs:317-322)
+        int rc = rnn_gemm_launch_ld(ctx, n, tq, dh, tk, s2 + hd * cnt, tk, h * cnt, 0,
+                                    kv + d->koff + hd * dh, d->kvstride, tk * d->kvstride, 0,
+                                    dq + d->qoff + hd * dh, d->qstride, tq * d->qstride, 1);
+        if (rc) return rc;
+        // dK += (tau dS)^T Q (attn.rs:324-330)
+        rc = rnn_gemm_launch_ld(ctx, n, tk, dh, tq, s2 + hd * cnt, tk, h * cnt, 1,
+                                q + d->qoff + hd * dh, d->qstride, tq * d->qstride, 0,
+                                dkv + d->koff + hd * dh, d->kvstride, tk * d->kvstride, 1);
+        if (rc) return rc;
+    }
+    return RNN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -650,9 +850,10 @@ int rnn_attn_forward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float
     if (!q || !kv || !tau || !rel || !p || !o)
         return rnn_fail(ctx, RNN_E_NULL, "attn_forward: null operand");
     if (n * d->h > 0x7fffffffu) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: too many problems");
-    set_lds_limits();
     rc = upload_rel(ctx, d);
     if (rc) return rc;
+    if (large_desc(d)) return attn_forward_large(ctx, d, n, q, kv, tau, rel, p, o);
+    set_lds_limits();
     AttnArgs g;
     fill_args(g, ctx, d, n);
     g.q = q;
@@ -686,9 +887,11 @@ int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const floa
     if (!q || !kv || !tau || !p || !dout || !dq || !dkv || !dtau || !drel)
         return rnn_fail(ctx, RNN_E_NULL, "attn_backward: null operand");
     if (n * d->h > 0x7fffffffu) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: too many problems");
-    set_lds_limits();
     rc = upload_rel(ctx, d);
     if (rc) return rc;
+    if (large_desc(d))
+        return attn_backward_large(ctx, d, n, q, kv, tau, p, dout, dq, dkv, dtau, drel);
+    set_lds_limits();
     AttnArgs g;
     fill_args(g, ctx, d, n);
     size_t parts = n * d->h + n * d->h * (size_t)d->nrel;

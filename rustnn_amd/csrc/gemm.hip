@@ -402,6 +402,15 @@ int rnn_ns_gemm_launch(rnn_ctx *ctx, const NsGemmProb *probs, int nprob, size_t 
     return RNN_OK;
 }
 
+int rnn_gemm_launch_ld(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
+                       size_t lda, size_t stride_a, int at, const float *b, size_t ldb,
+                       size_t stride_b, int bt, float *c, size_t ldc, size_t stride_c, int acc) {
+    if (lda > INT32_MAX || ldb > INT32_MAX || ldc > INT32_MAX)
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "gemm: leading dimension beyond 32 bits");
+    return gemm_enqueue(ctx, count, m, n, k, k * count, a, stride_a, (int)lda, at, b, stride_b,
+                        (int)ldb, bt, c, stride_c, (int)ldc, acc, nullptr);
+}
+
 static int fill(rnn_ctx *ctx, float *p, size_t len, float v) {
     if (!len) return RNN_OK;
     int blocks = (int)std::min<size_t>(rnn_div_up(len, 256), 4096);

@@ -132,6 +132,13 @@ struct NsGemmProb {
 int rnn_ns_gemm_launch(rnn_ctx *ctx, const NsGemmProb *probs, int nprob, size_t ntiles, int vec,
                        float alpha, float beta);
 
+// rnn_gemm_launch with explicit leading dimensions: op(A) [m x k] read from
+// rows of stride lda (A stored [k][m] with stride lda when at), likewise B
+// (ldb) and C (ldc); batch z at a + z*stride_a etc.  No bias.
+int rnn_gemm_launch_ld(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
+                       size_t lda, size_t stride_a, int at, const float *b, size_t ldb,
+                       size_t stride_b, int bt, float *c, size_t ldc, size_t stride_c, int acc);
+
 int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
                     size_t stride_a, int at, const float *b, size_t stride_b, int bt, float *c,
                     size_t stride_c, int acc, const float *bias);

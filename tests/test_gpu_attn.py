@@ -48,6 +48,10 @@ CASES = [
     ("gc_cross", 3, 2, 4, 3, 3, 6, 6, "lsa"),
     ("dh64_t16", 16, 6, 64, 4, 4, 4, 4, "lsa"),
     ("dh64_t64", 8, 4, 64, 8, 8, 8, 8, "lsa"),
+    # tq or tk above 64: the composed path (batched GEMMs + row kernels)
+    ("cross_tk256", 8, 4, 64, 8, 8, 16, 16, "lsa"),   # the rustvit's cross-attention
+    ("self_t100", 4, 2, 48, 10, 10, 10, 10, "lsa"),   # masked self-attention, 100 tokens
+    ("cross_tk81_dh80", 3, 2, 80, 3, 3, 9, 9, "lsa"),
 ]
 
 
@@ -88,13 +92,15 @@ def test_attn_parity(rnn, orc, name, n, h, dh, th, tw, mh, mw, variant):
     assert rel_frob(to_host(drel) - drel0, drel_w - drel0) < TOL, "drel"
 
 
-def test_attn_aliased_dq_dkv(rnn, orc):
+@pytest.mark.parametrize("n,h,dh,t", [(32, 4, 32, 8), (4, 2, 48, 10)])
+def test_attn_aliased_dq_dkv(rnn, orc, n, h, dh, t):
     """SelfAttn accumulates dq and dk/dv into one fused-QKV gradient buffer
-    (attn.rs:418-438); the device path may take them aliased."""
-    n, h, dh = 32, 4, 32
-    cs = make_case(orc, n, h, dh, 8, 8, 8, 8, "lsa", seed=13)
+    (attn.rs:418-438); the device path may take them aliased (both the
+    register-resident kernels and, at 100 tokens, the composed path)."""
+    cs = make_case(orc, n, h, dh, t, t, t, t, "lsa", seed=13)
     g = cs["geo"]
-    d = orc.attn_desc(h, dh, 64, 64, g["qstride"], 0, g["kvstride"], g["koff"], g["voff"],
+    T = t * t
+    d = orc.attn_desc(h, dh, T, T, g["qstride"], 0, g["kvstride"], g["koff"], g["voff"],
                       cs["relidx"], cs["nrel"], True)
     p_w, _ = orc.attn_forward(d, n, cs["q"], cs["kv"], cs["tau"], cs["rel"])
     z = np.zeros(cs["q"].size, np.float32)
@@ -102,7 +108,7 @@ def test_attn_aliased_dq_dkv(rnn, orc):
                                           np.zeros(h, np.float32),
                                           np.zeros(h * cs["nrel"], np.float32))
     want = dq_w + dkv_w  # attn.rs:438
-    core = rnn.Core(h, dh, 64, 64, cs["relidx"], cs["nrel"], True)
+    core = rnn.Core(h, dh, T, T, cs["relidx"], cs["nrel"], True)
     Q = to_dev(cs["q"])
     dab = to_dev(z.copy())
     dtau = to_dev(np.zeros(h, np.float32))
@@ -123,10 +129,10 @@ def test_rel_index_bit_exact(rnn, orc, th, tw, mh, mw):
 
 
 def test_attn_unsupported_shape_raises(rnn, orc):
-    relidx, nrel = orc.rel_index(8, 8, 16, 16)  # tk = 256: beyond the LDS-resident kernel
-    core = rnn.Core(4, 64, 64, 256, relidx, nrel, False)
-    q = to_dev(np.zeros(64 * 256, np.float32))
-    kv = to_dev(np.zeros(256 * 512, np.float32))
+    relidx, nrel = orc.rel_index(8, 8, 8, 8)  # dh = 80 at tq = tk = 64: beyond the kernel
+    core = rnn.Core(1, 80, 64, 64, relidx, nrel, False)
+    q = to_dev(np.zeros(64 * 80, np.float32))
+    kv = to_dev(np.zeros(64 * 160, np.float32))
     with pytest.raises(rnn.RnnError):
-        core.forward(1, q, 256, 0, kv, 512, 0, 256, to_dev(np.ones(4, np.float32)),
-                     to_dev(np.zeros(4 * nrel, np.float32)))
+        core.forward(1, q, 80, 0, kv, 160, 0, 80, to_dev(np.ones(1, np.float32)),
+                     to_dev(np.zeros(nrel, np.float32)))
