@@ -288,6 +288,35 @@ int rnn_kl_distill(rnn_ctx *ctx, size_t n, size_t nclass, const float *student,
 int rnn_hint_mse(rnn_ctx *ctx, size_t n, size_t c, const float *pred, const float *target,
                  float scale, float *dz, float *loss);
 
+/* ----------------------------------------------------------- vit.rs */
+/* DropPath (vit.rs:25-74) on n images of `per` floats, in place: image i is
+ * kept with the i-th uniform of Rng::new(seed) (rng.rs) below 1 - p and
+ * scaled by 1 / (1 - p), else zeroed; mask [n] (device) receives the factors
+ * for the backward.  0 < p < 1 (the reference skips the layer otherwise). */
+int rnn_drop_path_forward(rnn_ctx *ctx, size_t n, size_t per, float *x, float p, uint64_t seed,
+                          float *mask);
+int rnn_drop_path_backward(rnn_ctx *ctx, size_t n, size_t per, float *dy, const float *mask);
+/* y[r][j] += l[j] x[r][j]: Block's depthwise gate a += gamma * dw(h)
+ * (vit.rs:150-158).  Its backward is rnn_layerscale_backward. */
+int rnn_axpy_cols(rnn_ctx *ctx, size_t rows, size_t c, float *y, const float *l, const float *x);
+/* token_merge / token_merge_back (vit.rs:612-650): [n][th*th][c] <->
+ * [n][(th/2)^2][4c], the 2x2 neighbours (0,0), (0,1), (1,0), (1,1)
+ * concatenated; th even; the backward overwrites dz. */
+int rnn_token_merge(rnn_ctx *ctx, size_t n, size_t th, size_t c, const float *z, float *y);
+int rnn_token_merge_backward(rnn_ctx *ctx, size_t n, size_t th, size_t c, const float *dy,
+                             float *dz);
+/* TaxoHead (vit.rs:282-312): zf[i][j] += zc[i][parent[j]]; the backward's
+ * coarse gradient dc = dzc + the fine gradients summed by parent (in class
+ * order).  parent (device u32 [nf]). */
+int rnn_taxo_head_combine(rnn_ctx *ctx, size_t n, size_t nf, size_t nc, const uint32_t *parent,
+                          float *zf, const float *zc);
+int rnn_taxo_head_combine_backward(rnn_ctx *ctx, size_t n, size_t nf, size_t nc,
+                                   const uint32_t *parent, const float *dzf, const float *dzc,
+                                   float *dc);
+/* Tok::from_tensor / to_tensor (tok.rs): [n][c][hw] <-> [n][hw][c]. */
+int rnn_nchw_to_tokens(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, float *t);
+int rnn_tokens_to_nchw(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *t, float *x);
+
 /* ----------------------------------------------------------- optim.rs */
 /* Newton-Schulz orthogonalisation (newton_schulz, optim.rs:124-145), in
  * place on `count` [rows x cols] matrices at g + i*stride: X = G (G^T when

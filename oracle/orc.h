@@ -228,6 +228,14 @@ float orc_kl_distill(size_t n, size_t nc, const float *student, const float *tea
 float orc_hint_mse(size_t n, size_t c, const float *pred, const float *target, float scale,
                    float *dz);
 
+/* ---------------------------------------------------------------- vit.rs */
+void orc_drop_path(size_t n, size_t per, float *x, float p, uint64_t seed, float *mask);
+void orc_token_merge(size_t n, size_t th, size_t c, const float *z, float *y);
+void orc_taxo_combine(size_t n, size_t nf, size_t nc, const uint32_t *parent, float *zf,
+                      const float *zc);
+void orc_taxo_combine_backward(size_t n, size_t nf, size_t nc, const uint32_t *parent,
+                               const float *dzf, const float *dzc, float *dc);
+
 #ifdef __cplusplus
 }
 #endif

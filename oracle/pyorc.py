@@ -171,6 +171,10 @@ def lib():
         L.orc_kl_distill.restype = C.c_float
         L.orc_hint_mse.argtypes = [_sz, _sz, _f32p, _f32p, C.c_float, _f32p]
         L.orc_hint_mse.restype = C.c_float
+        L.orc_drop_path.argtypes = [_sz, _sz, _f32p, C.c_float, C.c_uint64, _f32p]
+        L.orc_token_merge.argtypes = [_sz, _sz, _sz, _f32p, _f32p]
+        L.orc_taxo_combine.argtypes = [_sz, _sz, _sz, _u32p, _f32p, _f32p]
+        L.orc_taxo_combine_backward.argtypes = [_sz, _sz, _sz, _u32p, _f32p, _f32p, _f32p]
         _lib = L
     return _lib
 
@@ -697,3 +701,35 @@ def hint_mse(pred, target, scale, dz):
     n, c = pred.shape
     return float(lib().orc_hint_mse(n, c, pred.reshape(-1), _f(target).reshape(-1), scale,
                                     dz.reshape(-1)))
+
+
+# ---------------------------------------------------------------- vit.rs
+def drop_path(x, n, p, seed):
+    """DropPath::forward (vit.rs:39-59): returns (scaled copy, mask [n])."""
+    x = _f(x).ravel().copy()
+    mask = np.empty(n, np.float32)
+    lib().orc_drop_path(n, x.size // n, x, p, C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF), mask)
+    return x, mask
+
+
+def token_merge(z, n, th, c):
+    y = np.empty(z.size, np.float32)
+    lib().orc_token_merge(n, th, c, _f(z).ravel(), y)
+    return y
+
+
+def taxo_combine(zf, zc, parent):
+    zf = _f(zf).copy()
+    n, nf = zf.shape
+    nc = zc.shape[1]
+    lib().orc_taxo_combine(n, nf, nc, _u32(parent), zf.reshape(-1), _f(zc).reshape(-1))
+    return zf
+
+
+def taxo_combine_backward(dzf, dzc, parent):
+    n, nf = dzf.shape
+    nc = dzc.shape[1]
+    dc = np.empty((n, nc), np.float32)
+    lib().orc_taxo_combine_backward(n, nf, nc, _u32(parent), _f(dzf).reshape(-1),
+                                    _f(dzc).reshape(-1), dc.reshape(-1))
+    return dc

@@ -161,6 +161,15 @@ def lib():
             "rnn_clip_grad_norm": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
             "rnn_ema_update": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
             "rnn_clip_params": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
+            "rnn_drop_path_forward": (_i, [_vp, _sz, _sz, _vp, C.c_float, C.c_uint64, _vp]),
+            "rnn_drop_path_backward": (_i, [_vp, _sz, _sz, _vp, _vp]),
+            "rnn_axpy_cols": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),
+            "rnn_token_merge": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
+            "rnn_token_merge_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
+            "rnn_taxo_head_combine": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp]),
+            "rnn_taxo_head_combine_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "rnn_nchw_to_tokens": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
+            "rnn_tokens_to_nchw": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
             "rnn_soft_targets": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, C.c_int,
                                       C.c_float, C.c_float, _vp, _vp]),
             "rnn_ce_soft": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp]),

@@ -1,0 +1,299 @@
+// vit.rs on the device: DropPath, the depthwise branch's per-channel gate,
+// the 2x2 token merge, TaxoHead's parent gather and the NCHW <-> token
+// layout changes (tok.rs).
+//
+// Reference: DropPath (vit.rs:25-74), Block's `a += gamma * dw(h)`
+// (vit.rs:150-158), token_merge / token_merge_back (vit.rs:612-650),
+// TaxoHead::forward / backward (vit.rs:282-312), Tok::from_tensor /
+// to_tensor (tok.rs).  All HBM-bound copies and scalings; DropPath's mask is
+// drawn on the device from Rng::new(seed) (rng.rs, splitmix64-seeded
+// xoshiro256++, 24-bit uniforms), so the step needs no host round trip and
+// draws the reference's mask bit for bit.
+#include "rnn_internal.h"
+
+#include <algorithm>
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int NT = 256;
+
+unsigned ew_grid(size_t len) {
+    return (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(len, NT), 16384));
+}
+
+// rng.rs on the device (Rng::new, next_u64, uniform).
+struct DevRng {
+    uint64_t s[4];
+    __device__ explicit DevRng(uint64_t seed) {
+        uint64_t z = seed + 0x9E3779B97F4A7C15ull;
+        for (int i = 0; i < 4; i++) {
+            z += 0x9E3779B97F4A7C15ull;
+            uint64_t x = z;
+            x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+            x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+            s[i] = x ^ (x >> 31);
+        }
+    }
+    __device__ static uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+    __device__ uint64_t next() {
+        const uint64_t r = rotl(s[0] + s[3], 23) + s[0];
+        const uint64_t t = s[1] << 17;
+        s[2] ^= s[0];
+        s[3] ^= s[1];
+        s[1] ^= s[2];
+        s[0] ^= s[3];
+        s[2] ^= t;
+        s[3] = rotl(s[3], 45);
+        return r;
+    }
+    __device__ float uniform() { return (float)(next() >> 40) * (1.0f / 16777216.0f); }
+};
+
+// DropPath::forward (vit.rs:39-59): image i keeps its branch with the i-th
+// uniform of Rng::new(seed) below 1 - p, scaled by 1 / keep, else 0.  Block
+// (i, chunk): thread 0 draws the i-th uniform (i + 1 steps of the generator),
+// chunk 0 records the mask; rows whose factor is not 1 are scaled.
+__global__ __launch_bounds__(NT) void drop_path_fwd_kernel(size_t per, float p, uint64_t seed,
+                                                           float *x, float *__restrict__ mask) {
+    __shared__ float sfac;
+    const size_t img = blockIdx.y;
+    if (threadIdx.x == 0) {
+        DevRng rng(seed);
+        float u = 0.0f;
+        for (size_t k = 0; k <= img; k++) u = rng.uniform();
+        const float keep = 1.0f - p;
+        const float f = u < keep ? 1.0f / keep : 0.0f;
+        sfac = f;
+        if (blockIdx.x == 0) mask[img] = f;
+    }
+    __syncthreads();
+    const float f = sfac;
+    if (f == 1.0f) return;
+    float *r = x + img * per;
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < per; i += (size_t)gridDim.x * NT)
+        r[i] *= f;
+}
+
+// DropPath::backward (vit.rs:61-73): dy rows times the kept mask.
+__global__ __launch_bounds__(NT) void drop_path_bwd_kernel(size_t per, float *dy,
+                                                           const float *__restrict__ mask) {
+    const size_t img = blockIdx.y;
+    const float f = mask[img];
+    if (f == 1.0f) return;
+    float *r = dy + img * per;
+    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < per; i += (size_t)gridDim.x * NT)
+        r[i] *= f;
+}
+
+// y[r][j] += l[j] x[r][j] (vit.rs:153-158: a += gamma * dw).
+__global__ void axpy_cols_kernel(size_t len, int c, float *y, const float *__restrict__ l,
+                                 const float *__restrict__ x) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x)
+        y[i] += l[i % c] * x[i];
+}
+
+// token_merge (vit.rs:612-630): y[n][t2*t2][4c] with the four neighbours
+// (0,0), (0,1), (1,0), (1,1) of each 2x2 cell concatenated; back = the
+// inverse copy.  One thread per element of y.
+__global__ void token_merge_kernel(size_t n, int th, int c, const float *__restrict__ z,
+                                   float *__restrict__ y, int back) {
+    const int t2 = th / 2;
+    const size_t len = n * (size_t)t2 * t2 * 4 * c;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < len;
+         e += (size_t)gridDim.x * blockDim.x) {
+        const int j = (int)(e % c);
+        const size_t r = e / c;
+        const int qd = (int)(r % 4);
+        const size_t cell = r / 4;
+        const int ox = (int)(cell % t2), oy = (int)((cell / t2) % t2);
+        const size_t img = cell / ((size_t)t2 * t2);
+        const int sy = 2 * oy + (qd >> 1), sx = 2 * ox + (qd & 1);
+        const size_t s = (img * th * th + (size_t)sy * th + sx) * c + j;
+        if (back)
+            const_cast<float *>(z)[s] = y[e];
+        else
+            y[e] = z[s];
+    }
+}
+
+// TaxoHead (vit.rs:282-293): zf[i][j] += zc[i][parent[j]].
+__global__ void taxo_fwd_kernel(size_t n, int nf, int nc, const uint32_t *__restrict__ parent,
+                                float *zf, const float *__restrict__ zc) {
+    const size_t len = n * nf;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < len;
+         e += (size_t)gridDim.x * blockDim.x) {
+        const size_t i = e / nf;
+        const int j = (int)(e - i * nf);
+        const uint32_t pj = parent[j];
+        zf[e] += pj < (uint32_t)nc ? zc[i * nc + pj] : NAN;
+    }
+}
+
+// TaxoHead::backward's coarse gradient (vit.rs:296-306): dc = dzc, then
+// dc[parent[j]] += dzf[j] for j in order; one thread per row.
+__global__ void taxo_bwd_kernel(size_t n, int nf, int nc, const uint32_t *__restrict__ parent,
+                                const float *__restrict__ dzf, const float *__restrict__ dzc,
+                                float *__restrict__ dc) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float *cr = dc + i * nc;
+    for (int k = 0; k < nc; k++) cr[k] = dzc[i * nc + k];
+    for (int j = 0; j < nf; j++) {
+        const uint32_t pj = parent[j];
+        if (pj < (uint32_t)nc) cr[pj] += dzf[i * nf + j];
+    }
+}
+
+// [n][c][hw] <-> [n][hw][c] (Tok::from_tensor / to_tensor): 32 x 32 tiles
+// through LDS so both sides are read and written along rows.
+__global__ __launch_bounds__(NT) void nchw_tok_kernel(int c, int hw, const float *__restrict__ src,
+                                                      float *__restrict__ dst, int to_tok) {
+    __shared__ float tile[32][33];
+    const size_t img = blockIdx.z;
+    const int rows = to_tok ? c : hw, cols = to_tok ? hw : c;  // src is [rows][cols]
+    const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+    const float *s = src + img * (size_t)c * hw;
+    float *d = dst + img * (size_t)c * hw;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int k = ty; k < 32; k += 8) {
+        const int r = r0 + k, cc = c0 + tx;
+        if (r < rows && cc < cols) tile[k][tx] = s[(size_t)r * cols + cc];
+    }
+    __syncthreads();
+    for (int k = ty; k < 32; k += 8) {
+        const int cc = c0 + k, r = r0 + tx;  // dst is [cols][rows]
+        if (cc < cols && r < rows) d[(size_t)cc * rows + r] = tile[tx][k];
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int rnn_drop_path_forward(rnn_ctx *ctx, size_t n, size_t per, float *x, float p, uint64_t seed,
+                          float *mask) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0) return RNN_OK;
+    if (!x || !mask) return rnn_fail(ctx, RNN_E_NULL, "drop_path: null operand");
+    if (!(p > 0.0f) || !(p < 1.0f) || n > 65535)
+        return rnn_fail(ctx, RNN_E_INVALID, "drop_path: p %g (0 < p < 1), n %zu (<= 65535)",
+                        (double)p, n);
+    const unsigned gx = (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(per, NT), 64));
+    drop_path_fwd_kernel<<<dim3(gx, (unsigned)n), NT, 0, ctx->stream>>>(per, p, seed, x, mask);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_drop_path_backward(rnn_ctx *ctx, size_t n, size_t per, float *dy, const float *mask) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0) return RNN_OK;
+    if (!dy || !mask) return rnn_fail(ctx, RNN_E_NULL, "drop_path_backward: null operand");
+    if (n > 65535) return rnn_fail(ctx, RNN_E_INVALID, "drop_path: n %zu (<= 65535)", n);
+    const unsigned gx = (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(per, NT), 64));
+    drop_path_bwd_kernel<<<dim3(gx, (unsigned)n), NT, 0, ctx->stream>>>(per, dy, mask);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_axpy_cols(rnn_ctx *ctx, size_t rows, size_t c, float *y, const float *l, const float *x) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!y || !l || !x) return rnn_fail(ctx, RNN_E_NULL, "axpy_cols: null operand");
+    if (c > 0x7fffffff) return rnn_fail(ctx, RNN_E_INVALID, "axpy_cols: c %zu", c);
+    axpy_cols_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, (int)c, y, l, x);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_token_merge(rnn_ctx *ctx, size_t n, size_t th, size_t c, const float *z, float *y) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || c == 0) return RNN_OK;
+    if (!z || !y) return rnn_fail(ctx, RNN_E_NULL, "token_merge: null operand");
+    if (th < 2 || th % 2 || th > 65536 || c > (1u << 24))
+        return rnn_fail(ctx, RNN_E_INVALID, "token_merge: th %zu (even), c %zu", th, c);
+    const size_t len = n * th * th * c;
+    token_merge_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)c, z, y, 0);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_token_merge_backward(rnn_ctx *ctx, size_t n, size_t th, size_t c, const float *dy,
+                             float *dz) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || c == 0) return RNN_OK;
+    if (!dy || !dz) return rnn_fail(ctx, RNN_E_NULL, "token_merge_backward: null operand");
+    if (th < 2 || th % 2 || th > 65536 || c > (1u << 24))
+        return rnn_fail(ctx, RNN_E_INVALID, "token_merge: th %zu (even), c %zu", th, c);
+    const size_t len = n * th * th * c;
+    token_merge_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)c, dz,
+                                                              const_cast<float *>(dy), 1);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_taxo_head_combine(rnn_ctx *ctx, size_t n, size_t nf, size_t nc, const uint32_t *parent,
+                          float *zf, const float *zc) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || nf == 0) return RNN_OK;
+    if (!parent || !zf || !zc) return rnn_fail(ctx, RNN_E_NULL, "taxo_head: null operand");
+    if (nf > (1u << 24) || nc > (1u << 24))
+        return rnn_fail(ctx, RNN_E_INVALID, "taxo_head: nf %zu nc %zu", nf, nc);
+    taxo_fwd_kernel<<<ew_grid(n * nf), NT, 0, ctx->stream>>>(n, (int)nf, (int)nc, parent, zf, zc);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_taxo_head_combine_backward(rnn_ctx *ctx, size_t n, size_t nf, size_t nc,
+                                   const uint32_t *parent, const float *dzf, const float *dzc,
+                                   float *dc) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || nc == 0) return RNN_OK;
+    if (!parent || !dzf || !dzc || !dc)
+        return rnn_fail(ctx, RNN_E_NULL, "taxo_head_backward: null operand");
+    if (nf > (1u << 24) || nc > (1u << 24))
+        return rnn_fail(ctx, RNN_E_INVALID, "taxo_head: nf %zu nc %zu", nf, nc);
+    taxo_bwd_kernel<<<(unsigned)rnn_div_up(n, (size_t)NT), NT, 0, ctx->stream>>>(
+        n, (int)nf, (int)nc, parent, dzf, dzc, dc);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_nchw_to_tokens(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, float *t) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || c == 0 || hw == 0) return RNN_OK;
+    if (!x || !t) return rnn_fail(ctx, RNN_E_NULL, "nchw_to_tokens: null operand");
+    if (n > 65535 || c > (1u << 24) || hw > (1u << 24))
+        return rnn_fail(ctx, RNN_E_INVALID, "nchw_to_tokens: %zu x %zu x %zu", n, c, hw);
+    const dim3 grid((unsigned)rnn_div_up(hw, (size_t)32), (unsigned)rnn_div_up(c, (size_t)32),
+                    (unsigned)n);
+    nchw_tok_kernel<<<grid, NT, 0, ctx->stream>>>((int)c, (int)hw, x, t, 1);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_tokens_to_nchw(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *t, float *x) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || c == 0 || hw == 0) return RNN_OK;
+    if (!x || !t) return rnn_fail(ctx, RNN_E_NULL, "tokens_to_nchw: null operand");
+    if (n > 65535 || c > (1u << 24) || hw > (1u << 24))
+        return rnn_fail(ctx, RNN_E_INVALID, "tokens_to_nchw: %zu x %zu x %zu", n, c, hw);
+    const dim3 grid((unsigned)rnn_div_up(c, (size_t)32), (unsigned)rnn_div_up(hw, (size_t)32),
+                    (unsigned)n);
+    nchw_tok_kernel<<<grid, NT, 0, ctx->stream>>>((int)c, (int)hw, t, x, 0);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,247 @@
+"""GPU parity: the vit.rs pieces on the device (rustnn_amd/vit.py over
+vit.hip, norm.hip, attn.hip and the GEMM core).
+
+* DropPath (mask from Rng::new(seed) drawn on the device), the token merge,
+  TaxoHead's combine and the NCHW <-> token layout: bit-exact against the
+  oracle;
+* the whole pre-LN Block (self-attention, depthwise gate, cross-attention
+  reader, SwiGLU, LayerScales) forward and every gradient -- x, the memory
+  and all parameters -- against an independent torch-CPU float64 statement
+  of vit.rs:138-250 at the same weights: relative 1e-5 (TOL);
+* the reference's block dircheck (check.rs:360-395: dx and dparams of a
+  reader block, eps 3e-4, tolerance 5e-3) with DropPath on, whose seeded
+  mask keeps the finite difference valid."""
+import numpy as np
+import pytest
+
+from conftest import TOL, rel_frob, to_dev, to_host
+
+import refcheck
+
+pytestmark = pytest.mark.gpu
+
+
+def _i32(a):
+    return to_dev(np.asarray(a, np.uint32).view(np.int32))
+
+
+def test_drop_path(rnn, orc):
+    import torch
+    from rustnn_amd.vit import DropPath
+    n, per = 256, 64 * 384
+    x = np.random.default_rng(0).standard_normal(n * per).astype(np.float32)
+    X = to_dev(x).reshape(n, 64, 384)
+    dp = DropPath(0.1)
+    seed = 0x1234 ^ 7 ^ 0x5151
+    dp.forward(X, True, seed)
+    want, mask = orc.drop_path(x, n, 0.1, seed)
+    assert np.array_equal(to_host(dp.mask), mask)
+    assert np.array_equal(to_host(X).ravel(), want)
+    dy = to_dev(x).reshape(n, 64, 384)
+    dp.backward(dy)
+    assert np.array_equal(to_host(dy).ravel(), want)
+    assert dp.forward(X, False, seed) is X and dp.mask is None  # eval: identity
+
+
+def test_token_merge_and_layout(rnn, orc):
+    from rustnn_amd.vit import nchw_to_tokens, token_merge, token_merge_back, tokens_to_nchw
+    n, th, c = 16, 8, 256
+    z = np.random.default_rng(1).standard_normal(n * th * th * c).astype(np.float32)
+    y = token_merge(to_dev(z).reshape(n, th * th, c), th)
+    assert np.array_equal(to_host(y).ravel(), orc.token_merge(z, n, th, c))
+    back = token_merge_back(y, th, c)
+    assert np.array_equal(to_host(back).ravel(), z)
+    x = np.random.default_rng(2).standard_normal((n, 96, 16, 16)).astype(np.float32)
+    t = nchw_to_tokens(to_dev(x).reshape(x.shape))
+    assert np.array_equal(to_host(t), x.reshape(n, 96, 256).transpose(0, 2, 1))
+    assert np.array_equal(to_host(tokens_to_nchw(t, 16, 16)), x)
+
+
+def test_taxo_head_combine(rnn, orc):
+    from rustnn_amd import default_ctx, lib, _ptr
+    rng = np.random.default_rng(3)
+    n, nf, nc = 256, 100, 20
+    parent = rng.permutation(np.arange(nf) // 5).astype(np.uint32)
+    zf = rng.standard_normal((n, nf)).astype(np.float32)
+    zc = rng.standard_normal((n, nc)).astype(np.float32)
+    ctx = default_ctx()
+    # every device buffer bound to a name for the whole call: a temporary
+    # would go back to the allocator before the kernel reads it
+    ZF, ZC, P = to_dev(zf), to_dev(zc), _i32(parent)
+    ctx.check(lib().rnn_taxo_head_combine(ctx.h, n, nf, nc, _ptr(P, nf, "p"), _ptr(ZF, n * nf, "zf"),
+                                          _ptr(ZC, n * nc, "zc")))
+    assert np.array_equal(to_host(ZF).reshape(n, nf), orc.taxo_combine(zf, zc, parent))
+    dzf = rng.standard_normal((n, nf)).astype(np.float32)
+    dzc = rng.standard_normal((n, nc)).astype(np.float32)
+    DC = to_dev(np.zeros(n * nc, np.float32))
+    DZF, DZC = to_dev(dzf), to_dev(dzc)
+    ctx.check(lib().rnn_taxo_head_combine_backward(ctx.h, n, nf, nc, _ptr(P, nf, "p"),
+                                                   _ptr(DZF, n * nf, "dzf"),
+                                                   _ptr(DZC, n * nc, "dzc"),
+                                                   _ptr(DC, n * nc, "dc")))
+    assert np.array_equal(to_host(DC).reshape(n, nc), orc.taxo_combine_backward(dzf, dzc, parent))
+
+
+# ------------------------------------------------------------------ Block
+def _params_of(obj):
+    ps = []
+    obj.for_each_param(lambda p: ps.append(p))
+    return ps
+
+
+def _torch_block(x, mem, W, c, h, th, mh, torch):
+    """vit.rs:138-172 in float64 (DropPath off): h = LN(x); x += l1 (SA(h) +
+    g DW(h)); x += lm CA(h, mem); x += l2 SwiGLU(LN(x))."""
+    F = torch.nn.functional
+    dh = c // h
+    n, t = x.shape[0], th * th
+
+    def ln(v, g, b):
+        return F.layer_norm(v, (c,), g, b, 1e-5)
+
+    def core(q, k, v, tau, rel, relidx, nrel, mask):
+        # q [n, tq, h, dh], k/v [n, tk, h, dh]
+        s = torch.einsum("nqhd,nkhd->nhqk", q, k)
+        bias = rel.view(h, nrel)[:, relidx]  # [h, tq, tk]
+        xx = tau.view(1, h, 1, 1) * s + bias.unsqueeze(0)
+        if mask:
+            eye = torch.eye(s.shape[-1], dtype=torch.bool)
+            xx = xx.masked_fill(eye, float("-inf"))
+        p = torch.softmax(xx, -1)
+        return torch.einsum("nhqk,nkhd->nqhd", p, v).reshape(n, -1, c)
+
+    hh = ln(x, W["n1.g"], W["n1.b"])
+    ab = hh @ W["qkv.w"].T + W["qkv.b"]
+    q, k, v = ab[..., :c], ab[..., c:2 * c], ab[..., 2 * c:]
+    sa = core(q.reshape(n, t, h, dh), k.reshape(n, t, h, dh), v.reshape(n, t, h, dh),
+              W["tau"], W["rel"], W["relidx"], W["nrel"], True)
+    sa = sa @ W["proj.w"].T + W["proj.b"]
+    hi = hh.reshape(n, th, th, c).permute(0, 3, 1, 2)
+    wdw = W["dw.w"].view(3, 3, c).permute(2, 0, 1).reshape(c, 1, 3, 3)
+    dw = F.conv2d(hi, wdw, W["dw.b"], padding=1, groups=c).permute(0, 2, 3, 1).reshape(n, t, c)
+    a = sa + W["gamma"] * dw
+    y = x + W["ls1"] * a
+    cq = hh @ W["wq.w"].T + W["wq.b"]
+    tk = mh * mh
+    ca = core(cq.reshape(n, t, h, dh), mem[..., :c].reshape(n, tk, h, dh),
+              mem[..., c:].reshape(n, tk, h, dh), W["ctau"], W["crel"], W["crelidx"],
+              W["cnrel"], False)
+    ca = ca @ W["cproj.w"].T + W["cproj.b"]
+    y = y + W["lsm"] * ca
+    h2 = ln(y, W["n2.g"], W["n2.b"])
+    g2 = h2 @ W["wg.w"].T + W["wg.b"]
+    hid = g2.shape[-1] // 2
+    u = F.silu(g2[..., :hid]) * g2[..., hid:]
+    m = u @ W["wd.w"].T + W["wd.b"]
+    return y + W["ls2"] * m
+
+
+@pytest.mark.parametrize("mh", [6, 9])  # memory of 36 tokens (register path), 81 (composed)
+def test_block_matches_torch_f64(rnn, orc, mh):
+    import torch
+    from rustnn_amd.vit import Block
+    n, c, h, th, depth = 3, 32, 2, 4, 7
+    t, tk = th * th, mh * mh
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    blk = Block(c, h, th, th, (mh, mh), depth, 0.0, 2, 1e-4, gen)
+    # non-trivial values for the parameters that start at constants
+    r = np.random.default_rng(mh)
+    for p in _params_of(blk):
+        if p.rows == 0:
+            p.v.copy_(to_dev((1.0 + 0.3 * r.standard_normal(p.v.numel())).astype(np.float32)))
+    x = r.standard_normal((n, t, c)).astype(np.float32)
+    mem = r.standard_normal((n, tk, 2 * c)).astype(np.float32)
+    dz = r.standard_normal((n, t, c)).astype(np.float32)
+    X, MEM = to_dev(x).reshape(n, t, c), to_dev(mem).reshape(n, tk, 2 * c)
+    y = blk.forward(X, MEM, True, 99)
+    dmem = torch.zeros(n * tk * 2 * c, device="cuda")
+    dx = blk.backward(to_dev(dz).reshape(n, t, c), MEM, dmem)
+
+    T = lambda a, g=True: torch.tensor(np.asarray(a, np.float64), requires_grad=g)
+    H = lambda tt: to_host(tt).astype(np.float64)
+    relidx, nrel = rnn.rel_index(th, th, th, th)
+    crelidx, cnrel = rnn.rel_index(th, th, mh, mh)
+    W = {"n1.g": T(H(blk.n1.g.v)), "n1.b": T(H(blk.n1.b.v)),
+         "qkv.w": T(H(blk.attn.qkv.w).reshape(3 * c, c)), "qkv.b": T(H(blk.attn.qkv.b)),
+         "proj.w": T(H(blk.attn.proj.w).reshape(c, c)), "proj.b": T(H(blk.attn.proj.b)),
+         "tau": T(H(blk.attn.tau.v)), "rel": T(H(blk.attn.rel.v)),
+         "relidx": torch.tensor(relidx.astype(np.int64).reshape(t, t)), "nrel": nrel,
+         "dw.w": T(H(blk.dw.w.v)), "dw.b": T(H(blk.dw.b.v)), "gamma": T(H(blk.gamma.v)),
+         "ls1": T(H(blk.ls1.l.v)),
+         "wq.w": T(H(blk.cross.wq.w).reshape(c, c)), "wq.b": T(H(blk.cross.wq.b)),
+         "cproj.w": T(H(blk.cross.proj.w).reshape(c, c)), "cproj.b": T(H(blk.cross.proj.b)),
+         "ctau": T(H(blk.cross.tau.v)), "crel": T(H(blk.cross.rel.v)),
+         "crelidx": torch.tensor(crelidx.astype(np.int64).reshape(t, tk)), "cnrel": cnrel,
+         "lsm": T(H(blk.lsm.l.v)), "n2.g": T(H(blk.n2.g.v)), "n2.b": T(H(blk.n2.b.v)),
+         "wg.w": T(H(blk.mlp.wg.w).reshape(-1, c)), "wg.b": T(H(blk.mlp.wg.b)),
+         "wd.w": T(H(blk.mlp.wd.w).reshape(c, -1)), "wd.b": T(H(blk.mlp.wd.b)),
+         "ls2": T(H(blk.ls2.l.v))}
+    xt, mt = T(x), T(mem)
+    yt = _torch_block(xt, mt, W, c, h, th, mh, torch)
+    assert rel_frob(to_host(y), yt.detach().numpy()) < TOL
+    yt.backward(torch.tensor(dz, dtype=torch.float64))
+    assert rel_frob(to_host(dx), xt.grad.numpy()) < TOL, "dx"
+    assert rel_frob(to_host(dmem), mt.grad.numpy().ravel()) < TOL, "dmem"
+    grads = {"n1.g": blk.n1.g.g, "n1.b": blk.n1.b.g, "qkv.w": blk.attn.qkv.gw,
+             "qkv.b": blk.attn.qkv.gb, "proj.w": blk.attn.proj.gw, "proj.b": blk.attn.proj.gb,
+             "tau": blk.attn.tau.g, "rel": blk.attn.rel.g, "dw.w": blk.dw.w.g,
+             "dw.b": blk.dw.b.g, "gamma": blk.gamma.g, "ls1": blk.ls1.l.g,
+             "wq.w": blk.cross.wq.gw, "wq.b": blk.cross.wq.gb, "cproj.w": blk.cross.proj.gw,
+             "cproj.b": blk.cross.proj.gb, "ctau": blk.cross.tau.g, "crel": blk.cross.rel.g,
+             "lsm": blk.lsm.l.g, "n2.g": blk.n2.g.g, "n2.b": blk.n2.b.g,
+             "wg.w": blk.mlp.wg.gw, "wg.b": blk.mlp.wg.gb, "wd.w": blk.mlp.wd.gw,
+             "wd.b": blk.mlp.wd.gb, "ls2": blk.ls2.l.g}
+    # dtau is one number per head: a sum of n*tq*tk products dS*S whose
+    # terms cancel to about 1% of their magnitude, so its f32 sums carry a
+    # larger relative error than the other gradients
+    tol = {"tau": 2e-4, "ctau": 2e-4}
+    for k, g in grads.items():
+        want = W[k].grad.numpy().ravel()
+        err = rel_frob(to_host(g).ravel(), want)
+        assert err < tol.get(k, TOL), (k, err)
+
+
+def test_reference_block_dircheck(rnn, orc):
+    """check.rs:360-395 shape class: a reader block with DropPath on, dx and
+    all parameters by dircheck (seed-stable masks)."""
+    import torch
+    from rustnn_amd.vit import Block
+    n, c, h, th, mh = 3, 8, 2, 3, 6
+    t, tk = th * th, mh * mh
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    blk = Block(c, h, th, th, (mh, mh), 4, 0.3, 1, 0.5, gen)
+    rng = orc.Rng(0x1234 ^ 9)
+    eps = refcheck.gc_eps()
+    x = rng.rand_vec(n * t * c)
+    mem = rng.rand_vec(n * tk * 2 * c)
+    r = rng.rand_vec(n * t * c)
+    MEM = to_dev(mem).reshape(n, tk, 2 * c)
+    seed = 77
+
+    def loss(v):
+        y = blk.forward(to_dev(v).reshape(n, t, c), MEM, True, seed)
+        return refcheck.dot32(to_host(y), r)
+
+    blk.forward(to_dev(x).reshape(n, t, c), MEM, True, seed)
+    dmem = torch.zeros(n * tk * 2 * c, device="cuda")
+    dx = blk.backward(to_dev(r).reshape(n, t, c), MEM, dmem)
+    e = refcheck.dircheck(x, to_host(dx).ravel(), eps, rng, loss)
+    assert e < refcheck.TOL, ("block dx", e)
+    ps = _params_of(blk)
+    for p in ps:
+        p.g.zero_()
+    blk.forward(to_dev(x).reshape(n, t, c), MEM, True, seed)
+    blk.backward(to_dev(r).reshape(n, t, c), MEM, torch.zeros_like(dmem))
+    base = np.concatenate([to_host(p.v).ravel() for p in ps])
+    grad = np.concatenate([to_host(p.g).ravel() for p in ps])
+    sizes = np.cumsum([p.v.numel() for p in ps])[:-1]
+
+    def lossp(v):
+        for p, part in zip(ps, np.split(v, sizes)):
+            p.v.copy_(to_dev(part))
+        return loss(x)
+
+    e = refcheck.dircheck(base, grad, eps, rng, lossp)
+    for p, part in zip(ps, np.split(base, sizes)):
+        p.v.copy_(to_dev(part))
+    assert e < refcheck.TOL, ("block dparams", e)
