@@ -424,6 +424,53 @@ def cpu_rustvit_optim(specs, budget_s):
                       f"over {threads} threads, the rest on one"}
 
 
+def bench_rustvit_step(R, ctx, steps, warmup, batch=128):
+    """the rustvit default train step at batch 128 --
+    forward, soft targets with the taxonomy (5 fine classes per superclass,
+    fixed seeded assignment), the multi-head loss, backward, clip, Muon /
+    AdamW and the EMA (train.rs:340-380).  Inputs uniform [0, 1] normalised,
+    labels uniform over 100 classes; all on the device.  Timed eagerly (the
+    Python layer issues every launch)."""
+    import numpy as np
+    import torch
+    from rustnn_amd.vit import RustViT, ViTStep
+    g = torch.Generator(device="cuda").manual_seed(2026)
+    parent_np = np.random.default_rng(7).permutation(np.arange(100) // 5).astype(np.int32)
+    parent = torch.from_numpy(parent_np).cuda()
+    net = RustViT(None, parent, 20, seed=7, ctx=ctx)
+    step = ViTStep(net, parent, 20)
+    u = torch.rand(batch, 3, 32, 32, device="cuda", generator=g)
+    mean = torch.tensor(CIFAR_MEAN, device="cuda").view(1, 3, 1, 1)
+    std = torch.tensor(CIFAR_STD, device="cuda").view(1, 3, 1, 1)
+    x = ((u - mean) / std).contiguous()
+    labels = torch.randint(0, 100, (batch,), device="cuda", generator=g, dtype=torch.int32)
+    coarse = parent[labels.long()].contiguous()
+    for i in range(warmup):
+        net.drop_seed = 1000 + i
+        step(x, labels, coarse)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        net.drop_seed = 2000 + i  # a fresh DropPath draw per step, as the trainer's rng gives
+        loss, _ = step(x, labels, coarse)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    cfg = net.cfg
+    return {"workload": "config4 rustvit default (width 32, cmid 96, d256 x 5 with memory readers "
+                        "at 1,3, d384 x 2) train step at batch %d: forward + taxonomy targets + "
+                        "multi-head loss + backward + clip + Muon/AdamW + EMA" % batch,
+            "batch": batch, "ms_per_step": round(ms, 3), "images_s": round(batch / (ms * 1e-3), 1),
+            "wall_ms_per_step": round(wall / steps * 1e3, 3), "loss": float(loss.item()),
+            "params": sum(p.v.numel() for p in step.params),
+            "reference_published": "102.6 img/s at batch 256 on a Core Ultra 265U CPU "
+                                   "(README.md:426, BASELINE.md)",
+            "timing": "eager, HIP events around the steps; drop_seed changes per step"}
+
+
 RESNET = dict(depth_n=3, width=32, nclass=100, batch=128, hw=32, smooth=0.1, lr=0.2, mom=0.9,
               wd=5e-4, seed=7)
 # Each conv op of the ResNet-20 step with its multiplicity (config-1 sweep
@@ -538,6 +585,8 @@ def main():
     ap.add_argument("--attn-only", type=int, default=0, metavar="REPS",
                     help="config 2 only: the attention forward / backward timing with REPS calls "
                          "per graph (the workload of the rocprofv3 kernel trace of attention)")
+    ap.add_argument("--vit-only", type=int, default=0, metavar="STEPS",
+                    help="only the config-4 rustvit train step, STEPS timed steps")
     ap.add_argument("--optim-only", type=int, default=0, metavar="REPS",
                     help="only the rustvit optimiser phase, REPS phases per graph")
     args = ap.parse_args()
@@ -558,6 +607,9 @@ def main():
         return
     if args.attn_only:
         print(json.dumps({"attn_only": bench_attention(R, ctx, args.attn_only)}))
+        return
+    if args.vit_only:
+        print(json.dumps({"vit_only": bench_rustvit_step(R, ctx, args.vit_only, 2)}))
         return
     if args.optim_only:
         print(json.dumps({"optim_only": bench_rustvit_optim(R, ctx, args.optim_only,
@@ -674,6 +726,7 @@ def main():
     attention = bench_attention(R, ctx, args.op_reps)
     gemms = bench_gemm(R, ctx, args.op_reps)
     vit_optim = bench_rustvit_optim(R, ctx, 5, 0 if args.no_cpu else args.cpu_budget / 4)
+    vit_step = bench_rustvit_step(R, ctx, 5, 2)
 
     cpu = sweep_cpu = None
     if not args.no_cpu:
@@ -709,6 +762,7 @@ def main():
             "flop_per_step": sweep_flops, "roofline": sweep_roof, "cpu_baseline": sweep_cpu,
             "per_op": per_op},
         "config2_attention": attention, "gemmbench": gemms, "rustvit_optimizer": vit_optim,
+        "config4_rustvit_step": vit_step,
     }
     print(json.dumps(out))
 

@@ -717,21 +717,43 @@ __global__ __launch_bounds__(256) void attn_head_sum_kernel(const float *__restr
     if (threadIdx.x == 0) dtau[hd] += (red[0] + red[1]) + (red[2] + red[3]);
 }
 
-// drel[hd*nrel + slot] += sum over images and the positions of the slot (the
-// inverse index, ascending) of dS.  One thread per (head, slot).
-__global__ __launch_bounds__(256) void attn_drel_gather_kernel(
+// drel partials: part[chunk][hd*nrel + slot] = sum over the images of the
+// chunk (in order) and the positions of the slot (the inverse index,
+// ascending) of dS.  One thread per (chunk, head, slot); 8 loads ahead.
+__global__ __launch_bounds__(256) void attn_drel_part_kernel(
     const float *__restrict__ ds, const uint32_t *__restrict__ rowptr,
-    const uint32_t *__restrict__ pos, long long n, int h, int nrel, long long cnt,
-    float *drel) {
+    const uint32_t *__restrict__ pos, long long n, long long ipc, int h, int nrel,
+    long long cnt, float *__restrict__ part) {
     const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (e >= (long long)h * nrel) return;
+    const long long per = (long long)h * nrel;
+    if (e >= per) return;
     const int hd = (int)(e / nrel), slot = (int)(e - (long long)hd * nrel);
     const uint32_t p0 = rowptr[slot], p1 = rowptr[slot + 1];
+    const long long i0 = (long long)blockIdx.y * ipc, i1 = min(n, i0 + ipc);
     float s = 0.f;
-    for (long long img = 0; img < n; img++) {
+    for (long long img = i0; img < i1; img++) {
         const float *base = ds + (img * h + hd) * cnt;
-        for (uint32_t i = p0; i < p1; i++) s += base[pos[i]];
+        uint32_t i = p0;
+        for (; i + 8 <= p1; i += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = base[pos[i + u]];
+#pragma unroll
+            for (int u = 0; u < 8; u++) s += v[u];
+        }
+        for (; i < p1; i++) s += base[pos[i]];
     }
+    part[(long long)blockIdx.y * per + e] = s;
+}
+
+// drel[e] += sum over chunks of part[chunk][e], in chunk order.
+__global__ __launch_bounds__(256) void attn_drel_sum_kernel(const float *__restrict__ part,
+                                                            int nchunk, long long per,
+                                                            float *drel) {
+    const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= per) return;
+    float s = 0.f;
+    for (int k = 0; k < nchunk; k++) s += part[(long long)k * per + e];
     drel[e] += s;
 }
 
@@ -787,11 +809,15 @@ int attn_backward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const fl
     const size_t tq = d->tq, tk = d->tk, dh = d->dh, h = d->h, c = h * dh;
     const size_t cnt = tq * tk, mat = n * h * cnt;
     const long long rows = (long long)n * h * tq;
+    const size_t per = h * d->nrel;
+    const size_t ipc = rnn_div_up(n, (size_t)16), nchunk = rnn_div_up(n, ipc);
     WsCarve cv;
     const size_t o1 = cv.take(mat * 4), o2 = cv.take(mat * 4), o3 = cv.take((size_t)rows * 4);
+    const size_t o4 = cv.take(nchunk * per * 4);
     char *ws = (char *)rnn_workspace(ctx, cv.off);
     if (!ws) return RNN_E_NOMEM;
     float *s1 = (float *)(ws + o1), *s2 = (float *)(ws + o2), *part = (float *)(ws + o3);
+    float *rpart = (float *)(ws + o4);
     for (size_t hd = 0; hd < h; hd++) {
         // dV += P^T dO (attn.rs:262-270)
         int rc = rnn_gemm_launch_ld(ctx, n, tk, dh, tq, p + hd * cnt, tk, h * cnt, 1,
@@ -815,11 +841,14 @@ int attn_backward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const fl
     attn_head_sum_kernel<<<(unsigned)h, 256, 0, ctx->stream>>>(part, (long long)n, (int)h,
                                                               (int)tq, dtau);
     RNN_LAUNCHED(ctx);
-    attn_drel_gather_kernel<<<(unsigned)rnn_div_up(h * d->nrel, (size_t)256), 256, 0,
-                              ctx->stream>>>(s1, ctx->rel_dev + cnt, ctx->rel_dev + cnt +
-                                                                         d->nrel + 1,
-                                             (long long)n, (int)h, (int)d->nrel,
-                                             (long long)cnt, drel);
+    attn_drel_part_kernel<<<dim3((unsigned)rnn_div_up(per, (size_t)256), (unsigned)nchunk), 256,
+                            0, ctx->stream>>>(s1, ctx->rel_dev + cnt,
+                                              ctx->rel_dev + cnt + d->nrel + 1, (long long)n,
+                                              (long long)ipc, (int)h, (int)d->nrel,
+                                              (long long)cnt, rpart);
+    RNN_LAUNCHED(ctx);
+    attn_drel_sum_kernel<<<(unsigned)rnn_div_up(per, (size_t)256), 256, 0, ctx->stream>>>(
+        rpart, (int)nchunk, (long long)per, drel);
     RNN_LAUNCHED(ctx);
     for (size_t hd = 0; hd < h; hd++) {
         // dQ += (tau dS) K (attn.rs:317-322)

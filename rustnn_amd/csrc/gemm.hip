@@ -283,8 +283,17 @@ __global__ void colsum_partial_kernel(const float *x, long long rows, int cols, 
     long long rb = blockIdx.y;
     if (c >= cols) return;
     long long r0 = rb * rpb, r1 = min(rows, r0 + rpb);
+    // rows in order; 8 loads issued ahead of their adds
     float s = 0.f;
-    for (long long r = r0; r < r1; r++) s += x[r * cols + c];
+    long long r = r0;
+    for (; r + 8 <= r1; r += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = x[(r + i) * cols + c];
+#pragma unroll
+        for (int i = 0; i < 8; i++) s += v[i];
+    }
+    for (; r < r1; r++) s += x[r * cols + c];
     part[rb * cols + c] = s;
 }
 
@@ -421,7 +430,7 @@ static int fill(rnn_ctx *ctx, float *p, size_t len, float v) {
 
 int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, float *out) {
     // out[c] += sum_r x[r][c], two fixed-order stages.
-    size_t rpb = 256;
+    size_t rpb = 64;
     size_t nrb = rnn_div_up(rows, rpb);
     if (nrb > 65535) {
         rpb = rnn_div_up(rows, 65535);

@@ -7,12 +7,13 @@
 // targets (train.rs:121-155).  Each runs rayon over rows.
 //
 // The rows are few (a batch) and short (100 or 20 classes, or a 384-wide
-// feature), so every row is one thread running the reference's loops in
-// their order, with contraction off: the per-row arithmetic matches the
-// reference except for the device's expf / logf.  The per-row losses go to
-// the workspace and one thread adds them in row order (ce_soft and
-// kl_distill collect and sum in order; hint_mse's rayon sum has no fixed
-// order).  Scalars land in device memory, so nothing waits on the host.
+// feature): one wave per row, the elementwise arithmetic in the reference's
+// operation order with contraction off, the sums over classes lane-strided
+// then a shuffle tree (the reference sums them sequentially), expf / logf on
+// the device.  The per-row losses go to the workspace and one thread adds
+// them in row order (ce_soft and kl_distill collect and sum in order;
+// hint_mse's rayon sum has no fixed order).  Scalars land in device memory,
+// so nothing waits on the host.
 #include "rnn_internal.h"
 
 #include <algorithm>
@@ -24,93 +25,126 @@ namespace {
 
 constexpr int NT = 256;
 
-// ce_soft per row: dz overwritten with scale (softmax - t) / n; part[i] = the
-// row's loss, hit[i] = argmax == hard[i] (first maximum, as `v > mx`).
-__global__ void ce_soft_kernel(size_t n, int nc, const float *__restrict__ logits,
-                               const float *__restrict__ target, const uint32_t *__restrict__ hard,
-                               float scale, float *__restrict__ dz, float *__restrict__ part,
-                               uint32_t *__restrict__ hit) {
-    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+__device__ __forceinline__ float wsum(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wmax(float v) {
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// ce_soft per row, one wave per row: dz overwritten with scale (softmax - t)
+// / n; part[i] = the row's loss, hit[i] = argmax == hard[i] (the first
+// maximum, as `v > mx`: ties go to the lower class).  Sums over classes are
+// lane-strided, then a shuffle tree.
+__global__ __launch_bounds__(NT) void ce_soft_kernel(size_t n, int nc,
+                                                     const float *__restrict__ logits,
+                                                     const float *__restrict__ target,
+                                                     const uint32_t *__restrict__ hard,
+                                                     float scale, float *__restrict__ dz,
+                                                     float *__restrict__ part,
+                                                     uint32_t *__restrict__ hit) {
+    const size_t i = (size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (i >= n) return;
     const float *z = logits + i * nc, *t = target + i * nc;
     float *d = dz + i * nc;
     const float inv = 1.0f / (float)n;
     float mx = -INFINITY;
-    int arg = 0;
-    for (int j = 0; j < nc; j++)
+    int arg = nc;
+    for (int j = lane; j < nc; j += 64)
         if (z[j] > mx) {
             mx = z[j];
             arg = j;
         }
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float om = __shfl_xor(mx, o, 64);
+        const int oa = __shfl_xor(arg, o, 64);
+        if (om > mx || (om == mx && oa < arg)) {
+            mx = om;
+            arg = oa;
+        }
+    }
     float sum = 0.0f;
-    for (int j = 0; j < nc; j++) {
+    for (int j = lane; j < nc; j += 64) {
         const float e = expf(z[j] - mx);
         d[j] = e;
         sum += e;
     }
+    sum = wsum(sum);
     const float lse = mx + logf(sum);
     float l = 0.0f;
-    for (int j = 0; j < nc; j++) {
+    for (int j = lane; j < nc; j += 64) {
         l += t[j] * (lse - z[j]);
         d[j] = (d[j] / sum - t[j]) * inv * scale;
     }
-    part[i] = l;
-    if (hit) hit[i] = (uint32_t)arg == hard[i] ? 1u : 0u;
+    l = wsum(l);
+    if (lane == 0) {
+        part[i] = l;
+        if (hit) hit[i] = (uint32_t)arg == hard[i] ? 1u : 0u;
+    }
 }
 
-// Softmax of z / temp as kl_distill's `soft` closure (loss.rs:104-113): the
-// maximum, then the sum of exp((z - mx) / temp), then the inverse.
-__device__ __forceinline__ void soft_stats(const float *z, int nc, float it, float *mx,
-                                           float *is) {
-    float m = -INFINITY;
-    for (int j = 0; j < nc; j++) m = fmaxf(m, z[j]);
-    float s = 0.0f;
-    for (int j = 0; j < nc; j++) s += expf((z[j] - m) * it);
-    *mx = m;
-    *is = 1.0f / s;
-}
-
-// kl_distill per row (loss.rs:114-126): dz += temp (ps - pt) / n * scale;
-// part[i] = temp^2 KL(pt || ps).  ps / pt are recomputed per class from the
-// row's max and 1/sum, which gives the values the reference stores.
-__global__ void kl_distill_kernel(size_t n, int nc, const float *__restrict__ student,
-                                  const float *__restrict__ teacher, float temp, float scale,
-                                  float *__restrict__ dz, float *__restrict__ part) {
-    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+// kl_distill per row (loss.rs:114-126), one wave per row: dz += temp (ps -
+// pt) / n * scale; part[i] = temp^2 KL(pt || ps), ps / pt the softmaxes of
+// z / temp (max, sum of exp((z - max) / temp), times the inverse).
+__global__ __launch_bounds__(NT) void kl_distill_kernel(size_t n, int nc,
+                                                        const float *__restrict__ student,
+                                                        const float *__restrict__ teacher,
+                                                        float temp, float scale,
+                                                        float *__restrict__ dz,
+                                                        float *__restrict__ part) {
+    const size_t i = (size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (i >= n) return;
     const float *zs = student + i * nc, *zt = teacher + i * nc;
     float *d = dz + i * nc;
     const float inv = 1.0f / (float)n, it = 1.0f / temp;
-    float ms, iss, mt, ist;
-    soft_stats(zs, nc, it, &ms, &iss);
-    soft_stats(zt, nc, it, &mt, &ist);
+    float ms = -INFINITY, mt = -INFINITY;
+    for (int j = lane; j < nc; j += 64) {
+        ms = fmaxf(ms, zs[j]);
+        mt = fmaxf(mt, zt[j]);
+    }
+    ms = wmax(ms);
+    mt = wmax(mt);
+    float ss = 0.0f, st = 0.0f;
+    for (int j = lane; j < nc; j += 64) {
+        ss += expf((zs[j] - ms) * it);
+        st += expf((zt[j] - mt) * it);
+    }
+    const float iss = 1.0f / wsum(ss), ist = 1.0f / wsum(st);
     float l = 0.0f;
-    for (int j = 0; j < nc; j++) {
+    for (int j = lane; j < nc; j += 64) {
         const float ps = expf((zs[j] - ms) * it) * iss;
         const float pt = expf((zt[j] - mt) * it) * ist;
         if (pt > 1e-9f) l += pt * (logf(fmaxf(pt, 1e-9f)) - logf(fmaxf(ps, 1e-9f)));
         d[j] += temp * (ps - pt) * inv * scale;
     }
-    part[i] = l * temp * temp;
+    l = wsum(l);
+    if (lane == 0) part[i] = l * temp * temp;
 }
 
-// hint_mse per row (loss.rs:139-150): dz += 2 e / (n c) * scale; part[i] =
-// sum e^2.
-__global__ void hint_mse_kernel(size_t n, int c, const float *__restrict__ pred,
-                                const float *__restrict__ target, float scale,
-                                float *__restrict__ dz, float *__restrict__ part) {
-    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+// hint_mse per row (loss.rs:139-150), one wave per row: dz += 2 e / (n c) *
+// scale; part[i] = sum e^2.
+__global__ __launch_bounds__(NT) void hint_mse_kernel(size_t n, int c, const float *__restrict__ pred,
+                                                      const float *__restrict__ target,
+                                                      float scale, float *__restrict__ dz,
+                                                      float *__restrict__ part) {
+    const size_t i = (size_t)blockIdx.x * (NT / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (i >= n) return;
     const float inv = 1.0f / (float)(n * c);
     const float *p = pred + i * c, *t = target + i * c;
     float *d = dz + i * c;
     float s = 0.0f;
-    for (int j = 0; j < c; j++) {
+    for (int j = lane; j < c; j += 64) {
         const float e = p[j] - t[j];
         s += e * e;
         d[j] += 2.0f * e * inv * scale;
     }
-    part[i] = s;
+    s = wsum(s);
+    if (lane == 0) part[i] = s;
 }
 
 // out = (sum of part in row order) * mul1 * mul2; hits summed likewise.
@@ -235,7 +269,7 @@ int rnn_ce_soft(rnn_ctx *ctx, size_t n, size_t nclass, const float *logits, cons
     if (!ws) return RNN_E_NOMEM;
     float *part = (float *)(ws + o_part);
     uint32_t *hit = correct ? (uint32_t *)(ws + o_hit) : nullptr;
-    ce_soft_kernel<<<(unsigned)rnn_div_up(n, NT), NT, 0, ctx->stream>>>(
+    ce_soft_kernel<<<(unsigned)rnn_div_up(n, (size_t)(NT / 64)), NT, 0, ctx->stream>>>(
         n, (int)nclass, logits, target, hard, scale, dz, part, hit);
     RNN_LAUNCHED(ctx);
     if (loss || correct) {
@@ -255,7 +289,7 @@ int rnn_kl_distill(rnn_ctx *ctx, size_t n, size_t nclass, const float *student,
     if (!rows_ok(ctx, n, nclass, "kl_distill")) return RNN_E_INVALID;
     float *part = (float *)rnn_workspace(ctx, n * sizeof(float));
     if (!part) return RNN_E_NOMEM;
-    kl_distill_kernel<<<(unsigned)rnn_div_up(n, NT), NT, 0, ctx->stream>>>(
+    kl_distill_kernel<<<(unsigned)rnn_div_up(n, (size_t)(NT / 64)), NT, 0, ctx->stream>>>(
         n, (int)nclass, student, teacher, temp, scale, dz, part);
     RNN_LAUNCHED(ctx);
     if (loss) {
@@ -275,7 +309,7 @@ int rnn_hint_mse(rnn_ctx *ctx, size_t n, size_t c, const float *pred, const floa
     if (!rows_ok(ctx, n, c, "hint_mse")) return RNN_E_INVALID;
     float *part = (float *)rnn_workspace(ctx, n * sizeof(float));
     if (!part) return RNN_E_NOMEM;
-    hint_mse_kernel<<<(unsigned)rnn_div_up(n, NT), NT, 0, ctx->stream>>>(n, (int)c, pred, target,
+    hint_mse_kernel<<<(unsigned)rnn_div_up(n, (size_t)(NT / 64)), NT, 0, ctx->stream>>>(n, (int)c, pred, target,
                                                                          scale, dz, part);
     RNN_LAUNCHED(ctx);
     if (loss) {

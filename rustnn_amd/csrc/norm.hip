@@ -109,7 +109,21 @@ __global__ __launch_bounds__(NT) void colsum_kernel(size_t rows, int c, size_t r
     if (j >= c) return;
     const size_t r0 = (size_t)blockIdx.y * rpb, r1 = min(rows, r0 + rpb);
     double sab = 0.0, sa = 0.0;
-    for (size_t r = r0; r < r1; r++) {
+    size_t r = r0;
+    for (; r + 8 <= r1; r += 8) {  // 8 rows' loads ahead of their (ordered) adds
+        float av[8], bv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            av[u] = a[(r + u) * c + j];
+            bv[u] = b ? b[(r + u) * c + j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            if (b) sab += (double)(av[u] * bv[u]);
+            sa += av[u];
+        }
+    }
+    for (; r < r1; r++) {
         const float av = a[r * c + j];
         if (b) sab += (double)(av * b[r * c + j]);
         sa += av;
@@ -117,6 +131,22 @@ __global__ __launch_bounds__(NT) void colsum_kernel(size_t rows, int c, size_t r
     const size_t nblk = gridDim.y;
     if (b) part[(size_t)blockIdx.y * c + j] = sab;
     if (want_a) part[(b ? nblk * c : 0) + (size_t)blockIdx.y * c + j] = sa;
+}
+
+// sum over k < nblk of part[k * len + j] in k order, 8 loads ahead of their adds.
+__device__ __forceinline__ double blocks_sum(const double *__restrict__ part, int nblk, size_t len,
+                                             size_t j) {
+    double s = 0.0;
+    int k = 0;
+    for (; k + 8 <= nblk; k += 8) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = part[(size_t)(k + u) * len + j];
+#pragma unroll
+        for (int u = 0; u < 8; u++) s += v[u];
+    }
+    for (; k < nblk; k++) s += part[(size_t)k * len + j];
+    return s;
 }
 
 // out0[j] += sum over blocks of part[blk][j] (block order, f64), likewise
@@ -127,14 +157,8 @@ __global__ __launch_bounds__(NT) void colred_kernel(int nblk, size_t len,
                                                     float *__restrict__ out1) {
     const size_t j = (size_t)blockIdx.x * NT + threadIdx.x;
     if (j >= len) return;
-    double s = 0.0;
-    for (int k = 0; k < nblk; k++) s += part[(size_t)k * len + j];
-    out0[j] += (float)s;
-    if (out1) {
-        double t = 0.0;
-        for (int k = 0; k < nblk; k++) t += part[(size_t)(nblk + k) * len + j];
-        out1[j] += (float)t;
-    }
+    out0[j] += (float)blocks_sum(part, nblk, len, j);
+    if (out1) out1[j] += (float)blocks_sum(part + (size_t)nblk * len, nblk, len, j);
 }
 
 // Like colred_kernel over one column set of length len, sending columns
@@ -145,8 +169,7 @@ __global__ __launch_bounds__(NT) void colred_split_kernel(int nblk, size_t len, 
                                                           float *__restrict__ out1) {
     const size_t j = (size_t)blockIdx.x * NT + threadIdx.x;
     if (j >= len) return;
-    double s = 0.0;
-    for (int k = 0; k < nblk; k++) s += part[(size_t)k * len + j];
+    const double s = blocks_sum(part, nblk, len, j);
     if (j < split)
         out0[j] += (float)s;
     else
@@ -379,11 +402,11 @@ unsigned ew_grid(size_t len) {
     return (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(len, NT), 16384));
 }
 
-// Rows per column-partial block: enough blocks to cover the chip.
+// Rows per column-partial block: about 64 blocks of rows, so that both the
+// partial pass (rows per thread) and the block-order pass (blocks per
+// column) are short chains.
 size_t rows_per_block(size_t rows, int c) {
-    const size_t cblk = rnn_div_up((size_t)c, NT);
-    const size_t want = std::max<size_t>(1, 2048 / cblk);
-    return std::max<size_t>(16, rnn_div_up(rows, want));
+    return std::max<size_t>(16, rnn_div_up(rows, 64));
 }
 
 // Column sums of a*b (b set) and of a over rows, added into outab / outa.

@@ -51,32 +51,19 @@ struct DevRng {
     __device__ float uniform() { return (float)(next() >> 40) * (1.0f / 16777216.0f); }
 };
 
-// DropPath::forward (vit.rs:39-59): image i keeps its branch with the i-th
-// uniform of Rng::new(seed) below 1 - p, scaled by 1 / keep, else 0.  Block
-// (i, chunk): thread 0 draws the i-th uniform (i + 1 steps of the generator),
-// chunk 0 records the mask; rows whose factor is not 1 are scaled.
-__global__ __launch_bounds__(NT) void drop_path_fwd_kernel(size_t per, float p, uint64_t seed,
-                                                           float *x, float *__restrict__ mask) {
-    __shared__ float sfac;
-    const size_t img = blockIdx.y;
-    if (threadIdx.x == 0) {
-        DevRng rng(seed);
-        float u = 0.0f;
-        for (size_t k = 0; k <= img; k++) u = rng.uniform();
-        const float keep = 1.0f - p;
-        const float f = u < keep ? 1.0f / keep : 0.0f;
-        sfac = f;
-        if (blockIdx.x == 0) mask[img] = f;
-    }
-    __syncthreads();
-    const float f = sfac;
-    if (f == 1.0f) return;
-    float *r = x + img * per;
-    for (size_t i = (size_t)blockIdx.x * NT + threadIdx.x; i < per; i += (size_t)gridDim.x * NT)
-        r[i] *= f;
+// DropPath::forward's mask (vit.rs:44-51): image i keeps its branch with the
+// i-th uniform of Rng::new(seed) below 1 - p, scaled by 1 / keep, else 0.
+// The generator is sequential: one thread draws all n.
+__global__ void drop_path_mask_kernel(size_t n, float p, uint64_t seed,
+                                      float *__restrict__ mask) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    DevRng rng(seed);
+    const float keep = 1.0f - p;
+    for (size_t i = 0; i < n; i++) mask[i] = rng.uniform() < keep ? 1.0f / keep : 0.0f;
 }
 
-// DropPath::backward (vit.rs:61-73): dy rows times the kept mask.
+// Rows times the mask, skipping the rows whose factor is 1 (the forward's
+// scaling, vit.rs:52-57, and DropPath::backward, vit.rs:61-73).
 __global__ __launch_bounds__(NT) void drop_path_bwd_kernel(size_t per, float *dy,
                                                            const float *__restrict__ mask) {
     const size_t img = blockIdx.y;
@@ -182,8 +169,10 @@ int rnn_drop_path_forward(rnn_ctx *ctx, size_t n, size_t per, float *x, float p,
     if (!(p > 0.0f) || !(p < 1.0f) || n > 65535)
         return rnn_fail(ctx, RNN_E_INVALID, "drop_path: p %g (0 < p < 1), n %zu (<= 65535)",
                         (double)p, n);
+    drop_path_mask_kernel<<<1, 64, 0, ctx->stream>>>(n, p, seed, mask);
+    RNN_LAUNCHED(ctx);
     const unsigned gx = (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(per, NT), 64));
-    drop_path_fwd_kernel<<<dim3(gx, (unsigned)n), NT, 0, ctx->stream>>>(per, p, seed, x, mask);
+    drop_path_bwd_kernel<<<dim3(gx, (unsigned)n), NT, 0, ctx->stream>>>(per, x, mask);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

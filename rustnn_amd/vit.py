@@ -380,3 +380,309 @@ def tokens_to_nchw(t, hh, ww, ctx=None):
     ctx.check(lib().rnn_tokens_to_nchw(ctx.h, n, c, hw, _ptr(t, t.numel(), "t"),
                                        _ptr(x, t.numel(), "x")))
     return x
+
+
+# ------------------------------------------------------------------ the network
+def _optim_param(v, g, decay):
+    """An optim Param sharing an existing value / gradient pair."""
+    import torch
+    p = Param.__new__(Param)
+    p.v, p.g = v, g
+    p.m, p.v2 = torch.zeros_like(v), torch.zeros_like(v)
+    p.decay, p.rows, p.cols = bool(decay), 0, 0
+    return p
+
+
+class _ConvBN:
+    """Conv2d (nn.rs:115-250) followed by BatchNorm2d (nn.rs:253-428), NCHW."""
+
+    def __init__(self, cin, cout, k, stride, pad, gen, dev, device, ctx, relu=False):
+        import torch
+        from . import Conv2d
+        from .nn import BatchNorm2d
+        fan = cin * k * k
+        w = torch.randn(cout * fan, generator=gen, device=dev) * math.sqrt(2.0 / fan)
+        self.conv = Conv2d(cin, cout, k, stride, pad, w, device, ctx)
+        self.bn = BatchNorm2d(cout, device, ctx)
+        self.relu, self.cout, self.k, self.stride, self.pad = relu, cout, k, stride, pad
+        self.wp = _optim_param(self.conv.w, self.conv.g, True)
+        self.gp = _optim_param(self.bn.g.v, self.bn.g.g, False)
+        self.bp = _optim_param(self.bn.b.v, self.bn.b.g, False)
+
+    def out_hw(self, h, w):
+        return ((h + 2 * self.pad - self.k) // self.stride + 1,
+                (w + 2 * self.pad - self.k) // self.stride + 1)
+
+    def forward(self, x, train):
+        n, _, h, w = x.shape
+        oh, ow = self.out_hw(h, w)
+        y = self.conv.forward(x, n, h, w, train).view(n, self.cout, oh, ow)
+        return self.bn.forward_relu(y, train) if self.relu else self.bn.forward(y, train)
+
+    def backward(self, dy, relu_out=None):
+        """dX; dW, dgamma, dbeta accumulate.  relu_out folds relu_back in."""
+        n, _, h, w = self.conv.xshape[0], 0, self.conv.xshape[1], self.conv.xshape[2]
+        d = self.bn.backward(dy, relu_out)
+        return self.conv.backward(d).view(n, -1, h, w)
+
+    def params(self):
+        return [self.wp, self.gp, self.bp]
+
+
+class BasicBlock:
+    """BasicBlock (model.rs:10-107): conv-BN-ReLU, conv-BN (gamma 0), a 1x1
+    conv-BN shortcut when the shape changes, add + ReLU."""
+
+    def __init__(self, cin, cout, stride, gen, dev, device, ctx):
+        self.ctx = ctx
+        self.a = _ConvBN(cin, cout, 3, stride, 1, gen, dev, device, ctx, relu=True)
+        self.b = _ConvBN(cout, cout, 3, 1, 1, gen, dev, device, ctx)
+        self.b.bn.zero_gamma()
+        self.down = (_ConvBN(cin, cout, 1, stride, 0, gen, dev, device, ctx)
+                     if stride != 1 or cin != cout else None)
+        self.h1 = self.out = None
+
+    def forward(self, x, train):
+        from .nn import add_relu_
+        h = self.a.forward(x, train)
+        y = self.b.forward(h, train)
+        add_relu_(y, self.down.forward(x, train) if self.down else x, self.ctx)
+        if train:
+            self.h1, self.out = h, y
+        return y
+
+    def backward(self, d):
+        from .nn import add_, relu_back_
+        d = d.clone()
+        relu_back_(d, self.out, self.ctx)
+        dmain = self.b.backward(d)
+        dx = self.a.backward(dmain, self.h1)
+        add_(dx, self.down.backward(d) if self.down else d, self.ctx)
+        return dx
+
+    def params(self):
+        ps = self.a.params() + self.b.params()
+        return ps + (self.down.params() if self.down else [])
+
+
+VIT_DEFAULT = dict(width=32, cmid=96, dim=256, heads=4, depth3=5, dim4=384, heads4=6, depth4=2,
+                   mem_at=(1, 3), droppath=0.1, img=32)
+
+
+class RustViT:
+    """RustViT (vit.rs:400-757): convolutional trunk (stem, two BasicBlocks),
+    a 16x16 memory of 2*dim channels (1x1 conv + LayerNorm), 8x8 tokens
+    (3x3/s2 conv + BN), depth3 Blocks (cross-attention readers at mem_at), a
+    2x2 token merge to dim4, depth4 Blocks, LayerNorm + SeqPool + TaxoHead,
+    and two exits (GAP of the trunk; SeqPool of the stage-3 tokens).  parent:
+    the superclass of each fine class (CUDA int32); seed seeds the weights."""
+
+    def __init__(self, cfg=None, parent=None, ncoarse=20, seed=0, device=0, ctx=None):
+        import torch
+        cfg = dict(VIT_DEFAULT, **(cfg or {}))
+        dev = f"cuda:{device}"
+        self.cfg, self.ctx = cfg, ctx or default_ctx(device)
+        gen = torch.Generator(device=dev).manual_seed(int(seed))
+        w, cm, d, d4 = cfg["width"], cfg["cmid"], cfg["dim"], cfg["dim4"]
+        self.mh, self.th = cfg["img"] // 2, cfg["img"] // 4
+        depth = cfg["depth3"] + cfg["depth4"]
+        nf = parent.numel()
+        self.nclass, ctx = nf, self.ctx
+        self.stem = _ConvBN(3, w, 3, 1, 1, gen, dev, device, ctx, relu=True)
+        self.c1 = BasicBlock(w, w, 1, gen, dev, device, ctx)
+        self.c2 = BasicBlock(w, cm, 2, gen, dev, device, ctx)
+        from . import Conv2d
+        mw = torch.randn(2 * d * cm, generator=gen, device=dev) * math.sqrt(2.0 / cm)
+        self.memconv = Conv2d(cm, 2 * d, 1, 1, 0, mw, device, ctx)
+        self.memln = LayerNorm(2 * d, device, ctx)
+        self.tok = _ConvBN(cm, d, 3, 2, 1, gen, dev, device, ctx)
+        div = max(depth, 2) - 1
+        self.blocks3 = [Block(d, cfg["heads"], self.th, self.th,
+                              (self.mh, self.mh) if i in cfg["mem_at"] else None, depth,
+                              cfg["droppath"] * i / div, i + 1, 1e-4, gen, device, ctx)
+                        for i in range(cfg["depth3"])]
+        self.mergeln = LayerNorm(4 * d, device, ctx)
+        self.merge = _linear(4 * d, d4, True, 0.02, gen, dev, ctx)
+        th4 = self.th // 2
+        self.blocks4 = [Block(d4, cfg["heads4"], th4, th4, None, depth,
+                              cfg["droppath"] * (cfg["depth3"] + i) / div,
+                              cfg["depth3"] + i + 1, 1e-4, gen, device, ctx)
+                        for i in range(cfg["depth4"])]
+        self.headln = LayerNorm(d4, device, ctx)
+        self.pool = SeqPool(d4, _trunc_normal(d4, 0.02, gen, dev), device, ctx)
+        self.head = TaxoHead(d4, parent, ncoarse, gen, device, ctx)
+        self.e1 = Exit(cm, nf, d4, gen, device, ctx)
+        self.pool2 = SeqPool(d, _trunc_normal(d, 0.02, gen, dev), device, ctx)
+        self.e2 = Exit(d, nf, d4, gen, device, ctx)
+        self.memw = _optim_param(self.memconv.w, self.memconv.g, True)
+        self.mergep = _linear_param(self.merge)
+        self.use_exits, self.drop_seed = True, 0
+        self.mem = self.c2_out = self.stem_out = None
+        self.n = 0
+
+    def forward(self, x, train):
+        """RustViT::forward (vit.rs:510-609): dict with logits, coarse and, in
+        training with exits, e1, e2, h1, h2; feat (the pooled feature)."""
+        from .nn import gap_forward
+        n, cfg, d = x.shape[0], self.cfg, self.cfg["dim"]
+        h = self.stem.forward(x, train)
+        if train:
+            self.stem_out = h
+        h = self.c1.forward(h, train)
+        h = self.c2.forward(h, train)
+        if train:
+            self.c2_out = h
+        mh = self.mh
+        memt = nchw_to_tokens(self.memconv.forward(h, n, mh, mh, train).view(n, 2 * d, mh, mh),
+                              self.ctx)
+        mem = self.memln.forward(memt, train)
+        z = nchw_to_tokens(self.tok.forward(h, train), self.ctx)
+        seed = self.drop_seed
+        for b in self.blocks3:
+            z = b.forward(z, mem, train, seed)
+        if train:
+            self.mem = mem
+        out = {}
+        if self.use_exits and train:
+            f = self.pool2.forward(z, train)
+            out["e2"], out["h2"] = self.e2.forward(f, n, train)
+        z = token_merge(z, self.th, self.ctx)
+        zn = self.mergeln.forward(z, train)
+        t4 = zn.shape[1]
+        z4 = self.merge.forward(zn.reshape(-1), n * t4, train).view(n, t4, cfg["dim4"])
+        for b in self.blocks4:
+            z4 = b.forward(z4, None, train, seed)
+        zf = self.headln.forward(z4, train)
+        feat = self.pool.forward(zf, train)
+        out["logits"], out["coarse"] = self.head.forward(feat, n, train)
+        out["feat"] = feat
+        if self.use_exits and train:
+            g = gap_forward(self.c2_out, self.ctx)
+            out["e1"], out["h1"] = self.e1.forward(g, n, train)
+        self.n = n
+        return out
+
+    def backward(self, g):
+        """RustViT::backward (vit.rs:628-688) from the output gradients
+        (logits, coarse; e1, e2, h1, h2 with exits; hfinal optional)."""
+        import torch
+        from .nn import add_, gap_backward, relu_back_
+        ctx, n, d, cm = self.ctx, self.n, self.cfg["dim"], self.cfg["cmid"]
+        dfeat = self.head.backward(g["logits"], g["coarse"])
+        if g.get("hfinal") is not None:
+            add_(dfeat, g["hfinal"], ctx)
+        dzf = self.pool.backward(dfeat)
+        dz4 = self.headln.backward(dzf)
+        for b in reversed(self.blocks4):
+            dz4 = b.backward(dz4)
+        t4 = dz4.shape[1]
+        dmg = self.merge.backward(dz4.reshape(-1)).view(n, t4, 4 * d)
+        dzn = self.mergeln.backward(dmg)
+        dz = token_merge_back(dzn, self.th, d, ctx)
+        if self.use_exits and g.get("e2") is not None:
+            df2 = self.e2.backward(g["e2"], g["h2"])
+            add_(dz, self.pool2.backward(df2.view(n, d)), ctx)
+        dmem = torch.zeros_like(self.mem)
+        for b in reversed(self.blocks3):
+            dz = b.backward(dz, self.mem, dmem)
+        dt = tokens_to_nchw(dz, self.th, self.th, ctx)
+        dc2 = self.tok.backward(dt)
+        mh = self.mh
+        dmemn = self.memln.backward(dmem)
+        dmc = self.memconv.backward(tokens_to_nchw(dmemn, mh, mh, ctx).reshape(-1))
+        add_(dc2, dmc, ctx)
+        if self.use_exits and g.get("e1") is not None:
+            dgv = self.e1.backward(g["e1"], g["h1"])
+            add_(dc2, gap_backward(dgv.view(n, cm), mh, mh, ctx), ctx)
+        dh = self.c2.backward(dc2)
+        dh = self.c1.backward(dh)
+        relu_back_(dh, self.stem_out, ctx)
+        dh = self.stem.bn.backward(dh)
+        self.stem.conv.backward_w(dh)
+
+    def for_each_param(self, f):
+        """RustViT::for_each_param (vit.rs:690-716)."""
+        for p in self.stem.params() + self.c1.params() + self.c2.params():
+            f(p)
+        f(self.memw)
+        self.memln.for_each_param(f)
+        for p in self.tok.params():
+            f(p)
+        for b in self.blocks3:
+            b.for_each_param(f)
+        self.mergeln.for_each_param(f)
+        for p in self.mergep:
+            f(p)
+        for b in self.blocks4:
+            b.for_each_param(f)
+        self.headln.for_each_param(f)
+        self.pool.for_each_param(f)
+        self.head.for_each_param(f)
+        if self.use_exits:
+            self.e1.for_each_param(f)
+            self.pool2.for_each_param(f)
+            self.e2.for_each_param(f)
+
+    def params(self):
+        ps = []
+        self.for_each_param(ps.append)
+        return ps
+
+
+VIT_TRAIN = dict(smooth=0.1, sib=0.7, coarse_w=0.4, exit_w=(0.3, 0.6), alpha=1.0, temp=3.0,
+                 beta=0.03, clip=1.0, ema=0.9998, lr=6e-4, wd=0.06, ns=3)
+
+
+class ViTStep:
+    """One Trainer::step of the rustvit (train.rs:340-380) on the device:
+    forward, soft targets (train.rs:121-155, taxonomy smoothing, no mixup
+    here), build_loss (train.rs:70-118: fine and coarse soft-target CE, the
+    two exits' CE, their distillation KL against the final logits and the
+    hint MSE to the pooled feature), backward, clip_, Optim::step_all (Muon)
+    and the EMA.  The loss stays on the device."""
+
+    def __init__(self, net, parent, ncoarse, hp=None):
+        from .optim import Ema, Optim
+        self.net, self.parent, self.nc = net, parent, ncoarse
+        self.hp = dict(VIT_TRAIN, **(hp or {}))
+        self.params = net.params()
+        self.opt = Optim(True, self.hp["ns"], ctx=net.ctx)
+        self.ema = Ema(self.hp["ema"], ctx=net.ctx) if self.hp["ema"] > 0 else None
+        self.norm = None
+
+    def __call__(self, x, labels, coarse, lr=None, wd=None):
+        import torch
+        from .loss import ce_soft, hint_mse, kl_distill, soft_targets
+        from .optim import clip_
+        hp, net, ctx = self.hp, self.net, self.net.ctx
+        nf = net.nclass
+        out = net.forward(x, True)
+        tf, tc = soft_targets(labels, nf, hp["smooth"], self.parent, hp["sib"], coarse, self.nc,
+                              ctx=ctx)
+        ce, correct, dlog = ce_soft(out["logits"], tf, labels, 1.0, ctx=ctx)
+        lc, _, dcoarse = ce_soft(out["coarse"], tc, coarse, hp["coarse_w"], ctx=ctx)
+        total = ce + hp["coarse_w"] * lc
+        g = {"logits": dlog, "coarse": dcoarse}
+        if net.use_exits:
+            l1, _, de1 = ce_soft(out["e1"], tf, labels, hp["exit_w"][0], ctx=ctx)
+            l2, _, de2 = ce_soft(out["e2"], tf, labels, hp["exit_w"][1], ctx=ctx)
+            total = total + hp["exit_w"][0] * l1 + hp["exit_w"][1] * l2
+            if hp["alpha"] > 0:
+                k1 = kl_distill(out["e1"], out["logits"], hp["temp"], hp["alpha"], de1, ctx=ctx)
+                k2 = kl_distill(out["e2"], out["logits"], hp["temp"], hp["alpha"], de2, ctx=ctx)
+                total = total + hp["alpha"] * (k1 + k2)
+            dh1, dh2 = torch.zeros_like(out["h1"]), torch.zeros_like(out["h2"])
+            if hp["beta"] > 0:
+                total = total + hint_mse(out["h1"], out["feat"], hp["beta"], dh1, ctx=ctx) + \
+                    hint_mse(out["h2"], out["feat"], hp["beta"], dh2, ctx=ctx)
+            g.update(e1=de1, e2=de2, h1=dh1, h2=dh2)
+        net.backward(g)
+        if self.norm is None:
+            self.norm = torch.zeros(1, device=x.device)
+        if hp["clip"] > 0:
+            clip_(self.params, hp["clip"], ctx=ctx, norm=self.norm)
+        self.opt.step_all(self.params, hp["lr"] if lr is None else lr,
+                          hp["wd"] if wd is None else wd)
+        if self.ema is not None:
+            self.ema.update(self.params)
+        return total, correct

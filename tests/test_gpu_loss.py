@@ -72,13 +72,18 @@ def test_kl_distill_and_hint(rnn, orc):
     n, nc, c = 256, 100, 384
     zs, zt = (rng.standard_normal((n, nc)) * 2).astype(np.float32), \
         (rng.standard_normal((n, nc)) * 2).astype(np.float32)
-    d0 = rng.standard_normal((n, nc)).astype(np.float32)
-    dz = to_dev(d0).reshape(n, nc)
-    loss = kl_distill(to_dev(zs).reshape(n, nc), to_dev(zt).reshape(n, nc), 2.0, 0.5, dz)
-    wd = d0.copy()
+    ZS, ZT = to_dev(zs).reshape(n, nc), to_dev(zt).reshape(n, nc)
+    dz = to_dev(np.zeros((n, nc), np.float32)).reshape(n, nc)
+    loss = kl_distill(ZS, ZT, 2.0, 0.5, dz)
+    wd = np.zeros((n, nc), np.float32)
     wl = orc.kl_distill(zs, zt, 2.0, 0.5, wd)
     assert abs(float(to_host(loss)[0]) - wl) <= 1e-6 * abs(wl)
-    assert rel_frob(to_host(dz) - d0, wd - d0) < 1e-5
+    assert rel_frob(to_host(dz), wd) < 1e-5
+    # the gradient accumulates: on top of d0 it is d0 + (the same increment)
+    d0 = rng.standard_normal((n, nc)).astype(np.float32)
+    acc = to_dev(d0).reshape(n, nc)
+    kl_distill(ZS, ZT, 2.0, 0.5, acc)
+    assert np.array_equal(to_host(acc), d0 + to_host(dz))
     p, t = rng.standard_normal((n, c)).astype(np.float32), rng.standard_normal((n, c)).astype(
         np.float32)
     h0 = rng.standard_normal((n, c)).astype(np.float32)

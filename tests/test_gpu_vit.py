@@ -245,3 +245,51 @@ def test_reference_block_dircheck(rnn, orc):
     for p, part in zip(ps, np.split(base, sizes)):
         p.v.copy_(to_dev(part))
     assert e < refcheck.TOL, ("block dparams", e)
+
+
+def test_reference_netcheck_rustvit(rnn, orc):
+    """check.rs:397-450: a small RustViT (img 16, width 4, cmid 6, dim 8 x 2
+    blocks with a memory reader, dim4 12 x 1, DropPath 0.2) with parameters
+    perturbed by 0.15 N(0, 1), batch 3, loss = <outputs, random gradients>
+    over the three heads, both hints and the pooled feature; one dircheck
+    over every parameter through the device path."""
+    import torch
+    from rustnn_amd.vit import RustViT
+    cfg = dict(width=4, cmid=6, dim=8, heads=2, depth3=2, dim4=12, heads4=2, depth4=1,
+               mem_at=(1,), droppath=0.2, img=16)
+    parent = _i32(np.array([0, 0, 1, 1, 2, 2], np.uint32))
+    net = RustViT(cfg, parent, 3, seed=0x1234 ^ 0xBEEF)
+    net.drop_seed = 4242
+    rng = orc.Rng(0x1234 ^ 0x77)
+    eps = refcheck.gc_eps()
+    ps = net.params()
+    for p in ps:
+        p.v.add_(to_dev(rng.rand_vec(p.v.numel()) * np.float32(0.15)))
+    bs, nf = 3, 6
+    x = to_dev(rng.rand_vec(bs * 3 * 16 * 16)).reshape(bs, 3, 16, 16)
+    g = {"logits": rng.rand_vec(bs * nf), "coarse": rng.rand_vec(bs * 3),
+         "e1": rng.rand_vec(bs * nf), "e2": rng.rand_vec(bs * nf), "h1": rng.rand_vec(bs * 12),
+         "h2": rng.rand_vec(bs * 12), "hfinal": rng.rand_vec(bs * 12)}
+    gd = {k: to_dev(v) for k, v in g.items()}
+
+    def lin(o):
+        return (refcheck.dot32(to_host(o["logits"]), g["logits"]) +
+                refcheck.dot32(to_host(o["coarse"]), g["coarse"]) +
+                refcheck.dot32(to_host(o["e1"]), g["e1"]) + refcheck.dot32(to_host(o["e2"]), g["e2"]) +
+                refcheck.dot32(to_host(o["h1"]), g["h1"]) + refcheck.dot32(to_host(o["h2"]), g["h2"]) +
+                refcheck.dot32(to_host(o["feat"]), g["hfinal"]))
+
+    net.forward(x, True)
+    net.backward(gd)
+    base = np.concatenate([to_host(p.v).ravel() for p in ps])
+    grad = np.concatenate([to_host(p.g).ravel() for p in ps])
+    assert np.isfinite(grad).all() and np.abs(grad).max() > 0
+    sizes = np.cumsum([p.v.numel() for p in ps])[:-1]
+
+    def lossp(v):
+        for p, part in zip(ps, np.split(v, sizes)):
+            p.v.copy_(to_dev(part))
+        return lin(net.forward(x, True))
+
+    e = refcheck.dircheck(base, grad, eps, rng, lossp)
+    assert e < refcheck.TOL, ("rustvit (all parameters)", e)
