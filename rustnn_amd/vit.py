@@ -488,6 +488,7 @@ class RustViT:
         depth = cfg["depth3"] + cfg["depth4"]
         nf = parent.numel()
         self.nclass, ctx = nf, self.ctx
+        self.parent_host = [int(v) for v in parent.cpu().tolist()]  # the checkpoint hash
         self.stem = _ConvBN(3, w, 3, 1, 1, gen, dev, device, ctx, relu=True)
         self.c1 = BasicBlock(w, w, 1, gen, dev, device, ctx)
         self.c2 = BasicBlock(w, cm, 2, gen, dev, device, ctx)
