@@ -317,6 +317,37 @@ int rnn_taxo_head_combine_backward(rnn_ctx *ctx, size_t n, size_t nf, size_t nc,
 int rnn_nchw_to_tokens(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *x, float *t);
 int rnn_tokens_to_nchw(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *t, float *x);
 
+/* ----------------------------------------------------------- data.rs */
+/* make_batch_train (data.rs:384-416) without RandAugment (ra_mag must be 0):
+ * for batch slot b, image idx[b] of the device-resident dataset (images
+ * [nimg][3][32][32] u8, fine / coarse labels u8), with Rng::new(seed ^ b *
+ * 0x9E3779B97F4A7C15): crop offsets in [-pad, pad], a horizontal flip,
+ * normalisation (border = -mean/std), random erasing with probability erase
+ * of an erase_side square of N(0,1) noise.  out [bs][3][32][32]; labels,
+ * coarse_out [bs] u32.  An index past nimg gives a NaN image and label
+ * 0xffffffff. */
+int rnn_cifar_batch_train(rnn_ctx *ctx, const uint8_t *images, const uint8_t *fine,
+                          const uint8_t *coarse, size_t nimg, const uint32_t *idx, size_t bs,
+                          size_t pad, float ra_mag, float erase, size_t erase_side, uint64_t seed,
+                          float *out, uint32_t *labels, uint32_t *coarse_out);
+/* make_batch_eval (data.rs:494-512): images start .. start + bs normalised
+ * (mirrored when flip); labels may be NULL. */
+int rnn_cifar_batch_eval(rnn_ctx *ctx, const uint8_t *images, const uint8_t *fine, size_t nimg,
+                         size_t start, size_t bs, int flip, float *out, uint32_t *labels);
+/* The host generator of the trainer (rng.rs): state = Rng::new(seed); next. */
+int rnn_rng_seed(uint64_t seed, uint64_t *state);
+uint64_t rnn_rng_next_u64(uint64_t *state);
+/* mix_batch's draws (data.rs:469-492) from the caller's generator state (4
+ * u64, advanced): perm [bs] (shuffle), lam [bs], *cut (cutmix or mixup), *l
+ * and, for cutmix, rect = y0, y1, x0, x1.  Host only. */
+int rnn_mix_plan(uint64_t *rng_state, size_t bs, float alpha_mix, float alpha_cut, float sw,
+                 uint32_t *perm, float *lam, int *cut, float *l, int *rect);
+/* The blend of that plan on the device (cutmix / mixup, data.rs:434-467):
+ * out [bs][3][32][32] from x (not aliased), perm on the device, rect on the
+ * host. */
+int rnn_mix_apply(rnn_ctx *ctx, const float *x, float *out, size_t bs, const uint32_t *perm,
+                  int cut, float l, const int *rect);
+
 /* ----------------------------------------------------------- optim.rs */
 /* Newton-Schulz orthogonalisation (newton_schulz, optim.rs:124-145), in
  * place on `count` [rows x cols] matrices at g + i*stride: X = G (G^T when

@@ -236,6 +236,15 @@ void orc_taxo_combine(size_t n, size_t nf, size_t nc, const uint32_t *parent, fl
 void orc_taxo_combine_backward(size_t n, size_t nf, size_t nc, const uint32_t *parent,
                                const float *dzf, const float *dzc, float *dc);
 
+/* ---------------------------------------------------------------- data.rs */
+void orc_crop_flip_normalize(const uint8_t *src, float *dst, long dy, long dx, int flip);
+void orc_cifar_batch_train(const uint8_t *images, const uint8_t *fine, const uint8_t *coarse,
+                           const uint32_t *idx, size_t bs, size_t pad, float erase,
+                           size_t erase_side, uint64_t seed, float *out, uint32_t *labels,
+                           uint32_t *coarse_out);
+void orc_mix_batch(float *x, size_t bs, float alpha_mix, float alpha_cut, float sw, orc_rng *r,
+                   uint32_t *perm, float *lam);
+
 #ifdef __cplusplus
 }
 #endif

@@ -175,6 +175,12 @@ def lib():
         L.orc_token_merge.argtypes = [_sz, _sz, _sz, _f32p, _f32p]
         L.orc_taxo_combine.argtypes = [_sz, _sz, _sz, _u32p, _f32p, _f32p]
         L.orc_taxo_combine_backward.argtypes = [_sz, _sz, _sz, _u32p, _f32p, _f32p, _f32p]
+        u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+        L.orc_crop_flip_normalize.argtypes = [u8p, _f32p, C.c_long, C.c_long, C.c_int]
+        L.orc_cifar_batch_train.argtypes = [u8p, u8p, u8p, _u32p, _sz, _sz, C.c_float, _sz,
+                                            C.c_uint64, _f32p, _u32p, _u32p]
+        L.orc_mix_batch.argtypes = [_f32p, _sz, C.c_float, C.c_float, C.c_float, P(RngState),
+                                    _u32p, _f32p]
         _lib = L
     return _lib
 
@@ -733,3 +739,36 @@ def taxo_combine_backward(dzf, dzc, parent):
     lib().orc_taxo_combine_backward(n, nf, nc, _u32(parent), _f(dzf).reshape(-1),
                                     _f(dzc).reshape(-1), dc.reshape(-1))
     return dc
+
+
+# ---------------------------------------------------------------- data.rs
+def crop_flip_normalize(src, dy, dx, flip):
+    """crop_flip_normalize (data.rs:331-362) of one u8 image [3*32*32]."""
+    out = np.empty(3 * 32 * 32, np.float32)
+    lib().orc_crop_flip_normalize(np.ascontiguousarray(src, np.uint8), out, dy, dx, int(flip))
+    return out
+
+
+def cifar_batch_train(images, fine, coarse, idx, pad, erase, erase_side, seed):
+    """make_batch_train (data.rs:384-416) without RandAugment: returns
+    (x [bs, 3, 32, 32], labels, coarse)."""
+    idx = _u32(idx)
+    bs = idx.size
+    out = np.empty((bs, 3, 32, 32), np.float32)
+    lab, co = np.empty(bs, np.uint32), np.empty(bs, np.uint32)
+    lib().orc_cifar_batch_train(np.ascontiguousarray(images, np.uint8).reshape(-1),
+                                np.ascontiguousarray(fine, np.uint8),
+                                np.ascontiguousarray(coarse, np.uint8), idx, bs, pad, erase,
+                                erase_side, C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF),
+                                out.reshape(-1), lab, co)
+    return out, lab, co
+
+
+def mix_batch(x, alpha_mix, alpha_cut, sw, rng):
+    """mix_batch (data.rs:469-492) in place on x [bs, ...] with the oracle
+    Rng `rng` (advanced); returns (perm, lam)."""
+    _chk(x)
+    bs = x.shape[0]
+    perm, lam = np.empty(bs, np.uint32), np.empty(bs, np.float32)
+    lib().orc_mix_batch(x.reshape(-1), bs, alpha_mix, alpha_cut, sw, C.byref(rng.st), perm, lam)
+    return perm, lam

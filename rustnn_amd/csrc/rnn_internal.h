@@ -81,6 +81,47 @@ void rnn_dev_table_free(RnnDevTable &t);
 // Slots of rnn_ctx::tables.
 enum { RNN_TABLE_CLIP = 1, RNN_TABLE_EMA = 2 };
 
+// rng.rs (Rng::new, next_u64, next_u32, below, uniform, normal) for host and
+// device code: splitmix64-seeded xoshiro256++, 24-bit uniforms, Box-Muller.
+// The integer stream is bit-identical to the reference's; normal() uses the
+// logf / sqrtf / cosf of the side it runs on.
+struct RnnRng {
+    uint64_t s[4];
+    __host__ __device__ explicit RnnRng(uint64_t seed) {
+        uint64_t z = seed + 0x9E3779B97F4A7C15ull;
+        for (int i = 0; i < 4; i++) {
+            z += 0x9E3779B97F4A7C15ull;
+            uint64_t x = z;
+            x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+            x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+            s[i] = x ^ (x >> 31);
+        }
+    }
+    __host__ __device__ static uint64_t rotl(uint64_t x, int k) {
+        return (x << k) | (x >> (64 - k));
+    }
+    __host__ __device__ uint64_t next() {
+        const uint64_t r = rotl(s[0] + s[3], 23) + s[0];
+        const uint64_t t = s[1] << 17;
+        s[2] ^= s[0];
+        s[3] ^= s[1];
+        s[1] ^= s[2];
+        s[0] ^= s[3];
+        s[2] ^= t;
+        s[3] = rotl(s[3], 45);
+        return r;
+    }
+    __host__ __device__ uint32_t next_u32() { return (uint32_t)(next() >> 32); }
+    __host__ __device__ uint64_t below(uint64_t n) { return next() % n; }
+    __host__ __device__ float uniform() { return (float)(next() >> 40) * (1.0f / 16777216.0f); }
+    __host__ __device__ float normal() {
+        float u1 = uniform();
+        if (!(u1 > 1e-7f)) u1 = 1e-7f;
+        const float u2 = uniform();
+        return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
+    }
+};
+
 // Bump allocator over one workspace block.
 struct WsCarve {
     size_t off = 0;

@@ -23,41 +23,13 @@ unsigned ew_grid(size_t len) {
     return (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(len, NT), 16384));
 }
 
-// rng.rs on the device (Rng::new, next_u64, uniform).
-struct DevRng {
-    uint64_t s[4];
-    __device__ explicit DevRng(uint64_t seed) {
-        uint64_t z = seed + 0x9E3779B97F4A7C15ull;
-        for (int i = 0; i < 4; i++) {
-            z += 0x9E3779B97F4A7C15ull;
-            uint64_t x = z;
-            x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
-            x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
-            s[i] = x ^ (x >> 31);
-        }
-    }
-    __device__ static uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
-    __device__ uint64_t next() {
-        const uint64_t r = rotl(s[0] + s[3], 23) + s[0];
-        const uint64_t t = s[1] << 17;
-        s[2] ^= s[0];
-        s[3] ^= s[1];
-        s[1] ^= s[2];
-        s[0] ^= s[3];
-        s[2] ^= t;
-        s[3] = rotl(s[3], 45);
-        return r;
-    }
-    __device__ float uniform() { return (float)(next() >> 40) * (1.0f / 16777216.0f); }
-};
-
 // DropPath::forward's mask (vit.rs:44-51): image i keeps its branch with the
 // i-th uniform of Rng::new(seed) below 1 - p, scaled by 1 / keep, else 0.
 // The generator is sequential: one thread draws all n.
 __global__ void drop_path_mask_kernel(size_t n, float p, uint64_t seed,
                                       float *__restrict__ mask) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    DevRng rng(seed);
+    RnnRng rng(seed);
     const float keep = 1.0f - p;
     for (size_t i = 0; i < n; i++) mask[i] = rng.uniform() < keep ? 1.0f / keep : 0.0f;
 }

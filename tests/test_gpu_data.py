@@ -1,0 +1,85 @@
+"""GPU parity: data.rs on the device (rustnn_amd/data.py over data.hip)
+against the oracle (oracle/orc_data.c): the training batch bit-exact without
+erasing (the per-image Rng draws the reference's crop and flip), the erased
+rectangle at the same place with N(0,1) noise equal to 1e-6 relative (the
+device's logf / cosf in Box-Muller), the evaluation batch bit-exact,
+mix_batch's plan and blend bit-exact for mixup and cutmix."""
+import numpy as np
+import pytest
+
+from conftest import to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def _set(n=300, seed=0):
+    rng = np.random.default_rng(seed)
+    images = rng.integers(0, 256, (n, 3, 32, 32), dtype=np.uint8)
+    fine = rng.integers(0, 100, n).astype(np.uint8)
+    coarse = (fine // 5).astype(np.uint8)
+    return images, fine, coarse
+
+
+def _i32(a):
+    return to_dev(np.asarray(a, np.uint32).view(np.int32))
+
+
+@pytest.mark.parametrize("erase", [0.0, 0.5, 1.0])
+def test_batch_train(rnn, orc, erase):
+    from rustnn_amd import data
+    images, fine, coarse = _set()
+    ds = data.Dataset.from_arrays(images, fine, coarse)
+    idx = np.random.default_rng(1).integers(0, len(fine), 128).astype(np.uint32)
+    seed = 0xDEADBEEF12345
+    x, lab, co = data.make_batch_train(ds, _i32(idx), seed, 4, erase, 8)
+    wx, wl, wc = orc.cifar_batch_train(images, fine, coarse, idx, 4, erase, 8, seed)
+    assert np.array_equal(to_host(lab).view(np.uint32), wl)
+    assert np.array_equal(to_host(co).view(np.uint32), wc)
+    got = to_host(x)
+    same = got == wx
+    if erase == 0.0:
+        assert same.all()
+    else:
+        # outside the erased squares bit-exact; inside, normals within 1e-6
+        assert np.allclose(got, wx, rtol=1e-6, atol=1e-6)
+        assert same.mean() > 0.9
+
+
+def test_batch_train_bad_index(rnn):
+    from rustnn_amd import data
+    images, fine, coarse = _set(10)
+    ds = data.Dataset.from_arrays(images, fine, coarse)
+    x, lab, _ = data.make_batch_train(ds, _i32([3, 10, 9]), 1)
+    h = to_host(x)
+    assert np.isnan(h[1]).all() and not np.isnan(h[[0, 2]]).any()
+    assert to_host(lab).view(np.uint32)[1] == 0xFFFFFFFF
+
+
+@pytest.mark.parametrize("flip", [False, True])
+def test_batch_eval(rnn, orc, flip):
+    from rustnn_amd import data
+    images, fine, coarse = _set()
+    ds = data.Dataset.from_arrays(images, fine, coarse)
+    x, lab = data.make_batch_eval(ds, 40, 100, flip)
+    got = to_host(x)
+    for b in range(100):
+        want = orc.crop_flip_normalize(images[40 + b].ravel(), 0, 0, flip).reshape(3, 32, 32)
+        assert np.array_equal(got[b], want), b
+    assert np.array_equal(to_host(lab), fine[40:140].astype(np.int32))
+
+
+@pytest.mark.parametrize("alpha_mix,alpha_cut", [(0.8, 0.0), (0.0, 1.0), (0.8, 1.0), (0.0, 0.0)])
+def test_mix_batch(rnn, orc, alpha_mix, alpha_cut):
+    from rustnn_amd import data
+    bs = 64
+    x = np.random.default_rng(2).standard_normal((bs, 3, 32, 32)).astype(np.float32)
+    rng_d, rng_o = data.Rng(77), orc.Rng(77)
+    for _ in range(3):  # the generator state carries over between batches
+        out, perm, lam = data.mix_batch(to_dev(x).reshape(x.shape), alpha_mix, alpha_cut, 0.5,
+                                        rng_d)
+        wx = x.copy()
+        wperm, wlam = orc.mix_batch(wx, alpha_mix, alpha_cut, 0.5, rng_o)
+        assert np.array_equal(to_host(perm).view(np.uint32), wperm)
+        assert np.array_equal(to_host(lam), wlam)
+        assert np.array_equal(to_host(out), wx)
+    assert rng_d.next_u64() == rng_o.next_u64()
