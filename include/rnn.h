@@ -334,6 +334,11 @@ int rnn_cifar_batch_train(rnn_ctx *ctx, const uint8_t *images, const uint8_t *fi
  * (mirrored when flip); labels may be NULL. */
 int rnn_cifar_batch_eval(rnn_ctx *ctx, const uint8_t *images, const uint8_t *fine, size_t nimg,
                          size_t start, size_t bs, int flip, float *out, uint32_t *labels);
+/* FNV-1a 64 continued over host bytes, or over host floats' bit patterns as
+ * 4 little-endian bytes each (fnv_f32, train.rs:478-484): the building blocks
+ * of Trainer::fingerprint (train.rs:450-470).  Host only. */
+uint64_t rnn_fnv1a_bytes(uint64_t hash, const uint8_t *bytes, size_t n);
+uint64_t rnn_fnv1a_f32(uint64_t hash, const float *values, size_t n);
 /* The host generator of the trainer (rng.rs): state = Rng::new(seed); next. */
 int rnn_rng_seed(uint64_t seed, uint64_t *state);
 uint64_t rnn_rng_next_u64(uint64_t *state);

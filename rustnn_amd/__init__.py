@@ -165,6 +165,8 @@ def lib():
                                            C.c_float, _sz, C.c_uint64, _vp, _vp, _vp]),
             "rnn_cifar_batch_eval": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp]),
             "rnn_rng_seed": (_i, [C.c_uint64, _vp]),
+            "rnn_fnv1a_bytes": (C.c_uint64, [C.c_uint64, _vp, _sz]),
+            "rnn_fnv1a_f32": (C.c_uint64, [C.c_uint64, _vp, _sz]),
             "rnn_rng_next_u64": (C.c_uint64, [_vp]),
             "rnn_mix_plan": (_i, [_vp, _sz, C.c_float, C.c_float, C.c_float, _vp, _vp, _vp, _vp,
                                   _vp]),

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <vector>
 
 #pragma clang fp contract(off)
@@ -203,6 +204,28 @@ int rnn_cifar_batch_eval(rnn_ctx *ctx, const uint8_t *images, const uint8_t *fin
                                                             labels);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
+}
+
+uint64_t rnn_fnv1a_bytes(uint64_t hash, const uint8_t *bytes, size_t n) {
+    // FNV-1a 64 (ckpt.rs:84-97, train.rs:476-483)
+    for (size_t i = 0; i < n; i++) {
+        hash ^= bytes[i];
+        hash *= 0x00000100000001B3ull;
+    }
+    return hash;
+}
+
+uint64_t rnn_fnv1a_f32(uint64_t hash, const float *values, size_t n) {
+    // fnv_f32 (train.rs:478-484): each value's bits as 4 little-endian bytes
+    for (size_t i = 0; i < n; i++) {
+        uint32_t b;
+        std::memcpy(&b, values + i, 4);
+        for (int k = 0; k < 4; k++) {
+            hash ^= (b >> (8 * k)) & 0xffu;
+            hash *= 0x00000100000001B3ull;
+        }
+    }
+    return hash;
 }
 
 int rnn_rng_seed(uint64_t seed, uint64_t *state) {

@@ -687,3 +687,39 @@ class ViTStep:
         if self.ema is not None:
             self.ema.update(self.params)
         return total, correct
+
+
+FNV_OFFSET = 0xCBF29CE484222325
+
+
+def fingerprint(step, last_loss):
+    """Trainer::fingerprint (train.rs:444-470): FNV-1a over every parameter's
+    value, momentum and (for the tensors AdamW has updated) second moment in
+    for_each_param order, then the EMA weights, the step count as 8
+    little-endian bytes and the last loss.  The state is copied to the host
+    and hashed there."""
+    import ctypes as C
+    import struct
+
+    import numpy as np
+    L = lib()
+
+    def fold(h, t):
+        a = np.ascontiguousarray(t.detach().cpu().numpy(), np.float32)
+        return int(L.rnn_fnv1a_f32(C.c_uint64(h), a.ctypes.data, a.size))
+
+    h = FNV_OFFSET
+    opt = step.opt
+    for p in step.params:
+        adam = not (opt.muon and p.rows > 0 and min(p.rows, p.cols) > 1)
+        h = fold(h, p.v)
+        h = fold(h, p.m)
+        if adam and opt.t > 0:  # v2 exists once AdamW has stepped (optim.rs:208-210)
+            h = fold(h, p.v2)
+    if step.ema is not None and step.ema.ready:
+        for w in step.ema.w:
+            h = fold(h, w)
+    tb = struct.pack("<Q", int(opt.t))
+    h = int(L.rnn_fnv1a_bytes(C.c_uint64(h), C.c_char_p(tb), 8))
+    lb = np.array([float(last_loss)], np.float32)
+    return int(L.rnn_fnv1a_f32(C.c_uint64(h), lb.ctypes.data, 1))

@@ -96,3 +96,20 @@ def test_resnet_buffer_layout():
         depth_n, width = 3, 32
     lens = ckpt._resnet_buffer_lens(N)
     assert len(lens) == 42 and sum(lens) == 2 * (32 + 6 * 32 + 6 * 64 + 6 * 128 + 64 + 128)
+
+
+def test_fnv1a_entry_points():
+    """rnn_fnv1a_bytes / rnn_fnv1a_f32 (host functions of librnn.so): the
+    published FNV-1a 64 vectors, and a float hashed as its 4 little-endian
+    bytes."""
+    import ctypes as C
+    from rustnn_amd import lib
+    L = lib()
+    off = 0xCBF29CE484222325
+    for s, want in ((b"", 0xCBF29CE484222325), (b"a", 0xAF63DC4C8601EC8C),
+                    (b"foobar", 0x85944171F73967E8)):
+        assert L.rnn_fnv1a_bytes(C.c_uint64(off), C.c_char_p(s), len(s)) == want
+    v = np.array([1.5, -0.0, np.float32(3.1415927)], np.float32)
+    got = L.rnn_fnv1a_f32(C.c_uint64(off), v.ctypes.data, 3)
+    raw = v.tobytes()  # little-endian on this host
+    assert got == L.rnn_fnv1a_bytes(C.c_uint64(off), C.c_char_p(raw), len(raw))

@@ -293,3 +293,32 @@ def test_reference_netcheck_rustvit(rnn, orc):
 
     e = refcheck.dircheck(base, grad, eps, rng, lossp)
     assert e < refcheck.TOL, ("rustvit (all parameters)", e)
+
+
+def test_fingerprint_reproducible(rnn):
+    """Trainer::fingerprint (train.rs:444-470) as the refactoring gate: two
+    runs of the same steps give the same hash (every reduction on the device
+    has a fixed order), and a different learning rate another one."""
+    import torch
+    from rustnn_amd.vit import RustViT, ViTStep, fingerprint
+    cfg = dict(width=4, cmid=6, dim=8, heads=2, depth3=2, dim4=12, heads4=2, depth4=1,
+               mem_at=(1,), droppath=0.2, img=16)
+    parent = _i32(np.array([0, 0, 1, 1, 2, 2], np.uint32))
+
+    def run(lr):
+        net = RustViT(cfg, parent, 3, seed=5)
+        step = ViTStep(net, parent, 3, dict(lr=lr))
+        g = torch.Generator(device="cuda").manual_seed(1)
+        x = torch.randn(4, 3, 16, 16, device="cuda", generator=g)
+        labels = _i32(np.array([0, 3, 5, 1], np.uint32))
+        coarse = _i32(np.array([0, 1, 2, 0], np.uint32))
+        loss = None
+        for i in range(3):
+            net.drop_seed = 100 + i
+            loss, _ = step(x, labels, coarse)
+        return fingerprint(step, float(loss.item())), step.opt.t
+
+    a, t = run(1e-3)
+    b, _ = run(1e-3)
+    c, _ = run(2e-3)
+    assert t == 3 and a == b and a != c
