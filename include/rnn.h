@@ -318,18 +318,19 @@ int rnn_nchw_to_tokens(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float 
 int rnn_tokens_to_nchw(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *t, float *x);
 
 /* ----------------------------------------------------------- data.rs */
-/* make_batch_train (data.rs:384-416) without RandAugment (ra_mag must be 0):
- * for batch slot b, image idx[b] of the device-resident dataset (images
- * [nimg][3][32][32] u8, fine / coarse labels u8), with Rng::new(seed ^ b *
- * 0x9E3779B97F4A7C15): crop offsets in [-pad, pad], a horizontal flip,
+/* make_batch_train (data.rs:384-416): for batch slot b, image idx[b] of the
+ * device-resident dataset (images [nimg][3][32][32] u8, fine / coarse labels
+ * u8), with Rng::new(seed ^ b * 0x9E3779B97F4A7C15): ra_n RandAugment
+ * operations of magnitude ra_mag (none when ra_mag <= 0; ra_n <= 16), crop
+ * offsets in [-pad, pad], a horizontal flip,
  * normalisation (border = -mean/std), random erasing with probability erase
  * of an erase_side square of N(0,1) noise.  out [bs][3][32][32]; labels,
  * coarse_out [bs] u32.  An index past nimg gives a NaN image and label
  * 0xffffffff. */
 int rnn_cifar_batch_train(rnn_ctx *ctx, const uint8_t *images, const uint8_t *fine,
                           const uint8_t *coarse, size_t nimg, const uint32_t *idx, size_t bs,
-                          size_t pad, float ra_mag, float erase, size_t erase_side, uint64_t seed,
-                          float *out, uint32_t *labels, uint32_t *coarse_out);
+                          size_t pad, float ra_mag, size_t ra_n, float erase, size_t erase_side,
+                          uint64_t seed, float *out, uint32_t *labels, uint32_t *coarse_out);
 /* make_batch_eval (data.rs:494-512): images start .. start + bs normalised
  * (mirrored when flip); labels may be NULL. */
 int rnn_cifar_batch_eval(rnn_ctx *ctx, const uint8_t *images, const uint8_t *fine, size_t nimg,

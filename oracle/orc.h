@@ -238,10 +238,12 @@ void orc_taxo_combine_backward(size_t n, size_t nf, size_t nc, const uint32_t *p
 
 /* ---------------------------------------------------------------- data.rs */
 void orc_crop_flip_normalize(const uint8_t *src, float *dst, long dy, long dx, int flip);
+void orc_ra_op(uint8_t *im, size_t op, float v, float sign);
+void orc_randaugment(uint8_t *im, float ra_mag, size_t ra_n, orc_rng *r);
 void orc_cifar_batch_train(const uint8_t *images, const uint8_t *fine, const uint8_t *coarse,
-                           const uint32_t *idx, size_t bs, size_t pad, float erase,
-                           size_t erase_side, uint64_t seed, float *out, uint32_t *labels,
-                           uint32_t *coarse_out);
+                           const uint32_t *idx, size_t bs, size_t pad, float ra_mag, size_t ra_n,
+                           float erase, size_t erase_side, uint64_t seed, float *out,
+                           uint32_t *labels, uint32_t *coarse_out);
 void orc_mix_batch(float *x, size_t bs, float alpha_mix, float alpha_cut, float sw, orc_rng *r,
                    uint32_t *perm, float *lam);
 

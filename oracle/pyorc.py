@@ -177,8 +177,10 @@ def lib():
         L.orc_taxo_combine_backward.argtypes = [_sz, _sz, _sz, _u32p, _f32p, _f32p, _f32p]
         u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
         L.orc_crop_flip_normalize.argtypes = [u8p, _f32p, C.c_long, C.c_long, C.c_int]
+        L.orc_randaugment.argtypes = [u8p, C.c_float, _sz, P(RngState)]
+        L.orc_ra_op.argtypes = [u8p, _sz, C.c_float, C.c_float]
         L.orc_cifar_batch_train.argtypes = [u8p, u8p, u8p, _u32p, _sz, _sz, C.c_float, _sz,
-                                            C.c_uint64, _f32p, _u32p, _u32p]
+                                            C.c_float, _sz, C.c_uint64, _f32p, _u32p, _u32p]
         L.orc_mix_batch.argtypes = [_f32p, _sz, C.c_float, C.c_float, C.c_float, P(RngState),
                                     _u32p, _f32p]
         _lib = L
@@ -749,17 +751,32 @@ def crop_flip_normalize(src, dy, dx, flip):
     return out
 
 
-def cifar_batch_train(images, fine, coarse, idx, pad, erase, erase_side, seed):
-    """make_batch_train (data.rs:384-416) without RandAugment: returns
-    (x [bs, 3, 32, 32], labels, coarse)."""
+def randaugment(img, ra_mag, ra_n, rng):
+    """randaugment (data.rs:303-314) on a copy of one u8 image [3*32*32]."""
+    im = np.ascontiguousarray(img, np.uint8).ravel().copy()
+    lib().orc_randaugment(im, ra_mag, ra_n, C.byref(rng.st))
+    return im
+
+
+def ra_op(img, op, v, sign):
+    """apply_op (data.rs:255-278) with the sign given: returns a new image."""
+    im = np.ascontiguousarray(img, np.uint8).ravel().copy()
+    lib().orc_ra_op(im, op, v, sign)
+    return im.reshape(np.shape(img))
+
+
+def cifar_batch_train(images, fine, coarse, idx, pad, erase, erase_side, seed, ra_mag=0.0,
+                      ra_n=2):
+    """make_batch_train (data.rs:384-416): returns (x [bs, 3, 32, 32], labels,
+    coarse)."""
     idx = _u32(idx)
     bs = idx.size
     out = np.empty((bs, 3, 32, 32), np.float32)
     lab, co = np.empty(bs, np.uint32), np.empty(bs, np.uint32)
     lib().orc_cifar_batch_train(np.ascontiguousarray(images, np.uint8).reshape(-1),
                                 np.ascontiguousarray(fine, np.uint8),
-                                np.ascontiguousarray(coarse, np.uint8), idx, bs, pad, erase,
-                                erase_side, C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF),
+                                np.ascontiguousarray(coarse, np.uint8), idx, bs, pad, ra_mag,
+                                ra_n, erase, erase_side, C.c_uint64(seed & 0xFFFFFFFFFFFFFFFF),
                                 out.reshape(-1), lab, co)
     return out, lab, co
 

@@ -162,7 +162,7 @@ def lib():
             "rnn_ema_update": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
             "rnn_clip_params": (_i, [_vp, _sz, _vp, C.c_float, _vp]),
             "rnn_cifar_batch_train": (_i, [_vp, _vp, _vp, _vp, _sz, _vp, _sz, _sz, C.c_float,
-                                           C.c_float, _sz, C.c_uint64, _vp, _vp, _vp]),
+                                           _sz, C.c_float, _sz, C.c_uint64, _vp, _vp, _vp]),
             "rnn_cifar_batch_eval": (_i, [_vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp]),
             "rnn_rng_seed": (_i, [C.c_uint64, _vp]),
             "rnn_fnv1a_bytes": (C.c_uint64, [C.c_uint64, _vp, _sz]),

@@ -83,8 +83,14 @@ enum { RNN_TABLE_CLIP = 1, RNN_TABLE_EMA = 2 };
 
 // rng.rs (Rng::new, next_u64, next_u32, below, uniform, normal) for host and
 // device code: splitmix64-seeded xoshiro256++, 24-bit uniforms, Box-Muller.
-// The integer stream is bit-identical to the reference's; normal() uses the
-// logf / sqrtf / cosf of the side it runs on.
+// The integer stream is bit-identical to the reference's.  normal() takes
+// the host's logf / cosf (the C library the reference's f32::ln / f32::cos
+// call); on the device it evaluates log and cos in double and rounds once, so
+// its floats are the correctly rounded values, which the host library's
+// results equal in all but rare cases (its own error is under one ulp).
+__device__ __forceinline__ float rnn_dev_logf(float x) { return (float)log((double)x); }
+__device__ __forceinline__ float rnn_dev_cosf(float x) { return (float)cos((double)x); }
+__device__ __forceinline__ float rnn_dev_sinf(float x) { return (float)sin((double)x); }
 struct RnnRng {
     uint64_t s[4];
     __host__ __device__ explicit RnnRng(uint64_t seed) {
@@ -118,7 +124,11 @@ struct RnnRng {
         float u1 = uniform();
         if (!(u1 > 1e-7f)) u1 = 1e-7f;
         const float u2 = uniform();
+#if defined(__HIP_DEVICE_COMPILE__)
+        return sqrtf(-2.0f * rnn_dev_logf(u1)) * rnn_dev_cosf(6.28318530717958647692f * u2);
+#else
         return sqrtf(-2.0f * logf(u1)) * cosf(6.28318530717958647692f * u2);
+#endif
     }
 };
 

@@ -7,8 +7,7 @@ assembly from images resident in HBM.
 * ``taxonomy(ds)``: parent superclass per fine class and the groups
   (data.rs:72-93);
 * ``make_batch_train`` / ``make_batch_eval``: data.rs:384-416 / 494-512 on
-  the device (crop, flip, normalise, random erasing; RandAugment is not on
-  this path);
+  the device (RandAugment, crop, flip, normalise, random erasing);
 * ``Rng`` (the trainer's generator, rng.rs, state on the host) and
   ``mix_batch`` (data.rs:469-492): the draws on the host, the blend on the
   device.
@@ -88,7 +87,8 @@ def taxonomy(ds):
     return parent.astype(np.uint32), groups, ncoarse
 
 
-def make_batch_train(ds, idx, seed, pad=4, erase=0.0, erase_side=8, ra_mag=0.0, ctx=None):
+def make_batch_train(ds, idx, seed, pad=4, erase=0.0, erase_side=8, ra_mag=0.0, ra_n=2,
+                     ctx=None):
     """make_batch_train (data.rs:384-416) on the device: idx (CUDA int32) picks
     the images; returns (x [bs, 3, 32, 32], labels, coarse) as CUDA tensors
     (int32 labels)."""
@@ -101,7 +101,7 @@ def make_batch_train(ds, idx, seed, pad=4, erase=0.0, erase_side=8, ra_mag=0.0, 
     ctx.check(lib().rnn_cifar_batch_train(
         ctx.h, _u8ptr(ds.images, ds.len * PIX, "images"), _u8ptr(ds.labels, ds.len, "labels"),
         _u8ptr(ds.coarse, ds.len, "coarse"), ds.len, _ptr(idx, bs, "idx"), bs, pad,
-        float(ra_mag), float(erase), erase_side, seed & 0xFFFFFFFFFFFFFFFF,
+        float(ra_mag), ra_n, float(erase), erase_side, seed & 0xFFFFFFFFFFFFFFFF,
         _ptr(out, bs * PIX, "out"), _ptr(labels, bs, "labels"), _ptr(coarse, bs, "coarse")))
     return out, labels, coarse
 

@@ -45,6 +45,36 @@ def test_batch_train(rnn, orc, erase):
         assert same.mean() > 0.9
 
 
+@pytest.mark.parametrize("ra_mag,ra_n", [(0.3, 2), (0.9, 3), (1.0, 1)])
+def test_batch_train_randaugment(rnn, orc, ra_mag, ra_n):
+    """RandAugment (data.rs:255-314) before the crop.  The integer ops and the
+    draws are exact.  The magnitude (Box-Muller) and the rotation's cos / sin
+    are correctly rounded on the device, while the host C library the
+    reference calls is off by an ulp at rare arguments (its sinf(0x3eaf8002)
+    gives 0x3eac155f, the correctly rounded value is 0x3eac155e); a float that
+    lands on a u8 truncation boundary then moves a pixel by a level, which a
+    later autocontrast can double.  Bound: at least 99.99% of values
+    bit-exact and none more than two levels (2 / (255 * std)) away."""
+    from rustnn_amd import data
+    images, fine, coarse = _set()
+    ds = data.Dataset.from_arrays(images, fine, coarse)
+    idx = np.random.default_rng(3).integers(0, len(fine), 256).astype(np.uint32)
+    seed = 0x5EED0000 + ra_n
+    x, lab, co = data.make_batch_train(ds, _i32(idx), seed, 4, 0.0, 8, ra_mag, ra_n)
+    wx, wl, wc = orc.cifar_batch_train(images, fine, coarse, idx, 4, 0.0, 8, seed,
+                                       ra_mag=ra_mag, ra_n=ra_n)
+    assert np.array_equal(to_host(lab).view(np.uint32), wl)
+    assert np.array_equal(to_host(co).view(np.uint32), wc)
+    got = to_host(x)
+    assert not np.isnan(got).any()
+    assert (got == wx).mean() >= 0.9999
+    level = 1.0 / (255.0 * 0.2564)  # one u8 level at the smallest std
+    assert np.abs(got - wx).max() <= 2 * level + 1e-5
+    # the augmentation did something: most images differ from the plain batch
+    plain, _, _ = orc.cifar_batch_train(images, fine, coarse, idx, 4, 0.0, 8, seed)
+    assert (np.abs(plain - wx).reshape(len(idx), -1).max(1) > 0).mean() > 0.5
+
+
 def test_batch_train_bad_index(rnn):
     from rustnn_amd import data
     images, fine, coarse = _set(10)
