@@ -9,9 +9,10 @@
 //
 // A workgroup owns a (co block, ci block) pair and walks a strided set of
 // pixel tiles (TR output rows of IMGS images, full width).  Four producer
-// waves stage each tile by DMA into one of two LDS buffers while four MFMA
-// waves compute the previous one (the memory pipeline's back-pressure stalls
-// only the producers):
+// waves stage each tile by DMA into one of two LDS buffers while the MFMA
+// waves (eight for 3x3: two per SIMD, each set owning half of the taps; four
+// for 1x1) compute the previous one (the memory pipeline's back-pressure
+// stalls only the producers):
 //   * the dY window [co][img][r][OWP] and the X halo window [ci][img][ty][TIWP]
 //     (stride 2: even columns then odd columns), one LDS channel every 64m+4
 //     words so that the 32 lanes of a b128 read hit distinct banks while no
@@ -22,8 +23,8 @@
 // pixels 4h..4h+3 of the group with one ds_read_b128 for dY and, per kernel
 // row kh, the 6 (or 5 + 4) X values those pixels touch, so the three kw taps
 // are register offsets into the same read.  MFMA k-step i takes pixels i and
-// 4 + i; the 9 tap accumulators are independent chains.  The 4 MFMA waves'
-// sums are added through LDS in a fixed pairwise order and the workgroup
+// 4 + i; a wave's tap accumulators (5 or 4) are independent chains.  The 4
+// waves of a tap set add their sums through LDS in a fixed pairwise order and the workgroup
 // writes one partial slab; slabs are added in slab order by one reduction
 // launch (no atomics: the result is bit-reproducible).
 #include "conv_common.h"
@@ -36,9 +37,22 @@
 
 namespace {
 
-constexpr int DW_NW = 4;  // MFMA waves per workgroup (one workgroup per CU, one per SIMD)
+constexpr int DW_NW = 4;  // MFMA waves per tap group (one workgroup per CU, one per SIMD)
 constexpr int DW_NP = 4;  // DMA producer waves per workgroup (one per SIMD)
-constexpr int DW_THREADS = 64 * (DW_NW + DW_NP);
+
+// Tap groups: a 3x3 kernel's 9 taps are split over two sets of DW_NW MFMA
+// waves (taps 0-4 and 5-8), so every SIMD runs two MFMA waves that cover
+// each other's operand waits and loop overhead; a 1x1 kernel keeps one set.
+// Each tap is still summed by the same wave sequence over the same groups.
+template <int K>
+constexpr int dw_tap_groups() {
+    return K == 3 ? 2 : 1;
+}
+template <int K>
+constexpr int dw_threads() {
+    return 64 * (DW_NW * dw_tap_groups<K>() + DW_NP);
+}
+inline int dw_threads_of(int k) { return k == 3 ? dw_threads<3>() : dw_threads<1>(); }
 
 struct DwArgs {
     const float *dy;  // [N][CO][OH][OW]
@@ -229,9 +243,10 @@ __device__ __forceinline__ void dw_issue_tile(const DwArgs &g, const DwLane<MT> 
         dw_issue_channel<MT>(g, d, pw + DW_NP * k, cob, cib, buf);
 }
 
-// MFMAs of one 8-pixel group: k-step i takes pixels i and 4 + i.
-template <int K, int S>
-__device__ __forceinline__ void dw_mma(const DwOps<K, S> &o, f32x16 (&acc)[K == 1 ? 4 : K * K]) {
+// MFMAs of one 8-pixel group for taps T0 .. T0 + NT - 1 (a 1x1 kernel: the
+// four k-steps into four accumulators): k-step i takes pixels i and 4 + i.
+template <int K, int S, int T0, int NT>
+__device__ __forceinline__ void dw_mma(const DwOps<K, S> &o, f32x16 (&acc)[NT]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if constexpr (K == 1) {
@@ -239,18 +254,18 @@ __device__ __forceinline__ void dw_mma(const DwOps<K, S> &o, f32x16 (&acc)[K == 
                                                           acc[i], 0, 0, 0);
         } else {
 #pragma unroll
-            for (int t = 0; t < K * K; t++)
-                acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                    o.a[i], dw_bval<K, S>(o, t / K, t % K, i), acc[t], 0, 0, 0);
+            for (int j = 0; j < NT; j++)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                    o.a[i], dw_bval<K, S>(o, (T0 + j) / K, (T0 + j) % K, i), acc[j], 0, 0, 0);
         }
     }
 }
 
 // Scheduling hint for one step: the LDS reads of the next group go out
 // among the first MFMAs of this one, so their latency hides under the rest.
-template <int K, int S>
+template <int K, int S, int NT>
 __device__ __forceinline__ void dw_step_schedule() {
-    constexpr int NMF = K == 1 ? 4 : 4 * K * K;
+    constexpr int NMF = K == 1 ? 4 : 4 * NT;
     constexpr int NRD = 1 + (K == 1 ? 1 : K * (S == 2 ? 3 : 2));
     static_for<0, NRD>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
@@ -263,10 +278,9 @@ __device__ __forceinline__ void dw_step_schedule() {
 // two operand sets alternate so that the reads of group n+1 overlap the
 // MFMAs of group n.  Reads past the tile's last group are clamped to group
 // `wave` (in range; their values are not used).
-template <int K, int S>
+template <int K, int S, int T0, int NT>
 __device__ __forceinline__ void dw_compute(const DwArgs &g, const float *__restrict__ cur,
-                                           int wave, int lane,
-                                           f32x16 (&acc)[K == 1 ? 4 : K * K]) {
+                                           int wave, int lane, f32x16 (&acc)[NT]) {
     const float *xs = cur, *ds = cur + g.xwords;
     const int nsteps = (g.ngroups - wave + DW_NW - 1) / DW_NW;
     auto grp = [&](int s) {
@@ -278,53 +292,95 @@ __device__ __forceinline__ void dw_compute(const DwArgs &g, const float *__restr
 #pragma unroll 1
     for (int s = 0; s < nsteps; s += 2) {
         dw_fetch<K, S>(g, xs, ds, grp(s + 1), lane, ob);
-        dw_mma<K, S>(oa, acc);
-        dw_step_schedule<K, S>();
+        dw_mma<K, S, T0, NT>(oa, acc);
+        dw_step_schedule<K, S, NT>();
         if (s + 1 >= nsteps) break;
         dw_fetch<K, S>(g, xs, ds, grp(s + 2), lane, oa);
-        dw_mma<K, S>(ob, acc);
-        dw_step_schedule<K, S>();
+        dw_mma<K, S, T0, NT>(ob, acc);
+        dw_step_schedule<K, S, NT>();
     }
 }
 
-// Accumulator v of tap t of this lane lives at slab-order slot
-// ((8*(v/4) + 4*h + v%4)*32 + l32)*KK + t = (lbase + 32*(8*(v/4) + v%4))*KK + t.
-template <int KK>
+// Accumulator v of tap t (accumulator j = t - T0 of this wave) of this lane
+// lives at slab-order slot ((8*(v/4) + 4*h + v%4)*32 + l32)*KK + t =
+// (lbase + 32*(8*(v/4) + v%4))*KK + t.
+template <int KK, int T0, int NT>
 __device__ __forceinline__ void dw_red_store(float *dst, int lbase, const f32x16 *acc) {
 #pragma unroll
-    for (int t = 0; t < KK; t++)
+    for (int j = 0; j < NT; j++)
 #pragma unroll
         for (int v = 0; v < 16; v++)
-            dst[(lbase + 32 * (8 * (v >> 2) + (v & 3))) * KK + t] = acc[t][v];
+            dst[(lbase + 32 * (8 * (v >> 2) + (v & 3))) * KK + T0 + j] = acc[j][v];
 }
 
-template <int KK>
+template <int KK, int T0, int NT>
 __device__ __forceinline__ void dw_red_add(const float *src, int lbase, f32x16 *acc) {
 #pragma unroll
-    for (int t = 0; t < KK; t++)
+    for (int j = 0; j < NT; j++)
 #pragma unroll
         for (int v = 0; v < 16; v++)
-            acc[t][v] += src[(lbase + 32 * (8 * (v >> 2) + (v & 3))) * KK + t];
+            acc[j][v] += src[(lbase + 32 * (8 * (v >> 2) + (v & 3))) * KK + T0 + j];
 }
 
-// Waves 0..7 compute (a pixel-group split of the tile); waves 8..11 only
-// stage tiles by DMA, so that the memory pipeline's back-pressure never
-// stalls an MFMA wave.  Double-buffered plans (NB = 2) stage the next tile
-// while this one is computed (one barrier per tile); single-buffered plans
-// stage it after the compute barrier.
+// An MFMA wave of tap group (T0, NT): tiles z, z + nz, ... (the same
+// barriers as the producers, one per tile, two with a single buffer), then
+// the sum of the DW_NW waves of the group in a fixed order, (w0 + w2) + (w1
+// + w3), through two LDS slices in slab order [co][ci][tap]
+// (bit-reproducible).  The groups' taps are disjoint, so both groups use
+// the same slices at once.
+template <int K, int S, int NB, int T0, int NT>
+__device__ __forceinline__ void dw_mfma_wave(const DwArgs &g, float *smem, float *red, int z,
+                                             int wq, int lane) {
+    constexpr int KK = K * K, SL = KK * 1024, NR = K == 1 ? 1 : NT;
+    f32x16 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
+    int s = 0;
+    for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
+        dma_wait_barrier();
+        if constexpr (NB == 2) {
+            dw_compute<K, S, T0, NT>(g, smem + (s & 1) * g.stage, wq, lane, acc);
+        } else {
+            dw_compute<K, S, T0, NT>(g, smem, wq, lane, acc);
+            __syncthreads();
+        }
+    }
+    if constexpr (K == 1) {
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+            acc[0][v] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
+    }
+    static_assert(DW_NW == 4, "reduction order written for four MFMA waves per group");
+    dma_wait_barrier();
+    const int lbase = 4 * (lane >> 5) * 32 + (lane & 31);  // slot of (v = 0, t = 0)
+    if (wq >= 2) dw_red_store<KK, T0, NR>(red + (wq - 2) * SL, lbase, acc);
+    __syncthreads();
+    if (wq < 2) dw_red_add<KK, T0, NR>(red + wq * SL, lbase, acc);
+    __syncthreads();
+    if (wq < 2) dw_red_store<KK, T0, NR>(red + wq * SL, lbase, acc);
+    __syncthreads();
+}
+
+// Waves 0 .. 4*NG-1 compute: wave w takes the pixel groups w%4, w%4 + 4, ...
+// of every tile for the taps of group w/4 (3x3: taps 0-4, then 5-8); the
+// last 4 waves only stage tiles by DMA, so that the memory pipeline's
+// back-pressure never stalls an MFMA wave.  Double-buffered plans (NB = 2)
+// stage the next tile while this one is computed (one barrier per tile);
+// single-buffered plans stage it after the compute barrier.
 template <int K, int S, int MT, int NB>
-__global__ __launch_bounds__(DW_THREADS) void conv_dw_kernel(DwArgs g) {
-    constexpr int KK = K * K, NA = K == 1 ? 4 : KK;
+__global__ __launch_bounds__(dw_threads<K>()) void conv_dw_kernel(DwArgs g) {
+    constexpr int KK = K * K, NG = dw_tap_groups<K>(), NMW = DW_NW * NG;
     extern __shared__ float smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
-    const int h = lane >> 5, l32 = lane & 31;
     const int z = blockIdx.x, cob = blockIdx.y, cib = blockIdx.z;
     float *red = smem;  // after the tiles: 2 slices of [32][32][KK]
     const int SL = KK * 1024;
-    if (wave >= DW_NW) {
+    if (wave >= NMW) {
         // producer: the same barriers as the MFMA waves, one per tile (two
         // with a single buffer), then those of the reduction
-        const int pw = wave - DW_NW;
+        const int pw = wave - NMW;
         DwLane<MT> L;
         dw_lane_init<K, S, MT>(g, L, lane);
         dw_issue_tile<MT>(g, L, z, cob, cib, smem, pw);
@@ -345,45 +401,17 @@ __global__ __launch_bounds__(DW_THREADS) void conv_dw_kernel(DwArgs g) {
         __syncthreads();
         __syncthreads();
         __syncthreads();
+    } else if constexpr (K == 1) {
+        dw_mfma_wave<K, S, NB, 0, 4>(g, smem, red, z, wave, lane);
+    } else if (wave < DW_NW) {
+        dw_mfma_wave<K, S, NB, 0, 5>(g, smem, red, z, wave, lane);
     } else {
-        f32x16 acc[NA];
-#pragma unroll
-        for (int t = 0; t < NA; t++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[t][v] = 0.f;
-        // Tiles z, z + nz, ...
-        int s = 0;
-        for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
-            dma_wait_barrier();
-            if constexpr (NB == 2) {
-                dw_compute<K, S>(g, smem + (s & 1) * g.stage, wave, lane, acc);
-            } else {
-                dw_compute<K, S>(g, smem, wave, lane, acc);
-                __syncthreads();
-            }
-        }
-        if constexpr (K == 1) {
-#pragma unroll
-            for (int v = 0; v < 16; v++)
-                acc[0][v] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
-        }
-        // Sum the MFMA waves' accumulators in a fixed order, (w0 + w2) + (w1 +
-        // w3), through two LDS slices in slab order [co][ci][tap]
-        // (bit-reproducible), then write contiguous slab rows.
-        static_assert(DW_NW == 4, "reduction order written for four MFMA waves");
-        dma_wait_barrier();
-        const int lbase = 4 * h * 32 + l32;  // slot of (v = 0, t = 0) for this lane
-        if (wave >= 2) dw_red_store<KK>(red + (wave - 2) * SL, lbase, acc);
-        __syncthreads();
-        if (wave < 2) dw_red_add<KK>(red + wave * SL, lbase, acc);
-        __syncthreads();
-        if (wave < 2) dw_red_store<KK>(red + wave * SL, lbase, acc);
-        __syncthreads();
+        dw_mfma_wave<K, S, NB, 5, KK - 5>(g, smem, red, z, wave - DW_NW, lane);
     }
     const int ckk = g.CI * KK, rowlen = 32 * KK;
     float *slab = g.part + (long long)z * g.CO * ckk + cib * 32 * KK;
     const int rlim = min(32, g.CI - cib * 32) * KK;
-    for (int e = tid; e < SL; e += DW_THREADS) {
+    for (int e = tid; e < SL; e += dw_threads<K>()) {
         const int co = e / rowlen, rem = e - co * rowlen;
         const float v = red[e] + red[SL + e];
         if (cob * 32 + co < g.CO && rem < rlim) slab[(long long)(cob * 32 + co) * ckk + rem] = v;
@@ -569,7 +597,7 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
             if (it != cache.end()) {
                 occ = it->second;
             } else {
-                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, DW_THREADS, l) !=
+                if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, dw_threads_of(K), l) !=
                         hipSuccess ||
                     occ < 1)
                     occ = 1;
@@ -633,7 +661,7 @@ int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const flo
     if (rc) return rc;
     L.g.part = slabs;
     void *args[] = {&L.g};
-    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(DW_THREADS), args, L.lds, ctx->stream));
+    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(dw_threads_of(sp->k)), args, L.lds, ctx->stream));
     if (nz) *nz = L.g.nz;
     return RNN_OK;
 }
@@ -648,7 +676,7 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
     if (!ws) return RNN_E_NOMEM;
     L.g.part = ws;
     void *args[] = {&L.g};
-    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(DW_THREADS), args, L.lds, ctx->stream));
+    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(dw_threads_of(sp->k)), args, L.lds, ctx->stream));
     hipLaunchKernelGGL(slab_reduce_kernel, dim3((unsigned)rnn_div_up(L.len, 32)), dim3(256), 0,
                        ctx->stream, ws, L.g.nz, (long long)L.len, dw);
     RNN_LAUNCHED(ctx);
