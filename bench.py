@@ -50,6 +50,10 @@ SWEEP = [  # name, cin, cout, k, stride, pad, h  (BASELINE config 1)
     ("1x1s2_64to128_16", 64, 128, 1, 2, 0, 16),
 ]
 PASSES = ("fwd", "dx", "dw")
+# Per-op rows also time the dW kernel alone ("dw_kernel": the split-K slabs
+# without their reduction), which is how each dW runs inside the ResNet step
+# (the step folds the slab sums into its gradient pass).
+OP_PASSES = PASSES + ("dw_kernel",)
 PEAK_HBM_GBS = 8000.0
 GEMMBENCH = [  # bench.rs:17-24 (--gemmbench): m, n, k, at, bt
     (16384, 768, 256, False, True, "S3 qkv fwd"),
@@ -629,8 +633,9 @@ def main():
         # W in the slab order of the forward / dX kernels (rnn_conv_pack_weights):
         # a train step packs each conv's weights once per update
         wpf, wpx = R.conv_pack_weights(sp, 0, w, ctx=ctx), R.conv_pack_weights(sp, 1, w, ctx=ctx)
+        slabs = torch.empty(R.conv2d_backward_w_slab_floats(sp, N, ctx=ctx), device="cuda")
         layers.append(dict(name=name, sp=sp, x=x, w=w, dy=dy, y=y, dx=dx, dw=dw, wpf=wpf,
-                           wpx=wpx, flops=pass_flops(cin, cout, k, s, p, h)))
+                           wpx=wpx, slabs=slabs, flops=pass_flops(cin, cout, k, s, p, h)))
 
     def run_op(L, ps, packed=True):
         if ps == "fwd":
@@ -644,6 +649,8 @@ def main():
                                            ctx=ctx)
             else:
                 R.conv2d_backward_x(L["sp"], N, L["dy"], L["w"], L["dx"], ctx=ctx)
+        elif ps == "dw_kernel":
+            R.conv2d_backward_w_slabs(L["sp"], N, L["dy"], L["x"], L["slabs"], ctx=ctx)
         elif ps == "pack":
             R.conv_pack_weights(L["sp"], 0, L["w"], L["wpf"], ctx=ctx)
             R.conv_pack_weights(L["sp"], 1, L["w"], L["wpx"], ctx=ctx)
@@ -671,11 +678,11 @@ def main():
         dst = torch.empty_like(src)
         dst.copy_(src)
         for L in layers:
-            for ps in PASSES:
+            for ps in OP_PASSES:
                 for _ in range(args.ops_only):
                     run_op(L, ps)
         torch.cuda.synchronize()
-        print(json.dumps({"ops_only": [f"{L['name']}:{ps}" for L in layers for ps in PASSES],
+        print(json.dumps({"ops_only": [f"{L['name']}:{ps}" for L in layers for ps in OP_PASSES],
                           "reps": args.ops_only, "copy_bytes": 2 * src.numel() * 4}))
         return
 
@@ -695,7 +702,7 @@ def main():
     # per-op durations: op-reps back-to-back launches replayed from a graph
     per_op = []
     for L in layers:
-        for ps in PASSES + ("pack",):
+        for ps in OP_PASSES + ("pack",):
             run_op(L, ps)
             t = time_graph(ctx, lambda: run_op(L, ps), args.op_reps)
             if ps == "pack":
@@ -715,12 +722,14 @@ def main():
                 "flop_per_launch": flops, "avg_launch_ms": op_row["ms"]}
 
     lay = {L["name"]: L for L in layers}
-    # dominant op of the ResNet step: largest multiplicity x duration
+    # dominant kernel of the ResNet step: largest multiplicity x duration among
+    # the kernels as the step launches them (forward, dX, dW kernel)
     conv_ops = [r for r in per_op if "tflops" in r]
-    dom = max(conv_ops, key=lambda r: r["ms"] * r["in_resnet_step"])
+    step_kernels = [r for r in conv_ops if not r["op"].endswith(":dw")]
+    dom = max(step_kernels, key=lambda r: r["ms"] * r["in_resnet_step"])
     roof = roofline(dom, lay[dom["op"].split(":")[0]]["flops"])
     roof["share_of_resnet_step"] = round(dom["ms"] * dom["in_resnet_step"] / rn["ms"], 4)
-    sdom = max(conv_ops, key=lambda r: r["ms"])
+    sdom = max(step_kernels, key=lambda r: r["ms"])
     sweep_roof = roofline(sdom, lay[sdom["op"].split(":")[0]]["flops"])
 
     attention = bench_attention(R, ctx, args.op_reps)

@@ -107,6 +107,16 @@ int rnn_conv2d_forward(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const fl
  * dw[cout][cin*k*k] += sum over images of dY im2col(X)^T. */
 int rnn_conv2d_backward_w(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
                           const float *x, float *dw);
+/* The per-worker half of Conv2d::backward_w (nn.rs:201-219): the batch's
+ * dW as *nz partial slabs of cout*cin*k*k floats in `slabs` (slab z: the sum
+ * over the pixel tiles workgroup z owns), without the final reduce
+ * (nn.rs:220-225).  Adding the slabs in slab order gives what
+ * rnn_conv2d_backward_w adds; a train step can fold that sum into its
+ * gradient pass.  `slabs` holds rnn_conv2d_backward_w_slab_floats(...)
+ * floats (0: no slab plan for the shape -- k not 1 or 3, stride not 1 or 2). */
+size_t rnn_conv2d_backward_w_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n);
+int rnn_conv2d_backward_w_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n,
+                                const float *dy, const float *x, float *slabs, int *nz);
 /* dX half of Conv2d::backward (nn.rs:230-250) -> conv::dx_image
  * (conv.rs:205-246): dx[n][cin][h][w] = col2im(W^T dY) (overwritten). */
 int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,

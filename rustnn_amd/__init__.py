@@ -202,6 +202,8 @@ def lib():
             "rnn_resnet_set_graph": (_i, [_vp, _i]),
             "rnn_resnet_graph_state": (_i, [_vp, P(C.c_char_p)]),
             "rnn_resnet_flops": (C.c_uint64, [_vp, _sz, _sz]),
+            "rnn_conv2d_backward_w_slab_floats": (_sz, [_vp, _vp, _sz]),
+            "rnn_conv2d_backward_w_slabs": (_i, [_vp, _vp, _sz, _vp, _vp, _vp, P(C.c_int)]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -352,6 +354,26 @@ def conv2d_backward_w(sp: ConvSpec, n, dy, x, dw, ctx=None):
                                           _ptr(x, n * sp.cin * sp.h * sp.w, "x"),
                                           _ptr(dw, sp.cout * sp.ckk, "dw")))
     return dw
+
+
+def conv2d_backward_w_slab_floats(sp: ConvSpec, n, ctx=None):
+    """Floats of the slab buffer rnn_conv2d_backward_w_slabs fills (0: no
+    slab plan for the shape)."""
+    ctx = ctx or default_ctx()
+    return int(lib().rnn_conv2d_backward_w_slab_floats(ctx.h, C.byref(sp), n))
+
+
+def conv2d_backward_w_slabs(sp: ConvSpec, n, dy, x, slabs, ctx=None):
+    """dW of the batch as partial slabs (nn.rs:201-219 per-worker folds):
+    returns the slab count nz; slabs[z*cout*ckk:(z+1)*cout*ckk] is slab z and
+    their in-order sum is the gradient rnn_conv2d_backward_w adds."""
+    ctx = ctx or default_ctx()
+    nz = C.c_int(0)
+    ctx.check(lib().rnn_conv2d_backward_w_slabs(
+        ctx.h, C.byref(sp), n, _ptr(dy, n * sp.cout * sp.hw, "dy"),
+        _ptr(x, n * sp.cin * sp.h * sp.w, "x"),
+        _ptr(slabs, conv2d_backward_w_slab_floats(sp, n, ctx), "slabs"), C.byref(nz)))
+    return nz.value
 
 
 def conv2d_backward_x(sp: ConvSpec, n, dy, w, dx=None, ctx=None):

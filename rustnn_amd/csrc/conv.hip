@@ -509,6 +509,25 @@ int rnn_conv2d_backward_w(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
     return rnn_conv_dw(ctx, sp, n, dy, x, dw);
 }
 
+size_t rnn_conv2d_backward_w_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n) {
+    if (!ctx || !sp || n == 0) return 0;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (check_spec(ctx, sp)) return 0;
+    return rnn_conv_dw_slab_floats(ctx, sp, n);
+}
+
+int rnn_conv2d_backward_w_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                                const float *x, float *slabs, int *nz) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    int rc = check_spec(ctx, sp);
+    if (rc) return rc;
+    if (n == 0) return rnn_fail(ctx, RNN_E_INVALID, "conv2d_backward_w_slabs: empty batch");
+    if (!dy || !x || !slabs)
+        return rnn_fail(ctx, RNN_E_NULL, "conv2d_backward_w_slabs: null operand");
+    return rnn_conv_dw_slabs(ctx, sp, n, dy, x, slabs, nz);
+}
+
 int rnn_dbg_im2col(rnn_ctx *ctx, const rnn_conv_spec *sp, const float *x_img, float *col) {
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);

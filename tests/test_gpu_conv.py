@@ -113,6 +113,40 @@ def test_conv_packed_weights_bit_exact(rnn, orc, name, n, cin, cout, k, s, p, h)
         assert per_ch >= cs
 
 
+@pytest.mark.parametrize("name,n,cin,cout,k,s,p,h", SHAPES, ids=[s[0] for s in SHAPES])
+def test_conv_dw_slabs(rnn, orc, name, n, cin, cout, k, s, p, h):
+    """rnn_conv2d_backward_w_slabs: nz partial slabs whose sum is the batch
+    dW.  Integer-valued inputs: the slab sum equals the oracle bit for bit;
+    seeded normal inputs: within TOL of the oracle, and the slab-order sum
+    matches what rnn_conv2d_backward_w adds."""
+    sp = orc.ConvSpec.make(cin, cout, k, s, p, h, h)
+    gsp = rnn.ConvSpec.make(cin, cout, k, s, p, h, h)
+    floats = rnn.conv2d_backward_w_slab_floats(gsp, n)
+    ln = sp.cout * sp.ckk
+    assert floats > 0 and floats % ln == 0, (floats, ln)
+    r = np.random.default_rng(zlib.crc32(name.encode()) + 1)
+    xi = r.integers(-2, 3, n * cin * h * h).astype(np.float32)
+    dyi = r.integers(-2, 3, n * sp.cout * sp.hw).astype(np.float32)
+    xg, _, dyg = inputs(orc, sp, n, seed=31)
+    for x, dy, exact in ((xi, dyi, True), (xg, dyg, False)):
+        with orc.threads(8):
+            want = orc.conv2d_backward_w(sp, n, dy, x).ravel()
+        X, DY = to_dev(x), to_dev(dy)
+        slabs = to_dev(np.full(floats, np.nan, np.float32))
+        nz = rnn.conv2d_backward_w_slabs(gsp, n, DY, X, slabs)
+        assert 1 <= nz <= floats // ln
+        sl = to_host(slabs)[: nz * ln].reshape(nz, ln)
+        assert np.isfinite(sl).all(), "every slab element is written"
+        got = sl.astype(np.float64).sum(axis=0)
+        if exact:
+            assert np.array_equal(got.astype(np.float32), want), name
+        else:
+            assert rel_frob(got, want) < TOL, name
+            dw = to_dev(np.zeros(ln, np.float32))
+            rnn.conv2d_backward_w(gsp, n, DY, X, dw)
+            assert rel_frob(to_host(dw), got) < 1e-6, name
+
+
 def test_conv_deterministic(rnn, orc):
     sp = rnn.ConvSpec.make(32, 32, 3, 1, 1, 32, 32)
     x, w, dy = inputs(orc, sp, 128, seed=99)
