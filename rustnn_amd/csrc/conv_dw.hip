@@ -450,6 +450,147 @@ __global__ __launch_bounds__(256) void slab_reduce_kernel(const float *part, int
     }
 }
 
+// Weight gradient of a 3x3 stride-1 convolution with few input channels
+// (cin * 9 <= 32, the network stem): the im2col rows (ci, kh, kw), numbered
+// r = ci*9 + kh*3 + kw as conv.rs's RowMap numbers them, make up a single
+// 32-wide MFMA N block, so a pixel pair costs one MFMA where the tap kernel
+// above spends nine 32x32 taps on zero-padded channels.
+//   * a workgroup (4 waves) takes the tiles z, z + nz, ... : SMC_R output
+//     rows of one image, full width; it stages dY [32 co][pixels] and the
+//     zero-padded X window [ci][R + 2][OW + 2] in LDS with plain loads;
+//   * MFMA k-step = a pixel pair: lane l reads dY[co = l%32][p] and
+//     X[ci][r + kh][c + kw] for column n = l%32 (0 for n >= cin*9), where
+//     p = 2q + l/32 is pixel (r, c) of the tile; wave w takes the pairs
+//     w, w + 4, ... into two alternating accumulators;
+//   * the 4 waves are added through LDS in the order (w0 + w1) + (w2 + w3),
+//     and the workgroup writes slab z; slabs are summed in slab order as for
+//     the tap kernel (bit-reproducible).
+constexpr int SMC_THREADS = 256;
+constexpr int SMC_PIX = 256;             // pixels per tile (at most; = SMC_THREADS)
+constexpr int SMC_DS = SMC_PIX + 1;      // LDS row stride of dY (conflict-free reads)
+constexpr int SMC_XMAX = 3 * 1300;       // LDS floats of the X window
+constexpr int SMC_RS = 33;               // row stride of the reduction slices
+
+struct DwSmallArgs {
+    const float *dy, *x;
+    float *part;  // [nz][CO][CI*9]
+    int N, CO, CI, H, W, OH, OW, pad;
+    int R, tiles_a, ntiles;
+    FastDiv fd_xplane, fd_xw;  // X window plane (R + 2) * (OW + 2) and row OW + 2
+};
+
+__global__ __launch_bounds__(SMC_THREADS) void conv_dw_smallc_kernel(DwSmallArgs g) {
+    __shared__ float sdy[32 * SMC_DS];
+    __shared__ float sx[SMC_XMAX];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int z = blockIdx.x, nz = gridDim.x, cob = blockIdx.y;
+    const int n = lane & 31, kidx = lane >> 5;
+    const int NV = g.CI * 9, XW = g.OW + 2, XR = g.R + 2;
+    // this lane's B column: (ci, kh, kw) of im2col row n
+    const int bci = n < NV ? n / 9 : 0, bkh = n < NV ? (n % 9) / 3 : 0,
+              bkw = n < NV ? n % 3 : 0;
+    const int boff = (bci * XR + bkh) * XW + bkw;
+    const int tpix = g.R * g.OW;
+    f32x16 acc0, acc1;
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc0[v] = acc1[v] = 0.f;
+    for (int tile = z; tile < g.ntiles; tile += nz) {
+        const int img = tile / g.tiles_a, a0 = (tile % g.tiles_a) * g.R;
+        const int rows = min(g.R, g.OH - a0), npix = rows * g.OW;
+        __syncthreads();  // the previous tile's reads are done
+        const float *dsrc = g.dy + ((long long)img * g.CO + cob * 32) * g.OH * g.OW +
+                            (long long)a0 * g.OW;
+        // all loads of the tile are issued before the first LDS store
+        const long long cst = (long long)g.OH * g.OW;
+        if ((g.OW & 3) == 0) {
+            // 16-byte loads: thread (co4 = tid / 64, j = tid % 64) takes
+            // pixels 4j .. 4j+3 of output channels co4, co4 + 4, ...
+            const int j = tid & 63, co4 = tid >> 6, p = 4 * j;
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int co = co4 + 4 * k;
+                v[k] = float4{0.f, 0.f, 0.f, 0.f};
+                if (p < npix && cob * 32 + co < g.CO)
+                    v[k] = *reinterpret_cast<const float4 *>(dsrc + co * cst + p);
+            }
+            if (p < tpix) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    float *d = sdy + (co4 + 4 * k) * SMC_DS + p;
+                    d[0] = v[k].x;
+                    d[1] = v[k].y;
+                    d[2] = v[k].z;
+                    d[3] = v[k].w;
+                }
+            }
+        } else if (tid < tpix) {  // tpix <= SMC_PIX = SMC_THREADS
+            const bool okp = tid < npix;
+            float v[32];
+#pragma unroll
+            for (int co = 0; co < 32; co++) {
+                v[co] = 0.f;
+                if (okp && cob * 32 + co < g.CO) v[co] = dsrc[co * cst + tid];
+            }
+#pragma unroll
+            for (int co = 0; co < 32; co++) sdy[co * SMC_DS + tid] = v[co];
+        }
+        const float *xsrc = g.x + (long long)img * g.CI * g.H * g.W;
+        const int xtot = g.CI * XR * XW;
+        float xv[SMC_XMAX / SMC_THREADS + 1];
+#pragma unroll
+        for (int k = 0; k <= SMC_XMAX / SMC_THREADS; k++) {
+            const int e = tid + k * SMC_THREADS;
+            const int ci = (int)fdiv((uint32_t)e, g.fd_xplane), rem = e - ci * (XR * XW);
+            const int t = (int)fdiv((uint32_t)rem, g.fd_xw), u = rem - t * XW;
+            const int y = a0 - g.pad + t, x = u - g.pad;
+            xv[k] = 0.f;
+            if (e < xtot && y >= 0 && y < g.H && x >= 0 && x < g.W)
+                xv[k] = xsrc[((long long)ci * g.H + y) * g.W + x];
+        }
+#pragma unroll
+        for (int k = 0; k <= SMC_XMAX / SMC_THREADS; k++) {
+            const int e = tid + k * SMC_THREADS;
+            if (e < xtot) sx[e] = xv[k];
+        }
+        __syncthreads();
+        const int npairs = (npix + 1) >> 1;
+        for (int q = wave; q < npairs; q += 8) {
+#pragma unroll
+            for (int h2 = 0; h2 < 2; h2++) {
+                const int qq = q + 4 * h2;
+                const int p = 2 * qq + kidx;
+                const bool ok = qq < npairs && p < npix;
+                const int pc = ok ? p : 0;
+                const int r = pc / g.OW, c = pc - r * g.OW;
+                const float a = ok ? sdy[n * SMC_DS + pc] : 0.f;
+                const float b = n < NV ? sx[boff + r * XW + c] : 0.f;
+                if (h2 == 0)
+                    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc0, 0, 0, 0);
+                else
+                    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc1, 0, 0, 0);
+            }
+        }
+    }
+    // acc register v of lane l: D row (co) 8*(v/4) + 4*(l/32) + v%4, column n = l%32
+    __syncthreads();
+    float *red = sdy;  // 4 slices of [32][SMC_RS]
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int co = 8 * (v >> 2) + 4 * kidx + (v & 3);
+        red[(wave * 32 + co) * SMC_RS + n] = acc0[v] + acc1[v];
+    }
+    __syncthreads();
+    float *slab = g.part + (long long)z * g.CO * NV;
+    for (int e = tid; e < 32 * NV; e += SMC_THREADS) {
+        const int co = e / NV, col = e - co * NV;
+        if (cob * 32 + co >= g.CO) continue;
+        const float v = (red[co * SMC_RS + col] + red[(32 + co) * SMC_RS + col]) +
+                        (red[(64 + co) * SMC_RS + col] + red[(96 + co) * SMC_RS + col]);
+        slab[(long long)(cob * 32 + co) * NV + col] = v;
+    }
+}
+
 constexpr int DW_MT[3] = {2, 4, 8};
 
 // Geometry of a (TR, IMGS) tile; returns LDS bytes, 0 if the tile does not
@@ -528,14 +669,71 @@ const void *dw_pick(int mt, int nb) {
 // bytes and the grid (NZ slabs x output-channel blocks x input-channel blocks).
 struct DwLaunch {
     DwArgs g;
+    DwSmallArgs gs;  // the few-input-channel kernel's arguments (small)
+    bool small = false;
     const void *kern;
     size_t lds;
     dim3 grid;
+    int threads;
+    int nz;      // slabs
     size_t len;  // floats of one slab: cout * cin * k * k
+    void set_part(float *p) {
+        if (small)
+            gs.part = p;
+        else
+            g.part = p;
+    }
+    void *arg() { return small ? (void *)&gs : (void *)&g; }
 };
+
+// Plan of the few-input-channel kernel (3x3, stride 1, cin * 9 <= 32), or
+// false when the shape is not one.
+static bool dw_small_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
+                          const float *x, DwLaunch &L) {
+    if (sp->k != 3 || sp->stride != 1 || sp->cin * 9 > 32 || sp->ow > SMC_PIX || n == 0)
+        return false;
+    DwSmallArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.dy = dy;
+    a.x = x;
+    a.N = (int)n;
+    a.CO = sp->cout;
+    a.CI = sp->cin;
+    a.H = sp->h;
+    a.W = sp->w;
+    a.OH = sp->oh;
+    a.OW = sp->ow;
+    a.pad = sp->pad;
+    a.R = std::max(1, std::min(SMC_PIX / a.OW, a.OH));
+    if ((long long)a.CI * (a.R + 2) * (a.OW + 2) > SMC_XMAX) return false;
+    if ((long long)n * std::max((long long)a.CI * a.H * a.W, (long long)a.CO * a.OH * a.OW) >=
+        (1ll << 40))
+        return false;
+    a.tiles_a = (a.OH + a.R - 1) / a.R;
+    a.ntiles = a.tiles_a * (int)n;
+    a.fd_xplane = make_fastdiv((a.R + 2) * (a.OW + 2));
+    a.fd_xw = make_fastdiv(a.OW + 2);
+    const int ncb = (a.CO + 31) / 32;
+    static int occ = 0;
+    if (occ == 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                         &occ, (const void *)conv_dw_smallc_kernel, SMC_THREADS, 0) != hipSuccess ||
+                     occ < 1))
+        occ = 1;
+    const int nz = std::min(std::max(1, occ * ctx->num_cus / ncb), a.ntiles);
+    L.small = true;
+    L.gs = a;
+    L.kern = (const void *)conv_dw_smallc_kernel;
+    L.lds = 0;
+    L.grid = dim3(nz, ncb, 1);
+    L.threads = SMC_THREADS;
+    L.nz = nz;
+    L.len = (size_t)a.CO * a.CI * 9;
+    return true;
+}
 
 static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
                    const float *x, DwLaunch &L) {
+    if (dw_small_plan(ctx, sp, n, dy, x, L)) return RNN_OK;
     const int K = sp->k;
     if (K != 1 && K != 3) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: k must be 1 or 3");
     if (sp->stride != 1 && sp->stride != 2)
@@ -644,6 +842,8 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
     L.kern = kern;
     L.lds = lds;
     L.grid = dim3(NZ, ncb, ncib);
+    L.threads = dw_threads_of(K);
+    L.nz = NZ;
     L.len = (size_t)g.CO * g.CI * K * K;
     return RNN_OK;
 }
@@ -651,7 +851,7 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
 size_t rnn_conv_dw_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n) {
     DwLaunch L;
     if (dw_plan(ctx, sp, n, nullptr, nullptr, L) != RNN_OK) return 0;
-    return (size_t)L.g.nz * L.len;
+    return (size_t)L.nz * L.len;
 }
 
 int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
@@ -659,10 +859,10 @@ int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const flo
     DwLaunch L;
     int rc = dw_plan(ctx, sp, n, dy, x, L);
     if (rc) return rc;
-    L.g.part = slabs;
-    void *args[] = {&L.g};
-    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(dw_threads_of(sp->k)), args, L.lds, ctx->stream));
-    if (nz) *nz = L.g.nz;
+    L.set_part(slabs);
+    void *args[] = {L.arg()};
+    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(L.threads), args, L.lds, ctx->stream));
+    if (nz) *nz = L.nz;
     return RNN_OK;
 }
 
@@ -672,13 +872,13 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
     DwLaunch L;
     int rc = dw_plan(ctx, sp, n, dy, x, L);
     if (rc) return rc;
-    float *ws = (float *)rnn_workspace(ctx, (size_t)L.g.nz * L.len * sizeof(float));
+    float *ws = (float *)rnn_workspace(ctx, (size_t)L.nz * L.len * sizeof(float));
     if (!ws) return RNN_E_NOMEM;
-    L.g.part = ws;
-    void *args[] = {&L.g};
-    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(dw_threads_of(sp->k)), args, L.lds, ctx->stream));
+    L.set_part(ws);
+    void *args[] = {L.arg()};
+    RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(L.threads), args, L.lds, ctx->stream));
     hipLaunchKernelGGL(slab_reduce_kernel, dim3((unsigned)rnn_div_up(L.len, 32)), dim3(256), 0,
-                       ctx->stream, ws, L.g.nz, (long long)L.len, dw);
+                       ctx->stream, ws, L.nz, (long long)L.len, dw);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
