@@ -117,6 +117,19 @@ int rnn_conv2d_backward_w(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
 size_t rnn_conv2d_backward_w_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n);
 int rnn_conv2d_backward_w_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n,
                                 const float *dy, const float *x, float *slabs, int *nz);
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): rnn_conv2d_backward_w with its partial slabs in a fixed
+ * device scratch array of 16 MiB (RNN_NOALLOC_SCRATCH_BYTES) that the library
+ * holds on each device until the process ends, instead of the context's
+ * growing workspace.  Same kernels, same summation order, same result.  It
+ * calls no hipMalloc / hipFree.  A shape whose slabs need more than the
+ * scratch (cout*cin*k*k*4 bytes times the slab count; 9.4 MB for the ResNet
+ * convs at batch 128) returns RNN_E_UNSUPPORTED.  Every call on one device
+ * shares that scratch: calls that overlap on one GPU (several contexts or
+ * streams at once) race and must be serialised by the caller. */
+int rnn_conv2d_backward_w_noalloc(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n,
+                                  const float *dy, const float *x, float *dw);
 /* dX half of Conv2d::backward (nn.rs:230-250) -> conv::dx_image
  * (conv.rs:205-246): dx[n][cin][h][w] = col2im(W^T dY) (overwritten). */
 int rnn_conv2d_backward_x(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,

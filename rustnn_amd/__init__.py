@@ -204,6 +204,7 @@ def lib():
             "rnn_resnet_flops": (C.c_uint64, [_vp, _sz, _sz]),
             "rnn_conv2d_backward_w_slab_floats": (_sz, [_vp, _vp, _sz]),
             "rnn_conv2d_backward_w_slabs": (_i, [_vp, _vp, _sz, _vp, _vp, _vp, P(C.c_int)]),
+            "rnn_conv2d_backward_w_noalloc": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
         }
         for name, (res, args) in sigs.items():
             f = getattr(L, name)
@@ -353,6 +354,17 @@ def conv2d_backward_w(sp: ConvSpec, n, dy, x, dw, ctx=None):
                                           _ptr(dy, n * sp.cout * sp.hw, "dy"),
                                           _ptr(x, n * sp.cin * sp.h * sp.w, "x"),
                                           _ptr(dw, sp.cout * sp.ckk, "dw")))
+    return dw
+
+
+def conv2d_backward_w_noalloc(sp: ConvSpec, n, dy, x, dw, ctx=None):
+    """conv2d_backward_w with its partial slabs in the library's fixed device
+    scratch (no device allocation; calls overlapping on one GPU race)."""
+    ctx = ctx or default_ctx()
+    ctx.check(lib().rnn_conv2d_backward_w_noalloc(ctx.h, C.byref(sp), n,
+                                                  _ptr(dy, n * sp.cout * sp.hw, "dy"),
+                                                  _ptr(x, n * sp.cin * sp.h * sp.w, "x"),
+                                                  _ptr(dw, sp.cout * sp.ckk, "dw")))
     return dw
 
 

@@ -509,6 +509,21 @@ int rnn_conv2d_backward_w(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
     return rnn_conv_dw(ctx, sp, n, dy, x, dw);
 }
 
+int rnn_conv2d_backward_w_noalloc(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n,
+                                  const float *dy, const float *x, float *dw) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    int rc = check_spec(ctx, sp);
+    if (rc) return rc;
+    if (n == 0) return RNN_OK;
+    if (!dy || !x || !dw)
+        return rnn_fail(ctx, RNN_E_NULL, "conv2d_backward_w_noalloc: null operand");
+    if (!ctx->noalloc_scratch)
+        return rnn_fail(ctx, RNN_E_HIP, "conv2d_backward_w_noalloc: no scratch address");
+    return rnn_conv_dw(ctx, sp, n, dy, x, dw, ctx->noalloc_scratch,
+                       RNN_NOALLOC_SCRATCH_BYTES / sizeof(float));
+}
+
 size_t rnn_conv2d_backward_w_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n) {
     if (!ctx || !sp || n == 0) return 0;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);

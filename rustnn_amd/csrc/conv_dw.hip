@@ -866,14 +866,25 @@ int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const flo
     return RNN_OK;
 }
 
-// dW += over the batch (k = 1 or 3): slabs in the workspace, then one reduce.
+// dW += over the batch (k = 1 or 3): slabs in `part` (cap floats) or, with
+// part null, in the context workspace; then one reduce in slab order.
 int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
-                float *dw) {
+                float *dw, float *part, size_t cap) {
     DwLaunch L;
     int rc = dw_plan(ctx, sp, n, dy, x, L);
     if (rc) return rc;
-    float *ws = (float *)rnn_workspace(ctx, (size_t)L.nz * L.len * sizeof(float));
-    if (!ws) return RNN_E_NOMEM;
+    const size_t need = (size_t)L.nz * L.len;
+    float *ws = part;
+    if (ws) {
+        if (need > cap)
+            return rnn_fail(ctx, RNN_E_UNSUPPORTED,
+                            "conv dW: %zu bytes of partial slabs exceed the fixed scratch of "
+                            "%zu bytes",
+                            need * sizeof(float), cap * sizeof(float));
+    } else {
+        ws = (float *)rnn_workspace(ctx, need * sizeof(float));
+        if (!ws) return RNN_E_NOMEM;
+    }
     L.set_part(ws);
     void *args[] = {L.arg()};
     RNN_HIP(ctx, hipLaunchKernel(L.kern, L.grid, dim3(L.threads), args, L.lds, ctx->stream));

@@ -8,6 +8,33 @@
 
 #include <cstring>
 
+// The fixed scratch of the no-allocation entry points: partial results that
+// the other entry points keep in the context's growing workspace.  Every
+// device the library runs on holds one copy until the process ends.  In host
+// code the array's name is only a stand-in for the device symbol; the device
+// address of each device's copy comes from hipGetSymbolAddress, looked up once
+// per device (with that device current) and kept in g_scratch_addr.
+static __device__ __align__(256) float scratch[RNN_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+static std::mutex g_scratch_mu;
+static std::map<int, float *> g_scratch_addr;
+
+// Device address of `device`'s scratch copy; device must be current.
+static int scratch_address(int device, float **out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto it = g_scratch_addr.find(device);
+    if (it != g_scratch_addr.end()) {
+        *out = it->second;
+        return RNN_OK;
+    }
+    float *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return RNN_E_HIP;
+    g_scratch_addr[device] = ptr;
+    *out = ptr;
+    return RNN_OK;
+}
+
 int rnn_fail(rnn_ctx *ctx, int code, const char *fmt, ...) {
     if (ctx) {
         va_list ap;
@@ -112,6 +139,11 @@ int rnn_ctx_create(int device, rnn_ctx **out) {
         return RNN_E_HIP;
     }
     c->own_stream = true;
+    if (scratch_address(device, &c->noalloc_scratch) != RNN_OK) {
+        (void)hipStreamDestroy(c->stream);
+        delete c;
+        return RNN_E_HIP;
+    }
     *out = c;
     return RNN_OK;
 }

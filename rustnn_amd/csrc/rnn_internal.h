@@ -27,6 +27,10 @@ struct rnn_ctx {
     hipStream_t stream = nullptr;
     bool own_stream = false;
     int num_cus = 256;
+    // Device address of this device's copy of the fixed scratch array of the
+    // no-allocation entry points (RNN_NOALLOC_SCRATCH_BYTES, rnn_ctx.hip),
+    // looked up once per device by rnn_ctx_create.
+    float *noalloc_scratch = nullptr;
     // Growing device workspace (split-K partials, packed weights, attention
     // reductions).  Reallocated only when a call needs more; the stream is
     // synchronised first so no in-flight kernel still reads the old block.
@@ -46,6 +50,9 @@ struct rnn_ctx {
     std::recursive_mutex mu;
     char err[512] = {0};
 };
+
+// Size of the fixed device scratch behind rnn_conv2d_backward_w_noalloc.
+#define RNN_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
 
 // Records a message and returns `code`.
 int rnn_fail(rnn_ctx *ctx, int code, const char *fmt, ...);
@@ -244,9 +251,11 @@ int rnn_conv2d_forward_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
                           const float *w, const float *wp, float *y);
 int rnn_conv2d_backward_x_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
                              const float *w, const float *wp, float *dx);
-// dW += over the batch (k = 1 or 3).
+// dW += over the batch (k = 1 or 3).  The partial slabs go to `part` (room
+// for `cap` floats; RNN_E_UNSUPPORTED when the plan needs more) or, with part
+// null, to the context workspace.
 int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy, const float *x,
-                float *dw);
+                float *dw, float *part = nullptr, size_t cap = 0);
 // The same dW left as *nz partial slabs of cout*cin*k*k floats in `slabs`
 // (rnn_conv_dw_slab_floats(...) floats, 0 when the shape is unsupported);
 // their slab-order sum is added by rnn_grad_finalize_launch.
