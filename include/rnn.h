@@ -297,6 +297,11 @@ int rnn_soft_targets(rnn_ctx *ctx, size_t n, size_t nf, size_t nc, const uint32_
                      const uint32_t *coarse, const uint32_t *perm, const float *lam,
                      const uint32_t *parent, int taxo, float eps, float sib, float *tf,
                      float *tc);
+/* The dominant label of each mixed image (Trainer::make_batch,
+ * train.rs:313-320): dom[i] = labels[i] when lam[i] >= 0.5, else
+ * labels[perm[i]] -- the hard label ce_soft counts hits against. */
+int rnn_mix_dominant(rnn_ctx *ctx, size_t n, const uint32_t *labels, const uint32_t *perm,
+                     const float *lam, uint32_t *dom);
 /* ce_soft (loss.rs:39-83): dz [n][nclass] overwritten with scale (softmax -
  * target) / n; *loss (device, may be NULL) the mean loss; *correct (device,
  * may be NULL) the argmax hits against hard. */
@@ -366,6 +371,13 @@ uint64_t rnn_fnv1a_f32(uint64_t hash, const float *values, size_t n);
 /* The host generator of the trainer (rng.rs): state = Rng::new(seed); next. */
 int rnn_rng_seed(uint64_t seed, uint64_t *state);
 uint64_t rnn_rng_next_u64(uint64_t *state);
+/* Normal draws from the caller's generator state (4 u64, advanced), host
+ * only: rand_vec (rng.rs:70-72) times scale -- Param::kaiming (nn.rs:95-100)
+ * with scale = sqrt(2 / fan_in) as f32 -- and Param::trunc_normal
+ * (nn.rs:77-89): up to 8 redraws while |z| > 2, clamped to [-2, 2], times
+ * std.  The initial weights of the reference's models, bit for bit. */
+int rnn_rng_normal_vec(uint64_t *state, size_t n, float scale, float *out);
+int rnn_rng_trunc_normal(uint64_t *state, size_t n, float std_, float *out);
 /* mix_batch's draws (data.rs:469-492) from the caller's generator state (4
  * u64, advanced): perm [bs] (shuffle), lam [bs], *cut (cutmix or mixup), *l
  * and, for cutmix, rect = y0, y1, x0, x1.  Host only. */
@@ -429,6 +441,9 @@ int rnn_ema_update_params(rnn_ctx *ctx, size_t nparam, float *const *w, const rn
                           float d);
 /* f32::powi as the reference's bias corrections compute it. */
 float rnn_powi_f32(float a, int b);
+/* lr_at (train.rs:21-28), host only: linear warm-up over `warm` steps, then a
+ * cosine from peak down to lo at step `total`, in f32. */
+float rnn_lr_at(float peak, float lo, size_t step, size_t total, size_t warm);
 
 /* ----------------------------------------------------------- model.rs */
 /* Device-resident CIFAR ResNet (ResNet::new, model.rs:113-135): depth_n

@@ -62,6 +62,7 @@ float orc_rng_uniform(orc_rng *r);
 float orc_rng_normal(orc_rng *r);
 void orc_rand_vec(orc_rng *r, float *out, size_t n);
 void orc_rand_uniform_vec(orc_rng *r, float *out, size_t n);
+void orc_trunc_normal(orc_rng *r, float *out, size_t n, float std_);
 void orc_rng_shuffle(orc_rng *r, size_t *v, size_t n);
 
 /* ------------------------------------------------------------- threading */
@@ -193,6 +194,7 @@ void orc_adam_step(size_t n, float *v, float *g, float *m, float *v2, int decay,
                    float wd, float b1, float b2, float eps, size_t t);
 float orc_clip(float *g, const size_t *lens, size_t nseg, float max);
 void orc_ema_update(size_t n, float *w, const float *v, float decay, size_t t);
+float orc_lr_at(float peak, float lo, size_t step, size_t total, size_t warm);
 
 /* ---------------------------------------------------------------- norm.rs */
 void orc_ln_forward(size_t rows, size_t c, const float *x, const float *g, const float *b,

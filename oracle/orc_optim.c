@@ -131,3 +131,12 @@ void orc_ema_update(size_t n, float *w, const float *v, float decay, size_t t) {
     const float d = decay < ceil_d ? decay : ceil_d;
     for (size_t i = 0; i < n; i++) w[i] = d * w[i] + (1.0f - d) * v[i];
 }
+
+/* lr_at (train.rs:21-28): linear warm-up, then a cosine to lo; f32 with the
+ * C library's cosf (Rust's f32::cos on linux-gnu). */
+float orc_lr_at(float peak, float lo, size_t step, size_t total, size_t warm) {
+    if (warm > 0 && step < warm) return lo + (peak - lo) * (float)(step + 1) / (float)warm;
+    const size_t span = total > warm ? total - warm : 1;
+    const float t = (float)(step - warm) / (float)span;
+    return lo + 0.5f * (peak - lo) * (1.0f + cosf(3.14159265358979323846f * t));
+}

@@ -69,6 +69,22 @@ void orc_rand_uniform_vec(orc_rng *r, float *out, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] = orc_rng_uniform(r);
 }
 
+/* Param::trunc_normal (nn.rs:77-89): a normal, redrawn at most 8 times while
+ * |z| > 2, clamped to [-2, 2] (f32::clamp), times std. */
+void orc_trunc_normal(orc_rng *r, float *out, size_t n, float std_) {
+    for (size_t i = 0; i < n; i++) {
+        float z = orc_rng_normal(r);
+        int tries = 0;
+        while (fabsf(z) > 2.0f && tries < 8) {
+            z = orc_rng_normal(r);
+            tries++;
+        }
+        if (z < -2.0f) z = -2.0f;
+        if (z > 2.0f) z = 2.0f;
+        out[i] = z * std_;
+    }
+}
+
 /* Rng::shuffle (rng.rs:61-65): Fisher-Yates from the top. */
 void orc_rng_shuffle(orc_rng *r, size_t *v, size_t n) {
     for (size_t i = n; i-- > 1;) {

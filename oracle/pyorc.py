@@ -85,6 +85,7 @@ def lib():
         L.orc_rng_normal.restype = C.c_float
         L.orc_rand_vec.argtypes = [P(RngState), _f32p, _sz]
         L.orc_rand_uniform_vec.argtypes = [P(RngState), _f32p, _sz]
+        L.orc_trunc_normal.argtypes = [P(RngState), _f32p, _sz, C.c_float]
         L.orc_set_threads.argtypes = [C.c_int]
         L.orc_set_threads.restype = C.c_int
         L.orc_get_threads.restype = C.c_int
@@ -148,6 +149,8 @@ def lib():
         L.orc_clip.argtypes = [_f32p, P(_sz), _sz, C.c_float]
         L.orc_clip.restype = C.c_float
         L.orc_ema_update.argtypes = [_sz, _f32p, _f32p, C.c_float, _sz]
+        L.orc_lr_at.argtypes = [C.c_float, C.c_float, _sz, _sz, _sz]
+        L.orc_lr_at.restype = C.c_float
         vp = C.c_void_p
         L.orc_ln_forward.argtypes = [_sz, _sz, _f32p, _f32p, _f32p, C.c_float, _f32p, vp, vp]
         L.orc_ln_backward.argtypes = [_sz, _sz, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p]
@@ -216,6 +219,13 @@ class Rng:
         out = np.empty(n, np.float32)
         if n:
             lib().orc_rand_vec(C.byref(self.st), out, n)
+        return out
+
+    def trunc_normal(self, n: int, std) -> np.ndarray:
+        """Param::trunc_normal's values (nn.rs:77-89); std is an f32."""
+        out = np.empty(n, np.float32)
+        if n:
+            lib().orc_trunc_normal(C.byref(self.st), out, n, float(np.float32(std)))
         return out
 
     def uniform_vec(self, n: int) -> np.ndarray:
@@ -539,6 +549,11 @@ def ema_update(w, v, decay, t):
     """Ema::update (optim.rs:270-288) after the first call, in place on w."""
     _chk(w)
     lib().orc_ema_update(w.size, w, _f(v).ravel(), decay, t)
+
+
+def lr_at(peak, lo, step, total, warm):
+    """lr_at (train.rs:21-28)."""
+    return float(lib().orc_lr_at(peak, lo, step, total, warm))
 
 
 # ---------------------------------------------------------------- norm.rs

@@ -168,6 +168,8 @@ def lib():
             "rnn_fnv1a_bytes": (C.c_uint64, [C.c_uint64, _vp, _sz]),
             "rnn_fnv1a_f32": (C.c_uint64, [C.c_uint64, _vp, _sz]),
             "rnn_rng_next_u64": (C.c_uint64, [_vp]),
+            "rnn_rng_normal_vec": (_i, [_vp, _sz, C.c_float, _vp]),
+            "rnn_rng_trunc_normal": (_i, [_vp, _sz, C.c_float, _vp]),
             "rnn_mix_plan": (_i, [_vp, _sz, C.c_float, C.c_float, C.c_float, _vp, _vp, _vp, _vp,
                                   _vp]),
             "rnn_mix_apply": (_i, [_vp, _vp, _vp, _sz, _vp, C.c_int, C.c_float, _vp]),
@@ -182,6 +184,7 @@ def lib():
             "rnn_tokens_to_nchw": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
             "rnn_soft_targets": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, C.c_int,
                                       C.c_float, C.c_float, _vp, _vp]),
+            "rnn_mix_dominant": (_i, [_vp, _sz, _vp, _vp, _vp, _vp]),
             "rnn_ce_soft": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp]),
             "rnn_kl_distill": (_i, [_vp, _sz, _sz, _vp, _vp, C.c_float, C.c_float, _vp, _vp]),
             "rnn_hint_mse": (_i, [_vp, _sz, _sz, _vp, _vp, C.c_float, _vp, _vp]),
@@ -198,6 +201,7 @@ def lib():
             "rnn_seqpool_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_ema_update_params": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
             "rnn_powi_f32": (C.c_float, [C.c_float, _i]),
+            "rnn_lr_at": (C.c_float, [C.c_float, C.c_float, _sz, _sz, _sz]),
             "rnn_resnet_logits": (_i, [_vp, _vp]),
             "rnn_resnet_set_graph": (_i, [_vp, _i]),
             "rnn_resnet_graph_state": (_i, [_vp, P(C.c_char_p)]),

@@ -415,6 +415,32 @@ uint64_t rnn_rng_next_u64(uint64_t *state) {
     return v;
 }
 
+int rnn_rng_normal_vec(uint64_t *state, size_t n, float scale, float *out) {
+    if (!state || (n && !out)) return RNN_E_NULL;
+    // rand_vec (rng.rs:70-72) times scale: Param::kaiming (nn.rs:95-100)
+    // passes scale = sqrt(2 / fan_in) as f32, rand_vec passes 1.
+    RnnRng r(0);
+    for (int k = 0; k < 4; k++) r.s[k] = state[k];
+    for (size_t i = 0; i < n; i++) out[i] = r.normal() * scale;
+    for (int k = 0; k < 4; k++) state[k] = r.s[k];
+    return RNN_OK;
+}
+
+int rnn_rng_trunc_normal(uint64_t *state, size_t n, float std_, float *out) {
+    if (!state || (n && !out)) return RNN_E_NULL;
+    // Param::trunc_normal (nn.rs:77-89): up to 8 redraws while |z| > 2, then
+    // clamp to [-2, 2] and scale.
+    RnnRng r(0);
+    for (int k = 0; k < 4; k++) r.s[k] = state[k];
+    for (size_t i = 0; i < n; i++) {
+        float z = r.normal();
+        for (int tries = 0; fabsf(z) > 2.0f && tries < 8; tries++) z = r.normal();
+        out[i] = fminf(fmaxf(z, -2.0f), 2.0f) * std_;
+    }
+    for (int k = 0; k < 4; k++) state[k] = r.s[k];
+    return RNN_OK;
+}
+
 int rnn_mix_plan(uint64_t *rng_state, size_t bs, float alpha_mix, float alpha_cut, float sw,
                  uint32_t *perm, float *lam, int *cut, float *l, int *rect) {
     if (!rng_state || !perm || !lam || !cut || !l || !rect) return RNN_E_NULL;

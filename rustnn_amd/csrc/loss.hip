@@ -180,6 +180,18 @@ __device__ __forceinline__ float taxo_at(int y, int j, int nf, const uint32_t *p
 }
 
 // targets (train.rs:121-155): tf[i][j] = lam a_j + (1 - lam) b_j with a, b the
+// The dominant label of a mixed image (Trainer::make_batch, train.rs:313-320):
+// its own label when lam >= 0.5, else its partner's.  A partner index out of
+// range gives 0xffffffff, which no hit count matches.
+__global__ void dominant_kernel(size_t n, const uint32_t *__restrict__ labels,
+                                const uint32_t *__restrict__ perm, const float *__restrict__ lam,
+                                uint32_t *__restrict__ dom) {
+    const size_t i = (size_t)blockIdx.x * NT + threadIdx.x;
+    if (i >= n) return;
+    const size_t pi = perm[i];
+    dom[i] = lam[i] >= 0.5f ? labels[i] : (pi < n ? labels[pi] : 0xffffffffu);
+}
+
 // fine targets of labels[i] and labels[perm[i]] (taxonomy or uniform); tc the
 // same over the coarse labels with uniform smoothing.
 __global__ void targets_kernel(size_t n, int nf, int nc, const uint32_t *__restrict__ labels,
@@ -251,6 +263,19 @@ int rnn_soft_targets(rnn_ctx *ctx, size_t n, size_t nf, size_t nc, const uint32_
     const unsigned grid = (unsigned)std::min<size_t>(rnn_div_up(len, NT), 4096);
     targets_kernel<<<grid, NT, 0, ctx->stream>>>(n, (int)nf, (int)nc, labels, coarse, perm, lam,
                                                  parent, taxo, eps, sib, tf, tc);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_mix_dominant(rnn_ctx *ctx, size_t n, const uint32_t *labels, const uint32_t *perm,
+                     const float *lam, uint32_t *dom) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0) return RNN_OK;
+    if (!labels || !perm || !lam || !dom)
+        return rnn_fail(ctx, RNN_E_NULL, "mix_dominant: null operand");
+    dominant_kernel<<<(unsigned)rnn_div_up(n, NT), NT, 0, ctx->stream>>>(n, labels, perm, lam,
+                                                                           dom);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

@@ -853,4 +853,13 @@ int rnn_ema_update_params(rnn_ctx *ctx, size_t nparam, float *const *w, const rn
 
 float rnn_powi_f32(float a, int b) { return powi_f32(a, b); }
 
+// lr_at (train.rs:21-28) in f32 with the C library's cosf, the function the
+// reference's f32::cos calls.
+float rnn_lr_at(float peak, float lo, size_t step, size_t total, size_t warm) {
+    if (warm > 0 && step < warm) return lo + (peak - lo) * (float)(step + 1) / (float)warm;
+    const size_t span = total > warm ? total - warm : 1;
+    const float t = (float)(step - warm) / (float)span;
+    return lo + 0.5f * (peak - lo) * (1.0f + cosf(3.14159265358979323846f * t));
+}
+
 }  // extern "C"

@@ -130,6 +130,25 @@ class Rng:
     def next_u64(self):
         return int(lib().rnn_rng_next_u64(C.cast(self.state, _vp)))
 
+    def normal_vec(self, n, scale=1.0):
+        """rand_vec (rng.rs:70-72) times an f32 scale (Param::kaiming with
+        scale = sqrt(2 / fan_in), nn.rs:95-100), drawn on the host."""
+        out = np.empty(n, np.float32)
+        rc = lib().rnn_rng_normal_vec(C.cast(self.state, _vp), n, float(np.float32(scale)),
+                                      out.ctypes.data)
+        if rc:
+            raise RnnError(rc, "rng normal_vec failed")
+        return out
+
+    def trunc_normal(self, n, std):
+        """Param::trunc_normal's values (nn.rs:77-89), drawn on the host."""
+        out = np.empty(n, np.float32)
+        rc = lib().rnn_rng_trunc_normal(C.cast(self.state, _vp), n, float(np.float32(std)),
+                                        out.ctypes.data)
+        if rc:
+            raise RnnError(rc, "rng trunc_normal failed")
+        return out
+
 
 def mix_batch(x, alpha_mix, alpha_cut, switch, rng, ctx=None):
     """mix_batch (data.rs:469-492): the permutation, lambda and cutmix box

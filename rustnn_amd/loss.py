@@ -28,6 +28,18 @@ def soft_targets(labels, nf, eps, parent=None, sib=0.0, coarse=None, nc=0, perm=
     return tf, tc
 
 
+def mix_dominant(labels, perm, lam, ctx=None):
+    """The dominant label of each mixed image (train.rs:313-320): labels[i]
+    when lam[i] >= 0.5, else labels[perm[i]] (CUDA int32)."""
+    import torch
+    ctx = ctx or default_ctx()
+    n = labels.numel()
+    dom = torch.empty(n, dtype=torch.int32, device=labels.device)
+    ctx.check(lib().rnn_mix_dominant(ctx.h, n, _ptr(labels, n, "labels"), _ptr(perm, n, "perm"),
+                                     _ptr(lam, n, "lam"), _ptr(dom, n, "dom")))
+    return dom
+
+
 def ce_soft(logits, target, hard, scale, dz=None, ctx=None):
     """ce_soft (loss.rs:39-83): returns (loss, correct, dz) with loss and
     correct as 1-element device tensors; dz [n, nclass] overwritten."""

@@ -6,40 +6,59 @@ over token tensors [n, t, c] (float32 CUDA, channel fastest):
 ``forward(x, ..., train)`` / ``backward(dy, ...)``; parameter gradients
 accumulate into ``rustnn_amd.optim.Param.g`` and ``for_each_param`` walks
 the parameters in the reference's order, so a list of them feeds
-``Optim.step_all`` / ``clip_`` / ``Ema`` directly.  Initial values are drawn
-with torch's generator (truncated normal as Param::trunc_normal), not with
-the reference's Rng stream.  Every compute call goes through librnn.so.
+``Optim.step_all`` / ``clip_`` / ``Ema`` directly.  Initial values come from
+the reference's generator (rng.rs, ``rustnn_amd.data.Rng``) in the
+reference's draw order, so a network built from a seed holds the same
+weights as the reference's built from that seed, bit for bit.  Every compute
+call goes through librnn.so.
 """
 from __future__ import annotations
 
-import math
+
+import numpy as np
 
 from . import Core, Linear, _ptr, default_ctx, lib, rel_index
+from .data import Rng
 from .norm import DwConv3, LayerNorm, LayerScale, SeqPool, SwiGlu, _linear_param
 from .optim import Param
 
 
-def _trunc_normal(n, std, gen, device):
-    """Param::trunc_normal (nn.rs:77-89) in distribution: N(0, 1) clamped to
-    +-2 (the reference redraws up to 8 times first), times std."""
+def _rng(rng, seed):
+    """A generator argument: an Rng, a seed, or None (Rng::new(seed))."""
+    if rng is None:
+        return Rng(seed)
+    return Rng(rng) if isinstance(rng, int) else rng
+
+
+def _trunc_normal(n, std, rng, device):
+    """Param::trunc_normal (nn.rs:77-89) from the reference's generator: a
+    normal redrawn up to 8 times while |z| > 2, clamped to [-2, 2], times
+    std (an f32)."""
     import torch
-    z = torch.randn(n, generator=gen, device=device)
-    for _ in range(8):
-        bad = z.abs() > 2.0
-        if not bool(bad.any()):
-            break
-        z = torch.where(bad, torch.randn(n, generator=gen, device=device), z)
-    return z.clamp(-2.0, 2.0) * std
+    return torch.from_numpy(rng.trunc_normal(n, std)).to(device)
 
 
-def _linear(fin, fout, bias, std, gen, device, ctx):
-    w = _trunc_normal(fin * fout, std, gen, device)
+def _kaiming(fan_in, n, rng, device):
+    """Param::kaiming (nn.rs:95-100): normal() * sqrt(2 / fan_in) in f32."""
+    import torch
+    s = np.sqrt(np.float32(2.0) / np.float32(fan_in))
+    return torch.from_numpy(rng.normal_vec(n, s)).to(device)
+
+
+def _linear(fin, fout, bias, std, rng, device, ctx):
+    """Linear::new (linear.rs:25-35): w [fout, fin] trunc_normal(std), b 0."""
+    w = _trunc_normal(fin * fout, std, rng, device)
     return Linear(fin, fout, bias, w, None, 0, ctx)
 
 
+def _inv_sqrt(dh):
+    """1 / sqrt(dh) in f32: tau's initial value (attn.rs:371, 479)."""
+    return float(np.float32(1.0) / np.sqrt(np.float32(dh)))
+
+
 def _scaled_std(depth):
-    """Linear::scaled (linear.rs:37-41)."""
-    return 0.02 / math.sqrt(2.0 * depth)
+    """Linear::scaled (linear.rs:37-41): 0.02 / sqrt(2 depth), in f32."""
+    return np.float32(0.02) / np.sqrt(np.float32(2.0) * np.float32(depth))
 
 
 def _add_(a, b, ctx):
@@ -51,16 +70,16 @@ class SelfAttn:
     """SelfAttn (attn.rs:346-448): fused qkv Linear(c, 3c) -> Core (masked
     diagonal) -> proj Linear::scaled; tau = 1/sqrt(dh), rel = 0."""
 
-    def __init__(self, c, h, th, tw, depth, gen=None, device=0, ctx=None):
+    def __init__(self, c, h, th, tw, depth, rng=None, device=0, ctx=None):
         import torch
         dev = f"cuda:{device}"
         self.ctx = ctx or default_ctx(device)
-        gen = gen or torch.Generator(device=dev).manual_seed(0)
+        rng = _rng(rng, 0)
         self.c, self.h, self.dh, self.t = c, h, c // h, th * tw
         relidx, nrel = rel_index(th, tw, th, tw)
-        self.qkv = _linear(c, 3 * c, True, 0.02, gen, dev, self.ctx)
-        self.proj = _linear(c, c, True, _scaled_std(depth), gen, dev, self.ctx)
-        self.tau = Param(torch.full((h,), 1.0 / math.sqrt(self.dh), device=dev), False)
+        self.qkv = _linear(c, 3 * c, True, 0.02, rng, dev, self.ctx)
+        self.proj = _linear(c, c, True, _scaled_std(depth), rng, dev, self.ctx)
+        self.tau = Param(torch.full((h,), _inv_sqrt(self.dh), device=dev), False)
         self.rel = Param(torch.zeros(h * nrel, device=dev), False)
         self.core = Core(h, self.dh, self.t, self.t, relidx, nrel, True, ctx=self.ctx)
         self._lin = _linear_param(self.qkv) + _linear_param(self.proj)
@@ -97,17 +116,17 @@ class CrossAttn:
     """CrossAttn (attn.rs:450-560): wq Linear(c, c) -> Core over the memory
     [n, mh*mw, 2c] (K at 0, V at c), no mask -> proj Linear::scaled."""
 
-    def __init__(self, c, h, th, tw, mh, mw, depth, gen=None, device=0, ctx=None):
+    def __init__(self, c, h, th, tw, mh, mw, depth, rng=None, device=0, ctx=None):
         import torch
         dev = f"cuda:{device}"
         self.ctx = ctx or default_ctx(device)
-        gen = gen or torch.Generator(device=dev).manual_seed(0)
+        rng = _rng(rng, 0)
         self.c, self.h, self.dh = c, h, c // h
         self.tq, self.tk = th * tw, mh * mw
         relidx, nrel = rel_index(th, tw, mh, mw)
-        self.wq = _linear(c, c, True, 0.02, gen, dev, self.ctx)
-        self.proj = _linear(c, c, True, _scaled_std(depth), gen, dev, self.ctx)
-        self.tau = Param(torch.full((h,), 1.0 / math.sqrt(self.dh), device=dev), False)
+        self.wq = _linear(c, c, True, 0.02, rng, dev, self.ctx)
+        self.proj = _linear(c, c, True, _scaled_std(depth), rng, dev, self.ctx)
+        self.tau = Param(torch.full((h,), _inv_sqrt(self.dh), device=dev), False)
         self.rel = Param(torch.zeros(h * nrel, device=dev), False)
         self.core = Core(h, self.dh, self.tq, self.tk, relidx, nrel, False, ctx=self.ctx)
         self._lin = _linear_param(self.wq) + _linear_param(self.proj)
@@ -177,25 +196,27 @@ class Block:
     h = LN(x); x += ls1 * dp1(SelfAttn(h) + gamma * DwConv3(h));
     x += lsm * dp2(CrossAttn(h, mem)) (reader blocks); x += ls2 * dp3(SwiGlu(LN(x)))."""
 
-    def __init__(self, c, h, th, tw, mem, depth, drop, idx, ls_init, gen=None, device=0,
+    def __init__(self, c, h, th, tw, mem, depth, drop, idx, ls_init, rng=None, device=0,
                  ctx=None):
+        """Block::new (vit.rs:117-143): draws, in order, SelfAttn (qkv, proj),
+        DwConv3, CrossAttn (wq, proj) for a reader block, SwiGlu (wg, wd)."""
         import torch
         dev = f"cuda:{device}"
         self.ctx = ctx or default_ctx(device)
-        gen = gen or torch.Generator(device=dev).manual_seed(int(idx))
+        rng = _rng(rng, int(idx))
         self.c, self.idx = c, int(idx)
         hidden = -(-(4 * c // 3) // 16) * 16
         self.n1 = LayerNorm(c, device, self.ctx)
-        self.attn = SelfAttn(c, h, th, tw, depth, gen, device, self.ctx)
-        self.dw = DwConv3(c, th, tw, _trunc_normal(9 * c, 0.1, gen, dev), None, device, self.ctx)
+        self.attn = SelfAttn(c, h, th, tw, depth, rng, device, self.ctx)
+        self.dw = DwConv3(c, th, tw, _trunc_normal(9 * c, 0.1, rng, dev), None, device, self.ctx)
         self.gamma = Param(torch.full((c,), 0.5, device=dev), False)
         self.ls1 = LayerScale(c, ls_init, device, self.ctx)
-        self.cross = (CrossAttn(c, h, th, tw, mem[0], mem[1], depth, gen, device, self.ctx)
+        self.cross = (CrossAttn(c, h, th, tw, mem[0], mem[1], depth, rng, device, self.ctx)
                       if mem else None)
         self.lsm = LayerScale(c, ls_init, device, self.ctx) if mem else None
         self.n2 = LayerNorm(c, device, self.ctx)
-        wg = _trunc_normal(2 * hidden * c, 0.02, gen, dev)
-        wd = _trunc_normal(hidden * c, _scaled_std(depth), gen, dev)
+        wg = _trunc_normal(2 * hidden * c, 0.02, rng, dev)
+        wd = _trunc_normal(hidden * c, _scaled_std(depth), rng, dev)
         self.mlp = SwiGlu(c, hidden, wg, None, wd, None, device, self.ctx)
         self.ls2 = LayerScale(c, ls_init, device, self.ctx)
         self.dp1, self.dp2, self.dp3 = (DropPath(drop, self.ctx), DropPath(drop, self.ctx),
@@ -295,14 +316,13 @@ class TaxoHead:
     """TaxoHead (vit.rs:254-318): coarse Linear(c, nc), resid Linear(c, nf);
     fine logits z_f[j] = z_c[parent[j]] + r[j].  parent: CUDA int32/uint32."""
 
-    def __init__(self, c, parent, nc, gen=None, device=0, ctx=None):
-        import torch
+    def __init__(self, c, parent, nc, rng=None, device=0, ctx=None):
         dev = f"cuda:{device}"
         self.ctx = ctx or default_ctx(device)
-        gen = gen or torch.Generator(device=dev).manual_seed(1)
+        rng = _rng(rng, 1)
         self.parent, self.nc, self.nf = parent, nc, parent.numel()
-        self.coarse = _linear(c, nc, True, 0.02, gen, dev, self.ctx)
-        self.resid = _linear(c, self.nf, True, 0.02, gen, dev, self.ctx)
+        self.coarse = _linear(c, nc, True, 0.02, rng, dev, self.ctx)
+        self.resid = _linear(c, self.nf, True, 0.02, rng, dev, self.ctx)
         self._params = _linear_param(self.coarse) + _linear_param(self.resid)
         self.n = 0
 
@@ -336,13 +356,12 @@ class Exit:
     """Exit (vit.rs:320-353): fc Linear(cin, nclass) and hint Linear(cin,
     chint, no bias) over the same feature."""
 
-    def __init__(self, cin, nclass, chint, gen=None, device=0, ctx=None):
-        import torch
+    def __init__(self, cin, nclass, chint, rng=None, device=0, ctx=None):
         dev = f"cuda:{device}"
         self.ctx = ctx or default_ctx(device)
-        gen = gen or torch.Generator(device=dev).manual_seed(2)
-        self.fc = _linear(cin, nclass, True, 0.02, gen, dev, self.ctx)
-        self.hint = _linear(cin, chint, False, 0.02, gen, dev, self.ctx)
+        rng = _rng(rng, 2)
+        self.fc = _linear(cin, nclass, True, 0.02, rng, dev, self.ctx)
+        self.hint = _linear(cin, chint, False, 0.02, rng, dev, self.ctx)
         self._params = _linear_param(self.fc) + _linear_param(self.hint)
         self.n = 0
 
@@ -396,12 +415,11 @@ def _optim_param(v, g, decay):
 class _ConvBN:
     """Conv2d (nn.rs:115-250) followed by BatchNorm2d (nn.rs:253-428), NCHW."""
 
-    def __init__(self, cin, cout, k, stride, pad, gen, dev, device, ctx, relu=False):
-        import torch
+    def __init__(self, cin, cout, k, stride, pad, rng, dev, device, ctx, relu=False):
         from . import Conv2d
         from .nn import BatchNorm2d
         fan = cin * k * k
-        w = torch.randn(cout * fan, generator=gen, device=dev) * math.sqrt(2.0 / fan)
+        w = _kaiming(fan, cout * fan, rng, dev)
         self.conv = Conv2d(cin, cout, k, stride, pad, w, device, ctx)
         self.bn = BatchNorm2d(cout, device, ctx)
         self.relu, self.cout, self.k, self.stride, self.pad = relu, cout, k, stride, pad
@@ -433,12 +451,13 @@ class BasicBlock:
     """BasicBlock (model.rs:10-107): conv-BN-ReLU, conv-BN (gamma 0), a 1x1
     conv-BN shortcut when the shape changes, add + ReLU."""
 
-    def __init__(self, cin, cout, stride, gen, dev, device, ctx):
+    def __init__(self, cin, cout, stride, rng, dev, device, ctx):
+        """BasicBlock::new (model.rs:20-39): draws c1, c2, then the shortcut."""
         self.ctx = ctx
-        self.a = _ConvBN(cin, cout, 3, stride, 1, gen, dev, device, ctx, relu=True)
-        self.b = _ConvBN(cout, cout, 3, 1, 1, gen, dev, device, ctx)
+        self.a = _ConvBN(cin, cout, 3, stride, 1, rng, dev, device, ctx, relu=True)
+        self.b = _ConvBN(cout, cout, 3, 1, 1, rng, dev, device, ctx)
         self.b.bn.zero_gamma()
-        self.down = (_ConvBN(cin, cout, 1, stride, 0, gen, dev, device, ctx)
+        self.down = (_ConvBN(cin, cout, 1, stride, 0, rng, dev, device, ctx)
                      if stride != 1 or cin != cout else None)
         self.h1 = self.out = None
 
@@ -478,43 +497,49 @@ class RustViT:
     the superclass of each fine class (CUDA int32); seed seeds the weights."""
 
     def __init__(self, cfg=None, parent=None, ncoarse=20, seed=0, device=0, ctx=None):
+        """RustViT::new (vit.rs:432-507): one Rng::new(seed) drawn in the
+        reference's order -- the stage-3 blocks, the stage-4 blocks, then the
+        stem, c1, c2, the memory conv, the token conv, the merge Linear, the
+        pool, the head, exit 1, pool2 and exit 2 -- so the weights equal the
+        reference's bit for bit."""
         import torch
         cfg = dict(VIT_DEFAULT, **(cfg or {}))
         dev = f"cuda:{device}"
         self.cfg, self.ctx = cfg, ctx or default_ctx(device)
-        gen = torch.Generator(device=dev).manual_seed(int(seed))
+        rng = Rng(int(seed))
         w, cm, d, d4 = cfg["width"], cfg["cmid"], cfg["dim"], cfg["dim4"]
         self.mh, self.th = cfg["img"] // 2, cfg["img"] // 4
         depth = cfg["depth3"] + cfg["depth4"]
         nf = parent.numel()
         self.nclass, ctx = nf, self.ctx
         self.parent_host = [int(v) for v in parent.cpu().tolist()]  # the checkpoint hash
-        self.stem = _ConvBN(3, w, 3, 1, 1, gen, dev, device, ctx, relu=True)
-        self.c1 = BasicBlock(w, w, 1, gen, dev, device, ctx)
-        self.c2 = BasicBlock(w, cm, 2, gen, dev, device, ctx)
-        from . import Conv2d
-        mw = torch.randn(2 * d * cm, generator=gen, device=dev) * math.sqrt(2.0 / cm)
-        self.memconv = Conv2d(cm, 2 * d, 1, 1, 0, mw, device, ctx)
-        self.memln = LayerNorm(2 * d, device, ctx)
-        self.tok = _ConvBN(cm, d, 3, 2, 1, gen, dev, device, ctx)
-        div = max(depth, 2) - 1
+        # DropPath rate cfg.droppath * i / (max(depth, 2) - 1), in f32
+        div = np.float32(max(depth, 2) - 1)
+        rate = lambda i: float(np.float32(cfg["droppath"]) * np.float32(i) / div)
         self.blocks3 = [Block(d, cfg["heads"], self.th, self.th,
                               (self.mh, self.mh) if i in cfg["mem_at"] else None, depth,
-                              cfg["droppath"] * i / div, i + 1, 1e-4, gen, device, ctx)
+                              rate(i), i + 1, 1e-4, rng, device, ctx)
                         for i in range(cfg["depth3"])]
-        self.mergeln = LayerNorm(4 * d, device, ctx)
-        self.merge = _linear(4 * d, d4, True, 0.02, gen, dev, ctx)
         th4 = self.th // 2
         self.blocks4 = [Block(d4, cfg["heads4"], th4, th4, None, depth,
-                              cfg["droppath"] * (cfg["depth3"] + i) / div,
-                              cfg["depth3"] + i + 1, 1e-4, gen, device, ctx)
+                              rate(cfg["depth3"] + i), cfg["depth3"] + i + 1, 1e-4, rng, device,
+                              ctx)
                         for i in range(cfg["depth4"])]
+        self.stem = _ConvBN(3, w, 3, 1, 1, rng, dev, device, ctx, relu=True)
+        self.c1 = BasicBlock(w, w, 1, rng, dev, device, ctx)
+        self.c2 = BasicBlock(w, cm, 2, rng, dev, device, ctx)
+        from . import Conv2d
+        self.memconv = Conv2d(cm, 2 * d, 1, 1, 0, _kaiming(cm, 2 * d * cm, rng, dev), device, ctx)
+        self.memln = LayerNorm(2 * d, device, ctx)
+        self.tok = _ConvBN(cm, d, 3, 2, 1, rng, dev, device, ctx)
+        self.mergeln = LayerNorm(4 * d, device, ctx)
+        self.merge = _linear(4 * d, d4, True, 0.02, rng, dev, ctx)
         self.headln = LayerNorm(d4, device, ctx)
-        self.pool = SeqPool(d4, _trunc_normal(d4, 0.02, gen, dev), device, ctx)
-        self.head = TaxoHead(d4, parent, ncoarse, gen, device, ctx)
-        self.e1 = Exit(cm, nf, d4, gen, device, ctx)
-        self.pool2 = SeqPool(d, _trunc_normal(d, 0.02, gen, dev), device, ctx)
-        self.e2 = Exit(d, nf, d4, gen, device, ctx)
+        self.pool = SeqPool(d4, _trunc_normal(d4, 0.02, rng, dev), device, ctx)
+        self.head = TaxoHead(d4, parent, ncoarse, rng, device, ctx)
+        self.e1 = Exit(cm, nf, d4, rng, device, ctx)
+        self.pool2 = SeqPool(d, _trunc_normal(d, 0.02, rng, dev), device, ctx)
+        self.e2 = Exit(d, nf, d4, rng, device, ctx)
         self.memw = _optim_param(self.memconv.w, self.memconv.g, True)
         self.mergep = _linear_param(self.merge)
         self.use_exits, self.drop_seed = True, 0
@@ -630,63 +655,126 @@ class RustViT:
         return ps
 
 
+# Config defaults of the rustvit trainer (cli.rs:62-120): loss weights, clip,
+# EMA, the optimiser and the learning-rate schedule's budget (ntrain images,
+# epochs and warm-up epochs at this batch size).
 VIT_TRAIN = dict(smooth=0.1, sib=0.7, coarse_w=0.4, exit_w=(0.3, 0.6), alpha=1.0, temp=3.0,
-                 beta=0.03, clip=1.0, ema=0.9998, lr=6e-4, wd=0.06, ns=3)
+                 beta=0.03, clip=1.0, ema=0.9998, ema_auto=True, lr=6e-4, lr_min=1e-5, wd=0.06,
+                 muon=True, ns=3, no_taxo=False, seed=1234, batch=128, ntrain=50000, epochs=100,
+                 warmup=10)
+
+
+def lr_at(peak, lo, step, total, warm):
+    """lr_at (train.rs:21-28), in f32 (rnn_lr_at): linear warm-up, then a
+    cosine down to lo."""
+    return float(lib().rnn_lr_at(float(np.float32(peak)), float(np.float32(lo)), int(step),
+                                 int(total), int(warm)))
 
 
 class ViTStep:
-    """One Trainer::step of the rustvit (train.rs:340-380) on the device:
-    forward, soft targets (train.rs:121-155, taxonomy smoothing, no mixup
-    here), build_loss (train.rs:70-118: fine and coarse soft-target CE, the
-    two exits' CE, their distillation KL against the final logits and the
-    hint MSE to the pooled feature), backward, clip_, Optim::step_all (Muon)
-    and the EMA.  The loss stays on the device."""
+    """Trainer::step of the rustvit (train.rs:346-387) on the device, from an
+    assembled batch: the soft targets of the (possibly mixed) batch and its
+    dominant labels (train.rs:121-155, 313-320), DropPath's seed drawn from
+    the trainer's generator, forward, build_loss (train.rs:70-118: the fine
+    soft-target CE, the coarse CE when coarse_w > 0 and the taxonomy is on,
+    the exits' CE, their distillation KL against the final logits and the
+    hint MSE to the pooled feature), backward, lr_at, clip_,
+    Optim::step_all and the EMA; the step counter advances.
+
+    The trainer's generator is ``self.rng`` = Rng::new(seed ^ 0xABCD)
+    (train.rs:260).  A caller that assembles batches as Trainer::make_batch
+    does draws the batch seed and the mix plan from it before calling (data
+    module: ``make_batch_train(.., seed=step.rng.next_u64())``,
+    ``mix_batch(.., step.rng)``) and passes perm and lam; without them the
+    batch counts as unmixed.  The losses stay on the device."""
 
     def __init__(self, net, parent, ncoarse, hp=None):
         from .optim import Ema, Optim
         self.net, self.parent, self.nc = net, parent, ncoarse
-        self.hp = dict(VIT_TRAIN, **(hp or {}))
+        self.hp = hp = dict(VIT_TRAIN, **(hp or {}))
         self.params = net.params()
-        self.opt = Optim(True, self.hp["ns"], ctx=net.ctx)
-        self.ema = Ema(self.hp["ema"], ctx=net.ctx) if self.hp["ema"] > 0 else None
+        self.opt = Optim(hp["muon"], hp["ns"], ctx=net.ctx)
+        self.rng = Rng(int(hp["seed"]) ^ 0xABCD)
+        # Trainer::new (train.rs:241-259): the schedule's budget and the EMA
+        # decay that keeps its window at a tenth of the run
+        self.steps_per_epoch = hp["ntrain"] // hp["batch"]
+        self.total_steps = self.steps_per_epoch * hp["epochs"]
+        self.warm_steps = self.steps_per_epoch * hp["warmup"]
+        f = np.float32
+        d = f(hp["ema"])
+        if hp["ema_auto"] and self.total_steps > 0:
+            d = min(f(1.0) - f(10.0) / f(self.total_steps), d)
+        self.ema_decay = float(d)
+        self.ema = Ema(d, ctx=net.ctx) if d > 0 else None
+        self.step = 0
         self.norm = None
+        self.lr = None
 
-    def __call__(self, x, labels, coarse, lr=None, wd=None):
+    def __call__(self, x, labels, coarse, perm=None, lam=None, lr=None, wd=None):
+        """One step; returns (total loss, hits against the dominant labels)
+        as device tensors.  lr / wd override the schedule and hp["wd"]."""
+        total, correct, _ = self.forward_backward(x, labels, coarse, perm, lam)
+        self.update(lr, wd)
+        return total, correct
+
+    def forward_backward(self, x, labels, coarse, perm=None, lam=None):
+        """The first half of Trainer::step (train.rs:348-362): targets, the
+        DropPath seed, forward, build_loss, backward (gradients accumulate in
+        the parameters).  Returns (total, correct, the output dict)."""
         import torch
-        from .loss import ce_soft, hint_mse, kl_distill, soft_targets
-        from .optim import clip_
+        from .loss import ce_soft, hint_mse, kl_distill, mix_dominant, soft_targets
         hp, net, ctx = self.hp, self.net, self.net.ctx
-        nf = net.nclass
+        nf, n = net.nclass, labels.numel()
+        taxo = not hp["no_taxo"]
+        tf, tc = soft_targets(labels, nf, hp["smooth"], self.parent if taxo else None,
+                              hp["sib"], coarse, self.nc, perm, lam, ctx=ctx)
+        dom = labels if perm is None else mix_dominant(labels, perm, lam, ctx=ctx)
+        net.drop_seed = self.rng.next_u64()
         out = net.forward(x, True)
-        tf, tc = soft_targets(labels, nf, hp["smooth"], self.parent, hp["sib"], coarse, self.nc,
-                              ctx=ctx)
-        ce, correct, dlog = ce_soft(out["logits"], tf, labels, 1.0, ctx=ctx)
-        lc, _, dcoarse = ce_soft(out["coarse"], tc, coarse, hp["coarse_w"], ctx=ctx)
-        total = ce + hp["coarse_w"] * lc
+        # build_loss (train.rs:70-118); the total adds its terms in the
+        # reference's order and grouping, in f32
+        ce, correct, dlog = ce_soft(out["logits"], tf, dom, 1.0, ctx=ctx)
+        total = ce
+        if hp["coarse_w"] > 0 and taxo:
+            lc, _, dcoarse = ce_soft(out["coarse"], tc, coarse, hp["coarse_w"], ctx=ctx)
+            total = total + hp["coarse_w"] * lc
+        else:
+            dcoarse = torch.zeros(n, self.nc, device=x.device)
         g = {"logits": dlog, "coarse": dcoarse}
-        if net.use_exits:
-            l1, _, de1 = ce_soft(out["e1"], tf, labels, hp["exit_w"][0], ctx=ctx)
-            l2, _, de2 = ce_soft(out["e2"], tf, labels, hp["exit_w"][1], ctx=ctx)
-            total = total + hp["exit_w"][0] * l1 + hp["exit_w"][1] * l2
+        if "e1" in out:
+            w1, w2 = hp["exit_w"]
+            l1, _, de1 = ce_soft(out["e1"], tf, dom, w1, ctx=ctx)
+            l2, _, de2 = ce_soft(out["e2"], tf, dom, w2, ctx=ctx)
+            total = total + (w1 * l1 + w2 * l2)
             if hp["alpha"] > 0:
                 k1 = kl_distill(out["e1"], out["logits"], hp["temp"], hp["alpha"], de1, ctx=ctx)
                 k2 = kl_distill(out["e2"], out["logits"], hp["temp"], hp["alpha"], de2, ctx=ctx)
                 total = total + hp["alpha"] * (k1 + k2)
             dh1, dh2 = torch.zeros_like(out["h1"]), torch.zeros_like(out["h2"])
             if hp["beta"] > 0:
-                total = total + hint_mse(out["h1"], out["feat"], hp["beta"], dh1, ctx=ctx) + \
-                    hint_mse(out["h2"], out["feat"], hp["beta"], dh2, ctx=ctx)
+                total = total + (hint_mse(out["h1"], out["feat"], hp["beta"], dh1, ctx=ctx) +
+                                 hint_mse(out["h2"], out["feat"], hp["beta"], dh2, ctx=ctx))
             g.update(e1=de1, e2=de2, h1=dh1, h2=dh2)
         net.backward(g)
+        return total, correct, out
+
+    def update(self, lr=None, wd=None):
+        """The second half of Trainer::step (train.rs:364-386): lr_at,
+        clip_, Optim::step_all, the EMA; the step counter advances."""
+        import torch
+        from .optim import clip_
+        hp, ctx = self.hp, self.net.ctx
+        if lr is None:
+            lr = lr_at(hp["lr"], hp["lr_min"], self.step, self.total_steps, self.warm_steps)
+        self.lr = lr
         if self.norm is None:
-            self.norm = torch.zeros(1, device=x.device)
+            self.norm = torch.zeros(1, device=self.params[0].v.device)
         if hp["clip"] > 0:
             clip_(self.params, hp["clip"], ctx=ctx, norm=self.norm)
-        self.opt.step_all(self.params, hp["lr"] if lr is None else lr,
-                          hp["wd"] if wd is None else wd)
+        self.opt.step_all(self.params, lr, hp["wd"] if wd is None else wd)
         if self.ema is not None:
             self.ema.update(self.params)
-        return total, correct
+        self.step += 1
 
 
 FNV_OFFSET = 0xCBF29CE484222325

@@ -142,8 +142,7 @@ def test_block_matches_torch_f64(rnn, orc, mh):
     from rustnn_amd.vit import Block
     n, c, h, th, depth = 3, 32, 2, 4, 7
     t, tk = th * th, mh * mh
-    gen = torch.Generator(device="cuda").manual_seed(5)
-    blk = Block(c, h, th, th, (mh, mh), depth, 0.0, 2, 1e-4, gen)
+    blk = Block(c, h, th, th, (mh, mh), depth, 0.0, 2, 1e-4, 5)
     # non-trivial values for the parameters that start at constants
     r = np.random.default_rng(mh)
     for p in _params_of(blk):
@@ -208,8 +207,7 @@ def test_reference_block_dircheck(rnn, orc):
     from rustnn_amd.vit import Block
     n, c, h, th, mh = 3, 8, 2, 3, 6
     t, tk = th * th, mh * mh
-    gen = torch.Generator(device="cuda").manual_seed(11)
-    blk = Block(c, h, th, th, (mh, mh), 4, 0.3, 1, 0.5, gen)
+    blk = Block(c, h, th, th, (mh, mh), 4, 0.3, 1, 0.5, 11)
     rng = orc.Rng(0x1234 ^ 9)
     eps = refcheck.gc_eps()
     x = rng.rand_vec(n * t * c)
