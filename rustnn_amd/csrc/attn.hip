@@ -28,7 +28,8 @@ constexpr int MAXDH = 64;  // head-dim limit
 struct AttnArgs {
     const float *q, *kv, *tau, *rel, *p, *dout;
     float *pout, *o, *dq, *dkv;
-    float *dtau_part, *drel_part;  // [n][h], [n][h][nrel]
+    double *dtau_part;             // [n][h]
+    float *drel_part;              // [n][h][nrel]
     const uint32_t *relidx;        // [tq*tk]
     const uint32_t *rowptr;        // [nrel+1] inverse index (drel gather)
     const uint32_t *pos;           // [tq*tk] LDS offsets (row*LS + col), by bias slot
@@ -51,6 +52,11 @@ __device__ __forceinline__ float half_sum(float v) {
     return v;
 }
 __device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
     return v;
@@ -305,7 +311,8 @@ template <int DHP, bool VEC>
 __global__ __launch_bounds__(128) void attn_bwd_kernel(AttnArgs g) {
     constexpr int HALF = DHP / 2, NDT = DHP / 32;
     extern __shared__ float smem[];
-    float *Pl = smem, *Sl = Pl + 64 * LS, *red = Sl + 64 * LS;
+    float *Pl = smem, *Sl = Pl + 64 * LS;
+    double *dred = (double *)(Sl + 64 * LS);  // 8-byte aligned: 2 * 64 * LS floats before it
     const int tid = threadIdx.x, lane = tid & 63, w = wave_index(), nthreads = blockDim.x;
     const int l32 = lane & 31, hh = lane >> 5;
     const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
@@ -376,8 +383,10 @@ __global__ __launch_bounds__(128) void attn_bwd_kernel(AttnArgs g) {
             Sl[qi * LS + kj] = d0;
             ds[nt][v] = d0 * t;  // attn.rs:316: dS *= tau
         }
-    tpart = wave_sum(tpart);
-    if (lane == 0) red[w] = tpart;
+    // dtau is a sum whose terms cancel to about 1% of their size: the lane
+    // partials are added in f64 from here on
+    const double tsum = wave_sum_d((double)tpart);
+    if (lane == 0) dred[w] = tsum;
     // dQ = tau*dS K (attn.rs:319-323): queries of this lane, from registers
     float *dqi = g.dq + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
 #pragma unroll
@@ -405,7 +414,7 @@ __global__ __launch_bounds__(128) void attn_bwd_kernel(AttnArgs g) {
         }
         drp[r] = sacc;
     }
-    if (tid == 0) g.dtau_part[(long long)img * g.h + hd] = red[0] + red[1];
+    if (tid == 0) g.dtau_part[(long long)img * g.h + hd] = dred[0] + dred[1];
     // dK = tau*dS^T Q and dV = P^T dO (attn.rs:270-274, 324-327): key rows
     // [32w, 32w + 32), A from LDS (transposed reads), Q / dO rows from HBM.
     float *dki = g.dkv + (long long)img * tk * g.kvstride + g.koff + (long long)hd * dh;
@@ -442,45 +451,56 @@ __global__ __launch_bounds__(128) void attn_bwd_kernel(AttnArgs g) {
 // (image order, attn.rs:333-342).  A block takes 32 elements; thread (j, e)
 // sums images [j*G, j*G + G) of element e with the loads issued ahead of the
 // in-order adds, then the 8 partials are added in j order (fixed order:
-// bit-reproducible).
+// bit-reproducible).  The dtau partials are f64 and summed in f64.
 constexpr int ATTN_RED_PARTS = 8;
-__global__ __launch_bounds__(256) void attn_reduce_kernel(const float *dtau_part,
+__global__ __launch_bounds__(256) void attn_reduce_kernel(const double *dtau_part,
                                                           const float *drel_part, int n, int h,
                                                           int nrel, float *dtau, float *drel) {
-    __shared__ float part[ATTN_RED_PARTS][32];
+    __shared__ double part[ATTN_RED_PARTS][32];
     const int el = threadIdx.x & 31, j = threadIdx.x >> 5;
     const int e = blockIdx.x * 32 + el;
     const int per = h * nrel;
     const bool is_rel = e < per, live = e < per + h;
-    const float *src = is_rel ? drel_part + e : dtau_part + (e - per);
     const long long stride = is_rel ? per : h;
     const int G = (n + ATTN_RED_PARTS - 1) / ATTN_RED_PARTS;
     const int i0 = j * G, i1 = min(n, i0 + G);
-    float s = 0.f;
-    if (live) {
+    double s = 0.0;
+    if (live && is_rel) {
+        float fs = 0.f;
+        const float *src = drel_part + e;
         for (int b = i0; b < i1; b += 16) {
             float v[16];
 #pragma unroll
             for (int u = 0; u < 16; u++) v[u] = b + u < i1 ? src[(long long)(b + u) * stride] : 0.f;
 #pragma unroll
             for (int u = 0; u < 16; u++)
-                if (b + u < i1) s = (b + u == i0) ? v[u] : s + v[u];
+                if (b + u < i1) fs = (b + u == i0) ? v[u] : fs + v[u];
         }
+        s = fs;
+    } else if (live) {
+        const double *src = dtau_part + (e - per);
+        for (int b = i0; b < i1; b++) s += src[(long long)b * stride];
     }
     part[j][el] = s;
     __syncthreads();
     if (j == 0 && live) {
-        float t = 0.f;
-        bool first = true;
-        for (int q = 0; q < ATTN_RED_PARTS; q++) {
-            if (q * G >= n) break;
-            t = first ? part[q][el] : t + part[q][el];
-            first = false;
-        }
-        if (is_rel)
+        if (is_rel) {
+            float t = 0.f;
+            bool first = true;
+            for (int q = 0; q < ATTN_RED_PARTS; q++) {
+                if (q * G >= n) break;
+                t = first ? (float)part[q][el] : t + (float)part[q][el];
+                first = false;
+            }
             drel[e] += t;
-        else
-            dtau[e - per] += t;
+        } else {
+            double t = 0.0;
+            for (int q = 0; q < ATTN_RED_PARTS; q++) {
+                if (q * G >= n) break;
+                t += part[q][el];
+            }
+            dtau[e - per] += (float)t;
+        }
     }
 }
 
@@ -673,10 +693,11 @@ __global__ __launch_bounds__(256) void attn_softmax_rows_kernel(
 
 // Backward rows (attn.rs:280-330): s1 holds dP, s2 the recomputed raw S.
 // dS = P o (dP - <dP, P>) goes to s1 (for drel), tau dS to s2 (for dQ, dK);
-// part[row] = sum dS o S_raw (the dtau share of the row).
+// part[row] = sum dS o S_raw (the dtau share of the row, summed in f64: dtau
+// is a sum whose terms cancel to about 1% of their size).
 __global__ __launch_bounds__(256) void attn_dsoft_rows_kernel(
     const float *__restrict__ p, float *s1, float *s2, const float *__restrict__ tau,
-    float *__restrict__ part, long long rows, int h, int tq, int tk) {
+    double *__restrict__ part, long long rows, int h, int tq, int tk) {
     const long long r = (long long)blockIdx.x * 4 + wave_index();
     if (r >= rows) return;
     const int lane = threadIdx.x & 63;
@@ -687,34 +708,34 @@ __global__ __launch_bounds__(256) void attn_dsoft_rows_kernel(
     for (int k = lane; k < tk; k += 64) dot += dp[k] * pr[k];
     for (int o = 32; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, 64);
     const float t = tau[hd];
-    float dt = 0.f;
+    double dt = 0.0;
     for (int k = lane; k < tk; k += 64) {
         const float ds = pr[k] * (dp[k] - dot);
-        dt += ds * sr[k];
+        dt += (double)(ds * sr[k]);
         dp[k] = ds;
         sr[k] = ds * t;
     }
-    for (int o = 32; o >= 1; o >>= 1) dt += __shfl_xor(dt, o, 64);
+    dt = wave_sum_d(dt);
     if (lane == 0) part[r] = dt;
 }
 
 // dtau[hd] += sum over (image, query) rows of head hd of part (block hd;
 // strided per thread, then a fixed tree).
-__global__ __launch_bounds__(256) void attn_head_sum_kernel(const float *__restrict__ part,
+__global__ __launch_bounds__(256) void attn_head_sum_kernel(const double *__restrict__ part,
                                                             long long n, int h, int tq,
                                                             float *dtau) {
-    __shared__ float red[4];
+    __shared__ double red[4];
     const int hd = blockIdx.x;
     const long long per = n * tq;
-    float s = 0.f;
+    double s = 0.0;
     for (long long i = threadIdx.x; i < per; i += 256) {
         const long long img = i / tq, q = i - img * tq;
         s += part[(img * h + hd) * tq + q];
     }
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+    s = wave_sum_d(s);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
-    if (threadIdx.x == 0) dtau[hd] += (red[0] + red[1]) + (red[2] + red[3]);
+    if (threadIdx.x == 0) dtau[hd] += (float)((red[0] + red[1]) + (red[2] + red[3]));
 }
 
 // drel partials: part[chunk][hd*nrel + slot] = sum over the images of the
@@ -757,7 +778,7 @@ __global__ __launch_bounds__(256) void attn_drel_sum_kernel(const float *__restr
     drel[e] += s;
 }
 
-size_t bwd_lds() { return ((size_t)2 * 64 * LS + 2) * 4; }
+size_t bwd_lds() { return (size_t)2 * 64 * LS * 4 + 2 * sizeof(double); }
 size_t fwd_lds(size_t nrel) { return ((size_t)64 * LS + 4096 + nrel) * 4; }
 
 bool lds_attr_done = false;
@@ -772,8 +793,11 @@ void set_lds_limits() {
                         (const void *)attn_fwd_kernel<32, true>,
                         (const void *)attn_fwd_kernel<64, false>,
                         (const void *)attn_fwd_kernel<64, true>};
+    // a refusal here leaves the default limit, which the launch then reports
     for (const void *k : ks)
-        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
+            hipSuccess)
+            (void)hipGetLastError();
 }
 
 // Core::forward on the composed path (see attn_softmax_rows_kernel).
@@ -812,11 +836,12 @@ int attn_backward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const fl
     const size_t per = h * d->nrel;
     const size_t ipc = rnn_div_up(n, (size_t)16), nchunk = rnn_div_up(n, ipc);
     WsCarve cv;
-    const size_t o1 = cv.take(mat * 4), o2 = cv.take(mat * 4), o3 = cv.take((size_t)rows * 4);
+    const size_t o1 = cv.take(mat * 4), o2 = cv.take(mat * 4), o3 = cv.take((size_t)rows * 8);
     const size_t o4 = cv.take(nchunk * per * 4);
     char *ws = (char *)rnn_workspace(ctx, cv.off);
     if (!ws) return RNN_E_NOMEM;
-    float *s1 = (float *)(ws + o1), *s2 = (float *)(ws + o2), *part = (float *)(ws + o3);
+    float *s1 = (float *)(ws + o1), *s2 = (float *)(ws + o2);
+    double *part = (double *)(ws + o3);
     float *rpart = (float *)(ws + o4);
     for (size_t hd = 0; hd < h; hd++) {
         // dV += P^T dO (attn.rs:262-270)
@@ -923,8 +948,8 @@ int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const floa
     set_lds_limits();
     AttnArgs g;
     fill_args(g, ctx, d, n);
-    size_t parts = n * d->h + n * d->h * (size_t)d->nrel;
-    float *ws = (float *)rnn_workspace(ctx, parts * sizeof(float));
+    const size_t tau_bytes = rnn_round_up(n * d->h * sizeof(double), 256);
+    char *ws = (char *)rnn_workspace(ctx, tau_bytes + n * d->h * (size_t)d->nrel * sizeof(float));
     if (!ws) return RNN_E_NOMEM;
     g.q = q;
     g.kv = kv;
@@ -933,8 +958,8 @@ int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const floa
     g.dout = dout;
     g.dq = dq;
     g.dkv = dkv;
-    g.dtau_part = ws;
-    g.drel_part = ws + n * d->h;
+    g.dtau_part = (double *)ws;
+    g.drel_part = (float *)(ws + tau_bytes);
     const dim3 grid((unsigned)(n * d->h));
     const bool vec = use_vec(g);
     auto go = [&](auto kern) {
@@ -947,7 +972,7 @@ int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const floa
     RNN_LAUNCHED(ctx);
     int tot = (int)(d->h * d->nrel + d->h);
     hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rnn_div_up(tot, 32)), dim3(256), 0,
-                       ctx->stream, (const float *)g.dtau_part, (const float *)g.drel_part, (int)n,
+                       ctx->stream, (const double *)g.dtau_part, (const float *)g.drel_part, (int)n,
                        (int)d->h, (int)d->nrel, dtau, drel);
     RNN_LAUNCHED(ctx);
     return RNN_OK;

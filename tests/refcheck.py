@@ -489,3 +489,301 @@ class GpuNN:
 
     def resnet(self, depth, width, nc, seed):
         return _GpuNet(depth, width, nc, seed)
+
+
+# ------------------------------------------------------------ vitcheck
+# vitcheck (check.rs:163-180): one Rng::new(seed ^ 0x1234) through gemmcheck's
+# draws, the token fixture (n 3, t 9, c 8), normcheck, attncheck and netcheck.
+GEMM_SHAPES = [(23, 37, 19), (64, 48, 96), (7, 16, 259)]  # check.rs:147
+VIT_NTC = (3, 9, 8)
+NET_CFG = dict(width=4, cmid=6, dim=8, heads=2, depth3=2, dim4=12, heads4=2, depth4=1,
+               mem_at=(1,), droppath=0.2, img=16)  # check.rs:401-413
+NET_PARENT = [0, 0, 1, 1, 2, 2]
+
+
+def skip_gemmcheck_draws(rng):
+    """gemmcheck (check.rs:145-161) draws a then b for each shape and each of
+    the four transpose combinations."""
+    for m, n, k in GEMM_SHAPES:
+        for _ in range(4):
+            rng.rand_vec(m * k)
+            rng.rand_vec(k * n)
+
+
+def check_params(layer, eps, rng, loss):
+    """check_params! (check.rs:75-99): one dircheck over every parameter of
+    `layer` (an adapter), the values restored afterwards."""
+    base, grad = layer.values(), layer.grads()
+
+    def lossp(v):
+        layer.set_values(v)
+        return loss()
+    e = dircheck(base, grad, eps, rng, lossp)
+    layer.set_values(base)
+    return e
+
+
+def attncheck(be, rng, x, r, n, c, eps):
+    """attncheck (check.rs:294-395) on backend `be`: SelfAttn (random rel),
+    CrossAttn over a 6x6 memory (dx, dmem, dparams) and a reader Block with
+    DropPath 0.2 and parameters perturbed by 0.2 N(0,1).  Returns
+    {tag: relative error}."""
+    out = {}
+    # 6. self-attention with LSA and the relative bias
+    at = be.self_attn(c, 2, 3, 3, 2, rng)
+    at.set_rel(rng.rand_vec(at.rel_len()))
+    at.fwd(x)
+    dx = at.bwd(r)
+    out["selfattn dx"] = dircheck(x, dx, eps, rng, lambda v: dot32(at.fwd(v), r))
+    at.zero_grads()
+    at.fwd(x)
+    at.bwd(r)
+    out["selfattn dparams"] = check_params(at, eps, rng, lambda: dot32(at.fwd(x), r))
+    # 7. cross-attention on the memory
+    mh = 6
+    cr = be.cross_attn(c, 2, 3, 3, mh, mh, 2, rng)
+    cr.set_rel(rng.rand_vec(cr.rel_len()))
+    mem = rng.rand_vec(n * mh * mh * 2 * c)
+    cr.fwd(x, mem)
+    dx, dmem = cr.bwd(r, mem)
+    out["crossattn dx"] = dircheck(x, dx, eps, rng, lambda v: dot32(cr.fwd(v, mem), r))
+    out["crossattn dmem"] = dircheck(mem, dmem, eps, rng, lambda v: dot32(cr.fwd(x, v), r))
+    cr.zero_grads()
+    cr.fwd(x, mem)
+    cr.bwd(r, mem)
+    out["crossattn dparams"] = check_params(cr, eps, rng, lambda: dot32(cr.fwd(x, mem), r))
+    # 8. the whole Block, with the memory and seeded stochastic depth
+    blk = be.block(c, 2, 3, 3, (mh, mh), 2, 0.2, 7, 0.3, rng)
+    v0 = blk.values()
+    blk.set_values((v0 + np.float32(0.2) * rng.rand_vec(v0.size)).astype(np.float32))
+    mem = rng.rand_vec(n * mh * mh * 2 * c)
+    blk.fwd(x, mem, 99)
+    dx, _ = blk.bwd(r, mem)
+    out["block dx"] = dircheck(x, dx, eps, rng, lambda v: dot32(blk.fwd(v, mem, 99), r))
+    blk.zero_grads()
+    blk.fwd(x, mem, 99)
+    blk.bwd(r, mem)
+    out["block dparams"] = check_params(blk, eps, rng, lambda: dot32(blk.fwd(x, mem, 99), r))
+    return out
+
+
+def netcheck(be, rng, eps, seed=SEED):
+    """netcheck (check.rs:396-460): the small RustViT of
+    RustViT::new(cfg, parent, 3, seed ^ 0xBEEF) with parameters perturbed by
+    0.15 N(0,1), batch 3, loss = <outputs, g> over the three heads, both
+    hints and the pooled feature; one dircheck over every parameter."""
+    net = be.rustvit(NET_CFG, NET_PARENT, 3, seed ^ 0xBEEF, 4242)
+    v0 = net.values()
+    net.set_values((v0 + np.float32(0.15) * rng.rand_vec(v0.size)).astype(np.float32))
+    bs, nf = 3, len(NET_PARENT)
+    x = rng.rand_vec(bs * 3 * 16 * 16)
+    keys = ("logits", "coarse", "e1", "e2", "h1", "h2", "hfinal")
+    sizes = (bs * nf, bs * 3, bs * nf, bs * nf, bs * 12, bs * 12, bs * 12)
+    g = {k: rng.rand_vec(s) for k, s in zip(keys, sizes)}
+
+    def lin(o):
+        return (dot32(o["logits"], g["logits"]) + dot32(o["coarse"], g["coarse"]) +
+                dot32(o["e1"], g["e1"]) + dot32(o["e2"], g["e2"]) + dot32(o["h1"], g["h1"]) +
+                dot32(o["h2"], g["h2"]) + dot32(o["feat"], g["hfinal"]))
+
+    net.fwd(x)
+    net.bwd(g)
+    return check_params(net, eps, rng, lambda: lin(net.fwd(x)))
+
+
+def vitcheck(orc, norm_be, attn_be, seed=SEED):
+    """vitcheck (check.rs:163-180) on the given backends: {tag: error}."""
+    from test_oracle_norm import normcheck
+    rng = orc.Rng(seed ^ 0x1234)
+    eps = gc_eps()
+    skip_gemmcheck_draws(rng)
+    n, t, c = VIT_NTC
+    x = rng.rand_vec(n * t * c)
+    r = rng.rand_vec(n * t * c)
+    out = dict(normcheck(orc, norm_be, rng, x, r))
+    out.update(attncheck(attn_be, rng, x, r, n, c, eps))
+    out["rustvit (all parameters)"] = netcheck(attn_be, rng, eps, seed)
+    return out
+
+
+class _Layer:
+    """Adapter over a layer whose parameters are Param objects with v / g
+    (oracle: numpy arrays; device: CUDA tensors)."""
+
+    def __init__(self, obj, params, to_np, from_np):
+        self.o, self.ps, self.h, self.d = obj, params, to_np, from_np
+
+    def values(self):
+        return np.concatenate([self.h(p.v).ravel() for p in self.ps]).astype(np.float32)
+
+    def grads(self):
+        return np.concatenate([self.h(p.g).ravel() for p in self.ps]).astype(np.float32)
+
+    def set_values(self, v):
+        off = 0
+        for p in self.ps:
+            k = p.v.size if isinstance(p.v, np.ndarray) else p.v.numel()
+            part = np.ascontiguousarray(v[off:off + k], np.float32)
+            if isinstance(p.v, np.ndarray):
+                p.v[:] = part
+            else:
+                p.v.copy_(self.d(part))
+            off += k
+
+    def zero_grads(self):
+        for p in self.ps:
+            if isinstance(p.g, np.ndarray):
+                p.g[:] = 0
+            else:
+                p.g.zero_()
+
+    def rel_len(self):
+        return self.o.rel.v.size if isinstance(self.o.rel.v, np.ndarray) else self.o.rel.v.numel()
+
+    def set_rel(self, v):
+        if isinstance(self.o.rel.v, np.ndarray):
+            self.o.rel.v[:] = v
+        else:
+            self.o.rel.v.copy_(self.d(v))
+
+
+class OracleAttn:
+    """attncheck / netcheck backend on the CPU oracle (oracle/pyvit.py)."""
+
+    def __init__(self):
+        from oracle import pyvit
+        self.V = pyvit
+
+    def _wrap(self, obj, kind, n, t, c):
+        L = _Layer(obj, obj.params(), lambda a: np.asarray(a), lambda a: a)
+        sh = lambda v: np.asarray(v, np.float32).reshape(n, t, c)
+        if kind == "self":
+            L.fwd = lambda x: obj.forward(sh(x), True).ravel()
+            L.bwd = lambda dy: obj.backward(sh(dy)).ravel()
+        else:
+            def bwd(dy, mem):
+                dmem = np.zeros(np.size(mem), np.float32)
+                if kind == "cross":
+                    dx = obj.backward(sh(dy), self._mem(mem, n, c), dmem)
+                else:
+                    dx = obj.backward(sh(dy), self._mem(mem, n, c), dmem)
+                return dx.ravel(), dmem
+            if kind == "cross":
+                L.fwd = lambda x, mem: obj.forward(sh(x), self._mem(mem, n, c), True).ravel()
+            else:
+                L.fwd = lambda x, mem, seed: obj.forward(sh(x), self._mem(mem, n, c), True,
+                                                         seed).ravel()
+            L.bwd = bwd
+        return L
+
+    @staticmethod
+    def _mem(mem, n, c):
+        return np.asarray(mem, np.float32).reshape(n, -1, 2 * c)
+
+    def self_attn(self, c, h, th, tw, depth, rng):
+        return self._wrap(self.V.SelfAttn(c, h, th, tw, depth, rng), "self", VIT_NTC[0],
+                          th * tw, c)
+
+    def cross_attn(self, c, h, th, tw, mh, mw, depth, rng):
+        return self._wrap(self.V.CrossAttn(c, h, th, tw, mh, mw, depth, rng), "cross",
+                          VIT_NTC[0], th * tw, c)
+
+    def block(self, c, h, th, tw, mem, depth, drop, idx, ls, rng):
+        return self._wrap(self.V.Block(c, h, th, tw, mem, depth, np.float32(drop), idx,
+                                       np.float32(ls), rng), "block", VIT_NTC[0], th * tw, c)
+
+    def rustvit(self, cfg, parent, nc, seed, drop_seed):
+        net = self.V.RustViT(cfg, parent, nc, seed)
+        net.drop_seed = drop_seed
+        L = _Layer(net, net.params(), lambda a: np.asarray(a), lambda a: a)
+        img = cfg["img"]
+        L.fwd = lambda x: {k: np.ravel(v) for k, v in
+                           net.forward(np.asarray(x, np.float32).reshape(-1, 3, img, img),
+                                       True).items()}
+        L.bwd = lambda g: net.backward(g)
+        return L
+
+
+class _SyncedRng:
+    """Runs a device constructor on the state of an oracle Rng: the device's
+    host generator (rustnn_amd.data.Rng) takes the oracle's state and hands
+    it back advanced, so one stream feeds both, as one Rng feeds the
+    reference's check."""
+
+    def __init__(self, orng):
+        self.o = orng
+
+    def __enter__(self):
+        from rustnn_amd.data import Rng
+        self.d = Rng(0)
+        for i in range(4):
+            self.d.state[i] = self.o.st.s[i]
+        return self.d
+
+    def __exit__(self, *a):
+        for i in range(4):
+            self.o.st.s[i] = self.d.state[i]
+
+
+class GpuAttn:
+    """attncheck / netcheck backend on the device layers (rustnn_amd.vit)."""
+
+    def _wrap(self, obj, kind, n, t, c):
+        import torch
+        ps = []
+        obj.for_each_param(ps.append)
+        L = _Layer(obj, ps, _host, _dev)
+        sh = lambda v: _dev(v).reshape(n, t, c)
+        mem_of = lambda mem: _dev(mem).reshape(n, -1, 2 * c)
+        if kind == "self":
+            L.fwd = lambda x: _host(obj.forward(sh(x), True)).ravel()
+            L.bwd = lambda dy: _host(obj.backward(sh(dy))).ravel()
+            return L
+
+        def bwd(dy, mem):
+            dmem = torch.zeros(np.size(mem), device="cuda")
+            dx = obj.backward(sh(dy), mem_of(mem), dmem)
+            return _host(dx).ravel(), _host(dmem).ravel()
+        if kind == "cross":
+            L.fwd = lambda x, mem: _host(obj.forward(sh(x), mem_of(mem), True)).ravel()
+        else:
+            L.fwd = lambda x, mem, seed: _host(obj.forward(sh(x), mem_of(mem), True,
+                                                           seed)).ravel()
+        L.bwd = bwd
+        return L
+
+    def self_attn(self, c, h, th, tw, depth, rng):
+        from rustnn_amd.vit import SelfAttn
+        with _SyncedRng(rng) as d:
+            obj = SelfAttn(c, h, th, tw, depth, d)
+        return self._wrap(obj, "self", VIT_NTC[0], th * tw, c)
+
+    def cross_attn(self, c, h, th, tw, mh, mw, depth, rng):
+        from rustnn_amd.vit import CrossAttn
+        with _SyncedRng(rng) as d:
+            obj = CrossAttn(c, h, th, tw, mh, mw, depth, d)
+        return self._wrap(obj, "cross", VIT_NTC[0], th * tw, c)
+
+    def block(self, c, h, th, tw, mem, depth, drop, idx, ls, rng):
+        from rustnn_amd.vit import Block
+        with _SyncedRng(rng) as d:
+            obj = Block(c, h, th, tw, mem, depth, float(np.float32(drop)), idx,
+                        float(np.float32(ls)), d)
+        return self._wrap(obj, "block", VIT_NTC[0], th * tw, c)
+
+    def rustvit(self, cfg, parent, nc, seed, drop_seed):
+        from rustnn_amd.vit import RustViT
+        par = _dev(np.asarray(parent, np.uint32).view(np.float32)).view(dtype=_i32dtype())
+        net = RustViT(cfg, par, nc, seed=seed)
+        net.drop_seed = drop_seed
+        L = _Layer(net, net.params(), _host, _dev)
+        img = cfg["img"]
+        L.fwd = lambda x: {k: _host(v).ravel() for k, v in
+                           net.forward(_dev(x).reshape(-1, 3, img, img), True).items()}
+        L.bwd = lambda g: net.backward({k: _dev(v) for k, v in g.items()})
+        return L
+
+
+def _i32dtype():
+    import torch
+    return torch.int32

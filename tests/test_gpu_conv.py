@@ -181,3 +181,14 @@ def test_conv_bad_spec_raises(rnn):
     w = to_dev(np.zeros(4 * 36, np.float32))
     with pytest.raises(rnn.RnnError):
         rnn.conv2d_forward(bad, 1, x, w, y=to_dev(np.zeros(4 * 81, np.float32)))
+
+
+def test_conv_layercheck_gpu(rnn, orc):
+    """The reference's conv gradcheck (check.rs:503-546: 3x3/s1, 1x1/s2 and
+    3x3/s2, dx and dw by dircheck at seed 1234, tolerance 5e-3) through the
+    HIP conv path, in the reference's Rng draw order."""
+    import refcheck
+    res = refcheck.conv_layercheck(orc.Rng, refcheck.GpuConv(rnn))
+    assert len(res) == 6
+    bad = [(t, e) for t, e in res if not e < refcheck.TOL]
+    assert not bad, res

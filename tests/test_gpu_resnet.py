@@ -20,13 +20,14 @@ import refcheck
 pytestmark = pytest.mark.gpu
 
 # Tolerances of the whole-network comparison (relative Frobenius): 1e-5 for
-# the logits and the whole gradient vector (measured on MI355X: 2.3e-7 and
-# 2.0e-6).  Single small tensors (a BN beta of 32 values whose gradient sums
-# cancel) get 1e-4: the convolutions sum in a different order than the
-# reference and BatchNorm's backward divides by the per-channel deviation.
+# the logits, the loss, the whole gradient vector and every gradient tensor.
+# A tensor above 1e-5 against the oracle must be no farther from an
+# independent float64 statement of the network (tests/torch_resnet.py) than
+# twice the oracle's own distance: the oracle itself sits up to 2.8e-5 from
+# float64 on the betas of the BNs whose gradient sums cancel (zero-initialised
+# gamma), so no f32 summation order can promise 1e-5 against it there.
 TOL_FWD = 1e-5
 TOL_GRAD = 1e-5
-TOL_TENSOR = 1e-4
 
 
 def _cfg3_inputs(orc, n, seed=2026):
@@ -86,11 +87,24 @@ def test_train_step_config3(rnn, orc):
     assert abs(float(to_host(loss)[0]) - loss_w) < 1e-5 * abs(loss_w)
     assert int(to_host(corr)[0]) == corr_w
     g_got, g_want = to_host(got.grads()), _oracle_flat(want, "g")
+    import torch_resnet
+    torch.set_num_threads(16)
+    z64, l64, g64 = torch_resnet.resnet_f64([p.v for p in want.params()], 3, 32, 100, x, labels,
+                                            0.1)
+    assert rel_frob(lg_w, z64) < TOL_FWD and abs(loss_w - l64) < 1e-5 * abs(l64)
     off = 0
-    for i, p in enumerate(want.params()):
-        e = rel_frob(g_got[off:off + p.v.size], p.g)
-        assert e < TOL_TENSOR, (i, p.v.size, e)
+    above = []
+    for i, (p, gf) in enumerate(zip(want.params(), g64)):
+        gd = g_got[off:off + p.v.size]
         off += p.v.size
+        e = rel_frob(gd, p.g)
+        if e < TOL_GRAD:
+            continue
+        ed, eo = rel_frob(gd, gf), rel_frob(p.g, gf)
+        above.append((i, p.v.size, e, ed, eo))
+        assert ed < max(TOL_GRAD, 2 * eo), (i, p.v.size, e, ed, eo)
+    print("tensors above 1e-5 vs the oracle (index, size, vs oracle, device vs f64, oracle "
+          "vs f64):", above)
     assert rel_frob(g_got, g_want) < TOL_GRAD
     assert rel_frob(to_host(got.buffers()), np.concatenate(want.buffers())) < 1e-6
     # the SGD step on those gradients

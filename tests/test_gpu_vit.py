@@ -89,9 +89,11 @@ def _params_of(obj):
     return ps
 
 
-def _torch_block(x, mem, W, c, h, th, mh, torch):
+def _torch_block(x, mem, W, c, h, th, mh, torch, keep=None):
     """vit.rs:138-172 in float64 (DropPath off): h = LN(x); x += l1 (SA(h) +
-    g DW(h)); x += lm CA(h, mem); x += l2 SwiGLU(LN(x))."""
+    g DW(h)); x += lm CA(h, mem); x += l2 SwiGLU(LN(x)).  `keep` (a list)
+    receives each core's raw scores S and logits (their gradient after the
+    backward is dS), for the conditioning of dtau."""
     F = torch.nn.functional
     dh = c // h
     n, t = x.shape[0], th * th
@@ -104,6 +106,9 @@ def _torch_block(x, mem, W, c, h, th, mh, torch):
         s = torch.einsum("nqhd,nkhd->nhqk", q, k)
         bias = rel.view(h, nrel)[:, relidx]  # [h, tq, tk]
         xx = tau.view(1, h, 1, 1) * s + bias.unsqueeze(0)
+        if keep is not None:
+            xx.retain_grad()
+            keep.append((s, xx))
         if mask:
             eye = torch.eye(s.shape[-1], dtype=torch.bool)
             xx = xx.masked_fill(eye, float("-inf"))
@@ -176,7 +181,8 @@ def test_block_matches_torch_f64(rnn, orc, mh):
          "wd.w": T(H(blk.mlp.wd.w).reshape(c, -1)), "wd.b": T(H(blk.mlp.wd.b)),
          "ls2": T(H(blk.ls2.l.v))}
     xt, mt = T(x), T(mem)
-    yt = _torch_block(xt, mt, W, c, h, th, mh, torch)
+    kept = []
+    yt = _torch_block(xt, mt, W, c, h, th, mh, torch, kept)
     assert rel_frob(to_host(y), yt.detach().numpy()) < TOL
     yt.backward(torch.tensor(dz, dtype=torch.float64))
     assert rel_frob(to_host(dx), xt.grad.numpy()) < TOL, "dx"
@@ -190,14 +196,36 @@ def test_block_matches_torch_f64(rnn, orc, mh):
              "lsm": blk.lsm.l.g, "n2.g": blk.n2.g.g, "n2.b": blk.n2.b.g,
              "wg.w": blk.mlp.wg.gw, "wg.b": blk.mlp.wg.gb, "wd.w": blk.mlp.wd.gw,
              "wd.b": blk.mlp.wd.gb, "ls2": blk.ls2.l.g}
-    # dtau is one number per head: a sum of n*tq*tk products dS*S whose
-    # terms cancel to about 1% of their magnitude, so its f32 sums carry a
-    # larger relative error than the other gradients
-    tol = {"tau": 2e-4, "ctau": 2e-4}
+    # dtau is one number per head: the sum over n*tq*tk products dS*S whose
+    # terms cancel (kappa = sum |dS S| / |sum dS S|, from the float64
+    # statement, is in the hundreds), so any f32 evaluation carries a relative
+    # error of order kappa * 2^-24 -- above 1e-5.  It is held to the oracle's
+    # own distance from float64 (the oracle Block at the same weights) and to
+    # that conditioning bound: the device no farther than max(TOL, 2 x the
+    # oracle, 16 kappa 2^-24).
+    kappa = {}
+    for name, (sc, xx) in zip(("tau", "ctau"), kept):
+        prod = (xx.grad * sc).detach().numpy()
+        prod = np.where(np.isfinite(prod), prod, 0.0)
+        kappa[name] = float(np.max(np.abs(prod).sum(axis=(0, 2, 3)) /
+                                   np.abs(prod.sum(axis=(0, 2, 3)))))
+    from oracle import pyvit
+    oblk = pyvit.Block(c, h, th, th, (mh, mh), depth, 0.0, 2, np.float32(1e-4), orc.Rng(5))
+    for po, pd in zip(oblk.params(), _params_of(blk)):
+        po.v[:] = to_host(pd.v).ravel()
+    oblk.forward(x.reshape(n, t, c), mem.reshape(n, tk, 2 * c), True, 99)
+    oblk.backward(dz.reshape(n, t, c), mem.reshape(n, tk, 2 * c),
+                  np.zeros(n * tk * 2 * c, np.float32))
+    oracle_g = {"tau": oblk.attn.tau.g, "ctau": oblk.cross.tau.g}
     for k, g in grads.items():
         want = W[k].grad.numpy().ravel()
         err = rel_frob(to_host(g).ravel(), want)
-        assert err < tol.get(k, TOL), (k, err)
+        if k in oracle_g:
+            eo = rel_frob(oracle_g[k], want)
+            bound = max(TOL, 2 * eo, 16 * kappa[k] * 2.0 ** -24)
+            assert err < bound, (k, err, eo, kappa[k])
+        else:
+            assert err < TOL, (k, err)
 
 
 def test_reference_block_dircheck(rnn, orc):

@@ -289,3 +289,16 @@ def test_trainer_step_default_batch128(rnn, orc, vit):
                              [host_o(p.v) for p in ops], lr, 0.06, 0, "default")
     print(f"default: worst gradient {max(errs):.2e}; worst update vs f64 (device, oracle, "
           f"f32 floor) {worst[0]:.2e} {worst[1]:.2e} {worst[2]:.2e}; device vs oracle {e:.2e}")
+
+
+def test_reference_vitcheck_on_gpu(rnn, orc, vit):
+    """vitcheck (check.rs:163-180) through the device layers: normcheck,
+    attncheck (SelfAttn, CrossAttn over a 6x6 memory with dmem, a reader Block
+    with DropPath) and netcheck, on one Rng stream that feeds the device
+    constructors too, every check under the reference's 5e-3."""
+    import refcheck
+    from test_gpu_norm import GpuNorm
+    errs = refcheck.vitcheck(orc, GpuNorm(), refcheck.GpuAttn())
+    assert len(errs) == 16
+    bad = {k: v for k, v in errs.items() if not v < refcheck.TOL}
+    assert not bad, errs

@@ -186,30 +186,38 @@ class OracleNorm:
         return o.linear_forward(rows, h, c, u, wd, bd)
 
 
-def normcheck(orc, be):
+def normcheck(orc, be, rng=None, x=None, r=None):
     """check.rs:182-291 on a backend: dx and the parameters of each layer by
-    dircheck at the reference's fixture (n=3, t=9, c=8).  Returns
-    {name: relative error}."""
-    rng = orc.Rng(1234 ^ 0x1234)
-    eps = refcheck.gc_eps()
+    dircheck at the reference's fixture (n=3, t=9, c=8), with the layers'
+    weights drawn as the reference's constructors draw them (SwiGlu::new(c,
+    16, 2), DwConv3::new, SeqPool::new: Param::trunc_normal).  Without rng /
+    x / r it starts its own stream (Rng::new(1234 ^ 0x1234), gemmcheck's
+    draws skipped, as vitcheck does).  Returns {name: relative error}."""
+    f = np.float32
     n, t, c = 3, 9, 8
-    x = rng.rand_vec(n * t * c)
-    r = rng.rand_vec(n * t * c)
+    if rng is None:
+        rng = orc.Rng(1234 ^ 0x1234)
+        refcheck.skip_gemmcheck_draws(rng)
+        x = rng.rand_vec(n * t * c)
+        r = rng.rand_vec(n * t * c)
+    eps = refcheck.gc_eps()
     X = lambda v: v.reshape(n * t, c)
     d32 = refcheck.dot32
-    dc = lambda base, grad, f: refcheck.dircheck(base, np.asarray(grad).ravel(), eps, rng, f)
+    dc = lambda base, grad, fn: refcheck.dircheck(base, np.asarray(grad).ravel(), eps, rng, fn)
     out = {}
-    g = (1.0 + 0.2 * rng.rand_vec(c)).astype(np.float32)
+    # 2. LayerNorm: g = 1 + 0.2 v, b = v
+    g = f(1.0) + f(0.2) * rng.rand_vec(c)
     b = rng.rand_vec(c)
     _, dx, dgb = be.ln(X(x), g, b, X(r))
     out["layernorm dx"] = dc(x, dx, lambda v: d32(be.ln_y(X(v), g, b), r))
     out["layernorm dparams"] = dc(np.concatenate([g, b]), dgb,
                                   lambda v: d32(be.ln_y(X(x), v[:c].copy(), v[c:].copy()), r))
+    # 3. SwiGlu::new(c, 16, 2): wg Linear(c, 32, 0.02), wd Linear::scaled(16, c, depth 2)
     h = 16
-    wg = (rng.rand_vec(2 * h * c) * 0.3).astype(np.float32)
-    bg = (rng.rand_vec(2 * h) * 0.1).astype(np.float32)
-    wd = (rng.rand_vec(c * h) * 0.3).astype(np.float32)
-    bd = (rng.rand_vec(c) * 0.1).astype(np.float32)
+    wg = rng.trunc_normal(2 * h * c, f(0.02))
+    bg = np.zeros(2 * h, np.float32)
+    wd = rng.trunc_normal(c * h, f(0.02) / np.sqrt(f(2.0) * f(2.0)))
+    bd = np.zeros(c, np.float32)
     _, dx, dps = be.sw(X(x), wg, bg, wd, bd, h, X(r))
     out["swiglu dx"] = dc(x, dx, lambda v: d32(be.sw_y(X(v), wg, bg, wd, bd, h), r))
     cut = np.cumsum([wg.size, bg.size, wd.size])
@@ -218,7 +226,8 @@ def normcheck(orc, be):
         a, bb, cc, dd = np.split(v, cut)
         return d32(be.sw_y(X(x), a.copy(), bb.copy(), cc.copy(), dd.copy(), h), r)
     out["swiglu dparams"] = dc(np.concatenate([wg, bg, wd, bd]), dps, sw_p)
-    w = (rng.rand_vec(9 * c) * 0.1).astype(np.float32).reshape(9, c)
+    # 4. DwConv3::new(c, 3, 3): w trunc_normal(0.1); then b = v
+    w = rng.trunc_normal(9 * c, f(0.1)).reshape(9, c)
     bb = rng.rand_vec(c)
     _, dx, dwb = be.dw(X(x), w, bb, n, 3, 3, X(r))
     out["dwconv3x3 dx"] = dc(x, dx, lambda v: d32(be.dw_y(X(v), w, bb, n, 3, 3), r))
@@ -226,7 +235,8 @@ def normcheck(orc, be):
         np.concatenate([w.ravel(), bb]), dwb,
         lambda v: d32(be.dw_y(X(x), v[:9 * c].reshape(9, c).copy(), v[9 * c:].copy(), n, 3, 3),
                       r))
-    p = (rng.rand_vec(c) * 0.02).astype(np.float32)
+    # 5. SeqPool::new(c): p trunc_normal(0.02); rz = v
+    p = rng.trunc_normal(c, f(0.02))
     rz = rng.rand_vec(n * c)
     T = lambda v: v.reshape(n, t, c)
     _, dx, dp = be.sp(T(x), p, n, t, rz)

@@ -240,3 +240,13 @@ def test_build_loss_matches_torch_f64(orc, vit):
     assert abs(total - tot.item()) / abs(tot.item()) < 1e-5
     for k in ("logits", "coarse", "e1", "e2", "h1", "h2"):
         assert rel_frob(g[k], T[k].grad.numpy()) < 1e-5, k
+
+
+def test_reference_vitcheck_on_oracle(orc, vit):
+    """vitcheck (check.rs:163-180) on the oracle: normcheck, attncheck and
+    netcheck on one Rng stream, every check under the reference's 5e-3."""
+    from test_oracle_norm import OracleNorm
+    errs = refcheck.vitcheck(orc, OracleNorm(orc), refcheck.OracleAttn())
+    assert len(errs) == 16  # 8 norm, 7 attention, 1 network
+    bad = {k: v for k, v in errs.items() if not v < refcheck.TOL}
+    assert not bad, errs
