@@ -31,11 +31,20 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
+# The CPU baseline's OpenMP threads stay on their cores (the reference's
+# protocol binds its rayon pool by running pinned; OMP_PROC_BIND=close is the
+# OpenMP statement of it).  Read when the OpenMP runtime starts, so set first.
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+# The CPUs this process may use, read before an OpenMP runtime binds the main
+# thread to one of them.
+USABLE_CPUS = sorted(os.sched_getaffinity(0))
 
 METRIC = "ResNet-20 W32 train images/s; implicit-GEMM conv TFLOP/s and % fp32 MFMA peak"
 PEAK_FP32_MFMA_TFLOPS = 157.3
@@ -88,45 +97,138 @@ def traffic_from_profiles(op):
     return None
 
 
-def cpu_baseline(budget_s=12.0):
-    """Oracle (restated reference CPU path) on a bounded sample of the sweep:
-    the 7 conv shapes x fwd/dX/dW on `sample` images, repeated until the time
-    budget is used (at least once).  Returns TFLOP/s and the sample."""
+def host_cpu():
+    """The host CPU as lscpu reports it, and the CPUs this process may use."""
+    info = {}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        txt = ""
+    for ln in txt.splitlines():
+        k, _, v = ln.partition(":")
+        k, v = k.strip(), v.strip()
+        if k in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)"):
+            info[k] = v
+    info["cpus_usable"] = len(USABLE_CPUS)
+    return info
+
+
+class _PinnedThread:
+    """Runs the block on one thread pinned to one usable CPU."""
+
+    def __enter__(self):
+        self.old = os.sched_getaffinity(0)
+        os.sched_setaffinity(0, {USABLE_CPUS[0]})
+        return self
+
+    def __exit__(self, *a):
+        os.sched_setaffinity(0, self.old)
+
+
+def cpu_protocol(samples=3, cooldown_s=1.0):
+    """The restated reference CPU path (oracle/: the 6x16 AVX2 micro-kernel,
+    KC 256 packing, fused im2col / col2im, per-image parallel convs, 6-row
+    panel parallel matmul, split-K matmul_dw, per-image attention) timed on
+    this host, as BASELINE.md's protocol asks: every workload with all the
+    usable cores (OpenMP, OMP_PROC_BIND=close) and with one pinned thread;
+    `samples` samples each, the best kept (regress.sh:57-76), with a
+    cooldown between samples; inputs seeded with the restated Rng (seed 7,
+    bench.rs:16).  Workloads: config 0 (forward, dX, dW at batch 128),
+    config 1 (the whole sweep, forward + dX + dW of every shape at batch
+    128), config 2 (Core forward and backward, 512 problems), the six
+    --gemmbench shapes (1 warm-up + 5 reps, bench.rs:29-35) and the config-3
+    ResNet-20 train step (batch 128 on all cores; a batch of 32 on one
+    thread, where a step of 128 would take about 8 s per sample; on one
+    thread each gemm shape is 1 warm-up + 1 timed call)."""
     import numpy as np
     from oracle import pyorc as O
+    from oracle import pymodel as M
     O.build()
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    threads = max(1, min(threads, 16, os.cpu_count() or 1))
-    sample = 8
-    layers = []
-    for name, cin, cout, k, s, p, h in SWEEP:
-        sp = O.ConvSpec.make(cin, cout, k, s, p, h, h)
-        r = np.random.default_rng(7)
-        x = r.standard_normal(sample * cin * h * h).astype(np.float32)
-        w = (r.standard_normal(cout * sp.ckk) * np.sqrt(2.0 / sp.ckk)).astype(np.float32)
-        dy = r.standard_normal(sample * cout * sp.hw).astype(np.float32)
-        layers.append((sp, x, w, dy))
-    flops = sum(3 * pass_flops(c[1], c[2], c[3], c[4], c[5], c[6], sample) for c in SWEEP)
+    allt = max(1, len(USABLE_CPUS))
+    rng = O.Rng(7)
+    convs = []
+    for name, cin, cout, k, st, p, h in SWEEP:
+        sp = O.ConvSpec.make(cin, cout, k, st, p, h, h)
+        x = rng.rand_vec(N * cin * h * h)
+        w = rng.rand_vec(cout * sp.ckk) * np.float32(np.sqrt(2.0 / sp.ckk))
+        dy = rng.rand_vec(N * cout * sp.hw)
+        convs.append((name, sp, x, w, dy, pass_flops(cin, cout, k, st, p, h)))
+    # config 2: SelfAttn buffer [128, 64, 384], tau 1, rel 0, no mask
+    n2, h2, dh2, t2 = 128, 4, 32, 64
+    c2 = h2 * dh2
+    relidx, nrel = O.rel_index(8, 8, 8, 8)
+    qkv = rng.rand_vec(n2 * t2 * 3 * c2) * np.float32(1 / np.sqrt(dh2))
+    dout = rng.rand_vec(n2 * t2 * c2)
+    tau, rel = np.ones(h2, np.float32), np.zeros(h2 * nrel, np.float32)
+    desc = O.attn_desc(h2, dh2, t2, t2, 3 * c2, 0, 3 * c2, c2, 2 * c2, relidx, nrel, False)
+    p_att, _ = O.attn_forward(desc, n2, qkv, qkv, tau, rel)
+    z = np.zeros(qkv.size, np.float32)
+    gem = []
+    for m, n, k, at, bt, tag in GEMMBENCH:
+        gem.append((tag, m, n, k, at, bt, rng.rand_vec(m * k), rng.rand_vec(k * n)))
+    c = RESNET
+    u = rng.uniform_vec(c["batch"] * 3 * 32 * 32).reshape(c["batch"], 3, 32, 32)
+    xr = ((u - np.array(CIFAR_MEAN, np.float32)[None, :, None, None]) /
+          np.array(CIFAR_STD, np.float32)[None, :, None, None]).astype(np.float32)
+    lab = np.array([rng.below(100) for _ in range(c["batch"])], np.uint32)
+    net = M.ResNet(c["depth_n"], c["width"], c["nclass"], c["seed"])
 
-    def one():
-        for sp, x, w, dy in layers:
-            O.conv2d_forward(sp, sample, x, w)
-            O.conv2d_backward_x(sp, sample, dy, w)
-            O.conv2d_backward_w(sp, sample, dy, x)
+    def timed(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
 
-    with O.threads(threads):
-        one()  # warm-up (bench.rs:29-30 protocol: one untimed call)
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            one()
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s or el / reps * (reps + 1) > 2.5 * budget_s:
-                break
-    return {"value": round(flops * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"config-1 sweep (7 conv shapes x fwd/dX/dW) on {sample} of 128 images, "
-                      f"{reps} reps in {el:.1f}s; oracle/ AVX2 restatement, OpenMP {threads} threads"}
+    def one_sample(threads):
+        r = {}
+        cfg0 = convs[0]
+        _, sp, x, w, dy, fl = cfg0
+        for ps, fn in (("fwd", lambda: O.conv2d_forward(sp, N, x, w)),
+                       ("dx", lambda: O.conv2d_backward_x(sp, N, dy, w)),
+                       ("dw", lambda: O.conv2d_backward_w(sp, N, dy, x))):
+            r["config0_" + ps] = fl / timed(fn) / 1e9
+        r["config1_sweep"] = sum(3 * cv[5] for cv in convs) / timed(lambda: [
+            (O.conv2d_forward(cv[1], N, cv[2], cv[3]), O.conv2d_backward_x(cv[1], N, cv[4], cv[3]),
+             O.conv2d_backward_w(cv[1], N, cv[4], cv[2])) for cv in convs]) / 1e9
+        r["config2_fwd"] = 2 * 2.0 * n2 * h2 * t2 * t2 * dh2 / timed(
+            lambda: O.attn_forward(desc, n2, qkv, qkv, tau, rel)) / 1e9
+        r["config2_bwd"] = 4 * 2.0 * n2 * h2 * t2 * t2 * dh2 / timed(
+            lambda: O.attn_backward(desc, n2, qkv, qkv, tau, p_att, dout, z, z,
+                                    np.zeros(h2, np.float32),
+                                    np.zeros(h2 * nrel, np.float32))) / 1e9
+        reps = 5 if threads > 1 else 1
+        for tag, m, n, k, at, bt, a, b in gem:
+            O.matmul(m, n, k, a, at, b, bt)  # bench.rs:29-30: one untimed call
+            r["gemm " + tag] = 2.0 * m * n * k * reps / timed(
+                lambda: [O.matmul(m, n, k, a, at, b, bt) for _ in range(reps)]) / 1e9
+        bs = c["batch"] if threads > 1 else 32
+        step = lambda: net.train_step(xr[:bs], lab[:bs], c["smooth"], c["lr"], c["mom"], c["wd"])
+        step()
+        r["config3_step"] = bs / timed(step)
+        return r
+
+    out = {}
+    for label, threads in (("all_cores", allt), ("one_thread", 1)):
+        best = {}
+        for i in range(samples):
+            if i:
+                time.sleep(cooldown_s)
+            with O.threads(threads):
+                if threads == 1:
+                    with _PinnedThread():
+                        r = one_sample(1)
+                else:
+                    r = one_sample(threads)
+            for k, v in r.items():
+                best[k] = max(best.get(k, 0.0), v)
+        out[label] = {"threads": threads, **{k: round(v, 2) for k, v in best.items()}}
+    out["units"] = {"config0_*, config1_sweep, config2_*, gemm *": "GFLOP/s",
+                    "config3_step": "images/s"}
+    out["protocol"] = (f"best of {samples} samples, {cooldown_s:g} s cooldown between samples, "
+                       "OMP_PROC_BIND=close; one thread pinned with sched_setaffinity; "
+                       "one thread: config 3 at batch 32, gemm shapes 1 warm-up + 1 call")
+    out["host"] = host_cpu()
+    out["label"] = "restated reference CPU path (oracle/, C + AVX2), not the Rust binary"
+    return out
 
 
 def time_gpu(fn, reps):
@@ -169,48 +271,87 @@ def time_graph(ctx, fn, reps):
     return a.elapsed_time(b) / (3 * reps)
 
 
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache: rotated inputs exceed it
+
+
 def bench_attention(R, ctx, reps):
     """128 images x 4 heads, T=64 (8x8), dh=32, SelfAttn
     buffer [128, 64, 384] (q/k/v at 0/128/256), tau=1, rel=0, no mask; Q, K, V
     ~N(0,1)/sqrt(32), dO ~N(0,1).  HBM-bound: algorithmic bytes (each tensor
-    once) fwd Q,K,V,O + P, bwd Q,K,V,dO,P in + dQ,dK,dV out."""
+    once) fwd Q,K,V,O + P, bwd Q,K,V,dO,P in + dQ,dK,dV out.  Timed twice:
+    the same buffers every call (they stay in the 256 MB Infinity Cache) and
+    with every call on its own copy of all its operands, rotating through
+    enough copies to exceed that cache, so each call reads HBM."""
     import torch
     n, h, dh, t = 128, 4, 32, 64
     c = h * dh
     g = torch.Generator(device="cuda").manual_seed(7)
-    qkv = torch.randn(n * t * 3 * c, device="cuda", generator=g) / dh ** 0.5
-    dout = torch.randn(n * t * c, device="cuda", generator=g)
     relidx, nrel = R.rel_index(8, 8, 8, 8)
     tau = torch.ones(h, device="cuda")
     rel = torch.zeros(h * nrel, device="cuda")
     core = R.Core(h, dh, t, t, relidx, nrel, False, ctx=ctx)
-    p = torch.empty(n * h * t * t, device="cuda")
-    o = torch.empty(n * t * c, device="cuda")
-    dqkv = torch.zeros_like(qkv)
-    dtau = torch.zeros(h, device="cuda")
-    drel = torch.zeros(h * nrel, device="cuda")
-    fwd = lambda: core.forward(n, qkv, 3 * c, 0, qkv, 3 * c, c, 2 * c, tau, rel, p, o)
-    bwd = lambda: core.backward(n, qkv, 3 * c, 0, qkv, 3 * c, c, 2 * c, tau, p, dout, dqkv, dqkv,
-                                dtau, drel)
-    fwd()
-    bwd()
-    # A call costs more host time than these kernels take, so back-to-back
-    # eager calls would time the host: record `reps` calls into a graph (on
-    # a capture stream given to the library's context) and time its replays.
-    tf, tb = time_graph(ctx, fwd, reps), time_graph(ctx, bwd, reps)
     mb = n * h * t * dh * 4  # one [n, h, t, dh] tensor, bytes
     pb = n * h * t * t * 4
+    ncopy = -(-MALL_BYTES // (7 * mb + pb)) + 1
+    sets = []
+    for _ in range(ncopy):
+        qkv = torch.randn(n * t * 3 * c, device="cuda", generator=g) / dh ** 0.5
+        sets.append(dict(qkv=qkv, dout=torch.randn(n * t * c, device="cuda", generator=g),
+                         p=torch.empty(n * h * t * t, device="cuda"),
+                         o=torch.empty(n * t * c, device="cuda"), dqkv=torch.zeros_like(qkv)))
+    dtau = torch.zeros(h, device="cuda")
+    drel = torch.zeros(h * nrel, device="cuda")
+    state = {"i": 0}
+
+    def fwd(rot):
+        b = sets[state["i"] % ncopy] if rot else sets[0]
+        state["i"] += 1
+        core.forward(n, b["qkv"], 3 * c, 0, b["qkv"], 3 * c, c, 2 * c, tau, rel, b["p"], b["o"])
+
+    def bwd(rot, acc=False):
+        # SelfAttn::backward (attn.rs:418-438): dq, dk, dv written into one
+        # fused-QKV gradient; acc: the accumulating form (reads dqkv as well)
+        b = sets[state["i"] % ncopy] if rot else sets[0]
+        state["i"] += 1
+        core.backward(n, b["qkv"], 3 * c, 0, b["qkv"], 3 * c, c, 2 * c, tau, b["p"], b["dout"],
+                      b["dqkv"], b["dqkv"], dtau, drel, set_dq=not acc, set_dkv=not acc)
+
+    for b in sets:  # every copy gets a P before the backward reads it
+        core.forward(n, b["qkv"], 3 * c, 0, b["qkv"], 3 * c, c, 2 * c, tau, rel, b["p"], b["o"])
+    bwd(False)
+    # A call costs more host time than these kernels take, so back-to-back
+    # eager calls would time the host: record the calls into a graph (on a
+    # capture stream given to the library's context) and time its replays.
+    nrep = max(reps, 2 * ncopy)
+    times = {}
+    for rot in (False, True):
+        times[("fwd", rot)] = time_graph(ctx, lambda: fwd(rot), nrep)
+        times[("bwd", rot)] = time_graph(ctx, lambda: bwd(rot), nrep)
+    times[("bwd_accumulate", True)] = time_graph(ctx, lambda: bwd(True, acc=True), nrep)
     fwd_bytes, bwd_bytes = 4 * mb + pb, 7 * mb + pb
     fwd_flop = 2 * 2.0 * n * h * t * t * dh
     bwd_flop = 4 * 2.0 * n * h * t * t * dh
     res = {}
-    for name, ms, by, fl in (("fwd", tf, fwd_bytes, fwd_flop), ("bwd", tb, bwd_bytes, bwd_flop)):
-        gbs = by / (ms * 1e-3) / 1e9
-        res[name] = {"us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
-                     "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
-                     "TFLOP_s": round(fl / (ms * 1e-3) / 1e12, 3)}
-    res["workload"] = "config2: 512 (image, head) problems, T=64, dh=32, fwd + bwd"
-    res["timing"] = "graph replays of back-to-back calls (per call: launch gap included)"
+    for name, by, fl in (("fwd", fwd_bytes, fwd_flop), ("bwd", bwd_bytes, bwd_flop)):
+        for rot in (True, False):
+            ms = times[(name, rot)]
+            gbs = by / (ms * 1e-3) / 1e9
+            res[name + ("" if rot else "_cache_resident")] = {
+                "us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
+                "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+                "TFLOP_s": round(fl / (ms * 1e-3) / 1e12, 3), "bytes": by}
+    ms = times[("bwd_accumulate", True)]
+    acc_bytes = bwd_bytes + 3 * mb  # the old dQ, dK, dV read as well
+    res["bwd_accumulate"] = {"us": round(ms * 1e3, 2),
+                             "GB_s": round(acc_bytes / (ms * 1e-3) / 1e9, 1),
+                             "hbm_frac": round(acc_bytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                             "bytes": acc_bytes}
+    res["workload"] = ("config2: 512 (image, head) problems, T=64, dh=32, fwd + bwd (bwd as "
+                       "SelfAttn::backward: dq, dk, dv written; bwd_accumulate: added to dqkv)")
+    res["timing"] = (f"graph replays of {nrep} back-to-back calls (launch gaps included); "
+                     f"fwd / bwd: each call on its own operands, rotating over {ncopy} copies "
+                     f"({ncopy * (7 * mb + pb) >> 20} MiB, past the 256 MiB Infinity Cache); "
+                     "*_cache_resident: one set of operands")
     return res
 
 
@@ -499,41 +640,6 @@ def resnet_inputs_gpu(n, seed):
     return x, labels
 
 
-def cpu_baseline_resnet(budget_s=12.0):
-    """The oracle's ResNet-20 train step (restated reference CPU path: AVX2
-    micro-kernel convs, f64 BN statistics, OpenMP over images / channels) on
-    config-3 batches of 128, one untimed warm-up step, then steps until the
-    budget is used.  Returns images/s."""
-    import numpy as np
-    from oracle import pyorc as O
-    from oracle import pymodel as M
-    O.build()
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    threads = max(1, min(threads, 16, os.cpu_count() or 1))
-    c = RESNET
-    rng = O.Rng(2026)
-    n = c["batch"]
-    u = rng.uniform_vec(n * 3 * 32 * 32).reshape(n, 3, 32, 32)
-    x = ((u - np.array(CIFAR_MEAN, np.float32)[None, :, None, None]) /
-         np.array(CIFAR_STD, np.float32)[None, :, None, None]).astype(np.float32)
-    labels = np.array([rng.below(100) for _ in range(n)], np.uint32)
-    net = M.ResNet(c["depth_n"], c["width"], c["nclass"], c["seed"])
-    with O.threads(threads):
-        net.train_step(x, labels, c["smooth"], c["lr"], c["mom"], c["wd"])  # warm-up
-        steps, t0 = 0, time.perf_counter()
-        while True:
-            net.train_step(x, labels, c["smooth"], c["lr"], c["mom"], c["wd"])
-            steps += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s or el / steps * (steps + 1) > 2.5 * budget_s:
-                break
-    return {"value": round(steps * n / el, 2), "unit": "images/s", "cores": threads,
-            "kind": "port",
-            "sample": f"config-3 ResNet-20 W32 train step (fwd + softmax-CE + bwd + SGD) at batch "
-                      f"{n}, {steps} steps in {el:.1f}s after 1 warm-up step; oracle/ AVX2 "
-                      f"restatement, OpenMP {threads} threads"}
-
-
 def bench_resnet(R, ctx, steps, warmup):
     """Config 3: the ResNet-20 train step through rnn_resnet_train_step."""
     import torch
@@ -737,10 +843,23 @@ def main():
     vit_optim = bench_rustvit_optim(R, ctx, 5, 0 if args.no_cpu else args.cpu_budget / 4)
     vit_step = bench_rustvit_step(R, ctx, 5, 2)
 
-    cpu = sweep_cpu = None
+    cpu = sweep_cpu = proto = None
     if not args.no_cpu:
-        cpu = cpu_baseline_resnet(args.cpu_budget)
-        sweep_cpu = cpu_baseline(args.cpu_budget / 2)
+        proto = cpu_protocol()
+        a1, a0 = proto["all_cores"], proto["one_thread"]
+        cpu = {"value": a1["config3_step"], "unit": "images/s", "cores": a1["threads"],
+               "kind": "port",
+               "sample": "config-3 ResNet-20 W32 train step (fwd + softmax-CE + bwd + SGD) at "
+                         "batch 128 on the same inputs, one step per sample after a warm-up "
+                         f"step, best of 3 with cooldown; {proto['label']}, OpenMP "
+                         f"{a1['threads']} threads",
+               "one_thread_value": a0["config3_step"],
+               "host": proto["host"]}
+        sweep_cpu = {"value": round(a1["config1_sweep"] / 1e3, 4), "unit": "TFLOP/s",
+                     "cores": a1["threads"], "kind": "port",
+                     "sample": "config-1 sweep (7 conv shapes x fwd/dX/dW) at batch 128, best of "
+                               f"3; {proto['label']}",
+                     "one_thread_value": round(a0["config1_sweep"] / 1e3, 4)}
 
     c = RESNET
     model_tf = rn["flop_per_image"] * rn["images_s"] / 1e12
@@ -771,7 +890,7 @@ def main():
             "flop_per_step": sweep_flops, "roofline": sweep_roof, "cpu_baseline": sweep_cpu,
             "per_op": per_op},
         "config2_attention": attention, "gemmbench": gemms, "rustvit_optimizer": vit_optim,
-        "config4_rustvit_step": vit_step,
+        "config4_rustvit_step": vit_step, "cpu_reference_path": proto,
     }
     print(json.dumps(out))
 

@@ -180,6 +180,17 @@ int rnn_attn_forward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float
 int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
                       const float *kv, const float *tau, const float *p, const float *dout,
                       float *dq, float *dkv, float *dtau, float *drel);
+/* Core::backward with dq and/or dkv OVERWRITTEN instead of accumulated
+ * (flags: RNN_ATTN_SET_DQ, RNN_ATTN_SET_DKV; dtau and drel always
+ * accumulate).  SelfAttn::backward (attn.rs:418-438) accumulates into freshly
+ * zeroed dq and dkv buffers and CrossAttn::backward (attn.rs:533-551) into a
+ * zeroed dq: the same values, without the clearing pass and the read of the
+ * old contents.  flags 0 is rnn_attn_backward. */
+#define RNN_ATTN_SET_DQ 1u
+#define RNN_ATTN_SET_DKV 2u
+int rnn_attn_backward_ex(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
+                         const float *kv, const float *tau, const float *p, const float *dout,
+                         float *dq, float *dkv, float *dtau, float *drel, uint32_t flags);
 
 /* ---------------------------------------------------------- linear.rs */
 /* Linear::forward (linear.rs:44-63): y[rows x fout] = x W^T + b (b may be NULL). */

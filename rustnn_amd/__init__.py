@@ -118,6 +118,8 @@ def lib():
             "rnn_attn_forward": (_i, [_vp, P(AttnDesc), _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_attn_backward": (_i, [_vp, P(AttnDesc), _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                        _vp, _vp]),
+            "rnn_attn_backward_ex": (_i, [_vp, P(AttnDesc), _sz, _vp, _vp, _vp, _vp, _vp, _vp,
+                                          _vp, _vp, _vp, _u32]),
             "rnn_linear_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
             "rnn_linear_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_dbg_im2col": (_i, [_vp, P(ConvSpec), _vp, _vp]),
@@ -525,17 +527,20 @@ class Core:
         return p, o
 
     def backward(self, n, q, qstride, qoff, kv, kvstride, koff, voff, tau, p, dout, dq, dkv, dtau,
-                 drel):
-        """Core::backward (attn.rs:226-343): accumulates into dq, dkv, dtau, drel."""
+                 drel, set_dq=False, set_dkv=False):
+        """Core::backward (attn.rs:226-343): accumulates into dq, dkv, dtau, drel;
+        set_dq / set_dkv overwrite dq / dkv instead (the values zeroed buffers
+        would receive)."""
         d = self.desc(qstride, qoff, kvstride, koff, voff)
         nq = (n * self.tq - 1) * qstride + qoff + self.h * self.dh if n else 0
         nkv = (n * self.tk - 1) * kvstride + max(koff, voff) + self.h * self.dh if n else 0
-        self.ctx.check(lib().rnn_attn_backward(
+        flags = (1 if set_dq else 0) | (2 if set_dkv else 0)
+        self.ctx.check(lib().rnn_attn_backward_ex(
             self.ctx.h, C.byref(d), n, _ptr(q, nq, "q"), _ptr(kv, nkv, "kv"),
             _ptr(tau, self.h, "tau"), _ptr(p, n * self.h * self.tq * self.tk, "p"),
             _ptr(dout, n * self.tq * self.h * self.dh, "dout"), _ptr(dq, nq, "dq"),
             _ptr(dkv, nkv, "dkv"), _ptr(dtau, self.h, "dtau"),
-            _ptr(drel, self.h * self.nrel, "drel")))
+            _ptr(drel, self.h * self.nrel, "drel"), flags))
 
 
 # ------------------------------------------------------------------ linear.rs

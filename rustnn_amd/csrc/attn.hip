@@ -1,9 +1,4 @@
-// Batched small attention (attn.rs Core) on gfx950: one workgroup of two
-// waves per (image, head), each wave 32 query rows; the operands live in
-// registers (contiguous half-row loads in the k order the MFMA A and B
-// layouts share), the score tiles are computed transposed (S^T = K Q^T) so
-// that a query row spans lanes l and l^32 only, and 32x32 fp32 MFMA tiles
-// do every product.
+// Batched small attention (attn.rs Core) on gfx950.
 //
 // Reference: Core::forward (attn.rs:148-223) runs per image (rayon) and per
 // head: gather Q/K/V rows, S = QK^T (gemm_small), x = tau*S + rel[idx] with the
@@ -11,10 +6,28 @@
 // dV = P^T dO, dP = dO V^T, dS = P o (dP - rowdot), recomputed raw S for dtau,
 // drel scatter by rel index, dQ = tau*dS K, dK = tau*dS^T Q.
 //
-// Here dtau and drel are reduced without atomics: each workgroup writes its
-// (image, head) partial -- drel through an inverse index (for every bias slot,
-// the positions that map to it, in ascending order) -- and a second kernel
-// adds the partials over images in image order.
+// tq, tk <= 64 and dh <= 64 (every Core of the reference's models but the
+// rustvit's cross-attention over 256 memory tokens): one workgroup per
+// (image, head) of up to four waves; wave w owns queries [16w, 16w + 16) and
+// every product runs on 16x16x4 fp32 MFMA tiles.  K and V (and, in the
+// backward, Q and dO) are staged once per workgroup in LDS and shared by the
+// waves, so HBM sees each tensor once.
+//
+// Score tiles are computed transposed (S^T = K Q^T): lane l of wave w then
+// holds query 16w + l%16 and, in register v of key tile t, key 16t + 4(l/16)
+// + v.  A query's row spans the four lanes l%16 + 16g: max and sum take two
+// cross-lane steps, and P's registers are, step for step, the A operand of the
+// products over keys (O = P V, dS K) -- step (t, v) pairs key 16t + 4(l/16) +
+// v for A and B alike, which the B operands read as 4 consecutive floats of a
+// transposed LDS copy.
+//
+// dtau uses the identity sum dS o (Q K^T) = sum_q Q[q] . (dS K)[q]: the
+// product dS K is the one dQ needs anyway, so the reference's recomputed QK^T
+// is not needed; the partial sums are f64 (the terms cancel to about 1% of
+// their size).  dtau and drel are reduced without atomics: each workgroup
+// writes its (image, head) partial -- drel through an inverse index (for
+// every bias slot, the positions that map to it, in ascending order) -- and a
+// second kernel adds the partials over images in image order.
 #include "rnn_internal.h"
 
 #include <algorithm>
@@ -22,428 +35,546 @@
 
 namespace {
 
-constexpr int MAXT = 64;   // tq, tk limit (padded to 32 or 64)
+constexpr int MAXT = 64;   // tq, tk limit of the workgroup kernels
 constexpr int MAXDH = 64;  // head-dim limit
+constexpr int TS = 68;     // LDS row stride of the [64]-wide transposed tiles
+constexpr int LT = 4096;   // u32 entries of the lane-order relidx table
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct AttnArgs {
     const float *q, *kv, *tau, *rel, *p, *dout;
     float *pout, *o, *dq, *dkv;
-    double *dtau_part;             // [n][h]
-    float *drel_part;              // [n][h][nrel]
-    const uint32_t *relidx;        // [tq*tk]
-    const uint32_t *rowptr;        // [nrel+1] inverse index (drel gather)
-    const uint32_t *pos;           // [tq*tk] LDS offsets (row*LS + col), by bias slot
-    const uint32_t *rperm;         // [64][2][32] relidx in lane order (see key_of)
+    double *dtau_part;          // [n][h]
+    float *drel_part;           // [n][h][nrel]
+    const uint32_t *rowptr;     // [nrel+1] inverse index (drel gather)
+    const uint32_t *pos;        // [tq*tk] LDS offsets key*TS + q in the dS^T tile, by slot
+    const uint4 *lidx;          // [4 w][4 t][64 lanes] relidx of (query, keys) in lane order
     long long qstride, qoff, kvstride, koff, voff;
     int n, h, dh, tq, tk, nrel, mask;
-    int DHP;  // dh padded to 32 or 64
+    const u32x4 *blob;  // the drel index blob: rowptr u32 [nrel+1], positions u16 [tq*tk]
+    int blob_chunks;    // its 16-byte chunks, 0: gather through rowptr / pos in HBM
 };
 
-// Row reductions over the 32 lanes of a wave half (the 32 columns a 32x32
-// MFMA tile spreads over lanes): xor offsets below 32 stay inside the half.
-__device__ __forceinline__ float half_max(float v) {
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ float half_sum(float v) {
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+
+// v from the lane a DPP pattern names (both 32-bit halves moved).
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_mov_dpp((int)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+// Sum over the 64 lanes, every lane receiving it (a fixed tree: quads by
+// DPP xor 1 and 2, rows of 8 and 16 by DPP mirrors, then xor 16 and 32).
 __device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    v += dpp_d<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_d<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_d<0x141>(v);  // row_half_mirror
+    v += dpp_d<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
     return v;
 }
 
-__device__ __forceinline__ void zero16(f32x16 &a) {
-#pragma unroll
-    for (int v = 0; v < 16; v++) a[v] = 0.f;
-}
-
-// MFMA operands of a product over the head dimension (S = Q K^T, dP = dO V^T):
-// step s of lane half hh takes k = hh*HALF + s, for A and B alike, so a lane
-// holds HALF consecutive columns of one row -- a contiguous half-row.
-//
-// Loads are unconditional, from clamped (in-range) addresses.  Rows past the
-// matrix need no zeroing: they only reach score entries that are masked or
-// products with a zero P.  Columns past dh are summed over, so they are
-// zeroed (VEC = false only; VEC means dh == DHP with aligned rows, read as
-// float4).  A guarded load -- or a select the compiler may turn back into one
-// -- becomes a branch of its own, and the loads can no longer be issued
-// together.
 __device__ __forceinline__ float keep(float v, bool c) {
     return __uint_as_float(__float_as_uint(v) & (c ? 0xffffffffu : 0u));
 }
 
-template <int HALF, bool VEC>
-__device__ __forceinline__ void load_half(float (&r)[HALF], const float *base, long long stride,
-                                          int row, int nrows, int c0, int dh) {
+// Four consecutive floats of row `row` (clamped into [0, nrows)) at column
+// c0: one float4 load when VEC, else four loads from columns clamped below
+// dh.  Nothing is masked here -- an operation on a loaded value waits for the
+// load, and a branch around one splits the loads into blocks waited on in
+// turn -- so callers zero what lies past (nrows, dh) with mask4 where they
+// use the values.
+template <bool VEC>
+__device__ __forceinline__ float4 load4(const float *base, long long stride, int row, int nrows,
+                                        int c0, int dh) {
     const float *p = base + (long long)min(row, nrows - 1) * stride;
-    if constexpr (VEC) {
-#pragma unroll
-        for (int i = 0; i < HALF; i += 4) {
-            const float4 t = *reinterpret_cast<const float4 *>(p + c0 + i);
-            r[i] = t.x;
-            r[i + 1] = t.y;
-            r[i + 2] = t.z;
-            r[i + 3] = t.w;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < HALF; i++) r[i] = keep(p[min(c0 + i, dh - 1)], c0 + i < dh);
-    }
+    if constexpr (VEC) return *reinterpret_cast<const float4 *>(p + c0);
+    float4 r;
+    r.x = p[min(c0, dh - 1)];
+    r.y = p[min(c0 + 1, dh - 1)];
+    r.z = p[min(c0 + 2, dh - 1)];
+    r.w = p[min(c0 + 3, dh - 1)];
+    return r;
+}
+// v with every column past dh, or all of it when !row_ok, set to 0.
+__device__ __forceinline__ float4 mask4(float4 v, bool row_ok, int c0, int dh) {
+    return make_float4(keep(v.x, row_ok && c0 < dh), keep(v.y, row_ok && c0 + 1 < dh),
+                       keep(v.z, row_ok && c0 + 2 < dh), keep(v.w, row_ok && c0 + 3 < dh));
 }
 
-template <int HALF>
-__device__ __forceinline__ void mma_half(f32x16 &acc, const float (&a)[HALF],
-                                         const float (&b)[HALF]) {
-#pragma unroll
-    for (int s = 0; s < HALF; s++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], b[s], acc, 0, 0, 0);
-}
-
-// Rows [0, 64) x cols [0, DHP) of a strided matrix into LDS (row stride XS),
-// zero past (nrows, dh); 4-float groups with float4 loads when `vec`.
+// Rows [0, 64) x columns [0, DHP) of a strided [rows][dh] matrix, staged
+// into LDS by the 256 threads of a workgroup in two halves: load() issues the
+// thread's DHP/16 float4 loads together, store() zeroes what lies past
+// (nrows, dh) and puts them in LDS transposed (dst[c][r], stride TS) or as
+// rows (dst[r][c], stride DHP + 4).  Several tiles' loads are issued before
+// any store, so their latencies overlap.
 template <int DHP>
-__device__ __forceinline__ void stage_rows(float *dst, int XS, const float *src, long long stride,
-                                           int nrows, int dh, bool vec, int tid, int nthreads) {
-    constexpr int G = DHP / 4;  // 4-float groups per row (a power of two)
-    for (int idx = tid; idx < 64 * G; idx += nthreads) {
-        const int r = idx / G, c = (idx % G) * 4;
-        float t[4] = {0.f, 0.f, 0.f, 0.f};
-        if (r < nrows) {
-            const float *p = src + (long long)r * stride + c;
-            if (vec && c + 4 <= dh) {
-                const float4 v = *reinterpret_cast<const float4 *>(p);
-                t[0] = v.x;
-                t[1] = v.y;
-                t[2] = v.z;
-                t[3] = v.w;
-            } else {
+struct Tile {
+    static constexpr int G = DHP / 4, CPT = 64 * G / 256;  // float4 chunks per thread
+    float4 v[CPT];
+    template <bool VEC>
+    __device__ __forceinline__ void load(const float *src, long long stride, int nrows, int dh,
+                                         int tid) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) t[i] = c + i < dh ? p[i] : 0.f;
+        for (int j = 0; j < CPT; j++) {
+            const int i = tid + 256 * j, r = i / G, c = (i % G) * 4;
+            v[j] = load4<VEC>(src, stride, r, nrows, c, dh);
+        }
+    }
+    template <bool TRANS>
+    __device__ __forceinline__ void store(float *dst, int nrows, int dh, int tid) const {
+#pragma unroll
+        for (int j = 0; j < CPT; j++) {
+            const int i = tid + 256 * j, r = i / G, c = (i % G) * 4;
+            const float4 x = mask4(v[j], r < nrows, c, dh);
+            if constexpr (TRANS) {
+                dst[(c + 0) * TS + r] = x.x;
+                dst[(c + 1) * TS + r] = x.y;
+                dst[(c + 2) * TS + r] = x.z;
+                dst[(c + 3) * TS + r] = x.w;
+            } else {
+                *reinterpret_cast<float4 *>(dst + r * (DHP + 4) + c) = x;
             }
         }
-#pragma unroll
-        for (int i = 0; i < 4; i++) dst[r * XS + c + i] = t[i];
     }
-}
+};
 
-constexpr int LS = 65;  // LDS row stride of the 64 x 64 P / dS tiles
+__device__ __forceinline__ float4 lds4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
-// Transposed score tiles: S^T = K Q^T with A = K (key rows) and B = Q (query
-// rows), so in the accumulator layout lane l holds query qi = 32w + l%32 and
-// register v of key tile nt holds key kj = 32nt + 8(v/4) + 4(l/32) + v%4.  A
-// query row is then split over two lanes only (l and l ^ 32): row max and
-// sum take one cross-lane step.  And those registers are, step for step, the
-// A operand of a product over keys (O = P V, dQ = dS K): MFMA step s = 16nt
-// + v pairs key kj(s, half) for both operands.
-__device__ __forceinline__ int key_of(int nt, int v, int hh) {
-    return 32 * nt + 8 * (v >> 2) + 4 * hh + (v & 3);
-}
-
-// dst[r][d] += acc[v] for the 16 rows r = r0 + 8(v/4) + 4hh + v%4 of an
-// accumulator tile (column d): the 16 old values are loaded together (clamped
-// addresses), then added and stored where in range.
-__device__ __forceinline__ void accumulate16(float *dst, long long stride, int r0, int nrows, int d,
-                                             int dh, int hh, const f32x16 &acc) {
-    float old[16];
-    const int dc = min(d, dh - 1);
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int r = min(r0 + 8 * (v >> 2) + 4 * hh + (v & 3), nrows - 1);
-        old[v] = dst[(long long)r * stride + dc];
-    }
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int r = r0 + 8 * (v >> 2) + 4 * hh + (v & 3);
-        if (r < nrows && d < dh) dst[(long long)r * stride + d] = old[v] + acc[v];
-    }
-}
-
-// Core::forward (attn.rs:148-223) for one (image, head), tq, tk <= 64,
-// dh <= DHP (32 or 64).  Two waves; wave w owns queries [32w, 32w + 32):
-//   * S^T from half-row operands (K, Q straight from HBM into registers);
-//   * x = tau*S + rel[relidx] (the head's bias slots and the index table
-//     staged in LDS), diagonal -> -inf when masked, -inf outside (tq, tk);
-//   * softmax per query: exp(x - max) (-inf -> 0), times 1/sum (attn.rs:
-//     199-210), max and sum in-lane plus one exchange with lane ^ 32;
-//   * O = P V with P from the registers and V rows from HBM.
-template <int DHP, bool VEC>
-__global__ __launch_bounds__(128) void attn_fwd_kernel(AttnArgs g) {
-    constexpr int HALF = DHP / 2, NDT = DHP / 32;
+// Core::forward (attn.rs:148-223) for one (image, head): DHP (16, 32, 64) is
+// dh padded, NT = ceil(tk / 16) key tiles, one wave per 16 queries.
+//   * K rows and V^T staged in LDS, the head's bias slots too; each lane's Q
+//     slice (query 16w + l%16, head dims [g DHP/4, (g+1) DHP/4), g = l/16)
+//     and its 4 NT relidx entries straight from HBM; V is loaded last and
+//     stored to LDS after the softmax, so its latency overlaps the scores;
+//   * S^T = K Q^T, x = tau*S + rel[relidx], the diagonal -inf when masked,
+//     -inf past tk; softmax per query: max, exp(x - max) (-inf -> 0), times
+//     1/sum (attn.rs:199-210);
+//   * P rows to HBM (4 consecutive keys per lane and tile), O = P V.
+template <int DHP, int NT, bool VEC>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs g) {
+    constexpr int KSL = DHP / 4;  // head dims per lane slice
     extern __shared__ float smem[];
-    float *Pw = smem + wave_index() * 32 * LS;  // [32][LS] P rows of this wave
-    uint32_t *rp = reinterpret_cast<uint32_t *>(smem + 64 * LS);  // [64][2][32] lane-order relidx
-    float *rels = smem + 64 * LS + 4096;        // [nrel] bias slots of the head
-    const int tid = threadIdx.x, lane = tid & 63, w = wave_index();
-    const int l32 = lane & 31, hh = lane >> 5;
+    float *Kl = smem;                    // [64][DHP + 4]
+    float *Vt = Kl + 64 * (DHP + 4);     // [DHP][TS]
+    float *rels = Vt + DHP * TS;         // [nrel]
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_index(), nth = blockDim.x;
+    const int l16 = lane & 15, grp = lane >> 4;
     const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
     const int tq = g.tq, tk = g.tk, dh = g.dh;
     const float *qb = g.q + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
     const float *kb = g.kv + (long long)img * tk * g.kvstride + g.koff + (long long)hd * dh;
     const float *vb = g.kv + (long long)img * tk * g.kvstride + g.voff + (long long)hd * dh;
-    const int qi = 32 * w + l32;
+    const int qi = 16 * w + l16;
+    const float tau = g.tau[hd];  // (issued before the barrier, not waited for at it)
 
-    // Operands of S^T first (the load counter is in order: what is needed
-    // first is issued first), then the tables, then V.
-    float qb_[HALF], ka[2][HALF];
-    load_half<HALF, VEC>(qb_, qb, g.qstride, qi, tq, hh * HALF, dh);
+    // this lane's operands first (the load counter is in order), then the
+    // staged tiles
+    float4 qraw[KSL / 4];
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++)
-        load_half<HALF, VEC>(ka[nt], kb, g.kvstride, 32 * nt + l32, tk, hh * HALF, dh);
-    {  // relidx in lane order: 16 KB, coalesced 16-byte loads
-        const uint4 *src = reinterpret_cast<const uint4 *>(g.rperm);
-        uint4 t4[8];
+    for (int i = 0; i < KSL; i += 4) qraw[i / 4] = load4<VEC>(qb, g.qstride, qi, tq, grp * KSL + i, dh);
+    uint4 ri[NT];
 #pragma unroll
-        for (int i = 0; i < 8; i++) t4[i] = src[tid + 128 * i];
-#pragma unroll
-        for (int i = 0; i < 8; i++) reinterpret_cast<uint4 *>(rp)[tid + 128 * i] = t4[i];
-    }
-    for (int e = tid; e < g.nrel; e += blockDim.x) rels[e] = g.rel[(long long)hd * g.nrel + e];
-    f32x16 st[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        zero16(st[nt]);
-        mma_half<HALF>(st[nt], ka[nt], qb_);
-    }
-    // V rows as the B operand of O = P V (step s = 16nt + v).
-    float vv[NDT][32];
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-        for (int s2 = 0; s2 < 32; s2++) {
-            const int kj = key_of(s2 >> 4, s2 & 15, hh), d = 32 * dt + l32;
-            // rows past tk meet P = 0; columns past dh are not stored
-            vv[dt][s2] = vb[(long long)min(kj, tk - 1) * g.kvstride + min(d, dh - 1)];
-        }
+    for (int t = 0; t < NT; t++) ri[t] = g.lidx[(w * 4 + t) * 64 + lane];
+    Tile<DHP> kt, vt;
+    kt.template load<VEC>(kb, g.kvstride, tk, dh, tid);
+    const float *relh = g.rel + (long long)hd * g.nrel;
+    const float rel0 = relh[min(tid, g.nrel - 1)];
+    // V last: only O = P V needs it, so its latency overlaps the scores
+    vt.template load<VEC>(vb, g.kvstride, tk, dh, tid);
+    kt.template store<false>(Kl, tk, dh, tid);
+    if (tid < g.nrel) rels[tid] = rel0;
+    for (int e = tid + nth; e < g.nrel; e += nth) rels[e] = relh[e];
     __syncthreads();
-    const float t = g.tau[hd];
-    float x[2][16];
-    // bias reads first, all of them (the table holds valid slots everywhere)
-    {
-        const uint4 *mine = reinterpret_cast<const uint4 *>(rp + (qi * 2 + hh) * 32);
+
+    float qs[KSL];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint4 r4 = mine[i];
-            x[i >> 2][(i & 3) * 4 + 0] = rels[r4.x];
-            x[i >> 2][(i & 3) * 4 + 1] = rels[r4.y];
-            x[i >> 2][(i & 3) * 4 + 2] = rels[r4.z];
-            x[i >> 2][(i & 3) * 4 + 3] = rels[r4.w];
+    for (int i = 0; i < KSL; i += 4) {
+        const float4 t4 = mask4(qraw[i / 4], qi < tq, grp * KSL + i, dh);
+        qs[i] = t4.x;
+        qs[i + 1] = t4.y;
+        qs[i + 2] = t4.z;
+        qs[i + 3] = t4.w;
+    }
+
+    f32x4 st[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        st[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const float *kr = Kl + (16 * t + l16) * (DHP + 4) + grp * KSL;
+#pragma unroll
+        for (int s = 0; s < KSL; s += 4) {
+            const float4 a = lds4(kr + s);
+            st[t] = mfma16(a.x, qs[s], st[t]);
+            st[t] = mfma16(a.y, qs[s + 1], st[t]);
+            st[t] = mfma16(a.z, qs[s + 2], st[t]);
+            st[t] = mfma16(a.w, qs[s + 3], st[t]);
         }
     }
+    float x[NT][4];
     float mx = -INFINITY;
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++)
+    for (int t = 0; t < NT; t++) {
+        const uint32_t idx[4] = {ri[t].x, ri[t].y, ri[t].z, ri[t].w};
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int kj = key_of(nt, v, hh);
-            const bool live = qi < tq && kj < tk && !(g.mask && kj == qi);
-            const float xv = t * st[nt][v] + x[nt][v];
-            x[nt][v] = __uint_as_float(live ? __float_as_uint(xv) : 0xff800000u);  // -inf
-            mx = fmaxf(mx, x[nt][v]);
+        for (int v = 0; v < 4; v++) {
+            const int kj = 16 * t + 4 * grp + v;
+            const bool live = kj < tk && !(g.mask && kj == qi);
+            const float xv = tau * st[t][v] + rels[idx[v]];
+            x[t][v] = __uint_as_float(live ? __float_as_uint(xv) : 0xff800000u);  // -inf
+            mx = fmaxf(mx, x[t][v]);
         }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     float sum = 0.f;
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++)
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const float e = x[nt][v] == -INFINITY ? 0.f : __expf(x[nt][v] - mx);
-            x[nt][v] = e;
+        for (int v = 0; v < 4; v++) {
+            const float e = x[t][v] == -INFINITY ? 0.f : __expf(x[t][v] - mx);
+            x[t][v] = e;
             sum += e;
         }
+    sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
     const float inv = 1.0f / sum;
+    const bool qlive = qi < tq;
 #pragma unroll
-    for (int nt = 0; nt < 2; nt++)
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const float p = qi < tq ? x[nt][v] * inv : 0.f;
-            x[nt][v] = p;
-            Pw[l32 * LS + key_of(nt, v, hh)] = p;
+        for (int v = 0; v < 4; v++) x[t][v] = qlive ? x[t][v] * inv : 0.f;
+
+    if (qlive) {
+        float *pr = g.pout + (((long long)img * g.h + hd) * tq + qi) * tk;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int k0 = 16 * t + 4 * grp;
+            if constexpr (VEC) {
+                if (k0 < tk)
+                    *reinterpret_cast<float4 *>(pr + k0) =
+                        make_float4(x[t][0], x[t][1], x[t][2], x[t][3]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; v++)
+                    if (k0 + v < tk) pr[k0 + v] = x[t][v];
+            }
         }
-    // P rows to HBM through LDS: one coalesced row per store instruction.
-    float *pg = g.pout + ((long long)img * g.h + hd) * tq * tk;
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes done
-    __builtin_amdgcn_wave_barrier();
-    const int rows = min(32, tq - 32 * w);
-    if (lane < tk) {
-        float pr[32];
-#pragma unroll
-        for (int r = 0; r < 32; r++) pr[r] = Pw[r * LS + lane];
-#pragma unroll
-        for (int r = 0; r < 32; r++)
-            if (r < rows) pg[(long long)(32 * w + r) * tk + lane] = pr[r];
     }
+    vt.template store<true>(Vt, tk, dh, tid);
+    __syncthreads();
+    // O = P V: A = P (this lane's registers), B = V^T rows from LDS
     const int c = g.h * dh;
     float *od = g.o + (long long)img * tq * c + (long long)hd * dh;
 #pragma unroll
-    for (int dt = 0; dt < NDT; dt++) {
-        f32x16 acc;
-        zero16(acc);
+    for (int dt = 0; dt < DHP / 16; dt++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const float *vr = Vt + (16 * dt + l16) * TS + 4 * grp;
 #pragma unroll
-        for (int s2 = 0; s2 < 32; s2++)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(x[s2 >> 4][s2 & 15], vv[dt][s2], acc, 0, 0, 0);
+        for (int t = 0; t < NT; t++) {
+            const float4 b = lds4(vr + 16 * t);
+            acc = mfma16(x[t][0], b.x, acc);
+            acc = mfma16(x[t][1], b.y, acc);
+            acc = mfma16(x[t][2], b.z, acc);
+            acc = mfma16(x[t][3], b.w, acc);
+        }
+        const int d = 16 * dt + l16;
 #pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int q = 32 * w + 8 * (v >> 2) + 4 * hh + (v & 3), d = 32 * dt + l32;
+        for (int v = 0; v < 4; v++) {
+            const int q = 16 * w + 4 * grp + v;
             if (q < tq && d < dh) od[(long long)q * c + d] = acc[v];
         }
     }
 }
 
-// Core::backward (attn.rs:226-343) for one (image, head), same limits and
-// waves.  Phase 1 in registers, lane = query (as the forward): dP^T = V dO^T,
-// the recomputed raw S^T = K Q^T, P from HBM, the row dot <dP, P> (in-lane
-// plus one exchange), dS = P o (dP - dot), the dtau partial sum(dS o S).
-// dQ = tau*dS K takes dS straight from the registers and K rows from HBM.
-// P and dS go to LDS for the drel partial (inverse index, ascending
-// positions) and for dK = tau*dS^T Q and dV = P^T dO (key rows, Q and dO rows
-// from HBM).  dQ, dK, dV accumulate into HBM.
-template <int DHP, bool VEC>
-__global__ __launch_bounds__(128) void attn_bwd_kernel(AttnArgs g) {
-    constexpr int HALF = DHP / 2, NDT = DHP / 32;
+// dst[r][d] = old[v] + scale * val[v] (ACC) or scale * val[v] for the 4
+// rows r = r0 + v (column d), where in range; old holds the values loaded
+// earlier (old4).
+__device__ __forceinline__ void old4(float (&old)[4], const float *dst, long long stride, int r0,
+                                     int nrows, int d, int dh) {
+    const int dc = min(d, dh - 1);
+#pragma unroll
+    for (int v = 0; v < 4; v++) old[v] = dst[(long long)min(r0 + v, nrows - 1) * stride + dc];
+}
+template <bool ACC>
+__device__ __forceinline__ void store4(float *dst, long long stride, int r0, int nrows, int d,
+                                       int dh, const float (&old)[4], const f32x4 &val,
+                                       float scale) {
+#pragma unroll
+    for (int v = 0; v < 4; v++)
+        if (r0 + v < nrows && d < dh)
+            dst[(long long)(r0 + v) * stride + d] = ACC ? old[v] + scale * val[v] : scale * val[v];
+}
+
+// u32 chunks of 16 bytes of the drel index blob a thread carries in
+// registers from the start of the backward to the LDS it is copied to.
+constexpr int BLOB_CHUNKS = 6;
+
+// Core::backward (attn.rs:226-343) for one (image, head), same limits.
+// ACC: dQ, dK, dV accumulate (the reference's scatter_add); else they are
+// overwritten, which is what SelfAttn::backward's zeroed buffers yield
+// (attn.rs:418-438) without reading them.
+//
+// Loads in two groups, each thread's in issue order (the load counter
+// retires in order, so a wait for the first group leaves the second in
+// flight):
+//   1. phase 1's operands: P (query 16w + l%16, keys 16t + 4(l/16) + v) into
+//      registers; dO, V and K tiles, staged as dO^T, V rows, K^T;
+//   2. Q (staged as Q^T after phase 1), the old dQ, dK, dV (ACC) and the
+//      drel index blob (rowptr u32, positions u16), carried in registers
+//      into the LDS of V and K^T once phase 1 is done with them.
+// Phase 1 (wave w, queries [16w, 16w + 16)): dP^T = V dO^T, the row dot
+// <dP, P>, dS = P o (dP - dot); P^T and dS^T to LDS; dSK = dS K.  After the
+// second barrier: dQ = tau dSK and dtau += Q . dSK; phase 2 (wave w, keys
+// [16w, 16w + 16)): dV = P^T dO and dK = tau dS^T Q over the query tiles;
+// then the drel partial of the (image, head) through the inverse index.  QT
+// / NT: query / key tiles; the waves cover max(QT, NT).
+template <int DHP, int NT, bool VEC, bool ACC>
+__global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs g) {
+    constexpr int KSL = DHP / 4, NDT = DHP / 16;
     extern __shared__ float smem[];
-    float *Pl = smem, *Sl = Pl + 64 * LS;
-    double *dred = (double *)(Sl + 64 * LS);  // 8-byte aligned: 2 * 64 * LS floats before it
-    const int tid = threadIdx.x, lane = tid & 63, w = wave_index(), nthreads = blockDim.x;
-    const int l32 = lane & 31, hh = lane >> 5;
+    float *Vr = smem;                // [64][DHP + 4]
+    float *Kt = Vr + 64 * (DHP + 4); // [DHP][TS]
+    float *Qt = Kt + DHP * TS;       // [DHP][TS]
+    float *Ot = Qt + DHP * TS;       // [DHP][TS] dO^T
+    float *Pt = Ot + DHP * TS;       // [64][TS] P^T  [key][q]
+    float *St = Pt + 64 * TS;        // [64][TS] dS^T [key][q]
+    double *dred = reinterpret_cast<double *>(St + 64 * TS);  // [4], 8-byte aligned
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_index(), nth = blockDim.x;
+    const int l16 = lane & 15, grp = lane >> 4;
     const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
     const int tq = g.tq, tk = g.tk, dh = g.dh, c = g.h * dh;
+    const int QT = (tq + 15) >> 4;
     const float *qb = g.q + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
     const float *kb = g.kv + (long long)img * tk * g.kvstride + g.koff + (long long)hd * dh;
     const float *vb = g.kv + (long long)img * tk * g.kvstride + g.voff + (long long)hd * dh;
     const float *ob = g.dout + (long long)img * tq * c + (long long)hd * dh;
-    const float *pb = g.p + ((long long)img * g.h + hd) * tq * tk;
-    const int qi = 32 * w + l32;
-
-    // P of this wave's rows into LDS with coalesced row loads (0 outside).
-#pragma unroll 8
-    for (int r = 0; r < 32; r++) {
-        const int q = 32 * w + r;
-        const float t0 = pb[(long long)min(q, tq - 1) * tk + min(lane, tk - 1)];
-        Pl[q * LS + lane] = keep(t0, q < tq && lane < tk);
-    }
-    float qv[HALF], ov[HALF];
-    load_half<HALF, VEC>(qv, qb, g.qstride, qi, tq, hh * HALF, dh);
-    load_half<HALF, VEC>(ov, ob, c, qi, tq, hh * HALF, dh);
-    f32x16 dp[2], sr[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++) {
-        float ka[HALF], va[HALF];
-        load_half<HALF, VEC>(ka, kb, g.kvstride, 32 * nt + l32, tk, hh * HALF, dh);
-        load_half<HALF, VEC>(va, vb, g.kvstride, 32 * nt + l32, tk, hh * HALF, dh);
-        zero16(dp[nt]);
-        zero16(sr[nt]);
-        mma_half<HALF>(dp[nt], va, ov);
-        mma_half<HALF>(sr[nt], ka, qv);
-    }
-    // K rows as the B operand of dQ = dS K (step s = 16nt + v).
-    float kk[NDT][32];
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++)
-#pragma unroll
-        for (int s2 = 0; s2 < 32; s2++) {
-            const int kj = key_of(s2 >> 4, s2 & 15, hh), d = 32 * dt + l32;
-            // rows past tk meet dS = 0; columns past dh are not stored
-            kk[dt][s2] = kb[(long long)min(kj, tk - 1) * g.kvstride + min(d, dh - 1)];
-        }
-    // P in the accumulator layout, from this wave's LDS rows.
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-    float pv[2][16];
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) pv[nt][v] = Pl[qi * LS + key_of(nt, v, hh)];
-    // dS = P o (dP - <dP, P>) (attn.rs:280-290); dtau partial (attn.rs:292-308)
-    float dot = 0.f;
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) dot += dp[nt][v] * pv[nt][v];
-    dot += __shfl_xor(dot, 32, 64);
-    float tpart = 0.f;
-    const float t = g.tau[hd];
-    float ds[2][16];
-#pragma unroll
-    for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) {
-            const int kj = key_of(nt, v, hh);
-            const float d0 = pv[nt][v] * (dp[nt][v] - dot);  // 0 outside (tq, tk): P is 0
-            tpart += d0 * sr[nt][v];
-            Sl[qi * LS + kj] = d0;
-            ds[nt][v] = d0 * t;  // attn.rs:316: dS *= tau
-        }
-    // dtau is a sum whose terms cancel to about 1% of their size: the lane
-    // partials are added in f64 from here on
-    const double tsum = wave_sum_d((double)tpart);
-    if (lane == 0) dred[w] = tsum;
-    // dQ = tau*dS K (attn.rs:319-323): queries of this lane, from registers
     float *dqi = g.dq + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
-#pragma unroll
-    for (int dt = 0; dt < NDT; dt++) {
-        f32x16 acc;
-        zero16(acc);
-#pragma unroll
-        for (int s2 = 0; s2 < 32; s2++)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ds[s2 >> 4][s2 & 15], kk[dt][s2], acc, 0, 0, 0);
-        accumulate16(dqi, g.qstride, 32 * w, tq, 32 * dt + l32, dh, hh, acc);
-    }
-    __syncthreads();
-    // drel partial: gather by inverse index in ascending position (attn.rs:309-315)
-    float *drp = g.drel_part + ((long long)img * g.h + hd) * g.nrel;
-    for (int r = tid; r < g.nrel; r += nthreads) {
-        float sacc = 0.f;
-        const uint32_t e0 = g.rowptr[r], e1 = g.rowptr[r + 1];
-        for (uint32_t e = e0; e < e1; e += 8) {
-            uint32_t off[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) off[u] = e + u < e1 ? g.pos[e + u] : 0u;
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (e + u < e1) sacc += Sl[off[u]];
-        }
-        drp[r] = sacc;
-    }
-    if (tid == 0) g.dtau_part[(long long)img * g.h + hd] = dred[0] + dred[1];
-    // dK = tau*dS^T Q and dV = P^T dO (attn.rs:270-274, 324-327): key rows
-    // [32w, 32w + 32), A from LDS (transposed reads), Q / dO rows from HBM.
     float *dki = g.dkv + (long long)img * tk * g.kvstride + g.koff + (long long)hd * dh;
     float *dvi = g.dkv + (long long)img * tk * g.kvstride + g.voff + (long long)hd * dh;
-    const int kr = 32 * w + l32;
+    const int qi = 16 * w + l16, r0 = 16 * w + 4 * grp;
+    const bool qwave = w < QT, qlive = qi < tq, kwave = 16 * w < tk;
+    const float tau = g.tau[hd];
+
+    // (every load unconditional, from clamped addresses: a branch would
+    // split them into blocks the compiler waits between)
+    float pv[NT][4];
+    {
+        const float *pr = g.p + (((long long)img * g.h + hd) * tq + min(qi, tq - 1)) * tk;
 #pragma unroll
-    for (int dt = 0; dt < NDT; dt++) {
-        f32x16 ak, av;
-        zero16(ak);
-        zero16(av);
-        for (int s0 = 0; s0 < 32; s0 += 16) {
-            float qv2[16], ov2[16];
+        for (int t = 0; t < NT; t++) {
+            const int k0 = 16 * t + 4 * grp;
+            if constexpr (VEC) {
+                const float4 p4 = *reinterpret_cast<const float4 *>(pr + min(k0, tk - 4));
+                pv[t][0] = p4.x;
+                pv[t][1] = p4.y;
+                pv[t][2] = p4.z;
+                pv[t][3] = p4.w;
+            } else {
 #pragma unroll
-            for (int u = 0; u < 16; u++) {
-                const int q = key_of((s0 + u) >> 4, (s0 + u) & 15, hh), d = 32 * dt + l32;
-                // rows past tq meet dS = P = 0; columns past dh are not stored
-                const int qc = min(q, tq - 1), dc = min(d, dh - 1);
-                qv2[u] = qb[(long long)qc * g.qstride + dc];
-                ov2[u] = ob[(long long)qc * c + dc];
-            }
-#pragma unroll
-            for (int u = 0; u < 16; u++) {
-                const int q = key_of((s0 + u) >> 4, (s0 + u) & 15, hh);
-                ak = __builtin_amdgcn_mfma_f32_32x32x2f32(t * Sl[q * LS + kr], qv2[u], ak, 0, 0, 0);
-                av = __builtin_amdgcn_mfma_f32_32x32x2f32(Pl[q * LS + kr], ov2[u], av, 0, 0, 0);
+                for (int v = 0; v < 4; v++) pv[t][v] = pr[min(k0 + v, tk - 1)];
             }
         }
-        accumulate16(dki, g.kvstride, 32 * w, tk, 32 * dt + l32, dh, hh, ak);
-        accumulate16(dvi, g.kvstride, 32 * w, tk, 32 * dt + l32, dh, hh, av);
+    }
+    Tile<DHP> ot, vt, kt, qt;
+    ot.template load<VEC>(ob, c, tq, dh, tid);
+    vt.template load<VEC>(vb, g.kvstride, tk, dh, tid);
+    kt.template load<VEC>(kb, g.kvstride, tk, dh, tid);
+    qt.template load<VEC>(qb, g.qstride, tq, dh, tid);
+    float oq[NDT][4], ok[NDT][4], ov[NDT][4];
+    if constexpr (ACC) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            old4(oq[dt], dqi, g.qstride, r0, tq, 16 * dt + l16, dh);
+            old4(ok[dt], dki, g.kvstride, r0, tk, 16 * dt + l16, dh);
+            old4(ov[dt], dvi, g.kvstride, r0, tk, 16 * dt + l16, dh);
+        }
+    }
+    // (a native vector type: a HIP uint4 array is copied through scratch)
+    u32x4 blob[BLOB_CHUNKS];
+    {
+        const int last = max(g.blob_chunks, 1) - 1;  // the blob holds one chunk at least
+#pragma unroll
+        for (int j = 0; j < BLOB_CHUNKS; j++) blob[j] = g.blob[min(tid + j * nth, last)];
+    }
+    ot.template store<true>(Ot, tq, dh, tid);
+    vt.template store<false>(Vr, tk, dh, tid);
+    kt.template store<true>(Kt, tk, dh, tid);
+    __syncthreads();
+
+    f32x4 dsk[NDT];
+    if (qwave) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++)
+                pv[t][v] = keep(pv[t][v], qlive && 16 * t + 4 * grp + v < tk);
+        // this lane's dO slice (query qi, head dims [grp KSL, (grp+1) KSL))
+        float os[KSL];
+#pragma unroll
+        for (int s = 0; s < KSL; s++) os[s] = Ot[(grp * KSL + s) * TS + qi];
+        // dP^T = V dO^T (attn.rs:272-278): the score-tile layout of P
+        f32x4 dp[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            dp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const float *vr = Vr + (16 * t + l16) * (DHP + 4) + grp * KSL;
+#pragma unroll
+            for (int s = 0; s < KSL; s += 4) {
+                const float4 a = lds4(vr + s);
+                dp[t] = mfma16(a.x, os[s], dp[t]);
+                dp[t] = mfma16(a.y, os[s + 1], dp[t]);
+                dp[t] = mfma16(a.z, os[s + 2], dp[t]);
+                dp[t] = mfma16(a.w, os[s + 3], dp[t]);
+            }
+        }
+        // dS = P o (dP - <dP, P>) (attn.rs:280-290)
+        float dot = 0.f;
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) dot += dp[t][v] * pv[t][v];
+        dot += __shfl_xor(dot, 16, 64);
+        dot += __shfl_xor(dot, 32, 64);
+        float ds[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                ds[t][v] = pv[t][v] * (dp[t][v] - dot);  // 0 where P is 0
+                const int kj = 16 * t + 4 * grp + v;
+                Pt[kj * TS + qi] = pv[t][v];
+                St[kj * TS + qi] = ds[t][v];
+            }
+        // dSK = dS K (attn.rs:316-323, before the tau scaling)
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            dsk[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const float *kr = Kt + (16 * dt + l16) * TS + 4 * grp;
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                const float4 b = lds4(kr + 16 * t);
+                dsk[dt] = mfma16(ds[t][0], b.x, dsk[dt]);
+                dsk[dt] = mfma16(ds[t][1], b.y, dsk[dt]);
+                dsk[dt] = mfma16(ds[t][2], b.z, dsk[dt]);
+                dsk[dt] = mfma16(ds[t][3], b.w, dsk[dt]);
+            }
+        }
+    }
+    // (waves past the query tiles write no P^T / dS^T columns: phase 2 reads
+    // only the columns of the first QT tiles)
+    qt.template store<true>(Qt, tq, dh, tid);
+    __syncthreads();
+
+    double tpart = 0.0;
+    if (qwave) {
+        // dQ = tau dSK (attn.rs:316-323); dtau += Q . dSK
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const int d = 16 * dt + l16;
+            const float4 q4 = lds4(Qt + d * TS + r0);
+            tpart += (double)(dsk[dt][0] * q4.x) + (double)(dsk[dt][1] * q4.y) +
+                     (double)(dsk[dt][2] * q4.z) + (double)(dsk[dt][3] * q4.w);
+            store4<ACC>(dqi, g.qstride, r0, tq, d, dh, oq[dt], dsk[dt], tau);
+        }
+    }
+    tpart = wave_sum_d(tpart);
+    if (lane == 0) dred[w] = tpart;
+
+    // V and K^T are dead: the drel index blob goes where they were
+    uint32_t *lblob = reinterpret_cast<uint32_t *>(smem);
+    if (g.blob_chunks) {
+#pragma unroll
+        for (int j = 0; j < BLOB_CHUNKS; j++) {
+            const int ch = tid + j * nth;
+            if (ch < g.blob_chunks) reinterpret_cast<u32x4 *>(lblob)[ch] = blob[j];
+        }
+    }
+    // phase 2: keys [16w, 16w + 16); k runs over queries q = 16ta + 4grp + v
+    // (per query tile: P^T and dS^T read once, 2 NDT accumulators)
+    if (kwave) {
+        const int kr0 = 16 * w + l16;
+        f32x4 av[NDT], ak[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            av[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            ak[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int ta = 0; ta < 4; ta++) {
+            if (ta >= QT) break;
+            const int q0 = 16 * ta + 4 * grp;
+            const float4 pa = lds4(Pt + kr0 * TS + q0);
+            const float4 sa = lds4(St + kr0 * TS + q0);
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                const int d = 16 * dt + l16;
+                const float4 ob4 = lds4(Ot + d * TS + q0);
+                const float4 qb4 = lds4(Qt + d * TS + q0);
+                av[dt] = mfma16(pa.x, ob4.x, av[dt]);
+                ak[dt] = mfma16(sa.x, qb4.x, ak[dt]);
+                av[dt] = mfma16(pa.y, ob4.y, av[dt]);
+                ak[dt] = mfma16(sa.y, qb4.y, ak[dt]);
+                av[dt] = mfma16(pa.z, ob4.z, av[dt]);
+                ak[dt] = mfma16(sa.z, qb4.z, ak[dt]);
+                av[dt] = mfma16(pa.w, ob4.w, av[dt]);
+                ak[dt] = mfma16(sa.w, qb4.w, ak[dt]);
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const int d = 16 * dt + l16;
+            store4<ACC>(dvi, g.kvstride, r0, tk, d, dh, ov[dt], av[dt], 1.0f);
+            store4<ACC>(dki, g.kvstride, r0, tk, d, dh, ok[dt], ak[dt], tau);
+        }
+    }
+    __syncthreads();  // the blob in LDS, the dtau shares in dred
+    // drel partial: gather by inverse index in ascending position (attn.rs:309-315)
+    float *drp = g.drel_part + ((long long)img * g.h + hd) * g.nrel;
+    if (g.blob_chunks) {
+        const uint16_t *lpos = reinterpret_cast<const uint16_t *>(lblob + g.nrel + 1);
+        for (int r = tid; r < g.nrel; r += nth) {
+            float sacc = 0.f;
+            const uint32_t e0 = lblob[r], e1 = lblob[r + 1];
+            // 8 positions, then 8 values, read ahead of the in-order adds
+            for (uint32_t e = e0; e < e1; e += 8) {
+                uint32_t off[8];
+                float val[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) off[u] = lpos[min(e + u, e1 - 1)];
+#pragma unroll
+                for (int u = 0; u < 8; u++) val[u] = St[off[u]];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (e + u < e1) sacc += val[u];
+            }
+            drp[r] = sacc;
+        }
+    } else {
+        for (int r = tid; r < g.nrel; r += nth) {
+            float sacc = 0.f;
+            const uint32_t e0 = g.rowptr[r], e1 = g.rowptr[r + 1];
+            for (uint32_t e = e0; e < e1; e += 8) {
+                uint32_t off[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) off[u] = e + u < e1 ? g.pos[e + u] : 0u;
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (e + u < e1) sacc += St[off[u]];
+            }
+            drp[r] = sacc;
+        }
+    }
+    if (tid == 0) {
+        double s = 0.0;
+        for (int i = 0; i < (int)(blockDim.x >> 6); i++) s += dred[i];
+        g.dtau_part[(long long)img * g.h + hd] = s;
     }
 }
 
@@ -464,6 +595,9 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const double *dtau_par
     const long long stride = is_rel ? per : h;
     const int G = (n + ATTN_RED_PARTS - 1) / ATTN_RED_PARTS;
     const int i0 = j * G, i1 = min(n, i0 + G);
+    // the value added to, loaded ahead (its latency overlaps the partials')
+    float old = 0.f;
+    if (j == 0 && live) old = is_rel ? drel[e] : dtau[e - per];
     double s = 0.0;
     if (live && is_rel) {
         float fs = 0.f;
@@ -479,7 +613,14 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const double *dtau_par
         s = fs;
     } else if (live) {
         const double *src = dtau_part + (e - per);
-        for (int b = i0; b < i1; b++) s += src[(long long)b * stride];
+        for (int b = i0; b < i1; b += 16) {
+            double v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = b + u < i1 ? src[(long long)(b + u) * stride] : 0.0;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (b + u < i1) s += v[u];
+        }
     }
     part[j][el] = s;
     __syncthreads();
@@ -492,16 +633,27 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(const double *dtau_par
                 t = first ? (float)part[q][el] : t + (float)part[q][el];
                 first = false;
             }
-            drel[e] += t;
+            drel[e] = old + t;
         } else {
             double t = 0.0;
             for (int q = 0; q < ATTN_RED_PARTS; q++) {
                 if (q * G >= n) break;
                 t += part[q][el];
             }
-            dtau[e - per] += (float)t;
+            dtau[e - per] = old + (float)t;
         }
     }
+}
+
+// Columns [off, off + width) of `rows` rows of stride `stride` set to 0:
+// one wave per row (4 per block).
+__global__ __launch_bounds__(256) void attn_zero_cols_kernel(float *x, long long rows,
+                                                             long long stride, long long off,
+                                                             int width) {
+    const long long r = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    float *row = x + r * stride + off;
+    for (int j = threadIdx.x & 63; j < width; j += 64) row[j] = 0.f;
 }
 
 __global__ void rel_index_kernel(int th, int tw, int mh, int mw, uint32_t *idx) {
@@ -530,125 +682,6 @@ __global__ void rel_index_kernel(int th, int tw, int mh, int mw, uint32_t *idx) 
 }
 
 // tq or tk above 64: the composed path (batched GEMMs + row kernels).
-bool large_desc(const rnn_attn_desc *d) { return d->tq > MAXT || d->tk > MAXT; }
-
-int check_desc(rnn_ctx *ctx, const rnn_attn_desc *d) {
-    if (!d) return rnn_fail(ctx, RNN_E_NULL, "attn: desc is null");
-    if (!d->relidx) return rnn_fail(ctx, RNN_E_NULL, "attn: relidx is null");
-    if (!d->h || !d->dh || !d->tq || !d->tk || !d->nrel)
-        return rnn_fail(ctx, RNN_E_INVALID, "attn: zero dimension");
-    if (d->dh > MAXDH && !large_desc(d))
-        return rnn_fail(ctx, RNN_E_UNSUPPORTED,
-                        "attn: dh=%u beyond the register-resident kernel (64) at tq=%u tk=%u",
-                        d->dh, d->tq, d->tk);
-    if ((size_t)d->tq * d->tk > ((size_t)1 << 26) || d->tk > (1u << 20))
-        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: tq=%u tk=%u too large", d->tq, d->tk);
-    // The table last uploaded was validated already.
-    const size_t cnt = (size_t)d->tq * d->tk;
-    if (ctx->rel_dev && ctx->rel_nrel == d->nrel && ctx->rel_host.size() == cnt &&
-        std::memcmp(ctx->rel_host.data(), d->relidx, cnt * 4) == 0)
-        return RNN_OK;
-    for (size_t i = 0; i < cnt; i++)
-        if (d->relidx[i] >= d->nrel) return rnn_fail(ctx, RNN_E_INVALID, "attn: relidx >= nrel");
-    return RNN_OK;
-}
-
-// The lane-order table's place in the uploaded block: after relidx, rowptr
-// and pos, rounded up to 16 bytes.
-uint32_t *rperm_of(uint32_t *base, size_t cnt, size_t nrel) {
-    return base + rnn_round_up(cnt + (nrel + 1) + cnt, 4);
-}
-
-// Uploads relidx, its inverse index (CSR over bias slots) and the lane-order
-// table when the table differs from the last one.
-int upload_rel(rnn_ctx *ctx, const rnn_attn_desc *d) {
-    size_t cnt = (size_t)d->tq * d->tk;
-    if (ctx->rel_dev && ctx->rel_nrel == d->nrel && ctx->rel_host.size() == cnt &&
-        ctx->rel_tk == d->tk && std::memcmp(ctx->rel_host.data(), d->relidx, cnt * 4) == 0)
-        return RNN_OK;
-    const bool large = large_desc(d);
-    // + the lane-order table (16-byte aligned) of the register-resident kernels
-    size_t need = cnt + (d->nrel + 1) + cnt + (large ? 0 : 4096 + 4);
-    // The previous upload (and kernels reading it) must be done before reuse.
-    RNN_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    if (need > ctx->rel_cap) {
-        if (ctx->rel_dev) (void)hipFree(ctx->rel_dev);
-        ctx->rel_dev = nullptr;
-        RNN_HIP(ctx, hipMalloc(&ctx->rel_dev, need * 4));
-        ctx->rel_cap = need;
-    }
-    if (need > ctx->rel_pinned_cap) {
-        if (ctx->rel_pinned) (void)hipHostFree(ctx->rel_pinned);
-        ctx->rel_pinned = nullptr;
-        RNN_HIP(ctx, hipHostMalloc((void **)&ctx->rel_pinned, need * 4, hipHostMallocDefault));
-        ctx->rel_pinned_cap = need;
-    }
-    uint32_t *h = ctx->rel_pinned;
-    std::memcpy(h, d->relidx, cnt * 4);
-    uint32_t *rowptr = h + cnt, *pos = rowptr + d->nrel + 1;
-    std::vector<uint32_t> count(d->nrel + 1, 0);
-    for (size_t i = 0; i < cnt; i++) count[d->relidx[i] + 1]++;
-    for (uint32_t r = 0; r < d->nrel; r++) count[r + 1] += count[r];
-    for (uint32_t r = 0; r <= d->nrel; r++) rowptr[r] = count[r];
-    // positions: offsets into the kernels' LDS [tq][LS] score tiles, or, on
-    // the composed path, flat offsets q*tk + k into a [tq][tk] score matrix
-    for (size_t i = 0; i < cnt; i++)
-        pos[count[d->relidx[i]]++] =
-            large ? (uint32_t)i : (uint32_t)((i / d->tk) * LS + i % d->tk);
-    // relidx in the forward's lane order: entry (qi*2 + half)*32 + 16nt + v is
-    // the slot of query qi, key key_of(nt, v, half); clamped into the table,
-    // so every entry is a valid slot.
-    if (!large) {
-        uint32_t *rperm = rperm_of(h, cnt, d->nrel);
-        for (int q = 0; q < 64; q++)
-            for (int hf = 0; hf < 2; hf++)
-                for (int nt = 0; nt < 2; nt++)
-                    for (int v = 0; v < 16; v++) {
-                        const int kj = 32 * nt + 8 * (v >> 2) + 4 * hf + (v & 3);
-                        const int qc = std::min(q, (int)d->tq - 1);
-                        const int kc = std::min(kj, (int)d->tk - 1);
-                        rperm[(q * 2 + hf) * 32 + 16 * nt + v] =
-                            d->relidx[(size_t)qc * d->tk + kc];
-                    }
-    }
-    RNN_HIP(ctx, hipMemcpyAsync(ctx->rel_dev, h, need * 4, hipMemcpyHostToDevice, ctx->stream));
-    ctx->rel_host.assign(d->relidx, d->relidx + cnt);
-    ctx->rel_nrel = d->nrel;
-    ctx->rel_tk = d->tk;
-    return RNN_OK;
-}
-
-void fill_args(AttnArgs &g, rnn_ctx *ctx, const rnn_attn_desc *d, size_t n) {
-    std::memset(&g, 0, sizeof(g));
-    g.qstride = (long long)d->qstride;
-    g.qoff = (long long)d->qoff;
-    g.kvstride = (long long)d->kvstride;
-    g.koff = (long long)d->koff;
-    g.voff = (long long)d->voff;
-    g.n = (int)n;
-    g.h = d->h;
-    g.dh = d->dh;
-    g.tq = d->tq;
-    g.tk = d->tk;
-    g.nrel = d->nrel;
-    g.mask = d->mask_diag ? 1 : 0;
-    g.DHP = d->dh <= 32 ? 32 : 64;
-    size_t cnt = (size_t)d->tq * d->tk;
-    g.relidx = ctx->rel_dev;
-    g.rowptr = ctx->rel_dev + cnt;
-    g.pos = ctx->rel_dev + cnt + d->nrel + 1;
-    g.rperm = rperm_of(ctx->rel_dev, cnt, d->nrel);
-}
-
-inline bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
-
-// float4 row loads need 16-byte aligned row starts for every image and head.
-// VEC kernels: dh == DHP (no column padding) and float4-aligned rows.
-bool use_vec(const AttnArgs &g) {
-    return g.dh == g.DHP && g.qstride % 4 == 0 && g.qoff % 4 == 0 && al16(g.q) &&
-           g.kvstride % 4 == 0 && g.koff % 4 == 0 && g.voff % 4 == 0 && al16(g.kv) &&
-           (g.dout == nullptr || al16(g.dout));
-}
 
 // ---------------------------------------------------------------------------
 // The composed path for tq or tk above 64 (the rustvit's cross-attention:
@@ -778,31 +811,221 @@ __global__ __launch_bounds__(256) void attn_drel_sum_kernel(const float *__restr
     drel[e] += s;
 }
 
-size_t bwd_lds() { return (size_t)2 * 64 * LS * 4 + 2 * sizeof(double); }
-size_t fwd_lds(size_t nrel) { return ((size_t)64 * LS + 4096 + nrel) * 4; }
 
-bool lds_attr_done = false;
-void set_lds_limits() {
-    if (lds_attr_done) return;
-    lds_attr_done = true;
-    const void *ks[] = {(const void *)attn_bwd_kernel<32, false>,
-                        (const void *)attn_bwd_kernel<32, true>,
-                        (const void *)attn_bwd_kernel<64, false>,
-                        (const void *)attn_bwd_kernel<64, true>,
-                        (const void *)attn_fwd_kernel<32, false>,
-                        (const void *)attn_fwd_kernel<32, true>,
-                        (const void *)attn_fwd_kernel<64, false>,
-                        (const void *)attn_fwd_kernel<64, true>};
-    // a refusal here leaves the default limit, which the launch then reports
-    for (const void *k : ks)
-        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
-            hipSuccess)
-            (void)hipGetLastError();
+// tq or tk above 64: the composed path (batched GEMMs + row kernels).
+bool large_desc(const rnn_attn_desc *d) { return d->tq > MAXT || d->tk > MAXT; }
+
+int check_desc(rnn_ctx *ctx, const rnn_attn_desc *d) {
+    if (!d) return rnn_fail(ctx, RNN_E_NULL, "attn: desc is null");
+    if (!d->relidx) return rnn_fail(ctx, RNN_E_NULL, "attn: relidx is null");
+    if (!d->h || !d->dh || !d->tq || !d->tk || !d->nrel)
+        return rnn_fail(ctx, RNN_E_INVALID, "attn: zero dimension");
+    if (d->dh > MAXDH && !large_desc(d))
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED,
+                        "attn: dh=%u beyond the workgroup kernels (64) at tq=%u tk=%u", d->dh,
+                        d->tq, d->tk);
+    if ((size_t)d->tq * d->tk > ((size_t)1 << 26) || d->tk > (1u << 20))
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: tq=%u tk=%u too large", d->tq, d->tk);
+    return RNN_OK;
 }
 
+// u32 offset of the lane-order table in a table's device block (16-byte
+// aligned): after relidx, rowptr and pos; then the drel index blob (rowptr
+// u32, positions u16) that the backward copies into LDS.
+size_t lane_table_off(size_t cnt, size_t nrel) { return rnn_round_up(cnt + (nrel + 1) + cnt, 4); }
+size_t blob_off(size_t cnt, size_t nrel) { return lane_table_off(cnt, nrel) + LT; }
+size_t blob_bytes(size_t cnt, size_t nrel) { return rnn_round_up(4 * (nrel + 1) + 2 * cnt, 16); }
+
+// The device copy of the relidx table of `d`: found by content among the
+// tables this context has uploaded (the last one used first), else checked
+// (every slot below nrel), completed on the host with its inverse index --
+// for every bias slot the positions that map to it, ascending, as offsets
+// into the backward's dS^T tile (key * TS + q) or, on the composed path, into
+// the [tq][tk] score matrix -- and, for the workgroup kernels, the table in
+// lane order, then uploaded once.  The copy runs on the context's stream from
+// a pinned buffer kept with the table, so no call waits for the device and
+// every table a step uses stays resident (a graph can replay them).
+int rel_table(rnn_ctx *ctx, const rnn_attn_desc *d, const RnnRelTable **out) {
+    const size_t cnt = (size_t)d->tq * d->tk;
+    auto same = [&](const RnnRelTable &t) {
+        return t.tq == d->tq && t.tk == d->tk && t.nrel == d->nrel &&
+               std::memcmp(t.host.data(), d->relidx, cnt * 4) == 0;
+    };
+    auto &tabs = ctx->rel_tables;
+    if (ctx->rel_last < tabs.size() && same(tabs[ctx->rel_last])) {
+        *out = &tabs[ctx->rel_last];
+        return RNN_OK;
+    }
+    for (size_t i = 0; i < tabs.size(); i++)
+        if (same(tabs[i])) {
+            ctx->rel_last = i;
+            *out = &tabs[i];
+            return RNN_OK;
+        }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    RNN_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+        return rnn_fail(ctx, RNN_E_INVALID,
+                        "attn: a new relidx table during graph capture (call once before "
+                        "capturing)");
+    for (size_t i = 0; i < cnt; i++)
+        if (d->relidx[i] >= d->nrel) return rnn_fail(ctx, RNN_E_INVALID, "attn: relidx >= nrel");
+    const bool large = large_desc(d);
+    const size_t lane_off = lane_table_off(cnt, d->nrel);
+    const size_t need = large ? cnt + (d->nrel + 1) + cnt
+                              : blob_off(cnt, d->nrel) + blob_bytes(cnt, d->nrel) / 4;
+    RnnRelTable t;
+    t.tq = d->tq;
+    t.tk = d->tk;
+    t.nrel = d->nrel;
+    t.host.assign(d->relidx, d->relidx + cnt);
+    RNN_HIP(ctx, hipHostMalloc((void **)&t.pinned, need * 4, hipHostMallocDefault));
+    hipError_t e = hipMalloc((void **)&t.dev, need * 4);
+    if (e != hipSuccess) {
+        (void)hipHostFree(t.pinned);
+        return rnn_fail(ctx, RNN_E_NOMEM, "attn: relidx table hipMalloc: %s", hipGetErrorString(e));
+    }
+    uint32_t *h = t.pinned;
+    std::memset(h, 0, need * 4);
+    std::memcpy(h, d->relidx, cnt * 4);
+    uint32_t *rowptr = h + cnt, *pos = rowptr + d->nrel + 1;
+    std::vector<uint32_t> count(d->nrel + 1, 0);
+    for (size_t i = 0; i < cnt; i++) count[d->relidx[i] + 1]++;
+    for (uint32_t r = 0; r < d->nrel; r++) count[r + 1] += count[r];
+    for (uint32_t r = 0; r <= d->nrel; r++) rowptr[r] = count[r];
+    for (size_t i = 0; i < cnt; i++) {
+        const uint32_t q = (uint32_t)(i / d->tk), k = (uint32_t)(i % d->tk);
+        pos[count[d->relidx[i]]++] = large ? (uint32_t)i : k * TS + q;
+    }
+    if (!large) {
+        // entry ((w*4 + t)*64 + lane)*4 + v: query 16w + lane%16, key
+        // 16t + 4(lane/16) + v, both clamped into the table (a valid slot)
+        uint32_t *lt = h + lane_off;
+        for (int w = 0; w < 4; w++)
+            for (int tt = 0; tt < 4; tt++)
+                for (int l = 0; l < 64; l++)
+                    for (int v = 0; v < 4; v++) {
+                        const int q = std::min(16 * w + (l & 15), (int)d->tq - 1);
+                        const int k = std::min(16 * tt + 4 * (l >> 4) + v, (int)d->tk - 1);
+                        lt[((w * 4 + tt) * 64 + l) * 4 + v] = d->relidx[(size_t)q * d->tk + k];
+                    }
+        // the blob: rowptr, then the positions as u16 (below 64 * TS)
+        uint32_t *bl = h + blob_off(cnt, d->nrel);
+        std::memcpy(bl, rowptr, (d->nrel + 1) * 4);
+        uint16_t *p16 = reinterpret_cast<uint16_t *>(bl + d->nrel + 1);
+        for (size_t i = 0; i < cnt; i++) p16[i] = (uint16_t)pos[i];
+    }
+    e = hipMemcpyAsync(t.dev, h, need * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(t.dev);
+        (void)hipHostFree(t.pinned);
+        return rnn_fail(ctx, RNN_E_HIP, "attn: relidx upload: %s", hipGetErrorString(e));
+    }
+    tabs.push_back(std::move(t));
+    ctx->rel_last = tabs.size() - 1;
+    *out = &tabs.back();
+    return RNN_OK;
+}
+
+void fill_args(AttnArgs &g, const RnnRelTable &tab, const rnn_attn_desc *d, size_t n) {
+    std::memset(&g, 0, sizeof(g));
+    g.qstride = (long long)d->qstride;
+    g.qoff = (long long)d->qoff;
+    g.kvstride = (long long)d->kvstride;
+    g.koff = (long long)d->koff;
+    g.voff = (long long)d->voff;
+    g.n = (int)n;
+    g.h = d->h;
+    g.dh = d->dh;
+    g.tq = d->tq;
+    g.tk = d->tk;
+    g.nrel = d->nrel;
+    g.mask = d->mask_diag ? 1 : 0;
+    const size_t cnt = (size_t)d->tq * d->tk;
+    g.rowptr = tab.dev + cnt;
+    g.pos = tab.dev + cnt + d->nrel + 1;
+    g.lidx = reinterpret_cast<const uint4 *>(tab.dev + lane_table_off(cnt, d->nrel));
+    g.blob = reinterpret_cast<const u32x4 *>(tab.dev + blob_off(cnt, d->nrel));
+}
+
+int dhp_of(uint32_t dh) { return dh <= 16 ? 16 : dh <= 32 ? 32 : 64; }
+
+inline bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// float4 accesses need dh == DHP (no column padding) and 16-byte aligned row
+// starts for every image and head.
+int use_vec(const AttnArgs &g) {
+    return g.dh == dhp_of(g.dh) && g.qstride % 4 == 0 && g.qoff % 4 == 0 && al16(g.q) &&
+           g.kvstride % 4 == 0 && g.koff % 4 == 0 && g.voff % 4 == 0 && al16(g.kv) &&
+           (g.dout == nullptr || al16(g.dout));
+}
+
+size_t fwd_lds(int dhp, size_t nrel) { return ((size_t)64 * (dhp + 4) + dhp * TS + nrel) * 4; }
+size_t bwd_lds(int dhp) {
+    return ((size_t)64 * (dhp + 4) + 3 * dhp * TS + 2 * 64 * TS) * 4 + 4 * sizeof(double);
+}
+
+template <int DHP, bool VEC>
+const void *fwd_kernel_nt(int nt) {
+    switch (nt) {
+        case 1: return (const void *)attn_fwd_kernel<DHP, 1, VEC>;
+        case 2: return (const void *)attn_fwd_kernel<DHP, 2, VEC>;
+        case 3: return (const void *)attn_fwd_kernel<DHP, 3, VEC>;
+        default: return (const void *)attn_fwd_kernel<DHP, 4, VEC>;
+    }
+}
+template <int DHP, bool VEC, bool ACC>
+const void *bwd_kernel_nt(int nt) {
+    switch (nt) {
+        case 1: return (const void *)attn_bwd_kernel<DHP, 1, VEC, ACC>;
+        case 2: return (const void *)attn_bwd_kernel<DHP, 2, VEC, ACC>;
+        case 3: return (const void *)attn_bwd_kernel<DHP, 3, VEC, ACC>;
+        default: return (const void *)attn_bwd_kernel<DHP, 4, VEC, ACC>;
+    }
+}
+template <bool VEC>
+const void *fwd_kernel_v(int dhp, int nt) {
+    return dhp == 16 ? fwd_kernel_nt<16, VEC>(nt) : dhp == 32 ? fwd_kernel_nt<32, VEC>(nt)
+                                                              : fwd_kernel_nt<64, VEC>(nt);
+}
+template <bool VEC, bool ACC>
+const void *bwd_kernel_v(int dhp, int nt) {
+    return dhp == 16   ? bwd_kernel_nt<16, VEC, ACC>(nt)
+           : dhp == 32 ? bwd_kernel_nt<32, VEC, ACC>(nt)
+                       : bwd_kernel_nt<64, VEC, ACC>(nt);
+}
+// VEC: float4 accesses (dh == DHP, every row start 16-byte aligned, tk % 4
+// == 0 and P 16-byte aligned); else scalar accesses throughout.
+const void *fwd_kernel(int dhp, int nt, bool vec) {
+    return vec ? fwd_kernel_v<true>(dhp, nt) : fwd_kernel_v<false>(dhp, nt);
+}
+const void *bwd_kernel(int dhp, int nt, bool vec, bool acc) {
+    return vec ? (acc ? bwd_kernel_v<true, true>(dhp, nt) : bwd_kernel_v<true, false>(dhp, nt))
+               : (acc ? bwd_kernel_v<false, true>(dhp, nt) : bwd_kernel_v<false, false>(dhp, nt));
+}
+
+// Above 64 KiB of dynamic LDS a kernel needs the attribute raised, once.
+std::once_flag lds_attr_once;
+void set_lds_limits() {
+    std::call_once(lds_attr_once, [] {
+        for (int dhp : {16, 32, 64})
+            for (int nt = 1; nt <= 4; nt++)
+                for (const void *k :
+                     {fwd_kernel(dhp, nt, false), fwd_kernel(dhp, nt, true),
+                      bwd_kernel(dhp, nt, false, false), bwd_kernel(dhp, nt, false, true),
+                      bwd_kernel(dhp, nt, true, false), bwd_kernel(dhp, nt, true, true)})
+                    // a refusal leaves the default limit, which the launch reports
+                    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            160 * 1024) != hipSuccess)
+                        (void)hipGetLastError();
+    });
+}
+
+
 // Core::forward on the composed path (see attn_softmax_rows_kernel).
-int attn_forward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
-                       const float *kv, const float *tau, const float *rel, float *p, float *o) {
+int attn_forward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_desc *d, size_t n,
+                       const float *q, const float *kv, const float *tau, const float *rel,
+                       float *p, float *o) {
     const size_t tq = d->tq, tk = d->tk, dh = d->dh, h = d->h, c = h * dh;
     for (size_t hd = 0; hd < h; hd++) {
         int rc = rnn_gemm_launch_ld(ctx, n, tq, tk, dh, q + d->qoff + hd * dh, d->qstride,
@@ -812,7 +1035,7 @@ int attn_forward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const flo
     }
     const long long rows = (long long)n * h * tq;
     attn_softmax_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
-        p, tau, rel, ctx->rel_dev, rows, (int)h, (int)tq, (int)tk, (int)d->nrel,
+        p, tau, rel, tab.dev, rows, (int)h, (int)tq, (int)tk, (int)d->nrel,
         d->mask_diag ? 1 : 0);
     RNN_LAUNCHED(ctx);
     for (size_t hd = 0; hd < h; hd++) {
@@ -826,10 +1049,12 @@ int attn_forward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const flo
 
 // Core::backward on the composed path: dV = P^T dO, dP = dO V^T, the raw S
 // recomputed, the row kernel (dS, tau dS, dtau shares), dtau and drel, then
-// dQ = (tau dS) K and dK = (tau dS)^T Q; dq, dkv, dtau, drel accumulate.
-int attn_backward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
-                        const float *kv, const float *tau, const float *p, const float *dout,
-                        float *dq, float *dkv, float *dtau, float *drel) {
+// dQ = (tau dS) K and dK = (tau dS)^T Q; dtau and drel accumulate, dq and
+// dkv too unless flags overwrite them.
+int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_desc *d, size_t n,
+                        const float *q, const float *kv, const float *tau, const float *p, const float *dout,
+                        float *dq, float *dkv, float *dtau, float *drel, uint32_t flags) {
+    const int acc_q = (flags & RNN_ATTN_SET_DQ) ? 0 : 1, acc_kv = (flags & RNN_ATTN_SET_DKV) ? 0 : 1;
     const size_t tq = d->tq, tk = d->tk, dh = d->dh, h = d->h, c = h * dh;
     const size_t cnt = tq * tk, mat = n * h * cnt;
     const long long rows = (long long)n * h * tq;
@@ -847,7 +1072,7 @@ int attn_backward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const fl
         // dV += P^T dO (attn.rs:262-270)
         int rc = rnn_gemm_launch_ld(ctx, n, tk, dh, tq, p + hd * cnt, tk, h * cnt, 1,
                                     dout + hd * dh, c, tq * c, 0, dkv + d->voff + hd * dh,
-                                    d->kvstride, tk * d->kvstride, 1);
+                                    d->kvstride, tk * d->kvstride, acc_kv);
         if (rc) return rc;
         // dP = dO V^T (attn.rs:272-278)
         rc = rnn_gemm_launch_ld(ctx, n, tq, tk, dh, dout + hd * dh, c, tq * c, 0,
@@ -867,8 +1092,8 @@ int attn_backward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const fl
                                                               (int)tq, dtau);
     RNN_LAUNCHED(ctx);
     attn_drel_part_kernel<<<dim3((unsigned)rnn_div_up(per, (size_t)256), (unsigned)nchunk), 256,
-                            0, ctx->stream>>>(s1, ctx->rel_dev + cnt,
-                                              ctx->rel_dev + cnt + d->nrel + 1, (long long)n,
+                            0, ctx->stream>>>(s1, tab.dev + cnt,
+                                              tab.dev + cnt + d->nrel + 1, (long long)n,
                                               (long long)ipc, (int)h, (int)d->nrel,
                                               (long long)cnt, rpart);
     RNN_LAUNCHED(ctx);
@@ -879,16 +1104,17 @@ int attn_backward_large(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const fl
         // dQ += (tau dS) K (attn.rs:317-322)
         int rc = rnn_gemm_launch_ld(ctx, n, tq, dh, tk, s2 + hd * cnt, tk, h * cnt, 0,
                                     kv + d->koff + hd * dh, d->kvstride, tk * d->kvstride, 0,
-                                    dq + d->qoff + hd * dh, d->qstride, tq * d->qstride, 1);
+                                    dq + d->qoff + hd * dh, d->qstride, tq * d->qstride, acc_q);
         if (rc) return rc;
         // dK += (tau dS)^T Q (attn.rs:324-330)
         rc = rnn_gemm_launch_ld(ctx, n, tk, dh, tq, s2 + hd * cnt, tk, h * cnt, 1,
                                 q + d->qoff + hd * dh, d->qstride, tq * d->qstride, 0,
-                                dkv + d->koff + hd * dh, d->kvstride, tk * d->kvstride, 1);
+                                dkv + d->koff + hd * dh, d->kvstride, tk * d->kvstride, acc_kv);
         if (rc) return rc;
     }
     return RNN_OK;
 }
+
 
 }  // namespace
 
@@ -904,50 +1130,76 @@ int rnn_attn_forward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float
     if (!q || !kv || !tau || !rel || !p || !o)
         return rnn_fail(ctx, RNN_E_NULL, "attn_forward: null operand");
     if (n * d->h > 0x7fffffffu) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: too many problems");
-    rc = upload_rel(ctx, d);
+    const RnnRelTable *tab = nullptr;
+    rc = rel_table(ctx, d, &tab);
     if (rc) return rc;
-    if (large_desc(d)) return attn_forward_large(ctx, d, n, q, kv, tau, rel, p, o);
+    if (large_desc(d)) return attn_forward_large(ctx, *tab, d, n, q, kv, tau, rel, p, o);
     set_lds_limits();
     AttnArgs g;
-    fill_args(g, ctx, d, n);
+    fill_args(g, *tab, d, n);
     g.q = q;
     g.kv = kv;
     g.tau = tau;
     g.rel = rel;
     g.pout = p;
     g.o = o;
-    const dim3 grid((unsigned)(n * d->h));
-    const size_t lds = fwd_lds(d->nrel);
+    const bool vec = use_vec(g) && d->tk % 4 == 0 && al16(p);
+    const int dhp = dhp_of(d->dh), nt = (int)(d->tk + 15) / 16;
+    const size_t lds = fwd_lds(dhp, d->nrel);
     if (lds > 160 * 1024)
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: nrel %u bias slots exceed LDS", d->nrel);
-    const bool vec = use_vec(g);
-    auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(128), lds, ctx->stream, g); };
-    if (g.DHP == 32)
-        vec ? go(attn_fwd_kernel<32, true>) : go(attn_fwd_kernel<32, false>);
-    else
-        vec ? go(attn_fwd_kernel<64, true>) : go(attn_fwd_kernel<64, false>);
-    RNN_LAUNCHED(ctx);
+    void *args[] = {&g};
+    RNN_HIP(ctx, hipLaunchKernel(fwd_kernel(dhp, nt, vec), dim3((unsigned)(n * d->h)), dim3(256),
+                                 args, lds, ctx->stream));
     return RNN_OK;
 }
 
 int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
                       const float *kv, const float *tau, const float *p, const float *dout,
                       float *dq, float *dkv, float *dtau, float *drel) {
+    return rnn_attn_backward_ex(ctx, d, n, q, kv, tau, p, dout, dq, dkv, dtau, drel, 0);
+}
+
+int rnn_attn_backward_ex(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
+                         const float *kv, const float *tau, const float *p, const float *dout,
+                         float *dq, float *dkv, float *dtau, float *drel, uint32_t flags) {
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     int rc = check_desc(ctx, d);
     if (rc) return rc;
+    if (flags & ~(uint32_t)(RNN_ATTN_SET_DQ | RNN_ATTN_SET_DKV))
+        return rnn_fail(ctx, RNN_E_INVALID, "attn_backward: unknown flags 0x%x", flags);
     if (n == 0) return RNN_OK;
     if (!q || !kv || !tau || !p || !dout || !dq || !dkv || !dtau || !drel)
         return rnn_fail(ctx, RNN_E_NULL, "attn_backward: null operand");
     if (n * d->h > 0x7fffffffu) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "attn: too many problems");
-    rc = upload_rel(ctx, d);
+    const RnnRelTable *tab = nullptr;
+    rc = rel_table(ctx, d, &tab);
     if (rc) return rc;
     if (large_desc(d))
-        return attn_backward_large(ctx, d, n, q, kv, tau, p, dout, dq, dkv, dtau, drel);
+        return attn_backward_large(ctx, *tab, d, n, q, kv, tau, p, dout, dq, dkv, dtau, drel,
+                                   flags);
     set_lds_limits();
+    // The workgroup kernels overwrite both or accumulate into both; with one
+    // flag only, the overwritten operand's columns are cleared first.
+    const bool set_q = flags & RNN_ATTN_SET_DQ, set_kv = flags & RNN_ATTN_SET_DKV;
+    const bool acc = !(set_q && set_kv);
+    if (acc && set_q) {
+        hipLaunchKernelGGL(attn_zero_cols_kernel, dim3((unsigned)rnn_div_up(n * d->tq, (size_t)4)),
+                           dim3(256), 0, ctx->stream, dq, (long long)(n * d->tq),
+                           (long long)d->qstride, (long long)d->qoff, (int)(d->h * d->dh));
+        RNN_LAUNCHED(ctx);
+    }
+    if (acc && set_kv)
+        for (size_t off : {(size_t)d->koff, (size_t)d->voff}) {
+            hipLaunchKernelGGL(attn_zero_cols_kernel,
+                               dim3((unsigned)rnn_div_up(n * d->tk, (size_t)4)), dim3(256), 0,
+                               ctx->stream, dkv, (long long)(n * d->tk), (long long)d->kvstride,
+                               (long long)off, (int)(d->h * d->dh));
+            RNN_LAUNCHED(ctx);
+        }
     AttnArgs g;
-    fill_args(g, ctx, d, n);
+    fill_args(g, *tab, d, n);
     const size_t tau_bytes = rnn_round_up(n * d->h * sizeof(double), 256);
     char *ws = (char *)rnn_workspace(ctx, tau_bytes + n * d->h * (size_t)d->nrel * sizeof(float));
     if (!ws) return RNN_E_NOMEM;
@@ -960,16 +1212,17 @@ int rnn_attn_backward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const floa
     g.dkv = dkv;
     g.dtau_part = (double *)ws;
     g.drel_part = (float *)(ws + tau_bytes);
-    const dim3 grid((unsigned)(n * d->h));
-    const bool vec = use_vec(g);
-    auto go = [&](auto kern) {
-        hipLaunchKernelGGL(kern, grid, dim3(128), bwd_lds(), ctx->stream, g);
-    };
-    if (g.DHP == 32)
-        vec ? go(attn_bwd_kernel<32, true>) : go(attn_bwd_kernel<32, false>);
-    else
-        vec ? go(attn_bwd_kernel<64, true>) : go(attn_bwd_kernel<64, false>);
-    RNN_LAUNCHED(ctx);
+    const bool vec = use_vec(g) && d->tk % 4 == 0 && al16(p);
+    const int dhp = dhp_of(d->dh), nt = (int)(d->tk + 15) / 16;
+    const int nth = 256;  // four waves: the staging splits every tile over 256 threads
+    // the drel index blob rides in registers into the LDS of V and K^T when
+    // it fits both
+    const size_t bb = blob_bytes((size_t)d->tq * d->tk, d->nrel);
+    const size_t region = ((size_t)64 * (dhp + 4) + (size_t)dhp * TS) * 4;
+    g.blob_chunks = (bb <= region && bb / 16 <= (size_t)BLOB_CHUNKS * nth) ? (int)(bb / 16) : 0;
+    void *args[] = {&g};
+    RNN_HIP(ctx, hipLaunchKernel(bwd_kernel(dhp, nt, vec, acc), dim3((unsigned)(n * d->h)),
+                                 dim3(nth), args, bwd_lds(dhp), ctx->stream));
     int tot = (int)(d->h * d->nrel + d->h);
     hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rnn_div_up(tot, 32)), dim3(256), 0,
                        ctx->stream, (const double *)g.dtau_part, (const float *)g.drel_part, (int)n,

@@ -153,8 +153,10 @@ int rnn_ctx_destroy(rnn_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
-    if (ctx->rel_dev) (void)hipFree(ctx->rel_dev);
-    if (ctx->rel_pinned) (void)hipHostFree(ctx->rel_pinned);
+    for (auto &t : ctx->rel_tables) {
+        if (t.dev) (void)hipFree(t.dev);
+        if (t.pinned) (void)hipHostFree(t.pinned);
+    }
     for (auto &kv : ctx->tables) rnn_dev_table_free(kv.second);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;

@@ -22,6 +22,16 @@ struct RnnDevTable {
     size_t cap = 0;
 };
 
+// One attention relidx table on the device: relidx [tq*tk], the inverse
+// index (rowptr [nrel+1], positions [tq*tk]) and, for the workgroup kernels,
+// the table in lane order; the host copy identifies it.
+struct RnnRelTable {
+    std::vector<uint32_t> host;
+    uint32_t tq = 0, tk = 0, nrel = 0;
+    uint32_t *dev = nullptr;
+    uint32_t *pinned = nullptr;  // the upload's staging, kept with the table
+};
+
 struct rnn_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -36,15 +46,10 @@ struct rnn_ctx {
     // synchronised first so no in-flight kernel still reads the old block.
     void *ws = nullptr;
     size_t ws_bytes = 0;
-    // Attention relative-index tables (forward index + inverse CSR), uploaded
-    // once per distinct table.
-    std::vector<uint32_t> rel_host;  // last uploaded relidx (host copy)
-    uint32_t *rel_dev = nullptr;     // [tq*tk] relidx, then CSR rowptr[nrel+1], then pos[tq*tk]
-    size_t rel_cap = 0;              // u32 capacity of rel_dev
-    uint32_t *rel_pinned = nullptr;  // staging for the async upload
-    size_t rel_pinned_cap = 0;
-    uint32_t rel_nrel = 0;
-    uint32_t rel_tk = 0;
+    // Attention relative-index tables, each uploaded once and kept until the
+    // context ends (a step that switches between geometries never waits).
+    std::vector<RnnRelTable> rel_tables;
+    size_t rel_last = 0;  // the table the last attention call used
     // Tensor-list tables of the optimizer entry points (slot -> table).
     std::map<int, RnnDevTable> tables;
     std::recursive_mutex mu;

@@ -99,10 +99,11 @@ class SelfAttn:
         import torch
         n, t, c = self.n, self.t, self.c
         do = self.proj.backward(dy.reshape(-1))
-        # dq and dk/dv land in one fused-QKV gradient (attn.rs:418-438)
-        dab = torch.zeros(n * t * 3 * c, device=dy.device)
+        # dq and dk/dv land in one fused-QKV gradient (attn.rs:418-438: zeroed
+        # buffers, accumulated into; here written directly)
+        dab = torch.empty(n * t * 3 * c, device=dy.device)
         self.core.backward(n, self.ab, 3 * c, 0, self.ab, 3 * c, c, 2 * c, self.tau.v, self.p,
-                           do, dab, dab, self.tau.g, self.rel.g)
+                           do, dab, dab, self.tau.g, self.rel.g, set_dq=True, set_dkv=True)
         return self.qkv.backward(dab).view(n, t, c)
 
     def for_each_param(self, f):
@@ -147,9 +148,9 @@ class CrossAttn:
         import torch
         n, t, c = self.n, self.tq, self.c
         do = self.proj.backward(dy.reshape(-1))
-        dq = torch.zeros(n * t * c, device=dy.device)
+        dq = torch.empty(n * t * c, device=dy.device)
         self.core.backward(n, self.q, c, 0, mem, 2 * c, 0, c, self.tau.v, self.p, do, dq, dmem,
-                           self.tau.g, self.rel.g)
+                           self.tau.g, self.rel.g, set_dq=True)
         return self.wq.backward(dq).view(n, t, c)
 
     def for_each_param(self, f):

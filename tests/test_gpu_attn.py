@@ -92,6 +92,68 @@ def test_attn_parity(rnn, orc, name, n, h, dh, th, tw, mh, mw, variant):
     assert rel_frob(to_host(drel) - drel0, drel_w - drel0) < TOL, "drel"
 
 
+def _cols(size, stride, offs, width):
+    """Mask of the columns [off, off + width) of every row, for each off."""
+    m = np.zeros((size // stride, stride), bool)
+    for off in offs:
+        m[:, off:off + width] = True
+    return m.ravel()
+
+
+SET_CASES = [c for c in CASES if c[0] in ("cfg2_lsa", "gc_cross", "dh64_t16", "cross_tk256",
+                                          "self_t100")]
+
+
+@pytest.mark.parametrize("flags", [1, 2, 3])
+@pytest.mark.parametrize("name,n,h,dh,th,tw,mh,mw,variant", SET_CASES,
+                         ids=[c[0] for c in SET_CASES])
+def test_attn_backward_set(rnn, orc, flags, name, n, h, dh, th, tw, mh, mw, variant):
+    """rnn_attn_backward_ex: an operand flagged for overwriting receives what
+    accumulating into a zeroed buffer gives (bit for bit), and its old
+    contents (NaN here) are never read; an unflagged one accumulates."""
+    cs = make_case(orc, n, h, dh, th, tw, mh, mw, variant, seed=11)
+    g = cs["geo"]
+    d = orc.attn_desc(h, dh, cs["tq"], cs["tk"], g["qstride"], g["qoff"], g["kvstride"],
+                      g["koff"], g["voff"], cs["relidx"], cs["nrel"], cs["mask"])
+    with orc.threads(8):
+        p_w, _ = orc.attn_forward(d, n, cs["q"], cs["kv"], cs["tau"], cs["rel"])
+    core = rnn.Core(h, dh, cs["tq"], cs["tk"], cs["relidx"], cs["nrel"], cs["mask"])
+    Q = to_dev(cs["q"])
+    KV = Q if cs["selfattn"] else to_dev(cs["kv"])
+    TAU, P, DO = to_dev(cs["tau"]), to_dev(p_w), to_dev(cs["dout"])
+    nq, nkv = cs["q"].size, cs["kv"].size
+    r = np.random.default_rng(5)
+    set_q, set_kv = bool(flags & 1), bool(flags & 2)
+    dq0 = np.zeros(nq, np.float32) if set_q else r.standard_normal(nq).astype(np.float32)
+    dkv0 = np.zeros(nkv, np.float32) if set_kv else r.standard_normal(nkv).astype(np.float32)
+    dtau0 = r.standard_normal(h).astype(np.float32)
+    drel0 = r.standard_normal(h * cs["nrel"]).astype(np.float32)
+    # the accumulating call into zeroed buffers, then the flagged call into NaN
+    want = [to_dev(a.copy()) for a in (dq0, dkv0, dtau0, drel0)]
+    core.backward(n, Q, g["qstride"], g["qoff"], KV, g["kvstride"], g["koff"], g["voff"], TAU, P,
+                  DO, *want)
+    nan = np.float32(np.nan)
+    got = [to_dev(np.full(nq, nan) if set_q else dq0.copy()),
+           to_dev(np.full(nkv, nan) if set_kv else dkv0.copy()),
+           to_dev(dtau0.copy()), to_dev(drel0.copy())]
+    core.backward(n, Q, g["qstride"], g["qoff"], KV, g["kvstride"], g["koff"], g["voff"], TAU, P,
+                  DO, *got, set_dq=set_q, set_dkv=set_kv)
+    width = h * dh
+    mq = _cols(nq, g["qstride"], [g["qoff"]], width)
+    mkv = _cols(nkv, g["kvstride"], [g["koff"], g["voff"]], width)
+    for nm, a, b, m in (("dq", got[0], want[0], mq), ("dkv", got[1], want[1], mkv),
+                        ("dtau", got[2], want[2], None), ("drel", got[3], want[3], None)):
+        a, b = to_host(a), to_host(b)
+        if m is not None:
+            a, b = a[m], b[m]
+        assert np.isfinite(a).all() and np.array_equal(a, b), nm
+    with orc.threads(8):
+        dq_w, dkv_w, _, _ = orc.attn_backward(d, n, cs["q"], cs["kv"], cs["tau"], p_w, cs["dout"],
+                                              dq0, dkv0, dtau0, drel0)
+    assert rel_frob(to_host(got[0])[mq] - dq0[mq], dq_w[mq] - dq0[mq]) < TOL
+    assert rel_frob(to_host(got[1])[mkv] - dkv0[mkv], dkv_w[mkv] - dkv0[mkv]) < TOL
+
+
 @pytest.mark.parametrize("n,h,dh,t", [(32, 4, 32, 8), (4, 2, 48, 10)])
 def test_attn_aliased_dq_dkv(rnn, orc, n, h, dh, t):
     """SelfAttn accumulates dq and dk/dv into one fused-QKV gradient buffer
