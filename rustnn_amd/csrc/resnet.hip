@@ -80,6 +80,9 @@ struct NetConv {
     int nz = 0;
     // weights packed for the forward / dX kernels (per plan); null: unpacked
     float *wp_f = nullptr, *wp_x = nullptr;
+    // this conv's output gradient in the backward (per plan): its own buffer,
+    // so the dW reading it on the side stream overlaps the work after it
+    float *dyb = nullptr;
     rnn_conv_spec spec(uint32_t h, uint32_t w_) const {
         rnn_conv_spec sp;
         rnn_conv_spec_init(&sp, cin, cout, k, stride, pad, h, w_);
@@ -143,6 +146,12 @@ struct rnn_resnet {
     hipGraph_t graph = nullptr;
     hipGraphExec_t gexec = nullptr;
     hipStream_t rec_stream = nullptr;  // default priority, used only to record
+    // Weight gradients run on a second stream (default priority) beside the
+    // dX chain: one event per fork (dy ready) and one for the join.
+    hipStream_t side = nullptr;
+    std::vector<hipEvent_t> events;
+    bool overlap = true;
+    bool capturing = false;  // recording the step graph: no side stream there
     int step_calls = 0;
     bool use_graph = true;
     char graph_err[160] = {0};
@@ -227,6 +236,12 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     f32.push_back({&r->t3, maxact});
     f32.push_back({&r->scal, 4});
     f32.push_back({&r->loss, 1});
+    for (auto &b : r->blocks) {
+        const size_t a = n * b.c1.cout * b.hout * b.wout;
+        f32.push_back({&b.c1.dyb, a});
+        f32.push_back({&b.c2.dyb, a});
+        if (b.down) f32.push_back({&b.cd.dyb, a});
+    }
     std::vector<size_t> offs;
     for (auto &e : f32) offs.push_back(cv.take(e.second * sizeof(float)));
     const size_t o_part = cv.take(maxpart * sizeof(double));
@@ -508,9 +523,49 @@ int resid(rnn_resnet *r, size_t i, size_t c, size_t hw, float *a, const float *a
 // The conv weight gradients are left as slabs; the finalisation adds them
 // into pg (Param::g) -- and with `sgd` also takes the Nesterov step -- in one
 // pass over all parameters.
+// dW of conv c on the side stream once dy (written just before on the main
+// stream) is ready; dy stays untouched until the join.
+bool use_side(const rnn_resnet *r) { return r->overlap && !r->capturing; }
+
+int conv_dw_side(rnn_resnet *r, const NetConv &c, const rnn_conv_spec &sp, const float *dy,
+                 const float *x, size_t &ev) {
+    rnn_ctx *ctx = r->ctx;
+    if (!use_side(r)) return conv_dw(r, c, sp, dy, x);
+    if (!r->side) RNN_HIP(ctx, hipStreamCreateWithFlags(&r->side, hipStreamNonBlocking));
+    if (ev == r->events.size()) {
+        hipEvent_t e;
+        RNN_HIP(ctx, hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        r->events.push_back(e);
+    }
+    hipEvent_t e = r->events[ev++];
+    RNN_HIP(ctx, hipEventRecord(e, ctx->stream));
+    RNN_HIP(ctx, hipStreamWaitEvent(r->side, e, 0));
+    hipStream_t main = ctx->stream;
+    ctx->stream = r->side;
+    const int rc = conv_dw(r, c, sp, dy, x);
+    ctx->stream = main;
+    return rc;
+}
+
+// The main stream waits for every dW issued on the side stream.
+int join_side(rnn_resnet *r, size_t &ev) {
+    rnn_ctx *ctx = r->ctx;
+    if (!use_side(r) || ev == 0) return RNN_OK;
+    if (ev == r->events.size()) {
+        hipEvent_t e;
+        RNN_HIP(ctx, hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        r->events.push_back(e);
+    }
+    hipEvent_t e = r->events[ev++];
+    RNN_HIP(ctx, hipEventRecord(e, r->side));
+    RNN_HIP(ctx, hipStreamWaitEvent(ctx->stream, e, 0));
+    return RNN_OK;
+}
+
 int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
     rnn_ctx *ctx = r->ctx;
     const size_t n = r->n, nb = r->blocks.size();
+    size_t ev = 0;
     TRY(rnn_fc_backward_launch(ctx, n, r->fin, r->nclass, dlogits, r->pooled, pv_of(r, r->fc_w),
                                pg_of(r, r->fc_w), pg_of(r, r->fc_b), r->dpool));
     const float *feat = nb == 0 ? r->s0 : r->blocks.back().out;
@@ -520,23 +575,26 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
     for (size_t i = nb; i-- > 0;) {
         NetBlock &b = r->blocks[i];
         const size_t hw = (size_t)b.hout * b.wout;
+        float *dy2 = use_side(r) ? b.c2.dyb : r->t1;
         TRY(rnn_bn_backward_apply_launch(ctx, n, b.b2.c, hw, d, nullptr, b.y2,
-                                         bn_state(r, b.b2), b.b2.part, r->t1));
+                                         bn_state(r, b.b2), b.b2.part, dy2));
         rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
-        TRY(conv_dw(r, b.c2, s2, r->t1, b.h));
-        TRY(rnn_conv2d_backward_x_wp(ctx, &s2, n, r->t1, pv_of(r, b.c2.w), b.c2.wp_x, r->t2));
+        TRY(conv_dw_side(r, b.c2, s2, dy2, b.h, ev));
+        TRY(rnn_conv2d_backward_x_wp(ctx, &s2, n, dy2, pv_of(r, b.c2.w), b.c2.wp_x, r->t2));
+        float *dy1 = use_side(r) ? b.c1.dyb : r->t1;
         TRY(rnn_bn_backward_launch(ctx, n, b.b1.c, hw, r->t2, b.h, b.y1, bn_state(r, b.b1),
-                                   r->part, r->t1));
+                                   r->part, dy1));
         rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
-        TRY(conv_dw(r, b.c1, s1, r->t1, b.in));
-        TRY(rnn_conv2d_backward_x_wp(ctx, &s1, n, r->t1, pv_of(r, b.c1.w), b.c1.wp_x, other));
+        TRY(conv_dw_side(r, b.c1, s1, dy1, b.in, ev));
+        TRY(rnn_conv2d_backward_x_wp(ctx, &s1, n, dy1, pv_of(r, b.c1.w), b.c1.wp_x, other));
         const float *add = d;  // dx = c1 dX + d (add_, model.rs:72)
         if (b.down) {
+            float *dyd = use_side(r) ? b.cd.dyb : r->t2;
             TRY(rnn_bn_backward_apply_launch(ctx, n, b.bd.c, hw, d, nullptr, b.ys,
-                                             bn_state(r, b.bd), b.bd.part, r->t2));
+                                             bn_state(r, b.bd), b.bd.part, dyd));
             rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
-            TRY(conv_dw(r, b.cd, sd, r->t2, b.in));
-            TRY(rnn_conv2d_backward_x_wp(ctx, &sd, n, r->t2, pv_of(r, b.cd.w), b.cd.wp_x, r->t3));
+            TRY(conv_dw_side(r, b.cd, sd, dyd, b.in, ev));
+            TRY(rnn_conv2d_backward_x_wp(ctx, &sd, n, dyd, pv_of(r, b.cd.w), b.cd.wp_x, r->t3));
             add = r->t3;  // dx = c1 dX + shortcut dX (add_, model.rs:70-71)
         }
         TRY(resid(r, i, b.c1.cin, (size_t)b.hin * b.win, other, add, b.in, nullptr));
@@ -548,6 +606,7 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
                                      r->y0, bn_state(r, r->stem_bn), r->stem_bn.part, r->t1));
     // The stem's dX would be the image gradient: discarded (model.rs:161).
     TRY(conv_dw(r, r->stem, sp, r->t1, r->x));
+    TRY(join_side(r, ev));
     TRY(rnn_grad_finalize_launch(ctx, r->segs, r->nseg, r->nseg_blocks, r->pv, r->pg, r->pm,
                                  r->scal, sgd ? 1 : 0));
     // the step changed the weights: their packed copies follow
@@ -587,7 +646,9 @@ int run_step(rnn_resnet *r) {
         int st = RNN_E_HIP;
         hipGraph_t g = nullptr;
         if (e == hipSuccess) {
+            r->capturing = true;
             st = step_body(r);
+            r->capturing = false;
             e = hipStreamEndCapture(ctx->stream, &g);
         }
         ctx->stream = caller;
@@ -634,8 +695,15 @@ int rnn_resnet_create(rnn_ctx *ctx, size_t depth_n, size_t width, size_t nclass,
     r->depth = (uint32_t)depth_n;
     r->width = (uint32_t)width;
     r->nclass = (uint32_t)nclass;
+    // Steps run eagerly with the weight gradients on a second stream
+    // (RNN_DW_OVERLAP=0: on the main stream) unless RNN_GRAPH=1 or
+    // rnn_resnet_set_graph asks for the recorded graph: in a graph the
+    // cross-stream edges cost more than the overlap gains, so a recorded step
+    // keeps every kernel on one stream.
+    const char *ov = getenv("RNN_DW_OVERLAP");
+    r->overlap = !(ov && ov[0] == '0');
     const char *g = getenv("RNN_GRAPH");
-    r->use_graph = !(g && g[0] == '0');
+    r->use_graph = g ? g[0] != '0' : !r->overlap;
     // ResNet::new (model.rs:113-135): blocks first (their convs draw from the
     // Rng in c1, c2, shortcut order), then the stem conv, then the classifier.
     const uint32_t widths[3] = {(uint32_t)width, (uint32_t)width * 2, (uint32_t)width * 4};
@@ -774,6 +842,11 @@ int rnn_resnet_destroy(rnn_resnet *r) {
     (void)hipStreamSynchronize(ctx->stream);
     drop_graph(r);
     if (r->rec_stream) (void)hipStreamDestroy(r->rec_stream);
+    if (r->side) {
+        (void)hipStreamSynchronize(r->side);
+        (void)hipStreamDestroy(r->side);
+    }
+    for (hipEvent_t e : r->events) (void)hipEventDestroy(e);
     if (r->arena) (void)hipFree(r->arena);
     if (r->pv) (void)hipFree(r->pv);
     delete r;

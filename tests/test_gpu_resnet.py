@@ -125,6 +125,7 @@ def test_fused_train_step_matches_layer_calls(rnn, orc):
     from rustnn_amd.nn import softmax_ce
     n = 32
     a, b = ResNet(3, 32, 100, 11), ResNet(3, 32, 100, 11)
+    a.set_graph(True)  # b's backward runs its weight gradients on the side stream
     loss = torch.zeros(1, device="cuda")
     corr = torch.zeros(1, dtype=torch.int32, device="cuda")
     for step in range(4):
@@ -155,6 +156,7 @@ def test_train_step_from_input_slots(rnn, orc):
     from rustnn_amd.model import ResNet
     n = 32
     a, b = ResNet(3, 32, 100, 5), ResNet(3, 32, 100, 5)
+    a.set_graph(True)
     xs, ls = a.inputs(n, 32, 32)
     assert tuple(xs.shape) == (n, 3, 32, 32) and tuple(ls.shape) == (n,)
     la, lb = torch.zeros(1, device="cuda"), torch.zeros(1, device="cuda")
@@ -175,12 +177,14 @@ def test_train_step_from_input_slots(rnn, orc):
 
 
 def test_graph_replays_match_eager(rnn, orc):
-    """Graph replays with eager work and synchronisation in between, each
-    checked against an eager network stepping on the same inputs."""
+    """Graph replays (one stream) with eager work and synchronisation in
+    between, each checked against an eager network stepping on the same
+    inputs (weight gradients on the side stream), bit for bit."""
     import torch
     from rustnn_amd.model import ResNet
     n = 64
     g, e = ResNet(3, 32, 100, 3), ResNet(3, 32, 100, 3)
+    g.set_graph(True)
     e.set_graph(False)
     for step in range(5):
         x, labels = _cfg3_inputs(orc, n, seed=80 + step)
