@@ -98,82 +98,85 @@ __global__ __launch_bounds__(NT) void ln_bwd_kernel(size_t rows, int c, const fl
     }
 }
 
-// Column partial sums over a block of rows: thread j (channel) adds
-// a[r][j] b[r][j] (when b is set) and a[r][j] over rows r of its block, in row
-// order, in f64.  part: [nblk][c] products, then [nblk][c] plain sums.
-__global__ __launch_bounds__(NT) void colsum_kernel(size_t rows, int c, size_t rpb,
-                                                    const float *__restrict__ a,
-                                                    const float *__restrict__ b, int want_a,
-                                                    double *__restrict__ part) {
-    const int j = blockIdx.x * NT + threadIdx.x;
-    if (j >= c) return;
-    const size_t r0 = (size_t)blockIdx.y * rpb, r1 = min(rows, r0 + rpb);
+// Column sums in two fixed-order stages.  Stage 1, block (x, y): columns
+// [64x, 64x + 64), rows [CS_ROWS y, CS_ROWS (y + 1)); wave g sums the rows
+// g, g + 4, ... of the block in order (8 loads ahead of their adds), and the
+// four wave sums are added in wave order.  part: [block row][nout * c], the
+// sums of a*b (b set) first, then those of a.
+constexpr int CS_ROWS = 64;
+constexpr int CS_RED_COLS = 16;  // columns per stage-2 block (16 groups each)
+
+__global__ __launch_bounds__(NT) void colsum_part_kernel(size_t rows, int c,
+                                                         const float *__restrict__ a,
+                                                         const float *__restrict__ b, int want_a,
+                                                         double *__restrict__ part) {
+    __shared__ double red[2][NT / 64][64];
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const int j = blockIdx.x * 64 + lane, jc = min(j, c - 1);
+    const size_t r0 = (size_t)blockIdx.y * CS_ROWS, r1 = min(rows, r0 + CS_ROWS);
     double sab = 0.0, sa = 0.0;
-    size_t r = r0;
-    for (; r + 8 <= r1; r += 8) {  // 8 rows' loads ahead of their (ordered) adds
+    for (size_t r = r0 + g; r < r1; r += 8 * (NT / 64)) {
         float av[8], bv[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            av[u] = a[(r + u) * c + j];
-            bv[u] = b ? b[(r + u) * c + j] : 0.0f;
+            const size_t rr = min(r + (size_t)(NT / 64) * u, r1 - 1);
+            av[u] = a[rr * c + jc];
+            bv[u] = b ? b[rr * c + jc] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
+            if (r + (size_t)(NT / 64) * u >= r1) break;
             if (b) sab += (double)(av[u] * bv[u]);
             sa += av[u];
         }
     }
-    for (; r < r1; r++) {
-        const float av = a[r * c + j];
-        if (b) sab += (double)(av * b[r * c + j]);
-        sa += av;
+    red[0][g][lane] = sab;
+    red[1][g][lane] = sa;
+    __syncthreads();
+    if (g != 0 || j >= c) return;
+    double tab = red[0][0][lane], ta = red[1][0][lane];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) {
+        tab += red[0][w][lane];
+        ta += red[1][w][lane];
     }
-    const size_t nblk = gridDim.y;
-    if (b) part[(size_t)blockIdx.y * c + j] = sab;
-    if (want_a) part[(b ? nblk * c : 0) + (size_t)blockIdx.y * c + j] = sa;
+    const size_t len = (size_t)((b ? 1 : 0) + (want_a ? 1 : 0)) * c;
+    double *row = part + (size_t)blockIdx.y * len;
+    if (b) row[j] = tab;
+    if (want_a) row[(b ? c : 0) + j] = ta;
 }
 
-// sum over k < nblk of part[k * len + j] in k order, 8 loads ahead of their adds.
-__device__ __forceinline__ double blocks_sum(const double *__restrict__ part, int nblk, size_t len,
-                                             size_t j) {
+// Stage 2: column j of part ([nblk][len]) summed over the block rows in
+// order -- 16 consecutive groups of rows, each summed in order, then the 16
+// group sums in order -- and added into out0[j] (j < split) or
+// out1[j - split].
+__global__ __launch_bounds__(NT) void colsum_red_kernel(int nblk, size_t len, size_t split,
+                                                        const double *__restrict__ part,
+                                                        float *__restrict__ out0,
+                                                        float *__restrict__ out1) {
+    constexpr int NG = NT / CS_RED_COLS;
+    __shared__ double red[NG][CS_RED_COLS];
+    const int jl = threadIdx.x % CS_RED_COLS, q = threadIdx.x / CS_RED_COLS;
+    const size_t j = (size_t)blockIdx.x * CS_RED_COLS + jl, jc = min(j, len - 1);
+    const int G = (nblk + NG - 1) / NG, k0 = min(nblk, q * G), k1 = min(nblk, k0 + G);
     double s = 0.0;
-    int k = 0;
-    for (; k + 8 <= nblk; k += 8) {
+    for (int k = k0; k < k1; k += 8) {
         double v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = part[(size_t)(k + u) * len + j];
+        for (int u = 0; u < 8; u++) v[u] = part[(size_t)min(k + u, k1 - 1) * len + jc];
 #pragma unroll
-        for (int u = 0; u < 8; u++) s += v[u];
+        for (int u = 0; u < 8; u++)
+            if (k + u < k1) s += v[u];
     }
-    for (; k < nblk; k++) s += part[(size_t)k * len + j];
-    return s;
-}
-
-// out0[j] += sum over blocks of part[blk][j] (block order, f64), likewise
-// out1 from the second half when set.
-__global__ __launch_bounds__(NT) void colred_kernel(int nblk, size_t len,
-                                                    const double *__restrict__ part,
-                                                    float *__restrict__ out0,
-                                                    float *__restrict__ out1) {
-    const size_t j = (size_t)blockIdx.x * NT + threadIdx.x;
-    if (j >= len) return;
-    out0[j] += (float)blocks_sum(part, nblk, len, j);
-    if (out1) out1[j] += (float)blocks_sum(part + (size_t)nblk * len, nblk, len, j);
-}
-
-// Like colred_kernel over one column set of length len, sending columns
-// below `split` to out0 and the rest to out1 (out1[j - split]).
-__global__ __launch_bounds__(NT) void colred_split_kernel(int nblk, size_t len, size_t split,
-                                                          const double *__restrict__ part,
-                                                          float *__restrict__ out0,
-                                                          float *__restrict__ out1) {
-    const size_t j = (size_t)blockIdx.x * NT + threadIdx.x;
-    if (j >= len) return;
-    const double s = blocks_sum(part, nblk, len, j);
+    red[q][jl] = s;
+    __syncthreads();
+    if (q != 0 || j >= len) return;
+    double t = red[0][jl];
+    for (int g = 1; g < NG; g++) t += red[g][jl];
     if (j < split)
-        out0[j] += (float)s;
+        out0[j] += (float)t;
     else
-        out1[j - split] += (float)s;
+        out1[j - split] += (float)t;
 }
 
 // ------------------------------------------------------------ LayerScale
@@ -271,39 +274,56 @@ __global__ void dw3_bwd_x_kernel(size_t n, int th, int tw, int c, const float *_
     }
 }
 
-// dW [9][c] and db [c] partials over a block of images: thread = channel,
-// f64 sums in (image, output position, tap) order (norm.rs:377-418).
-// part: [nblk][10][c] (taps 0-8, then db).
-__global__ __launch_bounds__(NT) void dw3_bwd_w_kernel(size_t n, int th, int tw, int c,
-                                                       size_t ipb, const float *__restrict__ dy,
+// dW [9][c] and db [c] partials over output rows [rb*RB, rb*RB + RB) of
+// image im (block y = im * nrb + rb): thread = channel, f64 sums in (output
+// row, output column, tap) order (norm.rs:377-418).  The 3x3 input window
+// slides along the row in registers (3 loads per output position); taps
+// outside the image hold 0 and add nothing.  part: [n * nrb][10][c] (taps
+// 0-8, then db).
+__global__ __launch_bounds__(NT) void dw3_bwd_w_kernel(int th, int tw, int c, int RB, int nrb,
+                                                       const float *__restrict__ dy,
                                                        const float *__restrict__ x,
                                                        double *__restrict__ part) {
     const int ch = blockIdx.x * NT + threadIdx.x;
     if (ch >= c) return;
-    const size_t i0 = (size_t)blockIdx.y * ipb, i1 = min(n, i0 + ipb);
+    const size_t im = blockIdx.y / nrb;
+    const int rb = blockIdx.y % nrb, oy0 = rb * RB, oy1 = min(th, oy0 + RB);
     double aw[9], ab = 0.0;
+#pragma unroll
     for (int k = 0; k < 9; k++) aw[k] = 0.0;
     const size_t img = (size_t)th * tw * c;
-    for (size_t im = i0; im < i1; im++) {
-        const float *di = dy + im * img, *xi = x + im * img;
-        for (int oy = 0; oy < th; oy++)
-            for (int ox = 0; ox < tw; ox++) {
-                const float d = di[((size_t)oy * tw + ox) * c + ch];
-                ab += d;
+    const float *di = dy + im * img + ch, *xi = x + im * img + ch;
+    auto xat = [&](int sy, int sx) {
+        return (sy >= 0 && sy < th && sx >= 0 && sx < tw) ? xi[((size_t)sy * tw + sx) * c] : 0.0f;
+    };
+    for (int oy = oy0; oy < oy1; oy++) {
+        float win[3][3];
 #pragma unroll
-                for (int ky = 0; ky < 3; ky++) {
-                    const int sy = oy + ky - 1;
-                    if (sy < 0 || sy >= th) continue;
+        for (int ky = 0; ky < 3; ky++) {
+            win[ky][0] = 0.0f;
+            win[ky][1] = xat(oy + ky - 1, 0);
+            win[ky][2] = xat(oy + ky - 1, 1);
+        }
+        for (int ox = 0; ox < tw; ox++) {
+            const float d = di[((size_t)oy * tw + ox) * c];
+            float nxt[3];
 #pragma unroll
-                    for (int kx = 0; kx < 3; kx++) {
-                        const int sx = ox + kx - 1;
-                        if (sx < 0 || sx >= tw) continue;
-                        aw[ky * 3 + kx] += (double)(d * xi[((size_t)sy * tw + sx) * c + ch]);
-                    }
-                }
+            for (int ky = 0; ky < 3; ky++) nxt[ky] = xat(oy + ky - 1, ox + 2);
+            ab += d;
+#pragma unroll
+            for (int ky = 0; ky < 3; ky++)
+#pragma unroll
+                for (int kx = 0; kx < 3; kx++) aw[ky * 3 + kx] += (double)(d * win[ky][kx]);
+#pragma unroll
+            for (int ky = 0; ky < 3; ky++) {
+                win[ky][0] = win[ky][1];
+                win[ky][1] = win[ky][2];
+                win[ky][2] = nxt[ky];
             }
+        }
     }
     double *pb = part + (size_t)blockIdx.y * 10 * c;
+#pragma unroll
     for (int k = 0; k < 9; k++) pb[(size_t)k * c + ch] = aw[k];
     pb[(size_t)9 * c + ch] = ab;
 }
@@ -402,30 +422,34 @@ unsigned ew_grid(size_t len) {
     return (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(len, NT), 16384));
 }
 
-// Rows per column-partial block: about 64 blocks of rows, so that both the
-// partial pass (rows per thread) and the block-order pass (blocks per
-// column) are short chains.
-size_t rows_per_block(size_t rows, int c) {
-    return std::max<size_t>(16, rnn_div_up(rows, 64));
-}
+}  // namespace
 
 // Column sums of a*b (b set) and of a over rows, added into outab / outa.
-int colsum_add(rnn_ctx *ctx, size_t rows, int c, const float *a, const float *b, float *outab,
-               float *outa) {
+// Many short chains: blocks of CS_ROWS rows x 64 columns (colsum_part_kernel),
+// then the blocks' partials in order, 16 groups per column (colsum_red_kernel).
+int rnn_colsum_f64(rnn_ctx *ctx, size_t rows, int c, const float *a, const float *b,
+                   float *outab, float *outa) {
     if (rows == 0 || c == 0) return RNN_OK;
-    const size_t rpb = rows_per_block(rows, c);
-    const size_t nblk = rnn_div_up(rows, rpb);
+    const size_t nblk = rnn_div_up(rows, (size_t)CS_ROWS);
     if (nblk > 65535) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "column sums: too many rows");
     const int nout = (b ? 1 : 0) + (outa ? 1 : 0);
-    double *part = (double *)rnn_workspace(ctx, nout * nblk * c * sizeof(double));
+    const size_t len = (size_t)nout * c;
+    double *part = (double *)rnn_workspace(ctx, nblk * len * sizeof(double));
     if (!part) return RNN_E_NOMEM;
-    colsum_kernel<<<dim3((unsigned)rnn_div_up((size_t)c, NT), (unsigned)nblk), NT, 0,
-                    ctx->stream>>>(rows, c, rpb, a, b, outa != nullptr, part);
+    colsum_part_kernel<<<dim3((unsigned)rnn_div_up((size_t)c, (size_t)64), (unsigned)nblk), NT, 0,
+                         ctx->stream>>>(rows, c, a, b, outa != nullptr, part);
     RNN_LAUNCHED(ctx);
-    colred_kernel<<<(unsigned)rnn_div_up((size_t)c, NT), NT, 0, ctx->stream>>>(
-        (int)nblk, (size_t)c, part, b ? outab : outa, b ? outa : nullptr);
+    colsum_red_kernel<<<(unsigned)rnn_div_up(len, (size_t)CS_RED_COLS), NT, 0, ctx->stream>>>(
+        (int)nblk, len, (size_t)(b ? c : len), part, b ? outab : outa, b ? outa : nullptr);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
+}
+
+namespace {
+
+int colsum_add(rnn_ctx *ctx, size_t rows, int c, const float *a, const float *b, float *outab,
+               float *outa) {
+    return rnn_colsum_f64(ctx, rows, c, a, b, outab, outa);
 }
 
 bool dims_ok(size_t rows, size_t c) { return c <= (1u << 20) && rows <= ((size_t)1 << 40); }
@@ -540,18 +564,20 @@ int rnn_dwconv3_backward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c,
         return rnn_fail(ctx, RNN_E_NULL, "dwconv3_backward: null operand");
     if (th > 65536 || tw > 65536 || !dims_ok(n * th * tw, c))
         return rnn_fail(ctx, RNN_E_INVALID, "dwconv3: %zu x %zu x %zu x %zu", n, th, tw, c);
-    // dW and db partials per block of images, then the block-order sum
+    // dW and db partials per block of output rows (about 1024 blocks), then
+    // the block-order sum
     const size_t cblk = rnn_div_up(c, (size_t)NT);
-    const size_t ipb = std::max<size_t>(1, rnn_div_up(n, std::max<size_t>(1, 1024 / cblk)));
-    const size_t nblk = rnn_div_up(n, ipb);
+    const size_t want = std::max<size_t>(1, 1024 / (cblk * n));
+    const size_t nrb = std::min(th, want), RB = rnn_div_up(th, nrb);
+    const size_t nrb_used = rnn_div_up(th, RB), nblk = n * nrb_used;
     if (nblk > 65535) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "dwconv3: too many images");
     double *part = (double *)rnn_workspace(ctx, nblk * 10 * c * sizeof(double));
     if (!part) return RNN_E_NOMEM;
     dw3_bwd_w_kernel<<<dim3((unsigned)cblk, (unsigned)nblk), NT, 0, ctx->stream>>>(
-        n, (int)th, (int)tw, (int)c, ipb, dy, x, part);
+        (int)th, (int)tw, (int)c, (int)RB, (int)nrb_used, dy, x, part);
     RNN_LAUNCHED(ctx);
     // part is [nblk][10c]: taps 0-8 (dW's [9][c] order), then db
-    colred_split_kernel<<<(unsigned)rnn_div_up(10 * c, (size_t)NT), NT, 0, ctx->stream>>>(
+    colsum_red_kernel<<<(unsigned)rnn_div_up(10 * c, (size_t)CS_RED_COLS), NT, 0, ctx->stream>>>(
         (int)nblk, 10 * c, 9 * c, part, dw, db);
     RNN_LAUNCHED(ctx);
     const size_t len = n * th * tw * c;
