@@ -277,6 +277,14 @@ int rnn_layerscale_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, 
                            float *y);
 int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *x,
                             const float *l, float *dx, float *dl);
+/* DropPath::backward then LayerScale::backward (vit.rs:61-73,
+ * norm.rs:182-212) in one pass that reads dy without changing it:
+ * g = dy * mask[r / rpi] (mask NULL: g = dy), dl += sum_r g x, dx = g l
+ * (dx must not be dy).  Block::backward's branches (vit.rs:175-232) read the
+ * same dy twice or three times, so no copy of it is needed. */
+int rnn_drop_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy,
+                                 const float *x, const float *l, const float *mask, size_t rpi,
+                                 float *dx, float *dl);
 /* The SwiGLU gate between SwiGlu's two Linear calls (norm.rs:250-288): ab is
  * [rows][2h] (a | b), u = a sigmoid(a) b [rows][h]; the backward writes
  * dab [rows][2h] from du [rows][h]. */

@@ -194,6 +194,8 @@ def lib():
             "rnn_ln_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_layerscale_forward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),
             "rnn_layerscale_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_drop_layerscale_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _sz, _vp,
+                                                  _vp]),
             "rnn_swiglu_forward": (_i, [_vp, _sz, _sz, _vp, _vp]),
             "rnn_swiglu_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),
             "rnn_dwconv3_forward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),

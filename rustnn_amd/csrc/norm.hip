@@ -102,13 +102,15 @@ __global__ __launch_bounds__(NT) void ln_bwd_kernel(size_t rows, int c, const fl
 // [64x, 64x + 64), rows [CS_ROWS y, CS_ROWS (y + 1)); wave g sums the rows
 // g, g + 4, ... of the block in order (8 loads ahead of their adds), and the
 // four wave sums are added in wave order.  part: [block row][nout * c], the
-// sums of a*b (b set) first, then those of a.
+// sums of a*b (b set) first, then those of a.  With rs set, a's row r is
+// first multiplied by rs[r / rpi].
 constexpr int CS_ROWS = 64;
 constexpr int CS_RED_COLS = 16;  // columns per stage-2 block (16 groups each)
 
 __global__ __launch_bounds__(NT) void colsum_part_kernel(size_t rows, int c,
                                                          const float *__restrict__ a,
                                                          const float *__restrict__ b, int want_a,
+                                                         const float *__restrict__ rs, size_t rpi,
                                                          double *__restrict__ part) {
     __shared__ double red[2][NT / 64][64];
     const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
@@ -121,6 +123,7 @@ __global__ __launch_bounds__(NT) void colsum_part_kernel(size_t rows, int c,
         for (int u = 0; u < 8; u++) {
             const size_t rr = min(r + (size_t)(NT / 64) * u, r1 - 1);
             av[u] = a[rr * c + jc];
+            if (rs) av[u] = av[u] * rs[rr / rpi];
             bv[u] = b ? b[rr * c + jc] : 0.0f;
         }
 #pragma unroll
@@ -186,6 +189,16 @@ __global__ void scale_cols_kernel(size_t len, int c, const float *x, const float
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
          i += (size_t)gridDim.x * blockDim.x)
         y[i] = x[i] * l[i % c];
+}
+
+// dx = (dy m) l with m = mask[i / per] (DropPath::backward, vit.rs:61-73,
+// then LayerScale's, norm.rs:205-211).
+__global__ void scale_cols_masked_kernel(size_t len, int c, size_t per, const float *dy,
+                                         const float *__restrict__ l,
+                                         const float *__restrict__ mask, float *dx) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x)
+        dx[i] = (dy[i] * mask[i / per]) * l[i % c];
 }
 
 // ------------------------------------------------------------ SwiGLU gate
@@ -428,7 +441,7 @@ unsigned ew_grid(size_t len) {
 // Many short chains: blocks of CS_ROWS rows x 64 columns (colsum_part_kernel),
 // then the blocks' partials in order, 16 groups per column (colsum_red_kernel).
 int rnn_colsum_f64(rnn_ctx *ctx, size_t rows, int c, const float *a, const float *b,
-                   float *outab, float *outa) {
+                   float *outab, float *outa, const float *rs, size_t rpi) {
     if (rows == 0 || c == 0) return RNN_OK;
     const size_t nblk = rnn_div_up(rows, (size_t)CS_ROWS);
     if (nblk > 65535) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "column sums: too many rows");
@@ -437,7 +450,7 @@ int rnn_colsum_f64(rnn_ctx *ctx, size_t rows, int c, const float *a, const float
     double *part = (double *)rnn_workspace(ctx, nblk * len * sizeof(double));
     if (!part) return RNN_E_NOMEM;
     colsum_part_kernel<<<dim3((unsigned)rnn_div_up((size_t)c, (size_t)64), (unsigned)nblk), NT, 0,
-                         ctx->stream>>>(rows, c, a, b, outa != nullptr, part);
+                         ctx->stream>>>(rows, c, a, b, outa != nullptr, rs, rpi, part);
     RNN_LAUNCHED(ctx);
     colsum_red_kernel<<<(unsigned)rnn_div_up(len, (size_t)CS_RED_COLS), NT, 0, ctx->stream>>>(
         (int)nblk, len, (size_t)(b ? c : len), part, b ? outab : outa, b ? outa : nullptr);
@@ -449,7 +462,7 @@ namespace {
 
 int colsum_add(rnn_ctx *ctx, size_t rows, int c, const float *a, const float *b, float *outab,
                float *outa) {
-    return rnn_colsum_f64(ctx, rows, c, a, b, outab, outa);
+    return rnn_colsum_f64(ctx, rows, c, a, b, outab, outa, nullptr, 1);
 }
 
 bool dims_ok(size_t rows, size_t c) { return c <= (1u << 20) && rows <= ((size_t)1 << 40); }
@@ -514,6 +527,31 @@ int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy
     int rc = colsum_add(ctx, rows, (int)c, dy, x, dl, nullptr);
     if (rc) return rc;
     scale_cols_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, (int)c, dy, l, dx);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_drop_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy,
+                                 const float *x, const float *l, const float *mask, size_t rpi,
+                                 float *dx, float *dl) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!dy || !x || !l || !dx || !dl)
+        return rnn_fail(ctx, RNN_E_NULL, "drop_layerscale_backward: null operand");
+    if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "layerscale: %zu x %zu", rows, c);
+    if (dx == dy) return rnn_fail(ctx, RNN_E_INVALID, "drop_layerscale_backward: dx is dy");
+    if (mask && (rpi == 0 || rows % rpi))
+        return rnn_fail(ctx, RNN_E_INVALID, "drop_layerscale_backward: %zu rows per image of %zu",
+                        rpi, rows);
+    // dl += sum (dy m) x, then dx = (dy m) l
+    int rc = rnn_colsum_f64(ctx, rows, (int)c, dy, x, dl, nullptr, mask, mask ? rpi : 1);
+    if (rc) return rc;
+    if (mask)
+        scale_cols_masked_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, (int)c,
+                                                                           rpi * c, dy, l, mask, dx);
+    else
+        scale_cols_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, (int)c, dy, l, dx);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

@@ -208,8 +208,9 @@ int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, co
 int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, float *out);
 // outab[j] += sum_r a[r][j] b[r][j] (b set), outa[j] += sum_r a[r][j] (outa
 // set): f64 sums in a fixed order (two launches).
+// With rs set, a's row r counts as a[r] * rs[r / rpi].
 int rnn_colsum_f64(rnn_ctx *ctx, size_t rows, int c, const float *a, const float *b,
-                   float *outab, float *outa);
+                   float *outab, float *outa, const float *rs = nullptr, size_t rpi = 1);
 // Specialised forward (dx = 0) / dX (dx = 1) convolution; RNN_E_UNSUPPORTED
 // when (k, stride, pad) has no specialisation.  wp: the weights packed by
 // rnn_conv_pack for this direction (the kernels then load each stage's

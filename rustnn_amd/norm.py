@@ -73,24 +73,33 @@ class LayerScale:
         self.x = None
 
     def forward(self, x, train):
-        """Scales x in place, as the reference consumes its input."""
+        """y = x lambda.  Training keeps x for the backward (the caller must
+        not change it) and returns a new tensor; eval scales x in place, as
+        the reference consumes its input."""
+        import torch
         rows, c = _rows_c(x)
         if c != self.c:
             raise ValueError(f"LayerScale: {c} channels, the layer has {self.c}")
+        y = torch.empty_like(x) if train else x
         if train:
-            self.x = x.clone()
+            self.x = x
         self.ctx.check(lib().rnn_layerscale_forward(self.ctx.h, rows, c, _ptr(x, rows * c, "x"),
                                                     _ptr(self.l.v, c, "l"),
-                                                    _ptr(x, rows * c, "y")))
-        return x
+                                                    _ptr(y, rows * c, "y")))
+        return y
 
-    def backward(self, dy):
-        """Scales dy in place (norm.rs:182-212)."""
+    def backward(self, dy, mask=None):
+        """norm.rs:182-212, after DropPath::backward's per-image mask when
+        one is given (vit.rs:61-73): returns a new dx; dy is not changed."""
+        import torch
         rows, c = _rows_c(dy)
-        self.ctx.check(lib().rnn_layerscale_backward(
+        dx = torch.empty_like(dy)
+        rpi = rows // mask.numel() if mask is not None else 1
+        self.ctx.check(lib().rnn_drop_layerscale_backward(
             self.ctx.h, rows, c, _ptr(dy, rows * c, "dy"), _ptr(self.x, rows * c, "x"),
-            _ptr(self.l.v, c, "l"), _ptr(dy, rows * c, "dx"), _ptr(self.l.g, c, "dl")))
-        return dy
+            _ptr(self.l.v, c, "l"), _ptr(mask, mask.numel(), "mask") if mask is not None else None,
+            rpi, _ptr(dx, rows * c, "dx"), _ptr(self.l.g, c, "dl")))
+        return dx
 
     def for_each_param(self, f):
         f(self.l)

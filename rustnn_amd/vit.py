@@ -254,15 +254,16 @@ class Block:
         """Returns dx; dmem accumulates the memory's gradient (vit.rs:175-249)."""
         import torch
         L, ctx, c = lib(), self.ctx, self.c
-        dm = self.ls2.backward(self.dp3.backward(dz.clone()))
+        # each branch's DropPath + LayerScale backward reads dz / dy unchanged
+        dm = self.ls2.backward(dz, self.dp3.mask)
         dh2 = self.mlp.backward(dm)
-        dy = dz.clone()
-        _add_(dy, self.n2.backward(dh2), ctx)
-        dh = torch.zeros_like(dy)
+        dy = self.n2.backward(dh2)  # a new tensor
+        _add_(dy, dz, ctx)
+        dh = None  # the branches' input gradients, added in branch order
         if self.cross is not None:
-            dc = self.lsm.backward(self.dp2.backward(dy.clone()))
-            _add_(dh, self.cross.backward(dc, mem, dmem), ctx)
-        da = self.ls1.backward(self.dp1.backward(dy.clone()))
+            dc = self.lsm.backward(dy, self.dp2.mask)
+            dh = self.cross.backward(dc, mem, dmem)
+        da = self.ls1.backward(dy, self.dp1.mask)
         # gamma.g += sum da * dwo; ddw = gamma * da: the LayerScale backward
         rows = da.numel() // c
         ddw = torch.empty_like(da)
@@ -271,7 +272,11 @@ class Block:
                                             _ptr(self.gamma.v, c, "gamma"),
                                             _ptr(ddw, rows * c, "ddw"),
                                             _ptr(self.gamma.g, c, "dgamma")))
-        _add_(dh, self.attn.backward(da), ctx)
+        ga = self.attn.backward(da)
+        if dh is None:
+            dh = ga
+        else:
+            _add_(dh, ga, ctx)
         _add_(dh, self.dw.backward(ddw), ctx)
         _add_(dy, self.n1.backward(dh), ctx)
         return dy

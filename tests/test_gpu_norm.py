@@ -75,6 +75,29 @@ def test_layerscale(rnn, orc):
     assert rel_frob(to_host(ls.l.g), dl) < TOL
 
 
+@pytest.mark.parametrize("n,t,c", [(16, 64, 256), (3, 7, 33)])
+def test_drop_layerscale_backward(rnn, orc, n, t, c):
+    """rnn_drop_layerscale_backward == DropPath::backward (dy times the
+    image's mask) then LayerScale::backward, dy left unchanged."""
+    from rustnn_amd.norm import LayerScale
+    rows = n * t
+    x, l, dy = _r((rows, c), 14), _r(c, 15, 1e-2), _r((rows, c), 16)
+    keep = np.float32(0.8)
+    mask = np.where(np.arange(n) % 3 == 1, np.float32(0.0), np.float32(1.0) / keep)
+    mask = mask.astype(np.float32)
+    ls = LayerScale(c, 1e-4)
+    ls.l.v.copy_(to_dev(l))
+    ls.forward(_dev(x), True)
+    g = (dy.reshape(n, t, c) * mask[:, None, None]).reshape(rows, c).astype(np.float32)
+    dl = np.zeros(c, np.float32)
+    wdx = orc.layerscale_backward(g, x, l, dl)
+    DY = _dev(dy)
+    dx = to_host(ls.backward(DY, to_dev(mask)))
+    assert np.array_equal(dx.reshape(rows, c), wdx)
+    assert rel_frob(to_host(ls.l.g), dl) < TOL
+    assert np.array_equal(to_host(DY).reshape(rows, c), dy.reshape(rows, c))
+
+
 @pytest.mark.parametrize("rows,h", [(4096, 352), (1000, 512), (7, 5)])
 def test_swiglu_gate(rnn, orc, rows, h):
     import torch
