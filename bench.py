@@ -97,6 +97,30 @@ def traffic_from_profiles(op):
     return None
 
 
+def profile_kernels(op):
+    """The kernel rows of `op` in the committed rocprofv3 kernel-trace summary
+    profiles/conv_sweep_kernel_stats.md: [(kernel template, avg us)], the
+    op's main kernel first; [] when the op is not in it."""
+    path = os.path.join(ROOT, "profiles", "conv_sweep_kernel_stats.md")
+    if not os.path.exists(path):
+        return []
+    out, cur = [], None
+    for ln in open(path):
+        if not ln.startswith("|") or ln.startswith("|---"):
+            continue
+        cells = [c.strip() for c in ln.strip().strip("|").split("|")]
+        if len(cells) < 3:
+            continue
+        if cells[0]:
+            cur = cells[0].strip("`")
+        if cur == op:
+            try:
+                out.append((cells[1].strip("`").split(" (")[0], float(cells[2])))
+            except ValueError:
+                pass
+    return out
+
+
 def host_cpu():
     """The host CPU as lscpu reports it, and the CPUs this process may use."""
     info = {}
@@ -353,6 +377,50 @@ def bench_attention(R, ctx, reps):
                      f"({ncopy * (7 * mb + pb) >> 20} MiB, past the 256 MiB Infinity Cache); "
                      "*_cache_resident: one set of operands")
     return res
+
+
+def bench_1x1_rotated(R, ctx, layers, run_op, reps):
+    """The 1x1 stride-2 shortcut convs are HBM-bound: their passes in GB/s
+    against 8 TB/s, each call on its own copy of its operands, rotating over
+    enough copies to exceed the 256 MB Infinity Cache.  Algorithmic bytes:
+    forward x at the sampled positions + W + y; dX dY + W + dX (written
+    whole: the skipped positions get zeros); dW dY + x at the sampled
+    positions + the weight-gradient slabs the kernel writes."""
+    import torch
+    out = []
+    for L in layers:
+        sp = L["sp"]
+        if sp.k != 1 or sp.stride != 2:
+            continue
+        n_in, n_out = N * sp.cin * sp.h * sp.w, N * sp.cout * sp.oh * sp.ow
+        sampled = N * sp.cin * sp.oh * sp.ow
+        per_set = 4 * (2 * n_in + 2 * n_out)
+        ncopy = -(-MALL_BYTES // per_set) + 1
+        sets = []
+        for _ in range(ncopy):
+            c = dict(L)
+            c["x"] = torch.randn(n_in, device="cuda")
+            c["dy"] = torch.randn(n_out, device="cuda")
+            c["y"] = torch.empty(n_out, device="cuda")
+            c["dx"] = torch.empty(n_in, device="cuda")
+            sets.append(c)
+        wb = 4 * sp.cout * sp.cin
+        slab_b = 4 * L["slabs"].numel()
+        bytes_of = {"fwd": 4 * (sampled + n_out) + wb, "dx": 4 * (n_out + n_in) + wb,
+                    "dw_kernel": 4 * (n_out + sampled) + slab_b}
+        for ps, by in bytes_of.items():
+            st = {"i": 0}
+
+            def one():
+                run_op(sets[st["i"] % ncopy], ps)
+                st["i"] += 1
+            one()
+            ms = time_graph(ctx, one, max(reps, 2 * ncopy))
+            gbs = by / (ms * 1e-3) / 1e9
+            out.append({"op": f"{L['name']}:{ps}", "us": round(ms * 1e3, 2), "bytes": by,
+                        "GB_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+                        "copies": ncopy})
+    return out
 
 
 def bench_gemm(R, ctx, reps):
@@ -822,21 +890,51 @@ def main():
 
     def roofline(op_row, flops):
         achieved = flops / (op_row["ms"] * 1e-3) / 1e12
-        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-                "traffic": traffic_from_profiles(op_row["op"]), "kernel": op_row["op"],
-                "flop_per_launch": flops, "avg_launch_ms": op_row["ms"]}
+        out = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+               "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+               "traffic": traffic_from_profiles(op_row["op"]), "kernel": op_row["op"],
+               "flop_per_launch": flops, "avg_launch_ms": op_row["ms"],
+               "timing": "graph replays of op-reps back-to-back launches (launch gaps "
+                         "included), HIP events on the library's stream"}
+        prof = profile_kernels(op_row["op"])
+        if prof:
+            # the same kernel's average duration in the committed kernel trace
+            # (kernel time alone, no launch gaps)
+            us = prof[0][1]
+            out["template"] = prof[0][0]
+            out["rocprof"] = {"avg_launch_us": us,
+                              "frac": round(flops / (us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
+                              "source": "profiles/conv_sweep_kernel_stats.md"}
+        return out
 
     lay = {L["name"]: L for L in layers}
-    # dominant kernel of the ResNet step: largest multiplicity x duration among
-    # the kernels as the step launches them (forward, dX, dW kernel)
+    # Dominant kernel of the ResNet step: the kernel template (from the
+    # committed kernel trace's op -> kernel table) with the largest
+    # multiplicity x duration over all the ops the step launches it for
+    # (forward, dX, dW kernel); its roofline row is the op of that template
+    # with the most launch time.
     conv_ops = [r for r in per_op if "tflops" in r]
     step_kernels = [r for r in conv_ops if not r["op"].endswith(":dw")]
-    dom = max(step_kernels, key=lambda r: r["ms"] * r["in_resnet_step"])
+    tmpl = {r["op"]: (profile_kernels(r["op"]) or [(r["op"], 0)])[0][0] for r in step_kernels}
+    by_t = {}
+    for r in step_kernels:
+        by_t.setdefault(tmpl[r["op"]], []).append(r)
+    t_dom = max(by_t, key=lambda t: sum(r["ms"] * r["in_resnet_step"] for r in by_t[t]))
+    rows_t = by_t[t_dom]
+    dom = max(rows_t, key=lambda r: r["ms"] * r["in_resnet_step"])
     roof = roofline(dom, lay[dom["op"].split(":")[0]]["flops"])
-    roof["share_of_resnet_step"] = round(dom["ms"] * dom["in_resnet_step"] / rn["ms"], 4)
+    t_ms = sum(r["ms"] * r["in_resnet_step"] for r in rows_t)
+    t_fl = sum(lay[r["op"].split(":")[0]]["flops"] * r["in_resnet_step"] for r in rows_t)
+    roof["share_of_resnet_step"] = round(t_ms / rn["ms"], 4)
+    roof["template_launches_per_step"] = sum(r["in_resnet_step"] for r in rows_t)
+    roof["template_ops"] = [r["op"] for r in rows_t]
+    roof["template_frac"] = round(t_fl / (t_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)
+    roof["share_note"] = ("launch time of every launch of the template per step / step time; "
+                          "the step runs weight gradients on a second stream, so kernels "
+                          "overlap and shares of different kernels can sum past 1")
     sdom = max(step_kernels, key=lambda r: r["ms"])
     sweep_roof = roofline(sdom, lay[sdom["op"].split(":")[0]]["flops"])
+    ones = bench_1x1_rotated(R, ctx, layers, run_op, args.op_reps)
 
     attention = bench_attention(R, ctx, args.op_reps)
     gemms = bench_gemm(R, ctx, args.op_reps)
@@ -888,7 +986,7 @@ def main():
             "tflops_unpacked_weights": round(sweep_flops / (sweep_ms_unpacked * 1e-3) / 1e12,
                                              3),
             "flop_per_step": sweep_flops, "roofline": sweep_roof, "cpu_baseline": sweep_cpu,
-            "per_op": per_op},
+            "per_op": per_op, "ops_1x1_s2_hbm": ones},
         "config2_attention": attention, "gemmbench": gemms, "rustvit_optimizer": vit_optim,
         "config4_rustvit_step": vit_step, "cpu_reference_path": proto,
     }
