@@ -476,6 +476,7 @@ struct DwSmallArgs {
     float *part;  // [nz][CO][CI*9]
     int N, CO, CI, H, W, OH, OW, pad;
     int R, tiles_a, ntiles;
+    int vec;                   // OW % 4 == 0 and dY 16-byte aligned: float4 dY loads
     FastDiv fd_xplane, fd_xw;  // X window plane (R + 2) * (OW + 2) and row OW + 2
 };
 
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(SMC_THREADS) void conv_dw_smallc_kernel(DwSmallArgs
                             (long long)a0 * g.OW;
         // all loads of the tile are issued before the first LDS store
         const long long cst = (long long)g.OH * g.OW;
-        if ((g.OW & 3) == 0) {
+        if (g.vec) {
             // 16-byte loads: thread (co4 = tid / 64, j = tid % 64) takes
             // pixels 4j .. 4j+3 of output channels co4, co4 + 4, ...
             const int j = tid & 63, co4 = tid >> 6, p = 4 * j;
@@ -704,6 +705,8 @@ static bool dw_small_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
     a.OH = sp->oh;
     a.OW = sp->ow;
     a.pad = sp->pad;
+    // every row start of dY is then 16-byte aligned too (OW, OH*OW multiples of 4)
+    a.vec = (a.OW & 3) == 0 && ((uintptr_t)dy & 15) == 0;
     a.R = std::max(1, std::min(SMC_PIX / a.OW, a.OH));
     if ((long long)a.CI * (a.R + 2) * (a.OW + 2) > SMC_XMAX) return false;
     if ((long long)n * std::max((long long)a.CI * a.H * a.W, (long long)a.CO * a.OH * a.OW) >=

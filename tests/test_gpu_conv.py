@@ -26,6 +26,10 @@ SHAPES = [
     ("gc_3x3s2_4to5_7", 2, 4, 5, 3, 2, 1, 7),
     ("odd_3x3s1_5to40_9", 3, 5, 40, 3, 1, 1, 9),
     ("odd_3x3s2_34to33_11", 5, 34, 33, 3, 2, 1, 11),
+    # the few-input-channel dW kernel: cin 1 and 2, pad 0, a partial last
+    # tile of output rows (20 rows in tiles of 12) with 16-byte dY loads
+    ("smallc_3x3s1_1to8_20", 3, 1, 8, 3, 1, 1, 20),
+    ("smallc_3x3s1_2to40_22_p0", 3, 2, 40, 3, 1, 0, 22),
 ]
 
 
@@ -92,6 +96,9 @@ def test_conv_packed_weights_bit_exact(rnn, orc, name, n, cin, cout, k, s, p, h)
     X, W, DY = to_dev(x), to_dev(w), to_dev(dy)
     for dx in (0, 1):
         wp = R.conv_pack_weights(sp, dx, W)
+        if (k, s, p) not in ((3, 1, 1), (3, 2, 1), (1, 2, 0), (1, 1, 0)):
+            assert wp is None  # no specialised kernel for this (k, stride, pad): nothing to pack
+            return
         assert wp is not None
         if dx == 0:
             want = to_host(R.conv2d_forward(sp, n, X, W))
@@ -145,6 +152,29 @@ def test_conv_dw_slabs(rnn, orc, name, n, cin, cout, k, s, p, h):
             dw = to_dev(np.zeros(ln, np.float32))
             rnn.conv2d_backward_w(gsp, n, DY, X, dw)
             assert rel_frob(to_host(dw), got) < 1e-6, name
+
+
+@pytest.mark.parametrize("cin,p,h", [(3, 1, 32), (2, 0, 22)])
+def test_conv_dw_smallc_unaligned_dy(rnn, orc, cin, p, h):
+    """The few-input-channel dW kernel reads dY with 16-byte loads only when
+    dY is 16-byte aligned: a dY starting 4 bytes into its buffer takes the
+    scalar path and gives the same sums."""
+    n, cout = 4, 32
+    sp = orc.ConvSpec.make(cin, cout, 3, 1, p, h, h)
+    gsp = rnn.ConvSpec.make(cin, cout, 3, 1, p, h, h)
+    x, _, dy = inputs(orc, sp, n, seed=41)
+    with orc.threads(8):
+        want = orc.conv2d_backward_w(sp, n, dy, x).ravel()
+    buf = to_dev(np.concatenate([np.zeros(1, np.float32), dy]))
+    DY = buf[1:]
+    assert DY.data_ptr() % 16 != 0
+    got = []
+    for d in (DY, to_dev(dy)):
+        dw = to_dev(np.zeros(sp.cout * sp.ckk, np.float32))
+        rnn.conv2d_backward_w(gsp, n, d, to_dev(x), dw)
+        got.append(to_host(dw))
+    assert rel_frob(got[0], want) < TOL
+    assert np.array_equal(got[0], got[1])
 
 
 def test_conv_deterministic(rnn, orc):

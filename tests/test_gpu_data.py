@@ -54,7 +54,10 @@ def test_batch_train_randaugment(rnn, orc, ra_mag, ra_n):
     gives 0x3eac155f, the correctly rounded value is 0x3eac155e); a float that
     lands on a u8 truncation boundary then moves a pixel by a level, which a
     later autocontrast can double.  Bound: at least 99.99% of values
-    bit-exact and none more than two levels (2 / (255 * std)) away."""
+    bit-exact and none more than two levels (2 / (255 * std)) away -- for
+    these seeds only: a magnitude one ulp off can also change posterize's bit
+    count or cross solarize's threshold (p -> 255 - p), so this path is
+    parity-unpinned beyond the seeds tested here."""
     from rustnn_amd import data
     images, fine, coarse = _set()
     ds = data.Dataset.from_arrays(images, fine, coarse)
