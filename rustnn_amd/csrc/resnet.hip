@@ -83,6 +83,10 @@ struct NetConv {
     // this conv's output gradient in the backward (per plan): its own buffer,
     // so the dW reading it on the side stream overlaps the work after it
     float *dyb = nullptr;
+    // Side-stream slab sums (per plan): this conv's gradient segment in the
+    // side table, or -1 (summed with the rest).
+    int fseg = -1;
+    long long fblk = 0;
     rnn_conv_spec spec(uint32_t h, uint32_t w_) const {
         rnn_conv_spec sp;
         rnn_conv_spec_init(&sp, cin, cout, k, stride, pad, h, w_);
@@ -129,6 +133,13 @@ struct rnn_resnet {
     GradSeg *segs = nullptr;
     int nseg = 0;
     long long nseg_blocks = 0;
+    // With the side stream: each conv's segment alone (fsegs, blk0 = 0),
+    // its slabs summed into g on the side stream right after its dW; the
+    // other segments with slabs (the stem) in rsegs after the join, then the
+    // SGD step over every parameter.
+    GradSeg *fsegs = nullptr, *rsegs = nullptr;
+    int nrseg = 0;
+    long long nrseg_blocks = 0;
     uint32_t *labels = nullptr, *correct = nullptr;
     double *part = nullptr;
     // Packed conv weights: one segment per (conv, direction), refreshed by
@@ -299,6 +310,8 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     }
     const size_t o_psegs = cv.take(std::max<size_t>(packs.size(), 1) * sizeof(PackSeg));
     const size_t o_segs = cv.take(r->params.size() * sizeof(GradSeg));
+    const size_t o_fsegs = cv.take(r->params.size() * sizeof(GradSeg));
+    const size_t o_rsegs = cv.take(r->params.size() * sizeof(GradSeg));
     const size_t o_lab = cv.take(n * sizeof(uint32_t));
     const size_t o_cor = cv.take(sizeof(uint32_t));
     void *mem = nullptr;
@@ -377,6 +390,38 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
         g.decay = ps.decay ? 1 : 0;
         segs[k] = g;
         blk += (long long)rnn_div_up(ps.len, 32);
+    }
+    // the segments with slabs split: each conv's but the stem's alone, the rest
+    std::vector<GradSeg> fsv, rsv;
+    long long rblk = 0;
+    for (size_t k = 0; k < order.size(); k++) {
+        NetConv *c = const_cast<NetConv *>(conv_of[order[k]]);
+        GradSeg g = segs[k];
+        if (c) c->fseg = -1;
+        if (c && c != &r->stem && g.slabs) {
+            g.blk0 = 0;
+            c->fseg = (int)fsv.size();
+            c->fblk = (long long)rnn_div_up((size_t)g.len, (size_t)32);
+            fsv.push_back(g);
+        } else if (g.slabs) {
+            g.blk0 = rblk;
+            rblk += (long long)rnn_div_up((size_t)g.len, (size_t)32);
+            rsv.push_back(g);
+        }
+    }
+    r->fsegs = (GradSeg *)(base + o_fsegs);
+    r->rsegs = (GradSeg *)(base + o_rsegs);
+    r->nrseg = (int)rsv.size();
+    r->nrseg_blocks = rblk;
+    for (auto *tab : {&fsv, &rsv}) {
+        if (tab->empty()) continue;
+        hipError_t fe = hipMemcpy(tab == &fsv ? r->fsegs : r->rsegs, tab->data(),
+                                  tab->size() * sizeof(GradSeg), hipMemcpyHostToDevice);
+        if (fe != hipSuccess) {
+            (void)hipFree(r->arena);
+            r->arena = nullptr;
+            return rnn_fail(ctx, RNN_E_HIP, "resnet plan upload: %s", hipGetErrorString(fe));
+        }
     }
     r->segs = (GradSeg *)(base + o_segs);
     r->nseg = (int)segs.size();
@@ -542,7 +587,11 @@ int conv_dw_side(rnn_resnet *r, const NetConv &c, const rnn_conv_spec &sp, const
     RNN_HIP(ctx, hipStreamWaitEvent(r->side, e, 0));
     hipStream_t main = ctx->stream;
     ctx->stream = r->side;
-    const int rc = conv_dw(r, c, sp, dy, x);
+    int rc = conv_dw(r, c, sp, dy, x);
+    // its slab sums into g right away, off the step's critical tail
+    if (rc == RNN_OK && c.fseg >= 0)
+        rc = rnn_grad_finalize_launch(ctx, r->fsegs + c.fseg, 1, c.fblk, r->pv, r->pg, r->pm,
+                                      r->scal, 0);
     ctx->stream = main;
     return rc;
 }
@@ -606,7 +655,15 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
                                      r->y0, bn_state(r, r->stem_bn), r->stem_bn.part, r->t1));
     // The stem's dX would be the image gradient: discarded (model.rs:161).
     TRY(conv_dw(r, r->stem, sp, r->t1, r->x));
-    TRY(join_side(r, ev));
+    if (use_side(r)) {
+        // the side stream summed the other convs' slabs into g
+        TRY(join_side(r, ev));
+        TRY(rnn_grad_finalize_launch(ctx, r->rsegs, r->nrseg, r->nrseg_blocks, r->pv, r->pg,
+                                     r->pm, r->scal, 0));
+        if (!sgd) return RNN_OK;
+        TRY(rnn_sgd_launch(ctx, r->np, r->ndecay, r->pv, r->pg, r->pm, 0.f, 0.f, 0.f, r->scal));
+        return pack_all(r);
+    }
     TRY(rnn_grad_finalize_launch(ctx, r->segs, r->nseg, r->nseg_blocks, r->pv, r->pg, r->pm,
                                  r->scal, sgd ? 1 : 0));
     // the step changed the weights: their packed copies follow
