@@ -30,15 +30,15 @@ namespace {
 
 constexpr int NT = 256;  // threads per block
 
-__device__ __forceinline__ double wave_sum(double v) {
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 // ------------------------------------------------------------ LayerNorm
 // One wave per row: f64 sums of x and x^2 (norm.rs:56-62), mu, var =
 // max(s2/c - mu^2, 0) as f32, invstd = 1 / sqrt(var + eps) in f32; then
-// xhat = (x - mu) invstd and y = g xhat + b (norm.rs:63-69).
+// xhat = (x - mu) invstd and y = g xhat + b (norm.rs:63-69).  NV > 0: the
+// row's c <= 64 NV values stay in registers (lane l holds columns l, l + 64,
+// ...; every load issued before the sums), the wave sums take a DPP tree;
+// NV = 0: any c, strided loops.
+template <int NV>
 __global__ __launch_bounds__(NT) void ln_fwd_kernel(size_t rows, int c, const float *__restrict__ x,
                                                     const float *__restrict__ g,
                                                     const float *__restrict__ b, float eps,
@@ -48,31 +48,66 @@ __global__ __launch_bounds__(NT) void ln_fwd_kernel(size_t rows, int c, const fl
     const size_t r = (size_t)blockIdx.x * (NT / 64) + wave_index();
     if (r >= rows) return;
     const float *xr = x + r * c;
-    double s = 0.0, s2 = 0.0;
-    for (int j = lane; j < c; j += 64) {
-        const double v = xr[j];
-        s += v;
-        s2 += v * v;
-    }
-    s = wave_sum(s);
-    s2 = wave_sum(s2);
-    const double m = (double)c;
-    const double mu = s / m;
-    const float var = (float)fmax(s2 / m - mu * mu, 0.0);
-    const float inv = 1.0f / sqrtf(var + eps);
-    const float muf = (float)mu;
     float *yr = y + r * c;
     float *hr = xhat ? xhat + r * c : nullptr;
-    for (int j = lane; j < c; j += 64) {
-        const float h = (xr[j] - muf) * inv;
-        if (hr) hr[j] = h;
-        yr[j] = g[j] * h + b[j];
+    const double m = (double)c;
+    if constexpr (NV > 0) {
+        float xv[NV], gv[NV], bv[NV];
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = min(lane + 64 * i, c - 1);
+            xv[i] = xr[j];
+            gv[i] = g[j];
+            bv[i] = b[j];
+        }
+        double s = 0.0, s2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            if (lane + 64 * i < c) {
+                const double v = xv[i];
+                s += v;
+                s2 += v * v;
+            }
+        s = rnn_wave_sum_d(s);
+        s2 = rnn_wave_sum_d(s2);
+        const double mu = s / m;
+        const float var = (float)fmax(s2 / m - mu * mu, 0.0);
+        const float inv = 1.0f / sqrtf(var + eps);
+        const float muf = (float)mu;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = lane + 64 * i;
+            if (j >= c) break;
+            const float h = (xv[i] - muf) * inv;
+            if (hr) hr[j] = h;
+            yr[j] = gv[i] * h + bv[i];
+        }
+        if (invstd && lane == 0) invstd[r] = inv;
+    } else {
+        double s = 0.0, s2 = 0.0;
+        for (int j = lane; j < c; j += 64) {
+            const double v = xr[j];
+            s += v;
+            s2 += v * v;
+        }
+        s = rnn_wave_sum_d(s);
+        s2 = rnn_wave_sum_d(s2);
+        const double mu = s / m;
+        const float var = (float)fmax(s2 / m - mu * mu, 0.0);
+        const float inv = 1.0f / sqrtf(var + eps);
+        const float muf = (float)mu;
+        for (int j = lane; j < c; j += 64) {
+            const float h = (xr[j] - muf) * inv;
+            if (hr) hr[j] = h;
+            yr[j] = g[j] * h + b[j];
+        }
+        if (invstd && lane == 0) invstd[r] = inv;
     }
-    if (invstd && lane == 0) invstd[r] = inv;
 }
 
 // dx per row (norm.rs:121-135): d = dy g; m1 = sum d, m2 = sum d xhat;
-// dx = invstd (d - m1/c - xhat m2/c).
+// dx = invstd (d - m1/c - xhat m2/c).  NV as in the forward.
+template <int NV>
 __global__ __launch_bounds__(NT) void ln_bwd_kernel(size_t rows, int c, const float *__restrict__ dy,
                                                     const float *__restrict__ xhat,
                                                     const float *__restrict__ invstd,
@@ -82,19 +117,46 @@ __global__ __launch_bounds__(NT) void ln_bwd_kernel(size_t rows, int c, const fl
     const size_t r = (size_t)blockIdx.x * (NT / 64) + wave_index();
     if (r >= rows) return;
     const float *dr = dy + r * c, *hr = xhat + r * c;
-    double m1 = 0.0, m2 = 0.0;
-    for (int j = lane; j < c; j += 64) {
-        const float d = dr[j] * g[j];
-        m1 += d;
-        m2 += (double)(d * hr[j]);
-    }
-    const float s1 = (float)wave_sum(m1), s2 = (float)wave_sum(m2);
     const float inv = 1.0f / (float)c;
     const float is = invstd[r];
     float *xr = dx + r * c;
-    for (int j = lane; j < c; j += 64) {
-        const float d = dr[j] * g[j];
-        xr[j] = is * (d - s1 * inv - hr[j] * s2 * inv);
+    if constexpr (NV > 0) {
+        float dv[NV], hv[NV], gv[NV];
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = min(lane + 64 * i, c - 1);
+            dv[i] = dr[j];
+            hv[i] = hr[j];
+            gv[i] = g[j];
+        }
+        double m1 = 0.0, m2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            if (lane + 64 * i < c) {
+                const float d = dv[i] * gv[i];
+                m1 += d;
+                m2 += (double)(d * hv[i]);
+            }
+        const float s1 = (float)rnn_wave_sum_d(m1), s2 = (float)rnn_wave_sum_d(m2);
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = lane + 64 * i;
+            if (j >= c) break;
+            const float d = dv[i] * gv[i];
+            xr[j] = is * (d - s1 * inv - hv[i] * s2 * inv);
+        }
+    } else {
+        double m1 = 0.0, m2 = 0.0;
+        for (int j = lane; j < c; j += 64) {
+            const float d = dr[j] * g[j];
+            m1 += d;
+            m2 += (double)(d * hr[j]);
+        }
+        const float s1 = (float)rnn_wave_sum_d(m1), s2 = (float)rnn_wave_sum_d(m2);
+        for (int j = lane; j < c; j += 64) {
+            const float d = dr[j] * g[j];
+            xr[j] = is * (d - s1 * inv - hr[j] * s2 * inv);
+        }
     }
 }
 
@@ -480,8 +542,22 @@ int rnn_ln_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const fl
     if ((xhat == nullptr) != (invstd == nullptr))
         return rnn_fail(ctx, RNN_E_INVALID, "ln_forward: xhat and invstd go together");
     if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "ln_forward: %zu x %zu", rows, c);
-    ln_fwd_kernel<<<(unsigned)rnn_div_up(rows, NT / 64), NT, 0, ctx->stream>>>(
-        rows, (int)c, x, g, b, eps, y, xhat, invstd);
+    const unsigned grid = (unsigned)rnn_div_up(rows, NT / 64);
+    const int nv = (int)rnn_div_up(c, (size_t)64);
+    auto fwd = [&](auto kern) {
+        kern<<<grid, NT, 0, ctx->stream>>>(rows, (int)c, x, g, b, eps, y, xhat, invstd);
+    };
+    switch (nv) {
+        case 1: fwd(ln_fwd_kernel<1>); break;
+        case 2: fwd(ln_fwd_kernel<2>); break;
+        case 3: fwd(ln_fwd_kernel<3>); break;
+        case 4: fwd(ln_fwd_kernel<4>); break;
+        case 5: fwd(ln_fwd_kernel<5>); break;
+        case 6: fwd(ln_fwd_kernel<6>); break;
+        case 7: fwd(ln_fwd_kernel<7>); break;
+        case 8: fwd(ln_fwd_kernel<8>); break;
+        default: fwd(ln_fwd_kernel<0>); break;
+    }
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -497,8 +573,22 @@ int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const 
     // dgamma += sum dy xhat, dbeta += sum dy (norm.rs:94-119)
     int rc = colsum_add(ctx, rows, (int)c, dy, xhat, dg, db);
     if (rc) return rc;
-    ln_bwd_kernel<<<(unsigned)rnn_div_up(rows, NT / 64), NT, 0, ctx->stream>>>(
-        rows, (int)c, dy, xhat, invstd, g, dx);
+    const unsigned grid = (unsigned)rnn_div_up(rows, NT / 64);
+    const int nv = (int)rnn_div_up(c, (size_t)64);
+    auto bwd = [&](auto kern) {
+        kern<<<grid, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, dx);
+    };
+    switch (nv) {
+        case 1: bwd(ln_bwd_kernel<1>); break;
+        case 2: bwd(ln_bwd_kernel<2>); break;
+        case 3: bwd(ln_bwd_kernel<3>); break;
+        case 4: bwd(ln_bwd_kernel<4>); break;
+        case 5: bwd(ln_bwd_kernel<5>); break;
+        case 6: bwd(ln_bwd_kernel<6>); break;
+        case 7: bwd(ln_bwd_kernel<7>); break;
+        case 8: bwd(ln_bwd_kernel<8>); break;
+        default: bwd(ln_bwd_kernel<0>); break;
+    }
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

@@ -167,6 +167,27 @@ __device__ __forceinline__ int wave_index() {
     return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 
+// v from the lane a DPP pattern names (both 32-bit halves moved).
+template <int CTRL>
+__device__ __forceinline__ double rnn_dpp_d(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_mov_dpp((int)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned)lo);
+}
+// Sum over the 64 lanes of a wave with every lane active, every lane
+// receiving it, in a fixed tree: quads by DPP xor 1 and 2, rows of 8 and 16
+// by DPP mirrors, then xor 16 and 32 across rows.
+__device__ __forceinline__ double rnn_wave_sum_d(double v) {
+    v += rnn_dpp_d<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+    v += rnn_dpp_d<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+    v += rnn_dpp_d<0x141>(v);  // row_half_mirror
+    v += rnn_dpp_d<0x140>(v);  // row_mirror
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
 // Entry points implemented in the kernel sources, called from the C ABI.
 // One batch of the grouped Newton-Schulz GEMMs (rnn_ns_gemm_launch): cnt
 // products C_z = op(A_z) op(B_z) of one shape, [M x K] times [K x N].  The
