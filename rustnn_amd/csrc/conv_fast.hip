@@ -478,7 +478,9 @@ static bool plan_ok(FastPlan &p, int CS, int GA, int GB, FastArgs &a) {
 // per wave when an image has 256 or more positions, else 128 positions (whole
 // images); strided 3x3 forward takes 64 positions with the waves split two
 // ways along output channels, so every wave has a 32x32 block.  A plan that
-// does not fit falls back to shrinking the tile.
+// does not fit falls back to shrinking the tile; a strided 3x3 forward gives
+// up channels per chunk before positions (at 96 source channels, 24-channel
+// chunks with 32 positions ran at half the rate of 8-channel chunks with 64).
 template <int K, int S, int P, bool DX>
 static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs &a) {
     using T = ConvTaps<K, S, P, DX>;
@@ -493,6 +495,7 @@ static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs
     }
     if (GB > 256) return false;
     const int ch = T::KK == 1 ? 32 : std::max(8, std::min(32, (CS / 4 + 7) & ~7));
+    const bool strided = T::KK == 9 && T::IS == 2;
     FastPlan r{};
     r.CH = ch;
     r.NPW = 1;
@@ -504,7 +507,7 @@ static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs
             r.NPW = 2;
             npos = 256;
         }
-    } else if (T::KK == 9 && T::IS == 2) {
+    } else if (strided) {
         npos = 64;
         if (CD > 32) r.WM = 2;
     } else if (T::KK == 1 && T::NCLS == 1 && GA * GB >= 256) {
@@ -526,6 +529,8 @@ static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs
         }
         if (r.IMGS > 1)
             r.IMGS /= 2;
+        else if (strided && r.CH > 8)
+            r.CH = std::max(8, (r.CH / 2) & ~7);
         else if (r.TR > 1)
             r.TR = (r.TR + 1) / 2;
         else if (r.CH > 8)

@@ -30,6 +30,9 @@ SHAPES = [
     # tile of output rows (20 rows in tiles of 12) with 16-byte dY loads
     ("smallc_3x3s1_1to8_20", 3, 1, 8, 3, 1, 1, 20),
     ("smallc_3x3s1_2to40_22_p0", 3, 2, 40, 3, 1, 0, 22),
+    # strided forward whose quarter-of-channels chunk (24) does not fit LDS
+    # at 64 positions: the plan falls back to 8-channel chunks
+    ("tok_3x3s2_96to256_16", 4, 96, 256, 3, 2, 1, 16),
 ]
 
 
