@@ -51,15 +51,6 @@ static inline void tilegeo_finish(TileGeo &t) {
 // LDS words reserved for a staged region: whole 64-word DMA rows.
 static inline size_t dma_region(size_t words) { return (words + 63) & ~(size_t)63; }
 
-typedef __attribute__((address_space(3))) void *lds_ptr_t;
-
-// Buffer resource over [base, base + bytes) with bytes < 2^31: a load at a
-// byte offset >= bytes returns 0 (used for the zero halo of a window).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
-                                             0x00020000);
-}
-constexpr uint32_t DMA_OOB = 0x7FFFFFF0u;
 
 // Asynchronously stages a window with buffer_load_dword ... lds: LDS word L of
 // [0, nch*t.chs) receives source element (n0 + img, c0 + ch, y0 + ty*rowstep,

@@ -3,13 +3,20 @@
 //
 // Reference: gemm.rs (6x16 AVX2 micro-kernel over KC=256 packed panels,
 // parallel over 6-row C panels), linear.rs.  Here one workgroup owns a
-// BM x BN tile of C; its 4 waves each own a (BM/2) x (BN/2) sub-tile made of
-// 32x32 v_mfma_f32_32x32x2f32 accumulators.  A and B are staged through LDS
-// "k-contiguous" (row = m or n, 16 k values + 4 pad floats) so each lane
-// fetches the operands of 4 MFMA steps with one ds_read_b128; the k order
-// inside a 16-wide block is permuted identically for A and B
-// (step s of group g, lane half h  <->  k = 8g + 4h + s).
+// BM x BN tile of C; its 4 compute waves each own a (BM/2) x (BN/2) sub-tile
+// made of 32x32 v_mfma_f32_32x32x2f32 accumulators.  The k order inside a
+// block of 8 is permuted identically for A and B (step s of group g, lane
+// half h  <->  k = 8g + 4h + s), so a k-contiguous operand gives a lane the
+// values of 4 MFMA steps with one ds_read_b128.  Two ways to stage operands:
+//   * gemm_dma_kernel (every operand whose 16-byte quads are whole): 4 more
+//     waves DMA the slabs from HBM straight into a multi-stage LDS ring;
+//   * gemm_kernel (any shape and alignment): the 4 waves load a slab into
+//     registers and store it k-contiguous (16 k values + 4 pad floats a row)
+//     into a double-buffered LDS tile.
 #include "rnn_internal.h"
+
+#include <algorithm>
+#include <cstdlib>
 
 namespace {
 
@@ -164,6 +171,215 @@ struct GemmTile {
                       acc[i][j][v]);
     }
 };
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS variant.  Operand slabs go from HBM straight into an NS-stage
+// LDS ring by buffer_load_dwordx4 ... lds (16 bytes per lane, no registers,
+// no LDS writes by the waves); stage it + NS - 1 is in flight while stage it
+// is multiplied.  Each operand keeps the layout it has in memory:
+//   * k-contiguous (A [m][k], B^T [n][k]): [row][BK] with the 16-byte quad q
+//     of row r at position q ^ kswz(r), so the ds_read_b128 of 8 (or 16)
+//     consecutive rows at one quad hit distinct banks;
+//   * row-contiguous (A^T [k][m], B [k][n]): [BK][rows] as stored, read one
+//     float per MFMA step (32 consecutive floats per half-wave).
+// k order inside a stage matches the register-staged kernel: step s of
+// group g, lane half h <-> k = 8g + 4h + s.  Eligible when every 16-byte quad
+// is either wholly inside the operand or wholly outside (rows and k multiples
+// of 4 where they run along a quad, 16-byte aligned bases): a quad outside
+// the k range reads zero through an out-of-range offset; rows beyond M / N
+// only feed C rows / columns that are never stored.
+
+// s_waitcnt with vmcnt <= N, other counters not waited on (vmcnt bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Quad position swizzle of a k-contiguous row: conflict-free b128 reads for
+// both 8-lane (32-bank) and 16-lane (64-bank) LDS read phases.
+template <int BK>
+__device__ __forceinline__ int kswz(int r) {
+    if constexpr (BK == 32)
+        return (r ^ (r >> 3)) & 7;
+    else
+        return ((r >> 1) ^ (r >> 2)) & 3;
+}
+
+template <int R, int BK, bool KMAJOR>
+struct DmaOperand {
+    static constexpr int WORDS = R * BK;             // LDS floats per stage
+    static constexpr int PER = WORDS / 4 / 256;      // dwordx4 DMAs per thread
+    static_assert(WORDS % 1024 == 0, "whole DMA rows");
+
+    // Issues this thread's DMAs of rows r0.. (KMAJOR) or columns r0.. of
+    // k values k0 .. k0 + BK (of kz) into lds.
+    __device__ __forceinline__ static void issue(__amdgpu_buffer_rsrc_t rs, int ld, int rows,
+                                                 int r0, int k0, int kz, float *lds, int wave,
+                                                 int lane) {
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int c0 = (u * 4 + wave) * 64;  // first quad of this wave instruction
+            const int j = c0 + lane;
+            uint32_t off;
+            if (KMAJOR) {
+                constexpr int QPR = BK / 4;
+                const int r = j / QPR, q = (j % QPR) ^ kswz<BK>(r);
+                const int row = r0 + r, k = k0 + 4 * q;
+                off = (row < rows && k < kz) ? (uint32_t)(row * ld + k) * 4u : DMA_OOB;
+            } else {
+                constexpr int QPR = R / 4;
+                const int kr = j / QPR, col = r0 + (j % QPR) * 4, k = k0 + kr;
+                off = (k < kz && col < rows) ? (uint32_t)(k * ld + col) * 4u : DMA_OOB;
+            }
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(lds + 4 * c0), 16, off, 0, 0,
+                                                     0);
+        }
+    }
+
+    // The operand values of MFMA steps 0..3 of group g for tile row (or
+    // column) `row` and lane half h.
+    __device__ __forceinline__ static f32x4 frag(const float *lds, int row, int g, int h) {
+        if (KMAJOR) {
+            const int q = (2 * g + h) ^ kswz<BK>(row);
+            return *reinterpret_cast<const f32x4 *>(lds + row * BK + 4 * q);
+        } else {
+            const float *p = lds + (8 * g + 4 * h) * R + row;
+            f32x4 v;
+            v[0] = p[0];
+            v[1] = p[R];
+            v[2] = p[2 * R];
+            v[3] = p[3 * R];
+            return v;
+        }
+    }
+};
+
+// Waves 0..3 multiply (a 2 x 2 grid of (BM/2) x (BN/2) sub-tiles); waves
+// 4..7 only issue the DMAs, a whole stage at a time, so the compute waves
+// never wait on the memory pipeline.  One barrier per stage: when it
+// completes, stage it has landed (each producer waited for its own DMAs) and
+// every compute wave is done with stage it - 1, whose buffer the producers
+// then refill with stage it + NS - 1.  A wave with a single 32 x 32 block
+// alternates two accumulators so that consecutive MFMAs are independent.
+template <int BM, int BN, int BK, int NS, bool AT, bool BT>
+__global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
+    extern __shared__ float lds[];
+    using OA = DmaOperand<BM, BK, !AT>;
+    using OB = DmaOperand<BN, BK, BT>;
+    constexpr int STAGE = OA::WORDS + OB::WORDS;
+    constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
+    constexpr int NACC = TM * TN == 1 ? 2 : 1;
+    const long long z = blockIdx.z;
+    const int kz = min(g.kchunk, g.ktotal - (int)z * g.kchunk);
+    // XCD-aware tile order, as in gemm_kernel
+    const int gx = gridDim.x, T = gx * gridDim.y;
+    const int L = blockIdx.y * gx + blockIdx.x;
+    const int per = T >> 3, rem = T & 7, xcd = L & 7, loc = L >> 3;
+    const int tl = xcd < rem ? xcd * (per + 1) + loc : rem * (per + 1) + (xcd - rem) * per + loc;
+    const int m0 = (tl / gx) * BM, n0 = (tl % gx) * BN;
+    const int lane = threadIdx.x & 63, wave = wave_index();
+    const int nk = (kz + BK - 1) / BK;
+
+    if (wave >= 4) {
+        // producer: operand extents from this problem's base (below 2^31
+        // bytes, checked by the host)
+        const int pw = wave - 4;
+        const float *A = g.a + z * g.stride_a;
+        const float *B = g.b + z * g.stride_b;
+        const uint32_t abytes =
+            (uint32_t)((AT ? (long long)kz * g.lda : (long long)g.M * g.lda) * 4);
+        const uint32_t bbytes =
+            (uint32_t)((BT ? (long long)g.N * g.ldb : (long long)kz * g.ldb) * 4);
+        const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, abytes), rb = make_rsrc(B, bbytes);
+        auto issue = [&](int st) {
+            float *buf = lds + (st % NS) * STAGE;
+            OA::issue(ra, g.lda, g.M, m0, st * BK, kz, buf, pw, lane);
+            OB::issue(rb, g.ldb, g.N, n0, st * BK, kz, buf + OA::WORDS, pw, lane);
+        };
+#pragma unroll
+        for (int st = 0; st < NS - 1; st++)
+            if (st < nk) issue(st);
+        for (int it = 0; it < nk; it++) {
+            if (it + NS - 2 < nk)
+                wait_vmcnt<(NS - 2) * (OA::PER + OB::PER)>();
+            else
+                wait_vmcnt<0>();
+            // a bare barrier: __syncthreads()'s release fence would also wait
+            // for the DMAs of the later stages still in flight
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (it + NS - 1 < nk) issue(it + NS - 1);
+        }
+        return;
+    }
+
+    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+    f32x16 acc[TM][TN][NACC];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int a = 0; a < NACC; a++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[i][j][a][v] = 0.f;
+    for (int it = 0; it < nk; it++) {
+        __syncthreads();
+        const float *As = lds + (it % NS) * STAGE, *Bs = As + OA::WORDS;
+        f32x4 af[TM], bf[TN];
+#pragma unroll
+        for (int i = 0; i < TM; i++) af[i] = OA::frag(As, wm * WTM + i * 32 + lr, 0, lh);
+#pragma unroll
+        for (int j = 0; j < TN; j++) bf[j] = OB::frag(Bs, wn * WTN + j * 32 + lr, 0, lh);
+#pragma unroll
+        for (int gk = 0; gk < BK / 8; gk++) {
+            f32x4 an[TM], bn[TN];
+            if (gk + 1 < BK / 8) {
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    an[i] = OA::frag(As, wm * WTM + i * 32 + lr, gk + 1, lh);
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    bn[j] = OB::frag(Bs, wn * WTN + j * 32 + lr, gk + 1, lh);
+            }
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        acc[i][j][s % NACC] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                            af[i][s], bf[j][s], acc[i][j][s % NACC], 0, 0, 0);
+            if (gk + 1 < BK / 8) {
+#pragma unroll
+                for (int i = 0; i < TM; i++) af[i] = an[i];
+#pragma unroll
+                for (int j = 0; j < TN; j++) bf[j] = bn[j];
+            }
+        }
+    }
+    float *Cp = g.c + z * g.stride_c;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int row = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                const int col = n0 + wn * WTN + j * 32 + lr;
+                if (row < g.M && col < g.N) {
+                    float val = acc[i][j][0][v];
+                    if (NACC == 2) val += acc[i][j][NACC - 1][v];
+                    if (g.bias) val += g.bias[col];
+                    float *cp = Cp + (long long)row * g.ldc + col;
+                    if (g.acc) val = *cp + val;
+                    *cp = val;
+                }
+            }
+}
 
 template <int BM, int BN, bool AT, bool BT, bool VEC>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
@@ -329,6 +545,30 @@ int launch_t(rnn_ctx *ctx, const GemmArgs &g, int count, bool vec) {
     return RNN_OK;
 }
 
+template <int BM, int BN, int BK, int NS, bool AT, bool BT>
+int launch_dma_t(rnn_ctx *ctx, const GemmArgs &g, int count) {
+    constexpr size_t lds = (size_t)NS * (BM + BN) * BK * 4;
+    static bool attr = false;
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute((const void *)gemm_dma_kernel<BM, BN, BK, NS, AT, BT>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    }
+    dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM, count);
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, AT, BT>), grid, dim3(512), lds,
+                       ctx->stream, g);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+template <int BM, int BN, int BK, int NS>
+int launch_dma_bm(rnn_ctx *ctx, const GemmArgs &g, int count, bool at, bool bt) {
+    if (!at && !bt) return launch_dma_t<BM, BN, BK, NS, false, false>(ctx, g, count);
+    if (!at && bt) return launch_dma_t<BM, BN, BK, NS, false, true>(ctx, g, count);
+    if (at && !bt) return launch_dma_t<BM, BN, BK, NS, true, false>(ctx, g, count);
+    return launch_dma_t<BM, BN, BK, NS, true, true>(ctx, g, count);
+}
+
 template <int BM, int BN>
 int launch_bm(rnn_ctx *ctx, const GemmArgs &g, int count, bool at, bool bt, bool vec) {
     if (!at && !bt) return launch_t<BM, BN, false, false>(ctx, g, count, vec);
@@ -340,6 +580,27 @@ int launch_bm(rnn_ctx *ctx, const GemmArgs &g, int count, bool at, bool bt, bool
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
+
+// Whether every operand quad of the direct-to-LDS kernel is wholly inside or
+// wholly outside its operand, and every problem's operand spans under 2^31
+// bytes (buffer offsets).
+static bool dma_ok(size_t count, size_t m, size_t n, size_t kchunk, size_t ktotal, const float *a,
+                   size_t stride_a, int lda, int at, const float *b, size_t stride_b, int ldb,
+                   int bt) {
+    const size_t lim = 0x7FFF0000u / 4;
+    const size_t kz = std::min(kchunk, ktotal);
+    auto aligned = [](const void *p, size_t stride, int ld) {
+        return ((uintptr_t)p & 15) == 0 && stride % 4 == 0 && ld % 4 == 0;
+    };
+    if (!aligned(a, stride_a, lda) || !aligned(b, stride_b, ldb)) return false;
+    // quads run along k for k-contiguous operands, along m / n otherwise
+    if ((!at || bt) && (kchunk % 4 || ktotal % 4)) return false;
+    if (at && m % 4) return false;
+    if (!bt && n % 4) return false;
+    const size_t ea = at ? kz * (size_t)lda : m * (size_t)lda;
+    const size_t eb = bt ? n * (size_t)ldb : kz * (size_t)ldb;
+    return ea < lim && eb < lim;
+}
 
 // Enqueues `count` GEMMs C_z = op(A_z) op(B_z) (+C_z) (+bias) with problem z
 // covering k = min(kchunk, ktotal - z*kchunk) (kchunk = k for plain batches).
@@ -370,8 +631,18 @@ static int gemm_enqueue(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k
     if (!at) vec = vec && aligned16(a) && (lda % 4 == 0) && (stride_a % 4 == 0);
     if (bt) vec = vec && aligned16(b) && (ldb % 4 == 0) && (stride_b % 4 == 0);
     size_t tiles128 = rnn_div_up(m, 128) * rnn_div_up(n, 128) * count;
-    if (m >= 128 && n >= 128 && tiles128 >= (size_t)ctx->num_cus)
-        return launch_bm<128, 128>(ctx, g, (int)count, at, bt, vec);
+    static const bool no_dma = getenv("RNN_GEMM_NODMA") != nullptr;
+    if (!no_dma && dma_ok(count, m, n, kchunk, ktotal, a, stride_a, lda, at, b, stride_b, ldb, bt)) {
+        // 128 x 128 tiles only from four tiles per CU: below that the 64 x 64
+        // grid's extra workgroups hide more latency than the larger tile's
+        // operand reuse saves (measured on MI355X: 8192x768x256 99 vs 79
+        // TFLOP/s, 4096^3 124 vs 136)
+        if (m >= 128 && n >= 128 && tiles128 >= 4 * (size_t)ctx->num_cus)
+            return launch_dma_bm<128, 128, 16, 4>(ctx, g, (int)count, at, bt);
+        return launch_dma_bm<64, 64, 32, 3>(ctx, g, (int)count, at, bt);
+    }
+    const bool big = m >= 128 && n >= 128 && tiles128 >= (size_t)ctx->num_cus;
+    if (big) return launch_bm<128, 128>(ctx, g, (int)count, at, bt, vec);
     return launch_bm<64, 64>(ctx, g, (int)count, at, bt, vec);
 }
 

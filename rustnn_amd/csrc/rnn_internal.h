@@ -161,6 +161,16 @@ static inline size_t rnn_round_up(size_t a, size_t b) { return rnn_div_up(a, b) 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+
+// Buffer resource over [base, base + bytes) with bytes < 2^31: a load at a
+// byte offset >= bytes returns 0 (used for zero halos and tile edges).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+constexpr uint32_t DMA_OOB = 0x7FFFFFF0u;
+
 // Index of the calling wave in its workgroup, as a wave-uniform (scalar)
 // value: loops and branches on it stay scalar instead of exec-masked.
 __device__ __forceinline__ int wave_index() {
