@@ -345,6 +345,8 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
                 for (int j = 0; j < TN; j++)
                     bn[j] = OB::frag(Bs, wn * WTN + j * 32 + lr, gk + 1, lh);
             }
+            // keep the next group's reads ahead of this group's MFMAs
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int s = 0; s < 4; s++)
 #pragma unroll
