@@ -32,6 +32,11 @@ struct GemmArgs {
     int kchunk, ktotal;    // problem z covers k = min(kchunk, ktotal - z*kchunk)
     int lda, ldb, ldc;
     int acc;               // C += result
+    // Row sums of op(A) over this problem's k (gemm_dma_kernel with RS):
+    // added into rsum_out[m] (one problem), or stored as f64 partials
+    // rsum_part[z * M + m] (split-K problems, reduced in z order).
+    float *rsum_out;
+    double *rsum_part;
 };
 
 // 4 consecutive elements starting at p[0], p[step], ... with bounds
@@ -263,7 +268,7 @@ struct DmaOperand {
 // every compute wave is done with stage it - 1, whose buffer the producers
 // then refill with stage it + NS - 1.  A wave with a single 32 x 32 block
 // alternates two accumulators so that consecutive MFMAs are independent.
-template <int BM, int BN, int BK, int NS, bool AT, bool BT>
+template <int BM, int BN, int BK, int NS, bool AT, bool BT, bool RS>
 __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
     extern __shared__ float lds[];
     using OA = DmaOperand<BM, BK, !AT>;
@@ -317,6 +322,13 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
     }
 
     const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+    // RS: the compute waves of the first column tile also sum the A values
+    // they multiply, in f64: lane (lr, lh) of fragment i adds those of row
+    // wm*WTM + 32i + lr at k = 8g + 4lh + s, stage by stage in k order.
+    const bool rsum = RS && n0 == 0 && wn == 0;
+    double rs[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++) rs[i] = 0.0;
     f32x16 acc[TM][TN][NACC];
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -347,6 +359,12 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
             }
             // keep the next group's reads ahead of this group's MFMAs
             __builtin_amdgcn_sched_barrier(0);
+            if (rsum) {
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int s = 0; s < 4; s++) rs[i] += (double)af[i][s];
+            }
 #pragma unroll
             for (int s = 0; s < 4; s++)
 #pragma unroll
@@ -360,6 +378,21 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
                 for (int i = 0; i < TM; i++) af[i] = an[i];
 #pragma unroll
                 for (int j = 0; j < TN; j++) bf[j] = bn[j];
+            }
+        }
+    }
+    if (rsum) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            // the two lane halves' sums, added in half order on both halves
+            const double o = __shfl_xor(rs[i], 32, 64);
+            const double t = lh == 0 ? rs[i] + o : o + rs[i];
+            const int row = m0 + wm * WTM + i * 32 + lr;
+            if (lh == 0 && row < g.M) {
+                if (g.rsum_part)
+                    g.rsum_part[z * g.M + row] = t;
+                else
+                    g.rsum_out[row] += (float)t;
             }
         }
     }
@@ -487,9 +520,17 @@ __global__ void fill_kernel(float *p, long long n, float v) {
 // out[e] (+)= sum_z part[z*len + e], z in order (deterministic split-K
 // reduce).  Loads go out 8 at a time ahead of the in-order adds.
 __global__ void splitk_reduce_kernel(const float *part, int nz, long long len, float *out,
-                                     int accumulate) {
+                                     int accumulate, const double *rpart, int rlen, float *rout) {
     long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= len) return;
+    if (e >= len) {
+        // the split-K row sums of op(A): rout[m] += sum_z rpart[z][m], z in order
+        const long long m = e - len;
+        if (!rpart || m >= rlen) return;
+        double t = 0.0;
+        for (int z = 0; z < nz; z++) t += rpart[(long long)z * rlen + m];
+        rout[m] += (float)t;
+        return;
+    }
     float s = 0.f;
     for (int z0 = 0; z0 < nz; z0 += 8) {
         float v[8];
@@ -547,28 +588,33 @@ int launch_t(rnn_ctx *ctx, const GemmArgs &g, int count, bool vec) {
     return RNN_OK;
 }
 
-template <int BM, int BN, int BK, int NS, bool AT, bool BT>
+template <int BM, int BN, int BK, int NS, bool AT, bool BT, bool RS>
 int launch_dma_t(rnn_ctx *ctx, const GemmArgs &g, int count) {
     constexpr size_t lds = (size_t)NS * (BM + BN) * BK * 4;
     static bool attr = false;
     if (!attr) {
         attr = true;
-        (void)hipFuncSetAttribute((const void *)gemm_dma_kernel<BM, BN, BK, NS, AT, BT>,
+        (void)hipFuncSetAttribute((const void *)gemm_dma_kernel<BM, BN, BK, NS, AT, BT, RS>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     }
     dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM, count);
-    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, AT, BT>), grid, dim3(512), lds,
+    hipLaunchKernelGGL((gemm_dma_kernel<BM, BN, BK, NS, AT, BT, RS>), grid, dim3(512), lds,
                        ctx->stream, g);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
 
+// The row sums of op(A) ride along only in the weight-gradient layout (A^T B).
 template <int BM, int BN, int BK, int NS>
 int launch_dma_bm(rnn_ctx *ctx, const GemmArgs &g, int count, bool at, bool bt) {
-    if (!at && !bt) return launch_dma_t<BM, BN, BK, NS, false, false>(ctx, g, count);
-    if (!at && bt) return launch_dma_t<BM, BN, BK, NS, false, true>(ctx, g, count);
-    if (at && !bt) return launch_dma_t<BM, BN, BK, NS, true, false>(ctx, g, count);
-    return launch_dma_t<BM, BN, BK, NS, true, true>(ctx, g, count);
+    if (g.rsum_out || g.rsum_part) {
+        if (!at || bt) return rnn_fail(ctx, RNN_E_INVALID, "gemm: row sums need the A^T B layout");
+        return launch_dma_t<BM, BN, BK, NS, true, false, true>(ctx, g, count);
+    }
+    if (!at && !bt) return launch_dma_t<BM, BN, BK, NS, false, false, false>(ctx, g, count);
+    if (!at && bt) return launch_dma_t<BM, BN, BK, NS, false, true, false>(ctx, g, count);
+    if (at && !bt) return launch_dma_t<BM, BN, BK, NS, true, false, false>(ctx, g, count);
+    return launch_dma_t<BM, BN, BK, NS, true, true, false>(ctx, g, count);
 }
 
 template <int BM, int BN>
@@ -606,10 +652,24 @@ static bool dma_ok(size_t count, size_t m, size_t n, size_t kchunk, size_t ktota
 
 // Enqueues `count` GEMMs C_z = op(A_z) op(B_z) (+C_z) (+bias) with problem z
 // covering k = min(kchunk, ktotal - z*kchunk) (kchunk = k for plain batches).
+static bool dma_enabled() {
+    static const bool on = getenv("RNN_GEMM_NODMA") == nullptr;
+    return on;
+}
+
+// Whether C += A^T B (A [k x m], B [k x n]) takes the direct-to-LDS kernel,
+// which can then also sum A's columns (the row sums of A^T).
+static bool dw_rowsum_ok(size_t m, size_t n, size_t k, const float *a, const float *b) {
+    return dma_enabled() && dma_ok(1, m, n, k, k, a, 0, (int)m, 1, b, 0, (int)n, 0);
+}
+
+// rs_out / rs_part: the row sums of op(A) (A^T B layout and the direct-to-LDS
+// kernel only; the caller checks dw_rowsum_ok).
 static int gemm_enqueue(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t kchunk,
                         size_t ktotal, const float *a, size_t stride_a, int lda, int at,
                         const float *b, size_t stride_b, int ldb, int bt, float *c,
-                        size_t stride_c, int ldc, int acc, const float *bias) {
+                        size_t stride_c, int ldc, int acc, const float *bias,
+                        float *rs_out = nullptr, double *rs_part = nullptr) {
     if (m > INT32_MAX || n > INT32_MAX || ktotal > INT32_MAX || count > 65535)
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "gemm: dimension beyond 32-bit tile indexing");
     GemmArgs g;
@@ -628,13 +688,15 @@ static int gemm_enqueue(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k
     g.ldb = ldb;
     g.ldc = ldc;
     g.acc = acc;
+    g.rsum_out = rs_out;
+    g.rsum_part = rs_part;
     // float4 loads along k need 16-byte aligned rows of the k-contiguous operands.
     bool vec = true;
     if (!at) vec = vec && aligned16(a) && (lda % 4 == 0) && (stride_a % 4 == 0);
     if (bt) vec = vec && aligned16(b) && (ldb % 4 == 0) && (stride_b % 4 == 0);
     size_t tiles128 = rnn_div_up(m, 128) * rnn_div_up(n, 128) * count;
-    static const bool no_dma = getenv("RNN_GEMM_NODMA") != nullptr;
-    if (!no_dma && dma_ok(count, m, n, kchunk, ktotal, a, stride_a, lda, at, b, stride_b, ldb, bt)) {
+    if (dma_enabled() &&
+        dma_ok(count, m, n, kchunk, ktotal, a, stride_a, lda, at, b, stride_b, ldb, bt)) {
         // 128 x 128 tiles only from four tiles per CU: below that the 64 x 64
         // grid's extra workgroups hide more latency than the larger tile's
         // operand reuse saves (measured on MI355X: 8192x768x256 99 vs 79
@@ -643,6 +705,7 @@ static int gemm_enqueue(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k
             return launch_dma_bm<128, 128, 16, 4>(ctx, g, (int)count, at, bt);
         return launch_dma_bm<64, 64, 32, 3>(ctx, g, (int)count, at, bt);
     }
+    if (rs_out || rs_part) return rnn_fail(ctx, RNN_E_INVALID, "gemm: row sums need the DMA path");
     const bool big = m >= 128 && n >= 128 && tiles128 >= (size_t)ctx->num_cus;
     if (big) return launch_bm<128, 128>(ctx, g, (int)count, at, bt, vec);
     return launch_bm<64, 64>(ctx, g, (int)count, at, bt, vec);
@@ -698,7 +761,7 @@ int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, fl
 // the C tiles alone cannot fill the chip; the chunk partials are added into C
 // in chunk order (deterministic).  Returns -1 when splitting does not pay.
 static int gemm_splitk(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, int at,
-                       const float *b, int bt, float *c, int acc) {
+                       const float *b, int bt, float *c, int acc, float *rsum = nullptr) {
     const size_t tiles = rnn_div_up(m, 64) * rnn_div_up(n, 64);
     if (tiles >= (size_t)ctx->num_cus || k < 1024) return -1;
     // about three workgroups per CU, each over at least 512 values of k
@@ -708,16 +771,19 @@ static int gemm_splitk(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *
     if (nz <= 1) return -1;
     const size_t kchunk = rnn_round_up(rnn_div_up(k, nz), 16);
     nz = rnn_div_up(k, kchunk);
-    float *part = (float *)rnn_workspace(ctx, nz * m * n * sizeof(float));
+    const size_t pbytes = rnn_round_up(nz * m * n * sizeof(float), 256);
+    float *part = (float *)rnn_workspace(ctx, pbytes + (rsum ? nz * m * sizeof(double) : 0));
     if (!part) return RNN_E_NOMEM;
+    double *rpart = rsum ? (double *)((char *)part + pbytes) : nullptr;
     // chunk z of A: rows z*kchunk of [k x m] (at) or columns z*kchunk of [m x k]
     const size_t sa = at ? kchunk * m : kchunk, sb = bt ? kchunk : kchunk * n;
     const int lda = at ? (int)m : (int)k, ldb = bt ? (int)k : (int)n;
     int rc = gemm_enqueue(ctx, nz, m, n, kchunk, k, a, sa, lda, at, b, sb, ldb, bt, part, m * n,
-                          (int)n, 0, nullptr);
+                          (int)n, 0, nullptr, nullptr, rpart);
     if (rc) return rc;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rnn_div_up(m * n, 256)), dim3(256), 0,
-                       ctx->stream, part, (int)nz, (long long)(m * n), c, acc);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rnn_div_up(m * n + (rsum ? m : 0), 256)),
+                       dim3(256), 0, ctx->stream, part, (int)nz, (long long)(m * n), c, acc,
+                       (const double *)rpart, (int)m, rsum);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -789,12 +855,23 @@ int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, cons
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     if (!dy || !x || !w || !dw || !dx)
         return rnn_fail(ctx, RNN_E_NULL, "linear_backward: null operand");
-    // dW[fout, fin] += dY^T X (linear.rs:69)
-    int rc = rnn_matmul_dw(ctx, fout, fin, rows, dy, x, dw);
-    if (rc) return rc;
-    if (db && rows && fout) {
-        rc = rnn_colsum_launch(ctx, rows, fout, dy, db);  // linear.rs:70-89
+    // dW[fout, fin] += dY^T X (linear.rs:69); db += the column sums of dY
+    // (linear.rs:70-89), summed in f64 by the dW GEMM itself when it takes
+    // the direct-to-LDS kernel, else by the column-sum kernels
+    int rc;
+    if (db && rows && fout && fin && dw_rowsum_ok(fout, fin, rows, dy, x)) {
+        rc = gemm_splitk(ctx, fout, fin, rows, dy, 1, x, 0, dw, 1, db);
+        if (rc == -1)
+            rc = gemm_enqueue(ctx, 1, fout, fin, rows, rows, dy, 0, (int)fout, 1, x, 0, (int)fin,
+                              0, dw, 0, (int)fin, 1, nullptr, db, nullptr);
         if (rc) return rc;
+    } else {
+        rc = rnn_matmul_dw(ctx, fout, fin, rows, dy, x, dw);
+        if (rc) return rc;
+        if (db && rows && fout) {
+            rc = rnn_colsum_launch(ctx, rows, fout, dy, db);
+            if (rc) return rc;
+        }
     }
     // dX[rows, fin] = dY W (linear.rs:91-94)
     return rnn_matmul(ctx, rows, fin, fout, dy, 0, w, 0, dx, 0);

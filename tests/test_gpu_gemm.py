@@ -137,8 +137,13 @@ def test_matmul_dw_integer_exact(rnn, orc):
     assert np.array_equal(to_host(c), want)
 
 
+# db is summed by the dW GEMM itself on its direct-to-LDS path (fout and fin
+# multiples of 4): split-K (8192 rows; 4096 rows with a partial last row
+# tile), one launch (27 rows), 128 x 128 tiles (4096 x 4096); fout = 30 takes
+# the column-sum kernels.
 @pytest.mark.parametrize("rows,fin,fout,bias", [(8192, 256, 768, True), (27, 8, 24, True),
-                                                 (64, 384, 1024, False)])
+                                                 (64, 384, 1024, False), (4096, 36, 100, True),
+                                                 (64, 4096, 4096, True), (100, 64, 30, True)])
 def test_linear(rnn, orc, rows, fin, fout, bias):
     rng = orc.Rng(21)
     x, w = rng.rand_vec(rows * fin), rng.rand_vec(fout * fin) * np.float32(0.02)
