@@ -261,6 +261,7 @@ struct DmaOperand {
     }
 };
 
+// One BM x BN tile of C = op(A) op(B) over kz values of k by 8 waves.
 // Waves 0..3 multiply (a 2 x 2 grid of (BM/2) x (BN/2) sub-tiles); waves
 // 4..7 only issue the DMAs, a whole stage at a time, so the compute waves
 // never wait on the memory pipeline.  One barrier per stage: when it
@@ -268,14 +269,135 @@ struct DmaOperand {
 // every compute wave is done with stage it - 1, whose buffer the producers
 // then refill with stage it + NS - 1.  A wave with a single 32 x 32 block
 // alternates two accumulators so that consecutive MFMAs are independent.
+template <int BM, int BN, int BK, int NS, bool AT, bool BT>
+struct DmaTile {
+    using OA = DmaOperand<BM, BK, !AT>;
+    using OB = DmaOperand<BN, BK, BT>;
+    static constexpr int STAGE = OA::WORDS + OB::WORDS;
+    static constexpr size_t LDS_BYTES = (size_t)NS * STAGE * 4;
+    static constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
+    static constexpr int NACC = TM * TN == 1 ? 2 : 1;
+    f32x16 acc[TM][TN][NACC];
+    // With rsum, the f64 sums of the A values this lane multiplies: row
+    // wm*WTM + 32i + lr at k = 8g + 4lh + s, stage by stage in k order.
+    double rs[TM];
+
+    // Producer waves return false once their last DMA is issued; compute
+    // waves return true with the tile in acc.  A, B: this problem's operands
+    // (extents below 2^31 bytes, checked by the host).
+    __device__ __forceinline__ bool run(const float *A, int lda, int M, const float *B, int ldb,
+                                        int N, int kz, int m0, int n0, bool rsum, float *lds) {
+        const int lane = threadIdx.x & 63, wave = wave_index();
+        const int nk = (kz + BK - 1) / BK;
+        if (wave >= 4) {
+            const int pw = wave - 4;
+            const uint32_t abytes = (uint32_t)((AT ? (long long)kz * lda : (long long)M * lda) * 4);
+            const uint32_t bbytes = (uint32_t)((BT ? (long long)N * ldb : (long long)kz * ldb) * 4);
+            const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, abytes), rb = make_rsrc(B, bbytes);
+            auto issue = [&](int st) {
+                float *buf = lds + (st % NS) * STAGE;
+                OA::issue(ra, lda, M, m0, st * BK, kz, buf, pw, lane);
+                OB::issue(rb, ldb, N, n0, st * BK, kz, buf + OA::WORDS, pw, lane);
+            };
+#pragma unroll
+            for (int st = 0; st < NS - 1; st++)
+                if (st < nk) issue(st);
+            for (int it = 0; it < nk; it++) {
+                if (it + NS - 2 < nk)
+                    wait_vmcnt<(NS - 2) * (OA::PER + OB::PER)>();
+                else
+                    wait_vmcnt<0>();
+                // a bare barrier: __syncthreads()'s release fence would also
+                // wait for the DMAs of the later stages still in flight
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                if (it + NS - 1 < nk) issue(it + NS - 1);
+            }
+            return false;
+        }
+        const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+#pragma unroll
+        for (int i = 0; i < TM; i++) rs[i] = 0.0;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int a = 0; a < NACC; a++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[i][j][a][v] = 0.f;
+        for (int it = 0; it < nk; it++) {
+            __syncthreads();
+            const float *As = lds + (it % NS) * STAGE, *Bs = As + OA::WORDS;
+            f32x4 af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) af[i] = OA::frag(As, wm * WTM + i * 32 + lr, 0, lh);
+#pragma unroll
+            for (int j = 0; j < TN; j++) bf[j] = OB::frag(Bs, wn * WTN + j * 32 + lr, 0, lh);
+#pragma unroll
+            for (int gk = 0; gk < BK / 8; gk++) {
+                f32x4 an[TM], bn[TN];
+                if (gk + 1 < BK / 8) {
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+                        an[i] = OA::frag(As, wm * WTM + i * 32 + lr, gk + 1, lh);
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        bn[j] = OB::frag(Bs, wn * WTN + j * 32 + lr, gk + 1, lh);
+                }
+                // keep the next group's reads ahead of this group's MFMAs
+                __builtin_amdgcn_sched_barrier(0);
+                if (rsum) {
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int s = 0; s < 4; s++) rs[i] += (double)af[i][s];
+                }
+#pragma unroll
+                for (int s = 0; s < 4; s++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int j = 0; j < TN; j++)
+                            acc[i][j][s % NACC] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                                af[i][s], bf[j][s], acc[i][j][s % NACC], 0, 0, 0);
+                if (gk + 1 < BK / 8) {
+#pragma unroll
+                    for (int i = 0; i < TM; i++) af[i] = an[i];
+#pragma unroll
+                    for (int j = 0; j < TN; j++) bf[j] = bn[j];
+                }
+            }
+        }
+        return true;
+    }
+
+    // f(r, c, v) for each element of the tile this compute lane holds (tile
+    // row r = wm*WTM + 32i + 8(v/4) + 4(lane/32) + v%4, column wn*WTN + 32j +
+    // lane%32: the 32x32 MFMA accumulator layout).
+    template <typename F>
+    __device__ __forceinline__ void each(F f) const {
+        const int lane = threadIdx.x & 63, wave = wave_index();
+        const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    float val = acc[i][j][0][v];
+                    if (NACC == 2) val += acc[i][j][NACC - 1][v];
+                    f(wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3), wn * WTN + j * 32 + lr,
+                      val);
+                }
+    }
+};
+
 template <int BM, int BN, int BK, int NS, bool AT, bool BT, bool RS>
 __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
     extern __shared__ float lds[];
-    using OA = DmaOperand<BM, BK, !AT>;
-    using OB = DmaOperand<BN, BK, BT>;
-    constexpr int STAGE = OA::WORDS + OB::WORDS;
-    constexpr int WTM = BM / 2, WTN = BN / 2, TM = WTM / 32, TN = WTN / 32;
-    constexpr int NACC = TM * TN == 1 ? 2 : 1;
+    using Tile = DmaTile<BM, BN, BK, NS, AT, BT>;
     const long long z = blockIdx.z;
     const int kz = min(g.kchunk, g.ktotal - (int)z * g.kchunk);
     // XCD-aware tile order, as in gemm_kernel
@@ -284,136 +406,38 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
     const int per = T >> 3, rem = T & 7, xcd = L & 7, loc = L >> 3;
     const int tl = xcd < rem ? xcd * (per + 1) + loc : rem * (per + 1) + (xcd - rem) * per + loc;
     const int m0 = (tl / gx) * BM, n0 = (tl % gx) * BN;
-    const int lane = threadIdx.x & 63, wave = wave_index();
-    const int nk = (kz + BK - 1) / BK;
-
-    if (wave >= 4) {
-        // producer: operand extents from this problem's base (below 2^31
-        // bytes, checked by the host)
-        const int pw = wave - 4;
-        const float *A = g.a + z * g.stride_a;
-        const float *B = g.b + z * g.stride_b;
-        const uint32_t abytes =
-            (uint32_t)((AT ? (long long)kz * g.lda : (long long)g.M * g.lda) * 4);
-        const uint32_t bbytes =
-            (uint32_t)((BT ? (long long)g.N * g.ldb : (long long)kz * g.ldb) * 4);
-        const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, abytes), rb = make_rsrc(B, bbytes);
-        auto issue = [&](int st) {
-            float *buf = lds + (st % NS) * STAGE;
-            OA::issue(ra, g.lda, g.M, m0, st * BK, kz, buf, pw, lane);
-            OB::issue(rb, g.ldb, g.N, n0, st * BK, kz, buf + OA::WORDS, pw, lane);
-        };
-#pragma unroll
-        for (int st = 0; st < NS - 1; st++)
-            if (st < nk) issue(st);
-        for (int it = 0; it < nk; it++) {
-            if (it + NS - 2 < nk)
-                wait_vmcnt<(NS - 2) * (OA::PER + OB::PER)>();
-            else
-                wait_vmcnt<0>();
-            // a bare barrier: __syncthreads()'s release fence would also wait
-            // for the DMAs of the later stages still in flight
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_s_barrier();
-            asm volatile("" ::: "memory");
-            if (it + NS - 1 < nk) issue(it + NS - 1);
-        }
+    // RS: the compute waves of the first column tile also sum A's values
+    const int lane = threadIdx.x & 63, wave = wave_index(), lr = lane & 31, lh = lane >> 5;
+    const bool rsum = RS && n0 == 0 && (wave & 1) == 0;
+    Tile t;
+    if (!t.run(g.a + z * g.stride_a, g.lda, g.M, g.b + z * g.stride_b, g.ldb, g.N, kz, m0, n0,
+               rsum, lds))
         return;
-    }
-
-    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lh = lane >> 5;
-    // RS: the compute waves of the first column tile also sum the A values
-    // they multiply, in f64: lane (lr, lh) of fragment i adds those of row
-    // wm*WTM + 32i + lr at k = 8g + 4lh + s, stage by stage in k order.
-    const bool rsum = RS && n0 == 0 && wn == 0;
-    double rs[TM];
-#pragma unroll
-    for (int i = 0; i < TM; i++) rs[i] = 0.0;
-    f32x16 acc[TM][TN][NACC];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int a = 0; a < NACC; a++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) acc[i][j][a][v] = 0.f;
-    for (int it = 0; it < nk; it++) {
-        __syncthreads();
-        const float *As = lds + (it % NS) * STAGE, *Bs = As + OA::WORDS;
-        f32x4 af[TM], bf[TN];
-#pragma unroll
-        for (int i = 0; i < TM; i++) af[i] = OA::frag(As, wm * WTM + i * 32 + lr, 0, lh);
-#pragma unroll
-        for (int j = 0; j < TN; j++) bf[j] = OB::frag(Bs, wn * WTN + j * 32 + lr, 0, lh);
-#pragma unroll
-        for (int gk = 0; gk < BK / 8; gk++) {
-            f32x4 an[TM], bn[TN];
-            if (gk + 1 < BK / 8) {
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-                    an[i] = OA::frag(As, wm * WTM + i * 32 + lr, gk + 1, lh);
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    bn[j] = OB::frag(Bs, wn * WTN + j * 32 + lr, gk + 1, lh);
-            }
-            // keep the next group's reads ahead of this group's MFMAs
-            __builtin_amdgcn_sched_barrier(0);
-            if (rsum) {
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int s = 0; s < 4; s++) rs[i] += (double)af[i][s];
-            }
-#pragma unroll
-            for (int s = 0; s < 4; s++)
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j][s % NACC] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                            af[i][s], bf[j][s], acc[i][j][s % NACC], 0, 0, 0);
-            if (gk + 1 < BK / 8) {
-#pragma unroll
-                for (int i = 0; i < TM; i++) af[i] = an[i];
-#pragma unroll
-                for (int j = 0; j < TN; j++) bf[j] = bn[j];
-            }
-        }
-    }
     if (rsum) {
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
+        for (int i = 0; i < Tile::TM; i++) {
             // the two lane halves' sums, added in half order on both halves
-            const double o = __shfl_xor(rs[i], 32, 64);
-            const double t = lh == 0 ? rs[i] + o : o + rs[i];
-            const int row = m0 + wm * WTM + i * 32 + lr;
+            const double o = __shfl_xor(t.rs[i], 32, 64);
+            const double s = lh == 0 ? t.rs[i] + o : o + t.rs[i];
+            const int row = m0 + (wave >> 1) * Tile::WTM + i * 32 + lr;
             if (lh == 0 && row < g.M) {
                 if (g.rsum_part)
-                    g.rsum_part[z * g.M + row] = t;
+                    g.rsum_part[z * g.M + row] = s;
                 else
-                    g.rsum_out[row] += (float)t;
+                    g.rsum_out[row] += (float)s;
             }
         }
     }
     float *Cp = g.c + z * g.stride_c;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int row = m0 + wm * WTM + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                const int col = n0 + wn * WTN + j * 32 + lr;
-                if (row < g.M && col < g.N) {
-                    float val = acc[i][j][0][v];
-                    if (NACC == 2) val += acc[i][j][NACC - 1][v];
-                    if (g.bias) val += g.bias[col];
-                    float *cp = Cp + (long long)row * g.ldc + col;
-                    if (g.acc) val = *cp + val;
-                    *cp = val;
-                }
-            }
+    t.each([&](int r, int c, float val) {
+        const int row = m0 + r, col = n0 + c;
+        if (row < g.M && col < g.N) {
+            if (g.bias) val += g.bias[col];
+            float *cp = Cp + (long long)row * g.ldc + col;
+            if (g.acc) val = *cp + val;
+            *cp = val;
+        }
+    });
 }
 
 template <int BM, int BN, bool AT, bool BT, bool VEC>
@@ -511,6 +535,66 @@ __global__ __launch_bounds__(256) void ns_gemm_kernel(const NsGemmProb *__restri
         ns_tile<false, false, VEC>(p, z, ti, tj, alpha, beta, As, Bs);
 }
 
+// ns_gemm_kernel on the direct-to-LDS tile (every operand of every problem
+// of the launch with whole 16-byte quads): 8 waves, 64 x 64 tiles.
+template <bool AT, bool BT>
+__device__ __forceinline__ void ns_tile_dma(const NsGemmProb &p, uint32_t z, int ti, int tj,
+                                            float alpha, float beta, float *lds) {
+#pragma clang fp contract(off)
+    using Tile = DmaTile<64, 64, 32, 3, AT, BT>;
+    const int m0 = ti * 64, n0 = tj * 64;
+    Tile t;
+    if (!t.run(p.a + z * p.stride_a, p.lda, p.M, p.b + z * p.stride_b, p.ldb, p.N, p.K, m0, n0,
+               false, lds))
+        return;
+    float *Cp = p.c + z * p.stride_c;
+    const float *Ep = p.e ? p.e + z * p.stride_c : nullptr;
+    const bool mirror = p.sym && ti != tj;
+    t.each([&](int rr, int cc, float val) {
+        const int row = m0 + rr, col = n0 + cc;
+        if (row < p.M && col < p.N) {
+            const long long o = (long long)row * p.ldc + col;
+            const float v = Ep ? alpha * Ep[o] + beta * val : val;
+            Cp[o] = v;
+            if (mirror) Cp[(long long)col * p.ldc + row] = v;
+        }
+    });
+}
+
+constexpr size_t NS_DMA_LDS = DmaTile<64, 64, 32, 3, false, false>::LDS_BYTES;
+
+__global__ __launch_bounds__(512) void ns_gemm_dma_kernel(const NsGemmProb *__restrict__ probs,
+                                                          int nprob, float alpha, float beta) {
+    extern __shared__ float lds[];
+    int lo = 0, hi = nprob - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (probs[mid].tile0 <= blockIdx.x)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const NsGemmProb p = probs[lo];
+    const uint32_t local = blockIdx.x - p.tile0;
+    const uint32_t z = local / p.tmn;
+    uint32_t r = local - z * p.tmn;
+    int ti, tj;
+    if (p.sym) {
+        ti = 0;
+        while (r >= p.tn - (uint32_t)ti) r -= p.tn - (uint32_t)ti++;
+        tj = ti + (int)r;
+    } else {
+        ti = (int)(r / p.tn);
+        tj = (int)(r % p.tn);
+    }
+    if (p.lay == NS_LAY_NT)
+        ns_tile_dma<false, true>(p, z, ti, tj, alpha, beta, lds);
+    else if (p.lay == NS_LAY_TN)
+        ns_tile_dma<true, false>(p, z, ti, tj, alpha, beta, lds);
+    else
+        ns_tile_dma<false, false>(p, z, ti, tj, alpha, beta, lds);
+}
+
 __global__ void fill_kernel(float *p, long long n, float v) {
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long st = (long long)gridDim.x * blockDim.x;
@@ -590,7 +674,7 @@ int launch_t(rnn_ctx *ctx, const GemmArgs &g, int count, bool vec) {
 
 template <int BM, int BN, int BK, int NS, bool AT, bool BT, bool RS>
 int launch_dma_t(rnn_ctx *ctx, const GemmArgs &g, int count) {
-    constexpr size_t lds = (size_t)NS * (BM + BN) * BK * 4;
+    constexpr size_t lds = DmaTile<BM, BN, BK, NS, AT, BT>::LDS_BYTES;
     static bool attr = false;
     if (!attr) {
         attr = true;
@@ -652,6 +736,12 @@ static bool dma_ok(size_t count, size_t m, size_t n, size_t kchunk, size_t ktota
 
 // Enqueues `count` GEMMs C_z = op(A_z) op(B_z) (+C_z) (+bias) with problem z
 // covering k = min(kchunk, ktotal - z*kchunk) (kchunk = k for plain batches).
+bool ns_dma_ok(const NsGemmProb &p, size_t count) {
+    const int at = p.lay == NS_LAY_TN, bt = p.lay == NS_LAY_NT;
+    return dma_ok(count, (size_t)p.M, (size_t)p.N, (size_t)p.K, (size_t)p.K, p.a,
+                  (size_t)p.stride_a, p.lda, at, p.b, (size_t)p.stride_b, p.ldb, bt);
+}
+
 static bool dma_enabled() {
     static const bool on = getenv("RNN_GEMM_NODMA") == nullptr;
     return on;
@@ -724,7 +814,16 @@ int rnn_ns_gemm_launch(rnn_ctx *ctx, const NsGemmProb *probs, int nprob, size_t 
     if (ntiles == 0) return RNN_OK;
     if (ntiles > 0x7fffffffu) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "ns_gemm: too many tiles");
     const dim3 grid((unsigned)ntiles);
-    if (vec)
+    if (vec == 2) {
+        static bool attr = false;
+        if (!attr) {
+            attr = true;
+            (void)hipFuncSetAttribute((const void *)ns_gemm_dma_kernel,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)NS_DMA_LDS);
+        }
+        hipLaunchKernelGGL(ns_gemm_dma_kernel, grid, dim3(512), NS_DMA_LDS, ctx->stream, probs,
+                           nprob, alpha, beta);
+    } else if (vec)
         hipLaunchKernelGGL(ns_gemm_kernel<true>, grid, dim3(256), 0, ctx->stream, probs, nprob,
                            alpha, beta);
     else

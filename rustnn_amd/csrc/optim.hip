@@ -321,7 +321,7 @@ struct NsPlan {
         int vec = 0;
         float alpha = 0.0f, beta = 0.0f;
     };
-    std::vector<Op> ops;  // 3 per quintic step
+    std::vector<Op> ops;  // per quintic step 3, or 6 when some problems need the register tile
 };
 
 struct rnn_optim {
@@ -460,8 +460,10 @@ void ns_layout(const std::vector<NsIn> &mats, size_t steps, char *base, TableBuf
             std::stable_sort(order.begin(), order.end(), [&](size_t p, size_t q) {
                 return (op == 0 ? grps[p].n : grps[p].m) > (op == 0 ? grps[q].n : grps[q].m);
             });
-            std::vector<NsGemmProb> probs;
-            uint32_t tile = 0;
+            // problems that take the direct-to-LDS tile go in one launch,
+            // the others in a second
+            std::vector<NsGemmProb> probs, dprobs;
+            uint32_t tile = 0, dtile = 0;
             bool vec = true;
             for (size_t k : order) {
                 const Grp &g = grps[k];
@@ -482,7 +484,6 @@ void ns_layout(const std::vector<NsIn> &mats, size_t steps, char *base, TableBuf
                     p.ldc = (int)m;
                     p.lay = tall ? NS_LAY_TN : NS_LAY_NT;
                     p.sym = 1;
-                    if (!tall) vec = vec && n % 4 == 0;
                 } else if (op == 1) {
                     // B = b A + c A A^T, into the AA slot
                     p.a = p.b = F(g.a);
@@ -493,7 +494,6 @@ void ns_layout(const std::vector<NsIn> &mats, size_t steps, char *base, TableBuf
                     p.lda = p.ldb = p.ldc = (int)m;
                     p.lay = NS_LAY_NT;
                     p.sym = 1;
-                    vec = vec && m % 4 == 0;
                 } else if (!tall) {
                     // X' = a X + B X: [m x m] [m x n]
                     p.a = F(g.aa);
@@ -508,7 +508,6 @@ void ns_layout(const std::vector<NsIn> &mats, size_t steps, char *base, TableBuf
                     p.lda = (int)m;
                     p.ldb = p.ldc = (int)n;
                     p.lay = NS_LAY_NN;
-                    vec = vec && m % 4 == 0;
                 } else {
                     // Y' = a Y + Y B^T: [n x m] [m x m]
                     p.a = xs;
@@ -522,23 +521,34 @@ void ns_layout(const std::vector<NsIn> &mats, size_t steps, char *base, TableBuf
                     p.K = (int)m;
                     p.lda = p.ldb = p.ldc = (int)m;
                     p.lay = NS_LAY_NT;
-                    vec = vec && m % 4 == 0;
                 }
                 p.tn = (uint32_t)rnn_div_up((size_t)p.N, 64);
                 p.tmn = p.sym ? p.tn * (p.tn + 1) / 2
                               : (uint32_t)rnn_div_up((size_t)p.M, 64) * p.tn;
+                if (ns_dma_ok(p, g.cnt)) {
+                    p.tile0 = dtile;
+                    dtile += (uint32_t)(g.cnt * p.tmn);
+                    dprobs.push_back(p);
+                    continue;
+                }
+                if (op == 0 && !tall) vec = vec && n % 4 == 0;
+                if (op != 0) vec = vec && m % 4 == 0;
                 p.tile0 = tile;
                 tile += (uint32_t)(g.cnt * p.tmn);
                 probs.push_back(p);
             }
-            NsPlan::Op o;
-            o.probs = tab.put(probs.data(), probs.size() * sizeof(NsGemmProb));
-            o.nprob = probs.size();
-            o.tiles = tile;
-            o.vec = vec;
-            o.alpha = op == 0 ? 0.0f : (op == 1 ? NS_B : NS_A);
-            o.beta = op == 0 ? 0.0f : (op == 1 ? NS_C : 1.0f);
-            plan.ops.push_back(o);
+            for (int d = 0; d < 2; d++) {
+                const std::vector<NsGemmProb> &pv = d ? probs : dprobs;
+                if (pv.empty()) continue;
+                NsPlan::Op o;
+                o.probs = tab.put(pv.data(), pv.size() * sizeof(NsGemmProb));
+                o.nprob = pv.size();
+                o.tiles = d ? tile : dtile;
+                o.vec = d ? (int)vec : 2;
+                o.alpha = op == 0 ? 0.0f : (op == 1 ? NS_B : NS_A);
+                o.beta = op == 0 ? 0.0f : (op == 1 ? NS_C : 1.0f);
+                plan.ops.push_back(o);
+            }
         }
     }
 }

@@ -221,10 +221,15 @@ struct NsGemmProb {
 
 // One launch over `nprob` problems (device table, sorted by tile0, the first
 // at 0) covering `ntiles` tiles: C = alpha E + beta (A op(B)) where E is set,
-// else the product.  vec: every k-contiguous operand row and batch stride is a
-// multiple of 4 floats and 16-byte aligned.
+// else the product.  vec: 1 when every k-contiguous operand row and batch
+// stride is a multiple of 4 floats and 16-byte aligned; 2 when moreover
+// every operand of every problem meets ns_dma_ok (the direct-to-LDS tile).
 int rnn_ns_gemm_launch(rnn_ctx *ctx, const NsGemmProb *probs, int nprob, size_t ntiles, int vec,
                        float alpha, float beta);
+// Whether problem p (host copy, device pointers) can take the direct-to-LDS
+// tile: every 16-byte operand quad wholly inside or outside its operand,
+// 16-byte aligned bases and batch strides, extents below 2^31 bytes.
+bool ns_dma_ok(const NsGemmProb &p, size_t count);
 
 // rnn_gemm_launch with explicit leading dimensions: op(A) [m x k] read from
 // rows of stride lda (A stored [k][m] with stride lda when at), likewise B
