@@ -343,6 +343,13 @@ int rnn_hint_mse(rnn_ctx *ctx, size_t n, size_t c, const float *pred, const floa
 int rnn_drop_path_forward(rnn_ctx *ctx, size_t n, size_t per, float *x, float p, uint64_t seed,
                           float *mask);
 int rnn_drop_path_backward(rnn_ctx *ctx, size_t n, size_t per, float *dy, const float *mask);
+/* The masks alone of `count` DropPath layers over n images, in one launch:
+ * masks[k] (device, [n]) receives rnn_drop_path_forward's factors for p[k]
+ * and seeds[k] (p, seeds and masks are host arrays).  A layer whose mask is
+ * drawn here is applied with rnn_drop_path_backward (the same per-image
+ * scaling).  Batches DropPath::forward's draws (vit.rs:44-51) of a step. */
+int rnn_drop_path_masks(rnn_ctx *ctx, size_t count, size_t n, const float *p,
+                        const uint64_t *seeds, float *const *masks);
 /* y[r][j] += l[j] x[r][j]: Block's depthwise gate a += gamma * dw(h)
  * (vit.rs:150-158).  Its backward is rnn_layerscale_backward. */
 int rnn_axpy_cols(rnn_ctx *ctx, size_t rows, size_t c, float *y, const float *l, const float *x);

@@ -121,6 +121,7 @@ extern "C" {
     pub fn rnn_hint_mse(ctx: *mut rnn_ctx, n: usize, c: usize, pred: *const f32, target: *const f32, scale: f32, dz: *mut f32, loss: *mut f32) -> c_int;
     pub fn rnn_drop_path_forward(ctx: *mut rnn_ctx, n: usize, per: usize, x: *mut f32, p: f32, seed: u64, mask: *mut f32) -> c_int;
     pub fn rnn_drop_path_backward(ctx: *mut rnn_ctx, n: usize, per: usize, dy: *mut f32, mask: *const f32) -> c_int;
+    pub fn rnn_drop_path_masks(ctx: *mut rnn_ctx, count: usize, n: usize, p: *const f32, seeds: *const u64, masks: *mut *mut float  const) -> c_int;
     pub fn rnn_axpy_cols(ctx: *mut rnn_ctx, rows: usize, c: usize, y: *mut f32, l: *const f32, x: *const f32) -> c_int;
     pub fn rnn_token_merge(ctx: *mut rnn_ctx, n: usize, th: usize, c: usize, z: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_token_merge_backward(ctx: *mut rnn_ctx, n: usize, th: usize, c: usize, dy: *const f32, dz: *mut f32) -> c_int;

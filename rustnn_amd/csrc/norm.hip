@@ -160,6 +160,141 @@ __global__ __launch_bounds__(NT) void ln_bwd_kernel(size_t rows, int c, const fl
     }
 }
 
+// ------------------------------------------- row kernels with column sums
+// A block of 4 waves takes RB_ROWS consecutive rows, wave w the rows w,
+// w + 4, ... of them in order, each lane columns lane + 64 i (i < NV).  Its
+// lanes keep f64 column sums over their rows, and the block stores the four
+// waves' sums, added in wave order, as partial row blockIdx.x of
+// part[nblk][NO * c] -- the stage-1 layout of colsum_red_kernel.
+constexpr int RB_ROWS = 16;
+
+template <int NV, int NO>
+__device__ __forceinline__ void store_col_partials(const double (&p)[NO][NV], int c,
+                                                   double *__restrict__ part) {
+    __shared__ double red[NO][NT / 64][NV * 64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 0; o < NO; o++)
+#pragma unroll
+        for (int i = 0; i < NV; i++) red[o][w][lane + 64 * i] = p[o][i];
+    __syncthreads();
+    double *row = part + (size_t)blockIdx.x * NO * c;
+    for (int j = threadIdx.x; j < c; j += NT)
+#pragma unroll
+        for (int o = 0; o < NO; o++) {
+            double t = red[o][0][j];
+#pragma unroll
+            for (int q = 1; q < NT / 64; q++) t += red[o][q][j];
+            row[(size_t)o * c + j] = t;
+        }
+}
+
+// LayerNorm backward (ln_bwd_kernel per row) with dgamma's and dbeta's
+// partials: sums of (double)(dy xhat) and of dy.  A wave loads all its rows'
+// dy and xhat before the first row's reductions.
+template <int NV>
+__global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
+                                                       const float *__restrict__ dy,
+                                                       const float *__restrict__ xhat,
+                                                       const float *__restrict__ invstd,
+                                                       const float *__restrict__ g,
+                                                       float *__restrict__ dx,
+                                                       double *__restrict__ part) {
+    constexpr int RPW = RB_ROWS / 4;
+    const int lane = threadIdx.x & 63, w = wave_index();
+    const size_t r0 = (size_t)blockIdx.x * RB_ROWS + w;
+    const int nr = r0 < rows ? (int)min((size_t)RPW, (rows - r0 + 3) / 4) : 0;
+    const float inv = 1.0f / (float)c;
+    double p[2][NV];
+    float gv[NV], dv[RPW][NV], hv[RPW][NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int j = min(lane + 64 * i, c - 1);
+        gv[i] = g[j];
+        p[0][i] = p[1][i] = 0.0;
+#pragma unroll
+        for (int k = 0; k < RPW; k++) {
+            const size_t r = min(r0 + 4 * (size_t)k, rows - 1);
+            dv[k][i] = dy[r * c + j];
+            hv[k][i] = xhat[r * c + j];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+        if (k >= nr) break;
+        const size_t r = r0 + 4 * (size_t)k;
+        double m1 = 0.0, m2 = 0.0;
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            if (lane + 64 * i < c) {
+                const float d = dv[k][i] * gv[i];
+                m1 += d;
+                m2 += (double)(d * hv[k][i]);
+                p[0][i] += (double)(dv[k][i] * hv[k][i]);
+                p[1][i] += dv[k][i];
+            }
+        const float s1 = (float)rnn_wave_sum_d(m1), s2 = (float)rnn_wave_sum_d(m2);
+        const float is = invstd[r];
+        float *xr = dx + r * c;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = lane + 64 * i;
+            if (j >= c) break;
+            const float d = dv[k][i] * gv[i];
+            xr[j] = is * (d - s1 * inv - hv[k][i] * s2 * inv);
+        }
+    }
+    store_col_partials<NV, 2>(p, c, part);
+}
+
+// DropPath + LayerScale backward (scale_cols_masked_kernel per row) with
+// dl's partials: sums of (double)((dy m) x), m = mask[r / rpi] (1 without a
+// mask).  dx may be dy: each element is read, then written, by one lane.
+template <int NV>
+__global__ __launch_bounds__(NT) void ls_bwd_cs_kernel(size_t rows, int c, const float *dy,
+                                                       const float *__restrict__ x,
+                                                       const float *__restrict__ l,
+                                                       const float *__restrict__ mask, size_t rpi,
+                                                       float *dx, double *__restrict__ part) {
+    constexpr int RPW = RB_ROWS / 4;
+    const int lane = threadIdx.x & 63, w = wave_index();
+    const size_t r0 = (size_t)blockIdx.x * RB_ROWS + w;
+    const int nr = r0 < rows ? (int)min((size_t)RPW, (rows - r0 + 3) / 4) : 0;
+    double p[1][NV];
+    float lv[NV], dv[RPW][NV], xv[RPW][NV], m[RPW];
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+        const size_t r = min(r0 + 4 * (size_t)k, rows - 1);
+        m[k] = mask ? mask[r / rpi] : 1.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int j = min(lane + 64 * i, c - 1);
+        lv[i] = l[j];
+        p[0][i] = 0.0;
+#pragma unroll
+        for (int k = 0; k < RPW; k++) {
+            const size_t r = min(r0 + 4 * (size_t)k, rows - 1);
+            dv[k][i] = dy[r * c + j];
+            xv[k][i] = x[r * c + j];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+        if (k >= nr) break;
+        float *xr = dx + (r0 + 4 * (size_t)k) * c;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = lane + 64 * i;
+            if (j >= c) break;
+            const float a = mask ? dv[k][i] * m[k] : dv[k][i];
+            p[0][i] += (double)(a * xv[k][i]);
+            xr[j] = a * lv[i];
+        }
+    }
+    store_col_partials<NV, 1>(p, c, part);
+}
+
 // Column sums in two fixed-order stages.  Stage 1, block (x, y): columns
 // [64x, 64x + 64), rows [CS_ROWS y, CS_ROWS (y + 1)); wave g sums the rows
 // g, g + 4, ... of the block in order (8 loads ahead of their adds), and the
@@ -571,10 +706,36 @@ int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const 
         return rnn_fail(ctx, RNN_E_NULL, "ln_backward: null operand");
     if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "ln_backward: %zu x %zu", rows, c);
     // dgamma += sum dy xhat, dbeta += sum dy (norm.rs:94-119)
+    const int nv = (int)rnn_div_up(c, (size_t)64);
+    if (nv <= 8) {
+        // one pass: dx and the column sums' partials, then their reduction
+        const size_t nblk = rnn_div_up(rows, (size_t)RB_ROWS);
+        if (nblk > 0x7fffffff) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "ln_backward: rows");
+        double *part = (double *)rnn_workspace(ctx, nblk * 2 * c * sizeof(double));
+        if (!part) return RNN_E_NOMEM;
+        auto cs = [&](auto kern) {
+            kern<<<(unsigned)nblk, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, dx,
+                                                         part);
+        };
+        switch (nv) {
+            case 1: cs(ln_bwd_cs_kernel<1>); break;
+            case 2: cs(ln_bwd_cs_kernel<2>); break;
+            case 3: cs(ln_bwd_cs_kernel<3>); break;
+            case 4: cs(ln_bwd_cs_kernel<4>); break;
+            case 5: cs(ln_bwd_cs_kernel<5>); break;
+            case 6: cs(ln_bwd_cs_kernel<6>); break;
+            case 7: cs(ln_bwd_cs_kernel<7>); break;
+            default: cs(ln_bwd_cs_kernel<8>); break;
+        }
+        RNN_LAUNCHED(ctx);
+        colsum_red_kernel<<<(unsigned)rnn_div_up(2 * c, (size_t)CS_RED_COLS), NT, 0,
+                            ctx->stream>>>((int)nblk, 2 * c, c, part, dg, db);
+        RNN_LAUNCHED(ctx);
+        return RNN_OK;
+    }
     int rc = colsum_add(ctx, rows, (int)c, dy, xhat, dg, db);
     if (rc) return rc;
     const unsigned grid = (unsigned)rnn_div_up(rows, NT / 64);
-    const int nv = (int)rnn_div_up(c, (size_t)64);
     auto bwd = [&](auto kern) {
         kern<<<grid, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, dx);
     };
@@ -605,6 +766,34 @@ int rnn_layerscale_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, 
     return RNN_OK;
 }
 
+// LayerScale backward (c <= 512) in one pass -- dx and dl's partials -- then
+// their reduction: dl += sum (dy m) x, dx = (dy m) l, m = mask[r / rpi] or 1.
+static int ls_backward_cs(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *x,
+                          const float *l, const float *mask, size_t rpi, float *dx, float *dl) {
+    const size_t nblk = rnn_div_up(rows, (size_t)RB_ROWS);
+    if (nblk > 0x7fffffff) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "layerscale: rows");
+    double *part = (double *)rnn_workspace(ctx, nblk * c * sizeof(double));
+    if (!part) return RNN_E_NOMEM;
+    auto cs = [&](auto kern) {
+        kern<<<(unsigned)nblk, NT, 0, ctx->stream>>>(rows, (int)c, dy, x, l, mask, rpi, dx, part);
+    };
+    switch ((int)rnn_div_up(c, (size_t)64)) {
+        case 1: cs(ls_bwd_cs_kernel<1>); break;
+        case 2: cs(ls_bwd_cs_kernel<2>); break;
+        case 3: cs(ls_bwd_cs_kernel<3>); break;
+        case 4: cs(ls_bwd_cs_kernel<4>); break;
+        case 5: cs(ls_bwd_cs_kernel<5>); break;
+        case 6: cs(ls_bwd_cs_kernel<6>); break;
+        case 7: cs(ls_bwd_cs_kernel<7>); break;
+        default: cs(ls_bwd_cs_kernel<8>); break;
+    }
+    RNN_LAUNCHED(ctx);
+    colsum_red_kernel<<<(unsigned)rnn_div_up(c, (size_t)CS_RED_COLS), NT, 0, ctx->stream>>>(
+        (int)nblk, c, c, part, dl, nullptr);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
 int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *x,
                             const float *l, float *dx, float *dl) {
     if (!ctx) return RNN_E_NULL;
@@ -614,6 +803,7 @@ int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy
         return rnn_fail(ctx, RNN_E_NULL, "layerscale_backward: null operand");
     if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "layerscale: %zu x %zu", rows, c);
     // dl += sum dy x (norm.rs:183-204), before dx may overwrite dy
+    if (c <= 512) return ls_backward_cs(ctx, rows, c, dy, x, l, nullptr, 1, dx, dl);
     int rc = colsum_add(ctx, rows, (int)c, dy, x, dl, nullptr);
     if (rc) return rc;
     scale_cols_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, (int)c, dy, l, dx);
@@ -635,6 +825,7 @@ int rnn_drop_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const floa
         return rnn_fail(ctx, RNN_E_INVALID, "drop_layerscale_backward: %zu rows per image of %zu",
                         rpi, rows);
     // dl += sum (dy m) x, then dx = (dy m) l
+    if (c <= 512) return ls_backward_cs(ctx, rows, c, dy, x, l, mask, mask ? rpi : 1, dx, dl);
     int rc = rnn_colsum_f64(ctx, rows, (int)c, dy, x, dl, nullptr, mask, mask ? rpi : 1);
     if (rc) return rc;
     if (mask)

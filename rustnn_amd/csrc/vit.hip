@@ -25,13 +25,37 @@ unsigned ew_grid(size_t len) {
 
 // DropPath::forward's mask (vit.rs:44-51): image i keeps its branch with the
 // i-th uniform of Rng::new(seed) below 1 - p, scaled by 1 / keep, else 0.
-// The generator is sequential: one thread draws all n.
-__global__ void drop_path_mask_kernel(size_t n, float p, uint64_t seed,
-                                      float *__restrict__ mask) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// The generator is sequential: one wave draws all n with the state
+// wave-uniform (scalar registers, scalar ALU), and lane i % 64 stores mask[i].
+__device__ __forceinline__ void draw_drop_mask(size_t n, float p, uint64_t seed,
+                                               float *__restrict__ mask) {
+    const int lane = (int)threadIdx.x;
     RnnRng rng(seed);
     const float keep = 1.0f - p;
-    for (size_t i = 0; i < n; i++) mask[i] = rng.uniform() < keep ? 1.0f / keep : 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        const float u = rng.uniform();
+        if ((int)(i & 63) == lane) mask[i] = u < keep ? 1.0f / keep : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(64) void drop_path_mask_kernel(size_t n, float p, uint64_t seed,
+                                                            float *__restrict__ mask) {
+    draw_drop_mask(n, p, seed, mask);
+}
+
+// The masks of up to DP_BATCH DropPath layers in one launch, one wave each
+// (the per-layer generators are independent).
+constexpr int DP_BATCH = 32;
+struct DropMasks {
+    uint64_t seed[DP_BATCH];
+    float *mask[DP_BATCH];
+    float p[DP_BATCH];
+    unsigned long long n;
+};
+
+__global__ __launch_bounds__(64) void drop_path_masks_kernel(DropMasks a) {
+    const int k = (int)blockIdx.x;
+    draw_drop_mask((size_t)a.n, a.p[k], a.seed[k], a.mask[k]);
 }
 
 // Rows times the mask, skipping the rows whose factor is 1 (the forward's
@@ -146,6 +170,33 @@ int rnn_drop_path_forward(rnn_ctx *ctx, size_t n, size_t per, float *x, float p,
     const unsigned gx = (unsigned)std::max<size_t>(1, std::min<size_t>(rnn_div_up(per, NT), 64));
     drop_path_bwd_kernel<<<dim3(gx, (unsigned)n), NT, 0, ctx->stream>>>(per, x, mask);
     RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_drop_path_masks(rnn_ctx *ctx, size_t count, size_t n, const float *p,
+                        const uint64_t *seeds, float *const *masks) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (count == 0 || n == 0) return RNN_OK;
+    if (!p || !seeds || !masks) return rnn_fail(ctx, RNN_E_NULL, "drop_path_masks: null operand");
+    if (n > 65535) return rnn_fail(ctx, RNN_E_INVALID, "drop_path_masks: n %zu (<= 65535)", n);
+    for (size_t k0 = 0; k0 < count; k0 += DP_BATCH) {
+        const size_t cnt = std::min<size_t>(DP_BATCH, count - k0);
+        DropMasks a{};
+        a.n = n;
+        for (size_t k = 0; k < cnt; k++) {
+            const float pk = p[k0 + k];
+            if (!(pk > 0.0f) || !(pk < 1.0f))
+                return rnn_fail(ctx, RNN_E_INVALID, "drop_path_masks: p %g (0 < p < 1)",
+                                (double)pk);
+            if (!masks[k0 + k]) return rnn_fail(ctx, RNN_E_NULL, "drop_path_masks: null mask");
+            a.seed[k] = seeds[k0 + k];
+            a.mask[k] = masks[k0 + k];
+            a.p[k] = pk;
+        }
+        drop_path_masks_kernel<<<(unsigned)cnt, 64, 0, ctx->stream>>>(a);
+        RNN_LAUNCHED(ctx);
+    }
     return RNN_OK;
 }
 

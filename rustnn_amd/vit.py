@@ -168,13 +168,22 @@ class DropPath:
         self.p = float(p)
         self.ctx = ctx or default_ctx()
         self.mask = None
+        self.premask = None  # drawn ahead by draw_masks for the next forward
 
     def forward(self, x, train, seed):
         import torch
         if not train or self.p <= 0.0:
-            self.mask = None
+            self.mask = self.premask = None
             return x
         n = x.shape[0]
+        if self.premask is not None and self.premask.numel() == n:
+            # the draw of Rng::new(seed) already made by draw_masks
+            self.mask, self.premask = self.premask, None
+            self.ctx.check(lib().rnn_drop_path_backward(self.ctx.h, n, x.numel() // n,
+                                                        _ptr(x, x.numel(), "x"),
+                                                        _ptr(self.mask, n, "mask")))
+            return x
+        self.premask = None
         self.mask = torch.empty(n, device=x.device)
         self.ctx.check(lib().rnn_drop_path_forward(self.ctx.h, n, x.numel() // n,
                                                    _ptr(x, x.numel(), "x"), self.p,
@@ -190,6 +199,26 @@ class DropPath:
                                                     _ptr(dy, dy.numel(), "dy"),
                                                     _ptr(self.mask, n, "mask")))
         return dy
+
+
+def draw_masks(layers, n, device, ctx):
+    """DropPath::forward's draws (vit.rs:44-51) of several layers in one
+    launch: ``layers`` lists (DropPath, seed); every layer with p > 0 gets
+    the mask of Rng::new(seed) over n images for its next forward."""
+    import ctypes as C
+
+    import torch
+    act = [(dp, s) for dp, s in layers if dp.p > 0.0]
+    if not act:
+        return
+    masks = [torch.empty(n, device=device) for _ in act]
+    k = len(act)
+    p = (C.c_float * k)(*[dp.p for dp, _ in act])
+    seeds = (C.c_uint64 * k)(*[s & 0xFFFFFFFFFFFFFFFF for _, s in act])
+    ptrs = (C.c_void_p * k)(*[m.data_ptr() for m in masks])
+    ctx.check(lib().rnn_drop_path_masks(ctx.h, k, n, p, seeds, ptrs))
+    for (dp, _), m in zip(act, masks):
+        dp.premask = m
 
 
 class Block:
@@ -223,6 +252,13 @@ class Block:
         self.dp1, self.dp2, self.dp3 = (DropPath(drop, self.ctx), DropPath(drop, self.ctx),
                                         DropPath(drop, self.ctx))
         self.dwo = None
+
+    def drop_layers(self, seed):
+        """(DropPath, seed) of this block's branches as forward draws them."""
+        out = [(self.dp1, seed ^ self.idx)]
+        if self.cross is not None:
+            out.append((self.dp2, seed ^ self.idx ^ 0x5151))
+        return out + [(self.dp3, seed ^ self.idx ^ 0xA2A2)]
 
     def forward(self, x, mem, train, seed):
         import torch
@@ -570,6 +606,10 @@ class RustViT:
         mem = self.memln.forward(memt, train)
         z = nchw_to_tokens(self.tok.forward(h, train), self.ctx)
         seed = self.drop_seed
+        if train:
+            # every block's DropPath masks in one launch
+            draw_masks([lay for b in self.blocks3 + self.blocks4 for lay in b.drop_layers(seed)],
+                       n, x.device, self.ctx)
         for b in self.blocks3:
             z = b.forward(z, mem, train, seed)
         if train:

@@ -43,6 +43,27 @@ def test_drop_path(rnn, orc):
     assert dp.forward(X, False, seed) is X and dp.mask is None  # eval: identity
 
 
+def test_drop_path_masks_batched(rnn, orc):
+    """rnn_drop_path_masks: 40 layers' masks (two launches of up to 32) in
+    one call equal the oracle's draws, and a DropPath given its mask ahead
+    applies it as its own draw would."""
+    from rustnn_amd.vit import DropPath, draw_masks
+    n, per = 128, 96
+    ps = [0.05 + 0.02 * (k % 7) for k in range(40)]
+    seeds = [(0xABCDEF0123456789 * (k + 1)) & 0xFFFFFFFFFFFFFFFF for k in range(40)]
+    dps = [DropPath(p) for p in ps]
+    x = np.random.default_rng(3).standard_normal(n * per).astype(np.float32)
+    draw_masks(list(zip(dps, seeds)), n, "cuda", rnn.default_ctx())
+    for dp, p, sd in zip(dps, ps, seeds):
+        want, mask = orc.drop_path(x, n, p, sd)
+        assert np.array_equal(to_host(dp.premask), mask)
+    X = to_dev(x).reshape(n, per)
+    dps[5].forward(X, True, seeds[5])
+    want, mask = orc.drop_path(x, n, ps[5], seeds[5])
+    assert dps[5].premask is None and np.array_equal(to_host(dps[5].mask), mask)
+    assert np.array_equal(to_host(X).ravel(), want)
+
+
 def test_token_merge_and_layout(rnn, orc):
     from rustnn_amd.vit import nchw_to_tokens, token_merge, token_merge_back, tokens_to_nchw
     n, th, c = 16, 8, 256
