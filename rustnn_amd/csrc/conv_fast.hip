@@ -26,6 +26,7 @@
 #include "conv_common.h"
 
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 
@@ -579,6 +580,9 @@ static bool setup(const rnn_conv_spec *sp, FastArgs &a, FastPlan &p) {
         a.sc = cin * T::KK;
     }
     if (!choose_plan<K, S, P, DX>(a.CS, a.CD, a.GA, a.GB, p, a)) return false;
+    if (getenv("RNN_CONV_DEBUG"))
+        fprintf(stderr, "conv k%d s%d p%d %s %dx%d->%d: plan %d,%d,%d,%d,%d,%d lds %zu\n", K, S, P,
+                DX ? "dx" : "fwd", a.CS, a.GA, a.CD, p.TR, p.IMGS, p.CH, p.NPW, p.MB, p.WM, p.lds);
     a.TR = p.TR;
     a.tiles_a = (a.GA + p.TR - 1) / p.TR;
     a.CH = p.CH;
