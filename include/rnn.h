@@ -285,6 +285,13 @@ int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy
 int rnn_drop_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy,
                                  const float *x, const float *l, const float *mask, size_t rpi,
                                  float *dx, float *dl);
+/* y = x + (a l) m, m = mask[r / rpi] per image (mask may be NULL: m = 1): one
+ * residual branch of Block::forward, x + DropPath(LayerScale(a))
+ * (vit.rs:155-176: the LayerScale, the DropPath scaling and add_ in that
+ * rounding order) in one pass.  y may be x (in place); a is left unchanged,
+ * as the LayerScale backward (rnn_drop_layerscale_backward) reads it. */
+int rnn_residual_add_scaled(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *a,
+                            const float *l, const float *mask, size_t rpi, float *y);
 /* The SwiGLU gate between SwiGlu's two Linear calls (norm.rs:250-288): ab is
  * [rows][2h] (a | b), u = a sigmoid(a) b [rows][h]; the backward writes
  * dab [rows][2h] from du [rows][h]. */

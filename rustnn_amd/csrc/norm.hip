@@ -398,6 +398,39 @@ __global__ void scale_cols_masked_kernel(size_t len, int c, size_t per, const fl
         dx[i] = (dy[i] * mask[i / per]) * l[i % c];
 }
 
+// y = x + (a l) m with m = mask[r / rpi] (1 without a mask): a residual
+// branch of Block::forward, x + DropPath(LayerScale(a)) (vit.rs:155-176 over
+// norm.rs:168-180, vit.rs:40-57 and add_, nn.rs:441-443), in one pass with
+// the reference's rounding order.  y may be x.  VEC: c % 4 == 0, 16-byte
+// aligned rows.
+template <bool VEC>
+__global__ void residual_add_scaled_kernel(size_t len, int c, size_t per, const float *x,
+                                           const float *__restrict__ a,
+                                           const float *__restrict__ l,
+                                           const float *__restrict__ mask, float *y) {
+    const size_t step = (size_t)gridDim.x * blockDim.x;
+    if constexpr (VEC) {
+        for (size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4; i < len; i += 4 * step) {
+            const float4 xv = *reinterpret_cast<const float4 *>(x + i);
+            const float4 av = *reinterpret_cast<const float4 *>(a + i);
+            const float4 lv = *reinterpret_cast<const float4 *>(l + i % c);
+            float4 t = make_float4(av.x * lv.x, av.y * lv.y, av.z * lv.z, av.w * lv.w);
+            if (mask) {
+                const float m = mask[i / per];
+                t = make_float4(t.x * m, t.y * m, t.z * m, t.w * m);
+            }
+            *reinterpret_cast<float4 *>(y + i) =
+                make_float4(xv.x + t.x, xv.y + t.y, xv.z + t.z, xv.w + t.w);
+        }
+    } else {
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len; i += step) {
+            float t = a[i] * l[i % c];
+            if (mask) t = t * mask[i / per];
+            y[i] = x[i] + t;
+        }
+    }
+}
+
 // ------------------------------------------------------------ SwiGLU gate
 __device__ __forceinline__ float sigmoid(float z) { return 1.0f / (1.0f + expf(-z)); }
 
@@ -833,6 +866,31 @@ int rnn_drop_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const floa
                                                                            rpi * c, dy, l, mask, dx);
     else
         scale_cols_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, (int)c, dy, l, dx);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_residual_add_scaled(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *a,
+                            const float *l, const float *mask, size_t rpi, float *y) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!x || !a || !l || !y) return rnn_fail(ctx, RNN_E_NULL, "residual_add_scaled: null operand");
+    if (!dims_ok(rows, c)) return rnn_fail(ctx, RNN_E_INVALID, "residual_add_scaled: %zu x %zu",
+                                           rows, c);
+    if (mask && (rpi == 0 || rows % rpi))
+        return rnn_fail(ctx, RNN_E_INVALID, "residual_add_scaled: %zu rows per image of %zu", rpi,
+                        rows);
+    if (a == y) return rnn_fail(ctx, RNN_E_INVALID, "residual_add_scaled: y is a");
+    const size_t len = rows * c, per = (mask ? rpi : rows) * c;
+    const bool vec = c % 4 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)a & 15) == 0 &&
+                     ((uintptr_t)l & 15) == 0 && ((uintptr_t)y & 15) == 0;
+    if (vec)
+        residual_add_scaled_kernel<true><<<ew_grid(rnn_div_up(len, (size_t)4)), NT, 0, ctx->stream>>>(
+            len, (int)c, per, x, a, l, mask, y);
+    else
+        residual_add_scaled_kernel<false><<<ew_grid(len), NT, 0, ctx->stream>>>(len, (int)c, per, x,
+                                                                                a, l, mask, y);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

@@ -191,6 +191,26 @@ class DropPath:
                                                    _ptr(self.mask, n, "mask")))
         return x
 
+    def take_mask(self, n, train, seed, device):
+        """This forward's mask without applying it (a fused consumer scales
+        by it): the one draw_masks made ahead, else a fresh draw of
+        Rng::new(seed); None in eval or when p is 0."""
+        import ctypes as C
+
+        import torch
+        if not train or self.p <= 0.0:
+            self.mask = self.premask = None
+            return None
+        if self.premask is not None and self.premask.numel() == n:
+            self.mask, self.premask = self.premask, None
+            return self.mask
+        self.premask = None
+        self.mask = torch.empty(n, device=device)
+        self.ctx.check(lib().rnn_drop_path_masks(
+            self.ctx.h, 1, n, (C.c_float * 1)(self.p),
+            (C.c_uint64 * 1)(seed & 0xFFFFFFFFFFFFFFFF), (C.c_void_p * 1)(self.mask.data_ptr())))
+        return self.mask
+
     def backward(self, dy):
         if self.mask is None:
             return dy
@@ -199,6 +219,21 @@ class DropPath:
                                                     _ptr(dy, dy.numel(), "dy"),
                                                     _ptr(self.mask, n, "mask")))
         return dy
+
+
+def _branch_add(x, a, ls, dp, train, seed, out):
+    """out = x + DropPath(LayerScale(a)) in one pass (rnn_residual_add_scaled,
+    the reference's rounding order; out may be x).  Keeps what the branch's
+    backward reads: the LayerScale's input a (training) and the mask."""
+    n = a.shape[0]
+    rows, c = a.numel() // a.shape[-1], a.shape[-1]
+    mask = dp.take_mask(n, train, seed, a.device)
+    if train:
+        ls.x = a
+    ls.ctx.check(lib().rnn_residual_add_scaled(
+        ls.ctx.h, rows, c, _ptr(x, rows * c, "x"), _ptr(a, rows * c, "a"), _ptr(ls.l.v, c, "l"),
+        _ptr(mask, n, "mask") if mask is not None else None, rows // n, _ptr(out, rows * c, "y")))
+    return out
 
 
 def draw_masks(layers, n, device, ctx):
@@ -271,19 +306,17 @@ class Block:
                                   _ptr(self.gamma.v, c, "gamma"), _ptr(d, rows * c, "d")))
         if train:
             self.dwo = d
-        a = self.dp1.forward(self.ls1.forward(a, train), train, seed ^ self.idx)
-        y = torch.clone(x)
-        _add_(y, a, ctx)
+        # y = x + dp1(ls1(a)), then the other branches added in place, each
+        # in one pass (vit.rs:155-176)
+        y = _branch_add(x, a, self.ls1, self.dp1, train, seed ^ self.idx, torch.empty_like(x))
         if self.cross is not None:
             if mem is None:
                 raise ValueError("Block: a reader block needs the memory")
             cm = self.cross.forward(h, mem, train)
-            cm = self.dp2.forward(self.lsm.forward(cm, train), train, seed ^ self.idx ^ 0x5151)
-            _add_(y, cm, ctx)
+            _branch_add(y, cm, self.lsm, self.dp2, train, seed ^ self.idx ^ 0x5151, y)
         h2 = self.n2.forward(y, train)
         m = self.mlp.forward(h2, train)
-        m = self.dp3.forward(self.ls2.forward(m, train), train, seed ^ self.idx ^ 0xA2A2)
-        _add_(y, m, ctx)
+        _branch_add(y, m, self.ls2, self.dp3, train, seed ^ self.idx ^ 0xA2A2, y)
         return y
 
     def backward(self, dz, mem=None, dmem=None):

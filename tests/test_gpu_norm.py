@@ -75,6 +75,35 @@ def test_layerscale(rnn, orc):
     assert rel_frob(to_host(ls.l.g), dl) < TOL
 
 
+@pytest.mark.parametrize("n,t,c,masked", [(16, 64, 256, True), (3, 7, 33, True),
+                                           (5, 16, 384, False)])
+def test_residual_add_scaled(rnn, orc, n, t, c, masked):
+    """rnn_residual_add_scaled == x + DropPath(LayerScale(a)) composed from
+    the oracle's LayerScale forward, the per-image mask and add_, bit for
+    bit, out of place and in place; a is left unchanged."""
+    import ctypes as C
+    from rustnn_amd import _ptr, lib
+    rows = n * t
+    x, a, l = _r((rows, c), 24), _r((rows, c), 25), _r(c, 26, 1e-2)
+    keep = np.float32(0.8)
+    mask = np.where(np.arange(n) % 3 == 1, np.float32(0.0), np.float32(1.0) / keep).astype(np.float32)
+    t_ = orc.layerscale_forward(a, l).reshape(n, t, c)
+    if masked:
+        t_ = np.where(mask[:, None, None] == 1.0, t_, t_ * mask[:, None, None]).astype(np.float32)
+    want = (x.reshape(n, t, c) + t_).astype(np.float32).reshape(rows, c)
+    ctx = rnn.default_ctx()
+    X, A, L = _dev(x), _dev(a), to_dev(l)
+    M = to_dev(mask) if masked else None
+    for inplace in (False, True):
+        Y = X.clone() if inplace else _dev(np.zeros((rows, c), np.float32))
+        src = Y if inplace else X
+        ctx.check(lib().rnn_residual_add_scaled(
+            ctx.h, rows, c, _ptr(src, rows * c, "x"), _ptr(A, rows * c, "a"), _ptr(L, c, "l"),
+            _ptr(M, n, "m") if masked else None, t, _ptr(Y, rows * c, "y")))
+        assert np.array_equal(to_host(Y).reshape(rows, c), want)
+    assert np.array_equal(to_host(A).reshape(rows, c), a.reshape(rows, c))
+
+
 @pytest.mark.parametrize("n,t,c", [(16, 64, 256), (3, 7, 33)])
 def test_drop_layerscale_backward(rnn, orc, n, t, c):
     """rnn_drop_layerscale_backward == DropPath::backward (dy times the
