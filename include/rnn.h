@@ -271,6 +271,13 @@ int rnn_ln_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const fl
 /* LayerNorm::backward (norm.rs:87-137). */
 int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
                     const float *invstd, const float *g, float *dx, float *dg, float *db);
+/* rnn_ln_backward followed by add_ (Block::backward, vit.rs:175-232: the
+ * norm's input gradient plus the residual's, dy = n2.backward(dh2) + dz and
+ * dy += n1.backward(dh)): dx = the LayerNorm input gradient + add, in the
+ * same pass for c <= 512.  add may be dx (in place). */
+int rnn_ln_backward_add(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
+                        const float *invstd, const float *g, const float *add, float *dx,
+                        float *dg, float *db);
 /* LayerScale::forward / backward (norm.rs:166-212): y = x l per channel (y may
  * be x); dl += sum dy x, dx = dy l (dx may be dy). */
 int rnn_layerscale_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *l,

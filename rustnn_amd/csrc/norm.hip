@@ -191,14 +191,16 @@ __device__ __forceinline__ void store_col_partials(const double (&p)[NO][NV], in
 
 // LayerNorm backward (ln_bwd_kernel per row) with dgamma's and dbeta's
 // partials: sums of (double)(dy xhat) and of dy.  A wave loads all its rows'
-// dy and xhat before the first row's reductions.
+// dy and xhat before the first row's reductions.  With `add` set, dx = the
+// row's gradient + add (Block::backward's add_ after the norm; add may be
+// dx: each element is read, then written, by one lane).
 template <int NV>
 __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
-                                                       const float *__restrict__ dy,
+                                                       const float *dy,
                                                        const float *__restrict__ xhat,
                                                        const float *__restrict__ invstd,
                                                        const float *__restrict__ g,
-                                                       float *__restrict__ dx,
+                                                       const float *add, float *dx,
                                                        double *__restrict__ part) {
     constexpr int RPW = RB_ROWS / 4;
     const int lane = threadIdx.x & 63, w = wave_index();
@@ -233,6 +235,11 @@ __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
                 p[0][i] += (double)(dv[k][i] * hv[k][i]);
                 p[1][i] += dv[k][i];
             }
+        float ad[NV];
+        if (add) {
+#pragma unroll
+            for (int i = 0; i < NV; i++) ad[i] = add[r * c + min(lane + 64 * i, c - 1)];
+        }
         const float s1 = (float)rnn_wave_sum_d(m1), s2 = (float)rnn_wave_sum_d(m2);
         const float is = invstd[r];
         float *xr = dx + r * c;
@@ -241,7 +248,8 @@ __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
             const int j = lane + 64 * i;
             if (j >= c) break;
             const float d = dv[k][i] * gv[i];
-            xr[j] = is * (d - s1 * inv - hv[k][i] * s2 * inv);
+            const float v = is * (d - s1 * inv - hv[k][i] * s2 * inv);
+            xr[j] = add ? v + ad[i] : v;
         }
     }
     store_col_partials<NV, 2>(p, c, part);
@@ -429,6 +437,13 @@ __global__ void residual_add_scaled_kernel(size_t len, int c, size_t per, const 
             y[i] = x[i] + t;
         }
     }
+}
+
+// y = a + b (y may be b).
+__global__ void sum2_kernel(size_t len, const float *__restrict__ a, const float *b, float *y) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x)
+        y[i] = a[i] + b[i];
 }
 
 // ------------------------------------------------------------ SwiGLU gate
@@ -730,10 +745,11 @@ int rnn_ln_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const fl
     return RNN_OK;
 }
 
-int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
-                    const float *invstd, const float *g, float *dx, float *dg, float *db) {
-    if (!ctx) return RNN_E_NULL;
-    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+// rnn_ln_backward, then dx += add where add is set (in one pass up to 512
+// columns).
+static int ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
+                       const float *invstd, const float *g, const float *add, float *dx,
+                       float *dg, float *db) {
     if (rows == 0 || c == 0) return RNN_OK;
     if (!dy || !xhat || !invstd || !g || !dx || !dg || !db)
         return rnn_fail(ctx, RNN_E_NULL, "ln_backward: null operand");
@@ -747,8 +763,8 @@ int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const 
         double *part = (double *)rnn_workspace(ctx, nblk * 2 * c * sizeof(double));
         if (!part) return RNN_E_NOMEM;
         auto cs = [&](auto kern) {
-            kern<<<(unsigned)nblk, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, dx,
-                                                         part);
+            kern<<<(unsigned)nblk, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, add,
+                                                         dx, part);
         };
         switch (nv) {
             case 1: cs(ln_bwd_cs_kernel<1>); break;
@@ -768,9 +784,16 @@ int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const 
     }
     int rc = colsum_add(ctx, rows, (int)c, dy, xhat, dg, db);
     if (rc) return rc;
+    // with `add`, the row gradients go to a workspace copy first, then
+    // dx = that + add (add may be dx or dy)
+    float *out = dx;
+    if (add) {
+        out = (float *)rnn_workspace(ctx, rows * c * sizeof(float));
+        if (!out) return RNN_E_NOMEM;
+    }
     const unsigned grid = (unsigned)rnn_div_up(rows, NT / 64);
     auto bwd = [&](auto kern) {
-        kern<<<grid, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, dx);
+        kern<<<grid, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, out);
     };
     switch (nv) {
         case 1: bwd(ln_bwd_kernel<1>); break;
@@ -784,7 +807,27 @@ int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const 
         default: bwd(ln_bwd_kernel<0>); break;
     }
     RNN_LAUNCHED(ctx);
+    if (add) {
+        sum2_kernel<<<ew_grid(rows * c), NT, 0, ctx->stream>>>(rows * c, out, add, dx);
+        RNN_LAUNCHED(ctx);
+    }
     return RNN_OK;
+}
+
+int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
+                    const float *invstd, const float *g, float *dx, float *dg, float *db) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    return ln_backward(ctx, rows, c, dy, xhat, invstd, g, nullptr, dx, dg, db);
+}
+
+int rnn_ln_backward_add(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
+                        const float *invstd, const float *g, const float *add, float *dx,
+                        float *dg, float *db) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (!add) return rnn_fail(ctx, RNN_E_NULL, "ln_backward_add: add is null");
+    return ln_backward(ctx, rows, c, dy, xhat, invstd, g, add, dx, dg, db);
 }
 
 int rnn_layerscale_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *l,

@@ -47,14 +47,24 @@ class LayerNorm:
             _ptr(xh, rows * c, "xhat"), _ptr(iv, rows, "invstd")))
         return y
 
-    def backward(self, dy):
+    def backward(self, dy, add=None, out=None):
+        """Returns dx; with ``add``, dx + add in the same pass (the add_ that
+        follows the norm in Block::backward), written to ``out`` (which may
+        be ``add``) or a new tensor."""
         import torch
         rows, c = _rows_c(dy)
-        dx = torch.empty_like(dy)
-        self.ctx.check(lib().rnn_ln_backward(
-            self.ctx.h, rows, c, _ptr(dy, rows * c, "dy"), _ptr(self.xhat, rows * c, "xhat"),
-            _ptr(self.invstd, rows, "invstd"), _ptr(self.g.v, c, "g"), _ptr(dx, rows * c, "dx"),
-            _ptr(self.g.g, c, "dg"), _ptr(self.b.g, c, "db")))
+        dx = out if out is not None else torch.empty_like(dy)
+        if add is None:
+            self.ctx.check(lib().rnn_ln_backward(
+                self.ctx.h, rows, c, _ptr(dy, rows * c, "dy"), _ptr(self.xhat, rows * c, "xhat"),
+                _ptr(self.invstd, rows, "invstd"), _ptr(self.g.v, c, "g"),
+                _ptr(dx, rows * c, "dx"), _ptr(self.g.g, c, "dg"), _ptr(self.b.g, c, "db")))
+        else:
+            self.ctx.check(lib().rnn_ln_backward_add(
+                self.ctx.h, rows, c, _ptr(dy, rows * c, "dy"), _ptr(self.xhat, rows * c, "xhat"),
+                _ptr(self.invstd, rows, "invstd"), _ptr(self.g.v, c, "g"),
+                _ptr(add, rows * c, "add"), _ptr(dx, rows * c, "dx"), _ptr(self.g.g, c, "dg"),
+                _ptr(self.b.g, c, "db")))
         return dx
 
     def for_each_param(self, f):

@@ -326,8 +326,7 @@ class Block:
         # each branch's DropPath + LayerScale backward reads dz / dy unchanged
         dm = self.ls2.backward(dz, self.dp3.mask)
         dh2 = self.mlp.backward(dm)
-        dy = self.n2.backward(dh2)  # a new tensor
-        _add_(dy, dz, ctx)
+        dy = self.n2.backward(dh2, add=dz)  # n2's input gradient + dz, a new tensor
         dh = None  # the branches' input gradients, added in branch order
         if self.cross is not None:
             dc = self.lsm.backward(dy, self.dp2.mask)
@@ -347,7 +346,7 @@ class Block:
         else:
             _add_(dh, ga, ctx)
         _add_(dh, self.dw.backward(ddw), ctx)
-        _add_(dy, self.n1.backward(dh), ctx)
+        self.n1.backward(dh, add=dy, out=dy)  # dy += n1's input gradient
         return dy
 
     def for_each_param(self, f):

@@ -60,6 +60,28 @@ def test_layernorm(rnn, orc, rows, c):
     assert rel_frob(to_host(ln.b.g), db) < TOL
 
 
+@pytest.mark.parametrize("rows,c", [(300, 256), (37, 1024)])
+def test_layernorm_backward_add(rnn, orc, rows, c):
+    """rnn_ln_backward_add == rnn_ln_backward then add_, bit for bit, into a
+    new tensor and in place on the addend (one pass for c <= 512, the
+    two-kernel path above)."""
+    from rustnn_amd.norm import LayerNorm
+    x, dy, r = _r((rows, c), 31, 2.0, 0.5), _r((rows, c), 32), _r((rows, c), 33)
+    ln = LayerNorm(c)
+    ln.g.v.copy_(to_dev(_r(c, 34, 0.2, 1.0)))
+    ln.forward(_dev(x), True)
+    plain = to_host(ln.backward(_dev(dy))).reshape(rows, c)
+    dg, db = to_host(ln.g.g).copy(), to_host(ln.b.g).copy()
+    want = (plain + r).astype(np.float32)
+    got = to_host(ln.backward(_dev(dy), add=_dev(r))).reshape(rows, c)
+    assert np.array_equal(got, want)
+    R = _dev(r)
+    ln.backward(_dev(dy), add=R, out=R)
+    assert np.array_equal(to_host(R).reshape(rows, c), want)
+    # the parameter gradients accumulate as the plain backward's did
+    assert rel_frob(to_host(ln.g.g), 3 * dg) < TOL and rel_frob(to_host(ln.b.g), 3 * db) < TOL
+
+
 def test_layerscale(rnn, orc):
     from rustnn_amd.norm import LayerScale
     rows, c = 2048, 384
