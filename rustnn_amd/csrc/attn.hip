@@ -693,10 +693,54 @@ __global__ void rel_index_kernel(int th, int tw, int mh, int mw, uint32_t *idx) 
 // Softmax of the rows of P in place (attn.rs:190-212): x = tau S + rel[idx],
 // the diagonal -inf when masked; max, exp(x - max) (-inf -> 0), sum, times
 // 1/sum.  One wave per row (image, head, query).
+// NV > 0: the row (tk <= 64 NV) held in registers, read and written once.
+template <int NV>
 __global__ __launch_bounds__(256) void attn_softmax_rows_kernel(
     float *p, const float *__restrict__ tau, const float *__restrict__ rel,
     const uint32_t *__restrict__ relidx, long long rows, int h, int tq, int tk, int nrel,
     int mask) {
+    if constexpr (NV > 0) {
+        const long long r = (long long)blockIdx.x * 4 + wave_index();
+        if (r >= rows) return;
+        const int lane = threadIdx.x & 63;
+        const int qi = (int)(r % tq), hd = (int)((r / tq) % h);
+        float *row = p + r * tk;
+        const float t = tau[hd];
+        const float *rh = rel + (long long)hd * nrel;
+        const uint32_t *ix = relidx + (long long)qi * tk;
+        float raw[NV], xv[NV];
+        uint32_t id[NV];
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = min(lane + 64 * i, tk - 1);
+            raw[i] = row[k];
+            id[i] = ix[k];
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = lane + 64 * i;
+            const float x = (k >= tk || (mask && k == qi)) ? -INFINITY : t * raw[i] + rh[id[i]];
+            xv[i] = x;
+            mx = fmaxf(mx, x);
+        }
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const float e = xv[i] == -INFINITY ? 0.f : expf(xv[i] - mx);
+            xv[i] = e;
+            sum += e;
+        }
+        for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o, 64);
+        const float inv = 1.0f / sum;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = lane + 64 * i;
+            if (k < tk) row[k] = xv[i] * inv;
+        }
+        return;
+    }
     const long long r = (long long)blockIdx.x * 4 + wave_index();
     if (r >= rows) return;
     const int lane = threadIdx.x & 63;
@@ -800,14 +844,22 @@ __global__ __launch_bounds__(256) void attn_drel_part_kernel(
     part[(long long)blockIdx.y * per + e] = s;
 }
 
-// drel[e] += sum over chunks of part[chunk][e], in chunk order.
+// drel[e] += sum over chunks of part[chunk][e], in chunk order (16 loads
+// ahead of their adds).
 __global__ __launch_bounds__(256) void attn_drel_sum_kernel(const float *__restrict__ part,
                                                             int nchunk, long long per,
                                                             float *drel) {
     const long long e = (long long)blockIdx.x * 256 + threadIdx.x;
     if (e >= per) return;
     float s = 0.f;
-    for (int k = 0; k < nchunk; k++) s += part[(long long)k * per + e];
+    for (int k0 = 0; k0 < nchunk; k0 += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = part[(long long)min(k0 + u, nchunk - 1) * per + e];
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (k0 + u < nchunk) s += v[u];
+    }
     drel[e] += s;
 }
 
@@ -1034,9 +1086,25 @@ int attn_forward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_desc
         if (rc) return rc;
     }
     const long long rows = (long long)n * h * tq;
-    attn_softmax_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
-        p, tau, rel, tab.dev, rows, (int)h, (int)tq, (int)tk, (int)d->nrel,
-        d->mask_diag ? 1 : 0);
+    {
+        const unsigned grid = (unsigned)rnn_div_up((size_t)rows, 4);
+        const int m = d->mask_diag ? 1 : 0;
+        auto sm = [&](auto kern) {
+            kern<<<grid, 256, 0, ctx->stream>>>(p, tau, rel, tab.dev, rows, (int)h, (int)tq,
+                                                (int)tk, (int)d->nrel, m);
+        };
+        switch (rnn_div_up(tk, (size_t)64)) {
+            case 1: sm(attn_softmax_rows_kernel<1>); break;
+            case 2: sm(attn_softmax_rows_kernel<2>); break;
+            case 3: sm(attn_softmax_rows_kernel<3>); break;
+            case 4: sm(attn_softmax_rows_kernel<4>); break;
+            case 5: sm(attn_softmax_rows_kernel<5>); break;
+            case 6: sm(attn_softmax_rows_kernel<6>); break;
+            case 7: sm(attn_softmax_rows_kernel<7>); break;
+            case 8: sm(attn_softmax_rows_kernel<8>); break;
+            default: sm(attn_softmax_rows_kernel<0>); break;
+        }
+    }
     RNN_LAUNCHED(ctx);
     for (size_t hd = 0; hd < h; hd++) {
         int rc = rnn_gemm_launch_ld(ctx, n, tq, dh, tk, p + hd * tq * tk, tk, h * tq * tk, 0,
@@ -1059,7 +1127,10 @@ int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_des
     const size_t cnt = tq * tk, mat = n * h * cnt;
     const long long rows = (long long)n * h * tq;
     const size_t per = h * d->nrel;
-    const size_t ipc = rnn_div_up(n, (size_t)16), nchunk = rnn_div_up(n, ipc);
+    // drel partials over chunks of ipc images: enough chunks to fill the
+    // chip (16 chunks left it latency-bound: 61 us a call at the rustvit's
+    // cross-attention shape)
+    const size_t ipc = rnn_div_up(n, (size_t)64), nchunk = rnn_div_up(n, ipc);
     WsCarve cv;
     const size_t o1 = cv.take(mat * 4), o2 = cv.take(mat * 4), o3 = cv.take((size_t)rows * 8);
     const size_t o4 = cv.take(nchunk * per * 4);

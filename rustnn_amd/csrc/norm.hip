@@ -590,15 +590,38 @@ __global__ __launch_bounds__(NT) void dw3_bwd_w_kernel(int th, int tw, int c, in
 // One block per image (norm.rs:488-519): s_j = sum_k x[j][k] p[k] in k order;
 // w = softmax(s) with a sequential sum and a multiply by 1/sum;
 // z[k] = sum_j w_j x[j][k] in j order.  s, w live in LDS (t <= SP_MAXT).
+// XL: the image's x [t][c] is first staged into LDS by the whole block
+// (coalesced float4 loads), so the per-token and per-channel chains read
+// LDS; the sums keep the orders above.
 constexpr int SP_MAXT = 1024;
+constexpr size_t SP_XL_BYTES = 96 * 1024;  // x staged in LDS up to this size
 
+// The image's x into xl ([t][c], dynamic LDS), 16 bytes a thread when c % 4 == 0.
+__device__ __forceinline__ void seqpool_stage(const float *__restrict__ xi, int t, int c,
+                                              float *xl) {
+    const int tot = t * c;
+    if ((c & 3) == 0 && ((uintptr_t)xi & 15) == 0) {
+        for (int e = threadIdx.x * 4; e < tot; e += NT * 4)
+            *reinterpret_cast<float4 *>(xl + e) = *reinterpret_cast<const float4 *>(xi + e);
+    } else {
+        for (int e = threadIdx.x; e < tot; e += NT) xl[e] = xi[e];
+    }
+    __syncthreads();
+}
+
+template <bool XL>
 __global__ __launch_bounds__(NT) void seqpool_fwd_kernel(int t, int c, const float *__restrict__ x,
                                                          const float *__restrict__ p,
                                                          float *__restrict__ z,
                                                          float *__restrict__ wout) {
     __shared__ float w[SP_MAXT];
+    extern __shared__ float xl[];
     const size_t im = blockIdx.x;
     const float *xi = x + im * t * c;
+    if constexpr (XL) {
+        seqpool_stage(xi, t, c, xl);
+        xi = xl;
+    }
     for (int j = threadIdx.x; j < t; j += NT) {
         float s = 0.0f;
         for (int k = 0; k < c; k++) s += xi[(size_t)j * c + k] * p[k];
@@ -628,6 +651,7 @@ __global__ __launch_bounds__(NT) void seqpool_fwd_kernel(int t, int c, const flo
 // Backward, one block per image (norm.rs:530-572): dw_j = sum_k dz_k x[j][k];
 // dot = sum_j dw_j w_j; ds_j = w_j (dw_j - dot); dx[j][k] = w_j dz_k +
 // ds_j p_k; the image's share of dp, sum_j ds_j x[j][k], into part[image][k].
+template <bool XL>
 __global__ __launch_bounds__(NT) void seqpool_bwd_kernel(int t, int c, const float *__restrict__ dz,
                                                          const float *__restrict__ wsave,
                                                          const float *__restrict__ x,
@@ -636,8 +660,13 @@ __global__ __launch_bounds__(NT) void seqpool_bwd_kernel(int t, int c, const flo
                                                          float *__restrict__ part) {
     __shared__ float dw[SP_MAXT];
     __shared__ float dot_s;
+    extern __shared__ float xl[];
     const size_t im = blockIdx.x;
     const float *xi = x + im * t * c, *dzi = dz + im * c, *wi = wsave + im * t;
+    if constexpr (XL) {
+        seqpool_stage(xi, t, c, xl);
+        xi = xl;
+    }
     for (int j = threadIdx.x; j < t; j += NT) {
         float s = 0.0f;
         for (int k = 0; k < c; k++) s += dzi[k] * xi[(size_t)j * c + k];
@@ -666,13 +695,21 @@ __global__ __launch_bounds__(NT) void seqpool_bwd_kernel(int t, int c, const flo
     }
 }
 
-// out[k] += sum over images of part[image][k] (image order, f64).
+// out[k] += sum over images of part[image][k] (image order, f64; 16 loads
+// ahead of their adds).
 __global__ void rowsum_add_kernel(size_t n, int c, const float *__restrict__ part,
                                   float *__restrict__ out) {
     const int k = blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= c) return;
     double s = 0.0;
-    for (size_t i = 0; i < n; i++) s += part[i * c + k];
+    for (size_t i0 = 0; i0 < n; i0 += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = part[min(i0 + u, n - 1) * c + k];
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (i0 + u < n) s += v[u];
+    }
     out[k] += (float)s;
 }
 
@@ -1015,7 +1052,19 @@ int rnn_seqpool_forward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float 
     if (t == 0 || t > SP_MAXT || n > 0x7fffffff || !dims_ok(n * t, c))
         return rnn_fail(ctx, RNN_E_INVALID, "seqpool: n %zu, t %zu (1..%d), c %zu", n, t, SP_MAXT,
                         c);
-    seqpool_fwd_kernel<<<(unsigned)n, NT, 0, ctx->stream>>>((int)t, (int)c, x, p, z, w);
+    const size_t xl = t * c * sizeof(float);
+    if (xl <= SP_XL_BYTES) {
+        static bool attr = false;
+        if (!attr) {
+            attr = true;
+            (void)hipFuncSetAttribute((const void *)seqpool_fwd_kernel<true>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)SP_XL_BYTES);
+        }
+        seqpool_fwd_kernel<true><<<(unsigned)n, NT, xl, ctx->stream>>>((int)t, (int)c, x, p, z, w);
+    } else {
+        seqpool_fwd_kernel<false><<<(unsigned)n, NT, 0, ctx->stream>>>((int)t, (int)c, x, p, z, w);
+    }
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -1032,7 +1081,21 @@ int rnn_seqpool_backward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float
                         c);
     float *part = (float *)rnn_workspace(ctx, n * c * sizeof(float));
     if (!part) return RNN_E_NOMEM;
-    seqpool_bwd_kernel<<<(unsigned)n, NT, 0, ctx->stream>>>((int)t, (int)c, dz, w, x, p, dx, part);
+    const size_t xl = t * c * sizeof(float);
+    if (xl <= SP_XL_BYTES) {
+        static bool attr = false;
+        if (!attr) {
+            attr = true;
+            (void)hipFuncSetAttribute((const void *)seqpool_bwd_kernel<true>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)SP_XL_BYTES);
+        }
+        seqpool_bwd_kernel<true><<<(unsigned)n, NT, xl, ctx->stream>>>((int)t, (int)c, dz, w, x,
+                                                                       p, dx, part);
+    } else {
+        seqpool_bwd_kernel<false><<<(unsigned)n, NT, 0, ctx->stream>>>((int)t, (int)c, dz, w, x,
+                                                                        p, dx, part);
+    }
     RNN_LAUNCHED(ctx);
     rowsum_add_kernel<<<(unsigned)rnn_div_up(c, (size_t)NT), NT, 0, ctx->stream>>>(n, (int)c, part,
                                                                                    dp);
