@@ -1079,12 +1079,11 @@ int attn_forward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_desc
                        const float *q, const float *kv, const float *tau, const float *rel,
                        float *p, float *o) {
     const size_t tq = d->tq, tk = d->tk, dh = d->dh, h = d->h, c = h * dh;
-    for (size_t hd = 0; hd < h; hd++) {
-        int rc = rnn_gemm_launch_ld(ctx, n, tq, tk, dh, q + d->qoff + hd * dh, d->qstride,
-                                    tq * d->qstride, 0, kv + d->koff + hd * dh, d->kvstride,
-                                    tk * d->kvstride, 1, p + hd * tq * tk, tk, h * tq * tk, 0);
-        if (rc) return rc;
-    }
+    // S = Q K^T for every (image, head) in one launch
+    int rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, q + d->qoff, d->qstride, tq * d->qstride,
+                                 dh, 0, kv + d->koff, d->kvstride, tk * d->kvstride, dh, 1, p, tk,
+                                 h * tq * tk, tq * tk, 0);
+    if (rc) return rc;
     const long long rows = (long long)n * h * tq;
     {
         const unsigned grid = (unsigned)rnn_div_up((size_t)rows, 4);
@@ -1106,13 +1105,10 @@ int attn_forward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_desc
         }
     }
     RNN_LAUNCHED(ctx);
-    for (size_t hd = 0; hd < h; hd++) {
-        int rc = rnn_gemm_launch_ld(ctx, n, tq, dh, tk, p + hd * tq * tk, tk, h * tq * tk, 0,
-                                    kv + d->voff + hd * dh, d->kvstride, tk * d->kvstride, 0,
-                                    o + hd * dh, c, tq * c, 0);
-        if (rc) return rc;
-    }
-    return RNN_OK;
+    // O = P V
+    return rnn_gemm_launch_ld2(ctx, n, h, tq, dh, tk, p, tk, h * tq * tk, tq * tk, 0,
+                               kv + d->voff, d->kvstride, tk * d->kvstride, dh, 0, o, c, tq * c,
+                               dh, 0);
 }
 
 // Core::backward on the composed path: dV = P^T dO, dP = dO V^T, the raw S
@@ -1139,23 +1135,20 @@ int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_des
     float *s1 = (float *)(ws + o1), *s2 = (float *)(ws + o2);
     double *part = (double *)(ws + o3);
     float *rpart = (float *)(ws + o4);
-    for (size_t hd = 0; hd < h; hd++) {
-        // dV += P^T dO (attn.rs:262-270)
-        int rc = rnn_gemm_launch_ld(ctx, n, tk, dh, tq, p + hd * cnt, tk, h * cnt, 1,
-                                    dout + hd * dh, c, tq * c, 0, dkv + d->voff + hd * dh,
-                                    d->kvstride, tk * d->kvstride, acc_kv);
-        if (rc) return rc;
-        // dP = dO V^T (attn.rs:272-278)
-        rc = rnn_gemm_launch_ld(ctx, n, tq, tk, dh, dout + hd * dh, c, tq * c, 0,
-                                kv + d->voff + hd * dh, d->kvstride, tk * d->kvstride, 1,
-                                s1 + hd * cnt, tk, h * cnt, 0);
-        if (rc) return rc;
-        // the raw scores again (attn.rs:292-300)
-        rc = rnn_gemm_launch_ld(ctx, n, tq, tk, dh, q + d->qoff + hd * dh, d->qstride,
-                                tq * d->qstride, 0, kv + d->koff + hd * dh, d->kvstride,
-                                tk * d->kvstride, 1, s2 + hd * cnt, tk, h * cnt, 0);
-        if (rc) return rc;
-    }
+    // each GEMM over every (image, head) in one launch
+    // dV += P^T dO (attn.rs:262-270)
+    int rc = rnn_gemm_launch_ld2(ctx, n, h, tk, dh, tq, p, tk, h * cnt, cnt, 1, dout, c, tq * c,
+                                 dh, 0, dkv + d->voff, d->kvstride, tk * d->kvstride, dh, acc_kv);
+    if (rc) return rc;
+    // dP = dO V^T (attn.rs:272-278)
+    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, dout, c, tq * c, dh, 0, kv + d->voff,
+                             d->kvstride, tk * d->kvstride, dh, 1, s1, tk, h * cnt, cnt, 0);
+    if (rc) return rc;
+    // the raw scores again (attn.rs:292-300)
+    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, q + d->qoff, d->qstride, tq * d->qstride, dh,
+                             0, kv + d->koff, d->kvstride, tk * d->kvstride, dh, 1, s2, tk,
+                             h * cnt, cnt, 0);
+    if (rc) return rc;
     attn_dsoft_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
         p, s1, s2, tau, part, rows, (int)h, (int)tq, (int)tk);
     RNN_LAUNCHED(ctx);
@@ -1171,19 +1164,15 @@ int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_des
     attn_drel_sum_kernel<<<(unsigned)rnn_div_up(per, (size_t)256), 256, 0, ctx->stream>>>(
         rpart, (int)nchunk, (long long)per, drel);
     RNN_LAUNCHED(ctx);
-    for (size_t hd = 0; hd < h; hd++) {
-        // dQ += (tau dS) K (attn.rs:317-322)
-        int rc = rnn_gemm_launch_ld(ctx, n, tq, dh, tk, s2 + hd * cnt, tk, h * cnt, 0,
-                                    kv + d->koff + hd * dh, d->kvstride, tk * d->kvstride, 0,
-                                    dq + d->qoff + hd * dh, d->qstride, tq * d->qstride, acc_q);
-        if (rc) return rc;
-        // dK += (tau dS)^T Q (attn.rs:324-330)
-        rc = rnn_gemm_launch_ld(ctx, n, tk, dh, tq, s2 + hd * cnt, tk, h * cnt, 1,
-                                q + d->qoff + hd * dh, d->qstride, tq * d->qstride, 0,
-                                dkv + d->koff + hd * dh, d->kvstride, tk * d->kvstride, acc_kv);
-        if (rc) return rc;
-    }
-    return RNN_OK;
+    // dQ += (tau dS) K (attn.rs:317-322)
+    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, dh, tk, s2, tk, h * cnt, cnt, 0, kv + d->koff,
+                             d->kvstride, tk * d->kvstride, dh, 0, dq + d->qoff, d->qstride,
+                             tq * d->qstride, dh, acc_q);
+    if (rc) return rc;
+    // dK += (tau dS)^T Q (attn.rs:324-330)
+    return rnn_gemm_launch_ld2(ctx, n, h, tk, dh, tq, s2, tk, h * cnt, cnt, 1, q + d->qoff,
+                               d->qstride, tq * d->qstride, dh, 0, dkv + d->koff, d->kvstride,
+                               tk * d->kvstride, dh, acc_kv);
 }
 
 

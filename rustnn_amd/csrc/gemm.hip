@@ -27,7 +27,12 @@ struct GemmArgs {
     const float *a, *b;
     float *c;
     const float *bias;     // per output column, may be null
-    long long stride_a, stride_b, stride_c;  // per z
+    long long stride_a, stride_b, stride_c;  // per z1 (z1 = z % zc1)
+    // A second batch level: problem z covers z1 = z % zc1 and z2 = z / zc1,
+    // operands at base + z1 * stride + z2 * stride2 (zc1 = the count and
+    // stride2 = 0 for a plain batch).
+    int zc1;
+    long long stride_a2, stride_b2, stride_c2;
     int M, N;
     int kchunk, ktotal;    // problem z covers k = min(kchunk, ktotal - z*kchunk)
     int lda, ldb, ldc;
@@ -38,6 +43,12 @@ struct GemmArgs {
     float *rsum_out;
     double *rsum_part;
 };
+
+__device__ __forceinline__ long long zoff(const GemmArgs &g, long long z, long long s1,
+                                          long long s2) {
+    const unsigned zu = (unsigned)z, c1 = (unsigned)g.zc1;  // z < 65536
+    return (long long)(zu % c1) * s1 + (long long)(zu / c1) * s2;
+}
 
 // 4 consecutive elements starting at p[0], p[step], ... with bounds
 // (count valid), zero elsewhere.
@@ -410,7 +421,8 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
     const int lane = threadIdx.x & 63, wave = wave_index(), lr = lane & 31, lh = lane >> 5;
     const bool rsum = RS && n0 == 0 && (wave & 1) == 0;
     Tile t;
-    if (!t.run(g.a + z * g.stride_a, g.lda, g.M, g.b + z * g.stride_b, g.ldb, g.N, kz, m0, n0,
+    if (!t.run(g.a + zoff(g, z, g.stride_a, g.stride_a2), g.lda, g.M,
+               g.b + zoff(g, z, g.stride_b, g.stride_b2), g.ldb, g.N, kz, m0, n0,
                rsum, lds))
         return;
     if (rsum) {
@@ -428,7 +440,7 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
             }
         }
     }
-    float *Cp = g.c + z * g.stride_c;
+    float *Cp = g.c + zoff(g, z, g.stride_c, g.stride_c2);
     t.each([&](int r, int c, float val) {
         const int row = m0 + r, col = n0 + c;
         if (row < g.M && col < g.N) {
@@ -445,9 +457,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     __shared__ float As[2][BM * LDK];
     __shared__ float Bs[2][BN * LDK];
     const long long z = blockIdx.z;
-    const float *A = g.a + z * g.stride_a;
-    const float *B = g.b + z * g.stride_b;
-    float *Cp = g.c + z * g.stride_c;
+    const float *A = g.a + zoff(g, z, g.stride_a, g.stride_a2);
+    const float *B = g.b + zoff(g, z, g.stride_b, g.stride_b2);
+    float *Cp = g.c + zoff(g, z, g.stride_c, g.stride_c2);
     const int kz = min(g.kchunk, g.ktotal - (int)z * g.kchunk);
     // XCD-aware tile order: workgroup L of a problem runs on XCD L % 8, so
     // XCD x takes the x-th contiguous run of tiles (row-major over (m, n)):
@@ -759,7 +771,8 @@ static int gemm_enqueue(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k
                         size_t ktotal, const float *a, size_t stride_a, int lda, int at,
                         const float *b, size_t stride_b, int ldb, int bt, float *c,
                         size_t stride_c, int ldc, int acc, const float *bias,
-                        float *rs_out = nullptr, double *rs_part = nullptr) {
+                        float *rs_out = nullptr, double *rs_part = nullptr, size_t zc1 = 0,
+                        size_t stride_a2 = 0, size_t stride_b2 = 0, size_t stride_c2 = 0) {
     if (m > INT32_MAX || n > INT32_MAX || ktotal > INT32_MAX || count > 65535)
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "gemm: dimension beyond 32-bit tile indexing");
     GemmArgs g;
@@ -780,12 +793,18 @@ static int gemm_enqueue(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k
     g.acc = acc;
     g.rsum_out = rs_out;
     g.rsum_part = rs_part;
+    g.zc1 = (int)(zc1 ? zc1 : count);
+    g.stride_a2 = (long long)stride_a2;
+    g.stride_b2 = (long long)stride_b2;
+    g.stride_c2 = (long long)stride_c2;
     // float4 loads along k need 16-byte aligned rows of the k-contiguous operands.
     bool vec = true;
-    if (!at) vec = vec && aligned16(a) && (lda % 4 == 0) && (stride_a % 4 == 0);
-    if (bt) vec = vec && aligned16(b) && (ldb % 4 == 0) && (stride_b % 4 == 0);
+    if (!at) vec = vec && aligned16(a) && (lda % 4 == 0) && (stride_a % 4 == 0) &&
+                   (stride_a2 % 4 == 0);
+    if (bt) vec = vec && aligned16(b) && (ldb % 4 == 0) && (stride_b % 4 == 0) &&
+                  (stride_b2 % 4 == 0);
     size_t tiles128 = rnn_div_up(m, 128) * rnn_div_up(n, 128) * count;
-    if (dma_enabled() &&
+    if (dma_enabled() && stride_a2 % 4 == 0 && stride_b2 % 4 == 0 &&
         dma_ok(count, m, n, kchunk, ktotal, a, stride_a, lda, at, b, stride_b, ldb, bt)) {
         // 128 x 128 tiles only from four tiles per CU: below that the 64 x 64
         // grid's extra workgroups hide more latency than the larger tile's
@@ -840,6 +859,19 @@ int rnn_gemm_launch_ld(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k,
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "gemm: leading dimension beyond 32 bits");
     return gemm_enqueue(ctx, count, m, n, k, k * count, a, stride_a, (int)lda, at, b, stride_b,
                         (int)ldb, bt, c, stride_c, (int)ldc, acc, nullptr);
+}
+
+int rnn_gemm_launch_ld2(rnn_ctx *ctx, size_t count1, size_t count2, size_t m, size_t n, size_t k,
+                        const float *a, size_t lda, size_t stride_a, size_t stride_a2, int at,
+                        const float *b, size_t ldb, size_t stride_b, size_t stride_b2, int bt,
+                        float *c, size_t ldc, size_t stride_c, size_t stride_c2, int acc) {
+    if (lda > INT32_MAX || ldb > INT32_MAX || ldc > INT32_MAX)
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "gemm: leading dimension beyond 32 bits");
+    const size_t count = count1 * count2;
+    if (count == 0) return RNN_OK;
+    return gemm_enqueue(ctx, count, m, n, k, k * count, a, stride_a, (int)lda, at, b, stride_b,
+                        (int)ldb, bt, c, stride_c, (int)ldc, acc, nullptr, nullptr, nullptr,
+                        count1, stride_a2, stride_b2, stride_c2);
 }
 
 static int fill(rnn_ctx *ctx, float *p, size_t len, float v) {

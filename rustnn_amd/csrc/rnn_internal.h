@@ -237,6 +237,13 @@ bool ns_dma_ok(const NsGemmProb &p, size_t count);
 int rnn_gemm_launch_ld(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
                        size_t lda, size_t stride_a, int at, const float *b, size_t ldb,
                        size_t stride_b, int bt, float *c, size_t ldc, size_t stride_c, int acc);
+// The same over a two-level batch in one launch: problem (z1, z2), z1 <
+// count1, z2 < count2, takes its operands at a + z1 stride_a + z2 stride_a2
+// (likewise B and C).  count1 * count2 <= 65535.
+int rnn_gemm_launch_ld2(rnn_ctx *ctx, size_t count1, size_t count2, size_t m, size_t n, size_t k,
+                        const float *a, size_t lda, size_t stride_a, size_t stride_a2, int at,
+                        const float *b, size_t ldb, size_t stride_b, size_t stride_b2, int bt,
+                        float *c, size_t ldc, size_t stride_c, size_t stride_c2, int acc);
 
 int rnn_gemm_launch(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k, const float *a,
                     size_t stride_a, int at, const float *b, size_t stride_b, int bt, float *c,
