@@ -50,6 +50,19 @@ int rnn_ctx_create(int device, rnn_ctx **out);
 int rnn_ctx_destroy(rnn_ctx *ctx);
 /* Use `stream` (a hipStream_t; NULL = the null stream) for later calls. */
 int rnn_ctx_set_stream(rnn_ctx *ctx, void *stream);
+/* Deferred parameter-gradient reductions (no counterpart in the reference:
+ * a launch-count device).  While on, the backward entry points whose last
+ * step only sums partial results into a parameter gradient leave that step
+ * queued: rnn_linear_backward (dW when split over rows, and db),
+ * rnn_ln_backward / rnn_ln_backward_add (dgamma, dbeta), the LayerScale
+ * backwards (dl), rnn_dwconv3_backward (dw, db) and the column sums.
+ * rnn_ctx_flush runs every queued reduction in one launch, in call order,
+ * with the same sums in the same order as the immediate path (results are
+ * bit-identical); those gradients are complete only after it.  Turning
+ * deferral off flushes first.  The partials stay in a context arena that
+ * grows (hipMalloc) when a step needs more. */
+int rnn_ctx_set_defer(rnn_ctx *ctx, int on);
+int rnn_ctx_flush(rnn_ctx *ctx);
 void *rnn_ctx_stream(rnn_ctx *ctx);
 int rnn_ctx_synchronize(rnn_ctx *ctx);
 const char *rnn_ctx_last_error(rnn_ctx *ctx);

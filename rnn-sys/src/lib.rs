@@ -62,6 +62,8 @@ extern "C" {
     pub fn rnn_ctx_create(device: c_int, out: *mut *mut rnn_ctx) -> c_int;
     pub fn rnn_ctx_destroy(ctx: *mut rnn_ctx) -> c_int;
     pub fn rnn_ctx_set_stream(ctx: *mut rnn_ctx, stream: *mut c_void) -> c_int;
+    pub fn rnn_ctx_set_defer(ctx: *mut rnn_ctx, on: c_int) -> c_int;
+    pub fn rnn_ctx_flush(ctx: *mut rnn_ctx) -> c_int;
     pub fn rnn_ctx_stream(ctx: *mut rnn_ctx) -> *mut c_void;
     pub fn rnn_ctx_synchronize(ctx: *mut rnn_ctx) -> c_int;
     pub fn rnn_ctx_last_error(ctx: *mut rnn_ctx) -> *const c_char;

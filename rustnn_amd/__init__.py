@@ -95,6 +95,8 @@ def lib():
             "rnn_ctx_set_stream": (_i, [_vp, _vp]),
             "rnn_ctx_stream": (_vp, [_vp]),
             "rnn_ctx_synchronize": (_i, [_vp]),
+            "rnn_ctx_set_defer": (_i, [_vp, _i]),
+            "rnn_ctx_flush": (_i, [_vp]),
             "rnn_ctx_last_error": (C.c_char_p, [_vp]),
             "rnn_status_string": (C.c_char_p, [_i]),
             "rnn_ctx_workspace_bytes": (_sz, [_vp]),
@@ -266,6 +268,14 @@ class Context:
 
     def synchronize(self):
         self.check(lib().rnn_ctx_synchronize(self.h))
+
+    def set_defer(self, on):
+        """Deferred parameter-gradient reductions on / off (off flushes)."""
+        self.check(lib().rnn_ctx_set_defer(self.h, 1 if on else 0))
+
+    def flush(self):
+        """Runs the queued parameter-gradient reductions (one launch)."""
+        self.check(lib().rnn_ctx_flush(self.h))
 
     def workspace_bytes(self) -> int:
         return int(lib().rnn_ctx_workspace_bytes(self.h))

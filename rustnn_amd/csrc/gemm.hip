@@ -622,21 +622,10 @@ __global__ void splitk_reduce_kernel(const float *part, int nz, long long len, f
         // the split-K row sums of op(A): rout[m] += sum_z rpart[z][m], z in order
         const long long m = e - len;
         if (!rpart || m >= rlen) return;
-        double t = 0.0;
-        for (int z = 0; z < nz; z++) t += rpart[(long long)z * rlen + m];
-        rout[m] += (float)t;
+        rnn_rows64_sum(rpart, nz, rlen, rout, m);
         return;
     }
-    float s = 0.f;
-    for (int z0 = 0; z0 < nz; z0 += 8) {
-        float v[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = z0 + i < nz ? part[(long long)(z0 + i) * len + e] : 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            if (z0 + i < nz) s = (z0 + i == 0) ? v[i] : s + v[i];
-    }
-    out[e] = accumulate ? out[e] + s : s;
+    rnn_chunk_sum(part, nz, len, out, accumulate, e);
 }
 
 // PackedA::pack / pack_t layout (gemm.rs:54-113): element e of block q =
@@ -892,7 +881,8 @@ int rnn_colsum_launch(rnn_ctx *ctx, size_t rows, size_t cols, const float *x, fl
 // the C tiles alone cannot fill the chip; the chunk partials are added into C
 // in chunk order (deterministic).  Returns -1 when splitting does not pay.
 static int gemm_splitk(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, int at,
-                       const float *b, int bt, float *c, int acc, float *rsum = nullptr) {
+                       const float *b, int bt, float *c, int acc, float *rsum = nullptr,
+                       bool deferrable = false) {
     const size_t tiles = rnn_div_up(m, 64) * rnn_div_up(n, 64);
     if (tiles >= (size_t)ctx->num_cus || k < 1024) return -1;
     // about three workgroups per CU, each over at least 512 values of k
@@ -902,8 +892,12 @@ static int gemm_splitk(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *
     if (nz <= 1) return -1;
     const size_t kchunk = rnn_round_up(rnn_div_up(k, nz), 16);
     nz = rnn_div_up(k, kchunk);
+    // a parameter gradient's partials wait in the deferral arena when the
+    // context defers (the flush adds them into C, and into rsum)
+    const bool defer = deferrable && ctx->defer;
     const size_t pbytes = rnn_round_up(nz * m * n * sizeof(float), 256);
-    float *part = (float *)rnn_workspace(ctx, pbytes + (rsum ? nz * m * sizeof(double) : 0));
+    const size_t bytes = pbytes + (rsum ? nz * m * sizeof(double) : 0);
+    float *part = (float *)(defer ? rnn_defer_take(ctx, bytes) : rnn_workspace(ctx, bytes));
     if (!part) return RNN_E_NOMEM;
     double *rpart = rsum ? (double *)((char *)part + pbytes) : nullptr;
     // chunk z of A: rows z*kchunk of [k x m] (at) or columns z*kchunk of [m x k]
@@ -912,6 +906,26 @@ static int gemm_splitk(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *
     int rc = gemm_enqueue(ctx, nz, m, n, kchunk, k, a, sa, lda, at, b, sb, ldb, bt, part, m * n,
                           (int)n, 0, nullptr, nullptr, rpart);
     if (rc) return rc;
+    if (defer) {
+        RnnDeferSeg sg{};
+        sg.part = part;
+        sg.out0 = c;
+        sg.len = (long long)(m * n);
+        sg.nrow = (int)nz;
+        sg.kind = RNN_DEFER_CHUNKS;
+        sg.acc = acc;
+        rnn_defer_push(ctx, sg);
+        if (rsum) {
+            RnnDeferSeg sr{};
+            sr.part = rpart;
+            sr.out0 = rsum;
+            sr.len = (long long)m;
+            sr.nrow = (int)nz;
+            sr.kind = RNN_DEFER_ROWS64;
+            rnn_defer_push(ctx, sr);
+        }
+        return RNN_OK;
+    }
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3(rnn_div_up(m * n + (rsum ? m : 0), 256)),
                        dim3(256), 0, ctx->stream, part, (int)nz, (long long)(m * n), c, acc,
                        (const double *)rpart, (int)m, rsum);
@@ -991,13 +1005,15 @@ int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, cons
     // the direct-to-LDS kernel, else by the column-sum kernels
     int rc;
     if (db && rows && fout && fin && dw_rowsum_ok(fout, fin, rows, dy, x)) {
-        rc = gemm_splitk(ctx, fout, fin, rows, dy, 1, x, 0, dw, 1, db);
+        rc = gemm_splitk(ctx, fout, fin, rows, dy, 1, x, 0, dw, 1, db, true);
         if (rc == -1)
             rc = gemm_enqueue(ctx, 1, fout, fin, rows, rows, dy, 0, (int)fout, 1, x, 0, (int)fin,
                               0, dw, 0, (int)fin, 1, nullptr, db, nullptr);
         if (rc) return rc;
     } else {
-        rc = rnn_matmul_dw(ctx, fout, fin, rows, dy, x, dw);
+        rc = rows && fout && fin ? gemm_splitk(ctx, fout, fin, rows, dy, 1, x, 0, dw, 1, nullptr, true)
+                                 : RNN_OK;
+        if (rc == -1) rc = rnn_matmul_dw(ctx, fout, fin, rows, dy, x, dw);
         if (rc) return rc;
         if (db && rows && fout) {
             rc = rnn_colsum_launch(ctx, rows, fout, dy, db);

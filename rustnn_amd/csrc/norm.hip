@@ -362,29 +362,8 @@ __global__ __launch_bounds__(NT) void colsum_red_kernel(int nblk, size_t len, si
                                                         const double *__restrict__ part,
                                                         float *__restrict__ out0,
                                                         float *__restrict__ out1) {
-    constexpr int NG = NT / CS_RED_COLS;
-    __shared__ double red[NG][CS_RED_COLS];
-    const int jl = threadIdx.x % CS_RED_COLS, q = threadIdx.x / CS_RED_COLS;
-    const size_t j = (size_t)blockIdx.x * CS_RED_COLS + jl, jc = min(j, len - 1);
-    const int G = (nblk + NG - 1) / NG, k0 = min(nblk, q * G), k1 = min(nblk, k0 + G);
-    double s = 0.0;
-    for (int k = k0; k < k1; k += 8) {
-        double v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = part[(size_t)min(k + u, k1 - 1) * len + jc];
-#pragma unroll
-        for (int u = 0; u < 8; u++)
-            if (k + u < k1) s += v[u];
-    }
-    red[q][jl] = s;
-    __syncthreads();
-    if (q != 0 || j >= len) return;
-    double t = red[0][jl];
-    for (int g = 1; g < NG; g++) t += red[g][jl];
-    if (j < split)
-        out0[j] += (float)t;
-    else
-        out1[j - split] += (float)t;
+    static_assert(NT == 256 && CS_RED_COLS == 16, "rnn_colsum_red_block's shape");
+    rnn_colsum_red_block(nblk, len, split, part, out0, out1, blockIdx.x);
 }
 
 // ------------------------------------------------------------ LayerScale
@@ -719,6 +698,34 @@ unsigned ew_grid(size_t len) {
 
 }  // namespace
 
+// Partial rows of a column reduction: in the workspace, or -- when the
+// context defers parameter-gradient reductions -- in its arena until the
+// flush.
+static double *col_part(rnn_ctx *ctx, size_t bytes) {
+    return (double *)(ctx->defer ? rnn_defer_take(ctx, bytes) : rnn_workspace(ctx, bytes));
+}
+
+// Stage 2 of a column reduction (colsum_red_kernel), launched now or queued.
+static int col_reduce(rnn_ctx *ctx, size_t nblk, size_t len, size_t split, const double *part,
+                      float *out0, float *out1) {
+    if (ctx->defer) {
+        RnnDeferSeg sg{};
+        sg.part = part;
+        sg.out0 = out0;
+        sg.out1 = out1;
+        sg.len = (long long)len;
+        sg.split = (long long)split;
+        sg.nrow = (int)nblk;
+        sg.kind = RNN_DEFER_COLS;
+        rnn_defer_push(ctx, sg);
+        return RNN_OK;
+    }
+    colsum_red_kernel<<<(unsigned)rnn_div_up(len, (size_t)CS_RED_COLS), NT, 0, ctx->stream>>>(
+        (int)nblk, len, split, part, out0, out1);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
 // Column sums of a*b (b set) and of a over rows, added into outab / outa.
 // Many short chains: blocks of CS_ROWS rows x 64 columns (colsum_part_kernel),
 // then the blocks' partials in order, 16 groups per column (colsum_red_kernel).
@@ -729,15 +736,13 @@ int rnn_colsum_f64(rnn_ctx *ctx, size_t rows, int c, const float *a, const float
     if (nblk > 65535) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "column sums: too many rows");
     const int nout = (b ? 1 : 0) + (outa ? 1 : 0);
     const size_t len = (size_t)nout * c;
-    double *part = (double *)rnn_workspace(ctx, nblk * len * sizeof(double));
+    double *part = col_part(ctx, nblk * len * sizeof(double));
     if (!part) return RNN_E_NOMEM;
     colsum_part_kernel<<<dim3((unsigned)rnn_div_up((size_t)c, (size_t)64), (unsigned)nblk), NT, 0,
                          ctx->stream>>>(rows, c, a, b, outa != nullptr, rs, rpi, part);
     RNN_LAUNCHED(ctx);
-    colsum_red_kernel<<<(unsigned)rnn_div_up(len, (size_t)CS_RED_COLS), NT, 0, ctx->stream>>>(
-        (int)nblk, len, (size_t)(b ? c : len), part, b ? outab : outa, b ? outa : nullptr);
-    RNN_LAUNCHED(ctx);
-    return RNN_OK;
+    return col_reduce(ctx, nblk, len, (size_t)(b ? c : len), part, b ? outab : outa,
+                      b ? outa : nullptr);
 }
 
 namespace {
@@ -797,7 +802,7 @@ static int ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, con
         // one pass: dx and the column sums' partials, then their reduction
         const size_t nblk = rnn_div_up(rows, (size_t)RB_ROWS);
         if (nblk > 0x7fffffff) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "ln_backward: rows");
-        double *part = (double *)rnn_workspace(ctx, nblk * 2 * c * sizeof(double));
+        double *part = col_part(ctx, nblk * 2 * c * sizeof(double));
         if (!part) return RNN_E_NOMEM;
         auto cs = [&](auto kern) {
             kern<<<(unsigned)nblk, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, add,
@@ -814,10 +819,7 @@ static int ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, con
             default: cs(ln_bwd_cs_kernel<8>); break;
         }
         RNN_LAUNCHED(ctx);
-        colsum_red_kernel<<<(unsigned)rnn_div_up(2 * c, (size_t)CS_RED_COLS), NT, 0,
-                            ctx->stream>>>((int)nblk, 2 * c, c, part, dg, db);
-        RNN_LAUNCHED(ctx);
-        return RNN_OK;
+        return col_reduce(ctx, nblk, 2 * c, c, part, dg, db);
     }
     int rc = colsum_add(ctx, rows, (int)c, dy, xhat, dg, db);
     if (rc) return rc;
@@ -885,7 +887,7 @@ static int ls_backward_cs(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, 
                           const float *l, const float *mask, size_t rpi, float *dx, float *dl) {
     const size_t nblk = rnn_div_up(rows, (size_t)RB_ROWS);
     if (nblk > 0x7fffffff) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "layerscale: rows");
-    double *part = (double *)rnn_workspace(ctx, nblk * c * sizeof(double));
+    double *part = col_part(ctx, nblk * c * sizeof(double));
     if (!part) return RNN_E_NOMEM;
     auto cs = [&](auto kern) {
         kern<<<(unsigned)nblk, NT, 0, ctx->stream>>>(rows, (int)c, dy, x, l, mask, rpi, dx, part);
@@ -901,10 +903,7 @@ static int ls_backward_cs(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, 
         default: cs(ls_bwd_cs_kernel<8>); break;
     }
     RNN_LAUNCHED(ctx);
-    colsum_red_kernel<<<(unsigned)rnn_div_up(c, (size_t)CS_RED_COLS), NT, 0, ctx->stream>>>(
-        (int)nblk, c, c, part, dl, nullptr);
-    RNN_LAUNCHED(ctx);
-    return RNN_OK;
+    return col_reduce(ctx, nblk, c, c, part, dl, nullptr);
 }
 
 int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *x,
@@ -1028,15 +1027,14 @@ int rnn_dwconv3_backward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c,
     const size_t nrb = std::min(th, want), RB = rnn_div_up(th, nrb);
     const size_t nrb_used = rnn_div_up(th, RB), nblk = n * nrb_used;
     if (nblk > 65535) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "dwconv3: too many images");
-    double *part = (double *)rnn_workspace(ctx, nblk * 10 * c * sizeof(double));
+    double *part = col_part(ctx, nblk * 10 * c * sizeof(double));
     if (!part) return RNN_E_NOMEM;
     dw3_bwd_w_kernel<<<dim3((unsigned)cblk, (unsigned)nblk), NT, 0, ctx->stream>>>(
         (int)th, (int)tw, (int)c, (int)RB, (int)nrb_used, dy, x, part);
     RNN_LAUNCHED(ctx);
     // part is [nblk][10c]: taps 0-8 (dW's [9][c] order), then db
-    colsum_red_kernel<<<(unsigned)rnn_div_up(10 * c, (size_t)CS_RED_COLS), NT, 0, ctx->stream>>>(
-        (int)nblk, 10 * c, 9 * c, part, dw, db);
-    RNN_LAUNCHED(ctx);
+    int rc = col_reduce(ctx, nblk, 10 * c, 9 * c, part, dw, db);
+    if (rc) return rc;
     const size_t len = n * th * tw * c;
     dw3_bwd_x_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)tw, (int)c, dy, w, dx);
     RNN_LAUNCHED(ctx);

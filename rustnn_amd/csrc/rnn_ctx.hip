@@ -6,6 +6,8 @@
 // only grows, so steady-state calls never allocate.
 #include "rnn_internal.h"
 
+#include <algorithm>
+
 #include <cstring>
 
 // The fixed scratch of the no-allocation entry points: partial results that
@@ -108,6 +110,100 @@ void rnn_dev_table_free(RnnDevTable &t) {
     t.host.clear();
 }
 
+// ------------------------------------------ deferred gradient reductions
+void *rnn_defer_take(rnn_ctx *ctx, size_t bytes) {
+    bytes = rnn_round_up(std::max<size_t>(bytes, 1), 256);
+    while (ctx->dblk < ctx->darena.size()) {
+        auto &b = ctx->darena[ctx->dblk];
+        if (ctx->doff + bytes <= b.second) {
+            void *p = b.first + ctx->doff;
+            ctx->doff += bytes;
+            return p;
+        }
+        ctx->dblk++;
+        ctx->doff = 0;
+    }
+    // a new block (earlier blocks keep their pending partials)
+    const size_t want = std::max<size_t>(bytes, (size_t)64 << 20);
+    char *mem = nullptr;
+    hipError_t e = hipMalloc((void **)&mem, want);
+    if (e != hipSuccess) {
+        rnn_fail(ctx, RNN_E_NOMEM, "deferred partials hipMalloc(%zu): %s", want,
+                 hipGetErrorString(e));
+        return nullptr;
+    }
+    ctx->darena.emplace_back(mem, want);
+    ctx->dblk = ctx->darena.size() - 1;
+    ctx->doff = bytes;
+    return mem;
+}
+
+void rnn_defer_push(rnn_ctx *ctx, const RnnDeferSeg &s) { ctx->dsegs.push_back(s); }
+
+namespace {
+
+constexpr int DEFER_BATCH = 48;  // segments per launch (kernel arguments by value)
+
+struct DeferBatch {
+    RnnDeferSeg seg[DEFER_BATCH];
+    unsigned blk0[DEFER_BATCH + 1];  // first block of each segment, then the total
+    int nseg;
+};
+
+unsigned defer_blocks(const RnnDeferSeg &s) {
+    return (unsigned)(s.kind == RNN_DEFER_COLS ? rnn_div_up((size_t)s.len, (size_t)16)
+                                               : rnn_div_up((size_t)s.len, (size_t)256));
+}
+
+// Every queued reduction of a batch: block b serves the segment whose block
+// range holds it, with the code of that segment's own reduction kernel.
+__global__ __launch_bounds__(256) void deferred_reduce_kernel(DeferBatch b) {
+    int lo = 0, hi = b.nseg - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (b.blk0[mid] <= blockIdx.x)
+            lo = mid;
+        else
+            hi = mid - 1;
+    }
+    const RnnDeferSeg &s = b.seg[lo];
+    const unsigned blk = blockIdx.x - b.blk0[lo];
+    if (s.kind == RNN_DEFER_COLS) {
+        rnn_colsum_red_block(s.nrow, (size_t)s.len, (size_t)s.split, (const double *)s.part,
+                             s.out0, s.out1, blk);
+        return;
+    }
+    const long long e = (long long)blk * 256 + threadIdx.x;
+    if (e >= s.len) return;
+    if (s.kind == RNN_DEFER_CHUNKS)
+        rnn_chunk_sum((const float *)s.part, s.nrow, s.len, s.out0, s.acc, e);
+    else
+        rnn_rows64_sum((const double *)s.part, s.nrow, s.len, s.out0, e);
+}
+
+int defer_flush(rnn_ctx *ctx) {
+    for (size_t i0 = 0; i0 < ctx->dsegs.size(); i0 += DEFER_BATCH) {
+        DeferBatch b{};
+        b.nseg = (int)std::min<size_t>(DEFER_BATCH, ctx->dsegs.size() - i0);
+        unsigned tot = 0;
+        for (int k = 0; k < b.nseg; k++) {
+            b.seg[k] = ctx->dsegs[i0 + k];
+            b.blk0[k] = tot;
+            tot += defer_blocks(b.seg[k]);
+        }
+        b.blk0[b.nseg] = tot;
+        if (tot == 0) continue;
+        hipLaunchKernelGGL(deferred_reduce_kernel, dim3(tot), dim3(256), 0, ctx->stream, b);
+        RNN_LAUNCHED(ctx);
+    }
+    ctx->dsegs.clear();
+    ctx->dblk = 0;
+    ctx->doff = 0;
+    return RNN_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char *rnn_status_string(int s) {
@@ -153,6 +249,7 @@ int rnn_ctx_destroy(rnn_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    for (auto &b : ctx->darena) (void)hipFree(b.first);
     for (auto &t : ctx->rel_tables) {
         if (t.dev) (void)hipFree(t.dev);
         if (t.pinned) (void)hipHostFree(t.pinned);
@@ -176,6 +273,23 @@ int rnn_ctx_set_stream(rnn_ctx *ctx, void *stream) {
 }
 
 void *rnn_ctx_stream(rnn_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int rnn_ctx_set_defer(rnn_ctx *ctx, int on) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (!on && !ctx->dsegs.empty()) {
+        const int rc = defer_flush(ctx);
+        if (rc) return rc;
+    }
+    ctx->defer = on != 0;
+    return RNN_OK;
+}
+
+int rnn_ctx_flush(rnn_ctx *ctx) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    return defer_flush(ctx);
+}
 
 int rnn_ctx_synchronize(rnn_ctx *ctx) {
     if (!ctx) return RNN_E_NULL;

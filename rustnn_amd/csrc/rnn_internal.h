@@ -32,6 +32,22 @@ struct RnnRelTable {
     uint32_t *pinned = nullptr;  // the upload's staging, kept with the table
 };
 
+// One deferred parameter-gradient reduction (rnn_ctx_set_defer): partial
+// rows left in the context's arena by a backward entry point, summed into
+// the gradient at the flush by the same code, in the same order, as the
+// entry point's own reduction kernel would have.
+enum {
+    RNN_DEFER_COLS = 0,    // f64 rows [nrow][len], 16 groups of rows (rnn_colsum_red_block)
+    RNN_DEFER_CHUNKS = 1,  // f32 rows [nrow][len] in row order (rnn_chunk_sum)
+    RNN_DEFER_ROWS64 = 2,  // f64 rows [nrow][len] in row order (rnn_rows64_sum)
+};
+struct RnnDeferSeg {
+    const void *part;
+    float *out0, *out1;  // COLS: columns j < split go to out0[j], the rest to out1[j - split]
+    long long len, split;
+    int nrow, kind, acc;  // CHUNKS: acc = 0 overwrites out0
+};
+
 struct rnn_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -52,9 +68,80 @@ struct rnn_ctx {
     size_t rel_last = 0;  // the table the last attention call used
     // Tensor-list tables of the optimizer entry points (slot -> table).
     std::map<int, RnnDevTable> tables;
+    // Deferred parameter-gradient reductions: on, the pending segments in
+    // call order, and the arena their partials live in until the flush
+    // (device blocks kept across flushes; block `dblk`, offset `doff` next).
+    bool defer = false;
+    std::vector<RnnDeferSeg> dsegs;
+    std::vector<std::pair<char *, size_t>> darena;
+    size_t dblk = 0, doff = 0;
     std::recursive_mutex mu;
     char err[512] = {0};
 };
+
+// Device memory that stays untouched until the next rnn_ctx_flush (deferred
+// partials); null (with the error recorded) when it cannot be allocated.
+void *rnn_defer_take(rnn_ctx *ctx, size_t bytes);
+// Queues a reduction for the flush.
+void rnn_defer_push(rnn_ctx *ctx, const RnnDeferSeg &s);
+
+// Block `blk` of a column reduction: columns [16 blk, 16 blk + 16) of part
+// [nblk][len] (f64), each summed over the rows in 16 consecutive groups --
+// each group in order, 8 loads ahead -- then the group sums in order, and
+// added into out0[j] (j < split) or out1[j - split].  256 threads.
+__device__ __forceinline__ void rnn_colsum_red_block(int nblk, size_t len, size_t split,
+                                                     const double *__restrict__ part,
+                                                     float *__restrict__ out0,
+                                                     float *__restrict__ out1, unsigned blk) {
+    constexpr int COLS = 16, NG = 256 / COLS;
+    __shared__ double red[NG][COLS];
+    const int jl = threadIdx.x % COLS, q = threadIdx.x / COLS;
+    const size_t j = (size_t)blk * COLS + jl, jc = min(j, len - 1);
+    const int G = (nblk + NG - 1) / NG, k0 = min(nblk, q * G), k1 = min(nblk, k0 + G);
+    double s = 0.0;
+    for (int k = k0; k < k1; k += 8) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = part[(size_t)min(k + u, k1 - 1) * len + jc];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (k + u < k1) s += v[u];
+    }
+    red[q][jl] = s;
+    __syncthreads();
+    if (q != 0 || j >= len) return;
+    double t = red[0][jl];
+    for (int g = 1; g < NG; g++) t += red[g][jl];
+    if (j < split)
+        out0[j] += (float)t;
+    else
+        out1[j - split] += (float)t;
+}
+
+// Element e of a chunk reduction: out[e] (+)= sum_z part[z][e] (f32, z in
+// order, 8 loads ahead of their adds).
+__device__ __forceinline__ void rnn_chunk_sum(const float *part, int nz, long long len, float *out,
+                                              int accumulate, long long e) {
+    float s = 0.f;
+    for (int z0 = 0; z0 < nz; z0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = z0 + i < nz ? part[(long long)(z0 + i) * len + e] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (z0 + i < nz) s = (z0 + i == 0) ? v[i] : s + v[i];
+    }
+    out[e] = accumulate ? out[e] + s : s;
+}
+
+// Element m of an f64 row reduction: out[m] += (float) sum_z part[z][m], z in
+// order.
+__device__ __forceinline__ void rnn_rows64_sum(const double *part, int nz, long long len,
+                                               float *out, long long m) {
+    double t = 0.0;
+    for (int z = 0; z < nz; z++) t += part[(long long)z * len + m];
+    out[m] += (float)t;
+}
 
 // Size of the fixed device scratch behind rnn_conv2d_backward_w_noalloc.
 #define RNN_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)

@@ -787,6 +787,9 @@ class ViTStep:
         self.step = 0
         self.norm = None
         self.lr = None
+        # the backward's parameter-gradient reductions queued and run in one
+        # launch at its end (rnn_ctx_set_defer; bit-identical results)
+        self.defer = True
 
     def __call__(self, x, labels, coarse, perm=None, lam=None, lr=None, wd=None):
         """One step; returns (total loss, hits against the dominant labels)
@@ -799,8 +802,7 @@ class ViTStep:
         """The first half of Trainer::step (train.rs:348-362): targets, the
         DropPath seed, forward, build_loss, backward (gradients accumulate in
         the parameters).  Returns (total, correct, the output dict)."""
-        import torch
-        from .loss import ce_soft, hint_mse, kl_distill, mix_dominant, soft_targets
+        from .loss import mix_dominant, soft_targets
         hp, net, ctx = self.hp, self.net, self.net.ctx
         nf, n = net.nclass, labels.numel()
         taxo = not hp["no_taxo"]
@@ -808,6 +810,18 @@ class ViTStep:
                               hp["sib"], coarse, self.nc, perm, lam, ctx=ctx)
         dom = labels if perm is None else mix_dominant(labels, perm, lam, ctx=ctx)
         net.drop_seed = self.rng.next_u64()
+        if self.defer:
+            ctx.set_defer(True)
+        try:
+            return self._forward_backward(x, labels, coarse, tf, tc, dom, n, taxo)
+        finally:
+            if self.defer:
+                ctx.set_defer(False)  # flushes: every gradient complete
+
+    def _forward_backward(self, x, labels, coarse, tf, tc, dom, n, taxo):
+        import torch
+        from .loss import ce_soft, hint_mse, kl_distill
+        hp, net, ctx = self.hp, self.net, self.net.ctx
         out = net.forward(x, True)
         # build_loss (train.rs:70-118); the total adds its terms in the
         # reference's order and grouping, in f32

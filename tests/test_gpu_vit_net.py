@@ -291,6 +291,25 @@ def test_trainer_step_default_batch128(rnn, orc, vit):
           f"f32 floor) {worst[0]:.2e} {worst[1]:.2e} {worst[2]:.2e}; device vs oracle {e:.2e}")
 
 
+def test_deferred_reductions_bit_identical(rnn, orc, vit):
+    """ViTStep queues its backward's parameter-gradient reductions and runs
+    them in one launch (rnn_ctx_set_defer / rnn_ctx_flush): every gradient
+    equals the immediate path's bit for bit (default network, batch 128)."""
+    from rustnn_amd.vit import RustViT, ViTStep
+    n = 128
+    x, labels, coarse, parent = config4_inputs(orc, n, 2027)
+    grads = []
+    for defer in (False, True):
+        net = RustViT(None, _i32(parent), 20, seed=99)
+        tr = ViTStep(net, _i32(parent), 20)
+        tr.defer = defer
+        tr.forward_backward(to_dev(x).reshape(x.shape), _i32(labels), _i32(coarse))
+        grads.append([to_host(p.g).ravel().copy() for p in net.params()])
+    assert len(grads[0]) == len(grads[1])
+    for i, (a, b) in enumerate(zip(*grads)):
+        assert np.array_equal(a, b), i
+
+
 def test_reference_vitcheck_on_gpu(rnn, orc, vit):
     """vitcheck (check.rs:163-180) through the device layers: normcheck,
     attncheck (SelfAttn, CrossAttn over a 6x6 memory with dmem, a reader Block
