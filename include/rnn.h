@@ -55,7 +55,8 @@ int rnn_ctx_set_stream(rnn_ctx *ctx, void *stream);
  * step only sums partial results into a parameter gradient leave that step
  * queued: rnn_linear_backward (dW when split over rows, and db),
  * rnn_ln_backward / rnn_ln_backward_add (dgamma, dbeta), the LayerScale
- * backwards (dl), rnn_dwconv3_backward (dw, db) and the column sums.
+ * backwards (dl), rnn_dwconv3_backward (dw, db), the column sums and
+ * rnn_attn_backward up to 64 tokens (dtau, drel).
  * rnn_ctx_flush runs every queued reduction in one launch, in call order,
  * with the same sums in the same order as the immediate path (results are
  * bit-identical); those gradients are complete only after it.  Turning

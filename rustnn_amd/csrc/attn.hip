@@ -583,66 +583,10 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs g) {
 // sums images [j*G, j*G + G) of element e with the loads issued ahead of the
 // in-order adds, then the 8 partials are added in j order (fixed order:
 // bit-reproducible).  The dtau partials are f64 and summed in f64.
-constexpr int ATTN_RED_PARTS = 8;
 __global__ __launch_bounds__(256) void attn_reduce_kernel(const double *dtau_part,
                                                           const float *drel_part, int n, int h,
                                                           int nrel, float *dtau, float *drel) {
-    __shared__ double part[ATTN_RED_PARTS][32];
-    const int el = threadIdx.x & 31, j = threadIdx.x >> 5;
-    const int e = blockIdx.x * 32 + el;
-    const int per = h * nrel;
-    const bool is_rel = e < per, live = e < per + h;
-    const long long stride = is_rel ? per : h;
-    const int G = (n + ATTN_RED_PARTS - 1) / ATTN_RED_PARTS;
-    const int i0 = j * G, i1 = min(n, i0 + G);
-    // the value added to, loaded ahead (its latency overlaps the partials')
-    float old = 0.f;
-    if (j == 0 && live) old = is_rel ? drel[e] : dtau[e - per];
-    double s = 0.0;
-    if (live && is_rel) {
-        float fs = 0.f;
-        const float *src = drel_part + e;
-        for (int b = i0; b < i1; b += 16) {
-            float v[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) v[u] = b + u < i1 ? src[(long long)(b + u) * stride] : 0.f;
-#pragma unroll
-            for (int u = 0; u < 16; u++)
-                if (b + u < i1) fs = (b + u == i0) ? v[u] : fs + v[u];
-        }
-        s = fs;
-    } else if (live) {
-        const double *src = dtau_part + (e - per);
-        for (int b = i0; b < i1; b += 16) {
-            double v[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) v[u] = b + u < i1 ? src[(long long)(b + u) * stride] : 0.0;
-#pragma unroll
-            for (int u = 0; u < 16; u++)
-                if (b + u < i1) s += v[u];
-        }
-    }
-    part[j][el] = s;
-    __syncthreads();
-    if (j == 0 && live) {
-        if (is_rel) {
-            float t = 0.f;
-            bool first = true;
-            for (int q = 0; q < ATTN_RED_PARTS; q++) {
-                if (q * G >= n) break;
-                t = first ? (float)part[q][el] : t + (float)part[q][el];
-                first = false;
-            }
-            drel[e] = old + t;
-        } else {
-            double t = 0.0;
-            for (int q = 0; q < ATTN_RED_PARTS; q++) {
-                if (q * G >= n) break;
-                t += part[q][el];
-            }
-            dtau[e - per] = old + (float)t;
-        }
-    }
+    rnn_attn_reduce_block(dtau_part, drel_part, n, h, nrel, dtau, drel, blockIdx.x);
 }
 
 // Columns [off, off + width) of `rows` rows of stride `stride` set to 0:
@@ -1261,7 +1205,10 @@ int rnn_attn_backward_ex(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const f
     AttnArgs g;
     fill_args(g, *tab, d, n);
     const size_t tau_bytes = rnn_round_up(n * d->h * sizeof(double), 256);
-    char *ws = (char *)rnn_workspace(ctx, tau_bytes + n * d->h * (size_t)d->nrel * sizeof(float));
+    const size_t ws_bytes = tau_bytes + n * d->h * (size_t)d->nrel * sizeof(float);
+    // the dtau / drel partials wait in the deferral arena when the context
+    // defers parameter-gradient reductions
+    char *ws = (char *)(ctx->defer ? rnn_defer_take(ctx, ws_bytes) : rnn_workspace(ctx, ws_bytes));
     if (!ws) return RNN_E_NOMEM;
     g.q = q;
     g.kv = kv;
@@ -1284,6 +1231,19 @@ int rnn_attn_backward_ex(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const f
     RNN_HIP(ctx, hipLaunchKernel(bwd_kernel(dhp, nt, vec, acc), dim3((unsigned)(n * d->h)),
                                  dim3(nth), args, bwd_lds(dhp), ctx->stream));
     int tot = (int)(d->h * d->nrel + d->h);
+    if (ctx->defer) {
+        RnnDeferSeg sg{};
+        sg.part = g.dtau_part;
+        sg.part2 = g.drel_part;
+        sg.out0 = drel;
+        sg.out1 = dtau;
+        sg.len = tot;
+        sg.split = (long long)(d->h * d->nrel);
+        sg.nrow = (int)n;
+        sg.kind = RNN_DEFER_ATTN;
+        rnn_defer_push(ctx, sg);
+        return RNN_OK;
+    }
     hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rnn_div_up(tot, 32)), dim3(256), 0,
                        ctx->stream, (const double *)g.dtau_part, (const float *)g.drel_part, (int)n,
                        (int)d->h, (int)d->nrel, dtau, drel);

@@ -151,8 +151,8 @@ struct DeferBatch {
 };
 
 unsigned defer_blocks(const RnnDeferSeg &s) {
-    return (unsigned)(s.kind == RNN_DEFER_COLS ? rnn_div_up((size_t)s.len, (size_t)16)
-                                               : rnn_div_up((size_t)s.len, (size_t)256));
+    const size_t per = s.kind == RNN_DEFER_COLS ? 16 : s.kind == RNN_DEFER_ATTN ? 32 : 256;
+    return (unsigned)rnn_div_up((size_t)s.len, per);
 }
 
 // Every queued reduction of a batch: block b serves the segment whose block
@@ -171,6 +171,12 @@ __global__ __launch_bounds__(256) void deferred_reduce_kernel(DeferBatch b) {
     if (s.kind == RNN_DEFER_COLS) {
         rnn_colsum_red_block(s.nrow, (size_t)s.len, (size_t)s.split, (const double *)s.part,
                              s.out0, s.out1, blk);
+        return;
+    }
+    if (s.kind == RNN_DEFER_ATTN) {
+        const int h = (int)(s.len - s.split);
+        rnn_attn_reduce_block((const double *)s.part, (const float *)s.part2, s.nrow, h,
+                              (int)(s.split / h), s.out1, s.out0, blk);
         return;
     }
     const long long e = (long long)blk * 256 + threadIdx.x;

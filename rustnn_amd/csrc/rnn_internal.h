@@ -40,9 +40,12 @@ enum {
     RNN_DEFER_COLS = 0,    // f64 rows [nrow][len], 16 groups of rows (rnn_colsum_red_block)
     RNN_DEFER_CHUNKS = 1,  // f32 rows [nrow][len] in row order (rnn_chunk_sum)
     RNN_DEFER_ROWS64 = 2,  // f64 rows [nrow][len] in row order (rnn_rows64_sum)
+    RNN_DEFER_ATTN = 3,    // attention dtau / drel (rnn_attn_reduce_block): part = dtau
+                           // partials, part2 = drel partials, out0 = drel, out1 = dtau,
+                           // len = h*nrel + h, split = h*nrel, nrow = n images
 };
 struct RnnDeferSeg {
-    const void *part;
+    const void *part, *part2;
     float *out0, *out1;  // COLS: columns j < split go to out0[j], the rest to out1[j - split]
     long long len, split;
     int nrow, kind, acc;  // CHUNKS: acc = 0 overwrites out0
@@ -132,6 +135,73 @@ __device__ __forceinline__ void rnn_chunk_sum(const float *part, int nz, long lo
             if (z0 + i < nz) s = (z0 + i == 0) ? v[i] : s + v[i];
     }
     out[e] = accumulate ? out[e] + s : s;
+}
+
+// Block `blk` of the attention parameter reduction (32 outputs a block, 256
+// threads): drel[e] (e < h*nrel) += the f32 sum of drel_part[i][e] over the
+// n (image) rows, dtau[e - h*nrel] += the f64 sum of dtau_part[i][...], each
+// over 8 consecutive groups of rows in order, then the group sums in order.
+__device__ __forceinline__ void rnn_attn_reduce_block(const double *dtau_part,
+                                                      const float *drel_part, int n, int h,
+                                                      int nrel, float *dtau, float *drel,
+                                                      unsigned blk) {
+    constexpr int ATTN_RED_PARTS = 8;
+    __shared__ double part[ATTN_RED_PARTS][32];
+    const int el = threadIdx.x & 31, j = threadIdx.x >> 5;
+    const int e = (int)blk * 32 + el;
+    const int per = h * nrel;
+    const bool is_rel = e < per, live = e < per + h;
+    const long long stride = is_rel ? per : h;
+    const int G = (n + ATTN_RED_PARTS - 1) / ATTN_RED_PARTS;
+    const int i0 = j * G, i1 = min(n, i0 + G);
+    // the value added to, loaded ahead (its latency overlaps the partials')
+    float old = 0.f;
+    if (j == 0 && live) old = is_rel ? drel[e] : dtau[e - per];
+    double s = 0.0;
+    if (live && is_rel) {
+        float fs = 0.f;
+        const float *src = drel_part + e;
+        for (int b = i0; b < i1; b += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = b + u < i1 ? src[(long long)(b + u) * stride] : 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (b + u < i1) fs = (b + u == i0) ? v[u] : fs + v[u];
+        }
+        s = fs;
+    } else if (live) {
+        const double *src = dtau_part + (e - per);
+        for (int b = i0; b < i1; b += 16) {
+            double v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = b + u < i1 ? src[(long long)(b + u) * stride] : 0.0;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (b + u < i1) s += v[u];
+        }
+    }
+    part[j][el] = s;
+    __syncthreads();
+    if (j == 0 && live) {
+        if (is_rel) {
+            float t = 0.f;
+            bool first = true;
+            for (int q = 0; q < ATTN_RED_PARTS; q++) {
+                if (q * G >= n) break;
+                t = first ? (float)part[q][el] : t + (float)part[q][el];
+                first = false;
+            }
+            drel[e] = old + t;
+        } else {
+            double t = 0.0;
+            for (int q = 0; q < ATTN_RED_PARTS; q++) {
+                if (q * G >= n) break;
+                t += part[q][el];
+            }
+            dtau[e - per] = old + (float)t;
+        }
+    }
 }
 
 // Element m of an f64 row reduction: out[m] += (float) sum_z part[z][m], z in
