@@ -511,6 +511,71 @@ __global__ void dw3_bwd_x_kernel(size_t n, int th, int tw, int c, const float *_
     }
 }
 
+// The same two passes for c % 4 == 0 with 16-byte rows: block (x, oy, img)
+// covers output row oy of image img, one thread per (column, channel quad),
+// 32-bit indexing.  The nine taps' inputs load unconditionally from clamped
+// addresses before the adds, which skip the taps outside the image in the
+// reference's order, so the sums are the ones above bit for bit.
+__device__ __forceinline__ float4 fma4(float4 acc, float4 w, float4 x) {
+    return make_float4(acc.x + w.x * x.x, acc.y + w.y * x.y, acc.z + w.z * x.z, acc.w + w.w * x.w);
+}
+
+__global__ __launch_bounds__(NT) void dw3_fwd4_kernel(int th, int tw, int c4,
+                                                      const float4 *__restrict__ x,
+                                                      const float4 *__restrict__ w,
+                                                      const float4 *__restrict__ b,
+                                                      float4 *__restrict__ y) {
+#pragma clang fp contract(off)
+    const int e = blockIdx.x * NT + threadIdx.x;
+    if (e >= tw * c4) return;
+    const int oy = blockIdx.y, img = blockIdx.z;
+    const int ox = e / c4, cq = e - ox * c4;
+    const float4 *xi = x + (size_t)img * th * tw * c4;
+    float4 xv[9], wv[9];
+#pragma unroll
+    for (int t = 0; t < 9; t++) {
+        const int sy = min(max(oy + t / 3 - 1, 0), th - 1), sx = min(max(ox + t % 3 - 1, 0), tw - 1);
+        xv[t] = xi[(sy * tw + sx) * c4 + cq];
+        wv[t] = w[t * c4 + cq];
+    }
+    float4 acc = b[cq];
+#pragma unroll
+    for (int t = 0; t < 9; t++) {
+        const int sy = oy + t / 3 - 1, sx = ox + t % 3 - 1;
+        if (sy >= 0 && sy < th && sx >= 0 && sx < tw) acc = fma4(acc, wv[t], xv[t]);
+    }
+    y[((size_t)img * th * tw + (size_t)oy * tw + ox) * c4 + cq] = acc;
+}
+
+__global__ __launch_bounds__(NT) void dw3_bwd_x4_kernel(int th, int tw, int c4,
+                                                        const float4 *__restrict__ dy,
+                                                        const float4 *__restrict__ w,
+                                                        float4 *__restrict__ dx) {
+#pragma clang fp contract(off)
+    const int e = blockIdx.x * NT + threadIdx.x;
+    if (e >= tw * c4) return;
+    const int sy = blockIdx.y, img = blockIdx.z;
+    const int sx = e / c4, cq = e - sx * c4;
+    const float4 *di = dy + (size_t)img * th * tw * c4;
+    // tap t = 8 - u, u = 0..8: output (sy - ky + 1, sx - kx + 1)
+    float4 dv[9], wv[9];
+#pragma unroll
+    for (int u = 0; u < 9; u++) {
+        const int t = 8 - u;
+        const int oy = min(max(sy - t / 3 + 1, 0), th - 1), ox = min(max(sx - t % 3 + 1, 0), tw - 1);
+        dv[u] = di[(oy * tw + ox) * c4 + cq];
+        wv[u] = w[t * c4 + cq];
+    }
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 9; u++) {
+        const int t = 8 - u;
+        const int oy = sy - t / 3 + 1, ox = sx - t % 3 + 1;
+        if (oy >= 0 && oy < th && ox >= 0 && ox < tw) acc = fma4(acc, wv[u], dv[u]);
+    }
+    dx[((size_t)img * th * tw + (size_t)sy * tw + sx) * c4 + cq] = acc;
+}
+
 // dW [9][c] and db [c] partials over output rows [rb*RB, rb*RB + RB) of
 // image im (block y = im * nrb + rb): thread = channel, f64 sums in (output
 // row, output column, tap) order (norm.rs:377-418).  The 3x3 input window
@@ -697,6 +762,13 @@ unsigned ew_grid(size_t len) {
 }
 
 }  // namespace
+
+// The float4 depthwise passes: channels a multiple of 4, 16-byte aligned
+// tensors, images within the grid's z range.
+static bool dw3_vec(const void *a, const void *w, const void *out, size_t c, size_t n) {
+    return c % 4 == 0 && n <= 65535 && ((uintptr_t)a & 15) == 0 && ((uintptr_t)w & 15) == 0 &&
+           ((uintptr_t)out & 15) == 0;
+}
 
 // Partial rows of a column reduction: in the workspace, or -- when the
 // context defers parameter-gradient reductions -- in its arena until the
@@ -1006,7 +1078,15 @@ int rnn_dwconv3_forward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, 
     if (th > 65536 || tw > 65536 || !dims_ok(n * th * tw, c))
         return rnn_fail(ctx, RNN_E_INVALID, "dwconv3: %zu x %zu x %zu x %zu", n, th, tw, c);
     const size_t len = n * th * tw * c;
-    dw3_fwd_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)tw, (int)c, x, w, b, y);
+    if (dw3_vec(x, w, y, c, n) && b && ((uintptr_t)b & 15) == 0) {
+        const int c4 = (int)(c / 4);
+        dw3_fwd4_kernel<<<dim3((unsigned)rnn_div_up(tw * c4, (size_t)NT), (unsigned)th, (unsigned)n),
+                          NT, 0, ctx->stream>>>((int)th, (int)tw, c4, (const float4 *)x,
+                                                (const float4 *)w, (const float4 *)b, (float4 *)y);
+    } else {
+        dw3_fwd_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)tw, (int)c, x, w, b,
+                                                             y);
+    }
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -1036,7 +1116,16 @@ int rnn_dwconv3_backward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c,
     int rc = col_reduce(ctx, nblk, 10 * c, 9 * c, part, dw, db);
     if (rc) return rc;
     const size_t len = n * th * tw * c;
-    dw3_bwd_x_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)tw, (int)c, dy, w, dx);
+    if (dw3_vec(dy, w, dx, c, n)) {
+        const int c4 = (int)(c / 4);
+        dw3_bwd_x4_kernel<<<dim3((unsigned)rnn_div_up(tw * c4, (size_t)NT), (unsigned)th,
+                                 (unsigned)n),
+                            NT, 0, ctx->stream>>>((int)th, (int)tw, c4, (const float4 *)dy,
+                                                  (const float4 *)w, (float4 *)dx);
+    } else {
+        dw3_bwd_x_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)tw, (int)c, dy, w,
+                                                               dx);
+    }
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
