@@ -152,11 +152,24 @@ __global__ void rows_total_kernel(size_t n, const float *__restrict__ part, floa
                                   float *__restrict__ out, const uint32_t *__restrict__ hit,
                                   uint32_t *__restrict__ correct) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    // in row order, 16 loads ahead of their adds
     float s = 0.0f;
     uint32_t h = 0;
-    for (size_t i = 0; i < n; i++) {
-        s += part[i];
-        if (hit) h += hit[i];
+    for (size_t i0 = 0; i0 < n; i0 += 16) {
+        float v[16];
+        uint32_t u16[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const size_t i = min(i0 + u, n - 1);
+            v[u] = part[i];
+            u16[u] = hit ? hit[i] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (i0 + u < n) {
+                s += v[u];
+                h += u16[u];
+            }
     }
     if (out) *out = s * mul1 * mul2;
     if (correct) *correct = h;

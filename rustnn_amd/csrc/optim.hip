@@ -94,8 +94,16 @@ __global__ __launch_bounds__(OPT_THREADS) void muon_momentum_kernel(const NsMat 
 __global__ __launch_bounds__(OPT_THREADS) void ns_load_kernel(const NsMat *__restrict__ mats,
                                                               int nmat) {
     const NsMat mt = mats[mat_of(mats, nmat, blockIdx.x)];
+    // the partials in chunk order, 16 loads ahead of their adds
     double ss = 0.0;
-    for (uint32_t k = 0; k < mt.nchunk; k++) ss += mt.part[k];
+    for (uint32_t k0 = 0; k0 < mt.nchunk; k0 += 16) {
+        double v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = mt.part[min(k0 + u, mt.nchunk - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (k0 + u < mt.nchunk) ss += v[u];
+    }
     const float norm = sqrtf((float)ss) + 1e-7f;
     const float inv = 1.0f / norm;
     const size_t len = (size_t)mt.rows * mt.cols;

@@ -130,6 +130,37 @@ __global__ void taxo_bwd_kernel(size_t n, int nf, int nc, const uint32_t *__rest
     }
 }
 
+// The same for nc <= TAXO_LDS_NC: the row's accumulators in LDS (the adds in
+// j order, as above), its dzf values loaded 16 ahead; 64 rows a block.
+constexpr int TAXO_LDS_NC = 128;
+__global__ __launch_bounds__(64) void taxo_bwd_lds_kernel(size_t n, int nf, int nc,
+                                                          const uint32_t *__restrict__ parent,
+                                                          const float *__restrict__ dzf,
+                                                          const float *__restrict__ dzc,
+                                                          float *__restrict__ dc) {
+    extern __shared__ float acc[];  // [64][nc + 1]
+    const size_t i = (size_t)blockIdx.x * 64 + threadIdx.x;
+    if (i >= n) return;
+    float *a = acc + threadIdx.x * (nc + 1);
+    for (int k = 0; k < nc; k++) a[k] = dzc[i * nc + k];
+    const float *dr = dzf + i * nf;
+    for (int j0 = 0; j0 < nf; j0 += 16) {
+        float v[16];
+        uint32_t pv[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int j = min(j0 + u, nf - 1);
+            v[u] = dr[j];
+            pv[u] = parent[j];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++)
+            if (j0 + u < nf && pv[u] < (uint32_t)nc) a[pv[u]] += v[u];
+    }
+    float *cr = dc + i * nc;
+    for (int k = 0; k < nc; k++) cr[k] = a[k];
+}
+
 // [n][c][hw] <-> [n][hw][c] (Tok::from_tensor / to_tensor): 32 x 32 tiles
 // through LDS so both sides are read and written along rows.
 __global__ __launch_bounds__(NT) void nchw_tok_kernel(int c, int hw, const float *__restrict__ src,
@@ -274,8 +305,13 @@ int rnn_taxo_head_combine_backward(rnn_ctx *ctx, size_t n, size_t nf, size_t nc,
         return rnn_fail(ctx, RNN_E_NULL, "taxo_head_backward: null operand");
     if (nf > (1u << 24) || nc > (1u << 24))
         return rnn_fail(ctx, RNN_E_INVALID, "taxo_head: nf %zu nc %zu", nf, nc);
-    taxo_bwd_kernel<<<(unsigned)rnn_div_up(n, (size_t)NT), NT, 0, ctx->stream>>>(
-        n, (int)nf, (int)nc, parent, dzf, dzc, dc);
+    if (nc <= (size_t)TAXO_LDS_NC)
+        taxo_bwd_lds_kernel<<<(unsigned)rnn_div_up(n, (size_t)64), 64,
+                              64 * (nc + 1) * sizeof(float), ctx->stream>>>(
+            n, (int)nf, (int)nc, parent, dzf, dzc, dc);
+    else
+        taxo_bwd_kernel<<<(unsigned)rnn_div_up(n, (size_t)NT), NT, 0, ctx->stream>>>(
+            n, (int)nf, (int)nc, parent, dzf, dzc, dc);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
