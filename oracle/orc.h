@@ -190,6 +190,9 @@ float orc_powi(float a, int b);
 void orc_newton_schulz(float *g, size_t rows, size_t cols, size_t steps);
 void orc_muon_step(float *v, float *g, float *m, size_t rows, size_t cols, int decay, float lr,
                    float wd, float mom, size_t ns_steps);
+void orc_muon_steps(size_t nmat, float *const *v, float *const *g, float *const *m,
+                    const size_t *rows, const size_t *cols, const int *decay, float lr, float wd,
+                    float mom, size_t ns_steps, int threads);
 void orc_adam_step(size_t n, float *v, float *g, float *m, float *v2, int decay, float lr,
                    float wd, float b1, float b2, float eps, size_t t);
 float orc_clip(float *g, const size_t *lens, size_t nseg, float max);

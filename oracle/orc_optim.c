@@ -87,6 +87,20 @@ void orc_muon_step(float *v, float *g, float *m, size_t rows, size_t cols, int d
     }
 }
 
+/* The Muon branch of Optim::step_all over a list of parameters, which the
+ * reference runs as a rayon par_iter over the parameters (optim.rs:177-196):
+ * one OpenMP loop over the matrices, each updated by orc_muon_step on one
+ * thread (the GEMM regions inside are nested, so they run serially).  The
+ * updates touch disjoint arrays, so the result equals orc_muon_step called
+ * per matrix in any order.  Used to time the CPU baseline. */
+void orc_muon_steps(size_t nmat, float *const *v, float *const *g, float *const *m,
+                    const size_t *rows, const size_t *cols, const int *decay, float lr, float wd,
+                    float mom, size_t ns_steps, int threads) {
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1) if (threads > 1)
+    for (size_t i = 0; i < nmat; i++)
+        orc_muon_step(v[i], g[i], m[i], rows[i], cols[i], decay[i], lr, wd, mom, ns_steps);
+}
+
 /* Optim::step_adam (optim.rs:207-235) at step count t (the step uses t + 1
  * for the bias corrections; the caller increments t after the whole step). */
 void orc_adam_step(size_t n, float *v, float *g, float *m, float *v2, int decay, float lr,

@@ -144,6 +144,9 @@ def lib():
         L.orc_newton_schulz.argtypes = [_f32p, _sz, _sz, _sz]
         L.orc_muon_step.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, C.c_int, C.c_float,
                                     C.c_float, C.c_float, _sz]
+        _pp = P(C.POINTER(C.c_float))
+        L.orc_muon_steps.argtypes = [_sz, _pp, _pp, _pp, P(_sz), P(_sz), P(C.c_int), C.c_float,
+                                     C.c_float, C.c_float, _sz, C.c_int]
         L.orc_adam_step.argtypes = [_sz, _f32p, _f32p, _f32p, _f32p, C.c_int, C.c_float,
                                     C.c_float, C.c_float, C.c_float, C.c_float, _sz]
         L.orc_clip.argtypes = [_f32p, P(_sz), _sz, C.c_float]
@@ -529,6 +532,29 @@ def muon_step(v, g, m, rows, cols, decay, lr, wd, mom=0.95, ns_steps=3):
     """The Muon branch of Optim::step_all (optim.rs:182-195), in place."""
     _chk(v, g, m)
     lib().orc_muon_step(v, g, m, rows, cols, int(decay), lr, wd, mom, ns_steps)
+
+
+def muon_steps(params, lr, wd, mom=0.95, ns_steps=3, threads=1):
+    """The Muon branch of Optim::step_all over a list of (v, g, m, rows,
+    cols, decay) parameters, on an OpenMP loop over the matrices (the
+    reference's par_iter over parameters, optim.rs:177-196); in place, equal
+    to muon_step per parameter."""
+    n = len(params)
+    fp = C.POINTER(C.c_float)
+    ptrs = []
+    for k in range(3):
+        arr = (fp * n)()
+        for i, p in enumerate(params):
+            _chk(p[k])
+            arr[i] = p[k].ctypes.data_as(fp)
+        ptrs.append(arr)
+    for p in params:
+        assert p[0].size == p[1].size == p[2].size == p[3] * p[4]
+    rows = (_sz * n)(*[p[3] for p in params])
+    cols = (_sz * n)(*[p[4] for p in params])
+    dec = (C.c_int * n)(*[int(p[5]) for p in params])
+    lib().orc_muon_steps(n, ptrs[0], ptrs[1], ptrs[2], rows, cols, dec, lr, wd, mom, ns_steps,
+                         int(threads))
 
 
 def adam_step(v, g, m, v2, decay, lr, wd, t, b1=0.9, b2=0.999, eps=1e-8):

@@ -78,6 +78,24 @@ def test_muon_step_matches_f64(orc):
     assert not g.any()
 
 
+def test_muon_steps_equals_per_matrix(orc):
+    """The OpenMP loop over matrices (the CPU baseline's form) gives exactly
+    what muon_step gives per matrix, on shapes both sides of the transpose."""
+    rng = np.random.default_rng(12)
+    shapes = [(48, 20, True), (20, 48, False), (33, 33, True), (64, 8, True), (5, 70, False)]
+    one, many = [], []
+    for r, c, d in shapes:
+        arrs = [rng.standard_normal(r * c).astype(np.float32) for _ in range(3)]
+        one.append([a.copy() for a in arrs] + [r, c, d])
+        many.append([a.copy() for a in arrs] + [r, c, d])
+    for v, g, m, r, c, d in one:
+        orc.muon_step(v, g, m, r, c, d, 0.02, 0.05, 0.95, 3)
+    orc.muon_steps(many, 0.02, 0.05, 0.95, 3, threads=4)
+    for a, b in zip(one, many):
+        for k in range(3):
+            assert np.array_equal(a[k], b[k])
+
+
 def test_adam_matches_torch_adamw(orc):
     import torch
     rng = np.random.default_rng(3)
