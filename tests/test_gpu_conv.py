@@ -196,7 +196,12 @@ def test_conv_deterministic(rnn, orc):
 
 @pytest.mark.parametrize("cin,cout,k,s,p,h", [(3, 4, 3, 1, 1, 6), (4, 6, 1, 2, 0, 8),
                                               (4, 5, 3, 2, 1, 7), (32, 32, 3, 1, 1, 32)])
-def test_im2col_bit_exact(rnn, orc, cin, cout, k, s, p, h):
+def test_dbg_im2col_export_bit_exact(rnn, orc, cin, cout, k, s, p, h):
+    """rnn_dbg_im2col, the debug export of the RowMap / gather_span layout
+    (conv.rs:68-120), equals the oracle's im2col.  The export is its own
+    small kernel: the conv kernels stage their windows by DMA instead, and
+    that indexing is pinned by test_conv_integer_bit_exact (every sum exact,
+    so any misplaced tap or halo element changes the result)."""
     sp = orc.ConvSpec.make(cin, cout, k, s, p, h, h)
     gsp = rnn.ConvSpec.make(cin, cout, k, s, p, h, h)
     x = orc.Rng(5).rand_vec(cin * h * h)
