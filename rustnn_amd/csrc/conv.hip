@@ -425,6 +425,24 @@ int rnn_conv2d_forward_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
                     sp->ow, 1, 0, 0, sp->stride, taps, KK, w, sp->cin * KK, KK, K);
 }
 
+int rnn_conv2d_forward_stats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
+                             const float *w, const float *wp, float *y, double *part) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    int rc = check_spec(ctx, sp);
+    if (rc) return rc;
+    if (n == 0) return RNN_OK;
+    if (!x || !w || !y || !part)
+        return rnn_fail(ctx, RNN_E_NULL, "conv2d_forward_stats: null operand");
+    ConvStats st;
+    st.part = part;
+    rc = rnn_conv_fast(ctx, 0, sp, n, x, w, wp, y, &st);
+    if (rc == RNN_E_UNSUPPORTED)
+        return rnn_fail(ctx, rc, "conv2d_forward_stats: no specialised kernel for k%u s%u p%u",
+                        sp->k, sp->stride, sp->pad);
+    return rc;
+}
+
 int rnn_conv2d_backward_x_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
                              const float *w, const float *wp, float *dx) {
     if (!ctx) return RNN_E_NULL;

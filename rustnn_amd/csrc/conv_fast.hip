@@ -65,6 +65,8 @@ struct FastArgs {
     TileGeo geo;       // window geometry in positions (chs unused)
     int tapoff[9];     // window-position offset of each tap
     uint32_t m_imgs, m_tiwp;  // FastDiv multipliers of geo.imgs and geo.TIWP
+    int npart;         // store-pass statistics: partials per channel (= ntiles)
+    ConvStats stats;   // store-pass statistics (forward with EPI = 1)
 };
 
 // Wave-uniform description of the stage being staged by DMA.
@@ -268,8 +270,82 @@ __device__ __forceinline__ void issue_stage(const FastArgs &g, StageDMA d, float
 // back-pressure stalls a producer and never the MFMA issue of a compute
 // wave.  One barrier per stage: when it completes, stage s has landed (each
 // producer waited for its own DMA) and stage s - 1's buffer is free.
-template <int K, int S, int P, bool DX, int NPW, int MB, int WM>
-__global__ __launch_bounds__(64 * FAST_NW * 2) void conv_fast_kernel(FastArgs g) {
+// Sums 4 values per lane over the 32 lanes of each half-wave: offsets 16 and
+// 8 each keep half of the values, offsets 4, 2, 1 add the rest; lane l ends
+// with the total of value 2*b4 + b3 (b = bits of l), the 8 lanes that share
+// those bits holding the same total.  The order is fixed.
+__device__ __forceinline__ double half_reduce4(const double (&x)[4], int l32) {
+    const bool b4 = l32 & 16, b3 = l32 & 8;
+    double a2[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+        a2[i] = (b4 ? x[i + 2] : x[i]) + __shfl_xor(b4 ? x[i] : x[i + 2], 16, 64);
+    double a1 = (b3 ? a2[1] : a2[0]) + __shfl_xor(b3 ? a2[0] : a2[1], 8, 64);
+    a1 = a1 + __shfl_xor(a1, 4, 64);
+    a1 = a1 + __shfl_xor(a1, 2, 64);
+    return a1 + __shfl_xor(a1, 1, 64);
+}
+
+// The forward's store pass with the batch statistics' sums (see ConvEpi):
+// the same stores as the plain pass, with the accumulator registers taken 4
+// at a time so that only 4 (sum y, sum y^2) pairs are live; each wave's
+// totals over the item's positions, reduced over its lanes, are left in red
+// (LDS) for the workgroup's fixed-order sum over its waves.
+template <int K, int S, int P, int NPW, int MB, int WM, int NACC>
+__device__ __forceinline__ void store_stats(
+    const FastArgs &g, const f32x16 (&acc)[1][MB][NPW][NACC], int wave, int lane, int grp,
+    int a0, int n0, double *__restrict__ red) {
+    constexpr int VG = 4, WP = FAST_NW / WM, SL = WM * MB;
+    const int h = lane >> 5, l32 = lane & 31;
+    const int tpix = g.TR * g.GB, npix = g.geo.IMGS * tpix;
+    const long long cst = (long long)g.HD * g.WD;
+    static_for<0, 16 / VG>([&](auto gc) {
+        constexpr int vbase = decltype(gc)::value * VG;
+        double es[MB][2][VG];
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int u = 0; u < VG; u++) es[mb][0][u] = es[mb][1][u] = 0.0;
+#pragma unroll
+        for (int j = 0; j < NPW; j++) {
+            const int p = ((wave % WP) * NPW + j) * 32 + l32;
+            const int img = p / tpix, rem = p - img * tpix, r = rem / g.GB, cb = rem - r * g.GB;
+            const int n = n0 + img, a = a0 + r;
+            if (p >= npix || n >= g.N || a >= g.GA) continue;
+            const long long o = ((long long)n * g.CD * g.HD + a) * g.WD + cb;
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++) {
+                f32x16 v16 = acc[0][mb][j][0];
+                if constexpr (NACC == 2) v16 += acc[0][mb][j][1];
+                static_for<0, VG>([&](auto uc) {
+                    constexpr int u = decltype(uc)::value, v = vbase + u;
+                    const int m = (grp * SL + (wave / WP) * MB + mb) * 32 + 8 * (v >> 2) + 4 * h +
+                                  (v & 3);
+                    if (m >= g.CD) return;
+                    const float y = v16[v];
+                    g.dst[o + m * cst] = y;
+                    es[mb][0][u] += (double)y;
+                    es[mb][1][u] += (double)y * (double)y;
+                });
+            }
+        }
+        // this wave's totals into red[wave % WP][channel of the group][kind]
+        const int v = vbase + ((l32 >> 4) & 1) * 2 + ((l32 >> 3) & 1);
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+            const double t0 = half_reduce4(es[mb][0], l32), t1 = half_reduce4(es[mb][1], l32);
+            const int cl = ((wave / WP) * MB + mb) * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            if ((l32 & 7) == 0) {
+                red[((wave % WP) * 32 * SL + cl) * 2] = t0;
+                red[((wave % WP) * 32 * SL + cl) * 2 + 1] = t1;
+            }
+        }
+    });
+}
+
+template <int K, int S, int P, bool DX, int NPW, int MB, int WM, int EPI>
+__global__ __launch_bounds__(64 * FAST_NW * 2)
+__attribute__((amdgpu_waves_per_eu(EPI ? 4 : 1))) void conv_fast_kernel(FastArgs g) {
     using T = ConvTaps<K, S, P, DX>;
     constexpr int NCLS = T::NCLS;
     // A wave with a single output block alternates two accumulators so that
@@ -306,6 +382,7 @@ __global__ __launch_bounds__(64 * FAST_NW * 2) void conv_fast_kernel(FastArgs g)
                     issue_stage<K, S, P, DX, SL>(g, d, nbuf, 0, L, rs_w, dw, lane);
                 }
             }
+            if constexpr (EPI != 0) __syncthreads();  // the compute waves' store-pass sums
         }
         return;
     }
@@ -344,6 +421,24 @@ __global__ __launch_bounds__(64 * FAST_NW * 2) void conv_fast_kernel(FastArgs g)
         // acc row 8*(v/4) + 4*h + v%4 = output channel in the block, column = position.
         const int tile = item % g.ntiles, grp = item / g.ntiles;
         const int a0 = (tile % g.tiles_a) * g.TR, n0 = (tile / g.tiles_a) * g.geo.IMGS;
+        if constexpr (EPI != 0) {
+            // Store pass with the statistics' sums; then the WP position
+            // waves' totals of each channel, summed in wave order, make partial
+            // `tile` of the channel.  The barrier pairs with the producers'
+            // one after the item.
+            constexpr int NCH = 32 * SL;
+            double *red = reinterpret_cast<double *>(smem + 2 * g.stage);
+            store_stats<K, S, P, NPW, MB, WM, NACC>(g, acc, wave, lane, grp, a0, n0, red);
+            __syncthreads();
+            for (int t = tid; t < 2 * NCH; t += 64 * FAST_NW) {
+                const int cl = t >> 1, m = grp * NCH + cl;
+                if (m >= g.CD) continue;
+                double tot = red[t];
+                for (int w = 1; w < WP; w++) tot += red[w * 2 * NCH + t];
+                g.stats.part[((long long)m * g.npart + tile) * 2 + (t & 1)] = tot;
+            }
+            continue;
+        }
 #pragma unroll
         for (int j = 0; j < NPW; j++) {
             const int p = ((wave % WP) * NPW + j) * 32 + l32;
@@ -543,10 +638,19 @@ static bool choose_plan(int CS, int CD, int GA, int GB, FastPlan &best, FastArgs
     }
 }
 
+// LDS after the two stage buffers for the store-pass sums: per position wave,
+// channel of the group and kind, one double.
+static size_t epi_lds(const FastPlan &p) {
+    return (size_t)(FAST_NW / p.WM) * 32 * p.WM * p.MB * 2 * sizeof(double);
+}
+
 template <int K, int S, int P, bool DX, int NPW, int MB, int WM>
 static void set_attr() {
-    (void)hipFuncSetAttribute((const void *)conv_fast_kernel<K, S, P, DX, NPW, MB, WM>,
+    (void)hipFuncSetAttribute((const void *)conv_fast_kernel<K, S, P, DX, NPW, MB, WM, 0>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if constexpr (!DX)
+        (void)hipFuncSetAttribute((const void *)conv_fast_kernel<K, S, P, DX, NPW, MB, WM, 1>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
 }
 
 // Operand roles, geometry and tile plan of a (k, stride, pad) forward / dX
@@ -606,7 +710,7 @@ static PackGeo pack_geo(const FastArgs &a) {
 
 template <int K, int S, int P, bool DX>
 static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src, const float *w,
-                  const float *wp, float *dst) {
+                  const float *wp, float *dst, const ConvStats *cs) {
     using T = ConvTaps<K, S, P, DX>;
     static bool attr = false;
     if (!attr) {
@@ -639,6 +743,16 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
     a.ngroups = (nmblk + p.MB * p.WM - 1) / (p.MB * p.WM);
     const long long nitems = (long long)a.ntiles * a.ngroups;
     if (nitems > 0x7fffffffll) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: too many tiles");
+    const bool stats = cs != nullptr;
+    if (stats) {
+        if (DX || !cs->part)
+            return rnn_fail(ctx, RNN_E_INVALID, "conv: store-pass statistics need a forward");
+        a.stats = *cs;
+        a.npart = a.ntiles;
+        p.lds += epi_lds(p);
+        if (p.lds > 160 * 1024)
+            return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv: no LDS for the store-pass sums");
+    }
     // Persistent grid: as many workgroups as fit on the chip at once.
     auto run = [&](auto kern) -> int {
         int occ = 0;
@@ -653,12 +767,28 @@ static int launch(rnn_ctx *ctx, const rnn_conv_spec *sp, int n, const float *src
         RNN_LAUNCHED(ctx);
         return RNN_OK;
     };
-    if constexpr (T::NCLS == 1) {
-        if (p.NPW == 2) return run(conv_fast_kernel<K, S, P, DX, 2, 1, 1>);
-        if (p.MB == 2) return run(conv_fast_kernel<K, S, P, DX, 1, 2, 1>);
-    }
-    if (p.WM == 2) return run(conv_fast_kernel<K, S, P, DX, 1, 1, 2>);
-    return run(conv_fast_kernel<K, S, P, DX, 1, 1, 1>);
+    auto pick = [&](auto ec) -> int {
+        constexpr int E = decltype(ec)::value;
+        if constexpr (T::NCLS == 1) {
+            if (p.NPW == 2) return run(conv_fast_kernel<K, S, P, DX, 2, 1, 1, E>);
+            if (p.MB == 2) return run(conv_fast_kernel<K, S, P, DX, 1, 2, 1, E>);
+        }
+        if (p.WM == 2) return run(conv_fast_kernel<K, S, P, DX, 1, 1, 2, E>);
+        return run(conv_fast_kernel<K, S, P, DX, 1, 1, 1, E>);
+    };
+    if constexpr (!DX)
+        if (stats) return pick(std::integral_constant<int, 1>{});
+    return pick(std::integral_constant<int, 0>{});
+}
+
+template <int K, int S, int P>
+static int parts_of(const rnn_conv_spec *sp, size_t n) {
+    FastArgs a;
+    FastPlan p;
+    if (!setup<K, S, P, false>(sp, a, p)) return -1;
+    if (p.lds + epi_lds(p) > 160 * 1024) return -1;
+    const long long np = (long long)a.tiles_a * (((long long)n + p.IMGS - 1) / p.IMGS);
+    return np > 0x3fffffffll ? -1 : (int)np;
 }
 
 
@@ -709,20 +839,33 @@ static int geo_of(const rnn_conv_spec *sp, PackGeo *pg) {
 // specialisation, so the caller can take the generic per-class path.  wp:
 // the weights packed by rnn_conv_pack for this direction, or null.
 int rnn_conv_fast(rnn_ctx *ctx, int dx, const rnn_conv_spec *sp, size_t n, const float *src,
-                  const float *w, const float *wp, float *dst) {
+                  const float *w, const float *wp, float *dst, const ConvStats *stats) {
     if (getenv("RNN_CONV_GENERIC")) return RNN_E_UNSUPPORTED;
     const int k = sp->k, s = sp->stride, p = sp->pad;
     const int ni = (int)n;
 #define RNN_CONV_CASE(K_, S_, P_)                                                               \
     if (k == K_ && s == S_ && p == P_)                                                          \
-        return dx ? launch<K_, S_, P_, true>(ctx, sp, ni, src, w, wp, dst)                      \
-                  : launch<K_, S_, P_, false>(ctx, sp, ni, src, w, wp, dst);
+        return dx ? launch<K_, S_, P_, true>(ctx, sp, ni, src, w, wp, dst, stats)               \
+                  : launch<K_, S_, P_, false>(ctx, sp, ni, src, w, wp, dst, stats);
     RNN_CONV_CASE(3, 1, 1)
     RNN_CONV_CASE(3, 2, 1)
     RNN_CONV_CASE(1, 2, 0)
     RNN_CONV_CASE(1, 1, 0)
 #undef RNN_CONV_CASE
     return RNN_E_UNSUPPORTED;
+}
+
+int rnn_conv_fast_parts(const rnn_conv_spec *sp, size_t n) {
+    if (getenv("RNN_CONV_GENERIC") || n == 0 || n > 0x7fffffff) return -1;
+    const int k = sp->k, s = sp->stride, p = sp->pad;
+#define RNN_CONV_CASE(K_, S_, P_) \
+    if (k == K_ && s == S_ && p == P_) return parts_of<K_, S_, P_>(sp, n);
+    RNN_CONV_CASE(3, 1, 1)
+    RNN_CONV_CASE(3, 2, 1)
+    RNN_CONV_CASE(1, 2, 0)
+    RNN_CONV_CASE(1, 1, 0)
+#undef RNN_CONV_CASE
+    return -1;
 }
 
 int rnn_conv_pack_geo(const rnn_conv_spec *sp, int dx, PackGeo *pg) {

@@ -53,6 +53,57 @@ __device__ __forceinline__ void block_sum2(double &a, double &b) {
     }
 }
 
+// The totals of the P partial pairs part[ci][k][0..1] of channel ci, in
+// every thread of the block (all threads must call it).  Up to 64 partials:
+// each thread adds them in order (uniform loads).  More (a conv store pass's
+// one partial per tile): thread t adds pairs t, t + 256, ... in order, its
+// loads issued four at a time, then the waves' fixed-order trees and the
+// waves in order.
+__device__ __forceinline__ void part_totals(const double *__restrict__ part, int ci, int P,
+                                            double &a, double &b) {
+    const double *pc = part + (size_t)ci * P * 2;
+    if (P <= 64) {
+        a = 0.0;
+        b = 0.0;
+        for (int k = 0; k < P; k++) {
+            a += pc[2 * k];
+            b += pc[2 * k + 1];
+        }
+        return;
+    }
+    __shared__ double red[2][RED_THREADS / 64];
+    constexpr int U = 4;
+    double sa = 0.0, sb = 0.0;
+    for (int k0 = threadIdx.x; k0 < P; k0 += U * RED_THREADS) {
+        double2 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int k = k0 + u * RED_THREADS;
+            v[u] = k < P ? *reinterpret_cast<const double2 *>(pc + 2 * k) : double2{0.0, 0.0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            sa += v[u].x;
+            sb += v[u].y;
+        }
+    }
+    sa = wave_sum(sa);
+    sb = wave_sum(sb);
+    const int wave = wave_index(), lane = threadIdx.x & 63;
+    if (lane == 0) {
+        red[0][wave] = sa;
+        red[1][wave] = sb;
+    }
+    __syncthreads();
+    a = red[0][0];
+    b = red[1][0];
+    for (int w = 1; w < RED_THREADS / 64; w++) {
+        a += red[0][w];
+        b += red[1][w];
+    }
+    __syncthreads();  // red is reused by the next call
+}
+
 // Geometry of the per-channel reductions: block (ci, p) sums images
 // [p*G, p*G + G) of channel ci.
 struct ChanSplit {
@@ -128,11 +179,8 @@ __device__ __forceinline__ void bn_channel(const RnnBn &s, int ci, bool first, f
         a = s.gamma[ci] * is;
         b = s.beta[ci] - s.gamma[ci] * is * s.rm[ci];
     } else {
-        double sx = 0.0, sx2 = 0.0;
-        for (int p = 0; p < s.P; p++) {
-            sx += s.part[((size_t)ci * s.P + p) * 2 + 0];
-            sx2 += s.part[((size_t)ci * s.P + p) * 2 + 1];
-        }
+        double sx, sx2;
+        part_totals(s.part, ci, s.P, sx, sx2);
         const double mu = sx / (double)s.m;
         const double va = sx2 / (double)s.m - mu * mu;
         const float meanf = (float)mu, varf = (float)(va > 0.0 ? va : 0.0);
@@ -287,15 +335,12 @@ __global__ __launch_bounds__(EW_THREADS) void bn_bwd_apply_kernel(
     const float *__restrict__ d, const float *__restrict__ mask, const float *__restrict__ x,
     RnnBn bn, const double *__restrict__ part, float *dx, int n, int C, int hw, int G,
     FastDiv fd_hw4, int vec) {
-    const int ci = blockIdx.x, p = blockIdx.y, P = gridDim.y;
+    const int ci = blockIdx.x, p = blockIdx.y;
     const int i0 = p * G, i1 = min(n, i0 + G);
     float dg, db, mu, is, m, s;
     auto coefs = [&]() {
-        double sa = 0.0, sb = 0.0;
-        for (int k = 0; k < P; k++) {
-            sa += part[((size_t)ci * P + k) * 2 + 0];
-            sb += part[((size_t)ci * P + k) * 2 + 1];
-        }
+        double sa, sb;
+        part_totals(part, ci, bn.P, sa, sb);
         dg = (float)sa;
         db = (float)sb;
         if (p == 0 && threadIdx.x == 0) {
@@ -861,10 +906,10 @@ int rnn_bn_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float
                         float *out) {
     if (n * c * hw == 0) return RNN_OK;
     ChanSplit s = chan_split(n, c);
-    bn.P = s.P;
+    if (bn.P <= 0) bn.P = s.P;  // else the partials come from a conv's store pass
     bn.m = (float)(n * hw);
     RnnBn sb = sbn ? *sbn : bn;
-    sb.P = s.P;
+    if (sb.P <= 0) sb.P = s.P;
     sb.m = bn.m;
     if (eval) {
         if (skip_mode == 0) {
@@ -898,7 +943,7 @@ int rnn_bn_backward_apply_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, co
                                  const double *part, float *dx) {
     if (n * c * hw == 0) return RNN_OK;
     ChanSplit s = chan_split(n, c);
-    bn.P = s.P;
+    if (bn.P <= 0) bn.P = s.P;  // else the partials come from a conv's store pass
     bn.m = (float)(n * hw);
     const FastDiv fd_hw4 = divider(hw / 4, (size_t)s.G * (hw / 4));
     const dim3 grid((unsigned)c, (unsigned)s.P);
@@ -928,6 +973,7 @@ int rnn_bn_backward_launch(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const fl
         bn_bwd_part_kernel<false><<<grid, RED_THREADS, 0, ctx->stream>>>(
             dy, mask, x, bn.mean, bn.invstd, (int)n, (int)c, (int)hw, vec, s.G, fd_hw4, part);
     RNN_LAUNCHED(ctx);
+    bn.P = s.P;  // the partials just taken
     return rnn_bn_backward_apply_launch(ctx, n, c, hw, dy, mask, x, bn, part, dx);
 }
 

@@ -87,6 +87,9 @@ struct NetConv {
     // side table, or -1 (summed with the rest).
     int fseg = -1;
     long long fblk = 0;
+    // Partials per channel of the batch statistics taken by this conv's
+    // forward store pass (per plan); -1: they run as a pass of their own.
+    int epf = -1;
     rnn_conv_spec spec(uint32_t h, uint32_t w_) const {
         rnn_conv_spec sp;
         rnn_conv_spec_init(&sp, cin, cout, k, stride, pad, h, w_);
@@ -100,6 +103,9 @@ struct NetBn {
     size_t buf = 0;      // rm at buf, rv at buf + c in the buffer array
     float *coef = nullptr;   // device [2c]: batch mean, invstd of the last train forward
     double *part = nullptr;  // device: partial sums of the batch statistics (per plan)
+    // partials per channel of the last forward's statistics in part (0: the
+    // per-image-range split of the separate pass)
+    int pf = 0;
 };
 
 struct NetBlock {
@@ -162,6 +168,9 @@ struct rnn_resnet {
     hipStream_t side = nullptr;
     std::vector<hipEvent_t> events;
     bool overlap = true;
+    // batch statistics in the forward convs' store passes
+    // (RNN_BN_PASSES=separate: in passes of their own)
+    bool fuse_bn = true;
     bool capturing = false;  // recording the step graph: no side stream there
     int step_calls = 0;
     bool use_graph = true;
@@ -256,15 +265,29 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     std::vector<size_t> offs;
     for (auto &e : f32) offs.push_back(cv.take(e.second * sizeof(float)));
     const size_t o_part = cv.take(maxpart * sizeof(double));
-    std::vector<std::pair<NetBn *, size_t>> bnparts;
-    auto bnpart = [&](NetBn &bn) {
-        bnparts.push_back({&bn, cv.take(rnn_bn_scratch_doubles(n, bn.c) * sizeof(double))});
+    // Store-pass batch statistics: partials per channel of each conv's forward.
+    auto ep = [&](NetConv &c, size_t hh, size_t ww) -> int {
+        if (!r->fuse_bn) return -1;
+        rnn_conv_spec sp = c.spec((uint32_t)hh, (uint32_t)ww);
+        return rnn_conv_fast_parts(&sp, n);
     };
-    bnpart(r->stem_bn);
+    r->stem.epf = ep(r->stem, H, W);
     for (auto &b : r->blocks) {
-        bnpart(b.b1);
-        bnpart(b.b2);
-        if (b.down) bnpart(b.bd);
+        b.c1.epf = ep(b.c1, b.hin, b.win);
+        b.c2.epf = ep(b.c2, b.hout, b.wout);
+        b.cd.epf = b.down ? ep(b.cd, b.hin, b.win) : -1;
+    }
+    std::vector<std::pair<NetBn *, size_t>> bnparts;
+    auto bnpart = [&](NetBn &bn, int pa) {
+        const size_t d = std::max(rnn_bn_scratch_doubles(n, bn.c),
+                                  (size_t)2 * bn.c * (size_t)std::max(pa, 0));
+        bnparts.push_back({&bn, cv.take(d * sizeof(double))});
+    };
+    bnpart(r->stem_bn, r->stem.epf);
+    for (auto &b : r->blocks) {
+        bnpart(b.b1, b.c1.epf);
+        bnpart(b.b2, b.c2.epf);
+        if (b.down) bnpart(b.bd, b.cd.epf);
     }
     // dW slabs of every conv, and the gradient segment table.
     std::vector<std::pair<NetConv *, size_t>> slabs;
@@ -465,6 +488,13 @@ RnnBn bn_state(rnn_resnet *r, const NetBn &bn) {
     return s;
 }
 
+// The same view with the partial count of the last forward's statistics.
+RnnBn bn_fwd(rnn_resnet *r, const NetBn &bn) {
+    RnnBn s = bn_state(r, bn);
+    s.P = bn.pf;
+    return s;
+}
+
 #define TRY(expr)                 \
     do {                          \
         int st_ = (expr);         \
@@ -487,31 +517,40 @@ int forward(rnn_resnet *r, bool train) {
     rnn_ctx *ctx = r->ctx;
     const size_t n = r->n;
     const bool ev = !train;
+    // conv c of src into y, with (train) the batch statistics' partial sums of
+    // bn: in the conv's store pass, or by a pass of their own
+    auto conv_bn = [&](NetConv &c, const rnn_conv_spec &sp, const float *src, float *y,
+                       NetBn &bn) -> int {
+        if (train && c.epf > 0) {
+            bn.pf = c.epf;
+            return rnn_conv2d_forward_stats(ctx, &sp, n, src, pv_of(r, c.w), c.wp_f, y, bn.part);
+        }
+        TRY(rnn_conv2d_forward_wp(ctx, &sp, n, src, pv_of(r, c.w), c.wp_f, y));
+        bn.pf = 0;
+        if (train) return rnn_bn_stats_launch(ctx, n, bn.c, (size_t)sp.oh * sp.ow, y, bn.part);
+        return RNN_OK;
+    };
     rnn_conv_spec sp = r->stem.spec((uint32_t)r->H, (uint32_t)r->W);
     const size_t hw0 = (size_t)sp.oh * sp.ow;
-    TRY(rnn_conv2d_forward_wp(ctx, &sp, n, r->x, pv_of(r, r->stem.w), r->stem.wp_f, r->y0));
-    if (train) TRY(rnn_bn_stats_launch(ctx, n, r->stem_bn.c, hw0, r->y0, r->stem_bn.part));
-    TRY(rnn_bn_apply_launch(ctx, n, r->stem_bn.c, hw0, r->y0, bn_state(r, r->stem_bn), ev, 1, 0,
+    TRY(conv_bn(r->stem, sp, r->x, r->y0, r->stem_bn));
+    TRY(rnn_bn_apply_launch(ctx, n, r->stem_bn.c, hw0, r->y0, bn_fwd(r, r->stem_bn), ev, 1, 0,
                             nullptr, nullptr, r->s0));
     for (auto &b : r->blocks) {
         const size_t hw = (size_t)b.hout * b.wout;
         rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
-        TRY(rnn_conv2d_forward_wp(ctx, &s1, n, b.in, pv_of(r, b.c1.w), b.c1.wp_f, b.y1));
-        if (train) TRY(rnn_bn_stats_launch(ctx, n, b.b1.c, hw, b.y1, b.b1.part));
-        TRY(rnn_bn_apply_launch(ctx, n, b.b1.c, hw, b.y1, bn_state(r, b.b1), ev, 1, 0, nullptr,
+        TRY(conv_bn(b.c1, s1, b.in, b.y1, b.b1));
+        TRY(rnn_bn_apply_launch(ctx, n, b.b1.c, hw, b.y1, bn_fwd(r, b.b1), ev, 1, 0, nullptr,
                                 nullptr, b.h));
         rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
-        TRY(rnn_conv2d_forward_wp(ctx, &s2, n, b.h, pv_of(r, b.c2.w), b.c2.wp_f, b.y2));
-        if (train) TRY(rnn_bn_stats_launch(ctx, n, b.b2.c, hw, b.y2, b.b2.part));
+        TRY(conv_bn(b.c2, s2, b.h, b.y2, b.b2));
         if (b.down) {
             rnn_conv_spec sd = b.cd.spec(b.hin, b.win);
-            TRY(rnn_conv2d_forward_wp(ctx, &sd, n, b.in, pv_of(r, b.cd.w), b.cd.wp_f, b.ys));
-            if (train) TRY(rnn_bn_stats_launch(ctx, n, b.bd.c, hw, b.ys, b.bd.part));
-            const RnnBn sd_bn = bn_state(r, b.bd);
-            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, bn_state(r, b.b2), ev, 1, 2, b.ys,
+            TRY(conv_bn(b.cd, sd, b.in, b.ys, b.bd));
+            const RnnBn sd_bn = bn_fwd(r, b.bd);
+            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, bn_fwd(r, b.b2), ev, 1, 2, b.ys,
                                     &sd_bn, b.out));
         } else {
-            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, bn_state(r, b.b2), ev, 1, 1, b.in,
+            TRY(rnn_bn_apply_launch(ctx, n, b.b2.c, hw, b.y2, bn_fwd(r, b.b2), ev, 1, 1, b.in,
                                     nullptr, b.out));
         }
     }
@@ -761,6 +800,8 @@ int rnn_resnet_create(rnn_ctx *ctx, size_t depth_n, size_t width, size_t nclass,
     r->overlap = !(ov && ov[0] == '0');
     const char *g = getenv("RNN_GRAPH");
     r->use_graph = g ? g[0] != '0' : !r->overlap;
+    const char *bp = getenv("RNN_BN_PASSES");
+    r->fuse_bn = !(bp && strcmp(bp, "separate") == 0);
     // ResNet::new (model.rs:113-135): blocks first (their convs draw from the
     // Rng in c1, c2, shortcut order), then the stem conv, then the classifier.
     const uint32_t widths[3] = {(uint32_t)width, (uint32_t)width * 2, (uint32_t)width * 4};

@@ -415,8 +415,19 @@ int rnn_colsum_f64(rnn_ctx *ctx, size_t rows, int c, const float *a, const float
 // when (k, stride, pad) has no specialisation.  wp: the weights packed by
 // rnn_conv_pack for this direction (the kernels then load each stage's
 // weights as one contiguous copy), or null.
+// The batch statistics of a forward convolution's output, taken in its store
+// pass for the BatchNorm that reads it: (sum y, sum y^2) per channel in f64,
+// part[channel][P][2] with P = rnn_conv_fast_parts (one partial per tile,
+// the workgroup's waves summed in order), as bn_stats_part_kernel lays out
+// its per-image-range partials.
+struct ConvStats {
+    double *part = nullptr;
+};
 int rnn_conv_fast(rnn_ctx *ctx, int dx, const rnn_conv_spec *sp, size_t n, const float *src,
-                  const float *w, const float *wp, float *dst);
+                  const float *w, const float *wp, float *dst, const ConvStats *stats = nullptr);
+// Partials per channel of the store-pass statistics of a forward of (sp, n);
+// -1 when the shape has no specialised plan.
+int rnn_conv_fast_parts(const rnn_conv_spec *sp, size_t n);
 
 // Packed weights of one direction: [m-block][chunk][quad][tap][lane 64][4]
 // with lane L of slab (quad q, tap t) holding rows m = 32*mblk + L%32 and
@@ -461,6 +472,10 @@ int rnn_conv2d_forward_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const
                           const float *w, const float *wp, float *y);
 int rnn_conv2d_backward_x_wp(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
                              const float *w, const float *wp, float *dx);
+// The forward with the batch statistics of y taken in its store pass
+// (ConvStats); RNN_E_UNSUPPORTED when the shape has no specialised kernel.
+int rnn_conv2d_forward_stats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
+                             const float *w, const float *wp, float *y, double *part);
 // dW += over the batch (k = 1 or 3).  The partial slabs go to `part` (room
 // for `cap` floats; RNN_E_UNSUPPORTED when the plan needs more) or, with part
 // null, to the context workspace.

@@ -117,6 +117,36 @@ def test_train_step_config3(rnn, orc):
     got.close()
 
 
+def test_bn_stats_in_conv_store_pass(rnn, orc, monkeypatch):
+    """The batch statistics taken in the forward convs' store passes (the
+    default) == the same network with the statistics in passes of their own
+    (RNN_BN_PASSES=separate).  Only the order of the f64 partial sums
+    differs, so the steps agree to f32 rounding."""
+    import torch
+    from rustnn_amd.model import ResNet
+    n = 64
+    fused = ResNet(3, 32, 100, 13)
+    monkeypatch.setenv("RNN_BN_PASSES", "separate")
+    sep = ResNet(3, 32, 100, 13)
+    monkeypatch.delenv("RNN_BN_PASSES")
+    for net in (fused, sep):
+        net.set_graph(False)
+    la, lb = torch.zeros(1, device="cuda"), torch.zeros(1, device="cuda")
+    for step in range(3):
+        x, labels = _cfg3_inputs(orc, n, seed=300 + step)
+        X = to_dev(x)
+        L = torch.from_numpy(labels.astype(np.int32)).cuda()
+        fused.train_step(X, L, 0.1, 0.2, 0.9, 5e-4, la)
+        sep.train_step(X, L, 0.1, 0.2, 0.9, 5e-4, lb)
+        assert abs(float(to_host(la)[0]) - float(to_host(lb)[0])) < 1e-6 * abs(
+            float(to_host(lb)[0])), step
+        assert rel_frob(to_host(fused.momenta()), to_host(sep.momenta())) < 1e-6, step
+        assert rel_frob(to_host(fused.params()), to_host(sep.params())) < 1e-6, step
+        assert rel_frob(to_host(fused.buffers()), to_host(sep.buffers())) < 1e-6, step
+    fused.close()
+    sep.close()
+
+
 def test_fused_train_step_matches_layer_calls(rnn, orc):
     """rnn_resnet_train_step (eager, then graph) == forward + softmax_ce +
     backward + step called one by one, bit for bit."""
