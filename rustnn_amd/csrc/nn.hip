@@ -681,16 +681,22 @@ __device__ __forceinline__ float wave_sumf(float v) {
 // gradient (softmax - target) / rows; the wave sums run in a tree order.
 // Thread 0 then adds the row losses and hits in row order.  `smooth` comes
 // from device memory when `scal` is set (scal[3]), else from the argument.
+// One block keeps the row results in LDS.  With `ticket` set, several blocks
+// share the rows (one per wave) and keep them in rowbuf [2*rows]; the block
+// that takes the last ticket adds them in row order and sets the ticket back
+// to 0 for the next launch.
 template <int ZR>
 __global__ __launch_bounds__(1024) void softmax_ce_kernel(
     const float *__restrict__ logits, const uint32_t *__restrict__ labels, int rows, int nclass,
-    float smooth_arg, const float *scal, float *dl, float *loss_out, uint32_t *correct_out) {
-    extern __shared__ float row_loss[];  // [rows] losses, then [rows] hits
+    float smooth_arg, const float *scal, float *dl, float *loss_out, uint32_t *correct_out,
+    uint32_t *ticket, float *rowbuf) {
+    extern __shared__ float row_lds[];  // [rows] losses, then [rows] hits
+    float *row_loss = ticket ? rowbuf : row_lds;
     const float smooth = scal ? scal[3] : smooth_arg;
     const float inv = 1.0f / (float)rows;
     const float on = 1.0f - smooth, off = smooth / (float)nclass;
     const int wave = wave_index(), lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-    for (int r = wave; r < rows; r += nw) {
+    for (int r = blockIdx.x * nw + wave; r < rows; r += gridDim.x * nw) {
         const float *z = logits + (size_t)r * nclass;
         float *d = dl + (size_t)r * nclass;
         const uint32_t yl = labels[r];
@@ -755,15 +761,30 @@ __global__ __launch_bounds__(1024) void softmax_ce_kernel(
         }
     }
     __syncthreads();
+    if (ticket) {
+        // the last block to finish gathers every block's rows into LDS
+        __shared__ int last;
+        if (threadIdx.x == 0) {
+            __threadfence();
+            last = atomicAdd(ticket, 1u) == gridDim.x - 1;
+        }
+        __syncthreads();
+        if (!last) return;
+        __threadfence();
+        for (int i = threadIdx.x; i < 2 * rows; i += blockDim.x)
+            row_lds[i] = __hip_atomic_load(rowbuf + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+    }
     if (threadIdx.x == 0) {
         float l = 0.0f;
         uint32_t ok = 0;
         for (int r = 0; r < rows; r++) {
-            l = l + row_loss[r];
-            ok += row_loss[rows + r] != 0.0f;
+            l = l + row_lds[r];
+            ok += row_lds[rows + r] != 0.0f;
         }
         if (loss_out) loss_out[0] = l * inv;
         if (correct_out) correct_out[0] = ok;
+        if (ticket) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1063,13 +1084,17 @@ int rnn_fc_backward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, c
 
 int rnn_softmax_ce_launch(rnn_ctx *ctx, size_t rows, size_t nclass, const float *logits,
                           const uint32_t *labels, float smooth, const float *scal, float *dl,
-                          float *loss, uint32_t *correct) {
+                          float *loss, uint32_t *correct, uint32_t *ticket, float *rowbuf) {
     if (rows == 0) return RNN_OK;
-    const unsigned threads = (unsigned)std::min<size_t>(64 * rows, 1024);
+    // with a ticket: one row per wave, four waves a block
+    const bool multi = ticket && rowbuf && rows > 4;
+    const unsigned threads = multi ? 256u : (unsigned)std::min<size_t>(64 * rows, 1024);
+    const unsigned blocks = multi ? (unsigned)rnn_div_up(rows, 4) : 1u;
     const size_t lds = 2 * rows * sizeof(float);
     auto go = [&](auto kern) {
-        kern<<<1, threads, lds, ctx->stream>>>(logits, labels, (int)rows, (int)nclass, smooth, scal,
-                                               dl, loss, correct);
+        kern<<<blocks, threads, lds, ctx->stream>>>(logits, labels, (int)rows, (int)nclass, smooth,
+                                                    scal, dl, loss, correct,
+                                                    multi ? ticket : nullptr, rowbuf);
     };
     if (nclass <= 64)
         go(softmax_ce_kernel<1>);

@@ -147,6 +147,10 @@ struct rnn_resnet {
     int nrseg = 0;
     long long nrseg_blocks = 0;
     uint32_t *labels = nullptr, *correct = nullptr;
+    // softmax-CE over several blocks: the last block's ticket (0 between
+    // steps) and the row losses / hits
+    uint32_t *ce_ticket = nullptr;
+    float *ce_rows = nullptr;
     double *part = nullptr;
     // Packed conv weights: one segment per (conv, direction), refreshed by
     // the pass after every SGD step inside the step; packs_dirty marks
@@ -337,6 +341,8 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     const size_t o_rsegs = cv.take(r->params.size() * sizeof(GradSeg));
     const size_t o_lab = cv.take(n * sizeof(uint32_t));
     const size_t o_cor = cv.take(sizeof(uint32_t));
+    const size_t o_tick = cv.take(sizeof(uint32_t));
+    const size_t o_cer = cv.take(2 * n * sizeof(float));
     void *mem = nullptr;
     hipError_t e = hipMalloc(&mem, cv.off);
     if (e != hipSuccess)
@@ -458,6 +464,14 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     }
     r->labels = (uint32_t *)(base + o_lab);
     r->correct = (uint32_t *)(base + o_cor);
+    r->ce_ticket = (uint32_t *)(base + o_tick);
+    r->ce_rows = (float *)(base + o_cer);
+    hipError_t te = hipMemset(r->ce_ticket, 0, sizeof(uint32_t));
+    if (te != hipSuccess) {
+        (void)hipFree(r->arena);
+        r->arena = nullptr;
+        return rnn_fail(ctx, RNN_E_HIP, "resnet plan: %s", hipGetErrorString(te));
+    }
     float *prev = r->s0;
     for (auto &b : r->blocks) {
         b.in = prev;
@@ -718,7 +732,7 @@ int sgd(rnn_resnet *r, const float *scal, float lr, float mom, float wd) {
 int step_body(rnn_resnet *r) {
     TRY(forward(r, true));
     TRY(rnn_softmax_ce_launch(r->ctx, r->n, r->nclass, r->logits, r->labels, 0.0f, r->scal,
-                              r->dlogits, r->loss, r->correct));
+                              r->dlogits, r->loss, r->correct, r->ce_ticket, r->ce_rows));
     return backward(r, r->dlogits, true);
 }
 

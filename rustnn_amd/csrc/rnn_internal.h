@@ -534,10 +534,14 @@ int rnn_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, co
                           const float *w, const float *b, float *y);
 int rnn_fc_backward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
                            const float *x, const float *w, float *dw, float *db, float *dx);
-// scal (device, may be null) overrides smooth with scal[3].
+// scal (device, may be null) overrides smooth with scal[3].  With ticket (a
+// device word that is 0 between launches) and rowbuf (2*rows floats) set,
+// the rows are spread over several blocks and the last one to finish adds
+// them; the same values as the one-block form.
 int rnn_softmax_ce_launch(rnn_ctx *ctx, size_t rows, size_t nclass, const float *logits,
                           const uint32_t *labels, float smooth, const float *scal, float *dl,
-                          float *loss, uint32_t *correct);
+                          float *loss, uint32_t *correct, uint32_t *ticket = nullptr,
+                          float *rowbuf = nullptr);
 // Nesterov SGD over [0, len), weight decay on [0, ndecay); scal (device, may
 // be null) overrides (lr, mom, wd) with scal[0..3].
 int rnn_sgd_launch(rnn_ctx *ctx, size_t len, size_t ndecay, float *v, float *g, float *m, float lr,
