@@ -491,7 +491,10 @@ int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const flo
 // ResNet layer launchers (nn.hip).  One BatchNorm2d layer's device state:
 struct RnnBn {
     const double *part = nullptr;  // train: [c][P][2] partial sums of the layer input
-    int P = 0;                     // set by the launchers
+    // partials per channel in part: 0 = the launchers' per-image-range split
+    // (rnn_bn_stats_launch / the backward's partial pass), else the count a
+    // conv's store pass wrote (rnn_conv_fast_parts)
+    int P = 0;
     float m = 0.f, mom = 0.1f, eps = 1e-5f;  // m = n*hw (set by the launchers)
     float *mean = nullptr, *invstd = nullptr;  // batch statistics (train forward writes)
     float *rm = nullptr, *rv = nullptr;        // running statistics (train: updated if set)
