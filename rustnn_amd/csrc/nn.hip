@@ -1069,7 +1069,7 @@ int rnn_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, co
 int rnn_fc_backward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
                            const float *x, const float *w, float *dw, float *db, float *dx) {
     const unsigned tb = (unsigned)std::min<size_t>(256, rnn_round_up(fin + 1, 64));
-    if (fout) {
+    if (fout && dw && db) {
         fc_bwd_w_kernel<<<(unsigned)fout, tb, 0, ctx->stream>>>(dy, x, (int)rows, (int)fin,
                                                                 (int)fout, dw, db);
         RNN_LAUNCHED(ctx);

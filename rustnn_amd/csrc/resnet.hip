@@ -625,10 +625,9 @@ int resid(rnn_resnet *r, size_t i, size_t c, size_t hw, float *a, const float *a
 // stream) is ready; dy stays untouched until the join.
 bool use_side(const rnn_resnet *r) { return r->overlap && !r->capturing; }
 
-int conv_dw_side(rnn_resnet *r, const NetConv &c, const rnn_conv_spec &sp, const float *dy,
-                 const float *x, size_t &ev) {
+// The side stream waits for the work issued so far on the main stream.
+int fork_side(rnn_resnet *r, size_t &ev) {
     rnn_ctx *ctx = r->ctx;
-    if (!use_side(r)) return conv_dw(r, c, sp, dy, x);
     if (!r->side) RNN_HIP(ctx, hipStreamCreateWithFlags(&r->side, hipStreamNonBlocking));
     if (ev == r->events.size()) {
         hipEvent_t e;
@@ -638,6 +637,14 @@ int conv_dw_side(rnn_resnet *r, const NetConv &c, const rnn_conv_spec &sp, const
     hipEvent_t e = r->events[ev++];
     RNN_HIP(ctx, hipEventRecord(e, ctx->stream));
     RNN_HIP(ctx, hipStreamWaitEvent(r->side, e, 0));
+    return RNN_OK;
+}
+
+int conv_dw_side(rnn_resnet *r, const NetConv &c, const rnn_conv_spec &sp, const float *dy,
+                 const float *x, size_t &ev) {
+    rnn_ctx *ctx = r->ctx;
+    if (!use_side(r)) return conv_dw(r, c, sp, dy, x);
+    TRY(fork_side(r, ev));
     hipStream_t main = ctx->stream;
     ctx->stream = r->side;
     int rc = conv_dw(r, c, sp, dy, x);
@@ -668,8 +675,24 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
     rnn_ctx *ctx = r->ctx;
     const size_t n = r->n, nb = r->blocks.size();
     size_t ev = 0;
-    TRY(rnn_fc_backward_launch(ctx, n, r->fin, r->nclass, dlogits, r->pooled, pv_of(r, r->fc_w),
-                               pg_of(r, r->fc_w), pg_of(r, r->fc_b), r->dpool));
+    if (use_side(r)) {
+        // the classifier's weight gradient on the side stream, its input
+        // gradient on the main one
+        TRY(fork_side(r, ev));
+        hipStream_t main = ctx->stream;
+        ctx->stream = r->side;
+        const int rc = rnn_fc_backward_launch(ctx, n, r->fin, r->nclass, dlogits, r->pooled,
+                                              pv_of(r, r->fc_w), pg_of(r, r->fc_w),
+                                              pg_of(r, r->fc_b), nullptr);
+        ctx->stream = main;
+        TRY(rc);
+        TRY(rnn_fc_backward_launch(ctx, n, r->fin, r->nclass, dlogits, r->pooled,
+                                   pv_of(r, r->fc_w), nullptr, nullptr, r->dpool));
+    } else {
+        TRY(rnn_fc_backward_launch(ctx, n, r->fin, r->nclass, dlogits, r->pooled,
+                                   pv_of(r, r->fc_w), pg_of(r, r->fc_w), pg_of(r, r->fc_b),
+                                   r->dpool));
+    }
     const float *feat = nb == 0 ? r->s0 : r->blocks.back().out;
     // GAP backward (nn.rs:465-473) masked by the last ReLU output
     TRY(resid(r, nb, r->fin, r->fh * r->fw, r->d0, nullptr, feat, r->dpool));
