@@ -263,13 +263,6 @@ __device__ __forceinline__ void issue_stage(const FastArgs &g, StageDMA d, float
     }
 }
 
-// Waves 0..3 compute: WP = 4 / WM along positions (NPW groups of 32 each)
-// times WM along output channels (MB blocks of 32 each).  Waves 4..7 only
-// move data: producer wave 4 + w issues the DMA rows that the row tables
-// assign to wave w, a whole stage at a time, so that the memory pipeline's
-// back-pressure stalls a producer and never the MFMA issue of a compute
-// wave.  One barrier per stage: when it completes, stage s has landed (each
-// producer waited for its own DMA) and stage s - 1's buffer is free.
 // Sums 4 values per lane over the 32 lanes of each half-wave: offsets 16 and
 // 8 each keep half of the values, offsets 4, 2, 1 add the rest; lane l ends
 // with the total of value 2*b4 + b3 (b = bits of l), the 8 lanes that share
@@ -286,7 +279,7 @@ __device__ __forceinline__ double half_reduce4(const double (&x)[4], int l32) {
     return a1 + __shfl_xor(a1, 1, 64);
 }
 
-// The forward's store pass with the batch statistics' sums (see ConvEpi):
+// The forward's store pass with the batch statistics' sums (see ConvStats):
 // the same stores as the plain pass, with the accumulator registers taken 4
 // at a time so that only 4 (sum y, sum y^2) pairs are live; each wave's
 // totals over the item's positions, reduced over its lanes, are left in red
@@ -343,6 +336,16 @@ __device__ __forceinline__ void store_stats(
     });
 }
 
+// Waves 0..3 compute: WP = 4 / WM along positions (NPW groups of 32 each)
+// times WM along output channels (MB blocks of 32 each).  Waves 4..7 only
+// move data: producer wave 4 + w issues the DMA rows that the row tables
+// assign to wave w, a whole stage at a time, so that the memory pipeline's
+// back-pressure stalls a producer and never the MFMA issue of a compute
+// wave.  One barrier per stage: when it completes, stage s has landed (each
+// producer waited for its own DMA) and stage s - 1's buffer is free.
+// EPI = 1: the forward's store pass also takes the batch statistics
+// (store_stats, ConvStats), with one more barrier per work item that the
+// producers match.
 template <int K, int S, int P, bool DX, int NPW, int MB, int WM, int EPI>
 __global__ __launch_bounds__(64 * FAST_NW * 2)
 __attribute__((amdgpu_waves_per_eu(EPI ? 4 : 1))) void conv_fast_kernel(FastArgs g) {
