@@ -593,6 +593,45 @@ __global__ void fc_fwd_kernel(const float *__restrict__ x, const float *__restri
     y[t] = s;
 }
 
+// gap then Linear::forward for image blockIdx.x in one launch: thread c <
+// fin pools channel c as gap_fwd_kernel does (the same adds in the same
+// order, then / hw) into pooled and LDS; thread o < fout then forms y[i][o]
+// as fc_fwd_kernel does (b[o], then w[o][j]*x[j] in j order).  The same bits
+// as the two launches.
+__global__ __launch_bounds__(1024) void gap_fc_fwd_kernel(const float *__restrict__ x, int hw,
+                                                          int fin, int fout, int vec,
+                                                          const float *__restrict__ w,
+                                                          const float *__restrict__ b,
+                                                          float *pooled, float *y) {
+    extern __shared__ float xs[];  // [fin]
+    const int i = blockIdx.x;
+    for (int c = threadIdx.x; c < fin; c += blockDim.x) {
+        const float *p = x + ((size_t)i * fin + c) * hw;
+        float s = 0.0f;
+        if (vec) {
+            for (int j = 0; j < hw; j += 4) {
+                const float4 v = *reinterpret_cast<const float4 *>(p + j);
+                s = s + v.x;
+                s = s + v.y;
+                s = s + v.z;
+                s = s + v.w;
+            }
+        } else {
+            for (int j = 0; j < hw; j++) s = s + p[j];
+        }
+        s = s / (float)hw;
+        pooled[(size_t)i * fin + c] = s;
+        xs[c] = s;
+    }
+    __syncthreads();
+    for (int o = threadIdx.x; o < fout; o += blockDim.x) {
+        const float *wr = w + (size_t)o * fin;
+        float s = b[o];
+        for (int j = 0; j < fin; j++) s = s + wr[j] * xs[j];
+        y[(size_t)i * fout + o] = s;
+    }
+}
+
 // Linear::backward_w (nn.rs:521-537): w.g[o][j] += dy[i][o]*x[i][j] in row
 // order, zero gradients skipped.  Block o; thread j (coalesced over x rows);
 // thread j == fin adds the bias: b.g[o] += dy[i][o].
@@ -1048,6 +1087,23 @@ int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy,
     if (nc * hw == 0) return RNN_OK;
     gap_bwd_kernel<<<ew_grid(ctx, nc * hw), EW_THREADS, 0, ctx->stream>>>(dy, (int)hw, nc * hw,
                                                                          dx);
+    RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+int rnn_gap_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t hw, size_t fout,
+                              const float *x, const float *w, const float *b, float *pooled,
+                              float *y) {
+    if (rows == 0 || fin == 0) return RNN_OK;
+    if (fin > 8192 || rows > 0x7fffffff) {
+        const int rc = rnn_gap_forward_launch(ctx, rows * fin, hw, x, pooled);
+        return rc ? rc : rnn_fc_forward_launch(ctx, rows, fin, fout, pooled, w, b, y);
+    }
+    const int vec = (hw & 3) == 0 && aligned16(x);
+    const unsigned threads =
+        (unsigned)std::min<size_t>(1024, rnn_round_up(std::max(fin, fout), 64));
+    gap_fc_fwd_kernel<<<(unsigned)rows, threads, fin * sizeof(float), ctx->stream>>>(
+        x, (int)hw, (int)fin, (int)fout, vec, w, b, pooled, y);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

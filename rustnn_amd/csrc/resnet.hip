@@ -569,9 +569,8 @@ int forward(rnn_resnet *r, bool train) {
         }
     }
     const float *feat = r->blocks.empty() ? r->s0 : r->blocks.back().out;
-    TRY(rnn_gap_forward_launch(ctx, n * r->fin, r->fh * r->fw, feat, r->pooled));
-    TRY(rnn_fc_forward_launch(ctx, n, r->fin, r->nclass, r->pooled, pv_of(r, r->fc_w),
-                              pv_of(r, r->fc_b), r->logits));
+    TRY(rnn_gap_fc_forward_launch(ctx, n, r->fin, r->fh * r->fw, r->nclass, feat,
+                                  pv_of(r, r->fc_w), pv_of(r, r->fc_b), r->pooled, r->logits));
     r->fwd_train = train;
     return RNN_OK;
 }

@@ -535,6 +535,11 @@ int rnn_gap_forward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *x, f
 int rnn_gap_backward_launch(rnn_ctx *ctx, size_t nc, size_t hw, const float *dy, float *dx);
 int rnn_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
                           const float *w, const float *b, float *y);
+// gap (pooled [rows][fin]) then the classifier y = pooled W^T + b in one
+// launch, the same bits as the two launches.
+int rnn_gap_fc_forward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t hw, size_t fout,
+                              const float *x, const float *w, const float *b, float *pooled,
+                              float *y);
 int rnn_fc_backward_launch(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
                            const float *x, const float *w, float *dw, float *db, float *dx);
 // scal (device, may be null) overrides smooth with scal[3].  With ticket (a
