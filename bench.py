@@ -8,14 +8,18 @@ Headline (`value`, images/s): BASELINE config 3, the full ResNet-20 (W=32)
 train step at batch 128 on 32x32 synthetic images -- forward, softmax
 cross-entropy (smoothing 0.1), backward and the Nesterov SGD step (lr 0.2,
 momentum 0.9, wd 5e-4) -- through the device-resident runtime (rnn_resnet_*,
-replayed from a hipGraph), every operand resident in HBM.  One "step" is one
-train step on one batch; `value` = steps * 128 / timed seconds.
+issued eagerly on two streams: the weight gradients run on a second stream
+beside the input-gradient chain), every operand resident in HBM.  One "step"
+is one train step on one batch; `value` = steps * 128 / timed seconds.
 
 Also reported:
-  * `roofline`: the kernel with the largest share of the ResNet step, timed
-    on its own with HIP events on the library's stream: its algorithmic FLOP
-    per launch / average launch duration vs the 157.3 TFLOP/s fp32 MFMA peak;
-    `traffic` from the committed rocprofv3 --pmc summary;
+  * `roofline`: the kernel with the largest share of the ResNet step: its
+    algorithmic FLOP per launch / its average launch duration in the
+    committed rocprofv3 kernel trace (profiles/conv_sweep_kernel_stats.md)
+    vs the 157.3 TFLOP/s fp32 MFMA peak (`frac`); the same kernel timed live
+    with HIP events on the library's stream beside it (`live`); `traffic`
+    from the committed rocprofv3 --pmc summary and `traffic_ratio` = that
+    traffic / the op's algorithmic bytes;
   * `cpu_baseline`: the restated reference CPU path (oracle/, AVX2 micro-kernel,
     OpenMP) running the same ResNet-20 train step on this host's cores for a
     bounded number of steps;
@@ -97,6 +101,27 @@ def traffic_from_profiles(op):
     return None
 
 
+def op_bytes(op):
+    """Algorithmic HBM bytes of one launch of a sweep op ("name:pass"), each
+    tensor once: fwd x + W + y, dx dY + W + dX, dw / dw_kernel dY + x + dW.
+    A 1x1 stride-2 op counts only the x positions its window samples.  None
+    for an op outside the sweep."""
+    name, _, ps = op.partition(":")
+    for nm, cin, cout, k, s, p, h in SWEEP:
+        if nm != name:
+            continue
+        oh = (h + 2 * p - k) // s + 1
+        xin = N * cin * (oh * oh if k == 1 else h * h)
+        w, yo = cout * cin * k * k, N * cout * oh * oh
+        if ps == "fwd":
+            return 4 * (xin + w + yo)
+        if ps == "dx":
+            return 4 * (yo + w + N * cin * h * h)
+        if ps in ("dw", "dw_kernel"):
+            return 4 * (yo + xin + w)
+    return None
+
+
 def profile_kernels(op):
     """The kernel rows of `op` in the committed rocprofv3 kernel-trace summary
     profiles/conv_sweep_kernel_stats.md: [(kernel template, avg us)], the
@@ -161,9 +186,8 @@ def cpu_protocol(samples=3, cooldown_s=1.0):
     config 1 (the whole sweep, forward + dX + dW of every shape at batch
     128), config 2 (Core forward and backward, 512 problems), the six
     --gemmbench shapes (1 warm-up + 5 reps, bench.rs:29-35) and the config-3
-    ResNet-20 train step (batch 128 on all cores; a batch of 32 on one
-    thread, where a step of 128 would take about 8 s per sample; on one
-    thread each gemm shape is 1 warm-up + 1 timed call)."""
+    ResNet-20 train step at batch 128 (one warm-up step, then one timed
+    step per sample), on all cores and on the one pinned thread alike."""
     import numpy as np
     from oracle import pyorc as O
     from oracle import pymodel as M
@@ -219,18 +243,21 @@ def cpu_protocol(samples=3, cooldown_s=1.0):
             lambda: O.attn_backward(desc, n2, qkv, qkv, tau, p_att, dout, z, z,
                                     np.zeros(h2, np.float32),
                                     np.zeros(h2 * nrel, np.float32))) / 1e9
-        reps = 5 if threads > 1 else 1
+        reps = 5
         for tag, m, n, k, at, bt, a, b in gem:
             O.matmul(m, n, k, a, at, b, bt)  # bench.rs:29-30: one untimed call
             r["gemm " + tag] = 2.0 * m * n * k * reps / timed(
                 lambda: [O.matmul(m, n, k, a, at, b, bt) for _ in range(reps)]) / 1e9
-        bs = c["batch"] if threads > 1 else 32
+        bs = c["batch"]
         step = lambda: net.train_step(xr[:bs], lab[:bs], c["smooth"], c["lr"], c["mom"], c["wd"])
-        step()
+        if threads not in warmed:
+            step()
+            warmed.add(threads)
         r["config3_step"] = bs / timed(step)
         return r
 
     out = {}
+    warmed = set()
     for label, threads in (("all_cores", allt), ("one_thread", 1)):
         best = {}
         for i in range(samples):
@@ -249,7 +276,9 @@ def cpu_protocol(samples=3, cooldown_s=1.0):
                     "config3_step": "images/s"}
     out["protocol"] = (f"best of {samples} samples, {cooldown_s:g} s cooldown between samples, "
                        "OMP_PROC_BIND=close; one thread pinned with sched_setaffinity; "
-                       "one thread: config 3 at batch 32, gemm shapes 1 warm-up + 1 call")
+                       "gemm shapes 1 warm-up + 5 timed calls (bench.rs:29-35); config-3 step "
+                       "at batch 128 after one warm-up step per thread count, one timed step "
+                       "per sample")
     out["host"] = host_cpu()
     out["label"] = "restated reference CPU path (oracle/, C + AVX2), not the Rust binary"
     return out
@@ -890,22 +919,31 @@ def main():
                                in_resnet_step=RESNET_OPS[L["name"]]))
 
     def roofline(op_row, flops):
-        achieved = flops / (op_row["ms"] * 1e-3) / 1e12
-        out = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
-               "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
-               "traffic": traffic_from_profiles(op_row["op"]), "kernel": op_row["op"],
-               "flop_per_launch": flops, "avg_launch_ms": op_row["ms"],
-               "timing": "graph replays of op-reps back-to-back launches (launch gaps "
-                         "included), HIP events on the library's stream"}
+        # `achieved` / `frac`: the kernel's average duration in the committed
+        # rocprofv3 kernel trace (every dispatch serialised and timed alone),
+        # so the figure follows from profiles/; the live graph-replay timing
+        # of this run (back-to-back launches, which hide part of each
+        # dispatch's start-up) sits beside it under `live`.
+        live_tf = flops / (op_row["ms"] * 1e-3) / 1e12
+        live = {"achieved": round(live_tf, 3), "frac": round(live_tf / PEAK_FP32_MFMA_TFLOPS, 4),
+                "avg_launch_ms": op_row["ms"],
+                "timing": "graph replays of op-reps back-to-back launches (launch gaps "
+                          "included), HIP events on the library's stream"}
         prof = profile_kernels(op_row["op"])
         if prof:
-            # the same kernel's average duration in the committed kernel trace
-            # (kernel time alone, no launch gaps)
             us = prof[0][1]
-            out["template"] = prof[0][0]
-            out["rocprof"] = {"avg_launch_us": us,
-                              "frac": round(flops / (us * 1e-6) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4),
-                              "source": "profiles/conv_sweep_kernel_stats.md"}
+            achieved, src = flops / (us * 1e-6) / 1e12, "profiles/conv_sweep_kernel_stats.md"
+        else:
+            us, achieved, src = op_row["ms"] * 1e3, live_tf, "live (op not in the kernel trace)"
+        traffic = traffic_from_profiles(op_row["op"])
+        alg = op_bytes(op_row["op"])
+        out = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+               "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+               "traffic": traffic,
+               "traffic_ratio": round(traffic / alg, 3) if traffic and alg else None,
+               "algorithmic_bytes": alg, "kernel": op_row["op"],
+               "template": prof[0][0] if prof else None,
+               "flop_per_launch": flops, "avg_launch_us": us, "source": src, "live": live}
         return out
 
     lay = {L["name"]: L for L in layers}

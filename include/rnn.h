@@ -47,6 +47,8 @@ typedef struct rnn_ctx rnn_ctx;
 /* Replaces the process-wide rayon pool + thread-local scratch
  * (main.rs:41-48, gemm.rs:411-420): one device, one stream, one workspace. */
 int rnn_ctx_create(int device, rnn_ctx **out);
+/* Runs any reductions the deferral below still holds (rnn_ctx_flush), waits
+ * for the stream, then frees the context; returns the flush's status. */
 int rnn_ctx_destroy(rnn_ctx *ctx);
 /* Use `stream` (a hipStream_t; NULL = the null stream) for later calls. */
 int rnn_ctx_set_stream(rnn_ctx *ctx, void *stream);
@@ -140,8 +142,14 @@ int rnn_conv2d_backward_w_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n,
  * calls no hipMalloc / hipFree.  A shape whose slabs need more than the
  * scratch (cout*cin*k*k*4 bytes times the slab count; 9.4 MB for the ResNet
  * convs at batch 128) returns RNN_E_UNSUPPORTED.  Every call on one device
- * shares that scratch: calls that overlap on one GPU (several contexts or
- * streams at once) race and must be serialised by the caller. */
+ * shares that scratch.  Outside graph capture the library orders them: a
+ * call on another stream than the device's previous call first waits for
+ * that call's kernels (hipStreamWaitEvent; one event per device, created by
+ * the first such call).  Under graph capture it does not: captured calls
+ * that could run at the same time on one GPU race, and the caller orders
+ * them (one stream, or graph edges between them).  The scratch address is
+ * looked up by the first call on a device (hipGetSymbolAddress); a failed
+ * lookup returns RNN_E_HIP from this call only. */
 int rnn_conv2d_backward_w_noalloc(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n,
                                   const float *dy, const float *x, float *dw);
 /* dX half of Conv2d::backward (nn.rs:230-250) -> conv::dx_image
@@ -214,6 +222,52 @@ int rnn_linear_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const
  * be NULL); dx = dy W (overwritten). */
 int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
                         const float *x, const float *w, float *dw, float *db, float *dx);
+
+/* ------------------------------------------ host-slice forms (Rust shim) */
+/* The same entry points over HOST memory, for the Rust shim, whose callers
+ * keep the reference's Vec<f32> tensors (nn.rs Tensor, linear.rs, attn.rs
+ * Tok): each call copies its operands into a device staging block the
+ * context keeps (it only grows), runs the device entry point on the context
+ * stream, runs any deferred reductions, copies the outputs back and returns
+ * after the stream has finished.  Arguments, accumulation and the k = 0 /
+ * empty cases are those of the device form; a host pointer passed for two
+ * operands (a fused QKV buffer as q and kv; dq == dkv as SelfAttn::backward
+ * passes them, attn.rs:418-438) is staged once.  Each replaces the same
+ * reference function as its device form:
+ *   rnn_matmul_host              matmul        (gemm.rs:434-493)
+ *   rnn_gemm_small_batched_host  gemm_small    (gemm.rs:500-545), C read back whole
+ *   rnn_matmul_dw_host           matmul_dw     (gemm.rs:555-598)
+ *   rnn_conv2d_forward_host      Conv2d::forward    (nn.rs:166-185)
+ *   rnn_conv2d_backward_w_host   Conv2d::backward_w (nn.rs:193-227)
+ *   rnn_conv2d_backward_x_host   dX of Conv2d::backward (nn.rs:230-250)
+ *   rnn_attn_forward_host        Core::forward (attn.rs:148-223)
+ *   rnn_attn_backward_host       Core::backward (attn.rs:226-343)
+ *   rnn_linear_forward_host      Linear::forward (linear.rs:44-64)
+ *   rnn_linear_backward_host     Linear::backward (linear.rs:66-96) */
+int rnn_matmul_host(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a, int at,
+                    const float *b, int bt, float *c, int acc);
+int rnn_gemm_small_batched_host(rnn_ctx *ctx, size_t count, size_t m, size_t n, size_t k,
+                                const float *a, size_t stride_a, int at, const float *b,
+                                size_t stride_b, int bt, float *c, size_t stride_c, int acc);
+int rnn_matmul_dw_host(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *a,
+                       const float *b, float *c);
+int rnn_conv2d_forward_host(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *x,
+                            const float *w, float *y);
+int rnn_conv2d_backward_w_host(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n,
+                               const float *dy, const float *x, float *dw);
+int rnn_conv2d_backward_x_host(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n,
+                               const float *dy, const float *w, float *dx);
+int rnn_attn_forward_host(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
+                          const float *kv, const float *tau, const float *rel, float *p,
+                          float *o);
+int rnn_attn_backward_host(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float *q,
+                           const float *kv, const float *tau, const float *p, const float *dout,
+                           float *dq, float *dkv, float *dtau, float *drel);
+int rnn_linear_forward_host(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
+                            const float *w, const float *b, float *y);
+int rnn_linear_backward_host(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout,
+                             const float *dy, const float *x, const float *w, float *dw,
+                             float *db, float *dx);
 
 /* -------------------------------------------------------------- nn.rs */
 /* The ResNet layers around the convs.  Elementwise formulas round exactly as

@@ -252,6 +252,10 @@ void orc_cifar_batch_train(const uint8_t *images, const uint8_t *fine, const uin
 void orc_mix_batch(float *x, size_t bs, float alpha_mix, float alpha_cut, float sw, orc_rng *r,
                    uint32_t *perm, float *lam);
 
+/* ---------------------------------------------------------------- train.rs */
+uint64_t orc_fnv1a_bytes(uint64_t h, const uint8_t *p, size_t n);
+uint64_t orc_fnv1a_f32(uint64_t h, const float *v, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

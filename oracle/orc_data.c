@@ -283,3 +283,28 @@ void orc_mix_batch(float *x, size_t bs, float alpha_mix, float alpha_cut, float 
     }
     free(p);
 }
+
+/* ---------------------------------------------------------------- train.rs
+ * FNV-1a 64 of Trainer::fingerprint (train.rs:474-484): offset basis
+ * 0xcbf29ce484222325, prime 0x100000001b3; per byte h = (h ^ b) * prime
+ * (mod 2^64).  fnv_f32 folds a float as the 4 little-endian bytes of its bit
+ * pattern. */
+uint64_t orc_fnv1a_bytes(uint64_t h, const uint8_t *p, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        h ^= (uint64_t)p[i];
+        h *= 0x00000100000001b3ull;
+    }
+    return h;
+}
+
+uint64_t orc_fnv1a_f32(uint64_t h, const float *v, size_t n) {
+    for (size_t i = 0; i < n; i++) {
+        uint32_t bits;
+        memcpy(&bits, &v[i], 4);
+        for (int k = 0; k < 4; k++) {
+            h ^= (uint64_t)((bits >> (8 * k)) & 0xffu);
+            h *= 0x00000100000001b3ull;
+        }
+    }
+    return h;
+}

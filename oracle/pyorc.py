@@ -189,6 +189,10 @@ def lib():
                                             C.c_float, _sz, C.c_uint64, _f32p, _u32p, _u32p]
         L.orc_mix_batch.argtypes = [_f32p, _sz, C.c_float, C.c_float, C.c_float, P(RngState),
                                     _u32p, _f32p]
+        L.orc_fnv1a_bytes.argtypes = [C.c_uint64, C.c_char_p, _sz]
+        L.orc_fnv1a_bytes.restype = C.c_uint64
+        L.orc_fnv1a_f32.argtypes = [C.c_uint64, _f32p, _sz]
+        L.orc_fnv1a_f32.restype = C.c_uint64
         _lib = L
     return _lib
 
@@ -830,3 +834,20 @@ def mix_batch(x, alpha_mix, alpha_cut, sw, rng):
     perm, lam = np.empty(bs, np.uint32), np.empty(bs, np.float32)
     lib().orc_mix_batch(x.reshape(-1), bs, alpha_mix, alpha_cut, sw, C.byref(rng.st), perm, lam)
     return perm, lam
+
+
+# ---------------------------------------------------------------- train.rs
+FNV_OFFSET = 0xCBF29CE484222325  # train.rs:474
+
+
+def fnv1a_bytes(h, data):
+    """FNV-1a 64 over bytes, continuing from hash h (train.rs:476-484)."""
+    data = bytes(data)
+    return int(lib().orc_fnv1a_bytes(C.c_uint64(h), data, len(data)))
+
+
+def fnv1a_f32(h, values):
+    """fnv_f32 (train.rs:479-484) over every value of `values` in order: each
+    float as the 4 little-endian bytes of its bit pattern."""
+    v = np.ascontiguousarray(np.asarray(values, np.float32).ravel())
+    return int(lib().orc_fnv1a_f32(C.c_uint64(h), v, v.size))

@@ -663,6 +663,24 @@ class Trainer:
         self.step_no += 1
         return lr
 
+    def fingerprint(self, last_loss):
+        """Trainer::fingerprint (train.rs:450-470): FNV-1a from the offset
+        basis over, per parameter in for_each_param order, its values, then
+        its momentum, then its AdamW second moment (empty -- nothing folded
+        -- until AdamW first steps the tensor, optim.rs:208-210, and always
+        for a Muon matrix); then every EMA tensor (none before the EMA's
+        first update, optim.rs:270-276); then Optim::t as 8 little-endian
+        bytes; then the last loss as an f32."""
+        h = O.FNV_OFFSET
+        for p in self.net.params():
+            for arr in (p.v, p.m, getattr(p, "v2", None)):
+                if arr is not None:
+                    h = O.fnv1a_f32(h, arr)
+        for w in self.ema_w or []:
+            h = O.fnv1a_f32(h, w)
+        h = O.fnv1a_bytes(h, int(self.t).to_bytes(8, "little"))
+        return O.fnv1a_f32(h, np.float32(last_loss))
+
     def step(self, x, labels, coarse, perm=None, lam=None, lr=None):
         """One Trainer::step; returns (total, ce, correct, lr, outputs)."""
         total, ce, correct, out = self.forward_backward(x, labels, coarse, perm, lam)

@@ -142,6 +142,10 @@ def render():
         tail = "" if r == "()" else f" -> {r}"
         out.append(f"    pub fn {name}({args}){tail};")
     out.append("}")
+    out.append("")
+    out.append("// Hand-written safe layer (src/safe.rs): the reference's call-site")
+    out.append("// signatures over the *_host entry points.")
+    out.append("pub mod safe;")
     return "\n".join(out) + "\n"
 
 

@@ -93,6 +93,16 @@ extern "C" {
     pub fn rnn_attn_backward_ex(ctx: *mut rnn_ctx, d: *const rnn_attn_desc, n: usize, q: *const f32, kv: *const f32, tau: *const f32, p: *const f32, dout: *const f32, dq: *mut f32, dkv: *mut f32, dtau: *mut f32, drel: *mut f32, flags: u32) -> c_int;
     pub fn rnn_linear_forward(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, x: *const f32, w: *const f32, b: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_linear_backward(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, dy: *const f32, x: *const f32, w: *const f32, dw: *mut f32, db: *mut f32, dx: *mut f32) -> c_int;
+    pub fn rnn_matmul_host(ctx: *mut rnn_ctx, m: usize, n: usize, k: usize, a: *const f32, at: c_int, b: *const f32, bt: c_int, c: *mut f32, acc: c_int) -> c_int;
+    pub fn rnn_gemm_small_batched_host(ctx: *mut rnn_ctx, count: usize, m: usize, n: usize, k: usize, a: *const f32, stride_a: usize, at: c_int, b: *const f32, stride_b: usize, bt: c_int, c: *mut f32, stride_c: usize, acc: c_int) -> c_int;
+    pub fn rnn_matmul_dw_host(ctx: *mut rnn_ctx, m: usize, n: usize, k: usize, a: *const f32, b: *const f32, c: *mut f32) -> c_int;
+    pub fn rnn_conv2d_forward_host(ctx: *mut rnn_ctx, sp: *const rnn_conv_spec, n: usize, x: *const f32, w: *const f32, y: *mut f32) -> c_int;
+    pub fn rnn_conv2d_backward_w_host(ctx: *mut rnn_ctx, sp: *const rnn_conv_spec, n: usize, dy: *const f32, x: *const f32, dw: *mut f32) -> c_int;
+    pub fn rnn_conv2d_backward_x_host(ctx: *mut rnn_ctx, sp: *const rnn_conv_spec, n: usize, dy: *const f32, w: *const f32, dx: *mut f32) -> c_int;
+    pub fn rnn_attn_forward_host(ctx: *mut rnn_ctx, d: *const rnn_attn_desc, n: usize, q: *const f32, kv: *const f32, tau: *const f32, rel: *const f32, p: *mut f32, o: *mut f32) -> c_int;
+    pub fn rnn_attn_backward_host(ctx: *mut rnn_ctx, d: *const rnn_attn_desc, n: usize, q: *const f32, kv: *const f32, tau: *const f32, p: *const f32, dout: *const f32, dq: *mut f32, dkv: *mut f32, dtau: *mut f32, drel: *mut f32) -> c_int;
+    pub fn rnn_linear_forward_host(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, x: *const f32, w: *const f32, b: *const f32, y: *mut f32) -> c_int;
+    pub fn rnn_linear_backward_host(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, dy: *const f32, x: *const f32, w: *const f32, dw: *mut f32, db: *mut f32, dx: *mut f32) -> c_int;
     pub fn rnn_bn_forward_train(ctx: *mut rnn_ctx, n: usize, c: usize, hw: usize, x: *const f32, y: *mut f32, gamma: *const f32, beta: *const f32, running_mean: *mut f32, running_var: *mut f32, mean: *mut f32, invstd: *mut f32, momentum: f32, eps: f32, relu: c_int) -> c_int;
     pub fn rnn_bn_forward_eval(ctx: *mut rnn_ctx, n: usize, c: usize, hw: usize, x: *const f32, y: *mut f32, gamma: *const f32, beta: *const f32, running_mean: *const f32, running_var: *const f32, eps: f32, relu: c_int) -> c_int;
     pub fn rnn_bn_backward(ctx: *mut rnn_ctx, n: usize, c: usize, hw: usize, dy: *const f32, relu_out: *const f32, x: *const f32, mean: *const f32, invstd: *const f32, gamma: *const f32, dx: *mut f32, dgamma: *mut f32, dbeta: *mut f32) -> c_int;
@@ -176,3 +186,7 @@ extern "C" {
     pub fn rnn_dbg_pack_b(ctx: *mut rnn_ctx, b: *const f32, n: usize, k: usize, transposed: c_int, out: *mut f32) -> c_int;
     pub fn rnn_dbg_rel_index(ctx: *mut rnn_ctx, th: u32, tw: u32, mh: u32, mw: u32, idx: *mut u32) -> c_int;
 }
+
+// Hand-written safe layer (src/safe.rs): the reference's call-site
+// signatures over the *_host entry points.
+pub mod safe;

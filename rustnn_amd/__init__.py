@@ -124,6 +124,20 @@ def lib():
                                           _vp, _vp, _vp, _u32]),
             "rnn_linear_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
             "rnn_linear_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_matmul_host": (_i, [_vp, _sz, _sz, _sz, _vp, _i, _vp, _i, _vp, _i]),
+            "rnn_gemm_small_batched_host": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _i, _vp,
+                                                 _sz, _i, _vp, _sz, _i]),
+            "rnn_matmul_dw_host": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp]),
+            "rnn_conv2d_forward_host": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
+            "rnn_conv2d_backward_w_host": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
+            "rnn_conv2d_backward_x_host": (_i, [_vp, P(ConvSpec), _sz, _vp, _vp, _vp]),
+            "rnn_attn_forward_host": (_i, [_vp, P(AttnDesc), _sz, _vp, _vp, _vp, _vp, _vp,
+                                           _vp]),
+            "rnn_attn_backward_host": (_i, [_vp, P(AttnDesc), _sz, _vp, _vp, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _vp]),
+            "rnn_linear_forward_host": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "rnn_linear_backward_host": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
+                                              _vp]),
             "rnn_dbg_im2col": (_i, [_vp, P(ConvSpec), _vp, _vp]),
             "rnn_dbg_pack_a": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
             "rnn_dbg_pack_b": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
@@ -281,9 +295,13 @@ class Context:
         return int(lib().rnn_ctx_workspace_bytes(self.h))
 
     def close(self):
+        """rnn_ctx_destroy: runs the reductions a deferral still holds, then
+        frees the context; raises if that flush failed."""
         if getattr(self, "h", None):
-            lib().rnn_ctx_destroy(self.h)
-            self.h = None
+            h, self.h = self.h, None
+            rc = lib().rnn_ctx_destroy(h)
+            if rc != RNN_OK:
+                raise RnnError(rc, lib().rnn_status_string(rc).decode())
 
     def __del__(self):
         try:

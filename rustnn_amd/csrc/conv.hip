@@ -536,10 +536,12 @@ int rnn_conv2d_backward_w_noalloc(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t 
     if (n == 0) return RNN_OK;
     if (!dy || !x || !dw)
         return rnn_fail(ctx, RNN_E_NULL, "conv2d_backward_w_noalloc: null operand");
-    if (!ctx->noalloc_scratch)
-        return rnn_fail(ctx, RNN_E_HIP, "conv2d_backward_w_noalloc: no scratch address");
-    return rnn_conv_dw(ctx, sp, n, dy, x, dw, ctx->noalloc_scratch,
-                       RNN_NOALLOC_SCRATCH_BYTES / sizeof(float));
+    float *scr = nullptr;
+    rc = rnn_noalloc_scratch(ctx, &scr);
+    if (rc) return rc;
+    return rnn_noalloc_run(ctx, [&] {
+        return rnn_conv_dw(ctx, sp, n, dy, x, dw, scr, RNN_NOALLOC_SCRATCH_BYTES / sizeof(float));
+    });
 }
 
 size_t rnn_conv2d_backward_w_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n) {

@@ -799,6 +799,10 @@ __global__ __launch_bounds__(1024) void softmax_ce_kernel(
             row_loss[rows + r] = arg == y ? 1.0f : 0.0f;
         }
     }
+    // every wave releases its own row stores at agent scope before the
+    // barrier, so the block's ticket below orders all of them, not only
+    // thread 0's
+    if (ticket) __threadfence();
     __syncthreads();
     if (ticket) {
         // the last block to finish gathers every block's rows into LDS

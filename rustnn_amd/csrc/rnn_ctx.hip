@@ -37,6 +37,57 @@ static int scratch_address(int device, float **out) {
     return RNN_OK;
 }
 
+// Per device: the lock the no-allocation calls hold while they enqueue, and
+// the event recorded after the last call's kernels with the stream it was
+// recorded on, so that a call on another stream waits for that one first.
+struct NoallocOrder {
+    std::mutex mu;
+    hipEvent_t last = nullptr;
+    hipStream_t last_stream = nullptr;
+    bool pending = false;
+};
+static std::mutex g_order_mu;
+static std::map<int, NoallocOrder> g_order;
+
+static NoallocOrder &noalloc_order(int device) {
+    std::lock_guard<std::mutex> lk(g_order_mu);
+    return g_order[device];
+}
+
+int rnn_noalloc_scratch(rnn_ctx *ctx, float **out) {
+    if (ctx->noalloc_scratch) {
+        *out = ctx->noalloc_scratch;
+        return RNN_OK;
+    }
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return RNN_E_HIP;
+    if (cur != ctx->device && hipSetDevice(ctx->device) != hipSuccess) return RNN_E_HIP;
+    const int rc = scratch_address(ctx->device, &ctx->noalloc_scratch);
+    if (cur != ctx->device) (void)hipSetDevice(cur);
+    if (rc != RNN_OK) return rnn_fail(ctx, rc, "no-allocation scratch: hipGetSymbolAddress failed");
+    *out = ctx->noalloc_scratch;
+    return RNN_OK;
+}
+
+int rnn_noalloc_run(rnn_ctx *ctx, const std::function<int()> &enqueue) {
+    NoallocOrder &o = noalloc_order(ctx->device);
+    std::lock_guard<std::mutex> lk(o.mu);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    RNN_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cap));
+    const bool eager = cap == hipStreamCaptureStatusNone;
+    // the previous call on this device ran on another stream: this stream
+    // waits for its kernels before reusing the scratch
+    if (eager && o.pending && o.last_stream != ctx->stream)
+        RNN_HIP(ctx, hipStreamWaitEvent(ctx->stream, o.last, 0));
+    const int rc = enqueue();
+    if (rc != RNN_OK || !eager) return rc;
+    if (!o.last) RNN_HIP(ctx, hipEventCreateWithFlags(&o.last, hipEventDisableTiming));
+    RNN_HIP(ctx, hipEventRecord(o.last, ctx->stream));
+    o.last_stream = ctx->stream;
+    o.pending = true;
+    return RNN_OK;
+}
+
 int rnn_fail(rnn_ctx *ctx, int code, const char *fmt, ...) {
     if (ctx) {
         va_list ap;
@@ -241,11 +292,6 @@ int rnn_ctx_create(int device, rnn_ctx **out) {
         return RNN_E_HIP;
     }
     c->own_stream = true;
-    if (scratch_address(device, &c->noalloc_scratch) != RNN_OK) {
-        (void)hipStreamDestroy(c->stream);
-        delete c;
-        return RNN_E_HIP;
-    }
     *out = c;
     return RNN_OK;
 }
@@ -253,8 +299,13 @@ int rnn_ctx_create(int device, rnn_ctx **out) {
 int rnn_ctx_destroy(rnn_ctx *ctx) {
     if (!ctx) return RNN_E_NULL;
     (void)hipSetDevice(ctx->device);
-    (void)hipStreamSynchronize(ctx->stream);
+    // gradient reductions still queued by the deferral run before the
+    // arena that holds their partials is freed
+    int rc = RNN_OK;
+    if (!ctx->dsegs.empty()) rc = defer_flush(ctx);
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess && rc == RNN_OK) rc = RNN_E_HIP;
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->hstage) (void)hipFree(ctx->hstage);
     for (auto &b : ctx->darena) (void)hipFree(b.first);
     for (auto &t : ctx->rel_tables) {
         if (t.dev) (void)hipFree(t.dev);
@@ -263,7 +314,7 @@ int rnn_ctx_destroy(rnn_ctx *ctx) {
     for (auto &kv : ctx->tables) rnn_dev_table_free(kv.second);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
-    return RNN_OK;
+    return rc;
 }
 
 int rnn_ctx_set_stream(rnn_ctx *ctx, void *stream) {

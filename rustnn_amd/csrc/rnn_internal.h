@@ -7,6 +7,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <cstdio>
+#include <functional>
 #include <map>
 #include <mutex>
 #include <vector>
@@ -58,13 +59,17 @@ struct rnn_ctx {
     int num_cus = 256;
     // Device address of this device's copy of the fixed scratch array of the
     // no-allocation entry points (RNN_NOALLOC_SCRATCH_BYTES, rnn_ctx.hip),
-    // looked up once per device by rnn_ctx_create.
+    // looked up by the first such call (rnn_noalloc_scratch).
     float *noalloc_scratch = nullptr;
     // Growing device workspace (split-K partials, packed weights, attention
     // reductions).  Reallocated only when a call needs more; the stream is
     // synchronised first so no in-flight kernel still reads the old block.
     void *ws = nullptr;
     size_t ws_bytes = 0;
+    // Staging block of the *_host entry points (host slices copied in and
+    // out around a device call); grows like the workspace.
+    void *hstage = nullptr;
+    size_t hstage_bytes = 0;
     // Attention relative-index tables, each uploaded once and kept until the
     // context ends (a step that switches between geometries never waits).
     std::vector<RnnRelTable> rel_tables;
@@ -215,6 +220,15 @@ __device__ __forceinline__ void rnn_rows64_sum(const double *part, int nz, long 
 
 // Size of the fixed device scratch behind rnn_conv2d_backward_w_noalloc.
 #define RNN_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+// The device address of ctx's device's copy of that scratch (looked up once
+// per device with hipGetSymbolAddress; no allocation).
+int rnn_noalloc_scratch(rnn_ctx *ctx, float **out);
+// Runs `enqueue` (the kernels that use the scratch) under the device's
+// no-allocation lock.  Outside graph capture, a call on another stream than
+// the previous call on the device first waits (hipStreamWaitEvent) for that
+// call's kernels, and an event is recorded after its own; under capture the
+// caller orders the calls.
+int rnn_noalloc_run(rnn_ctx *ctx, const std::function<int()> &enqueue);
 
 // Records a message and returns `code`.
 int rnn_fail(rnn_ctx *ctx, int code, const char *fmt, ...);

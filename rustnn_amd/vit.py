@@ -168,7 +168,9 @@ class DropPath:
         self.p = float(p)
         self.ctx = ctx or default_ctx()
         self.mask = None
-        self.premask = None  # drawn ahead by draw_masks for the next forward
+        # drawn ahead by draw_masks for the next forward: (mask, seed); used
+        # only by a forward with that seed and batch
+        self.premask = None
 
     def forward(self, x, train, seed):
         import torch
@@ -176,9 +178,10 @@ class DropPath:
             self.mask = self.premask = None
             return x
         n = x.shape[0]
-        if self.premask is not None and self.premask.numel() == n:
+        pre = self._take_premask(n, seed)
+        if pre is not None:
             # the draw of Rng::new(seed) already made by draw_masks
-            self.mask, self.premask = self.premask, None
+            self.mask = pre
             self.ctx.check(lib().rnn_drop_path_backward(self.ctx.h, n, x.numel() // n,
                                                         _ptr(x, x.numel(), "x"),
                                                         _ptr(self.mask, n, "mask")))
@@ -201,15 +204,26 @@ class DropPath:
         if not train or self.p <= 0.0:
             self.mask = self.premask = None
             return None
-        if self.premask is not None and self.premask.numel() == n:
-            self.mask, self.premask = self.premask, None
+        pre = self._take_premask(n, seed)
+        if pre is not None:
+            self.mask = pre
             return self.mask
-        self.premask = None
         self.mask = torch.empty(n, device=device)
         self.ctx.check(lib().rnn_drop_path_masks(
             self.ctx.h, 1, n, (C.c_float * 1)(self.p),
             (C.c_uint64 * 1)(seed & 0xFFFFFFFFFFFFFFFF), (C.c_void_p * 1)(self.mask.data_ptr())))
         return self.mask
+
+    def _take_premask(self, n, seed):
+        """The mask draw_masks drew ahead, when it was drawn for this seed
+        and batch size; it is dropped either way."""
+        pre, self.premask = self.premask, None
+        if pre is None:
+            return None
+        m, s = pre
+        if s != seed & 0xFFFFFFFFFFFFFFFF or m.numel() != n:
+            return None
+        return m
 
     def backward(self, dy):
         if self.mask is None:
@@ -252,8 +266,8 @@ def draw_masks(layers, n, device, ctx):
     seeds = (C.c_uint64 * k)(*[s & 0xFFFFFFFFFFFFFFFF for _, s in act])
     ptrs = (C.c_void_p * k)(*[m.data_ptr() for m in masks])
     ctx.check(lib().rnn_drop_path_masks(ctx.h, k, n, p, seeds, ptrs))
-    for (dp, _), m in zip(act, masks):
-        dp.premask = m
+    for (dp, s), m in zip(act, masks):
+        dp.premask = (m, s & 0xFFFFFFFFFFFFFFFF)
 
 
 class Block:

@@ -171,3 +171,25 @@ def test_pack_bit_exact(rnn, orc, m, k, tr):
     a = rng.rand_vec(m * k)
     assert np.array_equal(to_host(rnn.dbg_pack_a(to_dev(a), m, k, tr)), orc.pack_a(a, m, k, tr))
     assert np.array_equal(to_host(rnn.dbg_pack_b(to_dev(a), m, k, tr)), orc.pack_b(a, m, k, tr))
+
+
+def test_destroy_flushes_deferred_reductions(rnn, orc):
+    """A context destroyed with deferral on and reductions still queued runs
+    them first: the Linear backward's dW (split over rows) and bias
+    gradient equal the immediate path's, bit for bit."""
+    rows, fin, fout = 8192, 64, 96
+    rng = orc.Rng(31)
+    x, dy = to_dev(rng.rand_vec(rows * fin)), to_dev(rng.rand_vec(rows * fout))
+    w = to_dev(rng.rand_vec(fout * fin))
+    got = []
+    for defer in (False, True):
+        ctx = rnn.Context(0)
+        dw = to_dev(np.zeros(fout * fin, np.float32))
+        db = to_dev(np.zeros(fout, np.float32))
+        ctx.set_defer(defer)
+        rnn.linear_backward(rows, fin, fout, dy, x, w, dw, db, ctx=ctx)
+        ctx.close()  # no flush: destroy runs what is queued
+        got.append((to_host(dw), to_host(db)))
+    assert np.array_equal(got[0][0], got[1][0])
+    assert np.array_equal(got[0][1], got[1][1])
+    assert got[1][1].any()

@@ -147,13 +147,56 @@ def test_bn_stats_in_conv_store_pass(rnn, orc, monkeypatch):
     sep.close()
 
 
-def test_fused_train_step_matches_layer_calls(rnn, orc):
+def test_fused_step_batch128_vs_oracle(rnn, orc):
+    """The benchmarked path itself: rnn_resnet_train_step at BASELINE config
+    3's batch of 128, driven as bench.py drives it (the batch written into
+    the network's input slots, eager steps with the weight gradients on the
+    second stream, BN statistics in the forward convs' store passes, the
+    batch-128 dW tile plans) for two steps against the oracle's train_step
+    (train.rs:686-699; model.rs:39-71, nn.rs:102-110): loss, hits, updated
+    parameters, momenta and running statistics after each step."""
+    import torch
+    from oracle import pymodel
+    from rustnn_amd.model import ResNet
+    n = 128
+    want = pymodel.ResNet(3, 32, 100, 7)
+    got = ResNet(3, 32, 100, 7)
+    active, _ = got.graph_state()
+    assert not active  # the default: eager steps on two streams
+    xs, ls = got.inputs(n, 32, 32)
+    loss = torch.zeros(1, device="cuda")
+    corr = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for step in range(2):
+        x, labels = _cfg3_inputs(orc, n, seed=2026 + step)
+        with orc.threads(16):
+            loss_w, corr_w, _ = want.train_step(x, labels, 0.1, 0.2, 0.9, 5e-4)
+        xs.copy_(to_dev(x).reshape(xs.shape))
+        ls.copy_(torch.from_numpy(labels.astype(np.int32)).cuda())
+        got.train_step(None, None, 0.1, 0.2, 0.9, 5e-4, loss, corr)
+        e_loss = abs(float(to_host(loss)[0]) - loss_w) / abs(loss_w)
+        e_v = rel_frob(to_host(got.params()), _oracle_flat(want, "v"))
+        e_m = rel_frob(to_host(got.momenta()), _oracle_flat(want, "m"))
+        e_b = rel_frob(to_host(got.buffers()), np.concatenate(want.buffers()))
+        print(f"step {step}: loss {e_loss:.2e} params {e_v:.2e} momenta {e_m:.2e} "
+              f"buffers {e_b:.2e}")
+        assert e_loss < 1e-5, step
+        assert int(to_host(corr)[0]) == corr_w, step
+        assert e_v < 1e-6, step
+        # the momentum after the first step is the gradient (+ weight decay)
+        assert e_m < TOL_GRAD, step
+        assert e_b < 1e-6, step
+    assert not got.graph_state()[0]
+    got.close()
+
+
+@pytest.mark.parametrize("n", [32, 128])
+def test_fused_train_step_matches_layer_calls(rnn, orc, n):
     """rnn_resnet_train_step (eager, then graph) == forward + softmax_ce +
-    backward + step called one by one, bit for bit."""
+    backward + step called one by one, bit for bit, at batch 32 and at the
+    benchmark's batch of 128 (whose dW tile plans differ)."""
     import torch
     from rustnn_amd.model import ResNet
     from rustnn_amd.nn import softmax_ce
-    n = 32
     a, b = ResNet(3, 32, 100, 11), ResNet(3, 32, 100, 11)
     a.set_graph(True)  # b's backward runs its weight gradients on the side stream
     loss = torch.zeros(1, device="cuda")

@@ -56,11 +56,18 @@ def test_drop_path_masks_batched(rnn, orc):
     draw_masks(list(zip(dps, seeds)), n, "cuda", rnn.default_ctx())
     for dp, p, sd in zip(dps, ps, seeds):
         want, mask = orc.drop_path(x, n, p, sd)
-        assert np.array_equal(to_host(dp.premask), mask)
+        assert np.array_equal(to_host(dp.premask[0]), mask) and dp.premask[1] == sd
     X = to_dev(x).reshape(n, per)
     dps[5].forward(X, True, seeds[5])
     want, mask = orc.drop_path(x, n, ps[5], seeds[5])
     assert dps[5].premask is None and np.array_equal(to_host(dps[5].mask), mask)
+    assert np.array_equal(to_host(X).ravel(), want)
+    # a mask drawn ahead for another seed is not used: the forward draws
+    # Rng::new(seed) itself
+    X = to_dev(x).reshape(n, per)
+    dps[6].forward(X, True, seeds[7])
+    want, mask = orc.drop_path(x, n, ps[6], seeds[7])
+    assert dps[6].premask is None and np.array_equal(to_host(dps[6].mask), mask)
     assert np.array_equal(to_host(X).ravel(), want)
 
 
@@ -369,3 +376,43 @@ def test_fingerprint_reproducible(rnn):
     b, _ = run(1e-3)
     c, _ = run(2e-3)
     assert t == 3 and a == b and a != c
+
+
+def test_fingerprint_matches_oracle(rnn, orc):
+    """The device Trainer::fingerprint (train.rs:450-470) against the
+    oracle's restatement over identical states: at initialisation (both
+    networks draw bit-identical weights; no second moments, no EMA, t = 0),
+    then after two device train steps with the device's values, momenta,
+    AdamW second moments, EMA weights and step count copied into the oracle
+    trainer."""
+    from oracle import pyvit
+    from rustnn_amd.vit import RustViT, ViTStep, fingerprint
+    cfg = dict(width=4, cmid=6, dim=8, heads=2, depth3=2, dim4=12, heads4=2, depth4=1,
+               mem_at=(1,), droppath=0.2, img=16)
+    parent = np.array([0, 0, 1, 1, 2, 2], np.uint32)
+    hp = dict(ntrain=400, batch=4, epochs=10, warmup=1, seed=77)
+    dnet = RustViT(cfg, _i32(parent), 3, seed=5)
+    dstep = ViTStep(dnet, _i32(parent), 3, hp)
+    onet = pyvit.RustViT(cfg, list(parent), 3, 5)
+    otr = pyvit.Trainer(onet, parent, 3, hp)
+    assert fingerprint(dstep, 1.25) == otr.fingerprint(1.25)
+    rng = orc.Rng(9)
+    x = to_dev(rng.rand_vec(4 * 3 * 16 * 16)).reshape(4, 3, 16, 16)
+    labels = _i32(np.array([0, 3, 5, 1], np.uint32))
+    coarse = _i32(np.array([0, 1, 2, 0], np.uint32))
+    loss = None
+    for i in range(2):
+        dnet.drop_seed = 100 + i
+        loss, _ = dstep(x, labels, coarse)
+    last = float(loss.item())
+    opt = dstep.opt
+    for op, dp in zip(onet.params(), dnet.params()):
+        op.v[:] = to_host(dp.v).ravel()
+        op.m[:] = to_host(dp.m).ravel()
+        muon = opt.muon and dp.rows > 0 and min(dp.rows, dp.cols) > 1
+        op.v2 = None if muon else to_host(dp.v2).ravel().copy()
+    assert dstep.ema is not None and dstep.ema.ready
+    otr.ema_w = [to_host(w).ravel().copy() for w in dstep.ema.w]
+    otr.t = opt.t
+    assert opt.t == 2
+    assert fingerprint(dstep, last) == otr.fingerprint(last)

@@ -289,6 +289,13 @@ def test_trainer_step_default_batch128(rnn, orc, vit):
                              [host_o(p.v) for p in ops], lr, 0.06, 0, "default")
     print(f"default: worst gradient {max(errs):.2e}; worst update vs f64 (device, oracle, "
           f"f32 floor) {worst[0]:.2e} {worst[1]:.2e} {worst[2]:.2e}; device vs oracle {e:.2e}")
+    # the updated weights, whole vector (train.rs:346-387), and the EMA
+    e_v = rel_frob(np.concatenate([host_d(p.v) for p in dps]),
+                   np.concatenate([host_o(p.v) for p in ops]))
+    print(f"default: updated weights device vs oracle {e_v:.2e}")
+    assert e_v < TOL
+    ema_d = [to_host(w).ravel() for w in dtr.ema.w]
+    assert max(rel_frob(a, b) for a, b in zip(ema_d, otr.ema_w)) < TOL
 
 
 def test_deferred_reductions_bit_identical(rnn, orc, vit):

@@ -250,3 +250,69 @@ def test_reference_vitcheck_on_oracle(orc, vit):
     assert len(errs) == 16  # 8 norm, 7 attention, 1 network
     bad = {k: v for k, v in errs.items() if not v < refcheck.TOL}
     assert not bad, errs
+
+
+def test_fnv1a_oracle_published_vectors(orc):
+    """The oracle's FNV-1a 64 (train.rs:474-484) against the published
+    FNV-1a 64 test vectors, and fnv_f32 as the 4 little-endian bytes of each
+    float's bit pattern (a big-endian fold gives another hash)."""
+    import struct
+    off = orc.FNV_OFFSET
+    assert orc.fnv1a_bytes(off, b"") == 0xCBF29CE484222325
+    assert orc.fnv1a_bytes(off, b"a") == 0xAF63DC4C8601EC8C
+    assert orc.fnv1a_bytes(off, b"foobar") == 0x85944171F73967E8
+    v = np.array([1.0, -2.5, 3.0e-7, np.inf], np.float32)
+    le = b"".join(struct.pack("<f", float(x)) for x in v)
+    be = b"".join(struct.pack(">f", float(x)) for x in v)
+    assert orc.fnv1a_f32(off, v) == orc.fnv1a_bytes(off, le)
+    assert orc.fnv1a_f32(off, v) != orc.fnv1a_bytes(off, be)
+    # continuing from a hash = hashing the concatenation
+    assert orc.fnv1a_f32(orc.fnv1a_bytes(off, b"ab"), v) == orc.fnv1a_bytes(off, b"ab" + le)
+
+
+def test_oracle_fingerprint_composition(orc, vit):
+    """Trainer::fingerprint (train.rs:450-470) on the oracle trainer: the
+    hash of the byte stream [v, m, v2 of each parameter in for_each_param
+    order][every EMA tensor][Optim::t as u64 LE][last loss as f32 LE], where
+    v2 is empty until AdamW steps a tensor and always for a Muon matrix, and
+    the EMA has no tensors before its first update.  Checked before and after
+    one step; dropping or reordering a part changes the hash."""
+    import struct
+    net = vit.RustViT(SMALL, PARENT6, 3, 5)
+    tr = vit.Trainer(net, PARENT6, 3, dict(ntrain=400, batch=4, epochs=10, warmup=1, seed=77))
+    off = orc.FNV_OFFSET
+
+    def stream(params, ema, t, loss, order=("v", "m", "v2")):
+        parts = []
+        for p in params:
+            for k in order:
+                a = getattr(p, k, None)
+                if a is not None:
+                    parts.append(np.asarray(a, np.float32).tobytes())
+        for w in ema or []:
+            parts.append(np.asarray(w, np.float32).tobytes())
+        parts.append(struct.pack("<Q", t))
+        parts.append(struct.pack("<f", loss))
+        return b"".join(parts)
+
+    ps = net.params()
+    assert all(getattr(p, "v2", None) is None for p in ps) and tr.ema_w is None
+    h0 = tr.fingerprint(1.25)
+    assert h0 == orc.fnv1a_bytes(off, stream(ps, None, 0, 1.25))
+    rng = orc.Rng(5)
+    x = rng.rand_vec(4 * 3 * 16 * 16).reshape(4, 3, 16, 16)
+    labels = np.array([0, 3, 5, 1], np.uint32)
+    coarse = np.array(PARENT6, np.uint32)[labels]
+    total, _, _, _, _ = tr.step(x, labels, coarse)
+    muon = [p for p in ps if getattr(p, "rows", 0) > 0 and min(p.rows, p.cols) > 1]
+    assert muon and all(getattr(p, "v2", None) is None for p in muon)
+    adam = [p for p in ps if p not in muon]
+    assert adam and all(p.v2 is not None for p in adam) and any(p.v2.any() for p in adam)
+    assert tr.t == 1 and tr.ema_w is not None
+    h1 = tr.fingerprint(total)
+    assert h1 == orc.fnv1a_bytes(off, stream(ps, tr.ema_w, 1, np.float32(total)))
+    # planted mistakes: each changes the hash
+    assert h1 != orc.fnv1a_bytes(off, stream(ps, tr.ema_w, 1, np.float32(total),
+                                             order=("m", "v", "v2")))
+    assert h1 != orc.fnv1a_bytes(off, stream(ps, None, 1, np.float32(total)))
+    assert h1 != orc.fnv1a_bytes(off, stream(ps, tr.ema_w, 0, np.float32(total)))

@@ -108,3 +108,80 @@ def test_build_script_links_rnn():
     assert "rustc-link-lib=dylib=rnn" in b
     toml = open(os.path.join(ROOT, "rnn-sys", "Cargo.toml")).read()
     assert 'name = "rnn-sys"' in toml and 'links = "rnn"' in toml
+
+
+SAFE_RS = os.path.join(ROOT, "rnn-sys", "src", "safe.rs")
+
+# The reference's call-site signatures the safe layer keeps, written out from
+# the reference files (parameter name: type, in order):
+#   gemm.rs:434-444 matmul, gemm.rs:500-512 gemm_small, gemm.rs:555 matmul_dw,
+#   attn.rs:148-160 Core::forward, attn.rs:226-242 Core::backward.
+REF_SIGS = {
+    "matmul": [("m", "usize"), ("n", "usize"), ("k", "usize"), ("a", "&[f32]"), ("at", "bool"),
+               ("b", "&[f32]"), ("bt", "bool"), ("c", "&mut [f32]"), ("acc", "bool")],
+    "gemm_small": [("m", "usize"), ("n", "usize"), ("k", "usize"), ("a", "&[f32]"),
+                   ("at", "bool"), ("b", "&[f32]"), ("bt", "bool"), ("c", "&mut [f32]"),
+                   ("acc", "bool"), ("_ap", "&mut PackedA"), ("_bp", "&mut PackedB")],
+    "matmul_dw": [("m", "usize"), ("n", "usize"), ("k", "usize"), ("a", "&[f32]"),
+                  ("b", "&[f32]"), ("c", "&mut [f32]")],
+    "forward": [("&self", None), ("q", "&[f32]"), ("qstride", "usize"), ("qoff", "usize"),
+                ("kv", "&[f32]"), ("kvstride", "usize"), ("koff", "usize"), ("voff", "usize"),
+                ("tau", "&[f32]"), ("rel", "&[f32]"), ("p", "&mut [f32]"), ("o", "&mut [f32]")],
+    "backward": [("&self", None), ("q", "&[f32]"), ("qstride", "usize"), ("qoff", "usize"),
+                 ("kv", "&[f32]"), ("kvstride", "usize"), ("koff", "usize"),
+                 ("voff", "usize"), ("tau", "&[f32]"), ("p", "&[f32]"), ("dobuf", "&[f32]"),
+                 ("dq", "&mut [f32]"), ("dkv", "&mut [f32]"), ("dtau", "&mut [f32]"),
+                 ("drel", "&mut [f32]")],
+}
+# safe fn -> the *_host entry point it must call
+SAFE_CALLS = {"matmul": "rnn_matmul_host", "gemm_small": "rnn_gemm_small_batched_host",
+              "matmul_dw": "rnn_matmul_dw_host", "conv2d_forward": "rnn_conv2d_forward_host",
+              "conv2d_backward_w": "rnn_conv2d_backward_w_host",
+              "conv2d_backward_x": "rnn_conv2d_backward_x_host",
+              "forward": "rnn_attn_forward_host", "backward": "rnn_attn_backward_host",
+              "linear_forward": "rnn_linear_forward_host",
+              "linear_backward": "rnn_linear_backward_host"}
+
+
+def _safe_fns():
+    """{name: (params [(name, type)], body)} of the `pub fn`s of safe.rs."""
+    text = open(SAFE_RS).read()
+    out = {}
+    for m in re.finditer(r"pub fn (\w+)\(([^)]*)\)[^{]*\{", text):
+        params = []
+        for a in [x.strip() for x in m.group(2).replace("\n", " ").split(",") if x.strip()]:
+            if ":" in a:
+                n, t = a.split(":", 1)
+                params.append((n.strip(), " ".join(t.split())))
+            else:
+                params.append((a, None))
+        depth, i = 1, m.end()
+        while depth:
+            depth += {"{": 1, "}": -1}.get(text[i], 0)
+            i += 1
+        out.setdefault(m.group(1), (params, text[m.end():i]))
+    return out, text
+
+
+def test_safe_layer_keeps_reference_signatures():
+    fns, text = _safe_fns()
+    for name, want in REF_SIGS.items():
+        assert fns[name][0] == want, name
+    assert "pub struct Core {" in text and "pub relidx: Vec<u32>," in text
+    assert "pub mod safe;" in open(LIB_RS).read()
+
+
+def test_safe_layer_calls_host_entry_points():
+    """Each safe function calls its *_host entry point (declared in lib.rs and
+    exported by librnn.so) and no device-pointer entry point."""
+    fns, text = _safe_fns()
+    decl, _, _, _, _ = parse_lib_rs()
+    for name, host in SAFE_CALLS.items():
+        body = fns[name][1]
+        called = set(re.findall(r"\b(rnn_\w+)\(", body))
+        assert called == {host}, (name, called)
+        assert host in decl
+    every = set(re.findall(r"\b(rnn_\w+)\(", text))
+    assert every <= set(decl)
+    assert {c for c in every if not c.endswith("_host")} == {
+        "rnn_ctx_create", "rnn_ctx_last_error", "rnn_status_string"}

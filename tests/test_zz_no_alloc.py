@@ -76,3 +76,37 @@ def test_noalloc_rejects_oversize(rnn):
     assert b"scratch" in L.rnn_ctx_last_error(ctx.h)
     assert ctx.workspace_bytes() == 0
     ctx.close()
+
+
+def test_noalloc_calls_on_two_streams(rnn, orc):
+    """Two contexts on two streams of one GPU call the no-allocation entry
+    point back to back with no synchronisation between them: the library
+    orders them on the shared scratch, so each result equals
+    rnn_conv2d_backward_w's bit for bit."""
+    import torch
+    L = rnn.lib()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    ca, cb, cref = rnn.Context(0, stream=s1), rnn.Context(0, stream=s2), rnn.Context(0)
+    jobs = []
+    for i, (ctx, (n, cin, cout, k, s, p, h)) in enumerate(zip((ca, cb), CALLS[:2])):
+        sp = orc.ConvSpec.make(cin, cout, k, s, p, h, h)
+        gsp = rnn.ConvSpec.make(cin, cout, k, s, p, h, h)
+        x, dy, dw0 = _inputs(orc, sp, n, 300 + i)
+        X, DY = to_dev(x), to_dev(dy)
+        torch.cuda.synchronize()
+        jobs.append((ctx, gsp, n, X, DY, to_dev(dw0.copy()), to_dev(dw0.copy())))
+    for ctx, gsp, n, X, DY, dw_na, _ in jobs:
+        print(f"noalloc on stream {ctx.stream_ptr():#x}: n={n}", flush=True)
+        ctx.check(L.rnn_conv2d_backward_w_noalloc(ctx.h, C.byref(gsp), n,
+                                                  C.c_void_p(DY.data_ptr()),
+                                                  C.c_void_p(X.data_ptr()),
+                                                  C.c_void_p(dw_na.data_ptr())))
+    for ctx, gsp, n, X, DY, _, dw_ref in jobs:
+        cref.check(L.rnn_conv2d_backward_w(cref.h, C.byref(gsp), n, C.c_void_p(DY.data_ptr()),
+                                           C.c_void_p(X.data_ptr()),
+                                           C.c_void_p(dw_ref.data_ptr())))
+    torch.cuda.synchronize()
+    for i, (ctx, gsp, n, X, DY, dw_na, dw_ref) in enumerate(jobs):
+        assert np.array_equal(to_host(dw_na), to_host(dw_ref)), f"call {i}"
+    for c in (ca, cb, cref):
+        c.close()
