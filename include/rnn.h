@@ -612,6 +612,15 @@ uint64_t rnn_resnet_flops(const rnn_resnet *net, size_t h, size_t w);
 /* ------------------------------------------ debug exports (bit-exact tests) */
 /* im2col of ONE image through the same staging index math the conv kernels
  * use: col[cin*k*k][oh*ow] (gather_span, conv.rs:68-120). */
+/* The device buffers the train step keeps for block `block` of a ResNet
+ * (test access, read-only): which = 0 y1 (c1 output), 1 h (b1 + ReLU), 2 y2
+ * (c2 output), 3 ys (shortcut conv output), 4 out (block output), 5 / 6 / 7
+ * the output gradients of c1 / c2 / the shortcut conv of the last backward,
+ * 8 / 9 the batch mean then invstd of b1 / b2 ([2 cout]), 10 the block's
+ * input (the previous block's output; for block 0 the stem's ReLU output).
+ * *len: floats. */
+int rnn_dbg_resnet_buffer(rnn_resnet *net, size_t block, int which, const float **ptr,
+                          size_t *len);
 int rnn_dbg_im2col(rnn_ctx *ctx, const rnn_conv_spec *sp, const float *x_img, float *col);
 /* PackedA::pack / pack_t (gemm.rs:54-113) into out[nb*256*mpad] (positions the
  * reference never writes are left untouched). */

@@ -5,7 +5,12 @@ Usage: python -m rustnn_amd.build   (or rustnn_amd.build.build())
 Every .hip file under csrc/ is compiled with hipcc for gfx950 only, then linked
 into rustnn_amd/librnn.so, which travels with the source tree.  Packed FP32
 VALU ops are disabled (-packed-fp32-ops): the kernels compute on MFMA and plain
-scalar VALU only.
+scalar VALU only.  Floating-point contraction is off (-ffp-contract=off):
+a * b + c in the elementwise and reduction code rounds the product, then the
+sum, as the reference's Rust does (it never fuses a multiply-add unless
+written with mul_add), so results that feed a comparison -- the ReLU masks
+after BatchNorm, the max of a softmax row -- round as the reference's do.
+The matrix products run on MFMA builtins, which contraction does not touch.
 """
 from __future__ import annotations
 
@@ -22,7 +27,7 @@ LIB = os.path.join(HERE, "librnn.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 CFLAGS = [
-    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-ffp-contract=off",
     "-Wno-unused-function", "-Wno-unused-variable",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(HERE, "..", "include"),

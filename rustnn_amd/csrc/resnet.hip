@@ -1149,6 +1149,27 @@ int rnn_resnet_logits(rnn_resnet *r, float *logits) {
     return RNN_OK;
 }
 
+int rnn_dbg_resnet_buffer(rnn_resnet *r, size_t block, int which, const float **ptr,
+                          size_t *len) {
+    if (!r || !ptr || !len) return RNN_E_NULL;
+    *ptr = nullptr;
+    *len = 0;
+    if (!r->arena) return rnn_fail(r->ctx, RNN_E_INVALID, "dbg_resnet_buffer: no plan yet");
+    if (block >= r->blocks.size())
+        return rnn_fail(r->ctx, RNN_E_INVALID, "dbg_resnet_buffer: block %zu of %zu", block,
+                        r->blocks.size());
+    const NetBlock &b = r->blocks[block];
+    const size_t a = r->n * b.c1.cout * b.hout * b.wout;
+    const float *tab[11] = {b.y1,     b.h,      b.y2,      b.ys,      b.out,   b.c1.dyb,
+                            b.c2.dyb, b.cd.dyb, b.b1.coef, b.b2.coef, b.in};
+    if (which < 0 || which > 10 || !tab[which])
+        return rnn_fail(r->ctx, RNN_E_INVALID, "dbg_resnet_buffer: no buffer %d", which);
+    *ptr = tab[which];
+    *len = which == 10 ? r->n * (size_t)b.c1.cin * b.hin * b.win
+                       : (which >= 8 ? 2 * (size_t)b.c1.cout : a);
+    return RNN_OK;
+}
+
 uint64_t rnn_resnet_flops(const rnn_resnet *r, size_t h, size_t w) {
     // ResNet::flops (model.rs:179-198): forward FLOP per image.
     if (!r) return 0;

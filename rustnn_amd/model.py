@@ -130,6 +130,17 @@ class ResNet:
         return (torch.as_tensor(_DevArray(xp.value, (n, 3, h, w), "<f4"), device=dev),
                 torch.as_tensor(_DevArray(lp.value, (n,), "<i4"), device=dev))
 
+    def dbg_buffer(self, block, which):
+        """A copy of one of the buffers the step keeps for `block`
+        (rnn_dbg_resnet_buffer: 0 y1, 1 h, 2 y2, 3 ys, 4 out, 5-7 the c1 / c2
+        / shortcut output gradients, 8 / 9 b1 / b2 mean then invstd, 10 the
+        block's input)."""
+        import torch
+        p, n = _vp(), C.c_size_t()
+        self.ctx.check(lib().rnn_dbg_resnet_buffer(self.h, block, which, C.byref(p), C.byref(n)))
+        dev = torch.device("cuda", self.device)
+        return torch.as_tensor(_DevArray(p.value, (n.value,), "<f4"), device=dev).clone()
+
     def set_graph(self, on):
         self.ctx.check(lib().rnn_resnet_set_graph(self.h, int(bool(on))))
 

@@ -51,9 +51,10 @@ def test_gemm_small_and_matmul_dw_host(rnn, orc):
         c = c0.copy()
         ctx.check(L.rnn_gemm_small_batched_host(ctx.h, cnt, m, n, kk, _p(a), m * k, 1, _p(b),
                                                 k * n, 0, _p(c), m * n, acc))
-        Cd = to_dev(c0.copy())
-        ctx.check(L.rnn_gemm_small_batched(ctx.h, cnt, m, n, kk, _d(to_dev(a)), m * k, 1,
-                                           _d(to_dev(b)), k * n, 0, _d(Cd), m * n, acc))
+        # the device operands stay referenced until the call has run
+        A, B, Cd = to_dev(a), to_dev(b), to_dev(c0.copy())
+        ctx.check(L.rnn_gemm_small_batched(ctx.h, cnt, m, n, kk, _d(A), m * k, 1, _d(B), k * n,
+                                           0, _d(Cd), m * n, acc))
         assert np.array_equal(c, to_host(Cd))
         if kk == 0:
             assert np.array_equal(c, c0)  # gemm_small's k = 0 leaves C untouched
@@ -61,8 +62,8 @@ def test_gemm_small_and_matmul_dw_host(rnn, orc):
     a, b, c0 = rng.rand_vec(kk * mm), rng.rand_vec(kk * nn), rng.rand_vec(mm * nn)
     c = c0.copy()
     ctx.check(L.rnn_matmul_dw_host(ctx.h, mm, nn, kk, _p(a), _p(b), _p(c)))
-    Cd = to_dev(c0.copy())
-    ctx.check(L.rnn_matmul_dw(ctx.h, mm, nn, kk, _d(to_dev(a)), _d(to_dev(b)), _d(Cd)))
+    A, B, Cd = to_dev(a), to_dev(b), to_dev(c0.copy())
+    ctx.check(L.rnn_matmul_dw(ctx.h, mm, nn, kk, _d(A), _d(B), _d(Cd)))
     assert np.array_equal(c, to_host(Cd))
     assert rel_frob(c - c0, orc.matmul(mm, nn, kk, a, 1, b, 0)) < TOL
     ctx.close()
@@ -160,8 +161,10 @@ def test_linear_host(rnn, orc, bias):
     assert np.array_equal(dw, to_host(DW))
     if bias:
         assert np.array_equal(db, to_host(DB))
-    yw = orc.matmul(rows, fout, fin, x, 0, w, 1) + (b if bias else 0)
-    assert rel_frob(y, yw) < TOL
+    yw = orc.matmul(rows, fout, fin, x, 0, w, 1).reshape(rows, fout)
+    if bias:
+        yw = yw + b[None, :]
+    assert rel_frob(y, yw.ravel()) < TOL
     ctx.close()
 
 
