@@ -416,6 +416,30 @@ int rnn_kl_distill(rnn_ctx *ctx, size_t n, size_t nclass, const float *student,
  * scale * mean squared error. */
 int rnn_hint_mse(rnn_ctx *ctx, size_t n, size_t c, const float *pred, const float *target,
                  float scale, float *dz, float *loss);
+/* build_loss (train.rs:70-118) in one call: the soft-target cross-entropy of
+ * the logits (scale 1), of the coarse head when coarse_w > 0 and taxo (scale
+ * coarse_w), and with the exits (io->e1 set): the exits' cross-entropies
+ * (exit_w1, exit_w2), their distillation from the logits when alpha > 0
+ * (loss::kl_distill, temp) and the hint MSEs of h1 / h2 against feat when
+ * beta > 0.  Gradients are written (the reference's zeroed Grads receive
+ * them): dlogits, dcoarse (zeros without the coarse term), de1 / de2 (their
+ * cross-entropy, then the distillation added), dh1 / dh2 (zeros when beta
+ * is 0).  *total = ce (+ coarse_w lc) (+ (w1 l1 + w2 l2)) (+ alpha (k1 + k2))
+ * (+ (h1 + h2)) in f32, the reference's order and grouping; *ce the logits'
+ * loss; *correct its argmax hits (device pointers, any may be NULL).  nc:
+ * coarse classes (0: no coarse head); d4: the width of h1 / h2 / feat. */
+typedef struct {
+    float coarse_w, exit_w1, exit_w2, alpha, temp, beta;
+    int taxo;
+} rnn_loss_cfg;
+typedef struct {
+    const float *logits, *coarse, *e1, *e2, *h1, *h2, *feat;
+    float *dlogits, *dcoarse, *de1, *de2, *dh1, *dh2;
+} rnn_loss_io;
+int rnn_build_loss(rnn_ctx *ctx, size_t n, size_t nf, size_t nc, size_t d4, const float *tf,
+                   const float *tc, const uint32_t *hard, const uint32_t *hardc,
+                   const rnn_loss_cfg *cfg, const rnn_loss_io *io, float *total, float *ce,
+                   uint32_t *correct);
 
 /* ----------------------------------------------------------- vit.rs */
 /* DropPath (vit.rs:25-74) on n images of `per` floats, in place: image i is

@@ -46,6 +46,34 @@ pub struct rnn_attn_desc {
 }
 
 #[repr(C)] #[derive(Clone, Copy)]
+pub struct rnn_loss_cfg {
+    pub coarse_w: f32,
+    pub exit_w1: f32,
+    pub exit_w2: f32,
+    pub alpha: f32,
+    pub temp: f32,
+    pub beta: f32,
+    pub taxo: c_int,
+}
+
+#[repr(C)] #[derive(Clone, Copy)]
+pub struct rnn_loss_io {
+    pub logits: *const f32,
+    pub coarse: *const f32,
+    pub e1: *const f32,
+    pub e2: *const f32,
+    pub h1: *const f32,
+    pub h2: *const f32,
+    pub feat: *const f32,
+    pub dlogits: *mut f32,
+    pub dcoarse: *mut f32,
+    pub de1: *mut f32,
+    pub de2: *mut f32,
+    pub dh1: *mut f32,
+    pub dh2: *mut f32,
+}
+
+#[repr(C)] #[derive(Clone, Copy)]
 pub struct rnn_param {
     pub v: *mut f32,
     pub g: *mut f32,
@@ -133,6 +161,7 @@ extern "C" {
     pub fn rnn_ce_soft(ctx: *mut rnn_ctx, n: usize, nclass: usize, logits: *const f32, target: *const f32, hard: *const u32, scale: f32, dz: *mut f32, loss: *mut f32, correct: *mut u32) -> c_int;
     pub fn rnn_kl_distill(ctx: *mut rnn_ctx, n: usize, nclass: usize, student: *const f32, teacher: *const f32, temp: f32, scale: f32, dz: *mut f32, loss: *mut f32) -> c_int;
     pub fn rnn_hint_mse(ctx: *mut rnn_ctx, n: usize, c: usize, pred: *const f32, target: *const f32, scale: f32, dz: *mut f32, loss: *mut f32) -> c_int;
+    pub fn rnn_build_loss(ctx: *mut rnn_ctx, n: usize, nf: usize, nc: usize, d4: usize, tf: *const f32, tc: *const f32, hard: *const u32, hardc: *const u32, cfg: *const rnn_loss_cfg, io: *const rnn_loss_io, total: *mut f32, ce: *mut f32, correct: *mut u32) -> c_int;
     pub fn rnn_drop_path_forward(ctx: *mut rnn_ctx, n: usize, per: usize, x: *mut f32, p: f32, seed: u64, mask: *mut f32) -> c_int;
     pub fn rnn_drop_path_backward(ctx: *mut rnn_ctx, n: usize, per: usize, dy: *mut f32, mask: *const f32) -> c_int;
     pub fn rnn_drop_path_masks(ctx: *mut rnn_ctx, count: usize, n: usize, p: *const f32, seeds: *const u64, masks: *mut *mut float  const) -> c_int;

@@ -66,6 +66,18 @@ class ConvSpec(C.Structure):
         return self.oh * self.ow
 
 
+class LossCfg(C.Structure):
+    """rnn_loss_cfg: build_loss's weights (train.rs:70-118, cli.rs defaults)."""
+    _fields_ = [(n, C.c_float) for n in ("coarse_w", "exit_w1", "exit_w2", "alpha", "temp",
+                                         "beta")] + [("taxo", C.c_int)]
+
+
+class LossIO(C.Structure):
+    """rnn_loss_io: the heads build_loss reads and the gradients it writes."""
+    _fields_ = [(n, C.c_void_p) for n in ("logits", "coarse", "e1", "e2", "h1", "h2", "feat",
+                                          "dlogits", "dcoarse", "de1", "de2", "dh1", "dh2")]
+
+
 class AttnDesc(C.Structure):
     """rnn_attn_desc = Core (attn.rs:74-84) + forward/backward strides."""
     _fields_ = [("h", _u32), ("dh", _u32), ("tq", _u32), ("tk", _u32),
@@ -210,6 +222,8 @@ def lib():
             "rnn_ce_soft": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp]),
             "rnn_kl_distill": (_i, [_vp, _sz, _sz, _vp, _vp, C.c_float, C.c_float, _vp, _vp]),
             "rnn_hint_mse": (_i, [_vp, _sz, _sz, _vp, _vp, C.c_float, _vp, _vp]),
+            "rnn_build_loss": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, P(LossCfg),
+                                    P(LossIO), _vp, _vp, _vp]),
             "rnn_ln_forward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp]),
             "rnn_ln_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_layerscale_forward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),

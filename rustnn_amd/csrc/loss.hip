@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 
 #pragma clang fp contract(off)
 
@@ -127,6 +128,7 @@ __global__ __launch_bounds__(NT) void kl_distill_kernel(size_t n, int nc,
 
 // hint_mse per row (loss.rs:139-150), one wave per row: dz += 2 e / (n c) *
 // scale; part[i] = sum e^2.
+template <bool SET>
 __global__ __launch_bounds__(NT) void hint_mse_kernel(size_t n, int c, const float *__restrict__ pred,
                                                       const float *__restrict__ target,
                                                       float scale, float *__restrict__ dz,
@@ -141,7 +143,11 @@ __global__ __launch_bounds__(NT) void hint_mse_kernel(size_t n, int c, const flo
     for (int j = lane; j < c; j += 64) {
         const float e = p[j] - t[j];
         s += e * e;
-        d[j] += 2.0f * e * inv * scale;
+        // SET: dz starts at zero (build_loss's fresh g.h1 / g.h2), written
+        if constexpr (SET)
+            d[j] = 2.0f * e * inv * scale;
+        else
+            d[j] += 2.0f * e * inv * scale;
     }
     s = wsum(s);
     if (lane == 0) part[i] = s;
@@ -347,14 +353,176 @@ int rnn_hint_mse(rnn_ctx *ctx, size_t n, size_t c, const float *pred, const floa
     if (!rows_ok(ctx, n, c, "hint_mse")) return RNN_E_INVALID;
     float *part = (float *)rnn_workspace(ctx, n * sizeof(float));
     if (!part) return RNN_E_NOMEM;
-    hint_mse_kernel<<<(unsigned)rnn_div_up(n, (size_t)(NT / 64)), NT, 0, ctx->stream>>>(n, (int)c, pred, target,
-                                                                         scale, dz, part);
+    hint_mse_kernel<false><<<(unsigned)rnn_div_up(n, (size_t)(NT / 64)), NT, 0, ctx->stream>>>(
+        n, (int)c, pred, target, scale, dz, part);
     RNN_LAUNCHED(ctx);
     if (loss) {
         rows_total_kernel<<<1, 64, 0, ctx->stream>>>(n, part, 1.0f / (float)(n * c), scale, loss,
                                                      nullptr, nullptr);
         RNN_LAUNCHED(ctx);
     }
+    return RNN_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+// build_loss's totals (train.rs:70-118) in one launch: lane k of the one
+// wave sums the row partials of term k in row order as rows_total_kernel
+// does (16 loads ahead of the adds), then lane 0 adds the terms in the
+// reference's order and grouping, in f32:
+// total = ce (+ cw lc) (+ (w1 l1 + w2 l2)) (+ alpha (k1 + k2)) (+ (h1 + h2)).
+struct LossTerms {
+    const float *part[8];  // ce, lc, l1, l2, k1, k2, h1, h2 row partials (null: absent)
+    float mul1[8], mul2[8];
+    const uint32_t *hit;   // ce's row hits
+    float cw, w1, w2, alpha;
+};
+
+__global__ void loss_totals_kernel(size_t n, LossTerms t, float *__restrict__ total,
+                                   float *__restrict__ ce, uint32_t *__restrict__ correct) {
+    __shared__ float term[8];
+    __shared__ uint32_t hits;
+    const int k = threadIdx.x;
+    if (k < 8) {
+        float s = 0.0f;
+        uint32_t h = 0;
+        const float *part = t.part[k];
+        const uint32_t *hit = k == 0 ? t.hit : nullptr;
+        if (part) {
+            for (size_t i0 = 0; i0 < n; i0 += 16) {
+                float v[16];
+                uint32_t u16[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) {
+                    const size_t i = min(i0 + u, n - 1);
+                    v[u] = part[i];
+                    u16[u] = hit ? hit[i] : 0u;
+                }
+#pragma unroll
+                for (int u = 0; u < 16; u++)
+                    if (i0 + u < n) {
+                        s += v[u];
+                        h += u16[u];
+                    }
+            }
+        }
+        term[k] = s * t.mul1[k] * t.mul2[k];
+        if (k == 0) hits = h;
+    }
+    __syncthreads();
+    if (k != 0) return;
+    float tot = term[0];
+    if (t.part[1]) tot += t.cw * term[1];
+    if (t.part[2]) tot += t.w1 * term[2] + t.w2 * term[3];
+    if (t.part[4]) tot += t.alpha * (term[4] + term[5]);
+    if (t.part[6]) tot += term[6] + term[7];
+    if (total) *total = tot;
+    if (ce) *ce = term[0];
+    if (correct) *correct = hits;
+}
+
+__global__ void fill_zero_kernel(float *__restrict__ x, size_t len) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
+         i += (size_t)gridDim.x * blockDim.x)
+        x[i] = 0.0f;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rnn_build_loss(rnn_ctx *ctx, size_t n, size_t nf, size_t nc, size_t d4, const float *tf,
+                   const float *tc, const uint32_t *hard, const uint32_t *hardc,
+                   const rnn_loss_cfg *cfg, const rnn_loss_io *io, float *total, float *ce,
+                   uint32_t *correct) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (!cfg || !io) return rnn_fail(ctx, RNN_E_NULL, "build_loss: null cfg or io");
+    if (n == 0) return RNN_OK;
+    const bool coarse = cfg->coarse_w > 0.0f && cfg->taxo;
+    const bool exits = io->e1 != nullptr;
+    if (!io->logits || !io->dlogits || !tf || !hard)
+        return rnn_fail(ctx, RNN_E_NULL, "build_loss: null logits / targets");
+    if (nc && !io->dcoarse) return rnn_fail(ctx, RNN_E_NULL, "build_loss: null dcoarse");
+    if (coarse && (!io->coarse || !tc || !hardc))
+        return rnn_fail(ctx, RNN_E_NULL, "build_loss: null coarse operand");
+    if (exits && (!io->e2 || !io->de1 || !io->de2 || !io->h1 || !io->h2 || !io->feat ||
+                  !io->dh1 || !io->dh2))
+        return rnn_fail(ctx, RNN_E_NULL, "build_loss: null exit operand");
+    if (!rows_ok(ctx, n, nf, "build_loss") || (nc && !rows_ok(ctx, n, nc, "build_loss")) ||
+        (exits && !rows_ok(ctx, n, d4, "build_loss")))
+        return RNN_E_INVALID;
+    WsCarve cv;
+    size_t o_part[8];
+    for (int k = 0; k < 8; k++) o_part[k] = cv.take(n * sizeof(float));
+    const size_t o_hit = cv.take(n * sizeof(uint32_t));
+    char *ws = (char *)rnn_workspace(ctx, cv.off);
+    if (!ws) return RNN_E_NOMEM;
+    LossTerms t;
+    std::memset(&t, 0, sizeof(t));
+    float *part[8];
+    for (int k = 0; k < 8; k++) {
+        part[k] = (float *)(ws + o_part[k]);
+        t.mul1[k] = 1.0f / (float)n;
+        t.mul2[k] = 1.0f;
+    }
+    uint32_t *hit = (uint32_t *)(ws + o_hit);
+    t.hit = hit;
+    t.cw = cfg->coarse_w;
+    t.w1 = cfg->exit_w1;
+    t.w2 = cfg->exit_w2;
+    t.alpha = cfg->alpha;
+    const unsigned rows = (unsigned)rnn_div_up(n, (size_t)(NT / 64));
+    auto zero = [&](float *x, size_t len) {
+        fill_zero_kernel<<<(unsigned)std::min<size_t>(rnn_div_up(len, 256), 1024), 256, 0,
+                           ctx->stream>>>(x, len);
+    };
+    // loss::ce_soft(&out.logits, tf, hard, nf, 1.0, &mut g.logits)
+    ce_soft_kernel<<<rows, NT, 0, ctx->stream>>>(n, (int)nf, io->logits, tf, hard, 1.0f,
+                                                 io->dlogits, part[0], hit);
+    t.part[0] = part[0];
+    if (coarse) {
+        ce_soft_kernel<<<rows, NT, 0, ctx->stream>>>(n, (int)nc, io->coarse, tc, hardc,
+                                                     cfg->coarse_w, io->dcoarse, part[1], nullptr);
+        t.part[1] = part[1];
+    } else if (nc) {
+        zero(io->dcoarse, n * nc);
+    }
+    if (exits) {
+        ce_soft_kernel<<<rows, NT, 0, ctx->stream>>>(n, (int)nf, io->e1, tf, hard, cfg->exit_w1,
+                                                     io->de1, part[2], nullptr);
+        ce_soft_kernel<<<rows, NT, 0, ctx->stream>>>(n, (int)nf, io->e2, tf, hard, cfg->exit_w2,
+                                                     io->de2, part[3], nullptr);
+        t.part[2] = part[2];
+        t.part[3] = part[3];
+        if (cfg->alpha > 0.0f) {
+            kl_distill_kernel<<<rows, NT, 0, ctx->stream>>>(n, (int)nf, io->e1, io->logits,
+                                                            cfg->temp, cfg->alpha, io->de1,
+                                                            part[4]);
+            kl_distill_kernel<<<rows, NT, 0, ctx->stream>>>(n, (int)nf, io->e2, io->logits,
+                                                            cfg->temp, cfg->alpha, io->de2,
+                                                            part[5]);
+            t.part[4] = part[4];
+            t.part[5] = part[5];
+        }
+        if (cfg->beta > 0.0f) {
+            hint_mse_kernel<true><<<rows, NT, 0, ctx->stream>>>(n, (int)d4, io->h1, io->feat,
+                                                                cfg->beta, io->dh1, part[6]);
+            hint_mse_kernel<true><<<rows, NT, 0, ctx->stream>>>(n, (int)d4, io->h2, io->feat,
+                                                                cfg->beta, io->dh2, part[7]);
+            t.part[6] = part[6];
+            t.part[7] = part[7];
+            t.mul1[6] = t.mul1[7] = 1.0f / (float)(n * d4);
+            t.mul2[6] = t.mul2[7] = cfg->beta;
+        } else {
+            zero(io->dh1, n * d4);
+            zero(io->dh2, n * d4);
+        }
+    }
+    loss_totals_kernel<<<1, 64, 0, ctx->stream>>>(n, t, total, ce, correct);
+    RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
 

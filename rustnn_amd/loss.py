@@ -78,3 +78,41 @@ def hint_mse(pred, target, scale, dz, ctx=None):
                                  _ptr(target, n * c, "target"), float(scale),
                                  _ptr(dz, n * c, "dz"), _ptr(loss, 1, "loss")))
     return loss
+
+
+def build_loss(out, tf, tc, hard, hardc, nf, nc, hp, ctx=None):
+    """build_loss (train.rs:70-118) in one library call (rnn_build_loss):
+    returns (grads, total, ce, correct) -- grads the dict of gradients the
+    backward takes (logits, coarse and, with exits, e1, e2, h1, h2), written
+    by the library; total / ce / correct 1-element device tensors."""
+    import ctypes as C
+
+    import torch
+
+    from . import LossCfg, LossIO
+    ctx = ctx or default_ctx()
+    n = hard.numel()
+    dev = out["logits"].device
+    g = {"logits": torch.empty_like(out["logits"]),
+         "coarse": torch.empty(n, nc, device=dev) if nc else None}
+    exits = "e1" in out
+    if exits:
+        g.update(e1=torch.empty_like(out["e1"]), e2=torch.empty_like(out["e2"]),
+                 h1=torch.empty_like(out["h1"]), h2=torch.empty_like(out["h2"]))
+    d4 = out["h1"].shape[-1] if exits else 0
+    cfg = LossCfg(float(hp["coarse_w"]), float(hp["exit_w"][0]), float(hp["exit_w"][1]),
+                  float(hp["alpha"]), float(hp["temp"]), float(hp["beta"]),
+                  int(not hp["no_taxo"]))
+    p = lambda t: t.data_ptr() if t is not None else None
+    io = LossIO(p(out["logits"]), p(out.get("coarse")), p(out.get("e1")), p(out.get("e2")),
+                p(out.get("h1")), p(out.get("h2")), p(out.get("feat")), p(g["logits"]),
+                p(g["coarse"]), p(g.get("e1")), p(g.get("e2")), p(g.get("h1")), p(g.get("h2")))
+    total = torch.empty(1, device=dev)
+    ce = torch.empty(1, device=dev)
+    correct = torch.empty(1, dtype=torch.int32, device=dev)
+    ctx.check(lib().rnn_build_loss(
+        ctx.h, n, nf, nc, d4, _ptr(tf, n * nf, "tf"), _ptr(tc, n * nc, "tc") if tc is not None
+        else None, _ptr(hard, n, "hard"), _ptr(hardc, n, "hardc") if hardc is not None else None,
+        C.byref(cfg), C.byref(io), _ptr(total, 1, "total"), _ptr(ce, 1, "ce"),
+        _ptr(correct, 1, "correct")))
+    return g, total, ce, correct

@@ -833,34 +833,15 @@ class ViTStep:
                 ctx.set_defer(False)  # flushes: every gradient complete
 
     def _forward_backward(self, x, labels, coarse, tf, tc, dom, n, taxo):
-        import torch
-        from .loss import ce_soft, hint_mse, kl_distill
+        from .loss import build_loss
         hp, net, ctx = self.hp, self.net, self.net.ctx
         out = net.forward(x, True)
-        # build_loss (train.rs:70-118); the total adds its terms in the
-        # reference's order and grouping, in f32
-        ce, correct, dlog = ce_soft(out["logits"], tf, dom, 1.0, ctx=ctx)
-        total = ce
-        if hp["coarse_w"] > 0 and taxo:
-            lc, _, dcoarse = ce_soft(out["coarse"], tc, coarse, hp["coarse_w"], ctx=ctx)
-            total = total + hp["coarse_w"] * lc
-        else:
-            dcoarse = torch.zeros(n, self.nc, device=x.device)
-        g = {"logits": dlog, "coarse": dcoarse}
-        if "e1" in out:
-            w1, w2 = hp["exit_w"]
-            l1, _, de1 = ce_soft(out["e1"], tf, dom, w1, ctx=ctx)
-            l2, _, de2 = ce_soft(out["e2"], tf, dom, w2, ctx=ctx)
-            total = total + (w1 * l1 + w2 * l2)
-            if hp["alpha"] > 0:
-                k1 = kl_distill(out["e1"], out["logits"], hp["temp"], hp["alpha"], de1, ctx=ctx)
-                k2 = kl_distill(out["e2"], out["logits"], hp["temp"], hp["alpha"], de2, ctx=ctx)
-                total = total + hp["alpha"] * (k1 + k2)
-            dh1, dh2 = torch.zeros_like(out["h1"]), torch.zeros_like(out["h2"])
-            if hp["beta"] > 0:
-                total = total + (hint_mse(out["h1"], out["feat"], hp["beta"], dh1, ctx=ctx) +
-                                 hint_mse(out["h2"], out["feat"], hp["beta"], dh2, ctx=ctx))
-            g.update(e1=de1, e2=de2, h1=dh1, h2=dh2)
+        # build_loss (train.rs:70-118) in one library call: every loss term,
+        # the gradients written, the total in the reference's order and
+        # grouping (f32)
+        g, total, _, correct = build_loss(out, tf, tc if taxo else None, dom,
+                                          coarse if taxo else None, net.nclass, self.nc, hp,
+                                          ctx=ctx)
         net.backward(g)
         return total, correct, out
 

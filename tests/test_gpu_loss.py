@@ -112,3 +112,46 @@ class GpuLoss:
 def test_reference_losscheck_on_gpu(rnn, orc):
     errs = losscheck(orc, GpuLoss())
     assert all(v < refcheck.TOL for v in errs.values()), errs
+
+
+@pytest.mark.parametrize("variant", ["default", "no_taxo", "no_alpha_beta"])
+def test_build_loss_matches_oracle(rnn, orc, variant):
+    """rnn_build_loss (train.rs:70-118 in one call) against the oracle's
+    build_loss on the same heads and targets: the total, ce and hits, and
+    every gradient; the branches without the coarse term (no_taxo, whose
+    coarse gradient must be zeros) and without distillation / hints (the
+    hint gradients zeros)."""
+    import torch
+    from oracle import pyvit
+    from rustnn_amd.loss import build_loss, soft_targets
+    n, nf, nc, d4 = 64, 100, 20, 384
+    rng = orc.Rng(77)
+    hp = dict(pyvit.TRAIN_DEFAULT)
+    if variant == "no_taxo":
+        hp["no_taxo"] = True
+    if variant == "no_alpha_beta":
+        hp["alpha"], hp["beta"] = 0.0, 0.0
+    parent = np.arange(nf, dtype=np.uint32) // 5
+    labels = np.array([rng.below(nf) for _ in range(n)], np.uint32)
+    coarse = parent[labels]
+    out = {k: rng.rand_vec(n * m).reshape(n, m) * np.float32(2.0) for k, m in
+           (("logits", nf), ("coarse", nc), ("e1", nf), ("e2", nf), ("h1", d4), ("h2", d4),
+            ("feat", d4))}
+    taxo = not hp["no_taxo"]
+    tf_w, tc_w = orc.soft_targets(labels, nf, hp["smooth"], parent if taxo else None, hp["sib"],
+                                  coarse, nc)
+    g_w, total_w, ce_w, corr_w = pyvit.build_loss(out, tf_w, tc_w, labels, coarse, hp, n)
+    dev = {k: to_dev(v) for k, v in out.items()}
+    L, Cc = _i32(labels), _i32(coarse)
+    tf, tc = soft_targets(L, nf, hp["smooth"], _i32(parent) if taxo else None, hp["sib"], Cc, nc)
+    g, total, ce, corr = build_loss(dev, tf, tc if taxo else None, L, Cc if taxo else None, nf, nc,
+                                    hp)
+    assert abs(float(to_host(total)[0]) - total_w) <= 1e-5 * abs(total_w), variant
+    assert abs(float(to_host(ce)[0]) - ce_w) <= 1e-5 * abs(ce_w), variant
+    assert int(to_host(corr)[0]) == corr_w
+    for k, want in g_w.items():
+        got = to_host(g[k]).reshape(want.shape)
+        if not np.any(want):
+            assert not np.any(got), (variant, k)
+        else:
+            assert rel_frob(got, want) < 1e-5, (variant, k)
