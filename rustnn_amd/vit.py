@@ -143,14 +143,15 @@ class CrossAttn:
             self.q, self.p, self.n = q, p, n
         return y.view(n, t, c)
 
-    def backward(self, dy, mem, dmem):
-        """Returns dx; dmem ([n, tk, 2c]) accumulates."""
+    def backward(self, dy, mem, dmem, set_dmem=False):
+        """Returns dx; dmem ([n, tk, 2c]) accumulates (set_dmem: is
+        written, what a zeroed dmem would receive)."""
         import torch
         n, t, c = self.n, self.tq, self.c
         do = self.proj.backward(dy.reshape(-1))
         dq = torch.empty(n * t * c, device=dy.device)
         self.core.backward(n, self.q, c, 0, mem, 2 * c, 0, c, self.tau.v, self.p, do, dq, dmem,
-                           self.tau.g, self.rel.g, set_dq=True)
+                           self.tau.g, self.rel.g, set_dq=True, set_dkv=set_dmem)
         return self.wq.backward(dq).view(n, t, c)
 
     def for_each_param(self, f):
@@ -333,8 +334,9 @@ class Block:
         _branch_add(y, m, self.ls2, self.dp3, train, seed ^ self.idx ^ 0xA2A2, y)
         return y
 
-    def backward(self, dz, mem=None, dmem=None):
-        """Returns dx; dmem accumulates the memory's gradient (vit.rs:175-249)."""
+    def backward(self, dz, mem=None, dmem=None, set_dmem=False):
+        """Returns dx; dmem accumulates the memory's gradient (vit.rs:175-249)
+        -- set_dmem: is written, as a zeroed dmem would be."""
         import torch
         L, ctx, c = lib(), self.ctx, self.c
         # each branch's DropPath + LayerScale backward reads dz / dy unchanged
@@ -344,7 +346,7 @@ class Block:
         dh = None  # the branches' input gradients, added in branch order
         if self.cross is not None:
             dc = self.lsm.backward(dy, self.dp2.mask)
-            dh = self.cross.backward(dc, mem, dmem)
+            dh = self.cross.backward(dc, mem, dmem, set_dmem)
         da = self.ls1.backward(dy, self.dp1.mask)
         # gamma.g += sum da * dwo; ddw = gamma * da: the LayerScale backward
         rows = da.numel() // c
@@ -700,9 +702,16 @@ class RustViT:
         if self.use_exits and g.get("e2") is not None:
             df2 = self.e2.backward(g["e2"], g["h2"])
             add_(dz, self.pool2.backward(df2.view(n, d)), ctx)
-        dmem = torch.zeros_like(self.mem)
+        # the memory's gradient: the last reader block (the first in the
+        # backward) writes it, the others add to it -- what the reference's
+        # zeroed dmem receives (vit.rs:652-655)
+        dmem = torch.empty_like(self.mem)
+        first = True
         for b in reversed(self.blocks3):
-            dz = b.backward(dz, self.mem, dmem)
+            dz = b.backward(dz, self.mem, dmem, set_dmem=first and b.cross is not None)
+            first = first and b.cross is None
+        if first:
+            dmem.zero_()  # no reader block
         dt = tokens_to_nchw(dz, self.th, self.th, ctx)
         dc2 = self.tok.backward(dt)
         mh = self.mh
