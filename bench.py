@@ -178,7 +178,7 @@ def cpu_protocol(samples=3, cooldown_s=1.0):
     """The restated reference CPU path (oracle/: the 6x16 AVX2 micro-kernel,
     KC 256 packing, fused im2col / col2im, per-image parallel convs, 6-row
     panel parallel matmul, split-K matmul_dw, per-image attention) timed on
-    this host, as BASELINE.md's protocol asks: every workload with all the
+    this host by the reference's regression protocol: every workload with all the
     usable cores (OpenMP, OMP_PROC_BIND=close) and with one pinned thread;
     `samples` samples each, the best kept (regress.sh:57-76), with a
     cooldown between samples; inputs seeded with the restated Rng (seed 7,
@@ -710,7 +710,7 @@ def bench_rustvit_step(R, ctx, steps, warmup, batch=128):
             "wall_ms_per_step": round(wall / steps * 1e3, 3), "loss": float(loss.item()),
             "params": sum(p.v.numel() for p in step.params),
             "reference_published": "102.6 img/s at batch 256 on a Core Ultra 265U CPU "
-                                   "(README.md:426, BASELINE.md)",
+                                   "(the reference's README.md:426)",
             "timing": "eager, HIP events around the steps; drop_seed changes per step"}
 
 

@@ -4,8 +4,8 @@
  * Drop-in boundary for the reference's L2 kernels (lsiddd/rustnn, Rust): each
  * entry point names the reference function it replaces (file:line).  A thin
  * Rust FFI crate (extern "C" + #[link(name = "rnn")]) keeps the reference call
- * sites in conv.rs / attn.rs / linear.rs / nn.rs unchanged; the binding is
- * shown in INTEGRATION.md.
+ * sites in conv.rs / attn.rs / linear.rs / nn.rs unchanged (the crate rnn-sys,
+ * generated from this header).
  *
  * Conventions
  *  - Every float pointer is a DEVICE pointer (hipMalloc / torch CUDA tensor)

@@ -12,8 +12,8 @@
 //!   `linear_forward` / `linear_backward` are the bodies of
 //!   `Conv2d::{forward, backward_w, backward}` (nn.rs:166, 193, 230) and
 //!   `Linear::{forward, backward}` (linear.rs:44, 66) over slices: those
-//!   methods keep their signatures and call these (INTEGRATION.md shows the
-//!   swapped bodies).
+//!   methods keep their signatures and their bodies become one call of
+//!   these.
 //!
 //! Errors panic, which the reference's `panic = "abort"` turns into an abort,
 //! as a slice-bounds panic there does.  One library context serves the

@@ -1,6 +1,6 @@
 """Writes the golden fixtures under tests/golden/ (run in the build container).
 
-The reference ships no golden vectors, so these are produced by an
+The reference ships no golden vectors for this path, so these are produced by an
 independent library -- PyTorch on the CPU in float64 -- from seeded numpy
 inputs:
 
