@@ -74,6 +74,15 @@ struct DwArgs {
     int hw, ohw, cihw, cohw; // H*W, OH*OW, CI*H*W, CO*OH*OW
     FastDiv fd_gpr, fd_tr, fd_ximg, fd_tiwp, fd_dimg, fd_owp;
     int nbuf;                // stage buffers (1 or 2)
+    // 16-byte staging (3x3 stride 1 pad 1, whole tiles; the plan's MT = 0):
+    // X window rows of rch 16-byte chunks, x = -4 .. OW + 3 at row column
+    // x + 4 (the first and last chunk stay zero: the left and right padding);
+    // dY rows as they lie in memory.  Channels sit an odd number of chunks
+    // apart, as the 4-byte layout's 64m + 4 words do.
+    int rch;                 // chunks of an X window row: OW / 4 + 2
+    int xdata, xchunks;      // X data chunks per channel (IMGS * TIH * rch), LDS chunks (odd)
+    int ddata, dchunks;      // dY data chunks per channel (IMGS * TR * OW / 4), LDS chunks (odd)
+    int nix, nid;            // 64-lane 16-byte DMA instructions per tile (X, dY)
 };
 
 // Per-lane DMA table entry: (element offset in the image plane, 16 bits) |
@@ -186,18 +195,19 @@ __device__ __forceinline__ void dw_issue_channel(const DwArgs &g, const DwStage<
 }
 
 // Operands of one 8-pixel group.
-template <int K, int S>
+template <int K, int S, bool X4 = false>
 struct DwOps {
     float4 a;                                   // dY: pixels 4h .. 4h+3
     float4 x0[K];                               // X: 4 values from 4h (even part for S = 2)
-    float2 x1[K];                               // X: the 2 values after them
+    float2 x1[K];                               // X: the 2 values after them (X4: before them)
     float4 xo[(K == 3 && S == 2) ? K : 1];      // X odd columns (stride-2 3x3)
+    float xr[X4 ? K : 1];                       // X4: the value after x1's pair
 };
 
-template <int K, int S>
+template <int K, int S, bool X4>
 __device__ __forceinline__ void dw_fetch(const DwArgs &g, const float *__restrict__ xs,
                                          const float *__restrict__ ds, int grp, int lane,
-                                         DwOps<K, S> &o) {
+                                         DwOps<K, S, X4> &o) {
     const int h = lane >> 5, l32 = lane & 31;
     // group -> (tile row rr = img*TR + r, column group cq); the dY window is
     // dense in groups, so its offset is 8*grp
@@ -208,21 +218,32 @@ __device__ __forceinline__ void dw_fetch(const DwArgs &g, const float *__restric
         xs + l32 * g.chsx + img * g.ximg + r * g.xrow * g.TIWP + 8 * cq + 4 * h;
 #pragma unroll
     for (int kh = 0; kh < K; kh++) {
-        o.x0[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP);
-        if constexpr (K == 3) {
-            // 2 more values: b64 read of the next 4-aligned group
-            o.x1[kh] = *reinterpret_cast<const float2 *>(xr + kh * g.TIWP + 4);
+        if constexpr (X4) {
+            // pixels ox0 = 8cq + 4h .. +3 read x = ox0 - 1 .. ox0 + 4, stored
+            // at row column x + 4: x = ox0 - 2, ox0 - 1 / ox0 .. ox0 + 3 / ox0 + 4
+            o.x1[kh] = *reinterpret_cast<const float2 *>(xr + kh * g.TIWP + 2);
+            o.x0[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP + 4);
+            o.xr[kh] = xr[kh * g.TIWP + 8];
+        } else {
+            o.x0[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP);
+            if constexpr (K == 3) {
+                // 2 more values: b64 read of the next 4-aligned group
+                o.x1[kh] = *reinterpret_cast<const float2 *>(xr + kh * g.TIWP + 4);
+            }
+            if constexpr (K == 3 && S == 2)
+                o.xo[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP + g.HE);
         }
-        if constexpr (K == 3 && S == 2)
-            o.xo[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP + g.HE);
     }
 }
 
 // B value of tap (kh, kw) for k-step i.
-template <int K, int S>
-__device__ __forceinline__ float dw_bval(const DwOps<K, S> &o, int kh, int kw, int i) {
+template <int K, int S, bool X4>
+__device__ __forceinline__ float dw_bval(const DwOps<K, S, X4> &o, int kh, int kw, int i) {
     if constexpr (K == 1) {
         return o.x0[0][i];
+    } else if constexpr (X4) {
+        const int v = kw + i;  // x = ox0 - 1 + v
+        return v == 0 ? o.x1[kh].y : (v < 5 ? o.x0[kh][v - 1] : o.xr[kh]);
     } else if constexpr (S == 1) {
         const int v = kw + i;  // compile-time after unrolling
         return v < 4 ? o.x0[kh][v] : (v == 4 ? o.x1[kh].x : o.x1[kh].y);
@@ -243,30 +264,121 @@ __device__ __forceinline__ void dw_issue_tile(const DwArgs &g, const DwLane<MT> 
         dw_issue_channel<MT>(g, d, pw + DW_NP * k, cob, cib, buf);
 }
 
+// 16-byte staging.  A 64-lane DMA instruction fills 64 consecutive 16-byte
+// LDS chunks (1 KiB), lane i chunk i; instruction k of a tile's X (dY)
+// region fills chunks 64k .. 64k + 63 of [channel][xchunks] ([channel]
+// [dchunks]).  Which source chunk a lane loads depends only on k, the lane,
+// the conv and its (co, ci) blocks, so each producer lane keeps its byte
+// offsets for the whole job in registers -- one set per window kind, the
+// first row (top padding) and / or the last row (bottom padding) left out --
+// and a tile costs one buffer descriptor and the DMA instructions, with no
+// per-row address arithmetic.  Chunks without source data (padding columns,
+// padding rows, the odd-stride filler, channels past the convolution's) take
+// an offset past every buffer and are written as zeros.
+constexpr int DW4_XK = 11;  // X instructions per producer wave, at most
+constexpr int DW4_DK = 5;   // dY instructions per producer wave, at most
+
+struct DwLane4 {
+    uint32_t xo[4][DW4_XK];  // window kind (bit 0: no first row, bit 1: no last row)
+    uint32_t dof[DW4_DK];
+};
+
+__device__ __forceinline__ void dw_lane4_init(const DwArgs &g, DwLane4 &L, int pw, int lane,
+                                              int cob, int cib) {
+    const int rpi = g.TIH * g.rch;  // X chunks of one image's window
+#pragma unroll
+    for (int kk = 0; kk < DW4_XK; kk++) {
+        const int k = pw + DW_NP * kk;
+        const int q = 64 * k + lane;
+        const int c = q / g.xchunks, r = q - c * g.xchunks;
+        const int img = r / rpi, rem = r - img * rpi;
+        const int ty = rem / g.rch, m = rem - ty * g.rch;
+        const bool ok = k < g.nix && c < 32 && cib * 32 + c < g.CI && r < g.xdata && m > 0 &&
+                        m < g.rch - 1;
+        const int e = img * g.cihw + c * g.hw + 4 * (m - 1);
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            // rows lo .. hi of the window hold image rows; offsets are taken
+            // from the window's first such row
+            const int lo = w & 1, hi = g.TIH - 1 - (w >> 1);
+            const bool v = ok && ty >= lo && ty <= hi;
+            L.xo[w][kk] = v ? (uint32_t)(e + (ty - lo) * g.W) * 4u : DMA_OOB;
+        }
+    }
+    const int dpi = g.TR * (g.OW >> 2);  // dY chunks of one image's tile
+#pragma unroll
+    for (int kk = 0; kk < DW4_DK; kk++) {
+        const int k = pw + DW_NP * kk;
+        const int q = 64 * k + lane;
+        const int c = q / g.dchunks, r = q - c * g.dchunks;
+        const int img = r / dpi, rem = r - img * dpi;
+        const bool ok = k < g.nid && c < 32 && cob * 32 + c < g.CO && r < g.ddata;
+        L.dof[kk] = ok ? (uint32_t)(img * g.cohw + c * g.ohw + 4 * rem) * 4u : DMA_OOB;
+    }
+}
+
+// All DMA of one tile by producer wave pw (whole tiles: n0 + IMGS <= N and
+// a0 + TR <= OH).  The descriptors start at the tile's first image row that
+// the window reads (X) and at its first output row (dY) and end with the
+// tile's last image, so every chunk with source data lies inside them.
+__device__ __forceinline__ void dw_issue_tile4(const DwArgs &g, const DwLane4 &L, int tile,
+                                               int cob, int cib, float *__restrict__ buf, int pw) {
+    if (tile >= g.ntiles) return;
+    const int n0 = (tile / g.tiles_a) * g.IMGS, a0 = (tile % g.tiles_a) * g.TR;
+    const int y0 = a0 - g.pad;
+    const int kind = (y0 < 0 ? 1 : 0) | (a0 + g.TR >= g.OH ? 2 : 0);
+    const long long xend = (long long)(n0 + g.IMGS) * g.cihw;
+    const long long xo = (long long)n0 * g.cihw + (long long)cib * 32 * g.hw +
+                         (long long)max(y0, 0) * g.W;
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(g.x + xo, (uint32_t)((xend - xo) * 4));
+    const long long dend = (long long)(n0 + g.IMGS) * g.cohw;
+    const long long dq = (long long)n0 * g.cohw + (long long)cob * 32 * g.ohw + (long long)a0 * g.OW;
+    const __amdgpu_buffer_rsrc_t rd = make_rsrc(g.dy + dq, (uint32_t)((dend - dq) * 4));
+    auto issue_x = [&](auto wc) {
+        constexpr int w = decltype(wc)::value;
+#pragma unroll
+        for (int kk = 0; kk < DW4_XK; kk++)
+            if (pw + DW_NP * kk < g.nix)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rx, (lds_ptr_t)(buf + (pw + DW_NP * kk) * 256), 16, L.xo[w][kk], 0, 0, 0);
+    };
+    switch (kind) {
+        case 0: issue_x(std::integral_constant<int, 0>()); break;
+        case 1: issue_x(std::integral_constant<int, 1>()); break;
+        case 2: issue_x(std::integral_constant<int, 2>()); break;
+        default: issue_x(std::integral_constant<int, 3>()); break;
+    }
+#pragma unroll
+    for (int kk = 0; kk < DW4_DK; kk++)
+        if (pw + DW_NP * kk < g.nid)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rd, (lds_ptr_t)(buf + g.xwords + (pw + DW_NP * kk) * 256), 16, L.dof[kk], 0, 0, 0);
+}
+
 // MFMAs of one 8-pixel group for taps T0 .. T0 + NT - 1 (a 1x1 kernel: the
 // four k-steps into four accumulators): k-step i takes pixels i and 4 + i.
-template <int K, int S, int T0, int NT>
-__device__ __forceinline__ void dw_mma(const DwOps<K, S> &o, f32x16 (&acc)[NT]) {
+template <int K, int S, bool X4, int T0, int NT>
+__device__ __forceinline__ void dw_mma(const DwOps<K, S, X4> &o, f32x16 (&acc)[NT]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if constexpr (K == 1) {
-            acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i], dw_bval<K, S>(o, 0, 0, i),
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a[i], dw_bval<K, S, X4>(o, 0, 0, i),
                                                           acc[i], 0, 0, 0);
         } else {
 #pragma unroll
             for (int j = 0; j < NT; j++)
                 acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                    o.a[i], dw_bval<K, S>(o, (T0 + j) / K, (T0 + j) % K, i), acc[j], 0, 0, 0);
+                    o.a[i], dw_bval<K, S, X4>(o, (T0 + j) / K, (T0 + j) % K, i), acc[j], 0, 0, 0);
         }
     }
 }
 
 // Scheduling hint for one step: the LDS reads of the next group go out
 // among the first MFMAs of this one, so their latency hides under the rest.
-template <int K, int S, int NT>
+template <int K, int S, bool X4, int NT>
 __device__ __forceinline__ void dw_step_schedule() {
     constexpr int NMF = K == 1 ? 4 : 4 * NT;
-    constexpr int NRD = 1 + (K == 1 ? 1 : K * (S == 2 ? 3 : 2));
+    constexpr int NRD = 1 + (K == 1 ? 1 : K * (S == 2 || X4 ? 3 : 2));
     static_for<0, NRD>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
@@ -278,7 +390,7 @@ __device__ __forceinline__ void dw_step_schedule() {
 // two operand sets alternate so that the reads of group n+1 overlap the
 // MFMAs of group n.  Reads past the tile's last group are clamped to group
 // `wave` (in range; their values are not used).
-template <int K, int S, int T0, int NT>
+template <int K, int S, bool X4, int T0, int NT>
 __device__ __forceinline__ void dw_compute(const DwArgs &g, const float *__restrict__ cur,
                                            int wave, int lane, f32x16 (&acc)[NT]) {
     const float *xs = cur, *ds = cur + g.xwords;
@@ -287,17 +399,17 @@ __device__ __forceinline__ void dw_compute(const DwArgs &g, const float *__restr
         const int gi = wave + DW_NW * s;
         return gi < g.ngroups ? gi : min(wave, g.ngroups - 1);
     };
-    DwOps<K, S> oa, ob;
-    dw_fetch<K, S>(g, xs, ds, grp(0), lane, oa);
+    DwOps<K, S, X4> oa, ob;
+    dw_fetch<K, S, X4>(g, xs, ds, grp(0), lane, oa);
 #pragma unroll 1
     for (int s = 0; s < nsteps; s += 2) {
-        dw_fetch<K, S>(g, xs, ds, grp(s + 1), lane, ob);
-        dw_mma<K, S, T0, NT>(oa, acc);
-        dw_step_schedule<K, S, NT>();
+        dw_fetch<K, S, X4>(g, xs, ds, grp(s + 1), lane, ob);
+        dw_mma<K, S, X4, T0, NT>(oa, acc);
+        dw_step_schedule<K, S, X4, NT>();
         if (s + 1 >= nsteps) break;
-        dw_fetch<K, S>(g, xs, ds, grp(s + 2), lane, oa);
-        dw_mma<K, S, T0, NT>(ob, acc);
-        dw_step_schedule<K, S, NT>();
+        dw_fetch<K, S, X4>(g, xs, ds, grp(s + 2), lane, oa);
+        dw_mma<K, S, X4, T0, NT>(ob, acc);
+        dw_step_schedule<K, S, X4, NT>();
     }
 }
 
@@ -328,7 +440,7 @@ __device__ __forceinline__ void dw_red_add(const float *src, int lbase, f32x16 *
 // + w3), through two LDS slices in slab order [co][ci][tap]
 // (bit-reproducible).  The groups' taps are disjoint, so both groups use
 // the same slices at once.
-template <int K, int S, int NB, int T0, int NT>
+template <int K, int S, bool X4, int NB, int T0, int NT>
 __device__ __forceinline__ void dw_mfma_wave(const DwArgs &g, float *smem, float *red, int z,
                                              int wq, int lane) {
     constexpr int KK = K * K, SL = KK * 1024, NR = K == 1 ? 1 : NT;
@@ -341,9 +453,9 @@ __device__ __forceinline__ void dw_mfma_wave(const DwArgs &g, float *smem, float
     for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
         dma_wait_barrier();
         if constexpr (NB == 2) {
-            dw_compute<K, S, T0, NT>(g, smem + (s & 1) * g.stage, wq, lane, acc);
+            dw_compute<K, S, X4, T0, NT>(g, smem + (s & 1) * g.stage, wq, lane, acc);
         } else {
-            dw_compute<K, S, T0, NT>(g, smem, wq, lane, acc);
+            dw_compute<K, S, X4, T0, NT>(g, smem, wq, lane, acc);
             __syncthreads();
         }
     }
@@ -369,32 +481,46 @@ __device__ __forceinline__ void dw_mfma_wave(const DwArgs &g, float *smem, float
 // back-pressure never stalls an MFMA wave.  Double-buffered plans (NB = 2)
 // stage the next tile while this one is computed (one barrier per tile);
 // single-buffered plans stage it after the compute barrier.
+// MT = 0: the 16-byte staging of a 3x3 stride-1 pad-1 plan (whole tiles).
 template <int K, int S, int MT, int NB>
-__global__ __launch_bounds__(dw_threads<K>()) void conv_dw_kernel(DwArgs g) {
+__device__ __forceinline__ void dw_body(const DwArgs &g, int z, int cob, int cib) {
     constexpr int KK = K * K, NG = dw_tap_groups<K>(), NMW = DW_NW * NG;
+    constexpr bool X4 = MT == 0;
+    static_assert(!X4 || (K == 3 && S == 1 && NB == 2), "16-byte staging: 3x3 stride 1, two buffers");
     extern __shared__ float smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
-    const int z = blockIdx.x, cob = blockIdx.y, cib = blockIdx.z;
     float *red = smem;  // after the tiles: 2 slices of [32][32][KK]
     const int SL = KK * 1024;
     if (wave >= NMW) {
         // producer: the same barriers as the MFMA waves, one per tile (two
         // with a single buffer), then those of the reduction
         const int pw = wave - NMW;
-        DwLane<MT> L;
-        dw_lane_init<K, S, MT>(g, L, lane);
-        dw_issue_tile<MT>(g, L, z, cob, cib, smem, pw);
-        int s = 0;
-        for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
-            dma_wait_barrier();
-            const bool more = tile + g.nz < g.ntiles;
-            if constexpr (NB == 2) {
-                if (more)
-                    dw_issue_tile<MT>(g, L, tile + g.nz, cob, cib, smem + ((s + 1) & 1) * g.stage,
-                                      pw);
-            } else {
-                __syncthreads();
-                if (more) dw_issue_tile<MT>(g, L, tile + g.nz, cob, cib, smem, pw);
+        if constexpr (X4) {
+            DwLane4 L;
+            dw_lane4_init(g, L, pw, lane, cob, cib);
+            dw_issue_tile4(g, L, z, cob, cib, smem, pw);
+            int s = 0;
+            for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
+                dma_wait_barrier();
+                if (tile + g.nz < g.ntiles)
+                    dw_issue_tile4(g, L, tile + g.nz, cob, cib, smem + ((s + 1) & 1) * g.stage, pw);
+            }
+        } else {
+            DwLane<MT> L;
+            dw_lane_init<K, S, MT>(g, L, lane);
+            dw_issue_tile<MT>(g, L, z, cob, cib, smem, pw);
+            int s = 0;
+            for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
+                dma_wait_barrier();
+                const bool more = tile + g.nz < g.ntiles;
+                if constexpr (NB == 2) {
+                    if (more)
+                        dw_issue_tile<MT>(g, L, tile + g.nz, cob, cib,
+                                          smem + ((s + 1) & 1) * g.stage, pw);
+                } else {
+                    __syncthreads();
+                    if (more) dw_issue_tile<MT>(g, L, tile + g.nz, cob, cib, smem, pw);
+                }
             }
         }
         dma_wait_barrier();
@@ -402,11 +528,11 @@ __global__ __launch_bounds__(dw_threads<K>()) void conv_dw_kernel(DwArgs g) {
         __syncthreads();
         __syncthreads();
     } else if constexpr (K == 1) {
-        dw_mfma_wave<K, S, NB, 0, 4>(g, smem, red, z, wave, lane);
+        dw_mfma_wave<K, S, X4, NB, 0, 4>(g, smem, red, z, wave, lane);
     } else if (wave < DW_NW) {
-        dw_mfma_wave<K, S, NB, 0, 5>(g, smem, red, z, wave, lane);
+        dw_mfma_wave<K, S, X4, NB, 0, 5>(g, smem, red, z, wave, lane);
     } else {
-        dw_mfma_wave<K, S, NB, 5, KK - 5>(g, smem, red, z, wave - DW_NW, lane);
+        dw_mfma_wave<K, S, X4, NB, 5, KK - 5>(g, smem, red, z, wave - DW_NW, lane);
     }
     const int ckk = g.CI * KK, rowlen = 32 * KK;
     float *slab = g.part + (long long)z * g.CO * ckk + cib * 32 * KK;
@@ -416,6 +542,26 @@ __global__ __launch_bounds__(dw_threads<K>()) void conv_dw_kernel(DwArgs g) {
         const float v = red[e] + red[SL + e];
         if (cob * 32 + co < g.CO && rem < rlim) slab[(long long)(cob * 32 + co) * ckk + rem] = v;
     }
+}
+
+template <int K, int S, int MT, int NB>
+__global__ __launch_bounds__(dw_threads<K>()) void conv_dw_kernel(DwArgs g) {
+    dw_body<K, S, MT, NB>(g, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// The weight gradients of several convolutions of one kernel shape in one
+// launch (a network's backward, once every output gradient exists): a
+// workgroup takes job blockIdx.x = (conv, slab z, co block, ci block),
+// packed conv | z << 8 | cob << 20 | cib << 26, and runs that conv's plan
+// tab[conv] exactly as conv_dw_kernel runs workgroup (z, cob, cib).  One
+// launch pays the ramp, the first tile's DMA and the epilogue once instead
+// of once per conv, and each conv can take far fewer, longer slabs.
+template <int K, int S, int MT, int NB>
+__global__ __launch_bounds__(dw_threads<K>()) void conv_dw_group_kernel(
+    const DwArgs *__restrict__ tab, const uint32_t *__restrict__ jobs) {
+    const uint32_t j = jobs[blockIdx.x];
+    dw_body<K, S, MT, NB>(tab[j & 255u], (int)((j >> 8) & 4095u), (int)((j >> 20) & 63u),
+                          (int)(j >> 26));
 }
 
 // out[e] += sum over slabs z of part[z][e], in slab order, in one launch: a
@@ -640,6 +786,48 @@ size_t dw_geometry(DwArgs &g, int K, int TR, int IMGS, int nbuf) {
     return std::max((size_t)nbuf * g.stage * 4, (size_t)(DW_NW / 2) * K * K * 1024 * 4);
 }
 
+// Geometry of a (TR, IMGS) tile of the 16-byte staging (3x3 stride 1 pad
+// 1, W = OW a multiple of 8, whole tiles); returns LDS bytes, 0 if the shape
+// or tile does not qualify.
+size_t dw_geometry4(DwArgs &g, int TR, int IMGS, size_t n) {
+    if (g.S != 1 || g.pad != 1 || g.W != g.OW || g.H != g.OH || (g.OW & 7) || g.OH % TR ||
+        (long long)n % IMGS)
+        return 0;
+    g.nbuf = 2;
+    g.TR = TR;
+    g.IMGS = IMGS;
+    g.OWP = g.OW;
+    g.gpr = g.OW / 8;
+    g.ngroups = IMGS * TR * g.gpr;
+    g.xrow = 1;
+    g.xstep = 1;
+    g.TIH = TR + 2;
+    g.HE = 0;
+    g.rch = g.OW / 4 + 2;
+    g.TIWP = 4 * g.rch;
+    g.ximg = g.TIH * g.TIWP;
+    g.dimg = TR * g.OW;
+    g.fd_gpr = make_fastdiv(g.gpr);
+    g.fd_tr = make_fastdiv(TR);
+    g.fd_ximg = make_fastdiv(g.ximg);
+    g.fd_tiwp = make_fastdiv(g.TIWP);
+    g.fd_dimg = make_fastdiv(g.dimg);
+    g.fd_owp = make_fastdiv(g.OWP);
+    g.xdata = IMGS * g.TIH * g.rch;
+    g.xchunks = g.xdata | 1;
+    g.ddata = IMGS * TR * g.OW / 4;
+    g.dchunks = g.ddata | 1;
+    g.nix = (32 * g.xchunks + 63) / 64;
+    g.nid = (32 * g.dchunks + 63) / 64;
+    if (g.nix > DW_NP * DW4_XK || g.nid > DW_NP * DW4_DK || IMGS > 127) return 0;
+    g.mx = g.md = 0;
+    g.chsx = 4 * g.xchunks;
+    g.chsd = 4 * g.dchunks;
+    g.xwords = g.nix * 256;
+    g.stage = g.xwords + g.nid * 256;
+    return std::max((size_t)2 * g.stage * 4, (size_t)(DW_NW / 2) * 9 * 1024 * 4);
+}
+
 template <int K, int S, int MT, int NB>
 const void *dw_kernel_ptr() {
     static bool attr = false;
@@ -661,6 +849,32 @@ const void *dw_pick_mt(int mt) {
 template <int K, int S>
 const void *dw_pick(int mt, int nb) {
     return nb == 2 ? dw_pick_mt<K, S, 2>(mt) : dw_pick_mt<K, S, 1>(mt);
+}
+
+template <int S, int MT>
+const void *dw_group_ptr() {
+    static bool attr = false;
+    const void *k = (const void *)conv_dw_group_kernel<3, S, MT, 2>;
+    static_assert(MT > 0 || S == 1, "16-byte staging: stride 1");
+    if (!attr) {
+        attr = true;
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    }
+    return k;
+}
+
+// The grouped kernel (3x3, double-buffered tiles) for stride s and tables of
+// mt DMA rows (mt = 0: the 16-byte staging).
+const void *dw_group_pick(int s, int mt) {
+    if (s == 1) {
+        if (mt == 0) return dw_group_ptr<1, 0>();
+        if (mt <= DW_MT[0]) return dw_group_ptr<1, DW_MT[0]>();
+        if (mt <= DW_MT[1]) return dw_group_ptr<1, DW_MT[1]>();
+        return dw_group_ptr<1, DW_MT[2]>();
+    }
+    if (mt <= DW_MT[0]) return dw_group_ptr<2, DW_MT[0]>();
+    if (mt <= DW_MT[1]) return dw_group_ptr<2, DW_MT[1]>();
+    return dw_group_ptr<2, DW_MT[2]>();
 }
 
 }  // namespace
@@ -782,6 +996,7 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
     const int ncb = (g.CO + 31) / 32, ncib = (g.CI + 31) / 32;
     auto kernel_of = [&](const DwArgs &a) -> const void * {
         const int mt = std::max(a.mx, a.md);
+        if (K == 3 && mt == 0) return dw_kernel_ptr<3, 1, 0, 2>();  // 16-byte staging
         if (K == 3)
             return a.S == 1 ? dw_pick<3, 1>(mt, a.nbuf) : dw_pick<3, 2>(mt, a.nbuf);
         return a.S == 1 ? dw_pick<1, 1>(mt, a.nbuf) : dw_pick<1, 2>(mt, a.nbuf);
@@ -807,13 +1022,39 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
         }
         return std::min(std::max(1, occ * ctx->num_cus / (ncb * ncib)), ntiles);
     };
+    // 16-byte staging for 3x3 stride-1 pad-1 shapes with whole tiles
+    // (RNN_DW_X4=0: the 4-byte staging everywhere)
+    const char *x4env = getenv("RNN_DW_X4");
+    const bool try4 = K == 3 && !(x4env && x4env[0] == '0');
+    bool use4 = false;
+    if (TR > 0 && IMGS > 0 && try4 && NB == 2) {
+        DwArgs t = g;
+        use4 = dw_geometry4(t, TR, IMGS, n) != 0;
+    }
     if (TR <= 0 || IMGS <= 0) {
         // The tile with the shortest critical path: every workgroup walks
         // ceil(ntiles / NZ) tiles of ngroups 8-pixel groups plus a fixed
         // per-tile cost (the barrier and the restart of the operand
-        // pipeline, about two groups).  Double-buffered plans first; a
-        // single buffer only when no double-buffered tile fits.
+        // pipeline, about two groups).  The 16-byte staging first, then
+        // double-buffered plans; a single buffer only when no
+        // double-buffered tile fits.
         double best = 0;
+        if (try4)
+            for (int tr = 1; tr <= g.OH; tr++)
+                for (int im = 1; im <= (tr == g.OH ? 16 : 1); im *= 2) {
+                    const size_t l = dw_geometry4(g, tr, im, n);
+                    if (l == 0 || l > 160 * 1024) continue;
+                    const int ntiles = (g.OH / tr) * (int)(n / im);
+                    const int nz = slabs_of(kernel_of(g), l, ntiles);
+                    const double cost = (double)((ntiles + nz - 1) / nz) * (g.ngroups + 2);
+                    if (best == 0 || cost < best) {
+                        best = cost;
+                        TR = tr;
+                        IMGS = im;
+                        NB = 2;
+                        use4 = true;
+                    }
+                }
         for (int nb = 2; nb >= 1 && best == 0; nb--)
             for (int tr = 1; tr <= g.OH; tr++)
                 for (int im = 1; im <= (tr == g.OH ? 16 : 1); im *= 2) {
@@ -831,7 +1072,7 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
                 }
         if (best == 0) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: tile exceeds LDS");
     }
-    lds = dw_geometry(g, K, TR, IMGS, NB);
+    lds = use4 ? dw_geometry4(g, TR, IMGS, n) : dw_geometry(g, K, TR, IMGS, NB);
     if ((long long)IMGS * std::max(g.cihw, g.cohw) * 4 >= 0x7FFFFFF0ll)
         return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv dW: tile source beyond 2 GiB");
     g.tiles_a = (g.OH + g.TR - 1) / g.TR;
@@ -894,5 +1135,130 @@ int rnn_conv_dw(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy
     hipLaunchKernelGGL(slab_reduce_kernel, dim3((unsigned)rnn_div_up(L.len, 32)), dim3(256), 0,
                        ctx->stream, ws, L.nz, (long long)L.len, dw);
     RNN_LAUNCHED(ctx);
+    return RNN_OK;
+}
+
+// ------------------------------------------------------------ grouped dW
+
+// Plans one launch for the weight gradients of `count` 3x3 convolutions of
+// one stride (double-buffered tap-kernel plans; the few-input-channel stem
+// is not one of them).  Each conv keeps the tile its own plan takes; its
+// slab count nz is chosen so that the jobs -- (conv, slab, co block, ci
+// block), each walking ceil(ntiles / nz) tiles -- fill the chip's resident
+// workgroups with the smallest longest job: starting from one slab per
+// conv, the conv with the longest job gets the next slab count that
+// shortens it while the jobs still fit.  Sets m[i].nz; the caller then
+// allocates nz * cout * cin * 9 floats of slabs per conv and the table
+// (L->table_bytes) and calls rnn_conv_dw_group_upload.
+int rnn_conv_dw_group_plan(rnn_ctx *ctx, size_t n, DwGroupMember *m, int count,
+                           DwGroupLaunch *L) {
+    if (!ctx || !m || !L) return RNN_E_NULL;
+    if (count <= 0 || count > 255 || n == 0)
+        return rnn_fail(ctx, RNN_E_UNSUPPORTED, "grouped dW: 1 to 255 convolutions");
+    std::vector<DwLaunch> pl(count);
+    int S = -1, mt = 0;
+    size_t lds = 0;
+    for (int i = 0; i < count; i++) {
+        if (m[i].sp.k != 3 || (S >= 0 && (int)m[i].sp.stride != S))
+            return rnn_fail(ctx, RNN_E_UNSUPPORTED, "grouped dW: 3x3 convolutions of one stride");
+        S = (int)m[i].sp.stride;
+        const int rc = dw_plan(ctx, &m[i].sp, n, nullptr, nullptr, pl[i]);
+        if (rc) return rc;
+        if (pl[i].small || pl[i].g.nbuf != 2)
+            return rnn_fail(ctx, RNN_E_UNSUPPORTED, "grouped dW: conv %d has no tap-kernel plan", i);
+        const int ncb = (pl[i].g.CO + 31) / 32, ncib = (pl[i].g.CI + 31) / 32;
+        if (ncb > 64 || ncib > 64)
+            return rnn_fail(ctx, RNN_E_UNSUPPORTED, "grouped dW: more than 2048 channels");
+        const int mti = std::max(pl[i].g.mx, pl[i].g.md);  // 0: the 16-byte staging
+        if (i > 0 && (mti == 0) != (mt == 0))
+            return rnn_fail(ctx, RNN_E_UNSUPPORTED, "grouped dW: one staging for every conv");
+        mt = std::max(mt, mti);
+        lds = std::max(lds, pl[i].lds);
+    }
+    const void *kern = dw_group_pick(S, mt);
+    int occ = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, dw_threads<3>(), lds) !=
+            hipSuccess ||
+        occ < 1)
+        occ = 1;
+    const long long budget = (long long)occ * ctx->num_cus;
+    std::vector<int> nz(count, 1), pairs(count), tiles(count);
+    std::vector<long long> w(count);
+    long long jobs = 0;
+    for (int i = 0; i < count; i++) {
+        const DwArgs &g = pl[i].g;
+        pairs[i] = ((g.CO + 31) / 32) * ((g.CI + 31) / 32);
+        tiles[i] = g.ntiles;
+        w[i] = g.ngroups + 2;
+        jobs += pairs[i];
+    }
+    auto cost = [&](int i) { return (long long)((tiles[i] + nz[i] - 1) / nz[i]) * w[i]; };
+    for (;;) {
+        int worst = 0;
+        for (int i = 1; i < count; i++)
+            if (cost(i) > cost(worst)) worst = i;
+        const int per = (tiles[worst] + nz[worst] - 1) / nz[worst];
+        if (per <= 1) break;
+        const int next = (tiles[worst] + per - 2) / (per - 1);  // fewest slabs for per-1 tiles
+        if (next > 4095 || jobs + (long long)pairs[worst] * (next - nz[worst]) > budget) break;
+        jobs += (long long)pairs[worst] * (next - nz[worst]);
+        nz[worst] = next;
+    }
+    L->conv.clear();
+    L->jobs.clear();
+    for (int i = 0; i < count; i++) {
+        DwArgs g = pl[i].g;
+        g.nz = nz[i];
+        m[i].nz = nz[i];
+        const int ncb = (g.CO + 31) / 32, ncib = (g.CI + 31) / 32;
+        for (int z = 0; z < nz[i]; z++)
+            for (int cb = 0; cb < ncb; cb++)
+                for (int ib = 0; ib < ncib; ib++)
+                    L->jobs.push_back((uint32_t)i | (uint32_t)z << 8 | (uint32_t)cb << 20 |
+                                      (uint32_t)ib << 26);
+        std::vector<unsigned char> b(sizeof(DwArgs));
+        std::memcpy(b.data(), &g, sizeof(DwArgs));
+        L->conv.push_back(b);
+    }
+    L->kern = kern;
+    L->lds = lds;
+    L->threads = dw_threads<3>();
+    L->njobs = (int)L->jobs.size();
+    L->table_bytes = (size_t)count * sizeof(DwArgs) + L->jobs.size() * sizeof(uint32_t);
+    L->count = count;
+    return RNN_OK;
+}
+
+// Writes the operand and slab pointers of every conv into the plan and
+// uploads the tables to L->table (device, L->table_bytes, set by the
+// caller; synchronous).
+int rnn_conv_dw_group_upload(rnn_ctx *ctx, const DwGroupMember *m, DwGroupLaunch *L) {
+    if (!ctx || !m || !L || !L->table) return RNN_E_NULL;
+    std::vector<unsigned char> host(L->table_bytes);
+    for (int i = 0; i < L->count; i++) {
+        if (!m[i].dy || !m[i].x || !m[i].slabs)
+            return rnn_fail(ctx, RNN_E_NULL, "grouped dW: conv %d has a null operand", i);
+        DwArgs g;
+        std::memcpy(&g, L->conv[i].data(), sizeof(DwArgs));
+        g.dy = m[i].dy;
+        g.x = m[i].x;
+        g.part = m[i].slabs;
+        std::memcpy(host.data() + (size_t)i * sizeof(DwArgs), &g, sizeof(DwArgs));
+    }
+    std::memcpy(host.data() + (size_t)L->count * sizeof(DwArgs), L->jobs.data(),
+                L->jobs.size() * sizeof(uint32_t));
+    RNN_HIP(ctx, hipMemcpy(L->table, host.data(), host.size(), hipMemcpyHostToDevice));
+    return RNN_OK;
+}
+
+// The grouped launch on the context's stream: every conv's slabs written.
+int rnn_conv_dw_group_launch(rnn_ctx *ctx, const DwGroupLaunch *L) {
+    if (!L->njobs) return RNN_OK;
+    const DwArgs *tab = (const DwArgs *)L->table;
+    const uint32_t *jobs = (const uint32_t *)((const char *)L->table +
+                                              (size_t)L->count * sizeof(DwArgs));
+    void *args[] = {(void *)&tab, (void *)&jobs};
+    RNN_HIP(ctx, hipLaunchKernel(L->kern, dim3((unsigned)L->njobs), dim3(L->threads), args, L->lds,
+                                 ctx->stream));
     return RNN_OK;
 }

@@ -78,6 +78,10 @@ struct NetConv {
     // straight into the gradient instead
     float *slabs = nullptr;
     int nz = 0;
+    // dW in a grouped launch of the backward (group gset, member gidx)
+    // instead of a launch of its own
+    bool grouped = false;
+    int gset = -1, gidx = -1;
     // weights packed for the forward / dX kernels (per plan); null: unpacked
     float *wp_f = nullptr, *wp_x = nullptr;
     // this conv's output gradient in the backward (per plan): its own buffer,
@@ -176,6 +180,19 @@ struct rnn_resnet {
     // (RNN_BN_PASSES=separate: in passes of their own)
     bool fuse_bn = true;
     bool capturing = false;  // recording the step graph: no side stream there
+    // The 3x3 stride-1 convs' weight gradients in grouped launches
+    // (RNN_DW_GROUP): 1 = one launch after the dX chain; 2 = one per stage
+    // (the blocks of one width), on the side stream once the stage's
+    // output gradients exist; 0 = each conv's on its own, as the others'.
+    int group_dw = 1;
+    struct DwGroup {
+        DwGroupLaunch L;
+        std::vector<DwGroupMember> m;
+        std::vector<NetConv *> convs;
+        size_t first_block = 0;  // launched once this block's backward is done
+        size_t table_off = 0;
+    };
+    std::vector<DwGroup> dwgs;
     int step_calls = 0;
     bool use_graph = true;
     char graph_err[160] = {0};
@@ -293,12 +310,50 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
         bnpart(b.b2, b.c2.epf);
         if (b.down) bnpart(b.bd, b.cd.epf);
     }
+    // The grouped weight gradients: the 3x3 stride-1 convs but the stem,
+    // all in one group or one group per stage (blocks of one width).
+    r->dwgs.clear();
+    r->stem.grouped = false;
+    for (auto &b : r->blocks) b.c1.grouped = b.c2.grouped = b.cd.grouped = false;
+    if (r->group_dw) {
+        for (size_t i = 0; i < r->blocks.size(); i++) {
+            NetBlock &b = r->blocks[i];
+            if (r->dwgs.empty() ||
+                (r->group_dw == 2 && b.c2.cout != r->blocks[i - 1].c2.cout)) {
+                r->dwgs.emplace_back();
+                r->dwgs.back().first_block = i;  // its lowest block: the backward's last
+            }
+            auto &G = r->dwgs.back();
+            for (auto pr : {std::make_pair(&b.c1, std::make_pair(b.hin, b.win)),
+                            std::make_pair(&b.c2, std::make_pair(b.hout, b.wout))}) {
+                DwGroupMember mm;
+                mm.sp = pr.first->spec(pr.second.first, pr.second.second);
+                if (mm.sp.k != 3 || mm.sp.stride != 1) continue;
+                G.m.push_back(mm);
+                G.convs.push_back(pr.first);
+            }
+        }
+        for (size_t gi = 0; gi < r->dwgs.size(); gi++) {
+            auto &G = r->dwgs[gi];
+            if (G.convs.size() < 2 ||
+                rnn_conv_dw_group_plan(ctx, n, G.m.data(), (int)G.m.size(), &G.L) != RNN_OK) {
+                G.L = DwGroupLaunch();
+                continue;
+            }
+            for (size_t i = 0; i < G.convs.size(); i++) {
+                G.convs[i]->grouped = true;
+                G.convs[i]->gset = (int)gi;
+                G.convs[i]->gidx = (int)i;
+            }
+        }
+    }
     // dW slabs of every conv, and the gradient segment table.
     std::vector<std::pair<NetConv *, size_t>> slabs;
     auto slab = [&](NetConv &c, uint32_t h, uint32_t w) {
         rnn_conv_spec sp = c.spec(h, w);
-        const size_t f = rnn_conv_dw_slab_floats(ctx, &sp, n);
         const size_t len = (size_t)c.cout * c.cin * c.k * c.k;
+        const size_t f = c.grouped ? (size_t)r->dwgs[c.gset].m[c.gidx].nz * len
+                                   : rnn_conv_dw_slab_floats(ctx, &sp, n);
         c.nz = f ? (int)(f / len) : 0;
         if (f) slabs.push_back({&c, cv.take(f * sizeof(float))});
     };
@@ -343,6 +398,7 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     const size_t o_cor = cv.take(sizeof(uint32_t));
     const size_t o_tick = cv.take(sizeof(uint32_t));
     const size_t o_cer = cv.take(2 * n * sizeof(float));
+    for (auto &G : r->dwgs) G.table_off = cv.take(std::max<size_t>(G.L.table_bytes, 1));
     void *mem = nullptr;
     hipError_t e = hipMalloc(&mem, cv.off);
     if (e != hipSuccess)
@@ -427,7 +483,7 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
         NetConv *c = const_cast<NetConv *>(conv_of[order[k]]);
         GradSeg g = segs[k];
         if (c) c->fseg = -1;
-        if (c && c != &r->stem && g.slabs) {
+        if (c && c != &r->stem && !c->grouped && g.slabs) {
             g.blk0 = 0;
             c->fseg = (int)fsv.size();
             c->fblk = (long long)rnn_div_up((size_t)g.len, (size_t)32);
@@ -476,6 +532,27 @@ int plan(rnn_resnet *r, size_t n, size_t H, size_t W) {
     for (auto &b : r->blocks) {
         b.in = prev;
         prev = b.out;
+    }
+    // each grouped conv's output gradient buffer, input and slabs
+    for (auto &b : r->blocks)
+        for (auto pr : {std::make_pair(&b.c1, (const float *)b.in),
+                        std::make_pair(&b.c2, (const float *)b.h)}) {
+            NetConv &c = *pr.first;
+            if (!c.grouped) continue;
+            DwGroupMember &mm = r->dwgs[c.gset].m[c.gidx];
+            mm.dy = c.dyb;
+            mm.x = pr.second;
+            mm.slabs = c.slabs;
+        }
+    for (auto &G : r->dwgs) {
+        if (!G.L.njobs) continue;
+        G.L.table = base + G.table_off;
+        const int ue = rnn_conv_dw_group_upload(ctx, G.m.data(), &G.L);
+        if (ue != RNN_OK) {
+            (void)hipFree(r->arena);
+            r->arena = nullptr;
+            return ue;
+        }
     }
     r->n = n;
     r->H = H;
@@ -699,17 +776,19 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
     for (size_t i = nb; i-- > 0;) {
         NetBlock &b = r->blocks[i];
         const size_t hw = (size_t)b.hout * b.wout;
-        float *dy2 = use_side(r) ? b.c2.dyb : r->t1;
+        // a conv's output gradient keeps a buffer of its own while a dW
+        // reads it later (on the side stream, or in the grouped launch)
+        float *dy2 = use_side(r) || b.c2.grouped ? b.c2.dyb : r->t1;
         TRY(rnn_bn_backward_apply_launch(ctx, n, b.b2.c, hw, d, nullptr, b.y2,
                                          bn_state(r, b.b2), b.b2.part, dy2));
         rnn_conv_spec s2 = b.c2.spec(b.hout, b.wout);
-        TRY(conv_dw_side(r, b.c2, s2, dy2, b.h, ev));
+        if (!b.c2.grouped) TRY(conv_dw_side(r, b.c2, s2, dy2, b.h, ev));
         TRY(rnn_conv2d_backward_x_wp(ctx, &s2, n, dy2, pv_of(r, b.c2.w), b.c2.wp_x, r->t2));
-        float *dy1 = use_side(r) ? b.c1.dyb : r->t1;
+        float *dy1 = use_side(r) || b.c1.grouped ? b.c1.dyb : r->t1;
         TRY(rnn_bn_backward_launch(ctx, n, b.b1.c, hw, r->t2, b.h, b.y1, bn_state(r, b.b1),
                                    r->part, dy1));
         rnn_conv_spec s1 = b.c1.spec(b.hin, b.win);
-        TRY(conv_dw_side(r, b.c1, s1, dy1, b.in, ev));
+        if (!b.c1.grouped) TRY(conv_dw_side(r, b.c1, s1, dy1, b.in, ev));
         TRY(rnn_conv2d_backward_x_wp(ctx, &s1, n, dy1, pv_of(r, b.c1.w), b.c1.wp_x, other));
         const float *add = d;  // dx = c1 dX + d (add_, model.rs:72)
         if (b.down) {
@@ -723,6 +802,17 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
         }
         TRY(resid(r, i, b.c1.cin, (size_t)b.hin * b.win, other, add, b.in, nullptr));
         std::swap(d, other);
+        if (r->group_dw == 2 && use_side(r))
+            for (auto &G : r->dwgs)
+                if (G.first_block == i && G.L.njobs) {
+                    // this stage's output gradients are all written
+                    TRY(fork_side(r, ev));
+                    hipStream_t main = ctx->stream;
+                    ctx->stream = r->side;
+                    const int rc = rnn_conv_dw_group_launch(ctx, &G.L);
+                    ctx->stream = main;
+                    TRY(rc);
+                }
     }
     rnn_conv_spec sp = r->stem.spec((uint32_t)r->H, (uint32_t)r->W);
     // d is already relu_back_'d by the stem output (model.rs:159)
@@ -730,6 +820,9 @@ int backward(rnn_resnet *r, const float *dlogits, bool sgd) {
                                      r->y0, bn_state(r, r->stem_bn), r->stem_bn.part, r->t1));
     // The stem's dX would be the image gradient: discarded (model.rs:161).
     TRY(conv_dw(r, r->stem, sp, r->t1, r->x));
+    // the last grouped weight gradients, their output gradients all written
+    for (auto &G : r->dwgs)
+        if (!(r->group_dw == 2 && use_side(r))) TRY(rnn_conv_dw_group_launch(ctx, &G.L));
     if (use_side(r)) {
         // the side stream summed the other convs' slabs into g
         TRY(join_side(r, ev));
@@ -838,6 +931,8 @@ int rnn_resnet_create(rnn_ctx *ctx, size_t depth_n, size_t width, size_t nclass,
     r->use_graph = g ? g[0] != '0' : !r->overlap;
     const char *bp = getenv("RNN_BN_PASSES");
     r->fuse_bn = !(bp && strcmp(bp, "separate") == 0);
+    const char *gd = getenv("RNN_DW_GROUP");
+    if (gd) r->group_dw = gd[0] == '2' ? 2 : gd[0] == '0' ? 0 : 1;
     // ResNet::new (model.rs:113-135): blocks first (their convs draw from the
     // Rng in c1, c2, shortcut order), then the stem conv, then the classifier.
     const uint32_t widths[3] = {(uint32_t)width, (uint32_t)width * 2, (uint32_t)width * 4};

@@ -502,6 +502,33 @@ size_t rnn_conv_dw_slab_floats(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n);
 int rnn_conv_dw_slabs(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
                       const float *x, float *slabs, int *nz);
 
+// Grouped weight gradients: several 3x3 convolutions of one stride in one
+// launch (conv_dw.hip).  rnn_conv_dw_group_plan sets each member's slab
+// count nz and the launch (kernel, LDS, jobs, table bytes); the caller
+// allocates each member's nz * cout * cin * 9 floats of slabs and
+// table_bytes of device memory in `table`, then rnn_conv_dw_group_upload
+// writes the members' pointers there.  Every launch then writes each
+// member's slabs (summed in slab order by rnn_grad_finalize_launch).
+struct DwGroupMember {
+    rnn_conv_spec sp;
+    const float *dy = nullptr, *x = nullptr;
+    float *slabs = nullptr;
+    int nz = 0;
+};
+struct DwGroupLaunch {
+    const void *kern = nullptr;
+    size_t lds = 0;
+    int threads = 0, njobs = 0, count = 0;
+    size_t table_bytes = 0;
+    void *table = nullptr;
+    std::vector<std::vector<unsigned char>> conv;  // per member: its plan (host)
+    std::vector<uint32_t> jobs;                    // conv | z << 8 | cob << 20 | cib << 26
+};
+int rnn_conv_dw_group_plan(rnn_ctx *ctx, size_t n, DwGroupMember *m, int count,
+                           DwGroupLaunch *L);
+int rnn_conv_dw_group_upload(rnn_ctx *ctx, const DwGroupMember *m, DwGroupLaunch *L);
+int rnn_conv_dw_group_launch(rnn_ctx *ctx, const DwGroupLaunch *L);
+
 // ResNet layer launchers (nn.hip).  One BatchNorm2d layer's device state:
 struct RnnBn {
     const double *part = nullptr;  // train: [c][P][2] partial sums of the layer input
