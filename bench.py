@@ -8,18 +8,21 @@ Headline (`value`, images/s): BASELINE config 3, the full ResNet-20 (W=32)
 train step at batch 128 on 32x32 synthetic images -- forward, softmax
 cross-entropy (smoothing 0.1), backward and the Nesterov SGD step (lr 0.2,
 momentum 0.9, wd 5e-4) -- through the device-resident runtime (rnn_resnet_*,
-issued eagerly on two streams: the weight gradients run on a second stream
-beside the input-gradient chain), every operand resident in HBM.  One "step"
+issued eagerly; the 3x3 stride-1 weight gradients in one grouped launch
+after the input-gradient chain, the others on a second stream beside it),
+every operand resident in HBM.  One "step"
 is one train step on one batch; `value` = steps * 128 / timed seconds.
 
 Also reported:
-  * `roofline`: the kernel with the largest share of the ResNet step: its
-    algorithmic FLOP per launch / its average launch duration in the
-    committed rocprofv3 kernel trace (profiles/conv_sweep_kernel_stats.md)
-    vs the 157.3 TFLOP/s fp32 MFMA peak (`frac`); the same kernel timed live
-    with HIP events on the library's stream beside it (`live`); `traffic`
-    from the committed rocprofv3 --pmc summary and `traffic_ratio` = that
-    traffic / the op's algorithmic bytes;
+  * `roofline`: the kernel template with the most launch time per ResNet
+    step (`candidates` lists them all): its algorithmic FLOP per launch / its
+    average launch duration in the committed rocprofv3 kernel trace
+    (profiles/resnet20_step_kernel_stats.md for the step's grouped dW launch,
+    profiles/conv_sweep_kernel_stats.md for a sweep op) vs the 157.3 TFLOP/s
+    fp32 MFMA peak (`frac`); the same kernel timed live with HIP events on
+    the library's stream beside it (`live`); `traffic` from the committed
+    rocprofv3 --pmc summary and `traffic_ratio` = that traffic / the kernel's
+    algorithmic bytes;
   * `cpu_baseline`: the restated reference CPU path (oracle/, AVX2 micro-kernel,
     OpenMP) running the same ResNet-20 train step on this host's cores for a
     bounded number of steps;
@@ -120,6 +123,67 @@ def op_bytes(op):
         if ps in ("dw", "dw_kernel"):
             return 4 * (yo + xin + w)
     return None
+
+
+def step_profile_avg(template):
+    """Average duration (us) of kernel `template` in the committed kernel
+    trace of the ResNet step (profiles/resnet20_step_kernel_stats.md), or
+    None."""
+    path = os.path.join(ROOT, "profiles", "resnet20_step_kernel_stats.md")
+    if not os.path.exists(path):
+        return None
+    for ln in open(path):
+        cells = [c.strip().strip("`") for c in ln.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == template:
+            try:
+                return float(cells[3])
+            except ValueError:
+                return None
+    return None
+
+
+def step_profile_traffic(template):
+    """HBM bytes per launch of kernel `template` of the ResNet step from the
+    committed rocprofv3 --pmc summary profiles/resnet20_dw_group_hbm_traffic.md
+    (FETCH_SIZE + WRITE_SIZE, scaled as recorded there), or None."""
+    path = os.path.join(ROOT, "profiles", "resnet20_dw_group_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for ln in open(path):
+        cells = [c.strip().strip("`") for c in ln.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == template:
+            try:
+                return float(cells[4]) * 1024
+            except ValueError:
+                return None
+    return None
+
+
+DW_GROUP_TEMPLATE = "conv_dw_group_kernel<3, 1, 0, 2>"
+
+
+def step_profile_table():
+    """[(kernel template, us per step)] of the committed kernel trace of the
+    ResNet step (profiles/resnet20_step_kernel_stats.md), most time first."""
+    path = os.path.join(ROOT, "profiles", "resnet20_step_kernel_stats.md")
+    out = []
+    if not os.path.exists(path):
+        return out
+    for ln in open(path):
+        cells = [c.strip().strip("`") for c in ln.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] != "kernel":
+            try:
+                out.append((cells[0], float(cells[2])))
+            except ValueError:
+                pass
+    return sorted(out, key=lambda t: -t[1])
+
+
+def template_base(t):
+    """A conv_fast_kernel template without its last argument (the store-pass
+    statistics flag: the step's forward convs take the batch statistics in
+    the store pass, the sweep's forward ops do not), else t."""
+    return t.rsplit(",", 1)[0] if t.startswith("conv_fast_kernel<") else t
 
 
 def profile_kernels(op):
@@ -738,8 +802,9 @@ def resnet_inputs_gpu(n, seed):
     return x, labels
 
 
-def bench_resnet(R, ctx, steps, warmup):
-    """Config 3: the ResNet-20 train step through rnn_resnet_train_step."""
+def bench_resnet(R, ctx, steps, warmup, time_group=True):
+    """Config 3: the ResNet-20 train step through rnn_resnet_train_step
+    (and, with time_group, the step's grouped dW launch alone)."""
     import torch
     from rustnn_amd.model import ResNet
     c = RESNET
@@ -772,6 +837,15 @@ def bench_resnet(R, ctx, steps, warmup):
     out = {"ms": ms, "images_s": c["batch"] / (ms * 1e-3), "wall": wall, "graph": graph,
            "graph_note": why, "flop_per_image": flop_img,
            "loss": float(loss.item()), "params": net.num_params()}
+    # The step's grouped weight-gradient launch (every 3x3 stride-1 conv's dW
+    # in one persistent kernel) timed alone: graph replays of back-to-back
+    # launches over the buffers the last backward left, HIP events on the
+    # library's stream.
+    gfl = net.dw_group(launch=False)
+    if gfl and time_group:
+        net.dw_group()
+        torch.cuda.synchronize()
+        out["dw_group"] = {"flops": gfl, "ms": time_graph(ctx, lambda: net.dw_group(), 10)}
     net.close()
     return out
 
@@ -810,7 +884,7 @@ def main():
     ctx = R.default_ctx(0)
 
     if args.resnet_only:
-        r = bench_resnet(R, ctx, args.resnet_only, 2)
+        r = bench_resnet(R, ctx, args.resnet_only, 2, time_group=False)
         print(json.dumps({"resnet_only": args.resnet_only, "ms": r["ms"]}))
         return
     if args.attn_only:
@@ -947,30 +1021,91 @@ def main():
         return out
 
     lay = {L["name"]: L for L in layers}
-    # Dominant kernel of the ResNet step: the kernel template (from the
-    # committed kernel trace's op -> kernel table) with the largest
-    # multiplicity x duration over all the ops the step launches it for
-    # (forward, dX, dW kernel); its roofline row is the op of that template
-    # with the most launch time.
+    # Dominant kernel of the ResNet step: the kernel template with the most
+    # launch time per step.  Candidates: the conv kernel templates of the
+    # sweep ops the step launches (forward, dX, and the dW kernel of the
+    # shapes without a grouped launch) with their multiplicity in the step,
+    # and the step's grouped weight-gradient launch (one per step, timed
+    # alone above).  A sweep template's roofline row is its op with the most
+    # launch time.
     conv_ops = [r for r in per_op if "tflops" in r]
-    step_kernels = [r for r in conv_ops if not r["op"].endswith(":dw")]
+    grouped = set()
+    if rn.get("dw_group"):
+        grouped = {L["name"] for L in layers if L["sp"].k == 3 and L["sp"].stride == 1}
+    step_kernels = [r for r in conv_ops if not r["op"].endswith(":dw") and
+                    not (r["op"].endswith(":dw_kernel") and r["op"].split(":")[0] in grouped)]
     tmpl = {r["op"]: (profile_kernels(r["op"]) or [(r["op"], 0)])[0][0] for r in step_kernels}
     by_t = {}
     for r in step_kernels:
         by_t.setdefault(tmpl[r["op"]], []).append(r)
-    t_dom = max(by_t, key=lambda t: sum(r["ms"] * r["in_resnet_step"] for r in by_t[t]))
-    rows_t = by_t[t_dom]
-    dom = max(rows_t, key=lambda r: r["ms"] * r["in_resnet_step"])
-    roof = roofline(dom, lay[dom["op"].split(":")[0]]["flops"])
-    t_ms = sum(r["ms"] * r["in_resnet_step"] for r in rows_t)
-    t_fl = sum(lay[r["op"].split(":")[0]]["flops"] * r["in_resnet_step"] for r in rows_t)
-    roof["share_of_resnet_step"] = round(t_ms / rn["ms"], 4)
-    roof["template_launches_per_step"] = sum(r["in_resnet_step"] for r in rows_t)
-    roof["template_ops"] = [r["op"] for r in rows_t]
-    roof["template_frac"] = round(t_fl / (t_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)
-    roof["share_note"] = ("launch time of every launch of the template per step / step time; "
-                          "the step runs weight gradients on a second stream, so kernels "
-                          "overlap and shares of different kernels can sum past 1")
+    # The dominant template is the one with the most kernel time per step in
+    # the committed kernel trace of the step itself; without that file, the
+    # live timings of each kernel alone times its launches per step decide.
+    cands = {t: sum(r["ms"] * r["in_resnet_step"] for r in by_t[t]) for t in by_t}
+    if rn.get("dw_group"):
+        cands[DW_GROUP_TEMPLATE] = rn["dw_group"]["ms"]
+    step_tab = step_profile_table()
+    t_dom = None
+    if step_tab:
+        top = step_tab[0][0]
+        if top == DW_GROUP_TEMPLATE and rn.get("dw_group"):
+            t_dom = top
+        else:
+            t_dom = next((t for t in by_t if template_base(t) == template_base(top)), None)
+    if t_dom is None:
+        t_dom = max(cands, key=lambda t: cands[t])
+    candidates = {"step_trace_us_per_step": [{"template": t, "us_per_step": v}
+                                             for t, v in step_tab[:8]],
+                  "live_ms_per_step": [{"template": t, "ms_per_step": round(v, 5)}
+                                       for t, v in sorted(cands.items(), key=lambda kv: -kv[1])]}
+
+    def group_roofline():
+        gf, gms = rn["dw_group"]["flops"], rn["dw_group"]["ms"]
+        live_tf = gf / (gms * 1e-3) / 1e12
+        us = step_profile_avg(DW_GROUP_TEMPLATE)
+        if us:
+            achieved, src = gf / (us * 1e-6) / 1e12, "profiles/resnet20_step_kernel_stats.md"
+        else:
+            us, achieved, src = gms * 1e3, live_tf, "live (kernel not in the step trace)"
+        members = [(L["name"], RESNET_OPS[L["name"]]) for L in layers if L["name"] in grouped]
+        alg = sum(m * op_bytes(f"{nm}:dw_kernel") for nm, m in members)
+        traffic = step_profile_traffic(DW_GROUP_TEMPLATE)
+        return {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                "traffic": traffic,
+                "traffic_ratio": round(traffic / alg, 3) if traffic and alg else None,
+                "algorithmic_bytes": alg, "kernel": "resnet step: grouped dW of " +
+                ", ".join(f"{nm} x{m}" for nm, m in members),
+                "template": DW_GROUP_TEMPLATE, "flop_per_launch": gf, "avg_launch_us": us,
+                "source": src,
+                "live": {"achieved": round(live_tf, 3),
+                         "frac": round(live_tf / PEAK_FP32_MFMA_TFLOPS, 4),
+                         "avg_launch_ms": round(gms, 5),
+                         "timing": "graph replays of 10 back-to-back launches over the last "
+                                   "backward's buffers (rnn_dbg_resnet_dw_group), HIP events "
+                                   "on the library's stream"},
+                "share_of_resnet_step": round(gms / rn["ms"], 4),
+                "template_launches_per_step": 1}
+
+    if t_dom == DW_GROUP_TEMPLATE:
+        roof = group_roofline()
+    else:
+        rows_t = by_t[t_dom]
+        dom = max(rows_t, key=lambda r: r["ms"] * r["in_resnet_step"])
+        roof = roofline(dom, lay[dom["op"].split(":")[0]]["flops"])
+        t_ms = sum(r["ms"] * r["in_resnet_step"] for r in rows_t)
+        t_fl = sum(lay[r["op"].split(":")[0]]["flops"] * r["in_resnet_step"] for r in rows_t)
+        roof["share_of_resnet_step"] = round(t_ms / rn["ms"], 4)
+        roof["template_launches_per_step"] = sum(r["in_resnet_step"] for r in rows_t)
+        roof["template_ops"] = [r["op"] for r in rows_t]
+        roof["template_frac"] = round(t_fl / (t_ms * 1e-3) / 1e12 / PEAK_FP32_MFMA_TFLOPS, 4)
+        if template_base(t_dom) != t_dom:
+            roof["step_template_note"] = (
+                "the step runs this kernel with the batch statistics taken in its store pass "
+                "(last template argument 1); the sweep op above runs it without them")
+    roof["candidates"] = candidates
+    roof["share_note"] = ("launch time of every launch of the template per step / step time "
+                          "(live timings of each kernel alone)")
     sdom = max(step_kernels, key=lambda r: r["ms"])
     sweep_roof = roofline(sdom, lay[sdom["op"].split(":")[0]]["flops"])
     ones = bench_1x1_rotated(R, ctx, layers, run_op, args.op_reps)
@@ -1016,6 +1151,8 @@ def main():
                    "model_frac_of_fp32_mfma_peak": round(model_tf / PEAK_FP32_MFMA_TFLOPS, 4),
                    "hip_graph": rn["graph"], "wall_s_timed": round(rn["wall"], 3)},
         "roofline": roof, "cpu_baseline": cpu,
+        "roofline_dw_group": (group_roofline() if rn.get("dw_group") and
+                              t_dom != DW_GROUP_TEMPLATE else None),
         "vs_cpu_baseline": round(rn["images_s"] / cpu["value"], 1) if cpu else None,
         "config1_conv_sweep": {
             "value": round(sweep_tf, 3), "unit": "TFLOP/s", "ms_per_step": round(sweep_ms, 4),

@@ -645,6 +645,14 @@ uint64_t rnn_resnet_flops(const rnn_resnet *net, size_t h, size_t w);
  * *len: floats. */
 int rnn_dbg_resnet_buffer(rnn_resnet *net, size_t block, int which, const float **ptr,
                           size_t *len);
+/* The grouped weight-gradient launch(es) of the train step (every 3x3
+ * stride-1 conv's dW in one persistent launch), enqueued once more on the
+ * context's stream over the buffers the last backward left (its output
+ * gradients and activations; the slabs are rewritten with the same values),
+ * when `launch` is set.  *flops: the launch's algorithmic FLOP (0 when the
+ * current plan has no grouped launch).  No counterpart in the reference: it
+ * exists to time that kernel alone (benchmarks). */
+int rnn_dbg_resnet_dw_group(rnn_resnet *net, int launch, double *flops);
 int rnn_dbg_im2col(rnn_ctx *ctx, const rnn_conv_spec *sp, const float *x_img, float *col);
 /* PackedA::pack / pack_t (gemm.rs:54-113) into out[nb*256*mpad] (positions the
  * reference never writes are left untouched). */

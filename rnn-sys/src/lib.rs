@@ -211,6 +211,7 @@ extern "C" {
     pub fn rnn_resnet_graph_state(net: *const rnn_resnet, why: *mut *const c_char) -> c_int;
     pub fn rnn_resnet_flops(net: *const rnn_resnet, h: usize, w: usize) -> u64;
     pub fn rnn_dbg_resnet_buffer(net: *mut rnn_resnet, block: usize, which: c_int, ptr: *mut *const f32, len: *mut usize) -> c_int;
+    pub fn rnn_dbg_resnet_dw_group(net: *mut rnn_resnet, launch: c_int, flops: *mut f64) -> c_int;
     pub fn rnn_dbg_im2col(ctx: *mut rnn_ctx, sp: *const rnn_conv_spec, x_img: *const f32, col: *mut f32) -> c_int;
     pub fn rnn_dbg_pack_a(ctx: *mut rnn_ctx, a: *const f32, m: usize, k: usize, transposed: c_int, out: *mut f32) -> c_int;
     pub fn rnn_dbg_pack_b(ctx: *mut rnn_ctx, b: *const f32, n: usize, k: usize, transposed: c_int, out: *mut f32) -> c_int;

@@ -151,6 +151,7 @@ def lib():
             "rnn_linear_backward_host": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
                                               _vp]),
             "rnn_dbg_resnet_buffer": (_i, [_vp, _sz, _i, P(_vp), P(_sz)]),
+            "rnn_dbg_resnet_dw_group": (_i, [_vp, _i, P(C.c_double)]),
             "rnn_dbg_im2col": (_i, [_vp, P(ConvSpec), _vp, _vp]),
             "rnn_dbg_pack_a": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),
             "rnn_dbg_pack_b": (_i, [_vp, _vp, _sz, _sz, _i, _vp]),

@@ -1265,6 +1265,22 @@ int rnn_dbg_resnet_buffer(rnn_resnet *r, size_t block, int which, const float **
     return RNN_OK;
 }
 
+int rnn_dbg_resnet_dw_group(rnn_resnet *r, int launch, double *flops) {
+    if (!r || !flops) return RNN_E_NULL;
+    *flops = 0;
+    if (!r->arena) return rnn_fail(r->ctx, RNN_E_INVALID, "dbg_resnet_dw_group: no plan yet");
+    for (auto &G : r->dwgs) {
+        if (!G.L.njobs) continue;
+        for (auto &m : G.m)
+            *flops += 2.0 * m.sp.cout * m.sp.cin * m.sp.k * m.sp.k * m.sp.oh * m.sp.ow * (double)r->n;
+    }
+    if (!launch) return RNN_OK;
+    rnn_ctx *ctx = r->ctx;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    for (auto &G : r->dwgs) TRY(rnn_conv_dw_group_launch(ctx, &G.L));
+    return RNN_OK;
+}
+
 uint64_t rnn_resnet_flops(const rnn_resnet *r, size_t h, size_t w) {
     // ResNet::flops (model.rs:179-198): forward FLOP per image.
     if (!r) return 0;

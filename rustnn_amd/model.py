@@ -141,6 +141,14 @@ class ResNet:
         dev = torch.device("cuda", self.device)
         return torch.as_tensor(_DevArray(p.value, (n.value,), "<f4"), device=dev).clone()
 
+    def dw_group(self, launch=True):
+        """The algorithmic FLOP of the step's grouped weight-gradient launch,
+        enqueued once more over the last backward's buffers when `launch`
+        (rnn_dbg_resnet_dw_group; 0.0 without a grouped launch)."""
+        f = C.c_double()
+        self.ctx.check(lib().rnn_dbg_resnet_dw_group(self.h, int(bool(launch)), C.byref(f)))
+        return f.value
+
     def set_graph(self, on):
         self.ctx.check(lib().rnn_resnet_set_graph(self.h, int(bool(on))))
 
