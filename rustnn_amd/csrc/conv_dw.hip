@@ -200,8 +200,8 @@ struct DwOps {
     float4 a;                                   // dY: pixels 4h .. 4h+3
     float4 x0[K];                               // X: 4 values from 4h (even part for S = 2)
     float2 x1[K];                               // X: the 2 values after them (X4: before them)
-    float4 xo[(K == 3 && S == 2) ? K : 1];      // X odd columns (stride-2 3x3)
-    float xr[X4 ? K : 1];                       // X4: the value after x1's pair
+    float4 xo[(K == 3 && S == 2) ? K : 1];      // X odd columns (stride-2 3x3; X4: next 4)
+    float xr[X4 ? K : 1];                       // X4: one more value (see dw_fetch)
 };
 
 template <int K, int S, bool X4>
@@ -214,16 +214,22 @@ __device__ __forceinline__ void dw_fetch(const DwArgs &g, const float *__restric
     const int rr = (int)fdiv((uint32_t)grp, g.fd_gpr), cq = grp - rr * g.gpr;
     const int img = (int)fdiv((uint32_t)rr, g.fd_tr), r = rr - img * g.TR;
     o.a = *reinterpret_cast<const float4 *>(ds + l32 * g.chsd + 8 * grp + 4 * h);
-    const float *xr =
-        xs + l32 * g.chsx + img * g.ximg + r * g.xrow * g.TIWP + 8 * cq + 4 * h;
+    const float *xr = xs + l32 * g.chsx + img * g.ximg + r * g.xrow * g.TIWP +
+                      (X4 && S == 2 ? 16 * cq + 8 * h : 8 * cq + 4 * h);
 #pragma unroll
     for (int kh = 0; kh < K; kh++) {
-        if constexpr (X4) {
+        if constexpr (X4 && S == 1) {
             // pixels ox0 = 8cq + 4h .. +3 read x = ox0 - 1 .. ox0 + 4, stored
             // at row column x + 4: x = ox0 - 2, ox0 - 1 / ox0 .. ox0 + 3 / ox0 + 4
             o.x1[kh] = *reinterpret_cast<const float2 *>(xr + kh * g.TIWP + 2);
             o.x0[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP + 4);
             o.xr[kh] = xr[kh * g.TIWP + 8];
+        } else if constexpr (X4) {
+            // stride 2: pixels ox0 .. ox0 + 3 read x = 2ox0 - 1 .. 2ox0 + 7:
+            // 2ox0 - 1 / 2ox0 .. +3 / 2ox0 + 4 .. +7 at row column x + 4
+            o.xr[kh] = xr[kh * g.TIWP + 3];
+            o.x0[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP + 4);
+            o.xo[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP + 8);
         } else {
             o.x0[kh] = *reinterpret_cast<const float4 *>(xr + kh * g.TIWP);
             if constexpr (K == 3) {
@@ -241,9 +247,12 @@ template <int K, int S, bool X4>
 __device__ __forceinline__ float dw_bval(const DwOps<K, S, X4> &o, int kh, int kw, int i) {
     if constexpr (K == 1) {
         return o.x0[0][i];
-    } else if constexpr (X4) {
+    } else if constexpr (X4 && S == 1) {
         const int v = kw + i;  // x = ox0 - 1 + v
         return v == 0 ? o.x1[kh].y : (v < 5 ? o.x0[kh][v - 1] : o.xr[kh]);
+    } else if constexpr (X4) {
+        const int t = 2 * i + kw - 1;  // x = 2ox0 + t, t = -1 .. 7
+        return t < 0 ? o.xr[kh] : (t < 4 ? o.x0[kh][t] : o.xo[kh][t - 4]);
     } else if constexpr (S == 1) {
         const int v = kw + i;  // compile-time after unrolling
         return v < 4 ? o.x0[kh][v] : (v == 4 ? o.x1[kh].x : o.x1[kh].y);
@@ -275,19 +284,27 @@ __device__ __forceinline__ void dw_issue_tile(const DwArgs &g, const DwLane<MT> 
 // per-row address arithmetic.  Chunks without source data (padding columns,
 // padding rows, the odd-stride filler, channels past the convolution's) take
 // an offset past every buffer and are written as zeros.
-constexpr int DW4_XK = 11;  // X instructions per producer wave, at most
+// X instructions per producer wave, at most: stride-2 windows hold about
+// twice the rows (fewer table registers for stride 1 measured faster)
+template <int S>
+constexpr int dw4_xk() {
+    return S == 1 ? 11 : 13;
+}
 constexpr int DW4_DK = 5;   // dY instructions per producer wave, at most
 
+template <int S>
 struct DwLane4 {
-    uint32_t xo[4][DW4_XK];  // window kind (bit 0: no first row, bit 1: no last row)
+    static constexpr int XK = dw4_xk<S>();
+    uint32_t xo[4][XK];  // window kind (bit 0: no first row, bit 1: no last row)
     uint32_t dof[DW4_DK];
 };
 
-__device__ __forceinline__ void dw_lane4_init(const DwArgs &g, DwLane4 &L, int pw, int lane,
+template <int S>
+__device__ __forceinline__ void dw_lane4_init(const DwArgs &g, DwLane4<S> &L, int pw, int lane,
                                               int cob, int cib) {
     const int rpi = g.TIH * g.rch;  // X chunks of one image's window
 #pragma unroll
-    for (int kk = 0; kk < DW4_XK; kk++) {
+    for (int kk = 0; kk < DwLane4<S>::XK; kk++) {
         const int k = pw + DW_NP * kk;
         const int q = 64 * k + lane;
         const int c = q / g.xchunks, r = q - c * g.xchunks;
@@ -321,12 +338,13 @@ __device__ __forceinline__ void dw_lane4_init(const DwArgs &g, DwLane4 &L, int p
 // a0 + TR <= OH).  The descriptors start at the tile's first image row that
 // the window reads (X) and at its first output row (dY) and end with the
 // tile's last image, so every chunk with source data lies inside them.
-__device__ __forceinline__ void dw_issue_tile4(const DwArgs &g, const DwLane4 &L, int tile,
+template <int S>
+__device__ __forceinline__ void dw_issue_tile4(const DwArgs &g, const DwLane4<S> &L, int tile,
                                                int cob, int cib, float *__restrict__ buf, int pw) {
     if (tile >= g.ntiles) return;
     const int n0 = (tile / g.tiles_a) * g.IMGS, a0 = (tile % g.tiles_a) * g.TR;
-    const int y0 = a0 - g.pad;
-    const int kind = (y0 < 0 ? 1 : 0) | (a0 + g.TR >= g.OH ? 2 : 0);
+    const int y0 = a0 * g.S - g.pad;
+    const int kind = (y0 < 0 ? 1 : 0) | (y0 + g.TIH - 1 >= g.H ? 2 : 0);
     const long long xend = (long long)(n0 + g.IMGS) * g.cihw;
     const long long xo = (long long)n0 * g.cihw + (long long)cib * 32 * g.hw +
                          (long long)max(y0, 0) * g.W;
@@ -337,7 +355,7 @@ __device__ __forceinline__ void dw_issue_tile4(const DwArgs &g, const DwLane4 &L
     auto issue_x = [&](auto wc) {
         constexpr int w = decltype(wc)::value;
 #pragma unroll
-        for (int kk = 0; kk < DW4_XK; kk++)
+        for (int kk = 0; kk < DwLane4<S>::XK; kk++)
             if (pw + DW_NP * kk < g.nix)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     rx, (lds_ptr_t)(buf + (pw + DW_NP * kk) * 256), 16, L.xo[w][kk], 0, 0, 0);
@@ -481,12 +499,12 @@ __device__ __forceinline__ void dw_mfma_wave(const DwArgs &g, float *smem, float
 // back-pressure never stalls an MFMA wave.  Double-buffered plans (NB = 2)
 // stage the next tile while this one is computed (one barrier per tile);
 // single-buffered plans stage it after the compute barrier.
-// MT = 0: the 16-byte staging of a 3x3 stride-1 pad-1 plan (whole tiles).
+// MT = 0: the 16-byte staging of a 3x3 pad-1 plan (whole tiles).
 template <int K, int S, int MT, int NB>
 __device__ __forceinline__ void dw_body(const DwArgs &g, int z, int cob, int cib) {
     constexpr int KK = K * K, NG = dw_tap_groups<K>(), NMW = DW_NW * NG;
     constexpr bool X4 = MT == 0;
-    static_assert(!X4 || (K == 3 && S == 1 && NB == 2), "16-byte staging: 3x3 stride 1, two buffers");
+    static_assert(!X4 || (K == 3 && NB == 2), "16-byte staging: 3x3, two buffers");
     extern __shared__ float smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = wave_index();
     float *red = smem;  // after the tiles: 2 slices of [32][32][KK]
@@ -496,14 +514,15 @@ __device__ __forceinline__ void dw_body(const DwArgs &g, int z, int cob, int cib
         // with a single buffer), then those of the reduction
         const int pw = wave - NMW;
         if constexpr (X4) {
-            DwLane4 L;
-            dw_lane4_init(g, L, pw, lane, cob, cib);
-            dw_issue_tile4(g, L, z, cob, cib, smem, pw);
+            DwLane4<S> L;
+            dw_lane4_init<S>(g, L, pw, lane, cob, cib);
+            dw_issue_tile4<S>(g, L, z, cob, cib, smem, pw);
             int s = 0;
             for (int tile = z; tile < g.ntiles; tile += g.nz, s++) {
                 dma_wait_barrier();
                 if (tile + g.nz < g.ntiles)
-                    dw_issue_tile4(g, L, tile + g.nz, cob, cib, smem + ((s + 1) & 1) * g.stage, pw);
+                    dw_issue_tile4<S>(g, L, tile + g.nz, cob, cib, smem + ((s + 1) & 1) * g.stage,
+                                      pw);
             }
         } else {
             DwLane<MT> L;
@@ -786,12 +805,13 @@ size_t dw_geometry(DwArgs &g, int K, int TR, int IMGS, int nbuf) {
     return std::max((size_t)nbuf * g.stage * 4, (size_t)(DW_NW / 2) * K * K * 1024 * 4);
 }
 
-// Geometry of a (TR, IMGS) tile of the 16-byte staging (3x3 stride 1 pad
-// 1, W = OW a multiple of 8, whole tiles); returns LDS bytes, 0 if the shape
-// or tile does not qualify.
+// Geometry of a (TR, IMGS) tile of the 16-byte staging (3x3 pad 1, stride 1
+// or 2 with W = S*OW and H = S*OH, OW a multiple of 8, whole tiles); returns
+// LDS bytes, 0 if the shape or tile does not qualify.  A stride-2 window
+// holds 2 TR + 1 image rows (the last one always inside the image).
 size_t dw_geometry4(DwArgs &g, int TR, int IMGS, size_t n) {
-    if (g.S != 1 || g.pad != 1 || g.W != g.OW || g.H != g.OH || (g.OW & 7) || g.OH % TR ||
-        (long long)n % IMGS)
+    if ((g.S != 1 && g.S != 2) || g.pad != 1 || g.W != g.S * g.OW || g.H != g.S * g.OH ||
+        (g.OW & 7) || (g.W & 3) || g.OH % TR || (long long)n % IMGS)
         return 0;
     g.nbuf = 2;
     g.TR = TR;
@@ -799,11 +819,11 @@ size_t dw_geometry4(DwArgs &g, int TR, int IMGS, size_t n) {
     g.OWP = g.OW;
     g.gpr = g.OW / 8;
     g.ngroups = IMGS * TR * g.gpr;
-    g.xrow = 1;
+    g.xrow = g.S;
     g.xstep = 1;
-    g.TIH = TR + 2;
+    g.TIH = (TR - 1) * g.S + 3;
     g.HE = 0;
-    g.rch = g.OW / 4 + 2;
+    g.rch = g.W / 4 + 2;
     g.TIWP = 4 * g.rch;
     g.ximg = g.TIH * g.TIWP;
     g.dimg = TR * g.OW;
@@ -819,7 +839,8 @@ size_t dw_geometry4(DwArgs &g, int TR, int IMGS, size_t n) {
     g.dchunks = g.ddata | 1;
     g.nix = (32 * g.xchunks + 63) / 64;
     g.nid = (32 * g.dchunks + 63) / 64;
-    if (g.nix > DW_NP * DW4_XK || g.nid > DW_NP * DW4_DK || IMGS > 127) return 0;
+    const int xk = g.S == 1 ? dw4_xk<1>() : dw4_xk<2>();
+    if (g.nix > DW_NP * xk || g.nid > DW_NP * DW4_DK || IMGS > 127) return 0;
     g.mx = g.md = 0;
     g.chsx = 4 * g.xchunks;
     g.chsd = 4 * g.dchunks;
@@ -855,7 +876,6 @@ template <int S, int MT>
 const void *dw_group_ptr() {
     static bool attr = false;
     const void *k = (const void *)conv_dw_group_kernel<3, S, MT, 2>;
-    static_assert(MT > 0 || S == 1, "16-byte staging: stride 1");
     if (!attr) {
         attr = true;
         (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
@@ -872,6 +892,7 @@ const void *dw_group_pick(int s, int mt) {
         if (mt <= DW_MT[1]) return dw_group_ptr<1, DW_MT[1]>();
         return dw_group_ptr<1, DW_MT[2]>();
     }
+    if (mt == 0) return dw_group_ptr<2, 0>();
     if (mt <= DW_MT[0]) return dw_group_ptr<2, DW_MT[0]>();
     if (mt <= DW_MT[1]) return dw_group_ptr<2, DW_MT[1]>();
     return dw_group_ptr<2, DW_MT[2]>();
@@ -996,7 +1017,8 @@ static int dw_plan(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float 
     const int ncb = (g.CO + 31) / 32, ncib = (g.CI + 31) / 32;
     auto kernel_of = [&](const DwArgs &a) -> const void * {
         const int mt = std::max(a.mx, a.md);
-        if (K == 3 && mt == 0) return dw_kernel_ptr<3, 1, 0, 2>();  // 16-byte staging
+        if (K == 3 && mt == 0)  // 16-byte staging
+            return a.S == 1 ? dw_kernel_ptr<3, 1, 0, 2>() : dw_kernel_ptr<3, 2, 0, 2>();
         if (K == 3)
             return a.S == 1 ? dw_pick<3, 1>(mt, a.nbuf) : dw_pick<3, 2>(mt, a.nbuf);
         return a.S == 1 ? dw_pick<1, 1>(mt, a.nbuf) : dw_pick<1, 2>(mt, a.nbuf);

@@ -561,8 +561,9 @@ class BasicBlock:
         return y
 
     def backward(self, d):
+        """BasicBlock::backward (model.rs:56-71); like the reference, which
+        takes d by value, it masks d in place (d is overwritten)."""
         from .nn import add_, relu_back_
-        d = d.clone()
         relu_back_(d, self.out, self.ctx)
         dmain = self.b.backward(d)
         dx = self.a.backward(dmain, self.h1)
