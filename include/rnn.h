@@ -222,6 +222,14 @@ int rnn_linear_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const
  * be NULL); dx = dy W (overwritten). */
 int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
                         const float *x, const float *w, float *dw, float *db, float *dx);
+/* rnn_linear_backward with dx accumulated instead of overwritten when flags
+ * has RNN_LINEAR_ACC_DX: dx += dy W, the old value first, as add_ (nn.rs:441-443)
+ * of a separately computed dx.  Block::backward (vit.rs:175-232) sums its
+ * branches' input gradients this way without a separate pass. */
+#define RNN_LINEAR_ACC_DX 1u
+int rnn_linear_backward_ex(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
+                           const float *x, const float *w, float *dw, float *db, float *dx,
+                           uint32_t flags);
 
 /* ------------------------------------------ host-slice forms (Rust shim) */
 /* The same entry points over HOST memory, for the Rust shim, whose callers
@@ -379,6 +387,22 @@ int rnn_dwconv3_forward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, 
                         const float *w, const float *b, float *y);
 int rnn_dwconv3_backward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, const float *dy,
                          const float *x, const float *w, float *dx, float *dw, float *db);
+/* rnn_dwconv3_backward with dx accumulated (dx += the input gradient, the old
+ * value first) when flags has RNN_DW3_ACC_DX; dx must not be dy. */
+#define RNN_DW3_ACC_DX 1u
+int rnn_dwconv3_backward_ex(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c,
+                            const float *dy, const float *x, const float *w, float *dx, float *dw,
+                            float *db, uint32_t flags);
+/* Block::forward's first branch (vit.rs:150-160) in one pass: d =
+ * DwConv3(h) as rnn_dwconv3_forward computes it; a += gamma d (rnn_axpy_cols);
+ * y = x + (a l) m, m = mask[image] (mask may be NULL; rnn_residual_add_scaled
+ * with th * tw rows per image).  h, a, x, y, d are [n][th][tw][c]; gamma, l
+ * [c]; a is updated in place and y may be x; d, a, h and y are distinct, and x
+ * is not a. */
+int rnn_dwconv3_branch_forward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c,
+                               const float *h, const float *w, const float *b, float *d, float *a,
+                               const float *gamma, const float *x, const float *l,
+                               const float *mask, float *y);
 /* SeqPool (norm.rs:459-586): w = softmax_t(x p), z = sum_t w_t x_t; z [n][c];
  * the forward writes the softmax weights w [n][t] that the backward reads.
  * t <= 1024. */

@@ -11,6 +11,8 @@ pub const RNN_E_NOMEM: c_int = -4;
 pub const RNN_E_UNSUPPORTED: c_int = -5;
 pub const RNN_ATTN_SET_DQ: u32 = 1;
 pub const RNN_ATTN_SET_DKV: u32 = 2;
+pub const RNN_LINEAR_ACC_DX: u32 = 1;
+pub const RNN_DW3_ACC_DX: u32 = 1;
 
 #[repr(C)] pub struct rnn_ctx { _p: [u8; 0] }
 #[repr(C)] pub struct rnn_optim { _p: [u8; 0] }
@@ -121,6 +123,7 @@ extern "C" {
     pub fn rnn_attn_backward_ex(ctx: *mut rnn_ctx, d: *const rnn_attn_desc, n: usize, q: *const f32, kv: *const f32, tau: *const f32, p: *const f32, dout: *const f32, dq: *mut f32, dkv: *mut f32, dtau: *mut f32, drel: *mut f32, flags: u32) -> c_int;
     pub fn rnn_linear_forward(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, x: *const f32, w: *const f32, b: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_linear_backward(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, dy: *const f32, x: *const f32, w: *const f32, dw: *mut f32, db: *mut f32, dx: *mut f32) -> c_int;
+    pub fn rnn_linear_backward_ex(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, dy: *const f32, x: *const f32, w: *const f32, dw: *mut f32, db: *mut f32, dx: *mut f32, flags: u32) -> c_int;
     pub fn rnn_matmul_host(ctx: *mut rnn_ctx, m: usize, n: usize, k: usize, a: *const f32, at: c_int, b: *const f32, bt: c_int, c: *mut f32, acc: c_int) -> c_int;
     pub fn rnn_gemm_small_batched_host(ctx: *mut rnn_ctx, count: usize, m: usize, n: usize, k: usize, a: *const f32, stride_a: usize, at: c_int, b: *const f32, stride_b: usize, bt: c_int, c: *mut f32, stride_c: usize, acc: c_int) -> c_int;
     pub fn rnn_matmul_dw_host(ctx: *mut rnn_ctx, m: usize, n: usize, k: usize, a: *const f32, b: *const f32, c: *mut f32) -> c_int;
@@ -154,6 +157,8 @@ extern "C" {
     pub fn rnn_swiglu_backward(ctx: *mut rnn_ctx, rows: usize, h: usize, du: *const f32, ab: *const f32, dab: *mut f32) -> c_int;
     pub fn rnn_dwconv3_forward(ctx: *mut rnn_ctx, n: usize, th: usize, tw: usize, c: usize, x: *const f32, w: *const f32, b: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_dwconv3_backward(ctx: *mut rnn_ctx, n: usize, th: usize, tw: usize, c: usize, dy: *const f32, x: *const f32, w: *const f32, dx: *mut f32, dw: *mut f32, db: *mut f32) -> c_int;
+    pub fn rnn_dwconv3_backward_ex(ctx: *mut rnn_ctx, n: usize, th: usize, tw: usize, c: usize, dy: *const f32, x: *const f32, w: *const f32, dx: *mut f32, dw: *mut f32, db: *mut f32, flags: u32) -> c_int;
+    pub fn rnn_dwconv3_branch_forward(ctx: *mut rnn_ctx, n: usize, th: usize, tw: usize, c: usize, h: *const f32, w: *const f32, b: *const f32, d: *mut f32, a: *mut f32, gamma: *const f32, x: *const f32, l: *const f32, mask: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_seqpool_forward(ctx: *mut rnn_ctx, n: usize, t: usize, c: usize, x: *const f32, p: *const f32, z: *mut f32, w: *mut f32) -> c_int;
     pub fn rnn_seqpool_backward(ctx: *mut rnn_ctx, n: usize, t: usize, c: usize, dz: *const f32, w: *const f32, x: *const f32, p: *const f32, dx: *mut f32, dp: *mut f32) -> c_int;
     pub fn rnn_soft_targets(ctx: *mut rnn_ctx, n: usize, nf: usize, nc: usize, labels: *const u32, coarse: *const u32, perm: *const u32, lam: *const f32, parent: *const u32, taxo: c_int, eps: f32, sib: f32, tf: *mut f32, tc: *mut f32) -> c_int;

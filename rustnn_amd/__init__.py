@@ -31,6 +31,8 @@ LIB_PATH = os.path.join(HERE, "librnn.so")
 HEADER = os.path.join(HERE, "..", "include", "rnn.h")
 
 RNN_OK, RNN_E_INVALID, RNN_E_NULL, RNN_E_HIP, RNN_E_NOMEM, RNN_E_UNSUPPORTED = 0, -1, -2, -3, -4, -5
+RNN_LINEAR_ACC_DX = 1  # rnn_linear_backward_ex
+RNN_DW3_ACC_DX = 1  # rnn_dwconv3_backward_ex
 
 _sz = C.c_size_t
 _vp = C.c_void_p
@@ -136,6 +138,8 @@ def lib():
                                           _vp, _vp, _vp, _u32]),
             "rnn_linear_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
             "rnn_linear_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_linear_backward_ex": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
+                                            _u32]),
             "rnn_matmul_host": (_i, [_vp, _sz, _sz, _sz, _vp, _i, _vp, _i, _vp, _i]),
             "rnn_gemm_small_batched_host": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _sz, _i, _vp,
                                                  _sz, _i, _vp, _sz, _i]),
@@ -236,6 +240,10 @@ def lib():
             "rnn_dwconv3_forward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
             "rnn_dwconv3_backward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
                                           _vp]),
+            "rnn_dwconv3_backward_ex": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
+                                             _vp, _u32]),
+            "rnn_dwconv3_branch_forward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
+                                                _vp, _vp, _vp, _vp, _vp]),
             "rnn_seqpool_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
             "rnn_seqpool_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_ema_update_params": (_i, [_vp, _sz, _vp, _vp, C.c_float]),
@@ -602,13 +610,17 @@ def linear_forward(rows, fin, fout, x, w, b=None, y=None, ctx=None):
     return y
 
 
-def linear_backward(rows, fin, fout, dy, x, w, dw, db=None, dx=None, ctx=None):
+def linear_backward(rows, fin, fout, dy, x, w, dw, db=None, dx=None, ctx=None, acc_dx=False):
+    """Linear::backward (linear.rs:66-96); acc_dx: dx (given) += dy W."""
     ctx = ctx or default_ctx()
+    if acc_dx and dx is None:
+        raise ValueError("linear_backward: acc_dx needs dx")
     dx = _new(rows * fin, dy) if dx is None else dx
-    ctx.check(lib().rnn_linear_backward(ctx.h, rows, fin, fout, _ptr(dy, rows * fout, "dy"),
-                                        _ptr(x, rows * fin, "x"), _ptr(w, fout * fin, "w"),
-                                        _ptr(dw, fout * fin, "dw"), _ptr(db, fout, "db"),
-                                        _ptr(dx, rows * fin, "dx")))
+    ctx.check(lib().rnn_linear_backward_ex(ctx.h, rows, fin, fout, _ptr(dy, rows * fout, "dy"),
+                                           _ptr(x, rows * fin, "x"), _ptr(w, fout * fin, "w"),
+                                           _ptr(dw, fout * fin, "dw"), _ptr(db, fout, "db"),
+                                           _ptr(dx, rows * fin, "dx"),
+                                           RNN_LINEAR_ACC_DX if acc_dx else 0))
     return dx
 
 
@@ -632,9 +644,10 @@ class Linear:
             self.x, self.rows = x, rows
         return y
 
-    def backward(self, dy):
+    def backward(self, dy, acc_dx=None):
+        """dx, or acc_dx += dx (returned) when given."""
         return linear_backward(self.rows, self.fin, self.fout, dy, self.x, self.w, self.gw, self.gb,
-                               ctx=self.ctx)
+                               dx=acc_dx, ctx=self.ctx, acc_dx=acc_dx is not None)
 
 
 # ------------------------------------------------------------------ debug exports

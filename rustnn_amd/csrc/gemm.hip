@@ -996,10 +996,18 @@ int rnn_linear_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const
 
 int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
                         const float *x, const float *w, float *dw, float *db, float *dx) {
+    return rnn_linear_backward_ex(ctx, rows, fin, fout, dy, x, w, dw, db, dx, 0);
+}
+
+int rnn_linear_backward_ex(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,
+                           const float *x, const float *w, float *dw, float *db, float *dx,
+                           uint32_t flags) {
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     if (!dy || !x || !w || !dw || !dx)
         return rnn_fail(ctx, RNN_E_NULL, "linear_backward: null operand");
+    if (flags & ~RNN_LINEAR_ACC_DX)
+        return rnn_fail(ctx, RNN_E_INVALID, "linear_backward: flags 0x%x", flags);
     // dW[fout, fin] += dY^T X (linear.rs:69); db += the column sums of dY
     // (linear.rs:70-89), summed in f64 by the dW GEMM itself when it takes
     // the direct-to-LDS kernel, else by the column-sum kernels
@@ -1020,8 +1028,8 @@ int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, cons
             if (rc) return rc;
         }
     }
-    // dX[rows, fin] = dY W (linear.rs:91-94)
-    return rnn_matmul(ctx, rows, fin, fout, dy, 0, w, 0, dx, 0);
+    // dX[rows, fin] = dY W (linear.rs:91-94), or dX += dY W
+    return rnn_matmul(ctx, rows, fin, fout, dy, 0, w, 0, dx, (flags & RNN_LINEAR_ACC_DX) ? 1 : 0);
 }
 
 int rnn_dbg_pack_a(rnn_ctx *ctx, const float *a, size_t m, size_t k, int transposed, float *out) {

@@ -488,7 +488,7 @@ __global__ void dw3_fwd_kernel(size_t n, int th, int tw, int c, const float *__r
 // order the reference's scatter visits them (output raster order, i.e. taps
 // 8, 7, ..., 0; norm.rs:423-450).
 __global__ void dw3_bwd_x_kernel(size_t n, int th, int tw, int c, const float *__restrict__ dy,
-                                 const float *__restrict__ w, float *__restrict__ dx) {
+                                 const float *__restrict__ w, float *__restrict__ dx, int acc_dx) {
     const size_t len = n * th * tw * c;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < len;
          i += (size_t)gridDim.x * blockDim.x) {
@@ -507,7 +507,7 @@ __global__ void dw3_bwd_x_kernel(size_t n, int th, int tw, int c, const float *_
                 acc += w[(ky * 3 + kx) * c + ch] * di[((size_t)oy * tw + ox) * c + ch];
             }
         }
-        dx[i] = acc;
+        dx[i] = acc_dx ? dx[i] + acc : acc;
     }
 }
 
@@ -520,17 +520,12 @@ __device__ __forceinline__ float4 fma4(float4 acc, float4 w, float4 x) {
     return make_float4(acc.x + w.x * x.x, acc.y + w.y * x.y, acc.z + w.z * x.z, acc.w + w.w * x.w);
 }
 
-__global__ __launch_bounds__(NT) void dw3_fwd4_kernel(int th, int tw, int c4,
-                                                      const float4 *__restrict__ x,
-                                                      const float4 *__restrict__ w,
-                                                      const float4 *__restrict__ b,
-                                                      float4 *__restrict__ y) {
+// Output (oy, ox) of image img, channel quad cq (x: that image's first quad).
+__device__ __forceinline__ float4 dw3_out4(int th, int tw, int c4, int oy, int ox, int cq,
+                                           const float4 *__restrict__ xi,
+                                           const float4 *__restrict__ w,
+                                           const float4 *__restrict__ b) {
 #pragma clang fp contract(off)
-    const int e = blockIdx.x * NT + threadIdx.x;
-    if (e >= tw * c4) return;
-    const int oy = blockIdx.y, img = blockIdx.z;
-    const int ox = e / c4, cq = e - ox * c4;
-    const float4 *xi = x + (size_t)img * th * tw * c4;
     float4 xv[9], wv[9];
 #pragma unroll
     for (int t = 0; t < 9; t++) {
@@ -544,9 +539,55 @@ __global__ __launch_bounds__(NT) void dw3_fwd4_kernel(int th, int tw, int c4,
         const int sy = oy + t / 3 - 1, sx = ox + t % 3 - 1;
         if (sy >= 0 && sy < th && sx >= 0 && sx < tw) acc = fma4(acc, wv[t], xv[t]);
     }
-    y[((size_t)img * th * tw + (size_t)oy * tw + ox) * c4 + cq] = acc;
+    return acc;
 }
 
+__global__ __launch_bounds__(NT) void dw3_fwd4_kernel(int th, int tw, int c4,
+                                                      const float4 *__restrict__ x,
+                                                      const float4 *__restrict__ w,
+                                                      const float4 *__restrict__ b,
+                                                      float4 *__restrict__ y) {
+    const int e = blockIdx.x * NT + threadIdx.x;
+    if (e >= tw * c4) return;
+    const int oy = blockIdx.y, img = blockIdx.z;
+    const int ox = e / c4, cq = e - ox * c4;
+    const size_t o = ((size_t)img * th * tw + (size_t)oy * tw + ox) * c4 + cq;
+    y[o] = dw3_out4(th, tw, c4, oy, ox, cq, x + (size_t)img * th * tw * c4, w, b);
+}
+
+// Block::forward's first branch after the attention (vit.rs:150-160) in one
+// pass: d = DwConv3(h) (as dw3_fwd4_kernel), a += gamma d (axpy_cols_kernel's
+// rounding), y = x + (a l) m with m = mask[img] (1 without a mask;
+// residual_add_scaled_kernel's rounding).  a is updated in place; y may be x.
+__global__ __launch_bounds__(NT) void dw3_branch4_kernel(
+    int th, int tw, int c4, const float4 *__restrict__ h, const float4 *__restrict__ w,
+    const float4 *__restrict__ b, float4 *__restrict__ d, float4 *a,
+    const float4 *__restrict__ gamma, const float4 *x, const float4 *__restrict__ l,
+    const float *__restrict__ mask, float4 *y) {
+#pragma clang fp contract(off)
+    const int e = blockIdx.x * NT + threadIdx.x;
+    if (e >= tw * c4) return;
+    const int oy = blockIdx.y, img = blockIdx.z;
+    const int ox = e / c4, cq = e - ox * c4;
+    const size_t o = ((size_t)img * th * tw + (size_t)oy * tw + ox) * c4 + cq;
+    const float4 dv = dw3_out4(th, tw, c4, oy, ox, cq, h + (size_t)img * th * tw * c4, w, b);
+    d[o] = dv;
+    const float4 g = gamma[cq];
+    float4 av = a[o];
+    av = make_float4(av.x + g.x * dv.x, av.y + g.y * dv.y, av.z + g.z * dv.z, av.w + g.w * dv.w);
+    a[o] = av;
+    const float4 lv = l[cq];
+    float4 t = make_float4(av.x * lv.x, av.y * lv.y, av.z * lv.z, av.w * lv.w);
+    if (mask) {
+        const float m = mask[img];
+        t = make_float4(t.x * m, t.y * m, t.z * m, t.w * m);
+    }
+    const float4 xv = x[o];
+    y[o] = make_float4(xv.x + t.x, xv.y + t.y, xv.z + t.z, xv.w + t.w);
+}
+
+// ACC: dx += the input gradient (old value first, rnn_add's order).
+template <bool ACC>
 __global__ __launch_bounds__(NT) void dw3_bwd_x4_kernel(int th, int tw, int c4,
                                                         const float4 *__restrict__ dy,
                                                         const float4 *__restrict__ w,
@@ -573,7 +614,12 @@ __global__ __launch_bounds__(NT) void dw3_bwd_x4_kernel(int th, int tw, int c4,
         const int oy = sy - t / 3 + 1, ox = sx - t % 3 + 1;
         if (oy >= 0 && oy < th && ox >= 0 && ox < tw) acc = fma4(acc, wv[u], dv[u]);
     }
-    dx[((size_t)img * th * tw + (size_t)sy * tw + sx) * c4 + cq] = acc;
+    float4 *o = dx + ((size_t)img * th * tw + (size_t)sy * tw + sx) * c4 + cq;
+    if constexpr (ACC) {
+        const float4 v = *o;
+        acc = make_float4(v.x + acc.x, v.y + acc.y, v.z + acc.z, v.w + acc.w);
+    }
+    *o = acc;
 }
 
 // dW [9][c] and db [c] partials over output rows [rb*RB, rb*RB + RB) of
@@ -1091,15 +1137,58 @@ int rnn_dwconv3_forward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, 
     return RNN_OK;
 }
 
+int rnn_dwconv3_branch_forward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c,
+                               const float *h, const float *w, const float *b, float *d, float *a,
+                               const float *gamma, const float *x, const float *l,
+                               const float *mask, float *y) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (n == 0 || th == 0 || tw == 0 || c == 0) return RNN_OK;
+    if (!h || !w || !b || !d || !a || !gamma || !x || !l || !y)
+        return rnn_fail(ctx, RNN_E_NULL, "dwconv3_branch_forward: null operand");
+    if (th > 65536 || tw > 65536 || !dims_ok(n * th * tw, c))
+        return rnn_fail(ctx, RNN_E_INVALID, "dwconv3: %zu x %zu x %zu x %zu", n, th, tw, c);
+    if (y == a || x == a || d == a || d == h || d == x || d == y || a == h || y == h)
+        return rnn_fail(ctx, RNN_E_INVALID, "dwconv3_branch_forward: aliased operands");
+    auto al = [](const void *p) { return ((uintptr_t)p & 15) == 0; };
+    if (dw3_vec(h, w, d, c, n) && al(b) && al(a) && al(gamma) && al(x) && al(l) && al(y)) {
+        const int c4 = (int)(c / 4);
+        dw3_branch4_kernel<<<dim3((unsigned)rnn_div_up(tw * c4, (size_t)NT), (unsigned)th,
+                                  (unsigned)n),
+                             NT, 0, ctx->stream>>>(
+            (int)th, (int)tw, c4, (const float4 *)h, (const float4 *)w, (const float4 *)b,
+            (float4 *)d, (float4 *)a, (const float4 *)gamma, (const float4 *)x,
+            (const float4 *)l, mask, (float4 *)y);
+        RNN_LAUNCHED(ctx);
+        return RNN_OK;
+    }
+    // the same three steps as separate passes
+    const size_t rows = n * th * tw;
+    int rc = rnn_dwconv3_forward(ctx, n, th, tw, c, h, w, b, d);
+    if (!rc) rc = rnn_axpy_cols(ctx, rows, c, a, gamma, d);
+    if (!rc) rc = rnn_residual_add_scaled(ctx, rows, c, x, a, l, mask, th * tw, y);
+    return rc;
+}
+
 int rnn_dwconv3_backward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c, const float *dy,
                          const float *x, const float *w, float *dx, float *dw, float *db) {
+    return rnn_dwconv3_backward_ex(ctx, n, th, tw, c, dy, x, w, dx, dw, db, 0);
+}
+
+int rnn_dwconv3_backward_ex(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c,
+                            const float *dy, const float *x, const float *w, float *dx, float *dw,
+                            float *db, uint32_t flags) {
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     if (n == 0 || th == 0 || tw == 0 || c == 0) return RNN_OK;
     if (!dy || !x || !w || !dx || !dw || !db)
         return rnn_fail(ctx, RNN_E_NULL, "dwconv3_backward: null operand");
+    if (flags & ~RNN_DW3_ACC_DX)
+        return rnn_fail(ctx, RNN_E_INVALID, "dwconv3_backward: flags 0x%x", flags);
+    if (dx == dy) return rnn_fail(ctx, RNN_E_INVALID, "dwconv3_backward: dx is dy");
     if (th > 65536 || tw > 65536 || !dims_ok(n * th * tw, c))
         return rnn_fail(ctx, RNN_E_INVALID, "dwconv3: %zu x %zu x %zu x %zu", n, th, tw, c);
+    const bool acc = (flags & RNN_DW3_ACC_DX) != 0;
     // dW and db partials per block of output rows (about 1024 blocks), then
     // the block-order sum
     const size_t cblk = rnn_div_up(c, (size_t)NT);
@@ -1118,13 +1207,16 @@ int rnn_dwconv3_backward(rnn_ctx *ctx, size_t n, size_t th, size_t tw, size_t c,
     const size_t len = n * th * tw * c;
     if (dw3_vec(dy, w, dx, c, n)) {
         const int c4 = (int)(c / 4);
-        dw3_bwd_x4_kernel<<<dim3((unsigned)rnn_div_up(tw * c4, (size_t)NT), (unsigned)th,
-                                 (unsigned)n),
-                            NT, 0, ctx->stream>>>((int)th, (int)tw, c4, (const float4 *)dy,
-                                                  (const float4 *)w, (float4 *)dx);
+        const dim3 grid((unsigned)rnn_div_up(tw * c4, (size_t)NT), (unsigned)th, (unsigned)n);
+        if (acc)
+            dw3_bwd_x4_kernel<true><<<grid, NT, 0, ctx->stream>>>(
+                (int)th, (int)tw, c4, (const float4 *)dy, (const float4 *)w, (float4 *)dx);
+        else
+            dw3_bwd_x4_kernel<false><<<grid, NT, 0, ctx->stream>>>(
+                (int)th, (int)tw, c4, (const float4 *)dy, (const float4 *)w, (float4 *)dx);
     } else {
         dw3_bwd_x_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)tw, (int)c, dy, w,
-                                                               dx);
+                                                               dx, acc ? 1 : 0);
     }
     RNN_LAUNCHED(ctx);
     return RNN_OK;

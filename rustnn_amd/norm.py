@@ -9,7 +9,7 @@ librnn.so; there is no CPU fallback.
 """
 from __future__ import annotations
 
-from . import Linear, _ptr, default_ctx, lib
+from . import RNN_DW3_ACC_DX, Linear, _ptr, default_ctx, lib
 from .optim import Param
 
 
@@ -205,17 +205,36 @@ class DwConv3:
             self.x, self.n = x, n
         return y
 
-    def backward(self, dy):
+    def forward_branch(self, h, a, gamma, x, l, mask, y, train):
+        """Block::forward's first branch (vit.rs:150-160) in one pass: d =
+        forward(h) (returned), a += gamma d in place, y = x + (a l) m with m
+        the DropPath mask per image (None: 1) -- rnn_dwconv3_branch_forward."""
+        import torch
+        n, c = self._images(h), self.c
+        need = n * self.th * self.tw * c
+        d = torch.empty_like(h)
+        self.ctx.check(lib().rnn_dwconv3_branch_forward(
+            self.ctx.h, n, self.th, self.tw, c, _ptr(h, need, "h"), _ptr(self.w.v, 9 * c, "w"),
+            _ptr(self.b.v, c, "b"), _ptr(d, need, "d"), _ptr(a, need, "a"),
+            _ptr(gamma, c, "gamma"), _ptr(x, need, "x"), _ptr(l, c, "l"),
+            _ptr(mask, n, "mask") if mask is not None else None, _ptr(y, need, "y")))
+        if train:
+            self.x, self.n = h, n
+        return d
+
+    def backward(self, dy, acc_dx=None):
+        """dx, or acc_dx += dx (returned) when given."""
         import torch
         c = self.c
         if self._images(dy) != self.n:
             raise ValueError("DwConv3.backward: dy does not match the forward's input")
         need = self.n * self.th * self.tw * c
-        dx = torch.empty_like(dy)
-        self.ctx.check(lib().rnn_dwconv3_backward(
+        dx = torch.empty_like(dy) if acc_dx is None else acc_dx
+        self.ctx.check(lib().rnn_dwconv3_backward_ex(
             self.ctx.h, self.n, self.th, self.tw, c, _ptr(dy, need, "dy"),
             _ptr(self.x, need, "x"), _ptr(self.w.v, 9 * c, "w"), _ptr(dx, need, "dx"),
-            _ptr(self.w.g, 9 * c, "dw"), _ptr(self.b.g, c, "db")))
+            _ptr(self.w.g, 9 * c, "dw"), _ptr(self.b.g, c, "db"),
+            0 if acc_dx is None else RNN_DW3_ACC_DX))
         return dx
 
     def for_each_param(self, f):

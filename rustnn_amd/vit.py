@@ -95,7 +95,8 @@ class SelfAttn:
             self.ab, self.p, self.n = ab, p, n
         return y.view(n, t, c)
 
-    def backward(self, dy):
+    def backward(self, dy, acc_dx=None):
+        """dx, or acc_dx += dx (returned) when given."""
         import torch
         n, t, c = self.n, self.t, self.c
         do = self.proj.backward(dy.reshape(-1))
@@ -104,7 +105,8 @@ class SelfAttn:
         dab = torch.empty(n * t * 3 * c, device=dy.device)
         self.core.backward(n, self.ab, 3 * c, 0, self.ab, 3 * c, c, 2 * c, self.tau.v, self.p,
                            do, dab, dab, self.tau.g, self.rel.g, set_dq=True, set_dkv=True)
-        return self.qkv.backward(dab).view(n, t, c)
+        acc = acc_dx.reshape(-1) if acc_dx is not None else None
+        return self.qkv.backward(dab, acc_dx=acc).view(n, t, c)
 
     def for_each_param(self, f):
         for p in self._lin:
@@ -315,15 +317,14 @@ class Block:
         L, ctx, c = lib(), self.ctx, self.c
         h = self.n1.forward(x, train)
         a = self.attn.forward(h, train)
-        d = self.dw.forward(h, train)
-        rows = a.numel() // c
-        ctx.check(L.rnn_axpy_cols(ctx.h, rows, c, _ptr(a, rows * c, "a"),
-                                  _ptr(self.gamma.v, c, "gamma"), _ptr(d, rows * c, "d")))
+        # a += gamma * DwConv3(h); y = x + dp1(ls1(a)) in one pass, then the
+        # other branches added in place, each in one pass (vit.rs:150-176)
+        mask = self.dp1.take_mask(x.shape[0], train, seed ^ self.idx, x.device)
+        y = torch.empty_like(x)
+        d = self.dw.forward_branch(h, a, self.gamma.v, x, self.ls1.l.v, mask, y, train)
         if train:
             self.dwo = d
-        # y = x + dp1(ls1(a)), then the other branches added in place, each
-        # in one pass (vit.rs:155-176)
-        y = _branch_add(x, a, self.ls1, self.dp1, train, seed ^ self.idx, torch.empty_like(x))
+            self.ls1.x = a
         if self.cross is not None:
             if mem is None:
                 raise ValueError("Block: a reader block needs the memory")
@@ -356,12 +357,10 @@ class Block:
                                             _ptr(self.gamma.v, c, "gamma"),
                                             _ptr(ddw, rows * c, "ddw"),
                                             _ptr(self.gamma.g, c, "dgamma")))
-        ga = self.attn.backward(da)
-        if dh is None:
-            dh = ga
-        else:
-            _add_(dh, ga, ctx)
-        _add_(dh, self.dw.backward(ddw), ctx)
+        # the branches' input gradients summed in branch order, each added by
+        # the kernel that computes it
+        dh = self.attn.backward(da, acc_dx=dh)
+        self.dw.backward(ddw, acc_dx=dh)
         self.n1.backward(dh, add=dy, out=dy)  # dy += n1's input gradient
         return dy
 

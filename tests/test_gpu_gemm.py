@@ -164,6 +164,29 @@ def test_linear(rnn, orc, rows, fin, fout, bias):
         assert rel_frob(to_host(db), db_want) < TOL
 
 
+@pytest.mark.parametrize("rows,fin,fout", [(8192, 256, 768), (100, 64, 30), (27, 6, 10)])
+def test_linear_backward_acc(rnn, orc, rows, fin, fout):
+    """rnn_linear_backward_ex with RNN_LINEAR_ACC_DX: dx0 + the dx that
+    rnn_linear_backward writes, bit for bit (dW and db as the plain call's,
+    bit for bit), and within TOL of the oracle."""
+    rng = orc.Rng(22)
+    x, w = rng.rand_vec(rows * fin), rng.rand_vec(fout * fin) * np.float32(0.02)
+    dy, dx0 = rng.rand_vec(rows * fout), rng.rand_vec(rows * fin)
+    X, W, DY = to_dev(x), to_dev(w), to_dev(dy)
+    dw1, db1 = to_dev(np.zeros(fout * fin, np.float32)), to_dev(np.zeros(fout, np.float32))
+    dx = to_host(rnn.linear_backward(rows, fin, fout, DY, X, W, dw1, db1))
+    dw2, db2 = to_dev(np.zeros(fout * fin, np.float32)), to_dev(np.zeros(fout, np.float32))
+    DX = to_dev(dx0.copy())
+    out = rnn.linear_backward(rows, fin, fout, DY, X, W, dw2, db2, dx=DX, acc_dx=True)
+    assert out is DX
+    assert np.array_equal(to_host(DX), (dx0 + dx).astype(np.float32))
+    assert np.array_equal(to_host(dw1), to_host(dw2)) and np.array_equal(to_host(db1), to_host(db2))
+    with orc.threads(8):
+        _, _, dx_want = orc.linear_backward(rows, fin, fout, dy, x, w, np.zeros(fout * fin, np.float32),
+                                            np.zeros(fout, np.float32))
+    assert rel_frob(to_host(DX) - dx0, dx_want) < TOL
+
+
 @pytest.mark.parametrize("m,k", [(32, 288), (288, 32), (7, 259), (1, 1), (13, 600)])
 @pytest.mark.parametrize("tr", [False, True])
 def test_pack_bit_exact(rnn, orc, m, k, tr):

@@ -208,6 +208,55 @@ def test_dwconv3(rnn, orc, n, th, tw, c):
     assert rel_frob(to_host(dw.b.g), gb) < TOL
 
 
+@pytest.mark.parametrize("n,th,tw,c,masked", [(64, 8, 8, 256, True), (16, 4, 4, 384, False),
+                                               (3, 5, 4, 12, True), (2, 1, 7, 5, True)])
+def test_dwconv3_branch_forward(rnn, orc, n, th, tw, c, masked):
+    """rnn_dwconv3_branch_forward == the oracle's DwConv3 forward, then
+    a + gamma d and x + DropPath(LayerScale(a)) (vit.rs:150-160) composed in
+    numpy f32, bit for bit; out of place and with y = x (c = 5: the unfused
+    fallback)."""
+    from rustnn_amd.norm import DwConv3
+    t = th * tw
+    h, a, x = _r((n, t, c), 30), _r((n, t, c), 31), _r((n, t, c), 32)
+    w, b, gam, l = _r((9, c), 33, 0.1), _r(c, 34), _r(c, 35, 0.5), _r(c, 36, 1e-2)
+    keep = np.float32(0.8)
+    mask = np.where(np.arange(n) % 3 == 1, np.float32(0.0), np.float32(1.0) / keep).astype(np.float32)
+    wd = orc.dwconv3_forward(h, w, b, n, th, tw).reshape(n, t, c)
+    wa = (a + gam * wd).astype(np.float32)
+    ts = orc.layerscale_forward(wa.reshape(-1, c), l).reshape(n, t, c)
+    if masked:
+        ts = (ts * mask[:, None, None]).astype(np.float32)
+    wy = (x + ts).astype(np.float32)
+    dw = DwConv3(c, th, tw, to_dev(w.ravel()), to_dev(b))
+    for inplace in (False, True):
+        H, A, X = _dev(h), _dev(a), _dev(x)
+        Y = X if inplace else _dev(np.zeros((n, t, c), np.float32))
+        M = to_dev(mask) if masked else None
+        D = dw.forward_branch(H, A, to_dev(gam), X, to_dev(l), M, Y, True)
+        assert np.array_equal(to_host(D).reshape(n, t, c), wd)
+        assert np.array_equal(to_host(A).reshape(n, t, c), wa)
+        assert np.array_equal(to_host(Y).reshape(n, t, c), wy)
+        assert dw.x is H and dw.n == n
+
+
+@pytest.mark.parametrize("n,th,tw,c", [(64, 8, 8, 256), (2, 1, 7, 5)])
+def test_dwconv3_backward_acc(rnn, orc, n, th, tw, c):
+    """rnn_dwconv3_backward_ex with RNN_DW3_ACC_DX: dx0 + the oracle's input
+    gradient, bit for bit (c = 5: the scalar kernel)."""
+    from rustnn_amd.norm import DwConv3
+    x, dy, dx0 = _r((n, th * tw, c), 40), _r((n, th * tw, c), 41), _r((n, th * tw, c), 42)
+    w, b = _r((9, c), 43, 0.1), _r(c, 44)
+    dw = DwConv3(c, th, tw, to_dev(w.ravel()), to_dev(b))
+    dw.forward(_dev(x), True)
+    gw, gb = np.zeros((9, c), np.float32), np.zeros(c, np.float32)
+    wdx = orc.dwconv3_backward(dy, x, w, n, th, tw, gw, gb).reshape(x.shape)
+    DX = _dev(dx0)
+    out = dw.backward(_dev(dy), acc_dx=DX)
+    assert out is DX
+    assert np.array_equal(to_host(DX).reshape(x.shape), (dx0 + wdx).astype(np.float32))
+    assert rel_frob(to_host(dw.w.g), gw) < TOL
+
+
 @pytest.mark.parametrize("n,t,c", [(256, 16, 384), (64, 64, 256), (3, 9, 8), (5, 1, 33)])
 def test_seqpool(rnn, orc, n, t, c):
     from rustnn_amd.norm import SeqPool
