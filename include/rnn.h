@@ -173,6 +173,22 @@ int rnn_conv2d_forward_packed(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, c
                               const float *w, const float *wp, float *y);
 int rnn_conv2d_backward_x_packed(rnn_ctx *ctx, const rnn_conv_spec *sp, size_t n, const float *dy,
                                  const float *w, const float *wp, float *dx);
+/* Packed copies of several convolutions' weights, refreshed together in one
+ * launch (no counterpart in the reference: for a network whose convolutions
+ * run on packed weights and are re-packed after each weight update, such as
+ * the rustvit trunk).  Convolution i has spec specs[i] and weights w[i] (on
+ * the device, [cout][cin][k][k]; w[i] must stay allocated, at the same
+ * address, while the object lives).  create allocates the packed copies of
+ * both directions of every convolution and packs them on the context stream;
+ * update re-packs all of them from the current W; get returns convolution
+ * i's copy for the forward (dx = 0) or dX (dx = 1) -- for the _packed calls
+ * with the same spec -- or NULL when that shape has no packed form. */
+typedef struct rnn_conv_packs rnn_conv_packs;
+int rnn_conv_packs_create(rnn_ctx *ctx, size_t count, const rnn_conv_spec *specs, const float **w,
+                          rnn_conv_packs **out);
+int rnn_conv_packs_update(rnn_ctx *ctx, rnn_conv_packs *p);
+const float *rnn_conv_packs_get(const rnn_conv_packs *p, size_t i, int dx);
+void rnn_conv_packs_destroy(rnn_conv_packs *p);
 
 /* ------------------------------------------------------------ attn.rs */
 /* Core (attn.rs:74-84) plus the stride/offset arguments of Core::forward /

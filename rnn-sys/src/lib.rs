@@ -15,6 +15,7 @@ pub const RNN_LINEAR_ACC_DX: u32 = 1;
 pub const RNN_DW3_ACC_DX: u32 = 1;
 
 #[repr(C)] pub struct rnn_ctx { _p: [u8; 0] }
+#[repr(C)] pub struct rnn_conv_packs { _p: [u8; 0] }
 #[repr(C)] pub struct rnn_optim { _p: [u8; 0] }
 #[repr(C)] pub struct rnn_resnet { _p: [u8; 0] }
 
@@ -117,6 +118,10 @@ extern "C" {
     pub fn rnn_conv_pack_weights(ctx: *mut rnn_ctx, sp: *const rnn_conv_spec, dx: c_int, w: *const f32, wp: *mut f32) -> c_int;
     pub fn rnn_conv2d_forward_packed(ctx: *mut rnn_ctx, sp: *const rnn_conv_spec, n: usize, x: *const f32, w: *const f32, wp: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_conv2d_backward_x_packed(ctx: *mut rnn_ctx, sp: *const rnn_conv_spec, n: usize, dy: *const f32, w: *const f32, wp: *const f32, dx: *mut f32) -> c_int;
+    pub fn rnn_conv_packs_create(ctx: *mut rnn_ctx, count: usize, specs: *const rnn_conv_spec, w: *mut *const f32, out: *mut *mut rnn_conv_packs) -> c_int;
+    pub fn rnn_conv_packs_update(ctx: *mut rnn_ctx, p: *mut rnn_conv_packs) -> c_int;
+    pub fn rnn_conv_packs_get(p: *const rnn_conv_packs, i: usize, dx: c_int) -> *const f32;
+    pub fn rnn_conv_packs_destroy(p: *mut rnn_conv_packs);
     pub fn rnn_rel_index(th: u32, tw: u32, mh: u32, mw: u32, idx: *mut u32, nrel: *mut u32) -> c_int;
     pub fn rnn_attn_forward(ctx: *mut rnn_ctx, d: *const rnn_attn_desc, n: usize, q: *const f32, kv: *const f32, tau: *const f32, rel: *const f32, p: *mut f32, o: *mut f32) -> c_int;
     pub fn rnn_attn_backward(ctx: *mut rnn_ctx, d: *const rnn_attn_desc, n: usize, q: *const f32, kv: *const f32, tau: *const f32, p: *const f32, dout: *const f32, dq: *mut f32, dkv: *mut f32, dtau: *mut f32, drel: *mut f32) -> c_int;

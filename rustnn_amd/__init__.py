@@ -240,6 +240,10 @@ def lib():
             "rnn_dwconv3_forward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
             "rnn_dwconv3_backward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
                                           _vp]),
+            "rnn_conv_packs_create": (_i, [_vp, _sz, P(ConvSpec), P(_vp), P(_vp)]),
+            "rnn_conv_packs_update": (_i, [_vp, _vp]),
+            "rnn_conv_packs_get": (_vp, [_vp, _sz, _i]),
+            "rnn_conv_packs_destroy": (None, [_vp]),
             "rnn_dwconv3_backward_ex": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
                                              _vp, _u32]),
             "rnn_dwconv3_branch_forward": (_i, [_vp, _sz, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
@@ -520,14 +524,28 @@ class Conv2d:
         self.g = torch.zeros_like(self.w)
         self.x = None
         self.xshape = None
+        # ((h, w), forward copy, dX copy) from a ConvPacks kept current with w
+        self.packed = None
 
     def spec(self, h, w):
         """Conv2d::spec (nn.rs:152-164)."""
         return ConvSpec.make(self.cin, self.cout, self.k, self.stride, self.pad, h, w)
 
+    def _wp(self, h, w, dx):
+        """This input size's packed weights for the forward / dX, or None."""
+        pk = self.packed
+        return pk[1 + dx] if pk is not None and pk[0] == (h, w) and pk[1 + dx] else None
+
     def forward(self, x, n, h, w, train=True):
         sp = self.spec(h, w)
-        y = conv2d_forward(sp, n, x, self.w, ctx=self.ctx)
+        wp = self._wp(h, w, 0)
+        if wp is None:
+            y = conv2d_forward(sp, n, x, self.w, ctx=self.ctx)
+        else:
+            y = _new(n * sp.cout * sp.hw, x)
+            self.ctx.check(lib().rnn_conv2d_forward_packed(
+                self.ctx.h, C.byref(sp), n, _ptr(x, n * sp.cin * sp.h * sp.w, "x"),
+                _ptr(self.w, sp.cout * sp.ckk, "w"), wp, _ptr(y, n * sp.cout * sp.hw, "y")))
         if train:
             self.x, self.xshape = x, (n, h, w)
         return y
@@ -540,7 +558,59 @@ class Conv2d:
         """Returns dX and accumulates dW (nn.rs:230-250)."""
         self.backward_w(dy)
         n, h, w = self.xshape
-        return conv2d_backward_x(self.spec(h, w), n, dy, self.w, ctx=self.ctx)
+        sp = self.spec(h, w)
+        wp = self._wp(h, w, 1)
+        if wp is None:
+            return conv2d_backward_x(sp, n, dy, self.w, ctx=self.ctx)
+        dx = _new(n * sp.cin * sp.h * sp.w, dy)
+        self.ctx.check(lib().rnn_conv2d_backward_x_packed(
+            self.ctx.h, C.byref(sp), n, _ptr(dy, n * sp.cout * sp.hw, "dy"),
+            _ptr(self.w, sp.cout * sp.ckk, "w"), wp, _ptr(dx, n * sp.cin * sp.h * sp.w, "dx")))
+        return dx
+
+
+class ConvPacks:
+    """Packed weights of several Conv2d layers (rnn_conv_packs_*), re-packed
+    together in one launch by update(); convs: [(Conv2d, h, w)], the input
+    size each runs at.  Each layer then runs its forward / dX at that size on
+    the packed copies (results identical to the unpacked calls) until
+    close(); update() after every change of the weights (in place: the
+    copies are tied to the weight tensors' addresses)."""
+
+    def __init__(self, convs, ctx=None):
+        self.ctx = ctx or default_ctx()
+        self.h = None
+        k = len(convs)
+        specs = (ConvSpec * k)(*[c.spec(h, w) for c, h, w in convs])
+        ws = (C.c_void_p * k)(*[c.w.data_ptr() for c, _, _ in convs])
+        out = C.c_void_p()
+        self.ctx.check(lib().rnn_conv_packs_create(self.ctx.h, k, specs, ws, C.byref(out)))
+        self.h = out.value
+        self._w = [c.w for c, _, _ in convs]  # the addresses the copies are tied to
+        self.convs = [c for c, _, _ in convs]
+        for i, (c, h, w) in enumerate(convs):
+            c.packed = ((h, w), lib().rnn_conv_packs_get(self.h, i, 0),
+                        lib().rnn_conv_packs_get(self.h, i, 1))
+
+    def update(self):
+        for c, w in zip(self.convs, self._w):
+            if c.w.data_ptr() != w.data_ptr():
+                raise RuntimeError("ConvPacks: a layer's weights moved; build a new ConvPacks")
+        self.ctx.check(lib().rnn_conv_packs_update(self.ctx.h, self.h))
+
+    def close(self):
+        if self.h:
+            for c in self.convs:
+                c.packed = None
+            self.ctx.synchronize()
+            lib().rnn_conv_packs_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # interpreter shutdown: the library may be gone
+            pass
 
 
 # ------------------------------------------------------------------ attn.rs

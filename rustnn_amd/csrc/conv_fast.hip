@@ -29,6 +29,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <new>
 
 namespace {
 
@@ -901,4 +902,100 @@ int rnn_conv_pack_multi_launch(rnn_ctx *ctx, const PackSeg *segs, int nseg, int 
     conv_pack_multi_kernel<<<nblocks, 256, 0, ctx->stream>>>(src, segs, nseg, dst);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
+}
+
+// Packed copies of several convolutions' weights in one device block: the
+// data (each copy a whole number of 256-float slabs), then the segment table
+// that conv_pack_multi_kernel walks.  Sources are addressed from the lowest
+// W pointer, so a segment's source offset is its W's distance from it.
+struct rnn_conv_packs {
+    void *mem = nullptr;
+    PackSeg *segs = nullptr;
+    int nseg = 0, nblk = 0;
+    const float *src = nullptr;
+    float *data = nullptr;
+    std::vector<const float *> wp[2];
+};
+
+int rnn_conv_packs_create(rnn_ctx *ctx, size_t count, const rnn_conv_spec *specs, const float **w,
+                          rnn_conv_packs **out) {
+    if (!ctx || !out) return RNN_E_NULL;
+    *out = nullptr;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (count == 0 || !specs || !w) return rnn_fail(ctx, RNN_E_NULL, "conv_packs: no convolutions");
+    uintptr_t lo = UINTPTR_MAX;
+    for (size_t i = 0; i < count; i++) {
+        if (!w[i]) return rnn_fail(ctx, RNN_E_NULL, "conv_packs: null weights %zu", i);
+        if ((uintptr_t)w[i] & 3) return rnn_fail(ctx, RNN_E_INVALID, "conv_packs: unaligned W");
+        lo = std::min(lo, (uintptr_t)w[i]);
+    }
+    std::vector<PackSeg> segs;
+    std::vector<std::pair<size_t, int>> who;  // (conv, direction) of each segment
+    size_t floats = 0;
+    uint32_t blk = 0;
+    for (size_t i = 0; i < count; i++) {
+        for (int dx = 0; dx < 2; dx++) {
+            PackSeg sg;
+            if (rnn_conv_pack_geo(&specs[i], dx, &sg.geo) != RNN_OK) continue;
+            sg.src = ((uintptr_t)w[i] - lo) / sizeof(float);
+            sg.dst = floats;
+            sg.blk0 = blk;
+            sg.nblk = (uint32_t)std::min(sg.geo.slabs(), 512);
+            blk += sg.nblk;
+            floats += sg.geo.floats();
+            segs.push_back(sg);
+            who.push_back({i, dx});
+        }
+    }
+    if (blk > 0x7fffffffu) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "conv_packs: too many slabs");
+    auto *p = new (std::nothrow) rnn_conv_packs();
+    if (!p) return rnn_fail(ctx, RNN_E_NOMEM, "conv_packs: host allocation");
+    p->wp[0].assign(count, nullptr);
+    p->wp[1].assign(count, nullptr);
+    p->src = (const float *)lo;
+    p->nseg = (int)segs.size();
+    p->nblk = (int)blk;
+    if (!segs.empty()) {
+        const size_t dbytes = floats * sizeof(float), tbytes = segs.size() * sizeof(PackSeg);
+        hipError_t e = hipMalloc(&p->mem, dbytes + tbytes);
+        if (e != hipSuccess) {
+            delete p;
+            return rnn_fail(ctx, RNN_E_NOMEM, "conv_packs hipMalloc(%zu): %s", dbytes + tbytes,
+                            hipGetErrorString(e));
+        }
+        p->data = (float *)p->mem;
+        p->segs = (PackSeg *)((char *)p->mem + dbytes);
+        e = hipMemcpy(p->segs, segs.data(), tbytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(p->mem);
+            delete p;
+            return rnn_fail(ctx, RNN_E_HIP, "conv_packs table upload: %s", hipGetErrorString(e));
+        }
+        for (size_t k = 0; k < segs.size(); k++)
+            p->wp[who[k].second][who[k].first] = p->data + segs[k].dst;
+    }
+    const int rc = rnn_conv_pack_multi_launch(ctx, p->segs, p->nseg, p->nblk, p->src, p->data);
+    if (rc) {
+        rnn_conv_packs_destroy(p);
+        return rc;
+    }
+    *out = p;
+    return RNN_OK;
+}
+
+int rnn_conv_packs_update(rnn_ctx *ctx, rnn_conv_packs *p) {
+    if (!ctx || !p) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    return rnn_conv_pack_multi_launch(ctx, p->segs, p->nseg, p->nblk, p->src, p->data);
+}
+
+const float *rnn_conv_packs_get(const rnn_conv_packs *p, size_t i, int dx) {
+    if (!p || (dx != 0 && dx != 1) || i >= p->wp[0].size()) return nullptr;
+    return p->wp[dx][i];
+}
+
+void rnn_conv_packs_destroy(rnn_conv_packs *p) {
+    if (!p) return;
+    if (p->mem) (void)hipFree(p->mem);
+    delete p;
 }

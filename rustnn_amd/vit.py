@@ -635,12 +635,35 @@ class RustViT:
         self.use_exits, self.drop_seed = True, 0
         self.mem = self.c2_out = self.stem_out = None
         self.n = 0
+        self._packs = None
+
+    def _trunk_convs(self):
+        """(Conv2d, h, w) of every convolution of the trunk at its input size."""
+        s = self.cfg["img"]
+        out = [(self.stem.conv, s, s)]
+        for b in (self.c1, self.c2):
+            out += [(b.a.conv, s, s)]
+            if b.down:
+                out += [(b.down.conv, s, s)]
+            s = b.a.out_hw(s, s)[0]
+            out += [(b.b.conv, s, s)]
+        return out + [(self.memconv, self.mh, self.mh), (self.tok.conv, self.mh, self.mh)]
+
+    def _repack(self):
+        """The trunk's packed weights from the current ones: one launch per
+        forward (the optimiser, EMA or a checkpoint may have changed them)."""
+        from . import ConvPacks
+        if self._packs is None:
+            self._packs = ConvPacks(self._trunk_convs(), self.ctx)
+        else:
+            self._packs.update()
 
     def forward(self, x, train):
         """RustViT::forward (vit.rs:510-609): dict with logits, coarse and, in
         training with exits, e1, e2, h1, h2; feat (the pooled feature)."""
         from .nn import gap_forward
         n, cfg, d = x.shape[0], self.cfg, self.cfg["dim"]
+        self._repack()
         h = self.stem.forward(x, train)
         if train:
             self.stem_out = h

@@ -180,6 +180,54 @@ def test_conv_dw_smallc_unaligned_dy(rnn, orc, cin, p, h):
     assert np.array_equal(got[0], got[1])
 
 
+def test_conv_packs_object(rnn, orc):
+    """rnn_conv_packs_*: Conv2d layers on one ConvPacks give the unpacked
+    calls' forward and dX bit for bit -- before and after an in-place weight
+    change followed by update() -- and within TOL of the oracle; a shape with
+    no packed form (3x3 pad 0) keeps the plain path; a layer whose weights moved
+    makes update() raise."""
+    import torch
+    ctx = rnn.default_ctx()
+    shapes = [(3, 32, 3, 1, 1, 32), (32, 96, 3, 2, 1, 32), (32, 96, 1, 2, 0, 32),
+              (16, 24, 3, 1, 0, 12), (96, 64, 3, 1, 1, 16)]
+    n = 4
+    rng = orc.Rng(77)
+    layers = []
+    for (cin, cout, k, s_, p, h) in shapes:
+        w = to_dev(rng.rand_vec(cout * cin * k * k) * np.float32(0.1))
+        layers.append((rnn.Conv2d(cin, cout, k, s_, p, w, ctx=ctx), h))
+    packs = rnn.ConvPacks([(c, h, h) for c, h in layers], ctx=ctx)
+    assert layers[3][0].packed[1] is None and layers[3][0].packed[2] is None  # pad 0
+    assert all(c.packed[1] for c, _ in layers[:3] + layers[4:])
+
+    def run(c, h, x, dy):
+        y = c.forward(x, n, h, h, True)
+        dx = c.backward(dy)
+        return to_host(y), to_host(dx)
+
+    for step in range(2):
+        for c, h in layers:
+            sp = c.spec(h, h)
+            x = to_dev(rng.rand_vec(n * c.cin * h * h))
+            dy = to_dev(rng.rand_vec(n * c.cout * sp.hw))
+            got = run(c, h, x, dy)
+            keep, c.packed = c.packed, None
+            want = run(c, h, x, dy)
+            c.packed = keep
+            assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1])
+            osp = orc.ConvSpec.make(c.cin, c.cout, c.k, c.stride, c.pad, h, h)
+            assert rel_frob(got[0], orc.conv2d_forward(osp, n, to_host(x), to_host(c.w))) < TOL
+        for c, _ in layers:  # an optimiser step: W changes in place
+            c.w.mul_(0.5).add_(0.01)
+        packs.update()
+    c0 = layers[0][0]
+    c0.w = c0.w.clone()
+    with pytest.raises(RuntimeError):
+        packs.update()
+    packs.close()
+    assert all(c.packed is None for c, _ in layers)
+
+
 def test_conv_deterministic(rnn, orc):
     sp = rnn.ConvSpec.make(32, 32, 3, 1, 1, 32, 32)
     x, w, dy = inputs(orc, sp, 128, seed=99)

@@ -67,7 +67,8 @@ def test_functions_match_header():
 def test_structs_and_constants_match_header():
     consts, opaque, structs, _ = gb.parse_header()
     _, rstructs, ropaque, rconsts, _ = parse_lib_rs()
-    assert sorted(opaque) == sorted(ropaque) == ["rnn_ctx", "rnn_optim", "rnn_resnet"]
+    assert sorted(opaque) == sorted(ropaque) == ["rnn_conv_packs", "rnn_ctx", "rnn_optim",
+                                                 "rnn_resnet"]
     assert sorted(structs) == sorted(rstructs)
     for name, fields in structs.items():
         assert rstructs[name] == [(f, expect(t)) for f, t in fields], name
