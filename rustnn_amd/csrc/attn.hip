@@ -32,6 +32,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 
 namespace {
 
@@ -291,6 +292,160 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs g) {
             if (q < tq && d < dh) od[(long long)q * c + d] = acc[v];
         }
     }
+}
+
+// Core::forward for tq <= 64 and tk = 16 NT keys above 64 (the rustvit's
+// cross-attention over 256 memory tokens), one workgroup per (image, head),
+// as attn_fwd_kernel with float4 accesses: K rows staged in LDS [tk][DHP+4];
+// V loaded into registers while the scores run and stored transposed
+// ([DHP][tk+4]) over the K rows once every wave is done with them; the
+// relidx entries of the lane's query and keys read from the composed path's
+// [tq][tk] table.  Two workgroups fit a CU.
+template <int DHP, int NT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+attn_fwd_long_kernel(AttnArgs g, const uint32_t *__restrict__ relidx) {
+    constexpr int KSL = DHP / 4, TK = 16 * NT, KS = DHP + 4, VS = TK + 4;
+    constexpr int AW = TK * KS > DHP * VS ? TK * KS : DHP * VS;
+    constexpr int G = DHP / 4, CPT = TK * G / 256;  // float4 chunks of K (or V) per thread
+    extern __shared__ float smem[];
+    float *A = smem;          // K rows [TK][KS], then V^T [DHP][VS]
+    float *rels = smem + AW;  // [nrel]
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_index();
+    const int l16 = lane & 15, grp = lane >> 4;
+    const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
+    const int tq = g.tq, dh = g.dh;
+    const float *qb = g.q + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
+    const float *kb = g.kv + (long long)img * TK * g.kvstride + g.koff + (long long)hd * dh;
+    const float *vb = g.kv + (long long)img * TK * g.kvstride + g.voff + (long long)hd * dh;
+    const int qi = 16 * w + l16;
+    const float tau = g.tau[hd];
+    float4 qraw[KSL / 4];
+#pragma unroll
+    for (int i = 0; i < KSL; i += 4)
+        qraw[i / 4] = load4<true>(qb, g.qstride, qi, tq, grp * KSL + i, dh);
+    const uint32_t *rq = relidx + (long long)min(qi, tq - 1) * TK + 4 * grp;
+    uint4 ri[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) ri[t] = *reinterpret_cast<const uint4 *>(rq + 16 * t);
+    float4 kv4[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int i = tid + 256 * j, r = i / G, c = (i % G) * 4;
+        kv4[j] = load4<true>(kb, g.kvstride, r, TK, c, dh);
+    }
+    const float *relh = g.rel + (long long)hd * g.nrel;
+    const float rel0 = relh[min(tid, g.nrel - 1)];
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int i = tid + 256 * j, r = i / G, c = (i % G) * 4;
+        *reinterpret_cast<float4 *>(A + r * KS + c) = kv4[j];
+    }
+    // V next: only O = P V needs it, so its latency overlaps the scores
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int i = tid + 256 * j, r = i / G, c = (i % G) * 4;
+        kv4[j] = load4<true>(vb, g.kvstride, r, TK, c, dh);
+    }
+    if (tid < g.nrel) rels[tid] = rel0;
+    for (int e = tid + 256; e < g.nrel; e += 256) rels[e] = relh[e];
+    __syncthreads();
+
+    float qs[KSL];
+#pragma unroll
+    for (int i = 0; i < KSL; i += 4) {
+        const float4 t4 = mask4(qraw[i / 4], qi < tq, grp * KSL + i, dh);
+        qs[i] = t4.x;
+        qs[i + 1] = t4.y;
+        qs[i + 2] = t4.z;
+        qs[i + 3] = t4.w;
+    }
+    f32x4 st[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        st[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const float *kr = A + (16 * t + l16) * KS + grp * KSL;
+#pragma unroll
+        for (int s = 0; s < KSL; s += 4) {
+            const float4 a = lds4(kr + s);
+            st[t] = mfma16(a.x, qs[s], st[t]);
+            st[t] = mfma16(a.y, qs[s + 1], st[t]);
+            st[t] = mfma16(a.z, qs[s + 2], st[t]);
+            st[t] = mfma16(a.w, qs[s + 3], st[t]);
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const uint32_t idx[4] = {ri[t].x, ri[t].y, ri[t].z, ri[t].w};
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            st[t][v] = tau * st[t][v] + rels[idx[v]];
+            mx = fmaxf(mx, st[t][v]);
+        }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const float e = __expf(st[t][v] - mx);
+            st[t][v] = e;
+            sum += e;
+        }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    const float inv = 1.0f / sum;
+    const bool qlive = qi < tq;
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) st[t][v] = qlive ? st[t][v] * inv : 0.f;
+    if (qlive) {
+        float *pr = g.pout + (((long long)img * g.h + hd) * tq + qi) * TK + 4 * grp;
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            *reinterpret_cast<float4 *>(pr + 16 * t) =
+                make_float4(st[t][0], st[t][1], st[t][2], st[t][3]);
+    }
+    __syncthreads();  // every wave is done with the K rows
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int i = tid + 256 * j, r = i / G, c = (i % G) * 4;
+        A[(c + 0) * VS + r] = kv4[j].x;
+        A[(c + 1) * VS + r] = kv4[j].y;
+        A[(c + 2) * VS + r] = kv4[j].z;
+        A[(c + 3) * VS + r] = kv4[j].w;
+    }
+    __syncthreads();
+    const int c = g.h * dh;
+    float *od = g.o + (long long)img * tq * c + (long long)hd * dh;
+#pragma unroll
+    for (int dt = 0; dt < DHP / 16; dt++) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        const float *vr = A + (16 * dt + l16) * VS + 4 * grp;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float4 b = lds4(vr + 16 * t);
+            acc = mfma16(st[t][0], b.x, acc);
+            acc = mfma16(st[t][1], b.y, acc);
+            acc = mfma16(st[t][2], b.z, acc);
+            acc = mfma16(st[t][3], b.w, acc);
+        }
+        const int d = 16 * dt + l16;
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int q = 16 * w + 4 * grp + v;
+            if (q < tq) od[(long long)q * c + d] = acc[v];
+        }
+    }
+}
+
+template <int DHP, int NT>
+constexpr size_t fwd_long_words() {
+    return (size_t)((16 * NT) * (DHP + 4) > DHP * (16 * NT + 4) ? (16 * NT) * (DHP + 4)
+                                                               : DHP * (16 * NT + 4));
 }
 
 // dst[r][d] = old[v] + scale * val[v] (ACC) or scale * val[v] for the 4
@@ -1018,6 +1173,40 @@ void set_lds_limits() {
 }
 
 
+// The fused kernel for a long key axis (attn_fwd_long_kernel), or null:
+// tq <= 64, tk 128 or 256, dh 32 or 64 with float4 accesses, no diagonal
+// mask, the bias slots in LDS beside the tiles (RNN_ATTN_LONG=0: never).
+const void *fwd_long_kernel(const rnn_attn_desc *d, bool vec, size_t *lds) {
+    static const bool on = !(getenv("RNN_ATTN_LONG") && getenv("RNN_ATTN_LONG")[0] == '0');
+    if (!on || !vec || d->mask_diag || d->tq > MAXT || (d->tk != 128 && d->tk != 256) ||
+        (d->dh != 32 && d->dh != 64))
+        return nullptr;
+    const void *k;
+    size_t words;
+    if (d->dh == 64) {
+        k = d->tk == 256 ? (const void *)attn_fwd_long_kernel<64, 16>
+                         : (const void *)attn_fwd_long_kernel<64, 8>;
+        words = d->tk == 256 ? fwd_long_words<64, 16>() : fwd_long_words<64, 8>();
+    } else {
+        k = d->tk == 256 ? (const void *)attn_fwd_long_kernel<32, 16>
+                         : (const void *)attn_fwd_long_kernel<32, 8>;
+        words = d->tk == 256 ? fwd_long_words<32, 16>() : fwd_long_words<32, 8>();
+    }
+    *lds = (words + d->nrel) * 4;
+    if (*lds > 160 * 1024) return nullptr;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        for (const void *f : {(const void *)attn_fwd_long_kernel<64, 16>,
+                              (const void *)attn_fwd_long_kernel<64, 8>,
+                              (const void *)attn_fwd_long_kernel<32, 16>,
+                              (const void *)attn_fwd_long_kernel<32, 8>})
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
+                hipSuccess)
+                (void)hipGetLastError();
+    });
+    return k;
+}
+
 // Core::forward on the composed path (see attn_softmax_rows_kernel).
 int attn_forward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_desc *d, size_t n,
                        const float *q, const float *kv, const float *tau, const float *rel,
@@ -1137,8 +1326,6 @@ int rnn_attn_forward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float
     const RnnRelTable *tab = nullptr;
     rc = rel_table(ctx, d, &tab);
     if (rc) return rc;
-    if (large_desc(d)) return attn_forward_large(ctx, *tab, d, n, q, kv, tau, rel, p, o);
-    set_lds_limits();
     AttnArgs g;
     fill_args(g, *tab, d, n);
     g.q = q;
@@ -1148,6 +1335,18 @@ int rnn_attn_forward(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const float
     g.pout = p;
     g.o = o;
     const bool vec = use_vec(g) && d->tk % 4 == 0 && al16(p);
+    if (large_desc(d)) {
+        size_t llds = 0;
+        if (const void *k = fwd_long_kernel(d, vec, &llds)) {
+            const uint32_t *relidx = tab->dev;
+            void *largs[] = {&g, &relidx};
+            RNN_HIP(ctx, hipLaunchKernel(k, dim3((unsigned)(n * d->h)), dim3(256), largs, llds,
+                                         ctx->stream));
+            return RNN_OK;
+        }
+        return attn_forward_large(ctx, *tab, d, n, q, kv, tau, rel, p, o);
+    }
+    set_lds_limits();
     const int dhp = dhp_of(d->dh), nt = (int)(d->tk + 15) / 16;
     const size_t lds = fwd_lds(dhp, d->nrel);
     if (lds > 160 * 1024)

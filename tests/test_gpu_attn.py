@@ -49,7 +49,11 @@ CASES = [
     ("dh64_t16", 16, 6, 64, 4, 4, 4, 4, "lsa"),
     ("dh64_t64", 8, 4, 64, 8, 8, 8, 8, "lsa"),
     # tq or tk above 64: the composed path (batched GEMMs + row kernels)
+    # tq <= 64 and tk 128 / 256 with dh 32 / 64: one fused workgroup per
+    # (image, head) (attn_fwd_long_kernel) in the forward
     ("cross_tk256", 8, 4, 64, 8, 8, 16, 16, "lsa"),   # the rustvit's cross-attention
+    ("cross_tk128_dh32_tq49", 4, 3, 32, 7, 7, 8, 16, "lsa"),
+    ("cross_tk256_dh32_tq36", 4, 2, 32, 6, 6, 16, 16, "plain"),
     ("self_t100", 4, 2, 48, 10, 10, 10, 10, "lsa"),   # masked self-attention, 100 tokens
     ("cross_tk81_dh80", 3, 2, 80, 3, 3, 9, 9, "lsa"),
 ]
