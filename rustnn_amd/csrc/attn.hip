@@ -733,6 +733,167 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs g) {
     }
 }
 
+// Core::backward's query half for tq <= 64 and tk = 16 NT keys above 64
+// (the rustvit's cross-attention), one workgroup per (image, head), wave w
+// on queries [16w, 16w + 16) as in attn_bwd_kernel's phase 1: dP^T = V dO^T
+// with V's rows in LDS; dS = P o (dP - <dP, P>), written as dS (s1, for the
+// drel gather) and tau dS (s2, for dK = (tau dS)^T Q), both [tq][tk] per
+// (image, head); then dSK = dS K with K^T in LDS over V's rows (K held in
+// registers meanwhile); dQ = tau dSK, set or added (ACC); the (image, head)
+// share of dtau, sum Q . dSK in f64, into part.  dV and dK stay batched GEMMs.
+template <int DHP, int NT, bool ACC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
+attn_bwd_long_q_kernel(AttnArgs g, float *__restrict__ s1, float *__restrict__ s2,
+                       double *__restrict__ part) {
+    constexpr int KSL = DHP / 4, NDT = DHP / 16, TK = 16 * NT, KS = DHP + 4, VS = TK + 4;
+    constexpr int AW = TK * KS > DHP * VS ? TK * KS : DHP * VS;
+    constexpr int G = DHP / 4, CPT = TK * G / 256;
+    static_assert(AW % 2 == 0, "8-byte aligned reduction slots");
+    extern __shared__ float smem[];
+    float *A = smem;                                         // V rows, then K^T
+    double *dred = reinterpret_cast<double *>(smem + AW);    // [4]
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_index();
+    const int l16 = lane & 15, grp = lane >> 4;
+    const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
+    const int tq = g.tq, dh = g.dh, c = g.h * dh;
+    const float *qb = g.q + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
+    const float *kb = g.kv + (long long)img * TK * g.kvstride + g.koff + (long long)hd * dh;
+    const float *vb = g.kv + (long long)img * TK * g.kvstride + g.voff + (long long)hd * dh;
+    const float *ob = g.dout + (long long)img * tq * c + (long long)hd * dh;
+    float *dqi = g.dq + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
+    const int qi = 16 * w + l16, r0 = 16 * w + 4 * grp;
+    const bool qlive = qi < tq;
+    const float tau = g.tau[hd];
+    const long long prow = ((long long)img * g.h + hd) * tq;
+
+    float4 pv4[NT];
+    {
+        const float *pr = g.p + (prow + min(qi, tq - 1)) * TK + 4 * grp;
+#pragma unroll
+        for (int t = 0; t < NT; t++) pv4[t] = *reinterpret_cast<const float4 *>(pr + 16 * t);
+    }
+    float4 oraw[KSL / 4];
+#pragma unroll
+    for (int i = 0; i < KSL; i += 4) oraw[i / 4] = load4<true>(ob, c, qi, tq, grp * KSL + i, dh);
+    float4 kv4[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int i = tid + 256 * j, r = i / G, cc = (i % G) * 4;
+        kv4[j] = load4<true>(vb, g.kvstride, r, TK, cc, dh);
+    }
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int i = tid + 256 * j, r = i / G, cc = (i % G) * 4;
+        *reinterpret_cast<float4 *>(A + r * KS + cc) = kv4[j];
+    }
+    __syncthreads();
+
+    float os[KSL];
+#pragma unroll
+    for (int i = 0; i < KSL; i += 4) {
+        const float4 t4 = mask4(oraw[i / 4], qlive, grp * KSL + i, dh);
+        os[i] = t4.x;
+        os[i + 1] = t4.y;
+        os[i + 2] = t4.z;
+        os[i + 3] = t4.w;
+    }
+    // dP^T = V dO^T (attn.rs:272-278): the score-tile layout of P
+    f32x4 dp[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        dp[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const float *vr = A + (16 * t + l16) * KS + grp * KSL;
+#pragma unroll
+        for (int s = 0; s < KSL; s += 4) {
+            const float4 a = lds4(vr + s);
+            dp[t] = mfma16(a.x, os[s], dp[t]);
+            dp[t] = mfma16(a.y, os[s + 1], dp[t]);
+            dp[t] = mfma16(a.z, os[s + 2], dp[t]);
+            dp[t] = mfma16(a.w, os[s + 3], dp[t]);
+        }
+    }
+    // K next, once dO's slice is dead (the registers are scarce): only dS K
+    // needs it, so its latency overlaps dS and its stores
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int i = tid + 256 * j, r = i / G, cc = (i % G) * 4;
+        kv4[j] = load4<true>(kb, g.kvstride, r, TK, cc, dh);
+    }
+    // dS = P o (dP - <dP, P>) (attn.rs:280-290)
+    float pv[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        pv[t][0] = keep(pv4[t].x, qlive);
+        pv[t][1] = keep(pv4[t].y, qlive);
+        pv[t][2] = keep(pv4[t].z, qlive);
+        pv[t][3] = keep(pv4[t].w, qlive);
+    }
+    float dot = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) dot += dp[t][v] * pv[t][v];
+    dot += __shfl_xor(dot, 16, 64);
+    dot += __shfl_xor(dot, 32, 64);
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+        for (int v = 0; v < 4; v++) dp[t][v] = pv[t][v] * (dp[t][v] - dot);  // dS; 0 where P is 0
+    if (qlive) {
+        float *d1 = s1 + (prow + qi) * TK + 4 * grp, *d2 = s2 + (prow + qi) * TK + 4 * grp;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            *reinterpret_cast<float4 *>(d1 + 16 * t) =
+                make_float4(dp[t][0], dp[t][1], dp[t][2], dp[t][3]);
+            *reinterpret_cast<float4 *>(d2 + 16 * t) =
+                make_float4(dp[t][0] * tau, dp[t][1] * tau, dp[t][2] * tau, dp[t][3] * tau);
+        }
+    }
+    __syncthreads();  // every wave is done with V's rows
+#pragma unroll
+    for (int j = 0; j < CPT; j++) {
+        const int i = tid + 256 * j, r = i / G, cc = (i % G) * 4;
+        A[(cc + 0) * VS + r] = kv4[j].x;
+        A[(cc + 1) * VS + r] = kv4[j].y;
+        A[(cc + 2) * VS + r] = kv4[j].z;
+        A[(cc + 3) * VS + r] = kv4[j].w;
+    }
+    // Q (for dtau) and the old dQ: loaded late, the registers are scarce
+    float oq[NDT][4], qv[NDT][4];
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) {
+        if constexpr (ACC) old4(oq[dt], dqi, g.qstride, r0, tq, 16 * dt + l16, dh);
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            qv[dt][v] = qb[(long long)min(r0 + v, tq - 1) * g.qstride + 16 * dt + l16];
+    }
+    __syncthreads();
+    // dSK = dS K (attn.rs:316-323, before the tau scaling); dQ = tau dSK;
+    // dtau += Q . dSK
+    double tpart = 0.0;
+#pragma unroll
+    for (int dt = 0; dt < NDT; dt++) {
+        f32x4 dsk = {0.f, 0.f, 0.f, 0.f};
+        const float *kr = A + (16 * dt + l16) * VS + 4 * grp;
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const float4 b = lds4(kr + 16 * t);
+            dsk = mfma16(dp[t][0], b.x, dsk);
+            dsk = mfma16(dp[t][1], b.y, dsk);
+            dsk = mfma16(dp[t][2], b.z, dsk);
+            dsk = mfma16(dp[t][3], b.w, dsk);
+        }
+        tpart += (double)(dsk[0] * qv[dt][0]) + (double)(dsk[1] * qv[dt][1]) +
+                 (double)(dsk[2] * qv[dt][2]) + (double)(dsk[3] * qv[dt][3]);
+        store4<ACC>(dqi, g.qstride, r0, tq, 16 * dt + l16, dh, oq[dt], dsk, tau);
+    }
+    tpart = wave_sum_d(tpart);
+    if (lane == 0) dred[w] = tpart;
+    __syncthreads();
+    if (tid == 0) part[(long long)img * g.h + hd] = ((dred[0] + dred[1]) + dred[2]) + dred[3];
+}
+
 // dtau[h] += sum_img part[img][h]; drel[h*nrel + r] += sum_img part[img][h][r]
 // (image order, attn.rs:333-342).  A block takes 32 elements; thread (j, e)
 // sums images [j*G, j*G + G) of element e with the loads issued ahead of the
@@ -1207,6 +1368,45 @@ const void *fwd_long_kernel(const rnn_attn_desc *d, bool vec, size_t *lds) {
     return k;
 }
 
+// The fused query half of the backward for a long key axis
+// (attn_bwd_long_q_kernel), or null: the forward's conditions.
+const void *bwd_long_kernel(const rnn_attn_desc *d, bool vec, bool acc, size_t *lds) {
+    static const bool on = !(getenv("RNN_ATTN_LONG") && getenv("RNN_ATTN_LONG")[0] == '0');
+    if (!on || !vec || d->mask_diag || d->tq > MAXT || (d->tk != 128 && d->tk != 256) ||
+        (d->dh != 32 && d->dh != 64))
+        return nullptr;
+    const void *k;
+    size_t words;
+#define RNN_BWD_LONG(DH_, NT_)                                                                  \
+    (acc ? (const void *)attn_bwd_long_q_kernel<DH_, NT_, true>                                 \
+         : (const void *)attn_bwd_long_q_kernel<DH_, NT_, false>)
+    if (d->dh == 64) {
+        k = d->tk == 256 ? RNN_BWD_LONG(64, 16) : RNN_BWD_LONG(64, 8);
+        words = d->tk == 256 ? fwd_long_words<64, 16>() : fwd_long_words<64, 8>();
+    } else {
+        k = d->tk == 256 ? RNN_BWD_LONG(32, 16) : RNN_BWD_LONG(32, 8);
+        words = d->tk == 256 ? fwd_long_words<32, 16>() : fwd_long_words<32, 8>();
+    }
+    *lds = words * 4 + 4 * sizeof(double);
+    if (*lds > 160 * 1024) return nullptr;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        for (const void *f : {(const void *)attn_bwd_long_q_kernel<64, 16, true>,
+                              (const void *)attn_bwd_long_q_kernel<64, 16, false>,
+                              (const void *)attn_bwd_long_q_kernel<64, 8, true>,
+                              (const void *)attn_bwd_long_q_kernel<64, 8, false>,
+                              (const void *)attn_bwd_long_q_kernel<32, 16, true>,
+                              (const void *)attn_bwd_long_q_kernel<32, 16, false>,
+                              (const void *)attn_bwd_long_q_kernel<32, 8, true>,
+                              (const void *)attn_bwd_long_q_kernel<32, 8, false>})
+            if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
+                hipSuccess)
+                (void)hipGetLastError();
+    });
+#undef RNN_BWD_LONG
+    return k;
+}
+
 // Core::forward on the composed path (see attn_softmax_rows_kernel).
 int attn_forward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_desc *d, size_t n,
                        const float *q, const float *kv, const float *tau, const float *rel,
@@ -1273,21 +1473,42 @@ int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_des
     int rc = rnn_gemm_launch_ld2(ctx, n, h, tk, dh, tq, p, tk, h * cnt, cnt, 1, dout, c, tq * c,
                                  dh, 0, dkv + d->voff, d->kvstride, tk * d->kvstride, dh, acc_kv);
     if (rc) return rc;
-    // dP = dO V^T (attn.rs:272-278)
-    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, dout, c, tq * c, dh, 0, kv + d->voff,
-                             d->kvstride, tk * d->kvstride, dh, 1, s1, tk, h * cnt, cnt, 0);
-    if (rc) return rc;
-    // the raw scores again (attn.rs:292-300)
-    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, q + d->qoff, d->qstride, tq * d->qstride, dh,
-                             0, kv + d->koff, d->kvstride, tk * d->kvstride, dh, 1, s2, tk,
-                             h * cnt, cnt, 0);
-    if (rc) return rc;
-    attn_dsoft_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
-        p, s1, s2, tau, part, rows, (int)h, (int)tq, (int)tk);
-    RNN_LAUNCHED(ctx);
-    attn_head_sum_kernel<<<(unsigned)h, 256, 0, ctx->stream>>>(part, (long long)n, (int)h,
-                                                              (int)tq, dtau);
-    RNN_LAUNCHED(ctx);
+    AttnArgs g;
+    fill_args(g, tab, d, n);
+    g.q = q;
+    g.kv = kv;
+    g.tau = tau;
+    g.p = p;
+    g.dout = dout;
+    g.dq = dq;
+    g.dkv = dkv;
+    size_t llds = 0;
+    const void *lk = bwd_long_kernel(d, use_vec(g) && tk % 4 == 0 && al16(p), acc_q != 0, &llds);
+    if (lk) {
+        // dS, tau dS, dQ and the dtau shares in one fused launch
+        void *args[] = {&g, &s1, &s2, &part};
+        RNN_HIP(ctx, hipLaunchKernel(lk, dim3((unsigned)(n * h)), dim3(256), args, llds,
+                                     ctx->stream));
+        attn_head_sum_kernel<<<(unsigned)h, 256, 0, ctx->stream>>>(part, (long long)n, (int)h, 1,
+                                                                  dtau);
+        RNN_LAUNCHED(ctx);
+    } else {
+        // dP = dO V^T (attn.rs:272-278)
+        rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, dout, c, tq * c, dh, 0, kv + d->voff,
+                                 d->kvstride, tk * d->kvstride, dh, 1, s1, tk, h * cnt, cnt, 0);
+        if (rc) return rc;
+        // the raw scores again (attn.rs:292-300)
+        rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, q + d->qoff, d->qstride, tq * d->qstride,
+                                 dh, 0, kv + d->koff, d->kvstride, tk * d->kvstride, dh, 1, s2, tk,
+                                 h * cnt, cnt, 0);
+        if (rc) return rc;
+        attn_dsoft_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
+            p, s1, s2, tau, part, rows, (int)h, (int)tq, (int)tk);
+        RNN_LAUNCHED(ctx);
+        attn_head_sum_kernel<<<(unsigned)h, 256, 0, ctx->stream>>>(part, (long long)n, (int)h,
+                                                                  (int)tq, dtau);
+        RNN_LAUNCHED(ctx);
+    }
     attn_drel_part_kernel<<<dim3((unsigned)rnn_div_up(per, (size_t)256), (unsigned)nchunk), 256,
                             0, ctx->stream>>>(s1, tab.dev + cnt,
                                               tab.dev + cnt + d->nrel + 1, (long long)n,
@@ -1298,10 +1519,12 @@ int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_des
         rpart, (int)nchunk, (long long)per, drel);
     RNN_LAUNCHED(ctx);
     // dQ += (tau dS) K (attn.rs:317-322)
-    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, dh, tk, s2, tk, h * cnt, cnt, 0, kv + d->koff,
-                             d->kvstride, tk * d->kvstride, dh, 0, dq + d->qoff, d->qstride,
-                             tq * d->qstride, dh, acc_q);
-    if (rc) return rc;
+    if (!lk) {
+        rc = rnn_gemm_launch_ld2(ctx, n, h, tq, dh, tk, s2, tk, h * cnt, cnt, 0, kv + d->koff,
+                                 d->kvstride, tk * d->kvstride, dh, 0, dq + d->qoff, d->qstride,
+                                 tq * d->qstride, dh, acc_q);
+        if (rc) return rc;
+    }
     // dK += (tau dS)^T Q (attn.rs:324-330)
     return rnn_gemm_launch_ld2(ctx, n, h, tk, dh, tq, s2, tk, h * cnt, cnt, 1, q + d->qoff,
                                d->qstride, tq * d->qstride, dh, 0, dkv + d->koff, d->kvstride,
