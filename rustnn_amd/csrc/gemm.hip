@@ -441,13 +441,42 @@ __global__ __launch_bounds__(512) void gemm_dma_kernel(GemmArgs g) {
         }
     }
     float *Cp = g.c + zoff(g, z, g.stride_c, g.stride_c2);
+    if (g.acc) {
+        // eight old values at a time loaded (from clamped addresses) before
+        // their stores, so the loads are in flight together rather than each
+        // waiting behind the stores before it (eight: the registers keep
+        // three 64 x 64 workgroups a CU)
+        constexpr int TOT = Tile::TM * Tile::TN * 16;
+#pragma unroll
+        for (int h = 0; h < TOT / 8; h++) {
+            float old[8];
+            int e = 0;
+            t.each([&](int r, int c, float) {
+                if (e >= 8 * h && e < 8 * h + 8) {
+                    const int row = min(m0 + r, g.M - 1), col = min(n0 + c, g.N - 1);
+                    old[e - 8 * h] = Cp[(long long)row * g.ldc + col];
+                }
+                e++;
+            });
+            e = 0;
+            t.each([&](int r, int c, float val) {
+                if (e >= 8 * h && e < 8 * h + 8) {
+                    const int row = m0 + r, col = n0 + c;
+                    if (row < g.M && col < g.N) {
+                        if (g.bias) val += g.bias[col];
+                        Cp[(long long)row * g.ldc + col] = old[e - 8 * h] + val;
+                    }
+                }
+                e++;
+            });
+        }
+        return;
+    }
     t.each([&](int r, int c, float val) {
         const int row = m0 + r, col = n0 + c;
         if (row < g.M && col < g.N) {
             if (g.bias) val += g.bias[col];
-            float *cp = Cp + (long long)row * g.ldc + col;
-            if (g.acc) val = *cp + val;
-            *cp = val;
+            Cp[(long long)row * g.ldc + col] = val;
         }
     });
 }
