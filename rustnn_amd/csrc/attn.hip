@@ -443,6 +443,13 @@ attn_fwd_long_kernel(AttnArgs g, const uint32_t *__restrict__ relidx) {
 }
 
 template <int DHP, int NT>
+constexpr size_t bwd_long_words() {
+    return (size_t)(16 * NT) * (DHP + 4) > (size_t)DHP * (16 * NT + 4)
+               ? std::max<size_t>((size_t)(16 * NT) * (DHP + 4), (size_t)MAXT * 16 * NT)
+               : std::max<size_t>((size_t)DHP * (16 * NT + 4), (size_t)MAXT * 16 * NT);
+}
+
+template <int DHP, int NT>
 constexpr size_t fwd_long_words() {
     return (size_t)((16 * NT) * (DHP + 4) > DHP * (16 * NT + 4) ? (16 * NT) * (DHP + 4)
                                                                : DHP * (16 * NT + 4));
@@ -736,17 +743,19 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs g) {
 // Core::backward's query half for tq <= 64 and tk = 16 NT keys above 64
 // (the rustvit's cross-attention), one workgroup per (image, head), wave w
 // on queries [16w, 16w + 16) as in attn_bwd_kernel's phase 1: dP^T = V dO^T
-// with V's rows in LDS; dS = P o (dP - <dP, P>), written as dS (s1, for the
-// drel gather) and tau dS (s2, for dK = (tau dS)^T Q), both [tq][tk] per
-// (image, head); then dSK = dS K with K^T in LDS over V's rows (K held in
-// registers meanwhile); dQ = tau dSK, set or added (ACC); the (image, head)
-// share of dtau, sum Q . dSK in f64, into part.  dV and dK stay batched GEMMs.
+// with V's rows in LDS; dS = P o (dP - <dP, P>), with tau dS written to s2
+// ([tq][tk] per (image, head)) for the key half (attn_bwd_long_k_kernel);
+// then dSK = dS K with K^T in LDS over V's rows (K held in registers
+// meanwhile); dQ = tau dSK, set or added (ACC); the (image, head) shares of
+// dtau (sum Q . dSK, f64) and of drel (dS staged in LDS [tq][tk] over K^T and
+// gathered through the inverse index, each slot's positions in ascending
+// order) into g.dtau_part / g.drel_part.
 template <int DHP, int NT, bool ACC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void
-attn_bwd_long_q_kernel(AttnArgs g, float *__restrict__ s1, float *__restrict__ s2,
-                       double *__restrict__ part) {
+attn_bwd_long_q_kernel(AttnArgs g, float *__restrict__ s2) {
     constexpr int KSL = DHP / 4, NDT = DHP / 16, TK = 16 * NT, KS = DHP + 4, VS = TK + 4;
-    constexpr int AW = TK * KS > DHP * VS ? TK * KS : DHP * VS;
+    constexpr int AW0 = TK * KS > DHP * VS ? TK * KS : DHP * VS;
+    constexpr int AW = AW0 > MAXT * TK ? AW0 : MAXT * TK;  // also dS [64][tk]
     constexpr int G = DHP / 4, CPT = TK * G / 256;
     static_assert(AW % 2 == 0, "8-byte aligned reduction slots");
     extern __shared__ float smem[];
@@ -841,14 +850,11 @@ attn_bwd_long_q_kernel(AttnArgs g, float *__restrict__ s1, float *__restrict__ s
 #pragma unroll
         for (int v = 0; v < 4; v++) dp[t][v] = pv[t][v] * (dp[t][v] - dot);  // dS; 0 where P is 0
     if (qlive) {
-        float *d1 = s1 + (prow + qi) * TK + 4 * grp, *d2 = s2 + (prow + qi) * TK + 4 * grp;
+        float *d2 = s2 + (prow + qi) * TK + 4 * grp;
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            *reinterpret_cast<float4 *>(d1 + 16 * t) =
-                make_float4(dp[t][0], dp[t][1], dp[t][2], dp[t][3]);
+        for (int t = 0; t < NT; t++)
             *reinterpret_cast<float4 *>(d2 + 16 * t) =
                 make_float4(dp[t][0] * tau, dp[t][1] * tau, dp[t][2] * tau, dp[t][3] * tau);
-        }
     }
     __syncthreads();  // every wave is done with V's rows
 #pragma unroll
@@ -890,8 +896,126 @@ attn_bwd_long_q_kernel(AttnArgs g, float *__restrict__ s1, float *__restrict__ s
     }
     tpart = wave_sum_d(tpart);
     if (lane == 0) dred[w] = tpart;
+    __syncthreads();  // every wave is done with K^T; the dtau shares are in dred
+    if (tid == 0)
+        g.dtau_part[(long long)img * g.h + hd] = ((dred[0] + dred[1]) + dred[2]) + dred[3];
+    // dS in LDS as [tq][tk] (position q*tk + k, as the inverse index numbers
+    // them), then drel's share of every bias slot (attn.rs:309-315)
+    if (qlive) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            *reinterpret_cast<float4 *>(A + qi * TK + 16 * t + 4 * grp) =
+                make_float4(dp[t][0], dp[t][1], dp[t][2], dp[t][3]);
+    }
     __syncthreads();
-    if (tid == 0) part[(long long)img * g.h + hd] = ((dred[0] + dred[1]) + dred[2]) + dred[3];
+    float *drp = g.drel_part + ((long long)img * g.h + hd) * g.nrel;
+    for (int r = tid; r < g.nrel; r += 256) {
+        const uint32_t e0 = g.rowptr[r], e1 = g.rowptr[r + 1];
+        float sacc = 0.f;
+        for (uint32_t e = e0; e < e1; e += 8) {
+            uint32_t off[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) off[u] = g.pos[min(e + u, e1 - 1)];
+            float val[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) val[u] = A[off[u]];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (e + u < e1) sacc += val[u];
+        }
+        drp[r] = sacc;
+    }
+}
+
+// Core::backward's key half for the same shapes: dV = P^T dO and
+// dK = (tau dS)^T Q over the (image, head)'s queries, set or added (ACC);
+// wave w on keys [TK/4 w, TK/4 (w + 1)), 16 at a time, as attn_bwd_kernel's
+// phase 2: dO^T and Q^T staged in LDS, the A operands (P and tau dS for the
+// lane's key and four queries) read from HBM.
+template <int DHP, int NT, bool ACC>
+__global__ __launch_bounds__(256) void attn_bwd_long_k_kernel(AttnArgs g,
+                                                              const float *__restrict__ s2) {
+    constexpr int NDT = DHP / 16, TK = 16 * NT, KPW = NT / 4;  // key tiles a wave
+    extern __shared__ float smem[];
+    float *Qt = smem;            // [DHP][TS]
+    float *Ot = Qt + DHP * TS;   // [DHP][TS] dO^T
+    const int tid = threadIdx.x, lane = tid & 63, w = wave_index();
+    const int l16 = lane & 15, grp = lane >> 4;
+    const int img = blockIdx.x / g.h, hd = blockIdx.x % g.h;
+    const int tq = g.tq, dh = g.dh, c = g.h * dh;
+    const int QT = (tq + 15) >> 4;
+    const float *qb = g.q + (long long)img * tq * g.qstride + g.qoff + (long long)hd * dh;
+    const float *ob = g.dout + (long long)img * tq * c + (long long)hd * dh;
+    float *dki = g.dkv + (long long)img * TK * g.kvstride + g.koff + (long long)hd * dh;
+    float *dvi = g.dkv + (long long)img * TK * g.kvstride + g.voff + (long long)hd * dh;
+    const long long prow = ((long long)img * g.h + hd) * tq;
+    const float *pb = g.p + prow * TK, *sb = s2 + prow * TK;
+    Tile<DHP> ot, qt;
+    ot.template load<true>(ob, c, tq, dh, tid);
+    qt.template load<true>(qb, g.qstride, tq, dh, tid);
+    ot.template store<true>(Ot, tq, dh, tid);
+    qt.template store<true>(Qt, tq, dh, tid);
+    __syncthreads();
+#pragma unroll 1
+    for (int kt = 0; kt < KPW; kt++) {
+        const int k0 = 16 * (KPW * w + kt), kr = k0 + l16, r0 = k0 + 4 * grp;
+        float ov[NDT][4], ok[NDT][4];
+        if constexpr (ACC) {
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                old4(ov[dt], dvi, g.kvstride, r0, TK, 16 * dt + l16, dh);
+                old4(ok[dt], dki, g.kvstride, r0, TK, 16 * dt + l16, dh);
+            }
+        }
+        // the lane's key, queries 16 ta + 4 grp + v (rows past tq read row
+        // tq - 1 and are zeroed)
+        float pa[4][4], sa[4][4];
+#pragma unroll
+        for (int ta = 0; ta < 4; ta++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int q = 16 * ta + 4 * grp + v;
+                const long long o = (long long)min(q, tq - 1) * TK + kr;
+                pa[ta][v] = pb[o];
+                sa[ta][v] = sb[o];
+            }
+        f32x4 av[NDT], ak[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            av[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            ak[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int ta = 0; ta < 4; ta++) {
+            if (ta >= QT) break;
+            const int q0 = 16 * ta + 4 * grp;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                pa[ta][v] = keep(pa[ta][v], q0 + v < tq);
+                sa[ta][v] = keep(sa[ta][v], q0 + v < tq);
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) {
+                const int d = 16 * dt + l16;
+                const float4 ob4 = lds4(Ot + d * TS + q0);
+                const float4 qb4 = lds4(Qt + d * TS + q0);
+                av[dt] = mfma16(pa[ta][0], ob4.x, av[dt]);
+                ak[dt] = mfma16(sa[ta][0], qb4.x, ak[dt]);
+                av[dt] = mfma16(pa[ta][1], ob4.y, av[dt]);
+                ak[dt] = mfma16(sa[ta][1], qb4.y, ak[dt]);
+                av[dt] = mfma16(pa[ta][2], ob4.z, av[dt]);
+                ak[dt] = mfma16(sa[ta][2], qb4.z, ak[dt]);
+                av[dt] = mfma16(pa[ta][3], ob4.w, av[dt]);
+                ak[dt] = mfma16(sa[ta][3], qb4.w, ak[dt]);
+            }
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) {
+            const int d = 16 * dt + l16;
+            store4<ACC>(dvi, g.kvstride, r0, TK, d, dh, ov[dt], av[dt], 1.0f);
+            store4<ACC>(dki, g.kvstride, r0, TK, d, dh, ok[dt], ak[dt], 1.0f);
+        }
+    }
 }
 
 // dtau[h] += sum_img part[img][h]; drel[h*nrel + r] += sum_img part[img][h][r]
@@ -1368,27 +1492,39 @@ const void *fwd_long_kernel(const rnn_attn_desc *d, bool vec, size_t *lds) {
     return k;
 }
 
-// The fused query half of the backward for a long key axis
-// (attn_bwd_long_q_kernel), or null: the forward's conditions.
-const void *bwd_long_kernel(const rnn_attn_desc *d, bool vec, bool acc, size_t *lds) {
+// The fused backward for a long key axis under the forward's conditions:
+// the query half (acc_q: dQ added) and the key half (acc_kv: dK, dV added)
+// with their LDS bytes, or nulls.
+struct LongBwd {
+    const void *qk = nullptr, *kk = nullptr;
+    size_t qlds = 0, klds = 0;
+};
+LongBwd bwd_long_kernels(const rnn_attn_desc *d, bool vec, bool acc_q, bool acc_kv) {
     static const bool on = !(getenv("RNN_ATTN_LONG") && getenv("RNN_ATTN_LONG")[0] == '0');
+    LongBwd r;
     if (!on || !vec || d->mask_diag || d->tq > MAXT || (d->tk != 128 && d->tk != 256) ||
         (d->dh != 32 && d->dh != 64))
-        return nullptr;
-    const void *k;
+        return r;
     size_t words;
-#define RNN_BWD_LONG(DH_, NT_)                                                                  \
-    (acc ? (const void *)attn_bwd_long_q_kernel<DH_, NT_, true>                                 \
-         : (const void *)attn_bwd_long_q_kernel<DH_, NT_, false>)
-    if (d->dh == 64) {
-        k = d->tk == 256 ? RNN_BWD_LONG(64, 16) : RNN_BWD_LONG(64, 8);
-        words = d->tk == 256 ? fwd_long_words<64, 16>() : fwd_long_words<64, 8>();
+#define RNN_LONG_PAIR(DH_, NT_)                                                                 \
+    r.qk = acc_q ? (const void *)attn_bwd_long_q_kernel<DH_, NT_, true>                         \
+                 : (const void *)attn_bwd_long_q_kernel<DH_, NT_, false>;                       \
+    r.kk = acc_kv ? (const void *)attn_bwd_long_k_kernel<DH_, NT_, true>                        \
+                  : (const void *)attn_bwd_long_k_kernel<DH_, NT_, false>;                      \
+    words = bwd_long_words<DH_, NT_>();                                                         \
+    r.klds = (size_t)2 * DH_ * TS * 4;
+    if (d->dh == 64 && d->tk == 256) {
+        RNN_LONG_PAIR(64, 16)
+    } else if (d->dh == 64) {
+        RNN_LONG_PAIR(64, 8)
+    } else if (d->tk == 256) {
+        RNN_LONG_PAIR(32, 16)
     } else {
-        k = d->tk == 256 ? RNN_BWD_LONG(32, 16) : RNN_BWD_LONG(32, 8);
-        words = d->tk == 256 ? fwd_long_words<32, 16>() : fwd_long_words<32, 8>();
+        RNN_LONG_PAIR(32, 8)
     }
-    *lds = words * 4 + 4 * sizeof(double);
-    if (*lds > 160 * 1024) return nullptr;
+#undef RNN_LONG_PAIR
+    r.qlds = words * 4 + 4 * sizeof(double);
+    if (r.qlds > 160 * 1024) return LongBwd{};
     static std::once_flag once;
     std::call_once(once, [] {
         for (const void *f : {(const void *)attn_bwd_long_q_kernel<64, 16, true>,
@@ -1403,8 +1539,7 @@ const void *bwd_long_kernel(const rnn_attn_desc *d, bool vec, bool acc, size_t *
                 hipSuccess)
                 (void)hipGetLastError();
     });
-#undef RNN_BWD_LONG
-    return k;
+    return r;
 }
 
 // Core::forward on the composed path (see attn_softmax_rows_kernel).
@@ -1456,6 +1591,58 @@ int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_des
     const size_t cnt = tq * tk, mat = n * h * cnt;
     const long long rows = (long long)n * h * tq;
     const size_t per = h * d->nrel;
+    AttnArgs g;
+    fill_args(g, tab, d, n);
+    g.q = q;
+    g.kv = kv;
+    g.tau = tau;
+    g.p = p;
+    g.dout = dout;
+    g.dq = dq;
+    g.dkv = dkv;
+    const LongBwd lb = bwd_long_kernels(d, use_vec(g) && tk % 4 == 0 && al16(p), acc_q != 0,
+                                        acc_kv != 0);
+    if (lb.qk) {
+        // two fused launches, then the dtau / drel partials summed over the
+        // images in image order (deferred with the context's other
+        // parameter-gradient reductions when it defers them)
+        const size_t tau_bytes = rnn_round_up(n * h * sizeof(double), 256);
+        const size_t part_bytes = tau_bytes + n * per * sizeof(float);
+        WsCarve cv;
+        const size_t o_s2 = cv.take(mat * 4), o_pw = ctx->defer ? 0 : cv.take(part_bytes);
+        char *ws = (char *)rnn_workspace(ctx, cv.off);
+        if (!ws) return RNN_E_NOMEM;
+        float *s2 = (float *)(ws + o_s2);
+        char *pw = ctx->defer ? (char *)rnn_defer_take(ctx, part_bytes) : ws + o_pw;
+        if (!pw) return RNN_E_NOMEM;
+        g.dtau_part = (double *)pw;
+        g.drel_part = (float *)(pw + tau_bytes);
+        void *qargs[] = {&g, &s2};
+        RNN_HIP(ctx, hipLaunchKernel(lb.qk, dim3((unsigned)(n * h)), dim3(256), qargs, lb.qlds,
+                                     ctx->stream));
+        void *kargs[] = {&g, &s2};
+        RNN_HIP(ctx, hipLaunchKernel(lb.kk, dim3((unsigned)(n * h)), dim3(256), kargs, lb.klds,
+                                     ctx->stream));
+        const int tot = (int)(per + h);
+        if (ctx->defer) {
+            RnnDeferSeg sg{};
+            sg.part = g.dtau_part;
+            sg.part2 = g.drel_part;
+            sg.out0 = drel;
+            sg.out1 = dtau;
+            sg.len = tot;
+            sg.split = (long long)per;
+            sg.nrow = (int)n;
+            sg.kind = RNN_DEFER_ATTN;
+            rnn_defer_push(ctx, sg);
+            return RNN_OK;
+        }
+        hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)rnn_div_up(tot, 32)), dim3(256), 0,
+                           ctx->stream, (const double *)g.dtau_part, (const float *)g.drel_part,
+                           (int)n, (int)h, (int)d->nrel, dtau, drel);
+        RNN_LAUNCHED(ctx);
+        return RNN_OK;
+    }
     // drel partials over chunks of ipc images: enough chunks to fill the
     // chip (16 chunks left it latency-bound: 61 us a call at the rustvit's
     // cross-attention shape)
@@ -1473,42 +1660,21 @@ int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_des
     int rc = rnn_gemm_launch_ld2(ctx, n, h, tk, dh, tq, p, tk, h * cnt, cnt, 1, dout, c, tq * c,
                                  dh, 0, dkv + d->voff, d->kvstride, tk * d->kvstride, dh, acc_kv);
     if (rc) return rc;
-    AttnArgs g;
-    fill_args(g, tab, d, n);
-    g.q = q;
-    g.kv = kv;
-    g.tau = tau;
-    g.p = p;
-    g.dout = dout;
-    g.dq = dq;
-    g.dkv = dkv;
-    size_t llds = 0;
-    const void *lk = bwd_long_kernel(d, use_vec(g) && tk % 4 == 0 && al16(p), acc_q != 0, &llds);
-    if (lk) {
-        // dS, tau dS, dQ and the dtau shares in one fused launch
-        void *args[] = {&g, &s1, &s2, &part};
-        RNN_HIP(ctx, hipLaunchKernel(lk, dim3((unsigned)(n * h)), dim3(256), args, llds,
-                                     ctx->stream));
-        attn_head_sum_kernel<<<(unsigned)h, 256, 0, ctx->stream>>>(part, (long long)n, (int)h, 1,
-                                                                  dtau);
-        RNN_LAUNCHED(ctx);
-    } else {
-        // dP = dO V^T (attn.rs:272-278)
-        rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, dout, c, tq * c, dh, 0, kv + d->voff,
-                                 d->kvstride, tk * d->kvstride, dh, 1, s1, tk, h * cnt, cnt, 0);
-        if (rc) return rc;
-        // the raw scores again (attn.rs:292-300)
-        rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, q + d->qoff, d->qstride, tq * d->qstride,
-                                 dh, 0, kv + d->koff, d->kvstride, tk * d->kvstride, dh, 1, s2, tk,
-                                 h * cnt, cnt, 0);
-        if (rc) return rc;
-        attn_dsoft_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
-            p, s1, s2, tau, part, rows, (int)h, (int)tq, (int)tk);
-        RNN_LAUNCHED(ctx);
-        attn_head_sum_kernel<<<(unsigned)h, 256, 0, ctx->stream>>>(part, (long long)n, (int)h,
-                                                                  (int)tq, dtau);
-        RNN_LAUNCHED(ctx);
-    }
+    // dP = dO V^T (attn.rs:272-278)
+    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, dout, c, tq * c, dh, 0, kv + d->voff,
+                             d->kvstride, tk * d->kvstride, dh, 1, s1, tk, h * cnt, cnt, 0);
+    if (rc) return rc;
+    // the raw scores again (attn.rs:292-300)
+    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, tk, dh, q + d->qoff, d->qstride, tq * d->qstride, dh,
+                             0, kv + d->koff, d->kvstride, tk * d->kvstride, dh, 1, s2, tk,
+                             h * cnt, cnt, 0);
+    if (rc) return rc;
+    attn_dsoft_rows_kernel<<<(unsigned)rnn_div_up((size_t)rows, 4), 256, 0, ctx->stream>>>(
+        p, s1, s2, tau, part, rows, (int)h, (int)tq, (int)tk);
+    RNN_LAUNCHED(ctx);
+    attn_head_sum_kernel<<<(unsigned)h, 256, 0, ctx->stream>>>(part, (long long)n, (int)h,
+                                                              (int)tq, dtau);
+    RNN_LAUNCHED(ctx);
     attn_drel_part_kernel<<<dim3((unsigned)rnn_div_up(per, (size_t)256), (unsigned)nchunk), 256,
                             0, ctx->stream>>>(s1, tab.dev + cnt,
                                               tab.dev + cnt + d->nrel + 1, (long long)n,
@@ -1519,12 +1685,10 @@ int attn_backward_large(rnn_ctx *ctx, const RnnRelTable &tab, const rnn_attn_des
         rpart, (int)nchunk, (long long)per, drel);
     RNN_LAUNCHED(ctx);
     // dQ += (tau dS) K (attn.rs:317-322)
-    if (!lk) {
-        rc = rnn_gemm_launch_ld2(ctx, n, h, tq, dh, tk, s2, tk, h * cnt, cnt, 0, kv + d->koff,
-                                 d->kvstride, tk * d->kvstride, dh, 0, dq + d->qoff, d->qstride,
-                                 tq * d->qstride, dh, acc_q);
-        if (rc) return rc;
-    }
+    rc = rnn_gemm_launch_ld2(ctx, n, h, tq, dh, tk, s2, tk, h * cnt, cnt, 0, kv + d->koff,
+                             d->kvstride, tk * d->kvstride, dh, 0, dq + d->qoff, d->qstride,
+                             tq * d->qstride, dh, acc_q);
+    if (rc) return rc;
     // dK += (tau dS)^T Q (attn.rs:324-330)
     return rnn_gemm_launch_ld2(ctx, n, h, tk, dh, tq, s2, tk, h * cnt, cnt, 1, q + d->qoff,
                                d->qstride, tq * d->qstride, dh, 0, dkv + d->koff, d->kvstride,
