@@ -234,6 +234,14 @@ int rnn_attn_backward_ex(rnn_ctx *ctx, const rnn_attn_desc *d, size_t n, const f
 /* Linear::forward (linear.rs:44-63): y[rows x fout] = x W^T + b (b may be NULL). */
 int rnn_linear_forward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *x,
                        const float *w, const float *b, float *y);
+/* Linear::forward feeding a residual branch (vit.rs:155-176): y = x W^T + b
+ * as rnn_linear_forward, and out += (y l) m with m = mask[r / rpi] (mask may
+ * be NULL: m = 1) -- rnn_residual_add_scaled(out, y, ...) -- in the GEMM's
+ * epilogue (two passes when rpi is not a power of two).  out is neither x
+ * nor y. */
+int rnn_linear_forward_residual(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout,
+                                const float *x, const float *w, const float *b, float *y,
+                                const float *l, const float *mask, size_t rpi, float *out);
 /* Linear::backward (linear.rs:66-96): dw += dy^T x; db += colsum(dy) (db may
  * be NULL); dx = dy W (overwritten). */
 int rnn_linear_backward(rnn_ctx *ctx, size_t rows, size_t fin, size_t fout, const float *dy,

@@ -127,6 +127,7 @@ extern "C" {
     pub fn rnn_attn_backward(ctx: *mut rnn_ctx, d: *const rnn_attn_desc, n: usize, q: *const f32, kv: *const f32, tau: *const f32, p: *const f32, dout: *const f32, dq: *mut f32, dkv: *mut f32, dtau: *mut f32, drel: *mut f32) -> c_int;
     pub fn rnn_attn_backward_ex(ctx: *mut rnn_ctx, d: *const rnn_attn_desc, n: usize, q: *const f32, kv: *const f32, tau: *const f32, p: *const f32, dout: *const f32, dq: *mut f32, dkv: *mut f32, dtau: *mut f32, drel: *mut f32, flags: u32) -> c_int;
     pub fn rnn_linear_forward(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, x: *const f32, w: *const f32, b: *const f32, y: *mut f32) -> c_int;
+    pub fn rnn_linear_forward_residual(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, x: *const f32, w: *const f32, b: *const f32, y: *mut f32, l: *const f32, mask: *const f32, rpi: usize, out: *mut f32) -> c_int;
     pub fn rnn_linear_backward(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, dy: *const f32, x: *const f32, w: *const f32, dw: *mut f32, db: *mut f32, dx: *mut f32) -> c_int;
     pub fn rnn_linear_backward_ex(ctx: *mut rnn_ctx, rows: usize, fin: usize, fout: usize, dy: *const f32, x: *const f32, w: *const f32, dw: *mut f32, db: *mut f32, dx: *mut f32, flags: u32) -> c_int;
     pub fn rnn_matmul_host(ctx: *mut rnn_ctx, m: usize, n: usize, k: usize, a: *const f32, at: c_int, b: *const f32, bt: c_int, c: *mut f32, acc: c_int) -> c_int;

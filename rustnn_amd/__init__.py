@@ -137,6 +137,8 @@ def lib():
             "rnn_attn_backward_ex": (_i, [_vp, P(AttnDesc), _sz, _vp, _vp, _vp, _vp, _vp, _vp,
                                           _vp, _vp, _vp, _u32]),
             "rnn_linear_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+            "rnn_linear_forward_residual": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp,
+                                                 _vp, _sz, _vp]),
             "rnn_linear_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_linear_backward_ex": (_i, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
                                             _u32]),
@@ -680,6 +682,19 @@ def linear_forward(rows, fin, fout, x, w, b=None, y=None, ctx=None):
     return y
 
 
+def linear_forward_residual(rows, fin, fout, x, w, b, out, l, mask, rpi, y=None, ctx=None):
+    """y = x W^T + b, and out += (y l) mask[r / rpi] (a residual branch's
+    LayerScale and DropPath) in the GEMM's epilogue; returns y."""
+    ctx = ctx or default_ctx()
+    y = _new(rows * fout, x) if y is None else y
+    ctx.check(lib().rnn_linear_forward_residual(
+        ctx.h, rows, fin, fout, _ptr(x, rows * fin, "x"), _ptr(w, fout * fin, "w"),
+        _ptr(b, fout, "b"), _ptr(y, rows * fout, "y"), _ptr(l, fout, "l"),
+        _ptr(mask, rows // rpi, "mask") if mask is not None else None, rpi,
+        _ptr(out, rows * fout, "out")))
+    return y
+
+
 def linear_backward(rows, fin, fout, dy, x, w, dw, db=None, dx=None, ctx=None, acc_dx=False):
     """Linear::backward (linear.rs:66-96); acc_dx: dx (given) += dy W."""
     ctx = ctx or default_ctx()
@@ -708,8 +723,15 @@ class Linear:
         self.gb = torch.zeros_like(self.b) if bias else None
         self.x, self.rows = None, 0
 
-    def forward(self, x, rows, train=True):
-        y = linear_forward(rows, self.fin, self.fout, x, self.w, self.b, ctx=self.ctx)
+    def forward(self, x, rows, train=True, residual=None):
+        """y = x W^T + b; residual = (out, l, mask, rows per image): also
+        out += (y l) mask[image] in the same launch."""
+        if residual is None:
+            y = linear_forward(rows, self.fin, self.fout, x, self.w, self.b, ctx=self.ctx)
+        else:
+            out, l, mask, rpi = residual
+            y = linear_forward_residual(rows, self.fin, self.fout, x, self.w, self.b, out, l,
+                                        mask, rpi, ctx=self.ctx)
         if train:
             self.x, self.rows = x, rows
         return y

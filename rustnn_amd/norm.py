@@ -146,7 +146,9 @@ class SwiGlu:
         self.ab = None
         self.rows = 0
 
-    def forward(self, x, train):
+    def forward(self, x, train, residual=None):
+        """residual = (out, l, mask, rows per image): the down projection also
+        adds out += (y l) mask[image] (Linear.forward)."""
         import torch
         rows, c = _rows_c(x)
         h = self.h
@@ -156,7 +158,7 @@ class SwiGlu:
                                                 _ptr(u, rows * h, "u")))
         if train:
             self.ab, self.rows = ab, rows
-        return self.wd.forward(u, rows, train).view(x.shape)
+        return self.wd.forward(u, rows, train, residual).view(x.shape)
 
     def backward(self, dy):
         import torch

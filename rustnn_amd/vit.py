@@ -61,11 +61,6 @@ def _scaled_std(depth):
     return np.float32(0.02) / np.sqrt(np.float32(2.0) * np.float32(depth))
 
 
-def _add_(a, b, ctx):
-    ctx.check(lib().rnn_add(ctx.h, a.numel(), _ptr(a, a.numel(), "a"), _ptr(b, a.numel(), "b")))
-    return a
-
-
 class SelfAttn:
     """SelfAttn (attn.rs:346-448): fused qkv Linear(c, 3c) -> Core (masked
     diagonal) -> proj Linear::scaled; tau = 1/sqrt(dh), rel = 0."""
@@ -136,11 +131,14 @@ class CrossAttn:
         self.q = self.p = None
         self.n = 0
 
-    def forward(self, x, mem, train):
+    def forward(self, x, mem, train, residual=None):
+        """residual = (out, l, mask): the projection also adds
+        out += (y l) mask[image] (Linear.forward)."""
         n, t, c = x.shape
         q = self.wq.forward(x.reshape(-1), n * t, train)
         p, o = self.core.forward(n, q, c, 0, mem, 2 * c, 0, c, self.tau.v, self.rel.v)
-        y = self.proj.forward(o, n * t, train)
+        res = None if residual is None else (*residual, t)
+        y = self.proj.forward(o, n * t, train, res)
         if train:
             self.q, self.p, self.n = q, p, n
         return y.view(n, t, c)
@@ -238,21 +236,6 @@ class DropPath:
         return dy
 
 
-def _branch_add(x, a, ls, dp, train, seed, out):
-    """out = x + DropPath(LayerScale(a)) in one pass (rnn_residual_add_scaled,
-    the reference's rounding order; out may be x).  Keeps what the branch's
-    backward reads: the LayerScale's input a (training) and the mask."""
-    n = a.shape[0]
-    rows, c = a.numel() // a.shape[-1], a.shape[-1]
-    mask = dp.take_mask(n, train, seed, a.device)
-    if train:
-        ls.x = a
-    ls.ctx.check(lib().rnn_residual_add_scaled(
-        ls.ctx.h, rows, c, _ptr(x, rows * c, "x"), _ptr(a, rows * c, "a"), _ptr(ls.l.v, c, "l"),
-        _ptr(mask, n, "mask") if mask is not None else None, rows // n, _ptr(out, rows * c, "y")))
-    return out
-
-
 def draw_masks(layers, n, device, ctx):
     """DropPath::forward's draws (vit.rs:44-51) of several layers in one
     launch: ``layers`` lists (DropPath, seed); every layer with p > 0 gets
@@ -325,14 +308,21 @@ class Block:
         if train:
             self.dwo = d
             self.ls1.x = a
+        n = x.shape[0]
         if self.cross is not None:
             if mem is None:
                 raise ValueError("Block: a reader block needs the memory")
-            cm = self.cross.forward(h, mem, train)
-            _branch_add(y, cm, self.lsm, self.dp2, train, seed ^ self.idx ^ 0x5151, y)
+            # y += dp2(lsm(CrossAttn(h, mem))) in the projection's epilogue
+            mask = self.dp2.take_mask(n, train, seed ^ self.idx ^ 0x5151, x.device)
+            cm = self.cross.forward(h, mem, train, (y, self.lsm.l.v, mask))
+            if train:
+                self.lsm.x = cm
         h2 = self.n2.forward(y, train)
-        m = self.mlp.forward(h2, train)
-        _branch_add(y, m, self.ls2, self.dp3, train, seed ^ self.idx ^ 0xA2A2, y)
+        # y += dp3(ls2(SwiGlu(h2))) in the down projection's epilogue
+        mask = self.dp3.take_mask(n, train, seed ^ self.idx ^ 0xA2A2, x.device)
+        m = self.mlp.forward(h2, train, (y, self.ls2.l.v, mask, h2.numel() // (n * self.c)))
+        if train:
+            self.ls2.x = m
         return y
 
     def backward(self, dz, mem=None, dmem=None, set_dmem=False):
@@ -433,8 +423,7 @@ class TaxoHead:
             _ptr(dzf, n * self.nf, "dzf"), _ptr(dzc, n * self.nc, "dzc"),
             _ptr(dc, n * self.nc, "dc")))
         df = self.resid.backward(dzf.reshape(-1))
-        _add_(df, self.coarse.backward(dc), self.ctx)
-        return df
+        return self.coarse.backward(dc, acc_dx=df)  # df + the coarse Linear's dx
 
     def for_each_param(self, f):
         for p in self._params:
@@ -461,7 +450,7 @@ class Exit:
 
     def backward(self, dz, dh):
         d = self.fc.backward(dz.reshape(-1))
-        return _add_(d, self.hint.backward(dh.reshape(-1)), self.ctx)
+        return self.hint.backward(dh.reshape(-1), acc_dx=d)  # d + the hint Linear's dx
 
     def for_each_param(self, f):
         for p in self._params:

@@ -187,6 +187,40 @@ def test_linear_backward_acc(rnn, orc, rows, fin, fout):
     assert rel_frob(to_host(DX) - dx0, dx_want) < TOL
 
 
+@pytest.mark.parametrize("rows,fin,fout,rpi,masked", [(8192, 352, 256, 64, True),
+                                                      (2048, 256, 384, 16, False),
+                                                      (300, 40, 36, 10, True),
+                                                      (96, 6, 20, 32, True)])
+def test_linear_forward_residual(rnn, orc, rows, fin, fout, rpi, masked):
+    """rnn_linear_forward_residual == rnn_linear_forward then
+    rnn_residual_add_scaled(out, y, ...), bit for bit (rpi 10: the two-pass
+    fallback; fin 6: the register-staged GEMM's epilogue), y within TOL of the
+    oracle."""
+    import ctypes as C
+    from rustnn_amd import _ptr, lib
+    rng = orc.Rng(23)
+    x, w = rng.rand_vec(rows * fin), rng.rand_vec(fout * fin) * np.float32(0.05)
+    b, l, out0 = rng.rand_vec(fout), rng.rand_vec(fout), rng.rand_vec(rows * fout)
+    n = rows // rpi
+    mask = np.where(np.arange(n) % 3 == 1, 0.0, 1.25).astype(np.float32)
+    X, W, B, L = to_dev(x), to_dev(w), to_dev(b), to_dev(l)
+    M = to_dev(mask) if masked else None
+    y1 = rnn.linear_forward(rows, fin, fout, X, W, B)
+    O1 = to_dev(out0.copy())
+    ctx = rnn.default_ctx()
+    ctx.check(lib().rnn_residual_add_scaled(ctx.h, rows, fout, _ptr(O1, rows * fout, "x"),
+                                            _ptr(y1, rows * fout, "a"), _ptr(L, fout, "l"),
+                                            _ptr(M, n, "m") if masked else None, rpi,
+                                            _ptr(O1, rows * fout, "y")))
+    O2 = to_dev(out0.copy())
+    y2 = rnn.linear_forward_residual(rows, fin, fout, X, W, B, O2, L, M, rpi)
+    assert np.array_equal(to_host(y1), to_host(y2))
+    assert np.array_equal(to_host(O1), to_host(O2))
+    with orc.threads(8):
+        yw = orc.linear_forward(rows, fin, fout, x, w, b)
+    assert rel_frob(to_host(y2), yw) < TOL
+
+
 @pytest.mark.parametrize("m,k", [(32, 288), (288, 32), (7, 259), (1, 1), (13, 600)])
 @pytest.mark.parametrize("tr", [False, True])
 def test_pack_bit_exact(rnn, orc, m, k, tr):
