@@ -17,7 +17,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import Core, Linear, _ptr, default_ctx, lib, rel_index
+from . import Core, Linear, _ptr, default_ctx, lib, linear_backward, linear_forward, rel_index
 from .data import Rng
 from .norm import DwConv3, LayerNorm, LayerScale, SeqPool, SwiGlu, _linear_param
 from .optim import Param
@@ -622,7 +622,7 @@ class RustViT:
         self.memw = _optim_param(self.memconv.w, self.memconv.g, True)
         self.mergep = _linear_param(self.merge)
         self.use_exits, self.drop_seed = True, 0
-        self.mem = self.c2_out = self.stem_out = None
+        self.mem = self.c2_out = self.stem_out = self.mem_in = None
         self.n = 0
         self._packs = None
 
@@ -636,7 +636,7 @@ class RustViT:
                 out += [(b.down.conv, s, s)]
             s = b.a.out_hw(s, s)[0]
             out += [(b.b.conv, s, s)]
-        return out + [(self.memconv, self.mh, self.mh), (self.tok.conv, self.mh, self.mh)]
+        return out + [(self.tok.conv, self.mh, self.mh)]
 
     def _repack(self):
         """The trunk's packed weights from the current ones: one launch per
@@ -661,8 +661,14 @@ class RustViT:
         if train:
             self.c2_out = h
         mh = self.mh
-        memt = nchw_to_tokens(self.memconv.forward(h, n, mh, mh, train).view(n, 2 * d, mh, mh),
-                              self.ctx)
+        # the memory's 1x1 conv as the product it is, on the trunk's tokens:
+        # [n*mh*mh, cm] x W^T with W = [2d][cm] (the conv's weights)
+        cm = self.cfg["cmid"]
+        ht = nchw_to_tokens(h, self.ctx)
+        memt = linear_forward(n * mh * mh, cm, 2 * d, ht, self.memconv.w, None,
+                              ctx=self.ctx).view(n, mh * mh, 2 * d)
+        if train:
+            self.mem_in = ht
         mem = self.memln.forward(memt, train)
         z = nchw_to_tokens(self.tok.forward(h, train), self.ctx)
         seed = self.drop_seed
@@ -728,8 +734,9 @@ class RustViT:
         dc2 = self.tok.backward(dt)
         mh = self.mh
         dmemn = self.memln.backward(dmem)
-        dmc = self.memconv.backward(tokens_to_nchw(dmemn, mh, mh, ctx).reshape(-1))
-        add_(dc2, dmc, ctx)
+        dht = linear_backward(n * mh * mh, cm, 2 * d, dmemn, self.mem_in, self.memconv.w,
+                              self.memconv.g, ctx=ctx)
+        add_(dc2, tokens_to_nchw(dht.view(n, mh * mh, cm), mh, mh, ctx), ctx)
         if self.use_exits and g.get("e1") is not None:
             dgv = self.e1.backward(g["e1"], g["h1"])
             add_(dc2, gap_backward(dgv.view(n, cm), mh, mh, ctx), ctx)
