@@ -392,6 +392,20 @@ int rnn_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy
 int rnn_drop_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy,
                                  const float *x, const float *l, const float *mask, size_t rpi,
                                  float *dx, float *dl);
+/* The first residual's branch gradients in a Block backward (vit.rs:175-232)
+ * in one pass over dy: da = (dy m1) l1 with dl1 += sum (dy m1) a (the
+ * DropPath + LayerScale of the attention branch), ddw = da gamma with
+ * dgamma += sum da dwo (the depthwise branch's gamma gate) and, for a reader
+ * block (cm set), dc = (dy m2) lm with dlm += sum (dy m2) cm.  Each value
+ * equals what rnn_drop_layerscale_backward (lsm, then ls1) and
+ * rnn_layerscale_backward (gamma) called in turn write; m1 / m2 = mask[r /
+ * rpi] or 1 when NULL.  dy, a, dwo and cm are not changed; the outputs must
+ * not overlap them or each other. */
+int rnn_block_branch_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy,
+                              const float *a, const float *l1, const float *m1, const float *dwo,
+                              const float *gamma, const float *cm, const float *lm,
+                              const float *m2, size_t rpi, float *da, float *dl1, float *ddw,
+                              float *dgamma, float *dc, float *dlm);
 /* y = x + (a l) m, m = mask[r / rpi] per image (mask may be NULL: m = 1): one
  * residual branch of Block::forward, x + DropPath(LayerScale(a))
  * (vit.rs:155-176: the LayerScale, the DropPath scaling and add_ in that

@@ -158,6 +158,7 @@ extern "C" {
     pub fn rnn_layerscale_forward(ctx: *mut rnn_ctx, rows: usize, c: usize, x: *const f32, l: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_layerscale_backward(ctx: *mut rnn_ctx, rows: usize, c: usize, dy: *const f32, x: *const f32, l: *const f32, dx: *mut f32, dl: *mut f32) -> c_int;
     pub fn rnn_drop_layerscale_backward(ctx: *mut rnn_ctx, rows: usize, c: usize, dy: *const f32, x: *const f32, l: *const f32, mask: *const f32, rpi: usize, dx: *mut f32, dl: *mut f32) -> c_int;
+    pub fn rnn_block_branch_backward(ctx: *mut rnn_ctx, rows: usize, c: usize, dy: *const f32, a: *const f32, l1: *const f32, m1: *const f32, dwo: *const f32, gamma: *const f32, cm: *const f32, lm: *const f32, m2: *const f32, rpi: usize, da: *mut f32, dl1: *mut f32, ddw: *mut f32, dgamma: *mut f32, dc: *mut f32, dlm: *mut f32) -> c_int;
     pub fn rnn_residual_add_scaled(ctx: *mut rnn_ctx, rows: usize, c: usize, x: *const f32, a: *const f32, l: *const f32, mask: *const f32, rpi: usize, y: *mut f32) -> c_int;
     pub fn rnn_swiglu_forward(ctx: *mut rnn_ctx, rows: usize, h: usize, ab: *const f32, u: *mut f32) -> c_int;
     pub fn rnn_swiglu_backward(ctx: *mut rnn_ctx, rows: usize, h: usize, du: *const f32, ab: *const f32, dab: *mut f32) -> c_int;

@@ -235,6 +235,9 @@ def lib():
             "rnn_ln_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
             "rnn_layerscale_forward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),
             "rnn_layerscale_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_block_branch_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
+                                               _vp, _vp, _vp, _sz, _vp, _vp, _vp, _vp, _vp,
+                                               _vp]),
             "rnn_drop_layerscale_backward": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _sz, _vp,
                                                   _vp]),
             "rnn_swiglu_forward": (_i, [_vp, _sz, _sz, _vp, _vp]),

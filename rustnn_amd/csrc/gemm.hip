@@ -993,7 +993,10 @@ static int gemm_splitk(rnn_ctx *ctx, size_t m, size_t n, size_t k, const float *
         sg.out0 = c;
         sg.len = (long long)(m * n);
         sg.nrow = (int)nz;
-        sg.kind = RNN_DEFER_CHUNKS;
+        // part is 256-byte aligned, so its rows are 16-byte aligned when len is
+        // a multiple of 4
+        sg.kind = (m * n) % 4 == 0 && (uintptr_t)c % 16 == 0 ? RNN_DEFER_CHUNKS4
+                                                            : RNN_DEFER_CHUNKS;
         sg.acc = acc;
         rnn_defer_push(ctx, sg);
         if (rsum) {

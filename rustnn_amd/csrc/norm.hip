@@ -303,6 +303,84 @@ __global__ __launch_bounds__(NT) void ls_bwd_cs_kernel(size_t rows, int c, const
     store_col_partials<NV, 1>(p, c, part);
 }
 
+// The first residual's branch gradients of a Block backward in one pass
+// over dy, each value as ls_bwd_cs_kernel computes it: t1 = dy m1,
+// da = t1 l1, p1 += (double)(t1 a); then the gamma gate, ddw = da gamma,
+// pg += (double)(da dwo); with CROSS, t2 = dy m2, dc = t2 lm,
+// pm += (double)(t2 cm).  m1 / m2 = mask[r / rpi] when the mask is set.
+// part1 / partg / partm: [nblk][c] each, in store_col_partials' order.
+struct BranchBwd {
+    const float *dy, *a, *l1, *m1, *dwo, *gamma, *cm, *lm, *m2;
+    float *da, *ddw, *dc;
+    double *part1, *partg, *partm;
+    size_t rows, rpi;
+    int c;
+};
+
+template <int NV, bool CROSS>
+__global__ __launch_bounds__(NT) void branch_bwd_cs_kernel(BranchBwd g) {
+    constexpr int RPW = RB_ROWS / 4;
+    const int lane = threadIdx.x & 63, w = wave_index(), c = g.c;
+    const size_t rows = g.rows;
+    const size_t r0 = (size_t)blockIdx.x * RB_ROWS + w;
+    const int nr = r0 < rows ? (int)min((size_t)RPW, (rows - r0 + 3) / 4) : 0;
+    double p1[1][NV], pg[1][NV], pm[1][NV];
+    float l1v[NV], gv[NV], lmv[NV], m1[RPW], m2[RPW];
+    float dv[RPW][NV], av[RPW][NV], wv[RPW][NV], cv[RPW][NV];
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+        const size_t r = min(r0 + 4 * (size_t)k, rows - 1);
+        m1[k] = g.m1 ? g.m1[r / g.rpi] : 1.0f;
+        m2[k] = CROSS && g.m2 ? g.m2[r / g.rpi] : 1.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int j = min(lane + 64 * i, c - 1);
+        l1v[i] = g.l1[j];
+        gv[i] = g.gamma[j];
+        lmv[i] = CROSS ? g.lm[j] : 0.0f;
+        p1[0][i] = 0.0;
+        pg[0][i] = 0.0;
+        pm[0][i] = 0.0;
+#pragma unroll
+        for (int k = 0; k < RPW; k++) {
+            const size_t e = min(r0 + 4 * (size_t)k, rows - 1) * c + j;
+            dv[k][i] = g.dy[e];
+            av[k][i] = g.a[e];
+            wv[k][i] = g.dwo[e];
+            cv[k][i] = CROSS ? g.cm[e] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < RPW; k++) {
+        if (k >= nr) break;
+        const size_t rb = (r0 + 4 * (size_t)k) * c;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int j = lane + 64 * i;
+            if (j >= c) break;
+            const float t1 = g.m1 ? dv[k][i] * m1[k] : dv[k][i];
+            p1[0][i] += (double)(t1 * av[k][i]);
+            const float da = t1 * l1v[i];
+            g.da[rb + j] = da;
+            pg[0][i] += (double)(da * wv[k][i]);
+            g.ddw[rb + j] = da * gv[i];
+            if (CROSS) {
+                const float t2 = g.m2 ? dv[k][i] * m2[k] : dv[k][i];
+                pm[0][i] += (double)(t2 * cv[k][i]);
+                g.dc[rb + j] = t2 * lmv[i];
+            }
+        }
+    }
+    store_col_partials<NV, 1>(p1, c, g.part1);
+    __syncthreads();  // the partials' LDS staging is reused
+    store_col_partials<NV, 1>(pg, c, g.partg);
+    if (CROSS) {
+        __syncthreads();
+        store_col_partials<NV, 1>(pm, c, g.partm);
+    }
+}
+
 // Column sums in two fixed-order stages.  Stage 1, block (x, y): columns
 // [64x, 64x + 64), rows [CS_ROWS y, CS_ROWS (y + 1)); wave g sums the rows
 // g, g + 4, ... of the block in order (8 loads ahead of their adds), and the
@@ -454,6 +532,45 @@ __global__ void swiglu_bwd_kernel(size_t rows, int h, const float *__restrict__ 
         dab[r * 2 * h + j] = d * b * s * (1.0f + a * (1.0f - s));
         dab[r * 2 * h + h + j] = d * sa;
     }
+}
+
+// The same two passes four columns a thread (h % 4 == 0, 16-byte aligned
+// tensors): each element computed as above, with 16-byte loads and stores
+// and one division per four elements.
+__global__ void swiglu_fwd4_kernel(size_t rows, int hq, const float4 *__restrict__ ab,
+                                   float4 *__restrict__ u) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * hq) return;
+    const size_t r = i / hq, j = i - r * hq;
+    const float4 a = ab[r * 2 * hq + j], b = ab[r * 2 * hq + hq + j];
+    float4 o;
+    o.x = a.x * sigmoid(a.x) * b.x;
+    o.y = a.y * sigmoid(a.y) * b.y;
+    o.z = a.z * sigmoid(a.z) * b.z;
+    o.w = a.w * sigmoid(a.w) * b.w;
+    u[i] = o;
+}
+
+__device__ __forceinline__ void swiglu_bwd1(float d, float a, float b, float &da, float &db) {
+    const float s = sigmoid(a);
+    const float sa = a * s;
+    da = d * b * s * (1.0f + a * (1.0f - s));
+    db = d * sa;
+}
+
+__global__ void swiglu_bwd4_kernel(size_t rows, int hq, const float4 *__restrict__ du,
+                                   const float4 *__restrict__ ab, float4 *__restrict__ dab) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * hq) return;
+    const size_t r = i / hq, j = i - r * hq;
+    const float4 a = ab[r * 2 * hq + j], b = ab[r * 2 * hq + hq + j], d = du[i];
+    float4 ga, gb;
+    swiglu_bwd1(d.x, a.x, b.x, ga.x, gb.x);
+    swiglu_bwd1(d.y, a.y, b.y, ga.y, gb.y);
+    swiglu_bwd1(d.z, a.z, b.z, ga.z, gb.z);
+    swiglu_bwd1(d.w, a.w, b.w, ga.w, gb.w);
+    dab[r * 2 * hq + j] = ga;
+    dab[r * 2 * hq + hq + j] = gb;
 }
 
 // ------------------------------------------------------------ DwConv3
@@ -1067,6 +1184,69 @@ int rnn_drop_layerscale_backward(rnn_ctx *ctx, size_t rows, size_t c, const floa
     return RNN_OK;
 }
 
+int rnn_block_branch_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy,
+                              const float *a, const float *l1, const float *m1, const float *dwo,
+                              const float *gamma, const float *cm, const float *lm,
+                              const float *m2, size_t rpi, float *da, float *dl1, float *ddw,
+                              float *dgamma, float *dc, float *dlm) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!dy || !a || !l1 || !dwo || !gamma || !da || !dl1 || !ddw || !dgamma)
+        return rnn_fail(ctx, RNN_E_NULL, "block_branch_backward: null operand");
+    const bool cross = cm != nullptr;
+    if (cross && (!lm || !dc || !dlm))
+        return rnn_fail(ctx, RNN_E_NULL, "block_branch_backward: cm without lm, dc or dlm");
+    if (!dims_ok(rows, c))
+        return rnn_fail(ctx, RNN_E_INVALID, "block_branch_backward: %zu x %zu", rows, c);
+    if ((m1 || m2) && (rpi == 0 || rows % rpi))
+        return rnn_fail(ctx, RNN_E_INVALID, "block_branch_backward: %zu rows per image of %zu",
+                        rpi, rows);
+    if (da == dy || ddw == dy || ddw == da || (cross && (dc == dy || dc == da || dc == ddw)))
+        return rnn_fail(ctx, RNN_E_INVALID, "block_branch_backward: outputs overlap");
+    if (c > 512) {
+        // the separate passes, in the reference's order
+        int rc = RNN_OK;
+        if (cross) rc = rnn_drop_layerscale_backward(ctx, rows, c, dy, cm, lm, m2, rpi, dc, dlm);
+        if (!rc) rc = rnn_drop_layerscale_backward(ctx, rows, c, dy, a, l1, m1, rpi, da, dl1);
+        if (!rc) rc = rnn_layerscale_backward(ctx, rows, c, da, dwo, gamma, ddw, dgamma);
+        return rc;
+    }
+    const size_t nblk = rnn_div_up(rows, (size_t)RB_ROWS);
+    if (nblk > 0x7fffffff) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "block_branch_backward: rows");
+    const size_t pb = nblk * c * sizeof(double);
+    double *part = col_part(ctx, (cross ? 3 : 2) * pb);
+    if (!part) return RNN_E_NOMEM;
+    BranchBwd g{dy, a, l1, m1, dwo, gamma, cm, lm, m2, da, ddw, dc,
+                part, part + nblk * c, cross ? part + 2 * nblk * c : nullptr,
+                rows, (m1 || m2) ? rpi : 1, (int)c};
+    auto go = [&](auto kern) { kern<<<(unsigned)nblk, NT, 0, ctx->stream>>>(g); };
+    const int nv = (int)rnn_div_up(c, (size_t)64);
+#define RNN_BRANCH_NV(NV)                                         \
+    case NV:                                                       \
+        cross ? go(branch_bwd_cs_kernel<NV, true>) : go(branch_bwd_cs_kernel<NV, false>); \
+        break;
+    switch (nv) {
+        RNN_BRANCH_NV(1)
+        RNN_BRANCH_NV(2)
+        RNN_BRANCH_NV(3)
+        RNN_BRANCH_NV(4)
+        RNN_BRANCH_NV(5)
+        RNN_BRANCH_NV(6)
+        RNN_BRANCH_NV(7)
+        default:
+            cross ? go(branch_bwd_cs_kernel<8, true>) : go(branch_bwd_cs_kernel<8, false>);
+            break;
+    }
+#undef RNN_BRANCH_NV
+    RNN_LAUNCHED(ctx);
+    int rc = RNN_OK;
+    if (cross) rc = col_reduce(ctx, nblk, c, c, g.partm, dlm, nullptr);
+    if (!rc) rc = col_reduce(ctx, nblk, c, c, g.part1, dl1, nullptr);
+    if (!rc) rc = col_reduce(ctx, nblk, c, c, g.partg, dgamma, nullptr);
+    return rc;
+}
+
 int rnn_residual_add_scaled(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *a,
                             const float *l, const float *mask, size_t rpi, float *y) {
     if (!ctx) return RNN_E_NULL;
@@ -1092,13 +1272,22 @@ int rnn_residual_add_scaled(rnn_ctx *ctx, size_t rows, size_t c, const float *x,
     return RNN_OK;
 }
 
+// The float4 SwiGLU passes: h a multiple of 4, 16-byte aligned tensors.
+static bool swiglu_vec(size_t h, const void *a, const void *b, const void *c) {
+    return h % 4 == 0 && (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c) & 15) == 0;
+}
+
 int rnn_swiglu_forward(rnn_ctx *ctx, size_t rows, size_t h, const float *ab, float *u) {
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     if (rows == 0 || h == 0) return RNN_OK;
     if (!ab || !u) return rnn_fail(ctx, RNN_E_NULL, "swiglu_forward: null operand");
     if (!dims_ok(rows, h)) return rnn_fail(ctx, RNN_E_INVALID, "swiglu: %zu x %zu", rows, h);
-    swiglu_fwd_kernel<<<ew_grid(rows * h), NT, 0, ctx->stream>>>(rows, (int)h, ab, u);
+    if (swiglu_vec(h, ab, u, u) && rows * h / 4 < ((size_t)1 << 31))
+        swiglu_fwd4_kernel<<<(unsigned)rnn_div_up(rows * h / 4, (size_t)NT), NT, 0,
+                             ctx->stream>>>(rows, (int)(h / 4), (const float4 *)ab, (float4 *)u);
+    else
+        swiglu_fwd_kernel<<<ew_grid(rows * h), NT, 0, ctx->stream>>>(rows, (int)h, ab, u);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -1110,7 +1299,12 @@ int rnn_swiglu_backward(rnn_ctx *ctx, size_t rows, size_t h, const float *du, co
     if (rows == 0 || h == 0) return RNN_OK;
     if (!du || !ab || !dab) return rnn_fail(ctx, RNN_E_NULL, "swiglu_backward: null operand");
     if (!dims_ok(rows, h)) return rnn_fail(ctx, RNN_E_INVALID, "swiglu: %zu x %zu", rows, h);
-    swiglu_bwd_kernel<<<ew_grid(rows * h), NT, 0, ctx->stream>>>(rows, (int)h, du, ab, dab);
+    if (swiglu_vec(h, du, ab, dab) && rows * h / 4 < ((size_t)1 << 31))
+        swiglu_bwd4_kernel<<<(unsigned)rnn_div_up(rows * h / 4, (size_t)NT), NT, 0,
+                             ctx->stream>>>(rows, (int)(h / 4), (const float4 *)du,
+                                            (const float4 *)ab, (float4 *)dab);
+    else
+        swiglu_bwd_kernel<<<ew_grid(rows * h), NT, 0, ctx->stream>>>(rows, (int)h, du, ab, dab);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

@@ -202,7 +202,10 @@ struct DeferBatch {
 };
 
 unsigned defer_blocks(const RnnDeferSeg &s) {
-    const size_t per = s.kind == RNN_DEFER_COLS ? 16 : s.kind == RNN_DEFER_ATTN ? 32 : 256;
+    const size_t per = s.kind == RNN_DEFER_COLS     ? 16
+                       : s.kind == RNN_DEFER_ATTN    ? 32
+                       : s.kind == RNN_DEFER_CHUNKS4 ? 1024
+                                                     : 256;
     return (unsigned)rnn_div_up((size_t)s.len, per);
 }
 
@@ -231,6 +234,10 @@ __global__ __launch_bounds__(256) void deferred_reduce_kernel(DeferBatch b) {
         return;
     }
     const long long e = (long long)blk * 256 + threadIdx.x;
+    if (s.kind == RNN_DEFER_CHUNKS4) {
+        if (4 * e < s.len) rnn_chunk_sum4((const float *)s.part, s.nrow, s.len, s.out0, s.acc, 4 * e);
+        return;
+    }
     if (e >= s.len) return;
     if (s.kind == RNN_DEFER_CHUNKS)
         rnn_chunk_sum((const float *)s.part, s.nrow, s.len, s.out0, s.acc, e);

@@ -44,6 +44,8 @@ enum {
     RNN_DEFER_ATTN = 3,    // attention dtau / drel (rnn_attn_reduce_block): part = dtau
                            // partials, part2 = drel partials, out0 = drel, out1 = dtau,
                            // len = h*nrel + h, split = h*nrel, nrow = n images
+    RNN_DEFER_CHUNKS4 = 4, // CHUNKS with len % 4 == 0 and 16-byte aligned rows and out0,
+                           // four elements a thread (rnn_chunk_sum4)
 };
 struct RnnDeferSeg {
     const void *part, *part2;
@@ -95,7 +97,7 @@ void rnn_defer_push(rnn_ctx *ctx, const RnnDeferSeg &s);
 
 // Block `blk` of a column reduction: columns [16 blk, 16 blk + 16) of part
 // [nblk][len] (f64), each summed over the rows in 16 consecutive groups --
-// each group in order, 8 loads ahead -- then the group sums in order, and
+// each group in order, 16 loads ahead -- then the group sums in order, and
 // added into out0[j] (j < split) or out1[j - split].  256 threads.
 __device__ __forceinline__ void rnn_colsum_red_block(int nblk, size_t len, size_t split,
                                                      const double *__restrict__ part,
@@ -107,12 +109,12 @@ __device__ __forceinline__ void rnn_colsum_red_block(int nblk, size_t len, size_
     const size_t j = (size_t)blk * COLS + jl, jc = min(j, len - 1);
     const int G = (nblk + NG - 1) / NG, k0 = min(nblk, q * G), k1 = min(nblk, k0 + G);
     double s = 0.0;
-    for (int k = k0; k < k1; k += 8) {
-        double v[8];
+    for (int k = k0; k < k1; k += 16) {
+        double v[16];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = part[(size_t)min(k + u, k1 - 1) * len + jc];
+        for (int u = 0; u < 16; u++) v[u] = part[(size_t)min(k + u, k1 - 1) * len + jc];
 #pragma unroll
-        for (int u = 0; u < 8; u++)
+        for (int u = 0; u < 16; u++)
             if (k + u < k1) s += v[u];
     }
     red[q][jl] = s;
@@ -140,6 +142,42 @@ __device__ __forceinline__ void rnn_chunk_sum(const float *part, int nz, long lo
             if (z0 + i < nz) s = (z0 + i == 0) ? v[i] : s + v[i];
     }
     out[e] = accumulate ? out[e] + s : s;
+}
+
+// Elements e .. e + 3 (e % 4 == 0) of a chunk reduction, as rnn_chunk_sum
+// computes each of them (the same adds in the same order), with 16-byte
+// loads: part's rows and out 16-byte aligned, len % 4 == 0.
+__device__ __forceinline__ void rnn_chunk_sum4(const float *part, int nz, long long len,
+                                               float *out, int accumulate, long long e) {
+    float4 old = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (accumulate) old = *(const float4 *)(out + e);
+    float4 s = old;
+    for (int z0 = 0; z0 < nz; z0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            v[i] = z0 + i < nz ? *(const float4 *)(part + (long long)(z0 + i) * len + e)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (z0 + i >= nz) continue;
+            if (z0 + i == 0) {
+                s = v[i];
+            } else {
+                s.x = s.x + v[i].x;
+                s.y = s.y + v[i].y;
+                s.z = s.z + v[i].z;
+                s.w = s.w + v[i].w;
+            }
+        }
+    }
+    if (accumulate) {
+        s.x = old.x + s.x;
+        s.y = old.y + s.y;
+        s.z = old.z + s.z;
+        s.w = old.w + s.w;
+    }
+    *(float4 *)(out + e) = s;
 }
 
 // Block `blk` of the attention parameter reduction (32 outputs a block, 256

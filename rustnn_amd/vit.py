@@ -334,19 +334,24 @@ class Block:
         dm = self.ls2.backward(dz, self.dp3.mask)
         dh2 = self.mlp.backward(dm)
         dy = self.n2.backward(dh2, add=dz)  # n2's input gradient + dz, a new tensor
-        dh = None  # the branches' input gradients, added in branch order
-        if self.cross is not None:
-            dc = self.lsm.backward(dy, self.dp2.mask)
-            dh = self.cross.backward(dc, mem, dmem, set_dmem)
-        da = self.ls1.backward(dy, self.dp1.mask)
-        # gamma.g += sum da * dwo; ddw = gamma * da: the LayerScale backward
-        rows = da.numel() // c
-        ddw = torch.empty_like(da)
-        ctx.check(L.rnn_layerscale_backward(ctx.h, rows, c, _ptr(da, rows * c, "da"),
-                                            _ptr(self.dwo, rows * c, "dwo"),
-                                            _ptr(self.gamma.v, c, "gamma"),
-                                            _ptr(ddw, rows * c, "ddw"),
-                                            _ptr(self.gamma.g, c, "dgamma")))
+        # the first residual's branch gradients in one pass over dy: dc =
+        # lsm's DropPath + LayerScale backward (reader blocks), da = ls1's,
+        # ddw = gamma * da with gamma.g += sum da * dwo
+        rows = dy.numel() // c
+        cross = self.cross is not None
+        m1, m2 = self.dp1.mask, (self.dp2.mask if cross else None)
+        nimg = next((m.numel() for m in (m1, m2) if m is not None), 1)
+        da, ddw = torch.empty_like(dy), torch.empty_like(dy)
+        dc, cm, lm, dlm = ((torch.empty_like(dy), self.lsm.x, self.lsm.l.v, self.lsm.l.g)
+                           if cross else (None, None, None, None))
+        ctx.check(L.rnn_block_branch_backward(
+            ctx.h, rows, c, _ptr(dy, rows * c, "dy"), _ptr(self.ls1.x, rows * c, "a"),
+            _ptr(self.ls1.l.v, c, "l1"), _ptr(m1, nimg, "m1"), _ptr(self.dwo, rows * c, "dwo"),
+            _ptr(self.gamma.v, c, "gamma"), _ptr(cm, rows * c, "cm"), _ptr(lm, c, "lm"),
+            _ptr(m2, nimg, "m2"), rows // nimg, _ptr(da, rows * c, "da"),
+            _ptr(self.ls1.l.g, c, "dl1"), _ptr(ddw, rows * c, "ddw"),
+            _ptr(self.gamma.g, c, "dgamma"), _ptr(dc, rows * c, "dc"), _ptr(dlm, c, "dlm")))
+        dh = self.cross.backward(dc, mem, dmem, set_dmem) if cross else None
         # the branches' input gradients summed in branch order, each added by
         # the kernel that computes it
         dh = self.attn.backward(da, acc_dx=dh)

@@ -149,6 +149,57 @@ def test_drop_layerscale_backward(rnn, orc, n, t, c):
     assert np.array_equal(to_host(DY).reshape(rows, c), dy.reshape(rows, c))
 
 
+@pytest.mark.parametrize("n,t,c,cross,masked", [(8, 64, 256, True, (True, True)),
+                                                (8, 64, 256, False, (True, False)),
+                                                (3, 5, 200, True, (False, True)),
+                                                (2, 9, 600, True, (True, True)),
+                                                (4, 16, 384, True, (False, False))])
+def test_block_branch_backward(rnn, orc, n, t, c, cross, masked):
+    """rnn_block_branch_backward equals the separate calls it fuses, bit for
+    bit: lsm's and ls1's DropPath + LayerScale backward, then the gamma
+    gate's LayerScale backward over da (c = 600 takes the separate passes
+    themselves; 3 x 5 = 15 rows leave a partial row block)."""
+    import torch
+    from rustnn_amd import default_ctx, lib, _ptr
+    rows = n * t
+    dy, a, dwo, cm = (_dev(_r((rows, c), 40 + i)) for i in range(4))
+    l1, gam, lm = (_dev(_r(c, 50 + i, 0.3, 0.5)) for i in range(3))
+    mk = lambda s: _dev((np.random.default_rng(s).random(n) < 0.7).astype(np.float32) / 0.7)
+    m1 = mk(60) if masked[0] else None
+    m2 = mk(61) if masked[1] and cross else None
+    dl0 = [_dev(_r(c, 70 + i)) for i in range(3)]
+    ctx = default_ctx()
+    L = lib()
+    P = lambda x, k: _ptr(x, k, "x")
+    # the separate calls
+    dl1, dg, dlm = (d.clone() for d in dl0)
+    da, ddw, dc = (torch.empty_like(dy) for _ in range(3))
+    if cross:
+        ctx.check(L.rnn_drop_layerscale_backward(ctx.h, rows, c, P(dy, rows * c), P(cm, rows * c),
+                                                 P(lm, c), P(m2, n), t, P(dc, rows * c),
+                                                 P(dlm, c)))
+    ctx.check(L.rnn_drop_layerscale_backward(ctx.h, rows, c, P(dy, rows * c), P(a, rows * c),
+                                             P(l1, c), P(m1, n), t, P(da, rows * c), P(dl1, c)))
+    ctx.check(L.rnn_layerscale_backward(ctx.h, rows, c, P(da, rows * c), P(dwo, rows * c),
+                                        P(gam, c), P(ddw, rows * c), P(dg, c)))
+    # the fused pass
+    fl1, fg, flm = (d.clone() for d in dl0)
+    fa, fw, fc = (torch.full_like(dy, 7.0) for _ in range(3))
+    ctx.check(L.rnn_block_branch_backward(
+        ctx.h, rows, c, P(dy, rows * c), P(a, rows * c), P(l1, c), P(m1, n), P(dwo, rows * c),
+        P(gam, c), P(cm, rows * c) if cross else None, P(lm, c) if cross else None, P(m2, n), t,
+        P(fa, rows * c), P(fl1, c), P(fw, rows * c), P(fg, c),
+        P(fc, rows * c) if cross else None, P(flm, c) if cross else None))
+    pairs = [(fa, da), (fw, ddw), (fl1, dl1), (fg, dg)]
+    if cross:
+        pairs += [(fc, dc), (flm, dlm)]
+    else:
+        assert np.all(to_host(fc) == 7.0) and np.array_equal(to_host(flm), to_host(dl0[2]))
+    for got, want in pairs:
+        assert np.array_equal(to_host(got), to_host(want))
+    assert to_host(fl1).any() and to_host(fw).any()
+
+
 @pytest.mark.parametrize("rows,h", [(4096, 352), (1000, 512), (7, 5)])
 def test_swiglu_gate(rnn, orc, rows, h):
     import torch
@@ -165,6 +216,19 @@ def test_swiglu_gate(rnn, orc, rows, h):
                                         _ptr(A, ab.size, "ab"), _ptr(dab, ab.size, "dab")))
     assert rel_frob(to_host(u), orc.swiglu_forward(ab, h)) < 1e-6
     assert rel_frob(to_host(dab), orc.swiglu_backward(du, ab, h)) < 1e-6
+    if h % 4 == 0:
+        # operands one float off 16-byte alignment take the one-element
+        # kernels: the four-column kernels equal them bit for bit
+        A1, D1 = torch.zeros(ab.size + 1, device="cuda"), torch.zeros(du.size + 1, device="cuda")
+        A1[1:].copy_(A.reshape(-1))
+        D1[1:].copy_(D.reshape(-1))
+        u1 = torch.empty(rows * h + 1, device="cuda")
+        dab1 = torch.empty(rows * 2 * h + 1, device="cuda")
+        ctx.check(lib().rnn_swiglu_forward(ctx.h, rows, h, A1[1:].data_ptr(), u1[1:].data_ptr()))
+        ctx.check(lib().rnn_swiglu_backward(ctx.h, rows, h, D1[1:].data_ptr(), A1[1:].data_ptr(),
+                                            dab1[1:].data_ptr()))
+        assert np.array_equal(to_host(u1[1:]), to_host(u))
+        assert np.array_equal(to_host(dab1[1:]), to_host(dab))
 
 
 def test_swiglu_layer(rnn, orc):
