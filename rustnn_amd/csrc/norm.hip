@@ -798,21 +798,69 @@ __global__ __launch_bounds__(NT) void dw3_bwd_w_kernel(int th, int tw, int c, in
 // w = softmax(s) with a sequential sum and a multiply by 1/sum;
 // z[k] = sum_j w_j x[j][k] in j order.  s, w live in LDS (t <= SP_MAXT).
 // XL: the image's x [t][c] is first staged into LDS by the whole block
-// (coalesced float4 loads), so the per-token and per-channel chains read
-// LDS; the sums keep the orders above.
+// (coalesced float4 loads) with a row stride of c + 1 floats, so the
+// per-token chains (thread j reading row j) fall in distinct banks and the
+// per-channel chains read consecutive words; the sums keep the orders above.
+// The softmax's max and exps run one token a thread (the max is exact in any
+// order), its sum in token order on one thread.
 constexpr int SP_MAXT = 1024;
 constexpr size_t SP_XL_BYTES = 96 * 1024;  // x staged in LDS up to this size
 
-// The image's x into xl ([t][c], dynamic LDS), 16 bytes a thread when c % 4 == 0.
+__host__ __device__ constexpr size_t seqpool_xl_bytes(size_t t, size_t c) {
+    return t * (c + 1) * sizeof(float);
+}
+
+// The image's x into xl ([t][c + 1], dynamic LDS), 16-byte global loads when
+// c % 4 == 0.
 __device__ __forceinline__ void seqpool_stage(const float *__restrict__ xi, int t, int c,
                                               float *xl) {
     const int tot = t * c;
     if ((c & 3) == 0 && ((uintptr_t)xi & 15) == 0) {
-        for (int e = threadIdx.x * 4; e < tot; e += NT * 4)
-            *reinterpret_cast<float4 *>(xl + e) = *reinterpret_cast<const float4 *>(xi + e);
+        for (int e = threadIdx.x * 4; e < tot; e += NT * 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(xi + e);
+            const int j = e / c, k = e - j * c;  // the four stay in row j
+            float *d = xl + j * (c + 1) + k;
+            d[0] = v.x;
+            d[1] = v.y;
+            d[2] = v.z;
+            d[3] = v.w;
+        }
     } else {
-        for (int e = threadIdx.x; e < tot; e += NT) xl[e] = xi[e];
+        for (int e = threadIdx.x; e < tot; e += NT) {
+            const int j = e / c;
+            xl[e + j] = xi[e];
+        }
     }
+    __syncthreads();
+}
+
+// w[0..t) = softmax(w) in place (the forward's order: max, exps, the sum in
+// token order, a multiply by 1/sum).  All NT threads call it.
+__device__ __forceinline__ void seqpool_softmax(float *w, int t) {
+    __shared__ float red[NT / 64];
+    __shared__ float inv_s;
+    float mx = -INFINITY;
+    for (int j = threadIdx.x; j < t; j += NT) mx = w[j] > mx ? w[j] : mx;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v = __shfl_xor(mx, o);
+        mx = v > mx ? v : mx;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int q = 1; q < NT / 64; q++) mx = red[q] > mx ? red[q] : mx;
+    for (int j = threadIdx.x; j < t; j += NT) w[j] = expf(w[j] - mx);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        for (int j = 0; j < t; j++) sum += w[j];
+        inv_s = 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = inv_s;
+    for (int j = threadIdx.x; j < t; j += NT) w[j] *= inv;
     __syncthreads();
 }
 
@@ -825,32 +873,23 @@ __global__ __launch_bounds__(NT) void seqpool_fwd_kernel(int t, int c, const flo
     extern __shared__ float xl[];
     const size_t im = blockIdx.x;
     const float *xi = x + im * t * c;
+    size_t ld = c;
     if constexpr (XL) {
         seqpool_stage(xi, t, c, xl);
         xi = xl;
+        ld = c + 1;
     }
     for (int j = threadIdx.x; j < t; j += NT) {
         float s = 0.0f;
-        for (int k = 0; k < c; k++) s += xi[(size_t)j * c + k] * p[k];
+        for (int k = 0; k < c; k++) s += xi[(size_t)j * ld + k] * p[k];
         w[j] = s;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float mx = -INFINITY;
-        for (int j = 0; j < t; j++) mx = w[j] > mx ? w[j] : mx;
-        float sum = 0.0f;
-        for (int j = 0; j < t; j++) {
-            w[j] = expf(w[j] - mx);
-            sum += w[j];
-        }
-        const float inv = 1.0f / sum;
-        for (int j = 0; j < t; j++) w[j] *= inv;
-    }
-    __syncthreads();
+    seqpool_softmax(w, t);
     for (int j = threadIdx.x; j < t; j += NT) wout[im * t + j] = w[j];
     for (int k = threadIdx.x; k < c; k += NT) {
         float acc = 0.0f;
-        for (int j = 0; j < t; j++) acc += w[j] * xi[(size_t)j * c + k];
+        for (int j = 0; j < t; j++) acc += w[j] * xi[(size_t)j * ld + k];
         z[im * c + k] = acc;
     }
 }
@@ -870,13 +909,15 @@ __global__ __launch_bounds__(NT) void seqpool_bwd_kernel(int t, int c, const flo
     extern __shared__ float xl[];
     const size_t im = blockIdx.x;
     const float *xi = x + im * t * c, *dzi = dz + im * c, *wi = wsave + im * t;
+    size_t ld = c;
     if constexpr (XL) {
         seqpool_stage(xi, t, c, xl);
         xi = xl;
+        ld = c + 1;
     }
     for (int j = threadIdx.x; j < t; j += NT) {
         float s = 0.0f;
-        for (int k = 0; k < c; k++) s += dzi[k] * xi[(size_t)j * c + k];
+        for (int k = 0; k < c; k++) s += dzi[k] * xi[(size_t)j * ld + k];
         dw[j] = s;
     }
     __syncthreads();
@@ -896,25 +937,28 @@ __global__ __launch_bounds__(NT) void seqpool_bwd_kernel(int t, int c, const flo
         for (int j = 0; j < t; j++) {
             const float ds = dw[j];
             dxi[(size_t)j * c + k] = wi[j] * dzk + ds * pk;
-            adp += ds * xi[(size_t)j * c + k];
+            adp += ds * xi[(size_t)j * ld + k];
         }
         part[im * c + k] = adp;
     }
 }
 
-// out[k] += sum over images of part[image][k] (image order, f64; 16 loads
-// ahead of their adds).
-__global__ void rowsum_add_kernel(size_t n, int c, const float *__restrict__ part,
-                                  float *__restrict__ out) {
+// out[k] += sum over images of part[image][k] (image order, f64; 64 loads
+// ahead of their adds).  Launched with 64-thread blocks, so a few hundred
+// channels spread over several CUs.
+constexpr int RS_NT = 64;
+__global__ __launch_bounds__(RS_NT) void rowsum_add_kernel(size_t n, int c,
+                                                           const float *__restrict__ part,
+                                                           float *__restrict__ out) {
     const int k = blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= c) return;
     double s = 0.0;
-    for (size_t i0 = 0; i0 < n; i0 += 16) {
-        float v[16];
+    for (size_t i0 = 0; i0 < n; i0 += 64) {
+        float v[64];
 #pragma unroll
-        for (int u = 0; u < 16; u++) v[u] = part[min(i0 + u, n - 1) * c + k];
+        for (int u = 0; u < 64; u++) v[u] = part[min(i0 + u, n - 1) * c + k];
 #pragma unroll
-        for (int u = 0; u < 16; u++)
+        for (int u = 0; u < 64; u++)
             if (i0 + u < n) s += v[u];
     }
     out[k] += (float)s;
@@ -1425,7 +1469,7 @@ int rnn_seqpool_forward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float 
     if (t == 0 || t > SP_MAXT || n > 0x7fffffff || !dims_ok(n * t, c))
         return rnn_fail(ctx, RNN_E_INVALID, "seqpool: n %zu, t %zu (1..%d), c %zu", n, t, SP_MAXT,
                         c);
-    const size_t xl = t * c * sizeof(float);
+    const size_t xl = seqpool_xl_bytes(t, c);
     if (xl <= SP_XL_BYTES) {
         static bool attr = false;
         if (!attr) {
@@ -1454,7 +1498,7 @@ int rnn_seqpool_backward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float
                         c);
     float *part = (float *)rnn_workspace(ctx, n * c * sizeof(float));
     if (!part) return RNN_E_NOMEM;
-    const size_t xl = t * c * sizeof(float);
+    const size_t xl = seqpool_xl_bytes(t, c);
     if (xl <= SP_XL_BYTES) {
         static bool attr = false;
         if (!attr) {
@@ -1470,8 +1514,8 @@ int rnn_seqpool_backward(rnn_ctx *ctx, size_t n, size_t t, size_t c, const float
                                                                         p, dx, part);
     }
     RNN_LAUNCHED(ctx);
-    rowsum_add_kernel<<<(unsigned)rnn_div_up(c, (size_t)NT), NT, 0, ctx->stream>>>(n, (int)c, part,
-                                                                                   dp);
+    rowsum_add_kernel<<<(unsigned)rnn_div_up(c, (size_t)RS_NT), RS_NT, 0, ctx->stream>>>(
+        n, (int)c, part, dp);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
