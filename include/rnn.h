@@ -332,6 +332,10 @@ int rnn_bn_backward(rnn_ctx *ctx, size_t n, size_t c, size_t hw, const float *dy
 int rnn_relu_back(rnn_ctx *ctx, size_t len, float *d, const float *y);
 /* add_ (nn.rs:441-443): a += b. */
 int rnn_add(rnn_ctx *ctx, size_t len, float *a, const float *b);
+/* add_ after relu_back_ (nn.rs:432-443) without changing b: a += b where
+ * y > 0 (the value relu_back_(b, y) then add_(a, b) leave in a); a must
+ * not be b. */
+int rnn_add_relu_back(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *y);
 /* add_relu_ (nn.rs:446-450): a = max(a + b, 0). */
 int rnn_add_relu(rnn_ctx *ctx, size_t len, float *a, const float *b);
 /* gap_forward (nn.rs:455-463): y[n][c] = plane sum (pixel order) / hw. */

@@ -145,6 +145,7 @@ extern "C" {
     pub fn rnn_bn_backward(ctx: *mut rnn_ctx, n: usize, c: usize, hw: usize, dy: *const f32, relu_out: *const f32, x: *const f32, mean: *const f32, invstd: *const f32, gamma: *const f32, dx: *mut f32, dgamma: *mut f32, dbeta: *mut f32) -> c_int;
     pub fn rnn_relu_back(ctx: *mut rnn_ctx, len: usize, d: *mut f32, y: *const f32) -> c_int;
     pub fn rnn_add(ctx: *mut rnn_ctx, len: usize, a: *mut f32, b: *const f32) -> c_int;
+    pub fn rnn_add_relu_back(ctx: *mut rnn_ctx, len: usize, a: *mut f32, b: *const f32, y: *const f32) -> c_int;
     pub fn rnn_add_relu(ctx: *mut rnn_ctx, len: usize, a: *mut f32, b: *const f32) -> c_int;
     pub fn rnn_gap_forward(ctx: *mut rnn_ctx, n: usize, c: usize, hw: usize, x: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_gap_backward(ctx: *mut rnn_ctx, n: usize, c: usize, hw: usize, dy: *const f32, dx: *mut f32) -> c_int;

@@ -170,6 +170,7 @@ def lib():
                                      _vp]),
             "rnn_relu_back": (_i, [_vp, _sz, _vp, _vp]),
             "rnn_add": (_i, [_vp, _sz, _vp, _vp]),
+            "rnn_add_relu_back": (_i, [_vp, _sz, _vp, _vp, _vp]),
             "rnn_add_relu": (_i, [_vp, _sz, _vp, _vp]),
             "rnn_gap_forward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
             "rnn_gap_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),

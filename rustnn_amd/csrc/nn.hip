@@ -1294,6 +1294,15 @@ int rnn_add(rnn_ctx *ctx, size_t len, float *a, const float *b) {
     return rnn_add_launch(ctx, len, a, b, nullptr);
 }
 
+int rnn_add_relu_back(rnn_ctx *ctx, size_t len, float *a, const float *b, const float *y) {
+    if (!ctx) return RNN_E_NULL;
+    if (len == 0) return RNN_OK;
+    if (!a || !b || !y) return rnn_fail(ctx, RNN_E_NULL, "add_relu_back: null pointer");
+    if (a == b) return rnn_fail(ctx, RNN_E_INVALID, "add_relu_back: a is b");
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    return rnn_add_launch(ctx, len, a, b, y);
+}
+
 int rnn_add_relu(rnn_ctx *ctx, size_t len, float *a, const float *b) {
     if (!ctx) return RNN_E_NULL;
     if (len == 0) return RNN_OK;

@@ -811,19 +811,30 @@ __host__ __device__ constexpr size_t seqpool_xl_bytes(size_t t, size_t c) {
 }
 
 // The image's x into xl ([t][c + 1], dynamic LDS), 16-byte global loads when
-// c % 4 == 0.
+// c % 4 == 0, eight of them in flight a thread before their LDS stores.
 __device__ __forceinline__ void seqpool_stage(const float *__restrict__ xi, int t, int c,
                                               float *xl) {
     const int tot = t * c;
     if ((c & 3) == 0 && ((uintptr_t)xi & 15) == 0) {
-        for (int e = threadIdx.x * 4; e < tot; e += NT * 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(xi + e);
-            const int j = e / c, k = e - j * c;  // the four stay in row j
-            float *d = xl + j * (c + 1) + k;
-            d[0] = v.x;
-            d[1] = v.y;
-            d[2] = v.z;
-            d[3] = v.w;
+        constexpr int U = 8;
+        for (int e0 = threadIdx.x * 4; e0 < tot; e0 += NT * 4 * U) {
+            float4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int e = e0 + u * NT * 4;
+                if (e < tot) v[u] = *reinterpret_cast<const float4 *>(xi + e);
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int e = e0 + u * NT * 4;
+                if (e >= tot) break;
+                const int j = e / c, k = e - j * c;  // the four stay in row j
+                float *d = xl + j * (c + 1) + k;
+                d[0] = v[u].x;
+                d[1] = v[u].y;
+                d[2] = v[u].z;
+                d[3] = v[u].w;
+            }
         }
     } else {
         for (int e = threadIdx.x; e < tot; e += NT) {

@@ -115,6 +115,13 @@ def add_(a, b, ctx=None):
     ctx.check(lib().rnn_add(ctx.h, a.numel(), _ptr(a, 0, "a"), _ptr(b, a.numel(), "b")))
 
 
+def add_relu_back_(a, b, y, ctx=None):
+    """add_(a, relu_back_(b, y)) with b left unchanged (nn.rs:432-443)."""
+    ctx = ctx or default_ctx()
+    ctx.check(lib().rnn_add_relu_back(ctx.h, a.numel(), _ptr(a, 0, "a"), _ptr(b, a.numel(), "b"),
+                                      _ptr(y, a.numel(), "y")))
+
+
 def add_relu_(a, b, ctx=None):
     ctx = ctx or default_ctx()
     ctx.check(lib().rnn_add_relu(ctx.h, a.numel(), _ptr(a, 0, "a"), _ptr(b, a.numel(), "b")))

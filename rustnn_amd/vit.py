@@ -554,13 +554,17 @@ class BasicBlock:
         return y
 
     def backward(self, d):
-        """BasicBlock::backward (model.rs:56-71); like the reference, which
-        takes d by value, it masks d in place (d is overwritten)."""
-        from .nn import add_, relu_back_
-        relu_back_(d, self.out, self.ctx)
-        dmain = self.b.backward(d)
+        """BasicBlock::backward (model.rs:56-71).  relu_back_ of d by the
+        block's output is taken by the kernels that read d (the second BN's
+        and the shortcut's backward, or the shortcut's add), so d itself is
+        left unchanged."""
+        from .nn import add_, add_relu_back_
+        dmain = self.b.backward(d, self.out)
         dx = self.a.backward(dmain, self.h1)
-        add_(dx, self.down.backward(d) if self.down else d, self.ctx)
+        if self.down:
+            add_(dx, self.down.backward(d, self.out), self.ctx)
+        else:
+            add_relu_back_(dx, d, self.out, self.ctx)
         return dx
 
     def params(self):
@@ -709,7 +713,7 @@ class RustViT:
         """RustViT::backward (vit.rs:628-688) from the output gradients
         (logits, coarse; e1, e2, h1, h2 with exits; hfinal optional)."""
         import torch
-        from .nn import add_, gap_backward, relu_back_
+        from .nn import add_, gap_backward
         ctx, n, d, cm = self.ctx, self.n, self.cfg["dim"], self.cfg["cmid"]
         dfeat = self.head.backward(g["logits"], g["coarse"])
         if g.get("hfinal") is not None:
@@ -747,8 +751,7 @@ class RustViT:
             add_(dc2, gap_backward(dgv.view(n, cm), mh, mh, ctx), ctx)
         dh = self.c2.backward(dc2)
         dh = self.c1.backward(dh)
-        relu_back_(dh, self.stem_out, ctx)
-        dh = self.stem.bn.backward(dh)
+        dh = self.stem.bn.backward(dh, self.stem_out)  # relu_back_ folded in
         self.stem.conv.backward_w(dh)
 
     def for_each_param(self, f):

@@ -118,6 +118,16 @@ def test_elementwise_bit_exact(rnn, orc):
         w = b.copy()
         orc.relu_back(w, a)
         assert np.array_equal(to_host(D), w)
+        # add_relu_back_: add_(a, relu_back_(b, y)) with b unchanged (n = 5
+        # and 100003 leave a ragged tail past the float4 items)
+        y = rng.rand_vec(n)
+        A, B = to_dev(a), to_dev(b)
+        nn.add_relu_back_(A, B, to_dev(y))
+        m, w = b.copy(), a.copy()
+        orc.relu_back(m, y)
+        orc.add_(w, m)
+        assert np.array_equal(to_host(A), w)
+        assert np.array_equal(to_host(B), b)
 
 
 @pytest.mark.parametrize("n,c,h,w", [(128, 128, 8, 8), (3, 5, 7, 3), (2, 4, 4, 4)])
