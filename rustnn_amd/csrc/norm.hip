@@ -208,7 +208,7 @@ __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
     const int nr = r0 < rows ? (int)min((size_t)RPW, (rows - r0 + 3) / 4) : 0;
     const float inv = 1.0f / (float)c;
     double p[2][NV];
-    float gv[NV], dv[RPW][NV], hv[RPW][NV];
+    float gv[NV], dv[RPW][NV], hv[RPW][NV], ad[RPW][NV];
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int j = min(lane + 64 * i, c - 1);
@@ -219,6 +219,8 @@ __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
             const size_t r = min(r0 + 4 * (size_t)k, rows - 1);
             dv[k][i] = dy[r * c + j];
             hv[k][i] = xhat[r * c + j];
+            // add's values too, before any store (add may be dx)
+            ad[k][i] = add ? add[r * c + j] : 0.0f;
         }
     }
 #pragma unroll
@@ -235,11 +237,6 @@ __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
                 p[0][i] += (double)(dv[k][i] * hv[k][i]);
                 p[1][i] += dv[k][i];
             }
-        float ad[NV];
-        if (add) {
-#pragma unroll
-            for (int i = 0; i < NV; i++) ad[i] = add[r * c + min(lane + 64 * i, c - 1)];
-        }
         const float s1 = (float)rnn_wave_sum_d(m1), s2 = (float)rnn_wave_sum_d(m2);
         const float is = invstd[r];
         float *xr = dx + r * c;
@@ -249,7 +246,7 @@ __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
             if (j >= c) break;
             const float d = dv[k][i] * gv[i];
             const float v = is * (d - s1 * inv - hv[k][i] * s2 * inv);
-            xr[j] = add ? v + ad[i] : v;
+            xr[j] = add ? v + ad[k][i] : v;
         }
     }
     store_col_partials<NV, 2>(p, c, part);
@@ -1071,6 +1068,7 @@ int rnn_ln_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const fl
         case 6: fwd(ln_fwd_kernel<6>); break;
         case 7: fwd(ln_fwd_kernel<7>); break;
         case 8: fwd(ln_fwd_kernel<8>); break;
+        case 16: fwd(ln_fwd_kernel<16>); break;
         default: fwd(ln_fwd_kernel<0>); break;
     }
     RNN_LAUNCHED(ctx);
@@ -1133,6 +1131,7 @@ static int ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, con
         case 6: bwd(ln_bwd_kernel<6>); break;
         case 7: bwd(ln_bwd_kernel<7>); break;
         case 8: bwd(ln_bwd_kernel<8>); break;
+        case 16: bwd(ln_bwd_kernel<16>); break;
         default: bwd(ln_bwd_kernel<0>); break;
     }
     RNN_LAUNCHED(ctx);
