@@ -102,6 +102,25 @@ __global__ void token_merge_kernel(size_t n, int th, int c, const float *__restr
     }
 }
 
+// The same gather / scatter four channels a thread (c % 4 == 0, 16-byte
+// aligned tensors, fewer than 2^31 quads), with 32-bit index arithmetic.
+__global__ void token_merge4_kernel(uint32_t len4, int th, int c4, const float4 *__restrict__ z,
+                                    float4 *__restrict__ y, int back) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= len4) return;
+    const uint32_t t2 = (uint32_t)th / 2;
+    const uint32_t r = i / (uint32_t)c4, j4 = i - r * (uint32_t)c4;
+    const uint32_t qd = r & 3, cell = r >> 2;
+    const uint32_t rest = cell / t2, ox = cell - rest * t2;
+    const uint32_t img = rest / t2, oy = rest - img * t2;
+    const uint32_t sy = 2 * oy + (qd >> 1), sx = 2 * ox + (qd & 1);
+    const size_t s = ((size_t)img * th * th + (size_t)sy * th + sx) * c4 + j4;
+    if (back)
+        const_cast<float4 *>(z)[s] = y[i];
+    else
+        y[i] = z[s];
+}
+
 // TaxoHead (vit.rs:282-293): zf[i][j] += zc[i][parent[j]].
 __global__ void taxo_fwd_kernel(size_t n, int nf, int nc, const uint32_t *__restrict__ parent,
                                 float *zf, const float *__restrict__ zc) {
@@ -254,6 +273,12 @@ int rnn_axpy_cols(rnn_ctx *ctx, size_t rows, size_t c, float *y, const float *l,
     return RNN_OK;
 }
 
+// The four-channel token merge: c % 4 == 0, aligned tensors, quads in 32 bits.
+static bool merge_vec(size_t c, size_t len, const void *a, const void *b) {
+    return c % 4 == 0 && len / 4 < ((size_t)1 << 31) &&
+           (((uintptr_t)a | (uintptr_t)b) & 15) == 0;
+}
+
 int rnn_token_merge(rnn_ctx *ctx, size_t n, size_t th, size_t c, const float *z, float *y) {
     if (!ctx) return RNN_E_NULL;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
@@ -262,7 +287,11 @@ int rnn_token_merge(rnn_ctx *ctx, size_t n, size_t th, size_t c, const float *z,
     if (th < 2 || th % 2 || th > 65536 || c > (1u << 24))
         return rnn_fail(ctx, RNN_E_INVALID, "token_merge: th %zu (even), c %zu", th, c);
     const size_t len = n * th * th * c;
-    token_merge_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)c, z, y, 0);
+    if (merge_vec(c, len, z, y))
+        token_merge4_kernel<<<(unsigned)rnn_div_up(len / 4, (size_t)NT), NT, 0, ctx->stream>>>(
+            (uint32_t)(len / 4), (int)th, (int)(c / 4), (const float4 *)z, (float4 *)y, 0);
+    else
+        token_merge_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)c, z, y, 0);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }
@@ -276,8 +305,13 @@ int rnn_token_merge_backward(rnn_ctx *ctx, size_t n, size_t th, size_t c, const 
     if (th < 2 || th % 2 || th > 65536 || c > (1u << 24))
         return rnn_fail(ctx, RNN_E_INVALID, "token_merge: th %zu (even), c %zu", th, c);
     const size_t len = n * th * th * c;
-    token_merge_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)c, dz,
-                                                              const_cast<float *>(dy), 1);
+    if (merge_vec(c, len, dz, dy))
+        token_merge4_kernel<<<(unsigned)rnn_div_up(len / 4, (size_t)NT), NT, 0, ctx->stream>>>(
+            (uint32_t)(len / 4), (int)th, (int)(c / 4), (const float4 *)dz,
+            (float4 *)const_cast<float *>(dy), 1);
+    else
+        token_merge_kernel<<<ew_grid(len), NT, 0, ctx->stream>>>(n, (int)th, (int)c, dz,
+                                                                  const_cast<float *>(dy), 1);
     RNN_LAUNCHED(ctx);
     return RNN_OK;
 }

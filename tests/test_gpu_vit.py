@@ -71,9 +71,12 @@ def test_drop_path_masks_batched(rnn, orc):
     assert np.array_equal(to_host(X).ravel(), want)
 
 
-def test_token_merge_and_layout(rnn, orc):
+@pytest.mark.parametrize("n,th,c", [(16, 8, 256), (3, 4, 6)])
+def test_token_merge_and_layout(rnn, orc, n, th, c):
+    """token_merge / token_merge_back bit-exact against the oracle (c 256:
+    the four-channel kernel; c 6: the one-element kernel), and the NCHW <->
+    token layout changes."""
     from rustnn_amd.vit import nchw_to_tokens, token_merge, token_merge_back, tokens_to_nchw
-    n, th, c = 16, 8, 256
     z = np.random.default_rng(1).standard_normal(n * th * th * c).astype(np.float32)
     y = token_merge(to_dev(z).reshape(n, th * th, c), th)
     assert np.array_equal(to_host(y).ravel(), orc.token_merge(z, n, th, c))
