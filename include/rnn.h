@@ -382,6 +382,18 @@ int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const 
 int rnn_ln_backward_add(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
                         const float *invstd, const float *g, const float *add, float *dx,
                         float *dg, float *db);
+/* rnn_ln_backward_add, then the DropPath + LayerScale backward that reads
+ * its dx (the next block's first op in a backward over Blocks, vit.rs:175-
+ * 232): lsdx = (dx m) l and dl += sum (dx m) lsx, m = mask[r / rpi] or 1
+ * when NULL -- the values rnn_ln_backward_add then
+ * rnn_drop_layerscale_backward(dx, lsx, l, mask, rpi, lsdx, dl) give, bit
+ * for bit, in the same pass for c <= 512.  lsdx must not overlap dy, add,
+ * dx or lsx. */
+int rnn_ln_backward_add_ls(rnn_ctx *ctx, size_t rows, size_t c, const float *dy,
+                           const float *xhat, const float *invstd, const float *g,
+                           const float *add, float *dx, float *dg, float *db, const float *lsx,
+                           const float *l, const float *mask, size_t rpi, float *lsdx,
+                           float *dl);
 /* LayerScale::forward / backward (norm.rs:166-212): y = x l per channel (y may
  * be x); dl += sum dy x, dx = dy l (dx may be dy). */
 int rnn_layerscale_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const float *l,

@@ -156,6 +156,7 @@ extern "C" {
     pub fn rnn_ln_forward(ctx: *mut rnn_ctx, rows: usize, c: usize, x: *const f32, g: *const f32, b: *const f32, eps: f32, y: *mut f32, xhat: *mut f32, invstd: *mut f32) -> c_int;
     pub fn rnn_ln_backward(ctx: *mut rnn_ctx, rows: usize, c: usize, dy: *const f32, xhat: *const f32, invstd: *const f32, g: *const f32, dx: *mut f32, dg: *mut f32, db: *mut f32) -> c_int;
     pub fn rnn_ln_backward_add(ctx: *mut rnn_ctx, rows: usize, c: usize, dy: *const f32, xhat: *const f32, invstd: *const f32, g: *const f32, add: *const f32, dx: *mut f32, dg: *mut f32, db: *mut f32) -> c_int;
+    pub fn rnn_ln_backward_add_ls(ctx: *mut rnn_ctx, rows: usize, c: usize, dy: *const f32, xhat: *const f32, invstd: *const f32, g: *const f32, add: *const f32, dx: *mut f32, dg: *mut f32, db: *mut f32, lsx: *const f32, l: *const f32, mask: *const f32, rpi: usize, lsdx: *mut f32, dl: *mut f32) -> c_int;
     pub fn rnn_layerscale_forward(ctx: *mut rnn_ctx, rows: usize, c: usize, x: *const f32, l: *const f32, y: *mut f32) -> c_int;
     pub fn rnn_layerscale_backward(ctx: *mut rnn_ctx, rows: usize, c: usize, dy: *const f32, x: *const f32, l: *const f32, dx: *mut f32, dl: *mut f32) -> c_int;
     pub fn rnn_drop_layerscale_backward(ctx: *mut rnn_ctx, rows: usize, c: usize, dy: *const f32, x: *const f32, l: *const f32, mask: *const f32, rpi: usize, dx: *mut f32, dl: *mut f32) -> c_int;

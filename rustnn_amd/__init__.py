@@ -217,6 +217,8 @@ def lib():
             "rnn_drop_path_masks": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),
             "rnn_residual_add_scaled": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _sz, _vp]),
             "rnn_ln_backward_add": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+            "rnn_ln_backward_add_ls": (_i, [_vp, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _vp, _sz, _vp, _vp]),
             "rnn_axpy_cols": (_i, [_vp, _sz, _sz, _vp, _vp, _vp]),
             "rnn_token_merge": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),
             "rnn_token_merge_backward": (_i, [_vp, _sz, _sz, _sz, _vp, _vp]),

@@ -194,26 +194,48 @@ __device__ __forceinline__ void store_col_partials(const double (&p)[NO][NV], in
 // dy and xhat before the first row's reductions.  With `add` set, dx = the
 // row's gradient + add (Block::backward's add_ after the norm; add may be
 // dx: each element is read, then written, by one lane).
-template <int NV>
+// With LS, the DropPath + LayerScale backward that reads dx next
+// (ls_bwd_cs_kernel's values): t = dx m, lsdx = t l, dl's partials
+// (double)(t lsx) into lspart.
+struct LnLs {
+    const float *x, *l, *mask;
+    size_t rpi;
+    float *dx;
+    double *part;
+};
+
+template <int NV, bool LS = false>
 __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
                                                        const float *dy,
                                                        const float *__restrict__ xhat,
                                                        const float *__restrict__ invstd,
                                                        const float *__restrict__ g,
                                                        const float *add, float *dx,
-                                                       double *__restrict__ part) {
+                                                       double *__restrict__ part, LnLs ls = {}) {
     constexpr int RPW = RB_ROWS / 4;
     const int lane = threadIdx.x & 63, w = wave_index();
     const size_t r0 = (size_t)blockIdx.x * RB_ROWS + w;
     const int nr = r0 < rows ? (int)min((size_t)RPW, (rows - r0 + 3) / 4) : 0;
     const float inv = 1.0f / (float)c;
-    double p[2][NV];
+    double p[2][NV], pl[1][NV];
     float gv[NV], dv[RPW][NV], hv[RPW][NV], ad[RPW][NV];
+    float lv[NV], lx[RPW][NV], lm[RPW];
+    if constexpr (LS) {
+#pragma unroll
+        for (int k = 0; k < RPW; k++) {
+            const size_t r = min(r0 + 4 * (size_t)k, rows - 1);
+            lm[k] = ls.mask ? ls.mask[r / ls.rpi] : 1.0f;
+        }
+    }
 #pragma unroll
     for (int i = 0; i < NV; i++) {
         const int j = min(lane + 64 * i, c - 1);
         gv[i] = g[j];
         p[0][i] = p[1][i] = 0.0;
+        if constexpr (LS) {
+            lv[i] = ls.l[j];
+            pl[0][i] = 0.0;
+        }
 #pragma unroll
         for (int k = 0; k < RPW; k++) {
             const size_t r = min(r0 + 4 * (size_t)k, rows - 1);
@@ -221,6 +243,7 @@ __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
             hv[k][i] = xhat[r * c + j];
             // add's values too, before any store (add may be dx)
             ad[k][i] = add ? add[r * c + j] : 0.0f;
+            if constexpr (LS) lx[k][i] = ls.x[r * c + j];
         }
     }
 #pragma unroll
@@ -246,10 +269,20 @@ __global__ __launch_bounds__(NT) void ln_bwd_cs_kernel(size_t rows, int c,
             if (j >= c) break;
             const float d = dv[k][i] * gv[i];
             const float v = is * (d - s1 * inv - hv[k][i] * s2 * inv);
-            xr[j] = add ? v + ad[k][i] : v;
+            const float o = add ? v + ad[k][i] : v;
+            xr[j] = o;
+            if constexpr (LS) {
+                const float t = ls.mask ? o * lm[k] : o;
+                pl[0][i] += (double)(t * lx[k][i]);
+                ls.dx[r * c + j] = t * lv[i];
+            }
         }
     }
     store_col_partials<NV, 2>(p, c, part);
+    if constexpr (LS) {
+        __syncthreads();  // the partials' LDS staging is reused
+        store_col_partials<NV, 1>(pl, c, ls.part);
+    }
 }
 
 // DropPath + LayerScale backward (scale_cols_masked_kernel per row) with
@@ -1079,7 +1112,7 @@ int rnn_ln_forward(rnn_ctx *ctx, size_t rows, size_t c, const float *x, const fl
 // columns).
 static int ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,
                        const float *invstd, const float *g, const float *add, float *dx,
-                       float *dg, float *db) {
+                       float *dg, float *db, const LnLs *ls = nullptr, float *dl = nullptr) {
     if (rows == 0 || c == 0) return RNN_OK;
     if (!dy || !xhat || !invstd || !g || !dx || !dg || !db)
         return rnn_fail(ctx, RNN_E_NULL, "ln_backward: null operand");
@@ -1090,24 +1123,43 @@ static int ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, con
         // one pass: dx and the column sums' partials, then their reduction
         const size_t nblk = rnn_div_up(rows, (size_t)RB_ROWS);
         if (nblk > 0x7fffffff) return rnn_fail(ctx, RNN_E_UNSUPPORTED, "ln_backward: rows");
-        double *part = col_part(ctx, nblk * 2 * c * sizeof(double));
+        const size_t pb = nblk * 2 * c * sizeof(double);
+        double *part = col_part(ctx, pb + (ls ? nblk * c * sizeof(double) : 0));
         if (!part) return RNN_E_NOMEM;
+        LnLs l{};
+        if (ls) {
+            l = *ls;
+            l.part = part + nblk * 2 * c;
+        }
         auto cs = [&](auto kern) {
             kern<<<(unsigned)nblk, NT, 0, ctx->stream>>>(rows, (int)c, dy, xhat, invstd, g, add,
-                                                         dx, part);
+                                                         dx, part, l);
         };
+#define RNN_LN_CS(NV)                                                                     \
+    ls ? cs(ln_bwd_cs_kernel<NV, true>) : cs(ln_bwd_cs_kernel<NV, false>);               \
+    break;
         switch (nv) {
-            case 1: cs(ln_bwd_cs_kernel<1>); break;
-            case 2: cs(ln_bwd_cs_kernel<2>); break;
-            case 3: cs(ln_bwd_cs_kernel<3>); break;
-            case 4: cs(ln_bwd_cs_kernel<4>); break;
-            case 5: cs(ln_bwd_cs_kernel<5>); break;
-            case 6: cs(ln_bwd_cs_kernel<6>); break;
-            case 7: cs(ln_bwd_cs_kernel<7>); break;
-            default: cs(ln_bwd_cs_kernel<8>); break;
+            case 1: RNN_LN_CS(1)
+            case 2: RNN_LN_CS(2)
+            case 3: RNN_LN_CS(3)
+            case 4: RNN_LN_CS(4)
+            case 5: RNN_LN_CS(5)
+            case 6: RNN_LN_CS(6)
+            case 7: RNN_LN_CS(7)
+            default: RNN_LN_CS(8)
         }
+#undef RNN_LN_CS
         RNN_LAUNCHED(ctx);
-        return col_reduce(ctx, nblk, 2 * c, c, part, dg, db);
+        int rc = col_reduce(ctx, nblk, 2 * c, c, part, dg, db);
+        if (!rc && ls) rc = col_reduce(ctx, nblk, c, c, l.part, dl, nullptr);
+        return rc;
+    }
+    if (ls) {
+        // the two passes
+        int rc = ln_backward(ctx, rows, c, dy, xhat, invstd, g, add, dx, dg, db);
+        if (!rc) rc = rnn_drop_layerscale_backward(ctx, rows, c, dx, ls->x, ls->l, ls->mask,
+                                                   ls->rpi, ls->dx, dl);
+        return rc;
     }
     int rc = colsum_add(ctx, rows, (int)c, dy, xhat, dg, db);
     if (rc) return rc;
@@ -1140,6 +1192,25 @@ static int ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, con
         RNN_LAUNCHED(ctx);
     }
     return RNN_OK;
+}
+
+int rnn_ln_backward_add_ls(rnn_ctx *ctx, size_t rows, size_t c, const float *dy,
+                           const float *xhat, const float *invstd, const float *g,
+                           const float *add, float *dx, float *dg, float *db, const float *lsx,
+                           const float *l, const float *mask, size_t rpi, float *lsdx,
+                           float *dl) {
+    if (!ctx) return RNN_E_NULL;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (rows == 0 || c == 0) return RNN_OK;
+    if (!add || !lsx || !l || !lsdx || !dl)
+        return rnn_fail(ctx, RNN_E_NULL, "ln_backward_add_ls: null operand");
+    if (mask && (rpi == 0 || rows % rpi))
+        return rnn_fail(ctx, RNN_E_INVALID, "ln_backward_add_ls: %zu rows per image of %zu", rpi,
+                        rows);
+    if (lsdx == dx || lsdx == dy || lsdx == add || lsdx == lsx)
+        return rnn_fail(ctx, RNN_E_INVALID, "ln_backward_add_ls: lsdx overlaps an operand");
+    const LnLs ls{lsx, l, mask, mask ? rpi : 1, lsdx, nullptr};
+    return ln_backward(ctx, rows, c, dy, xhat, invstd, g, add, dx, dg, db, &ls, dl);
 }
 
 int rnn_ln_backward(rnn_ctx *ctx, size_t rows, size_t c, const float *dy, const float *xhat,

@@ -47,13 +47,29 @@ class LayerNorm:
             _ptr(xh, rows * c, "xhat"), _ptr(iv, rows, "invstd")))
         return y
 
-    def backward(self, dy, add=None, out=None):
+    def backward(self, dy, add=None, out=None, ls=None):
         """Returns dx; with ``add``, dx + add in the same pass (the add_ that
         follows the norm in Block::backward), written to ``out`` (which may
-        be ``add``) or a new tensor."""
+        be ``add``) or a new tensor.  With ``ls`` = (LayerScale, DropPath
+        mask or None) as well, that layer's backward over the returned dx
+        runs in the same pass: returns (dx, the LayerScale's input gradient),
+        as ``ls[0].backward(dx, ls[1])`` would."""
         import torch
         rows, c = _rows_c(dy)
         dx = out if out is not None else torch.empty_like(dy)
+        if ls is not None:
+            if add is None:
+                raise ValueError("LayerNorm.backward: ls needs add")
+            layer, mask = ls
+            lsdx = torch.empty_like(dy)
+            self.ctx.check(lib().rnn_ln_backward_add_ls(
+                self.ctx.h, rows, c, _ptr(dy, rows * c, "dy"), _ptr(self.xhat, rows * c, "xhat"),
+                _ptr(self.invstd, rows, "invstd"), _ptr(self.g.v, c, "g"),
+                _ptr(add, rows * c, "add"), _ptr(dx, rows * c, "dx"), _ptr(self.g.g, c, "dg"),
+                _ptr(self.b.g, c, "db"), _ptr(layer.x, rows * c, "lsx"), _ptr(layer.l.v, c, "l"),
+                _ptr(mask, 1, "mask"), rows // mask.numel() if mask is not None else 1,
+                _ptr(lsdx, rows * c, "lsdx"), _ptr(layer.l.g, c, "dl")))
+            return dx, lsdx
         if add is None:
             self.ctx.check(lib().rnn_ln_backward(
                 self.ctx.h, rows, c, _ptr(dy, rows * c, "dy"), _ptr(self.xhat, rows * c, "xhat"),

@@ -328,10 +328,19 @@ class Block:
     def backward(self, dz, mem=None, dmem=None, set_dmem=False):
         """Returns dx; dmem accumulates the memory's gradient (vit.rs:175-249)
         -- set_dmem: is written, as a zeroed dmem would be."""
+        return self.backward_fused(dz, mem, dmem, set_dmem)[0]
+
+    def backward_fused(self, dz, mem=None, dmem=None, set_dmem=False, dm=None, nxt=None):
+        """Block::backward with the seams between blocks fused: ``dm`` is this
+        block's ls2 input gradient when the previous call already computed it
+        (else ls2's backward runs here), and with ``nxt`` (the block whose
+        backward follows) its ls2 backward runs in this block's last
+        LayerNorm pass.  Returns (dx, nxt's ls2 input gradient or None)."""
         import torch
         L, ctx, c = lib(), self.ctx, self.c
         # each branch's DropPath + LayerScale backward reads dz / dy unchanged
-        dm = self.ls2.backward(dz, self.dp3.mask)
+        if dm is None:
+            dm = self.ls2.backward(dz, self.dp3.mask)
         dh2 = self.mlp.backward(dm)
         dy = self.n2.backward(dh2, add=dz)  # n2's input gradient + dz, a new tensor
         # the first residual's branch gradients in one pass over dy: dc =
@@ -356,8 +365,12 @@ class Block:
         # the kernel that computes it
         dh = self.attn.backward(da, acc_dx=dh)
         self.dw.backward(ddw, acc_dx=dh)
-        self.n1.backward(dh, add=dy, out=dy)  # dy += n1's input gradient
-        return dy
+        if nxt is None:
+            self.n1.backward(dh, add=dy, out=dy)  # dy += n1's input gradient
+            return dy, None
+        # dy += n1's input gradient, and the next block's ls2 backward of it
+        _, dm_next = self.n1.backward(dh, add=dy, out=dy, ls=(nxt.ls2, nxt.dp3.mask))
+        return dy, dm_next
 
     def for_each_param(self, f):
         """Block::for_each_param (vit.rs:234-249)."""
@@ -720,8 +733,11 @@ class RustViT:
             add_(dfeat, g["hfinal"], ctx)
         dzf = self.pool.backward(dfeat)
         dz4 = self.headln.backward(dzf)
-        for b in reversed(self.blocks4):
-            dz4 = b.backward(dz4)
+        # each block's last LayerNorm pass also runs the next one's ls2
+        # backward (Block.backward_fused)
+        order, dm = self.blocks4[::-1], None
+        for i, b in enumerate(order):
+            dz4, dm = b.backward_fused(dz4, dm=dm, nxt=order[i + 1] if i + 1 < len(order) else None)
         t4 = dz4.shape[1]
         dmg = self.merge.backward(dz4.reshape(-1)).view(n, t4, 4 * d)
         dzn = self.mergeln.backward(dmg)
@@ -734,8 +750,10 @@ class RustViT:
         # zeroed dmem receives (vit.rs:652-655)
         dmem = torch.empty_like(self.mem)
         first = True
-        for b in reversed(self.blocks3):
-            dz = b.backward(dz, self.mem, dmem, set_dmem=first and b.cross is not None)
+        order, dm = self.blocks3[::-1], None
+        for i, b in enumerate(order):
+            dz, dm = b.backward_fused(dz, self.mem, dmem, first and b.cross is not None, dm,
+                                      order[i + 1] if i + 1 < len(order) else None)
             first = first and b.cross is None
         if first:
             dmem.zero_()  # no reader block

@@ -82,6 +82,38 @@ def test_layernorm_backward_add(rnn, orc, rows, c):
     assert rel_frob(to_host(ln.g.g), 3 * dg) < TOL and rel_frob(to_host(ln.b.g), 3 * db) < TOL
 
 
+@pytest.mark.parametrize("n,t,c,masked", [(8, 64, 256, True), (3, 5, 384, False),
+                                          (2, 9, 600, True)])
+def test_layernorm_backward_add_ls(rnn, orc, n, t, c, masked):
+    """rnn_ln_backward_add_ls == rnn_ln_backward_add then the DropPath +
+    LayerScale backward of its dx (rnn_drop_layerscale_backward), bit for
+    bit: dx, the LayerScale's input gradient, dgamma / dbeta and dl (c 600:
+    the separate passes; 3 x 5 rows leave a partial row block)."""
+    from rustnn_amd.norm import LayerNorm, LayerScale
+    rows = n * t
+    x, dy, r, lx = (_r((rows, c), 41 + i, 1.5 if i == 0 else 1.0) for i in range(4))
+    mask = ((np.random.default_rng(45).random(n) < 0.7) / 0.7).astype(np.float32) if masked \
+        else None
+    outs = []
+    for fused in (False, True):
+        ln, ls = LayerNorm(c), LayerScale(c, 0.3)
+        ln.g.v.copy_(to_dev(_r(c, 46, 0.2, 1.0)))
+        ls.l.v.copy_(to_dev(_r(c, 47, 0.1, 0.4)))
+        ln.forward(_dev(x), True)
+        ls.x = _dev(lx)
+        M = to_dev(mask) if masked else None
+        R = _dev(r)
+        if fused:
+            dx, ldx = ln.backward(_dev(dy), add=R, out=R, ls=(ls, M))
+        else:
+            dx = ln.backward(_dev(dy), add=R, out=R)
+            ldx = ls.backward(dx, M)
+        outs.append([to_host(v).ravel() for v in (dx, ldx, ln.g.g, ln.b.g, ls.l.g)])
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    assert outs[1][4].any()
+
+
 def test_layerscale(rnn, orc):
     from rustnn_amd.norm import LayerScale
     rows, c = 2048, 384
