@@ -565,12 +565,21 @@ __global__ void gap_fwd_kernel(const float *__restrict__ x, int hw, size_t nc, i
     const float *p = x + i * hw;
     float s = 0.0f;
     if (vec) {
-        for (int j = 0; j < hw; j += 4) {
-            const float4 v = *reinterpret_cast<const float4 *>(p + j);
-            s = s + v.x;
-            s = s + v.y;
-            s = s + v.z;
-            s = s + v.w;
+        // 16 loads in flight ahead of their (pixel-order) adds
+        for (int j0 = 0; j0 < hw; j0 += 64) {
+            float4 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                v[u] = j0 + 4 * u < hw ? *reinterpret_cast<const float4 *>(p + j0 + 4 * u)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                if (j0 + 4 * u >= hw) break;
+                s = s + v[u].x;
+                s = s + v[u].y;
+                s = s + v[u].z;
+                s = s + v[u].w;
+            }
         }
     } else {
         for (int j = 0; j < hw; j++) s = s + p[j];

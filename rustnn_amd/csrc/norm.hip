@@ -945,16 +945,20 @@ __global__ __launch_bounds__(NT) void seqpool_bwd_kernel(int t, int c, const flo
                                                          const float *__restrict__ p,
                                                          float *__restrict__ dx,
                                                          float *__restrict__ part) {
-    __shared__ float dw[SP_MAXT];
+    __shared__ float dw[SP_MAXT], wi[SP_MAXT];
     __shared__ float dot_s;
     extern __shared__ float xl[];
     const size_t im = blockIdx.x;
-    const float *xi = x + im * t * c, *dzi = dz + im * c, *wi = wsave + im * t;
+    const float *xi = x + im * t * c, *dzi = dz + im * c;
+    // the image's softmax weights in LDS (read by every channel's loop)
+    for (int j = threadIdx.x; j < t; j += NT) wi[j] = wsave[im * t + j];
     size_t ld = c;
     if constexpr (XL) {
-        seqpool_stage(xi, t, c, xl);
+        seqpool_stage(xi, t, c, xl);  // (its barrier also covers wi)
         xi = xl;
         ld = c + 1;
+    } else {
+        __syncthreads();
     }
     for (int j = threadIdx.x; j < t; j += NT) {
         float s = 0.0f;
