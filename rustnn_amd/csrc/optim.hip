@@ -31,6 +31,10 @@ constexpr float NS_A = 3.4445f;
 constexpr float NS_B = -4.7750f;
 constexpr float NS_C = 2.0315f;
 constexpr int OPT_THREADS = 256;
+// Elements a thread loads before it stores any of them in the elementwise
+// passes (a store may alias a later load, so the compiler keeps them in
+// order; batching keeps OPT_U loads in flight).
+constexpr int OPT_U = 8;
 constexpr int NS_CHUNK = 4096;  // elements of one matrix per block in the norm passes
 
 // One matrix of a Newton-Schulz plan.  Its elementwise passes use one block
@@ -67,15 +71,29 @@ __global__ __launch_bounds__(OPT_THREADS) void muon_momentum_kernel(const NsMat 
     const size_t chunk = blockIdx.x - mt.blk0, len = (size_t)mt.rows * mt.cols;
     const size_t e0 = chunk * NS_CHUNK, e1 = min(len, e0 + NS_CHUNK);
     double s = 0.0;
-    for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS) {
-        float gi = mt.g[e];
-        if (momentum) {
-            const float mi = mom * mt.m[e] + gi;
-            mt.m[e] = mi;
-            gi += mom * mi;
-            mt.g[e] = gi;
+    // OPT_U elements' loads ahead of their stores (the elements, and the
+    // adds into s, in the order of a plain strided loop)
+    for (size_t b = e0 + threadIdx.x; b < e1; b += OPT_U * OPT_THREADS) {
+        float gv[OPT_U], mv[OPT_U];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            const size_t e = min(b + (size_t)u * OPT_THREADS, e1 - 1);
+            gv[u] = mt.g[e];
+            mv[u] = momentum ? mt.m[e] : 0.0f;
         }
-        s += (double)gi * (double)gi;
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            const size_t e = b + (size_t)u * OPT_THREADS;
+            if (e >= e1) break;
+            float gi = gv[u];
+            if (momentum) {
+                const float mi = mom * mv[u] + gi;
+                mt.m[e] = mi;
+                gi += mom * mi;
+                mt.g[e] = gi;
+            }
+            s += (double)gi * (double)gi;
+        }
     }
     for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
@@ -108,7 +126,17 @@ __global__ __launch_bounds__(OPT_THREADS) void ns_load_kernel(const NsMat *__res
     const float inv = 1.0f / norm;
     const size_t len = (size_t)mt.rows * mt.cols;
     const size_t e0 = (size_t)(blockIdx.x - mt.blk0) * NS_CHUNK, e1 = min(len, e0 + NS_CHUNK);
-    for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS) mt.x[e] = mt.g[e] * inv;
+    for (size_t b = e0 + threadIdx.x; b < e1; b += OPT_U * OPT_THREADS) {
+        float gv[OPT_U];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) gv[u] = mt.g[min(b + (size_t)u * OPT_THREADS, e1 - 1)];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            const size_t e = b + (size_t)u * OPT_THREADS;
+            if (e >= e1) break;
+            mt.x[e] = gv[u] * inv;
+        }
+    }
 }
 
 // End of a Muon step (optim.rs:191-195), reading the orthogonalised matrix
@@ -121,13 +149,25 @@ __global__ __launch_bounds__(OPT_THREADS) void muon_finish_kernel(const NsMat *_
     const size_t len = (size_t)mt.rows * mt.cols;
     const size_t e0 = (size_t)(blockIdx.x - mt.blk0) * NS_CHUNK, e1 = min(len, e0 + NS_CHUNK);
     const float wdp = mt.decay ? wd : 0.0f;
-    for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS) {
-        const float gx = mt.xf[e];
-        if (update) {
-            mt.v[e] -= lr * (mt.scale * gx + wdp * mt.v[e]);
-            mt.g[e] = 0.0f;
-        } else {
-            mt.g[e] = gx;
+    for (size_t b = e0 + threadIdx.x; b < e1; b += OPT_U * OPT_THREADS) {
+        float xv[OPT_U], vv[OPT_U];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            const size_t e = min(b + (size_t)u * OPT_THREADS, e1 - 1);
+            xv[u] = mt.xf[e];
+            vv[u] = update ? mt.v[e] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            const size_t e = b + (size_t)u * OPT_THREADS;
+            if (e >= e1) break;
+            const float gx = xv[u];
+            if (update) {
+                mt.v[e] = vv[u] - lr * (mt.scale * gx + wdp * vv[u]);
+                mt.g[e] = 0.0f;
+            } else {
+                mt.g[e] = gx;
+            }
         }
     }
 }
@@ -248,8 +288,16 @@ __global__ __launch_bounds__(OPT_THREADS) void clip_sumsq_kernel(const ClipSeg *
     const size_t e0 = (size_t)(blockIdx.x - sg.blk0) * CLIP_CHUNK;
     const size_t e1 = min(sg.len, e0 + CLIP_CHUNK);
     double s = 0.0;
-    for (size_t e = e0 + threadIdx.x; e < e1; e += OPT_THREADS)
-        s += (double)sg.g[e] * (double)sg.g[e];
+    for (size_t b = e0 + threadIdx.x; b < e1; b += OPT_U * OPT_THREADS) {
+        float gv[OPT_U];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) gv[u] = sg.g[min(b + (size_t)u * OPT_THREADS, e1 - 1)];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            if (b + (size_t)u * OPT_THREADS >= e1) break;
+            s += (double)gv[u] * (double)gv[u];
+        }
+    }
     for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
     __syncthreads();
@@ -271,9 +319,18 @@ __global__ __launch_bounds__(OPT_THREADS) void clip_scale_segs_kernel(
     if (sc[1] == 0.0f) return;
     const float f = sc[0];
     const ClipSeg sg = segs[sidx[seg_of(sidx, nseg, blockIdx.x)].seg];
-    for (size_t i = (size_t)(blockIdx.x - sg.cblk0) * OPT_THREADS + threadIdx.x; i < sg.len;
-         i += (size_t)sg.cnblk * OPT_THREADS)
-        sg.g[i] *= f;
+    const size_t st = (size_t)sg.cnblk * OPT_THREADS;
+    for (size_t b = (size_t)(blockIdx.x - sg.cblk0) * OPT_THREADS + threadIdx.x; b < sg.len;
+         b += OPT_U * st) {
+        float gv[OPT_U];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) gv[u] = sg.g[min(b + u * st, sg.len - 1)];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            if (b + u * st >= sg.len) break;
+            sg.g[b + u * st] = gv[u] * f;
+        }
+    }
 }
 
 // Stores zeros (a kernel rather than a memset node, for graph capture).
@@ -294,9 +351,22 @@ struct EmaSeg {
 __global__ __launch_bounds__(OPT_THREADS) void ema_segs_kernel(const EmaSeg *__restrict__ segs,
                                                                int nseg, float d) {
     const EmaSeg s = segs[seg_of(segs, nseg, blockIdx.x)];
-    for (size_t i = (size_t)(blockIdx.x - s.blk0) * OPT_THREADS + threadIdx.x; i < s.len;
-         i += (size_t)s.nblk * OPT_THREADS)
-        s.w[i] = d * s.w[i] + (1.0f - d) * s.v[i];
+    const size_t st = (size_t)s.nblk * OPT_THREADS;
+    for (size_t b = (size_t)(blockIdx.x - s.blk0) * OPT_THREADS + threadIdx.x; b < s.len;
+         b += OPT_U * st) {
+        float wv[OPT_U], vv[OPT_U];
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            const size_t i = min(b + u * st, s.len - 1);
+            wv[u] = s.w[i];
+            vv[u] = s.v[i];
+        }
+#pragma unroll
+        for (int u = 0; u < OPT_U; u++) {
+            if (b + u * st >= s.len) break;
+            s.w[b + u * st] = d * wv[u] + (1.0f - d) * vv[u];
+        }
+    }
 }
 
 unsigned grid_for(size_t items, unsigned threads) {
@@ -798,7 +868,7 @@ int rnn_clip_params(rnn_ctx *ctx, size_t nparam, const rnn_param *params, float 
         sg.blk0 = sblk;
         sg.nblk = (uint32_t)rnn_div_up(sg.len, CLIP_CHUNK);
         sg.cblk0 = cblk;
-        sg.cnblk = (uint32_t)std::min<size_t>(rnn_div_up(sg.len, OPT_THREADS), 1024);
+        sg.cnblk = (uint32_t)std::min<size_t>(rnn_div_up(sg.len, OPT_U * OPT_THREADS), 1024);
         sblk += sg.nblk;
         cblk += sg.cnblk;
         segs.push_back(sg);
@@ -854,7 +924,7 @@ int rnn_ema_update_params(rnn_ctx *ctx, size_t nparam, float *const *w, const rn
         sg.v = params[i].v;
         sg.len = params[i].len;
         sg.blk0 = blk;
-        sg.nblk = (uint32_t)std::min<size_t>(rnn_div_up(sg.len, OPT_THREADS), 1024);
+        sg.nblk = (uint32_t)std::min<size_t>(rnn_div_up(sg.len, OPT_U * OPT_THREADS), 1024);
         blk += sg.nblk;
         segs.push_back(sg);
     }
