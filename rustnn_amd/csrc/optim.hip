@@ -111,16 +111,32 @@ __global__ __launch_bounds__(OPT_THREADS) void muon_momentum_kernel(const NsMat 
 // no counterpart here; see ns_layout).
 __global__ __launch_bounds__(OPT_THREADS) void ns_load_kernel(const NsMat *__restrict__ mats,
                                                               int nmat) {
+    constexpr uint32_t NS_LDS_PARTS = 2048;
+    __shared__ double pl[NS_LDS_PARTS];
+    __shared__ double ss_s;
     const NsMat mt = mats[mat_of(mats, nmat, blockIdx.x)];
-    // the partials in chunk order, 16 loads ahead of their adds
+    // the partials added in chunk order: staged in LDS by the whole block
+    // (one round trip), then summed by one thread
     double ss = 0.0;
-    for (uint32_t k0 = 0; k0 < mt.nchunk; k0 += 16) {
-        double v[16];
+    if (mt.nchunk <= NS_LDS_PARTS) {
+        for (uint32_t k = threadIdx.x; k < mt.nchunk; k += OPT_THREADS) pl[k] = mt.part[k];
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double t = 0.0;
+            for (uint32_t k = 0; k < mt.nchunk; k++) t += pl[k];
+            ss_s = t;
+        }
+        __syncthreads();
+        ss = ss_s;
+    } else {
+        for (uint32_t k0 = 0; k0 < mt.nchunk; k0 += 16) {
+            double v[16];
 #pragma unroll
-        for (int u = 0; u < 16; u++) v[u] = mt.part[min(k0 + u, mt.nchunk - 1)];
+            for (int u = 0; u < 16; u++) v[u] = mt.part[min(k0 + u, mt.nchunk - 1)];
 #pragma unroll
-        for (int u = 0; u < 16; u++)
-            if (k0 + u < mt.nchunk) ss += v[u];
+            for (int u = 0; u < 16; u++)
+                if (k0 + u < mt.nchunk) ss += v[u];
+        }
     }
     const float norm = sqrtf((float)ss) + 1e-7f;
     const float inv = 1.0f / norm;
